@@ -1,0 +1,259 @@
+"""Benchmark: config 3 training step on one MI355X.
+
+One step = render (fused binning + forward raster) of 4096 closed cubic paths
+(4 segments, S=16) at 2040x1356 -> clamp(0,1) -> NCHW -> loss
+MSE + 0.2 * (1 - SSIM(11, 1.5)) against the synthetic target -> backward ->
+Adam on control points and colors.  Prints one JSON line (see the contract
+in the repository's build notes).
+
+python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+SSIM_WEIGHT = 0.2
+HBM_PEAK_GBS = 8000.0
+# MI355X published vector fp32 peak (packed FMA); non-packed VALU issue is half.
+VALU_PEAK_TFLOPS = 157.3
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--stage-iters", type=int, default=20)
+    return ap.parse_args()
+
+
+def make_problem(cfg):
+    import torch
+    from repo_amd import synth
+    sc = synth.make_scene(cfg).to("cuda")
+    cub = sc.cubics_norm.clone().requires_grad_(True)
+    col = sc.colors.clone().requires_grad_(True)
+    opt = torch.optim.Adam([cub, col], lr=1e-3)
+    return sc, cub, col, opt
+
+
+def render(sc, cub, col):
+    import manbo
+    if sc.stroke_widths is not None:
+        return manbo.ops.render_cubic_polyline_splat_tilelang(
+            cub, sc.seg_offsets, col, sc.opacities, sc.stroke_widths, sc.depths, sc.img_h,
+            sc.img_w, 16, 16, sc.background, aa_widths=sc.aa_widths, distance_samples=sc.S)
+    return manbo.ops.render_cubic_fill_splat_tilelang(
+        cub, sc.seg_offsets, col, sc.opacities, sc.depths, sc.img_h, sc.img_w, 16, 16,
+        sc.background, aa_widths=sc.aa_widths, distance_samples=sc.S)
+
+
+def loss_fn(img, target):
+    import manbo
+    x = img.clamp(0, 1).permute(2, 0, 1).unsqueeze(0).contiguous()
+    return manbo.mse_loss_tilelang(x, target) + SSIM_WEIGHT * (1.0 - manbo.ssim(x, target))
+
+
+def train_step(sc, cub, col, opt):
+    opt.zero_grad(set_to_none=True)
+    loss = loss_fn(render(sc, cub, col), sc.target)
+    loss.backward()
+    opt.step()
+    return loss
+
+
+def stage_times(sc, cub, col, iters):
+    """Average ms of the main stages, timed with HIP events on the stream the
+    kernels are launched on (torch's current stream)."""
+    import torch
+    from repo_amd import splat, metric
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    offs = sc.seg_offsets.to(torch.int32).contiguous()
+    widths = torch.clamp(sc.aa_widths.float(), min=1e-4).contiguous()
+    res = {}
+
+    def timed(name, fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = ev(), ev()
+        a.record()
+        for _ in range(iters):
+            out = fn()
+        b.record()
+        torch.cuda.synchronize()
+        res[name] = a.elapsed_time(b) / iters
+        return out
+
+    mode = splat.MODE_FILL if sc.stroke_widths is None else splat.MODE_STROKE
+    cubd = cub.detach().contiguous()
+    cold = col.detach().contiguous()
+    rules = sc.fill_rules.to(torch.int32).contiguous() if mode == 0 else None
+    sw = sc.stroke_widths
+
+    def do_bin():
+        return splat.bin_primitives(cubd, offs, cold, sc.opacities, sc.depths, rules, widths, sw,
+                                    sc.img_h, sc.img_w, sc.S, mode=mode)
+    b = timed("binning_ms", do_bin)
+    out, T, idx = timed("raster_fwd_ms", lambda: splat.rasterize_forward(b, sc.background))
+    g = torch.randn_like(out)
+    timed("raster_bwd_ms", lambda: splat.rasterize_backward(b, sc.background, T, idx, g))
+    x = out.clamp(0, 1).permute(2, 0, 1).unsqueeze(0).contiguous()
+    tgt = sc.target
+    timed("mse_fwd_ms", lambda: metric.mse_forward(x.view(-1), tgt.view(-1)))
+    xr = x.detach().requires_grad_(True)
+    m = metric._TileLangMSEFn.apply(xr, tgt, 256, 8, 1)
+    timed("mse_bwd_ms", lambda: torch.autograd.grad(m, xr, retain_graph=True))
+    timed("ssim_fwd_ms", lambda: metric._ssim_forward(x, tgt, 11, 1.5, 1e-4, 9e-4, False))
+    timed("ssim_fwd_grad_ms", lambda: metric._ssim_forward(x, tgt, 11, 1.5, 1e-4, 9e-4, True))
+    s = metric._SSIMFn.apply(xr, tgt, 11, 1.5, 1e-4, 9e-4)
+    timed("ssim_bwd_ms", lambda: torch.autograd.grad(s, xr, retain_graph=True))
+    res["num_intersects"] = b.num_intersects
+    res["_binned"] = b
+    res["_T"] = T
+    res["_idx"] = idx
+    return res
+
+
+def reference_edge_pixel_evals(b, T, idx):
+    """Edge-pixel evaluations the reference's forward performs: every pixel
+    evaluates all edges of each entry of its tile list up to and including the
+    entry where it stops (T <= 1e-4), or the whole list."""
+    import torch
+    H, W = b.img_h, b.img_w
+    tbx = (W + 15) // 16
+    eps = b.edges_per_segment
+    prim_edges = (b.prim_recs.view(torch.int32)[:, 9] - b.prim_recs.view(torch.int32)[:, 8]) * eps
+    ent = prim_edges[b.primitive_ids_sorted.long()].to(torch.int64)
+    csum = torch.zeros(ent.numel() + 1, dtype=torch.int64, device=ent.device)
+    csum[1:] = torch.cumsum(ent, 0)
+    ii = torch.arange(H, device=T.device).view(-1, 1).expand(H, W)
+    jj = torch.arange(W, device=T.device).view(1, -1).expand(H, W)
+    tile = (ii // 16) * tbx + (jj // 16)
+    g0 = b.tile_bins[tile.reshape(-1), 0].long()
+    g1 = b.tile_bins[tile.reshape(-1), 1].long()
+    stop = torch.where(T.reshape(-1) <= 1e-4, idx.reshape(-1).long() + 1, g1)
+    return int((csum[stop] - csum[g0]).sum())
+
+
+def cpu_baseline(cfg):
+    """Times the CPU oracle (single thread) on a bounded sample of one training
+    step: full binning, the forward and backward raster on four 32-row bands
+    spread over the image (scaled to all rows), and the float64 losses."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    from repo_amd import synth
+    sc = synth.make_scene(cfg)
+    d = dict(cubics_norm=sc.cubics_norm.numpy(), offs=sc.seg_offsets.numpy(),
+             colors=sc.colors.numpy(), opac=sc.opacities.numpy(), depths=sc.depths.numpy(),
+             aa=sc.aa_widths.numpy(), bg=sc.background.numpy())
+    H, W = sc.img_h, sc.img_w
+    t0 = time.perf_counter()
+    b = O.bin_scene(d["cubics_norm"], d["offs"], d["depths"], d["aa"], H, W, sc.S)
+    t_bin = time.perf_counter() - t0
+    band = 32
+    starts = [int(H * f) for f in (0.1, 0.35, 0.6, 0.85)]
+    t_fwd = t_bwd = 0.0
+    rng = np.random.default_rng(0)
+    for r0 in starts:
+        rows = (r0, r0 + band)
+        t0 = time.perf_counter()
+        out, T, idx = O.raster_forward(b, d["colors"], d["opac"], d["bg"], H, W, rows=rows)
+        t_fwd += time.perf_counter() - t0
+        fw = dict(b, out=out, final_T=T, final_idx=idx, mode=0, colors=d["colors"],
+                  opacities=d["opac"], fill_rules=None, stroke_widths=None, background=d["bg"],
+                  img_h=H, img_w=W, block_x=16, block_y=16, nseg=d["cubics_norm"].shape[0],
+                  rows=rows)
+        v = rng.standard_normal((H, W, 3)).astype(np.float32)
+        t0 = time.perf_counter()
+        O.render_backward(fw, v)
+        t_bwd += time.perf_counter() - t0
+    scale = H / float(band * len(starts))
+    x = torch.rand((1, 3, H, W), dtype=torch.float64)
+    y = torch.rand((1, 3, H, W), dtype=torch.float64)
+    torch.set_num_threads(1)
+    t0 = time.perf_counter()
+    xr = x.clone().requires_grad_(True)
+    loss = ((xr - y) ** 2).mean() + SSIM_WEIGHT * (1 - O.ssim_torch64(xr, y))
+    loss.backward()
+    t_loss = time.perf_counter() - t0
+    step_s = t_bin + (t_fwd + t_bwd) * scale + t_loss
+    return {"value": 1.0 / step_s, "unit": "it/s", "cores": 1, "kind": "port",
+            "sample": (f"C oracle, 1 thread: full binning ({t_bin:.2f}s), forward+backward "
+                       f"raster on {len(starts)}x{band} pixel rows ({t_fwd + t_bwd:.2f}s, scaled "
+                       f"x{scale:.1f} to {H} rows), float64 MSE+SSIM fwd+bwd ({t_loss:.2f}s); "
+                       f"{step_s:.1f}s per step")}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the screen-space sharding "
+                                   "design is described in DESIGN.md", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    torch.backends.cudnn.benchmark = False
+    sc, cub, col, opt = make_problem(args.config)
+    for _ in range(args.warmup):
+        train_step(sc, cub, col, opt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = train_step(sc, cub, col, opt)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = 1000.0 * elapsed / max(1, args.steps)
+    st = stage_times(sc, cub, col, args.stage_iters)
+    b, T, idx = st.pop("_binned"), st.pop("_T"), st.pop("_idx")
+    evals = reference_edge_pixel_evals(b, T, idx)
+    n_img = 3 * sc.img_h * sc.img_w
+    kern = {k: round(v, 4) for k, v in st.items() if k.endswith("_ms")}
+    gbs = lambda nbytes, ms_: nbytes / (ms_ * 1e-3) / 1e9  # noqa: E731
+    kern["mse_fwd_GBs"] = round(gbs(8 * n_img, st["mse_fwd_ms"]), 1)
+    kern["mse_bwd_GBs"] = round(gbs(12 * n_img, st["mse_bwd_ms"]), 1)
+    kern["ssim_fwd_GBs"] = round(gbs(8 * n_img, st["ssim_fwd_ms"]), 1)
+    kern["reference_edge_pixel_evals_fwd"] = evals
+    # Dominant kernel: the backward raster (VALU-bound).  Algorithmic work =
+    # the reference's edge-pixel evaluations x 20 fp32 flops (distance 12,
+    # crossing 8), the same evaluations replayed in reverse.
+    flops = evals * 20.0
+    bwd_ms = st["raster_bwd_ms"]
+    fwd_ms = st["raster_fwd_ms"]
+    dom_ms, dom = (bwd_ms, "raster_bwd") if bwd_ms >= fwd_ms else (fwd_ms, "raster_fwd")
+    achieved = flops / (dom_ms * 1e-3) / 1e12
+    roofline = {"kernel": dom, "bound": "valu", "achieved": round(achieved, 2),
+                "peak": VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / VALU_PEAK_TFLOPS, 4), "traffic": None,
+                "note": "algorithmic = reference edge-pixel evaluations x 20 flops; the "
+                        "kernel culls provably non-contributing evaluations, so effective "
+                        "throughput can exceed the executed rate"}
+    line = {
+        "metric": "train it/s, 4096 closed cubics @2040x1356 fp32",
+        "value": round(1000.0 / ms, 3), "unit": "it/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"config{args.config}: "
+                   + ("4096 closed cubic paths x 4 segments, S=16, 2040x1356, "
+                      "MSE+0.2*(1-SSIM 11x11 s=1.5), Adam on control points+colors"
+                      if args.config == 3 else "see repo_amd/synth.py"),
+                   "num_intersects": st["num_intersects"], "final_loss": float(loss)},
+        "fwd_ms": round(st["binning_ms"] + fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+        "kernels": kern, "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.config)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

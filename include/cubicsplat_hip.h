@@ -1,0 +1,187 @@
+/*
+ * C ABI of libcubicsplat_hip.so: the MI355X (gfx950) kernels of CubicSplat's
+ * differentiable cubic rasterizer hot path.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer to caller-owned memory; the library
+ *     allocates nothing and keeps no state between calls.
+ *   - Every call only enqueues work on `stream` (no device-wide sync) and is
+ *     safe to call from several host threads on different streams.
+ *   - Layouts are the reference's (row-major, fp32/int32 unless stated).
+ *   - Return value: CS_OK, or CS_ERR_ARGS for invalid sizes/arguments (nothing
+ *     was enqueued), or CS_ERR_HIP when a launch failed.
+ *
+ * Reference citations are paths under /root/reference/manbo.
+ */
+#ifndef CUBICSPLAT_HIP_H
+#define CUBICSPLAT_HIP_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CS_OK 0
+#define CS_ERR_ARGS 1
+#define CS_ERR_HIP 2
+
+/* ---------------- building blocks ---------------- */
+
+/* Temp element counts (uint32) for the scan and the radix sort of n items. */
+size_t cs_scan_temp_elems(int32_t n);
+size_t cs_radix_counts_elems(int32_t n);
+
+/* Exclusive prefix sum of uint32 counts; *total (device int32, optional)
+ * receives the sum.  Replaces torch.cumsum (ops/cubic_splatting.py:2877). */
+int cs_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int32_t n, uint32_t* temp,
+                          int32_t* total, hipStream_t stream);
+
+/* Stable LSD radix sort (8-bit digits) of (key, value) pairs on the low
+ * key_bits bits; *_alt are same-size scratch.  Replaces torch.sort + gather
+ * (ops/cubic_splatting.py:2895-2896). */
+int cs_radix_sort_pairs_u32(uint32_t* keys, int32_t* vals, uint32_t* keys_alt,
+                            int32_t* vals_alt, int32_t n, int32_t key_bits, uint32_t* counts,
+                            uint32_t* scan_temp, hipStream_t stream);
+
+/* ---------------- reference-layout kernels ---------------- */
+
+/* project_cubics_2d_forward_kernel (ops/cubic_splatting.py:546-747). */
+int cs_project_cubics_2d_forward(const float* cubics_norm, const float* stroke_widths,
+                                 const float* support_radii, int32_t nseg, int32_t img_h,
+                                 int32_t img_w, int32_t block_x, int32_t block_y, float aabb_pad,
+                                 int32_t aniso, float* cubics_px, int32_t* tile_ranges,
+                                 int32_t* num_tiles_hit, hipStream_t stream);
+
+/* primitive_tile_ranges_from_segment_ranges_kernel (ops/cubic_splatting.py:2071-2137). */
+int cs_primitive_tile_ranges(const int32_t* seg_tile_ranges, const int32_t* offs, int32_t nprim,
+                             int32_t tbx, int32_t tby, int32_t* prim_tile_ranges,
+                             int32_t* num_tiles_hit, hipStream_t stream);
+
+/* map_cubic_to_intersects_kernel (ops/cubic_splatting.py:750-819): int64 keys
+ * (tile << 32 | depth_key), primitive-major. */
+int cs_map_cubic_to_intersects(const int32_t* tile_ranges, const float* depths,
+                               const int32_t* cum_tiles_hit, int32_t nprim, int32_t tbx,
+                               int64_t* isect_ids, int32_t* curve_ids, hipStream_t stream);
+
+/* get_tile_bin_edges_kernel (ops/tile_bins.py:10-60); zero-fills num_rows rows first. */
+int cs_get_tile_bin_edges(const int64_t* isect_ids_sorted, int32_t num_intersects,
+                          int32_t num_rows, int32_t* tile_bins, hipStream_t stream);
+
+/* _build_fill_isect_edge_ranges (ops/cubic_splatting.py:1849-1860) for
+ * uniform flattening: [seg_offsets[p]*eps, seg_offsets[p+1]*eps]. */
+int cs_isect_edge_ranges(const int32_t* prim_ids_sorted, const int32_t* seg_offsets,
+                         int32_t num_intersects, int32_t edges_per_segment, int32_t* out,
+                         hipStream_t stream);
+
+/* ---------------- fused forward binning ---------------- */
+
+/* Size in bytes of one flattened edge record and one primitive record. */
+#define CS_EDGE_RECORD_BYTES 32
+#define CS_PRIM_RECORD_BYTES 64
+
+/* Stage 1 of _CubicFillSplatFunction.forward / _CubicPolylineSplatFunction.forward
+ * (ops/cubic_splatting.py:2815-2880, ops/cubic_polyline_splatting.py:1027-1098):
+ * project + exact AABB + tile ranges, uniform Bernstein flattening
+ * (ops/cubic_splatting.py:1709-1719), per-primitive tile counts, depth ranks,
+ * per-rank output offsets, and status[4] (device int32) = {intersection
+ * total, 1 if seg_offsets is not a valid CSR of nseg segments (the kernels
+ * then clamp every range), seg_offsets[0], seg_offsets[nprim]}.
+ * mode 0 = closed fill, 1 = open stroke (stroke_widths required). */
+int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const float* colors,
+                   const float* opacities, const float* depths, const int32_t* fill_rules,
+                   const float* aa_widths, const float* stroke_widths, int32_t nseg,
+                   int32_t nprim, int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
+                   int32_t samples, float aabb_pad, int32_t aniso, int32_t mode,
+                   float* cubics_px, int32_t* seg_tile_ranges, float* seg_bbox, void* edges,
+                   int32_t* prim_tile_ranges, uint32_t* num_tiles_hit, float* inv_sigma2s,
+                   void* prim_recs, uint32_t* keys, int32_t* order, uint32_t* keys_alt,
+                   int32_t* vals_alt, uint32_t* radix_counts, uint32_t* scan_temp,
+                   uint32_t* rank_offsets, int32_t* status, hipStream_t stream);
+
+/* Stage 2 (ops/cubic_splatting.py:2888-2908): emit (tile, primitive) pairs in
+ * depth-rank order, stable sort by tile, tile_bins [T,2].  Outputs are the
+ * reference's primitive_ids_sorted [I] and tile_bins, bit-exact. */
+int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges,
+                  const uint32_t* rank_offsets, int32_t nprim, int32_t num_intersects,
+                  int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
+                  uint32_t* tile_keys, int32_t* prim_ids_sorted, uint32_t* keys_alt,
+                  int32_t* vals_alt, uint32_t* radix_counts, uint32_t* scan_temp,
+                  int32_t* tile_bins, hipStream_t stream);
+
+/* ---------------- rasterization ---------------- */
+
+/* rasterize_cubic_fill_forward_kernel (ops/cubic_splatting.py:918-1194) when
+ * mode 0, rasterize_cubic_polyline_forward_kernel
+ * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  16x16 tiles only. */
+int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
+                         const void* edges, const float* seg_bbox, const void* prim_recs,
+                         const float* background, int32_t img_h, int32_t img_w,
+                         int32_t edges_per_segment, float* out_img, float* final_Ts,
+                         int32_t* final_idx, hipStream_t stream);
+
+/* rasterize_cubic_fill_backward_kernel (ops/cubic_splatting.py:1197-1651) /
+ * rasterize_cubic_polyline_backward_kernel (ops/cubic_polyline_splatting.py:252-660).
+ * Accumulates (atomically) into zero-initialised v_edges [E,2,2],
+ * v_colors [P,3], v_opacities [P], v_inv_sigma2s [P], v_stroke_widths [P]
+ * (mode 1), and optionally curve_contrib_rgb [P,3] / curve_isect_contrib [I]. */
+int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
+                          const void* edges, const float* seg_bbox, const void* prim_recs,
+                          const float* background, int32_t img_h, int32_t img_w,
+                          int32_t edges_per_segment, const float* final_Ts,
+                          const int32_t* final_idx, const float* v_output, float* v_edges,
+                          float* v_colors, float* v_opacities, float* v_inv_sigma2s,
+                          float* v_stroke_widths, float* curve_contrib_rgb,
+                          float* curve_isect_contrib, hipStream_t stream);
+
+/* _accumulate_edge_grads_to_cubics_kernel (ops/cubic_splatting.py:2308-2396)
+ * fused with the v_cubics_norm scaling (ops/cubic_splatting.py:3096-3100). */
+int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg, int32_t edges_per_segment,
+                             int32_t img_h, int32_t img_w, float* v_cubics_px,
+                             float* v_cubics_norm, hipStream_t stream);
+
+/* v_aa_widths = -2 v_inv_sigma2 / max(w^3, 1e-12) (ops/cubic_splatting.py:3103-3104). */
+int cs_aa_width_grads(const float* widths, const float* v_inv_sigma2s, int32_t nprim,
+                      float* v_aa_widths, hipStream_t stream);
+
+/* ---------------- losses ---------------- */
+
+/* Number of float partials cs_mse_forward / cs_ssim needs in `partials`. */
+size_t cs_mse_partials_elems(int64_t n);
+size_t cs_ssim_partials_elems(int32_t nc, int32_t h, int32_t w);
+
+/* mse_partial_sum_kernel + reduce_sum_partial_kernel (ops/metric.py:18-163,
+ * metric.py:102-131): *loss = sum((x-y)^2)/n.  `ticket` is one device uint32
+ * that must be 0 before the first call; the kernel leaves it at 0. */
+int cs_mse_forward(const float* x, const float* y, int64_t n, float* partials, uint32_t* ticket,
+                   float* loss, hipStream_t stream);
+
+/* mse_backward_diff_kernel (ops/metric.py:166-202) with the scale
+ * grad_loss * 2/n read on the device (metric.py:168 reads it on the host):
+ * grad_x = s (x - y), grad_y = -s (x - y); either output may be null. */
+int cs_mse_backward(const float* x, const float* y, int64_t n, const float* grad_loss,
+                    float* grad_x, float* grad_y, hipStream_t stream);
+
+/* ssim_map_kernel (ops/metric.py:205-341) + the means of metric.py:267-273,
+ * separable window `win1d` [win] (the 2D window is its outer product): *out =
+ * mean over the valid SSIM map of every (image, channel), then over them.
+ * If abc != null also stores, per map pixel, dS/dmu_x, dS/dE[x^2], dS/dE[xy]
+ * ([3, nc, oh, ow]) for cs_ssim_backward.  x, y: [nc, h, w]. */
+int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+            const float* win1d, int32_t win, float c1, float c2, float* partials,
+            uint32_t* ticket, float* out, float* abc, hipStream_t stream);
+
+/* Gradient of the SSIM mean w.r.t. x (the reference has no SSIM backward):
+ * grad_x = g * [W*(A) + 2 x W*(B) + y W*(C)] / (nc*oh*ow), W* the transposed
+ * (full) window correlation, g = *grad_out (device scalar). */
+int cs_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+                     const float* win1d, int32_t win, const float* abc, const float* grad_out,
+                     float* grad_x, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUBICSPLAT_HIP_H */

@@ -1,0 +1,493 @@
+/*
+ * CPU restatement of CubicSplat's differentiable cubic rasterizer hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (repo_amd/, manbo/) may
+ * link, load or call this file; only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py use it, always as the checker.
+ *
+ * Arithmetic spec (shared with the HIP kernels, which restate it on the GPU):
+ *   - fp32 everywhere, every + - * / sqrt correctly rounded (IEEE), no implicit
+ *     contraction (-ffp-contract=off); fused multiply-adds appear only where
+ *     the code calls fmaf() explicitly.
+ *   - constants that the reference writes as Python floats (0.999, 1/255, 1e-4,
+ *     1e-6) are the fp32 rounding of the double, i.e. (float)0.999.
+ *   - exp is cs_expf below (Cody-Waite reduction + degree-7 Taylor); the GPU
+ *     uses the same function so forward images are bit-identical.
+ *   - float->int conversion truncates and saturates (NaN -> 0), like the
+ *     hardware conversion the reference's kernels compile to.
+ *
+ * Gradient sums are accumulated in double here; the GPU accumulates fp32
+ * atomics in a nondeterministic order, so gradients are compared with a
+ * tolerance while forward images, T and final_idx are compared bit for bit.
+ *
+ * Reference files followed (all under /root/reference/manbo/ops/):
+ *   cubic_splatting.py:546-747   project_cubics_2d_forward_kernel  -> orc_project_cubics
+ *   cubic_splatting.py:1654-1728 _flatten_cubics_to_edges (bernstein) -> orc_flatten
+ *   cubic_splatting.py:918-1194  rasterize_cubic_fill_forward_kernel -> orc_raster_forward(mode 0)
+ *   cubic_splatting.py:1197-1651 rasterize_cubic_fill_backward_kernel -> orc_raster_backward(mode 0)
+ *   cubic_polyline_splatting.py:33-249  polyline forward  -> orc_raster_forward(mode 1)
+ *   cubic_polyline_splatting.py:252-660 polyline backward -> orc_raster_backward(mode 1)
+ *   cubic_splatting.py:2308-2396 _accumulate_edge_grads_to_cubics_kernel -> orc_accumulate_edge_grads
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORC_EPS ((float)1e-6)
+#define ORC_ALPHA_CAP ((float)0.999)
+#define ORC_ALPHA_MIN ((float)(1.0 / 255.0))
+#define ORC_T_STOP ((float)1e-4)
+
+/* exp(x) in fp32: n = rint(x*log2 e); r = x - n*ln2 (two-part Cody-Waite);
+ * e^r by Horner on the Taylor series to degree 7 (|r| <= 0.35, truncation
+ * error < 6e-9 relative); scale by 2^n in two exact steps so that the only
+ * rounding of the scale happens in the last multiply (denormal results). */
+float cs_expf(float x)
+{
+    if (!(x == x)) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -103.97208404541015625f) return 0.0f;
+    float kf = rintf(x * 1.44269502162933349609375f);
+    float r = fmaf(kf, -0.693145751953125f, x);
+    r = fmaf(kf, -1.428606765330187045037746429443359375e-06f, r);
+    float p = 1.98412698412698e-04f;          /* 1/7! */
+    p = fmaf(p, r, 1.38888888888889e-03f);    /* 1/6! */
+    p = fmaf(p, r, 8.33333333333333e-03f);    /* 1/5! */
+    p = fmaf(p, r, 4.16666666666667e-02f);    /* 1/4! */
+    p = fmaf(p, r, 1.66666666666667e-01f);    /* 1/3! */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int k = (int)kf;
+    int k1 = k >> 1;
+    int k2 = k - k1;
+    union { uint32_t u; float f; } s1, s2;
+    s1.u = (uint32_t)(k1 + 127) << 23;
+    s2.u = (uint32_t)(k2 + 127) << 23;
+    return (p * s1.f) * s2.f;
+}
+
+/* Truncating float->int32 with saturation; NaN -> 0. */
+static inline int32_t orc_f2i(float x)
+{
+    if (!(x == x)) return 0;
+    if (x >= 2147483648.0f) return INT32_MAX;
+    if (x < -2147483648.0f) return INT32_MIN;
+    return (int32_t)x;
+}
+
+static inline int32_t orc_clampi(int32_t v, int32_t lo, int32_t hi)
+{
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+/* One axis of the exact cubic AABB: the endpoints plus the interior roots of
+ * the derivative (cubic_splatting.py:606-688), in the reference's op order. */
+static void orc_axis_extent(float p0, float p1, float p2, float p3, float *mn, float *mx)
+{
+    const float three = 3.0f, two = 2.0f, four = 4.0f, one = 1.0f, zero = 0.0f;
+    float a = ((-p0 + three * p1) - three * p2) + p3;
+    float b = (three * p0 - 6.0f * p1) + three * p2;
+    float c = -three * p0 + three * p1;
+    float d = p0;
+    float lo = fminf(p0, p3), hi = fmaxf(p0, p3);
+    float q2 = three * a, q1 = two * b, q0 = c;
+    if (q2 > ORC_EPS || q2 < -ORC_EPS) {
+        float disc = q1 * q1 - four * q2 * q0;
+        if (disc >= -ORC_EPS) {
+            float sd = sqrtf(fmaxf(disc, zero));
+            float inv2q2 = one / (two * q2);
+            float t0 = (-q1 - sd) * inv2q2;
+            float t1 = (-q1 + sd) * inv2q2;
+            if (t0 > zero && t0 < one) {
+                float v = ((a * t0 + b) * t0 + c) * t0 + d;
+                lo = fminf(lo, v); hi = fmaxf(hi, v);
+            }
+            if (t1 > zero && t1 < one) {
+                float v = ((a * t1 + b) * t1 + c) * t1 + d;
+                lo = fminf(lo, v); hi = fmaxf(hi, v);
+            }
+        }
+    } else if (q1 > ORC_EPS || q1 < -ORC_EPS) {
+        float t = -q0 / q1;
+        if (t > zero && t < one) {
+            float v = ((a * t + b) * t + c) * t + d;
+            lo = fminf(lo, v); hi = fmaxf(hi, v);
+        }
+    }
+    *mn = lo;
+    *mx = hi;
+}
+
+/* Unpadded exact AABB of pixel-space cubics, [min_x, min_y, max_x, max_y] each. */
+void orc_cubic_aabb(const float *cubics_px, int32_t n, float *out)
+{
+    for (int32_t s = 0; s < n; ++s) {
+        const float *c = cubics_px + (size_t)s * 8;
+        orc_axis_extent(c[0], c[2], c[4], c[6], &out[4 * s + 0], &out[4 * s + 2]);
+        orc_axis_extent(c[1], c[3], c[5], c[7], &out[4 * s + 1], &out[4 * s + 3]);
+    }
+}
+
+/* cubic_splatting.py:546-747 (one iteration of the per-segment thread). */
+void orc_project_cubics(const float *cubics_norm, const float *stroke_widths,
+                        const float *support_radii, int32_t nseg, int32_t img_h,
+                        int32_t img_w, int32_t block_x, int32_t block_y, float aabb_pad,
+                        int32_t aniso, float *cubics_px, int32_t *tile_ranges,
+                        int32_t *num_tiles_hit)
+{
+    const float half_w = 0.5f * (float)img_w;
+    const float half_h = 0.5f * (float)img_h;
+    const int32_t tbx = (img_w + block_x - 1) / block_x;
+    const int32_t tby = (img_h + block_y - 1) / block_y;
+    const float bxf = (float)block_x, byf = (float)block_y;
+    for (int32_t s = 0; s < nseg; ++s) {
+        const float *c = cubics_norm + (size_t)s * 8;
+        float px[4], py[4];
+        for (int k = 0; k < 4; ++k) {
+            px[k] = c[2 * k] * half_w + half_w;
+            py[k] = c[2 * k + 1] * half_h + half_h;
+            cubics_px[(size_t)s * 8 + 2 * k] = px[k];
+            cubics_px[(size_t)s * 8 + 2 * k + 1] = py[k];
+        }
+        float min_x, max_x, min_y, max_y;
+        orc_axis_extent(px[0], px[1], px[2], px[3], &min_x, &max_x);
+        orc_axis_extent(py[0], py[1], py[2], py[3], &min_y, &max_y);
+        float half_sw = fmaxf(0.0f, stroke_widths[s]) * 0.5f;
+        float support = fmaxf(0.0f, support_radii[s]);
+        if (aniso) {
+            float cx = px[3] - px[0], cy = py[3] - py[0];
+            float chord2 = cx * cx + cy * cy;
+            float inv_chord = 1.0f / sqrtf(fmaxf(chord2, ORC_EPS));
+            float nx = fmaxf((float)0.20, fabsf(cy) * inv_chord);
+            float ny = fmaxf((float)0.20, fabsf(cx) * inv_chord);
+            float radial = half_sw + support;
+            float pad_x = aabb_pad + radial * nx;
+            float pad_y = aabb_pad + radial * ny;
+            min_x = min_x - pad_x; max_x = max_x + pad_x;
+            min_y = min_y - pad_y; max_y = max_y + pad_y;
+        } else {
+            float pad_i = fmaxf(aabb_pad, support);
+            min_x = min_x - half_sw - pad_i;
+            min_y = min_y - half_sw - pad_i;
+            max_x = max_x + half_sw + pad_i;
+            max_y = max_y + half_sw + pad_i;
+        }
+        int32_t tx0 = orc_clampi(orc_f2i(min_x / bxf), 0, tbx);
+        int32_t ty0 = orc_clampi(orc_f2i(min_y / byf), 0, tby);
+        int32_t tx1 = orc_clampi(orc_f2i(max_x / bxf + 1.0f), 0, tbx);
+        int32_t ty1 = orc_clampi(orc_f2i(max_y / byf + 1.0f), 0, tby);
+        tile_ranges[s * 4 + 0] = tx0;
+        tile_ranges[s * 4 + 1] = ty0;
+        tile_ranges[s * 4 + 2] = tx1;
+        tile_ranges[s * 4 + 3] = ty1;
+        int32_t area = (tx1 - tx0) * (ty1 - ty0);
+        num_tiles_hit[s] = area > 0 ? area : 0;
+    }
+}
+
+/* torch.linspace(0, 1, S) in fp32: the first half counts up from 0, the second
+ * half counts down from 1 (symmetric formula used by ATen's range kernels). */
+void orc_linspace01(int32_t S, float *t)
+{
+    if (S == 1) { t[0] = 0.0f; return; }
+    float step = (1.0f - 0.0f) / (float)(S - 1);
+    int32_t half = S / 2;
+    for (int32_t i = 0; i < S; ++i)
+        t[i] = i < half ? 0.0f + step * (float)i : 1.0f - step * (float)(S - i - 1);
+}
+
+/* cubic_splatting.py:1709-1719: pts = sum_k P_k b_k(t), edges = consecutive
+ * point pairs; the sum over k runs in order 0..3. */
+void orc_flatten(const float *cubics_px, int32_t nseg, int32_t S, float *edges)
+{
+    float t[1024];
+    float b[4][1024];
+    orc_linspace01(S, t);
+    for (int32_t i = 0; i < S; ++i) {
+        float omt = 1.0f - t[i];
+        b[0][i] = omt * omt * omt;
+        b[1][i] = 3.0f * omt * omt * t[i];
+        b[2][i] = 3.0f * omt * t[i] * t[i];
+        b[3][i] = t[i] * t[i] * t[i];
+    }
+    for (int32_t s = 0; s < nseg; ++s) {
+        const float *c = cubics_px + (size_t)s * 8;
+        float prevx = 0.0f, prevy = 0.0f;
+        for (int32_t i = 0; i < S; ++i) {
+            float x = c[0] * b[0][i];
+            x = x + c[2] * b[1][i];
+            x = x + c[4] * b[2][i];
+            x = x + c[6] * b[3][i];
+            float y = c[1] * b[0][i];
+            y = y + c[3] * b[1][i];
+            y = y + c[5] * b[2][i];
+            y = y + c[7] * b[3][i];
+            if (i > 0) {
+                float *e = edges + ((size_t)s * (S - 1) + (i - 1)) * 4;
+                e[0] = prevx; e[1] = prevy; e[2] = x; e[3] = y;
+            }
+            prevx = x; prevy = y;
+        }
+    }
+}
+
+/* Per-edge quantities every raster kernel needs (cubic_splatting.py:1084-1089):
+ * direction v = p1 - p0, |v|^2 (unfused), and u = v / max(|v|^2, eps) as a
+ * multiply by the correctly rounded reciprocal. */
+typedef struct { float x0, y0, y1, vx, vy, ux, uy; } orc_edge_t;
+
+static inline void orc_make_edge(const float *e, orc_edge_t *r)
+{
+    r->x0 = e[0]; r->y0 = e[1]; r->y1 = e[3];
+    r->vx = e[2] - e[0];
+    r->vy = e[3] - e[1];
+    float vv = r->vx * r->vx + r->vy * r->vy;
+    float ivv = 1.0f / fmaxf(vv, ORC_EPS);
+    r->ux = r->vx * ivv;
+    r->uy = r->vy * ivv;
+}
+
+typedef struct {
+    float min_d2;
+    int32_t best;       /* first edge (in edge order) with the strict minimum */
+    float best_proj, best_dx, best_dy;
+    int32_t parity, winding;
+} orc_geom_t;
+
+/* Distance from (px,py) to every edge of one primitive plus the crossing
+ * count of the +x ray (cubic_splatting.py:1095-1134 / 1458-1501). */
+static void orc_geom(const float *edges, int32_t e0, int32_t e1, float px, float py,
+                     int want_cross, orc_geom_t *g)
+{
+    g->min_d2 = 1e30f; g->best = -1;
+    g->best_proj = 0.0f; g->best_dx = 0.0f; g->best_dy = 0.0f;
+    g->parity = 0; g->winding = 0;
+    for (int32_t e = e0; e < e1; ++e) {
+        orc_edge_t E;
+        orc_make_edge(edges + (size_t)e * 4, &E);
+        float wx = px - E.x0, wy = py - E.y0;
+        float proj = fmaf(wx, E.ux, wy * E.uy);
+        proj = fminf(fmaxf(proj, 0.0f), 1.0f);
+        float dx = fmaf(proj, E.vx, -wx);
+        float dy = fmaf(proj, E.vy, -wy);
+        float d2 = fmaf(dx, dx, dy * dy);
+        if (d2 < g->min_d2) {
+            g->min_d2 = d2; g->best = e; g->best_proj = proj;
+            g->best_dx = dx; g->best_dy = dy;
+        }
+        if (want_cross) {
+            int below0 = E.y0 <= py, below1 = E.y1 <= py;
+            if (below0 != below1) {
+                float cr = fmaf(wy, E.vx, -(wx * E.vy));
+                int hit = below0 ? (cr > 0.0f) : (cr < 0.0f);
+                if (hit) {
+                    g->parity ^= 1;
+                    g->winding += below0 ? 1 : -1;
+                }
+            }
+        }
+    }
+}
+
+typedef struct {
+    const float *edges;          /* [E,2,2] */
+    const int32_t *prim_edge_offsets; /* [P+1] */
+    const float *colors;         /* [P,3] */
+    const float *opacities;      /* [P] */
+    const float *inv_sigma2s;    /* [P] */
+    const int32_t *fill_rules;   /* [P] (fill) */
+    const float *stroke_widths;  /* [P] (stroke) */
+    const int32_t *prim_ids_sorted; /* [I] */
+    const int32_t *tile_bins;    /* [T,2] */
+    const float *background;     /* [3] */
+    int32_t img_h, img_w, block_x, block_y;
+    int32_t mode;                /* 0 = closed fill, 1 = open stroke */
+} orc_scene_t;
+
+/* Coverage of one (pixel, primitive) pair: returns cov and fills the terms the
+ * backward needs.  Fill: cubic_splatting.py:1138-1170; stroke:
+ * cubic_polyline_splatting.py:219-226. */
+typedef struct { float cov, dist, inv_sigma, inv_sigma2, sgn, edge_d; int32_t inside; } orc_cov_t;
+
+static inline void orc_coverage(const orc_scene_t *sc, int32_t pid, const orc_geom_t *g,
+                                orc_cov_t *c)
+{
+    float dist = sqrtf(fmaxf(g->min_d2, 0.0f));
+    c->dist = dist;
+    c->inv_sigma2 = fmaxf(sc->inv_sigma2s[pid], ORC_EPS);
+    if (sc->mode == 0) {
+        int32_t rule = sc->fill_rules[pid];
+        c->inside = rule == 0 ? (g->parity != 0) : (g->winding != 0);
+        c->inv_sigma = sqrtf(c->inv_sigma2);
+        c->sgn = c->inside ? -1.0f : 1.0f;
+        float logit = dist * c->inv_sigma * 2.0f;
+        if (c->inside) logit = -logit;
+        logit = fmaxf(-60.0f, fminf(60.0f, logit));
+        c->cov = 1.0f / (1.0f + cs_expf(logit));
+        c->edge_d = 0.0f;
+    } else {
+        float half_sw = fmaxf(0.0f, sc->stroke_widths[pid]) * 0.5f;
+        float edge_d = fmaxf(0.0f, dist - half_sw);
+        float sigma = 0.5f * edge_d * edge_d * c->inv_sigma2;
+        c->cov = cs_expf(-sigma);
+        c->edge_d = edge_d;
+        c->inside = 0; c->sgn = 1.0f; c->inv_sigma = 0.0f;
+    }
+}
+
+/* Front-to-back compositing per pixel over its tile's sorted list
+ * (cubic_splatting.py:1036-1192), for pixel rows [row0, row1). */
+void orc_raster_forward(const orc_scene_t *sc, int32_t row0, int32_t row1, float *out_img,
+                        float *final_T, int32_t *final_idx)
+{
+    const int32_t W = sc->img_w;
+    const int32_t tbx = (W + sc->block_x - 1) / sc->block_x;
+    for (int32_t i = row0; i < row1; ++i) {
+        for (int32_t j = 0; j < W; ++j) {
+            int32_t tile = (i / sc->block_y) * tbx + (j / sc->block_x);
+            int32_t r0 = sc->tile_bins[2 * tile], r1 = sc->tile_bins[2 * tile + 1];
+            float px = (float)j + 0.5f, py = (float)i + 0.5f;
+            float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
+            int32_t cur = 0;
+            for (int32_t gidx = r0; gidx < r1; ++gidx) {
+                int32_t pid = sc->prim_ids_sorted[gidx];
+                orc_geom_t g;
+                orc_geom(sc->edges, sc->prim_edge_offsets[pid], sc->prim_edge_offsets[pid + 1],
+                         px, py, sc->mode == 0, &g);
+                orc_cov_t c;
+                orc_coverage(sc, pid, &g, &c);
+                float alpha = fminf(ORC_ALPHA_CAP, sc->opacities[pid] * c.cov);
+                if (alpha < ORC_ALPHA_MIN) continue;
+                float nT = T * (1.0f - alpha);
+                float vis = alpha * T;
+                const float *col = sc->colors + (size_t)pid * 3;
+                C0 = fmaf(col[0], vis, C0);
+                C1 = fmaf(col[1], vis, C1);
+                C2 = fmaf(col[2], vis, C2);
+                T = nT;
+                cur = gidx;
+                if (nT <= ORC_T_STOP) break;
+            }
+            size_t pix = (size_t)i * W + j;
+            final_T[pix] = T;
+            final_idx[pix] = cur;
+            out_img[pix * 3 + 0] = fmaf(T, sc->background[0], C0);
+            out_img[pix * 3 + 1] = fmaf(T, sc->background[1], C1);
+            out_img[pix * 3 + 2] = fmaf(T, sc->background[2], C2);
+        }
+    }
+}
+
+/* Reverse traversal recomputing transmittance (cubic_splatting.py:1339-1649,
+ * cubic_polyline_splatting.py:393-658) for pixel rows [row0, row1).  Sums go
+ * to double accumulators. */
+void orc_raster_backward(const orc_scene_t *sc, int32_t row0, int32_t row1,
+                         const float *final_T, const int32_t *final_idx, const float *v_out,
+                         double *v_edges, double *v_colors, double *v_opacity,
+                         double *v_inv_sigma2, double *v_stroke)
+{
+    const int32_t W = sc->img_w;
+    const int32_t tbx = (W + sc->block_x - 1) / sc->block_x;
+    for (int32_t i = row0; i < row1; ++i) {
+        for (int32_t j = 0; j < W; ++j) {
+            int32_t tile = (i / sc->block_y) * tbx + (j / sc->block_x);
+            int32_t r0 = sc->tile_bins[2 * tile], r1 = sc->tile_bins[2 * tile + 1];
+            float px = (float)j + 0.5f, py = (float)i + 0.5f;
+            size_t pix = (size_t)i * W + j;
+            float T = final_T[pix];
+            const float T_final = T;
+            const int32_t fidx = final_idx[pix];
+            const float v0 = v_out[pix * 3], v1 = v_out[pix * 3 + 1], v2 = v_out[pix * 3 + 2];
+            const float *bg = sc->background;
+            const float bg_dot = fmaf(bg[2], v2, fmaf(bg[1], v1, bg[0] * v0));
+            float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
+            for (int32_t gidx = r1 - 1; gidx >= r0; --gidx) {
+                if (gidx > fidx) continue;
+                int32_t pid = sc->prim_ids_sorted[gidx];
+                orc_geom_t g;
+                orc_geom(sc->edges, sc->prim_edge_offsets[pid], sc->prim_edge_offsets[pid + 1],
+                         px, py, sc->mode == 0, &g);
+                orc_cov_t c;
+                orc_coverage(sc, pid, &g, &c);
+                const float op = sc->opacities[pid];
+                float alpha = fminf(ORC_ALPHA_CAP, op * c.cov);
+                if (alpha < ORC_ALPHA_MIN) continue;
+                const float *col = sc->colors + (size_t)pid * 3;
+                float ra = 1.0f / (1.0f - alpha);
+                T = T * ra;
+                float fac = alpha * T;
+                v_colors[pid * 3 + 0] += (double)(fac * v0);
+                v_colors[pid * 3 + 1] += (double)(fac * v1);
+                v_colors[pid * 3 + 2] += (double)(fac * v2);
+                float va = fmaf(col[0], T, -(b0 * ra)) * v0;
+                va = fmaf(fmaf(col[1], T, -(b1 * ra)), v1, va);
+                va = fmaf(fmaf(col[2], T, -(b2 * ra)), v2, va);
+                va = fmaf(T_final * ra, -bg_dot, va);
+                b0 = fmaf(col[0], fac, b0);
+                b1 = fmaf(col[1], fac, b1);
+                b2 = fmaf(col[2], fac, b2);
+                if (!(alpha < ORC_ALPHA_CAP)) continue;
+                v_opacity[pid] += (double)(c.cov * va);
+                float gx = 0.0f, gy = 0.0f;
+                int geom = 0;
+                if (sc->mode == 0) {
+                    float v_cov = op * va;
+                    float v_logit = -v_cov * c.cov * (1.0f - c.cov);
+                    float v_is = v_logit * c.sgn * c.dist * 2.0f;
+                    v_inv_sigma2[pid] += (double)(v_is * 0.5f / fmaxf(c.inv_sigma, ORC_EPS));
+                    if (c.dist > ORC_EPS && g.best >= 0) {
+                        float v_dist = v_logit * c.sgn * c.inv_sigma * 2.0f;
+                        gx = v_dist * g.best_dx / c.dist;
+                        gy = v_dist * g.best_dy / c.dist;
+                        geom = 1;
+                    }
+                } else {
+                    float v_sigma = -op * c.cov * va;
+                    v_inv_sigma2[pid] += (double)(0.5f * c.edge_d * c.edge_d * v_sigma);
+                    if (c.edge_d > 0.0f) {
+                        float v_e = v_sigma * c.edge_d * c.inv_sigma2;
+                        v_stroke[pid] += (double)(-0.5f * v_e);
+                        if (c.dist > ORC_EPS && g.best >= 0) {
+                            gx = v_e * g.best_dx / c.dist;
+                            gy = v_e * g.best_dy / c.dist;
+                            geom = 1;
+                        }
+                    }
+                }
+                if (geom) {
+                    double *ve = v_edges + (size_t)g.best * 4;
+                    ve[0] += (double)((1.0f - g.best_proj) * gx);
+                    ve[1] += (double)((1.0f - g.best_proj) * gy);
+                    ve[2] += (double)(g.best_proj * gx);
+                    ve[3] += (double)(g.best_proj * gy);
+                }
+            }
+        }
+    }
+}
+
+/* cubic_splatting.py:2308-2396: v_P_k = sum_e gs_e b_k(t_e) + ge_e b_k(t_{e+1})
+ * with t_e = e * (1/(S-1)) in fp32 (note: not the linspace values). */
+void orc_accumulate_edge_grads(const double *v_edges, int32_t nseg, int32_t eps_per_seg,
+                               double *v_cubics)
+{
+    const float inv_e = 1.0f / (float)eps_per_seg;
+    for (int32_t s = 0; s < nseg; ++s) {
+        double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int32_t e = 0; e < eps_per_seg; ++e) {
+            float t0 = (float)e * inv_e, t1 = (float)(e + 1) * inv_e;
+            float o0 = 1.0f - t0, o1 = 1.0f - t1;
+            float o0s = o0 * o0, o1s = o1 * o1, t0s = t0 * t0, t1s = t1 * t1;
+            float b0[4] = {o0s * o0, 3.0f * o0s * t0, 3.0f * o0 * t0s, t0s * t0};
+            float b1[4] = {o1s * o1, 3.0f * o1s * t1, 3.0f * o1 * t1s, t1s * t1};
+            const double *g = v_edges + ((size_t)s * eps_per_seg + e) * 4;
+            for (int k = 0; k < 4; ++k) {
+                acc[2 * k] += g[0] * (double)b0[k] + g[2] * (double)b1[k];
+                acc[2 * k + 1] += g[1] * (double)b0[k] + g[3] * (double)b1[k];
+            }
+        }
+        memcpy(v_cubics + (size_t)s * 8, acc, sizeof(acc));
+    }
+}

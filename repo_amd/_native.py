@@ -1,0 +1,105 @@
+"""ctypes binding of libcubicsplat_hip.so (declared in include/cubicsplat_hip.h).
+
+There is no fallback: if the library is missing or a call fails, this module
+raises.  torch is imported first so that the library binds to the HIP runtime
+torch has already loaded (both use the soname libamdhip64.so.7).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcubicsplat_hip.so")
+
+CS_OK, CS_ERR_ARGS, CS_ERR_HIP = 0, 1, 2
+EDGE_RECORD_FLOATS = 8   # 32-byte edge record
+PRIM_RECORD_FLOATS = 16  # 64-byte primitive record
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+_SIGNATURES = {
+    "cs_scan_temp_elems": (_SZ, [_I32]),
+    "cs_radix_counts_elems": (_SZ, [_I32]),
+    "cs_scan_exclusive_u32": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P]),
+    "cs_radix_sort_pairs_u32": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _P, _P, _P]),
+    "cs_project_cubics_2d_forward": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F,
+                                                    _I32, _P, _P, _P, _P]),
+    "cs_primitive_tile_ranges": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _P, _P]),
+    "cs_map_cubic_to_intersects": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _P]),
+    "cs_get_tile_bin_edges": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
+    "cs_isect_edge_ranges": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _P]),
+    "cs_bin_prepare": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
+                                      _I32, _I32, _I32, _F, _I32, _I32, _P, _P, _P, _P, _P, _P,
+                                      _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cs_bin_finish": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
+                                     _P, _P, _P, _P, _P]),
+    "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
+                                            _P, _P]),
+    "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P,
+                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cs_accumulate_edge_grads": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P]),
+    "cs_aa_width_grads": (ctypes.c_int, [_P, _P, _I32, _P, _P]),
+    "cs_mse_partials_elems": (_SZ, [_I64]),
+    "cs_ssim_partials_elems": (_SZ, [_I32, _I32, _I32]),
+    "cs_mse_forward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
+    "cs_mse_backward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
+    "cs_ssim": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _F, _F, _P, _P, _P, _P, _P]),
+    "cs_ssim_backward": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m repo_amd.build` "
+                "(or __graft_entry__.build()) first")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGNATURES)
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def check(rc: int, what: str) -> None:
+    if rc == CS_OK:
+        return
+    kind = "invalid arguments" if rc == CS_ERR_ARGS else "HIP launch failure"
+    raise RuntimeError(f"{what}: {kind} (status {rc})")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def require_gpu(t: torch.Tensor, name: str) -> None:
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a CUDA (ROCm) tensor")

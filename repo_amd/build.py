@@ -1,0 +1,51 @@
+"""Builds libcubicsplat_hip.so (gfx950) in-tree with hipcc.
+
+Flags that are part of the numerical contract:
+  -ffp-contract=off     no implicit FMA contraction; the kernels write the
+                        fused multiply-adds they want explicitly (the CPU
+                        oracle restates the same expressions).
+  -fno-fast-math        IEEE division and square root.
+  -munsafe-fp-atomics   hardware fp32 global atomics instead of CAS loops.
+  -packed-fp32-ops off  no v_pk_*_f32 generation.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libcubicsplat_hip.so")
+SOURCES = ["binning.hip", "raster.hip", "metric.hip"]
+ARCH = os.environ.get("CS_OFFLOAD_ARCH", "gfx950")
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-mcode-object-version=5",
+    "-ffp-contract=off", "-fno-fast-math", "-munsafe-fp-atomics",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "bin", "hipcc"), "hipcc"):
+        if os.path.isabs(cand) and os.path.exists(cand):
+            return cand
+    return "hipcc"
+
+
+def build(verbose: bool = False) -> str:
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(HERE, "..", "include"), "-o", tmp, *srcs]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.check_call(cmd)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,795 @@
+// Tile binning for the cubic splat path on MI355X (gfx950).
+//
+// Pipeline (one forward):
+//   k_project_flatten  thread per cubic segment: normalized -> pixel space,
+//                      exact AABB -> padded 16x16 tile range, uniform
+//                      Bernstein flattening into 32-byte edge records and a
+//                      per-segment vertex bounding box.
+//   k_prim_prep        thread per primitive: union of its segments' tile
+//                      ranges, tile count, depth sort key, raster record.
+//   depth rank         stable LSD radix sort of the 32-bit depth keys.
+//   counts by rank + exclusive scan -> per-primitive output offsets, total I.
+//   k_emit             wave per primitive (in depth-rank order) writes its
+//                      tiles' ids and its primitive id.
+//   tile sort          stable LSD radix sort on the tile id only.
+//   k_tile_bins        [start, end) per tile from the sorted tile ids.
+//
+// Sorting ranks first and then tiles stably yields exactly the order of the
+// reference's single sort of (tile << 32 | depth_key) keys emitted
+// primitive-major with a stable tie order (ties broken by primitive id).
+#include "cs_common.h"
+#include "../../include/cubicsplat_hip.h"
+
+namespace cs {
+
+// ---------------------------------------------------------------- projection
+
+struct SegProj {
+    float px[4], py[4];
+    int32_t tx0, ty0, tx1, ty1;
+};
+
+// One axis of the exact cubic AABB (cubic_splatting.py:606-688), reference op order.
+__device__ __forceinline__ void axis_extent(float p0, float p1, float p2, float p3, float& mn,
+                                            float& mx) {
+    const float a = ((-p0 + 3.0f * p1) - 3.0f * p2) + p3;
+    const float b = (3.0f * p0 - 6.0f * p1) + 3.0f * p2;
+    const float c = -3.0f * p0 + 3.0f * p1;
+    const float d = p0;
+    float lo = fminf(p0, p3), hi = fmaxf(p0, p3);
+    const float q2 = 3.0f * a, q1 = 2.0f * b, q0 = c;
+    if (q2 > kEps || q2 < -kEps) {
+        const float disc = q1 * q1 - 4.0f * q2 * q0;
+        if (disc >= -kEps) {
+            const float sd = __builtin_sqrtf(fmaxf(disc, 0.0f));
+            const float inv2q2 = 1.0f / (2.0f * q2);
+            const float t0 = (-q1 - sd) * inv2q2;
+            const float t1 = (-q1 + sd) * inv2q2;
+            if (t0 > 0.0f && t0 < 1.0f) {
+                const float v = ((a * t0 + b) * t0 + c) * t0 + d;
+                lo = fminf(lo, v);
+                hi = fmaxf(hi, v);
+            }
+            if (t1 > 0.0f && t1 < 1.0f) {
+                const float v = ((a * t1 + b) * t1 + c) * t1 + d;
+                lo = fminf(lo, v);
+                hi = fmaxf(hi, v);
+            }
+        }
+    } else if (q1 > kEps || q1 < -kEps) {
+        const float t = -q0 / q1;
+        if (t > 0.0f && t < 1.0f) {
+            const float v = ((a * t + b) * t + c) * t + d;
+            lo = fminf(lo, v);
+            hi = fmaxf(hi, v);
+        }
+    }
+    mn = lo;
+    mx = hi;
+}
+
+// cubic_splatting.py:588-745 for one segment.
+__device__ __forceinline__ SegProj project_segment(const float* __restrict__ cn, float half_w,
+                                                   float half_h, float half_sw, float support,
+                                                   float aabb_pad, int aniso, int tbx, int tby,
+                                                   float bxf, float byf) {
+    SegProj r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        r.px[k] = cn[2 * k] * half_w + half_w;
+        r.py[k] = cn[2 * k + 1] * half_h + half_h;
+    }
+    float min_x, max_x, min_y, max_y;
+    axis_extent(r.px[0], r.px[1], r.px[2], r.px[3], min_x, max_x);
+    axis_extent(r.py[0], r.py[1], r.py[2], r.py[3], min_y, max_y);
+    if (aniso) {
+        const float cx = r.px[3] - r.px[0], cy = r.py[3] - r.py[0];
+        const float chord2 = cx * cx + cy * cy;
+        const float inv_chord = 1.0f / __builtin_sqrtf(fmaxf(chord2, kEps));
+        const float nx = fmaxf((float)0.20, fabsf(cy) * inv_chord);
+        const float ny = fmaxf((float)0.20, fabsf(cx) * inv_chord);
+        const float radial = half_sw + support;
+        const float pad_x = aabb_pad + radial * nx;
+        const float pad_y = aabb_pad + radial * ny;
+        min_x = min_x - pad_x;
+        max_x = max_x + pad_x;
+        min_y = min_y - pad_y;
+        max_y = max_y + pad_y;
+    } else {
+        const float pad_i = fmaxf(aabb_pad, support);
+        min_x = min_x - half_sw - pad_i;
+        min_y = min_y - half_sw - pad_i;
+        max_x = max_x + half_sw + pad_i;
+        max_y = max_y + half_sw + pad_i;
+    }
+    r.tx0 = clampi(f2i_sat(min_x / bxf), 0, tbx);
+    r.ty0 = clampi(f2i_sat(min_y / byf), 0, tby);
+    r.tx1 = clampi(f2i_sat(max_x / bxf + 1.0f), 0, tbx);
+    r.ty1 = clampi(f2i_sat(max_y / byf + 1.0f), 0, tby);
+    return r;
+}
+
+// Largest p in [0, P-1] with offs[p] <= s (the primitive owning segment s).
+__device__ __forceinline__ int owner_of(const int32_t* __restrict__ offs, int P, int s) {
+    int lo = 0, hi = P - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (offs[mid] <= s) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// torch.linspace(0, 1, S)[i] as ATen's device kernel computes it.
+__device__ __forceinline__ float linspace01(int S, int i) {
+    const float step = 1.0f / (float)(S - 1);
+    return i < (S >> 1) ? 0.0f + step * (float)i : 1.0f - step * (float)(S - i - 1);
+}
+
+__global__ __launch_bounds__(256) void k_project_flatten(
+    const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
+    const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
+    int img_h, int img_w, int block_x, int block_y, float aabb_pad, int aniso, int S,
+    float* __restrict__ cubics_px, int32_t* __restrict__ seg_tile_ranges,
+    float4* __restrict__ seg_bbox, EdgeRec* __restrict__ edges) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    const int p = owner_of(seg_offsets, P, s);
+    const float w = fmaxf(aa_widths[p], kWidthMin);
+    const float support = fmaxf(0.0f, w * 3.0f);
+    const float half_sw = stroke_widths ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
+    const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
+    const SegProj r = project_segment(cubics_norm + (size_t)s * 8, 0.5f * (float)img_w,
+                                      0.5f * (float)img_h, half_sw, support, aabb_pad, aniso, tbx,
+                                      tby, (float)block_x, (float)block_y);
+    float4* cp = reinterpret_cast<float4*>(cubics_px + (size_t)s * 8);
+    cp[0] = make_float4(r.px[0], r.py[0], r.px[1], r.py[1]);
+    cp[1] = make_float4(r.px[2], r.py[2], r.px[3], r.py[3]);
+    reinterpret_cast<int4*>(seg_tile_ranges)[s] = make_int4(r.tx0, r.ty0, r.tx1, r.ty1);
+
+    // Flatten: pts_i = ((P0 b0 + P1 b1) + P2 b2) + P3 b3 at t_i = linspace(0,1,S)[i].
+    float prevx = 0.0f, prevy = 0.0f;
+    float bx0 = __builtin_huge_valf(), by0 = bx0, bx1 = -bx0, by1 = -bx0;
+    EdgeRec* er = edges + (size_t)s * (S - 1);
+    for (int i = 0; i < S; ++i) {
+        const float t = linspace01(S, i);
+        const float omt = 1.0f - t;
+        const float b0 = omt * omt * omt;
+        const float b1 = 3.0f * omt * omt * t;
+        const float b2 = 3.0f * omt * t * t;
+        const float b3 = t * t * t;
+        float x = r.px[0] * b0;
+        x = x + r.px[1] * b1;
+        x = x + r.px[2] * b2;
+        x = x + r.px[3] * b3;
+        float y = r.py[0] * b0;
+        y = y + r.py[1] * b1;
+        y = y + r.py[2] * b2;
+        y = y + r.py[3] * b3;
+        bx0 = fminf(bx0, x); bx1 = fmaxf(bx1, x);
+        by0 = fminf(by0, y); by1 = fmaxf(by1, y);
+        if (i > 0) {
+            const float vx = x - prevx, vy = y - prevy;
+            const float vv = vx * vx + vy * vy;
+            const float ivv = 1.0f / fmaxf(vv, kEps);
+            float4* o = reinterpret_cast<float4*>(er + (i - 1));
+            o[0] = make_float4(prevx, prevy, x, y);
+            o[1] = make_float4(vx, vy, vx * ivv, vy * ivv);
+        }
+        prevx = x;
+        prevy = y;
+    }
+    seg_bbox[s] = make_float4(bx0, by0, bx1, by1);
+}
+
+// Conservative distance beyond which a pixel's coverage of this primitive is
+// decided without its exact distance: fill -> alpha < 1/255 outside, coverage
+// exactly 1.0f inside (2 d inv_sigma >= 16.64 makes 1 + exp(-.) round to 1);
+// stroke -> alpha < 1/255.  Margins absorb fp32 rounding of the cull test.
+__device__ __forceinline__ float cull_distance(int mode, float opacity, float inv_sigma,
+                                               float half_sw) {
+    if (!(opacity <= 3.0e38f)) return __builtin_huge_valf();
+    const float lo = __logf(fmaxf(255.0f * opacity, 1.0f));
+    if (mode == 0) return fmaxf(9.5f, 0.5f * (lo + 1.0f)) / inv_sigma + 0.25f;
+    return half_sw + __builtin_sqrtf(2.0f * lo + 1.0f) / inv_sigma + 0.25f;
+}
+
+__global__ __launch_bounds__(256) void k_prim_prep(
+    const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
+    const int32_t* __restrict__ seg_tile_ranges, const float4* __restrict__ seg_bbox,
+    const float* __restrict__ colors, const float* __restrict__ opacities,
+    const float* __restrict__ depths, const int32_t* __restrict__ fill_rules,
+    const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
+    int tbx, int tby, int mode, int32_t* __restrict__ status,
+    int32_t* __restrict__ prim_tile_ranges, uint32_t* __restrict__ counts,
+    float* __restrict__ inv_sigma2s, uint32_t* __restrict__ keys, int32_t* __restrict__ vals,
+    PrimRec* __restrict__ recs) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= P) return;
+    int s0 = seg_offsets[p], s1 = seg_offsets[p + 1];
+    // Invalid CSR offsets are reported through status[1] and clamped so that
+    // no kernel reads outside the segment arrays.
+    if (s0 < 0 || s1 < s0 || s1 > nseg) {
+        atomicOr(status + 1, 1);
+        s0 = clampi(s0, 0, nseg);
+        s1 = clampi(s1, s0, nseg);
+    }
+    // cubic_splatting.py:2103-2135
+    int4 tr = make_int4(0, 0, 0, 0);
+    uint32_t area = 0;
+    if (s1 > s0) {
+        int mnx = tbx, mny = tby, mxx = 0, mxy = 0;
+        for (int s = s0; s < s1; ++s) {
+            const int4 r = reinterpret_cast<const int4*>(seg_tile_ranges)[s];
+            mnx = min(mnx, r.x); mny = min(mny, r.y);
+            mxx = max(mxx, r.z); mxy = max(mxy, r.w);
+        }
+        tr = make_int4(mnx, mny, mxx, mxy);
+        area = (uint32_t)(max(0, mxx - mnx) * max(0, mxy - mny));
+    }
+    reinterpret_cast<int4*>(prim_tile_ranges)[p] = tr;
+    counts[p] = area;
+
+    // cubic_splatting.py:2820-2821 (widths clamp, inv_sigma2).
+    const float w = fmaxf(aa_widths[p], kWidthMin);
+    const float is2 = 1.0f / fmaxf(w * w, kEps);
+    inv_sigma2s[p] = is2;
+    const float is2c = fmaxf(is2, kEps);
+    const float isig = __builtin_sqrtf(is2c);
+
+    // cubic_splatting.py:801-805: float order as unsigned order.
+    const int32_t bits = __builtin_bit_cast(int32_t, depths[p]);
+    keys[p] = (uint32_t)(bits ^ ((bits >> 31) | (int32_t)0x80000000));
+    vals[p] = p;
+
+    PrimRec rec;
+    rec.r = colors[3 * p];
+    rec.g = colors[3 * p + 1];
+    rec.b = colors[3 * p + 2];
+    rec.opacity = opacities[p];
+    rec.inv_sigma2 = is2c;
+    rec.inv_sigma = isig;
+    rec.half_sw = (mode == 1 && stroke_widths) ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
+    rec.cull_d = cull_distance(mode, rec.opacity, isig, rec.half_sw);
+    rec.s0 = s0;
+    rec.s1 = s1;
+    rec.rule = fill_rules ? fill_rules[p] : 1;
+    int closed = 1;
+    float bx0 = __builtin_huge_valf(), by0 = bx0, bx1 = -bx0, by1 = -bx0;
+    for (int s = s0; s < s1; ++s) {
+        const int nx = (s + 1 < s1) ? s + 1 : s0;
+        const float* a = cubics_norm + (size_t)s * 8;
+        const float* b = cubics_norm + (size_t)nx * 8;
+        closed &= (a[6] == b[0]) & (a[7] == b[1]);
+        const float4 bb = seg_bbox[s];
+        bx0 = fminf(bx0, bb.x); by0 = fminf(by0, bb.y);
+        bx1 = fmaxf(bx1, bb.z); by1 = fmaxf(by1, bb.w);
+    }
+    rec.closed = closed;
+    rec.bx0 = bx0; rec.by0 = by0; rec.bx1 = bx1; rec.by1 = by1;
+    recs[p] = rec;
+}
+
+// status = [intersection total, bad-offsets flag, offs[0], offs[P]].
+__global__ void k_status_init(const int32_t* __restrict__ seg_offsets, int P,
+                              int32_t* __restrict__ status) {
+    status[0] = 0;
+    status[1] = 0;
+    status[2] = seg_offsets[0];
+    status[3] = seg_offsets[P];
+}
+
+// ------------------------------------------------------------ exclusive scan
+
+constexpr int kScanThreads = 1024;
+constexpr int kScanItems = 4;
+constexpr int kScanChunk = kScanThreads * kScanItems;
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x, int lane) {
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, kWave);
+        if (lane >= off) x += y;
+    }
+    return x;
+}
+
+// Exclusive scan of one value per thread over a 1024-thread block; returns the
+// block total in *total.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* sh, uint32_t* total) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const uint32_t incl = wave_incl_scan(v, lane);
+    if (lane == kWave - 1) sh[w] = incl;
+    __syncthreads();
+    if (w == 0) {
+        const uint32_t x = lane < (kScanThreads / kWave) ? sh[lane] : 0u;
+        const uint32_t xi = wave_incl_scan(x, lane);
+        if (lane < (kScanThreads / kWave)) sh[lane] = xi - x;
+        if (lane == kWave - 1) sh[kScanThreads / kWave] = xi;
+    }
+    __syncthreads();
+    const uint32_t r = sh[w] + incl - v;
+    *total = sh[kScanThreads / kWave];
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(kScanThreads) void k_scan_block_sums(const uint32_t* __restrict__ in,
+                                                                 int n,
+                                                                 uint32_t* __restrict__ sums) {
+    __shared__ uint32_t sh[kScanThreads / kWave + 1];
+    const size_t base = (size_t)blockIdx.x * kScanChunk + (size_t)threadIdx.x * kScanItems;
+    uint32_t acc = 0;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k)
+        if (base + k < (size_t)n) acc += in[base + k];
+    uint32_t total;
+    block_excl_scan(acc, sh, &total);
+    if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+// Single block: exclusive scan of sums[0..nb) in place (chunks with a carry).
+__global__ __launch_bounds__(kScanThreads) void k_scan_partials(uint32_t* __restrict__ sums,
+                                                               int nb) {
+    __shared__ uint32_t sh[kScanThreads / kWave + 1];
+    uint32_t carry = 0;
+    for (int c0 = 0; c0 < nb; c0 += kScanThreads) {
+        const int i = c0 + threadIdx.x;
+        const uint32_t v = i < nb ? sums[i] : 0u;
+        uint32_t total;
+        const uint32_t ex = block_excl_scan(v, sh, &total);
+        if (i < nb) sums[i] = carry + ex;
+        carry += total;
+    }
+}
+
+// Exclusive scan of in[0..n) into out; block b adds the scanned block sum.
+// The last block writes the grand total to *total_out (if given).
+__global__ __launch_bounds__(kScanThreads) void k_scan_apply(const uint32_t* __restrict__ in,
+                                                            uint32_t* __restrict__ out, int n,
+                                                            const uint32_t* __restrict__ sums,
+                                                            int32_t* __restrict__ total_out) {
+    __shared__ uint32_t sh[kScanThreads / kWave + 1];
+    const size_t base = (size_t)blockIdx.x * kScanChunk + (size_t)threadIdx.x * kScanItems;
+    uint32_t v[kScanItems];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        v[k] = (base + k < (size_t)n) ? in[base + k] : 0u;
+        acc += v[k];
+    }
+    uint32_t total;
+    uint32_t ex = block_excl_scan(acc, sh, &total);
+    ex += sums ? sums[blockIdx.x] : 0u;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        if (base + k < (size_t)n) out[base + k] = ex;
+        ex += v[k];
+    }
+    if (total_out && blockIdx.x == gridDim.x - 1 && threadIdx.x == kScanThreads - 1)
+        *total_out = (int32_t)ex;
+}
+
+// -------------------------------------------------------- stable radix sort
+
+constexpr int kRsThreads = 256;
+constexpr int kRsItems = 16;
+constexpr int kRsTile = kRsThreads * kRsItems;
+
+__global__ __launch_bounds__(kRsThreads) void k_rs_hist(const uint32_t* __restrict__ keys, int n,
+                                                       int shift, int nblk,
+                                                       uint32_t* __restrict__ counts) {
+    __shared__ uint32_t h[256];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    const int base = blockIdx.x * kRsTile;
+#pragma unroll 4
+    for (int k = 0; k < kRsItems; ++k) {
+        const int idx = base + k * kRsThreads + threadIdx.x;
+        if (idx < n) atomicAdd(&h[(keys[idx] >> shift) & 0xFFu], 1u);
+    }
+    __syncthreads();
+    counts[(size_t)threadIdx.x * nblk + blockIdx.x] = h[threadIdx.x];
+}
+
+// Stable scatter of one 8-bit digit.  Items are ranked in rounds of 256 in
+// input order: within a wave by matching digits with 8 ballots, across the
+// block's waves through LDS counters, across rounds by running per-digit bases.
+__global__ __launch_bounds__(kRsThreads) void k_rs_scatter(
+    const uint32_t* __restrict__ kin, const int32_t* __restrict__ vin,
+    uint32_t* __restrict__ kout, int32_t* __restrict__ vout, int n, int shift, int nblk,
+    const uint32_t* __restrict__ offsets) {
+    __shared__ uint32_t dbase[256];
+    __shared__ uint32_t wc[kRsThreads / kWave][256];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    dbase[t] = offsets[(size_t)t * nblk + blockIdx.x];
+    const uint64_t below = __lanemask_lt();
+    const int base = blockIdx.x * kRsTile;
+    for (int k = 0; k < kRsItems; ++k) {
+#pragma unroll
+        for (int q = 0; q < kRsThreads / kWave; ++q) wc[q][t] = 0;
+        __syncthreads();
+        const int idx = base + k * kRsThreads + t;
+        const bool valid = idx < n;
+        const uint32_t key = valid ? kin[idx] : 0u;
+        const int32_t val = valid ? vin[idx] : 0;
+        const uint32_t d = (key >> shift) & 0xFFu;
+        uint64_t peers = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const bool bit = (d >> b) & 1u;
+            const uint64_t m = __ballot(bit);
+            peers &= bit ? m : ~m;
+        }
+        const uint32_t rank = (uint32_t)__popcll(peers & below);
+        if (valid && rank == 0) wc[w][d] = (uint32_t)__popcll(peers);
+        __syncthreads();
+        if (valid) {
+            uint32_t off = dbase[d] + rank;
+            for (int q = 0; q < w; ++q) off += wc[q][d];
+            kout[off] = key;
+            vout[off] = val;
+        }
+        __syncthreads();
+        uint32_t add = 0;
+#pragma unroll
+        for (int q = 0; q < kRsThreads / kWave; ++q) add += wc[q][t];
+        dbase[t] += add;
+    }
+}
+
+// ------------------------------------------------------------ emit and bins
+
+__global__ __launch_bounds__(256) void k_rank_counts(const int32_t* __restrict__ order,
+                                                    const uint32_t* __restrict__ counts, int P,
+                                                    uint32_t* __restrict__ out) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < P) out[r] = counts[order[r]];
+}
+
+__global__ __launch_bounds__(256) void k_emit(const int32_t* __restrict__ order,
+                                             const int32_t* __restrict__ prim_tile_ranges,
+                                             const uint32_t* __restrict__ rank_offsets, int P,
+                                             int tbx, uint32_t* __restrict__ tile_keys,
+                                             int32_t* __restrict__ vals) {
+    const int lane = threadIdx.x & 63;
+    const int waves = (gridDim.x * blockDim.x) >> 6;
+    for (int r = (blockIdx.x * blockDim.x + threadIdx.x) >> 6; r < P; r += waves) {
+        const int p = order[r];
+        const int4 tr = reinterpret_cast<const int4*>(prim_tile_ranges)[p];
+        const int w = tr.z - tr.x, h = tr.w - tr.y;
+        if (w <= 0 || h <= 0) continue;
+        const int area = w * h;
+        const uint32_t base = rank_offsets[r];
+        for (int k = lane; k < area; k += kWave) {
+            const int row = k / w;
+            const int col = k - row * w;
+            tile_keys[base + k] = (uint32_t)((tr.y + row) * tbx + tr.x + col);
+            vals[base + k] = p;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ a, int n, int32_t v) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) a[i] = v;
+}
+
+// tile_bins.py:10-43 on 32-bit tile ids.
+__global__ __launch_bounds__(256) void k_tile_bins(const uint32_t* __restrict__ tiles, int n,
+                                                  int32_t* __restrict__ bins) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n) return;
+    const uint32_t cur = tiles[idx];
+    if (idx == 0) bins[2 * cur] = 0;
+    if (idx == n - 1) bins[2 * cur + 1] = n;
+    if (idx > 0) {
+        const uint32_t prev = tiles[idx - 1];
+        if (prev != cur) {
+            bins[2 * prev + 1] = idx;
+            bins[2 * cur] = idx;
+        }
+    }
+}
+
+// tile_bins.py:10-43 on the reference's int64 (tile << 32 | depth) keys.
+__global__ __launch_bounds__(256) void k_tile_bins_i64(const int64_t* __restrict__ keys, int n,
+                                                      int32_t* __restrict__ bins) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n) return;
+    const int32_t cur = (int32_t)(keys[idx] >> 32);
+    if (idx == 0) bins[2 * cur] = 0;
+    if (idx == n - 1) bins[2 * cur + 1] = n;
+    if (idx > 0) {
+        const int32_t prev = (int32_t)(keys[idx - 1] >> 32);
+        if (prev != cur) {
+            bins[2 * prev + 1] = idx;
+            bins[2 * cur] = idx;
+        }
+    }
+}
+
+// ------------------------------------------- reference-layout building blocks
+
+// project_cubics_2d_forward_kernel (cubic_splatting.py:546-747), per segment.
+__global__ __launch_bounds__(256) void k_project_ref(
+    const float* __restrict__ cubics_norm, const float* __restrict__ stroke_widths,
+    const float* __restrict__ support_radii, int nseg, int img_h, int img_w, int block_x,
+    int block_y, float aabb_pad, int aniso, float* __restrict__ cubics_px,
+    int32_t* __restrict__ tile_ranges, int32_t* __restrict__ num_tiles_hit) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
+    const SegProj r = project_segment(
+        cubics_norm + (size_t)s * 8, 0.5f * (float)img_w, 0.5f * (float)img_h,
+        fmaxf(0.0f, stroke_widths[s]) * 0.5f, fmaxf(0.0f, support_radii[s]), aabb_pad, aniso,
+        tbx, tby, (float)block_x, (float)block_y);
+    float4* cp = reinterpret_cast<float4*>(cubics_px + (size_t)s * 8);
+    cp[0] = make_float4(r.px[0], r.py[0], r.px[1], r.py[1]);
+    cp[1] = make_float4(r.px[2], r.py[2], r.px[3], r.py[3]);
+    reinterpret_cast<int4*>(tile_ranges)[s] = make_int4(r.tx0, r.ty0, r.tx1, r.ty1);
+    num_tiles_hit[s] = max(0, (r.tx1 - r.tx0) * (r.ty1 - r.ty0));
+}
+
+// primitive_tile_ranges_from_segment_ranges_kernel (cubic_splatting.py:2071-2137).
+__global__ __launch_bounds__(256) void k_prim_ranges_ref(const int32_t* __restrict__ seg_ranges,
+                                                        const int32_t* __restrict__ offs, int P,
+                                                        int tbx, int tby,
+                                                        int32_t* __restrict__ prim_ranges,
+                                                        int32_t* __restrict__ num_tiles_hit) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= P) return;
+    const int s0 = offs[p], s1 = offs[p + 1];
+    int4 tr = make_int4(0, 0, 0, 0);
+    int area = 0;
+    if (s1 > s0) {
+        int mnx = tbx, mny = tby, mxx = 0, mxy = 0;
+        for (int s = s0; s < s1; ++s) {
+            const int4 r = reinterpret_cast<const int4*>(seg_ranges)[s];
+            mnx = min(mnx, r.x); mny = min(mny, r.y);
+            mxx = max(mxx, r.z); mxy = max(mxy, r.w);
+        }
+        tr = make_int4(mnx, mny, mxx, mxy);
+        area = max(0, mxx - mnx) * max(0, mxy - mny);
+    }
+    reinterpret_cast<int4*>(prim_ranges)[p] = tr;
+    num_tiles_hit[p] = area;
+}
+
+// map_cubic_to_intersects_kernel (cubic_splatting.py:750-819): wave per
+// primitive, row-major over its tile rectangle, at offset cum[p-1].
+__global__ __launch_bounds__(256) void k_map_ref(const int32_t* __restrict__ tile_ranges,
+                                                const float* __restrict__ depths,
+                                                const int32_t* __restrict__ cum, int P, int tbx,
+                                                int64_t* __restrict__ isect_ids,
+                                                int32_t* __restrict__ curve_ids) {
+    const int lane = threadIdx.x & 63;
+    const int waves = (gridDim.x * blockDim.x) >> 6;
+    for (int p = (blockIdx.x * blockDim.x + threadIdx.x) >> 6; p < P; p += waves) {
+        const int4 tr = reinterpret_cast<const int4*>(tile_ranges)[p];
+        const int w = tr.z - tr.x, h = tr.w - tr.y;
+        if (w * h <= 0) continue;
+        const int base = p == 0 ? 0 : cum[p - 1];
+        const int32_t bits = __builtin_bit_cast(int32_t, depths[p]);
+        const int64_t dk =
+            (int64_t)(uint32_t)(bits ^ ((bits >> 31) | (int32_t)0x80000000));
+        for (int k = lane; k < w * h; k += kWave) {
+            const int row = k / w, col = k - row * w;
+            const int64_t tile = (int64_t)((tr.y + row) * tbx + tr.x + col);
+            isect_ids[base + k] = (tile << 32) | dk;
+            curve_ids[base + k] = p;
+        }
+    }
+}
+
+// _build_fill_isect_edge_ranges (cubic_splatting.py:1849-1860).
+__global__ __launch_bounds__(256) void k_isect_edge_ranges(const int32_t* __restrict__ ids,
+                                                          const int32_t* __restrict__ offs, int n,
+                                                          int eps, int32_t* __restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int p = ids[i];
+    out[2 * i] = offs[p] * eps;
+    out[2 * i + 1] = offs[p + 1] * eps;
+}
+
+}  // namespace cs
+
+// ===================================================================== C ABI
+
+using namespace cs;
+
+static inline int blocks_for(int64_t n, int t) { return (int)((n + t - 1) / t); }
+
+static int launch_status() {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? CS_OK : CS_ERR_HIP;
+}
+
+extern "C" size_t cs_scan_temp_elems(int32_t n) {
+    const int nb = blocks_for(n, kScanChunk);
+    return (size_t)(nb > 1 ? nb : 1);
+}
+
+extern "C" int cs_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int32_t n,
+                                     uint32_t* temp, int32_t* total, hipStream_t stream) {
+    if (n < 0) return CS_ERR_ARGS;
+    if (n == 0) {
+        if (total) {
+            hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(256), 0, stream, total, 1, 0);
+        }
+        return launch_status();
+    }
+    const int nb = blocks_for(n, kScanChunk);
+    if (nb > 1) {
+        hipLaunchKernelGGL(k_scan_block_sums, dim3(nb), dim3(kScanThreads), 0, stream, in, n, temp);
+        hipLaunchKernelGGL(k_scan_partials, dim3(1), dim3(kScanThreads), 0, stream, temp, nb);
+    }
+    hipLaunchKernelGGL(k_scan_apply, dim3(nb), dim3(kScanThreads), 0, stream, in, out, n,
+                       nb > 1 ? temp : nullptr, total);
+    return launch_status();
+}
+
+extern "C" size_t cs_radix_counts_elems(int32_t n) {
+    const int nb = blocks_for(n > 0 ? n : 1, kRsTile);
+    return (size_t)256 * nb;
+}
+
+extern "C" int cs_radix_sort_pairs_u32(uint32_t* keys, int32_t* vals, uint32_t* keys_alt,
+                                       int32_t* vals_alt, int32_t n, int32_t key_bits,
+                                       uint32_t* counts, uint32_t* scan_temp,
+                                       hipStream_t stream) {
+    if (n < 0 || key_bits < 0 || key_bits > 32) return CS_ERR_ARGS;
+    if (n <= 1 || key_bits == 0) return CS_OK;
+    const int nb = blocks_for(n, kRsTile);
+    const int passes = (key_bits + 7) / 8;
+    uint32_t *ki = keys, *ko = keys_alt;
+    int32_t *vi = vals, *vo = vals_alt;
+    for (int ps = 0; ps < passes; ++ps) {
+        const int shift = 8 * ps;
+        hipLaunchKernelGGL(k_rs_hist, dim3(nb), dim3(kRsThreads), 0, stream, ki, n, shift, nb,
+                           counts);
+        int rc = cs_scan_exclusive_u32(counts, counts, 256 * nb, scan_temp, nullptr, stream);
+        if (rc) return rc;
+        hipLaunchKernelGGL(k_rs_scatter, dim3(nb), dim3(kRsThreads), 0, stream, ki, vi, ko, vo, n,
+                           shift, nb, counts);
+        uint32_t* tk = ki; ki = ko; ko = tk;
+        int32_t* tv = vi; vi = vo; vo = tv;
+    }
+    if (ki != keys) {
+        if (hipMemcpyAsync(keys, ki, sizeof(uint32_t) * n, hipMemcpyDeviceToDevice, stream) !=
+                hipSuccess ||
+            hipMemcpyAsync(vals, vi, sizeof(int32_t) * n, hipMemcpyDeviceToDevice, stream) !=
+                hipSuccess)
+            return CS_ERR_HIP;
+    }
+    return launch_status();
+}
+
+static int bits_for(int64_t v) {
+    int b = 0;
+    while (b < 32 && ((int64_t)1 << b) < v) ++b;
+    return b;
+}
+
+extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets,
+                              const float* colors, const float* opacities, const float* depths,
+                              const int32_t* fill_rules, const float* aa_widths,
+                              const float* stroke_widths, int32_t nseg, int32_t nprim,
+                              int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
+                              int32_t samples, float aabb_pad, int32_t aniso, int32_t mode,
+                              float* cubics_px, int32_t* seg_tile_ranges, float* seg_bbox,
+                              void* edges, int32_t* prim_tile_ranges, uint32_t* num_tiles_hit,
+                              float* inv_sigma2s, void* prim_recs, uint32_t* keys,
+                              int32_t* order, uint32_t* keys_alt, int32_t* vals_alt,
+                              uint32_t* radix_counts, uint32_t* scan_temp,
+                              uint32_t* rank_offsets, int32_t* status, hipStream_t stream) {
+    if (nseg < 0 || nprim <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0 ||
+        samples < 2 || (mode != 0 && mode != 1))
+        return CS_ERR_ARGS;
+    const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
+    hipLaunchKernelGGL(k_status_init, dim3(1), dim3(1), 0, stream, seg_offsets, nprim, status);
+    if (nseg > 0)
+        hipLaunchKernelGGL(k_project_flatten, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
+                           cubics_norm, seg_offsets, nprim, aa_widths, stroke_widths, nseg, img_h,
+                           img_w, block_x, block_y, aabb_pad, aniso, samples, cubics_px,
+                           seg_tile_ranges, reinterpret_cast<float4*>(seg_bbox),
+                           reinterpret_cast<EdgeRec*>(edges));
+    hipLaunchKernelGGL(k_prim_prep, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
+                       cubics_norm, seg_offsets, nprim, seg_tile_ranges,
+                       reinterpret_cast<const float4*>(seg_bbox), colors, opacities, depths,
+                       fill_rules, aa_widths, stroke_widths, nseg, tbx, tby, mode, status,
+                       prim_tile_ranges,
+                       num_tiles_hit, inv_sigma2s, keys, order,
+                       reinterpret_cast<PrimRec*>(prim_recs));
+    int rc = cs_radix_sort_pairs_u32(keys, order, keys_alt, vals_alt, nprim, 32, radix_counts,
+                                     scan_temp, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_rank_counts, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream, order,
+                       num_tiles_hit, nprim, keys_alt);
+    return cs_scan_exclusive_u32(keys_alt, rank_offsets, nprim, scan_temp, status, stream);
+}
+
+extern "C" int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges,
+                             const uint32_t* rank_offsets, int32_t nprim, int32_t num_intersects,
+                             int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
+                             uint32_t* tile_keys, int32_t* prim_ids_sorted, uint32_t* keys_alt,
+                             int32_t* vals_alt, uint32_t* radix_counts, uint32_t* scan_temp,
+                             int32_t* tile_bins, hipStream_t stream) {
+    if (nprim <= 0 || num_intersects < 0 || block_x <= 0 || block_y <= 0) return CS_ERR_ARGS;
+    const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
+    const int ntiles = tbx * tby;
+    hipLaunchKernelGGL(k_fill_i32, dim3(blocks_for(2 * ntiles, 256)), dim3(256), 0, stream,
+                       tile_bins, 2 * ntiles, 0);
+    if (num_intersects == 0) return launch_status();
+    const int emit_blocks = blocks_for((int64_t)nprim * kWave, 256);
+    hipLaunchKernelGGL(k_emit, dim3(emit_blocks < 65535 ? emit_blocks : 65535), dim3(256), 0,
+                       stream, order, prim_tile_ranges, rank_offsets, nprim, tbx, tile_keys,
+                       prim_ids_sorted);
+    int rc = cs_radix_sort_pairs_u32(tile_keys, prim_ids_sorted, keys_alt, vals_alt,
+                                     num_intersects, bits_for(ntiles), radix_counts, scan_temp,
+                                     stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_tile_bins, dim3(blocks_for(num_intersects, 256)), dim3(256), 0, stream,
+                       tile_keys, num_intersects, tile_bins);
+    return launch_status();
+}
+
+extern "C" int cs_project_cubics_2d_forward(const float* cubics_norm, const float* stroke_widths,
+                                            const float* support_radii, int32_t nseg,
+                                            int32_t img_h, int32_t img_w, int32_t block_x,
+                                            int32_t block_y, float aabb_pad, int32_t aniso,
+                                            float* cubics_px, int32_t* tile_ranges,
+                                            int32_t* num_tiles_hit, hipStream_t stream) {
+    if (nseg < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0) return CS_ERR_ARGS;
+    if (nseg == 0) return CS_OK;
+    hipLaunchKernelGGL(k_project_ref, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
+                       cubics_norm, stroke_widths, support_radii, nseg, img_h, img_w, block_x,
+                       block_y, aabb_pad, aniso, cubics_px, tile_ranges, num_tiles_hit);
+    return launch_status();
+}
+
+extern "C" int cs_primitive_tile_ranges(const int32_t* seg_tile_ranges, const int32_t* offs,
+                                        int32_t nprim, int32_t tbx, int32_t tby,
+                                        int32_t* prim_tile_ranges, int32_t* num_tiles_hit,
+                                        hipStream_t stream) {
+    if (nprim < 0) return CS_ERR_ARGS;
+    if (nprim == 0) return CS_OK;
+    hipLaunchKernelGGL(k_prim_ranges_ref, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
+                       seg_tile_ranges, offs, nprim, tbx, tby, prim_tile_ranges, num_tiles_hit);
+    return launch_status();
+}
+
+extern "C" int cs_map_cubic_to_intersects(const int32_t* tile_ranges, const float* depths,
+                                          const int32_t* cum_tiles_hit, int32_t nprim,
+                                          int32_t tbx, int64_t* isect_ids, int32_t* curve_ids,
+                                          hipStream_t stream) {
+    if (nprim < 0 || tbx <= 0) return CS_ERR_ARGS;
+    if (nprim == 0) return CS_OK;
+    const int nb = blocks_for((int64_t)nprim * kWave, 256);
+    hipLaunchKernelGGL(k_map_ref, dim3(nb < 65535 ? nb : 65535), dim3(256), 0, stream,
+                       tile_ranges, depths, cum_tiles_hit, nprim, tbx, isect_ids, curve_ids);
+    return launch_status();
+}
+
+extern "C" int cs_get_tile_bin_edges(const int64_t* isect_ids_sorted, int32_t num_intersects,
+                                     int32_t num_rows, int32_t* tile_bins, hipStream_t stream) {
+    if (num_intersects < 0 || num_rows < 0) return CS_ERR_ARGS;
+    if (num_rows > 0)
+        hipLaunchKernelGGL(k_fill_i32, dim3(blocks_for(2 * (int64_t)num_rows, 256)), dim3(256), 0,
+                           stream, tile_bins, 2 * num_rows, 0);
+    if (num_intersects > 0)
+        hipLaunchKernelGGL(k_tile_bins_i64, dim3(blocks_for(num_intersects, 256)), dim3(256), 0,
+                           stream, isect_ids_sorted, num_intersects, tile_bins);
+    return launch_status();
+}
+
+extern "C" int cs_isect_edge_ranges(const int32_t* prim_ids_sorted, const int32_t* seg_offsets,
+                                    int32_t num_intersects, int32_t edges_per_segment,
+                                    int32_t* out, hipStream_t stream) {
+    if (num_intersects < 0 || edges_per_segment < 1) return CS_ERR_ARGS;
+    if (num_intersects == 0) return CS_OK;
+    hipLaunchKernelGGL(k_isect_edge_ranges, dim3(blocks_for(num_intersects, 256)), dim3(256), 0,
+                       stream, prim_ids_sorted, seg_offsets, num_intersects, edges_per_segment,
+                       out);
+    return launch_status();
+}

@@ -1,0 +1,104 @@
+// Shared device-side definitions for the CubicSplat MI355X kernels (gfx950,
+// wave64).  Every floating-point expression below is part of the arithmetic
+// spec that the CPU oracle also follows: IEEE-rounded + - * / sqrt, no
+// implicit contraction (the library is built with -ffp-contract=off), fused
+// multiply-adds only where fmaf() is written out.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cs {
+
+constexpr int kWave = 64;
+constexpr int kTile = 16;            // 16x16 pixel tiles, one workgroup each
+constexpr int kBlockThreads = 256;   // 4 waves; wave w owns tile rows 4w..4w+3
+
+// Constants the reference writes as Python floats, rounded once from double.
+constexpr float kEps = (float)1e-6;
+constexpr float kAlphaCap = (float)0.999;
+constexpr float kAlphaMin = (float)(1.0 / 255.0);
+constexpr float kTStop = (float)1e-4;
+constexpr float kWidthMin = (float)1e-4;
+
+// One flattened polyline edge, 32 bytes: endpoints, direction v = p1 - p0 and
+// u = v / max(|v|^2, eps) (multiply by the correctly rounded reciprocal).
+struct alignas(32) EdgeRec {
+    float x0, y0, x1, y1;
+    float vx, vy, ux, uy;
+};
+
+// Per-primitive raster record, built once per forward.
+struct alignas(16) PrimRec {
+    float r, g, b, opacity;
+    float inv_sigma2;   // max(inv_sigma2, eps)
+    float inv_sigma;    // sqrt(max(inv_sigma2, eps))
+    float half_sw;      // stroke half width max(0, sw) / 2 (0 for fill)
+    float cull_d;       // beyond this distance a pixel's result does not depend on it
+    int32_t s0, s1;     // segment range
+    int32_t rule;       // 0 even-odd, else nonzero (fill)
+    int32_t closed;     // 1 if the edge chain is closed
+    float bx0, by0, bx1, by1;  // bounding box of the polyline vertices
+};
+
+// exp(x): n = rint(x log2 e), r = x - n ln2 (two-part Cody-Waite), e^r by a
+// degree-7 Taylor polynomial in Horner form, scaled by 2^n in two exact steps.
+__device__ __forceinline__ float spec_expf(float x) {
+    if (!(x == x)) return x;
+    if (x > 88.72283935546875f) return __builtin_huge_valf();
+    if (x < -103.97208404541015625f) return 0.0f;
+    const float kf = __builtin_rintf(x * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(kf, -0.693145751953125f, x);
+    r = __builtin_fmaf(kf, -1.428606765330187045037746429443359375e-06f, r);
+    float p = 1.98412698412698e-04f;
+    p = __builtin_fmaf(p, r, 1.38888888888889e-03f);
+    p = __builtin_fmaf(p, r, 8.33333333333333e-03f);
+    p = __builtin_fmaf(p, r, 4.16666666666667e-02f);
+    p = __builtin_fmaf(p, r, 1.66666666666667e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int k = (int)kf;
+    const int k1 = k >> 1;
+    const int k2 = k - k1;
+    const float s1 = __builtin_bit_cast(float, (uint32_t)(k1 + 127) << 23);
+    const float s2 = __builtin_bit_cast(float, (uint32_t)(k2 + 127) << 23);
+    return (p * s1) * s2;
+}
+
+// Truncating float -> int32 with saturation, NaN -> 0.
+__device__ __forceinline__ int32_t f2i_sat(float x) {
+    if (!(x == x)) return 0;
+    if (x >= 2147483648.0f) return INT32_MAX;
+    if (x < -2147483648.0f) return INT32_MIN;
+    return (int32_t)x;
+}
+
+__device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Squared distance from the axis-aligned rectangle [rx0,rx1]x[ry0,ry1] to the
+// box [bx0,bx1]x[by0,by1] (0 when they overlap).
+__device__ __forceinline__ float rect_box_d2(float rx0, float ry0, float rx1, float ry1, float bx0,
+                                             float by0, float bx1, float by1) {
+    const float dx = fmaxf(fmaxf(bx0 - rx1, rx0 - bx1), 0.0f);
+    const float dy = fmaxf(fmaxf(by0 - ry1, ry0 - by1), 0.0f);
+    return dx * dx + dy * dy;
+}
+
+}  // namespace cs

@@ -1,0 +1,477 @@
+// Forward and backward rasterization of flattened cubic primitives on MI355X.
+//
+// Launch: one 256-thread workgroup per 16x16 tile.  Unlike a block-synchronous
+// design, each of the four waves owns four tile rows (64 pixels, one per lane)
+// and walks the tile's sorted list on its own: the list entry, the primitive
+// record, the segment boxes and the edge records are wave-uniform, so they
+// are read through the scalar cache and used as SGPR operands, and no LDS or
+// workgroup barrier is needed.  A wave leaves the list when all of its pixels
+// have reached the transmittance stop.
+//
+// Exactness-preserving culling per wave: a segment whose vertex box is farther
+// than the primitive's cull distance from the wave's pixel rectangle cannot
+// change any lane's result (outside: alpha < 1/255; inside: coverage is
+// exactly 1.0f), so its distance terms are skipped; its crossing terms are
+// skipped when its y-range misses the wave's four pixel rows.  Results stay
+// bit-identical to evaluating every edge.
+#include "cs_common.h"
+#include "../../include/cubicsplat_hip.h"
+
+namespace cs {
+
+static_assert(sizeof(EdgeRec) == CS_EDGE_RECORD_BYTES, "edge record layout");
+static_assert(sizeof(PrimRec) == CS_PRIM_RECORD_BYTES, "primitive record layout");
+
+// Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
+// contiguous run of tiles so neighbouring tiles (which share primitives and
+// their edge records) hit the same L2.  Bijective for any tile count.
+__device__ __forceinline__ int xcd_tile(int b, int n) {
+    const int q = n >> 3, r = n & 7;
+    const int x = b & 7, k = b >> 3;
+    return x * q + min(x, r) + k;
+}
+
+// Crossing parity equals winding & 1 (each crossing changes the winding by
+// +-1), so only the winding number is tracked.
+struct Geom {
+    float min_d2;
+    int winding;
+    int best;
+    float bproj, bdx, bdy;
+};
+
+// Distance (and optionally the best edge) and +x ray crossings of one
+// segment's edges, cubic_splatting.py:1095-1134 / 1451-1501.
+template <bool DIST, bool CROSS, bool BEST>
+__device__ __forceinline__ void scan_edges(const EdgeRec* __restrict__ ep, int n, int ebase,
+                                           float px, float py, Geom& G) {
+    for (int e = 0; e < n; ++e) {
+        const EdgeRec E = ep[e];
+        const float wx = px - E.x0, wy = py - E.y0;
+        if (DIST) {
+            float proj = __builtin_fmaf(wx, E.ux, wy * E.uy);
+            proj = fminf(fmaxf(proj, 0.0f), 1.0f);
+            const float dx = __builtin_fmaf(proj, E.vx, -wx);
+            const float dy = __builtin_fmaf(proj, E.vy, -wy);
+            const float d2 = __builtin_fmaf(dx, dx, dy * dy);
+            if (BEST) {
+                if (d2 < G.min_d2) {
+                    G.min_d2 = d2;
+                    G.best = ebase + e;
+                    G.bproj = proj;
+                    G.bdx = dx;
+                    G.bdy = dy;
+                }
+            } else {
+                G.min_d2 = fminf(G.min_d2, d2);
+            }
+        }
+        if (CROSS) {
+            // Upward crossing (y0 <= py < y1) counts +1 when the edge passes
+            // right of the pixel (cross product > 0), downward -1 when < 0.
+            const bool b0 = E.y0 <= py, b1 = E.y1 <= py;
+            const float cr = __builtin_fmaf(wy, E.vx, -(wx * E.vy));
+            const bool hit = (b0 != b1) & ((b0 ? cr : -cr) > 0.0f);
+            G.winding += (int)(hit & b0);
+            G.winding -= (int)(hit & !b0);
+        }
+    }
+}
+
+struct WaveRect {
+    float x0, y0, x1, y1;  // pixel centres covered by the wave
+};
+
+// Primitive-level cull: true when no lane of the wave can be affected.
+template <int MODE>
+__device__ __forceinline__ bool prim_culled(const PrimRec& pr, const WaveRect& R, float D2) {
+    if (rect_box_d2(R.x0, R.y0, R.x1, R.y1, pr.bx0, pr.by0, pr.bx1, pr.by1) <= D2) return false;
+    if (MODE == 1 || pr.closed) return true;
+    // Open chain in fill mode: the winding number can be non-zero left of the
+    // box, but not when the rows miss the box or the wave is right of it.
+    return pr.by0 > R.y1 || pr.by1 < R.y0 || R.x0 > pr.bx1;
+}
+
+template <int MODE, bool BEST>
+__device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& R, float D2,
+                                              const float4* __restrict__ seg_bbox,
+                                              const EdgeRec* __restrict__ edges, int eps,
+                                              float px, float py, Geom& G) {
+    G.min_d2 = 1e30f;
+    G.winding = 0;
+    G.best = -1;
+    G.bproj = 0.0f;
+    G.bdx = 0.0f;
+    G.bdy = 0.0f;
+    for (int s = pr.s0; s < pr.s1; ++s) {
+        const float4 bb = seg_bbox[s];
+        const bool near = rect_box_d2(R.x0, R.y0, R.x1, R.y1, bb.x, bb.y, bb.z, bb.w) <= D2;
+        const bool band = (MODE == 0) && !(bb.y > R.y1 || bb.w < R.y0);
+        const EdgeRec* ep = edges + (size_t)s * eps;
+        const int ebase = s * eps;
+        if (near) {
+            if (band) scan_edges<true, true, BEST>(ep, eps, ebase, px, py, G);
+            else scan_edges<true, false, BEST>(ep, eps, ebase, px, py, G);
+        } else if (band) {
+            scan_edges<false, true, false>(ep, eps, ebase, px, py, G);
+        }
+    }
+}
+
+struct Cov {
+    float cov, dist, sgn, ed;
+};
+
+// Fill: cubic_splatting.py:1138-1170; stroke: cubic_polyline_splatting.py:219-226.
+template <int MODE>
+__device__ __forceinline__ Cov coverage(const PrimRec& pr, const Geom& G) {
+    Cov c;
+    c.dist = __builtin_sqrtf(fmaxf(G.min_d2, 0.0f));
+    if (MODE == 0) {
+        const bool inside = pr.rule == 0 ? ((G.winding & 1) != 0) : (G.winding != 0);
+        c.sgn = inside ? -1.0f : 1.0f;
+        float logit = c.dist * pr.inv_sigma * 2.0f;
+        if (inside) logit = -logit;
+        logit = fmaxf(-60.0f, fminf(60.0f, logit));
+        c.cov = 1.0f / (1.0f + spec_expf(logit));
+        c.ed = 0.0f;
+    } else {
+        c.ed = fmaxf(0.0f, c.dist - pr.half_sw);
+        const float sigma = 0.5f * c.ed * c.ed * pr.inv_sigma2;
+        c.cov = spec_expf(-sigma);
+        c.sgn = 1.0f;
+    }
+    return c;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
+    const int32_t* __restrict__ prim_ids, const int32_t* __restrict__ bins,
+    const EdgeRec* __restrict__ edges, const float4* __restrict__ seg_bbox,
+    const PrimRec* __restrict__ prims, const float* __restrict__ bg, int img_h, int img_w,
+    int tbx, int ntiles, int eps, float* __restrict__ out, float* __restrict__ final_T,
+    int32_t* __restrict__ final_idx) {
+    const int tile = xcd_tile(blockIdx.x, ntiles);
+    const int tty = tile / tbx, ttx = tile - tty * tbx;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int i = tty * kTile + wv * 4 + (lane >> 4);
+    const int j = ttx * kTile + (lane & 15);
+    const bool in_img = (i < img_h) & (j < img_w);
+    const float px = (float)j + 0.5f, py = (float)i + 0.5f;
+    WaveRect R;
+    R.x0 = (float)(ttx * kTile) + 0.5f;
+    R.x1 = R.x0 + 15.0f;
+    R.y0 = (float)(tty * kTile + wv * 4) + 0.5f;
+    R.y1 = R.y0 + 3.0f;
+    const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
+    float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
+    int cur = 0;
+    bool done = !in_img;
+    for (int g = g0; g < g1; ++g) {
+        if (__ballot(!done) == 0) break;
+        const int pid = prim_ids[g];
+        const PrimRec pr = prims[pid];
+        const float D2 = pr.cull_d * pr.cull_d;
+        if (prim_culled<MODE>(pr, R, D2)) continue;
+        Geom G;
+        prim_geometry<MODE, false>(pr, R, D2, seg_bbox, edges, eps, px, py, G);
+        if (!done) {
+            const Cov c = coverage<MODE>(pr, G);
+            const float alpha = fminf(kAlphaCap, pr.opacity * c.cov);
+            if (alpha >= kAlphaMin) {
+                const float nT = T * (1.0f - alpha);
+                const float vis = alpha * T;
+                C0 = __builtin_fmaf(pr.r, vis, C0);
+                C1 = __builtin_fmaf(pr.g, vis, C1);
+                C2 = __builtin_fmaf(pr.b, vis, C2);
+                T = nT;
+                cur = g;
+                if (nT <= kTStop) done = true;
+            }
+        }
+    }
+    if (in_img) {
+        const size_t pix = (size_t)i * img_w + j;
+        final_T[pix] = T;
+        final_idx[pix] = cur;
+        out[3 * pix + 0] = __builtin_fmaf(T, bg[0], C0);
+        out[3 * pix + 1] = __builtin_fmaf(T, bg[1], C1);
+        out[3 * pix + 2] = __builtin_fmaf(T, bg[2], C2);
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
+    const int32_t* __restrict__ prim_ids, const int32_t* __restrict__ bins,
+    const EdgeRec* __restrict__ edges, const float4* __restrict__ seg_bbox,
+    const PrimRec* __restrict__ prims, const float* __restrict__ bg, int img_h, int img_w,
+    int tbx, int ntiles, int eps, const float* __restrict__ final_T,
+    const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
+    float* __restrict__ v_edges, float* __restrict__ v_colors, float* __restrict__ v_opac,
+    float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
+    float* __restrict__ isect_contrib) {
+    const int tile = xcd_tile(blockIdx.x, ntiles);
+    const int tty = tile / tbx, ttx = tile - tty * tbx;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int i = tty * kTile + wv * 4 + (lane >> 4);
+    const int j = ttx * kTile + (lane & 15);
+    const bool in_img = (i < img_h) & (j < img_w);
+    const float px = (float)j + 0.5f, py = (float)i + 0.5f;
+    WaveRect R;
+    R.x0 = (float)(ttx * kTile) + 0.5f;
+    R.x1 = R.x0 + 15.0f;
+    R.y0 = (float)(tty * kTile + wv * 4) + 0.5f;
+    R.y1 = R.y0 + 3.0f;
+    const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
+    const size_t pix = in_img ? (size_t)i * img_w + j : 0;
+    float T = in_img ? final_T[pix] : 1.0f;
+    const float T_final = T;
+    const int fidx = in_img ? final_idx[pix] : -1;
+    const float v0 = in_img ? v_out[3 * pix + 0] : 0.0f;
+    const float v1 = in_img ? v_out[3 * pix + 1] : 0.0f;
+    const float v2 = in_img ? v_out[3 * pix + 2] : 0.0f;
+    const float bg_dot = __builtin_fmaf(bg[2], v2, __builtin_fmaf(bg[1], v1, bg[0] * v0));
+    const bool want_contrib = (contrib_rgb != nullptr) | (isect_contrib != nullptr);
+    float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
+    const int gstart = min(g1 - 1, wave_max_i(fidx));
+    for (int g = gstart; g >= g0; --g) {
+        const bool valid = in_img & (g <= fidx);
+        if (__ballot(valid) == 0) continue;
+        const int pid = prim_ids[g];
+        const PrimRec pr = prims[pid];
+        const float D2 = pr.cull_d * pr.cull_d;
+        if (prim_culled<MODE>(pr, R, D2)) continue;
+        Geom G;
+        prim_geometry<MODE, true>(pr, R, D2, seg_bbox, edges, eps, px, py, G);
+        float vr = 0.0f, vg = 0.0f, vb = 0.0f, vop = 0.0f, vis2 = 0.0f, vsw = 0.0f;
+        float cr = 0.0f, cg = 0.0f, cb = 0.0f;
+        float e0 = 0.0f, e1 = 0.0f, e2 = 0.0f, e3 = 0.0f;
+        int gbest = -1;
+        bool contrib = false;
+        if (valid) {
+            const Cov c = coverage<MODE>(pr, G);
+            const float op = pr.opacity;
+            const float alpha = fminf(kAlphaCap, op * c.cov);
+            if (alpha >= kAlphaMin) {
+                contrib = true;
+                const float ra = 1.0f / (1.0f - alpha);
+                T = T * ra;
+                const float fac = alpha * T;
+                vr = fac * v0;
+                vg = fac * v1;
+                vb = fac * v2;
+                if (want_contrib) {
+                    cr = fac * pr.r;
+                    cg = fac * pr.g;
+                    cb = fac * pr.b;
+                }
+                float va = __builtin_fmaf(pr.r, T, -(b0 * ra)) * v0;
+                va = __builtin_fmaf(__builtin_fmaf(pr.g, T, -(b1 * ra)), v1, va);
+                va = __builtin_fmaf(__builtin_fmaf(pr.b, T, -(b2 * ra)), v2, va);
+                va = __builtin_fmaf(T_final * ra, -bg_dot, va);
+                b0 = __builtin_fmaf(pr.r, fac, b0);
+                b1 = __builtin_fmaf(pr.g, fac, b1);
+                b2 = __builtin_fmaf(pr.b, fac, b2);
+                if (alpha < kAlphaCap) {
+                    vop = c.cov * va;
+                    float gx = 0.0f, gy = 0.0f;
+                    bool geom = false;
+                    if (MODE == 0) {
+                        const float v_cov = op * va;
+                        const float v_logit = -v_cov * c.cov * (1.0f - c.cov);
+                        const float v_is = v_logit * c.sgn * c.dist * 2.0f;
+                        vis2 = v_is * 0.5f / fmaxf(pr.inv_sigma, kEps);
+                        if (c.dist > kEps && G.best >= 0) {
+                            const float v_dist = v_logit * c.sgn * pr.inv_sigma * 2.0f;
+                            gx = v_dist * G.bdx / c.dist;
+                            gy = v_dist * G.bdy / c.dist;
+                            geom = true;
+                        }
+                    } else {
+                        const float v_sigma = -op * c.cov * va;
+                        vis2 = 0.5f * c.ed * c.ed * v_sigma;
+                        if (c.ed > 0.0f) {
+                            const float v_e = v_sigma * c.ed * pr.inv_sigma2;
+                            vsw = -0.5f * v_e;
+                            if (c.dist > kEps && G.best >= 0) {
+                                gx = v_e * G.bdx / c.dist;
+                                gy = v_e * G.bdy / c.dist;
+                                geom = true;
+                            }
+                        }
+                    }
+                    if (geom) {
+                        gbest = G.best;
+                        e0 = (1.0f - G.bproj) * gx;
+                        e1 = (1.0f - G.bproj) * gy;
+                        e2 = G.bproj * gx;
+                        e3 = G.bproj * gy;
+                    }
+                }
+            }
+        }
+        if (__ballot(contrib) == 0) continue;
+        vr = wave_sum(vr);
+        vg = wave_sum(vg);
+        vb = wave_sum(vb);
+        vop = wave_sum(vop);
+        vis2 = wave_sum(vis2);
+        if (MODE == 1) vsw = wave_sum(vsw);
+        if (want_contrib) {
+            cr = wave_sum(cr);
+            cg = wave_sum(cg);
+            cb = wave_sum(cb);
+        }
+        if (lane == 0) {
+            atomicAdd(v_colors + 3 * pid + 0, vr);
+            atomicAdd(v_colors + 3 * pid + 1, vg);
+            atomicAdd(v_colors + 3 * pid + 2, vb);
+            atomicAdd(v_opac + pid, vop);
+            atomicAdd(v_is2 + pid, vis2);
+            if (MODE == 1) atomicAdd(v_sw + pid, vsw);
+            if (contrib_rgb) {
+                atomicAdd(contrib_rgb + 3 * pid + 0, cr);
+                atomicAdd(contrib_rgb + 3 * pid + 1, cg);
+                atomicAdd(contrib_rgb + 3 * pid + 2, cb);
+            }
+            if (isect_contrib) atomicAdd(isect_contrib + g, cr + cg + cb);
+        }
+        if (gbest >= 0) {
+            float* ve = v_edges + 4 * (size_t)gbest;
+            atomicAdd(ve + 0, e0);
+            atomicAdd(ve + 1, e1);
+            atomicAdd(ve + 2, e2);
+            atomicAdd(ve + 3, e3);
+        }
+    }
+}
+
+// _accumulate_edge_grads_to_cubics_kernel (cubic_splatting.py:2308-2396) and
+// the px -> normalized scaling (cubic_splatting.py:3096-3100).
+__global__ __launch_bounds__(256) void k_accumulate(const float4* __restrict__ v_edges, int nseg,
+                                                   int eps, float half_w, float half_h,
+                                                   float* __restrict__ v_px,
+                                                   float* __restrict__ v_norm) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    const float inv_e = 1.0f / (float)eps;
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < eps; ++e) {
+        const float t0 = (float)e * inv_e, t1 = (float)(e + 1) * inv_e;
+        const float o0 = 1.0f - t0, o1 = 1.0f - t1;
+        const float o0s = o0 * o0, o1s = o1 * o1, t0s = t0 * t0, t1s = t1 * t1;
+        const float bs[4] = {o0s * o0, 3.0f * o0s * t0, 3.0f * o0 * t0s, t0s * t0};
+        const float be[4] = {o1s * o1, 3.0f * o1s * t1, 3.0f * o1 * t1s, t1s * t1};
+        const float4 gr = v_edges[(size_t)s * eps + e];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            a[2 * k] = __builtin_fmaf(gr.z, be[k], __builtin_fmaf(gr.x, bs[k], a[2 * k]));
+            a[2 * k + 1] = __builtin_fmaf(gr.w, be[k], __builtin_fmaf(gr.y, bs[k], a[2 * k + 1]));
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        v_px[(size_t)s * 8 + 2 * k] = a[2 * k];
+        v_px[(size_t)s * 8 + 2 * k + 1] = a[2 * k + 1];
+        if (v_norm) {
+            v_norm[(size_t)s * 8 + 2 * k] = a[2 * k] * half_w;
+            v_norm[(size_t)s * 8 + 2 * k + 1] = a[2 * k + 1] * half_h;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_aa_grads(const float* __restrict__ widths,
+                                                 const float* __restrict__ v_is2, int P,
+                                                 float* __restrict__ v_aa) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= P) return;
+    const float w = widths[p];
+    v_aa[p] = (-2.0f * v_is2[p]) / fmaxf(w * w * w, (float)1e-12);
+}
+
+}  // namespace cs
+
+using namespace cs;
+
+static int raster_status() {
+    return hipGetLastError() == hipSuccess ? CS_OK : CS_ERR_HIP;
+}
+
+extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
+                                    const int32_t* tile_bins, const void* edges,
+                                    const float* seg_bbox, const void* prim_recs,
+                                    const float* background, int32_t img_h, int32_t img_w,
+                                    int32_t edges_per_segment, float* out_img, float* final_Ts,
+                                    int32_t* final_idx, hipStream_t stream) {
+    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1)
+        return CS_ERR_ARGS;
+    const int tbx = (img_w + kTile - 1) / kTile, tby = (img_h + kTile - 1) / kTile;
+    const int nt = tbx * tby;
+    auto* E = reinterpret_cast<const EdgeRec*>(edges);
+    auto* B = reinterpret_cast<const float4*>(seg_bbox);
+    auto* P = reinterpret_cast<const PrimRec*>(prim_recs);
+    if (mode == 0)
+        hipLaunchKernelGGL(k_raster_fwd<0>, dim3(nt), dim3(kBlockThreads), 0, stream,
+                           prim_ids_sorted, tile_bins, E, B, P, background, img_h, img_w, tbx, nt,
+                           edges_per_segment, out_img, final_Ts, final_idx);
+    else
+        hipLaunchKernelGGL(k_raster_fwd<1>, dim3(nt), dim3(kBlockThreads), 0, stream,
+                           prim_ids_sorted, tile_bins, E, B, P, background, img_h, img_w, tbx, nt,
+                           edges_per_segment, out_img, final_Ts, final_idx);
+    return raster_status();
+}
+
+extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
+                                     const int32_t* tile_bins, const void* edges,
+                                     const float* seg_bbox, const void* prim_recs,
+                                     const float* background, int32_t img_h, int32_t img_w,
+                                     int32_t edges_per_segment, const float* final_Ts,
+                                     const int32_t* final_idx, const float* v_output,
+                                     float* v_edges, float* v_colors, float* v_opacities,
+                                     float* v_inv_sigma2s, float* v_stroke_widths,
+                                     float* curve_contrib_rgb, float* curve_isect_contrib,
+                                     hipStream_t stream) {
+    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1)
+        return CS_ERR_ARGS;
+    if (mode == 1 && v_stroke_widths == nullptr) return CS_ERR_ARGS;
+    const int tbx = (img_w + kTile - 1) / kTile, tby = (img_h + kTile - 1) / kTile;
+    const int nt = tbx * tby;
+    auto* E = reinterpret_cast<const EdgeRec*>(edges);
+    auto* B = reinterpret_cast<const float4*>(seg_bbox);
+    auto* P = reinterpret_cast<const PrimRec*>(prim_recs);
+    if (mode == 0)
+        hipLaunchKernelGGL(k_raster_bwd<0>, dim3(nt), dim3(kBlockThreads), 0, stream,
+                           prim_ids_sorted, tile_bins, E, B, P, background, img_h, img_w, tbx, nt,
+                           edges_per_segment, final_Ts, final_idx, v_output, v_edges, v_colors,
+                           v_opacities, v_inv_sigma2s, v_stroke_widths, curve_contrib_rgb,
+                           curve_isect_contrib);
+    else
+        hipLaunchKernelGGL(k_raster_bwd<1>, dim3(nt), dim3(kBlockThreads), 0, stream,
+                           prim_ids_sorted, tile_bins, E, B, P, background, img_h, img_w, tbx, nt,
+                           edges_per_segment, final_Ts, final_idx, v_output, v_edges, v_colors,
+                           v_opacities, v_inv_sigma2s, v_stroke_widths, curve_contrib_rgb,
+                           curve_isect_contrib);
+    return raster_status();
+}
+
+extern "C" int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg,
+                                        int32_t edges_per_segment, int32_t img_h, int32_t img_w,
+                                        float* v_cubics_px, float* v_cubics_norm,
+                                        hipStream_t stream) {
+    if (nseg < 0 || edges_per_segment < 1) return CS_ERR_ARGS;
+    if (nseg == 0) return CS_OK;
+    const float half_w = (float)(0.5 * (double)img_w), half_h = (float)(0.5 * (double)img_h);
+    hipLaunchKernelGGL(k_accumulate, dim3((nseg + 255) / 256), dim3(256), 0, stream,
+                       reinterpret_cast<const float4*>(v_edges), nseg, edges_per_segment, half_w,
+                       half_h, v_cubics_px, v_cubics_norm);
+    return raster_status();
+}
+
+extern "C" int cs_aa_width_grads(const float* widths, const float* v_inv_sigma2s, int32_t nprim,
+                                 float* v_aa_widths, hipStream_t stream) {
+    if (nprim < 0) return CS_ERR_ARGS;
+    if (nprim == 0) return CS_OK;
+    hipLaunchKernelGGL(k_aa_grads, dim3((nprim + 255) / 256), dim3(256), 0, stream, widths,
+                       v_inv_sigma2s, nprim, v_aa_widths);
+    return raster_status();
+}

@@ -1,0 +1,482 @@
+"""Host side of the cubic splat path: binning, rasterization and the two
+``torch.autograd.Function``s that replace the reference's
+``_CubicFillSplatFunction`` (ops/cubic_splatting.py:2750-3125) and
+``_CubicPolylineSplatFunction`` (ops/cubic_polyline_splatting.py:962-1338).
+
+Every device computation is a call into libcubicsplat_hip.so on torch's
+current stream; there is no CPU or torch fallback.  Buffers come from torch's
+caching allocator.  One host synchronization per forward reads the
+intersection count to size the per-intersection buffers (the reference makes
+the same read at cubic_splatting.py:2879).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Callable, Mapping, MutableMapping, Optional
+
+import torch
+
+from . import _native as N
+
+BLOCK_X = 16
+BLOCK_Y = 16
+DEFAULT_THREADS = 256
+DEFAULT_AABB_PAD = 1.0
+DEFAULT_AA_WIDTH = 1.0
+DEFAULT_DISTANCE_SAMPLES = 24
+CUBIC_FLATTEN_METHOD_BERNSTEIN = "bernstein"
+CUBIC_FLATTEN_METHOD_DE_CASTELJAU = "de_casteljau"
+DEFAULT_CUBIC_FLATTEN_METHOD = CUBIC_FLATTEN_METHOD_BERNSTEIN
+_FLATTEN_ALIASES = {
+    "bernstein": CUBIC_FLATTEN_METHOD_BERNSTEIN,
+    "de_casteljau": CUBIC_FLATTEN_METHOD_DE_CASTELJAU,
+    "decasteljau": CUBIC_FLATTEN_METHOD_DE_CASTELJAU,
+    "de-casteljau": CUBIC_FLATTEN_METHOD_DE_CASTELJAU,
+}
+
+CubicProcessPayload = MutableMapping[str, Any]
+CubicProcessFn = Callable[[str, CubicProcessPayload], Optional[Mapping[str, Any]]]
+CubicFillProcessPayload = CubicProcessPayload
+CubicFillProcessFn = CubicProcessFn
+
+MODE_FILL = 0
+MODE_STROKE = 1
+
+
+def normalize_cubic_flatten_method(method: object) -> str:
+    """cubic_splatting.py:67-78."""
+    raw = str(method).strip().lower()
+    key = _FLATTEN_ALIASES.get(raw, raw)
+    if key not in {CUBIC_FLATTEN_METHOD_BERNSTEIN, CUBIC_FLATTEN_METHOD_DE_CASTELJAU}:
+        raise ValueError(
+            "flatten_method must be one of "
+            f"{sorted(_FLATTEN_ALIASES.keys())}, got {method!r}")
+    return key
+
+
+def _run_process_fn(process_fn, stage, payload):
+    """cubic_splatting.py:42-52."""
+    if process_fn is None:
+        return payload
+    updates = process_fn(stage, payload)
+    if updates:
+        payload.update(updates)
+    return payload
+
+
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().to(torch.float32).contiguous()
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().to(torch.int32).contiguous()
+
+
+def tile_bounds(img_h: int, img_w: int, block_x: int = BLOCK_X, block_y: int = BLOCK_Y):
+    return ((img_w + block_x - 1) // block_x, (img_h + block_y - 1) // block_y, 1)
+
+
+@dataclass
+class Binned:
+    """Everything the forward produces that the backward (and tests) use."""
+    mode: int
+    img_h: int
+    img_w: int
+    samples: int
+    nseg: int
+    nprim: int
+    num_intersects: int
+    cubics_px: torch.Tensor
+    seg_tile_ranges: torch.Tensor
+    seg_bbox: torch.Tensor
+    edges: torch.Tensor            # [E, 8] float32 records (x0 y0 x1 y1 vx vy ux uy)
+    prim_tile_ranges: torch.Tensor
+    num_tiles_hit: torch.Tensor
+    inv_sigma2s: torch.Tensor
+    prim_recs: torch.Tensor
+    order: torch.Tensor            # depth rank -> primitive id
+    primitive_ids_sorted: torch.Tensor
+    tile_keys_sorted: torch.Tensor
+    tile_bins: torch.Tensor
+
+    @property
+    def edges_per_segment(self) -> int:
+        return self.samples - 1
+
+    def edges_px(self) -> torch.Tensor:
+        """Edges in the reference's [E,2,2] layout."""
+        return self.edges[:, :4].reshape(-1, 2, 2)
+
+
+def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rules, widths,
+                   stroke_widths, img_h, img_w, samples, *, aabb_pad=DEFAULT_AABB_PAD,
+                   aniso=False, mode=MODE_FILL, block_x=BLOCK_X, block_y=BLOCK_Y) -> Binned:
+    """Project, flatten and bin (cubic_splatting.py:2815-2908).  All inputs are
+    contiguous device tensors of the reference's dtypes."""
+    dev = cubics_norm.device
+    lib = N.lib()
+    nseg = int(cubics_norm.shape[0])
+    P = int(seg_offsets.numel()) - 1
+    S = max(2, int(samples))
+    E = nseg * (S - 1)
+    tbx, tby, _ = tile_bounds(img_h, img_w, block_x, block_y)
+    f32, i32 = torch.float32, torch.int32
+    cubics_px = torch.empty((nseg, 4, 2), dtype=f32, device=dev)
+    seg_tile_ranges = torch.empty((nseg, 4), dtype=i32, device=dev)
+    seg_bbox = torch.empty((nseg, 4), dtype=f32, device=dev)
+    edges = torch.empty((E, N.EDGE_RECORD_FLOATS), dtype=f32, device=dev)
+    prim_tile_ranges = torch.empty((P, 4), dtype=i32, device=dev)
+    num_tiles_hit = torch.empty((P,), dtype=i32, device=dev)
+    inv_sigma2s = torch.empty((P,), dtype=f32, device=dev)
+    prim_recs = torch.empty((P, N.PRIM_RECORD_FLOATS), dtype=f32, device=dev)
+    keys = torch.empty((P,), dtype=i32, device=dev)
+    order = torch.empty((P,), dtype=i32, device=dev)
+    keys_alt = torch.empty((P,), dtype=i32, device=dev)
+    vals_alt = torch.empty((P,), dtype=i32, device=dev)
+    counts_p = int(lib.cs_radix_counts_elems(P))
+    radix_counts = torch.empty((counts_p,), dtype=i32, device=dev)
+    scan_temp = torch.empty((int(lib.cs_scan_temp_elems(max(P, counts_p))),), dtype=i32,
+                            device=dev)
+    rank_offsets = torch.empty((P,), dtype=i32, device=dev)
+    status = torch.empty((4,), dtype=i32, device=dev)
+    st = N.stream(dev)
+    N.call("cs_bin_prepare", N.ptr(cubics_norm), N.ptr(seg_offsets), N.ptr(colors),
+           N.ptr(opacities), N.ptr(depths), N.ptr(fill_rules), N.ptr(widths),
+           N.ptr(stroke_widths), nseg, P, img_h, img_w, block_x, block_y, S, float(aabb_pad),
+           int(bool(aniso)), mode, N.ptr(cubics_px), N.ptr(seg_tile_ranges), N.ptr(seg_bbox),
+           N.ptr(edges), N.ptr(prim_tile_ranges), N.ptr(num_tiles_hit), N.ptr(inv_sigma2s),
+           N.ptr(prim_recs), N.ptr(keys), N.ptr(order), N.ptr(keys_alt), N.ptr(vals_alt),
+           N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(rank_offsets), N.ptr(status), st)
+    I, bad, first, last = status.tolist()
+    if bad or first != 0 or last != nseg:
+        raise ValueError(
+            "primitive_seg_offsets must start at 0 and end at num_segments "
+            f"(got start={first}, end={last}, num_segments={nseg})"
+            + ("; offsets are not non-decreasing within [0, num_segments]" if bad else ""))
+    if I < 0:
+        raise RuntimeError(f"intersection count overflowed int32 ({I})")
+    tile_keys = torch.empty((I,), dtype=i32, device=dev)
+    prim_ids = torch.empty((I,), dtype=i32, device=dev)
+    tile_bins = torch.empty((tbx * tby, 2), dtype=i32, device=dev)
+    if I > 0:
+        kalt = torch.empty((I,), dtype=i32, device=dev)
+        valt = torch.empty((I,), dtype=i32, device=dev)
+        counts_i = int(lib.cs_radix_counts_elems(I))
+        rc_i = torch.empty((counts_i,), dtype=i32, device=dev)
+        st_i = torch.empty((int(lib.cs_scan_temp_elems(counts_i)),), dtype=i32, device=dev)
+    else:
+        kalt = valt = rc_i = st_i = None
+    N.call("cs_bin_finish", N.ptr(order), N.ptr(prim_tile_ranges), N.ptr(rank_offsets), P, I,
+           img_h, img_w, block_x, block_y, N.ptr(tile_keys), N.ptr(prim_ids), N.ptr(kalt),
+           N.ptr(valt), N.ptr(rc_i), N.ptr(st_i), N.ptr(tile_bins), st)
+    return Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P,
+                  num_intersects=I, cubics_px=cubics_px, seg_tile_ranges=seg_tile_ranges,
+                  seg_bbox=seg_bbox, edges=edges, prim_tile_ranges=prim_tile_ranges,
+                  num_tiles_hit=num_tiles_hit, inv_sigma2s=inv_sigma2s, prim_recs=prim_recs,
+                  order=order, primitive_ids_sorted=prim_ids, tile_keys_sorted=tile_keys,
+                  tile_bins=tile_bins)
+
+
+def rasterize_forward(b: Binned, background: torch.Tensor):
+    dev = b.edges.device
+    out = torch.empty((b.img_h, b.img_w, 3), dtype=torch.float32, device=dev)
+    final_T = torch.empty((b.img_h, b.img_w), dtype=torch.float32, device=dev)
+    final_idx = torch.empty((b.img_h, b.img_w), dtype=torch.int32, device=dev)
+    N.call("cs_rasterize_forward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
+           N.ptr(b.edges), N.ptr(b.seg_bbox), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
+           b.img_w, b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx),
+           N.stream(dev))
+    return out, final_T, final_idx
+
+
+def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
+                       curve_contrib_rgb=None, curve_isect_contrib=None):
+    """Returns (v_edges [E,4], v_colors [P,3], v_opacities [P], v_inv_sigma2s [P],
+    v_stroke_widths [P] or None), accumulating into fresh zero buffers."""
+    dev = b.edges.device
+    P = b.nprim
+    v_edges = torch.zeros((b.edges.shape[0], 4), dtype=torch.float32, device=dev)
+    v_colors = torch.zeros((P, 3), dtype=torch.float32, device=dev)
+    v_opac = torch.zeros((P,), dtype=torch.float32, device=dev)
+    v_is2 = torch.zeros((P,), dtype=torch.float32, device=dev)
+    v_sw = torch.zeros((P,), dtype=torch.float32, device=dev) if b.mode == MODE_STROKE else None
+    N.call("cs_rasterize_backward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
+           N.ptr(b.edges), N.ptr(b.seg_bbox), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
+           b.img_w, b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(v_output),
+           N.ptr(v_edges), N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw),
+           N.ptr(curve_contrib_rgb), N.ptr(curve_isect_contrib), N.stream(dev))
+    return v_edges, v_colors, v_opac, v_is2, v_sw
+
+
+def accumulate_edge_grads(b: Binned, v_edges):
+    dev = v_edges.device
+    v_px = torch.empty((b.nseg, 4, 2), dtype=torch.float32, device=dev)
+    v_norm = torch.empty((b.nseg, 4, 2), dtype=torch.float32, device=dev)
+    N.call("cs_accumulate_edge_grads", N.ptr(v_edges), b.nseg, b.edges_per_segment, b.img_h,
+           b.img_w, N.ptr(v_px), N.ptr(v_norm), N.stream(dev))
+    return v_px, v_norm
+
+
+def aa_width_grads(widths, v_inv_sigma2s):
+    out = torch.empty_like(v_inv_sigma2s)
+    N.call("cs_aa_width_grads", N.ptr(widths), N.ptr(v_inv_sigma2s), int(widths.numel()),
+           N.ptr(out), N.stream(widths.device))
+    return out
+
+
+_NONE19 = (None,) * 19
+
+
+def _check_block(block_x: int, block_y: int) -> None:
+    if int(block_x) != BLOCK_X or int(block_y) != BLOCK_Y:
+        raise NotImplementedError(
+            f"the MI355X raster kernels use {BLOCK_X}x{BLOCK_Y} tiles; got {block_x}x{block_y}")
+
+
+def _check_flatten(method: str) -> None:
+    if method != CUBIC_FLATTEN_METHOD_BERNSTEIN:
+        raise NotImplementedError("only uniform Bernstein flattening is implemented on MI355X")
+
+
+def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacities, depths,
+                   fill_rules, stroke_widths, img_h, img_w, block_x, block_y, background,
+                   aabb_pad, aniso_intersects, aa_widths, distance_samples, flatten_method,
+                   process_fn):
+    flatten_method_norm = normalize_cubic_flatten_method(flatten_method)
+    num_segments = int(cubics_norm.shape[0])
+    offs = _i32(primitive_seg_offsets).view(-1)
+    num_primitives = max(0, int(offs.numel()) - 1)
+    bg = background.to(device=cubics_norm.device, dtype=torch.float32).view(3).contiguous()
+    ctx.img_h, ctx.img_w = int(img_h), int(img_w)
+    if num_primitives <= 0:
+        ctx.empty = True
+        return bg.view(1, 1, 3).expand(int(img_h), int(img_w), 3).clone()
+    N.require_gpu(cubics_norm, "cubics_norm")
+    for name, t, k in (("colors", colors, None), ("opacities", opacities, 1),
+                       ("depths", depths, 1), ("fill_rules", fill_rules, 1),
+                       ("stroke_widths", stroke_widths, 1)):
+        if t is None:
+            continue
+        n = int(t.shape[0]) if k is None else int(t.reshape(-1).shape[0])
+        if n != num_primitives:
+            raise ValueError(
+                f"{name} size must match primitive count ({num_primitives}), got {n}"
+                if k is not None else
+                f"colors first dim must match primitive count ({num_primitives}), got {n}")
+    widths = _f32(aa_widths).view(-1)
+    if int(widths.numel()) != num_primitives:
+        raise ValueError(
+            f"aa_widths size must match primitive count ({num_primitives}), "
+            f"got {int(widths.numel())}")
+    widths = torch.clamp(widths, min=1e-4)
+    _check_block(block_x, block_y)
+    _check_flatten(flatten_method_norm)
+
+    colors_c = _f32(colors)
+    opac_c = _f32(opacities).view(-1)
+    rules_c = _i32(fill_rules).view(-1) if fill_rules is not None else None
+    sw_c = _f32(stroke_widths).view(-1) if stroke_widths is not None else None
+    b = bin_primitives(_f32(cubics_norm), offs, colors_c, opac_c, _f32(depths).view(-1),
+                       rules_c, widths, sw_c, int(img_h), int(img_w), int(distance_samples),
+                       aabb_pad=float(aabb_pad), aniso=bool(aniso_intersects), mode=mode,
+                       block_x=int(block_x), block_y=int(block_y))
+    if b.num_intersects <= 0:
+        ctx.empty = True
+        return bg.view(1, 1, 3).expand(int(img_h), int(img_w), 3).clone()
+    out, final_T, final_idx = rasterize_forward(b, bg)
+    ctx.empty = False
+    ctx.binned = b
+    ctx.process_fn = process_fn
+    ctx.flatten_method = flatten_method_norm
+    ctx.distance_samples = int(distance_samples)
+    ctx.mode = mode
+    ctx.save_for_backward(cubics_norm, offs, colors_c, opac_c, depths, widths, bg, final_T,
+                          final_idx, sw_c if sw_c is not None else torch.empty(0))
+    return out
+
+
+def _splat_backward(ctx, grad_out_img):
+    b: Binned = ctx.binned
+    (cubics_norm, offs, colors, opacities, depths, widths, bg, final_T, final_idx,
+     stroke_widths) = ctx.saved_tensors
+    process_fn = ctx.process_fn
+    pre = _run_process_fn(process_fn, "pre_backward_rasterize", {
+        "collect_curve_contrib_rgb": False,
+        "collect_curve_isect_contrib": False,
+        "num_primitives": int(colors.shape[0]),
+        "colors": colors,
+    })
+    collect_rgb = bool(pre.get("collect_curve_contrib_rgb", False))
+    collect_isect = bool(pre.get("collect_curve_isect_contrib", False))
+    curve_contrib_rgb = torch.zeros_like(colors) if collect_rgb else None
+    curve_isect_contrib = (torch.zeros((b.num_intersects,), dtype=torch.float32,
+                                       device=colors.device) if collect_isect else None)
+    v_output = _f32(grad_out_img)
+    v_edges, v_colors, v_opac, v_is2, v_sw = rasterize_backward(
+        b, bg, final_T, final_idx, v_output, curve_contrib_rgb=curve_contrib_rgb,
+        curve_isect_contrib=curve_isect_contrib)
+    v_cubics_px, v_cubics_norm = accumulate_edge_grads(b, v_edges)
+    payload = {
+        "v_cubics_px": v_cubics_px,
+        "v_colors": v_colors,
+        "v_opacity": v_opac,
+        "curve_contrib_rgb": curve_contrib_rgb,
+        "curve_isect_contrib": curve_isect_contrib,
+        "primitive_ids_sorted": b.primitive_ids_sorted,
+        "tile_bins": b.tile_bins,
+        "colors": colors,
+        "opacities": opacities,
+        "primitive_seg_offsets": offs,
+    }
+    if ctx.mode == MODE_STROKE:
+        payload["v_stroke"] = v_sw
+        payload["stroke_widths"] = stroke_widths
+    if process_fn is not None:
+        payload = _run_process_fn(process_fn, "post_backward_rasterize", payload)
+        if payload["v_cubics_px"] is not v_cubics_px:
+            v_cubics_px = payload["v_cubics_px"]
+            half_w, half_h = 0.5 * float(ctx.img_w), 0.5 * float(ctx.img_h)
+            v_cubics_norm = torch.empty_like(v_cubics_px)
+            v_cubics_norm[..., 0] = v_cubics_px[..., 0] * half_w
+            v_cubics_norm[..., 1] = v_cubics_px[..., 1] * half_h
+        v_colors = payload["v_colors"]
+        v_opac = payload["v_opacity"]
+        if ctx.mode == MODE_STROKE:
+            v_sw = payload["v_stroke"]
+    v_depths = torch.zeros_like(depths, dtype=torch.float32)
+    v_aa = aa_width_grads(widths, v_is2)
+    return v_cubics_norm.view_as(cubics_norm), v_colors, v_opac.view_as(opacities), v_sw, \
+        v_depths, v_aa
+
+
+class _CubicFillSplatFunction(torch.autograd.Function):
+    """Signature of cubic_splatting.py:2750-2773; backward returns the 19-tuple
+    of cubic_splatting.py:3105-3125."""
+
+    @staticmethod
+    def forward(ctx, cubics_norm, primitive_seg_offsets, colors, opacities, depths, fill_rules,
+                img_h, img_w, block_x, block_y, background, project_threads, map_threads,
+                aabb_pad, aniso_intersects, aa_widths, distance_samples,
+                flatten_method=DEFAULT_CUBIC_FLATTEN_METHOD, process_fn=None):
+        return _splat_forward(ctx, MODE_FILL, cubics_norm, primitive_seg_offsets, colors,
+                              opacities, depths, fill_rules, None, img_h, img_w, block_x,
+                              block_y, background, aabb_pad, aniso_intersects, aa_widths,
+                              distance_samples, flatten_method, process_fn)
+
+    @staticmethod
+    def backward(ctx, grad_out_img):
+        if getattr(ctx, "empty", False):
+            return _NONE19
+        v_cub, v_col, v_op, _, v_dep, v_aa = _splat_backward(ctx, grad_out_img)
+        return (v_cub, None, v_col, v_op, v_dep, None, None, None, None, None, None, None,
+                None, None, None, v_aa, None, None, None)
+
+
+class _CubicPolylineSplatFunction(torch.autograd.Function):
+    """Signature of cubic_polyline_splatting.py:962-985; backward returns the
+    19-tuple of cubic_polyline_splatting.py:1318-1338."""
+
+    @staticmethod
+    def forward(ctx, cubics_norm, primitive_seg_offsets, colors, opacities, stroke_widths,
+                depths, img_h, img_w, block_x, block_y, background, project_threads,
+                map_threads, aabb_pad, aniso_intersects, aa_widths, distance_samples,
+                flatten_method=DEFAULT_CUBIC_FLATTEN_METHOD, process_fn=None):
+        return _splat_forward(ctx, MODE_STROKE, cubics_norm, primitive_seg_offsets, colors,
+                              opacities, depths, None, stroke_widths, img_h, img_w, block_x,
+                              block_y, background, aabb_pad, aniso_intersects, aa_widths,
+                              distance_samples, flatten_method, process_fn)
+
+    @staticmethod
+    def backward(ctx, grad_out_img):
+        if getattr(ctx, "empty", False):
+            return _NONE19
+        v_cub, v_col, v_op, v_sw, v_dep, v_aa = _splat_backward(ctx, grad_out_img)
+        return (v_cub, None, v_col, v_op, v_sw, v_dep, None, None, None, None, None, None,
+                None, None, None, v_aa, None, None, None)
+
+
+def _prim_vector(t, num_primitives, name, device, dtype, default):
+    if t is None:
+        return torch.full((num_primitives,), default, device=device, dtype=dtype)
+    out = t.to(device=device, dtype=dtype).view(-1)
+    if int(out.numel()) == 1 and num_primitives > 1:
+        out = out.expand(num_primitives)
+    if int(out.numel()) != num_primitives:
+        raise ValueError(
+            f"{name} size must match primitive count ({num_primitives}), got {int(out.numel())}")
+    return out
+
+
+def _common_checks(cubics_norm, offs, colors, opacities, depths, num_primitives,
+                   stroke_widths=None):
+    if int(colors.shape[0]) != num_primitives:
+        raise ValueError(
+            f"colors first dim must match primitive count ({num_primitives}), "
+            f"got {int(colors.shape[0])}")
+    if int(opacities.reshape(-1).shape[0]) != num_primitives:
+        raise ValueError(
+            f"opacities size must match primitive count ({num_primitives}), "
+            f"got {int(opacities.reshape(-1).shape[0])}")
+    if stroke_widths is not None and int(stroke_widths.reshape(-1).shape[0]) != num_primitives:
+        raise ValueError(
+            f"stroke_widths size must match primitive count ({num_primitives}), "
+            f"got {int(stroke_widths.reshape(-1).shape[0])}")
+    if int(depths.reshape(-1).shape[0]) != num_primitives:
+        raise ValueError(
+            f"depths size must match primitive count ({num_primitives}), "
+            f"got {int(depths.reshape(-1).shape[0])}")
+
+
+def render_cubic_fill_splat_tilelang(cubics_norm, primitive_seg_offsets, colors, opacities,
+                                     depths, img_h, img_w, block_x, block_y, background, *,
+                                     fill_rules=None, project_threads=DEFAULT_THREADS,
+                                     map_threads=DEFAULT_THREADS, aabb_pad=DEFAULT_AABB_PAD,
+                                     aniso_intersects=False, aa_widths=None,
+                                     aa_width=DEFAULT_AA_WIDTH,
+                                     distance_samples=DEFAULT_DISTANCE_SAMPLES,
+                                     flatten_method=DEFAULT_CUBIC_FLATTEN_METHOD,
+                                     process_fn=None):
+    """cubic_splatting.py:3128-3229 -> [H, W, 3] image."""
+    offs = _i32(primitive_seg_offsets).view(-1)
+    num_primitives = max(0, int(offs.numel()) - 1)
+    if num_primitives <= 0:
+        bg = background.to(device=cubics_norm.device, dtype=torch.float32).view(1, 1, 3)
+        return bg.expand(int(img_h), int(img_w), 3).clone()
+    _common_checks(cubics_norm, offs, colors, opacities, depths, num_primitives)
+    dev = cubics_norm.device
+    rules = _prim_vector(fill_rules, num_primitives, "fill_rules", dev, torch.int32, 1)
+    widths = torch.clamp(_prim_vector(aa_widths, num_primitives, "aa_widths", dev,
+                                      torch.float32, float(aa_width)).contiguous(), min=1e-4)
+    return _CubicFillSplatFunction.apply(
+        cubics_norm, offs.contiguous(), colors.contiguous(), opacities.reshape(-1).contiguous(),
+        depths.reshape(-1).contiguous(), rules.contiguous(), int(img_h), int(img_w),
+        int(block_x), int(block_y), background, int(project_threads), int(map_threads),
+        float(aabb_pad), bool(aniso_intersects), widths, int(distance_samples),
+        normalize_cubic_flatten_method(flatten_method), process_fn)
+
+
+def render_cubic_polyline_splat_tilelang(cubics_norm, primitive_seg_offsets, colors, opacities,
+                                         stroke_widths, depths, img_h, img_w, block_x, block_y,
+                                         background, *, project_threads=DEFAULT_THREADS,
+                                         map_threads=DEFAULT_THREADS,
+                                         aabb_pad=DEFAULT_AABB_PAD, aniso_intersects=False,
+                                         aa_widths=None, aa_width=DEFAULT_AA_WIDTH,
+                                         distance_samples=DEFAULT_DISTANCE_SAMPLES,
+                                         flatten_method=DEFAULT_CUBIC_FLATTEN_METHOD,
+                                         process_fn=None):
+    """cubic_polyline_splatting.py:1341-1432 -> [H, W, 3] image."""
+    offs = _i32(primitive_seg_offsets).view(-1)
+    num_primitives = max(0, int(offs.numel()) - 1)
+    if num_primitives <= 0:
+        bg = background.to(device=cubics_norm.device, dtype=torch.float32).view(1, 1, 3)
+        return bg.expand(int(img_h), int(img_w), 3).clone()
+    _common_checks(cubics_norm, offs, colors, opacities, depths, num_primitives, stroke_widths)
+    dev = cubics_norm.device
+    widths = torch.clamp(_prim_vector(aa_widths, num_primitives, "aa_widths", dev,
+                                      torch.float32, float(aa_width)).contiguous(), min=1e-4)
+    return _CubicPolylineSplatFunction.apply(
+        cubics_norm, offs.contiguous(), colors.contiguous(), opacities.reshape(-1).contiguous(),
+        stroke_widths.reshape(-1).contiguous(), depths.reshape(-1).contiguous(), int(img_h),
+        int(img_w), int(block_x), int(block_y), background, int(project_threads),
+        int(map_threads), float(aabb_pad), bool(aniso_intersects), widths,
+        int(distance_samples), normalize_cubic_flatten_method(flatten_method), process_fn)

@@ -1,0 +1,52 @@
+"""Shared test helpers: run the HIP path and the oracle on the same scene."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import oracle as O
+
+
+def scene_np(sc):
+    sw = None if sc.stroke_widths is None else sc.stroke_widths.cpu().numpy()
+    return dict(cubics_norm=sc.cubics_norm.cpu().numpy(), offs=sc.seg_offsets.cpu().numpy(),
+                colors=sc.colors.cpu().numpy(), opacities=sc.opacities.cpu().numpy(),
+                depths=sc.depths.cpu().numpy(), aa_widths=sc.aa_widths.cpu().numpy(),
+                fill_rules=sc.fill_rules.cpu().numpy(), background=sc.background.cpu().numpy(),
+                stroke_widths=sw, img_h=sc.img_h, img_w=sc.img_w, S=sc.S)
+
+
+def oracle_forward(sc, rows=None):
+    d = scene_np(sc)
+    return O.render_forward(d["cubics_norm"], d["offs"], d["colors"], d["opacities"], d["depths"],
+                            d["img_h"], d["img_w"], d["background"], fill_rules=d["fill_rules"],
+                            aa_widths=d["aa_widths"], S=d["S"], stroke_widths=d["stroke_widths"],
+                            rows=rows)
+
+
+def hip_bin(sc, device="cuda"):
+    from repo_amd import splat
+    s = sc.to(device)
+    mode = splat.MODE_FILL if s.stroke_widths is None else splat.MODE_STROKE
+    widths = torch.clamp(s.aa_widths.float(), min=1e-4).contiguous()
+    return splat.bin_primitives(
+        s.cubics_norm.contiguous(), s.seg_offsets.to(torch.int32).contiguous(),
+        s.colors.contiguous(), s.opacities.contiguous(), s.depths.contiguous(),
+        s.fill_rules.to(torch.int32).contiguous() if mode == 0 else None, widths,
+        None if s.stroke_widths is None else s.stroke_widths.contiguous(), s.img_h, s.img_w,
+        s.S, mode=mode), s
+
+
+def grad_scale_tol(got, ref, rtol=1e-4, floor=1e-30):
+    """|got - ref| <= rtol * max|ref| elementwise (scale-aware tolerance for
+    sums accumulated in a different order)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = max(float(np.abs(ref).max()) if ref.size else 0.0, floor)
+    err = float(np.abs(got - ref).max()) if ref.size else 0.0
+    return err <= rtol * scale, err / scale
+
+
+def random_v_out(h, w, seed=7):
+    g = torch.Generator("cpu").manual_seed(seed)
+    return torch.randn((h, w, 3), generator=g, dtype=torch.float32)

@@ -1,0 +1,153 @@
+"""Binning on the GPU vs the oracle: bit-exact (cubic_splatting.py:2815-2908)."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import hip_bin, scene_np
+from oracle import oracle as O
+from repo_amd import synth
+
+SCENES = {
+    "small_fill": lambda: synth.small_scene(0),
+    "small_fill_big": lambda: synth.small_scene(3, P=40, h=100, w=130, rmax=60.0),
+    "small_stroke": lambda: synth.small_scene(1, stroke=True),
+    "cfg1": lambda: synth.make_scene(1),
+    "cfg2": lambda: synth.make_scene(2),
+    "cfg3": lambda: synth.make_scene(3),
+    "cfg4": lambda: synth.make_scene(4),
+    "cfg5_quarter": lambda: synth.make_scene(5, scale=0.25),
+}
+
+
+def _bits(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.int32) if a.dtype == np.float32 else a
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", list(SCENES))
+def test_binning_bit_exact(name):
+    print(f"[binning] {name}", flush=True)
+    sc = SCENES[name]()
+    b, _ = hip_bin(sc)
+    d = scene_np(sc)
+    ob = O.bin_scene(d["cubics_norm"], d["offs"], d["depths"], d["aa_widths"], d["img_h"],
+                     d["img_w"], d["S"], stroke_widths=d["stroke_widths"])
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(b.cubics_px.cpu().numpy()), _bits(ob["cubics_px"]))
+    np.testing.assert_array_equal(b.seg_tile_ranges.cpu().numpy(), ob["seg_tile_ranges"])
+    np.testing.assert_array_equal(b.prim_tile_ranges.cpu().numpy(), ob["prim_tile_ranges"])
+    np.testing.assert_array_equal(b.num_tiles_hit.cpu().numpy(), ob["num_tiles_hit"])
+    np.testing.assert_array_equal(_bits(b.edges_px().cpu().numpy()), _bits(ob["edges"]))
+    np.testing.assert_array_equal(_bits(b.inv_sigma2s.cpu().numpy()), _bits(ob["inv_sigma2s"]))
+    assert b.num_intersects == ob["primitive_ids_sorted"].shape[0]
+    np.testing.assert_array_equal(b.primitive_ids_sorted.cpu().numpy(),
+                                  ob["primitive_ids_sorted"])
+    np.testing.assert_array_equal(b.tile_bins.cpu().numpy(), ob["tile_bins"])
+    np.testing.assert_array_equal(b.tile_keys_sorted.cpu().numpy().astype(np.int64),
+                                  ob["isect_ids_sorted"] >> 32)
+
+
+@pytest.mark.gpu
+def test_binning_ties_stable_by_primitive_id():
+    """Equal depths (the training default, depth = sigmoid(1)) order each tile
+    list by primitive id (stable sort of primitive-major emission)."""
+    sc = synth.small_scene(5, P=30, h=64, w=64, rmax=30.0)
+    sc.depths = torch.full_like(sc.depths, 0.7310586)
+    b, _ = hip_bin(sc)
+    d = scene_np(sc)
+    ob = O.bin_scene(d["cubics_norm"], d["offs"], d["depths"], d["aa_widths"], d["img_h"],
+                     d["img_w"], d["S"])
+    ids = b.primitive_ids_sorted.cpu().numpy()
+    np.testing.assert_array_equal(ids, ob["primitive_ids_sorted"])
+    bins = b.tile_bins.cpu().numpy()
+    for s, e in bins:
+        assert np.all(np.diff(ids[s:e]) > 0)
+
+
+@pytest.mark.gpu
+def test_reference_layout_blocks():
+    """project / primitive ranges / map / tile bins with the reference's own
+    layouts (int64 keys) match the oracle, and the reference's pipeline on
+    those blocks (torch.sort stable) yields the fused path's lists."""
+    from repo_amd import blocks
+    sc = synth.make_scene(2)
+    d = scene_np(sc)
+    dev = "cuda"
+    P = sc.num_primitives
+    w, inv, support = O.prim_params(d["aa_widths"], P)
+    counts = np.diff(d["offs"])
+    sup_seg = np.repeat(support, counts)
+    sw_seg = np.zeros(sup_seg.shape, np.float32)
+    tb = (48, 32, 1)
+    px, tr, nh = blocks.project_cubics_2d_forward_tilelang(
+        sc.cubics_norm.to(dev), torch.from_numpy(sw_seg).to(dev),
+        torch.from_numpy(sup_seg).to(dev), sc.img_h, sc.img_w, tb)
+    opx, otr, onh = O.project_cubics(d["cubics_norm"], sw_seg, sup_seg, sc.img_h, sc.img_w)
+    np.testing.assert_array_equal(_bits(px.cpu().numpy()), _bits(opx))
+    np.testing.assert_array_equal(tr.cpu().numpy(), otr)
+    np.testing.assert_array_equal(nh.cpu().numpy(), onh)
+    ptr, phit = blocks.primitive_tile_ranges_from_segment_tile_ranges(
+        tr, sc.seg_offsets.to(dev), tb)
+    optr, ophit = O.prim_tile_ranges(otr, d["offs"], 48, 32)
+    np.testing.assert_array_equal(ptr.cpu().numpy(), optr)
+    np.testing.assert_array_equal(phit.cpu().numpy(), ophit)
+    cum = torch.cumsum(phit, 0, dtype=torch.int32)
+    keys, ids = blocks.map_cubic_to_intersects_tilelang(ptr, sc.depths.to(dev), cum, tb)
+    okeys, oids = O.map_intersects(optr, d["depths"], np.cumsum(ophit), 48)
+    np.testing.assert_array_equal(keys.cpu().numpy(), okeys)
+    np.testing.assert_array_equal(ids.cpu().numpy(), oids)
+    skeys, order = torch.sort(keys, stable=True)
+    bins = blocks.get_tile_bin_edges_tilelang(int(keys.numel()), skeys, num_tiles=48 * 32,
+                                              compact=True)
+    b, _ = hip_bin(sc)
+    np.testing.assert_array_equal(bins.cpu().numpy(), b.tile_bins.cpu().numpy())
+    np.testing.assert_array_equal(ids[order].cpu().numpy(), b.primitive_ids_sorted.cpu().numpy())
+    ranges = blocks.build_fill_isect_edge_ranges(b.primitive_ids_sorted, sc.seg_offsets.to(dev),
+                                                 sc.S - 1)
+    off_e = d["offs"].astype(np.int64) * (sc.S - 1)
+    pid = b.primitive_ids_sorted.cpu().numpy()
+    np.testing.assert_array_equal(ranges.cpu().numpy(), np.stack([off_e[pid], off_e[pid + 1]], 1))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,bits", [(0, 8), (1, 32), (2, 1), (255, 8), (4096, 14), (4097, 14),
+                                    (100003, 32), (300001, 17)])
+def test_radix_sort_stable(n, bits):
+    from repo_amd import _native as N
+    g = np.random.default_rng(n + bits)
+    hi = min(1 << bits, 1 << 31) if bits < 32 else 1 << 32
+    keys = g.integers(0, hi, size=n, dtype=np.uint64).astype(np.uint32)
+    keys[: n // 3] = keys[0] if n else 0  # many duplicates
+    vals = np.arange(n, dtype=np.int32)
+    dev = "cuda"
+    k = torch.from_numpy(keys.view(np.int32)).to(dev)
+    v = torch.from_numpy(vals).to(dev)
+    ka = torch.empty_like(k)
+    va = torch.empty_like(v)
+    L = N.lib()
+    cnt = torch.empty((int(L.cs_radix_counts_elems(n)),), dtype=torch.int32, device=dev)
+    tmp = torch.empty((int(L.cs_scan_temp_elems(int(cnt.numel()))),), dtype=torch.int32,
+                      device=dev)
+    N.call("cs_radix_sort_pairs_u32", N.ptr(k), N.ptr(v), N.ptr(ka), N.ptr(va), n, bits,
+           N.ptr(cnt), N.ptr(tmp), N.stream())
+    order = np.argsort(keys, kind="stable")
+    np.testing.assert_array_equal(v.cpu().numpy(), vals[order])
+    np.testing.assert_array_equal(k.cpu().numpy().view(np.uint32), keys[order])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 5, 4096, 4097, 1000003])
+def test_exclusive_scan(n):
+    from repo_amd import _native as N
+    g = np.random.default_rng(n)
+    x = g.integers(0, 200, size=n).astype(np.int32)
+    dev = "cuda"
+    xi = torch.from_numpy(x).to(dev)
+    out = torch.empty_like(xi)
+    tot = torch.empty((1,), dtype=torch.int32, device=dev)
+    tmp = torch.empty((int(N.lib().cs_scan_temp_elems(n)),), dtype=torch.int32, device=dev)
+    N.call("cs_scan_exclusive_u32", N.ptr(xi), N.ptr(out), n, N.ptr(tmp), N.ptr(tot), N.stream())
+    ref = np.concatenate([[0], np.cumsum(x)[:-1]])
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    assert int(tot.item()) == int(x.sum())

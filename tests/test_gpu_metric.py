@@ -1,0 +1,93 @@
+"""MSE / SSIM / PSNR on the GPU vs float64 restatements (metric.py:64-273).
+
+Tolerances: losses within 1e-5 relative; gradients within 1e-4 of the largest
+reference gradient (the GPU sums in fp32, the reference in float64).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+SHAPES = [(1, 3, 37, 53), (2, 3, 40, 50), (1, 3, 512, 768), (1, 3, 1356, 2040)]
+
+
+def _pair(shape, seed):
+    g = torch.Generator("cpu").manual_seed(seed)
+    x = torch.rand(shape, generator=g)
+    y = (x + 0.2 * torch.randn(shape, generator=g)).clamp(0, 1)
+    return x, y
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", SHAPES)
+def test_mse_forward_backward(shape):
+    import manbo
+    x, y = _pair(shape, 1)
+    xd = x.cuda().requires_grad_(True)
+    yd = y.cuda().requires_grad_(True)
+    loss = manbo.mse_loss_tilelang(xd, yd)
+    ref = O.mse(x.numpy(), y.numpy())
+    assert abs(float(loss) - ref) <= 1e-5 * ref
+    (loss * 3.0).backward()
+    n = x.numel()
+    s = np.float32(3.0) * np.float32(2.0 / n)
+    gref = s * (x.numpy() - y.numpy())
+    np.testing.assert_allclose(xd.grad.cpu().numpy(), gref, rtol=1e-6, atol=1e-12)
+    np.testing.assert_array_equal(yd.grad.cpu().numpy(), -xd.grad.cpu().numpy())
+
+
+@pytest.mark.gpu
+def test_mse_repeated_calls_reset_ticket():
+    import manbo
+    x, y = _pair((1, 3, 64, 64), 2)
+    vals = [float(manbo.mse_loss_tilelang(x.cuda(), y.cuda())) for _ in range(5)]
+    assert len(set(vals)) == 1
+
+
+@pytest.mark.gpu
+def test_psnr():
+    import manbo
+    x, y = _pair((1, 3, 100, 120), 3)
+    p = float(manbo.psnr(x.cuda(), y.cuda()))
+    ref = 10.0 * np.log10(1.0 / (O.mse(x.numpy(), y.numpy()) + 1e-12))
+    assert abs(p - ref) < 1e-4
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", SHAPES[:3])
+def test_ssim_forward(shape):
+    import manbo
+    x, y = _pair(shape, 4)
+    s = float(manbo.ssim(x.cuda(), y.cuda()))
+    ref = float(O.ssim_torch64(x.double(), y.double()))
+    assert abs(s - ref) <= 1e-5 * abs(ref), (s, ref)
+    one = float(manbo.ssim(x.cuda(), x.cuda()))
+    assert abs(one - 1.0) < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("win", [7, 11])
+def test_ssim_backward(win):
+    import manbo
+    x, y = _pair((1, 3, 96, 128), 5)
+    xd = x.cuda().requires_grad_(True)
+    s = manbo.ssim(xd, y.cuda(), win_size=win)
+    (2.0 * s).backward()
+    x64 = x.double().requires_grad_(True)
+    r = O.ssim_torch64(x64, y.double(), win_size=win)
+    (2.0 * r).backward()
+    got = xd.grad.cpu().numpy().astype(np.float64)
+    ref = x64.grad.numpy()
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err <= 1e-4, err
+    assert abs(float(s) - float(r)) <= 1e-5
+
+
+@pytest.mark.gpu
+def test_ssim_per_image_means():
+    import manbo
+    x, y = _pair((2, 3, 40, 44), 6)
+    per = manbo.ssim(x.cuda(), y.cuda(), size_average=False).cpu().numpy()
+    ref = [float(O.ssim_torch64(x[i:i + 1].double(), y[i:i + 1].double())) for i in range(2)]
+    np.testing.assert_allclose(per, ref, rtol=1e-5)
