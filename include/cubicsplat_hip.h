@@ -123,15 +123,16 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
                          int32_t* final_idx, hipStream_t stream);
 
 /* rasterize_cubic_fill_backward_kernel (ops/cubic_splatting.py:1197-1651) /
- * rasterize_cubic_polyline_backward_kernel (ops/cubic_polyline_splatting.py:252-660).
- * Accumulates (atomically) into zero-initialised v_edges [E,2,2],
+ * rasterize_cubic_polyline_backward_kernel (ops/cubic_polyline_splatting.py:252-660)
+ * fused with _accumulate_edge_grads_to_cubics (ops/cubic_splatting.py:2308-2396):
+ * accumulates (atomically) into zero-initialised v_cubics_px [nseg,4,2],
  * v_colors [P,3], v_opacities [P], v_inv_sigma2s [P], v_stroke_widths [P]
  * (mode 1), and optionally curve_contrib_rgb [P,3] / curve_isect_contrib [I]. */
 int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
                           const void* edges, const float* seg_bbox, const void* prim_recs,
                           const float* background, int32_t img_h, int32_t img_w,
                           int32_t edges_per_segment, const float* final_Ts,
-                          const int32_t* final_idx, const float* v_output, float* v_edges,
+                          const int32_t* final_idx, const float* v_output, float* v_cubics_px,
                           float* v_colors, float* v_opacities, float* v_inv_sigma2s,
                           float* v_stroke_widths, float* curve_contrib_rgb,
                           float* curve_isect_contrib, hipStream_t stream);
@@ -142,9 +143,11 @@ int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg, int32_t edges_p
                              int32_t img_h, int32_t img_w, float* v_cubics_px,
                              float* v_cubics_norm, hipStream_t stream);
 
-/* v_aa_widths = -2 v_inv_sigma2 / max(w^3, 1e-12) (ops/cubic_splatting.py:3103-3104). */
-int cs_aa_width_grads(const float* widths, const float* v_inv_sigma2s, int32_t nprim,
-                      float* v_aa_widths, hipStream_t stream);
+/* Backward epilogue (ops/cubic_splatting.py:3096-3104): v_cubics_norm =
+ * v_cubics_px * (W/2, H/2) and v_aa_widths = -2 v_inv_sigma2 / max(w^3, 1e-12). */
+int cs_backward_finalize(const float* v_cubics_px, int32_t nseg, int32_t img_h, int32_t img_w,
+                         const float* widths, const float* v_inv_sigma2s, int32_t nprim,
+                         float* v_cubics_norm, float* v_aa_widths, hipStream_t stream);
 
 /* ---------------- losses ---------------- */
 

@@ -86,6 +86,28 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// DPP move with zero for out-of-row sources (row_shr) or row broadcast.
+template <int CTRL, int ROW_MASK, bool ZERO_OOB>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf,
+                                           ZERO_OOB));
+}
+
+// Sum over the 64 lanes with six DPP adds; the total lands in lane 63.  Every
+// lane must be active (call it outside divergent code, with non-contributing
+// lanes holding 0).  row_shr 1,2,4,8 sums each 16-lane row into its lane 15;
+// row_bcast:15 (rows 1,3) and row_bcast:31 (rows 2,3) combine the rows.
+__device__ __forceinline__ float wave_sum_lane63(float x) {
+    x += dpp_f32<0x111, 0xf, true>(x);
+    x += dpp_f32<0x112, 0xf, true>(x);
+    x += dpp_f32<0x114, 0xf, true>(x);
+    x += dpp_f32<0x118, 0xf, true>(x);
+    x += dpp_f32<0x142, 0xa, false>(x);
+    x += dpp_f32<0x143, 0xc, false>(x);
+    return x;
+}
+
 __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off, kWave));

@@ -200,6 +200,26 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
     }
 }
 
+// Reference cubic-accumulation basis at t = e / eps (cubic_splatting.py:2353-2371).
+__device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
+    const float t = (float)e * inv_e;
+    const float o = 1.0f - t;
+    const float o2 = o * o, t2 = t * t;
+    b[0] = o2 * o;
+    b[1] = 3.0f * o2 * t;
+    b[2] = 3.0f * o * t2;
+    b[3] = t2 * t;
+}
+
+// Backward: the reverse traversal of cubic_splatting.py:1339-1649 (fill) and
+// cubic_polyline_splatting.py:393-658 (stroke).  Per-pixel terms are those of
+// the reference; the sums differ in how they are formed:
+//   * per-primitive gradients: DPP wave sum, one atomic per wave and entry;
+//   * geometry: each lane folds its best edge's endpoint gradients straight
+//     into the 8 control-point gradients of the edge's cubic segment with the
+//     reference's accumulation weights (cubic_splatting.py:2308-2396), then
+//     lanes that share a segment are summed (one leader pass per distinct
+//     segment) and one lane adds the 8 values to v_cubics_px.
 template <int MODE>
 __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     const int32_t* __restrict__ prim_ids, const int32_t* __restrict__ bins,
@@ -207,7 +227,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     const PrimRec* __restrict__ prims, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, int eps, const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
-    float* __restrict__ v_edges, float* __restrict__ v_colors, float* __restrict__ v_opac,
+    float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
     float* __restrict__ isect_contrib) {
     const int tile = xcd_tile(blockIdx.x, ntiles);
@@ -232,6 +252,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     const float v2 = in_img ? v_out[3 * pix + 2] : 0.0f;
     const float bg_dot = __builtin_fmaf(bg[2], v2, __builtin_fmaf(bg[1], v1, bg[0] * v0));
     const bool want_contrib = (contrib_rgb != nullptr) | (isect_contrib != nullptr);
+    const float inv_e = 1.0f / (float)eps;
     float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
     const int gstart = min(g1 - 1, wave_max_i(fidx));
     for (int g = gstart; g >= g0; --g) {
@@ -245,9 +266,8 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
         prim_geometry<MODE, true>(pr, R, D2, seg_bbox, edges, eps, px, py, G);
         float vr = 0.0f, vg = 0.0f, vb = 0.0f, vop = 0.0f, vis2 = 0.0f, vsw = 0.0f;
         float cr = 0.0f, cg = 0.0f, cb = 0.0f;
-        float e0 = 0.0f, e1 = 0.0f, e2 = 0.0f, e3 = 0.0f;
-        int gbest = -1;
-        bool contrib = false;
+        float gx = 0.0f, gy = 0.0f;
+        bool contrib = false, geom = false;
         if (valid) {
             const Cov c = coverage<MODE>(pr, G);
             const float op = pr.opacity;
@@ -274,8 +294,6 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
                 b2 = __builtin_fmaf(pr.b, fac, b2);
                 if (alpha < kAlphaCap) {
                     vop = c.cov * va;
-                    float gx = 0.0f, gy = 0.0f;
-                    bool geom = false;
                     if (MODE == 0) {
                         const float v_cov = op * va;
                         const float v_logit = -v_cov * c.cov * (1.0f - c.cov);
@@ -300,29 +318,23 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
                             }
                         }
                     }
-                    if (geom) {
-                        gbest = G.best;
-                        e0 = (1.0f - G.bproj) * gx;
-                        e1 = (1.0f - G.bproj) * gy;
-                        e2 = G.bproj * gx;
-                        e3 = G.bproj * gy;
-                    }
                 }
             }
         }
         if (__ballot(contrib) == 0) continue;
-        vr = wave_sum(vr);
-        vg = wave_sum(vg);
-        vb = wave_sum(vb);
-        vop = wave_sum(vop);
-        vis2 = wave_sum(vis2);
-        if (MODE == 1) vsw = wave_sum(vsw);
+        // Per-primitive gradients: one DPP sum each, lane 63 adds.
+        vr = wave_sum_lane63(vr);
+        vg = wave_sum_lane63(vg);
+        vb = wave_sum_lane63(vb);
+        vop = wave_sum_lane63(vop);
+        vis2 = wave_sum_lane63(vis2);
+        if (MODE == 1) vsw = wave_sum_lane63(vsw);
         if (want_contrib) {
-            cr = wave_sum(cr);
-            cg = wave_sum(cg);
-            cb = wave_sum(cb);
+            cr = wave_sum_lane63(cr);
+            cg = wave_sum_lane63(cg);
+            cb = wave_sum_lane63(cb);
         }
-        if (lane == 0) {
+        if (lane == kWave - 1) {
             atomicAdd(v_colors + 3 * pid + 0, vr);
             atomicAdd(v_colors + 3 * pid + 1, vg);
             atomicAdd(v_colors + 3 * pid + 2, vb);
@@ -336,12 +348,39 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
             }
             if (isect_contrib) atomicAdd(isect_contrib + g, cr + cg + cb);
         }
-        if (gbest >= 0) {
-            float* ve = v_edges + 4 * (size_t)gbest;
-            atomicAdd(ve + 0, e0);
-            atomicAdd(ve + 1, e1);
-            atomicAdd(ve + 2, e2);
-            atomicAdd(ve + 3, e3);
+        // Geometry: endpoint gradients ((1-t) g, t g) of the best edge, folded
+        // into its segment's control points.
+        uint64_t pending = __ballot(geom);
+        if (pending == 0) continue;
+        int gseg = -1;
+        float cp[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) cp[k] = 0.0f;
+        if (geom) {
+            gseg = G.best / eps;
+            const int el = G.best - gseg * eps;
+            float bs[4], be[4];
+            seg_basis(el, inv_e, bs);
+            seg_basis(el + 1, inv_e, be);
+            const float sx = (1.0f - G.bproj) * gx, sy = (1.0f - G.bproj) * gy;
+            const float ex = G.bproj * gx, ey = G.bproj * gy;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                cp[2 * k] = __builtin_fmaf(ex, be[k], sx * bs[k]);
+                cp[2 * k + 1] = __builtin_fmaf(ey, be[k], sy * bs[k]);
+            }
+        }
+        while (pending) {
+            const int leader = (int)__builtin_ctzll(pending);
+            const int s = __builtin_amdgcn_readlane(gseg, leader);
+            const bool mine = gseg == s;
+            pending &= ~__ballot(mine);
+            float* dst = v_cubics + 8 * (size_t)s;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float t = wave_sum_lane63(mine ? cp[k] : 0.0f);
+                if (lane == kWave - 1) atomicAdd(dst + k, t);
+            }
         }
     }
 }
@@ -357,11 +396,9 @@ __global__ __launch_bounds__(256) void k_accumulate(const float4* __restrict__ v
     const float inv_e = 1.0f / (float)eps;
     float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int e = 0; e < eps; ++e) {
-        const float t0 = (float)e * inv_e, t1 = (float)(e + 1) * inv_e;
-        const float o0 = 1.0f - t0, o1 = 1.0f - t1;
-        const float o0s = o0 * o0, o1s = o1 * o1, t0s = t0 * t0, t1s = t1 * t1;
-        const float bs[4] = {o0s * o0, 3.0f * o0s * t0, 3.0f * o0 * t0s, t0s * t0};
-        const float be[4] = {o1s * o1, 3.0f * o1s * t1, 3.0f * o1 * t1s, t1s * t1};
+        float bs[4], be[4];
+        seg_basis(e, inv_e, bs);
+        seg_basis(e + 1, inv_e, be);
         const float4 gr = v_edges[(size_t)s * eps + e];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -380,13 +417,20 @@ __global__ __launch_bounds__(256) void k_accumulate(const float4* __restrict__ v
     }
 }
 
-__global__ __launch_bounds__(256) void k_aa_grads(const float* __restrict__ widths,
+// v_cubics_norm = v_cubics_px * (W/2, H/2) (cubic_splatting.py:3096-3100) and
+// v_aa_widths = -2 v_inv_sigma2 / max(w^3, 1e-12) (cubic_splatting.py:3103-3104).
+__global__ __launch_bounds__(256) void k_finalize(const float* __restrict__ v_px, int nseg,
+                                                 float half_w, float half_h,
+                                                 const float* __restrict__ widths,
                                                  const float* __restrict__ v_is2, int P,
+                                                 float* __restrict__ v_norm,
                                                  float* __restrict__ v_aa) {
-    const int p = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= P) return;
-    const float w = widths[p];
-    v_aa[p] = (-2.0f * v_is2[p]) / fmaxf(w * w * w, (float)1e-12);
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < nseg * 8) v_norm[t] = v_px[t] * ((t & 1) ? half_h : half_w);
+    if (t < P) {
+        const float w = widths[t];
+        v_aa[t] = (-2.0f * v_is2[t]) / fmaxf(w * w * w, (float)1e-12);
+    }
 }
 
 }  // namespace cs
@@ -427,7 +471,7 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                                      const float* background, int32_t img_h, int32_t img_w,
                                      int32_t edges_per_segment, const float* final_Ts,
                                      const int32_t* final_idx, const float* v_output,
-                                     float* v_edges, float* v_colors, float* v_opacities,
+                                     float* v_cubics_px, float* v_colors, float* v_opacities,
                                      float* v_inv_sigma2s, float* v_stroke_widths,
                                      float* curve_contrib_rgb, float* curve_isect_contrib,
                                      hipStream_t stream) {
@@ -442,15 +486,15 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
     if (mode == 0)
         hipLaunchKernelGGL(k_raster_bwd<0>, dim3(nt), dim3(kBlockThreads), 0, stream,
                            prim_ids_sorted, tile_bins, E, B, P, background, img_h, img_w, tbx, nt,
-                           edges_per_segment, final_Ts, final_idx, v_output, v_edges, v_colors,
-                           v_opacities, v_inv_sigma2s, v_stroke_widths, curve_contrib_rgb,
-                           curve_isect_contrib);
+                           edges_per_segment, final_Ts, final_idx, v_output, v_cubics_px,
+                           v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
+                           curve_contrib_rgb, curve_isect_contrib);
     else
         hipLaunchKernelGGL(k_raster_bwd<1>, dim3(nt), dim3(kBlockThreads), 0, stream,
                            prim_ids_sorted, tile_bins, E, B, P, background, img_h, img_w, tbx, nt,
-                           edges_per_segment, final_Ts, final_idx, v_output, v_edges, v_colors,
-                           v_opacities, v_inv_sigma2s, v_stroke_widths, curve_contrib_rgb,
-                           curve_isect_contrib);
+                           edges_per_segment, final_Ts, final_idx, v_output, v_cubics_px,
+                           v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
+                           curve_contrib_rgb, curve_isect_contrib);
     return raster_status();
 }
 
@@ -467,11 +511,17 @@ extern "C" int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg,
     return raster_status();
 }
 
-extern "C" int cs_aa_width_grads(const float* widths, const float* v_inv_sigma2s, int32_t nprim,
-                                 float* v_aa_widths, hipStream_t stream) {
-    if (nprim < 0) return CS_ERR_ARGS;
-    if (nprim == 0) return CS_OK;
-    hipLaunchKernelGGL(k_aa_grads, dim3((nprim + 255) / 256), dim3(256), 0, stream, widths,
-                       v_inv_sigma2s, nprim, v_aa_widths);
+extern "C" int cs_backward_finalize(const float* v_cubics_px, int32_t nseg, int32_t img_h,
+                                    int32_t img_w, const float* widths,
+                                    const float* v_inv_sigma2s, int32_t nprim,
+                                    float* v_cubics_norm, float* v_aa_widths,
+                                    hipStream_t stream) {
+    if (nseg < 0 || nprim < 0) return CS_ERR_ARGS;
+    const int64_t n = (int64_t)nseg * 8 > nprim ? (int64_t)nseg * 8 : nprim;
+    if (n == 0) return CS_OK;
+    const float half_w = (float)(0.5 * (double)img_w), half_h = (float)(0.5 * (double)img_h);
+    hipLaunchKernelGGL(k_finalize, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       v_cubics_px, nseg, half_w, half_h, widths, v_inv_sigma2s, nprim,
+                       v_cubics_norm, v_aa_widths);
     return raster_status();
 }

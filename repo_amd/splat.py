@@ -191,24 +191,30 @@ def rasterize_forward(b: Binned, background: torch.Tensor):
 
 def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
                        curve_contrib_rgb=None, curve_isect_contrib=None):
-    """Returns (v_edges [E,4], v_colors [P,3], v_opacities [P], v_inv_sigma2s [P],
-    v_stroke_widths [P] or None), accumulating into fresh zero buffers."""
+    """Returns (v_cubics_px [nseg,4,2], v_colors [P,3], v_opacities [P],
+    v_inv_sigma2s [P], v_stroke_widths [P] or None), accumulated into fresh
+    zero buffers (cubic_splatting.py:2572-2747)."""
     dev = b.edges.device
     P = b.nprim
-    v_edges = torch.zeros((b.edges.shape[0], 4), dtype=torch.float32, device=dev)
-    v_colors = torch.zeros((P, 3), dtype=torch.float32, device=dev)
-    v_opac = torch.zeros((P,), dtype=torch.float32, device=dev)
-    v_is2 = torch.zeros((P,), dtype=torch.float32, device=dev)
-    v_sw = torch.zeros((P,), dtype=torch.float32, device=dev) if b.mode == MODE_STROKE else None
+    zeros = torch.zeros((b.nseg * 8 + P * (6 if b.mode == MODE_STROKE else 5),),
+                        dtype=torch.float32, device=dev)
+    v_px = zeros[: b.nseg * 8].view(b.nseg, 4, 2)
+    rest = zeros[b.nseg * 8:]
+    v_colors = rest[: 3 * P].view(P, 3)
+    v_opac = rest[3 * P: 4 * P]
+    v_is2 = rest[4 * P: 5 * P]
+    v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
     N.call("cs_rasterize_backward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
            N.ptr(b.edges), N.ptr(b.seg_bbox), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
            b.img_w, b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(v_output),
-           N.ptr(v_edges), N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw),
+           N.ptr(v_px), N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw),
            N.ptr(curve_contrib_rgb), N.ptr(curve_isect_contrib), N.stream(dev))
-    return v_edges, v_colors, v_opac, v_is2, v_sw
+    return v_px, v_colors, v_opac, v_is2, v_sw
 
 
 def accumulate_edge_grads(b: Binned, v_edges):
+    """Reference building block (cubic_splatting.py:2308-2396): v_edges [E,4]
+    -> (v_cubics_px, v_cubics_norm)."""
     dev = v_edges.device
     v_px = torch.empty((b.nseg, 4, 2), dtype=torch.float32, device=dev)
     v_norm = torch.empty((b.nseg, 4, 2), dtype=torch.float32, device=dev)
@@ -217,11 +223,14 @@ def accumulate_edge_grads(b: Binned, v_edges):
     return v_px, v_norm
 
 
-def aa_width_grads(widths, v_inv_sigma2s):
-    out = torch.empty_like(v_inv_sigma2s)
-    N.call("cs_aa_width_grads", N.ptr(widths), N.ptr(v_inv_sigma2s), int(widths.numel()),
-           N.ptr(out), N.stream(widths.device))
-    return out
+def backward_finalize(b: Binned, v_cubics_px, widths, v_inv_sigma2s):
+    """(v_cubics_norm, v_aa_widths) in one launch (cubic_splatting.py:3096-3104)."""
+    dev = v_cubics_px.device
+    v_norm = torch.empty_like(v_cubics_px)
+    v_aa = torch.empty_like(v_inv_sigma2s)
+    N.call("cs_backward_finalize", N.ptr(v_cubics_px), b.nseg, b.img_h, b.img_w, N.ptr(widths),
+           N.ptr(v_inv_sigma2s), int(widths.numel()), N.ptr(v_norm), N.ptr(v_aa), N.stream(dev))
+    return v_norm, v_aa
 
 
 _NONE19 = (None,) * 19
@@ -312,10 +321,9 @@ def _splat_backward(ctx, grad_out_img):
     curve_isect_contrib = (torch.zeros((b.num_intersects,), dtype=torch.float32,
                                        device=colors.device) if collect_isect else None)
     v_output = _f32(grad_out_img)
-    v_edges, v_colors, v_opac, v_is2, v_sw = rasterize_backward(
+    v_cubics_px, v_colors, v_opac, v_is2, v_sw = rasterize_backward(
         b, bg, final_T, final_idx, v_output, curve_contrib_rgb=curve_contrib_rgb,
         curve_isect_contrib=curve_isect_contrib)
-    v_cubics_px, v_cubics_norm = accumulate_edge_grads(b, v_edges)
     payload = {
         "v_cubics_px": v_cubics_px,
         "v_colors": v_colors,
@@ -333,18 +341,13 @@ def _splat_backward(ctx, grad_out_img):
         payload["stroke_widths"] = stroke_widths
     if process_fn is not None:
         payload = _run_process_fn(process_fn, "post_backward_rasterize", payload)
-        if payload["v_cubics_px"] is not v_cubics_px:
-            v_cubics_px = payload["v_cubics_px"]
-            half_w, half_h = 0.5 * float(ctx.img_w), 0.5 * float(ctx.img_h)
-            v_cubics_norm = torch.empty_like(v_cubics_px)
-            v_cubics_norm[..., 0] = v_cubics_px[..., 0] * half_w
-            v_cubics_norm[..., 1] = v_cubics_px[..., 1] * half_h
+        v_cubics_px = _f32(payload["v_cubics_px"])
         v_colors = payload["v_colors"]
         v_opac = payload["v_opacity"]
         if ctx.mode == MODE_STROKE:
             v_sw = payload["v_stroke"]
+    v_cubics_norm, v_aa = backward_finalize(b, v_cubics_px, widths, v_is2)
     v_depths = torch.zeros_like(depths, dtype=torch.float32)
-    v_aa = aa_width_grads(widths, v_is2)
     return v_cubics_norm.view_as(cubics_norm), v_colors, v_opac.view_as(opacities), v_sw, \
         v_depths, v_aa
 

@@ -63,20 +63,38 @@ def test_backward_matches_oracle(name):
         v[: rows[0]] = 0
         v[rows[1]:] = 0
     vd = v.cuda()
-    v_edges, v_col, v_op, v_is2, v_sw = splat.rasterize_backward(b, s.background.float(), T, idx,
-                                                                 vd)
-    v_px, v_norm = splat.accumulate_edge_grads(b, v_edges)
+    v_px, v_col, v_op, v_is2, v_sw = splat.rasterize_backward(b, s.background.float(), T, idx,
+                                                              vd)
+    widths = torch.clamp(s.aa_widths.float(), min=1e-4).contiguous()
+    v_norm, v_aa = splat.backward_finalize(b, v_px, widths, v_is2)
     g = O.render_backward(fw, v.numpy())
     checks = [("v_colors", v_col, g["v_colors"]), ("v_opacities", v_op, g["v_opacities"]),
               ("v_inv_sigma2s", v_is2, g["v_inv_sigma2s"]),
-              ("v_edges", v_edges.view(-1, 2, 2), g["v_edges"]),
               ("v_cubics_px", v_px, g["v_cubics_px"]),
-              ("v_cubics_norm", v_norm, g["v_cubics_norm"])]
+              ("v_cubics_norm", v_norm, g["v_cubics_norm"]),
+              ("v_aa_widths", v_aa, g["v_aa_widths"])]
     if v_sw is not None:
         checks.append(("v_stroke_widths", v_sw, g["v_stroke_widths"]))
     for key, got, ref in checks:
         ok, rel = grad_scale_tol(got.cpu().numpy(), ref)
         assert ok, f"{key}: max error {rel:.3e} of max|ref|"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("S", [2, 8, 16, 33])
+def test_accumulate_edge_grads_block(S):
+    """_accumulate_edge_grads_to_cubics (cubic_splatting.py:2308-2396) on
+    random edge gradients vs the oracle's float64 sums."""
+    sc = synth.small_scene(1, P=20, S=S)
+    b, _ = hip_bin(sc)
+    g = np.random.default_rng(S).standard_normal((b.edges.shape[0], 2, 2)).astype(np.float32)
+    v_px, v_norm = splat.accumulate_edge_grads(b, torch.from_numpy(g).cuda().view(-1, 4))
+    ref = O.accumulate_edge_grads(g.astype(np.float64), b.nseg, S)
+    ok, rel = grad_scale_tol(v_px.cpu().numpy(), ref, rtol=1e-5)
+    assert ok, rel
+    ref_n = ref * np.array([0.5 * sc.img_w, 0.5 * sc.img_h])
+    ok, rel = grad_scale_tol(v_norm.cpu().numpy(), ref_n, rtol=1e-5)
+    assert ok, rel
 
 
 @pytest.mark.gpu
