@@ -156,10 +156,10 @@ size_t cs_mse_partials_elems(int64_t n);
 size_t cs_ssim_partials_elems(int32_t nc, int32_t h, int32_t w);
 
 /* mse_partial_sum_kernel + reduce_sum_partial_kernel (ops/metric.py:18-163,
- * metric.py:102-131): *loss = sum((x-y)^2)/n.  `ticket` is one device uint32
- * that must be 0 before the first call; the kernel leaves it at 0. */
-int cs_mse_forward(const float* x, const float* y, int64_t n, float* partials, uint32_t* ticket,
-                   float* loss, hipStream_t stream);
+ * metric.py:102-131): *loss = sum((x-y)^2)/n (device scalar), two launches,
+ * deterministic summation order. */
+int cs_mse_forward(const float* x, const float* y, int64_t n, float* partials, float* loss,
+                   hipStream_t stream);
 
 /* mse_backward_diff_kernel (ops/metric.py:166-202) with the scale
  * grad_loss * 2/n read on the device (metric.py:168 reads it on the host):
@@ -173,8 +173,8 @@ int cs_mse_backward(const float* x, const float* y, int64_t n, const float* grad
  * If abc != null also stores, per map pixel, dS/dmu_x, dS/dE[x^2], dS/dE[xy]
  * ([3, nc, oh, ow]) for cs_ssim_backward.  x, y: [nc, h, w]. */
 int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
-            const float* win1d, int32_t win, float c1, float c2, float* partials,
-            uint32_t* ticket, float* out, float* abc, hipStream_t stream);
+            const float* win1d, int32_t win, float c1, float c2, float* partials, float* out,
+            float* abc, hipStream_t stream);
 
 /* Gradient of the SSIM mean w.r.t. x (the reference has no SSIM backward):
  * grad_x = g * [W*(A) + 2 x W*(B) + y W*(C)] / (nc*oh*ow), W* the transposed

@@ -1,16 +1,18 @@
 // MSE and SSIM losses (forward and backward) for MI355X.
 //
-// MSE: one launch; each workgroup reduces a contiguous chunk with 16-byte
-// loads, writes its partial, and the last workgroup to finish (ticket
-// counter) sums the partials in index order, so the result is deterministic.
+// Reductions are two launches: workgroups write partial sums, one workgroup
+// adds them in index order (deterministic).  A last-workgroup ticket would
+// save the launch but puts every workgroup's atomic on one device-scope
+// address, which serializes outside the XCD L2s.
 //
-// SSIM: valid-window SSIM of ops/metric.py:205-341 with the 2D Gaussian
-// window applied separably (the reference window is the outer product of one
-// normalized 1D Gaussian, metric.py:47-61): a 32x32 output tile stages its
-// (32+win-1)^2 inputs in LDS, a horizontal pass produces the five windowed
-// moments per row, a vertical pass finishes them.  The backward (absent from
-// the reference) uses the per-pixel partials A = dS/dmu_x, B = dS/dE[x^2],
-// C = dS/dE[xy] and one transposed separable correlation.
+// SSIM: valid-window SSIM of ops/metric.py:205-341 with the 2D Gaussian window
+// applied separably (the reference window is the outer product of one
+// normalized 1D Gaussian, metric.py:47-61).  A 32x32 output tile stages its
+// (32+win-1)^2 inputs in LDS; the horizontal pass gives each thread an 8-wide
+// strip (the 8+win-1 inputs are read once), the vertical pass a 4-tall strip
+// of the five moments.  The backward (absent from the reference) uses the
+// per-pixel partials A = dS/dmu_x, B = dS/dE[x^2], C = dS/dE[xy] and one
+// transposed separable correlation, blocked the same way.
 #include "cs_common.h"
 #include "../../include/cubicsplat_hip.h"
 
@@ -19,44 +21,53 @@ namespace cs {
 constexpr int kMseThreads = 256;
 constexpr int kMseItems = 16;  // float elements per thread
 constexpr int kMseChunk = kMseThreads * kMseItems;
+constexpr int kFinalThreads = 1024;
 
-__device__ __forceinline__ float block_sum_256(float v, float* sh) {
+__device__ __forceinline__ float block_sum(float v, float* sh) {
     v = wave_sum(v);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (lane == 0) sh[w] = v;
     __syncthreads();
     float r = 0.0f;
-    if (threadIdx.x == 0) r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    if (threadIdx.x == 0) {
+        const int nw = (blockDim.x + 63) >> 6;
+        for (int k = 0; k < nw; ++k) r += sh[k];
+    }
     __syncthreads();
     return r;
 }
 
-// Sums partials[0..n) in a fixed order with one workgroup; result in thread 0.
-__device__ __forceinline__ float block_sum_partials(const float* __restrict__ partials, int n,
-                                                   float* sh) {
+// out = scale * sum(partials[0..n)), one workgroup, fixed order.
+__global__ __launch_bounds__(kFinalThreads) void k_sum_partials(const float* __restrict__ partials,
+                                                               int n, float scale,
+                                                               float* __restrict__ out) {
+    __shared__ float sh[kFinalThreads / kWave];
     float acc = 0.0f;
-    for (int i = threadIdx.x; i < n; i += kMseThreads) acc += partials[i];
-    return block_sum_256(acc, sh);
+    for (int i = threadIdx.x; i < n; i += kFinalThreads) acc += partials[i];
+    const float tot = block_sum(acc, sh);
+    if (threadIdx.x == 0) *out = tot * scale;
 }
 
-__global__ __launch_bounds__(kMseThreads) void k_mse_fwd(const float* __restrict__ x,
-                                                        const float* __restrict__ y, int64_t n,
-                                                        float* __restrict__ partials,
-                                                        uint32_t* __restrict__ ticket,
-                                                        float* __restrict__ loss) {
-    __shared__ float sh[4];
-    __shared__ bool last;
+__global__ __launch_bounds__(kMseThreads) void k_mse_partial(const float* __restrict__ x,
+                                                            const float* __restrict__ y, int64_t n,
+                                                            float* __restrict__ partials) {
+    __shared__ float sh[kMseThreads / kWave];
     const int64_t base = (int64_t)blockIdx.x * kMseChunk;
     float acc = 0.0f;
     const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0;
     if (aligned && base + kMseChunk <= n) {
         const float4* x4 = reinterpret_cast<const float4*>(x + base);
         const float4* y4 = reinterpret_cast<const float4*>(y + base);
+        float4 a[kMseItems / 4], b[kMseItems / 4];
 #pragma unroll
         for (int k = 0; k < kMseItems / 4; ++k) {
-            const float4 a = x4[k * kMseThreads + threadIdx.x];
-            const float4 b = y4[k * kMseThreads + threadIdx.x];
-            const float d0 = a.x - b.x, d1 = a.y - b.y, d2 = a.z - b.z, d3 = a.w - b.w;
+            a[k] = x4[k * kMseThreads + threadIdx.x];
+            b[k] = y4[k * kMseThreads + threadIdx.x];
+        }
+#pragma unroll
+        for (int k = 0; k < kMseItems / 4; ++k) {
+            const float d0 = a[k].x - b[k].x, d1 = a[k].y - b[k].y;
+            const float d2 = a[k].z - b[k].z, d3 = a[k].w - b[k].w;
             acc = __builtin_fmaf(d0, d0, acc);
             acc = __builtin_fmaf(d1, d1, acc);
             acc = __builtin_fmaf(d2, d2, acc);
@@ -71,21 +82,8 @@ __global__ __launch_bounds__(kMseThreads) void k_mse_fwd(const float* __restrict
             }
         }
     }
-    const float bs = block_sum_256(acc, sh);
-    if (threadIdx.x == 0) {
-        partials[blockIdx.x] = bs;
-        __threadfence();
-        last = atomicAdd(ticket, 1u) == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (last) {
-        __threadfence();
-        const float tot = block_sum_partials(partials, gridDim.x, sh);
-        if (threadIdx.x == 0) {
-            *loss = tot / (float)n;
-            *ticket = 0u;
-        }
-    }
+    const float bs = block_sum(acc, sh);
+    if (threadIdx.x == 0) partials[blockIdx.x] = bs;
 }
 
 __global__ __launch_bounds__(256) void k_mse_bwd(const float* __restrict__ x,
@@ -113,13 +111,32 @@ __global__ __launch_bounds__(256) void k_mse_bwd(const float* __restrict__ x,
 
 // ------------------------------------------------------------------ SSIM
 
-constexpr int kSsimOT = 32;  // output tile edge
+constexpr int kSsimOT = 32;   // output tile edge
+constexpr int kHStrip = 8;    // horizontal-pass outputs per thread
+constexpr int kVStrip = 4;    // vertical-pass outputs per thread
 
 template <int WIN>
 struct SsimTile {
     static constexpr int IT = kSsimOT + WIN - 1;  // staged input tile edge
     static constexpr int ITP = IT + 1;             // padded LDS row
+    static constexpr int HP = kSsimOT + 1;         // padded horizontal-result row
 };
+
+// Loads a (IT x IT) tile starting at (y0, x0) of `src` (h x w) into LDS,
+// zero outside the image.  256 threads as 4 rows x 64 columns.
+template <int IT, int ITP>
+__device__ __forceinline__ void load_tile(const float* __restrict__ src, int h, int w, int y0,
+                                          int x0, float (*dst)[ITP]) {
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int r = ty; r < IT; r += 4) {
+        const int gy = y0 + r;
+        const bool rin = gy >= 0 && gy < h;
+        for (int c = tx; c < IT; c += 64) {
+            const int gx = x0 + c;
+            dst[r][c] = (rin && gx >= 0 && gx < w) ? src[(size_t)gy * w + gx] : 0.0f;
+        }
+    }
+}
 
 template <int WIN>
 __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
@@ -127,63 +144,82 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
                                                  int oh, int ow,
                                                  const float* __restrict__ win1d, float c1,
                                                  float c2, float* __restrict__ partials,
-                                                 uint32_t* __restrict__ ticket,
-                                                 float* __restrict__ out,
                                                  float* __restrict__ abc, int nc) {
-    constexpr int IT = SsimTile<WIN>::IT, ITP = SsimTile<WIN>::ITP;
+    constexpr int IT = SsimTile<WIN>::IT, ITP = SsimTile<WIN>::ITP, HP = SsimTile<WIN>::HP;
     __shared__ float xs[IT][ITP];
     __shared__ float ys[IT][ITP];
-    __shared__ float hm[5][IT][kSsimOT + 1];
+    __shared__ float hm[5][IT][HP];
     __shared__ float gw[WIN];
     __shared__ float sh[4];
-    __shared__ bool last;
     const int c = blockIdx.z;
     const int ox0 = blockIdx.x * kSsimOT, oy0 = blockIdx.y * kSsimOT;
-    const float* xc = x + (size_t)c * h * w;
-    const float* yc = y + (size_t)c * h * w;
     if (threadIdx.x < WIN) gw[threadIdx.x] = win1d[threadIdx.x];
-    for (int idx = threadIdx.x; idx < IT * IT; idx += 256) {
-        const int r = idx / IT, q = idx - r * IT;
-        const int gy = oy0 + r, gx = ox0 + q;
-        const bool in = gy < h && gx < w;
-        xs[r][q] = in ? xc[(size_t)gy * w + gx] : 0.0f;
-        ys[r][q] = in ? yc[(size_t)gy * w + gx] : 0.0f;
-    }
+    load_tile<IT, ITP>(x + (size_t)c * h * w, h, w, oy0, ox0, xs);
+    load_tile<IT, ITP>(y + (size_t)c * h * w, h, w, oy0, ox0, ys);
     __syncthreads();
-    for (int idx = threadIdx.x; idx < IT * kSsimOT; idx += 256) {
-        const int r = idx / kSsimOT, q = idx - r * kSsimOT;
-        float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f, m4 = 0.f;
+    // Horizontal: thread -> (row, 8-wide strip); IT rows x 4 strips.
+    for (int item = threadIdx.x; item < IT * (kSsimOT / kHStrip); item += 256) {
+        const int r = item >> 2, q0 = (item & 3) * kHStrip;
+        float a[kHStrip + WIN - 1], b[kHStrip + WIN - 1];
 #pragma unroll
-        for (int k = 0; k < WIN; ++k) {
-            const float g = gw[k];
-            const float a = xs[r][q + k], b = ys[r][q + k];
-            m0 = __builtin_fmaf(g, a, m0);
-            m1 = __builtin_fmaf(g, b, m1);
-            m2 = __builtin_fmaf(g, a * a, m2);
-            m3 = __builtin_fmaf(g, b * b, m3);
-            m4 = __builtin_fmaf(g, a * b, m4);
+        for (int k = 0; k < kHStrip + WIN - 1; ++k) {
+            a[k] = xs[r][q0 + k];
+            b[k] = ys[r][q0 + k];
         }
-        hm[0][r][q] = m0; hm[1][r][q] = m1; hm[2][r][q] = m2; hm[3][r][q] = m3; hm[4][r][q] = m4;
+#pragma unroll
+        for (int o = 0; o < kHStrip; ++o) {
+            float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f, m4 = 0.f;
+#pragma unroll
+            for (int k = 0; k < WIN; ++k) {
+                const float g = gw[k];
+                const float av = a[o + k], bv = b[o + k];
+                m0 = __builtin_fmaf(g, av, m0);
+                m1 = __builtin_fmaf(g, bv, m1);
+                m2 = __builtin_fmaf(g, av * av, m2);
+                m3 = __builtin_fmaf(g, bv * bv, m3);
+                m4 = __builtin_fmaf(g, av * bv, m4);
+            }
+            hm[0][r][q0 + o] = m0;
+            hm[1][r][q0 + o] = m1;
+            hm[2][r][q0 + o] = m2;
+            hm[3][r][q0 + o] = m3;
+            hm[4][r][q0 + o] = m4;
+        }
     }
     __syncthreads();
+    // Vertical: thread -> (column, 4-tall strip); 32 columns x 8 strips.
+    const int q = threadIdx.x & 31, r0 = (threadIdx.x >> 5) * kVStrip;
+    float mom[5][kVStrip];
+#pragma unroll
+    for (int m = 0; m < 5; ++m)
+#pragma unroll
+        for (int o = 0; o < kVStrip; ++o) mom[m][o] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kVStrip + WIN - 1; ++k) {
+        float v[5];
+#pragma unroll
+        for (int m = 0; m < 5; ++m) v[m] = hm[m][r0 + k][q];
+#pragma unroll
+        for (int o = 0; o < kVStrip; ++o) {
+            const int t = k - o;
+            if (t >= 0 && t < WIN) {
+                const float g = gw[t];
+#pragma unroll
+                for (int m = 0; m < 5; ++m) mom[m][o] = __builtin_fmaf(g, v[m], mom[m][o]);
+            }
+        }
+    }
     float acc = 0.0f;
     const size_t plane = (size_t)oh * ow;
-    for (int idx = threadIdx.x; idx < kSsimOT * kSsimOT; idx += 256) {
-        const int r = idx / kSsimOT, q = idx - r * kSsimOT;
-        const int oy = oy0 + r, ox = ox0 + q;
-        if (oy >= oh || ox >= ow) continue;
-        float mu1 = 0.f, mu2 = 0.f, ex2 = 0.f, ey2 = 0.f, exy = 0.f;
+    const size_t stride = (size_t)nc * plane;
+    const int ox = ox0 + q;
 #pragma unroll
-        for (int k = 0; k < WIN; ++k) {
-            const float g = gw[k];
-            mu1 = __builtin_fmaf(g, hm[0][r + k][q], mu1);
-            mu2 = __builtin_fmaf(g, hm[1][r + k][q], mu2);
-            ex2 = __builtin_fmaf(g, hm[2][r + k][q], ex2);
-            ey2 = __builtin_fmaf(g, hm[3][r + k][q], ey2);
-            exy = __builtin_fmaf(g, hm[4][r + k][q], exy);
-        }
+    for (int o = 0; o < kVStrip; ++o) {
+        const int oy = oy0 + r0 + o;
+        if (oy >= oh || ox >= ow) continue;
+        const float mu1 = mom[0][o], mu2 = mom[1][o];
         const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2, mu12 = mu1 * mu2;
-        const float s1 = ex2 - mu1_sq, s2 = ey2 - mu2_sq, s12 = exy - mu12;
+        const float s1 = mom[2][o] - mu1_sq, s2 = mom[3][o] - mu2_sq, s12 = mom[4][o] - mu12;
         const float n1 = 2.0f * mu12 + c1, d1 = mu1_sq + mu2_sq + c1;
         const float n2 = 2.0f * s12 + c2, d2 = s1 + s2 + c2;
         const float l = n1 / d1, cs_ = n2 / d2;
@@ -191,30 +227,15 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
         if (abc) {
             const float dl = 2.0f * (mu2 - l * mu1) / d1;
             const float dcs = 2.0f * (mu1 * cs_ - mu2) / d2;
-            const size_t o = (size_t)c * plane + (size_t)oy * ow + ox;
-            const size_t stride = (size_t)nc * plane;
-            abc[o] = cs_ * dl + l * dcs;
-            abc[stride + o] = -l * cs_ / d2;
-            abc[2 * stride + o] = 2.0f * l / d2;
+            const size_t oi = (size_t)c * plane + (size_t)oy * ow + ox;
+            abc[oi] = cs_ * dl + l * dcs;
+            abc[stride + oi] = -l * cs_ / d2;
+            abc[2 * stride + oi] = 2.0f * l / d2;
         }
     }
-    const float bs = block_sum_256(acc, sh);
-    const int nblk = gridDim.x * gridDim.y * gridDim.z;
-    const int bid = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-    if (threadIdx.x == 0) {
-        partials[bid] = bs;
-        __threadfence();
-        last = atomicAdd(ticket, 1u) == (uint32_t)nblk - 1;
-    }
-    __syncthreads();
-    if (last) {
-        __threadfence();
-        const float tot = block_sum_partials(partials, nblk, sh);
-        if (threadIdx.x == 0) {
-            *out = tot / ((float)nc * (float)plane);
-            *ticket = 0u;
-        }
-    }
+    const float bs = block_sum(acc, sh);
+    if (threadIdx.x == 0)
+        partials[(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x] = bs;
 }
 
 template <int WIN>
@@ -225,59 +246,70 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
                                                  const float* __restrict__ abc,
                                                  const float* __restrict__ grad_out, float inv_cnt,
                                                  int nc, float* __restrict__ gx) {
-    constexpr int IT = SsimTile<WIN>::IT, ITP = SsimTile<WIN>::ITP;
+    constexpr int IT = SsimTile<WIN>::IT, ITP = SsimTile<WIN>::ITP, HP = SsimTile<WIN>::HP;
     __shared__ float as[3][IT][ITP];
-    __shared__ float hs[3][IT][kSsimOT + 1];
+    __shared__ float hs[3][IT][HP];
     __shared__ float gw[WIN];
     const int c = blockIdx.z;
     const int px0 = blockIdx.x * kSsimOT, py0 = blockIdx.y * kSsimOT;
     const size_t plane = (size_t)oh * ow;
     const size_t stride = (size_t)nc * plane;
-    const float* A = abc + (size_t)c * plane;
     if (threadIdx.x < WIN) gw[threadIdx.x] = win1d[threadIdx.x];
-    // Tile of A, B, C for map pixels o in [p - (WIN-1), p].
-    for (int idx = threadIdx.x; idx < IT * IT; idx += 256) {
-        const int r = idx / IT, q = idx - r * IT;
-        const int oy = py0 - (WIN - 1) + r, ox = px0 - (WIN - 1) + q;
-        const bool in = oy >= 0 && oy < oh && ox >= 0 && ox < ow;
-        const size_t o = in ? (size_t)oy * ow + ox : 0;
-        as[0][r][q] = in ? A[o] : 0.0f;
-        as[1][r][q] = in ? A[stride + o] : 0.0f;
-        as[2][r][q] = in ? A[2 * stride + o] : 0.0f;
-    }
+    // Map pixels o in [p - (WIN-1), p] of A, B, C.
+    for (int m = 0; m < 3; ++m)
+        load_tile<IT, ITP>(abc + m * stride + (size_t)c * plane, oh, ow, py0 - (WIN - 1),
+                           px0 - (WIN - 1), as[m]);
     __syncthreads();
-    for (int idx = threadIdx.x; idx < IT * kSsimOT; idx += 256) {
-        const int r = idx / kSsimOT, q = idx - r * kSsimOT;
-        float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+    // Horizontal full correlation: hs[r][q] = sum_k g[k] as[r][q + WIN-1-k].
+    for (int item = threadIdx.x; item < IT * (kSsimOT / kHStrip); item += 256) {
+        const int r = item >> 2, q0 = (item & 3) * kHStrip;
 #pragma unroll
-        for (int k = 0; k < WIN; ++k) {
-            const float g = gw[k];
-            s0 = __builtin_fmaf(g, as[0][r][q + WIN - 1 - k], s0);
-            s1 = __builtin_fmaf(g, as[1][r][q + WIN - 1 - k], s1);
-            s2 = __builtin_fmaf(g, as[2][r][q + WIN - 1 - k], s2);
+        for (int m = 0; m < 3; ++m) {
+            float a[kHStrip + WIN - 1];
+#pragma unroll
+            for (int k = 0; k < kHStrip + WIN - 1; ++k) a[k] = as[m][r][q0 + k];
+#pragma unroll
+            for (int o = 0; o < kHStrip; ++o) {
+                float s = 0.0f;
+#pragma unroll
+                for (int k = 0; k < WIN; ++k) s = __builtin_fmaf(gw[k], a[o + WIN - 1 - k], s);
+                hs[m][r][q0 + o] = s;
+            }
         }
-        hs[0][r][q] = s0; hs[1][r][q] = s1; hs[2][r][q] = s2;
     }
     __syncthreads();
+    const int q = threadIdx.x & 31, r0 = (threadIdx.x >> 5) * kVStrip;
+    float gsum[3][kVStrip];
+#pragma unroll
+    for (int m = 0; m < 3; ++m)
+#pragma unroll
+        for (int o = 0; o < kVStrip; ++o) gsum[m][o] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kVStrip + WIN - 1; ++k) {
+        float v[3];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) v[m] = hs[m][r0 + k][q];
+#pragma unroll
+        for (int o = 0; o < kVStrip; ++o) {
+            const int t = o + WIN - 1 - k;
+            if (t >= 0 && t < WIN) {
+                const float g = gw[t];
+#pragma unroll
+                for (int m = 0; m < 3; ++m) gsum[m][o] = __builtin_fmaf(g, v[m], gsum[m][o]);
+            }
+        }
+    }
     const float scale = (*grad_out) * inv_cnt;
     const float* xc = x + (size_t)c * h * w;
     const float* yc = y + (size_t)c * h * w;
     float* gc = gx + (size_t)c * h * w;
-    for (int idx = threadIdx.x; idx < kSsimOT * kSsimOT; idx += 256) {
-        const int r = idx / kSsimOT, q = idx - r * kSsimOT;
-        const int py = py0 + r, px = px0 + q;
-        if (py >= h || px >= w) continue;
-        float ga = 0.f, gb = 0.f, gcc = 0.f;
+    const int px = px0 + q;
 #pragma unroll
-        for (int k = 0; k < WIN; ++k) {
-            const float g = gw[k];
-            ga = __builtin_fmaf(g, hs[0][r + WIN - 1 - k][q], ga);
-            gb = __builtin_fmaf(g, hs[1][r + WIN - 1 - k][q], gb);
-            gcc = __builtin_fmaf(g, hs[2][r + WIN - 1 - k][q], gcc);
-        }
+    for (int o = 0; o < kVStrip; ++o) {
+        const int py = py0 + r0 + o;
+        if (py >= h || px >= w) continue;
         const size_t pi = (size_t)py * w + px;
-        const float xv = xc[pi], yv = yc[pi];
-        gc[pi] = scale * (ga + 2.0f * xv * gb + yv * gcc);
+        gc[pi] = scale * (gsum[0][o] + 2.0f * xc[pi] * gsum[1][o] + yc[pi] * gsum[2][o]);
     }
 }
 
@@ -288,16 +320,19 @@ using namespace cs;
 static int metric_status() { return hipGetLastError() == hipSuccess ? CS_OK : CS_ERR_HIP; }
 
 extern "C" size_t cs_mse_partials_elems(int64_t n) {
-    return (size_t)((n + kMseChunk - 1) / kMseChunk > 0 ? (n + kMseChunk - 1) / kMseChunk : 1);
+    const int64_t nb = (n + kMseChunk - 1) / kMseChunk;
+    return (size_t)(nb > 0 ? nb : 1);
 }
 
 extern "C" int cs_mse_forward(const float* x, const float* y, int64_t n, float* partials,
-                              uint32_t* ticket, float* loss, hipStream_t stream) {
+                              float* loss, hipStream_t stream) {
     if (n <= 0) return CS_ERR_ARGS;
     const int64_t nb = (n + kMseChunk - 1) / kMseChunk;
     if (nb > 0x7fffffff) return CS_ERR_ARGS;
-    hipLaunchKernelGGL(k_mse_fwd, dim3((unsigned)nb), dim3(kMseThreads), 0, stream, x, y, n,
-                       partials, ticket, loss);
+    hipLaunchKernelGGL(k_mse_partial, dim3((unsigned)nb), dim3(kMseThreads), 0, stream, x, y, n,
+                       partials);
+    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials, (int)nb,
+                       1.0f / (float)n, loss);
     return metric_status();
 }
 
@@ -321,14 +356,14 @@ extern "C" size_t cs_ssim_partials_elems(int32_t nc, int32_t h, int32_t w) {
 
 extern "C" int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                        const float* win1d, int32_t win, float c1, float c2, float* partials,
-                       uint32_t* ticket, float* out, float* abc, hipStream_t stream) {
+                       float* out, float* abc, hipStream_t stream) {
     if (nc <= 0 || win <= 0 || (win & 1) == 0 || win > 15 || h < win || w < win)
         return CS_ERR_ARGS;
     const int oh = h - win + 1, ow = w - win + 1;
     const dim3 grid((ow + kSsimOT - 1) / kSsimOT, (oh + kSsimOT - 1) / kSsimOT, nc);
 #define CS_SSIM_FWD(W_)                                                                       \
     hipLaunchKernelGGL(k_ssim_fwd<W_>, grid, dim3(256), 0, stream, x, y, h, w, oh, ow, win1d, \
-                       c1, c2, partials, ticket, out, abc, nc)
+                       c1, c2, partials, abc, nc)
     switch (win) {
         CS_SSIM_DISPATCH(1, CS_SSIM_FWD)
         CS_SSIM_DISPATCH(3, CS_SSIM_FWD)
@@ -341,6 +376,9 @@ extern "C" int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, in
         default: return CS_ERR_ARGS;
     }
 #undef CS_SSIM_FWD
+    const int nblk = (int)(grid.x * grid.y * grid.z);
+    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials, nblk,
+                       1.0f / ((float)nc * (float)oh * (float)ow), out);
     return metric_status();
 }
 

@@ -40,13 +40,12 @@ struct Geom {
     float bproj, bdx, bdy;
 };
 
-// Distance (and optionally the best edge) and +x ray crossings of one
-// segment's edges, cubic_splatting.py:1095-1134 / 1451-1501.
+// Distance (and optionally the best edge) and +x ray crossings of one edge,
+// cubic_splatting.py:1095-1134 / 1451-1501.
 template <bool DIST, bool CROSS, bool BEST>
-__device__ __forceinline__ void scan_edges(const EdgeRec* __restrict__ ep, int n, int ebase,
-                                           float px, float py, Geom& G) {
-    for (int e = 0; e < n; ++e) {
-        const EdgeRec E = ep[e];
+__device__ __forceinline__ void edge_step(const EdgeRec& E, int eid, float px, float py,
+                                          Geom& G) {
+    {
         const float wx = px - E.x0, wy = py - E.y0;
         if (DIST) {
             float proj = __builtin_fmaf(wx, E.ux, wy * E.uy);
@@ -57,7 +56,7 @@ __device__ __forceinline__ void scan_edges(const EdgeRec* __restrict__ ep, int n
             if (BEST) {
                 if (d2 < G.min_d2) {
                     G.min_d2 = d2;
-                    G.best = ebase + e;
+                    G.best = eid;
                     G.bproj = proj;
                     G.bdx = dx;
                     G.bdy = dy;
@@ -78,6 +77,29 @@ __device__ __forceinline__ void scan_edges(const EdgeRec* __restrict__ ep, int n
     }
 }
 
+// Unroll factor of the best-edge (backward) loop: a full unroll keeps too many
+// candidates live (registers -> occupancy), so it is partial.
+#ifndef CS_BEST_UNROLL
+#define CS_BEST_UNROLL 3
+#endif
+
+// One segment's edges; EPS > 0 fixes the edge count at compile time so the
+// loop unrolls and the scalar loads of the edge records batch up.
+template <bool DIST, bool CROSS, bool BEST, int EPS>
+__device__ __forceinline__ void scan_edges(const EdgeRec* __restrict__ ep, int n, int ebase,
+                                           float px, float py, Geom& G) {
+    if constexpr (EPS > 0 && !BEST) {
+#pragma unroll
+        for (int e = 0; e < EPS; ++e) edge_step<DIST, CROSS, BEST>(ep[e], ebase + e, px, py, G);
+    } else if constexpr (EPS > 0) {
+#pragma unroll CS_BEST_UNROLL
+        for (int e = 0; e < EPS; ++e) edge_step<DIST, CROSS, BEST>(ep[e], ebase + e, px, py, G);
+    } else {
+#pragma unroll 4
+        for (int e = 0; e < n; ++e) edge_step<DIST, CROSS, BEST>(ep[e], ebase + e, px, py, G);
+    }
+}
+
 struct WaveRect {
     float x0, y0, x1, y1;  // pixel centres covered by the wave
 };
@@ -92,7 +114,7 @@ __device__ __forceinline__ bool prim_culled(const PrimRec& pr, const WaveRect& R
     return pr.by0 > R.y1 || pr.by1 < R.y0 || R.x0 > pr.bx1;
 }
 
-template <int MODE, bool BEST>
+template <int MODE, bool BEST, int EPS>
 __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& R, float D2,
                                               const float4* __restrict__ seg_bbox,
                                               const EdgeRec* __restrict__ edges, int eps,
@@ -110,10 +132,10 @@ __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect&
         const EdgeRec* ep = edges + (size_t)s * eps;
         const int ebase = s * eps;
         if (near) {
-            if (band) scan_edges<true, true, BEST>(ep, eps, ebase, px, py, G);
-            else scan_edges<true, false, BEST>(ep, eps, ebase, px, py, G);
+            if (band) scan_edges<true, true, BEST, EPS>(ep, eps, ebase, px, py, G);
+            else scan_edges<true, false, BEST, EPS>(ep, eps, ebase, px, py, G);
         } else if (band) {
-            scan_edges<false, true, false>(ep, eps, ebase, px, py, G);
+            scan_edges<false, true, false, EPS>(ep, eps, ebase, px, py, G);
         }
     }
 }
@@ -123,28 +145,37 @@ struct Cov {
 };
 
 // Fill: cubic_splatting.py:1138-1170; stroke: cubic_polyline_splatting.py:219-226.
+// A lane whose minimum over the evaluated edges exceeds the cull distance is
+// decided without exp/div/sqrt: inside a fill its coverage is exactly 1.0f
+// (1 + exp(-2 d inv_sigma) rounds to 1), outside (or for a stroke) its alpha
+// is below 1/255, which cov = 0 reproduces.  The exact branch only runs when
+// some lane of the wave needs it.
 template <int MODE>
-__device__ __forceinline__ Cov coverage(const PrimRec& pr, const Geom& G) {
+__device__ __forceinline__ Cov coverage(const PrimRec& pr, const Geom& G, float D2) {
     Cov c;
-    c.dist = __builtin_sqrtf(fmaxf(G.min_d2, 0.0f));
-    if (MODE == 0) {
-        const bool inside = pr.rule == 0 ? ((G.winding & 1) != 0) : (G.winding != 0);
-        c.sgn = inside ? -1.0f : 1.0f;
-        float logit = c.dist * pr.inv_sigma * 2.0f;
-        if (inside) logit = -logit;
-        logit = fmaxf(-60.0f, fminf(60.0f, logit));
-        c.cov = 1.0f / (1.0f + spec_expf(logit));
-        c.ed = 0.0f;
-    } else {
-        c.ed = fmaxf(0.0f, c.dist - pr.half_sw);
-        const float sigma = 0.5f * c.ed * c.ed * pr.inv_sigma2;
-        c.cov = spec_expf(-sigma);
-        c.sgn = 1.0f;
+    const bool inside =
+        MODE == 0 && (pr.rule == 0 ? ((G.winding & 1) != 0) : (G.winding != 0));
+    c.sgn = inside ? -1.0f : 1.0f;
+    c.cov = inside ? 1.0f : 0.0f;
+    c.dist = 0.0f;
+    c.ed = 0.0f;
+    if (!(G.min_d2 > D2)) {
+        c.dist = __builtin_sqrtf(fmaxf(G.min_d2, 0.0f));
+        if (MODE == 0) {
+            float logit = c.dist * pr.inv_sigma * 2.0f;
+            if (inside) logit = -logit;
+            logit = fmaxf(-60.0f, fminf(60.0f, logit));
+            c.cov = 1.0f / (1.0f + spec_expf(logit));
+        } else {
+            c.ed = fmaxf(0.0f, c.dist - pr.half_sw);
+            const float sigma = 0.5f * c.ed * c.ed * pr.inv_sigma2;
+            c.cov = spec_expf(-sigma);
+        }
     }
     return c;
 }
 
-template <int MODE>
+template <int MODE, int EPS>
 __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
     const int32_t* __restrict__ prim_ids, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges, const float4* __restrict__ seg_bbox,
@@ -167,16 +198,18 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
     float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
     int cur = 0;
     bool done = !in_img;
+    int pid_next = g0 < g1 ? prim_ids[g0] : 0;
     for (int g = g0; g < g1; ++g) {
         if (__ballot(!done) == 0) break;
-        const int pid = prim_ids[g];
+        const int pid = pid_next;
+        pid_next = prim_ids[min(g + 1, g1 - 1)];
         const PrimRec pr = prims[pid];
         const float D2 = pr.cull_d * pr.cull_d;
         if (prim_culled<MODE>(pr, R, D2)) continue;
         Geom G;
-        prim_geometry<MODE, false>(pr, R, D2, seg_bbox, edges, eps, px, py, G);
+        prim_geometry<MODE, false, EPS>(pr, R, D2, seg_bbox, edges, eps, px, py, G);
         if (!done) {
-            const Cov c = coverage<MODE>(pr, G);
+            const Cov c = coverage<MODE>(pr, G, D2);
             const float alpha = fminf(kAlphaCap, pr.opacity * c.cov);
             if (alpha >= kAlphaMin) {
                 const float nT = T * (1.0f - alpha);
@@ -220,7 +253,7 @@ __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
 //     reference's accumulation weights (cubic_splatting.py:2308-2396), then
 //     lanes that share a segment are summed (one leader pass per distinct
 //     segment) and one lane adds the 8 values to v_cubics_px.
-template <int MODE>
+template <int MODE, int EPS>
 __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     const int32_t* __restrict__ prim_ids, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges, const float4* __restrict__ seg_bbox,
@@ -255,21 +288,23 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     const float inv_e = 1.0f / (float)eps;
     float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
     const int gstart = min(g1 - 1, wave_max_i(fidx));
+    int pid_next = gstart >= g0 ? prim_ids[gstart] : 0;
     for (int g = gstart; g >= g0; --g) {
         const bool valid = in_img & (g <= fidx);
+        const int pid = pid_next;
+        pid_next = prim_ids[max(g - 1, g0)];
         if (__ballot(valid) == 0) continue;
-        const int pid = prim_ids[g];
         const PrimRec pr = prims[pid];
         const float D2 = pr.cull_d * pr.cull_d;
         if (prim_culled<MODE>(pr, R, D2)) continue;
         Geom G;
-        prim_geometry<MODE, true>(pr, R, D2, seg_bbox, edges, eps, px, py, G);
+        prim_geometry<MODE, true, EPS>(pr, R, D2, seg_bbox, edges, eps, px, py, G);
         float vr = 0.0f, vg = 0.0f, vb = 0.0f, vop = 0.0f, vis2 = 0.0f, vsw = 0.0f;
         float cr = 0.0f, cg = 0.0f, cb = 0.0f;
         float gx = 0.0f, gy = 0.0f;
         bool contrib = false, geom = false;
         if (valid) {
-            const Cov c = coverage<MODE>(pr, G);
+            const Cov c = coverage<MODE>(pr, G, D2);
             const float op = pr.opacity;
             const float alpha = fminf(kAlphaCap, op * c.cov);
             if (alpha >= kAlphaMin) {
@@ -441,6 +476,80 @@ static int raster_status() {
     return hipGetLastError() == hipSuccess ? CS_OK : CS_ERR_HIP;
 }
 
+struct RasterArgs {
+    int mode, nt, tbx, img_h, img_w, eps;
+    const int32_t* ids;
+    const int32_t* bins;
+    const EdgeRec* E;
+    const float4* B;
+    const PrimRec* P;
+    const float* bg;
+    // forward outputs
+    float* out;
+    float* final_T;
+    int32_t* final_idx;
+    // backward inputs / outputs
+    const float* fT;
+    const int32_t* fidx;
+    const float* v_out;
+    float *v_cub, *v_col, *v_op, *v_is2, *v_sw, *c_rgb, *c_isect;
+    hipStream_t stream;
+};
+
+template <int MODE, int EPS>
+static void launch_fwd(const RasterArgs& a) {
+    hipLaunchKernelGGL((k_raster_fwd<MODE, EPS>), dim3(a.nt), dim3(kBlockThreads), 0, a.stream,
+                       a.ids, a.bins, a.E, a.B, a.P, a.bg, a.img_h, a.img_w, a.tbx, a.nt, a.eps,
+                       a.out, a.final_T, a.final_idx);
+}
+
+template <int MODE, int EPS>
+static void launch_bwd(const RasterArgs& a) {
+    hipLaunchKernelGGL((k_raster_bwd<MODE, EPS>), dim3(a.nt), dim3(kBlockThreads), 0, a.stream,
+                       a.ids, a.bins, a.E, a.B, a.P, a.bg, a.img_h, a.img_w, a.tbx, a.nt, a.eps,
+                       a.fT, a.fidx, a.v_out, a.v_cub, a.v_col, a.v_op, a.v_is2, a.v_sw, a.c_rgb,
+                       a.c_isect);
+}
+
+// Edge counts per segment with an unrolled instantiation: S = 8, 12, 16, 18,
+// 24, 32 samples (the training defaults 12/18, the paper's 24, the configs'
+// 8/16/32); any other count runs the generic loop.
+template <bool BWD, int MODE>
+static void dispatch(const RasterArgs& a) {
+#define CS_LAUNCH(E_) (BWD ? launch_bwd<MODE, E_>(a) : launch_fwd<MODE, E_>(a))
+    switch (a.eps) {
+        case 7: CS_LAUNCH(7); break;
+        case 11: CS_LAUNCH(11); break;
+        case 15: CS_LAUNCH(15); break;
+        case 17: CS_LAUNCH(17); break;
+        case 23: CS_LAUNCH(23); break;
+        case 31: CS_LAUNCH(31); break;
+        default: CS_LAUNCH(0); break;
+    }
+#undef CS_LAUNCH
+}
+
+static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* bins,
+                              const void* edges, const float* seg_bbox, const void* prims,
+                              const float* bg, int32_t img_h, int32_t img_w, int32_t eps,
+                              hipStream_t stream) {
+    RasterArgs a{};
+    a.mode = mode;
+    a.tbx = (img_w + kTile - 1) / kTile;
+    a.nt = a.tbx * ((img_h + kTile - 1) / kTile);
+    a.img_h = img_h;
+    a.img_w = img_w;
+    a.eps = eps;
+    a.ids = ids;
+    a.bins = bins;
+    a.E = reinterpret_cast<const EdgeRec*>(edges);
+    a.B = reinterpret_cast<const float4*>(seg_bbox);
+    a.P = reinterpret_cast<const PrimRec*>(prims);
+    a.bg = bg;
+    a.stream = stream;
+    return a;
+}
+
 extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                                     const int32_t* tile_bins, const void* edges,
                                     const float* seg_bbox, const void* prim_recs,
@@ -449,19 +558,13 @@ extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted
                                     int32_t* final_idx, hipStream_t stream) {
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1)
         return CS_ERR_ARGS;
-    const int tbx = (img_w + kTile - 1) / kTile, tby = (img_h + kTile - 1) / kTile;
-    const int nt = tbx * tby;
-    auto* E = reinterpret_cast<const EdgeRec*>(edges);
-    auto* B = reinterpret_cast<const float4*>(seg_bbox);
-    auto* P = reinterpret_cast<const PrimRec*>(prim_recs);
-    if (mode == 0)
-        hipLaunchKernelGGL(k_raster_fwd<0>, dim3(nt), dim3(kBlockThreads), 0, stream,
-                           prim_ids_sorted, tile_bins, E, B, P, background, img_h, img_w, tbx, nt,
-                           edges_per_segment, out_img, final_Ts, final_idx);
-    else
-        hipLaunchKernelGGL(k_raster_fwd<1>, dim3(nt), dim3(kBlockThreads), 0, stream,
-                           prim_ids_sorted, tile_bins, E, B, P, background, img_h, img_w, tbx, nt,
-                           edges_per_segment, out_img, final_Ts, final_idx);
+    RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, seg_bbox, prim_recs,
+                               background, img_h, img_w, edges_per_segment, stream);
+    a.out = out_img;
+    a.final_T = final_Ts;
+    a.final_idx = final_idx;
+    if (mode == 0) dispatch<false, 0>(a);
+    else dispatch<false, 1>(a);
     return raster_status();
 }
 
@@ -478,23 +581,20 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1)
         return CS_ERR_ARGS;
     if (mode == 1 && v_stroke_widths == nullptr) return CS_ERR_ARGS;
-    const int tbx = (img_w + kTile - 1) / kTile, tby = (img_h + kTile - 1) / kTile;
-    const int nt = tbx * tby;
-    auto* E = reinterpret_cast<const EdgeRec*>(edges);
-    auto* B = reinterpret_cast<const float4*>(seg_bbox);
-    auto* P = reinterpret_cast<const PrimRec*>(prim_recs);
-    if (mode == 0)
-        hipLaunchKernelGGL(k_raster_bwd<0>, dim3(nt), dim3(kBlockThreads), 0, stream,
-                           prim_ids_sorted, tile_bins, E, B, P, background, img_h, img_w, tbx, nt,
-                           edges_per_segment, final_Ts, final_idx, v_output, v_cubics_px,
-                           v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
-                           curve_contrib_rgb, curve_isect_contrib);
-    else
-        hipLaunchKernelGGL(k_raster_bwd<1>, dim3(nt), dim3(kBlockThreads), 0, stream,
-                           prim_ids_sorted, tile_bins, E, B, P, background, img_h, img_w, tbx, nt,
-                           edges_per_segment, final_Ts, final_idx, v_output, v_cubics_px,
-                           v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
-                           curve_contrib_rgb, curve_isect_contrib);
+    RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, seg_bbox, prim_recs,
+                               background, img_h, img_w, edges_per_segment, stream);
+    a.fT = final_Ts;
+    a.fidx = final_idx;
+    a.v_out = v_output;
+    a.v_cub = v_cubics_px;
+    a.v_col = v_colors;
+    a.v_op = v_opacities;
+    a.v_is2 = v_inv_sigma2s;
+    a.v_sw = v_stroke_widths;
+    a.c_rgb = curve_contrib_rgb;
+    a.c_isect = curve_isect_contrib;
+    if (mode == 0) dispatch<true, 0>(a);
+    else dispatch<true, 1>(a);
     return raster_status();
 }
 

@@ -20,7 +20,6 @@ DEFAULT_SSIM_BLOCK_H = 8
 DEFAULT_SSIM_BLOCK_W = 16
 
 _WINDOW_CACHE: Dict[Tuple[str, int, float], torch.Tensor] = {}
-_TICKETS: Dict[Tuple[str, int], torch.Tensor] = {}
 
 
 def _validate_pair_4d(x: torch.Tensor, y: torch.Tensor) -> None:
@@ -38,17 +37,6 @@ def _as_f32(x: torch.Tensor, name: str) -> torch.Tensor:
     if x.device.type != "cuda":
         raise ValueError(f"{name} must be a CUDA tensor")
     return x.detach().to(torch.float32).contiguous()
-
-
-def _ticket(device: torch.device) -> torch.Tensor:
-    """A device counter that every loss kernel leaves at zero.  One per
-    (device, stream): calls on one stream are ordered, so they may share it."""
-    key = (str(device), torch.cuda.current_stream(device).cuda_stream)
-    t = _TICKETS.get(key)
-    if t is None:
-        t = torch.zeros((1,), dtype=torch.int32, device=device)
-        _TICKETS[key] = t
-    return t
 
 
 def gaussian_window_1d(win_size: int, win_sigma: float, device) -> torch.Tensor:
@@ -72,8 +60,8 @@ def mse_forward(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
     partials = torch.empty((int(N.lib().cs_mse_partials_elems(n)),), dtype=torch.float32,
                            device=dev)
     loss = torch.empty((), dtype=torch.float32, device=dev)
-    N.call("cs_mse_forward", N.ptr(x), N.ptr(y), n, N.ptr(partials), N.ptr(_ticket(dev)),
-           N.ptr(loss), N.stream(dev))
+    N.call("cs_mse_forward", N.ptr(x), N.ptr(y), n, N.ptr(partials), N.ptr(loss),
+           N.stream(dev))
     return loss
 
 
@@ -141,7 +129,7 @@ def _ssim_forward(x32, y32, win_size, win_sigma, c1, c2, want_grad):
     abc = (torch.empty((3, n * c, oh, ow), dtype=torch.float32, device=dev)
            if want_grad else None)
     N.call("cs_ssim", N.ptr(x32), N.ptr(y32), n * c, h, w, N.ptr(g), int(win_size),
-           float(c1), float(c2), N.ptr(partials), N.ptr(_ticket(dev)), N.ptr(out), N.ptr(abc),
+           float(c1), float(c2), N.ptr(partials), N.ptr(out), N.ptr(abc),
            N.stream(dev))
     return out, abc, g
 

@@ -38,7 +38,7 @@ def test_mse_forward_backward(shape):
 
 
 @pytest.mark.gpu
-def test_mse_repeated_calls_reset_ticket():
+def test_mse_repeated_calls_deterministic():
     import manbo
     x, y = _pair((1, 3, 64, 64), 2)
     vals = [float(manbo.mse_loss_tilelang(x.cuda(), y.cuda())) for _ in range(5)]
