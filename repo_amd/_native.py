@@ -15,7 +15,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libcubicsplat_hip.so")
 
 CS_OK, CS_ERR_ARGS, CS_ERR_HIP = 0, 1, 2
-EDGE_RECORD_FLOATS = 8   # 32-byte edge record
+EDGE_RECORD_FLOATS = 12  # 48-byte edge record
+SEG_RECORD_INTS = 4      # 16-byte segment record
 PRIM_RECORD_FLOATS = 16  # 64-byte primitive record
 
 _P = ctypes.c_void_p

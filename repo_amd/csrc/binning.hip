@@ -119,6 +119,47 @@ __device__ __forceinline__ int owner_of(const int32_t* __restrict__ offs, int P,
     return lo;
 }
 
+// Conservative distance beyond which a pixel's coverage of this primitive is
+// decided without its exact distance: fill -> alpha < 1/255 outside, coverage
+// exactly 1.0f inside (2 d inv_sigma >= 16.64 makes 1 + exp(-.) round to 1);
+// stroke -> alpha < 1/255.  Margins absorb fp32 rounding of the cull tests.
+__device__ __forceinline__ float cull_distance(int mode, float opacity, float inv_sigma,
+                                               float half_sw) {
+    if (!(opacity <= 3.0e38f)) return __builtin_huge_valf();
+    const float lo = __logf(fmaxf(255.0f * opacity, 1.0f));
+    if (mode == 0) return fmaxf(9.5f, 0.5f * (lo + 1.0f)) / inv_sigma + 0.25f;
+    return half_sw + __builtin_sqrtf(2.0f * lo + 1.0f) / inv_sigma + 0.25f;
+}
+
+struct PrimParams {
+    float inv_sigma2;  // 1 / max(w^2, eps) (cubic_splatting.py:2820-2821)
+    float inv_sigma;   // sqrt(max(inv_sigma2, eps))
+    float half_sw;
+    float cull_d;
+};
+
+__device__ __forceinline__ PrimParams prim_params(int mode, float aa_width, float opacity,
+                                                  const float* __restrict__ stroke_widths,
+                                                  int p) {
+    PrimParams q;
+    const float w = fmaxf(aa_width, kWidthMin);
+    q.inv_sigma2 = 1.0f / fmaxf(w * w, kEps);
+    q.inv_sigma = __builtin_sqrtf(fmaxf(q.inv_sigma2, kEps));
+    q.half_sw = (mode == 1 && stroke_widths) ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
+    q.cull_d = cull_distance(mode, opacity, q.inv_sigma, q.half_sw);
+    return q;
+}
+
+__device__ __forceinline__ int32_t px_index(float v) {
+    return f2i_sat(fminf(fmaxf(v, -40000.0f), 40000.0f));
+}
+
+// Packed range of pixel indices k whose centre k + 0.5 can lie in
+// [lo - d, hi + d], widened by one pixel on each side.
+__device__ __forceinline__ int32_t pixel_range(float lo, float hi, float d) {
+    return pack_range(px_index(floorf(lo - d - 0.5f)) - 1, px_index(ceilf(hi + d - 0.5f)) + 1);
+}
+
 // torch.linspace(0, 1, S)[i] as ATen's device kernel computes it.
 __device__ __forceinline__ float linspace01(int S, int i) {
     const float step = 1.0f / (float)(S - 1);
@@ -127,16 +168,18 @@ __device__ __forceinline__ float linspace01(int S, int i) {
 
 __global__ __launch_bounds__(256) void k_project_flatten(
     const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
-    const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
-    int img_h, int img_w, int block_x, int block_y, float aabb_pad, int aniso, int S,
-    float* __restrict__ cubics_px, int32_t* __restrict__ seg_tile_ranges,
-    float4* __restrict__ seg_bbox, EdgeRec* __restrict__ edges) {
+    const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths,
+    const float* __restrict__ opacities, int mode, int nseg, int img_h, int img_w, int block_x,
+    int block_y, float aabb_pad, int aniso, int S, float* __restrict__ cubics_px,
+    int32_t* __restrict__ seg_tile_ranges, SegRec* __restrict__ seg_recs,
+    EdgeRec* __restrict__ edges) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
     const int p = owner_of(seg_offsets, P, s);
     const float w = fmaxf(aa_widths[p], kWidthMin);
     const float support = fmaxf(0.0f, w * 3.0f);
     const float half_sw = stroke_widths ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
+    const float D = prim_params(mode, aa_widths[p], opacities[p], stroke_widths, p).cull_d;
     const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
     const SegProj r = project_segment(cubics_norm + (size_t)s * 8, 0.5f * (float)img_w,
                                       0.5f * (float)img_h, half_sw, support, aabb_pad, aniso, tbx,
@@ -171,31 +214,30 @@ __global__ __launch_bounds__(256) void k_project_flatten(
             const float vx = x - prevx, vy = y - prevy;
             const float vv = vx * vx + vy * vy;
             const float ivv = 1.0f / fmaxf(vv, kEps);
-            float4* o = reinterpret_cast<float4*>(er + (i - 1));
-            o[0] = make_float4(prevx, prevy, x, y);
-            o[1] = make_float4(vx, vy, vx * ivv, vy * ivv);
+            const float ex0 = fminf(prevx, x), ex1 = fmaxf(prevx, x);
+            const float ey0 = fminf(prevy, y), ey1 = fmaxf(prevy, y);
+            int4* o = reinterpret_cast<int4*>(er + (i - 1));
+            o[0] = make_int4(__builtin_bit_cast(int, prevx), __builtin_bit_cast(int, prevy),
+                             __builtin_bit_cast(int, x), __builtin_bit_cast(int, y));
+            o[1] = make_int4(__builtin_bit_cast(int, vx), __builtin_bit_cast(int, vy),
+                             __builtin_bit_cast(int, vx * ivv), __builtin_bit_cast(int, vy * ivv));
+            o[2] = make_int4(pixel_range(ex0, ex1, D), pixel_range(ey0, ey1, D),
+                             pixel_range(ey0, ey1, 0.0f), 0);
         }
         prevx = x;
         prevy = y;
     }
-    seg_bbox[s] = make_float4(bx0, by0, bx1, by1);
-}
-
-// Conservative distance beyond which a pixel's coverage of this primitive is
-// decided without its exact distance: fill -> alpha < 1/255 outside, coverage
-// exactly 1.0f inside (2 d inv_sigma >= 16.64 makes 1 + exp(-.) round to 1);
-// stroke -> alpha < 1/255.  Margins absorb fp32 rounding of the cull test.
-__device__ __forceinline__ float cull_distance(int mode, float opacity, float inv_sigma,
-                                               float half_sw) {
-    if (!(opacity <= 3.0e38f)) return __builtin_huge_valf();
-    const float lo = __logf(fmaxf(255.0f * opacity, 1.0f));
-    if (mode == 0) return fmaxf(9.5f, 0.5f * (lo + 1.0f)) / inv_sigma + 0.25f;
-    return half_sw + __builtin_sqrtf(2.0f * lo + 1.0f) / inv_sigma + 0.25f;
+    SegRec sr;
+    sr.near_x = pixel_range(bx0, bx1, D);
+    sr.near_y = pixel_range(by0, by1, D);
+    sr.cross_y = pixel_range(by0, by1, 0.0f);
+    sr.x_last = px_index(ceilf(bx1 - 0.5f)) + 1;
+    seg_recs[s] = sr;
 }
 
 __global__ __launch_bounds__(256) void k_prim_prep(
     const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
-    const int32_t* __restrict__ seg_tile_ranges, const float4* __restrict__ seg_bbox,
+    const int32_t* __restrict__ seg_tile_ranges, const SegRec* __restrict__ seg_recs,
     const float* __restrict__ colors, const float* __restrict__ opacities,
     const float* __restrict__ depths, const int32_t* __restrict__ fill_rules,
     const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
@@ -229,12 +271,9 @@ __global__ __launch_bounds__(256) void k_prim_prep(
     reinterpret_cast<int4*>(prim_tile_ranges)[p] = tr;
     counts[p] = area;
 
-    // cubic_splatting.py:2820-2821 (widths clamp, inv_sigma2).
-    const float w = fmaxf(aa_widths[p], kWidthMin);
-    const float is2 = 1.0f / fmaxf(w * w, kEps);
-    inv_sigma2s[p] = is2;
-    const float is2c = fmaxf(is2, kEps);
-    const float isig = __builtin_sqrtf(is2c);
+    // cubic_splatting.py:2820-2821 (widths clamp, inv_sigma2) and the cull distance.
+    const PrimParams q = prim_params(mode, aa_widths[p], opacities[p], stroke_widths, p);
+    inv_sigma2s[p] = q.inv_sigma2;
 
     // cubic_splatting.py:801-805: float order as unsigned order.
     const int32_t bits = __builtin_bit_cast(int32_t, depths[p]);
@@ -246,26 +285,32 @@ __global__ __launch_bounds__(256) void k_prim_prep(
     rec.g = colors[3 * p + 1];
     rec.b = colors[3 * p + 2];
     rec.opacity = opacities[p];
-    rec.inv_sigma2 = is2c;
-    rec.inv_sigma = isig;
-    rec.half_sw = (mode == 1 && stroke_widths) ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
-    rec.cull_d = cull_distance(mode, rec.opacity, isig, rec.half_sw);
+    rec.inv_sigma2 = fmaxf(q.inv_sigma2, kEps);
+    rec.inv_sigma = q.inv_sigma;
+    rec.half_sw = q.half_sw;
+    rec.cull_d = q.cull_d;
     rec.s0 = s0;
     rec.s1 = s1;
     rec.rule = fill_rules ? fill_rules[p] : 1;
     int closed = 1;
-    float bx0 = __builtin_huge_valf(), by0 = bx0, bx1 = -bx0, by1 = -bx0;
+    const int32_t empty = pack_range(32767, -32768);
+    int32_t nxr = empty, nyr = empty, cyr = empty, x_last = -32768;
     for (int s = s0; s < s1; ++s) {
         const int nx = (s + 1 < s1) ? s + 1 : s0;
         const float* a = cubics_norm + (size_t)s * 8;
         const float* b = cubics_norm + (size_t)nx * 8;
         closed &= (a[6] == b[0]) & (a[7] == b[1]);
-        const float4 bb = seg_bbox[s];
-        bx0 = fminf(bx0, bb.x); by0 = fminf(by0, bb.y);
-        bx1 = fmaxf(bx1, bb.z); by1 = fmaxf(by1, bb.w);
+        const SegRec sr = seg_recs[s];
+        nxr = range_union(nxr, sr.near_x);
+        nyr = range_union(nyr, sr.near_y);
+        cyr = range_union(cyr, sr.cross_y);
+        x_last = max(x_last, sr.x_last);
     }
     rec.closed = closed;
-    rec.bx0 = bx0; rec.by0 = by0; rec.bx1 = bx1; rec.by1 = by1;
+    rec.near_x = nxr;
+    rec.near_y = nyr;
+    rec.cross_y = cyr;
+    rec.x_last = x_last;
     recs[p] = rec;
 }
 
@@ -677,7 +722,7 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                               const float* stroke_widths, int32_t nseg, int32_t nprim,
                               int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
                               int32_t samples, float aabb_pad, int32_t aniso, int32_t mode,
-                              float* cubics_px, int32_t* seg_tile_ranges, float* seg_bbox,
+                              float* cubics_px, int32_t* seg_tile_ranges, void* seg_recs,
                               void* edges, int32_t* prim_tile_ranges, uint32_t* num_tiles_hit,
                               float* inv_sigma2s, void* prim_recs, uint32_t* keys,
                               int32_t* order, uint32_t* keys_alt, int32_t* vals_alt,
@@ -690,13 +735,13 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
     hipLaunchKernelGGL(k_status_init, dim3(1), dim3(1), 0, stream, seg_offsets, nprim, status);
     if (nseg > 0)
         hipLaunchKernelGGL(k_project_flatten, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
-                           cubics_norm, seg_offsets, nprim, aa_widths, stroke_widths, nseg, img_h,
-                           img_w, block_x, block_y, aabb_pad, aniso, samples, cubics_px,
-                           seg_tile_ranges, reinterpret_cast<float4*>(seg_bbox),
+                           cubics_norm, seg_offsets, nprim, aa_widths, stroke_widths, opacities,
+                           mode, nseg, img_h, img_w, block_x, block_y, aabb_pad, aniso, samples,
+                           cubics_px, seg_tile_ranges, reinterpret_cast<SegRec*>(seg_recs),
                            reinterpret_cast<EdgeRec*>(edges));
     hipLaunchKernelGGL(k_prim_prep, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
                        cubics_norm, seg_offsets, nprim, seg_tile_ranges,
-                       reinterpret_cast<const float4*>(seg_bbox), colors, opacities, depths,
+                       reinterpret_cast<const SegRec*>(seg_recs), colors, opacities, depths,
                        fill_rules, aa_widths, stroke_widths, nseg, tbx, tby, mode, status,
                        prim_tile_ranges,
                        num_tiles_hit, inv_sigma2s, keys, order,

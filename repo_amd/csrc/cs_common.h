@@ -23,9 +23,23 @@ constexpr float kWidthMin = (float)1e-4;
 
 // One flattened polyline edge, 32 bytes: endpoints, direction v = p1 - p0 and
 // u = v / max(|v|^2, eps) (multiply by the correctly rounded reciprocal).
-struct alignas(32) EdgeRec {
+//
+// Cull ranges are inclusive integer pixel ranges packed as two int16 (low
+// half = first, high half = last): `near_x`/`near_y` hold every pixel column /
+// row whose centre can lie within the owning primitive's cull distance of the
+// geometry, `cross_y` every pixel row whose centre lies in the geometry's
+// y-range (where a +x ray crossing is possible).  Each range is widened by
+// one pixel beyond its fp32 bound, so integer tests on them are conservative.
+struct alignas(16) EdgeRec {
     float x0, y0, x1, y1;
     float vx, vy, ux, uy;
+    int32_t near_x, near_y, cross_y, pad;
+};
+
+// Per cubic segment: the cull ranges of all its edges, plus the last pixel
+// column that can lie left of one of its vertices (for open chains).
+struct alignas(16) SegRec {
+    int32_t near_x, near_y, cross_y, x_last;
 };
 
 // Per-primitive raster record, built once per forward.
@@ -38,8 +52,42 @@ struct alignas(16) PrimRec {
     int32_t s0, s1;     // segment range
     int32_t rule;       // 0 even-odd, else nonzero (fill)
     int32_t closed;     // 1 if the edge chain is closed
-    float bx0, by0, bx1, by1;  // bounding box of the polyline vertices
+    int32_t near_x, near_y, cross_y, x_last;  // unions over the segments
 };
+
+// Read-only data for the raster kernels, reached through the constant address
+// space so that wave-uniform loads compile to scalar (SMEM) loads even in
+// kernels that also issue global atomics.
+// (The host pass that parses the kernels has no address spaces.)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define CS_CONST __attribute__((address_space(4)))
+#else
+#define CS_CONST
+#endif
+template <class T>
+using cptr = const CS_CONST T*;
+template <class T>
+__device__ __forceinline__ cptr<T> as_const(const T* p) {
+    return (cptr<T>)p;
+}
+
+__device__ __forceinline__ int32_t pack_range(int32_t lo, int32_t hi) {
+    lo = lo < -32768 ? -32768 : (lo > 32767 ? 32767 : lo);
+    hi = hi < -32768 ? -32768 : (hi > 32767 ? 32767 : hi);
+    return (int32_t)(((uint32_t)hi << 16) | ((uint32_t)lo & 0xffffu));
+}
+__device__ __forceinline__ int32_t range_lo(int32_t v) { return (int32_t)(v << 16) >> 16; }
+__device__ __forceinline__ int32_t range_hi(int32_t v) { return v >> 16; }
+
+// Union of two packed ranges.
+__device__ __forceinline__ int32_t range_union(int32_t a, int32_t b) {
+    return pack_range(min(range_lo(a), range_lo(b)), max(range_hi(a), range_hi(b)));
+}
+
+// Inclusive ranges [first, last] overlap.
+__device__ __forceinline__ bool range_hits(int32_t v, int32_t first, int32_t last) {
+    return range_lo(v) <= last && range_hi(v) >= first;
+}
 
 // exp(x): n = rint(x log2 e), r = x - n ln2 (two-part Cody-Waite), e^r by a
 // degree-7 Taylor polynomial in Horner form, scaled by 2^n in two exact steps.

@@ -3,17 +3,19 @@
 // Launch: one 256-thread workgroup per 16x16 tile.  Unlike a block-synchronous
 // design, each of the four waves owns four tile rows (64 pixels, one per lane)
 // and walks the tile's sorted list on its own: the list entry, the primitive
-// record, the segment boxes and the edge records are wave-uniform, so they
+// record, the segment records and the edge records are wave-uniform, so they
 // are read through the scalar cache and used as SGPR operands, and no LDS or
 // workgroup barrier is needed.  A wave leaves the list when all of its pixels
 // have reached the transmittance stop.
 //
-// Exactness-preserving culling per wave: a segment whose vertex box is farther
-// than the primitive's cull distance from the wave's pixel rectangle cannot
-// change any lane's result (outside: alpha < 1/255; inside: coverage is
+// Exactness-preserving culling per wave, on integer pixel ranges tested with
+// scalar instructions: geometry whose near ranges miss the wave's pixel
+// rectangle is farther than the primitive's cull distance from every lane and
+// cannot change any lane's result (outside: alpha < 1/255; inside: coverage is
 // exactly 1.0f), so its distance terms are skipped; its crossing terms are
-// skipped when its y-range misses the wave's four pixel rows.  Results stay
-// bit-identical to evaluating every edge.
+// skipped when its y-range misses the wave's four pixel rows.  The forward
+// culls per primitive and per segment, the backward also per edge.  Results
+// stay bit-identical to evaluating every edge.
 #include "cs_common.h"
 #include "../../include/cubicsplat_hip.h"
 
@@ -21,6 +23,7 @@ namespace cs {
 
 static_assert(sizeof(EdgeRec) == CS_EDGE_RECORD_BYTES, "edge record layout");
 static_assert(sizeof(PrimRec) == CS_PRIM_RECORD_BYTES, "primitive record layout");
+static_assert(sizeof(SegRec) == CS_SEG_RECORD_BYTES, "segment record layout");
 
 // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
 // contiguous run of tiles so neighbouring tiles (which share primitives and
@@ -40,41 +43,60 @@ struct Geom {
     float bproj, bdx, bdy;
 };
 
-// Distance (and optionally the best edge) and +x ray crossings of one edge,
-// cubic_splatting.py:1095-1134 / 1451-1501.
-template <bool DIST, bool CROSS, bool BEST>
-__device__ __forceinline__ void edge_step(const EdgeRec& E, int eid, float px, float py,
+// Wave-uniform integer pixel rectangle: columns [c0, c1], rows [r0, r1].
+struct WaveRect {
+    int c0, c1, r0, r1;
+};
+
+__device__ __forceinline__ bool near_wave(int32_t near_x, int32_t near_y, const WaveRect& W) {
+    return range_hits(near_x, W.c0, W.c1) && range_hits(near_y, W.r0, W.r1);
+}
+
+__device__ __forceinline__ bool rows_hit(int32_t cross_y, const WaveRect& W) {
+    return range_hits(cross_y, W.r0, W.r1);
+}
+
+// Distance (and optionally the best edge) of one edge, with w = pixel - p0,
+// cubic_splatting.py:1095-1118 / 1451-1484.
+template <bool BEST>
+__device__ __forceinline__ void dist_term(const EdgeRec& E, int eid, float wx, float wy,
                                           Geom& G) {
-    {
-        const float wx = px - E.x0, wy = py - E.y0;
-        if (DIST) {
-            float proj = __builtin_fmaf(wx, E.ux, wy * E.uy);
-            proj = fminf(fmaxf(proj, 0.0f), 1.0f);
-            const float dx = __builtin_fmaf(proj, E.vx, -wx);
-            const float dy = __builtin_fmaf(proj, E.vy, -wy);
-            const float d2 = __builtin_fmaf(dx, dx, dy * dy);
-            if (BEST) {
-                if (d2 < G.min_d2) {
-                    G.min_d2 = d2;
-                    G.best = eid;
-                    G.bproj = proj;
-                    G.bdx = dx;
-                    G.bdy = dy;
-                }
-            } else {
-                G.min_d2 = fminf(G.min_d2, d2);
-            }
+    float proj = __builtin_fmaf(wx, E.ux, wy * E.uy);
+    proj = fminf(fmaxf(proj, 0.0f), 1.0f);
+    const float dx = __builtin_fmaf(proj, E.vx, -wx);
+    const float dy = __builtin_fmaf(proj, E.vy, -wy);
+    const float d2 = __builtin_fmaf(dx, dx, dy * dy);
+    if (BEST) {
+        if (d2 < G.min_d2) {
+            G.min_d2 = d2;
+            G.best = eid;
+            G.bproj = proj;
+            G.bdx = dx;
+            G.bdy = dy;
         }
-        if (CROSS) {
-            // Upward crossing (y0 <= py < y1) counts +1 when the edge passes
-            // right of the pixel (cross product > 0), downward -1 when < 0.
-            const bool b0 = E.y0 <= py, b1 = E.y1 <= py;
-            const float cr = __builtin_fmaf(wy, E.vx, -(wx * E.vy));
-            const bool hit = (b0 != b1) & ((b0 ? cr : -cr) > 0.0f);
-            G.winding += (int)(hit & b0);
-            G.winding -= (int)(hit & !b0);
-        }
+    } else {
+        G.min_d2 = fminf(G.min_d2, d2);
     }
+}
+
+// +x ray crossing of one edge, cubic_splatting.py:1119-1134 / 1485-1501.
+// Upward crossing (y0 <= py < y1) counts +1 when the edge passes right of the
+// pixel (cross product > 0), downward -1 when < 0.
+__device__ __forceinline__ void cross_term(const EdgeRec& E, float wx, float wy, float py,
+                                           Geom& G) {
+    const bool b0 = E.y0 <= py, b1 = E.y1 <= py;
+    const float cr = __builtin_fmaf(wy, E.vx, -(wx * E.vy));
+    const bool hit = (b0 != b1) & ((b0 ? cr : -cr) > 0.0f);
+    G.winding += (int)(hit & b0);
+    G.winding -= (int)(hit & !b0);
+}
+
+template <bool DIST, bool CROSS, bool BEST>
+__device__ __forceinline__ void edge_eval(const EdgeRec& E, int eid, float px, float py,
+                                          Geom& G) {
+    const float wx = px - E.x0, wy = py - E.y0;
+    if (DIST) dist_term<BEST>(E, eid, wx, wy, G);
+    if (CROSS) cross_term(E, wx, wy, py, G);
 }
 
 // Unroll factor of the best-edge (backward) loop: a full unroll keeps too many
@@ -83,41 +105,77 @@ __device__ __forceinline__ void edge_step(const EdgeRec& E, int eid, float px, f
 #define CS_BEST_UNROLL 3
 #endif
 
-// One segment's edges; EPS > 0 fixes the edge count at compile time so the
-// loop unrolls and the scalar loads of the edge records batch up.
-template <bool DIST, bool CROSS, bool BEST, int EPS>
-__device__ __forceinline__ void scan_edges(const EdgeRec* __restrict__ ep, int n, int ebase,
-                                           float px, float py, Geom& G) {
-    if constexpr (EPS > 0 && !BEST) {
+// Every edge of one segment with the same terms (forward).  EPS > 0 fixes the
+// edge count at compile time: the loop unrolls, its scalar loads batch up and
+// it has no branches.
+template <bool DIST, bool CROSS, int EPS>
+__device__ __forceinline__ void scan_all(cptr<EdgeRec> ep, int n, float px, float py, Geom& G) {
+    if constexpr (EPS > 0) {
 #pragma unroll
-        for (int e = 0; e < EPS; ++e) edge_step<DIST, CROSS, BEST>(ep[e], ebase + e, px, py, G);
-    } else if constexpr (EPS > 0) {
-#pragma unroll CS_BEST_UNROLL
-        for (int e = 0; e < EPS; ++e) edge_step<DIST, CROSS, BEST>(ep[e], ebase + e, px, py, G);
+        for (int e = 0; e < EPS; ++e) edge_eval<DIST, CROSS, false>(ep[e], 0, px, py, G);
     } else {
 #pragma unroll 4
-        for (int e = 0; e < n; ++e) edge_step<DIST, CROSS, BEST>(ep[e], ebase + e, px, py, G);
+        for (int e = 0; e < n; ++e) edge_eval<DIST, CROSS, false>(ep[e], 0, px, py, G);
     }
 }
 
-struct WaveRect {
-    float x0, y0, x1, y1;  // pixel centres covered by the wave
-};
+// One edge of the backward scan, with its wave-uniform cull decisions: the
+// distance terms only where the edge's near ranges meet the wave, the
+// crossing terms only where its y-range meets the wave's rows.
+template <bool MAYCROSS>
+__device__ __forceinline__ void edge_culled(const EdgeRec& E, int eid, bool seg_near,
+                                            bool seg_band, const WaveRect& W, float px,
+                                            float py, Geom& G) {
+    const bool dn = seg_near && near_wave(E.near_x, E.near_y, W);
+    const bool cb = MAYCROSS && seg_band && rows_hit(E.cross_y, W);
+    if (!(dn || cb)) return;
+    const float wx = px - E.x0, wy = py - E.y0;
+    if (dn) dist_term<true>(E, eid, wx, wy, G);
+    if (cb) cross_term(E, wx, wy, py, G);
+}
+
+// One segment's edges with per-edge culling (backward: its per-lane work per
+// evaluated edge is larger, so skipping edges pays for the branches).  The
+// records of a chunk are loaded before any of them is tested, so their scalar
+// loads are in flight together.
+template <bool MAYCROSS, int EPS>
+__device__ __forceinline__ void scan_culled(cptr<EdgeRec> ep, int n, int ebase, bool seg_near,
+                                            bool seg_band, const WaveRect& W, float px,
+                                            float py, Geom& G) {
+    if constexpr (EPS > 0) {
+        constexpr int CH = CS_BEST_UNROLL;
+#pragma unroll
+        for (int c0 = 0; c0 < EPS; c0 += CH) {
+            EdgeRec Es[CH];
+#pragma unroll
+            for (int k = 0; k < CH; ++k)
+                if (c0 + k < EPS) Es[k] = ep[c0 + k];
+#pragma unroll
+            for (int k = 0; k < CH; ++k)
+                if (c0 + k < EPS)
+                    edge_culled<MAYCROSS>(Es[k], ebase + c0 + k, seg_near, seg_band, W, px, py, G);
+        }
+    } else {
+#pragma unroll 4
+        for (int e = 0; e < n; ++e)
+            edge_culled<MAYCROSS>(ep[e], ebase + e, seg_near, seg_band, W, px, py, G);
+    }
+}
 
 // Primitive-level cull: true when no lane of the wave can be affected.
 template <int MODE>
-__device__ __forceinline__ bool prim_culled(const PrimRec& pr, const WaveRect& R, float D2) {
-    if (rect_box_d2(R.x0, R.y0, R.x1, R.y1, pr.bx0, pr.by0, pr.bx1, pr.by1) <= D2) return false;
+__device__ __forceinline__ bool prim_culled(const PrimRec& pr, const WaveRect& W) {
+    if (near_wave(pr.near_x, pr.near_y, W)) return false;
     if (MODE == 1 || pr.closed) return true;
     // Open chain in fill mode: the winding number can be non-zero left of the
-    // box, but not when the rows miss the box or the wave is right of it.
-    return pr.by0 > R.y1 || pr.by1 < R.y0 || R.x0 > pr.bx1;
+    // vertices, but not when the rows miss their y-range or the wave lies
+    // right of every vertex.
+    return !rows_hit(pr.cross_y, W) || W.c0 > pr.x_last;
 }
 
 template <int MODE, bool BEST, int EPS>
-__device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& R, float D2,
-                                              const float4* __restrict__ seg_bbox,
-                                              const EdgeRec* __restrict__ edges, int eps,
+__device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& W,
+                                              cptr<SegRec> segs, cptr<EdgeRec> edges, int eps,
                                               float px, float py, Geom& G) {
     G.min_d2 = 1e30f;
     G.winding = 0;
@@ -126,16 +184,18 @@ __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect&
     G.bdx = 0.0f;
     G.bdy = 0.0f;
     for (int s = pr.s0; s < pr.s1; ++s) {
-        const float4 bb = seg_bbox[s];
-        const bool near = rect_box_d2(R.x0, R.y0, R.x1, R.y1, bb.x, bb.y, bb.z, bb.w) <= D2;
-        const bool band = (MODE == 0) && !(bb.y > R.y1 || bb.w < R.y0);
-        const EdgeRec* ep = edges + (size_t)s * eps;
-        const int ebase = s * eps;
-        if (near) {
-            if (band) scan_edges<true, true, BEST, EPS>(ep, eps, ebase, px, py, G);
-            else scan_edges<true, false, BEST, EPS>(ep, eps, ebase, px, py, G);
-        } else if (band) {
-            scan_edges<false, true, false, EPS>(ep, eps, ebase, px, py, G);
+        const SegRec sg = segs[s];
+        const bool near = near_wave(sg.near_x, sg.near_y, W);
+        const bool band = MODE == 0 && rows_hit(sg.cross_y, W);
+        if (!(near || band)) continue;
+        cptr<EdgeRec> ep = edges + (size_t)s * eps;
+        if constexpr (BEST) {
+            scan_culled<MODE == 0, EPS>(ep, eps, s * eps, near, band, W, px, py, G);
+        } else if (near) {
+            if (band) scan_all<true, true, EPS>(ep, eps, px, py, G);
+            else scan_all<true, false, EPS>(ep, eps, px, py, G);
+        } else {
+            scan_all<false, true, EPS>(ep, eps, px, py, G);
         }
     }
 }
@@ -177,23 +237,25 @@ __device__ __forceinline__ Cov coverage(const PrimRec& pr, const Geom& G, float 
 
 template <int MODE, int EPS>
 __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
-    const int32_t* __restrict__ prim_ids, const int32_t* __restrict__ bins,
-    const EdgeRec* __restrict__ edges, const float4* __restrict__ seg_bbox,
-    const PrimRec* __restrict__ prims, const float* __restrict__ bg, int img_h, int img_w,
+    const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
+    const EdgeRec* __restrict__ edges_g, const SegRec* __restrict__ segs_g,
+    const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, int eps, float* __restrict__ out, float* __restrict__ final_T,
     int32_t* __restrict__ final_idx) {
     const int tile = xcd_tile(blockIdx.x, ntiles);
     const int tty = tile / tbx, ttx = tile - tty * tbx;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int i = tty * kTile + wv * 4 + (lane >> 4);
     const int j = ttx * kTile + (lane & 15);
     const bool in_img = (i < img_h) & (j < img_w);
     const float px = (float)j + 0.5f, py = (float)i + 0.5f;
-    WaveRect R;
-    R.x0 = (float)(ttx * kTile) + 0.5f;
-    R.x1 = R.x0 + 15.0f;
-    R.y0 = (float)(tty * kTile + wv * 4) + 0.5f;
-    R.y1 = R.y0 + 3.0f;
+    const WaveRect W{ttx * kTile, ttx * kTile + kTile - 1, tty * kTile + wv * 4,
+                     tty * kTile + wv * 4 + 3};
+    const cptr<int32_t> prim_ids = as_const(prim_ids_g);
+    const cptr<PrimRec> prims = as_const(prims_g);
+    const cptr<SegRec> segs = as_const(segs_g);
+    const cptr<EdgeRec> edges = as_const(edges_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
     float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
     int cur = 0;
@@ -205,9 +267,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
         pid_next = prim_ids[min(g + 1, g1 - 1)];
         const PrimRec pr = prims[pid];
         const float D2 = pr.cull_d * pr.cull_d;
-        if (prim_culled<MODE>(pr, R, D2)) continue;
+        if (prim_culled<MODE>(pr, W)) continue;
         Geom G;
-        prim_geometry<MODE, false, EPS>(pr, R, D2, seg_bbox, edges, eps, px, py, G);
+        prim_geometry<MODE, false, EPS>(pr, W, segs, edges, eps, px, py, G);
         if (!done) {
             const Cov c = coverage<MODE>(pr, G, D2);
             const float alpha = fminf(kAlphaCap, pr.opacity * c.cov);
@@ -255,9 +317,9 @@ __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
 //     segment) and one lane adds the 8 values to v_cubics_px.
 template <int MODE, int EPS>
 __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
-    const int32_t* __restrict__ prim_ids, const int32_t* __restrict__ bins,
-    const EdgeRec* __restrict__ edges, const float4* __restrict__ seg_bbox,
-    const PrimRec* __restrict__ prims, const float* __restrict__ bg, int img_h, int img_w,
+    const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
+    const EdgeRec* __restrict__ edges_g, const SegRec* __restrict__ segs_g,
+    const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, int eps, const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
@@ -265,16 +327,18 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     float* __restrict__ isect_contrib) {
     const int tile = xcd_tile(blockIdx.x, ntiles);
     const int tty = tile / tbx, ttx = tile - tty * tbx;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int i = tty * kTile + wv * 4 + (lane >> 4);
     const int j = ttx * kTile + (lane & 15);
     const bool in_img = (i < img_h) & (j < img_w);
     const float px = (float)j + 0.5f, py = (float)i + 0.5f;
-    WaveRect R;
-    R.x0 = (float)(ttx * kTile) + 0.5f;
-    R.x1 = R.x0 + 15.0f;
-    R.y0 = (float)(tty * kTile + wv * 4) + 0.5f;
-    R.y1 = R.y0 + 3.0f;
+    const WaveRect W{ttx * kTile, ttx * kTile + kTile - 1, tty * kTile + wv * 4,
+                     tty * kTile + wv * 4 + 3};
+    const cptr<int32_t> prim_ids = as_const(prim_ids_g);
+    const cptr<PrimRec> prims = as_const(prims_g);
+    const cptr<SegRec> segs = as_const(segs_g);
+    const cptr<EdgeRec> edges = as_const(edges_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
     const size_t pix = in_img ? (size_t)i * img_w + j : 0;
     float T = in_img ? final_T[pix] : 1.0f;
@@ -287,7 +351,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     const bool want_contrib = (contrib_rgb != nullptr) | (isect_contrib != nullptr);
     const float inv_e = 1.0f / (float)eps;
     float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
-    const int gstart = min(g1 - 1, wave_max_i(fidx));
+    // The wave maximum is uniform; readfirstlane tells the compiler so, which
+    // keeps every load that depends on the entry index scalar.
+    const int gstart = min(g1 - 1, __builtin_amdgcn_readfirstlane(wave_max_i(fidx)));
     int pid_next = gstart >= g0 ? prim_ids[gstart] : 0;
     for (int g = gstart; g >= g0; --g) {
         const bool valid = in_img & (g <= fidx);
@@ -296,9 +362,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
         if (__ballot(valid) == 0) continue;
         const PrimRec pr = prims[pid];
         const float D2 = pr.cull_d * pr.cull_d;
-        if (prim_culled<MODE>(pr, R, D2)) continue;
+        if (prim_culled<MODE>(pr, W)) continue;
         Geom G;
-        prim_geometry<MODE, true, EPS>(pr, R, D2, seg_bbox, edges, eps, px, py, G);
+        prim_geometry<MODE, true, EPS>(pr, W, segs, edges, eps, px, py, G);
         float vr = 0.0f, vg = 0.0f, vb = 0.0f, vop = 0.0f, vis2 = 0.0f, vsw = 0.0f;
         float cr = 0.0f, cg = 0.0f, cb = 0.0f;
         float gx = 0.0f, gy = 0.0f;
@@ -481,7 +547,7 @@ struct RasterArgs {
     const int32_t* ids;
     const int32_t* bins;
     const EdgeRec* E;
-    const float4* B;
+    const SegRec* B;
     const PrimRec* P;
     const float* bg;
     // forward outputs
@@ -530,7 +596,7 @@ static void dispatch(const RasterArgs& a) {
 }
 
 static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* bins,
-                              const void* edges, const float* seg_bbox, const void* prims,
+                              const void* edges, const void* seg_recs, const void* prims,
                               const float* bg, int32_t img_h, int32_t img_w, int32_t eps,
                               hipStream_t stream) {
     RasterArgs a{};
@@ -543,7 +609,7 @@ static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* b
     a.ids = ids;
     a.bins = bins;
     a.E = reinterpret_cast<const EdgeRec*>(edges);
-    a.B = reinterpret_cast<const float4*>(seg_bbox);
+    a.B = reinterpret_cast<const SegRec*>(seg_recs);
     a.P = reinterpret_cast<const PrimRec*>(prims);
     a.bg = bg;
     a.stream = stream;
@@ -552,13 +618,13 @@ static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* b
 
 extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                                     const int32_t* tile_bins, const void* edges,
-                                    const float* seg_bbox, const void* prim_recs,
+                                    const void* seg_recs, const void* prim_recs,
                                     const float* background, int32_t img_h, int32_t img_w,
                                     int32_t edges_per_segment, float* out_img, float* final_Ts,
                                     int32_t* final_idx, hipStream_t stream) {
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1)
         return CS_ERR_ARGS;
-    RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, seg_bbox, prim_recs,
+    RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, seg_recs, prim_recs,
                                background, img_h, img_w, edges_per_segment, stream);
     a.out = out_img;
     a.final_T = final_Ts;
@@ -570,7 +636,7 @@ extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted
 
 extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                                      const int32_t* tile_bins, const void* edges,
-                                     const float* seg_bbox, const void* prim_recs,
+                                     const void* seg_recs, const void* prim_recs,
                                      const float* background, int32_t img_h, int32_t img_w,
                                      int32_t edges_per_segment, const float* final_Ts,
                                      const int32_t* final_idx, const float* v_output,
@@ -581,7 +647,7 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1)
         return CS_ERR_ARGS;
     if (mode == 1 && v_stroke_widths == nullptr) return CS_ERR_ARGS;
-    RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, seg_bbox, prim_recs,
+    RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, seg_recs, prim_recs,
                                background, img_h, img_w, edges_per_segment, stream);
     a.fT = final_Ts;
     a.fidx = final_idx;

@@ -88,8 +88,8 @@ class Binned:
     num_intersects: int
     cubics_px: torch.Tensor
     seg_tile_ranges: torch.Tensor
-    seg_bbox: torch.Tensor
-    edges: torch.Tensor            # [E, 8] float32 records (x0 y0 x1 y1 vx vy ux uy)
+    seg_recs: torch.Tensor         # [nseg, 4] int32 packed cull ranges
+    edges: torch.Tensor            # [E, 12] 48-byte records (x0 y0 x1 y1 vx vy ux uy + ranges)
     prim_tile_ranges: torch.Tensor
     num_tiles_hit: torch.Tensor
     inv_sigma2s: torch.Tensor
@@ -123,7 +123,7 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     f32, i32 = torch.float32, torch.int32
     cubics_px = torch.empty((nseg, 4, 2), dtype=f32, device=dev)
     seg_tile_ranges = torch.empty((nseg, 4), dtype=i32, device=dev)
-    seg_bbox = torch.empty((nseg, 4), dtype=f32, device=dev)
+    seg_recs = torch.empty((nseg, N.SEG_RECORD_INTS), dtype=i32, device=dev)
     edges = torch.empty((E, N.EDGE_RECORD_FLOATS), dtype=f32, device=dev)
     prim_tile_ranges = torch.empty((P, 4), dtype=i32, device=dev)
     num_tiles_hit = torch.empty((P,), dtype=i32, device=dev)
@@ -143,7 +143,7 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     N.call("cs_bin_prepare", N.ptr(cubics_norm), N.ptr(seg_offsets), N.ptr(colors),
            N.ptr(opacities), N.ptr(depths), N.ptr(fill_rules), N.ptr(widths),
            N.ptr(stroke_widths), nseg, P, img_h, img_w, block_x, block_y, S, float(aabb_pad),
-           int(bool(aniso)), mode, N.ptr(cubics_px), N.ptr(seg_tile_ranges), N.ptr(seg_bbox),
+           int(bool(aniso)), mode, N.ptr(cubics_px), N.ptr(seg_tile_ranges), N.ptr(seg_recs),
            N.ptr(edges), N.ptr(prim_tile_ranges), N.ptr(num_tiles_hit), N.ptr(inv_sigma2s),
            N.ptr(prim_recs), N.ptr(keys), N.ptr(order), N.ptr(keys_alt), N.ptr(vals_alt),
            N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(rank_offsets), N.ptr(status), st)
@@ -171,7 +171,7 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
            N.ptr(valt), N.ptr(rc_i), N.ptr(st_i), N.ptr(tile_bins), st)
     return Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P,
                   num_intersects=I, cubics_px=cubics_px, seg_tile_ranges=seg_tile_ranges,
-                  seg_bbox=seg_bbox, edges=edges, prim_tile_ranges=prim_tile_ranges,
+                  seg_recs=seg_recs, edges=edges, prim_tile_ranges=prim_tile_ranges,
                   num_tiles_hit=num_tiles_hit, inv_sigma2s=inv_sigma2s, prim_recs=prim_recs,
                   order=order, primitive_ids_sorted=prim_ids, tile_keys_sorted=tile_keys,
                   tile_bins=tile_bins)
@@ -183,7 +183,7 @@ def rasterize_forward(b: Binned, background: torch.Tensor):
     final_T = torch.empty((b.img_h, b.img_w), dtype=torch.float32, device=dev)
     final_idx = torch.empty((b.img_h, b.img_w), dtype=torch.int32, device=dev)
     N.call("cs_rasterize_forward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
-           N.ptr(b.edges), N.ptr(b.seg_bbox), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
+           N.ptr(b.edges), N.ptr(b.seg_recs), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
            b.img_w, b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx),
            N.stream(dev))
     return out, final_T, final_idx
@@ -205,7 +205,7 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_is2 = rest[4 * P: 5 * P]
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
     N.call("cs_rasterize_backward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
-           N.ptr(b.edges), N.ptr(b.seg_bbox), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
+           N.ptr(b.edges), N.ptr(b.seg_recs), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
            b.img_w, b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(v_output),
            N.ptr(v_px), N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw),
            N.ptr(curve_contrib_rgb), N.ptr(curve_isect_contrib), N.stream(dev))
