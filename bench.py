@@ -22,8 +22,15 @@ if ROOT not in sys.path:
 
 SSIM_WEIGHT = 0.2
 HBM_PEAK_GBS = 8000.0
-# MI355X published vector fp32 peak (packed FMA); non-packed VALU issue is half.
-VALU_PEAK_TFLOPS = 157.3
+# MI355X published fp32 compute peak (TFLOP/s); the vector ALUs reach it with
+# packed FMAs, plain fp32 vector issue reaches half of it.
+FP32_PEAK_TFLOPS = 157.3
+# fp32 operations of one (pixel, edge) evaluation of the reference's edge
+# loop: distance 15 (2 sub, mul + fma, 2 clamp, 2 fma, mul + fma, min; fma =
+# 2), crossing 6 (2 compares, mul + fma, compare).  Strokes have no crossing.
+FLOPS_PER_EVAL = {0: 21.0, 1: 15.0}
+RASTER_LABELS = {"cubic.fwd.rast": "raster_fwd", "cubic.bwd.rast": "raster_bwd"}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_{kernel}_cfg{cfg}.json")
 
 
 def parse():
@@ -34,6 +41,9 @@ def parse():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--stage-iters", type=int, default=20)
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="after the run, copy a buffer of this size three times (the "
+                         "reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -125,14 +135,17 @@ def stage_times(sc, cub, col, iters):
 
 
 def reference_edge_pixel_evals(b, T, idx):
-    """Edge-pixel evaluations the reference's forward performs: every pixel
-    evaluates all edges of each entry of its tile list up to and including the
-    entry where it stops (T <= 1e-4), or the whole list."""
+    """(forward, backward) edge-pixel evaluations of the reference's kernels.
+    Forward: every pixel evaluates all edges of each entry of its tile list up
+    to and including the entry where it stops (T <= 1e-4), or the whole list.
+    Backward: every entry with global index <= final_idx (the last entry that
+    contributed)."""
     import torch
     H, W = b.img_h, b.img_w
     tbx = (W + 15) // 16
     eps = b.edges_per_segment
-    prim_edges = (b.prim_recs.view(torch.int32)[:, 9] - b.prim_recs.view(torch.int32)[:, 8]) * eps
+    pr = b.prim_recs.view(torch.int32)
+    prim_edges = (pr[:, 9] - pr[:, 8]) * eps
     ent = prim_edges[b.primitive_ids_sorted.long()].to(torch.int64)
     csum = torch.zeros(ent.numel() + 1, dtype=torch.int64, device=ent.device)
     csum[1:] = torch.cumsum(ent, 0)
@@ -141,8 +154,12 @@ def reference_edge_pixel_evals(b, T, idx):
     tile = (ii // 16) * tbx + (jj // 16)
     g0 = b.tile_bins[tile.reshape(-1), 0].long()
     g1 = b.tile_bins[tile.reshape(-1), 1].long()
-    stop = torch.where(T.reshape(-1) <= 1e-4, idx.reshape(-1).long() + 1, g1)
-    return int((csum[stop] - csum[g0]).sum())
+    last = idx.reshape(-1).long()
+    stop_f = torch.where(T.reshape(-1) <= 1e-4, last + 1, g1)
+    stop_b = torch.maximum(torch.minimum(last + 1, g1), g0)
+    fwd = int((csum[stop_f] - csum[g0]).sum())
+    bwd = int((csum[stop_b] - csum[g0]).sum())
+    return fwd, bwd
 
 
 def cpu_baseline(cfg):
@@ -195,6 +212,26 @@ def cpu_baseline(cfg):
                        f"{step_s:.1f}s per step")}
 
 
+def load_traffic(kernel, cfg):
+    """HBM bytes per launch of `kernel` measured with rocprofv3 FETCH_SIZE and
+    WRITE_SIZE (the committed summary for this config), or None."""
+    path = TRAFFIC_FILE.format(kernel=kernel, cfg=cfg)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def copy_calibration(mib):
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.rand(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -202,41 +239,52 @@ def main():
                                    "design is described in DESIGN.md", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
+    from repo_amd import _native, profiling
     torch.backends.cudnn.benchmark = False
     sc, cub, col, opt = make_problem(args.config)
     for _ in range(args.warmup):
         train_step(sc, cub, col, opt)
+    # The raster launches of the timed steps are bracketed by HIP events on
+    # the stream they run on (torch's current stream).
+    timer = profiling.EventTimer(RASTER_LABELS)
+    _native.set_profile_ctx_factory(timer)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         loss = train_step(sc, cub, col, opt)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    _native.set_profile_ctx_factory(None)
     ms = 1000.0 * elapsed / max(1, args.steps)
+    launch_ms = {RASTER_LABELS[k]: timer.mean_ms(k) for k in RASTER_LABELS}
     st = stage_times(sc, cub, col, args.stage_iters)
     b, T, idx = st.pop("_binned"), st.pop("_T"), st.pop("_idx")
-    evals = reference_edge_pixel_evals(b, T, idx)
+    evals_fwd, evals_bwd = reference_edge_pixel_evals(b, T, idx)
     n_img = 3 * sc.img_h * sc.img_w
     kern = {k: round(v, 4) for k, v in st.items() if k.endswith("_ms")}
     gbs = lambda nbytes, ms_: nbytes / (ms_ * 1e-3) / 1e9  # noqa: E731
     kern["mse_fwd_GBs"] = round(gbs(8 * n_img, st["mse_fwd_ms"]), 1)
     kern["mse_bwd_GBs"] = round(gbs(12 * n_img, st["mse_bwd_ms"]), 1)
     kern["ssim_fwd_GBs"] = round(gbs(8 * n_img, st["ssim_fwd_ms"]), 1)
-    kern["reference_edge_pixel_evals_fwd"] = evals
-    # Dominant kernel: the backward raster (VALU-bound).  Algorithmic work =
-    # the reference's edge-pixel evaluations x 20 fp32 flops (distance 12,
-    # crossing 8), the same evaluations replayed in reverse.
-    flops = evals * 20.0
-    bwd_ms = st["raster_bwd_ms"]
-    fwd_ms = st["raster_fwd_ms"]
-    dom_ms, dom = (bwd_ms, "raster_bwd") if bwd_ms >= fwd_ms else (fwd_ms, "raster_fwd")
+    kern["reference_edge_pixel_evals"] = {"raster_fwd": evals_fwd, "raster_bwd": evals_bwd}
+    kern["timed_region_launch_ms"] = {k: round(v, 4) for k, v in launch_ms.items()}
+    # Dominant kernel (the longer raster launch in the timed steps).
+    # Algorithmic work = the reference's edge-pixel evaluations for that
+    # launch x fp32 operations per evaluation.
+    dom = max(launch_ms, key=lambda k: launch_ms[k])
+    dom_ms = launch_ms[dom]
+    units = evals_bwd if dom == "raster_bwd" else evals_fwd
+    flops = units * FLOPS_PER_EVAL[b.mode]
     achieved = flops / (dom_ms * 1e-3) / 1e12
-    roofline = {"kernel": dom, "bound": "valu", "achieved": round(achieved, 2),
-                "peak": VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / VALU_PEAK_TFLOPS, 4), "traffic": None,
-                "note": "algorithmic = reference edge-pixel evaluations x 20 flops; the "
-                        "kernel culls provably non-contributing evaluations, so effective "
-                        "throughput can exceed the executed rate"}
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
+                "traffic": load_traffic(dom, args.config), "kernel": dom,
+                "launch_ms": round(dom_ms, 4), "units_per_launch": units,
+                "flops_per_unit": FLOPS_PER_EVAL[b.mode],
+                "note": "compute-bound on the fp32 vector ALUs (no matrix instructions on this "
+                        "path), priced against the published fp32 compute peak; units are the "
+                        "reference kernel's edge-pixel evaluations, some of which this kernel "
+                        "proves non-contributing and skips"}
     line = {
         "metric": "train it/s, 4096 closed cubics @2040x1356 fp32",
         "value": round(1000.0 / ms, 3), "unit": "it/s", "n_gpus": 1, "steps": args.steps,
@@ -247,11 +295,12 @@ def main():
                       "MSE+0.2*(1-SSIM 11x11 s=1.5), Adam on control points+colors"
                       if args.config == 3 else "see repo_amd/synth.py"),
                    "num_intersects": st["num_intersects"], "final_loss": float(loss)},
-        "fwd_ms": round(st["binning_ms"] + fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
         "kernels": kern, "roofline": roofline,
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.config)
+    if args.copy_calibration_mib > 0:
+        copy_calibration(args.copy_calibration_mib)
     print(json.dumps(line), flush=True)
 
 

@@ -8,6 +8,8 @@ from __future__ import annotations
 
 import ctypes
 import os
+from contextlib import nullcontext
+from typing import Callable, ContextManager, Optional
 
 import torch
 
@@ -99,6 +101,27 @@ def check(rc: int, what: str) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args), name)
+
+
+ProfileCtxFactory = Callable[[str], ContextManager]
+_PROFILE_CTX_FACTORY: Optional[ProfileCtxFactory] = None
+
+
+def set_profile_ctx_factory(factory: Optional[ProfileCtxFactory]) -> None:
+    """Installs a factory of context managers that wrap each library launch,
+    keyed by a stage label such as "cubic.bwd.rast" (the same protocol as the
+    reference's set_gs_profile_ctx_factory, tilelang_renderer.py:31-39).  The
+    context is entered right before the C-ABI call and left right after it,
+    so HIP events recorded on the current stream inside it bracket exactly
+    that call's kernels."""
+    global _PROFILE_CTX_FACTORY
+    _PROFILE_CTX_FACTORY = factory
+
+
+def prof(label: str):
+    if _PROFILE_CTX_FACTORY is None:
+        return nullcontext()
+    return _PROFILE_CTX_FACTORY(label)
 
 
 def require_gpu(t: torch.Tensor, name: str) -> None:

@@ -60,8 +60,9 @@ def mse_forward(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
     partials = torch.empty((int(N.lib().cs_mse_partials_elems(n)),), dtype=torch.float32,
                            device=dev)
     loss = torch.empty((), dtype=torch.float32, device=dev)
-    N.call("cs_mse_forward", N.ptr(x), N.ptr(y), n, N.ptr(partials), N.ptr(loss),
-           N.stream(dev))
+    with N.prof("loss.mse_fwd"):
+        N.call("cs_mse_forward", N.ptr(x), N.ptr(y), n, N.ptr(partials), N.ptr(loss),
+               N.stream(dev))
     return loss
 
 
@@ -88,8 +89,9 @@ class _TileLangMSEFn(torch.autograd.Function):
         g = grad_output.detach().to(torch.float32).contiguous()
         gx = torch.empty_like(x) if need_x else None
         gy = torch.empty_like(y) if need_y else None
-        N.call("cs_mse_backward", N.ptr(x), N.ptr(y), x.numel(), N.ptr(g), N.ptr(gx), N.ptr(gy),
-               N.stream(x.device))
+        with N.prof("loss.mse_bwd"):
+            N.call("cs_mse_backward", N.ptr(x), N.ptr(y), x.numel(), N.ptr(g), N.ptr(gx), N.ptr(gy),
+                   N.stream(x.device))
         if gx is not None:
             gx = gx.view(ctx.shape).to(ctx.x_dtype)
         if gy is not None:
@@ -128,9 +130,10 @@ def _ssim_forward(x32, y32, win_size, win_sigma, c1, c2, want_grad):
     oh, ow = h - win_size + 1, w - win_size + 1
     abc = (torch.empty((3, n * c, oh, ow), dtype=torch.float32, device=dev)
            if want_grad else None)
-    N.call("cs_ssim", N.ptr(x32), N.ptr(y32), n * c, h, w, N.ptr(g), int(win_size),
-           float(c1), float(c2), N.ptr(partials), N.ptr(out), N.ptr(abc),
-           N.stream(dev))
+    with N.prof("loss.ssim_fwd"):
+        N.call("cs_ssim", N.ptr(x32), N.ptr(y32), n * c, h, w, N.ptr(g), int(win_size),
+               float(c1), float(c2), N.ptr(partials), N.ptr(out), N.ptr(abc),
+               N.stream(dev))
     return out, abc, g
 
 
@@ -156,8 +159,9 @@ class _SSIMFn(torch.autograd.Function):
         n, c, h, w = x.shape
         gx = torch.empty_like(x)
         go = grad_output.detach().to(torch.float32).contiguous()
-        N.call("cs_ssim_backward", N.ptr(x), N.ptr(y), n * c, h, w, N.ptr(g), ctx.win_size,
-               N.ptr(abc), N.ptr(go), N.ptr(gx), N.stream(x.device))
+        with N.prof("loss.ssim_bwd"):
+            N.call("cs_ssim_backward", N.ptr(x), N.ptr(y), n * c, h, w, N.ptr(g), ctx.win_size,
+                   N.ptr(abc), N.ptr(go), N.ptr(gx), N.stream(x.device))
         return gx.to(ctx.x_dtype), None, None, None, None, None
 
 

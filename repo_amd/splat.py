@@ -140,13 +140,14 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     rank_offsets = torch.empty((P,), dtype=i32, device=dev)
     status = torch.empty((4,), dtype=i32, device=dev)
     st = N.stream(dev)
-    N.call("cs_bin_prepare", N.ptr(cubics_norm), N.ptr(seg_offsets), N.ptr(colors),
-           N.ptr(opacities), N.ptr(depths), N.ptr(fill_rules), N.ptr(widths),
-           N.ptr(stroke_widths), nseg, P, img_h, img_w, block_x, block_y, S, float(aabb_pad),
-           int(bool(aniso)), mode, N.ptr(cubics_px), N.ptr(seg_tile_ranges), N.ptr(seg_recs),
-           N.ptr(edges), N.ptr(prim_tile_ranges), N.ptr(num_tiles_hit), N.ptr(inv_sigma2s),
-           N.ptr(prim_recs), N.ptr(keys), N.ptr(order), N.ptr(keys_alt), N.ptr(vals_alt),
-           N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(rank_offsets), N.ptr(status), st)
+    with N.prof("cubic.fwd.bin_prepare"):
+        N.call("cs_bin_prepare", N.ptr(cubics_norm), N.ptr(seg_offsets), N.ptr(colors),
+               N.ptr(opacities), N.ptr(depths), N.ptr(fill_rules), N.ptr(widths),
+               N.ptr(stroke_widths), nseg, P, img_h, img_w, block_x, block_y, S, float(aabb_pad),
+               int(bool(aniso)), mode, N.ptr(cubics_px), N.ptr(seg_tile_ranges), N.ptr(seg_recs),
+               N.ptr(edges), N.ptr(prim_tile_ranges), N.ptr(num_tiles_hit), N.ptr(inv_sigma2s),
+               N.ptr(prim_recs), N.ptr(keys), N.ptr(order), N.ptr(keys_alt), N.ptr(vals_alt),
+               N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(rank_offsets), N.ptr(status), st)
     I, bad, first, last = status.tolist()
     if bad or first != 0 or last != nseg:
         raise ValueError(
@@ -166,9 +167,10 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
         st_i = torch.empty((int(lib.cs_scan_temp_elems(counts_i)),), dtype=i32, device=dev)
     else:
         kalt = valt = rc_i = st_i = None
-    N.call("cs_bin_finish", N.ptr(order), N.ptr(prim_tile_ranges), N.ptr(rank_offsets), P, I,
-           img_h, img_w, block_x, block_y, N.ptr(tile_keys), N.ptr(prim_ids), N.ptr(kalt),
-           N.ptr(valt), N.ptr(rc_i), N.ptr(st_i), N.ptr(tile_bins), st)
+    with N.prof("cubic.fwd.bin_finish"):
+        N.call("cs_bin_finish", N.ptr(order), N.ptr(prim_tile_ranges), N.ptr(rank_offsets), P, I,
+               img_h, img_w, block_x, block_y, N.ptr(tile_keys), N.ptr(prim_ids), N.ptr(kalt),
+               N.ptr(valt), N.ptr(rc_i), N.ptr(st_i), N.ptr(tile_bins), st)
     return Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P,
                   num_intersects=I, cubics_px=cubics_px, seg_tile_ranges=seg_tile_ranges,
                   seg_recs=seg_recs, edges=edges, prim_tile_ranges=prim_tile_ranges,
@@ -182,10 +184,11 @@ def rasterize_forward(b: Binned, background: torch.Tensor):
     out = torch.empty((b.img_h, b.img_w, 3), dtype=torch.float32, device=dev)
     final_T = torch.empty((b.img_h, b.img_w), dtype=torch.float32, device=dev)
     final_idx = torch.empty((b.img_h, b.img_w), dtype=torch.int32, device=dev)
-    N.call("cs_rasterize_forward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
-           N.ptr(b.edges), N.ptr(b.seg_recs), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
-           b.img_w, b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx),
-           N.stream(dev))
+    with N.prof("cubic.fwd.rast"):
+        N.call("cs_rasterize_forward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
+               N.ptr(b.edges), N.ptr(b.seg_recs), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
+               b.img_w, b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx),
+               N.stream(dev))
     return out, final_T, final_idx
 
 
@@ -204,11 +207,12 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_opac = rest[3 * P: 4 * P]
     v_is2 = rest[4 * P: 5 * P]
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
-    N.call("cs_rasterize_backward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
-           N.ptr(b.edges), N.ptr(b.seg_recs), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
-           b.img_w, b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(v_output),
-           N.ptr(v_px), N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw),
-           N.ptr(curve_contrib_rgb), N.ptr(curve_isect_contrib), N.stream(dev))
+    with N.prof("cubic.bwd.rast"):
+        N.call("cs_rasterize_backward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
+               N.ptr(b.edges), N.ptr(b.seg_recs), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
+               b.img_w, b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(v_output),
+               N.ptr(v_px), N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw),
+               N.ptr(curve_contrib_rgb), N.ptr(curve_isect_contrib), N.stream(dev))
     return v_px, v_colors, v_opac, v_is2, v_sw
 
 
@@ -228,8 +232,9 @@ def backward_finalize(b: Binned, v_cubics_px, widths, v_inv_sigma2s):
     dev = v_cubics_px.device
     v_norm = torch.empty_like(v_cubics_px)
     v_aa = torch.empty_like(v_inv_sigma2s)
-    N.call("cs_backward_finalize", N.ptr(v_cubics_px), b.nseg, b.img_h, b.img_w, N.ptr(widths),
-           N.ptr(v_inv_sigma2s), int(widths.numel()), N.ptr(v_norm), N.ptr(v_aa), N.stream(dev))
+    with N.prof("cubic.bwd.finalize"):
+        N.call("cs_backward_finalize", N.ptr(v_cubics_px), b.nseg, b.img_h, b.img_w, N.ptr(widths),
+               N.ptr(v_inv_sigma2s), int(widths.numel()), N.ptr(v_norm), N.ptr(v_aa), N.stream(dev))
     return v_norm, v_aa
 
 
