@@ -265,6 +265,8 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
     if num_primitives <= 0:
         ctx.empty = True
         return bg.view(1, 1, 3).expand(int(img_h), int(img_w), 3).clone()
+    _check_block(block_x, block_y)
+    _check_flatten(flatten_method_norm)
     N.require_gpu(cubics_norm, "cubics_norm")
     for name, t, k in (("colors", colors, None), ("opacities", opacities, 1),
                        ("depths", depths, 1), ("fill_rules", fill_rules, 1),
@@ -283,8 +285,6 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
             f"aa_widths size must match primitive count ({num_primitives}), "
             f"got {int(widths.numel())}")
     widths = torch.clamp(widths, min=1e-4)
-    _check_block(block_x, block_y)
-    _check_flatten(flatten_method_norm)
 
     colors_c = _f32(colors)
     opac_c = _f32(opacities).view(-1)

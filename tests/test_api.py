@@ -1,0 +1,207 @@
+"""CPU checks of the drop-in boundary: the C ABI (library loads, exports every
+symbol include/cubicsplat_hip.h declares with the declared arity), the Python
+names and signatures of the reference's manbo API, and the argument errors
+raised before any device work."""
+from __future__ import annotations
+
+import inspect
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cubicsplat_hip.h")
+
+
+def header_functions():
+    """name -> parameter count of every function the header declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(cs_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = len(params)
+    return out
+
+
+def test_header_matches_bindings():
+    from repo_amd import _native as N
+    decl = header_functions()
+    assert len(decl) >= 20
+    assert set(decl) == set(N._SIGNATURES)
+    for name, (_, args) in N._SIGNATURES.items():
+        assert len(args) == decl[name], name
+
+
+def test_library_loads_and_exports_every_symbol():
+    from repo_amd import _native as N
+    if not os.path.exists(N.LIB_PATH):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = N.lib()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    # Host-only size queries (no device work).
+    assert lib.cs_scan_temp_elems(0) >= 0
+    assert lib.cs_radix_counts_elems(1 << 20) > 0
+    assert lib.cs_mse_partials_elems(1 << 20) > 0
+
+
+def test_record_sizes_match_header():
+    from repo_amd import _native as N
+    text = open(HEADER).read()
+    sizes = dict(re.findall(r"#define (CS_\w+_RECORD_BYTES) (\d+)", text))
+    assert int(sizes["CS_EDGE_RECORD_BYTES"]) == 4 * N.EDGE_RECORD_FLOATS
+    assert int(sizes["CS_SEG_RECORD_BYTES"]) == 4 * N.SEG_RECORD_INTS
+    assert int(sizes["CS_PRIM_RECORD_BYTES"]) == 4 * N.PRIM_RECORD_FLOATS
+
+
+# Parameter lists of the reference's public functions
+# (ops/cubic_splatting.py:3128-3150, ops/cubic_polyline_splatting.py:1341-1363,
+# metric.py:64-99, 198-229, tilelang_renderer.py:493-523).
+REFERENCE_SIGNATURES = {
+    "render_cubic_fill_splat_tilelang": [
+        "cubics_norm", "primitive_seg_offsets", "colors", "opacities", "depths", "img_h",
+        "img_w", "block_x", "block_y", "background", "*fill_rules", "*project_threads",
+        "*map_threads", "*aabb_pad", "*aniso_intersects", "*aa_widths", "*aa_width",
+        "*distance_samples", "*flatten_method", "*process_fn"],
+    "render_cubic_polyline_splat_tilelang": [
+        "cubics_norm", "primitive_seg_offsets", "colors", "opacities", "stroke_widths", "depths",
+        "img_h", "img_w", "block_x", "block_y", "background", "*project_threads",
+        "*map_threads", "*aabb_pad", "*aniso_intersects", "*aa_widths", "*aa_width",
+        "*distance_samples", "*flatten_method", "*process_fn"],
+    "mse_loss_tilelang": ["x", "y", "*threads", "*items_per_thread", "*tilelang_backward"],
+    "ssim": ["x", "y", "*data_range", "*size_average", "*win_size", "*win_sigma", "*k1", "*k2",
+             "*nonnegative_ssim", "*block_h", "*block_w", "*threads"],
+    "psnr": ["x", "y", "*data_range", "*eps", "*threads", "*items_per_thread"],
+    "gs_render": ["means2d", "scales2d", "rotation", "colors", "opacities", "img_h", "img_w",
+                  "block_x", "block_y", "bg", "process_fn", "*profile_fwd_prefix",
+                  "*profile_bwd_prefix"],
+}
+
+
+def _params(fn):
+    out = []
+    for p in inspect.signature(fn).parameters.values():
+        out.append(("*" if p.kind == p.KEYWORD_ONLY else "") + p.name)
+    return out
+
+
+@pytest.mark.parametrize("name", list(REFERENCE_SIGNATURES))
+def test_public_signatures(name):
+    import manbo
+    fn = getattr(manbo.ops, name, None) or getattr(manbo, name)
+    assert _params(fn) == REFERENCE_SIGNATURES[name]
+
+
+def test_defaults_follow_reference():
+    import manbo
+    sig = inspect.signature(manbo.ops.render_cubic_fill_splat_tilelang).parameters
+    assert sig["aabb_pad"].default == 1.0
+    assert sig["aa_width"].default == 1.0
+    assert sig["distance_samples"].default == 24
+    assert sig["flatten_method"].default == "bernstein"
+    s = inspect.signature(manbo.ssim).parameters
+    assert (s["win_size"].default, s["win_sigma"].default) == (11, 1.5)
+    assert (s["k1"].default, s["k2"].default) == (0.01, 0.03)
+
+
+def test_autograd_function_forward_signatures():
+    from manbo.ops.cubic_polyline_splatting import _CubicPolylineSplatFunction
+    from manbo.ops.cubic_splatting import _CubicFillSplatFunction
+    fill = _params(_CubicFillSplatFunction.forward)
+    assert fill[:7] == ["ctx", "cubics_norm", "primitive_seg_offsets", "colors", "opacities",
+                        "depths", "fill_rules"]
+    assert len(fill) == 20 and fill[-1] == "process_fn"
+    poly = _params(_CubicPolylineSplatFunction.forward)
+    assert poly[4:7] == ["opacities", "stroke_widths", "depths"]
+    assert len(poly) == 20 and poly[-1] == "process_fn"
+
+
+def _scene_args(P=3, nseg=2):
+    cub = torch.zeros((P * nseg, 4, 2))
+    offs = torch.arange(0, P * nseg + 1, nseg, dtype=torch.int32)
+    return cub, offs, torch.rand(P, 3), torch.rand(P), torch.rand(P)
+
+
+def test_size_errors_are_value_errors():
+    import manbo
+    cub, offs, col, op, dep = _scene_args()
+    bg = torch.ones(3)
+    with pytest.raises(ValueError, match="colors"):
+        manbo.ops.render_cubic_fill_splat_tilelang(cub, offs, col[:2], op, dep, 32, 32, 16, 16,
+                                                   bg)
+    with pytest.raises(ValueError, match="depths"):
+        manbo.ops.render_cubic_fill_splat_tilelang(cub, offs, col, op, dep[:1], 32, 32, 16, 16,
+                                                   bg)
+    with pytest.raises(ValueError, match="aa_widths"):
+        manbo.ops.render_cubic_fill_splat_tilelang(cub, offs, col, op, dep, 32, 32, 16, 16, bg,
+                                                   aa_widths=torch.ones(2))
+    with pytest.raises(ValueError, match="stroke_widths"):
+        manbo.ops.render_cubic_polyline_splat_tilelang(cub, offs, col, op, torch.ones(2), dep,
+                                                       32, 32, 16, 16, bg)
+
+
+def test_host_tensors_are_rejected():
+    """No CPU fallback: host tensors fail loudly before any work."""
+    import manbo
+    cub, offs, col, op, dep = _scene_args()
+    with pytest.raises(ValueError, match="CUDA"):
+        manbo.ops.render_cubic_fill_splat_tilelang(cub, offs, col, op, dep, 32, 32, 16, 16,
+                                                   torch.ones(3))
+    x = torch.rand(1, 3, 16, 16)
+    with pytest.raises(ValueError, match="CUDA"):
+        manbo.mse_loss_tilelang(x, x)
+    with pytest.raises(ValueError, match="CUDA"):
+        manbo.ssim(x, x)
+
+
+def test_metric_argument_errors():
+    import manbo
+    x = torch.rand(1, 3, 16, 16)
+    with pytest.raises(ValueError):
+        manbo.ssim(x, torch.rand(1, 3, 16, 15))
+    with pytest.raises(ValueError):
+        manbo.ssim(x, x, win_size=4)
+    with pytest.raises(ValueError):
+        manbo.psnr(x, x, data_range=0.0)
+
+
+def test_empty_scene_returns_background():
+    import manbo
+    img = manbo.ops.render_cubic_fill_splat_tilelang(
+        torch.zeros((0, 4, 2)), torch.zeros(1, dtype=torch.int32), torch.zeros(0, 3),
+        torch.zeros(0), torch.zeros(0), 20, 24, 16, 16, torch.tensor([0.2, 0.3, 0.4]))
+    assert img.shape == (20, 24, 3)
+    assert torch.equal(img[7, 9], torch.tensor([0.2, 0.3, 0.4]))
+
+
+def test_flatten_method_and_tile_size_scope():
+    import manbo
+    from repo_amd import splat
+    assert splat.normalize_cubic_flatten_method("bernstein") == "bernstein"
+    with pytest.raises(ValueError):
+        splat.normalize_cubic_flatten_method("nope")
+    cub, offs, col, op, dep = _scene_args()
+    with pytest.raises(NotImplementedError):
+        manbo.ops.render_cubic_fill_splat_tilelang(cub, offs, col, op, dep, 32, 32, 8, 8,
+                                                   torch.ones(3))
+
+
+def test_gaussian_renderer_is_out_of_scope():
+    import manbo
+    seen = []
+    manbo.set_gs_profile_ctx_factory(lambda label: seen.append(label))
+    manbo.set_gs_profile_ctx_factory(None)
+    with pytest.raises(NotImplementedError):
+        manbo.gs_render(*([None] * 10))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stdout

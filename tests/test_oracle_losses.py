@@ -1,0 +1,99 @@
+"""Pins of the oracle's losses (oracle.mse, oracle.gaussian_window_1d,
+oracle.ssim_torch64) against closed forms, an independent brute-force loop
+and finite differences."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from oracle import oracle as O
+
+
+def test_gaussian_window():
+    g = O.gaussian_window_1d(11, 1.5).astype(np.float64)
+    assert abs(g.sum() - 1.0) < 1e-6
+    np.testing.assert_allclose(g, g[::-1], rtol=0, atol=0)
+    for k in range(11):
+        assert abs(g[k] / g[5] - math.exp(-((k - 5) ** 2) / (2 * 1.5 ** 2))) < 1e-6
+    assert int(np.argmax(g)) == 5
+
+
+def test_mse_closed_form():
+    x = np.full((1, 3, 8, 9), 0.75, np.float32)
+    y = np.full((1, 3, 8, 9), 0.25, np.float32)
+    assert O.mse(x, y) == 0.25
+    r = np.random.default_rng(0).standard_normal((2, 3, 5, 7))
+    assert abs(O.mse(r, 0 * r) - float(np.mean(r * r))) < 1e-15
+
+
+def test_ssim_identity_and_constants():
+    x = torch.rand((1, 3, 20, 23), dtype=torch.float64, generator=torch.Generator().manual_seed(1))
+    assert abs(float(O.ssim_torch64(x, x)) - 1.0) < 1e-12
+    a, b = 0.3, 0.8
+    xa = torch.full((1, 1, 16, 16), a, dtype=torch.float64)
+    yb = torch.full((1, 1, 16, 16), b, dtype=torch.float64)
+    c1, c2 = 0.01 ** 2, 0.03 ** 2
+    # The window is normalised in fp32 (metric.py:55-59), so its 2D sum s is
+    # 1 + O(1e-7): mu = a s, E[x^2] = a^2 s, sigma^2 = a^2 (s - s^2).
+    s = float(O.gaussian_window_1d(11, 1.5).astype(np.float64).sum()) ** 2
+    v = s - s * s
+    expect = (((2 * a * b * s * s + c1) / ((a * a + b * b) * s * s + c1))
+              * ((2 * a * b * v + c2) / ((a * a + b * b) * v + c2)))
+    assert abs(float(O.ssim_torch64(xa, yb)) - expect) < 1e-12
+    # With an exactly normalised window this is the textbook (2ab+c1)/(a^2+b^2+c1).
+    assert abs(expect - (2 * a * b + c1) / (a * a + b * b + c1)) < 1e-4
+
+
+def _ssim_loops(x, y, win=11, sigma=1.5):
+    """Scalar loops over the valid window positions (2D window = outer(g, g))."""
+    g = O.gaussian_window_1d(win, sigma).astype(np.float64)
+    h, w = x.shape
+    c1, c2 = 0.01 ** 2, 0.03 ** 2
+    vals = []
+    for i in range(h - win + 1):
+        for j in range(w - win + 1):
+            mx = my = exx = eyy = exy = 0.0
+            for a in range(win):
+                for b in range(win):
+                    k = g[a] * g[b]
+                    u, v = x[i + a, j + b], y[i + a, j + b]
+                    mx += k * u
+                    my += k * v
+                    exx += k * u * u
+                    eyy += k * v * v
+                    exy += k * u * v
+            sx, sy, sxy = exx - mx * mx, eyy - my * my, exy - mx * my
+            vals.append(((2 * mx * my + c1) / (mx * mx + my * my + c1))
+                        * ((2 * sxy + c2) / (sx + sy + c2)))
+    return float(np.mean(vals))
+
+
+def test_ssim_brute_force_and_channel_mean():
+    rng = np.random.default_rng(3)
+    x = rng.random((2, 14, 15))
+    y = np.clip(x + 0.2 * rng.standard_normal(x.shape), 0, 1)
+    per = [_ssim_loops(x[c], y[c]) for c in range(2)]
+    got = float(O.ssim_torch64(torch.from_numpy(x)[None], torch.from_numpy(y)[None]))
+    assert abs(got - np.mean(per)) < 1e-12
+    # Window offsets: a 7-tap window on a non-square image.
+    x7, y7 = x[0, :10, :12], y[0, :10, :12]
+    got7 = float(O.ssim_torch64(torch.from_numpy(x7)[None, None], torch.from_numpy(y7)[None, None],
+                                win_size=7))
+    assert abs(got7 - _ssim_loops(x7, y7, win=7)) < 1e-12
+
+
+def test_ssim_gradient_finite_differences():
+    rng = np.random.default_rng(4)
+    x = torch.from_numpy(rng.random((1, 1, 13, 14)))
+    y = torch.from_numpy(rng.random((1, 1, 13, 14)))
+    xr = x.clone().requires_grad_(True)
+    O.ssim_torch64(xr, y).backward()
+    h = 1e-6
+    for (i, j) in [(0, 0), (6, 7), (12, 13), (3, 10)]:
+        xp, xm = x.clone(), x.clone()
+        xp[0, 0, i, j] += h
+        xm[0, 0, i, j] -= h
+        fd = (float(O.ssim_torch64(xp, y)) - float(O.ssim_torch64(xm, y))) / (2 * h)
+        assert abs(fd - float(xr.grad[0, 0, i, j])) < 1e-7
