@@ -78,11 +78,16 @@ int cs_isect_edge_ranges(const int32_t* prim_ids_sorted, const int32_t* seg_offs
 
 /* ---------------- fused forward binning ---------------- */
 
-/* Size in bytes of one flattened edge record, one segment record and one
- * primitive record (opaque to callers; the raster entry points read them). */
-#define CS_EDGE_RECORD_BYTES 48
-#define CS_SEG_RECORD_BYTES 16
-#define CS_PRIM_RECORD_BYTES 64
+/* Size in bytes of one flattened edge record (geometry), one edge cull
+ * record, one segment record and one primitive record (opaque to callers;
+ * the raster entry points read them).  The cull records pack pixel indices as
+ * int16, so every entry point that takes them requires img_h, img_w <=
+ * CS_MAX_IMAGE_DIM. */
+#define CS_EDGE_RECORD_BYTES 32
+#define CS_EDGE_CULL_BYTES 16
+#define CS_SEG_RECORD_BYTES 32
+#define CS_PRIM_RECORD_BYTES 80
+#define CS_MAX_IMAGE_DIM 16384
 
 /* Stage 1 of _CubicFillSplatFunction.forward / _CubicPolylineSplatFunction.forward
  * (ops/cubic_splatting.py:2815-2880, ops/cubic_polyline_splatting.py:1027-1098):
@@ -98,7 +103,7 @@ int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const f
                    int32_t nprim, int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
                    int32_t samples, float aabb_pad, int32_t aniso, int32_t mode,
                    float* cubics_px, int32_t* seg_tile_ranges, void* seg_recs, void* edges,
-                   int32_t* prim_tile_ranges, uint32_t* num_tiles_hit, float* inv_sigma2s,
+                   void* edge_culls, int32_t* prim_tile_ranges, uint32_t* num_tiles_hit, float* inv_sigma2s,
                    void* prim_recs, uint32_t* keys, int32_t* order, uint32_t* keys_alt,
                    int32_t* vals_alt, uint32_t* radix_counts, uint32_t* scan_temp,
                    uint32_t* rank_offsets, int32_t* status, hipStream_t stream);
@@ -119,7 +124,7 @@ int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges,
  * mode 0, rasterize_cubic_polyline_forward_kernel
  * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  16x16 tiles only. */
 int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
-                         const void* edges, const void* seg_recs, const void* prim_recs,
+                         const void* edges, const void* edge_culls, const void* prim_recs,
                          const float* background, int32_t img_h, int32_t img_w,
                          int32_t edges_per_segment, float* out_img, float* final_Ts,
                          int32_t* final_idx, hipStream_t stream);
@@ -131,7 +136,7 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
  * v_colors [P,3], v_opacities [P], v_inv_sigma2s [P], v_stroke_widths [P]
  * (mode 1), and optionally curve_contrib_rgb [P,3] / curve_isect_contrib [I]. */
 int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
-                          const void* edges, const void* seg_recs, const void* prim_recs,
+                          const void* edges, const void* edge_culls, const void* prim_recs,
                           const float* background, int32_t img_h, int32_t img_w,
                           int32_t edges_per_segment, const float* final_Ts,
                           const int32_t* final_idx, const float* v_output, float* v_cubics_px,

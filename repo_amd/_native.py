@@ -17,9 +17,11 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libcubicsplat_hip.so")
 
 CS_OK, CS_ERR_ARGS, CS_ERR_HIP = 0, 1, 2
-EDGE_RECORD_FLOATS = 12  # 48-byte edge record
-SEG_RECORD_INTS = 4      # 16-byte segment record
-PRIM_RECORD_FLOATS = 16  # 64-byte primitive record
+EDGE_RECORD_FLOATS = 8   # 32-byte edge record (geometry)
+EDGE_CULL_INTS = 4       # 16-byte edge cull record
+MAX_IMAGE_DIM = 16384
+SEG_RECORD_INTS = 8      # 32-byte segment record
+PRIM_RECORD_FLOATS = 20  # 80-byte primitive record
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -40,7 +42,7 @@ _SIGNATURES = {
     "cs_isect_edge_ranges": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _P]),
     "cs_bin_prepare": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                       _I32, _I32, _I32, _F, _I32, _I32, _P, _P, _P, _P, _P, _P,
-                                      _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+                                      _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_bin_finish": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
                                      _P, _P, _P, _P, _P]),
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P,

@@ -22,6 +22,8 @@
 
 namespace cs {
 
+static_assert(sizeof(SegRec) == CS_SEG_RECORD_BYTES, "segment record layout");
+
 // ---------------------------------------------------------------- projection
 
 struct SegProj {
@@ -154,10 +156,26 @@ __device__ __forceinline__ int32_t px_index(float v) {
     return f2i_sat(fminf(fmaxf(v, -40000.0f), 40000.0f));
 }
 
-// Packed range of pixel indices k whose centre k + 0.5 can lie in
+// Inclusive range of pixel indices k whose centre k + 0.5 can lie in
 // [lo - d, hi + d], widened by one pixel on each side.
-__device__ __forceinline__ int32_t pixel_range(float lo, float hi, float d) {
-    return pack_range(px_index(floorf(lo - d - 0.5f)) - 1, px_index(ceilf(hi + d - 0.5f)) + 1);
+struct IRange {
+    int32_t lo, hi;
+};
+
+__device__ __forceinline__ IRange pixel_range(float lo, float hi, float d) {
+    return IRange{px_index(floorf(lo - d - 0.5f)) - 1, px_index(ceilf(hi + d - 0.5f)) + 1};
+}
+
+__device__ __forceinline__ int32_t span_x(IRange r) { return r.hi - r.lo + kWaveColsExt; }
+__device__ __forceinline__ int32_t span_y(IRange r) { return r.hi - r.lo + kWaveRowsExt; }
+
+// (lo, span) as two int16.  Indices below -2 or above kMaxImageDim + 16 meet
+// no wave of an image of at most kMaxImageDim pixels, so clamping them there
+// keeps every test's result.
+__device__ __forceinline__ int32_t packed_range(IRange r, int ext) {
+    const int lo = clampi(r.lo, -2, kMaxImageDim + 16);
+    const int hi = clampi(r.hi, -2, kMaxImageDim + 16);
+    return pack_lo_span(lo, hi - lo + ext);
 }
 
 // torch.linspace(0, 1, S)[i] as ATen's device kernel computes it.
@@ -172,7 +190,7 @@ __global__ __launch_bounds__(256) void k_project_flatten(
     const float* __restrict__ opacities, int mode, int nseg, int img_h, int img_w, int block_x,
     int block_y, float aabb_pad, int aniso, int S, float* __restrict__ cubics_px,
     int32_t* __restrict__ seg_tile_ranges, SegRec* __restrict__ seg_recs,
-    EdgeRec* __restrict__ edges) {
+    EdgeRec* __restrict__ edges, EdgeCull* __restrict__ culls) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
     const int p = owner_of(seg_offsets, P, s);
@@ -193,6 +211,7 @@ __global__ __launch_bounds__(256) void k_project_flatten(
     float prevx = 0.0f, prevy = 0.0f;
     float bx0 = __builtin_huge_valf(), by0 = bx0, bx1 = -bx0, by1 = -bx0;
     EdgeRec* er = edges + (size_t)s * (S - 1);
+    EdgeCull* ec = culls + (size_t)s * (S - 1);
     for (int i = 0; i < S; ++i) {
         const float t = linspace01(S, i);
         const float omt = 1.0f - t;
@@ -221,17 +240,26 @@ __global__ __launch_bounds__(256) void k_project_flatten(
                              __builtin_bit_cast(int, x), __builtin_bit_cast(int, y));
             o[1] = make_int4(__builtin_bit_cast(int, vx), __builtin_bit_cast(int, vy),
                              __builtin_bit_cast(int, vx * ivv), __builtin_bit_cast(int, vy * ivv));
-            o[2] = make_int4(pixel_range(ex0, ex1, D), pixel_range(ey0, ey1, D),
-                             pixel_range(ey0, ey1, 0.0f), 0);
+            const IRange nx = pixel_range(ex0, ex1, D), ny = pixel_range(ey0, ey1, D);
+            const IRange cy = pixel_range(ey0, ey1, 0.0f);
+            reinterpret_cast<int4*>(ec)[i - 1] =
+                make_int4(packed_range(ny, kWaveRowsExt), packed_range(cy, kWaveRowsExt),
+                          packed_range(nx, kWaveColsExt), 0);
         }
         prevx = x;
         prevy = y;
     }
+    const IRange nx = pixel_range(bx0, bx1, D), ny = pixel_range(by0, by1, D);
+    const IRange cy = pixel_range(by0, by1, 0.0f);
     SegRec sr;
-    sr.near_x = pixel_range(bx0, bx1, D);
-    sr.near_y = pixel_range(by0, by1, D);
-    sr.cross_y = pixel_range(by0, by1, 0.0f);
+    sr.ny_lo = ny.lo;
+    sr.ny_span = span_y(ny);
+    sr.cy_lo = cy.lo;
+    sr.cy_span = span_y(cy);
+    sr.nx_lo = nx.lo;
+    sr.nx_span = span_x(nx);
     sr.x_last = px_index(ceilf(bx1 - 0.5f)) + 1;
+    sr.pad = 0;
     seg_recs[s] = sr;
 }
 
@@ -293,24 +321,31 @@ __global__ __launch_bounds__(256) void k_prim_prep(
     rec.s1 = s1;
     rec.rule = fill_rules ? fill_rules[p] : 1;
     int closed = 1;
-    const int32_t empty = pack_range(32767, -32768);
-    int32_t nxr = empty, nyr = empty, cyr = empty, x_last = -32768;
+    IRange nx{kRangeLimit, -kRangeLimit}, ny = nx, cy = nx;
+    int32_t x_last = -kRangeLimit;
     for (int s = s0; s < s1; ++s) {
-        const int nx = (s + 1 < s1) ? s + 1 : s0;
+        const int nxt = (s + 1 < s1) ? s + 1 : s0;
         const float* a = cubics_norm + (size_t)s * 8;
-        const float* b = cubics_norm + (size_t)nx * 8;
+        const float* b = cubics_norm + (size_t)nxt * 8;
         closed &= (a[6] == b[0]) & (a[7] == b[1]);
         const SegRec sr = seg_recs[s];
-        nxr = range_union(nxr, sr.near_x);
-        nyr = range_union(nyr, sr.near_y);
-        cyr = range_union(cyr, sr.cross_y);
+        nx.lo = min(nx.lo, sr.nx_lo);
+        nx.hi = max(nx.hi, sr.nx_lo + sr.nx_span - kWaveColsExt);
+        ny.lo = min(ny.lo, sr.ny_lo);
+        ny.hi = max(ny.hi, sr.ny_lo + sr.ny_span - kWaveRowsExt);
+        cy.lo = min(cy.lo, sr.cy_lo);
+        cy.hi = max(cy.hi, sr.cy_lo + sr.cy_span - kWaveRowsExt);
         x_last = max(x_last, sr.x_last);
     }
     rec.closed = closed;
-    rec.near_x = nxr;
-    rec.near_y = nyr;
-    rec.cross_y = cyr;
+    rec.ny_lo = ny.lo;
+    rec.ny_span = span_y(ny);
+    rec.cy_lo = cy.lo;
+    rec.cy_span = span_y(cy);
+    rec.nx_lo = nx.lo;
+    rec.nx_span = span_x(nx);
     rec.x_last = x_last;
+    rec.pad = 0;
     recs[p] = rec;
 }
 
@@ -723,13 +758,15 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                               int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
                               int32_t samples, float aabb_pad, int32_t aniso, int32_t mode,
                               float* cubics_px, int32_t* seg_tile_ranges, void* seg_recs,
-                              void* edges, int32_t* prim_tile_ranges, uint32_t* num_tiles_hit,
+                              void* edges, void* edge_culls, int32_t* prim_tile_ranges,
+                              uint32_t* num_tiles_hit,
                               float* inv_sigma2s, void* prim_recs, uint32_t* keys,
                               int32_t* order, uint32_t* keys_alt, int32_t* vals_alt,
                               uint32_t* radix_counts, uint32_t* scan_temp,
                               uint32_t* rank_offsets, int32_t* status, hipStream_t stream) {
     if (nseg < 0 || nprim <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0 ||
-        samples < 2 || (mode != 0 && mode != 1))
+        samples < 2 || (mode != 0 && mode != 1) || img_h > kMaxImageDim ||
+        img_w > kMaxImageDim)
         return CS_ERR_ARGS;
     const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
     hipLaunchKernelGGL(k_status_init, dim3(1), dim3(1), 0, stream, seg_offsets, nprim, status);
@@ -738,7 +775,8 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                            cubics_norm, seg_offsets, nprim, aa_widths, stroke_widths, opacities,
                            mode, nseg, img_h, img_w, block_x, block_y, aabb_pad, aniso, samples,
                            cubics_px, seg_tile_ranges, reinterpret_cast<SegRec*>(seg_recs),
-                           reinterpret_cast<EdgeRec*>(edges));
+                           reinterpret_cast<EdgeRec*>(edges),
+                           reinterpret_cast<EdgeCull*>(edge_culls));
     hipLaunchKernelGGL(k_prim_prep, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
                        cubics_norm, seg_offsets, nprim, seg_tile_ranges,
                        reinterpret_cast<const SegRec*>(seg_recs), colors, opacities, depths,

@@ -21,25 +21,52 @@ constexpr float kAlphaMin = (float)(1.0 / 255.0);
 constexpr float kTStop = (float)1e-4;
 constexpr float kWidthMin = (float)1e-4;
 
+// Integer cull ranges.  A range holds every pixel index k (column or row)
+// whose centre k + 0.5 can matter, widened by one pixel beyond its fp32 bound,
+// so integer tests on it are conservative.  It is stored as (lo, span) with
+// span = hi - lo + ext, where ext + 1 is the wave's extent along that axis
+// (16 columns, 4 rows): [lo, hi] then meets the wave's [last - ext, last]
+// exactly when 0 <= last - lo <= span, which span_hits tests with one OR and a
+// sign check (no unpacking).  An empty range has span < ext.
+constexpr int kWaveColsExt = kTile - 1;  // a wave spans 16 columns
+constexpr int kWaveRowsExt = 3;          // and 4 rows
+constexpr int32_t kRangeLimit = 1 << 20;
+
+__device__ __forceinline__ bool span_hits(int32_t lo, int32_t span, int32_t last) {
+    const int32_t t = last - lo;
+    return (t | (span - t)) >= 0;
+}
+
 // One flattened polyline edge, 32 bytes: endpoints, direction v = p1 - p0 and
 // u = v / max(|v|^2, eps) (multiply by the correctly rounded reciprocal).
-//
-// Cull ranges are inclusive integer pixel ranges packed as two int16 (low
-// half = first, high half = last): `near_x`/`near_y` hold every pixel column /
-// row whose centre can lie within the owning primitive's cull distance of the
-// geometry, `cross_y` every pixel row whose centre lies in the geometry's
-// y-range (where a +x ray crossing is possible).  Each range is widened by
-// one pixel beyond its fp32 bound, so integer tests on them are conservative.
 struct alignas(16) EdgeRec {
     float x0, y0, x1, y1;
     float vx, vy, ux, uy;
-    int32_t near_x, near_y, cross_y, pad;
 };
 
-// Per cubic segment: the cull ranges of all its edges, plus the last pixel
+// The cull ranges of one edge, 16 bytes, each range packed as two int16
+// (low half lo, high half span): near rows, crossing rows (the edge's
+// y-range, where a +x ray crossing is possible; a subset of the near rows),
+// near columns.  Kept apart from the geometry so that the forward reads only
+// geometry and the backward reads the ranges of a whole primitive with one
+// vector load.  Packing limits pixel indices to int16, so images are at most
+// kMaxImageDim on a side.
+struct alignas(16) EdgeCull {
+    int32_t ny, cy, nx, pad;
+};
+constexpr int kMaxImageDim = 16384;
+
+__device__ __forceinline__ int32_t pack_lo_span(int32_t lo, int32_t span) {
+    return (int32_t)(((uint32_t)span << 16) | ((uint32_t)lo & 0xffffu));
+}
+__device__ __forceinline__ int32_t packed_lo(int32_t v) { return (int32_t)(v << 16) >> 16; }
+__device__ __forceinline__ int32_t packed_span(int32_t v) { return v >> 16; }
+
+// Per cubic segment: the unions of its edges' ranges, plus the last pixel
 // column that can lie left of one of its vertices (for open chains).
 struct alignas(16) SegRec {
-    int32_t near_x, near_y, cross_y, x_last;
+    int32_t ny_lo, ny_span, cy_lo, cy_span;
+    int32_t nx_lo, nx_span, x_last, pad;
 };
 
 // Per-primitive raster record, built once per forward.
@@ -52,7 +79,8 @@ struct alignas(16) PrimRec {
     int32_t s0, s1;     // segment range
     int32_t rule;       // 0 even-odd, else nonzero (fill)
     int32_t closed;     // 1 if the edge chain is closed
-    int32_t near_x, near_y, cross_y, x_last;  // unions over the segments
+    int32_t ny_lo, ny_span, cy_lo, cy_span;  // unions over the segments
+    int32_t nx_lo, nx_span, x_last, pad;
 };
 
 // Read-only data for the raster kernels, reached through the constant address
@@ -69,24 +97,6 @@ using cptr = const CS_CONST T*;
 template <class T>
 __device__ __forceinline__ cptr<T> as_const(const T* p) {
     return (cptr<T>)p;
-}
-
-__device__ __forceinline__ int32_t pack_range(int32_t lo, int32_t hi) {
-    lo = lo < -32768 ? -32768 : (lo > 32767 ? 32767 : lo);
-    hi = hi < -32768 ? -32768 : (hi > 32767 ? 32767 : hi);
-    return (int32_t)(((uint32_t)hi << 16) | ((uint32_t)lo & 0xffffu));
-}
-__device__ __forceinline__ int32_t range_lo(int32_t v) { return (int32_t)(v << 16) >> 16; }
-__device__ __forceinline__ int32_t range_hi(int32_t v) { return v >> 16; }
-
-// Union of two packed ranges.
-__device__ __forceinline__ int32_t range_union(int32_t a, int32_t b) {
-    return pack_range(min(range_lo(a), range_lo(b)), max(range_hi(a), range_hi(b)));
-}
-
-// Inclusive ranges [first, last] overlap.
-__device__ __forceinline__ bool range_hits(int32_t v, int32_t first, int32_t last) {
-    return range_lo(v) <= last && range_hi(v) >= first;
 }
 
 // exp(x): n = rint(x log2 e), r = x - n ln2 (two-part Cody-Waite), e^r by a

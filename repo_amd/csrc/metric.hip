@@ -10,7 +10,7 @@
 // normalized 1D Gaussian, metric.py:47-61).  A 32x32 output tile stages its
 // (32+win-1)^2 inputs in LDS; the horizontal pass gives each thread an 8-wide
 // strip (the 8+win-1 inputs are read once), the vertical pass a 4-tall strip
-// of the five moments.  The backward (absent from the reference) uses the
+// of the five moments (taken about a per-tile constant, see k_ssim_fwd).  The backward (absent from the reference) uses the
 // per-pixel partials A = dS/dmu_x, B = dS/dE[x^2], C = dS/dE[xy] and one
 // transposed separable correlation, blocked the same way.
 #include "cs_common.h"
@@ -157,14 +157,19 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
     load_tile<IT, ITP>(x + (size_t)c * h * w, h, w, oy0, ox0, xs);
     load_tile<IT, ITP>(y + (size_t)c * h * w, h, w, oy0, ox0, ys);
     __syncthreads();
+    // Moments are taken of x - kx and y - ky, with kx, ky one staged value per
+    // workgroup: sigma^2 = E[(x-k)^2] - (mu-k)^2 holds for any constant k and
+    // avoids the cancellation of E[x^2] - mu^2 in flat regions (where it
+    // would leave fp32 noise of order 1e-7 against c2 = 9e-4).
+    const float kx = xs[IT / 2][IT / 2], ky = ys[IT / 2][IT / 2];
     // Horizontal: thread -> (row, 8-wide strip); IT rows x 4 strips.
     for (int item = threadIdx.x; item < IT * (kSsimOT / kHStrip); item += 256) {
         const int r = item >> 2, q0 = (item & 3) * kHStrip;
         float a[kHStrip + WIN - 1], b[kHStrip + WIN - 1];
 #pragma unroll
         for (int k = 0; k < kHStrip + WIN - 1; ++k) {
-            a[k] = xs[r][q0 + k];
-            b[k] = ys[r][q0 + k];
+            a[k] = xs[r][q0 + k] - kx;
+            b[k] = ys[r][q0 + k] - ky;
         }
 #pragma unroll
         for (int o = 0; o < kHStrip; ++o) {
@@ -217,9 +222,11 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
     for (int o = 0; o < kVStrip; ++o) {
         const int oy = oy0 + r0 + o;
         if (oy >= oh || ox >= ow) continue;
-        const float mu1 = mom[0][o], mu2 = mom[1][o];
+        const float m1 = mom[0][o], m2 = mom[1][o];  // shifted means
+        const float s1 = mom[2][o] - m1 * m1, s2 = mom[3][o] - m2 * m2;
+        const float s12 = mom[4][o] - m1 * m2;
+        const float mu1 = m1 + kx, mu2 = m2 + ky;
         const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2, mu12 = mu1 * mu2;
-        const float s1 = mom[2][o] - mu1_sq, s2 = mom[3][o] - mu2_sq, s12 = mom[4][o] - mu12;
         const float n1 = 2.0f * mu12 + c1, d1 = mu1_sq + mu2_sq + c1;
         const float n2 = 2.0f * s12 + c2, d2 = s1 + s2 + c2;
         const float l = n1 / d1, cs_ = n2 / d2;

@@ -3,19 +3,20 @@
 // Launch: one 256-thread workgroup per 16x16 tile.  Unlike a block-synchronous
 // design, each of the four waves owns four tile rows (64 pixels, one per lane)
 // and walks the tile's sorted list on its own: the list entry, the primitive
-// record, the segment records and the edge records are wave-uniform, so they
-// are read through the scalar cache and used as SGPR operands, and no LDS or
-// workgroup barrier is needed.  A wave leaves the list when all of its pixels
-// have reached the transmittance stop.
+// record and the edge geometry are wave-uniform, so they are read through the
+// scalar cache and used as SGPR operands, and no LDS or workgroup barrier is
+// needed.  A wave leaves the list when all of its pixels have reached the
+// transmittance stop.
 //
-// Exactness-preserving culling per wave, on integer pixel ranges tested with
-// scalar instructions: geometry whose near ranges miss the wave's pixel
-// rectangle is farther than the primitive's cull distance from every lane and
-// cannot change any lane's result (outside: alpha < 1/255; inside: coverage is
-// exactly 1.0f), so its distance terms are skipped; its crossing terms are
-// skipped when its y-range misses the wave's four pixel rows.  The forward
-// culls per primitive and per segment, the backward also per edge.  Results
-// stay bit-identical to evaluating every edge.
+// Exactness-preserving culling per wave, on integer pixel ranges: geometry
+// whose near ranges miss the wave's pixel rectangle is farther than the
+// primitive's cull distance from every lane and cannot change any lane's
+// result (outside: alpha < 1/255; inside: coverage is exactly 1.0f), so its
+// distance terms are skipped; its crossing terms are skipped when its y-range
+// misses the wave's four pixel rows.  A primitive is tested as a whole with
+// scalar instructions; its edges are tested lane-parallel (one edge per lane,
+// one ballot per test), and the wave then evaluates only the edges that can
+// matter.  Results stay bit-identical to evaluating every edge.
 #include "cs_common.h"
 #include "../../include/cubicsplat_hip.h"
 
@@ -23,7 +24,7 @@ namespace cs {
 
 static_assert(sizeof(EdgeRec) == CS_EDGE_RECORD_BYTES, "edge record layout");
 static_assert(sizeof(PrimRec) == CS_PRIM_RECORD_BYTES, "primitive record layout");
-static_assert(sizeof(SegRec) == CS_SEG_RECORD_BYTES, "segment record layout");
+static_assert(sizeof(EdgeCull) == CS_EDGE_CULL_BYTES, "edge cull record layout");
 
 // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
 // contiguous run of tiles so neighbouring tiles (which share primitives and
@@ -48,12 +49,22 @@ struct WaveRect {
     int c0, c1, r0, r1;
 };
 
-__device__ __forceinline__ bool near_wave(int32_t near_x, int32_t near_y, const WaveRect& W) {
-    return range_hits(near_x, W.c0, W.c1) && range_hits(near_y, W.r0, W.r1);
+// Cull tests of a record's ranges against the wave (all wave-uniform).
+template <class R>
+__device__ __forceinline__ bool near_rows(const R& r, const WaveRect& W) {
+    return span_hits(r.ny_lo, r.ny_span, W.r1);
 }
-
-__device__ __forceinline__ bool rows_hit(int32_t cross_y, const WaveRect& W) {
-    return range_hits(cross_y, W.r0, W.r1);
+template <class R>
+__device__ __forceinline__ bool near_cols(const R& r, const WaveRect& W) {
+    return span_hits(r.nx_lo, r.nx_span, W.c1);
+}
+template <class R>
+__device__ __forceinline__ bool cross_rows(const R& r, const WaveRect& W) {
+    return span_hits(r.cy_lo, r.cy_span, W.r1);
+}
+template <class R>
+__device__ __forceinline__ bool near_wave(const R& r, const WaveRect& W) {
+    return near_rows(r, W) && near_cols(r, W);
 }
 
 // Distance (and optionally the best edge) of one edge, with w = pixel - p0,
@@ -91,111 +102,54 @@ __device__ __forceinline__ void cross_term(const EdgeRec& E, float wx, float wy,
     G.winding -= (int)(hit & !b0);
 }
 
-template <bool DIST, bool CROSS, bool BEST>
-__device__ __forceinline__ void edge_eval(const EdgeRec& E, int eid, float px, float py,
-                                          Geom& G) {
-    const float wx = px - E.x0, wy = py - E.y0;
-    if (DIST) dist_term<BEST>(E, eid, wx, wy, G);
-    if (CROSS) cross_term(E, wx, wy, py, G);
-}
-
-// Unroll factor of the best-edge (backward) loop: a full unroll keeps too many
-// candidates live (registers -> occupancy), so it is partial.
-#ifndef CS_BEST_UNROLL
-#define CS_BEST_UNROLL 3
-#endif
-
-// Every edge of one segment with the same terms (forward).  EPS > 0 fixes the
-// edge count at compile time: the loop unrolls, its scalar loads batch up and
-// it has no branches.
-template <bool DIST, bool CROSS, int EPS>
-__device__ __forceinline__ void scan_all(cptr<EdgeRec> ep, int n, float px, float py, Geom& G) {
-    if constexpr (EPS > 0) {
-#pragma unroll
-        for (int e = 0; e < EPS; ++e) edge_eval<DIST, CROSS, false>(ep[e], 0, px, py, G);
-    } else {
-#pragma unroll 4
-        for (int e = 0; e < n; ++e) edge_eval<DIST, CROSS, false>(ep[e], 0, px, py, G);
-    }
-}
-
-// One edge of the backward scan, with its wave-uniform cull decisions: the
-// distance terms only where the edge's near ranges meet the wave, the
-// crossing terms only where its y-range meets the wave's rows.
-template <bool MAYCROSS>
-__device__ __forceinline__ void edge_culled(const EdgeRec& E, int eid, bool seg_near,
-                                            bool seg_band, const WaveRect& W, float px,
-                                            float py, Geom& G) {
-    const bool dn = seg_near && near_wave(E.near_x, E.near_y, W);
-    const bool cb = MAYCROSS && seg_band && rows_hit(E.cross_y, W);
-    if (!(dn || cb)) return;
-    const float wx = px - E.x0, wy = py - E.y0;
-    if (dn) dist_term<true>(E, eid, wx, wy, G);
-    if (cb) cross_term(E, wx, wy, py, G);
-}
-
-// One segment's edges with per-edge culling (backward: its per-lane work per
-// evaluated edge is larger, so skipping edges pays for the branches).  The
-// records of a chunk are loaded before any of them is tested, so their scalar
-// loads are in flight together.
-template <bool MAYCROSS, int EPS>
-__device__ __forceinline__ void scan_culled(cptr<EdgeRec> ep, int n, int ebase, bool seg_near,
-                                            bool seg_band, const WaveRect& W, float px,
-                                            float py, Geom& G) {
-    if constexpr (EPS > 0) {
-        constexpr int CH = CS_BEST_UNROLL;
-#pragma unroll
-        for (int c0 = 0; c0 < EPS; c0 += CH) {
-            EdgeRec Es[CH];
-#pragma unroll
-            for (int k = 0; k < CH; ++k)
-                if (c0 + k < EPS) Es[k] = ep[c0 + k];
-#pragma unroll
-            for (int k = 0; k < CH; ++k)
-                if (c0 + k < EPS)
-                    edge_culled<MAYCROSS>(Es[k], ebase + c0 + k, seg_near, seg_band, W, px, py, G);
-        }
-    } else {
-#pragma unroll 4
-        for (int e = 0; e < n; ++e)
-            edge_culled<MAYCROSS>(ep[e], ebase + e, seg_near, seg_band, W, px, py, G);
-    }
-}
-
 // Primitive-level cull: true when no lane of the wave can be affected.
 template <int MODE>
 __device__ __forceinline__ bool prim_culled(const PrimRec& pr, const WaveRect& W) {
-    if (near_wave(pr.near_x, pr.near_y, W)) return false;
+    if (near_wave(pr, W)) return false;
     if (MODE == 1 || pr.closed) return true;
     // Open chain in fill mode: the winding number can be non-zero left of the
     // vertices, but not when the rows miss their y-range or the wave lies
     // right of every vertex.
-    return !rows_hit(pr.cross_y, W) || W.c0 > pr.x_last;
+    return !cross_rows(pr, W) || W.c0 > pr.x_last;
 }
 
-template <int MODE, bool BEST, int EPS>
+// All edges of a primitive with per-edge culling decided lane-parallel: lane
+// k loads the packed ranges of edge k of a 64-edge chunk (one vector load),
+// tests them against the wave, and two ballots give the edges whose distance
+// and crossing terms can matter.  The wave then visits only those edges, in
+// ascending index order (so the best edge is the first strict minimum, as in
+// the reference), loading each one's geometry through the scalar cache.
+template <int MODE, bool BEST>
 __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& W,
-                                              cptr<SegRec> segs, cptr<EdgeRec> edges, int eps,
-                                              float px, float py, Geom& G) {
+                                              const EdgeCull* __restrict__ culls,
+                                              cptr<EdgeRec> edges, int eps, float px, float py,
+                                              Geom& G) {
     G.min_d2 = 1e30f;
     G.winding = 0;
     G.best = -1;
     G.bproj = 0.0f;
     G.bdx = 0.0f;
     G.bdy = 0.0f;
-    for (int s = pr.s0; s < pr.s1; ++s) {
-        const SegRec sg = segs[s];
-        const bool near = near_wave(sg.near_x, sg.near_y, W);
-        const bool band = MODE == 0 && rows_hit(sg.cross_y, W);
-        if (!(near || band)) continue;
-        cptr<EdgeRec> ep = edges + (size_t)s * eps;
-        if constexpr (BEST) {
-            scan_culled<MODE == 0, EPS>(ep, eps, s * eps, near, band, W, px, py, G);
-        } else if (near) {
-            if (band) scan_all<true, true, EPS>(ep, eps, px, py, G);
-            else scan_all<true, false, EPS>(ep, eps, px, py, G);
-        } else {
-            scan_all<false, true, EPS>(ep, eps, px, py, G);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int e1 = pr.s1 * eps;
+    for (int c = pr.s0 * eps; c < e1; c += kWave) {
+        bool dn = false, cb = false;
+        if (c + lane < e1) {
+            const int4 q = *reinterpret_cast<const int4*>(culls + c + lane);
+            dn = span_hits(packed_lo(q.x), packed_span(q.x), W.r1) &&
+                 span_hits(packed_lo(q.z), packed_span(q.z), W.c1);
+            cb = MODE == 0 && span_hits(packed_lo(q.y), packed_span(q.y), W.r1);
+        }
+        const uint64_t mdn = __ballot(dn);
+        const uint64_t mcb = MODE == 0 ? (uint64_t)__ballot(cb) : 0ull;
+        uint64_t todo = mdn | mcb;
+        while (todo) {
+            const int k = (int)__builtin_ctzll(todo);
+            todo &= todo - 1;
+            const EdgeRec E = edges[c + k];
+            const float wx = px - E.x0, wy = py - E.y0;
+            if ((mdn >> k) & 1) dist_term<BEST>(E, c + k, wx, wy, G);
+            if (MODE == 0 && ((mcb >> k) & 1)) cross_term(E, wx, wy, py, G);
         }
     }
 }
@@ -235,10 +189,10 @@ __device__ __forceinline__ Cov coverage(const PrimRec& pr, const Geom& G, float 
     return c;
 }
 
-template <int MODE, int EPS>
+template <int MODE>
 __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
-    const EdgeRec* __restrict__ edges_g, const SegRec* __restrict__ segs_g,
+    const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, int eps, float* __restrict__ out, float* __restrict__ final_T,
     int32_t* __restrict__ final_idx) {
@@ -254,7 +208,6 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
                      tty * kTile + wv * 4 + 3};
     const cptr<int32_t> prim_ids = as_const(prim_ids_g);
     const cptr<PrimRec> prims = as_const(prims_g);
-    const cptr<SegRec> segs = as_const(segs_g);
     const cptr<EdgeRec> edges = as_const(edges_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
     float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
@@ -269,7 +222,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
         const float D2 = pr.cull_d * pr.cull_d;
         if (prim_culled<MODE>(pr, W)) continue;
         Geom G;
-        prim_geometry<MODE, false, EPS>(pr, W, segs, edges, eps, px, py, G);
+        prim_geometry<MODE, false>(pr, W, culls, edges, eps, px, py, G);
         if (!done) {
             const Cov c = coverage<MODE>(pr, G, D2);
             const float alpha = fminf(kAlphaCap, pr.opacity * c.cov);
@@ -315,10 +268,10 @@ __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
 //     reference's accumulation weights (cubic_splatting.py:2308-2396), then
 //     lanes that share a segment are summed (one leader pass per distinct
 //     segment) and one lane adds the 8 values to v_cubics_px.
-template <int MODE, int EPS>
+template <int MODE>
 __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
-    const EdgeRec* __restrict__ edges_g, const SegRec* __restrict__ segs_g,
+    const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, int eps, const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
@@ -337,7 +290,6 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
                      tty * kTile + wv * 4 + 3};
     const cptr<int32_t> prim_ids = as_const(prim_ids_g);
     const cptr<PrimRec> prims = as_const(prims_g);
-    const cptr<SegRec> segs = as_const(segs_g);
     const cptr<EdgeRec> edges = as_const(edges_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
     const size_t pix = in_img ? (size_t)i * img_w + j : 0;
@@ -364,7 +316,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
         const float D2 = pr.cull_d * pr.cull_d;
         if (prim_culled<MODE>(pr, W)) continue;
         Geom G;
-        prim_geometry<MODE, true, EPS>(pr, W, segs, edges, eps, px, py, G);
+        prim_geometry<MODE, true>(pr, W, culls, edges, eps, px, py, G);
         float vr = 0.0f, vg = 0.0f, vb = 0.0f, vop = 0.0f, vis2 = 0.0f, vsw = 0.0f;
         float cr = 0.0f, cg = 0.0f, cb = 0.0f;
         float gx = 0.0f, gy = 0.0f;
@@ -547,7 +499,7 @@ struct RasterArgs {
     const int32_t* ids;
     const int32_t* bins;
     const EdgeRec* E;
-    const SegRec* B;
+    const EdgeCull* C;
     const PrimRec* P;
     const float* bg;
     // forward outputs
@@ -562,41 +514,23 @@ struct RasterArgs {
     hipStream_t stream;
 };
 
-template <int MODE, int EPS>
+template <int MODE>
 static void launch_fwd(const RasterArgs& a) {
-    hipLaunchKernelGGL((k_raster_fwd<MODE, EPS>), dim3(a.nt), dim3(kBlockThreads), 0, a.stream,
-                       a.ids, a.bins, a.E, a.B, a.P, a.bg, a.img_h, a.img_w, a.tbx, a.nt, a.eps,
-                       a.out, a.final_T, a.final_idx);
+    hipLaunchKernelGGL((k_raster_fwd<MODE>), dim3(a.nt), dim3(kBlockThreads), 0, a.stream,
+                       a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx, a.nt,
+                       a.eps, a.out, a.final_T, a.final_idx);
 }
 
-template <int MODE, int EPS>
+template <int MODE>
 static void launch_bwd(const RasterArgs& a) {
-    hipLaunchKernelGGL((k_raster_bwd<MODE, EPS>), dim3(a.nt), dim3(kBlockThreads), 0, a.stream,
-                       a.ids, a.bins, a.E, a.B, a.P, a.bg, a.img_h, a.img_w, a.tbx, a.nt, a.eps,
-                       a.fT, a.fidx, a.v_out, a.v_cub, a.v_col, a.v_op, a.v_is2, a.v_sw, a.c_rgb,
+    hipLaunchKernelGGL((k_raster_bwd<MODE>), dim3(a.nt), dim3(kBlockThreads), 0, a.stream,
+                       a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx, a.nt,
+                       a.eps, a.fT, a.fidx, a.v_out, a.v_cub, a.v_col, a.v_op, a.v_is2, a.v_sw, a.c_rgb,
                        a.c_isect);
 }
 
-// Edge counts per segment with an unrolled instantiation: S = 8, 12, 16, 18,
-// 24, 32 samples (the training defaults 12/18, the paper's 24, the configs'
-// 8/16/32); any other count runs the generic loop.
-template <bool BWD, int MODE>
-static void dispatch(const RasterArgs& a) {
-#define CS_LAUNCH(E_) (BWD ? launch_bwd<MODE, E_>(a) : launch_fwd<MODE, E_>(a))
-    switch (a.eps) {
-        case 7: CS_LAUNCH(7); break;
-        case 11: CS_LAUNCH(11); break;
-        case 15: CS_LAUNCH(15); break;
-        case 17: CS_LAUNCH(17); break;
-        case 23: CS_LAUNCH(23); break;
-        case 31: CS_LAUNCH(31); break;
-        default: CS_LAUNCH(0); break;
-    }
-#undef CS_LAUNCH
-}
-
 static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* bins,
-                              const void* edges, const void* seg_recs, const void* prims,
+                              const void* edges, const void* edge_culls, const void* prims,
                               const float* bg, int32_t img_h, int32_t img_w, int32_t eps,
                               hipStream_t stream) {
     RasterArgs a{};
@@ -609,7 +543,7 @@ static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* b
     a.ids = ids;
     a.bins = bins;
     a.E = reinterpret_cast<const EdgeRec*>(edges);
-    a.B = reinterpret_cast<const SegRec*>(seg_recs);
+    a.C = reinterpret_cast<const EdgeCull*>(edge_culls);
     a.P = reinterpret_cast<const PrimRec*>(prims);
     a.bg = bg;
     a.stream = stream;
@@ -618,36 +552,40 @@ static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* b
 
 extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                                     const int32_t* tile_bins, const void* edges,
-                                    const void* seg_recs, const void* prim_recs,
-                                    const float* background, int32_t img_h, int32_t img_w,
-                                    int32_t edges_per_segment, float* out_img, float* final_Ts,
+                                    const void* edge_culls, const void* prim_recs,
+                                    const float* background,
+                                    int32_t img_h, int32_t img_w, int32_t edges_per_segment,
+                                    float* out_img, float* final_Ts,
                                     int32_t* final_idx, hipStream_t stream) {
-    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1)
+    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1 ||
+        img_h > kMaxImageDim || img_w > kMaxImageDim)
         return CS_ERR_ARGS;
-    RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, seg_recs, prim_recs,
+    RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                                background, img_h, img_w, edges_per_segment, stream);
     a.out = out_img;
     a.final_T = final_Ts;
     a.final_idx = final_idx;
-    if (mode == 0) dispatch<false, 0>(a);
-    else dispatch<false, 1>(a);
+    if (mode == 0) launch_fwd<0>(a);
+    else launch_fwd<1>(a);
     return raster_status();
 }
 
 extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                                      const int32_t* tile_bins, const void* edges,
-                                     const void* seg_recs, const void* prim_recs,
-                                     const float* background, int32_t img_h, int32_t img_w,
+                                     const void* edge_culls, const void* prim_recs,
+                                     const float* background,
+                                     int32_t img_h, int32_t img_w,
                                      int32_t edges_per_segment, const float* final_Ts,
                                      const int32_t* final_idx, const float* v_output,
                                      float* v_cubics_px, float* v_colors, float* v_opacities,
                                      float* v_inv_sigma2s, float* v_stroke_widths,
                                      float* curve_contrib_rgb, float* curve_isect_contrib,
                                      hipStream_t stream) {
-    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1)
+    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1 ||
+        img_h > kMaxImageDim || img_w > kMaxImageDim)
         return CS_ERR_ARGS;
     if (mode == 1 && v_stroke_widths == nullptr) return CS_ERR_ARGS;
-    RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, seg_recs, prim_recs,
+    RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                                background, img_h, img_w, edges_per_segment, stream);
     a.fT = final_Ts;
     a.fidx = final_idx;
@@ -659,8 +597,8 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
     a.v_sw = v_stroke_widths;
     a.c_rgb = curve_contrib_rgb;
     a.c_isect = curve_isect_contrib;
-    if (mode == 0) dispatch<true, 0>(a);
-    else dispatch<true, 1>(a);
+    if (mode == 0) launch_bwd<0>(a);
+    else launch_bwd<1>(a);
     return raster_status();
 }
 

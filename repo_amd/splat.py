@@ -88,8 +88,9 @@ class Binned:
     num_intersects: int
     cubics_px: torch.Tensor
     seg_tile_ranges: torch.Tensor
-    seg_recs: torch.Tensor         # [nseg, 4] int32 packed cull ranges
-    edges: torch.Tensor            # [E, 12] 48-byte records (x0 y0 x1 y1 vx vy ux uy + ranges)
+    seg_recs: torch.Tensor         # [nseg, 8] int32 cull ranges
+    edges: torch.Tensor            # [E, 8] x0 y0 x1 y1 vx vy ux uy
+    edge_culls: torch.Tensor       # [E, 4] int32 packed cull ranges
     prim_tile_ranges: torch.Tensor
     num_tiles_hit: torch.Tensor
     inv_sigma2s: torch.Tensor
@@ -125,6 +126,7 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     seg_tile_ranges = torch.empty((nseg, 4), dtype=i32, device=dev)
     seg_recs = torch.empty((nseg, N.SEG_RECORD_INTS), dtype=i32, device=dev)
     edges = torch.empty((E, N.EDGE_RECORD_FLOATS), dtype=f32, device=dev)
+    edge_culls = torch.empty((E, N.EDGE_CULL_INTS), dtype=i32, device=dev)
     prim_tile_ranges = torch.empty((P, 4), dtype=i32, device=dev)
     num_tiles_hit = torch.empty((P,), dtype=i32, device=dev)
     inv_sigma2s = torch.empty((P,), dtype=f32, device=dev)
@@ -145,7 +147,8 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
                N.ptr(opacities), N.ptr(depths), N.ptr(fill_rules), N.ptr(widths),
                N.ptr(stroke_widths), nseg, P, img_h, img_w, block_x, block_y, S, float(aabb_pad),
                int(bool(aniso)), mode, N.ptr(cubics_px), N.ptr(seg_tile_ranges), N.ptr(seg_recs),
-               N.ptr(edges), N.ptr(prim_tile_ranges), N.ptr(num_tiles_hit), N.ptr(inv_sigma2s),
+               N.ptr(edges), N.ptr(edge_culls), N.ptr(prim_tile_ranges), N.ptr(num_tiles_hit),
+               N.ptr(inv_sigma2s),
                N.ptr(prim_recs), N.ptr(keys), N.ptr(order), N.ptr(keys_alt), N.ptr(vals_alt),
                N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(rank_offsets), N.ptr(status), st)
     I, bad, first, last = status.tolist()
@@ -173,7 +176,8 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
                N.ptr(valt), N.ptr(rc_i), N.ptr(st_i), N.ptr(tile_bins), st)
     return Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P,
                   num_intersects=I, cubics_px=cubics_px, seg_tile_ranges=seg_tile_ranges,
-                  seg_recs=seg_recs, edges=edges, prim_tile_ranges=prim_tile_ranges,
+                  seg_recs=seg_recs, edges=edges, edge_culls=edge_culls,
+                  prim_tile_ranges=prim_tile_ranges,
                   num_tiles_hit=num_tiles_hit, inv_sigma2s=inv_sigma2s, prim_recs=prim_recs,
                   order=order, primitive_ids_sorted=prim_ids, tile_keys_sorted=tile_keys,
                   tile_bins=tile_bins)
@@ -186,9 +190,9 @@ def rasterize_forward(b: Binned, background: torch.Tensor):
     final_idx = torch.empty((b.img_h, b.img_w), dtype=torch.int32, device=dev)
     with N.prof("cubic.fwd.rast"):
         N.call("cs_rasterize_forward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
-               N.ptr(b.edges), N.ptr(b.seg_recs), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
-               b.img_w, b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx),
-               N.stream(dev))
+               N.ptr(b.edges), N.ptr(b.edge_culls), N.ptr(b.prim_recs), N.ptr(background),
+               b.img_h, b.img_w, b.edges_per_segment, N.ptr(out), N.ptr(final_T),
+               N.ptr(final_idx), N.stream(dev))
     return out, final_T, final_idx
 
 
@@ -209,8 +213,9 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
     with N.prof("cubic.bwd.rast"):
         N.call("cs_rasterize_backward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
-               N.ptr(b.edges), N.ptr(b.seg_recs), N.ptr(b.prim_recs), N.ptr(background), b.img_h,
-               b.img_w, b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(v_output),
+               N.ptr(b.edges), N.ptr(b.edge_culls), N.ptr(b.prim_recs), N.ptr(background),
+               b.img_h, b.img_w, b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx),
+               N.ptr(v_output),
                N.ptr(v_px), N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw),
                N.ptr(curve_contrib_rgb), N.ptr(curve_isect_contrib), N.stream(dev))
     return v_px, v_colors, v_opac, v_is2, v_sw
@@ -267,6 +272,9 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
         return bg.view(1, 1, 3).expand(int(img_h), int(img_w), 3).clone()
     _check_block(block_x, block_y)
     _check_flatten(flatten_method_norm)
+    if int(img_h) > N.MAX_IMAGE_DIM or int(img_w) > N.MAX_IMAGE_DIM:
+        raise ValueError(f"img_h and img_w must be at most {N.MAX_IMAGE_DIM} "
+                         f"(got {int(img_h)}x{int(img_w)})")
     N.require_gpu(cubics_norm, "cubics_norm")
     for name, t, k in (("colors", colors, None), ("opacities", opacities, 1),
                        ("depths", depths, 1), ("fill_rules", fill_rules, 1),

@@ -9,7 +9,8 @@ random generators staying the same), the reference's binning outputs
 final_Ts, final_idx), the gradients of a fixed upstream gradient and, for the
 config-1 case, the MSE and SSIM values against a fixed target plus the SSIM
 gradient at sampled pixels and along fixed directions.  Upstream gradients
-and targets are integer-hash patterns (exact on any platform).
+and targets are integer-hash patterns (exact on any platform); the loss
+target mixes the rendered image with such a pattern.
 
 Cases:
   cfg1_fill    the reference's CPU-runnable configuration (64 self-intersecting
@@ -80,8 +81,11 @@ def v_out_pattern(h, w, salt):
     return hash_pattern((h, w, 3), salt)
 
 
-def target_pattern(h, w):
-    return hash_pattern((1, 3, h, w), 7, 0.0, 1.0)
+def target_pattern(x):
+    """A target correlated with the rendered image x [1,3,h,w] (as a training
+    target is), so that SSIM is far from zero."""
+    return np.clip(np.float32(0.7) * x + np.float32(0.3) * hash_pattern(x.shape, 7, 0.0, 1.0),
+                   0.0, 1.0).astype(np.float32)
 
 
 def expected(inp, with_losses):
@@ -111,7 +115,7 @@ def expected(inp, with_losses):
     if with_losses:
         import torch
         x = np.clip(fw["out"], 0.0, 1.0).transpose(2, 0, 1)[None].astype(np.float32)
-        y = target_pattern(h, w)
+        y = target_pattern(x)
         out["loss_mse"] = np.float64(O.mse(x, y))
         xt = torch.from_numpy(x.astype(np.float64)).requires_grad_(True)
         s = O.ssim_torch64(xt, torch.from_numpy(y.astype(np.float64)))

@@ -53,10 +53,12 @@ def test_library_loads_and_exports_every_symbol():
 def test_record_sizes_match_header():
     from repo_amd import _native as N
     text = open(HEADER).read()
-    sizes = dict(re.findall(r"#define (CS_\w+_RECORD_BYTES) (\d+)", text))
+    sizes = dict(re.findall(r"#define (CS_\w+_BYTES) (\d+)", text))
     assert int(sizes["CS_EDGE_RECORD_BYTES"]) == 4 * N.EDGE_RECORD_FLOATS
     assert int(sizes["CS_SEG_RECORD_BYTES"]) == 4 * N.SEG_RECORD_INTS
     assert int(sizes["CS_PRIM_RECORD_BYTES"]) == 4 * N.PRIM_RECORD_FLOATS
+    assert int(sizes["CS_EDGE_CULL_BYTES"]) == 4 * N.EDGE_CULL_INTS
+    assert int(re.search(r"#define CS_MAX_IMAGE_DIM (\d+)", text).group(1)) == N.MAX_IMAGE_DIM
 
 
 # Parameter lists of the reference's public functions
@@ -143,6 +145,15 @@ def test_size_errors_are_value_errors():
     with pytest.raises(ValueError, match="stroke_widths"):
         manbo.ops.render_cubic_polyline_splat_tilelang(cub, offs, col, op, torch.ones(2), dep,
                                                        32, 32, 16, 16, bg)
+
+
+def test_image_size_limit():
+    import manbo
+    from repo_amd import _native as N
+    cub, offs, col, op, dep = _scene_args()
+    with pytest.raises(ValueError, match="at most"):
+        manbo.ops.render_cubic_fill_splat_tilelang(cub, offs, col, op, dep, 32,
+                                                   N.MAX_IMAGE_DIM + 1, 16, 16, torch.ones(3))
 
 
 def test_host_tensors_are_rejected():

@@ -81,7 +81,7 @@ def test_losses_match_fixture():
     fx = load("cfg1_fill")
     h, w = int(fx["in_meta"][0]), int(fx["in_meta"][1])
     x = np.clip(fx["fwd_out"], 0.0, 1.0).transpose(2, 0, 1)[None].copy()
-    y = torch.from_numpy(G.target_pattern(h, w)).cuda()
+    y = torch.from_numpy(G.target_pattern(x)).cuda()
     xd = torch.from_numpy(x).cuda().requires_grad_(True)
     mse = float(manbo.mse_loss_tilelang(xd, y))
     assert abs(mse - float(fx["loss_mse"])) <= 1e-5 * abs(float(fx["loss_mse"]))
