@@ -142,14 +142,38 @@ __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect&
         }
         const uint64_t mdn = __ballot(dn);
         const uint64_t mcb = MODE == 0 ? (uint64_t)__ballot(cb) : 0ull;
-        uint64_t todo = mdn | mcb;
-        while (todo) {
-            const int k = (int)__builtin_ctzll(todo);
-            todo &= todo - 1;
-            const EdgeRec E = edges[c + k];
-            const float wx = px - E.x0, wy = py - E.y0;
-            if ((mdn >> k) & 1) dist_term<BEST>(E, c + k, wx, wy, G);
-            if (MODE == 0 && ((mcb >> k) & 1)) cross_term(E, wx, wy, py, G);
+        const cptr<EdgeRec> ec = edges + c;
+        if constexpr (BEST) {
+            // Distance terms in ascending edge order (the first strict minimum
+            // wins ties); the crossing terms' order does not matter.
+            for (uint64_t todo = mdn; todo; todo &= todo - 1) {
+                const int k = (int)__builtin_ctzll(todo);
+                const EdgeRec E = ec[k];
+                const float wx = px - E.x0, wy = py - E.y0;
+                dist_term<true>(E, c + k, wx, wy, G);
+                if (MODE == 0 && ((mcb >> k) & 1)) cross_term(E, wx, wy, py, G);
+            }
+            for (uint64_t todo = mcb & ~mdn; todo; todo &= todo - 1) {
+                const EdgeRec E = ec[__builtin_ctzll(todo)];
+                cross_term(E, px - E.x0, py - E.y0, py, G);
+            }
+        } else {
+            // The minimum and the winding number do not depend on the order:
+            // three loops without per-edge tests.
+            for (uint64_t todo = mdn & mcb; todo; todo &= todo - 1) {
+                const EdgeRec E = ec[__builtin_ctzll(todo)];
+                const float wx = px - E.x0, wy = py - E.y0;
+                dist_term<false>(E, 0, wx, wy, G);
+                cross_term(E, wx, wy, py, G);
+            }
+            for (uint64_t todo = mdn & ~mcb; todo; todo &= todo - 1) {
+                const EdgeRec E = ec[__builtin_ctzll(todo)];
+                dist_term<false>(E, 0, px - E.x0, py - E.y0, G);
+            }
+            for (uint64_t todo = mcb & ~mdn; todo; todo &= todo - 1) {
+                const EdgeRec E = ec[__builtin_ctzll(todo)];
+                cross_term(E, px - E.x0, py - E.y0, py, G);
+            }
         }
     }
 }
@@ -248,6 +272,10 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
     }
 }
 
+// Quotients that only feed gradients (never the image, T or a decision) use
+// the hardware reciprocal (within 1 ulp) instead of an IEEE division.
+__device__ __forceinline__ float grad_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
 // Reference cubic-accumulation basis at t = e / eps (cubic_splatting.py:2353-2371).
 __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
     const float t = (float)e * inv_e;
@@ -327,7 +355,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
             const float alpha = fminf(kAlphaCap, op * c.cov);
             if (alpha >= kAlphaMin) {
                 contrib = true;
-                const float ra = 1.0f / (1.0f - alpha);
+                const float ra = grad_rcp(1.0f - alpha);
                 T = T * ra;
                 const float fac = alpha * T;
                 vr = fac * v0;
@@ -351,11 +379,12 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
                         const float v_cov = op * va;
                         const float v_logit = -v_cov * c.cov * (1.0f - c.cov);
                         const float v_is = v_logit * c.sgn * c.dist * 2.0f;
-                        vis2 = v_is * 0.5f / fmaxf(pr.inv_sigma, kEps);
+                        vis2 = v_is * 0.5f * grad_rcp(fmaxf(pr.inv_sigma, kEps));
                         if (c.dist > kEps && G.best >= 0) {
                             const float v_dist = v_logit * c.sgn * pr.inv_sigma * 2.0f;
-                            gx = v_dist * G.bdx / c.dist;
-                            gy = v_dist * G.bdy / c.dist;
+                            const float rd = grad_rcp(c.dist);
+                            gx = v_dist * G.bdx * rd;
+                            gy = v_dist * G.bdy * rd;
                             geom = true;
                         }
                     } else {
@@ -365,8 +394,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
                             const float v_e = v_sigma * c.ed * pr.inv_sigma2;
                             vsw = -0.5f * v_e;
                             if (c.dist > kEps && G.best >= 0) {
-                                gx = v_e * G.bdx / c.dist;
-                                gy = v_e * G.bdy / c.dist;
+                                const float rd = grad_rcp(c.dist);
+                                gx = v_e * G.bdx * rd;
+                                gy = v_e * G.bdy * rd;
                                 geom = true;
                             }
                         }
