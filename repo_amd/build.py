@@ -7,6 +7,13 @@ Flags that are part of the numerical contract:
   -fno-fast-math        IEEE division and square root.
   -munsafe-fp-atomics   hardware fp32 global atomics instead of CAS loops.
   -packed-fp32-ops off  no v_pk_*_f32 generation.
+
+Code-generation flag:
+  -amdgpu-atomic-optimizer-strategy=None
+                        every global atomic in these kernels is issued by one
+                        lane after an explicit wave reduction; the compiler's
+                        atomic optimizer would wrap each in a redundant
+                        scan loop.
 """
 from __future__ import annotations
 
@@ -25,6 +32,7 @@ HIPCC_FLAGS = [
     "-mcode-object-version=5",
     "-ffp-contract=off", "-fno-fast-math", "-munsafe-fp-atomics",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wno-unused-result",
 ]
 

@@ -272,6 +272,15 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
     }
 }
 
+// n / eps for 0 <= n < 2^31 with magic = ceil(2^32 / eps) (eps >= 2): the
+// high product is n/eps or one more, which one comparison corrects.
+__device__ __forceinline__ int div_eps(int n, int eps, uint32_t magic) {
+    if (eps == 1) return n;
+    int q = (int)__umulhi((uint32_t)n, magic);
+    if (q * eps > n) --q;
+    return q;
+}
+
 // Quotients that only feed gradients (never the image, T or a decision) use
 // the hardware reciprocal (within 1 ulp) instead of an IEEE division.
 __device__ __forceinline__ float grad_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
@@ -301,7 +310,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
-    int tbx, int ntiles, int eps, const float* __restrict__ final_T,
+    int tbx, int ntiles, int eps, uint32_t eps_magic, const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
@@ -330,6 +339,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     const float bg_dot = __builtin_fmaf(bg[2], v2, __builtin_fmaf(bg[1], v1, bg[0] * v0));
     const bool want_contrib = (contrib_rgb != nullptr) | (isect_contrib != nullptr);
     const float inv_e = 1.0f / (float)eps;
+
     float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
     // The wave maximum is uniform; readfirstlane tells the compiler so, which
     // keeps every load that depends on the entry index scalar.
@@ -440,7 +450,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
 #pragma unroll
         for (int k = 0; k < 8; ++k) cp[k] = 0.0f;
         if (geom) {
-            gseg = G.best / eps;
+            gseg = div_eps(G.best, eps, eps_magic);
             const int el = G.best - gseg * eps;
             float bs[4], be[4];
             seg_basis(el, inv_e, bs);
@@ -477,6 +487,7 @@ __global__ __launch_bounds__(256) void k_accumulate(const float4* __restrict__ v
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
     const float inv_e = 1.0f / (float)eps;
+
     float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int e = 0; e < eps; ++e) {
         float bs[4], be[4];
@@ -553,9 +564,12 @@ static void launch_fwd(const RasterArgs& a) {
 
 template <int MODE>
 static void launch_bwd(const RasterArgs& a) {
+    // ceil(2^32 / eps) for div_eps (unused when eps == 1).
+    const uint32_t magic =
+        a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
     hipLaunchKernelGGL((k_raster_bwd<MODE>), dim3(a.nt), dim3(kBlockThreads), 0, a.stream,
                        a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx, a.nt,
-                       a.eps, a.fT, a.fidx, a.v_out, a.v_cub, a.v_col, a.v_op, a.v_is2, a.v_sw, a.c_rgb,
+                       a.eps, magic, a.fT, a.fidx, a.v_out, a.v_cub, a.v_col, a.v_op, a.v_is2, a.v_sw, a.c_rgb,
                        a.c_isect);
 }
 
