@@ -166,6 +166,64 @@ __device__ __forceinline__ float wave_sum_lane63(float x) {
     return x;
 }
 
+// t + (t moved by `STRIDE` lanes) on the lower half of each 2*STRIDE group,
+// with v_permlane16_swap / v_permlane32_swap: the swap exchanges the upper
+// rows of its first register with the lower rows of its second, so swapping t
+// against a zero register leaves t's lower part in the first and its upper
+// part in the second, lane-aligned.  (Written as inline assembly with two
+// separate in/out registers: the compiler builtin's second result is not
+// reliable.  The s_nop covers the VALU-write to permlane-read hazard.)
+template <int STRIDE>
+__device__ __forceinline__ float row_pair_add(float t) {
+    float a = t, b = 0.0f;
+    if constexpr (STRIDE == 16)
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    else
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+
+// Eight sums over the 64 lanes at once (v[k] summed over lanes, k = 0..7).
+// Three pairwise exchanges inside each 8-lane block (half-row mirror, xor 1,
+// xor 2) each keep half of the values, so that afterwards lane b of a block
+// holds the block's sum of v[reduce8_slot(b)]; a row shift by 8 and the
+// permlane16/permlane32 swaps then add the eight blocks.  The result is valid
+// on lanes 8..15, lane l holding the total of v[reduce8_slot(l & 7)].  26 VALU operations instead of eight
+// separate wave sums; every lane must be active.
+__device__ __forceinline__ int reduce8_slot(int b) {
+    return 4 * ((b >> 2) & 1) + 2 * (b & 1) + ((b >> 1) & 1);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_all(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_reduce8(const float (&v)[8]) {
+    const int b = threadIdx.x & 7;
+    const bool p = (b >> 2) & 1, q = b & 1, r = (b >> 1) & 1;
+    float w[4], u[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // half-row mirror: b <-> 7 - b
+        const float keep = p ? v[j + 4] : v[j];
+        const float send = p ? v[j] : v[j + 4];
+        w[j] = keep + dpp_all<0x141>(send);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {  // quad_perm [1,0,3,2]: b <-> b ^ 1
+        const float keep = q ? w[j + 2] : w[j];
+        const float send = q ? w[j] : w[j + 2];
+        u[j] = keep + dpp_all<0xB1>(send);
+    }
+    const float keep = r ? u[1] : u[0];  // quad_perm [2,3,0,1]: b <-> b ^ 2
+    const float send = r ? u[0] : u[1];
+    float t = keep + dpp_all<0x4E>(send);
+    t += dpp_f32<0x118, 0xf, true>(t);  // row_shr:8: lanes 8..15 add lanes 0..7
+    t = row_pair_add<16>(t);  // rows 0+1 -> row 0, rows 2+3 -> row 2
+    return row_pair_add<32>(t);  // lanes 0..31 + lanes 32..63 -> lanes 0..31
+}
+
 __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off, kWave));

@@ -415,31 +415,26 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
             }
         }
         if (__ballot(contrib) == 0) continue;
-        // Per-primitive gradients: one DPP sum each, lane 63 adds.
-        vr = wave_sum_lane63(vr);
-        vg = wave_sum_lane63(vg);
-        vb = wave_sum_lane63(vb);
-        vop = wave_sum_lane63(vop);
-        vis2 = wave_sum_lane63(vis2);
-        if (MODE == 1) vsw = wave_sum_lane63(vsw);
-        if (want_contrib) {
-            cr = wave_sum_lane63(cr);
-            cg = wave_sum_lane63(cg);
-            cb = wave_sum_lane63(cb);
-        }
-        if (lane == kWave - 1) {
-            atomicAdd(v_colors + 3 * pid + 0, vr);
-            atomicAdd(v_colors + 3 * pid + 1, vg);
-            atomicAdd(v_colors + 3 * pid + 2, vb);
-            atomicAdd(v_opac + pid, vop);
-            atomicAdd(v_is2 + pid, vis2);
-            if (MODE == 1) atomicAdd(v_sw + pid, vsw);
-            if (contrib_rgb) {
-                atomicAdd(contrib_rgb + 3 * pid + 0, cr);
-                atomicAdd(contrib_rgb + 3 * pid + 1, cg);
-                atomicAdd(contrib_rgb + 3 * pid + 2, cb);
+        // Per-primitive gradients: one 8-way transposed reduction; lanes 8..15
+        // then hold the totals and each adds one of them.
+        const int slot = reduce8_slot(lane & 7);
+        const bool adder = (lane & ~7) == 8;
+        {
+            const float pv[8] = {vr, vg, vb, vop, vis2, MODE == 1 ? vsw : 0.0f, 0.0f, 0.0f};
+            const float t = wave_reduce8(pv);
+            if (adder && slot < (MODE == 1 ? 6 : 5)) {
+                float* dst = slot < 3 ? v_colors + 3 * pid + slot
+                           : slot == 3 ? v_opac + pid
+                           : slot == 4 ? v_is2 + pid
+                                       : v_sw + pid;
+                atomicAdd(dst, t);
             }
-            if (isect_contrib) atomicAdd(isect_contrib + g, cr + cg + cb);
+        }
+        if (want_contrib) {
+            const float cv[8] = {cr, cg, cb, cr + cg + cb, 0.0f, 0.0f, 0.0f, 0.0f};
+            const float t = wave_reduce8(cv);
+            if (adder && slot < 3 && contrib_rgb) atomicAdd(contrib_rgb + 3 * pid + slot, t);
+            if (adder && slot == 3 && isect_contrib) atomicAdd(isect_contrib + g, t);
         }
         // Geometry: endpoint gradients ((1-t) g, t g) of the best edge, folded
         // into its segment's control points.
@@ -468,12 +463,11 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
             const int s = __builtin_amdgcn_readlane(gseg, leader);
             const bool mine = gseg == s;
             pending &= ~__ballot(mine);
-            float* dst = v_cubics + 8 * (size_t)s;
+            float sv[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float t = wave_sum_lane63(mine ? cp[k] : 0.0f);
-                if (lane == kWave - 1) atomicAdd(dst + k, t);
-            }
+            for (int k = 0; k < 8; ++k) sv[k] = mine ? cp[k] : 0.0f;
+            const float t = wave_reduce8(sv);
+            if (adder) atomicAdd(v_cubics + 8 * (size_t)s + slot, t);
         }
     }
 }
