@@ -158,9 +158,11 @@ int cs_backward_finalize(const float* v_cubics_px, int32_t nseg, int32_t img_h, 
 
 /* ---------------- losses ---------------- */
 
-/* Number of float partials cs_mse_forward / cs_ssim needs in `partials`. */
+/* Number of float partials cs_mse_forward / cs_ssim needs in `partials`, and
+ * of floats in cs_ssim's `abc` maps ([3, nc, oh, ow rounded up to 4]). */
 size_t cs_mse_partials_elems(int64_t n);
 size_t cs_ssim_partials_elems(int32_t nc, int32_t h, int32_t w);
+size_t cs_ssim_abc_elems(int32_t nc, int32_t h, int32_t w, int32_t win);
 
 /* mse_partial_sum_kernel + reduce_sum_partial_kernel (ops/metric.py:18-163,
  * metric.py:102-131): *loss = sum((x-y)^2)/n (device scalar), two launches,
@@ -178,7 +180,8 @@ int cs_mse_backward(const float* x, const float* y, int64_t n, const float* grad
  * separable window `win1d` [win] (the 2D window is its outer product): *out =
  * mean over the valid SSIM map of every (image, channel), then over them.
  * If abc != null also stores, per map pixel, dS/dmu_x, dS/dE[x^2], dS/dE[xy]
- * ([3, nc, oh, ow]) for cs_ssim_backward.  x, y: [nc, h, w]. */
+ * (cs_ssim_abc_elems floats: [3, nc, oh, ow] with rows padded to a multiple of
+ * 4 floats) for cs_ssim_backward.  x, y: [nc, h, w]. */
 int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
             const float* win1d, int32_t win, float c1, float c2, float* partials, float* out,
             float* abc, hipStream_t stream);

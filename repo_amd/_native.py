@@ -53,6 +53,7 @@ _SIGNATURES = {
     "cs_backward_finalize": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P]),
     "cs_mse_partials_elems": (_SZ, [_I64]),
     "cs_ssim_partials_elems": (_SZ, [_I32, _I32, _I32]),
+    "cs_ssim_abc_elems": (_SZ, [_I32, _I32, _I32, _I32]),
     "cs_mse_forward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P]),
     "cs_mse_backward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
     "cs_ssim": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _F, _F, _P, _P, _P, _P]),

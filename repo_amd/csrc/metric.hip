@@ -7,12 +7,12 @@
 //
 // SSIM: valid-window SSIM of ops/metric.py:205-341 with the 2D Gaussian window
 // applied separably (the reference window is the outer product of one
-// normalized 1D Gaussian, metric.py:47-61).  A 32x32 output tile stages its
-// (32+win-1)^2 inputs in LDS; the horizontal pass gives each thread an 8-wide
-// strip (the 8+win-1 inputs are read once), the vertical pass a 4-tall strip
-// of the five moments (taken about a per-tile constant, see k_ssim_fwd).  The backward (absent from the reference) uses the
-// per-pixel partials A = dS/dmu_x, B = dS/dE[x^2], C = dS/dE[xy] and one
-// transposed separable correlation, blocked the same way.
+// normalized 1D Gaussian, metric.py:47-61): a horizontal pass over input rows
+// into LDS, then a vertical pass, blocked in register strips (see k_ssim_fwd).
+// Moments are taken about a per-tile constant.  The backward (absent from the
+// reference) uses the per-pixel partials A = dS/dmu_x, B = dS/dE[x^2],
+// C = dS/dE[xy] and one transposed separable correlation, blocked the same
+// way.
 #include "cs_common.h"
 #include "../../include/cubicsplat_hip.h"
 
@@ -111,32 +111,66 @@ __global__ __launch_bounds__(256) void k_mse_bwd(const float* __restrict__ x,
 
 // ------------------------------------------------------------------ SSIM
 
-constexpr int kSsimOT = 32;   // output tile edge
+// Output tile: 32 columns x 48 rows per 256-thread workgroup.  The horizontal
+// pass gives each thread a row and an 8-wide column strip (IT = 48 + win - 1
+// rows x 4 strips, 232 items for win 11) and reads its inputs straight from
+// global memory (through the vector cache, float4 where the strip is inside
+// the image); only the horizontal results live in LDS.  The vertical pass
+// gives each thread a column and a 6-tall row strip (32 x 8 items).
+constexpr int kSsimTW = 32;   // output tile width
+constexpr int kSsimTH = 48;   // output tile height
 constexpr int kHStrip = 8;    // horizontal-pass outputs per thread
-constexpr int kVStrip = 4;    // vertical-pass outputs per thread
+constexpr int kVStrip = 6;    // vertical-pass outputs per thread
+static_assert(kSsimTW * (kSsimTH / kVStrip) == 256, "vertical pass covers the tile");
 
 template <int WIN>
 struct SsimTile {
-    static constexpr int IT = kSsimOT + WIN - 1;  // staged input tile edge
-    static constexpr int ITP = IT + 1;             // padded LDS row
-    static constexpr int HP = kSsimOT + 1;         // padded horizontal-result row
+    static constexpr int IT = kSsimTH + WIN - 1;   // input rows per tile
+    static constexpr int HP = kSsimTW + 1;         // padded horizontal-result row
+    static constexpr int NIN = kHStrip + WIN - 1;  // inputs per horizontal strip
+    // The backward's strips start WIN-1 map columns before a multiple of 8.
+    static constexpr int BOFF = (4 - (WIN - 1) % 4) % 4;
 };
 
-// Loads a (IT x IT) tile starting at (y0, x0) of `src` (h x w) into LDS,
-// zero outside the image.  256 threads as 4 rows x 64 columns.
-template <int IT, int ITP>
-__device__ __forceinline__ void load_tile(const float* __restrict__ src, int h, int w, int y0,
-                                          int x0, float (*dst)[ITP]) {
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    for (int r = ty; r < IT; r += 4) {
-        const int gy = y0 + r;
-        const bool rin = gy >= 0 && gy < h;
-        for (int c = tx; c < IT; c += 64) {
-            const int gx = x0 + c;
-            dst[r][c] = (rin && gx >= 0 && gx < w) ? src[(size_t)gy * w + gx] : 0.0f;
+// Loads plane[gy][gx0 .. gx0 + N) of an image with h rows of w valid columns
+// stored with row stride ld (zero outside).  When rows are 16-byte aligned
+// (vec_ok), gx0 - OFF is a multiple of 4 and the rounded-up strip lies inside
+// the row, it uses float4 loads starting OFF columns early.
+template <int N, int OFF>
+__device__ __forceinline__ void load_strip(const float* __restrict__ plane, int h, int w,
+                                           size_t ld, int gy, int gx0, bool vec_ok,
+                                           float (&dst)[N]) {
+    constexpr int NV4 = (N + OFF + 3) / 4;
+    if (gy < 0 || gy >= h) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) dst[k] = 0.0f;
+        return;
+    }
+    const float* row = plane + (size_t)gy * ld;
+    const int s0 = gx0 - OFF;
+    if (vec_ok && s0 >= 0 && s0 + 4 * NV4 <= w) {
+        float t[4 * NV4];
+#pragma unroll
+        for (int v = 0; v < NV4; ++v) {
+            const float4 q = *reinterpret_cast<const float4*>(row + s0 + 4 * v);
+            t[4 * v] = q.x;
+            t[4 * v + 1] = q.y;
+            t[4 * v + 2] = q.z;
+            t[4 * v + 3] = q.w;
+        }
+#pragma unroll
+        for (int k = 0; k < N; ++k) dst[k] = t[OFF + k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int gx = gx0 + k;
+            dst[k] = (gx >= 0 && gx < w) ? row[gx] : 0.0f;
         }
     }
 }
+
+// Row stride of the per-pixel maps A, B, C (rows padded to 16 bytes).
+__host__ __device__ __forceinline__ int abc_ld(int ow) { return (ow + 3) & ~3; }
 
 template <int WIN>
 __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
@@ -145,44 +179,50 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
                                                  const float* __restrict__ win1d, float c1,
                                                  float c2, float* __restrict__ partials,
                                                  float* __restrict__ abc, int nc) {
-    constexpr int IT = SsimTile<WIN>::IT, ITP = SsimTile<WIN>::ITP, HP = SsimTile<WIN>::HP;
-    __shared__ float xs[IT][ITP];
-    __shared__ float ys[IT][ITP];
+    using TT = SsimTile<WIN>;
+    constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
     __shared__ float hm[5][IT][HP];
-    __shared__ float gw[WIN];
     __shared__ float sh[4];
     const int c = blockIdx.z;
-    const int ox0 = blockIdx.x * kSsimOT, oy0 = blockIdx.y * kSsimOT;
-    if (threadIdx.x < WIN) gw[threadIdx.x] = win1d[threadIdx.x];
-    load_tile<IT, ITP>(x + (size_t)c * h * w, h, w, oy0, ox0, xs);
-    load_tile<IT, ITP>(y + (size_t)c * h * w, h, w, oy0, ox0, ys);
-    __syncthreads();
-    // Moments are taken of x - kx and y - ky, with kx, ky one staged value per
+    const int ox0 = blockIdx.x * kSsimTW, oy0 = blockIdx.y * kSsimTH;
+    const float* xc = x + (size_t)c * h * w;
+    const float* yc = y + (size_t)c * h * w;
+    float g[WIN];
+#pragma unroll
+    for (int k = 0; k < WIN; ++k) g[k] = win1d[k];
+    // Moments are taken of x - kx and y - ky, with kx, ky one input value per
     // workgroup: sigma^2 = E[(x-k)^2] - (mu-k)^2 holds for any constant k and
     // avoids the cancellation of E[x^2] - mu^2 in flat regions (where it
     // would leave fp32 noise of order 1e-7 against c2 = 9e-4).
-    const float kx = xs[IT / 2][IT / 2], ky = ys[IT / 2][IT / 2];
-    // Horizontal: thread -> (row, 8-wide strip); IT rows x 4 strips.
-    for (int item = threadIdx.x; item < IT * (kSsimOT / kHStrip); item += 256) {
+    const size_t kpix = (size_t)min(oy0 + kSsimTH / 2, h - 1) * w + min(ox0 + kSsimTW / 2, w - 1);
+    const float kx = xc[kpix], ky = yc[kpix];
+    const bool vec_ok = ((w & 3) == 0) &&
+                        ((reinterpret_cast<uintptr_t>(xc) | reinterpret_cast<uintptr_t>(yc)) & 15) == 0;
+    // Horizontal: thread -> (row, 8-wide strip).
+    for (int item = threadIdx.x; item < IT * (kSsimTW / kHStrip); item += 256) {
         const int r = item >> 2, q0 = (item & 3) * kHStrip;
-        float a[kHStrip + WIN - 1], b[kHStrip + WIN - 1];
+        float a[NIN], b[NIN];
+        load_strip<NIN, 0>(xc, h, w, w, oy0 + r, ox0 + q0, vec_ok, a);
+        load_strip<NIN, 0>(yc, h, w, w, oy0 + r, ox0 + q0, vec_ok, b);
+        float aa[NIN], bb[NIN], ab[NIN];
 #pragma unroll
-        for (int k = 0; k < kHStrip + WIN - 1; ++k) {
-            a[k] = xs[r][q0 + k] - kx;
-            b[k] = ys[r][q0 + k] - ky;
+        for (int k = 0; k < NIN; ++k) {
+            a[k] -= kx;
+            b[k] -= ky;
+            aa[k] = a[k] * a[k];
+            bb[k] = b[k] * b[k];
+            ab[k] = a[k] * b[k];
         }
 #pragma unroll
         for (int o = 0; o < kHStrip; ++o) {
             float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f, m4 = 0.f;
 #pragma unroll
             for (int k = 0; k < WIN; ++k) {
-                const float g = gw[k];
-                const float av = a[o + k], bv = b[o + k];
-                m0 = __builtin_fmaf(g, av, m0);
-                m1 = __builtin_fmaf(g, bv, m1);
-                m2 = __builtin_fmaf(g, av * av, m2);
-                m3 = __builtin_fmaf(g, bv * bv, m3);
-                m4 = __builtin_fmaf(g, av * bv, m4);
+                m0 = __builtin_fmaf(g[k], a[o + k], m0);
+                m1 = __builtin_fmaf(g[k], b[o + k], m1);
+                m2 = __builtin_fmaf(g[k], aa[o + k], m2);
+                m3 = __builtin_fmaf(g[k], bb[o + k], m3);
+                m4 = __builtin_fmaf(g[k], ab[o + k], m4);
             }
             hm[0][r][q0 + o] = m0;
             hm[1][r][q0 + o] = m1;
@@ -192,8 +232,8 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
         }
     }
     __syncthreads();
-    // Vertical: thread -> (column, 4-tall strip); 32 columns x 8 strips.
-    const int q = threadIdx.x & 31, r0 = (threadIdx.x >> 5) * kVStrip;
+    // Vertical: thread -> (column, 6-tall strip).
+    const int q = threadIdx.x & (kSsimTW - 1), r0 = (threadIdx.x / kSsimTW) * kVStrip;
     float mom[5][kVStrip];
 #pragma unroll
     for (int m = 0; m < 5; ++m)
@@ -208,14 +248,14 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
         for (int o = 0; o < kVStrip; ++o) {
             const int t = k - o;
             if (t >= 0 && t < WIN) {
-                const float g = gw[t];
 #pragma unroll
-                for (int m = 0; m < 5; ++m) mom[m][o] = __builtin_fmaf(g, v[m], mom[m][o]);
+                for (int m = 0; m < 5; ++m) mom[m][o] = __builtin_fmaf(g[t], v[m], mom[m][o]);
             }
         }
     }
     float acc = 0.0f;
-    const size_t plane = (size_t)oh * ow;
+    const size_t ld = abc_ld(ow);
+    const size_t plane = (size_t)oh * ld;
     const size_t stride = (size_t)nc * plane;
     const int ox = ox0 + q;
 #pragma unroll
@@ -234,7 +274,7 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
         if (abc) {
             const float dl = 2.0f * (mu2 - l * mu1) / d1;
             const float dcs = 2.0f * (mu1 * cs_ - mu2) / d2;
-            const size_t oi = (size_t)c * plane + (size_t)oy * ow + ox;
+            const size_t oi = (size_t)c * plane + (size_t)oy * ld + ox;
             abc[oi] = cs_ * dl + l * dcs;
             abc[stride + oi] = -l * cs_ / d2;
             abc[2 * stride + oi] = 2.0f * l / d2;
@@ -245,6 +285,10 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
         partials[(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x] = bs;
 }
 
+// grad_x[p] = scale * sum over map pixels o of the window w(p - o) times
+// (A[o] + 2 x[p] B[o] + y[p] C[o]): a full (transposed) correlation of the
+// three maps, blocked like the forward (horizontal strips read the maps from
+// global memory, vertical strips from LDS).
 template <int WIN>
 __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
                                                  const float* __restrict__ y, int h, int w,
@@ -253,39 +297,39 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
                                                  const float* __restrict__ abc,
                                                  const float* __restrict__ grad_out, float inv_cnt,
                                                  int nc, float* __restrict__ gx) {
-    constexpr int IT = SsimTile<WIN>::IT, ITP = SsimTile<WIN>::ITP, HP = SsimTile<WIN>::HP;
-    __shared__ float as[3][IT][ITP];
+    using TT = SsimTile<WIN>;
+    constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
     __shared__ float hs[3][IT][HP];
-    __shared__ float gw[WIN];
     const int c = blockIdx.z;
-    const int px0 = blockIdx.x * kSsimOT, py0 = blockIdx.y * kSsimOT;
-    const size_t plane = (size_t)oh * ow;
+    const int px0 = blockIdx.x * kSsimTW, py0 = blockIdx.y * kSsimTH;
+    const size_t ld = abc_ld(ow);
+    const size_t plane = (size_t)oh * ld;
     const size_t stride = (size_t)nc * plane;
-    if (threadIdx.x < WIN) gw[threadIdx.x] = win1d[threadIdx.x];
-    // Map pixels o in [p - (WIN-1), p] of A, B, C.
-    for (int m = 0; m < 3; ++m)
-        load_tile<IT, ITP>(abc + m * stride + (size_t)c * plane, oh, ow, py0 - (WIN - 1),
-                           px0 - (WIN - 1), as[m]);
-    __syncthreads();
-    // Horizontal full correlation: hs[r][q] = sum_k g[k] as[r][q + WIN-1-k].
-    for (int item = threadIdx.x; item < IT * (kSsimOT / kHStrip); item += 256) {
+    float g[WIN];
+#pragma unroll
+    for (int k = 0; k < WIN; ++k) g[k] = win1d[k];
+    const bool vec_ok = (reinterpret_cast<uintptr_t>(abc) & 15) == 0;
+    // Horizontal full correlation over map columns px0 - (WIN-1) + [0, 32 + WIN - 1):
+    // hs[r][q] = sum_k g[k] M[r][q + WIN-1-k], map rows py0 - (WIN-1) + r.
+    for (int item = threadIdx.x; item < IT * (kSsimTW / kHStrip); item += 256) {
         const int r = item >> 2, q0 = (item & 3) * kHStrip;
+        const int my = py0 - (WIN - 1) + r, mx0 = px0 - (WIN - 1) + q0;
 #pragma unroll
         for (int m = 0; m < 3; ++m) {
-            float a[kHStrip + WIN - 1];
-#pragma unroll
-            for (int k = 0; k < kHStrip + WIN - 1; ++k) a[k] = as[m][r][q0 + k];
+            float a[NIN];
+            load_strip<NIN, TT::BOFF>(abc + m * stride + (size_t)c * plane, oh, ow, ld, my, mx0,
+                                      vec_ok, a);
 #pragma unroll
             for (int o = 0; o < kHStrip; ++o) {
                 float s = 0.0f;
 #pragma unroll
-                for (int k = 0; k < WIN; ++k) s = __builtin_fmaf(gw[k], a[o + WIN - 1 - k], s);
+                for (int k = 0; k < WIN; ++k) s = __builtin_fmaf(g[k], a[o + WIN - 1 - k], s);
                 hs[m][r][q0 + o] = s;
             }
         }
     }
     __syncthreads();
-    const int q = threadIdx.x & 31, r0 = (threadIdx.x >> 5) * kVStrip;
+    const int q = threadIdx.x & (kSsimTW - 1), r0 = (threadIdx.x / kSsimTW) * kVStrip;
     float gsum[3][kVStrip];
 #pragma unroll
     for (int m = 0; m < 3; ++m)
@@ -300,9 +344,8 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
         for (int o = 0; o < kVStrip; ++o) {
             const int t = o + WIN - 1 - k;
             if (t >= 0 && t < WIN) {
-                const float g = gw[t];
 #pragma unroll
-                for (int m = 0; m < 3; ++m) gsum[m][o] = __builtin_fmaf(g, v[m], gsum[m][o]);
+                for (int m = 0; m < 3; ++m) gsum[m][o] = __builtin_fmaf(g[t], v[m], gsum[m][o]);
             }
         }
     }
@@ -355,7 +398,13 @@ extern "C" int cs_mse_backward(const float* x, const float* y, int64_t n, const 
 
 extern "C" size_t cs_ssim_partials_elems(int32_t nc, int32_t h, int32_t w) {
     const int64_t oh = h, ow = w;  // upper bound for any window
-    return (size_t)(((ow + kSsimOT - 1) / kSsimOT) * ((oh + kSsimOT - 1) / kSsimOT) * nc);
+    return (size_t)(((ow + kSsimTW - 1) / kSsimTW) * ((oh + kSsimTH - 1) / kSsimTH) * nc);
+}
+
+extern "C" size_t cs_ssim_abc_elems(int32_t nc, int32_t h, int32_t w, int32_t win) {
+    if (nc <= 0 || win <= 0 || h < win || w < win) return 0;
+    const int64_t oh = h - win + 1, ow = w - win + 1;
+    return (size_t)(3 * (int64_t)nc * oh * abc_ld((int)ow));
 }
 
 #define CS_SSIM_DISPATCH(WIN_, CALL) \
@@ -367,7 +416,7 @@ extern "C" int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, in
     if (nc <= 0 || win <= 0 || (win & 1) == 0 || win > 15 || h < win || w < win)
         return CS_ERR_ARGS;
     const int oh = h - win + 1, ow = w - win + 1;
-    const dim3 grid((ow + kSsimOT - 1) / kSsimOT, (oh + kSsimOT - 1) / kSsimOT, nc);
+    const dim3 grid((ow + kSsimTW - 1) / kSsimTW, (oh + kSsimTH - 1) / kSsimTH, nc);
 #define CS_SSIM_FWD(W_)                                                                       \
     hipLaunchKernelGGL(k_ssim_fwd<W_>, grid, dim3(256), 0, stream, x, y, h, w, oh, ow, win1d, \
                        c1, c2, partials, abc, nc)
@@ -396,7 +445,7 @@ extern "C" int cs_ssim_backward(const float* x, const float* y, int32_t nc, int3
         return CS_ERR_ARGS;
     const int oh = h - win + 1, ow = w - win + 1;
     const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
-    const dim3 grid((w + kSsimOT - 1) / kSsimOT, (h + kSsimOT - 1) / kSsimOT, nc);
+    const dim3 grid((w + kSsimTW - 1) / kSsimTW, (h + kSsimTH - 1) / kSsimTH, nc);
 #define CS_SSIM_BWD(W_)                                                                     \
     hipLaunchKernelGGL(k_ssim_bwd<W_>, grid, dim3(256), 0, stream, x, y, h, w, oh, ow, win1d, \
                        abc, grad_out, inv_cnt, nc, grad_x)

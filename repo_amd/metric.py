@@ -127,8 +127,9 @@ def _ssim_forward(x32, y32, win_size, win_sigma, c1, c2, want_grad):
     partials = torch.empty((int(N.lib().cs_ssim_partials_elems(n * c, h, w)),),
                            dtype=torch.float32, device=dev)
     out = torch.empty((), dtype=torch.float32, device=dev)
-    oh, ow = h - win_size + 1, w - win_size + 1
-    abc = (torch.empty((3, n * c, oh, ow), dtype=torch.float32, device=dev)
+    # Per-pixel partials for the backward, [3, n*c, oh, ow rounded up to 4].
+    abc = (torch.empty((int(N.lib().cs_ssim_abc_elems(n * c, h, w, int(win_size))),),
+                       dtype=torch.float32, device=dev)
            if want_grad else None)
     with N.prof("loss.ssim_fwd"):
         N.call("cs_ssim", N.ptr(x32), N.ptr(y32), n * c, h, w, N.ptr(g), int(win_size),
