@@ -69,9 +69,12 @@ def render(sc, cub, col):
 
 
 def loss_fn(img, target):
-    import manbo
-    x = img.clamp(0, 1).permute(2, 0, 1).unsqueeze(0).contiguous()
-    return manbo.mse_loss_tilelang(x, target) + SSIM_WEIGHT * (1.0 - manbo.ssim(x, target))
+    """clamp(0, 1) -> NCHW -> MSE + 0.2 (1 - SSIM), with the fused kernels
+    (the same values as manbo.mse_loss_tilelang + manbo.ssim on
+    img.clamp(0, 1).permute(2, 0, 1).unsqueeze(0))."""
+    from repo_amd import fused
+    loss, _ = fused.mse_ssim_loss(fused.clamp_to_nchw(img), target, SSIM_WEIGHT)
+    return loss
 
 
 def train_step(sc, cub, col, opt):
@@ -127,6 +130,11 @@ def stage_times(sc, cub, col, iters):
     timed("ssim_fwd_grad_ms", lambda: metric._ssim_forward(x, tgt, 11, 1.5, 1e-4, 9e-4, True))
     s = metric._SSIMFn.apply(xr, tgt, 11, 1.5, 1e-4, 9e-4)
     timed("ssim_bwd_ms", lambda: torch.autograd.grad(s, xr, retain_graph=True))
+    from repo_amd import fused
+    timed("glue_clamp_nchw_ms", lambda: fused.clamp_to_nchw(out))
+    timed("loss_fused_fwd_ms", lambda: fused.mse_ssim_loss(xr, tgt, SSIM_WEIGHT))
+    lf, _ = fused.mse_ssim_loss(xr, tgt, SSIM_WEIGHT)
+    timed("loss_fused_bwd_ms", lambda: torch.autograd.grad(lf, xr, retain_graph=True))
     res["num_intersects"] = b.num_intersects
     res["_binned"] = b
     res["_T"] = T

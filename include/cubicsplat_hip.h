@@ -193,6 +193,31 @@ int cs_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int3
                      const float* win1d, int32_t win, const float* abc, const float* grad_out,
                      float* grad_x, hipStream_t stream);
 
+/* ---------------- fused training-step operations ---------------- */
+
+/* The caller's glue between the render and the losses,
+ * gaussian_trace/render.py:1309-1310: out [3, h, w] = clamp(img, lo, hi)
+ * permuted from img [h, w, 3]; and its gradient, grad_img [h, w, 3] =
+ * grad [3, h, w] where lo <= img <= hi, else 0 (torch's clamp gradient). */
+int cs_clamp_hwc_to_nchw(const float* img, int32_t h, int32_t w, float lo, float hi, float* out,
+                         hipStream_t stream);
+int cs_clamp_hwc_to_nchw_backward(const float* img, const float* grad, int32_t h, int32_t w,
+                                  float lo, float hi, float* grad_img, hipStream_t stream);
+
+/* loss = MSE(x, y) + ssim_weight * (1 - SSIM(x, y)) in one call (the MSE of
+ * metric.py:102-212 and the SSIM of metric.py:215-273 as cs_mse_forward and
+ * cs_ssim compute them): out[0] = loss, out[1] = MSE, out[2] = SSIM (device);
+ * `partials` holds cs_mse_ssim_partials_elems floats; abc as for cs_ssim.
+ * The backward writes grad_x = g (2 (x - y) / n - ssim_weight dSSIM/dx) in one
+ * pass, g = *grad_loss. */
+size_t cs_mse_ssim_partials_elems(int32_t nc, int32_t h, int32_t w);
+int cs_mse_ssim_loss(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+                     const float* win1d, int32_t win, float c1, float c2, float ssim_weight,
+                     float* partials, float* out, float* abc, hipStream_t stream);
+int cs_mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+                         const float* win1d, int32_t win, const float* abc, float ssim_weight,
+                         const float* grad_loss, float* grad_x, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

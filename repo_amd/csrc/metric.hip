@@ -295,8 +295,8 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
                                                  int oh, int ow,
                                                  const float* __restrict__ win1d,
                                                  const float* __restrict__ abc,
-                                                 const float* __restrict__ grad_out, float inv_cnt,
-                                                 int nc, float* __restrict__ gx) {
+                                                 const float* __restrict__ grad_out, float ssim_coef,
+                                                 float mse_coef, int nc, float* __restrict__ gx) {
     using TT = SsimTile<WIN>;
     constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
     __shared__ float hs[3][IT][HP];
@@ -349,7 +349,10 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
             }
         }
     }
-    const float scale = (*grad_out) * inv_cnt;
+    // grad = g * ssim_coef * (SSIM-mean term) [+ g * mse_coef * (x - y) when
+    // the MSE gradient is fused in].
+    const float go = *grad_out;
+    const float scale = go * ssim_coef, mscale = go * mse_coef;
     const float* xc = x + (size_t)c * h * w;
     const float* yc = y + (size_t)c * h * w;
     float* gc = gx + (size_t)c * h * w;
@@ -359,7 +362,58 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
         const int py = py0 + r0 + o;
         if (py >= h || px >= w) continue;
         const size_t pi = (size_t)py * w + px;
-        gc[pi] = scale * (gsum[0][o] + 2.0f * xc[pi] * gsum[1][o] + yc[pi] * gsum[2][o]);
+        const float xv = xc[pi], yv = yc[pi];
+        float gv = scale * (gsum[0][o] + 2.0f * xv * gsum[1][o] + yv * gsum[2][o]);
+        if (mse_coef != 0.0f) gv = __builtin_fmaf(mscale, xv - yv, gv);
+        gc[pi] = gv;
+    }
+}
+
+// loss = mse_sum * inv_n + w * (1 - ssim_sum * inv_m); out[1] = MSE, out[2] =
+// SSIM.  One workgroup, fixed summation order.
+__global__ __launch_bounds__(kFinalThreads) void k_mse_ssim_combine(
+    const float* __restrict__ mse_partials, int n_mse, const float* __restrict__ ssim_partials,
+    int n_ssim, float inv_n, float inv_m, float weight, float* __restrict__ out) {
+    __shared__ float sh[kFinalThreads / kWave];
+    float a = 0.0f, b = 0.0f;
+    for (int i = threadIdx.x; i < n_mse; i += kFinalThreads) a += mse_partials[i];
+    for (int i = threadIdx.x; i < n_ssim; i += kFinalThreads) b += ssim_partials[i];
+    const float ta = block_sum(a, sh);
+    const float tb = block_sum(b, sh);
+    if (threadIdx.x == 0) {
+        const float mse = ta * inv_n, ss = tb * inv_m;
+        out[0] = mse + weight * (1.0f - ss);
+        out[1] = mse;
+        out[2] = ss;
+    }
+}
+
+// out[c][i][j] = clamp(img[i][j][c], lo, hi) for an [h, w, 3] image (the
+// caller's clamp(0, 1).permute(2, 0, 1) glue, gaussian_trace/render.py:1309-1310).
+__global__ __launch_bounds__(256) void k_clamp_hwc_to_chw(const float* __restrict__ img, int64_t hw,
+                                                         float lo, float hi,
+                                                         float* __restrict__ out) {
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= hw) return;
+    const float r = img[3 * p], g = img[3 * p + 1], b = img[3 * p + 2];
+    out[p] = fminf(fmaxf(r, lo), hi);
+    out[hw + p] = fminf(fmaxf(g, lo), hi);
+    out[2 * hw + p] = fminf(fmaxf(b, lo), hi);
+}
+
+// grad_img[i][j][c] = grad[c][i][j] where lo <= img <= hi, else 0 (the
+// gradient of clamp as torch defines it).
+__global__ __launch_bounds__(256) void k_clamp_hwc_to_chw_bwd(const float* __restrict__ img,
+                                                             const float* __restrict__ grad,
+                                                             int64_t hw, float lo, float hi,
+                                                             float* __restrict__ grad_img) {
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= hw) return;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const float v = img[3 * p + c];
+        const bool pass = (v >= lo) & (v <= hi);
+        grad_img[3 * p + c] = pass ? grad[c * hw + p] : 0.0f;
     }
 }
 
@@ -410,11 +464,14 @@ extern "C" size_t cs_ssim_abc_elems(int32_t nc, int32_t h, int32_t w, int32_t wi
 #define CS_SSIM_DISPATCH(WIN_, CALL) \
     case WIN_: CALL(WIN_); break;
 
-extern "C" int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
-                       const float* win1d, int32_t win, float c1, float c2, float* partials,
-                       float* out, float* abc, hipStream_t stream) {
-    if (nc <= 0 || win <= 0 || (win & 1) == 0 || win > 15 || h < win || w < win)
-        return CS_ERR_ARGS;
+static bool ssim_args_ok(int32_t nc, int32_t h, int32_t w, int32_t win) {
+    return nc > 0 && win > 0 && (win & 1) == 1 && win <= 15 && h >= win && w >= win;
+}
+
+// SSIM partial sums (one per output tile) and, when abc != null, the maps.
+static int launch_ssim_fwd(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+                           const float* win1d, int32_t win, float c1, float c2,
+                           float* partials, float* abc, hipStream_t stream, int* nblk) {
     const int oh = h - win + 1, ow = w - win + 1;
     const dim3 grid((ow + kSsimTW - 1) / kSsimTW, (oh + kSsimTH - 1) / kSsimTH, nc);
 #define CS_SSIM_FWD(W_)                                                                       \
@@ -432,23 +489,19 @@ extern "C" int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, in
         default: return CS_ERR_ARGS;
     }
 #undef CS_SSIM_FWD
-    const int nblk = (int)(grid.x * grid.y * grid.z);
-    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials, nblk,
-                       1.0f / ((float)nc * (float)oh * (float)ow), out);
-    return metric_status();
+    *nblk = (int)(grid.x * grid.y * grid.z);
+    return CS_OK;
 }
 
-extern "C" int cs_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
-                                const float* win1d, int32_t win, const float* abc,
-                                const float* grad_out, float* grad_x, hipStream_t stream) {
-    if (nc <= 0 || win <= 0 || (win & 1) == 0 || win > 15 || h < win || w < win)
-        return CS_ERR_ARGS;
+static int launch_ssim_bwd(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+                           const float* win1d, int32_t win, const float* abc,
+                           const float* grad_out, float ssim_coef, float mse_coef, float* grad_x,
+                           hipStream_t stream) {
     const int oh = h - win + 1, ow = w - win + 1;
-    const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
     const dim3 grid((w + kSsimTW - 1) / kSsimTW, (h + kSsimTH - 1) / kSsimTH, nc);
 #define CS_SSIM_BWD(W_)                                                                     \
     hipLaunchKernelGGL(k_ssim_bwd<W_>, grid, dim3(256), 0, stream, x, y, h, w, oh, ow, win1d, \
-                       abc, grad_out, inv_cnt, nc, grad_x)
+                       abc, grad_out, ssim_coef, mse_coef, nc, grad_x)
     switch (win) {
         CS_SSIM_DISPATCH(1, CS_SSIM_BWD)
         CS_SSIM_DISPATCH(3, CS_SSIM_BWD)
@@ -461,5 +514,89 @@ extern "C" int cs_ssim_backward(const float* x, const float* y, int32_t nc, int3
         default: return CS_ERR_ARGS;
     }
 #undef CS_SSIM_BWD
+    return CS_OK;
+}
+
+extern "C" int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+                       const float* win1d, int32_t win, float c1, float c2, float* partials,
+                       float* out, float* abc, hipStream_t stream) {
+    if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
+    int nblk = 0;
+    const int rc = launch_ssim_fwd(x, y, nc, h, w, win1d, win, c1, c2, partials, abc, stream,
+                                   &nblk);
+    if (rc) return rc;
+    const int oh = h - win + 1, ow = w - win + 1;
+    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials, nblk,
+                       1.0f / ((float)nc * (float)oh * (float)ow), out);
+    return metric_status();
+}
+
+extern "C" int cs_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+                                const float* win1d, int32_t win, const float* abc,
+                                const float* grad_out, float* grad_x, hipStream_t stream) {
+    if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
+    const int oh = h - win + 1, ow = w - win + 1;
+    const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
+    const int rc = launch_ssim_bwd(x, y, nc, h, w, win1d, win, abc, grad_out, inv_cnt, 0.0f,
+                                   grad_x, stream);
+    return rc ? rc : metric_status();
+}
+
+extern "C" size_t cs_mse_ssim_partials_elems(int32_t nc, int32_t h, int32_t w) {
+    return cs_mse_partials_elems((int64_t)nc * h * w) + cs_ssim_partials_elems(nc, h, w);
+}
+
+extern "C" int cs_mse_ssim_loss(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+                                const float* win1d, int32_t win, float c1, float c2,
+                                float ssim_weight, float* partials, float* out, float* abc,
+                                hipStream_t stream) {
+    if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
+    const int64_t n = (int64_t)nc * h * w;
+    const int64_t nb = (n + kMseChunk - 1) / kMseChunk;
+    if (nb > 0x7fffffff) return CS_ERR_ARGS;
+    float* mse_partials = partials;
+    float* ssim_partials = partials + cs_mse_partials_elems(n);
+    hipLaunchKernelGGL(k_mse_partial, dim3((unsigned)nb), dim3(kMseThreads), 0, stream, x, y, n,
+                       mse_partials);
+    int nblk = 0;
+    const int rc = launch_ssim_fwd(x, y, nc, h, w, win1d, win, c1, c2, ssim_partials, abc,
+                                   stream, &nblk);
+    if (rc) return rc;
+    const int oh = h - win + 1, ow = w - win + 1;
+    hipLaunchKernelGGL(k_mse_ssim_combine, dim3(1), dim3(kFinalThreads), 0, stream, mse_partials,
+                       (int)nb, ssim_partials, nblk, 1.0f / (float)n,
+                       1.0f / ((float)nc * (float)oh * (float)ow), ssim_weight, out);
+    return metric_status();
+}
+
+extern "C" int cs_mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h,
+                                    int32_t w, const float* win1d, int32_t win, const float* abc,
+                                    float ssim_weight, const float* grad_loss, float* grad_x,
+                                    hipStream_t stream) {
+    if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
+    const int oh = h - win + 1, ow = w - win + 1;
+    const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
+    const float mse_coef = (float)(2.0 / ((double)nc * h * w));
+    const int rc = launch_ssim_bwd(x, y, nc, h, w, win1d, win, abc, grad_loss,
+                                   -ssim_weight * inv_cnt, mse_coef, grad_x, stream);
+    return rc ? rc : metric_status();
+}
+
+extern "C" int cs_clamp_hwc_to_nchw(const float* img, int32_t h, int32_t w, float lo, float hi,
+                                    float* out, hipStream_t stream) {
+    if (h <= 0 || w <= 0) return CS_ERR_ARGS;
+    const int64_t hw = (int64_t)h * w;
+    hipLaunchKernelGGL(k_clamp_hwc_to_chw, dim3((unsigned)((hw + 255) / 256)), dim3(256), 0,
+                       stream, img, hw, lo, hi, out);
+    return metric_status();
+}
+
+extern "C" int cs_clamp_hwc_to_nchw_backward(const float* img, const float* grad, int32_t h,
+                                             int32_t w, float lo, float hi, float* grad_img,
+                                             hipStream_t stream) {
+    if (h <= 0 || w <= 0) return CS_ERR_ARGS;
+    const int64_t hw = (int64_t)h * w;
+    hipLaunchKernelGGL(k_clamp_hwc_to_chw_bwd, dim3((unsigned)((hw + 255) / 256)), dim3(256), 0,
+                       stream, img, grad, hw, lo, hi, grad_img);
     return metric_status();
 }

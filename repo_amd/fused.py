@@ -1,0 +1,115 @@
+"""Fused operations for the training step around the renderer.
+
+The reference's training code turns the rendered [H, W, 3] image into the
+loss input with ``img.clamp(0, 1).permute(2, 0, 1).unsqueeze(0)``
+(gaussian_trace/render.py:1309-1310) and, in this build's benchmark step,
+combines ``mse_loss_tilelang`` (metric.py:198-212) with ``ssim``
+(metric.py:215-273) as ``MSE + w * (1 - SSIM)``.  Done with torch and the
+separate loss calls, that is several full passes over 33 MB images per step
+(clamp, permute copy, their backward, the two loss gradients and their sum);
+here each direction is one kernel:
+
+* ``clamp_to_nchw(img)``: one pass forward, one masked pass backward;
+* ``mse_ssim_loss(x, y, w)``: one call for both losses (MSE partial sums,
+  SSIM tiles, one combining workgroup) and one backward kernel that writes
+  ``g * (2 (x - y) / n - w dSSIM/dx)``.
+
+Values equal the separate calls (same kernels and summation structure); the
+autograd graph is shorter.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+from .metric import _as_f32, _validate_pair_4d, gaussian_window_1d
+
+
+class _ClampToNCHW(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, img, lo, hi):
+        N.require_gpu(img, "img")
+        if img.dim() != 3 or img.shape[2] != 3:
+            raise ValueError(f"img must be [H, W, 3], got {tuple(img.shape)}")
+        x = _as_f32(img, "img")
+        h, w = int(x.shape[0]), int(x.shape[1])
+        out = torch.empty((1, 3, h, w), dtype=torch.float32, device=x.device)
+        with N.prof("glue.clamp_nchw"):
+            N.call("cs_clamp_hwc_to_nchw", N.ptr(x), h, w, float(lo), float(hi), N.ptr(out),
+                   N.stream(x.device))
+        ctx.save_for_backward(x)
+        ctx.lo, ctx.hi = float(lo), float(hi)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        (x,) = ctx.saved_tensors
+        h, w = int(x.shape[0]), int(x.shape[1])
+        g = grad.detach().to(torch.float32).contiguous()
+        gi = torch.empty_like(x)
+        with N.prof("glue.clamp_nchw_bwd"):
+            N.call("cs_clamp_hwc_to_nchw_backward", N.ptr(x), N.ptr(g), h, w, ctx.lo, ctx.hi,
+                   N.ptr(gi), N.stream(x.device))
+        return gi, None, None
+
+
+def clamp_to_nchw(img: torch.Tensor, lo: float = 0.0, hi: float = 1.0) -> torch.Tensor:
+    """``img.clamp(lo, hi).permute(2, 0, 1).unsqueeze(0)`` as one kernel (and
+    one for its gradient); returns a contiguous [1, 3, H, W] tensor."""
+    return _ClampToNCHW.apply(img, lo, hi)
+
+
+class _MseSsimLoss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, y, ssim_weight, win_size, win_sigma, c1, c2):
+        _validate_pair_4d(x, y)
+        x32 = _as_f32(x, "x")
+        y32 = _as_f32(y, "y")
+        n, c, h, w = x32.shape
+        dev = x32.device
+        g = gaussian_window_1d(win_size, win_sigma, dev)
+        partials = torch.empty((int(N.lib().cs_mse_ssim_partials_elems(n * c, h, w)),),
+                               dtype=torch.float32, device=dev)
+        out = torch.empty((3,), dtype=torch.float32, device=dev)
+        abc = (torch.empty((int(N.lib().cs_ssim_abc_elems(n * c, h, w, int(win_size))),),
+                           dtype=torch.float32, device=dev)
+               if ctx.needs_input_grad[0] else None)
+        with N.prof("loss.mse_ssim"):
+            N.call("cs_mse_ssim_loss", N.ptr(x32), N.ptr(y32), n * c, h, w, N.ptr(g),
+                   int(win_size), float(c1), float(c2), float(ssim_weight), N.ptr(partials),
+                   N.ptr(out), N.ptr(abc), N.stream(dev))
+        ctx.save_for_backward(x32, y32, abc if abc is not None else torch.empty(0), g)
+        ctx.win_size = int(win_size)
+        ctx.ssim_weight = float(ssim_weight)
+        ctx.x_dtype = x.dtype
+        parts = out[1:]
+        ctx.mark_non_differentiable(parts)
+        return out[0], parts
+
+    @staticmethod
+    def backward(ctx, grad_loss, _grad_parts):
+        x, y, abc, g = ctx.saved_tensors
+        if not ctx.needs_input_grad[0]:
+            return (None,) * 7
+        n, c, h, w = x.shape
+        gx = torch.empty_like(x)
+        go = grad_loss.detach().to(torch.float32).contiguous()
+        with N.prof("loss.mse_ssim_bwd"):
+            N.call("cs_mse_ssim_backward", N.ptr(x), N.ptr(y), n * c, h, w, N.ptr(g),
+                   ctx.win_size, N.ptr(abc), ctx.ssim_weight, N.ptr(go), N.ptr(gx),
+                   N.stream(x.device))
+        return gx.to(ctx.x_dtype), None, None, None, None, None, None
+
+
+def mse_ssim_loss(x, y, ssim_weight: float = 0.2, *, win_size: int = 11, win_sigma: float = 1.5,
+                  data_range: float = 1.0, k1: float = 0.01, k2: float = 0.03):
+    """``mse_loss_tilelang(x, y) + ssim_weight * (1 - ssim(x, y))`` in one call.
+    Returns (loss, parts) with parts = [MSE, SSIM] (device, no gradient);
+    only ``loss`` is differentiable (w.r.t. x)."""
+    if win_size <= 0 or win_size % 2 == 0:
+        raise ValueError("win_size must be odd")
+    if data_range <= 0.0:
+        raise ValueError("data_range must be > 0")
+    c1 = (k1 * data_range) ** 2
+    c2 = (k2 * data_range) ** 2
+    return _MseSsimLoss.apply(x, y, float(ssim_weight), int(win_size), float(win_sigma), c1, c2)

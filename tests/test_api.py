@@ -216,3 +216,14 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stdout
+
+
+def test_fused_ops_argument_errors():
+    from repo_amd import fused
+    x = torch.rand(1, 3, 16, 16)
+    with pytest.raises(ValueError, match="CUDA"):
+        fused.clamp_to_nchw(torch.rand(8, 8, 3))
+    with pytest.raises(ValueError):
+        fused.mse_ssim_loss(x, torch.rand(1, 3, 16, 15))
+    with pytest.raises(ValueError):
+        fused.mse_ssim_loss(x, x, win_size=4)

@@ -1,0 +1,88 @@
+"""Fused training-step operations (repo_amd.fused) against the separate
+reference-API calls and the float64 oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+
+def _img(h, w, seed):
+    g = torch.Generator().manual_seed(seed)
+    img = torch.rand((h, w, 3), generator=g) * 1.4 - 0.2  # values below 0 and above 1
+    img[0, :4] = torch.tensor([0.0, 1.0, 0.0])  # exactly on the clamp bounds
+    return img
+
+
+@pytest.mark.gpu
+def test_clamp_to_nchw_matches_torch():
+    from repo_amd import fused
+    img = _img(37, 53, 1).cuda()
+    a = img.clone().requires_grad_(True)
+    b = img.clone().requires_grad_(True)
+    out = fused.clamp_to_nchw(a)
+    ref = b.clamp(0, 1).permute(2, 0, 1).unsqueeze(0).contiguous()
+    assert out.shape == ref.shape and out.is_contiguous()
+    assert torch.equal(out, ref)
+    g = torch.randn_like(ref)
+    out.backward(g)
+    ref.backward(g)
+    assert torch.equal(a.grad, b.grad)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,weight", [((1, 3, 64, 80), 0.2), ((2, 3, 45, 61), 0.7)])
+def test_mse_ssim_loss_matches_separate_calls_and_oracle(shape, weight):
+    import manbo
+    from repo_amd import fused
+    g = torch.Generator().manual_seed(3)
+    y = torch.rand(shape, generator=g)
+    x = (0.6 * y + 0.4 * torch.rand(shape, generator=g)).clamp(0, 1)
+    xd = x.cuda().requires_grad_(True)
+    loss, parts = fused.mse_ssim_loss(xd, y.cuda(), weight)
+    sep = manbo.mse_loss_tilelang(x.cuda(), y.cuda()) + weight * (1 - manbo.ssim(x.cuda(),
+                                                                                 y.cuda()))
+    assert abs(float(loss) - float(sep)) <= 2e-6 * abs(float(sep))
+    x64 = x.double().requires_grad_(True)
+    ref = ((x64 - y.double()) ** 2).mean() + weight * (1 - O.ssim_torch64(x64, y.double()))
+    assert abs(float(loss) - float(ref)) <= 1e-5 * abs(float(ref))
+    assert abs(float(parts[0]) - float(((x64 - y.double()) ** 2).mean())) <= 1e-5 * float(
+        ((x64 - y.double()) ** 2).mean())
+    (1.5 * loss).backward()
+    (1.5 * ref).backward()
+    got = xd.grad.cpu().double().numpy()
+    want = x64.grad.numpy()
+    assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
+
+
+@pytest.mark.gpu
+def test_fused_step_gradients_match_unfused():
+    """Render -> clamp/permute -> MSE + 0.2 (1 - SSIM) -> backward: control-point
+    and colour gradients through the fused ops equal the separate-call path."""
+    import manbo
+    from repo_amd import fused, synth
+    sc = synth.small_scene(21, P=30, h=96, w=112, rmax=40.0)
+    dev = "cuda"
+    target = torch.rand((1, 3, sc.img_h, sc.img_w), generator=torch.Generator().manual_seed(4))
+    target = target.to(dev)
+    grads = []
+    for use_fused in (True, False):
+        cub = sc.cubics_norm.to(dev).requires_grad_(True)
+        col = sc.colors.to(dev).requires_grad_(True)
+        img = manbo.ops.render_cubic_fill_splat_tilelang(
+            cub, sc.seg_offsets.to(dev), col, sc.opacities.to(dev), sc.depths.to(dev), sc.img_h,
+            sc.img_w, 16, 16, sc.background.to(dev), aa_widths=sc.aa_widths.to(dev),
+            distance_samples=sc.S)
+        if use_fused:
+            loss, _ = fused.mse_ssim_loss(fused.clamp_to_nchw(img), target, 0.2)
+        else:
+            x = img.clamp(0, 1).permute(2, 0, 1).unsqueeze(0).contiguous()
+            loss = manbo.mse_loss_tilelang(x, target) + 0.2 * (1 - manbo.ssim(x, target))
+        loss.backward()
+        grads.append((float(loss), cub.grad.cpu().numpy(), col.grad.cpu().numpy()))
+    (lf, cf, kf), (lu, cu, ku) = grads
+    assert abs(lf - lu) <= 2e-6 * abs(lu)
+    for a, b in ((cf, cu), (kf, ku)):
+        assert np.abs(a - b).max() <= 1e-4 * np.abs(b).max()
