@@ -53,7 +53,8 @@ def make_problem(cfg):
     sc = synth.make_scene(cfg).to("cuda")
     cub = sc.cubics_norm.clone().requires_grad_(True)
     col = sc.colors.clone().requires_grad_(True)
-    opt = torch.optim.Adam([cub, col], lr=1e-3)
+    # Adam (model.py:185-189), torch's single-kernel implementation.
+    opt = torch.optim.Adam([cub, col], lr=1e-3, fused=True)
     return sc, cub, col, opt
 
 

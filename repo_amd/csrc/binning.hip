@@ -517,6 +517,97 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_scatter(
     }
 }
 
+// Stable LSD radix sort of up to kSmallSortMax (key, value) pairs by one
+// 1024-thread workgroup, entirely in LDS (one launch instead of 5 per pass):
+// per 8-bit pass a histogram (LDS atomics), an exclusive scan of the 256
+// digit counts, and a stable scatter in rounds of 1024 items in input order,
+// ranked like k_rs_scatter (8 ballots within a wave, per-wave digit counts
+// across the waves, running per-digit bases across rounds).
+constexpr int kSmallSortThreads = 1024;
+constexpr int kSmallSortMax = 8192;
+
+__global__ __launch_bounds__(kSmallSortThreads) void k_sort_small(uint32_t* __restrict__ keys,
+                                                                 int32_t* __restrict__ vals,
+                                                                 int n, int passes) {
+    constexpr int kW = kSmallSortThreads / kWave;
+    __shared__ uint32_t kb[2][kSmallSortMax];
+    __shared__ int32_t vb[2][kSmallSortMax];
+    __shared__ uint32_t base[256];
+    __shared__ uint32_t wtot[4];
+    __shared__ uint32_t wc[kW][256];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    for (int i = t; i < n; i += kSmallSortThreads) {
+        kb[0][i] = keys[i];
+        vb[0][i] = vals[i];
+    }
+    const uint64_t below = __lanemask_lt();
+    int cur = 0;
+    for (int ps = 0; ps < passes; ++ps) {
+        const int shift = 8 * ps;
+        if (t < 256) base[t] = 0;
+        __syncthreads();
+        for (int i = t; i < n; i += kSmallSortThreads)
+            atomicAdd(&base[(kb[cur][i] >> shift) & 0xFFu], 1u);
+        __syncthreads();
+        // Exclusive scan of the 256 counts (waves 0..3, one count per lane).
+        uint32_t cnt = 0, incl = 0;
+        if (t < 256) {
+            cnt = base[t];
+            incl = cnt;
+#pragma unroll
+            for (int off = 1; off < kWave; off <<= 1) {
+                const uint32_t o = __shfl_up(incl, off, kWave);
+                if (lane >= off) incl += o;
+            }
+            if (lane == kWave - 1) wtot[w] = incl;
+        }
+        __syncthreads();
+        if (t < 256) {
+            uint32_t pre = 0;
+            for (int q = 0; q < w; ++q) pre += wtot[q];
+            base[t] = pre + incl - cnt;
+        }
+        for (int r0 = 0; r0 < n; r0 += kSmallSortThreads) {
+            for (int i = t; i < kW * 256; i += kSmallSortThreads) (&wc[0][0])[i] = 0;
+            __syncthreads();
+            const int idx = r0 + t;
+            const bool valid = idx < n;
+            const uint32_t key = valid ? kb[cur][idx] : 0u;
+            const int32_t val = valid ? vb[cur][idx] : 0;
+            const uint32_t d = (key >> shift) & 0xFFu;
+            uint64_t peers = __ballot(valid);
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const bool bit = (d >> b) & 1u;
+                const uint64_t m = __ballot(bit);
+                peers &= bit ? m : ~m;
+            }
+            const uint32_t rank = (uint32_t)__popcll(peers & below);
+            if (valid && rank == 0) wc[w][d] = (uint32_t)__popcll(peers);
+            __syncthreads();
+            if (valid) {
+                uint32_t off = base[d] + rank;
+                for (int q = 0; q < w; ++q) off += wc[q][d];
+                kb[cur ^ 1][off] = key;
+                vb[cur ^ 1][off] = val;
+            }
+            __syncthreads();
+            if (t < 256) {
+                uint32_t add = 0;
+#pragma unroll
+                for (int q = 0; q < kW; ++q) add += wc[q][t];
+                base[t] += add;
+            }
+            __syncthreads();
+        }
+        cur ^= 1;
+    }
+    for (int i = t; i < n; i += kSmallSortThreads) {
+        keys[i] = kb[cur][i];
+        vals[i] = vb[cur][i];
+    }
+}
+
 // ------------------------------------------------------------ emit and bins
 
 __global__ __launch_bounds__(256) void k_rank_counts(const int32_t* __restrict__ order,
@@ -722,6 +813,11 @@ extern "C" int cs_radix_sort_pairs_u32(uint32_t* keys, int32_t* vals, uint32_t* 
     if (n <= 1 || key_bits == 0) return CS_OK;
     const int nb = blocks_for(n, kRsTile);
     const int passes = (key_bits + 7) / 8;
+    if (n <= kSmallSortMax) {
+        hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(kSmallSortThreads), 0, stream, keys, vals,
+                           n, passes);
+        return launch_status();
+    }
     uint32_t *ki = keys, *ko = keys_alt;
     int32_t *vi = vals, *vo = vals_alt;
     for (int ps = 0; ps < passes; ++ps) {
