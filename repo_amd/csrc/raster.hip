@@ -113,8 +113,64 @@ __device__ __forceinline__ bool prim_culled(const PrimRec& pr, const WaveRect& W
     return !cross_rows(pr, W) || W.c0 > pr.x_last;
 }
 
+// Lane's cull words of edge min(c + lane, e1 - 1) of a primitive whose edges
+// end at e1.  Always issued (so that the compiler can count outstanding vector
+// loads statically); lanes past e1 are masked at use.  Every list entry's
+// primitive has at least one segment (a primitive without segments covers no
+// tile), so the index is a valid edge.
+__device__ __forceinline__ int4 load_culls(const EdgeCull* __restrict__ culls, int c, int e1) {
+    const int lane = threadIdx.x & (kWave - 1);
+    return *reinterpret_cast<const int4*>(culls + max(min(c + lane, e1 - 1), 0));
+}
+
+// One 64-edge chunk starting at edge c: lane tests, ballots and the edge walks.
+template <int MODE, bool BEST>
+__device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const WaveRect& W,
+                                               cptr<EdgeRec> edges, float px, float py,
+                                               Geom& G) {
+    const bool in = c + (int)(threadIdx.x & (kWave - 1)) < e1;
+    const bool dn = in && span_hits(packed_lo(q.x), packed_span(q.x), W.r1) &&
+                    span_hits(packed_lo(q.z), packed_span(q.z), W.c1);
+    const bool cb = MODE == 0 && in && span_hits(packed_lo(q.y), packed_span(q.y), W.r1);
+    const uint64_t mdn = __ballot(dn);
+    const uint64_t mcb = MODE == 0 ? (uint64_t)__ballot(cb) : 0ull;
+    const cptr<EdgeRec> ec = edges + c;
+    if constexpr (BEST) {
+        // Distance terms in ascending edge order (the first strict minimum
+        // wins ties); the crossing terms' order does not matter.
+        for (uint64_t todo = mdn; todo; todo &= todo - 1) {
+            const int k = (int)__builtin_ctzll(todo);
+            const EdgeRec E = ec[k];
+            const float wx = px - E.x0, wy = py - E.y0;
+            dist_term<true>(E, c + k, wx, wy, G);
+            if (MODE == 0 && ((mcb >> k) & 1)) cross_term(E, wx, wy, py, G);
+        }
+        for (uint64_t todo = mcb & ~mdn; todo; todo &= todo - 1) {
+            const EdgeRec E = ec[__builtin_ctzll(todo)];
+            cross_term(E, px - E.x0, py - E.y0, py, G);
+        }
+    } else {
+        // The minimum and the winding number do not depend on the order:
+        // three loops without per-edge tests.
+        for (uint64_t todo = mdn & mcb; todo; todo &= todo - 1) {
+            const EdgeRec E = ec[__builtin_ctzll(todo)];
+            const float wx = px - E.x0, wy = py - E.y0;
+            dist_term<false>(E, 0, wx, wy, G);
+            cross_term(E, wx, wy, py, G);
+        }
+        for (uint64_t todo = mdn & ~mcb; todo; todo &= todo - 1) {
+            const EdgeRec E = ec[__builtin_ctzll(todo)];
+            dist_term<false>(E, 0, px - E.x0, py - E.y0, G);
+        }
+        for (uint64_t todo = mcb & ~mdn; todo; todo &= todo - 1) {
+            const EdgeRec E = ec[__builtin_ctzll(todo)];
+            cross_term(E, px - E.x0, py - E.y0, py, G);
+        }
+    }
+}
+
 // All edges of a primitive with per-edge culling decided lane-parallel: lane
-// k loads the packed ranges of edge k of a 64-edge chunk (one vector load),
+// k holds the packed ranges of edge k of a 64-edge chunk (one vector load),
 // tests them against the wave, and two ballots give the edges whose distance
 // and crossing terms can matter.  The wave then visits only those edges, in
 // ascending index order (so the best edge is the first strict minimum, as in
@@ -123,59 +179,18 @@ template <int MODE, bool BEST>
 __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& W,
                                               const EdgeCull* __restrict__ culls,
                                               cptr<EdgeRec> edges, int eps, float px, float py,
-                                              Geom& G) {
+                                              int4 first, Geom& G) {
     G.min_d2 = 1e30f;
     G.winding = 0;
     G.best = -1;
     G.bproj = 0.0f;
     G.bdx = 0.0f;
     G.bdy = 0.0f;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int e1 = pr.s1 * eps;
-    for (int c = pr.s0 * eps; c < e1; c += kWave) {
-        bool dn = false, cb = false;
-        if (c + lane < e1) {
-            const int4 q = *reinterpret_cast<const int4*>(culls + c + lane);
-            dn = span_hits(packed_lo(q.x), packed_span(q.x), W.r1) &&
-                 span_hits(packed_lo(q.z), packed_span(q.z), W.c1);
-            cb = MODE == 0 && span_hits(packed_lo(q.y), packed_span(q.y), W.r1);
-        }
-        const uint64_t mdn = __ballot(dn);
-        const uint64_t mcb = MODE == 0 ? (uint64_t)__ballot(cb) : 0ull;
-        const cptr<EdgeRec> ec = edges + c;
-        if constexpr (BEST) {
-            // Distance terms in ascending edge order (the first strict minimum
-            // wins ties); the crossing terms' order does not matter.
-            for (uint64_t todo = mdn; todo; todo &= todo - 1) {
-                const int k = (int)__builtin_ctzll(todo);
-                const EdgeRec E = ec[k];
-                const float wx = px - E.x0, wy = py - E.y0;
-                dist_term<true>(E, c + k, wx, wy, G);
-                if (MODE == 0 && ((mcb >> k) & 1)) cross_term(E, wx, wy, py, G);
-            }
-            for (uint64_t todo = mcb & ~mdn; todo; todo &= todo - 1) {
-                const EdgeRec E = ec[__builtin_ctzll(todo)];
-                cross_term(E, px - E.x0, py - E.y0, py, G);
-            }
-        } else {
-            // The minimum and the winding number do not depend on the order:
-            // three loops without per-edge tests.
-            for (uint64_t todo = mdn & mcb; todo; todo &= todo - 1) {
-                const EdgeRec E = ec[__builtin_ctzll(todo)];
-                const float wx = px - E.x0, wy = py - E.y0;
-                dist_term<false>(E, 0, wx, wy, G);
-                cross_term(E, wx, wy, py, G);
-            }
-            for (uint64_t todo = mdn & ~mcb; todo; todo &= todo - 1) {
-                const EdgeRec E = ec[__builtin_ctzll(todo)];
-                dist_term<false>(E, 0, px - E.x0, py - E.y0, G);
-            }
-            for (uint64_t todo = mcb & ~mdn; todo; todo &= todo - 1) {
-                const EdgeRec E = ec[__builtin_ctzll(todo)];
-                cross_term(E, px - E.x0, py - E.y0, py, G);
-            }
-        }
-    }
+    // The first chunk's words were loaded ahead by the caller.
+    const int c0 = pr.s0 * eps, e1 = pr.s1 * eps;
+    chunk_geometry<MODE, BEST>(first, c0, e1, W, edges, px, py, G);
+    for (int c = c0 + kWave; c < e1; c += kWave)
+        chunk_geometry<MODE, BEST>(load_culls(culls, c, e1), c, e1, W, edges, px, py, G);
 }
 
 struct Cov {
@@ -237,16 +252,25 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
     float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
     int cur = 0;
     bool done = !in_img;
-    int pid_next = g0 < g1 ? prim_ids[g0] : 0;
+    // The cull words of the next entry's first 64 edges are loaded one entry
+    // ahead, so that vector load is in flight while this entry is processed.
+    int pid = g0 < g1 ? prim_ids[g0] : 0;
+    int pid_next = prim_ids[min(g0 + 1, g1 - 1)];
+    int4 q_next = g0 < g1 ? load_culls(culls, prims[pid].s0 * eps, prims[pid].s1 * eps)
+                          : make_int4(0, -1, 0, -1);
     for (int g = g0; g < g1; ++g) {
         if (__ballot(!done) == 0) break;
-        const int pid = pid_next;
-        pid_next = prim_ids[min(g + 1, g1 - 1)];
         const PrimRec pr = prims[pid];
+        const int ns0 = prims[pid_next].s0, ns1 = prims[pid_next].s1;
+        const int pid_after = prim_ids[min(g + 2, g1 - 1)];
+        const int4 q = q_next;
+        q_next = load_culls(culls, ns0 * eps, ns1 * eps);
+        pid = pid_next;
+        pid_next = pid_after;
         const float D2 = pr.cull_d * pr.cull_d;
         if (prim_culled<MODE>(pr, W)) continue;
         Geom G;
-        prim_geometry<MODE, false>(pr, W, culls, edges, eps, px, py, G);
+        prim_geometry<MODE, false>(pr, W, culls, edges, eps, px, py, q, G);
         if (!done) {
             const Cov c = coverage<MODE>(pr, G, D2);
             const float alpha = fminf(kAlphaCap, pr.opacity * c.cov);
@@ -344,17 +368,27 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     // The wave maximum is uniform; readfirstlane tells the compiler so, which
     // keeps every load that depends on the entry index scalar.
     const int gstart = min(g1 - 1, __builtin_amdgcn_readfirstlane(wave_max_i(fidx)));
-    int pid_next = gstart >= g0 ? prim_ids[gstart] : 0;
+    // As in the forward, the next entry's first cull words are loaded one
+    // entry ahead (here the next entry is g - 1).
+    int pid = gstart >= g0 ? prim_ids[gstart] : 0;
+    int pid_next = prim_ids[max(gstart - 1, g0)];
+    int4 q_next = gstart >= g0 ? load_culls(culls, prims[pid].s0 * eps, prims[pid].s1 * eps)
+                               : make_int4(0, -1, 0, -1);
     for (int g = gstart; g >= g0; --g) {
         const bool valid = in_img & (g <= fidx);
-        const int pid = pid_next;
-        pid_next = prim_ids[max(g - 1, g0)];
+        const int pid_cur = pid;
+        const PrimRec pr = prims[pid_cur];
+        const int ns0 = prims[pid_next].s0, ns1 = prims[pid_next].s1;
+        const int pid_after = prim_ids[max(g - 2, g0)];
+        const int4 q = q_next;
+        q_next = load_culls(culls, ns0 * eps, ns1 * eps);
+        pid = pid_next;
+        pid_next = pid_after;
         if (__ballot(valid) == 0) continue;
-        const PrimRec pr = prims[pid];
         const float D2 = pr.cull_d * pr.cull_d;
         if (prim_culled<MODE>(pr, W)) continue;
         Geom G;
-        prim_geometry<MODE, true>(pr, W, culls, edges, eps, px, py, G);
+        prim_geometry<MODE, true>(pr, W, culls, edges, eps, px, py, q, G);
         float vr = 0.0f, vg = 0.0f, vb = 0.0f, vop = 0.0f, vis2 = 0.0f, vsw = 0.0f;
         float cr = 0.0f, cg = 0.0f, cb = 0.0f;
         float gx = 0.0f, gy = 0.0f;
@@ -423,17 +457,17 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
             const float pv[8] = {vr, vg, vb, vop, vis2, MODE == 1 ? vsw : 0.0f, 0.0f, 0.0f};
             const float t = wave_reduce8(pv);
             if (adder && slot < (MODE == 1 ? 6 : 5)) {
-                float* dst = slot < 3 ? v_colors + 3 * pid + slot
-                           : slot == 3 ? v_opac + pid
-                           : slot == 4 ? v_is2 + pid
-                                       : v_sw + pid;
+                float* dst = slot < 3 ? v_colors + 3 * pid_cur + slot
+                           : slot == 3 ? v_opac + pid_cur
+                           : slot == 4 ? v_is2 + pid_cur
+                                       : v_sw + pid_cur;
                 atomicAdd(dst, t);
             }
         }
         if (want_contrib) {
             const float cv[8] = {cr, cg, cb, cr + cg + cb, 0.0f, 0.0f, 0.0f, 0.0f};
             const float t = wave_reduce8(cv);
-            if (adder && slot < 3 && contrib_rgb) atomicAdd(contrib_rgb + 3 * pid + slot, t);
+            if (adder && slot < 3 && contrib_rgb) atomicAdd(contrib_rgb + 3 * pid_cur + slot, t);
             if (adder && slot == 3 && isect_contrib) atomicAdd(isect_contrib + g, t);
         }
         // Geometry: endpoint gradients ((1-t) g, t g) of the best edge, folded
