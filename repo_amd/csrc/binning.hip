@@ -517,94 +517,51 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_scatter(
     }
 }
 
-// Stable LSD radix sort of up to kSmallSortMax (key, value) pairs by one
-// 1024-thread workgroup, entirely in LDS (one launch instead of 5 per pass):
-// per 8-bit pass a histogram (LDS atomics), an exclusive scan of the 256
-// digit counts, and a stable scatter in rounds of 1024 items in input order,
-// ranked like k_rs_scatter (8 ballots within a wave, per-wave digit counts
-// across the waves, running per-digit bases across rounds).
-constexpr int kSmallSortThreads = 1024;
-constexpr int kSmallSortMax = 8192;
+// Stable sort of up to kRankSortMax keys by counting, one wave per key: key
+// i's position in the ascending stable order is the number of keys that are
+// smaller, or equal with a smaller index.  Lanes count over interleaved
+// (coalesced) slices of the key array, which every wave reads from cache, and
+// one wave sum gives the position.  n^2 comparisons spread over n waves: one
+// launch, where the radix sort needs five per 8-bit pass.
+constexpr int kRankSortMax = 16384;
 
-__global__ __launch_bounds__(kSmallSortThreads) void k_sort_small(uint32_t* __restrict__ keys,
-                                                                 int32_t* __restrict__ vals,
-                                                                 int n, int passes) {
-    constexpr int kW = kSmallSortThreads / kWave;
-    __shared__ uint32_t kb[2][kSmallSortMax];
-    __shared__ int32_t vb[2][kSmallSortMax];
-    __shared__ uint32_t base[256];
-    __shared__ uint32_t wtot[4];
-    __shared__ uint32_t wc[kW][256];
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    for (int i = t; i < n; i += kSmallSortThreads) {
-        kb[0][i] = keys[i];
-        vb[0][i] = vals[i];
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ int stable_rank(const uint32_t* __restrict__ keys, int n, int i,
+                                           uint32_t ki) {
+    int cnt = 0;
+    for (int j = threadIdx.x & (kWave - 1); j < n; j += kWave) {
+        const uint32_t kj = keys[j];
+        cnt += (int)((kj < ki) | ((kj == ki) & (j < i)));
     }
-    const uint64_t below = __lanemask_lt();
-    int cur = 0;
-    for (int ps = 0; ps < passes; ++ps) {
-        const int shift = 8 * ps;
-        if (t < 256) base[t] = 0;
-        __syncthreads();
-        for (int i = t; i < n; i += kSmallSortThreads)
-            atomicAdd(&base[(kb[cur][i] >> shift) & 0xFFu], 1u);
-        __syncthreads();
-        // Exclusive scan of the 256 counts (waves 0..3, one count per lane).
-        uint32_t cnt = 0, incl = 0;
-        if (t < 256) {
-            cnt = base[t];
-            incl = cnt;
-#pragma unroll
-            for (int off = 1; off < kWave; off <<= 1) {
-                const uint32_t o = __shfl_up(incl, off, kWave);
-                if (lane >= off) incl += o;
-            }
-            if (lane == kWave - 1) wtot[w] = incl;
-        }
-        __syncthreads();
-        if (t < 256) {
-            uint32_t pre = 0;
-            for (int q = 0; q < w; ++q) pre += wtot[q];
-            base[t] = pre + incl - cnt;
-        }
-        for (int r0 = 0; r0 < n; r0 += kSmallSortThreads) {
-            for (int i = t; i < kW * 256; i += kSmallSortThreads) (&wc[0][0])[i] = 0;
-            __syncthreads();
-            const int idx = r0 + t;
-            const bool valid = idx < n;
-            const uint32_t key = valid ? kb[cur][idx] : 0u;
-            const int32_t val = valid ? vb[cur][idx] : 0;
-            const uint32_t d = (key >> shift) & 0xFFu;
-            uint64_t peers = __ballot(valid);
-#pragma unroll
-            for (int b = 0; b < 8; ++b) {
-                const bool bit = (d >> b) & 1u;
-                const uint64_t m = __ballot(bit);
-                peers &= bit ? m : ~m;
-            }
-            const uint32_t rank = (uint32_t)__popcll(peers & below);
-            if (valid && rank == 0) wc[w][d] = (uint32_t)__popcll(peers);
-            __syncthreads();
-            if (valid) {
-                uint32_t off = base[d] + rank;
-                for (int q = 0; q < w; ++q) off += wc[q][d];
-                kb[cur ^ 1][off] = key;
-                vb[cur ^ 1][off] = val;
-            }
-            __syncthreads();
-            if (t < 256) {
-                uint32_t add = 0;
-#pragma unroll
-                for (int q = 0; q < kW; ++q) add += wc[q][t];
-                base[t] += add;
-            }
-            __syncthreads();
-        }
-        cur ^= 1;
-    }
-    for (int i = t; i < n; i += kSmallSortThreads) {
-        keys[i] = kb[cur][i];
-        vals[i] = vb[cur][i];
+    return wave_sum_i(cnt);
+}
+
+// order[position of key i] = i.
+__global__ __launch_bounds__(256) void k_rank_order(const uint32_t* __restrict__ keys, int n,
+                                                   int32_t* __restrict__ order) {
+    const int i = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (i >= n) return;
+    const int pos = stable_rank(keys, n, i, keys[i]);
+    if ((threadIdx.x & (kWave - 1)) == 0) order[pos] = i;
+}
+
+// (key, value) pairs into their stable sorted positions of kout / vout.
+__global__ __launch_bounds__(256) void k_rank_pairs(const uint32_t* __restrict__ keys,
+                                                   const int32_t* __restrict__ vals, int n,
+                                                   uint32_t* __restrict__ kout,
+                                                   int32_t* __restrict__ vout) {
+    const int i = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (i >= n) return;
+    const uint32_t ki = keys[i];
+    const int pos = stable_rank(keys, n, i, ki);
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        kout[pos] = ki;
+        vout[pos] = vals[i];
     }
 }
 
@@ -813,9 +770,14 @@ extern "C" int cs_radix_sort_pairs_u32(uint32_t* keys, int32_t* vals, uint32_t* 
     if (n <= 1 || key_bits == 0) return CS_OK;
     const int nb = blocks_for(n, kRsTile);
     const int passes = (key_bits + 7) / 8;
-    if (n <= kSmallSortMax) {
-        hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(kSmallSortThreads), 0, stream, keys, vals,
-                           n, passes);
+    if (n <= kRankSortMax) {
+        hipLaunchKernelGGL(k_rank_pairs, dim3((n + 3) / 4), dim3(256), 0, stream, keys, vals, n,
+                           keys_alt, vals_alt);
+        if (hipMemcpyAsync(keys, keys_alt, sizeof(uint32_t) * n, hipMemcpyDeviceToDevice,
+                           stream) != hipSuccess ||
+            hipMemcpyAsync(vals, vals_alt, sizeof(int32_t) * n, hipMemcpyDeviceToDevice,
+                           stream) != hipSuccess)
+            return CS_ERR_HIP;
         return launch_status();
     }
     uint32_t *ki = keys, *ko = keys_alt;
@@ -880,9 +842,16 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                        prim_tile_ranges,
                        num_tiles_hit, inv_sigma2s, keys, order,
                        reinterpret_cast<PrimRec*>(prim_recs));
-    int rc = cs_radix_sort_pairs_u32(keys, order, keys_alt, vals_alt, nprim, 32, radix_counts,
-                                     scan_temp, stream);
-    if (rc) return rc;
+    // Depth ranks: order[r] = primitive with the r-th smallest depth key
+    // (ties by primitive id).
+    if (nprim <= kRankSortMax) {
+        hipLaunchKernelGGL(k_rank_order, dim3((nprim + 3) / 4), dim3(256), 0, stream, keys,
+                           nprim, order);
+    } else {
+        const int rc = cs_radix_sort_pairs_u32(keys, order, keys_alt, vals_alt, nprim, 32,
+                                               radix_counts, scan_temp, stream);
+        if (rc) return rc;
+    }
     hipLaunchKernelGGL(k_rank_counts, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream, order,
                        num_tiles_hit, nprim, keys_alt);
     return cs_scan_exclusive_u32(keys_alt, rank_offsets, nprim, scan_temp, status, stream);

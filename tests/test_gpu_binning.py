@@ -112,7 +112,7 @@ def test_reference_layout_blocks():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("n,bits", [(0, 8), (1, 32), (2, 1), (255, 8), (1000, 32), (4096, 14),
-                                    (4097, 14), (8192, 32), (8193, 32), (100003, 32),
+                                    (4097, 14), (8192, 32), (16384, 32), (16385, 32), (100003, 32),
                                     (300001, 17)])
 def test_radix_sort_stable(n, bits):
     from repo_amd import _native as N
