@@ -110,7 +110,11 @@ int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const f
 
 /* Stage 2 (ops/cubic_splatting.py:2888-2908): emit (tile, primitive) pairs in
  * depth-rank order, stable sort by tile, tile_bins [T,2].  Outputs are the
- * reference's primitive_ids_sorted [I] and tile_bins, bit-exact. */
+ * reference's primitive_ids_sorted [I] and tile_bins, bit-exact.  radix_counts
+ * holds cs_bin_finish_counts_elems(...) uint32, scan_temp cs_scan_temp_elems of
+ * that; keys_alt / vals_alt hold num_intersects elements. */
+size_t cs_bin_finish_counts_elems(int32_t nprim, int32_t num_intersects, int32_t img_h,
+                                  int32_t img_w, int32_t block_x, int32_t block_y);
 int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges,
                   const uint32_t* rank_offsets, int32_t nprim, int32_t num_intersects,
                   int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,

@@ -32,6 +32,7 @@ _SZ = ctypes.c_size_t
 _SIGNATURES = {
     "cs_scan_temp_elems": (_SZ, [_I32]),
     "cs_radix_counts_elems": (_SZ, [_I32]),
+    "cs_bin_finish_counts_elems": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
     "cs_scan_exclusive_u32": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P]),
     "cs_radix_sort_pairs_u32": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _P, _P, _P]),
     "cs_project_cubics_2d_forward": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F,

@@ -422,18 +422,22 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_partials(uint32_t* __rest
     }
 }
 
-// Exclusive scan of in[0..n) into out; block b adds the scanned block sum.
-// The last block writes the grand total to *total_out (if given).
+// Exclusive scan of in[0..n) into out, ITEMS consecutive items per thread;
+// block b adds the scanned block sum.  The last block writes the grand total
+// to *total_out (if given).
+
+template <int ITEMS>
 __global__ __launch_bounds__(kScanThreads) void k_scan_apply(const uint32_t* __restrict__ in,
                                                             uint32_t* __restrict__ out, int n,
                                                             const uint32_t* __restrict__ sums,
                                                             int32_t* __restrict__ total_out) {
     __shared__ uint32_t sh[kScanThreads / kWave + 1];
-    const size_t base = (size_t)blockIdx.x * kScanChunk + (size_t)threadIdx.x * kScanItems;
-    uint32_t v[kScanItems];
+    const size_t base =
+        (size_t)blockIdx.x * kScanThreads * ITEMS + (size_t)threadIdx.x * ITEMS;
+    uint32_t v[ITEMS];
     uint32_t acc = 0;
 #pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
+    for (int k = 0; k < ITEMS; ++k) {
         v[k] = (base + k < (size_t)n) ? in[base + k] : 0u;
         acc += v[k];
     }
@@ -441,7 +445,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_apply(const uint32_t* __r
     uint32_t ex = block_excl_scan(acc, sh, &total);
     ex += sums ? sums[blockIdx.x] : 0u;
 #pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
+    for (int k = 0; k < ITEMS; ++k) {
         if (base + k < (size_t)n) out[base + k] = ex;
         ex += v[k];
     }
@@ -531,13 +535,29 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     return v;
 }
 
+__device__ __forceinline__ int precedes(uint32_t kj, int j, uint32_t ki, int i) {
+    return (int)((kj < ki) | ((kj == ki) & (j < i)));
+}
+
+// Lanes take 4 consecutive keys per step (one 16-byte load), 4 steps unrolled
+// so that the loads overlap.
 __device__ __forceinline__ int stable_rank(const uint32_t* __restrict__ keys, int n, int i,
                                            uint32_t ki) {
+    const int lane = threadIdx.x & (kWave - 1);
     int cnt = 0;
-    for (int j = threadIdx.x & (kWave - 1); j < n; j += kWave) {
-        const uint32_t kj = keys[j];
-        cnt += (int)((kj < ki) | ((kj == ki) & (j < i)));
+    const int n4 = n & ~3;
+    const bool vec = (reinterpret_cast<uintptr_t>(keys) & 15) == 0;
+    int j0 = 0;
+    if (vec) {
+#pragma unroll 4
+        for (j0 = 4 * lane; j0 < n4; j0 += 4 * kWave) {
+            const uint4 q = *reinterpret_cast<const uint4*>(keys + j0);
+            cnt += precedes(q.x, j0, ki, i) + precedes(q.y, j0 + 1, ki, i) +
+                   precedes(q.z, j0 + 2, ki, i) + precedes(q.w, j0 + 3, ki, i);
+        }
+        j0 = n4;
     }
+    for (int j = j0 + lane; j < n; j += kWave) cnt += precedes(keys[j], j, ki, i);
     return wave_sum_i(cnt);
 }
 
@@ -748,12 +768,15 @@ extern "C" int cs_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int32_t 
         return launch_status();
     }
     const int nb = blocks_for(n, kScanChunk);
-    if (nb > 1) {
+    if (nb == 1) {
+        hipLaunchKernelGGL(k_scan_apply<kScanItems>, dim3(1), dim3(kScanThreads), 0, stream, in,
+                           out, n, nullptr, total);
+    } else {
         hipLaunchKernelGGL(k_scan_block_sums, dim3(nb), dim3(kScanThreads), 0, stream, in, n, temp);
         hipLaunchKernelGGL(k_scan_partials, dim3(1), dim3(kScanThreads), 0, stream, temp, nb);
+        hipLaunchKernelGGL(k_scan_apply<kScanItems>, dim3(nb), dim3(kScanThreads), 0, stream, in,
+                           out, n, temp, total);
     }
-    hipLaunchKernelGGL(k_scan_apply, dim3(nb), dim3(kScanThreads), 0, stream, in, out, n,
-                       nb > 1 ? temp : nullptr, total);
     return launch_status();
 }
 
@@ -855,6 +878,15 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
     hipLaunchKernelGGL(k_rank_counts, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream, order,
                        num_tiles_hit, nprim, keys_alt);
     return cs_scan_exclusive_u32(keys_alt, rank_offsets, nprim, scan_temp, status, stream);
+}
+
+extern "C" size_t cs_bin_finish_counts_elems(int32_t nprim, int32_t num_intersects,
+                                              int32_t img_h, int32_t img_w, int32_t block_x,
+                                              int32_t block_y) {
+    if (nprim <= 0 || num_intersects < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 ||
+        block_y <= 0)
+        return 0;
+    return cs_radix_counts_elems(num_intersects > 0 ? num_intersects : 1);
 }
 
 extern "C" int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges,

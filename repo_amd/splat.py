@@ -165,7 +165,7 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     if I > 0:
         kalt = torch.empty((I,), dtype=i32, device=dev)
         valt = torch.empty((I,), dtype=i32, device=dev)
-        counts_i = int(lib.cs_radix_counts_elems(I))
+        counts_i = int(lib.cs_bin_finish_counts_elems(P, I, img_h, img_w, block_x, block_y))
         rc_i = torch.empty((counts_i,), dtype=i32, device=dev)
         st_i = torch.empty((int(lib.cs_scan_temp_elems(counts_i)),), dtype=i32, device=dev)
     else:

@@ -138,7 +138,7 @@ def test_radix_sort_stable(n, bits):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [1, 5, 4096, 4097, 1000003])
+@pytest.mark.parametrize("n", [1, 5, 4096, 4097, 32768, 32769, 1000003])
 def test_exclusive_scan(n):
     from repo_amd import _native as N
     g = np.random.default_rng(n)
