@@ -53,8 +53,9 @@ def make_problem(cfg):
     sc = synth.make_scene(cfg).to("cuda")
     cub = sc.cubics_norm.clone().requires_grad_(True)
     col = sc.colors.clone().requires_grad_(True)
-    # Adam (model.py:185-189), torch's single-kernel implementation.
-    opt = torch.optim.Adam([cub, col], lr=1e-3, fused=True)
+    # Adam (gaussian_trace/model.py:185-189) as one HIP launch per step.
+    from repo_amd.optim import Adam
+    opt = Adam([cub, col], lr=1e-3)
     return sc, cub, col, opt
 
 

@@ -222,6 +222,24 @@ int cs_mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, 
                          const float* win1d, int32_t win, const float* abc, float ssim_weight,
                          const float* grad_loss, float* grad_x, hipStream_t stream);
 
+/* ---------------- optimizer ---------------- */
+
+/* One Adam step (torch.optim.Adam as gaussian_trace/model.py:172-189 builds
+ * it: per-group learning rates, amsgrad and maximize off) over up to
+ * CS_ADAM_MAX_TENSORS fp32 tensors in one launch.  The arrays are host arrays
+ * of ntensors entries; the pointers in them are device pointers.  Per tensor
+ * k: step_sizes[k] = lr / (1 - beta1^step), bias_correction2_sqrts[k] =
+ * sqrt(1 - beta2^step) (> 0), weight_decays[k] the L2 coefficient.  The
+ * hyperparameters are doubles, as torch's Python floats: 1 - beta is formed in
+ * double and rounded to fp32 once.  Updates params, exp_avgs and exp_avg_sqs
+ * in place. */
+#define CS_ADAM_MAX_TENSORS 16
+int cs_adam_step(int32_t ntensors, float* const* params, const float* const* grads,
+                 float* const* exp_avgs, float* const* exp_avg_sqs, const int64_t* numels,
+                 const float* step_sizes, const float* bias_correction2_sqrts,
+                 const float* weight_decays, double beta1, double beta2, double eps,
+                 hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

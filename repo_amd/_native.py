@@ -27,6 +27,7 @@ _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
 _F = ctypes.c_float
+_D = ctypes.c_double
 _SZ = ctypes.c_size_t
 
 _SIGNATURES = {
@@ -66,6 +67,7 @@ _SIGNATURES = {
                                         _P, _P]),
     "cs_mse_ssim_backward": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _F, _P, _P,
                                             _P]),
+    "cs_adam_step": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _D, _D, _D, _P]),
 }
 
 _lib = None
