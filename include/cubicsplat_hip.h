@@ -148,6 +148,32 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
                           float* v_stroke_widths, float* curve_contrib_rgb,
                           float* curve_isect_contrib, hipStream_t stream);
 
+/* cs_rasterize_forward / cs_rasterize_backward with the same results, plus
+ * evaluation counts added into eval_counts[4] (device uint64, caller-zeroed):
+ * [0] distance terms and [1] crossing terms evaluated, each an (edge, pixel)
+ * pair of the reference's edge loop (cubic_splatting.py:1095-1134) that the
+ * kernel did not prove irrelevant; [2] (wave, list entry) pairs processed past
+ * the primitive cull; [3] exact coverage evaluations (pixels within the cull
+ * distance).  Measurement only (no reference counterpart): the counting
+ * instantiation is slower than the plain one. */
+int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
+                                 const int32_t* tile_bins, const void* edges,
+                                 const void* edge_culls, const void* prim_recs,
+                                 const float* background, int32_t img_h, int32_t img_w,
+                                 int32_t edges_per_segment, float* out_img, float* final_Ts,
+                                 int32_t* final_idx, unsigned long long* eval_counts,
+                                 hipStream_t stream);
+int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
+                                  const int32_t* tile_bins, const void* edges,
+                                  const void* edge_culls, const void* prim_recs,
+                                  const float* background, int32_t img_h, int32_t img_w,
+                                  int32_t edges_per_segment, const float* final_Ts,
+                                  const int32_t* final_idx, const float* v_output,
+                                  float* v_cubics_px, float* v_colors, float* v_opacities,
+                                  float* v_inv_sigma2s, float* v_stroke_widths,
+                                  float* curve_contrib_rgb, float* curve_isect_contrib,
+                                  unsigned long long* eval_counts, hipStream_t stream);
+
 /* _accumulate_edge_grads_to_cubics_kernel (ops/cubic_splatting.py:2308-2396)
  * fused with the v_cubics_norm scaling (ops/cubic_splatting.py:3096-3100). */
 int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg, int32_t edges_per_segment,

@@ -51,6 +51,11 @@ _SIGNATURES = {
                                             _P, _P]),
     "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P,
                                              _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cs_rasterize_forward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                                    _P, _P, _P, _P, _P]),
+    "cs_rasterize_backward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
+                                                     _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                     _P, _P, _P]),
     "cs_accumulate_edge_grads": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P]),
     "cs_backward_finalize": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P]),
     "cs_mse_partials_elems": (_SZ, [_I64]),

@@ -12,7 +12,12 @@ namespace cs {
 
 constexpr int kWave = 64;
 constexpr int kTile = 16;            // 16x16 pixel tiles, one workgroup each
-constexpr int kBlockThreads = 256;   // 4 waves; wave w owns tile rows 4w..4w+3
+// Raster launch shape: two pixels per lane (rows r and r + 4 of one column),
+// so a wave owns 8 tile rows and a tile is two waves.
+constexpr int kPix = 2;
+constexpr int kWaveRows = 4 * kPix;
+constexpr int kRasterThreads = kTile * kTile / kPix;
+static_assert(kPix == 2, "the backward's segment-leader walk assumes two pixels per lane");
 
 // Constants the reference writes as Python floats, rounded once from double.
 constexpr float kEps = (float)1e-6;
@@ -25,11 +30,11 @@ constexpr float kWidthMin = (float)1e-4;
 // whose centre k + 0.5 can matter, widened by one pixel beyond its fp32 bound,
 // so integer tests on it are conservative.  It is stored as (lo, span) with
 // span = hi - lo + ext, where ext + 1 is the wave's extent along that axis
-// (16 columns, 4 rows): [lo, hi] then meets the wave's [last - ext, last]
+// (16 columns, kWaveRows rows): [lo, hi] then meets the wave's [last - ext, last]
 // exactly when 0 <= last - lo <= span, which span_hits tests with one OR and a
 // sign check (no unpacking).  An empty range has span < ext.
-constexpr int kWaveColsExt = kTile - 1;  // a wave spans 16 columns
-constexpr int kWaveRowsExt = 3;          // and 4 rows
+constexpr int kWaveColsExt = kTile - 1;      // a wave spans 16 columns
+constexpr int kWaveRowsExt = kWaveRows - 1;  // and kWaveRows rows
 constexpr int32_t kRangeLimit = 1 << 20;
 
 __device__ __forceinline__ bool span_hits(int32_t lo, int32_t span, int32_t last) {

@@ -1,8 +1,10 @@
 // Forward and backward rasterization of flattened cubic primitives on MI355X.
 //
-// Launch: one 256-thread workgroup per 16x16 tile.  Unlike a block-synchronous
-// design, each of the four waves owns four tile rows (64 pixels, one per lane)
-// and walks the tile's sorted list on its own: the list entry, the primitive
+// Launch: one 128-thread workgroup per 16x16 tile.  Unlike a block-synchronous
+// design, each of the two waves owns eight tile rows (128 pixels, two per lane:
+// rows r and r + 4 of one column) and walks the tile's sorted list on its own,
+// so every per-entry scalar step, edge-record load and wave reduction serves
+// 128 pixels.  The list entry, the primitive
 // record and the edge geometry are wave-uniform, so they are read through the
 // scalar cache and used as SGPR operands, and no LDS or workgroup barrier is
 // needed.  A wave leaves the list when all of its pixels have reached the
@@ -13,7 +15,7 @@
 // primitive's cull distance from every lane and cannot change any lane's
 // result (outside: alpha < 1/255; inside: coverage is exactly 1.0f), so its
 // distance terms are skipped; its crossing terms are skipped when its y-range
-// misses the wave's four pixel rows.  A primitive is tested as a whole with
+// misses the wave's eight pixel rows.  A primitive is tested as a whole with
 // scalar instructions; its edges are tested lane-parallel (one edge per lane,
 // one ballot per test), and the wave then evaluates only the edges that can
 // matter.  Results stay bit-identical to evaluating every edge.
@@ -123,17 +125,40 @@ __device__ __forceinline__ int4 load_culls(const EdgeCull* __restrict__ culls, i
     return *reinterpret_cast<const int4*>(culls + max(min(c + lane, e1 - 1), 0));
 }
 
-// One 64-edge chunk starting at edge c: lane tests, ballots and the edge walks.
-template <int MODE, bool BEST>
+// Wave-uniform evaluation counters of the counting instantiation: distance and
+// crossing terms evaluated (edge visits times the wave's active pixels), list
+// entries a wave processed past the primitive cull, and exact coverage
+// evaluations (pixels within the cull distance).
+struct EvalCounts {
+    uint64_t dist, cross, entries, cover;
+};
+
+// Number of the wave's pixels with `a` set (both pixels of every lane).
+__device__ __forceinline__ int wave_count(const bool (&a)[kPix]) {
+    int n = 0;
+#pragma unroll
+    for (int p = 0; p < kPix; ++p) n += __builtin_popcountll(__ballot(a[p]));
+    return n;
+}
+
+// One 64-edge chunk starting at edge c: lane tests, ballots and the edge walks
+// for the lane's pixels (one column px, rows py[p]).  Each edge record is
+// loaded once through the scalar cache and evaluated for every pixel.
+template <int MODE, bool BEST, bool COUNT>
 __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const WaveRect& W,
-                                               cptr<EdgeRec> edges, float px, float py,
-                                               Geom& G) {
+                                               cptr<EdgeRec> edges, float px,
+                                               const float (&py)[kPix], Geom (&G)[kPix],
+                                               EvalCounts& n, int npix) {
     const bool in = c + (int)(threadIdx.x & (kWave - 1)) < e1;
     const bool dn = in && span_hits(packed_lo(q.x), packed_span(q.x), W.r1) &&
                     span_hits(packed_lo(q.z), packed_span(q.z), W.c1);
     const bool cb = MODE == 0 && in && span_hits(packed_lo(q.y), packed_span(q.y), W.r1);
     const uint64_t mdn = __ballot(dn);
     const uint64_t mcb = MODE == 0 ? (uint64_t)__ballot(cb) : 0ull;
+    if constexpr (COUNT) {
+        n.dist += (uint64_t)__builtin_popcountll(mdn) * npix;
+        n.cross += (uint64_t)__builtin_popcountll(mcb) * npix;
+    }
     const cptr<EdgeRec> ec = edges + c;
     if constexpr (BEST) {
         // Distance terms in ascending edge order (the first strict minimum
@@ -141,30 +166,45 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
         for (uint64_t todo = mdn; todo; todo &= todo - 1) {
             const int k = (int)__builtin_ctzll(todo);
             const EdgeRec E = ec[k];
-            const float wx = px - E.x0, wy = py - E.y0;
-            dist_term<true>(E, c + k, wx, wy, G);
-            if (MODE == 0 && ((mcb >> k) & 1)) cross_term(E, wx, wy, py, G);
+            const float wx = px - E.x0;
+            const bool cross = MODE == 0 && ((mcb >> k) & 1);
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) {
+                const float wy = py[p] - E.y0;
+                dist_term<true>(E, c + k, wx, wy, G[p]);
+                if (cross) cross_term(E, wx, wy, py[p], G[p]);
+            }
         }
         for (uint64_t todo = mcb & ~mdn; todo; todo &= todo - 1) {
             const EdgeRec E = ec[__builtin_ctzll(todo)];
-            cross_term(E, px - E.x0, py - E.y0, py, G);
+            const float wx = px - E.x0;
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) cross_term(E, wx, py[p] - E.y0, py[p], G[p]);
         }
     } else {
         // The minimum and the winding number do not depend on the order:
         // three loops without per-edge tests.
         for (uint64_t todo = mdn & mcb; todo; todo &= todo - 1) {
             const EdgeRec E = ec[__builtin_ctzll(todo)];
-            const float wx = px - E.x0, wy = py - E.y0;
-            dist_term<false>(E, 0, wx, wy, G);
-            cross_term(E, wx, wy, py, G);
+            const float wx = px - E.x0;
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) {
+                const float wy = py[p] - E.y0;
+                dist_term<false>(E, 0, wx, wy, G[p]);
+                cross_term(E, wx, wy, py[p], G[p]);
+            }
         }
         for (uint64_t todo = mdn & ~mcb; todo; todo &= todo - 1) {
             const EdgeRec E = ec[__builtin_ctzll(todo)];
-            dist_term<false>(E, 0, px - E.x0, py - E.y0, G);
+            const float wx = px - E.x0;
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) dist_term<false>(E, 0, wx, py[p] - E.y0, G[p]);
         }
         for (uint64_t todo = mcb & ~mdn; todo; todo &= todo - 1) {
             const EdgeRec E = ec[__builtin_ctzll(todo)];
-            cross_term(E, px - E.x0, py - E.y0, py, G);
+            const float wx = px - E.x0;
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) cross_term(E, wx, py[p] - E.y0, py[p], G[p]);
         }
     }
 }
@@ -175,22 +215,27 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
 // and crossing terms can matter.  The wave then visits only those edges, in
 // ascending index order (so the best edge is the first strict minimum, as in
 // the reference), loading each one's geometry through the scalar cache.
-template <int MODE, bool BEST>
+template <int MODE, bool BEST, bool COUNT>
 __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& W,
                                               const EdgeCull* __restrict__ culls,
-                                              cptr<EdgeRec> edges, int eps, float px, float py,
-                                              int4 first, Geom& G) {
-    G.min_d2 = 1e30f;
-    G.winding = 0;
-    G.best = -1;
-    G.bproj = 0.0f;
-    G.bdx = 0.0f;
-    G.bdy = 0.0f;
+                                              cptr<EdgeRec> edges, int eps, float px,
+                                              const float (&py)[kPix], int4 first,
+                                              Geom (&G)[kPix], EvalCounts& n, int npix) {
+#pragma unroll
+    for (int p = 0; p < kPix; ++p) {
+        G[p].min_d2 = 1e30f;
+        G[p].winding = 0;
+        G[p].best = -1;
+        G[p].bproj = 0.0f;
+        G[p].bdx = 0.0f;
+        G[p].bdy = 0.0f;
+    }
     // The first chunk's words were loaded ahead by the caller.
     const int c0 = pr.s0 * eps, e1 = pr.s1 * eps;
-    chunk_geometry<MODE, BEST>(first, c0, e1, W, edges, px, py, G);
+    chunk_geometry<MODE, BEST, COUNT>(first, c0, e1, W, edges, px, py, G, n, npix);
     for (int c = c0 + kWave; c < e1; c += kWave)
-        chunk_geometry<MODE, BEST>(load_culls(culls, c, e1), c, e1, W, edges, px, py, G);
+        chunk_geometry<MODE, BEST, COUNT>(load_culls(culls, c, e1), c, e1, W, edges, px, py, G,
+                                          n, npix);
 }
 
 struct Cov {
@@ -228,30 +273,68 @@ __device__ __forceinline__ Cov coverage(const PrimRec& pr, const Geom& G, float 
     return c;
 }
 
-template <int MODE>
-__global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
+__device__ __forceinline__ void flush_counts(const EvalCounts& n,
+                                             unsigned long long* __restrict__ counts) {
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        atomicAdd(counts + 0, (unsigned long long)n.dist);
+        atomicAdd(counts + 1, (unsigned long long)n.cross);
+        atomicAdd(counts + 2, (unsigned long long)n.entries);
+        atomicAdd(counts + 3, (unsigned long long)n.cover);
+    }
+}
+
+// The lane's pixels: column j, rows i[p] = first row of the wave + (lane >> 4)
+// + 4 p, so that each wave covers an 8 x 16 block of its tile.
+struct LanePixels {
+    int j;
+    int i[kPix];
+    bool in_img[kPix];
+    float px;
+    float py[kPix];
+};
+
+__device__ __forceinline__ LanePixels lane_pixels(int r0, int c0, int img_h, int img_w) {
+    LanePixels L;
+    const int lane = threadIdx.x & (kWave - 1);
+    L.j = c0 + (lane & 15);
+    L.px = (float)L.j + 0.5f;
+#pragma unroll
+    for (int p = 0; p < kPix; ++p) {
+        L.i[p] = r0 + (lane >> 4) + 4 * p;
+        L.in_img[p] = (L.i[p] < img_h) & (L.j < img_w);
+        L.py[p] = (float)L.i[p] + 0.5f;
+    }
+    return L;
+}
+
+template <int MODE, bool COUNT>
+__global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, int eps, float* __restrict__ out, float* __restrict__ final_T,
-    int32_t* __restrict__ final_idx) {
+    int32_t* __restrict__ final_idx, unsigned long long* __restrict__ counts) {
     const int tile = xcd_tile(blockIdx.x, ntiles);
     const int tty = tile / tbx, ttx = tile - tty * tbx;
-    const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int i = tty * kTile + wv * 4 + (lane >> 4);
-    const int j = ttx * kTile + (lane & 15);
-    const bool in_img = (i < img_h) & (j < img_w);
-    const float px = (float)j + 0.5f, py = (float)i + 0.5f;
-    const WaveRect W{ttx * kTile, ttx * kTile + kTile - 1, tty * kTile + wv * 4,
-                     tty * kTile + wv * 4 + 3};
+    const int r0 = tty * kTile + wv * kWaveRows;
+    const LanePixels L = lane_pixels(r0, ttx * kTile, img_h, img_w);
+    const WaveRect W{ttx * kTile, ttx * kTile + kTile - 1, r0, r0 + kWaveRows - 1};
     const cptr<int32_t> prim_ids = as_const(prim_ids_g);
     const cptr<PrimRec> prims = as_const(prims_g);
     const cptr<EdgeRec> edges = as_const(edges_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
-    float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
-    int cur = 0;
-    bool done = !in_img;
+    float T[kPix], C0[kPix], C1[kPix], C2[kPix];
+    int cur[kPix];
+    bool done[kPix];
+#pragma unroll
+    for (int p = 0; p < kPix; ++p) {
+        T[p] = 1.0f;
+        C0[p] = C1[p] = C2[p] = 0.0f;
+        cur[p] = 0;
+        done[p] = !L.in_img[p];
+    }
+    EvalCounts n{};
     // The cull words of the next entry's first 64 edges are loaded one entry
     // ahead, so that vector load is in flight while this entry is processed.
     int pid = g0 < g1 ? prim_ids[g0] : 0;
@@ -259,7 +342,14 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
     int4 q_next = g0 < g1 ? load_culls(culls, prims[pid].s0 * eps, prims[pid].s1 * eps)
                           : make_int4(0, -1, 0, -1);
     for (int g = g0; g < g1; ++g) {
-        if (__ballot(!done) == 0) break;
+        bool live[kPix];
+        bool any_live = false;
+#pragma unroll
+        for (int p = 0; p < kPix; ++p) {
+            live[p] = !done[p];
+            any_live |= live[p];
+        }
+        if (__ballot(any_live) == 0) break;
         const PrimRec pr = prims[pid];
         const int ns0 = prims[pid_next].s0, ns1 = prims[pid_next].s1;
         const int pid_after = prim_ids[min(g + 2, g1 - 1)];
@@ -269,31 +359,47 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_fwd(
         pid_next = pid_after;
         const float D2 = pr.cull_d * pr.cull_d;
         if (prim_culled<MODE>(pr, W)) continue;
-        Geom G;
-        prim_geometry<MODE, false>(pr, W, culls, edges, eps, px, py, q, G);
-        if (!done) {
-            const Cov c = coverage<MODE>(pr, G, D2);
+        int npix = 0;
+        if constexpr (COUNT) {
+            npix = wave_count(live);
+            n.entries += 1;
+        }
+        Geom G[kPix];
+        prim_geometry<MODE, false, COUNT>(pr, W, culls, edges, eps, L.px, L.py, q, G, n, npix);
+        if constexpr (COUNT) {
+            bool ex[kPix];
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) ex[p] = live[p] && !(G[p].min_d2 > D2);
+            n.cover += (uint64_t)wave_count(ex);
+        }
+#pragma unroll
+        for (int p = 0; p < kPix; ++p) {
+            if (done[p]) continue;
+            const Cov c = coverage<MODE>(pr, G[p], D2);
             const float alpha = fminf(kAlphaCap, pr.opacity * c.cov);
             if (alpha >= kAlphaMin) {
-                const float nT = T * (1.0f - alpha);
-                const float vis = alpha * T;
-                C0 = __builtin_fmaf(pr.r, vis, C0);
-                C1 = __builtin_fmaf(pr.g, vis, C1);
-                C2 = __builtin_fmaf(pr.b, vis, C2);
-                T = nT;
-                cur = g;
-                if (nT <= kTStop) done = true;
+                const float nT = T[p] * (1.0f - alpha);
+                const float vis = alpha * T[p];
+                C0[p] = __builtin_fmaf(pr.r, vis, C0[p]);
+                C1[p] = __builtin_fmaf(pr.g, vis, C1[p]);
+                C2[p] = __builtin_fmaf(pr.b, vis, C2[p]);
+                T[p] = nT;
+                cur[p] = g;
+                if (nT <= kTStop) done[p] = true;
             }
         }
     }
-    if (in_img) {
-        const size_t pix = (size_t)i * img_w + j;
-        final_T[pix] = T;
-        final_idx[pix] = cur;
-        out[3 * pix + 0] = __builtin_fmaf(T, bg[0], C0);
-        out[3 * pix + 1] = __builtin_fmaf(T, bg[1], C1);
-        out[3 * pix + 2] = __builtin_fmaf(T, bg[2], C2);
+#pragma unroll
+    for (int p = 0; p < kPix; ++p) {
+        if (!L.in_img[p]) continue;
+        const size_t pix = (size_t)L.i[p] * img_w + L.j;
+        final_T[pix] = T[p];
+        final_idx[pix] = cur[p];
+        out[3 * pix + 0] = __builtin_fmaf(T[p], bg[0], C0[p]);
+        out[3 * pix + 1] = __builtin_fmaf(T[p], bg[1], C1[p]);
+        out[3 * pix + 2] = __builtin_fmaf(T[p], bg[2], C2[p]);
     }
+    if constexpr (COUNT) flush_counts(n, counts);
 }
 
 // n / eps for 0 <= n < 2^31 with magic = ceil(2^32 / eps) (eps >= 2): the
@@ -323,14 +429,15 @@ __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
 // Backward: the reverse traversal of cubic_splatting.py:1339-1649 (fill) and
 // cubic_polyline_splatting.py:393-658 (stroke).  Per-pixel terms are those of
 // the reference; the sums differ in how they are formed:
-//   * per-primitive gradients: DPP wave sum, one atomic per wave and entry;
-//   * geometry: each lane folds its best edge's endpoint gradients straight
+//   * per-primitive gradients: the lane's two pixels are added, then one DPP
+//     wave reduction and one atomic per value, wave and entry;
+//   * geometry: each pixel folds its best edge's endpoint gradients straight
 //     into the 8 control-point gradients of the edge's cubic segment with the
 //     reference's accumulation weights (cubic_splatting.py:2308-2396), then
-//     lanes that share a segment are summed (one leader pass per distinct
-//     segment) and one lane adds the 8 values to v_cubics_px.
-template <int MODE>
-__global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
+//     the pixels that share a segment are summed (one leader pass per distinct
+//     segment) and one 8-lane atomic adds the 8 values to v_cubics_px.
+template <int MODE, bool COUNT>
+__global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
@@ -338,44 +445,60 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
-    float* __restrict__ isect_contrib) {
+    float* __restrict__ isect_contrib, unsigned long long* __restrict__ counts) {
     const int tile = xcd_tile(blockIdx.x, ntiles);
     const int tty = tile / tbx, ttx = tile - tty * tbx;
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int i = tty * kTile + wv * 4 + (lane >> 4);
-    const int j = ttx * kTile + (lane & 15);
-    const bool in_img = (i < img_h) & (j < img_w);
-    const float px = (float)j + 0.5f, py = (float)i + 0.5f;
-    const WaveRect W{ttx * kTile, ttx * kTile + kTile - 1, tty * kTile + wv * 4,
-                     tty * kTile + wv * 4 + 3};
+    const int r0 = tty * kTile + wv * kWaveRows;
+    const LanePixels L = lane_pixels(r0, ttx * kTile, img_h, img_w);
+    const WaveRect W{ttx * kTile, ttx * kTile + kTile - 1, r0, r0 + kWaveRows - 1};
     const cptr<int32_t> prim_ids = as_const(prim_ids_g);
     const cptr<PrimRec> prims = as_const(prims_g);
     const cptr<EdgeRec> edges = as_const(edges_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
-    const size_t pix = in_img ? (size_t)i * img_w + j : 0;
-    float T = in_img ? final_T[pix] : 1.0f;
-    const float T_final = T;
-    const int fidx = in_img ? final_idx[pix] : -1;
-    const float v0 = in_img ? v_out[3 * pix + 0] : 0.0f;
-    const float v1 = in_img ? v_out[3 * pix + 1] : 0.0f;
-    const float v2 = in_img ? v_out[3 * pix + 2] : 0.0f;
-    const float bg_dot = __builtin_fmaf(bg[2], v2, __builtin_fmaf(bg[1], v1, bg[0] * v0));
+    const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
+    float T[kPix], T_final[kPix], v0[kPix], v1[kPix], v2[kPix], bg_dot[kPix];
+    float b0[kPix], b1[kPix], b2[kPix];
+    int fidx[kPix];
+    int fmax = -1;
+#pragma unroll
+    for (int p = 0; p < kPix; ++p) {
+        const bool in = L.in_img[p];
+        const size_t pix = in ? (size_t)L.i[p] * img_w + L.j : 0;
+        T[p] = in ? final_T[pix] : 1.0f;
+        T_final[p] = T[p];
+        fidx[p] = in ? final_idx[pix] : -1;
+        v0[p] = in ? v_out[3 * pix + 0] : 0.0f;
+        v1[p] = in ? v_out[3 * pix + 1] : 0.0f;
+        v2[p] = in ? v_out[3 * pix + 2] : 0.0f;
+        bg_dot[p] = __builtin_fmaf(bg2, v2[p], __builtin_fmaf(bg1, v1[p], bg0 * v0[p]));
+        b0[p] = b1[p] = b2[p] = 0.0f;
+        fmax = max(fmax, fidx[p]);
+    }
     const bool want_contrib = (contrib_rgb != nullptr) | (isect_contrib != nullptr);
     const float inv_e = 1.0f / (float)eps;
+    EvalCounts n{};
 
-    float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
     // The wave maximum is uniform; readfirstlane tells the compiler so, which
     // keeps every load that depends on the entry index scalar.
-    const int gstart = min(g1 - 1, __builtin_amdgcn_readfirstlane(wave_max_i(fidx)));
+    const int gstart = min(g1 - 1, __builtin_amdgcn_readfirstlane(wave_max_i(fmax)));
     // As in the forward, the next entry's first cull words are loaded one
     // entry ahead (here the next entry is g - 1).
     int pid = gstart >= g0 ? prim_ids[gstart] : 0;
     int pid_next = prim_ids[max(gstart - 1, g0)];
     int4 q_next = gstart >= g0 ? load_culls(culls, prims[pid].s0 * eps, prims[pid].s1 * eps)
                                : make_int4(0, -1, 0, -1);
+    const int slot = reduce8_slot(lane & 7);
+    const bool adder = (lane & ~7) == 8;
     for (int g = gstart; g >= g0; --g) {
-        const bool valid = in_img & (g <= fidx);
+        bool valid[kPix];
+        bool any_valid = false;
+#pragma unroll
+        for (int p = 0; p < kPix; ++p) {
+            valid[p] = L.in_img[p] & (g <= fidx[p]);
+            any_valid |= valid[p];
+        }
         const int pid_cur = pid;
         const PrimRec pr = prims[pid_cur];
         const int ns0 = prims[pid_next].s0, ns1 = prims[pid_next].s1;
@@ -384,66 +507,84 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
         q_next = load_culls(culls, ns0 * eps, ns1 * eps);
         pid = pid_next;
         pid_next = pid_after;
-        if (__ballot(valid) == 0) continue;
+        if (__ballot(any_valid) == 0) continue;
         const float D2 = pr.cull_d * pr.cull_d;
         if (prim_culled<MODE>(pr, W)) continue;
-        Geom G;
-        prim_geometry<MODE, true>(pr, W, culls, edges, eps, px, py, q, G);
-        float vr = 0.0f, vg = 0.0f, vb = 0.0f, vop = 0.0f, vis2 = 0.0f, vsw = 0.0f;
-        float cr = 0.0f, cg = 0.0f, cb = 0.0f;
-        float gx = 0.0f, gy = 0.0f;
-        bool contrib = false, geom = false;
-        if (valid) {
-            const Cov c = coverage<MODE>(pr, G, D2);
+        int npix = 0;
+        if constexpr (COUNT) {
+            npix = wave_count(valid);
+            n.entries += 1;
+        }
+        Geom G[kPix];
+        prim_geometry<MODE, true, COUNT>(pr, W, culls, edges, eps, L.px, L.py, q, G, n, npix);
+        if constexpr (COUNT) {
+            bool ex[kPix];
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) ex[p] = valid[p] && !(G[p].min_d2 > D2);
+            n.cover += (uint64_t)wave_count(ex);
+        }
+        // Per-primitive sums over the lane's pixels: v_r, v_g, v_b, v_opacity,
+        // v_inv_sigma2, v_stroke; contribution sums r, g, b, r + g + b.
+        float pv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        float cv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float gx[kPix], gy[kPix];
+        bool geom[kPix];
+        bool contrib = false;
+#pragma unroll
+        for (int p = 0; p < kPix; ++p) {
+            gx[p] = gy[p] = 0.0f;
+            geom[p] = false;
+            if (!valid[p]) continue;
+            const Cov c = coverage<MODE>(pr, G[p], D2);
             const float op = pr.opacity;
             const float alpha = fminf(kAlphaCap, op * c.cov);
-            if (alpha >= kAlphaMin) {
-                contrib = true;
-                const float ra = grad_rcp(1.0f - alpha);
-                T = T * ra;
-                const float fac = alpha * T;
-                vr = fac * v0;
-                vg = fac * v1;
-                vb = fac * v2;
-                if (want_contrib) {
-                    cr = fac * pr.r;
-                    cg = fac * pr.g;
-                    cb = fac * pr.b;
+            if (!(alpha >= kAlphaMin)) continue;
+            contrib = true;
+            const float ra = grad_rcp(1.0f - alpha);
+            T[p] = T[p] * ra;
+            const float fac = alpha * T[p];
+            pv[0] = __builtin_fmaf(fac, v0[p], pv[0]);
+            pv[1] = __builtin_fmaf(fac, v1[p], pv[1]);
+            pv[2] = __builtin_fmaf(fac, v2[p], pv[2]);
+            if (want_contrib) {
+                const float cr = fac * pr.r, cg = fac * pr.g, cb = fac * pr.b;
+                cv[0] += cr;
+                cv[1] += cg;
+                cv[2] += cb;
+                cv[3] += cr + cg + cb;
+            }
+            float va = __builtin_fmaf(pr.r, T[p], -(b0[p] * ra)) * v0[p];
+            va = __builtin_fmaf(__builtin_fmaf(pr.g, T[p], -(b1[p] * ra)), v1[p], va);
+            va = __builtin_fmaf(__builtin_fmaf(pr.b, T[p], -(b2[p] * ra)), v2[p], va);
+            va = __builtin_fmaf(T_final[p] * ra, -bg_dot[p], va);
+            b0[p] = __builtin_fmaf(pr.r, fac, b0[p]);
+            b1[p] = __builtin_fmaf(pr.g, fac, b1[p]);
+            b2[p] = __builtin_fmaf(pr.b, fac, b2[p]);
+            if (!(alpha < kAlphaCap)) continue;
+            pv[3] = __builtin_fmaf(c.cov, va, pv[3]);
+            if (MODE == 0) {
+                const float v_cov = op * va;
+                const float v_logit = -v_cov * c.cov * (1.0f - c.cov);
+                const float v_is = v_logit * c.sgn * c.dist * 2.0f;
+                pv[4] += v_is * 0.5f * grad_rcp(fmaxf(pr.inv_sigma, kEps));
+                if (c.dist > kEps && G[p].best >= 0) {
+                    const float v_dist = v_logit * c.sgn * pr.inv_sigma * 2.0f;
+                    const float rd = grad_rcp(c.dist);
+                    gx[p] = v_dist * G[p].bdx * rd;
+                    gy[p] = v_dist * G[p].bdy * rd;
+                    geom[p] = true;
                 }
-                float va = __builtin_fmaf(pr.r, T, -(b0 * ra)) * v0;
-                va = __builtin_fmaf(__builtin_fmaf(pr.g, T, -(b1 * ra)), v1, va);
-                va = __builtin_fmaf(__builtin_fmaf(pr.b, T, -(b2 * ra)), v2, va);
-                va = __builtin_fmaf(T_final * ra, -bg_dot, va);
-                b0 = __builtin_fmaf(pr.r, fac, b0);
-                b1 = __builtin_fmaf(pr.g, fac, b1);
-                b2 = __builtin_fmaf(pr.b, fac, b2);
-                if (alpha < kAlphaCap) {
-                    vop = c.cov * va;
-                    if (MODE == 0) {
-                        const float v_cov = op * va;
-                        const float v_logit = -v_cov * c.cov * (1.0f - c.cov);
-                        const float v_is = v_logit * c.sgn * c.dist * 2.0f;
-                        vis2 = v_is * 0.5f * grad_rcp(fmaxf(pr.inv_sigma, kEps));
-                        if (c.dist > kEps && G.best >= 0) {
-                            const float v_dist = v_logit * c.sgn * pr.inv_sigma * 2.0f;
-                            const float rd = grad_rcp(c.dist);
-                            gx = v_dist * G.bdx * rd;
-                            gy = v_dist * G.bdy * rd;
-                            geom = true;
-                        }
-                    } else {
-                        const float v_sigma = -op * c.cov * va;
-                        vis2 = 0.5f * c.ed * c.ed * v_sigma;
-                        if (c.ed > 0.0f) {
-                            const float v_e = v_sigma * c.ed * pr.inv_sigma2;
-                            vsw = -0.5f * v_e;
-                            if (c.dist > kEps && G.best >= 0) {
-                                const float rd = grad_rcp(c.dist);
-                                gx = v_e * G.bdx * rd;
-                                gy = v_e * G.bdy * rd;
-                                geom = true;
-                            }
-                        }
+            } else {
+                const float v_sigma = -op * c.cov * va;
+                pv[4] += 0.5f * c.ed * c.ed * v_sigma;
+                if (c.ed > 0.0f) {
+                    const float v_e = v_sigma * c.ed * pr.inv_sigma2;
+                    pv[5] += -0.5f * v_e;
+                    if (c.dist > kEps && G[p].best >= 0) {
+                        const float rd = grad_rcp(c.dist);
+                        gx[p] = v_e * G[p].bdx * rd;
+                        gy[p] = v_e * G[p].bdy * rd;
+                        geom[p] = true;
                     }
                 }
             }
@@ -451,10 +592,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
         if (__ballot(contrib) == 0) continue;
         // Per-primitive gradients: one 8-way transposed reduction; lanes 8..15
         // then hold the totals and each adds one of them.
-        const int slot = reduce8_slot(lane & 7);
-        const bool adder = (lane & ~7) == 8;
         {
-            const float pv[8] = {vr, vg, vb, vop, vis2, MODE == 1 ? vsw : 0.0f, 0.0f, 0.0f};
             const float t = wave_reduce8(pv);
             if (adder && slot < (MODE == 1 ? 6 : 5)) {
                 float* dst = slot < 3 ? v_colors + 3 * pid_cur + slot
@@ -465,45 +603,63 @@ __global__ __launch_bounds__(kBlockThreads) void k_raster_bwd(
             }
         }
         if (want_contrib) {
-            const float cv[8] = {cr, cg, cb, cr + cg + cb, 0.0f, 0.0f, 0.0f, 0.0f};
-            const float t = wave_reduce8(cv);
+            const float cw[8] = {cv[0], cv[1], cv[2], cv[3], 0.0f, 0.0f, 0.0f, 0.0f};
+            const float t = wave_reduce8(cw);
             if (adder && slot < 3 && contrib_rgb) atomicAdd(contrib_rgb + 3 * pid_cur + slot, t);
             if (adder && slot == 3 && isect_contrib) atomicAdd(isect_contrib + g, t);
         }
-        // Geometry: endpoint gradients ((1-t) g, t g) of the best edge, folded
-        // into its segment's control points.
-        uint64_t pending = __ballot(geom);
-        if (pending == 0) continue;
-        int gseg = -1;
-        float cp[8];
+        // Geometry: endpoint gradients ((1-t) g, t g) of each pixel's best
+        // edge, folded into its segment's control points.
+        uint64_t pend[kPix];
+        uint64_t any_pend = 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) cp[k] = 0.0f;
-        if (geom) {
-            gseg = div_eps(G.best, eps, eps_magic);
-            const int el = G.best - gseg * eps;
+        for (int p = 0; p < kPix; ++p) {
+            pend[p] = __ballot(geom[p]);
+            any_pend |= pend[p];
+        }
+        if (any_pend == 0) continue;
+        int gseg[kPix];
+        float cp[kPix][8];
+#pragma unroll
+        for (int p = 0; p < kPix; ++p) {
+            gseg[p] = -1;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) cp[p][k] = 0.0f;
+            if (!geom[p]) continue;
+            gseg[p] = div_eps(G[p].best, eps, eps_magic);
+            const int el = G[p].best - gseg[p] * eps;
             float bs[4], be[4];
             seg_basis(el, inv_e, bs);
             seg_basis(el + 1, inv_e, be);
-            const float sx = (1.0f - G.bproj) * gx, sy = (1.0f - G.bproj) * gy;
-            const float ex = G.bproj * gx, ey = G.bproj * gy;
+            const float sx = (1.0f - G[p].bproj) * gx[p], sy = (1.0f - G[p].bproj) * gy[p];
+            const float ex = G[p].bproj * gx[p], ey = G[p].bproj * gy[p];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                cp[2 * k] = __builtin_fmaf(ex, be[k], sx * bs[k]);
-                cp[2 * k + 1] = __builtin_fmaf(ey, be[k], sy * bs[k]);
+                cp[p][2 * k] = __builtin_fmaf(ex, be[k], sx * bs[k]);
+                cp[p][2 * k + 1] = __builtin_fmaf(ey, be[k], sy * bs[k]);
             }
         }
-        while (pending) {
-            const int leader = (int)__builtin_ctzll(pending);
-            const int s = __builtin_amdgcn_readlane(gseg, leader);
-            const bool mine = gseg == s;
-            pending &= ~__ballot(mine);
-            float sv[8];
+        while (any_pend) {
+            // Leader: the lowest pending pixel (first pixel row before the
+            // second); its segment is processed for every pixel that has it.
+            const bool first_row = pend[0] != 0;
+            const int leader = (int)__builtin_ctzll(first_row ? pend[0] : pend[kPix - 1]);
+            const int s = __builtin_amdgcn_readlane(first_row ? gseg[0] : gseg[kPix - 1], leader);
+            float sv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            any_pend = 0;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) sv[k] = mine ? cp[k] : 0.0f;
+            for (int p = 0; p < kPix; ++p) {
+                const bool mine = gseg[p] == s;
+                pend[p] &= ~__ballot(mine);
+                any_pend |= pend[p];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) sv[k] += mine ? cp[p][k] : 0.0f;
+            }
             const float t = wave_reduce8(sv);
             if (adder) atomicAdd(v_cubics + 8 * (size_t)s + slot, t);
         }
     }
+    if constexpr (COUNT) flush_counts(n, counts);
 }
 
 // _accumulate_edge_grads_to_cubics_kernel (cubic_splatting.py:2308-2396) and
@@ -580,25 +736,39 @@ struct RasterArgs {
     const int32_t* fidx;
     const float* v_out;
     float *v_cub, *v_col, *v_op, *v_is2, *v_sw, *c_rgb, *c_isect;
+    // evaluation counters of the counting entry points
+    unsigned long long* counts;
     hipStream_t stream;
 };
 
-template <int MODE>
+template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
-    hipLaunchKernelGGL((k_raster_fwd<MODE>), dim3(a.nt), dim3(kBlockThreads), 0, a.stream,
-                       a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx, a.nt,
-                       a.eps, a.out, a.final_T, a.final_idx);
+    hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.nt), dim3(kRasterThreads), 0,
+                       a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
+                       a.nt, a.eps, a.out, a.final_T, a.final_idx, a.counts);
 }
 
-template <int MODE>
+template <int MODE, bool COUNT>
 static void launch_bwd(const RasterArgs& a) {
     // ceil(2^32 / eps) for div_eps (unused when eps == 1).
     const uint32_t magic =
         a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
-    hipLaunchKernelGGL((k_raster_bwd<MODE>), dim3(a.nt), dim3(kBlockThreads), 0, a.stream,
-                       a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx, a.nt,
-                       a.eps, magic, a.fT, a.fidx, a.v_out, a.v_cub, a.v_col, a.v_op, a.v_is2, a.v_sw, a.c_rgb,
-                       a.c_isect);
+    hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT>), dim3(a.nt), dim3(kRasterThreads), 0,
+                       a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
+                       a.nt, a.eps, magic, a.fT, a.fidx, a.v_out, a.v_cub, a.v_col, a.v_op,
+                       a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.counts);
+}
+
+template <bool COUNT>
+static void launch_fwd_mode(const RasterArgs& a) {
+    if (a.mode == 0) launch_fwd<0, COUNT>(a);
+    else launch_fwd<1, COUNT>(a);
+}
+
+template <bool COUNT>
+static void launch_bwd_mode(const RasterArgs& a) {
+    if (a.mode == 0) launch_bwd<0, COUNT>(a);
+    else launch_bwd<1, COUNT>(a);
 }
 
 static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* bins,
@@ -622,13 +792,12 @@ static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* b
     return a;
 }
 
-extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
-                                    const int32_t* tile_bins, const void* edges,
-                                    const void* edge_culls, const void* prim_recs,
-                                    const float* background,
-                                    int32_t img_h, int32_t img_w, int32_t edges_per_segment,
-                                    float* out_img, float* final_Ts,
-                                    int32_t* final_idx, hipStream_t stream) {
+static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
+                             const int32_t* tile_bins, const void* edges, const void* edge_culls,
+                             const void* prim_recs, const float* background, int32_t img_h,
+                             int32_t img_w, int32_t edges_per_segment, float* out_img,
+                             float* final_Ts, int32_t* final_idx,
+                             unsigned long long* eval_counts, hipStream_t stream) {
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1 ||
         img_h > kMaxImageDim || img_w > kMaxImageDim)
         return CS_ERR_ARGS;
@@ -637,22 +806,48 @@ extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted
     a.out = out_img;
     a.final_T = final_Ts;
     a.final_idx = final_idx;
-    if (mode == 0) launch_fwd<0>(a);
-    else launch_fwd<1>(a);
+    a.counts = eval_counts;
+    if (eval_counts) launch_fwd_mode<true>(a);
+    else launch_fwd_mode<false>(a);
     return raster_status();
 }
 
-extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
-                                     const int32_t* tile_bins, const void* edges,
-                                     const void* edge_culls, const void* prim_recs,
-                                     const float* background,
-                                     int32_t img_h, int32_t img_w,
-                                     int32_t edges_per_segment, const float* final_Ts,
-                                     const int32_t* final_idx, const float* v_output,
-                                     float* v_cubics_px, float* v_colors, float* v_opacities,
-                                     float* v_inv_sigma2s, float* v_stroke_widths,
-                                     float* curve_contrib_rgb, float* curve_isect_contrib,
-                                     hipStream_t stream) {
+extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
+                                    const int32_t* tile_bins, const void* edges,
+                                    const void* edge_culls, const void* prim_recs,
+                                    const float* background,
+                                    int32_t img_h, int32_t img_w, int32_t edges_per_segment,
+                                    float* out_img, float* final_Ts,
+                                    int32_t* final_idx, hipStream_t stream) {
+    return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
+                             background, img_h, img_w, edges_per_segment, out_img, final_Ts,
+                             final_idx, nullptr, stream);
+}
+
+extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
+                                            const int32_t* tile_bins, const void* edges,
+                                            const void* edge_culls, const void* prim_recs,
+                                            const float* background, int32_t img_h,
+                                            int32_t img_w, int32_t edges_per_segment,
+                                            float* out_img, float* final_Ts, int32_t* final_idx,
+                                            unsigned long long* eval_counts,
+                                            hipStream_t stream) {
+    if (!eval_counts) return CS_ERR_ARGS;
+    return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
+                             background, img_h, img_w, edges_per_segment, out_img, final_Ts,
+                             final_idx, eval_counts, stream);
+}
+
+static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
+                              const int32_t* tile_bins, const void* edges,
+                              const void* edge_culls, const void* prim_recs,
+                              const float* background, int32_t img_h, int32_t img_w,
+                              int32_t edges_per_segment, const float* final_Ts,
+                              const int32_t* final_idx, const float* v_output,
+                              float* v_cubics_px, float* v_colors, float* v_opacities,
+                              float* v_inv_sigma2s, float* v_stroke_widths,
+                              float* curve_contrib_rgb, float* curve_isect_contrib,
+                              unsigned long long* eval_counts, hipStream_t stream) {
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1 ||
         img_h > kMaxImageDim || img_w > kMaxImageDim)
         return CS_ERR_ARGS;
@@ -669,9 +864,43 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
     a.v_sw = v_stroke_widths;
     a.c_rgb = curve_contrib_rgb;
     a.c_isect = curve_isect_contrib;
-    if (mode == 0) launch_bwd<0>(a);
-    else launch_bwd<1>(a);
+    a.counts = eval_counts;
+    if (eval_counts) launch_bwd_mode<true>(a);
+    else launch_bwd_mode<false>(a);
     return raster_status();
+}
+
+extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
+                                     const int32_t* tile_bins, const void* edges,
+                                     const void* edge_culls, const void* prim_recs,
+                                     const float* background,
+                                     int32_t img_h, int32_t img_w,
+                                     int32_t edges_per_segment, const float* final_Ts,
+                                     const int32_t* final_idx, const float* v_output,
+                                     float* v_cubics_px, float* v_colors, float* v_opacities,
+                                     float* v_inv_sigma2s, float* v_stroke_widths,
+                                     float* curve_contrib_rgb, float* curve_isect_contrib,
+                                     hipStream_t stream) {
+    return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
+                              background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
+                              v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
+                              v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
+                              stream);
+}
+
+extern "C" int cs_rasterize_backward_counted(
+    int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
+    const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
+    int32_t img_w, int32_t edges_per_segment, const float* final_Ts, const int32_t* final_idx,
+    const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
+    float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
+    float* curve_isect_contrib, unsigned long long* eval_counts, hipStream_t stream) {
+    if (!eval_counts) return CS_ERR_ARGS;
+    return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
+                              background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
+                              v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
+                              v_stroke_widths, curve_contrib_rgb, curve_isect_contrib,
+                              eval_counts, stream);
 }
 
 extern "C" int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg,

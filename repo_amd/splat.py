@@ -183,24 +183,38 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
                   tile_bins=tile_bins)
 
 
-def rasterize_forward(b: Binned, background: torch.Tensor):
+def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
+    """(image [H,W,3], final_Ts, final_idx).  With eval_counts (int64 [4],
+    zeroed, on the device) the counting instantiation runs and adds the
+    evaluation counts of cs_rasterize_forward_counted into it."""
     dev = b.edges.device
     out = torch.empty((b.img_h, b.img_w, 3), dtype=torch.float32, device=dev)
     final_T = torch.empty((b.img_h, b.img_w), dtype=torch.float32, device=dev)
     final_idx = torch.empty((b.img_h, b.img_w), dtype=torch.int32, device=dev)
-    with N.prof("cubic.fwd.rast"):
-        N.call("cs_rasterize_forward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
-               N.ptr(b.edges), N.ptr(b.edge_culls), N.ptr(b.prim_recs), N.ptr(background),
-               b.img_h, b.img_w, b.edges_per_segment, N.ptr(out), N.ptr(final_T),
-               N.ptr(final_idx), N.stream(dev))
+    args = (b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins), N.ptr(b.edges),
+            N.ptr(b.edge_culls), N.ptr(b.prim_recs), N.ptr(background), b.img_h, b.img_w,
+            b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx))
+    if eval_counts is not None:
+        N.call("cs_rasterize_forward_counted", *args, N.ptr(_counts_buffer(eval_counts)),
+               N.stream(dev))
+    else:
+        with N.prof("cubic.fwd.rast"):
+            N.call("cs_rasterize_forward", *args, N.stream(dev))
     return out, final_T, final_idx
 
 
+def _counts_buffer(t):
+    if t.dtype != torch.int64 or t.numel() != 4 or not t.is_contiguous():
+        raise ValueError("eval_counts must be a contiguous int64 tensor of 4 elements")
+    return t
+
+
 def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
-                       curve_contrib_rgb=None, curve_isect_contrib=None):
+                       curve_contrib_rgb=None, curve_isect_contrib=None, eval_counts=None):
     """Returns (v_cubics_px [nseg,4,2], v_colors [P,3], v_opacities [P],
     v_inv_sigma2s [P], v_stroke_widths [P] or None), accumulated into fresh
-    zero buffers (cubic_splatting.py:2572-2747)."""
+    zero buffers (cubic_splatting.py:2572-2747).  eval_counts as for
+    rasterize_forward (cs_rasterize_backward_counted)."""
     dev = b.edges.device
     P = b.nprim
     zeros = torch.zeros((b.nseg * 8 + P * (6 if b.mode == MODE_STROKE else 5),),
@@ -211,13 +225,17 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_opac = rest[3 * P: 4 * P]
     v_is2 = rest[4 * P: 5 * P]
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
-    with N.prof("cubic.bwd.rast"):
-        N.call("cs_rasterize_backward", b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins),
-               N.ptr(b.edges), N.ptr(b.edge_culls), N.ptr(b.prim_recs), N.ptr(background),
-               b.img_h, b.img_w, b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx),
-               N.ptr(v_output),
-               N.ptr(v_px), N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw),
-               N.ptr(curve_contrib_rgb), N.ptr(curve_isect_contrib), N.stream(dev))
+    args = (b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins), N.ptr(b.edges),
+            N.ptr(b.edge_culls), N.ptr(b.prim_recs), N.ptr(background), b.img_h, b.img_w,
+            b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(v_output), N.ptr(v_px),
+            N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
+            N.ptr(curve_isect_contrib))
+    if eval_counts is not None:
+        N.call("cs_rasterize_backward_counted", *args, N.ptr(_counts_buffer(eval_counts)),
+               N.stream(dev))
+    else:
+        with N.prof("cubic.bwd.rast"):
+            N.call("cs_rasterize_backward", *args, N.stream(dev))
     return v_px, v_colors, v_opac, v_is2, v_sw
 
 
