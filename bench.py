@@ -28,8 +28,9 @@ FP32_PEAK_TFLOPS = 157.3
 # fp32 operations of one (pixel, edge) term of the reference's edge loop
 # (cubic_splatting.py:1095-1134): distance 15 (2 sub, mul + fma, 2 clamp,
 # 2 fma, mul + fma, min; fma = 2), crossing 6 (2 compares, mul + fma,
-# compare).  Strokes have no crossing term.
-FLOPS_DIST, FLOPS_CROSS = 15.0, 6.0
+# compare).  Strokes have no crossing term.  A far edge's crossing term
+# decided by its row span alone: 2 compares + 1 add.
+FLOPS_DIST, FLOPS_CROSS, FLOPS_ROW = 15.0, 6.0, 3.0
 FLOPS_PER_EVAL = {0: FLOPS_DIST + FLOPS_CROSS, 1: FLOPS_DIST}
 RASTER_LABELS = {"cubic.fwd.rast": "raster_fwd", "cubic.bwd.rast": "raster_bwd"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_{kernel}_cfg{cfg}.json")
@@ -179,18 +180,18 @@ def performed_evaluations(b, bg, T, idx, v):
     forward and one backward launch on this scene: the counting entry points
     cs_rasterize_{forward,backward}_counted, run once outside the timed region.
     Returns {"raster_fwd": counts, "raster_bwd": counts} with counts =
-    {dist, cross, entries, cover}."""
+    {dist, cross, row, entries, cover}."""
     import torch
     from repo_amd import splat
     res = {}
     for name in ("raster_fwd", "raster_bwd"):
-        c = torch.zeros(4, dtype=torch.int64, device=T.device)
+        c = torch.zeros(5, dtype=torch.int64, device=T.device)
         if name == "raster_fwd":
             splat.rasterize_forward(b, bg, eval_counts=c)
         else:
             splat.rasterize_backward(b, bg, T, idx, v, eval_counts=c)
-        d, x, e, cov = (int(t) for t in c.tolist())
-        res[name] = {"dist": d, "cross": x, "entries": e, "cover": cov}
+        d, x, r, e, cov = (int(t) for t in c.tolist())
+        res[name] = {"dist": d, "cross": x, "row": r, "entries": e, "cover": cov}
     return res
 
 
@@ -310,7 +311,7 @@ def main():
     dom = max(launch_ms, key=lambda k: launch_ms[k])
     dom_ms = launch_ms[dom]
     pc = performed[dom]
-    flops = pc["dist"] * FLOPS_DIST + pc["cross"] * FLOPS_CROSS
+    flops = pc["dist"] * FLOPS_DIST + pc["cross"] * FLOPS_CROSS + pc["row"] * FLOPS_ROW
     achieved = flops / (dom_ms * 1e-3) / 1e12
     ref_units = evals_bwd if dom == "raster_bwd" else evals_fwd
     ref_equiv = ref_units * FLOPS_PER_EVAL[b.mode] / (dom_ms * 1e-3) / 1e12
@@ -318,8 +319,9 @@ def main():
                 "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
                 "traffic": load_traffic(dom, args.config), "kernel": dom,
                 "launch_ms": round(dom_ms, 4),
-                "units_per_launch": {"dist_terms": pc["dist"], "cross_terms": pc["cross"]},
-                "flops_per_unit": {"dist": FLOPS_DIST, "cross": FLOPS_CROSS},
+                "units_per_launch": {"dist_terms": pc["dist"], "cross_terms": pc["cross"],
+                                     "row_cross_terms": pc["row"]},
+                "flops_per_unit": {"dist": FLOPS_DIST, "cross": FLOPS_CROSS, "row": FLOPS_ROW},
                 "reference_equivalent_TFLOPs": round(ref_equiv, 2),
                 "note": "fp32 vector-ALU compute roof (no matrix instructions on this path), "
                         "priced against the published fp32 peak; units are the (edge, pixel) "

@@ -149,13 +149,15 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
                           float* curve_isect_contrib, hipStream_t stream);
 
 /* cs_rasterize_forward / cs_rasterize_backward with the same results, plus
- * evaluation counts added into eval_counts[4] (device uint64, caller-zeroed):
- * [0] distance terms and [1] crossing terms evaluated, each an (edge, pixel)
- * pair of the reference's edge loop (cubic_splatting.py:1095-1134) that the
- * kernel did not prove irrelevant; [2] (wave, list entry) pairs processed past
- * the primitive cull; [3] exact coverage evaluations (pixels within the cull
- * distance).  Measurement only (no reference counterpart): the counting
- * instantiation is slower than the plain one. */
+ * evaluation counts added into eval_counts[5] (device uint64, caller-zeroed),
+ * each an (edge, pixel) term of the reference's edge loop
+ * (cubic_splatting.py:1095-1134) that the kernel evaluated rather than
+ * proved irrelevant: [0] distance terms, [1] crossing terms evaluated with
+ * the cross product, [2] crossing terms of far edges decided by the row span
+ * alone; then [3] (wave, list entry) pairs processed past the primitive cull
+ * and [4] exact coverage evaluations (pixels within the cull distance).
+ * Measurement only (no reference counterpart): the counting instantiation is
+ * slower than the plain one. */
 int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                  const int32_t* tile_bins, const void* edges,
                                  const void* edge_culls, const void* prim_recs,

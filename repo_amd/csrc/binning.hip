@@ -244,7 +244,9 @@ __global__ __launch_bounds__(256) void k_project_flatten(
             const IRange cy = pixel_range(ey0, ey1, 0.0f);
             reinterpret_cast<int4*>(ec)[i - 1] =
                 make_int4(packed_range(ny, kWaveRowsExt), packed_range(cy, kWaveRowsExt),
-                          packed_range(nx, kWaveColsExt), 0);
+                          packed_range(nx, kWaveColsExt),
+                          (fabsf(prevx) <= kFarCrossMaxX && fabsf(x) <= kFarCrossMaxX)
+                              ? kCullFarCrossExact : 0);
         }
         prevx = x;
         prevy = y;

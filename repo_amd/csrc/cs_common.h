@@ -57,8 +57,21 @@ struct alignas(16) EdgeRec {
 // vector load.  Packing limits pixel indices to int16, so images are at most
 // kMaxImageDim on a side.
 struct alignas(16) EdgeCull {
-    int32_t ny, cy, nx, pad;
+    int32_t ny, cy, nx, flags;
 };
+
+// EdgeCull.flags bit: the edge's x coordinates lie within +-kFarCrossMaxX, so
+// for any wave whose near columns it misses, the sign of its crossing cross
+// product is decided by geometry alone.  Such an edge lies at least D + 1 >=
+// 1.25 px (D >= 0.25 px) horizontally from every pixel of the wave, on one
+// side: |cr| = |vy| |x_c - px| >= 1.25 |vy|, while the fp32 evaluation of cr
+// = fma(wy, vx, -(wx vy)) differs from the exact value by at most
+// 2^-24 |vy| (2 |wx| + |vx|) (|wy| <= |vy| on a crossing row), which stays
+// below 1.25 |vy| for |x| <= 2^20 and pixel centres below 16384.  Its term is
+// then +1 / -1 on every row it spans when it lies right of the wave and 0
+// when it lies left, exactly as the per-pixel test evaluates it.
+constexpr int32_t kCullFarCrossExact = 1;
+constexpr float kFarCrossMaxX = 1048576.0f;
 constexpr int kMaxImageDim = 16384;
 
 __device__ __forceinline__ int32_t pack_lo_span(int32_t lo, int32_t span) {

@@ -125,12 +125,13 @@ __device__ __forceinline__ int4 load_culls(const EdgeCull* __restrict__ culls, i
     return *reinterpret_cast<const int4*>(culls + max(min(c + lane, e1 - 1), 0));
 }
 
-// Wave-uniform evaluation counters of the counting instantiation: distance and
-// crossing terms evaluated (edge visits times the wave's active pixels), list
-// entries a wave processed past the primitive cull, and exact coverage
-// evaluations (pixels within the cull distance).
+// Wave-uniform evaluation counters of the counting instantiation: distance
+// terms and exact crossing terms evaluated (edge visits times the wave's
+// active pixels), row-span crossing terms of far edges, list entries a wave
+// processed past the primitive cull, and exact coverage evaluations (pixels
+// within the cull distance).
 struct EvalCounts {
-    uint64_t dist, cross, entries, cover;
+    uint64_t dist, cross, row, entries, cover;
 };
 
 // Number of the wave's pixels with `a` set (both pixels of every lane).
@@ -141,9 +142,23 @@ __device__ __forceinline__ int wave_count(const bool (&a)[kPix]) {
     return n;
 }
 
+// Crossing term of an edge that lies entirely right of the wave (flag
+// kCullFarCrossExact): +1 on the rows an upward edge spans, -1 for a
+// downward one; cross_term evaluates to the same value there.
+__device__ __forceinline__ void row_cross_term(const EdgeRec& E, float py, Geom& G) {
+    const bool b0 = E.y0 <= py, b1 = E.y1 <= py;
+    G.winding += (b0 != b1) ? (b0 ? 1 : -1) : 0;
+}
+
 // One 64-edge chunk starting at edge c: lane tests, ballots and the edge walks
 // for the lane's pixels (one column px, rows py[p]).  Each edge record is
-// loaded once through the scalar cache and evaluated for every pixel.
+// loaded once through the scalar cache and evaluated for every pixel.  Edge
+// classes (all exact):
+//   near (distance can matter)           distance term, and the crossing
+//                                        term when the edge spans a row;
+//   far, spans a row, flagged, right     row-span crossing term only;
+//   far, spans a row, flagged, left      nothing (its crossing term is 0);
+//   far, spans a row, not flagged        exact crossing term.
 template <int MODE, bool BEST, bool COUNT>
 __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const WaveRect& W,
                                                cptr<EdgeRec> edges, float px,
@@ -153,11 +168,17 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
     const bool dn = in && span_hits(packed_lo(q.x), packed_span(q.x), W.r1) &&
                     span_hits(packed_lo(q.z), packed_span(q.z), W.c1);
     const bool cb = MODE == 0 && in && span_hits(packed_lo(q.y), packed_span(q.y), W.r1);
+    const bool far_exact = cb && !dn && (q.w & kCullFarCrossExact);
     const uint64_t mdn = __ballot(dn);
     const uint64_t mcb = MODE == 0 ? (uint64_t)__ballot(cb) : 0ull;
+    const uint64_t mfar = MODE == 0 ? (uint64_t)__ballot(far_exact) : 0ull;
+    const uint64_t mright =
+        MODE == 0 ? (uint64_t)__ballot(far_exact && packed_lo(q.z) > W.c1) : 0ull;
+    const uint64_t mcross = mcb & ~mfar;  // exact crossing terms
     if constexpr (COUNT) {
         n.dist += (uint64_t)__builtin_popcountll(mdn) * npix;
-        n.cross += (uint64_t)__builtin_popcountll(mcb) * npix;
+        n.cross += (uint64_t)__builtin_popcountll(mcross) * npix;
+        n.row += (uint64_t)__builtin_popcountll(mright) * npix;
     }
     const cptr<EdgeRec> ec = edges + c;
     if constexpr (BEST) {
@@ -167,7 +188,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
             const int k = (int)__builtin_ctzll(todo);
             const EdgeRec E = ec[k];
             const float wx = px - E.x0;
-            const bool cross = MODE == 0 && ((mcb >> k) & 1);
+            const bool cross = MODE == 0 && ((mcross >> k) & 1);
 #pragma unroll
             for (int p = 0; p < kPix; ++p) {
                 const float wy = py[p] - E.y0;
@@ -175,16 +196,10 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
                 if (cross) cross_term(E, wx, wy, py[p], G[p]);
             }
         }
-        for (uint64_t todo = mcb & ~mdn; todo; todo &= todo - 1) {
-            const EdgeRec E = ec[__builtin_ctzll(todo)];
-            const float wx = px - E.x0;
-#pragma unroll
-            for (int p = 0; p < kPix; ++p) cross_term(E, wx, py[p] - E.y0, py[p], G[p]);
-        }
     } else {
         // The minimum and the winding number do not depend on the order:
-        // three loops without per-edge tests.
-        for (uint64_t todo = mdn & mcb; todo; todo &= todo - 1) {
+        // loops without per-edge tests.
+        for (uint64_t todo = mdn & mcross; todo; todo &= todo - 1) {
             const EdgeRec E = ec[__builtin_ctzll(todo)];
             const float wx = px - E.x0;
 #pragma unroll
@@ -194,17 +209,24 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
                 cross_term(E, wx, wy, py[p], G[p]);
             }
         }
-        for (uint64_t todo = mdn & ~mcb; todo; todo &= todo - 1) {
+        for (uint64_t todo = mdn & ~mcross; todo; todo &= todo - 1) {
             const EdgeRec E = ec[__builtin_ctzll(todo)];
             const float wx = px - E.x0;
 #pragma unroll
             for (int p = 0; p < kPix; ++p) dist_term<false>(E, 0, wx, py[p] - E.y0, G[p]);
         }
-        for (uint64_t todo = mcb & ~mdn; todo; todo &= todo - 1) {
+    }
+    if constexpr (MODE == 0) {
+        for (uint64_t todo = mcross & ~mdn; todo; todo &= todo - 1) {
             const EdgeRec E = ec[__builtin_ctzll(todo)];
             const float wx = px - E.x0;
 #pragma unroll
             for (int p = 0; p < kPix; ++p) cross_term(E, wx, py[p] - E.y0, py[p], G[p]);
+        }
+        for (uint64_t todo = mright; todo; todo &= todo - 1) {
+            const EdgeRec E = ec[__builtin_ctzll(todo)];
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) row_cross_term(E, py[p], G[p]);
         }
     }
 }
@@ -278,8 +300,9 @@ __device__ __forceinline__ void flush_counts(const EvalCounts& n,
     if ((threadIdx.x & (kWave - 1)) == 0) {
         atomicAdd(counts + 0, (unsigned long long)n.dist);
         atomicAdd(counts + 1, (unsigned long long)n.cross);
-        atomicAdd(counts + 2, (unsigned long long)n.entries);
-        atomicAdd(counts + 3, (unsigned long long)n.cover);
+        atomicAdd(counts + 2, (unsigned long long)n.row);
+        atomicAdd(counts + 3, (unsigned long long)n.entries);
+        atomicAdd(counts + 4, (unsigned long long)n.cover);
     }
 }
 

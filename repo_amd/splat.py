@@ -184,7 +184,7 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
 
 
 def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
-    """(image [H,W,3], final_Ts, final_idx).  With eval_counts (int64 [4],
+    """(image [H,W,3], final_Ts, final_idx).  With eval_counts (int64 [5],
     zeroed, on the device) the counting instantiation runs and adds the
     evaluation counts of cs_rasterize_forward_counted into it."""
     dev = b.edges.device
@@ -204,8 +204,8 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
 
 
 def _counts_buffer(t):
-    if t.dtype != torch.int64 or t.numel() != 4 or not t.is_contiguous():
-        raise ValueError("eval_counts must be a contiguous int64 tensor of 4 elements")
+    if t.dtype != torch.int64 or t.numel() != 5 or not t.is_contiguous():
+        raise ValueError("eval_counts must be a contiguous int64 tensor of 5 elements")
     return t
 
 

@@ -16,7 +16,30 @@ from helpers import grad_scale_tol, hip_bin, oracle_forward, random_v_out
 from oracle import oracle as O
 from repo_amd import splat, synth
 
+def _far_coords_scene():
+    """Rings whose inner control points of some segments lie millions of pixels
+    off the image: their flattened edges reach past +-2^20 px (the crossing
+    test's far-edge shortcut does not apply to them) while others stay near."""
+    sc = synth.small_scene(5, P=12, h=64, w=96, rmax=30.0)
+    cub = sc.cubics_norm.clone()
+    half_w = sc.img_w / 2.0
+    for k, x in ((1, 5.0e6), (6, -3.0e6), (13, 2.0e6), (30, 1.1e6)):
+        cub[k, 1, 0] = x / half_w - 1.0
+        cub[k, 2, 0] = -0.5 * x / half_w - 1.0
+    sc.cubics_norm = cub
+    return sc
+
+
+def _tiny_width_scene():
+    """aa width 1e-4 (the clamp floor): cull distance 0.25 px, hard edges."""
+    sc = synth.small_scene(6, P=10, h=64, w=80, rmax=25.0)
+    sc.aa_widths = torch.full_like(sc.aa_widths, 1e-4)
+    return sc
+
+
 CASES = {
+    "far_coords": (_far_coords_scene, None),
+    "tiny_width": (_tiny_width_scene, None),
     "small_fill": (lambda: synth.small_scene(0), None),
     "small_fill_big": (lambda: synth.small_scene(3, P=40, h=100, w=130, rmax=60.0), None),
     "small_stroke": (lambda: synth.small_scene(1, stroke=True), None),
