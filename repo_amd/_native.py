@@ -33,7 +33,7 @@ _SZ = ctypes.c_size_t
 _SIGNATURES = {
     "cs_scan_temp_elems": (_SZ, [_I32]),
     "cs_radix_counts_elems": (_SZ, [_I32]),
-    "cs_bin_finish_counts_elems": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "cs_bin_tile_parts": (_I32, [_I32, _I32, _I32, _I32, _I32]),
     "cs_scan_exclusive_u32": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P]),
     "cs_radix_sort_pairs_u32": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _P, _P, _P]),
     "cs_project_cubics_2d_forward": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F,
@@ -44,9 +44,9 @@ _SIGNATURES = {
     "cs_isect_edge_ranges": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _P]),
     "cs_bin_prepare": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                       _I32, _I32, _I32, _F, _I32, _I32, _P, _P, _P, _P, _P, _P,
-                                      _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
-    "cs_bin_finish": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
-                                     _P, _P, _P, _P, _P]),
+                                      _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cs_bin_finish": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P,
+                                     _P, _P]),
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
                                             _P, _P]),
     "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P,

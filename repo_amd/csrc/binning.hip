@@ -7,15 +7,17 @@
 //                      per-segment vertex bounding box.
 //   k_prim_prep        thread per primitive: union of its segments' tile
 //                      ranges, tile count, depth sort key, raster record.
-//   depth rank         stable LSD radix sort of the 32-bit depth keys.
-//   counts by rank + exclusive scan -> per-primitive output offsets, total I.
-//   k_emit             wave per primitive (in depth-rank order) writes its
-//                      tiles' ids and its primitive id.
-//   tile sort          stable LSD radix sort on the tile id only.
-//   k_tile_bins        [start, end) per tile from the sorted tile ids.
+//   depth rank         stable rank of the 32-bit depth keys (ties by
+//                      primitive id): one rank-by-counting launch up to 16K
+//                      primitives, LSD radix sort above.
+//   k_tile_lists<0>    per (tile, rank part) counts of the primitives whose
+//                      tile rectangle covers the tile, prefix over parts.
+//   exclusive scan     tile totals -> first slot of each tile, total I.
+//   k_tile_lists<1>    each tile's primitives, in rank order, into its slots;
+//                      tile_bins [start, end) per tile.
 //
-// Sorting ranks first and then tiles stably yields exactly the order of the
-// reference's single sort of (tile << 32 | depth_key) keys emitted
+// Listing each tile's primitives in depth-rank order yields exactly the order
+// of the reference's single sort of (tile << 32 | depth_key) keys emitted
 // primitive-major with a stable tie order (ties broken by primitive id).
 #include "cs_common.h"
 #include "../../include/cubicsplat_hip.h"
@@ -364,6 +366,7 @@ __global__ void k_status_init(const int32_t* __restrict__ seg_offsets, int P,
 
 constexpr int kScanThreads = 1024;
 constexpr int kScanItems = 4;
+constexpr int kScanItemsLarge = 16;
 constexpr int kScanChunk = kScanThreads * kScanItems;
 
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x, int lane) {
@@ -589,55 +592,84 @@ __global__ __launch_bounds__(256) void k_rank_pairs(const uint32_t* __restrict__
 
 // ------------------------------------------------------------ emit and bins
 
-__global__ __launch_bounds__(256) void k_rank_counts(const int32_t* __restrict__ order,
-                                                    const uint32_t* __restrict__ counts, int P,
-                                                    uint32_t* __restrict__ out) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r < P) out[r] = counts[order[r]];
-}
-
-__global__ __launch_bounds__(256) void k_emit(const int32_t* __restrict__ order,
-                                             const int32_t* __restrict__ prim_tile_ranges,
-                                             const uint32_t* __restrict__ rank_offsets, int P,
-                                             int tbx, uint32_t* __restrict__ tile_keys,
-                                             int32_t* __restrict__ vals) {
-    const int lane = threadIdx.x & 63;
-    const int waves = (gridDim.x * blockDim.x) >> 6;
-    for (int r = (blockIdx.x * blockDim.x + threadIdx.x) >> 6; r < P; r += waves) {
-        const int p = order[r];
-        const int4 tr = reinterpret_cast<const int4*>(prim_tile_ranges)[p];
-        const int w = tr.z - tr.x, h = tr.w - tr.y;
-        if (w <= 0 || h <= 0) continue;
-        const int area = w * h;
-        const uint32_t base = rank_offsets[r];
-        for (int k = lane; k < area; k += kWave) {
-            const int row = k / w;
-            const int col = k - row * w;
-            tile_keys[base + k] = (uint32_t)((tr.y + row) * tbx + tr.x + col);
-            vals[base + k] = p;
-        }
-    }
-}
-
 __global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ a, int n, int32_t v) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) a[i] = v;
 }
 
-// tile_bins.py:10-43 on 32-bit tile ids.
-__global__ __launch_bounds__(256) void k_tile_bins(const uint32_t* __restrict__ tiles, int n,
-                                                  int32_t* __restrict__ bins) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= n) return;
-    const uint32_t cur = tiles[idx];
-    if (idx == 0) bins[2 * cur] = 0;
-    if (idx == n - 1) bins[2 * cur + 1] = n;
-    if (idx > 0) {
-        const uint32_t prev = tiles[idx - 1];
-        if (prev != cur) {
-            bins[2 * prev + 1] = idx;
-            bins[2 * cur] = idx;
+// Per-tile lists without a global sort.  Primitives cover rectangles of
+// tiles and arrive in depth-rank order (order[r]), so the list of tile t is
+// the subsequence of ranks whose rectangle contains t, and a stable counting
+// sort by tile needs, per (tile, rank), the number of earlier ranks covering
+// the tile.  One workgroup owns a row segment of up to 64 tiles (lane = tile
+// column) and splits the ranks into K contiguous parts, one wave each.  A wave
+// walks its part in 64-rank chunks: lanes test one primitive's rectangle
+// against the segment's row and columns, and for each hit (in rank order) every
+// lane checks its own column.  The counting launch leaves per-part counts;
+// their prefix over parts, plus the exclusive scan of the tile totals, gives
+// each (part, tile) its first output slot; the scatter launch walks the same
+// ranks again with a per-lane cursor.
+constexpr int kSegTiles = kWave;
+constexpr int kMaxTileParts = 16;
+
+template <bool SCATTER>
+__global__ __launch_bounds__(kWave * kMaxTileParts) void k_tile_lists(
+    const int32_t* __restrict__ order, const int4* __restrict__ prim_tile_ranges, int P,
+    int ranks_per_part, int tbx, int tby, int nsegcols, uint32_t* __restrict__ part_base,
+    uint32_t* __restrict__ tile_count, const uint32_t* __restrict__ tile_start,
+    int32_t* __restrict__ prim_ids_sorted, int32_t* __restrict__ tile_bins) {
+    __shared__ uint32_t cnt[kMaxTileParts][kWave];
+    const int K = (int)(blockDim.x / kWave);
+    const int part = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+    const int lane = threadIdx.x & (kWave - 1);
+    const int ty = blockIdx.x / nsegcols;
+    const int sx0 = (blockIdx.x - ty * nsegcols) * kSegTiles;
+    const int sx1 = min(sx0 + kSegTiles, tbx);
+    const int tx = sx0 + lane;
+    const bool tile_ok = tx < sx1;
+    const size_t T = (size_t)tbx * tby;
+    const size_t t = (size_t)ty * tbx + tx;
+    const int r0 = part * ranks_per_part, r1 = min(r0 + ranks_per_part, P);
+    uint32_t cur = 0;
+    if (SCATTER && tile_ok) cur = tile_start[t] + part_base[(size_t)part * T + t];
+    for (int c = r0; c < r1; c += kWave) {
+        const int r = c + lane;
+        int p = 0;
+        int4 tr = make_int4(0, 0, 0, 0);
+        if (r < r1) {
+            p = order[r];
+            tr = prim_tile_ranges[p];
         }
+        const bool hit = r < r1 && tr.y <= ty && ty < tr.w && tr.x < sx1 && tr.z > sx0;
+        for (uint64_t m = __ballot(hit); m; m &= m - 1) {
+            const int b = (int)__builtin_ctzll(m);
+            const int x0 = __builtin_amdgcn_readlane(tr.x, b);
+            const int x1 = __builtin_amdgcn_readlane(tr.z, b);
+            const bool in = tile_ok && tx >= x0 && tx < x1;
+            if (SCATTER) {
+                const int pid = __builtin_amdgcn_readlane(p, b);
+                if (in) prim_ids_sorted[cur] = pid;
+            }
+            cur += in ? 1u : 0u;
+        }
+    }
+    if (!SCATTER) {
+        cnt[part][lane] = cur;
+        __syncthreads();
+        if (part == 0 && tile_ok) {
+            uint32_t acc = 0;
+            for (int k = 0; k < K; ++k) {
+                const uint32_t v = cnt[k][lane];
+                part_base[(size_t)k * T + t] = acc;
+                acc += v;
+            }
+            tile_count[t] = acc;
+        }
+    } else if (part == 0 && tile_ok) {
+        // tile_bins.py:10-43: [start, end) per tile, (0, 0) when empty.
+        const uint32_t n = tile_count[t], s0 = tile_start[t];
+        tile_bins[2 * t] = n ? (int32_t)s0 : 0;
+        tile_bins[2 * t + 1] = n ? (int32_t)(s0 + n) : 0;
     }
 }
 
@@ -773,6 +805,10 @@ extern "C" int cs_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int32_t 
     if (nb == 1) {
         hipLaunchKernelGGL(k_scan_apply<kScanItems>, dim3(1), dim3(kScanThreads), 0, stream, in,
                            out, n, nullptr, total);
+    } else if (n <= kScanThreads * kScanItemsLarge) {
+        // One workgroup with more items per thread beats three launches.
+        hipLaunchKernelGGL(k_scan_apply<kScanItemsLarge>, dim3(1), dim3(kScanThreads), 0, stream,
+                           in, out, n, nullptr, total);
     } else {
         hipLaunchKernelGGL(k_scan_block_sums, dim3(nb), dim3(kScanThreads), 0, stream, in, n, temp);
         hipLaunchKernelGGL(k_scan_partials, dim3(1), dim3(kScanThreads), 0, stream, temp, nb);
@@ -828,10 +864,22 @@ extern "C" int cs_radix_sort_pairs_u32(uint32_t* keys, int32_t* vals, uint32_t* 
     return launch_status();
 }
 
-static int bits_for(int64_t v) {
-    int b = 0;
-    while (b < 32 && ((int64_t)1 << b) < v) ++b;
-    return b;
+
+// Parts per row segment for the tile lists: enough waves to fill the chip
+// (about 4096), at least 64 ranks per part, at most kMaxTileParts.
+static int tile_parts(int nprim, int tbx, int tby) {
+    const int64_t nsegs = (int64_t)tby * ((tbx + kSegTiles - 1) / kSegTiles);
+    int64_t k = (4096 + nsegs - 1) / nsegs;
+    const int64_t by_ranks = (nprim + kWave - 1) / kWave;
+    if (k > by_ranks) k = by_ranks;
+    if (k > kMaxTileParts) k = kMaxTileParts;
+    return (int)(k < 1 ? 1 : k);
+}
+
+extern "C" int32_t cs_bin_tile_parts(int32_t nprim, int32_t img_h, int32_t img_w,
+                                     int32_t block_x, int32_t block_y) {
+    if (nprim <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0) return 0;
+    return tile_parts(nprim, (img_w + block_x - 1) / block_x, (img_h + block_y - 1) / block_y);
 }
 
 extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets,
@@ -846,7 +894,8 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                               float* inv_sigma2s, void* prim_recs, uint32_t* keys,
                               int32_t* order, uint32_t* keys_alt, int32_t* vals_alt,
                               uint32_t* radix_counts, uint32_t* scan_temp,
-                              uint32_t* rank_offsets, int32_t* status, hipStream_t stream) {
+                              uint32_t* tile_part_base, uint32_t* tile_count,
+                              uint32_t* tile_start, int32_t* status, hipStream_t stream) {
     if (nseg < 0 || nprim <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0 ||
         samples < 2 || (mode != 0 && mode != 1) || img_h > kMaxImageDim ||
         img_w > kMaxImageDim)
@@ -877,42 +926,34 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                                                radix_counts, scan_temp, stream);
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(k_rank_counts, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream, order,
-                       num_tiles_hit, nprim, keys_alt);
-    return cs_scan_exclusive_u32(keys_alt, rank_offsets, nprim, scan_temp, status, stream);
-}
-
-extern "C" size_t cs_bin_finish_counts_elems(int32_t nprim, int32_t num_intersects,
-                                              int32_t img_h, int32_t img_w, int32_t block_x,
-                                              int32_t block_y) {
-    if (nprim <= 0 || num_intersects < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 ||
-        block_y <= 0)
-        return 0;
-    return cs_radix_counts_elems(num_intersects > 0 ? num_intersects : 1);
+    // Per-(part, tile) counts and their prefix over parts, then the tiles'
+    // first slots; status[0] receives the intersection total.
+    const int K = tile_parts(nprim, tbx, tby);
+    const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
+    const int ranks_per_part = (nprim + K - 1) / K;
+    hipLaunchKernelGGL(k_tile_lists<false>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
+                       order, reinterpret_cast<const int4*>(prim_tile_ranges), nprim,
+                       ranks_per_part, tbx, tby, nsegcols, tile_part_base, tile_count,
+                       (const uint32_t*)nullptr, (int32_t*)nullptr, (int32_t*)nullptr);
+    return cs_scan_exclusive_u32(tile_count, tile_start, tbx * tby, scan_temp, status, stream);
 }
 
 extern "C" int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges,
-                             const uint32_t* rank_offsets, int32_t nprim, int32_t num_intersects,
-                             int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
-                             uint32_t* tile_keys, int32_t* prim_ids_sorted, uint32_t* keys_alt,
-                             int32_t* vals_alt, uint32_t* radix_counts, uint32_t* scan_temp,
-                             int32_t* tile_bins, hipStream_t stream) {
-    if (nprim <= 0 || num_intersects < 0 || block_x <= 0 || block_y <= 0) return CS_ERR_ARGS;
+                             int32_t nprim, int32_t num_intersects, int32_t img_h, int32_t img_w,
+                             int32_t block_x, int32_t block_y, uint32_t* tile_part_base,
+                             uint32_t* tile_count, const uint32_t* tile_start,
+                             int32_t* prim_ids_sorted, int32_t* tile_bins, hipStream_t stream) {
+    if (nprim <= 0 || num_intersects < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 ||
+        block_y <= 0)
+        return CS_ERR_ARGS;
     const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
-    const int ntiles = tbx * tby;
-    hipLaunchKernelGGL(k_fill_i32, dim3(blocks_for(2 * ntiles, 256)), dim3(256), 0, stream,
-                       tile_bins, 2 * ntiles, 0);
-    if (num_intersects == 0) return launch_status();
-    const int emit_blocks = blocks_for((int64_t)nprim * kWave, 256);
-    hipLaunchKernelGGL(k_emit, dim3(emit_blocks < 65535 ? emit_blocks : 65535), dim3(256), 0,
-                       stream, order, prim_tile_ranges, rank_offsets, nprim, tbx, tile_keys,
-                       prim_ids_sorted);
-    int rc = cs_radix_sort_pairs_u32(tile_keys, prim_ids_sorted, keys_alt, vals_alt,
-                                     num_intersects, bits_for(ntiles), radix_counts, scan_temp,
-                                     stream);
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_tile_bins, dim3(blocks_for(num_intersects, 256)), dim3(256), 0, stream,
-                       tile_keys, num_intersects, tile_bins);
+    const int K = tile_parts(nprim, tbx, tby);
+    const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
+    const int ranks_per_part = (nprim + K - 1) / K;
+    hipLaunchKernelGGL(k_tile_lists<true>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
+                       order, reinterpret_cast<const int4*>(prim_tile_ranges), nprim,
+                       ranks_per_part, tbx, tby, nsegcols, tile_part_base, tile_count, tile_start,
+                       prim_ids_sorted, tile_bins);
     return launch_status();
 }
 

@@ -97,7 +97,6 @@ class Binned:
     prim_recs: torch.Tensor
     order: torch.Tensor            # depth rank -> primitive id
     primitive_ids_sorted: torch.Tensor
-    tile_keys_sorted: torch.Tensor
     tile_bins: torch.Tensor
 
     @property
@@ -135,11 +134,13 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     order = torch.empty((P,), dtype=i32, device=dev)
     keys_alt = torch.empty((P,), dtype=i32, device=dev)
     vals_alt = torch.empty((P,), dtype=i32, device=dev)
-    counts_p = int(lib.cs_radix_counts_elems(P))
-    radix_counts = torch.empty((counts_p,), dtype=i32, device=dev)
-    scan_temp = torch.empty((int(lib.cs_scan_temp_elems(max(P, counts_p))),), dtype=i32,
-                            device=dev)
-    rank_offsets = torch.empty((P,), dtype=i32, device=dev)
+    radix_counts = torch.empty((int(lib.cs_radix_counts_elems(P)),), dtype=i32, device=dev)
+    T = tbx * tby
+    scan_temp = torch.empty((int(lib.cs_scan_temp_elems(max(P, T))),), dtype=i32, device=dev)
+    K = int(lib.cs_bin_tile_parts(P, img_h, img_w, block_x, block_y))
+    tile_part_base = torch.empty((K * T,), dtype=i32, device=dev)
+    tile_count = torch.empty((T,), dtype=i32, device=dev)
+    tile_start = torch.empty((T,), dtype=i32, device=dev)
     status = torch.empty((4,), dtype=i32, device=dev)
     st = N.stream(dev)
     with N.prof("cubic.fwd.bin_prepare"):
@@ -148,9 +149,11 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
                N.ptr(stroke_widths), nseg, P, img_h, img_w, block_x, block_y, S, float(aabb_pad),
                int(bool(aniso)), mode, N.ptr(cubics_px), N.ptr(seg_tile_ranges), N.ptr(seg_recs),
                N.ptr(edges), N.ptr(edge_culls), N.ptr(prim_tile_ranges), N.ptr(num_tiles_hit),
-               N.ptr(inv_sigma2s),
-               N.ptr(prim_recs), N.ptr(keys), N.ptr(order), N.ptr(keys_alt), N.ptr(vals_alt),
-               N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(rank_offsets), N.ptr(status), st)
+               N.ptr(inv_sigma2s), N.ptr(prim_recs), N.ptr(keys), N.ptr(order), N.ptr(keys_alt),
+               N.ptr(vals_alt), N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(tile_part_base),
+               N.ptr(tile_count), N.ptr(tile_start), N.ptr(status), st)
+    # The one host read of the forward (the reference reads the same count,
+    # cubic_splatting.py:2879).
     I, bad, first, last = status.tolist()
     if bad or first != 0 or last != nseg:
         raise ValueError(
@@ -159,28 +162,18 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
             + ("; offsets are not non-decreasing within [0, num_segments]" if bad else ""))
     if I < 0:
         raise RuntimeError(f"intersection count overflowed int32 ({I})")
-    tile_keys = torch.empty((I,), dtype=i32, device=dev)
     prim_ids = torch.empty((I,), dtype=i32, device=dev)
-    tile_bins = torch.empty((tbx * tby, 2), dtype=i32, device=dev)
-    if I > 0:
-        kalt = torch.empty((I,), dtype=i32, device=dev)
-        valt = torch.empty((I,), dtype=i32, device=dev)
-        counts_i = int(lib.cs_bin_finish_counts_elems(P, I, img_h, img_w, block_x, block_y))
-        rc_i = torch.empty((counts_i,), dtype=i32, device=dev)
-        st_i = torch.empty((int(lib.cs_scan_temp_elems(counts_i)),), dtype=i32, device=dev)
-    else:
-        kalt = valt = rc_i = st_i = None
+    tile_bins = torch.empty((T, 2), dtype=i32, device=dev)
     with N.prof("cubic.fwd.bin_finish"):
-        N.call("cs_bin_finish", N.ptr(order), N.ptr(prim_tile_ranges), N.ptr(rank_offsets), P, I,
-               img_h, img_w, block_x, block_y, N.ptr(tile_keys), N.ptr(prim_ids), N.ptr(kalt),
-               N.ptr(valt), N.ptr(rc_i), N.ptr(st_i), N.ptr(tile_bins), st)
+        N.call("cs_bin_finish", N.ptr(order), N.ptr(prim_tile_ranges), P, I, img_h, img_w,
+               block_x, block_y, N.ptr(tile_part_base), N.ptr(tile_count), N.ptr(tile_start),
+               N.ptr(prim_ids), N.ptr(tile_bins), st)
     return Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P,
                   num_intersects=I, cubics_px=cubics_px, seg_tile_ranges=seg_tile_ranges,
                   seg_recs=seg_recs, edges=edges, edge_culls=edge_culls,
                   prim_tile_ranges=prim_tile_ranges,
                   num_tiles_hit=num_tiles_hit, inv_sigma2s=inv_sigma2s, prim_recs=prim_recs,
-                  order=order, primitive_ids_sorted=prim_ids, tile_keys_sorted=tile_keys,
-                  tile_bins=tile_bins)
+                  order=order, primitive_ids_sorted=prim_ids, tile_bins=tile_bins)
 
 
 def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
