@@ -120,12 +120,14 @@ int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const f
  * get_tile_bin_edges of ops/tile_bins.py:10-60): each tile's primitives in
  * depth-rank order into primitive_ids_sorted [num_intersects] and tile_bins
  * [T,2] ((0, 0) for empty tiles) -- the reference's values, bit-exact, without
- * a global sort.  Inputs are stage 1's outputs. */
+ * a global sort.  Inputs are stage 1's outputs.  zero_buf (optional, zero_n
+ * floats) is cleared by the same launch: the caller's gradient accumulators
+ * for cs_rasterize_backward, which saves that step a separate fill. */
 int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges, int32_t nprim,
                   int32_t num_intersects, int32_t img_h, int32_t img_w, int32_t block_x,
                   int32_t block_y, uint32_t* tile_part_base, uint32_t* tile_count,
                   const uint32_t* tile_start, int32_t* prim_ids_sorted, int32_t* tile_bins,
-                  hipStream_t stream);
+                  float* zero_buf, int64_t zero_n, hipStream_t stream);
 
 /* ---------------- rasterization ---------------- */
 
@@ -188,7 +190,8 @@ int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg, int32_t edges_p
                              float* v_cubics_norm, hipStream_t stream);
 
 /* Backward epilogue (ops/cubic_splatting.py:3096-3104): v_cubics_norm =
- * v_cubics_px * (W/2, H/2) and v_aa_widths = -2 v_inv_sigma2 / max(w^3, 1e-12). */
+ * v_cubics_px * (W/2, H/2) and v_aa_widths = -2 v_inv_sigma2 / max(w^3, 1e-12)
+ * with w = max(widths, 1e-4) (the clamp of ops/cubic_splatting.py:2820). */
 int cs_backward_finalize(const float* v_cubics_px, int32_t nseg, int32_t img_h, int32_t img_w,
                          const float* widths, const float* v_inv_sigma2s, int32_t nprim,
                          float* v_cubics_norm, float* v_aa_widths, hipStream_t stream);

@@ -617,8 +617,14 @@ __global__ __launch_bounds__(kWave * kMaxTileParts) void k_tile_lists(
     const int32_t* __restrict__ order, const int4* __restrict__ prim_tile_ranges, int P,
     int ranks_per_part, int tbx, int tby, int nsegcols, uint32_t* __restrict__ part_base,
     uint32_t* __restrict__ tile_count, const uint32_t* __restrict__ tile_start,
-    int32_t* __restrict__ prim_ids_sorted, int32_t* __restrict__ tile_bins) {
+    int32_t* __restrict__ prim_ids_sorted, int32_t* __restrict__ tile_bins,
+    float* __restrict__ zero_buf, int64_t zero_n) {
     __shared__ uint32_t cnt[kMaxTileParts][kWave];
+    if (SCATTER && zero_buf) {
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += stride)
+            zero_buf[i] = 0.0f;
+    }
     const int K = (int)(blockDim.x / kWave);
     const int part = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     const int lane = threadIdx.x & (kWave - 1);
@@ -934,7 +940,8 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
     hipLaunchKernelGGL(k_tile_lists<false>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
                        order, reinterpret_cast<const int4*>(prim_tile_ranges), nprim,
                        ranks_per_part, tbx, tby, nsegcols, tile_part_base, tile_count,
-                       (const uint32_t*)nullptr, (int32_t*)nullptr, (int32_t*)nullptr);
+                       (const uint32_t*)nullptr, (int32_t*)nullptr, (int32_t*)nullptr,
+                       (float*)nullptr, (int64_t)0);
     return cs_scan_exclusive_u32(tile_count, tile_start, tbx * tby, scan_temp, status, stream);
 }
 
@@ -942,9 +949,10 @@ extern "C" int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_rang
                              int32_t nprim, int32_t num_intersects, int32_t img_h, int32_t img_w,
                              int32_t block_x, int32_t block_y, uint32_t* tile_part_base,
                              uint32_t* tile_count, const uint32_t* tile_start,
-                             int32_t* prim_ids_sorted, int32_t* tile_bins, hipStream_t stream) {
+                             int32_t* prim_ids_sorted, int32_t* tile_bins, float* zero_buf,
+                             int64_t zero_n, hipStream_t stream) {
     if (nprim <= 0 || num_intersects < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 ||
-        block_y <= 0)
+        block_y <= 0 || zero_n < 0 || (zero_n > 0 && !zero_buf))
         return CS_ERR_ARGS;
     const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
     const int K = tile_parts(nprim, tbx, tby);
@@ -953,7 +961,7 @@ extern "C" int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_rang
     hipLaunchKernelGGL(k_tile_lists<true>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
                        order, reinterpret_cast<const int4*>(prim_tile_ranges), nprim,
                        ranks_per_part, tbx, tby, nsegcols, tile_part_base, tile_count, tile_start,
-                       prim_ids_sorted, tile_bins);
+                       prim_ids_sorted, tile_bins, zero_n > 0 ? zero_buf : nullptr, zero_n);
     return launch_status();
 }
 

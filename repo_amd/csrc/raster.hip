@@ -719,7 +719,8 @@ __global__ __launch_bounds__(256) void k_accumulate(const float4* __restrict__ v
 }
 
 // v_cubics_norm = v_cubics_px * (W/2, H/2) (cubic_splatting.py:3096-3100) and
-// v_aa_widths = -2 v_inv_sigma2 / max(w^3, 1e-12) (cubic_splatting.py:3103-3104).
+// v_aa_widths = -2 v_inv_sigma2 / max(w^3, 1e-12) (cubic_splatting.py:3103-3104),
+// w = max(aa_width, 1e-4) (the clamp of cubic_splatting.py:2820).
 __global__ __launch_bounds__(256) void k_finalize(const float* __restrict__ v_px, int nseg,
                                                  float half_w, float half_h,
                                                  const float* __restrict__ widths,
@@ -729,7 +730,7 @@ __global__ __launch_bounds__(256) void k_finalize(const float* __restrict__ v_px
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t < nseg * 8) v_norm[t] = v_px[t] * ((t & 1) ? half_h : half_w);
     if (t < P) {
-        const float w = widths[t];
+        const float w = fmaxf(widths[t], kWidthMin);
         v_aa[t] = (-2.0f * v_is2[t]) / fmaxf(w * w * w, (float)1e-12);
     }
 }

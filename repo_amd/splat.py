@@ -98,6 +98,11 @@ class Binned:
     order: torch.Tensor            # depth rank -> primitive id
     primitive_ids_sorted: torch.Tensor
     tile_bins: torch.Tensor
+    # Gradient accumulators of the backward ([nseg*8 + P*(5|6)] fp32), cleared
+    # by the binning's last launch; `grad_accum_clean` turns False once a
+    # backward has used them.
+    grad_accum: Optional[torch.Tensor] = None
+    grad_accum_clean: bool = False
 
     @property
     def edges_per_segment(self) -> int:
@@ -164,16 +169,22 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
         raise RuntimeError(f"intersection count overflowed int32 ({I})")
     prim_ids = torch.empty((I,), dtype=i32, device=dev)
     tile_bins = torch.empty((T, 2), dtype=i32, device=dev)
+    grad_accum = torch.empty((_grad_accum_elems(nseg, P, mode),), dtype=f32, device=dev)
     with N.prof("cubic.fwd.bin_finish"):
         N.call("cs_bin_finish", N.ptr(order), N.ptr(prim_tile_ranges), P, I, img_h, img_w,
                block_x, block_y, N.ptr(tile_part_base), N.ptr(tile_count), N.ptr(tile_start),
-               N.ptr(prim_ids), N.ptr(tile_bins), st)
+               N.ptr(prim_ids), N.ptr(tile_bins), N.ptr(grad_accum), int(grad_accum.numel()), st)
     return Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P,
                   num_intersects=I, cubics_px=cubics_px, seg_tile_ranges=seg_tile_ranges,
                   seg_recs=seg_recs, edges=edges, edge_culls=edge_culls,
                   prim_tile_ranges=prim_tile_ranges,
                   num_tiles_hit=num_tiles_hit, inv_sigma2s=inv_sigma2s, prim_recs=prim_recs,
-                  order=order, primitive_ids_sorted=prim_ids, tile_bins=tile_bins)
+                  order=order, primitive_ids_sorted=prim_ids, tile_bins=tile_bins,
+                  grad_accum=grad_accum, grad_accum_clean=True)
+
+
+def _grad_accum_elems(nseg: int, nprim: int, mode: int) -> int:
+    return nseg * 8 + nprim * (6 if mode == MODE_STROKE else 5)
 
 
 def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
@@ -210,8 +221,12 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     rasterize_forward (cs_rasterize_backward_counted)."""
     dev = b.edges.device
     P = b.nprim
-    zeros = torch.zeros((b.nseg * 8 + P * (6 if b.mode == MODE_STROKE else 5),),
-                        dtype=torch.float32, device=dev)
+    if b.grad_accum is not None and b.grad_accum_clean:
+        zeros = b.grad_accum
+        b.grad_accum_clean = False
+    else:  # a second backward through the same forward
+        zeros = torch.zeros((_grad_accum_elems(b.nseg, P, b.mode),), dtype=torch.float32,
+                            device=dev)
     v_px = zeros[: b.nseg * 8].view(b.nseg, 4, 2)
     rest = zeros[b.nseg * 8:]
     v_colors = rest[: 3 * P].view(P, 3)
@@ -298,12 +313,13 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
                 f"{name} size must match primitive count ({num_primitives}), got {n}"
                 if k is not None else
                 f"colors first dim must match primitive count ({num_primitives}), got {n}")
+    # The reference clamps the widths to >= 1e-4 here (cubic_splatting.py:2820);
+    # every kernel that reads them applies that clamp itself.
     widths = _f32(aa_widths).view(-1)
     if int(widths.numel()) != num_primitives:
         raise ValueError(
             f"aa_widths size must match primitive count ({num_primitives}), "
             f"got {int(widths.numel())}")
-    widths = torch.clamp(widths, min=1e-4)
 
     colors_c = _f32(colors)
     opac_c = _f32(opacities).view(-1)
@@ -371,7 +387,10 @@ def _splat_backward(ctx, grad_out_img):
         if ctx.mode == MODE_STROKE:
             v_sw = payload["v_stroke"]
     v_cubics_norm, v_aa = backward_finalize(b, v_cubics_px, widths, v_is2)
-    v_depths = torch.zeros_like(depths, dtype=torch.float32)
+    # The reference returns zeros for the depths (cubic_splatting.py:3102).
+    depth_index = 5 if ctx.mode == MODE_STROKE else 4
+    v_depths = (torch.zeros_like(depths, dtype=torch.float32)
+                if ctx.needs_input_grad[depth_index] else None)
     return v_cubics_norm.view_as(cubics_norm), v_colors, v_opac.view_as(opacities), v_sw, \
         v_depths, v_aa
 
@@ -471,12 +490,16 @@ def render_cubic_fill_splat_tilelang(cubics_norm, primitive_seg_offsets, colors,
         return bg.expand(int(img_h), int(img_w), 3).clone()
     _common_checks(cubics_norm, offs, colors, opacities, depths, num_primitives)
     dev = cubics_norm.device
-    rules = _prim_vector(fill_rules, num_primitives, "fill_rules", dev, torch.int32, 1)
+    # Default: nonzero rule for every primitive (cubic_splatting.py:3175-3178),
+    # which the kernels apply when no rules are passed.
+    rules = (None if fill_rules is None else
+             _prim_vector(fill_rules, num_primitives, "fill_rules", dev, torch.int32, 1)
+             .contiguous())
     widths = torch.clamp(_prim_vector(aa_widths, num_primitives, "aa_widths", dev,
                                       torch.float32, float(aa_width)).contiguous(), min=1e-4)
     return _CubicFillSplatFunction.apply(
         cubics_norm, offs.contiguous(), colors.contiguous(), opacities.reshape(-1).contiguous(),
-        depths.reshape(-1).contiguous(), rules.contiguous(), int(img_h), int(img_w),
+        depths.reshape(-1).contiguous(), rules, int(img_h), int(img_w),
         int(block_x), int(block_y), background, int(project_threads), int(map_threads),
         float(aabb_pad), bool(aniso_intersects), widths, int(distance_samples),
         normalize_cubic_flatten_method(flatten_method), process_fn)
