@@ -118,16 +118,20 @@ int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const f
 
 /* Stage 2 (ops/cubic_splatting.py:2888-2908, the sort of :2895-2896 and
  * get_tile_bin_edges of ops/tile_bins.py:10-60): each tile's primitives in
- * depth-rank order into primitive_ids_sorted [num_intersects] and tile_bins
- * [T,2] ((0, 0) for empty tiles) -- the reference's values, bit-exact, without
- * a global sort.  Inputs are stage 1's outputs.  zero_buf (optional, zero_n
- * floats) is cleared by the same launch: the caller's gradient accumulators
- * for cs_rasterize_backward, which saves that step a separate fill. */
+ * depth-rank order into primitive_ids_sorted and tile_bins [T,2] ((0, 0) for
+ * empty tiles) -- the reference's values, bit-exact, without a global sort.
+ * Inputs are stage 1's outputs, status included: the intersection total is
+ * read on the device, so this call can be enqueued before the host has read
+ * it.  primitive_ids_sorted holds `capacity` elements; when the total exceeds
+ * it, nothing is written except empty tile_bins (the caller retries with a
+ * larger buffer).  zero_buf (optional, zero_n floats) is cleared by the same
+ * launch: the caller's gradient accumulators for cs_rasterize_backward, which
+ * saves that step a separate fill. */
 int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges, int32_t nprim,
-                  int32_t num_intersects, int32_t img_h, int32_t img_w, int32_t block_x,
-                  int32_t block_y, uint32_t* tile_part_base, uint32_t* tile_count,
-                  const uint32_t* tile_start, int32_t* prim_ids_sorted, int32_t* tile_bins,
-                  float* zero_buf, int64_t zero_n, hipStream_t stream);
+                  const int32_t* status, int64_t capacity, int32_t img_h, int32_t img_w,
+                  int32_t block_x, int32_t block_y, uint32_t* tile_part_base,
+                  uint32_t* tile_count, const uint32_t* tile_start, int32_t* prim_ids_sorted,
+                  int32_t* tile_bins, float* zero_buf, int64_t zero_n, hipStream_t stream);
 
 /* ---------------- rasterization ---------------- */
 

@@ -618,7 +618,8 @@ __global__ __launch_bounds__(kWave * kMaxTileParts) void k_tile_lists(
     int ranks_per_part, int tbx, int tby, int nsegcols, uint32_t* __restrict__ part_base,
     uint32_t* __restrict__ tile_count, const uint32_t* __restrict__ tile_start,
     int32_t* __restrict__ prim_ids_sorted, int32_t* __restrict__ tile_bins,
-    float* __restrict__ zero_buf, int64_t zero_n) {
+    float* __restrict__ zero_buf, int64_t zero_n, const int32_t* __restrict__ total,
+    int64_t capacity) {
     __shared__ uint32_t cnt[kMaxTileParts][kWave];
     if (SCATTER && zero_buf) {
         const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -636,6 +637,15 @@ __global__ __launch_bounds__(kWave * kMaxTileParts) void k_tile_lists(
     const size_t T = (size_t)tbx * tby;
     const size_t t = (size_t)ty * tbx + tx;
     const int r0 = part * ranks_per_part, r1 = min(r0 + ranks_per_part, P);
+    if (SCATTER && (uint64_t)(uint32_t)*total > (uint64_t)capacity) {
+        // The lists do not fit the caller's buffer: every tile reads as
+        // empty, nothing is scattered, and the caller retries at full size.
+        if (part == 0 && tile_ok) {
+            tile_bins[2 * t] = 0;
+            tile_bins[2 * t + 1] = 0;
+        }
+        return;
+    }
     uint32_t cur = 0;
     if (SCATTER && tile_ok) cur = tile_start[t] + part_base[(size_t)part * T + t];
     for (int c = r0; c < r1; c += kWave) {
@@ -941,17 +951,18 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                        order, reinterpret_cast<const int4*>(prim_tile_ranges), nprim,
                        ranks_per_part, tbx, tby, nsegcols, tile_part_base, tile_count,
                        (const uint32_t*)nullptr, (int32_t*)nullptr, (int32_t*)nullptr,
-                       (float*)nullptr, (int64_t)0);
+                       (float*)nullptr, (int64_t)0, (const int32_t*)nullptr, (int64_t)0);
     return cs_scan_exclusive_u32(tile_count, tile_start, tbx * tby, scan_temp, status, stream);
 }
 
 extern "C" int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges,
-                             int32_t nprim, int32_t num_intersects, int32_t img_h, int32_t img_w,
-                             int32_t block_x, int32_t block_y, uint32_t* tile_part_base,
-                             uint32_t* tile_count, const uint32_t* tile_start,
-                             int32_t* prim_ids_sorted, int32_t* tile_bins, float* zero_buf,
-                             int64_t zero_n, hipStream_t stream) {
-    if (nprim <= 0 || num_intersects < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 ||
+                             int32_t nprim, const int32_t* status, int64_t capacity,
+                             int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
+                             uint32_t* tile_part_base, uint32_t* tile_count,
+                             const uint32_t* tile_start, int32_t* prim_ids_sorted,
+                             int32_t* tile_bins, float* zero_buf, int64_t zero_n,
+                             hipStream_t stream) {
+    if (nprim <= 0 || !status || capacity < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 ||
         block_y <= 0 || zero_n < 0 || (zero_n > 0 && !zero_buf))
         return CS_ERR_ARGS;
     const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
@@ -961,7 +972,8 @@ extern "C" int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_rang
     hipLaunchKernelGGL(k_tile_lists<true>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
                        order, reinterpret_cast<const int4*>(prim_tile_ranges), nprim,
                        ranks_per_part, tbx, tby, nsegcols, tile_part_base, tile_count, tile_start,
-                       prim_ids_sorted, tile_bins, zero_n > 0 ? zero_buf : nullptr, zero_n);
+                       prim_ids_sorted, tile_bins, zero_n > 0 ? zero_buf : nullptr, zero_n,
+                       status, capacity);
     return launch_status();
 }
 

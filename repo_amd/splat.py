@@ -103,6 +103,9 @@ class Binned:
     # backward has used them.
     grad_accum: Optional[torch.Tensor] = None
     grad_accum_clean: bool = False
+    # Set while the intersection count has not been read on the host yet
+    # (bin_primitives with a capacity hint); resolve_binned() settles it.
+    pending: Optional["_PendingCount"] = None
 
     @property
     def edges_per_segment(self) -> int:
@@ -113,11 +116,23 @@ class Binned:
         return self.edges[:, :4].reshape(-1, 2, 2)
 
 
+@dataclass
+class _PendingCount:
+    status_host: torch.Tensor   # pinned int32 [4], filled by an async copy
+    event: Any                  # recorded after that copy
+    capacity: int               # elements of the primitive_ids_sorted buffer
+    finish: Callable[[int], torch.Tensor]  # cs_bin_finish into a new buffer of that size
+
+
 def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rules, widths,
                    stroke_widths, img_h, img_w, samples, *, aabb_pad=DEFAULT_AABB_PAD,
-                   aniso=False, mode=MODE_FILL, block_x=BLOCK_X, block_y=BLOCK_Y) -> Binned:
+                   aniso=False, mode=MODE_FILL, block_x=BLOCK_X, block_y=BLOCK_Y,
+                   capacity_hint=None) -> Binned:
     """Project, flatten and bin (cubic_splatting.py:2815-2908).  All inputs are
-    contiguous device tensors of the reference's dtypes."""
+    contiguous device tensors of the reference's dtypes.  Without
+    capacity_hint the host reads the intersection count before the lists are
+    built; with it, the lists go into a buffer of that many entries and the
+    result is pending until resolve_binned()."""
     dev = cubics_norm.device
     lib = N.lib()
     nseg = int(cubics_norm.shape[0])
@@ -157,9 +172,47 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
                N.ptr(inv_sigma2s), N.ptr(prim_recs), N.ptr(keys), N.ptr(order), N.ptr(keys_alt),
                N.ptr(vals_alt), N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(tile_part_base),
                N.ptr(tile_count), N.ptr(tile_start), N.ptr(status), st)
+    grad_accum = torch.empty((_grad_accum_elems(nseg, P, mode),), dtype=f32, device=dev)
+    tile_bins = torch.empty((T, 2), dtype=i32, device=dev)
+
+    def finish(capacity: int) -> torch.Tensor:
+        ids = torch.empty((capacity,), dtype=i32, device=dev)
+        with N.prof("cubic.fwd.bin_finish"):
+            N.call("cs_bin_finish", N.ptr(order), N.ptr(prim_tile_ranges), P, N.ptr(status),
+                   capacity, img_h, img_w, block_x, block_y, N.ptr(tile_part_base),
+                   N.ptr(tile_count), N.ptr(tile_start), N.ptr(ids), N.ptr(tile_bins),
+                   N.ptr(grad_accum), int(grad_accum.numel()), st)
+        return ids
+
     # The one host read of the forward (the reference reads the same count,
-    # cubic_splatting.py:2879).
-    I, bad, first, last = status.tolist()
+    # cubic_splatting.py:2879).  With a capacity hint the lists are built into
+    # a buffer of that size first and the count is checked afterwards, so the
+    # GPU does not idle while the host waits for it.
+    status_host = torch.empty((4,), dtype=i32, pin_memory=True)
+    status_host.copy_(status, non_blocking=True)
+    event = torch.cuda.Event()
+    event.record(torch.cuda.current_stream(dev))
+    pending = _PendingCount(status_host, event, -1, finish)
+    if capacity_hint is None:
+        I = _read_count(pending, nseg)
+        prim_ids = finish(I)
+        pending = None
+    else:
+        I = -1
+        pending.capacity = max(0, int(capacity_hint))
+        prim_ids = finish(pending.capacity)
+    return Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P,
+                  num_intersects=I, cubics_px=cubics_px, seg_tile_ranges=seg_tile_ranges,
+                  seg_recs=seg_recs, edges=edges, edge_culls=edge_culls,
+                  prim_tile_ranges=prim_tile_ranges,
+                  num_tiles_hit=num_tiles_hit, inv_sigma2s=inv_sigma2s, prim_recs=prim_recs,
+                  order=order, primitive_ids_sorted=prim_ids, tile_bins=tile_bins,
+                  grad_accum=grad_accum, grad_accum_clean=True, pending=pending)
+
+
+def _read_count(pending: "_PendingCount", nseg: int) -> int:
+    pending.event.synchronize()
+    I, bad, first, last = pending.status_host.tolist()
     if bad or first != 0 or last != nseg:
         raise ValueError(
             "primitive_seg_offsets must start at 0 and end at num_segments "
@@ -167,20 +220,33 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
             + ("; offsets are not non-decreasing within [0, num_segments]" if bad else ""))
     if I < 0:
         raise RuntimeError(f"intersection count overflowed int32 ({I})")
-    prim_ids = torch.empty((I,), dtype=i32, device=dev)
-    tile_bins = torch.empty((T, 2), dtype=i32, device=dev)
-    grad_accum = torch.empty((_grad_accum_elems(nseg, P, mode),), dtype=f32, device=dev)
-    with N.prof("cubic.fwd.bin_finish"):
-        N.call("cs_bin_finish", N.ptr(order), N.ptr(prim_tile_ranges), P, I, img_h, img_w,
-               block_x, block_y, N.ptr(tile_part_base), N.ptr(tile_count), N.ptr(tile_start),
-               N.ptr(prim_ids), N.ptr(tile_bins), N.ptr(grad_accum), int(grad_accum.numel()), st)
-    return Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P,
-                  num_intersects=I, cubics_px=cubics_px, seg_tile_ranges=seg_tile_ranges,
-                  seg_recs=seg_recs, edges=edges, edge_culls=edge_culls,
-                  prim_tile_ranges=prim_tile_ranges,
-                  num_tiles_hit=num_tiles_hit, inv_sigma2s=inv_sigma2s, prim_recs=prim_recs,
-                  order=order, primitive_ids_sorted=prim_ids, tile_bins=tile_bins,
-                  grad_accum=grad_accum, grad_accum_clean=True)
+    return I
+
+
+def resolve_binned(b: Binned) -> bool:
+    """Reads the intersection count of a deferred bin_primitives call and sets
+    num_intersects / primitive_ids_sorted.  Returns True when the lists did
+    not fit the hinted buffer and were rebuilt at full size (outputs computed
+    from the first build must then be computed again)."""
+    pend = b.pending
+    if pend is None:
+        return False
+    I = _read_count(pend, b.nseg)
+    b.pending = None
+    b.num_intersects = I
+    if I <= pend.capacity:
+        b.primitive_ids_sorted = b.primitive_ids_sorted[:I]
+        return False
+    b.primitive_ids_sorted = pend.finish(I)
+    b.grad_accum_clean = True
+    return True
+
+
+def intersection_capacity(num_intersects: int) -> int:
+    """Buffer size hint for the next forward of a scene whose last count was
+    num_intersects: 25% headroom, rounded up to 4096."""
+    want = num_intersects + num_intersects // 4 + 4096
+    return (want + 4095) // 4096 * 4096
 
 
 def _grad_accum_elems(nseg: int, nprim: int, mode: int) -> int:
@@ -271,6 +337,18 @@ def backward_finalize(b: Binned, v_cubics_px, widths, v_inv_sigma2s):
 
 _NONE19 = (None,) * 19
 
+# Last intersection-buffer size per scene shape, the capacity hint of the next
+# forward of that shape (bounded: the oldest entries are dropped).
+_CAPACITY_HINTS: "dict[tuple, int]" = {}
+_MAX_HINTS = 64
+
+
+def _remember_capacity(key, num_intersects: int) -> None:
+    _CAPACITY_HINTS.pop(key, None)
+    if len(_CAPACITY_HINTS) >= _MAX_HINTS:
+        _CAPACITY_HINTS.pop(next(iter(_CAPACITY_HINTS)))
+    _CAPACITY_HINTS[key] = intersection_capacity(max(0, num_intersects))
+
 
 def _check_block(block_x: int, block_y: int) -> None:
     if int(block_x) != BLOCK_X or int(block_y) != BLOCK_Y:
@@ -325,14 +403,22 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
     opac_c = _f32(opacities).view(-1)
     rules_c = _i32(fill_rules).view(-1) if fill_rules is not None else None
     sw_c = _f32(stroke_widths).view(-1) if stroke_widths is not None else None
+    hint_key = (cubics_norm.device.index, mode, num_primitives, num_segments, int(img_h),
+                int(img_w), int(distance_samples))
     b = bin_primitives(_f32(cubics_norm), offs, colors_c, opac_c, _f32(depths).view(-1),
                        rules_c, widths, sw_c, int(img_h), int(img_w), int(distance_samples),
                        aabb_pad=float(aabb_pad), aniso=bool(aniso_intersects), mode=mode,
-                       block_x=int(block_x), block_y=int(block_y))
+                       block_x=int(block_x), block_y=int(block_y),
+                       capacity_hint=_CAPACITY_HINTS.get(hint_key))
+    # With a hint the raster is enqueued before the host reads the count; if
+    # the lists did not fit, they and the raster are redone at full size.
+    out, final_T, final_idx = rasterize_forward(b, bg)
+    if resolve_binned(b):
+        out, final_T, final_idx = rasterize_forward(b, bg)
+    _remember_capacity(hint_key, b.num_intersects)
     if b.num_intersects <= 0:
         ctx.empty = True
         return bg.view(1, 1, 3).expand(int(img_h), int(img_w), 3).clone()
-    out, final_T, final_idx = rasterize_forward(b, bg)
     ctx.empty = False
     ctx.binned = b
     ctx.process_fn = process_fn

@@ -150,3 +150,54 @@ def test_exclusive_scan(n):
     ref = np.concatenate([[0], np.cumsum(x)[:-1]])
     np.testing.assert_array_equal(out.cpu().numpy(), ref)
     assert int(tot.item()) == int(x.sum())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hint", [0, 1, 17, None, 10 ** 6])
+def test_deferred_count_matches_synchronous(hint):
+    """bin_primitives with a capacity hint builds the lists before the host
+    reads the intersection count; a too-small buffer leaves every tile empty
+    until resolve_binned() rebuilds at full size.  Either way the lists, and
+    the raster of them, equal the synchronous path's."""
+    from repo_amd import splat
+    print(f"[deferred] hint={hint}", flush=True)
+    sc = synth.small_scene(8, P=24, h=80, w=112, rmax=40.0)
+    ref, s = hip_bin(sc)
+    bg = s.background.float().contiguous()
+    out_ref, T_ref, idx_ref = splat.rasterize_forward(ref, bg)
+    widths = torch.clamp(s.aa_widths.float(), min=1e-4).contiguous()
+    b = splat.bin_primitives(
+        s.cubics_norm.contiguous(), s.seg_offsets.to(torch.int32).contiguous(),
+        s.colors.contiguous(), s.opacities.contiguous(), s.depths.contiguous(),
+        s.fill_rules.to(torch.int32).contiguous(), widths, None, s.img_h, s.img_w, s.S,
+        capacity_hint=hint if hint is not None else ref.num_intersects)
+    out, T, idx = splat.rasterize_forward(b, bg)
+    rebuilt = splat.resolve_binned(b)
+    cap = hint if hint is not None else ref.num_intersects
+    assert rebuilt == (cap < ref.num_intersects)
+    if rebuilt:
+        out, T, idx = splat.rasterize_forward(b, bg)
+    assert b.num_intersects == ref.num_intersects and b.pending is None
+    np.testing.assert_array_equal(b.primitive_ids_sorted.cpu().numpy(),
+                                  ref.primitive_ids_sorted.cpu().numpy())
+    np.testing.assert_array_equal(b.tile_bins.cpu().numpy(), ref.tile_bins.cpu().numpy())
+    assert torch.equal(out, out_ref) and torch.equal(T, T_ref) and torch.equal(idx, idx_ref)
+
+
+@pytest.mark.gpu
+def test_function_forward_reuses_capacity_hint_across_scene_growth():
+    """Repeated renders of one scene shape: the second render grows past the
+    first one's buffer hint (rebuild path), the third fits; all bit-exact."""
+    import manbo
+    from repo_amd import splat
+    from helpers import oracle_forward
+    splat._CAPACITY_HINTS.clear()
+    for k, rmax in enumerate((6.0, 45.0, 44.0)):
+        sc = synth.small_scene(9, P=16, h=64, w=96, rmax=rmax)
+        s = sc.to("cuda")
+        img = manbo.ops.render_cubic_fill_splat_tilelang(
+            s.cubics_norm, s.seg_offsets, s.colors, s.opacities, s.depths, s.img_h, s.img_w,
+            16, 16, s.background, aa_widths=s.aa_widths, distance_samples=s.S)
+        fw = oracle_forward(sc)
+        np.testing.assert_array_equal(_bits(img.cpu().numpy()), _bits(fw["out"]))
+    assert len(splat._CAPACITY_HINTS) == 1
