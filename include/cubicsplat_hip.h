@@ -93,14 +93,15 @@ int cs_isect_edge_ranges(const int32_t* prim_ids_sorted, const int32_t* seg_offs
  * (ops/cubic_splatting.py:2815-2880, ops/cubic_polyline_splatting.py:1027-1098):
  * project + exact AABB + tile ranges, uniform Bernstein flattening
  * (ops/cubic_splatting.py:1709-1719), per-primitive tile counts, depth ranks
- * (order[r] = primitive of depth rank r, ties by primitive id), per-tile list
- * lengths (tile_count [T]) and first slots (tile_start [T]) with their per-part
- * offsets (tile_part_base [K*T], K = cs_bin_tile_parts(...)), and status[4]
- * (device int32) = {intersection total, 1 if seg_offsets is not a valid CSR
- * of nseg segments (the kernels then clamp every range), seg_offsets[0],
- * seg_offsets[nprim]}.  T = ceil(W/block_x) * ceil(H/block_y).  keys, keys_alt,
- * vals_alt hold nprim elements; radix_counts cs_radix_counts_elems(nprim);
- * scan_temp cs_scan_temp_elems(max(nprim, T)).
+ * (order[r] = primitive of depth rank r, ties by primitive id, and
+ * rank_tile_ranges [nprim,4] its tile rectangle), per-tile list lengths
+ * (tile_count [T]) with their per-part offsets (tile_part_base [K*T],
+ * K = cs_bin_tile_parts(...)), per-row-segment first slots (tile_scratch [T]),
+ * and status[4] (device int32) = {intersection total, 1 if seg_offsets is not
+ * a valid CSR of nseg segments (the kernels then clamp every range),
+ * seg_offsets[0], seg_offsets[nprim]}.  T = ceil(W/block_x) * ceil(H/block_y).
+ * keys, keys_alt, vals_alt hold nprim elements; radix_counts
+ * cs_radix_counts_elems(nprim); scan_temp cs_scan_temp_elems(max(nprim, T)).
  * mode 0 = closed fill, 1 = open stroke (stroke_widths required). */
 int32_t cs_bin_tile_parts(int32_t nprim, int32_t img_h, int32_t img_w, int32_t block_x,
                           int32_t block_y);
@@ -113,8 +114,9 @@ int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const f
                    void* edge_culls, int32_t* prim_tile_ranges, uint32_t* num_tiles_hit,
                    float* inv_sigma2s, void* prim_recs, uint32_t* keys, int32_t* order,
                    uint32_t* keys_alt, int32_t* vals_alt, uint32_t* radix_counts,
-                   uint32_t* scan_temp, uint32_t* tile_part_base, uint32_t* tile_count,
-                   uint32_t* tile_start, int32_t* status, hipStream_t stream);
+                   uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_part_base,
+                   uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
+                   hipStream_t stream);
 
 /* Stage 2 (ops/cubic_splatting.py:2888-2908, the sort of :2895-2896 and
  * get_tile_bin_edges of ops/tile_bins.py:10-60): each tile's primitives in
@@ -127,10 +129,10 @@ int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const f
  * larger buffer).  zero_buf (optional, zero_n floats) is cleared by the same
  * launch: the caller's gradient accumulators for cs_rasterize_backward, which
  * saves that step a separate fill. */
-int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges, int32_t nprim,
+int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t nprim,
                   const int32_t* status, int64_t capacity, int32_t img_h, int32_t img_w,
                   int32_t block_x, int32_t block_y, uint32_t* tile_part_base,
-                  uint32_t* tile_count, const uint32_t* tile_start, int32_t* prim_ids_sorted,
+                  uint32_t* tile_count, uint32_t* tile_scratch, int32_t* prim_ids_sorted,
                   int32_t* tile_bins, float* zero_buf, int64_t zero_n, hipStream_t stream);
 
 /* ---------------- rasterization ---------------- */

@@ -567,12 +567,26 @@ __device__ __forceinline__ int stable_rank(const uint32_t* __restrict__ keys, in
 }
 
 // order[position of key i] = i.
+// Also copies primitive i's tile rectangle to its rank's slot of rank_rects.
 __global__ __launch_bounds__(256) void k_rank_order(const uint32_t* __restrict__ keys, int n,
-                                                   int32_t* __restrict__ order) {
+                                                   const int4* __restrict__ prim_rects,
+                                                   int32_t* __restrict__ order,
+                                                   int4* __restrict__ rank_rects) {
     const int i = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (i >= n) return;
     const int pos = stable_rank(keys, n, i, keys[i]);
-    if ((threadIdx.x & (kWave - 1)) == 0) order[pos] = i;
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        order[pos] = i;
+        rank_rects[pos] = prim_rects[i];
+    }
+}
+
+// rank_rects[r] = prim_rects[order[r]] (after the radix sort of many keys).
+__global__ __launch_bounds__(256) void k_gather_rects(const int32_t* __restrict__ order, int n,
+                                                     const int4* __restrict__ prim_rects,
+                                                     int4* __restrict__ rank_rects) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < n) rank_rects[r] = prim_rects[order[r]];
 }
 
 // (key, value) pairs into their stable sorted positions of kout / vout.
@@ -598,25 +612,28 @@ __global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ a, int n
 }
 
 // Per-tile lists without a global sort.  Primitives cover rectangles of
-// tiles and arrive in depth-rank order (order[r]), so the list of tile t is
-// the subsequence of ranks whose rectangle contains t, and a stable counting
-// sort by tile needs, per (tile, rank), the number of earlier ranks covering
-// the tile.  One workgroup owns a row segment of up to 64 tiles (lane = tile
-// column) and splits the ranks into K contiguous parts, one wave each.  A wave
-// walks its part in 64-rank chunks: lanes test one primitive's rectangle
-// against the segment's row and columns, and for each hit (in rank order) every
-// lane checks its own column.  The counting launch leaves per-part counts;
-// their prefix over parts, plus the exclusive scan of the tile totals, gives
-// each (part, tile) its first output slot; the scatter launch walks the same
-// ranks again with a per-lane cursor.
+// tiles and arrive in depth-rank order (order[r], rank_rects[r]), so the list
+// of tile t is the subsequence of ranks whose rectangle contains t, and a
+// stable counting sort by tile needs, per (tile, rank), the number of earlier
+// ranks covering the tile.  One workgroup owns a row segment of up to 64 tiles
+// (lane = tile column) and splits the ranks into K contiguous parts, one wave
+// each.  A wave walks its part in 64-rank chunks (the next chunk's loads in
+// flight): lanes test one rectangle each against the segment's row and
+// columns, and for each hit (in rank order) every lane checks its own column.
+//   counting launch: per-part counts -> their prefix over parts (part_base),
+//     tile totals (tile_count) and the segment's total (seg_scratch[seg]);
+//   exclusive scan of the segment totals (in place; its total is I);
+//   scatter launch: tile start = segment start + prefix of the segment's tile
+//     totals; each wave walks its ranks again with a per-lane cursor, and the
+//     first wave writes tile_bins.
 constexpr int kSegTiles = kWave;
 constexpr int kMaxTileParts = 16;
 
 template <bool SCATTER>
 __global__ __launch_bounds__(kWave * kMaxTileParts) void k_tile_lists(
-    const int32_t* __restrict__ order, const int4* __restrict__ prim_tile_ranges, int P,
+    const int32_t* __restrict__ order, const int4* __restrict__ rank_rects, int P,
     int ranks_per_part, int tbx, int tby, int nsegcols, uint32_t* __restrict__ part_base,
-    uint32_t* __restrict__ tile_count, const uint32_t* __restrict__ tile_start,
+    uint32_t* __restrict__ tile_count, uint32_t* __restrict__ seg_scratch,
     int32_t* __restrict__ prim_ids_sorted, int32_t* __restrict__ tile_bins,
     float* __restrict__ zero_buf, int64_t zero_n, const int32_t* __restrict__ total,
     int64_t capacity) {
@@ -637,26 +654,41 @@ __global__ __launch_bounds__(kWave * kMaxTileParts) void k_tile_lists(
     const size_t T = (size_t)tbx * tby;
     const size_t t = (size_t)ty * tbx + tx;
     const int r0 = part * ranks_per_part, r1 = min(r0 + ranks_per_part, P);
-    if (SCATTER && (uint64_t)(uint32_t)*total > (uint64_t)capacity) {
-        // The lists do not fit the caller's buffer: every tile reads as
-        // empty, nothing is scattered, and the caller retries at full size.
-        if (part == 0 && tile_ok) {
-            tile_bins[2 * t] = 0;
-            tile_bins[2 * t + 1] = 0;
-        }
-        return;
-    }
     uint32_t cur = 0;
-    if (SCATTER && tile_ok) cur = tile_start[t] + part_base[(size_t)part * T + t];
-    for (int c = r0; c < r1; c += kWave) {
-        const int r = c + lane;
-        int p = 0;
-        int4 tr = make_int4(0, 0, 0, 0);
-        if (r < r1) {
-            p = order[r];
-            tr = prim_tile_ranges[p];
+    if (SCATTER) {
+        if ((uint64_t)(uint32_t)*total > (uint64_t)capacity) {
+            // The lists do not fit the caller's buffer: every tile reads as
+            // empty, nothing is scattered, and the caller retries at full size.
+            if (part == 0 && tile_ok) {
+                tile_bins[2 * t] = 0;
+                tile_bins[2 * t + 1] = 0;
+            }
+            return;
         }
-        const bool hit = r < r1 && tr.y <= ty && ty < tr.w && tr.x < sx1 && tr.z > sx0;
+        const uint32_t n = tile_ok ? tile_count[t] : 0u;
+        const uint32_t start = seg_scratch[blockIdx.x] + wave_incl_scan(n, lane) - n;
+        if (tile_ok) cur = start + part_base[(size_t)part * T + t];
+        if (part == 0 && tile_ok) {
+            // tile_bins.py:10-43: [start, end) per tile, (0, 0) when empty.
+            tile_bins[2 * t] = n ? (int32_t)start : 0;
+            tile_bins[2 * t + 1] = n ? (int32_t)(start + n) : 0;
+        }
+    }
+    int p_next = 0;
+    int4 tr_next = make_int4(0, 0, 0, 0);
+    if (r0 + lane < r1) {
+        p_next = order[r0 + lane];
+        tr_next = rank_rects[r0 + lane];
+    }
+    for (int c = r0; c < r1; c += kWave) {
+        const int p = p_next;
+        const int4 tr = tr_next;
+        const bool valid = c + lane < r1;
+        if (c + kWave + lane < r1) {
+            p_next = order[c + kWave + lane];
+            tr_next = rank_rects[c + kWave + lane];
+        }
+        const bool hit = valid && tr.y <= ty && ty < tr.w && tr.x < sx1 && tr.z > sx0;
         for (uint64_t m = __ballot(hit); m; m &= m - 1) {
             const int b = (int)__builtin_ctzll(m);
             const int x0 = __builtin_amdgcn_readlane(tr.x, b);
@@ -672,20 +704,19 @@ __global__ __launch_bounds__(kWave * kMaxTileParts) void k_tile_lists(
     if (!SCATTER) {
         cnt[part][lane] = cur;
         __syncthreads();
-        if (part == 0 && tile_ok) {
+        if (part == 0) {
             uint32_t acc = 0;
-            for (int k = 0; k < K; ++k) {
-                const uint32_t v = cnt[k][lane];
-                part_base[(size_t)k * T + t] = acc;
-                acc += v;
+            if (tile_ok) {
+                for (int k = 0; k < K; ++k) {
+                    const uint32_t v = cnt[k][lane];
+                    part_base[(size_t)k * T + t] = acc;
+                    acc += v;
+                }
+                tile_count[t] = acc;
             }
-            tile_count[t] = acc;
+            const uint32_t seg = (uint32_t)wave_sum_i((int)acc);
+            if (lane == 0) seg_scratch[blockIdx.x] = seg;
         }
-    } else if (part == 0 && tile_ok) {
-        // tile_bins.py:10-43: [start, end) per tile, (0, 0) when empty.
-        const uint32_t n = tile_count[t], s0 = tile_start[t];
-        tile_bins[2 * t] = n ? (int32_t)s0 : 0;
-        tile_bins[2 * t + 1] = n ? (int32_t)(s0 + n) : 0;
     }
 }
 
@@ -910,8 +941,9 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                               float* inv_sigma2s, void* prim_recs, uint32_t* keys,
                               int32_t* order, uint32_t* keys_alt, int32_t* vals_alt,
                               uint32_t* radix_counts, uint32_t* scan_temp,
-                              uint32_t* tile_part_base, uint32_t* tile_count,
-                              uint32_t* tile_start, int32_t* status, hipStream_t stream) {
+                              int32_t* rank_tile_ranges, uint32_t* tile_part_base,
+                              uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
+                              hipStream_t stream) {
     if (nseg < 0 || nprim <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0 ||
         samples < 2 || (mode != 0 && mode != 1) || img_h > kMaxImageDim ||
         img_w > kMaxImageDim)
@@ -933,33 +965,38 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                        num_tiles_hit, inv_sigma2s, keys, order,
                        reinterpret_cast<PrimRec*>(prim_recs));
     // Depth ranks: order[r] = primitive with the r-th smallest depth key
-    // (ties by primitive id).
+    // (ties by primitive id), and the ranks' tile rectangles.
+    int4* rank_rects = reinterpret_cast<int4*>(rank_tile_ranges);
+    const int4* prim_rects = reinterpret_cast<const int4*>(prim_tile_ranges);
     if (nprim <= kRankSortMax) {
         hipLaunchKernelGGL(k_rank_order, dim3((nprim + 3) / 4), dim3(256), 0, stream, keys,
-                           nprim, order);
+                           nprim, prim_rects, order, rank_rects);
     } else {
         const int rc = cs_radix_sort_pairs_u32(keys, order, keys_alt, vals_alt, nprim, 32,
                                                radix_counts, scan_temp, stream);
         if (rc) return rc;
+        hipLaunchKernelGGL(k_gather_rects, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
+                           order, nprim, prim_rects, rank_rects);
     }
-    // Per-(part, tile) counts and their prefix over parts, then the tiles'
-    // first slots; status[0] receives the intersection total.
+    // Per-(part, tile) counts and their prefix over parts, per-segment totals,
+    // then the segments' first slots; status[0] receives the intersection total.
     const int K = tile_parts(nprim, tbx, tby);
     const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
     const int ranks_per_part = (nprim + K - 1) / K;
     hipLaunchKernelGGL(k_tile_lists<false>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
-                       order, reinterpret_cast<const int4*>(prim_tile_ranges), nprim,
-                       ranks_per_part, tbx, tby, nsegcols, tile_part_base, tile_count,
-                       (const uint32_t*)nullptr, (int32_t*)nullptr, (int32_t*)nullptr,
-                       (float*)nullptr, (int64_t)0, (const int32_t*)nullptr, (int64_t)0);
-    return cs_scan_exclusive_u32(tile_count, tile_start, tbx * tby, scan_temp, status, stream);
+                       order, rank_rects, nprim, ranks_per_part, tbx, tby, nsegcols,
+                       tile_part_base, tile_count, tile_scratch, (int32_t*)nullptr,
+                       (int32_t*)nullptr, (float*)nullptr, (int64_t)0, (const int32_t*)nullptr,
+                       (int64_t)0);
+    return cs_scan_exclusive_u32(tile_scratch, tile_scratch, nsegcols * tby, scan_temp, status,
+                                 stream);
 }
 
-extern "C" int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_ranges,
+extern "C" int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges,
                              int32_t nprim, const int32_t* status, int64_t capacity,
                              int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
                              uint32_t* tile_part_base, uint32_t* tile_count,
-                             const uint32_t* tile_start, int32_t* prim_ids_sorted,
+                             uint32_t* tile_scratch, int32_t* prim_ids_sorted,
                              int32_t* tile_bins, float* zero_buf, int64_t zero_n,
                              hipStream_t stream) {
     if (nprim <= 0 || !status || capacity < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 ||
@@ -970,10 +1007,10 @@ extern "C" int cs_bin_finish(const int32_t* order, const int32_t* prim_tile_rang
     const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
     const int ranks_per_part = (nprim + K - 1) / K;
     hipLaunchKernelGGL(k_tile_lists<true>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
-                       order, reinterpret_cast<const int4*>(prim_tile_ranges), nprim,
-                       ranks_per_part, tbx, tby, nsegcols, tile_part_base, tile_count, tile_start,
-                       prim_ids_sorted, tile_bins, zero_n > 0 ? zero_buf : nullptr, zero_n,
-                       status, capacity);
+                       order, reinterpret_cast<const int4*>(rank_tile_ranges), nprim,
+                       ranks_per_part, tbx, tby, nsegcols, tile_part_base, tile_count,
+                       tile_scratch, prim_ids_sorted, tile_bins,
+                       zero_n > 0 ? zero_buf : nullptr, zero_n, status, capacity);
     return launch_status();
 }
 

@@ -150,6 +150,16 @@ __device__ __forceinline__ int32_t f2i_sat(float x) {
     return (int32_t)x;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (block b on XCD b % 8);
+// this maps block b to tile index x * ceil-share + k so that each XCD gets a
+// contiguous run of tiles and neighbouring tiles (which share input rows,
+// halos or primitives) hit the same L2.  Bijective on [0, n) for any n.
+__device__ __forceinline__ int xcd_tile(int b, int n) {
+    const int q = n >> 3, r = n & 7;
+    const int x = b & 7, k = b >> 3;
+    return x * q + min(x, r) + k;
+}
+
 __device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) {
     return v < lo ? lo : (v > hi ? hi : v);
 }

@@ -183,8 +183,12 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
     constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
     __shared__ float hm[5][IT][HP];
     __shared__ float sh[4];
-    const int c = blockIdx.z;
-    const int ox0 = blockIdx.x * kSsimTW, oy0 = blockIdx.y * kSsimTH;
+    // 1D grid over (channel, tile row, tile column), XCD-aware.
+    const int ntx = (ow + kSsimTW - 1) / kSsimTW, nty = (oh + kSsimTH - 1) / kSsimTH;
+    const int tile = xcd_tile(blockIdx.x, ntx * nty * nc);
+    const int c = tile / (ntx * nty);
+    const int ty = (tile - c * ntx * nty) / ntx, tx = tile - c * ntx * nty - ty * ntx;
+    const int ox0 = tx * kSsimTW, oy0 = ty * kSsimTH;
     const float* xc = x + (size_t)c * h * w;
     const float* yc = y + (size_t)c * h * w;
     float g[WIN];
@@ -281,8 +285,7 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
         }
     }
     const float bs = block_sum(acc, sh);
-    if (threadIdx.x == 0)
-        partials[(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x] = bs;
+    if (threadIdx.x == 0) partials[tile] = bs;
 }
 
 // grad_x[p] = scale * sum over map pixels o of the window w(p - o) times
@@ -300,8 +303,12 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
     using TT = SsimTile<WIN>;
     constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
     __shared__ float hs[3][IT][HP];
-    const int c = blockIdx.z;
-    const int px0 = blockIdx.x * kSsimTW, py0 = blockIdx.y * kSsimTH;
+    // 1D grid over (channel, tile row, tile column), XCD-aware.
+    const int ntx = (w + kSsimTW - 1) / kSsimTW, nty = (h + kSsimTH - 1) / kSsimTH;
+    const int tile = xcd_tile(blockIdx.x, ntx * nty * nc);
+    const int c = tile / (ntx * nty);
+    const int ty = (tile - c * ntx * nty) / ntx, tx = tile - c * ntx * nty - ty * ntx;
+    const int px0 = tx * kSsimTW, py0 = ty * kSsimTH;
     const size_t ld = abc_ld(ow);
     const size_t plane = (size_t)oh * ld;
     const size_t stride = (size_t)nc * plane;
@@ -473,7 +480,7 @@ static int launch_ssim_fwd(const float* x, const float* y, int32_t nc, int32_t h
                            const float* win1d, int32_t win, float c1, float c2,
                            float* partials, float* abc, hipStream_t stream, int* nblk) {
     const int oh = h - win + 1, ow = w - win + 1;
-    const dim3 grid((ow + kSsimTW - 1) / kSsimTW, (oh + kSsimTH - 1) / kSsimTH, nc);
+    const dim3 grid(((ow + kSsimTW - 1) / kSsimTW) * ((oh + kSsimTH - 1) / kSsimTH) * nc);
 #define CS_SSIM_FWD(W_)                                                                       \
     hipLaunchKernelGGL(k_ssim_fwd<W_>, grid, dim3(256), 0, stream, x, y, h, w, oh, ow, win1d, \
                        c1, c2, partials, abc, nc)
@@ -498,7 +505,7 @@ static int launch_ssim_bwd(const float* x, const float* y, int32_t nc, int32_t h
                            const float* grad_out, float ssim_coef, float mse_coef, float* grad_x,
                            hipStream_t stream) {
     const int oh = h - win + 1, ow = w - win + 1;
-    const dim3 grid((w + kSsimTW - 1) / kSsimTW, (h + kSsimTH - 1) / kSsimTH, nc);
+    const dim3 grid(((w + kSsimTW - 1) / kSsimTW) * ((h + kSsimTH - 1) / kSsimTH) * nc);
 #define CS_SSIM_BWD(W_)                                                                     \
     hipLaunchKernelGGL(k_ssim_bwd<W_>, grid, dim3(256), 0, stream, x, y, h, w, oh, ow, win1d, \
                        abc, grad_out, ssim_coef, mse_coef, nc, grad_x)

@@ -28,15 +28,6 @@ static_assert(sizeof(EdgeRec) == CS_EDGE_RECORD_BYTES, "edge record layout");
 static_assert(sizeof(PrimRec) == CS_PRIM_RECORD_BYTES, "primitive record layout");
 static_assert(sizeof(EdgeCull) == CS_EDGE_CULL_BYTES, "edge cull record layout");
 
-// Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
-// contiguous run of tiles so neighbouring tiles (which share primitives and
-// their edge records) hit the same L2.  Bijective for any tile count.
-__device__ __forceinline__ int xcd_tile(int b, int n) {
-    const int q = n >> 3, r = n & 7;
-    const int x = b & 7, k = b >> 3;
-    return x * q + min(x, r) + k;
-}
-
 // Crossing parity equals winding & 1 (each crossing changes the winding by
 // +-1), so only the winding number is tracked.
 struct Geom {

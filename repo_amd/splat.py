@@ -158,9 +158,10 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     T = tbx * tby
     scan_temp = torch.empty((int(lib.cs_scan_temp_elems(max(P, T))),), dtype=i32, device=dev)
     K = int(lib.cs_bin_tile_parts(P, img_h, img_w, block_x, block_y))
+    rank_tile_ranges = torch.empty((P, 4), dtype=i32, device=dev)
     tile_part_base = torch.empty((K * T,), dtype=i32, device=dev)
     tile_count = torch.empty((T,), dtype=i32, device=dev)
-    tile_start = torch.empty((T,), dtype=i32, device=dev)
+    tile_scratch = torch.empty((T,), dtype=i32, device=dev)
     status = torch.empty((4,), dtype=i32, device=dev)
     st = N.stream(dev)
     with N.prof("cubic.fwd.bin_prepare"):
@@ -170,17 +171,17 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
                int(bool(aniso)), mode, N.ptr(cubics_px), N.ptr(seg_tile_ranges), N.ptr(seg_recs),
                N.ptr(edges), N.ptr(edge_culls), N.ptr(prim_tile_ranges), N.ptr(num_tiles_hit),
                N.ptr(inv_sigma2s), N.ptr(prim_recs), N.ptr(keys), N.ptr(order), N.ptr(keys_alt),
-               N.ptr(vals_alt), N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(tile_part_base),
-               N.ptr(tile_count), N.ptr(tile_start), N.ptr(status), st)
+               N.ptr(vals_alt), N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(rank_tile_ranges),
+               N.ptr(tile_part_base), N.ptr(tile_count), N.ptr(tile_scratch), N.ptr(status), st)
     grad_accum = torch.empty((_grad_accum_elems(nseg, P, mode),), dtype=f32, device=dev)
     tile_bins = torch.empty((T, 2), dtype=i32, device=dev)
 
     def finish(capacity: int) -> torch.Tensor:
         ids = torch.empty((capacity,), dtype=i32, device=dev)
         with N.prof("cubic.fwd.bin_finish"):
-            N.call("cs_bin_finish", N.ptr(order), N.ptr(prim_tile_ranges), P, N.ptr(status),
+            N.call("cs_bin_finish", N.ptr(order), N.ptr(rank_tile_ranges), P, N.ptr(status),
                    capacity, img_h, img_w, block_x, block_y, N.ptr(tile_part_base),
-                   N.ptr(tile_count), N.ptr(tile_start), N.ptr(ids), N.ptr(tile_bins),
+                   N.ptr(tile_count), N.ptr(tile_scratch), N.ptr(ids), N.ptr(tile_bins),
                    N.ptr(grad_accum), int(grad_accum.numel()), st)
         return ids
 
