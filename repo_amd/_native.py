@@ -101,14 +101,26 @@ def exported_symbols():
 
 
 def ptr(t):
-    """Device pointer of a tensor (None -> NULL)."""
+    """Device pointer of a tensor as an int (None -> NULL); ctypes passes ints
+    for c_void_p parameters without building pointer objects."""
     if t is None:
         return None
-    return ctypes.c_void_p(t.data_ptr())
+    return t.data_ptr()
 
 
-def stream(device=None):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+_raw_stream = torch._C._cuda_getCurrentRawStream
+
+
+def stream(device=None) -> int:
+    """torch's current stream on `device` (a torch.device, an index or None
+    for the current device) as the raw hipStream_t."""
+    if device is None:
+        idx = torch.cuda.current_device()
+    elif isinstance(device, int):
+        idx = device
+    else:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+    return _raw_stream(idx)
 
 
 def check(rc: int, what: str) -> None:
@@ -118,8 +130,16 @@ def check(rc: int, what: str) -> None:
     raise RuntimeError(f"{what}: {kind} (status {rc})")
 
 
+_FUNCS = {}
+
+
 def call(name: str, *args) -> None:
-    check(getattr(lib(), name)(*args), name)
+    fn = _FUNCS.get(name)
+    if fn is None:
+        fn = _FUNCS[name] = getattr(lib(), name)
+    rc = fn(*args)
+    if rc != CS_OK:
+        check(rc, name)
 
 
 ProfileCtxFactory = Callable[[str], ContextManager]

@@ -6,18 +6,37 @@ a drop-in for that class on fp32 device parameters: same constructor, param
 groups, ``state`` entries (``step``, ``exp_avg``, ``exp_avg_sq``) and
 ``state_dict`` layout, so a checkpoint moves between the two.  The update is
 torch's single-tensor Adam (amsgrad and maximize off); one ``cs_adam_step``
-launch covers up to 16 tensors.
+launch covers up to 16 tensors.  Optimizer step pre/post hooks (global and
+per instance) run as for torch's optimizers; the profiler range torch wraps
+around ``step`` is left out, since it costs more host time than the launch.
 """
 from __future__ import annotations
 
 import ctypes
 import math
+from itertools import chain
 
 import torch
+from torch.optim import optimizer as _torch_optimizer
 
 from . import _native as N
 
 MAX_TENSORS_PER_LAUNCH = 16
+
+
+class _LaunchArgs:
+    """ctypes argument arrays for one launch of n tensors, reused across steps."""
+
+    def __init__(self, n):
+        self.n = n
+        self.params = (ctypes.c_void_p * n)()
+        self.grads = (ctypes.c_void_p * n)()
+        self.ms = (ctypes.c_void_p * n)()
+        self.vs = (ctypes.c_void_p * n)()
+        self.numels = (ctypes.c_int64 * n)()
+        self.step_sizes = (ctypes.c_float * n)()
+        self.bc2s = (ctypes.c_float * n)()
+        self.wds = (ctypes.c_float * n)()
 
 
 class Adam(torch.optim.Optimizer):
@@ -42,9 +61,22 @@ class Adam(torch.optim.Optimizer):
                         maximize=False, foreach=None, capturable=False, differentiable=False,
                         fused=None)
         super().__init__(params, defaults)
+        self._launch_args = {}
 
     @torch.no_grad()
     def step(self, closure=None):
+        args, kwargs = (self,), {"closure": closure} if closure is not None else {}
+        for pre_hook in chain(_torch_optimizer._global_optimizer_pre_hooks.values(),
+                              self._optimizer_step_pre_hooks.values()):
+            result = pre_hook(self, args, kwargs)
+            if result is not None:
+                if isinstance(result, tuple) and len(result) == 2:
+                    args, kwargs = result
+                else:
+                    raise RuntimeError(
+                        "optimizer step pre-hooks must return None or (args, kwargs), got "
+                        f"{result}")
+        closure = kwargs.get("closure", closure)
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -53,44 +85,57 @@ class Adam(torch.optim.Optimizer):
         for group in self.param_groups:
             beta1, beta2 = group["betas"]
             key = (float(beta1), float(beta2), float(group["eps"]))
+            lr, wd = float(group["lr"]), float(group["weight_decay"])
             for p in group["params"]:
-                if p.grad is None:
+                g = p.grad
+                if g is None:
                     continue
-                if p.grad.is_sparse:
+                if g.is_sparse:
                     raise RuntimeError("Adam does not support sparse gradients")
-                N.require_gpu(p, "parameter")
-                if p.dtype != torch.float32 or not p.is_contiguous():
-                    raise ValueError("repo_amd.optim.Adam needs contiguous float32 parameters")
+                if p.dtype != torch.float32 or not p.is_contiguous() or p.device.type != "cuda":
+                    raise ValueError(
+                        "repo_amd.optim.Adam needs contiguous float32 CUDA (ROCm) parameters")
                 st = self.state[p]
                 if len(st) == 0:
                     st["step"] = torch.tensor(0.0, dtype=torch.float32)
                     st["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
                     st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
-                st["step"] += 1
-                step = float(st["step"].item())
+                step_t = st["step"]
+                step_t += 1
+                step = float(step_t)
                 bc1 = 1.0 - beta1 ** step
                 bc2 = 1.0 - beta2 ** step
-                grad = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
-                batches.setdefault((p.device, key), []).append(
-                    (p, grad, st["exp_avg"], st["exp_avg_sq"], float(group["lr"]) / bc1,
-                     math.sqrt(bc2), float(group["weight_decay"])))
+                if not g.is_contiguous():
+                    g = g.contiguous()
+                batches.setdefault((p.device.index, key), []).append(
+                    (p, g, st["exp_avg"], st["exp_avg_sq"], lr / bc1, math.sqrt(bc2), wd))
         for (dev, (beta1, beta2, eps)), items in batches.items():
             for k in range(0, len(items), MAX_TENSORS_PER_LAUNCH):
                 self._launch(dev, items[k:k + MAX_TENSORS_PER_LAUNCH], beta1, beta2, eps)
+        self._optimizer_step_code()
+        for post_hook in chain(self._optimizer_step_post_hooks.values(),
+                               _torch_optimizer._global_optimizer_post_hooks.values()):
+            post_hook(self, args, kwargs)
         return loss
 
-    @staticmethod
-    def _launch(dev, items, beta1, beta2, eps):
+    # torch's Optimizer wraps `step` of each subclass in a profiler range unless
+    # the function is marked as already hooked; the hooks are called above.
+    step.hooked = True
+
+    def _launch(self, dev, items, beta1, beta2, eps):
         n = len(items)
-        vp = ctypes.c_void_p * n
-        params = vp(*[t[0].data_ptr() for t in items])
-        grads = vp(*[t[1].data_ptr() for t in items])
-        ms = vp(*[t[2].data_ptr() for t in items])
-        vs = vp(*[t[3].data_ptr() for t in items])
-        numels = (ctypes.c_int64 * n)(*[t[0].numel() for t in items])
-        step_sizes = (ctypes.c_float * n)(*[t[4] for t in items])
-        bc2s = (ctypes.c_float * n)(*[t[5] for t in items])
-        wds = (ctypes.c_float * n)(*[t[6] for t in items])
+        a = self._launch_args.get(n)
+        if a is None:
+            a = self._launch_args[n] = _LaunchArgs(n)
+        for k, (p, g, m, v, step_size, bc2s, wd) in enumerate(items):
+            a.params[k] = p.data_ptr()
+            a.grads[k] = g.data_ptr()
+            a.ms[k] = m.data_ptr()
+            a.vs[k] = v.data_ptr()
+            a.numels[k] = p.numel()
+            a.step_sizes[k] = step_size
+            a.bc2s[k] = bc2s
+            a.wds[k] = wd
         with N.prof("optim.adam"):
-            N.call("cs_adam_step", n, params, grads, ms, vs, numels, step_sizes, bc2s, wds,
-                   float(beta1), float(beta2), float(eps), N.stream(dev))
+            N.call("cs_adam_step", n, a.params, a.grads, a.ms, a.vs, a.numels, a.step_sizes,
+                   a.bc2s, a.wds, beta1, beta2, eps, N.stream(dev))

@@ -76,36 +76,99 @@ def tile_bounds(img_h: int, img_w: int, block_x: int = BLOCK_X, block_y: int = B
     return ((img_w + block_x - 1) // block_x, (img_h + block_y - 1) // block_y, 1)
 
 
-@dataclass
+# Buffers of one binning, carved from one arena allocation: name -> (dtype,
+# shape).  Shapes depend on (nseg, P, S, T, K, scratch sizes).
+def _binning_fields(nseg, P, E, T, K, radix_elems, scan_elems, grad_elems):
+    f32, i32 = torch.float32, torch.int32
+    return (
+        ("cubics_px", f32, (nseg, 4, 2)),
+        ("seg_tile_ranges", i32, (nseg, 4)),
+        ("seg_recs", i32, (nseg, N.SEG_RECORD_INTS)),
+        ("edges", f32, (E, N.EDGE_RECORD_FLOATS)),
+        ("edge_culls", i32, (E, N.EDGE_CULL_INTS)),
+        ("prim_tile_ranges", i32, (P, 4)),
+        ("num_tiles_hit", i32, (P,)),
+        ("inv_sigma2s", f32, (P,)),
+        ("prim_recs", f32, (P, N.PRIM_RECORD_FLOATS)),
+        ("keys", i32, (P,)),
+        ("order", i32, (P,)),
+        ("keys_alt", i32, (P,)),
+        ("vals_alt", i32, (P,)),
+        ("radix_counts", i32, (radix_elems,)),
+        ("scan_temp", i32, (scan_elems,)),
+        ("rank_tile_ranges", i32, (P, 4)),
+        ("tile_part_base", i32, (K * T,)),
+        ("tile_count", i32, (T,)),
+        ("tile_scratch", i32, (T,)),
+        ("status", i32, (4,)),
+        ("tile_bins", i32, (T, 2)),
+        ("grad_accum", f32, (grad_elems,)),
+    )
+
+
+_ALIGN = 256
+_LAYOUTS: "dict[tuple, tuple]" = {}
+
+
+def _layout(key, fields):
+    """{name: (byte offset, dtype, shape)} and the total size, cached per key."""
+    lay = _LAYOUTS.get(key)
+    if lay is None:
+        off, table = 0, {}
+        for name, dt, shape in fields:
+            n = 1
+            for d in shape:
+                n *= int(d)
+            table[name] = (off, dt, tuple(int(d) for d in shape))
+            off += (n * torch.empty((), dtype=dt).element_size() + _ALIGN - 1) // _ALIGN * _ALIGN
+        if len(_LAYOUTS) >= 64:
+            _LAYOUTS.pop(next(iter(_LAYOUTS)))
+        lay = _LAYOUTS[key] = (table, max(off, _ALIGN))
+    return lay
+
+
 class Binned:
-    """Everything the forward produces that the backward (and tests) use."""
-    mode: int
-    img_h: int
-    img_w: int
-    samples: int
-    nseg: int
-    nprim: int
-    num_intersects: int
-    cubics_px: torch.Tensor
-    seg_tile_ranges: torch.Tensor
-    seg_recs: torch.Tensor         # [nseg, 8] int32 cull ranges
-    edges: torch.Tensor            # [E, 8] x0 y0 x1 y1 vx vy ux uy
-    edge_culls: torch.Tensor       # [E, 4] int32 packed cull ranges
-    prim_tile_ranges: torch.Tensor
-    num_tiles_hit: torch.Tensor
-    inv_sigma2s: torch.Tensor
-    prim_recs: torch.Tensor
-    order: torch.Tensor            # depth rank -> primitive id
-    primitive_ids_sorted: torch.Tensor
-    tile_bins: torch.Tensor
-    # Gradient accumulators of the backward ([nseg*8 + P*(5|6)] fp32), cleared
-    # by the binning's last launch; `grad_accum_clean` turns False once a
-    # backward has used them.
-    grad_accum: Optional[torch.Tensor] = None
-    grad_accum_clean: bool = False
-    # Set while the intersection count has not been read on the host yet
-    # (bin_primitives with a capacity hint); resolve_binned() settles it.
-    pending: Optional["_PendingCount"] = None
+    """Everything the forward produces that the backward (and tests) use.
+    The binning buffers live in one arena; `ptr(name)` is a buffer's device
+    address and the attribute of the same name its tensor view (made on
+    first use): cubics_px [nseg,4,2], seg_tile_ranges [nseg,4], seg_recs
+    [nseg,8] (cull ranges), edges [E,8] (x0 y0 x1 y1 vx vy ux uy), edge_culls
+    [E,4], prim_tile_ranges [P,4], num_tiles_hit [P], inv_sigma2s [P],
+    prim_recs [P,20], order [P] (depth rank -> primitive id), tile_bins [T,2],
+    grad_accum (the backward's accumulators, cleared by the binning's last
+    launch)."""
+
+    def __init__(self, *, mode, img_h, img_w, samples, nseg, nprim, arena, table):
+        self.mode, self.img_h, self.img_w, self.samples = mode, img_h, img_w, samples
+        self.nseg, self.nprim = nseg, nprim
+        self.num_intersects = -1
+        self.arena = arena
+        self._table = table
+        self._base = arena.data_ptr()
+        self._views = {}
+        self.primitive_ids_sorted: Optional[torch.Tensor] = None
+        self.grad_accum_clean = True
+        # Set while the intersection count has not been read on the host yet
+        # (bin_primitives with a capacity hint); resolve_binned() settles it.
+        self.pending: Optional["_PendingCount"] = None
+
+    def ptr(self, name: str) -> int:
+        return self._base + self._table[name][0]
+
+    def __getattr__(self, name):
+        table = self.__dict__.get("_table")
+        if table is None or name not in table:
+            raise AttributeError(name)
+        v = self._views.get(name)
+        if v is None:
+            off, dt, shape = table[name]
+            n = 1
+            for d in shape:
+                n *= d
+            nbytes = n * torch.empty((), dtype=dt).element_size()
+            v = self.arena[off:off + nbytes].view(dt).view(shape)
+            self._views[name] = v
+        return v
 
     @property
     def edges_per_segment(self) -> int:
@@ -124,6 +187,21 @@ class _PendingCount:
     finish: Callable[[int], torch.Tensor]  # cs_bin_finish into a new buffer of that size
 
 
+# Pinned status buffers and their events, reused across forwards.
+_PINNED_POOL: "list[tuple]" = []
+
+
+def _take_pinned():
+    if _PINNED_POOL:
+        return _PINNED_POOL.pop()
+    return (torch.empty((4,), dtype=torch.int32, pin_memory=True), torch.cuda.Event())
+
+
+def _give_pinned(pair) -> None:
+    if len(_PINNED_POOL) < 16:
+        _PINNED_POOL.append(pair)
+
+
 def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rules, widths,
                    stroke_widths, img_h, img_w, samples, *, aabb_pad=DEFAULT_AABB_PAD,
                    aniso=False, mode=MODE_FILL, block_x=BLOCK_X, block_y=BLOCK_Y,
@@ -140,80 +218,71 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     S = max(2, int(samples))
     E = nseg * (S - 1)
     tbx, tby, _ = tile_bounds(img_h, img_w, block_x, block_y)
-    f32, i32 = torch.float32, torch.int32
-    cubics_px = torch.empty((nseg, 4, 2), dtype=f32, device=dev)
-    seg_tile_ranges = torch.empty((nseg, 4), dtype=i32, device=dev)
-    seg_recs = torch.empty((nseg, N.SEG_RECORD_INTS), dtype=i32, device=dev)
-    edges = torch.empty((E, N.EDGE_RECORD_FLOATS), dtype=f32, device=dev)
-    edge_culls = torch.empty((E, N.EDGE_CULL_INTS), dtype=i32, device=dev)
-    prim_tile_ranges = torch.empty((P, 4), dtype=i32, device=dev)
-    num_tiles_hit = torch.empty((P,), dtype=i32, device=dev)
-    inv_sigma2s = torch.empty((P,), dtype=f32, device=dev)
-    prim_recs = torch.empty((P, N.PRIM_RECORD_FLOATS), dtype=f32, device=dev)
-    keys = torch.empty((P,), dtype=i32, device=dev)
-    order = torch.empty((P,), dtype=i32, device=dev)
-    keys_alt = torch.empty((P,), dtype=i32, device=dev)
-    vals_alt = torch.empty((P,), dtype=i32, device=dev)
-    radix_counts = torch.empty((int(lib.cs_radix_counts_elems(P)),), dtype=i32, device=dev)
     T = tbx * tby
-    scan_temp = torch.empty((int(lib.cs_scan_temp_elems(max(P, T))),), dtype=i32, device=dev)
-    K = int(lib.cs_bin_tile_parts(P, img_h, img_w, block_x, block_y))
-    rank_tile_ranges = torch.empty((P, 4), dtype=i32, device=dev)
-    tile_part_base = torch.empty((K * T,), dtype=i32, device=dev)
-    tile_count = torch.empty((T,), dtype=i32, device=dev)
-    tile_scratch = torch.empty((T,), dtype=i32, device=dev)
-    status = torch.empty((4,), dtype=i32, device=dev)
+    key = (dev.index, mode, nseg, P, S, img_h, img_w, block_x, block_y)
+    lay = _LAYOUTS.get(key)
+    if lay is None:
+        K = int(lib.cs_bin_tile_parts(P, img_h, img_w, block_x, block_y))
+        fields = _binning_fields(nseg, P, E, T, K, int(lib.cs_radix_counts_elems(P)),
+                                 int(lib.cs_scan_temp_elems(max(P, T))),
+                                 _grad_accum_elems(nseg, P, mode))
+        lay = _layout(key, fields)
+    table, nbytes = lay
+    arena = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    b = Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P, arena=arena,
+               table=table)
+    q = b.ptr
     st = N.stream(dev)
     with N.prof("cubic.fwd.bin_prepare"):
         N.call("cs_bin_prepare", N.ptr(cubics_norm), N.ptr(seg_offsets), N.ptr(colors),
                N.ptr(opacities), N.ptr(depths), N.ptr(fill_rules), N.ptr(widths),
                N.ptr(stroke_widths), nseg, P, img_h, img_w, block_x, block_y, S, float(aabb_pad),
-               int(bool(aniso)), mode, N.ptr(cubics_px), N.ptr(seg_tile_ranges), N.ptr(seg_recs),
-               N.ptr(edges), N.ptr(edge_culls), N.ptr(prim_tile_ranges), N.ptr(num_tiles_hit),
-               N.ptr(inv_sigma2s), N.ptr(prim_recs), N.ptr(keys), N.ptr(order), N.ptr(keys_alt),
-               N.ptr(vals_alt), N.ptr(radix_counts), N.ptr(scan_temp), N.ptr(rank_tile_ranges),
-               N.ptr(tile_part_base), N.ptr(tile_count), N.ptr(tile_scratch), N.ptr(status), st)
-    grad_accum = torch.empty((_grad_accum_elems(nseg, P, mode),), dtype=f32, device=dev)
-    tile_bins = torch.empty((T, 2), dtype=i32, device=dev)
+               int(bool(aniso)), mode, q("cubics_px"), q("seg_tile_ranges"), q("seg_recs"),
+               q("edges"), q("edge_culls"), q("prim_tile_ranges"), q("num_tiles_hit"),
+               q("inv_sigma2s"), q("prim_recs"), q("keys"), q("order"), q("keys_alt"),
+               q("vals_alt"), q("radix_counts"), q("scan_temp"), q("rank_tile_ranges"),
+               q("tile_part_base"), q("tile_count"), q("tile_scratch"), q("status"), st)
+    grad_n = table["grad_accum"][2][0]
 
     def finish(capacity: int) -> torch.Tensor:
-        ids = torch.empty((capacity,), dtype=i32, device=dev)
+        ids = torch.empty((capacity,), dtype=torch.int32, device=dev)
         with N.prof("cubic.fwd.bin_finish"):
-            N.call("cs_bin_finish", N.ptr(order), N.ptr(rank_tile_ranges), P, N.ptr(status),
-                   capacity, img_h, img_w, block_x, block_y, N.ptr(tile_part_base),
-                   N.ptr(tile_count), N.ptr(tile_scratch), N.ptr(ids), N.ptr(tile_bins),
-                   N.ptr(grad_accum), int(grad_accum.numel()), st)
+            N.call("cs_bin_finish", q("order"), q("rank_tile_ranges"), P, q("status"), capacity,
+                   img_h, img_w, block_x, block_y, q("tile_part_base"), q("tile_count"),
+                   q("tile_scratch"), ids.data_ptr(), q("tile_bins"), q("grad_accum"), grad_n,
+                   st)
         return ids
 
     # The one host read of the forward (the reference reads the same count,
     # cubic_splatting.py:2879).  With a capacity hint the lists are built into
     # a buffer of that size first and the count is checked afterwards, so the
     # GPU does not idle while the host waits for it.
-    status_host = torch.empty((4,), dtype=i32, pin_memory=True)
-    status_host.copy_(status, non_blocking=True)
-    event = torch.cuda.Event()
-    event.record(torch.cuda.current_stream(dev))
+    status_host, event = _take_pinned()
+    status_host.copy_(b.status, non_blocking=True)
+    if dev.index == torch.cuda.current_device():
+        event.record()
+    else:
+        event.record(torch.cuda.current_stream(dev))
     pending = _PendingCount(status_host, event, -1, finish)
     if capacity_hint is None:
         I = _read_count(pending, nseg)
-        prim_ids = finish(I)
-        pending = None
+        b.primitive_ids_sorted = finish(I)
+        b.num_intersects = I
     else:
-        I = -1
         pending.capacity = max(0, int(capacity_hint))
-        prim_ids = finish(pending.capacity)
-    return Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P,
-                  num_intersects=I, cubics_px=cubics_px, seg_tile_ranges=seg_tile_ranges,
-                  seg_recs=seg_recs, edges=edges, edge_culls=edge_culls,
-                  prim_tile_ranges=prim_tile_ranges,
-                  num_tiles_hit=num_tiles_hit, inv_sigma2s=inv_sigma2s, prim_recs=prim_recs,
-                  order=order, primitive_ids_sorted=prim_ids, tile_bins=tile_bins,
-                  grad_accum=grad_accum, grad_accum_clean=True, pending=pending)
+        b.primitive_ids_sorted = finish(pending.capacity)
+        b.pending = pending
+    return b
+
+
+def _grad_accum_elems(nseg: int, nprim: int, mode: int) -> int:
+    return nseg * 8 + nprim * (6 if mode == MODE_STROKE else 5)
 
 
 def _read_count(pending: "_PendingCount", nseg: int) -> int:
     pending.event.synchronize()
     I, bad, first, last = pending.status_host.tolist()
+    _give_pinned((pending.status_host, pending.event))
     if bad or first != 0 or last != nseg:
         raise ValueError(
             "primitive_seg_offsets must start at 0 and end at num_segments "
@@ -250,20 +319,17 @@ def intersection_capacity(num_intersects: int) -> int:
     return (want + 4095) // 4096 * 4096
 
 
-def _grad_accum_elems(nseg: int, nprim: int, mode: int) -> int:
-    return nseg * 8 + nprim * (6 if mode == MODE_STROKE else 5)
-
-
 def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
     """(image [H,W,3], final_Ts, final_idx).  With eval_counts (int64 [5],
     zeroed, on the device) the counting instantiation runs and adds the
     evaluation counts of cs_rasterize_forward_counted into it."""
-    dev = b.edges.device
+    dev = b.arena.device
     out = torch.empty((b.img_h, b.img_w, 3), dtype=torch.float32, device=dev)
-    final_T = torch.empty((b.img_h, b.img_w), dtype=torch.float32, device=dev)
-    final_idx = torch.empty((b.img_h, b.img_w), dtype=torch.int32, device=dev)
-    args = (b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins), N.ptr(b.edges),
-            N.ptr(b.edge_culls), N.ptr(b.prim_recs), N.ptr(background), b.img_h, b.img_w,
+    # final_Ts and final_idx share one allocation (both 4-byte, [H, W]).
+    tid = torch.empty((2, b.img_h, b.img_w), dtype=torch.float32, device=dev)
+    final_T, final_idx = tid[0], tid[1].view(torch.int32)
+    args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
+            b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
             b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx))
     if eval_counts is not None:
         N.call("cs_rasterize_forward_counted", *args, N.ptr(_counts_buffer(eval_counts)),
@@ -286,9 +352,9 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_inv_sigma2s [P], v_stroke_widths [P] or None), accumulated into fresh
     zero buffers (cubic_splatting.py:2572-2747).  eval_counts as for
     rasterize_forward (cs_rasterize_backward_counted)."""
-    dev = b.edges.device
+    dev = b.arena.device
     P = b.nprim
-    if b.grad_accum is not None and b.grad_accum_clean:
+    if b.grad_accum_clean:
         zeros = b.grad_accum
         b.grad_accum_clean = False
     else:  # a second backward through the same forward
@@ -300,8 +366,8 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_opac = rest[3 * P: 4 * P]
     v_is2 = rest[4 * P: 5 * P]
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
-    args = (b.mode, N.ptr(b.primitive_ids_sorted), N.ptr(b.tile_bins), N.ptr(b.edges),
-            N.ptr(b.edge_culls), N.ptr(b.prim_recs), N.ptr(background), b.img_h, b.img_w,
+    args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
+            b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
             b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(v_output), N.ptr(v_px),
             N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
             N.ptr(curve_isect_contrib))
@@ -328,8 +394,10 @@ def accumulate_edge_grads(b: Binned, v_edges):
 def backward_finalize(b: Binned, v_cubics_px, widths, v_inv_sigma2s):
     """(v_cubics_norm, v_aa_widths) in one launch (cubic_splatting.py:3096-3104)."""
     dev = v_cubics_px.device
-    v_norm = torch.empty_like(v_cubics_px)
-    v_aa = torch.empty_like(v_inv_sigma2s)
+    n_cp, n_w = v_cubics_px.numel(), v_inv_sigma2s.numel()
+    buf = torch.empty((n_cp + n_w,), dtype=torch.float32, device=dev)
+    v_norm = buf[:n_cp].view(v_cubics_px.shape)
+    v_aa = buf[n_cp:]
     with N.prof("cubic.bwd.finalize"):
         N.call("cs_backward_finalize", N.ptr(v_cubics_px), b.nseg, b.img_h, b.img_w, N.ptr(widths),
                N.ptr(v_inv_sigma2s), int(widths.numel()), N.ptr(v_norm), N.ptr(v_aa), N.stream(dev))
@@ -427,7 +495,7 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
     ctx.distance_samples = int(distance_samples)
     ctx.mode = mode
     ctx.save_for_backward(cubics_norm, offs, colors_c, opac_c, depths, widths, bg, final_T,
-                          final_idx, sw_c if sw_c is not None else torch.empty(0))
+                          final_idx, sw_c)
     return out
 
 

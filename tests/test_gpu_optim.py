@@ -71,3 +71,24 @@ def test_adam_rejects_unsupported_options():
         Adam(p, amsgrad=True)
     with pytest.raises(ValueError):
         Adam(p, lr=-1.0)
+
+
+@pytest.mark.gpu
+def test_adam_runs_step_hooks_and_state_dict_round_trips():
+    from repo_amd.optim import Adam
+    p = torch.zeros(5, device="cuda", requires_grad=True)
+    opt = Adam([p], lr=0.1)
+    seen = []
+    h1 = opt.register_step_pre_hook(lambda o, a, k: seen.append("pre"))
+    h2 = opt.register_step_post_hook(lambda o, a, k: seen.append("post"))
+    p.grad = torch.ones_like(p)
+    opt.step()
+    assert seen == ["pre", "post"]
+    h1.remove()
+    h2.remove()
+    sd = opt.state_dict()
+    q = torch.zeros(5, device="cuda", requires_grad=True)
+    ref = torch.optim.Adam([q], lr=0.1)
+    ref.load_state_dict(sd)
+    assert float(ref.state[q]["step"]) == 1.0
+    assert torch.equal(ref.state[q]["exp_avg"], opt.state[p]["exp_avg"])
