@@ -135,6 +135,17 @@ __device__ __forceinline__ float cull_distance(int mode, float opacity, float in
     return half_sw + __builtin_sqrtf(2.0f * lo + 1.0f) / inv_sigma + 0.25f;
 }
 
+// The outside part of that bound for a fill: beyond it alpha < 1/255 (o cov
+// <= o exp(-2 d inv_sigma) and 2 d inv_sigma >= ln(255 o) + 1), whatever the
+// inside bound needs.  For strokes every pixel is outside: the cull distance.
+__device__ __forceinline__ float cull_distance_outside(int mode, float opacity, float inv_sigma,
+                                                       float half_sw) {
+    if (mode != 0) return cull_distance(mode, opacity, inv_sigma, half_sw);
+    if (!(opacity <= 3.0e38f)) return __builtin_huge_valf();
+    const float lo = __logf(fmaxf(255.0f * opacity, 1.0f));
+    return 0.5f * (lo + 1.0f) / inv_sigma + 0.25f;
+}
+
 struct PrimParams {
     float inv_sigma2;  // 1 / max(w^2, eps) (cubic_splatting.py:2820-2821)
     float inv_sigma;   // sqrt(max(inv_sigma2, eps))
@@ -349,7 +360,7 @@ __global__ __launch_bounds__(256) void k_prim_prep(
     rec.nx_lo = nx.lo;
     rec.nx_span = span_x(nx);
     rec.x_last = x_last;
-    rec.pad = 0;
+    rec.cull_out = cull_distance_outside(mode, opacities[p], q.inv_sigma, q.half_sw);
     recs[p] = rec;
 }
 

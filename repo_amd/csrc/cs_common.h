@@ -98,7 +98,8 @@ struct alignas(16) PrimRec {
     int32_t rule;       // 0 even-odd, else nonzero (fill)
     int32_t closed;     // 1 if the edge chain is closed
     int32_t ny_lo, ny_span, cy_lo, cy_span;  // unions over the segments
-    int32_t nx_lo, nx_span, x_last, pad;
+    int32_t nx_lo, nx_span, x_last;
+    float cull_out;     // the same for pixels outside a fill (alpha < 1/255 beyond it)
 };
 
 // Read-only data for the raster kernels, reached through the constant address

@@ -133,6 +133,22 @@ __device__ __forceinline__ int wave_count(const bool (&a)[kPix]) {
     return n;
 }
 
+// One edge record through the scalar cache as a single 32-byte load.
+typedef float v8f __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ EdgeRec load_edge(cptr<EdgeRec> ec, int k) {
+    const v8f v = *reinterpret_cast<cptr<v8f>>(ec + k);
+    EdgeRec e;
+    e.x0 = v[0];
+    e.y0 = v[1];
+    e.x1 = v[2];
+    e.y1 = v[3];
+    e.vx = v[4];
+    e.vy = v[5];
+    e.ux = v[6];
+    e.uy = v[7];
+    return e;
+}
+
 // Crossing term of an edge that lies entirely right of the wave (flag
 // kCullFarCrossExact): +1 on the rows an upward edge spans, -1 for a
 // downward one; cross_term evaluates to the same value there.
@@ -177,7 +193,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
         // wins ties); the crossing terms' order does not matter.
         for (uint64_t todo = mdn; todo; todo &= todo - 1) {
             const int k = (int)__builtin_ctzll(todo);
-            const EdgeRec E = ec[k];
+            const EdgeRec E = load_edge(ec, k);
             const float wx = px - E.x0;
             const bool cross = MODE == 0 && ((mcross >> k) & 1);
 #pragma unroll
@@ -191,7 +207,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
         // The minimum and the winding number do not depend on the order:
         // loops without per-edge tests.
         for (uint64_t todo = mdn & mcross; todo; todo &= todo - 1) {
-            const EdgeRec E = ec[__builtin_ctzll(todo)];
+            const EdgeRec E = load_edge(ec, (int)__builtin_ctzll(todo));
             const float wx = px - E.x0;
 #pragma unroll
             for (int p = 0; p < kPix; ++p) {
@@ -201,7 +217,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
             }
         }
         for (uint64_t todo = mdn & ~mcross; todo; todo &= todo - 1) {
-            const EdgeRec E = ec[__builtin_ctzll(todo)];
+            const EdgeRec E = load_edge(ec, (int)__builtin_ctzll(todo));
             const float wx = px - E.x0;
 #pragma unroll
             for (int p = 0; p < kPix; ++p) dist_term<false>(E, 0, wx, py[p] - E.y0, G[p]);
@@ -209,13 +225,13 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
     }
     if constexpr (MODE == 0) {
         for (uint64_t todo = mcross & ~mdn; todo; todo &= todo - 1) {
-            const EdgeRec E = ec[__builtin_ctzll(todo)];
+            const EdgeRec E = load_edge(ec, (int)__builtin_ctzll(todo));
             const float wx = px - E.x0;
 #pragma unroll
             for (int p = 0; p < kPix; ++p) cross_term(E, wx, py[p] - E.y0, py[p], G[p]);
         }
         for (uint64_t todo = mright; todo; todo &= todo - 1) {
-            const EdgeRec E = ec[__builtin_ctzll(todo)];
+            const EdgeRec E = load_edge(ec, (int)__builtin_ctzll(todo));
 #pragma unroll
             for (int p = 0; p < kPix; ++p) row_cross_term(E, py[p], G[p]);
         }
@@ -256,21 +272,35 @@ struct Cov {
 };
 
 // Fill: cubic_splatting.py:1138-1170; stroke: cubic_polyline_splatting.py:219-226.
-// A lane whose minimum over the evaluated edges exceeds the cull distance is
-// decided without exp/div/sqrt: inside a fill its coverage is exactly 1.0f
-// (1 + exp(-2 d inv_sigma) rounds to 1), outside (or for a stroke) its alpha
-// is below 1/255, which cov = 0 reproduces.  The exact branch only runs when
-// some lane of the wave needs it.
+// A lane whose minimum over the evaluated edges exceeds its bound is decided
+// without exp/div/sqrt: inside a fill beyond the cull distance its coverage is
+// exactly 1.0f (1 + exp(-2 d inv_sigma) rounds to 1); outside (or for a
+// stroke) beyond the smaller outside bound its alpha is below 1/255, which
+// cov = 0 reproduces.  The exact branch only runs when some lane of the wave
+// needs it.
 template <int MODE>
-__device__ __forceinline__ Cov coverage(const PrimRec& pr, const Geom& G, float D2) {
+__device__ __forceinline__ bool inside_of(const PrimRec& pr, const Geom& G) {
+    return MODE == 0 && (pr.rule == 0 ? ((G.winding & 1) != 0) : (G.winding != 0));
+}
+
+// Squared distance beyond which the lane's coverage is decided in closed form:
+// the cull distance inside a fill, the (smaller) outside bound elsewhere.
+template <int MODE>
+__device__ __forceinline__ bool needs_exact(const PrimRec& pr, const Geom& G, float D2_in,
+                                            float D2_out) {
+    return !(G.min_d2 > (inside_of<MODE>(pr, G) ? D2_in : D2_out));
+}
+
+template <int MODE>
+__device__ __forceinline__ Cov coverage(const PrimRec& pr, const Geom& G, float D2_in,
+                                        float D2_out) {
     Cov c;
-    const bool inside =
-        MODE == 0 && (pr.rule == 0 ? ((G.winding & 1) != 0) : (G.winding != 0));
+    const bool inside = inside_of<MODE>(pr, G);
     c.sgn = inside ? -1.0f : 1.0f;
     c.cov = inside ? 1.0f : 0.0f;
     c.dist = 0.0f;
     c.ed = 0.0f;
-    if (!(G.min_d2 > D2)) {
+    if (!(G.min_d2 > (inside ? D2_in : D2_out))) {
         c.dist = __builtin_sqrtf(fmaxf(G.min_d2, 0.0f));
         if (MODE == 0) {
             float logit = c.dist * pr.inv_sigma * 2.0f;
@@ -371,7 +401,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
         q_next = load_culls(culls, ns0 * eps, ns1 * eps);
         pid = pid_next;
         pid_next = pid_after;
-        const float D2 = pr.cull_d * pr.cull_d;
+        const float D2 = pr.cull_d * pr.cull_d, D2o = pr.cull_out * pr.cull_out;
         if (prim_culled<MODE>(pr, W)) continue;
         int npix = 0;
         if constexpr (COUNT) {
@@ -383,13 +413,14 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
         if constexpr (COUNT) {
             bool ex[kPix];
 #pragma unroll
-            for (int p = 0; p < kPix; ++p) ex[p] = live[p] && !(G[p].min_d2 > D2);
+            for (int p = 0; p < kPix; ++p)
+                ex[p] = live[p] && needs_exact<MODE>(pr, G[p], D2, D2o);
             n.cover += (uint64_t)wave_count(ex);
         }
 #pragma unroll
         for (int p = 0; p < kPix; ++p) {
             if (done[p]) continue;
-            const Cov c = coverage<MODE>(pr, G[p], D2);
+            const Cov c = coverage<MODE>(pr, G[p], D2, D2o);
             const float alpha = fminf(kAlphaCap, pr.opacity * c.cov);
             if (alpha >= kAlphaMin) {
                 const float nT = T[p] * (1.0f - alpha);
@@ -522,7 +553,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
         pid = pid_next;
         pid_next = pid_after;
         if (__ballot(any_valid) == 0) continue;
-        const float D2 = pr.cull_d * pr.cull_d;
+        const float D2 = pr.cull_d * pr.cull_d, D2o = pr.cull_out * pr.cull_out;
         if (prim_culled<MODE>(pr, W)) continue;
         int npix = 0;
         if constexpr (COUNT) {
@@ -534,7 +565,8 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
         if constexpr (COUNT) {
             bool ex[kPix];
 #pragma unroll
-            for (int p = 0; p < kPix; ++p) ex[p] = valid[p] && !(G[p].min_d2 > D2);
+            for (int p = 0; p < kPix; ++p)
+                ex[p] = valid[p] && needs_exact<MODE>(pr, G[p], D2, D2o);
             n.cover += (uint64_t)wave_count(ex);
         }
         // Per-primitive sums over the lane's pixels: v_r, v_g, v_b, v_opacity,
@@ -549,7 +581,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
             gx[p] = gy[p] = 0.0f;
             geom[p] = false;
             if (!valid[p]) continue;
-            const Cov c = coverage<MODE>(pr, G[p], D2);
+            const Cov c = coverage<MODE>(pr, G[p], D2, D2o);
             const float op = pr.opacity;
             const float alpha = fminf(kAlphaCap, op * c.cov);
             if (!(alpha >= kAlphaMin)) continue;
