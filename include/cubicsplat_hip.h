@@ -202,6 +202,25 @@ int cs_backward_finalize(const float* v_cubics_px, int32_t nseg, int32_t img_h, 
                          const float* widths, const float* v_inv_sigma2s, int32_t nprim,
                          float* v_cubics_norm, float* v_aa_widths, hipStream_t stream);
 
+/* ---------------- closed rings -> cubic segments ---------------- */
+
+/* closed_cubic_fill_segments_forward_kernel (ops/cubic_splatting.py:137-268):
+ * control_points [num_curves, K, 2] (K >= 4, K even; 8-byte aligned) ->
+ * out_segments [num_curves * 2 * subdiv, 4, 2] (16-byte aligned), with the
+ * basis tables of _closed_fill_piecewise_basis_tensors (:81-134): basis
+ * [subdiv+1, kb], deriv_basis [subdiv+1, kb-1], dt [subdiv], kb = (K+2)/2. */
+int cs_closed_ring_segments(const float* control_points, int32_t num_curves, int32_t K,
+                            int32_t subdiv, const float* basis, const float* deriv_basis,
+                            const float* dt, float* out_segments, hipStream_t stream);
+
+/* closed_cubic_fill_segments_backward_kernel (ops/cubic_splatting.py:271-383):
+ * grad_control_points [num_curves, K, 2] (written, not accumulated; 8-byte
+ * aligned) from grad_segments (16-byte aligned), deterministic (no atomics). */
+int cs_closed_ring_segments_backward(const float* grad_segments, int32_t num_curves, int32_t K,
+                                     int32_t subdiv, const float* basis,
+                                     const float* deriv_basis, const float* dt,
+                                     float* grad_control_points, hipStream_t stream);
+
 /* ---------------- losses ---------------- */
 
 /* Number of float partials cs_mse_forward / cs_ssim needs in `partials`, and

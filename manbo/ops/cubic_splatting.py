@@ -6,6 +6,11 @@ from repo_amd.blocks import (  # noqa: F401
     primitive_tile_ranges_from_segment_tile_ranges as _primitive_tile_ranges_from_segment_tile_ranges,
     project_cubics_2d_forward_tilelang,
 )
+from repo_amd.rings import (  # noqa: F401
+    _ClosedCubicFillSegmentsFn,
+    _closed_fill_piecewise_basis_tensors,
+    closed_cubic_fill_segments_tilelang,
+)
 from repo_amd.splat import (  # noqa: F401
     BLOCK_X,
     BLOCK_Y,
@@ -37,6 +42,7 @@ __all__ = [
     "DEFAULT_CUBIC_FLATTEN_METHOD",
     "DEFAULT_THREADS",
     "normalize_cubic_flatten_method",
+    "closed_cubic_fill_segments_tilelang",
     "map_cubic_to_intersects_tilelang",
     "project_cubics_2d_forward_tilelang",
     "render_cubic_fill_splat_tilelang",

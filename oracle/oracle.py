@@ -389,3 +389,75 @@ def ssim_torch64(x, y, win_size=11, win_sigma=1.5, data_range=1.0, k1=0.01, k2=0
     s12 = exy - mu1 * mu2
     m = ((2 * mu1 * mu2 + c1) / (mu1 * mu1 + mu2 * mu2 + c1)) * ((2 * s12 + c2) / (s1 + s2 + c2))
     return m.view(n, c, -1).mean(-1).mean()
+
+
+# ------------------------------------------------ closed ring -> Hermite cubics
+
+
+def closed_ring_basis(kb: int, subdiv: int):
+    """_closed_fill_piecewise_basis_tensors (ops/cubic_splatting.py:81-134) in
+    float64: Bernstein basis of degree kb-1 and of its derivative (degree
+    kb-2) at t = linspace(0, 1, subdiv+1), and the sample spacing."""
+    from math import comb
+    t = np.linspace(0.0, 1.0, subdiv + 1)
+    n = kb - 1
+    basis = np.stack([comb(n, i) * (1.0 - t) ** (n - i) * t ** i for i in range(kb)], 1)
+    deriv = np.stack([comb(n - 1, i) * (1.0 - t) ** (n - 1 - i) * t ** i for i in range(kb - 1)],
+                     1)
+    return basis, deriv, np.diff(t)
+
+
+def closed_ring_segments(cp, subdiv: int, basis=None, deriv=None, dt=None) -> np.ndarray:
+    """closed_cubic_fill_segments_forward_kernel (ops/cubic_splatting.py:137-268)
+    in float64: control polygon [N, K, 2] (K >= 4, K even) -> [N*2*subdiv, 4, 2].
+    Branch b in {0, 1} is the Bezier curve of degree kb-1 = K/2 on control
+    points b*(kb-1) + i (mod K); each branch is cut at the subdiv+1 samples
+    into cubic Hermite pieces: P0, P3 on the curve and P1 = P0 + d0 dt/3,
+    P2 = P3 - d1 dt/3 with d the curve's derivative."""
+    cp = np.asarray(cp, np.float64)
+    N, K, _ = cp.shape
+    kb = (K + 2) // 2
+    if basis is None:
+        basis, deriv, dt = closed_ring_basis(kb, subdiv)
+    basis, deriv, dt = (np.asarray(a, np.float64) for a in (basis, deriv, dt))
+    out = np.zeros((N, 2, subdiv, 4, 2))
+    for b in range(2):
+        idx = (b * (kb - 1) + np.arange(kb)) % K
+        pts = cp[:, idx]                                   # [N, kb, 2]
+        diffs = pts[:, 1:] - pts[:, :-1]                   # [N, kb-1, 2]
+        P = np.einsum("sk,nkc->nsc", basis, pts)           # [N, S+1, 2]
+        D = (kb - 1) * np.einsum("sk,nkc->nsc", deriv, diffs)
+        third = (dt / 3.0)[None, :, None]
+        out[:, b, :, 0] = P[:, :-1]
+        out[:, b, :, 3] = P[:, 1:]
+        out[:, b, :, 1] = P[:, :-1] + D[:, :-1] * third
+        out[:, b, :, 2] = P[:, 1:] - D[:, 1:] * third
+    return out.reshape(N * 2 * subdiv, 4, 2)
+
+
+def closed_ring_segments_backward(grad, N: int, K: int, subdiv: int, basis=None, deriv=None,
+                                  dt=None) -> np.ndarray:
+    """closed_cubic_fill_segments_backward_kernel (ops/cubic_splatting.py:271-383)
+    in float64: the transpose of the (linear) forward map applied to
+    grad [N*2*subdiv, 4, 2] -> [N, K, 2]."""
+    kb = (K + 2) // 2
+    if basis is None:
+        basis, deriv, dt = closed_ring_basis(kb, subdiv)
+    basis, deriv, dt = (np.asarray(a, np.float64) for a in (basis, deriv, dt))
+    g = np.asarray(grad, np.float64).reshape(N, 2, subdiv, 4, 2)
+    out = np.zeros((N, K, 2))
+    third = (dt / 3.0)[None, :, None]
+    for b in range(2):
+        idx = (b * (kb - 1) + np.arange(kb)) % K
+        gP = np.zeros((N, subdiv + 1, 2))
+        gD = np.zeros((N, subdiv + 1, 2))
+        gP[:, :-1] += g[:, b, :, 0] + g[:, b, :, 1]
+        gP[:, 1:] += g[:, b, :, 3] + g[:, b, :, 2]
+        gD[:, :-1] += g[:, b, :, 1] * third
+        gD[:, 1:] -= g[:, b, :, 2] * third
+        gpts = np.einsum("sk,nsc->nkc", basis, gP)
+        gdiff = (kb - 1) * np.einsum("sk,nsc->nkc", deriv, gD)
+        gpts[:, 1:] += gdiff
+        gpts[:, :-1] -= gdiff
+        np.add.at(out, (slice(None), idx), gpts)
+    return out
