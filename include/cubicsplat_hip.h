@@ -301,6 +301,84 @@ int cs_adam_step(int32_t ntensors, float* const* params, const float* const* gra
                  const float* weight_decays, double beta1, double beta2, double eps,
                  hipStream_t stream);
 
+/* ---------------- 2D Gaussian splats (GsRenderFunction) ---------------- */
+
+/* project_gaussians_2d_scale_rot_forward_kernel (ops/forward2d.py:14-164):
+ * means2d [n,2] in the normalized [-1,1] frame, scales2d [n,2], rotation [n]
+ * (8-byte aligned [n,2] arrays) -> xys [n,2], depths [n] (zeros), radii [n],
+ * conics [n,3], num_tiles_hit [n]; all zero for a Gaussian whose tile
+ * rectangle is empty.  block_x * block_y <= 1024. */
+int cs_gs_project_forward(const float* means2d, const float* scales2d, const float* rotation,
+                          int32_t n, int32_t img_h, int32_t img_w, int32_t block_x,
+                          int32_t block_y, float* xys, float* depths, int32_t* radii,
+                          float* conics, int32_t* num_tiles_hit, hipStream_t stream);
+
+/* Replaces tilelang_renderer.py:224-269 (cumsum, map_gaussian_to_intersects,
+ * torch.sort, get_tile_bin_edges) up to the count: per Gaussian the tile
+ * rectangle of ops/intersects.py:34-121 (tile_rects [n,4], 16-byte aligned)
+ * and the raw depth bits as key; depth ranks (ties by id: the stable order of
+ * the reference's sort); tile-list counts; status[0] = intersection total,
+ * status[1..3] = 0.  Scratch sizes as for cs_bin_prepare.  cs_bin_finish then
+ * writes gaussian_ids_sorted and tile_bins ([start, end) per tile, (0,0) when
+ * empty). */
+int cs_gs_bin_prepare(const float* xys, const float* conics, const int32_t* radii,
+                      const float* depths, int32_t n, int32_t img_h, int32_t img_w,
+                      int32_t block_x, int32_t block_y, int32_t* tile_rects, uint32_t* keys,
+                      int32_t* order, uint32_t* keys_alt, int32_t* vals_alt,
+                      uint32_t* radix_counts, uint32_t* scan_temp, int32_t* rank_tile_ranges,
+                      uint32_t* tile_part_base, uint32_t* tile_count, uint32_t* tile_scratch,
+                      int32_t* status, hipStream_t stream);
+
+/* The per-Gaussian raster records (48 bytes each, 16-byte aligned) that the
+ * two raster entry points read: centre, halved conic, opacity and its alpha
+ * cut, colour, conic diagonal.  No reference counterpart: the reference's
+ * raster kernels gather these fields from xys / conics / colors / opacities
+ * into shared memory per batch (ops/rasterize.py:92-103, :300-311). */
+#define CS_GS_RECORD_BYTES 48
+int cs_gs_pack_records(const float* xys, const float* conics, const float* colors,
+                       const float* opacities, int32_t n, void* records, hipStream_t stream);
+
+/* rasterize_forward_kernel (ops/rasterize.py:18-157): out_img [H,W,3],
+ * final_Ts [H,W], final_idx [H,W] (index of the pixel's last contributing
+ * intersection, 0 if none). */
+int cs_gs_rasterize_forward(const int32_t* gaussian_ids_sorted, const int32_t* tile_bins,
+                            const void* records, const float* background, int32_t img_h,
+                            int32_t img_w, int32_t block_x, int32_t block_y, float* out_img,
+                            float* final_Ts, int32_t* final_idx, hipStream_t stream);
+
+/* rasterize_backward_kernel (ops/rasterize.py:160-529): ADDS into v_xy [n,2],
+ * v_conic [n,3], v_rgb [n,3], v_opacity [n] and, when not NULL, contrib_rgb
+ * [n,3] and isect_contrib [num_intersects] (the caller zeroes them).
+ * intersect_meta_sorted NULL enables every intersection's geometry
+ * gradients; v_output_alpha NULL reads as zeros. */
+int cs_gs_rasterize_backward(const int32_t* gaussian_ids_sorted,
+                             const int32_t* intersect_meta_sorted, const int32_t* tile_bins,
+                             const void* records, const float* background, int32_t img_h,
+                             int32_t img_w, int32_t block_x, int32_t block_y,
+                             const float* final_Ts, const int32_t* final_idx,
+                             const float* v_output, const float* v_output_alpha, float* v_xy,
+                             float* v_conic, float* v_rgb, float* v_opacity, float* contrib_rgb,
+                             float* isect_contrib, hipStream_t stream);
+
+/* project_gaussians_2d_scale_rot_backward_kernel (ops/backward2d.py:8-151)
+ * with the gaussian_meta scaling of tilelang_renderer.py:111-116 (meta NULL:
+ * none).  v_cov2d may be NULL. */
+int cs_gs_project_backward(const float* scales2d, const float* rotation, const int32_t* radii,
+                           const float* conics, const float* v_xy, const float* v_conic,
+                           const int32_t* gaussian_meta, int32_t n, int32_t img_h, int32_t img_w,
+                           float* v_cov2d, float* v_mean2d, float* v_scale, float* v_rot,
+                           hipStream_t stream);
+
+/* map_gaussian_to_intersects{,_isotropic}_kernel (ops/intersects.py:12-226):
+ * the reference's int64 (tile << 32 | depth bits) keys and Gaussian ids at
+ * [cum_tiles_hit[g-1], cum_tiles_hit[g]); conics NULL selects the isotropic
+ * rectangle.  Entries outside [0, num_intersects) are not written. */
+int cs_gs_map_to_intersects(const float* xys, const float* conics, const float* depths,
+                            const int32_t* radii, const int32_t* cum_tiles_hit, int32_t n,
+                            int64_t num_intersects, int32_t tile_bound_x, int32_t tile_bound_y,
+                            int32_t block_x, int32_t block_y, int64_t* isect_ids,
+                            int32_t* gaussian_ids, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,6 +19,7 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _SRC = os.path.join(_HERE, "cs_oracle.c")
+_SRC_GS = os.path.join(_HERE, "gs_oracle.c")
 _LIB_PATH = os.path.join(_HERE, "_build", "libcs_oracle.so")
 _CFLAGS = ["-O2", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
            "-fno-math-errno", "-mfma", "-msse4.1"]
@@ -31,7 +32,7 @@ def build() -> str:
     """Compile the C restatement with gcc into oracle/_build/."""
     os.makedirs(os.path.dirname(_LIB_PATH), exist_ok=True)
     tmp = _LIB_PATH + ".tmp"
-    subprocess.check_call(["gcc", *_CFLAGS, "-o", tmp, _SRC, "-lm"])
+    subprocess.check_call(["gcc", *_CFLAGS, "-o", tmp, _SRC, _SRC_GS, "-lm"])
     os.replace(tmp, _LIB_PATH)
     return _LIB_PATH
 
@@ -42,7 +43,8 @@ _lib = None
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(_LIB_PATH):
+        if not os.path.exists(_LIB_PATH) or any(
+                os.path.getmtime(src) > os.path.getmtime(_LIB_PATH) for src in (_SRC, _SRC_GS)):
             build()
         L = ctypes.CDLL(_LIB_PATH)
         L.cs_expf.restype = ctypes.c_float
@@ -461,3 +463,140 @@ def closed_ring_segments_backward(grad, N: int, K: int, subdiv: int, basis=None,
         gpts[:, :-1] -= gdiff
         np.add.at(out, (slice(None), idx), gpts)
     return out
+
+
+# ------------------------------------------------------------ 2D Gaussians
+
+
+def sincosf(x):
+    """The spec sin/cos (gs_oracle.c orc_sincosf; the GPU's spec_sincosf)."""
+    x = _f32(x).reshape(-1)
+    sn = np.empty_like(x)
+    cs = np.empty_like(x)
+    lib().orc_sincosf_n(_p(x), ctypes.c_int32(x.size), _p(sn), _p(cs))
+    return sn, cs
+
+
+def gs_project(means2d, scales2d, rotation, img_h: int, img_w: int, block_x: int = 16,
+               block_y: int = 16):
+    """forward2d.py:14-164 -> (xys [N,2], depths [N] (zeros), radii [N] int32,
+    conics [N,3], num_tiles_hit [N] int32)."""
+    m, s, r = _f32(means2d).reshape(-1, 2), _f32(scales2d).reshape(-1, 2), _f32(rotation).reshape(-1)
+    n = m.shape[0]
+    xys = np.empty((n, 2), np.float32)
+    depths = np.empty(n, np.float32)
+    radii = np.empty(n, np.int32)
+    conics = np.empty((n, 3), np.float32)
+    tiles = np.empty(n, np.int32)
+    lib().orc_gs_project(_p(m), _p(s), _p(r), ctypes.c_int32(n), ctypes.c_int32(img_h),
+                         ctypes.c_int32(img_w), ctypes.c_int32(block_x), ctypes.c_int32(block_y),
+                         _p(xys), _p(depths), _p(radii), _p(conics), _p(tiles))
+    return xys, depths, radii, conics, tiles
+
+
+def gs_rects(xys, conics, radii, block_x: int, block_y: int, tbx: int, tby: int) -> np.ndarray:
+    """The tile rectangle (x0, y0, x1, y1) intersects.py:34-121 emits per
+    Gaussian; zeros when it emits nothing."""
+    xy, q, rad = _f32(xys).reshape(-1, 2), _f32(conics).reshape(-1, 3), _i32(radii).reshape(-1)
+    n = xy.shape[0]
+    rects = np.empty((n, 4), np.int32)
+    lib().orc_gs_rects(_p(xy), _p(q), _p(rad), ctypes.c_int32(n), ctypes.c_int32(block_x),
+                       ctypes.c_int32(block_y), ctypes.c_int32(tbx), ctypes.c_int32(tby),
+                       _p(rects))
+    return rects
+
+
+def gs_depth_keys(depths) -> np.ndarray:
+    """intersects.py:107-109: the raw fp32 bits as an unsigned 32-bit key."""
+    return _f32(depths).view(np.uint32)
+
+
+def gs_map_intersects(rects, depths, tbx: int):
+    """intersects.py:96-121: Gaussian-major, row-major emission of
+    (tile << 32 | depth bits) keys with the Gaussian id as value."""
+    rects = _i32(rects).reshape(-1, 4)
+    area = np.maximum(rects[:, 2] - rects[:, 0], 0) * np.maximum(rects[:, 3] - rects[:, 1], 0)
+    cum = np.cumsum(area.astype(np.int64))
+    n_total = int(cum[-1]) if cum.size else 0
+    keys = np.empty(n_total, np.int64)
+    ids = np.empty(n_total, np.int32)
+    dk = gs_depth_keys(depths).astype(np.int64)
+    for g in np.nonzero(area > 0)[0]:
+        x0, y0, x1, y1 = (int(v) for v in rects[g])
+        base = int(cum[g - 1]) if g > 0 else 0
+        ty, tx = np.meshgrid(np.arange(y0, y1), np.arange(x0, x1), indexing="ij")
+        tiles = (ty * tbx + tx).reshape(-1).astype(np.int64)
+        keys[base:base + tiles.size] = (tiles << 32) | dk[g]
+        ids[base:base + tiles.size] = g
+    return keys, ids
+
+
+def gs_bin(xys, conics, radii, depths, img_h: int, img_w: int, block_x: int, block_y: int):
+    """tilelang_renderer.py:224-269 (cumsum, map, stable sort, tile bins) ->
+    (gaussian_ids_sorted, tile_bins [T,2], isect_ids_sorted)."""
+    tbx, tby = tile_bounds(img_h, img_w, block_x, block_y)
+    rects = gs_rects(xys, conics, radii, block_x, block_y, tbx, tby)
+    keys, ids = gs_map_intersects(rects, depths, tbx)
+    keys_s, ids_s = sort_intersects(keys, ids)
+    return ids_s, tile_bins_from_sorted(keys_s, tbx * tby), keys_s
+
+
+def gs_raster_forward(ids_sorted, tile_bins, xys, conics, colors, opacities, background,
+                      img_h: int, img_w: int, block_x: int, block_y: int, rows=None):
+    """rasterize.py:18-157 -> (out [H,W,3], final_T [H,W], final_idx [H,W]).
+    `rows` = (row0, row1) restricts the work to those pixel rows (the other
+    rows of the outputs are left zero)."""
+    ids, bins = _i32(ids_sorted), _i32(tile_bins)
+    xy, q, col = _f32(xys), _f32(conics), _f32(colors)
+    op, bg = _f32(opacities).reshape(-1), _f32(background).reshape(-1)
+    r0, r1 = (0, img_h) if rows is None else rows
+    out = np.zeros((img_h, img_w, 3), np.float32)
+    fT = np.zeros((img_h, img_w), np.float32)
+    fi = np.zeros((img_h, img_w), np.int32)
+    lib().orc_gs_raster_forward(_p(ids), _p(bins), _p(xy), _p(q), _p(col), _p(op), _p(bg),
+                                ctypes.c_int32(img_h), ctypes.c_int32(img_w),
+                                ctypes.c_int32(block_x), ctypes.c_int32(block_y),
+                                ctypes.c_int32(r0), ctypes.c_int32(r1), _p(out), _p(fT), _p(fi))
+    return out, fT, fi
+
+
+def gs_raster_backward(ids_sorted, tile_bins, xys, conics, colors, opacities, background,
+                       img_h: int, img_w: int, block_x: int, block_y: int, final_T, final_idx,
+                       v_out, v_out_alpha=None, intersect_meta=None, rows=None):
+    """rasterize.py:160-529 -> float64 (v_xy, v_conic, v_rgb, v_opacity,
+    contrib_rgb, isect_contrib)."""
+    ids, bins = _i32(ids_sorted), _i32(tile_bins)
+    xy, q, col = _f32(xys), _f32(conics), _f32(colors)
+    op, bg = _f32(opacities).reshape(-1), _f32(background).reshape(-1)
+    fT, fi, vo = _f32(final_T), _i32(final_idx), _f32(v_out)
+    va = None if v_out_alpha is None else _f32(v_out_alpha)
+    meta = None if intersect_meta is None else _i32(intersect_meta)
+    n = op.shape[0]
+    r0, r1 = (0, img_h) if rows is None else rows
+    v_xy, v_conic, v_rgb = np.zeros((n, 2)), np.zeros((n, 3)), np.zeros((n, 3))
+    v_op, contrib, isect = np.zeros(n), np.zeros((n, 3)), np.zeros(ids.shape[0])
+    lib().orc_gs_raster_backward(
+        _p(ids), None if meta is None else _p(meta), _p(bins), _p(xy), _p(q), _p(col), _p(op),
+        _p(bg), ctypes.c_int32(img_h), ctypes.c_int32(img_w), ctypes.c_int32(block_x),
+        ctypes.c_int32(block_y), ctypes.c_int32(r0), ctypes.c_int32(r1), _p(fT), _p(fi), _p(vo),
+        None if va is None else _p(va), _p(v_xy), _p(v_conic), _p(v_rgb), _p(v_op), _p(contrib),
+        _p(isect))
+    return v_xy, v_conic, v_rgb, v_op, contrib, isect
+
+
+def gs_project_backward(scales2d, rotation, radii, conics, v_xy, v_conic, img_h: int,
+                        img_w: int, gaussian_meta=None):
+    """backward2d.py:8-151 (with tilelang_renderer.py:111-116's meta scaling)
+    -> float64 (v_cov2d, v_mean2d, v_scale, v_rot)."""
+    s, r = _f32(scales2d).reshape(-1, 2), _f32(rotation).reshape(-1)
+    rad, q = _i32(radii).reshape(-1), _f32(conics).reshape(-1, 3)
+    vxy = np.ascontiguousarray(np.asarray(v_xy, np.float64).reshape(-1, 2))
+    vq = np.ascontiguousarray(np.asarray(v_conic, np.float64).reshape(-1, 3))
+    meta = None if gaussian_meta is None else _i32(gaussian_meta).reshape(-1)
+    n = r.shape[0]
+    v_cov, v_mean, v_scale, v_rot = np.empty((n, 3)), np.empty((n, 2)), np.empty((n, 2)), np.empty(n)
+    lib().orc_gs_project_backward(_p(s), _p(r), _p(rad), _p(q), _p(vxy), _p(vq),
+                                  None if meta is None else _p(meta), ctypes.c_int32(n),
+                                  ctypes.c_int32(img_h), ctypes.c_int32(img_w), _p(v_cov),
+                                  _p(v_mean), _p(v_scale), _p(v_rot))
+    return v_cov, v_mean, v_scale, v_rot

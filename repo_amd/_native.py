@@ -77,7 +77,21 @@ _SIGNATURES = {
     "cs_closed_ring_segments_backward": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P,
                                                         _P]),
     "cs_adam_step": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _D, _D, _D, _P]),
+    "cs_gs_project_forward": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
+                                             _P, _P, _P]),
+    "cs_gs_bin_prepare": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
+                                         _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cs_gs_pack_records": (ctypes.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
+    "cs_gs_rasterize_forward": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _P, _P,
+                                               _P]),
+    "cs_gs_rasterize_backward": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _P,
+                                                _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cs_gs_project_backward": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
+                                              _P, _P, _P]),
+    "cs_gs_map_to_intersects": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I64, _I32, _I32, _I32,
+                                               _I32, _P, _P, _P]),
 }
+GS_RECORD_BYTES = 48     # per-Gaussian raster record
 
 _lib = None
 

@@ -24,7 +24,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libcubicsplat_hip.so")
-SOURCES = ["binning.hip", "raster.hip", "metric.hip", "optim.hip", "rings.hip"]
+SOURCES = ["binning.hip", "raster.hip", "metric.hip", "optim.hip", "rings.hip", "gaussian.hip"]
 ARCH = os.environ.get("CS_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

@@ -940,6 +940,37 @@ extern "C" int32_t cs_bin_tile_parts(int32_t nprim, int32_t img_h, int32_t img_w
     return tile_parts(nprim, (img_w + block_x - 1) / block_x, (img_h + block_y - 1) / block_y);
 }
 
+// Depth ranks, then the tile-list counts: order[r] = primitive with the r-th
+// smallest key (ties by primitive id) and rank_rects[r] its tile rectangle;
+// per-(part, tile) counts and their prefix over parts, per-segment totals,
+// then the segments' first slots; status[0] receives the intersection total.
+static int rank_and_count(uint32_t* keys, int32_t* order, const int4* prim_rects,
+                          int4* rank_rects, int nprim, int tbx, int tby, uint32_t* keys_alt,
+                          int32_t* vals_alt, uint32_t* radix_counts, uint32_t* scan_temp,
+                          uint32_t* tile_part_base, uint32_t* tile_count,
+                          uint32_t* tile_scratch, int32_t* status, hipStream_t stream) {
+    if (nprim <= kRankSortMax) {
+        hipLaunchKernelGGL(k_rank_order, dim3((nprim + 3) / 4), dim3(256), 0, stream, keys,
+                           nprim, prim_rects, order, rank_rects);
+    } else {
+        const int rc = cs_radix_sort_pairs_u32(keys, order, keys_alt, vals_alt, nprim, 32,
+                                               radix_counts, scan_temp, stream);
+        if (rc) return rc;
+        hipLaunchKernelGGL(k_gather_rects, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
+                           order, nprim, prim_rects, rank_rects);
+    }
+    const int K = tile_parts(nprim, tbx, tby);
+    const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
+    const int ranks_per_part = (nprim + K - 1) / K;
+    hipLaunchKernelGGL(k_tile_lists<false>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
+                       order, rank_rects, nprim, ranks_per_part, tbx, tby, nsegcols,
+                       tile_part_base, tile_count, tile_scratch, (int32_t*)nullptr,
+                       (int32_t*)nullptr, (float*)nullptr, (int64_t)0, (const int32_t*)nullptr,
+                       (int64_t)0);
+    return cs_scan_exclusive_u32(tile_scratch, tile_scratch, nsegcols * tby, scan_temp, status,
+                                 stream);
+}
+
 extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets,
                               const float* colors, const float* opacities, const float* depths,
                               const int32_t* fill_rules, const float* aa_widths,
@@ -975,32 +1006,59 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                        prim_tile_ranges,
                        num_tiles_hit, inv_sigma2s, keys, order,
                        reinterpret_cast<PrimRec*>(prim_recs));
-    // Depth ranks: order[r] = primitive with the r-th smallest depth key
-    // (ties by primitive id), and the ranks' tile rectangles.
-    int4* rank_rects = reinterpret_cast<int4*>(rank_tile_ranges);
-    const int4* prim_rects = reinterpret_cast<const int4*>(prim_tile_ranges);
-    if (nprim <= kRankSortMax) {
-        hipLaunchKernelGGL(k_rank_order, dim3((nprim + 3) / 4), dim3(256), 0, stream, keys,
-                           nprim, prim_rects, order, rank_rects);
-    } else {
-        const int rc = cs_radix_sort_pairs_u32(keys, order, keys_alt, vals_alt, nprim, 32,
-                                               radix_counts, scan_temp, stream);
-        if (rc) return rc;
-        hipLaunchKernelGGL(k_gather_rects, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
-                           order, nprim, prim_rects, rank_rects);
+    return rank_and_count(keys, order, reinterpret_cast<const int4*>(prim_tile_ranges),
+                          reinterpret_cast<int4*>(rank_tile_ranges), nprim, tbx, tby, keys_alt,
+                          vals_alt, radix_counts, scan_temp, tile_part_base, tile_count,
+                          tile_scratch, status, stream);
+}
+
+// 2D Gaussians: the tile rectangle map_gaussian_to_intersects_kernel emits
+// (intersects.py:34-121; empty when radius <= 0 or the area is not positive)
+// and the key of the sort, the raw depth bits (intersects.py:107-109), for
+// tilelang_renderer.py:224-269.  Thread 0 also clears the status words.
+__global__ __launch_bounds__(256) void k_gs_keys_rects(
+    const float* __restrict__ xys, const float* __restrict__ conics,
+    const int32_t* __restrict__ radii, const float* __restrict__ depths, int n, int bx, int by,
+    int tbx, int tby, int4* __restrict__ rects, uint32_t* __restrict__ keys,
+    int32_t* __restrict__ order, int32_t* __restrict__ status) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g == 0) {
+        status[1] = 0;
+        status[2] = 0;
+        status[3] = 0;
     }
-    // Per-(part, tile) counts and their prefix over parts, per-segment totals,
-    // then the segments' first slots; status[0] receives the intersection total.
-    const int K = tile_parts(nprim, tbx, tby);
-    const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
-    const int ranks_per_part = (nprim + K - 1) / K;
-    hipLaunchKernelGGL(k_tile_lists<false>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
-                       order, rank_rects, nprim, ranks_per_part, tbx, tby, nsegcols,
-                       tile_part_base, tile_count, tile_scratch, (int32_t*)nullptr,
-                       (int32_t*)nullptr, (float*)nullptr, (int64_t)0, (const int32_t*)nullptr,
-                       (int64_t)0);
-    return cs_scan_exclusive_u32(tile_scratch, tile_scratch, nsegcols * tby, scan_temp, status,
-                                 stream);
+    if (g >= n) return;
+    int4 r = make_int4(0, 0, 0, 0);
+    if (radii[g] > 0) {
+        r = gs_tile_rect(xys[2 * g], xys[2 * g + 1], conics[3 * g], conics[3 * g + 1],
+                         conics[3 * g + 2], (float)radii[g], bx, by, tbx, tby);
+        if ((r.z - r.x) * (r.w - r.y) <= 0) r = make_int4(0, 0, 0, 0);
+    }
+    rects[g] = r;
+    keys[g] = __builtin_bit_cast(uint32_t, depths[g]);
+    order[g] = g;
+}
+
+extern "C" int cs_gs_bin_prepare(const float* xys, const float* conics, const int32_t* radii,
+                                 const float* depths, int32_t n, int32_t img_h, int32_t img_w,
+                                 int32_t block_x, int32_t block_y, int32_t* tile_rects,
+                                 uint32_t* keys, int32_t* order, uint32_t* keys_alt,
+                                 int32_t* vals_alt, uint32_t* radix_counts, uint32_t* scan_temp,
+                                 int32_t* rank_tile_ranges, uint32_t* tile_part_base,
+                                 uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
+                                 hipStream_t stream) {
+    if (n <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0 ||
+        (reinterpret_cast<uintptr_t>(tile_rects) & 15) != 0 ||
+        (reinterpret_cast<uintptr_t>(rank_tile_ranges) & 15) != 0)
+        return CS_ERR_ARGS;
+    const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
+    hipLaunchKernelGGL(k_gs_keys_rects, dim3(blocks_for(n, 256)), dim3(256), 0, stream, xys,
+                       conics, radii, depths, n, block_x, block_y, tbx, tby,
+                       reinterpret_cast<int4*>(tile_rects), keys, order, status);
+    return rank_and_count(keys, order, reinterpret_cast<const int4*>(tile_rects),
+                          reinterpret_cast<int4*>(rank_tile_ranges), n, tbx, tby, keys_alt,
+                          vals_alt, radix_counts, scan_temp, tile_part_base, tile_count,
+                          tile_scratch, status, stream);
 }
 
 extern "C" int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges,

@@ -143,6 +143,34 @@ __device__ __forceinline__ float spec_expf(float x) {
     return (p * s1) * s2;
 }
 
+// sin and cos of x in fp32: k = rint(x 2/pi), r = x - k pi/2 by a three-part
+// Cody-Waite reduction with fused multiply-adds, then the single-precision
+// sin/cos polynomials of the Cephes library (S. L. Moshier, sinf.c/cosf.c)
+// on |r| <= pi/4 and the quadrant k mod 4.  Within 2 ulp-scale absolute error
+// of the true values for |x| up to ~1e5; deterministic everywhere (NaN and
+// inf give NaN).
+__device__ __forceinline__ void spec_sincosf(float x, float* sn, float* cs) {
+    if (!(x - x == 0.0f)) {
+        *sn = x - x;
+        *cs = x - x;
+        return;
+    }
+    const float kf = __builtin_rintf(x * 0.636619746685028076171875f);
+    float r = __builtin_fmaf(kf, -1.57079637050628662109375f, x);
+    r = __builtin_fmaf(kf, 4.37113882867379300296306610107421875e-08f, r);
+    r = __builtin_fmaf(kf, 1.77635683940025046467781066894531250e-15f, r);
+    const float z = r * r;
+    float ps = __builtin_fmaf(-1.9515295891e-4f, z, 8.3321608736e-3f);
+    ps = __builtin_fmaf(ps, z, -1.6666654611e-1f);
+    const float s = __builtin_fmaf(ps * z, r, r);
+    float pc = __builtin_fmaf(2.443315711809948e-5f, z, -1.388731625493765e-3f);
+    pc = __builtin_fmaf(pc, z, 4.166664568298827e-2f);
+    const float c = __builtin_fmaf(pc * z, z, __builtin_fmaf(-0.5f, z, 1.0f));
+    const int q = (int)kf & 3;
+    *sn = q == 0 ? s : q == 1 ? c : q == 2 ? -s : -c;
+    *cs = q == 0 ? c : q == 1 ? -s : q == 2 ? -c : s;
+}
+
 // Truncating float -> int32 with saturation, NaN -> 0.
 __device__ __forceinline__ int32_t f2i_sat(float x) {
     if (!(x == x)) return 0;
@@ -163,6 +191,47 @@ __device__ __forceinline__ int xcd_tile(int b, int n) {
 
 __device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) {
     return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// ------------------------------------------------------- 2D Gaussian splats
+
+// Tile rectangle [x0, x1) x [y0, y1) of a Gaussian from its centre, conic
+// (inverse covariance) and radius: the axis extents 3 sqrt(qyy / det Q),
+// 3 sqrt(qxx / det Q) of a positive definite conic, else the radius
+// (forward2d.py:97-151 and intersects.py:42-95 use the same expressions).
+__device__ __forceinline__ int4 gs_tile_rect(float cx, float cy, float qxx, float qxy, float qyy,
+                                             float radius, int block_x, int block_y, int tbx,
+                                             int tby) {
+    const float q_det = qxx * qyy - qxy * qxy;
+    float rx = radius, ry = radius;
+    if (qxx > 0.0f && qyy > 0.0f && q_det > (float)1e-12) {
+        rx = 3.0f * __builtin_sqrtf(qyy / q_det);
+        ry = 3.0f * __builtin_sqrtf(qxx / q_det);
+    }
+    const float bxf = (float)block_x, byf = (float)block_y;
+    const float tcx = cx / bxf, tcy = cy / byf;
+    const float trx = rx / bxf, try_ = ry / byf;
+    return make_int4(clampi(f2i_sat(tcx - trx), 0, tbx), clampi(f2i_sat(tcy - try_), 0, tby),
+                     clampi(f2i_sat(tcx + trx + 1.0f), 0, tbx),
+                     clampi(f2i_sat(tcy + try_ + 1.0f), 0, tby));
+}
+
+// Raster record of one Gaussian, 48 bytes, read with scalar loads:
+// centre, the conic's halves a = qxx / 2, c = qyy / 2 and b = qxy (so that
+// sigma = a dx^2 + b dx dy + c dy^2 = dx (a dx + b dy) + c dy^2), opacity,
+// the alpha cut (below), colour.
+struct alignas(16) GsRec {
+    float x, y, a, b, c, opac, cut, r, g, bl, pad0, pad1;
+};
+
+// Pixels with sigma > cut have opac * exp(-sigma) < 1/255 (alpha is then
+// below the reference's 1/255 threshold, rasterize.py:116-117 and :371-373):
+// cut = ln(255 opac) + 1/64 keeps a factor e^(-1/64) below the threshold,
+// far more than the error of the logarithm, the exponential and the
+// product.  Callers test !(sigma > cut), so a NaN sigma or opacity takes the
+// exact path.
+__device__ __forceinline__ float gs_alpha_cut(float opac) {
+    return __logf(255.0f * opac) + 0.015625f;
 }
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
