@@ -156,9 +156,8 @@ def reference_edge_pixel_evals(b, T, idx):
     import torch
     H, W = b.img_h, b.img_w
     tbx = (W + 15) // 16
-    eps = b.edges_per_segment
     pr = b.prim_recs.view(torch.int32)
-    prim_edges = (pr[:, 9] - pr[:, 8]) * eps
+    prim_edges = pr[:, 9] - pr[:, 8]   # the record's edge range [e0, e1)
     ent = prim_edges[b.primitive_ids_sorted.long()].to(torch.int64)
     csum = torch.zeros(ent.numel() + 1, dtype=torch.int64, device=ent.device)
     csum[1:] = torch.cumsum(ent, 0)

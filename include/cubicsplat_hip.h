@@ -88,6 +88,8 @@ int cs_isect_edge_ranges(const int32_t* prim_ids_sorted, const int32_t* seg_offs
 #define CS_SEG_RECORD_BYTES 32
 #define CS_PRIM_RECORD_BYTES 80
 #define CS_MAX_IMAGE_DIM 16384
+/* Per-edge record of the adaptive flattening: int32 segment, float t0, t1, pad. */
+#define CS_EDGE_AUX_BYTES 16
 
 /* Stage 1 of _CubicFillSplatFunction.forward / _CubicPolylineSplatFunction.forward
  * (ops/cubic_splatting.py:2815-2880, ops/cubic_polyline_splatting.py:1027-1098):
@@ -118,6 +120,68 @@ int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const f
                    uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
                    hipStream_t stream);
 
+/* ---------------- adaptive (de Casteljau) flattening ---------------- */
+
+/* Edges per segment the adaptive flattening can emit at most: 2^d with
+ * d = ceil(log2(samples - 1)) (the reference's max_depth,
+ * ops/cubic_splatting.py:1733); 0 when samples < 2 or d > 24. */
+int32_t cs_de_casteljau_max_edges_per_segment(int32_t samples);
+
+/* cs_bin_prepare with flatten_method="de_casteljau"
+ * (ops/cubic_splatting.py:1729-1832): each pixel-space cubic is halved at
+ * t = 0.5 until it is flat within 0.5 px
+ * (cubic_adaptive_flatness_flags_kernel, :1863-1915) or at depth d; its
+ * leaves, left to right, become its edges (chord P0 -> P3).  edges,
+ * edge_culls and edge_aux hold nseg * cs_de_casteljau_max_edges_per_segment
+ * records; leaf_counts [nseg] is scratch; seg_edge_offsets [nseg + 1]
+ * receives the segment CSR (seg_edge_offsets[nseg] = edge total); edge_aux
+ * receives each edge's (segment, t0, t1).  scan_temp holds
+ * cs_scan_temp_elems(max(nprim, T, nseg)).  The primitive records carry the
+ * edge ranges, so cs_rasterize_forward reads them unchanged (pass
+ * edges_per_segment 0); the backward is cs_rasterize_backward_de_casteljau. */
+int cs_bin_prepare_de_casteljau(
+    const float* cubics_norm, const int32_t* seg_offsets, const float* colors,
+    const float* opacities, const float* depths, const int32_t* fill_rules,
+    const float* aa_widths, const float* stroke_widths, int32_t nseg, int32_t nprim,
+    int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y, int32_t samples,
+    float aabb_pad, int32_t aniso, int32_t mode, float* cubics_px, int32_t* seg_tile_ranges,
+    void* seg_recs, void* edges, void* edge_culls, int32_t* prim_tile_ranges,
+    uint32_t* num_tiles_hit, float* inv_sigma2s, void* prim_recs, uint32_t* keys,
+    int32_t* order, uint32_t* keys_alt, int32_t* vals_alt, uint32_t* radix_counts,
+    uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_part_base,
+    uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status, int32_t* seg_edge_offsets,
+    void* edge_aux, uint32_t* leaf_counts, hipStream_t stream);
+
+/* _flatten_cubics_to_edges, de Casteljau branch (ops/cubic_splatting.py:1729-1832),
+ * in the reference's layout: edges_px [E,2,2], edge_t_starts / edge_t_ends [E]
+ * (capacity nseg * cs_de_casteljau_max_edges_per_segment(samples)),
+ * segment_edge_offsets [nseg + 1] and, when not NULL, primitive_edge_offsets
+ * [nprim + 1] = segment_edge_offsets[seg_offsets].  leaf_counts [nseg] and
+ * scan_temp (cs_scan_temp_elems(nseg)) are scratch. */
+int cs_flatten_cubics_de_casteljau(const float* cubics_px, const int32_t* seg_offsets,
+                                   int32_t nprim, int32_t nseg, int32_t samples,
+                                   uint32_t* leaf_counts, uint32_t* scan_temp,
+                                   int32_t* segment_edge_offsets, int32_t* primitive_edge_offsets,
+                                   float* edges_px, float* edge_t_starts, float* edge_t_ends,
+                                   hipStream_t stream);
+
+/* _flatten_cubics_to_edges, Bernstein branch (ops/cubic_splatting.py:1709-1719),
+ * in the reference's layout: edges_px [nseg * (samples - 1), 2, 2], the
+ * points of cs_bin_prepare's edge records. */
+int cs_flatten_cubics_bernstein(const float* cubics_px, int32_t nseg, int32_t samples,
+                                float* edges_px, hipStream_t stream);
+
+/* cubic_adaptive_flatness_flags_kernel (ops/cubic_splatting.py:1863-1915):
+ * out_flat[i] = 1 when cubic i [n,4,2] is flat within max(1e-4, tol_px) (or
+ * force_flat), else 0. */
+int cs_cubic_flatness_flags(const float* cubics, int32_t n, float tol_px, int32_t force_flat,
+                            uint8_t* out_flat, hipStream_t stream);
+
+/* cubic_split_half_kernel (ops/cubic_splatting.py:1968-2030): the halves of
+ * each cubic [n,4,2] at t = 0.5. */
+int cs_cubic_split_half(const float* cubics, int32_t n, float* left, float* right,
+                        hipStream_t stream);
+
 /* Stage 2 (ops/cubic_splatting.py:2888-2908, the sort of :2895-2896 and
  * get_tile_bin_edges of ops/tile_bins.py:10-60): each tile's primitives in
  * depth-rank order into primitive_ids_sorted and tile_bins [T,2] ((0, 0) for
@@ -139,7 +203,9 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
 
 /* rasterize_cubic_fill_forward_kernel (ops/cubic_splatting.py:918-1194) when
  * mode 0, rasterize_cubic_polyline_forward_kernel
- * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  16x16 tiles only. */
+ * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  16x16 tiles only.
+ * The primitive records hold each primitive's edge range, so
+ * edges_per_segment is not used (>= 0; 0 for adaptive records). */
 int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
                          const void* edges, const void* edge_culls, const void* prim_recs,
                          const float* background, int32_t img_h, int32_t img_w,
@@ -160,6 +226,20 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
                           float* v_colors, float* v_opacities, float* v_inv_sigma2s,
                           float* v_stroke_widths, float* curve_contrib_rgb,
                           float* curve_isect_contrib, hipStream_t stream);
+
+/* cs_rasterize_backward for records from cs_bin_prepare_de_casteljau
+ * (the reference's flatten_method="de_casteljau" backward: the raster kernel
+ * plus _accumulate_edge_grads_to_cubics_csr_kernel,
+ * ops/cubic_splatting.py:2399-2487): each edge's gradient is folded into its
+ * segment's control points with the Bernstein weights at its edge_aux
+ * interval [t0, t1]. */
+int cs_rasterize_backward_de_casteljau(
+    int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
+    const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
+    int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
+    const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
+    float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
+    float* curve_isect_contrib, hipStream_t stream);
 
 /* cs_rasterize_forward / cs_rasterize_backward with the same results, plus
  * evaluation counts added into eval_counts[5] (device uint64, caller-zeroed),
@@ -194,6 +274,14 @@ int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
 int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg, int32_t edges_per_segment,
                              int32_t img_h, int32_t img_w, float* v_cubics_px,
                              float* v_cubics_norm, hipStream_t stream);
+
+/* _accumulate_edge_grads_to_cubics_csr_kernel (ops/cubic_splatting.py:2399-2487)
+ * fused with the v_cubics_norm scaling: v_edges [E,2,2], edge_t_starts /
+ * edge_t_ends [E], segment_edge_offsets [nseg + 1]; v_cubics_norm may be NULL. */
+int cs_accumulate_edge_grads_csr(const float* v_edges, const float* edge_t_starts,
+                                 const float* edge_t_ends, const int32_t* segment_edge_offsets,
+                                 int32_t nseg, int32_t img_h, int32_t img_w, float* v_cubics_px,
+                                 float* v_cubics_norm, hipStream_t stream);
 
 /* Backward epilogue (ops/cubic_splatting.py:3096-3104): v_cubics_norm =
  * v_cubics_px * (W/2, H/2) and v_aa_widths = -2 v_inv_sigma2 / max(w^3, 1e-12)

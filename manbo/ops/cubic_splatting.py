@@ -1,7 +1,12 @@
 """manbo.ops.cubic_splatting (reference ops/cubic_splatting.py) on MI355X:
 the closed-fill splat path and its binning building blocks."""
 from repo_amd.blocks import (  # noqa: F401
+    DE_CASTELJAU_FLATNESS_TOL_PX as DEFAULT_DE_CASTELJAU_FLATNESS_TOL_PX,
+    accumulate_edge_grads_to_cubics as _accumulate_edge_grads_to_cubics,
     build_fill_isect_edge_ranges as _build_fill_isect_edge_ranges_uniform,
+    cubic_adaptive_flatness_flags_tilelang,
+    cubic_split_half_tilelang,
+    flatten_cubics_to_edges as _flatten_cubics_to_edges,
     map_cubic_to_intersects_tilelang,
     primitive_tile_ranges_from_segment_tile_ranges as _primitive_tile_ranges_from_segment_tile_ranges,
     project_cubics_2d_forward_tilelang,

@@ -20,6 +20,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _SRC = os.path.join(_HERE, "cs_oracle.c")
 _SRC_GS = os.path.join(_HERE, "gs_oracle.c")
+_SRC_DC = os.path.join(_HERE, "decas_oracle.c")
 _LIB_PATH = os.path.join(_HERE, "_build", "libcs_oracle.so")
 _CFLAGS = ["-O2", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
            "-fno-math-errno", "-mfma", "-msse4.1"]
@@ -32,7 +33,7 @@ def build() -> str:
     """Compile the C restatement with gcc into oracle/_build/."""
     os.makedirs(os.path.dirname(_LIB_PATH), exist_ok=True)
     tmp = _LIB_PATH + ".tmp"
-    subprocess.check_call(["gcc", *_CFLAGS, "-o", tmp, _SRC, _SRC_GS, "-lm"])
+    subprocess.check_call(["gcc", *_CFLAGS, "-o", tmp, _SRC, _SRC_GS, _SRC_DC, "-lm"])
     os.replace(tmp, _LIB_PATH)
     return _LIB_PATH
 
@@ -44,7 +45,7 @@ def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(_LIB_PATH) or any(
-                os.path.getmtime(src) > os.path.getmtime(_LIB_PATH) for src in (_SRC, _SRC_GS)):
+                os.path.getmtime(src) > os.path.getmtime(_LIB_PATH) for src in (_SRC, _SRC_GS, _SRC_DC)):
             build()
         L = ctypes.CDLL(_LIB_PATH)
         L.cs_expf.restype = ctypes.c_float
@@ -210,7 +211,7 @@ def prim_params(aa_widths, P: int):
 
 
 def bin_scene(cubics_norm, offs, depths, aa_widths, img_h, img_w, S, *, stroke_widths=None,
-              block_x=16, block_y=16, aabb_pad=1.0, aniso=False):
+              block_x=16, block_y=16, aabb_pad=1.0, aniso=False, flatten_method="bernstein"):
     """Forward up to the sorted per-tile lists (cubic_splatting.py:2815-2908)."""
     offs = _i32(offs)
     P = offs.shape[0] - 1
@@ -227,8 +228,13 @@ def bin_scene(cubics_norm, offs, depths, aa_widths, img_h, img_w, S, *, stroke_w
     cubics_px, seg_ranges, _ = project_cubics(cn, sw_seg, sup_seg, img_h, img_w, block_x,
                                               block_y, aabb_pad, aniso)
     S = max(2, int(S))
-    edges = flatten(cubics_px, S)
-    prim_edge_offsets = (offs.astype(np.int64) * (S - 1)).astype(np.int32)
+    seo = t_starts = t_ends = None
+    if flatten_method == "de_casteljau":
+        edges, seo, t_starts, t_ends = flatten_decas(cubics_px, S)
+        prim_edge_offsets = seo[np.clip(offs, 0, nseg)].astype(np.int32)
+    else:
+        edges = flatten(cubics_px, S)
+        prim_edge_offsets = (offs.astype(np.int64) * (S - 1)).astype(np.int32)
     prim_ranges, num_hit = prim_tile_ranges(seg_ranges, offs, tbx, tby)
     cum = np.cumsum(num_hit.astype(np.int64))
     keys, ids = map_intersects(prim_ranges, depths, cum, tbx)
@@ -237,7 +243,9 @@ def bin_scene(cubics_norm, offs, depths, aa_widths, img_h, img_w, S, *, stroke_w
     return dict(widths=w, inv_sigma2s=inv_s2, support=support, cubics_px=cubics_px,
                 seg_tile_ranges=seg_ranges, edges=edges, prim_edge_offsets=prim_edge_offsets,
                 prim_tile_ranges=prim_ranges, num_tiles_hit=num_hit, isect_ids_sorted=skeys,
-                primitive_ids_sorted=sids, tile_bins=bins, S=S, tbx=tbx, tby=tby)
+                primitive_ids_sorted=sids, tile_bins=bins, S=S, tbx=tbx, tby=tby,
+                flatten_method=flatten_method, segment_edge_offsets=seo, edge_t_starts=t_starts,
+                edge_t_ends=t_ends)
 
 
 def _scene(b, colors, opacities, fill_rules, stroke_widths, background, img_h, img_w,
@@ -307,9 +315,68 @@ def accumulate_edge_grads(v_edges, nseg: int, S: int) -> np.ndarray:
     return out
 
 
+# ---- adaptive (de Casteljau) flattening, cubic_splatting.py:1729-1832, 1863-2068, 2399-2487 ----
+
+DECAS_TOL_PX = 0.5   # DEFAULT_DE_CASTELJAU_FLATNESS_TOL_PX (cubic_splatting.py:18)
+
+
+def decas_max_depth(S: int) -> int:
+    """cubic_splatting.py:1733."""
+    return int(lib().orc_decas_max_depth(ctypes.c_int32(int(S))))
+
+
+def flatness_flags(cubics, tol=DECAS_TOL_PX, force=False) -> np.ndarray:
+    """cubic_adaptive_flatness_flags_tilelang (cubic_splatting.py:1918-1965) -> uint8 [n]."""
+    c = _f32(cubics).reshape(-1, 4, 2)
+    out = np.zeros(c.shape[0], np.uint8)
+    if c.shape[0]:
+        lib().orc_flatness_flags(_p(c), ctypes.c_int32(c.shape[0]), ctypes.c_float(tol),
+                                 ctypes.c_int32(int(bool(force))), _p(out))
+    return out
+
+
+def split_half(cubics):
+    """cubic_split_half_tilelang (cubic_splatting.py:2033-2068) -> (left, right) [n,4,2]."""
+    c = _f32(cubics).reshape(-1, 4, 2)
+    left, right = np.empty_like(c), np.empty_like(c)
+    if c.shape[0]:
+        lib().orc_split_half(_p(c), ctypes.c_int32(c.shape[0]), _p(left), _p(right))
+    return left, right
+
+
+def flatten_decas(cubics_px, S: int):
+    """_flatten_cubics_to_edges, de Casteljau branch (cubic_splatting.py:1729-1832):
+    -> (edges [E,2,2], segment_edge_offsets [nseg+1], t_starts [E], t_ends [E])."""
+    c = _f32(cubics_px).reshape(-1, 4, 2)
+    nseg = c.shape[0]
+    cap = max(1, nseg << decas_max_depth(S))
+    edges = np.zeros((cap, 2, 2), np.float32)
+    t0 = np.zeros(cap, np.float32)
+    t1 = np.zeros(cap, np.float32)
+    seo = np.zeros(nseg + 1, np.int32)
+    n = lib().orc_flatten_decas(_p(c), ctypes.c_int32(nseg), ctypes.c_int32(int(S)), _p(edges),
+                                _p(t0), _p(t1), _p(seo), ctypes.c_int32(cap))
+    if n < 0:
+        raise MemoryError("orc_flatten_decas failed")
+    return edges[:n].copy(), seo, t0[:n].copy(), t1[:n].copy()
+
+
+def accumulate_edge_grads_csr(v_edges, seo, t_starts, t_ends, nseg: int) -> np.ndarray:
+    """_accumulate_edge_grads_to_cubics_csr_kernel (cubic_splatting.py:2399-2487)
+    -> v_cubics_px [nseg,4,2] (float64 sums)."""
+    ve = np.ascontiguousarray(np.asarray(v_edges, np.float64)).reshape(-1, 2, 2)
+    out = np.zeros((nseg, 4, 2), np.float64)
+    if nseg > 0:
+        so, a, b = _i32(seo), _f32(t_starts), _f32(t_ends)
+        lib().orc_accumulate_edge_grads_csr(_p(ve), _p(so), _p(a), _p(b), ctypes.c_int32(nseg),
+                                            _p(out))
+    return out
+
+
 def render_forward(cubics_norm, offs, colors, opacities, depths, img_h, img_w, background, *,
                    fill_rules=None, aa_widths=None, aa_width=1.0, S=24, stroke_widths=None,
-                   block_x=16, block_y=16, aabb_pad=1.0, aniso=False, rows=None):
+                   block_x=16, block_y=16, aabb_pad=1.0, aniso=False, rows=None,
+                   flatten_method="bernstein"):
     """Whole forward of _CubicFillSplatFunction (cubic_splatting.py:2752-2962) or,
     with stroke_widths, _CubicPolylineSplatFunction (cubic_polyline_splatting.py:964-1173)."""
     offs = _i32(offs)
@@ -319,7 +386,7 @@ def render_forward(cubics_norm, offs, colors, opacities, depths, img_h, img_w, b
     mode = 0 if stroke_widths is None else 1
     b = bin_scene(cubics_norm, offs, depths, aa_widths, img_h, img_w, S,
                   stroke_widths=stroke_widths, block_x=block_x, block_y=block_y,
-                  aabb_pad=aabb_pad, aniso=aniso)
+                  aabb_pad=aabb_pad, aniso=aniso, flatten_method=flatten_method)
     out, T, idx = raster_forward(b, colors, opacities, background, img_h, img_w,
                                  fill_rules=fill_rules, stroke_widths=stroke_widths, mode=mode,
                                  block_x=block_x, block_y=block_y, rows=rows)
@@ -339,7 +406,11 @@ def render_backward(fw, v_out):
                         fill_rules=fw["fill_rules"], stroke_widths=fw["stroke_widths"],
                         mode=fw["mode"], block_x=fw["block_x"], block_y=fw["block_y"],
                         rows=fw.get("rows"))
-    v_px = accumulate_edge_grads(g["v_edges"], fw["nseg"], fw["S"])
+    if fw.get("flatten_method") == "de_casteljau":
+        v_px = accumulate_edge_grads_csr(g["v_edges"], fw["segment_edge_offsets"],
+                                         fw["edge_t_starts"], fw["edge_t_ends"], fw["nseg"])
+    else:
+        v_px = accumulate_edge_grads(g["v_edges"], fw["nseg"], fw["S"])
     half_w = 0.5 * float(fw["img_w"])
     half_h = 0.5 * float(fw["img_h"])
     v_norm = v_px.copy()

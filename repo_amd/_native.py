@@ -22,6 +22,7 @@ EDGE_CULL_INTS = 4       # 16-byte edge cull record
 MAX_IMAGE_DIM = 16384
 SEG_RECORD_INTS = 8      # 32-byte segment record
 PRIM_RECORD_FLOATS = 20  # 80-byte primitive record
+EDGE_AUX_INTS = 4        # 16-byte (segment, t0, t1) record of the adaptive flattening
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -58,6 +59,22 @@ _SIGNATURES = {
                                                      _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                                      _P, _P, _P]),
     "cs_accumulate_edge_grads": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P]),
+    "cs_de_casteljau_max_edges_per_segment": (_I32, [_I32]),
+    "cs_bin_prepare_de_casteljau": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32,
+                                                   _I32, _I32, _I32, _I32, _I32, _F, _I32, _I32,
+                                                   _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                   _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                   _P, _P]),
+    "cs_flatten_cubics_de_casteljau": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P,
+                                                      _P, _P, _P, _P]),
+    "cs_flatten_cubics_bernstein": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
+    "cs_cubic_flatness_flags": (ctypes.c_int, [_P, _I32, _F, _I32, _P, _P]),
+    "cs_cubic_split_half": (ctypes.c_int, [_P, _I32, _P, _P, _P]),
+    "cs_rasterize_backward_de_casteljau": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32,
+                                                          _I32, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                          _P, _P, _P, _P]),
+    "cs_accumulate_edge_grads_csr": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
+                                                    _P]),
     "cs_backward_finalize": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P]),
     "cs_mse_partials_elems": (_SZ, [_I64]),
     "cs_ssim_partials_elems": (_SZ, [_I32, _I32, _I32]),

@@ -2,9 +2,13 @@
 project_cubics_2d_forward_tilelang (ops/cubic_splatting.py:822-871),
 map_cubic_to_intersects_tilelang (:874-915),
 _primitive_tile_ranges_from_segment_tile_ranges (:2140-2178),
-_build_fill_isect_edge_ranges (:1849-1860) and get_tile_bin_edges_tilelang
-(ops/tile_bins.py:46-60).  The fused forward (repo_amd.splat) does not use
-them; they keep the reference's intermediate API callable."""
+_build_fill_isect_edge_ranges (:1849-1860), get_tile_bin_edges_tilelang
+(ops/tile_bins.py:46-60), and the flattening blocks
+_flatten_cubics_to_edges (:1654-1846, both methods),
+cubic_adaptive_flatness_flags_tilelang (:1918-1965),
+cubic_split_half_tilelang (:2033-2068) and _accumulate_edge_grads_to_cubics
+(:2490-2545).  The fused forward (repo_amd.splat) does not use them; they
+keep the reference's intermediate API callable."""
 from __future__ import annotations
 
 import torch
@@ -90,3 +94,111 @@ def get_tile_bin_edges_tilelang(num_intersects, isect_ids_sorted, *, num_tiles, 
     N.call("cs_get_tile_bin_edges", N.ptr(keys), int(num_intersects), rows, N.ptr(bins),
            N.stream(keys.device))
     return bins
+
+
+# ---- flattening blocks (ops/cubic_splatting.py:1654-2068, 2399-2526) ----
+
+DE_CASTELJAU_FLATNESS_TOL_PX = 0.5   # DEFAULT_DE_CASTELJAU_FLATNESS_TOL_PX (:18)
+
+
+def cubic_adaptive_flatness_flags_tilelang(cubics, *, tol_px, force_flat=False,
+                                           threads=DEFAULT_THREADS):
+    """cubic_splatting.py:1918-1965 -> uint8 [n] (1 = flat within tol_px)."""
+    c = _f32(cubics)
+    n = int(c.shape[0])
+    out = torch.empty((n,), dtype=torch.uint8, device=c.device)
+    if n:
+        N.call("cs_cubic_flatness_flags", N.ptr(c), n, float(tol_px), int(bool(force_flat)),
+               N.ptr(out), N.stream(c.device))
+    return out
+
+
+def cubic_split_half_tilelang(cubics, *, threads=DEFAULT_THREADS):
+    """cubic_splatting.py:2033-2068 -> (left, right) halves at t = 0.5, [n,4,2] each."""
+    c = _f32(cubics)
+    n = int(c.shape[0])
+    halves = torch.empty((2, n, 4, 2), dtype=torch.float32, device=c.device)
+    if n:
+        N.call("cs_cubic_split_half", N.ptr(c), n, N.ptr(halves[0]), N.ptr(halves[1]),
+               N.stream(c.device))
+    return halves[0], halves[1]
+
+
+def flatten_cubics_to_edges(cubics_px, primitive_seg_offsets, *, distance_samples,
+                            flatten_method="bernstein"):
+    """_flatten_cubics_to_edges (cubic_splatting.py:1654-1846) -> (edges_px [E,2,2],
+    primitive_edge_offsets [P+1], segment_edge_offsets [nseg+1], edge_t_starts,
+    edge_t_ends); the last two are None for the Bernstein flattening.  The
+    adaptive branch reads its edge count back to the host to size the outputs,
+    as the reference does."""
+    from .splat import normalize_cubic_flatten_method
+    c = _f32(cubics_px)
+    offs = _i32(primitive_seg_offsets).view(-1)
+    if c.dim() != 3 or tuple(c.shape[1:]) != (4, 2):
+        raise ValueError(f"cubics_px must be [N,4,2], got {tuple(c.shape)}")
+    if offs.dim() != 1 or int(offs.numel()) <= 0:
+        raise ValueError(
+            f"primitive_seg_offsets must be non-empty 1D tensor, got {tuple(offs.shape)}")
+    method = normalize_cubic_flatten_method(flatten_method)
+    dev = c.device
+    nseg = int(c.shape[0])
+    P = int(offs.numel()) - 1
+    S = max(2, int(distance_samples))
+    eps = S - 1
+    if method == "bernstein":
+        edges = torch.empty((nseg * eps, 2, 2), dtype=torch.float32, device=dev)
+        if nseg:
+            N.call("cs_flatten_cubics_bernstein", N.ptr(c), nseg, S, N.ptr(edges), N.stream(dev))
+        prim_eo = (offs.to(torch.int64) * eps).to(torch.int32)
+        seg_eo = torch.arange(0, (nseg + 1) * eps, eps, dtype=torch.int32, device=dev)
+        return edges, prim_eo, seg_eo, None, None
+    per_seg = int(N.lib().cs_de_casteljau_max_edges_per_segment(S))
+    if per_seg <= 0 or nseg * per_seg >= 2 ** 31:
+        raise ValueError(f"de_casteljau flattening of {nseg} segments with "
+                         f"distance_samples={S} exceeds the supported edge count")
+    cap = max(1, nseg * per_seg)
+    ints = torch.empty((nseg + (nseg + 1) + (P + 1),), dtype=torch.int32, device=dev)
+    leaf_counts, seg_eo, prim_eo = ints[:nseg], ints[nseg:2 * nseg + 1], ints[2 * nseg + 1:]
+    scan_temp = torch.empty((int(N.lib().cs_scan_temp_elems(max(nseg, 1))),), dtype=torch.int32,
+                            device=dev)
+    edges = torch.empty((cap, 2, 2), dtype=torch.float32, device=dev)
+    ts = torch.empty((2, cap), dtype=torch.float32, device=dev)
+    N.call("cs_flatten_cubics_de_casteljau", N.ptr(c), N.ptr(offs), P, nseg, S, N.ptr(leaf_counts),
+           N.ptr(scan_temp), N.ptr(seg_eo), N.ptr(prim_eo), N.ptr(edges), N.ptr(ts[0]),
+           N.ptr(ts[1]), N.stream(dev))
+    E = int(seg_eo[-1].item())
+    return edges[:E], prim_eo, seg_eo, ts[0, :E], ts[1, :E]
+
+
+def accumulate_edge_grads_to_cubics(v_edges, num_segments, *, distance_samples,
+                                    flatten_method="bernstein", segment_edge_offsets=None,
+                                    edge_t_starts=None, edge_t_ends=None,
+                                    threads=DEFAULT_THREADS):
+    """_accumulate_edge_grads_to_cubics (cubic_splatting.py:2490-2545) -> v_cubics_px
+    [nseg,4,2]."""
+    from .splat import normalize_cubic_flatten_method
+    method = normalize_cubic_flatten_method(flatten_method)
+    nseg = int(num_segments)
+    ve = _f32(v_edges)
+    dev = ve.device
+    v_px = torch.empty((max(nseg, 0), 4, 2), dtype=torch.float32, device=dev)
+    if nseg <= 0:
+        return v_px
+    if method == "bernstein":
+        eps = max(2, int(distance_samples)) - 1
+        if int(ve.shape[0]) != nseg * eps:
+            raise ValueError(f"v_edges size mismatch: got {int(ve.shape[0])}, "
+                             f"expected {nseg * eps}")
+        N.call("cs_accumulate_edge_grads", N.ptr(ve), nseg, eps, 2, 2, N.ptr(v_px), None,
+               N.stream(dev))
+        return v_px
+    if segment_edge_offsets is None or edge_t_starts is None or edge_t_ends is None:
+        raise ValueError("de_casteljau flatten backward requires CSR metadata "
+                         "(segment_edge_offsets, edge_t_starts, edge_t_ends)")
+    seo = _i32(segment_edge_offsets).view(-1)
+    if int(seo.numel()) != nseg + 1:
+        raise ValueError(f"segment_edge_offsets size mismatch: got {int(seo.numel())}, "
+                         f"expected {nseg + 1}")
+    N.call("cs_accumulate_edge_grads_csr", N.ptr(ve), N.ptr(_f32(edge_t_starts)),
+           N.ptr(_f32(edge_t_ends)), N.ptr(seo), nseg, 2, 2, N.ptr(v_px), None, N.stream(dev))
+    return v_px

@@ -197,13 +197,185 @@ __device__ __forceinline__ float linspace01(int S, int i) {
     return i < (S >> 1) ? 0.0f + step * (float)i : 1.0f - step * (float)(S - i - 1);
 }
 
+// One edge's geometry and cull records (shared by both flattenings).
+__device__ __forceinline__ void write_edge(float ax, float ay, float bx, float by, float D,
+                                           EdgeRec* __restrict__ er, EdgeCull* __restrict__ ec) {
+    const float vx = bx - ax, vy = by - ay;
+    const float vv = vx * vx + vy * vy;
+    const float ivv = 1.0f / fmaxf(vv, kEps);
+    const float ex0 = fminf(ax, bx), ex1 = fmaxf(ax, bx);
+    const float ey0 = fminf(ay, by), ey1 = fmaxf(ay, by);
+    int4* o = reinterpret_cast<int4*>(er);
+    o[0] = make_int4(__builtin_bit_cast(int, ax), __builtin_bit_cast(int, ay),
+                     __builtin_bit_cast(int, bx), __builtin_bit_cast(int, by));
+    o[1] = make_int4(__builtin_bit_cast(int, vx), __builtin_bit_cast(int, vy),
+                     __builtin_bit_cast(int, vx * ivv), __builtin_bit_cast(int, vy * ivv));
+    const IRange nx = pixel_range(ex0, ex1, D), ny = pixel_range(ey0, ey1, D);
+    const IRange cy = pixel_range(ey0, ey1, 0.0f);
+    *reinterpret_cast<int4*>(ec) =
+        make_int4(packed_range(ny, kWaveRowsExt), packed_range(cy, kWaveRowsExt),
+                  packed_range(nx, kWaveColsExt),
+                  (fabsf(ax) <= kFarCrossMaxX && fabsf(bx) <= kFarCrossMaxX) ? kCullFarCrossExact
+                                                                             : 0);
+}
+
+// Bounding box of a segment's polyline vertices -> its segment record.
+struct VBox {
+    float x0, y0, x1, y1;
+};
+
+__device__ __forceinline__ VBox vbox_empty() {
+    const float inf = __builtin_huge_valf();
+    return VBox{inf, inf, -inf, -inf};
+}
+
+__device__ __forceinline__ void vbox_add(VBox& b, float x, float y) {
+    b.x0 = fminf(b.x0, x);
+    b.x1 = fmaxf(b.x1, x);
+    b.y0 = fminf(b.y0, y);
+    b.y1 = fmaxf(b.y1, y);
+}
+
+__device__ __forceinline__ SegRec seg_record(const VBox& b, float D) {
+    const IRange nx = pixel_range(b.x0, b.x1, D), ny = pixel_range(b.y0, b.y1, D);
+    const IRange cy = pixel_range(b.y0, b.y1, 0.0f);
+    SegRec sr;
+    sr.ny_lo = ny.lo;
+    sr.ny_span = span_y(ny);
+    sr.cy_lo = cy.lo;
+    sr.cy_span = span_y(cy);
+    sr.nx_lo = nx.lo;
+    sr.nx_span = span_x(nx);
+    sr.x_last = px_index(ceilf(b.x1 - 0.5f)) + 1;
+    sr.pad = 0;
+    return sr;
+}
+
+// ------------------------------------------- adaptive (de Casteljau) flattening
+
+// Control points of one cubic in pixel space.
+struct Cub {
+    float x[4], y[4];
+};
+
+__device__ __forceinline__ Cub load_cub(const float* __restrict__ c) {
+    Cub r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        r.x[k] = c[2 * k];
+        r.y[k] = c[2 * k + 1];
+    }
+    return r;
+}
+
+// cubic_adaptive_flatness_flags_kernel (cubic_splatting.py:1863-1915): the
+// larger distance of the inner control points from the chord line (or, for a
+// chord shorter than sqrt(1e-6), from P0) is at most tol.
+__device__ __forceinline__ bool cub_flat(const Cub& c, float tol) {
+    const float lx = c.x[3] - c.x[0], ly = c.y[3] - c.y[0];
+    const float chord2 = lx * lx + ly * ly;
+    const float chord = __builtin_sqrtf(fmaxf(chord2, kEps));
+    const float v1x = c.x[1] - c.x[0], v1y = c.y[1] - c.y[0];
+    const float v2x = c.x[2] - c.x[0], v2y = c.y[2] - c.y[0];
+    const float cross1 = fabsf(lx * v1y - ly * v1x);
+    const float cross2 = fabsf(lx * v2y - ly * v2x);
+    const float dline = fmaxf(cross1 / chord, cross2 / chord);
+    float dmax = dline;
+    if (chord2 <= kEps) {
+        const float n1 = __builtin_sqrtf(fmaxf(v1x * v1x + v1y * v1y, 0.0f));
+        const float n2 = __builtin_sqrtf(fmaxf(v2x * v2x + v2y * v2y, 0.0f));
+        const float n3 = __builtin_sqrtf(fmaxf(chord2, 0.0f));
+        dmax = fmaxf(n1, fmaxf(n2, n3));
+    }
+    return dmax <= tol;
+}
+
+// cubic_split_half_kernel (cubic_splatting.py:1968-2030): halves at t = 0.5.
+__device__ __forceinline__ void cub_split(const Cub& c, Cub& l, Cub& r) {
+#define CS_SPLIT_AXIS(A)                                   \
+    {                                                      \
+        const float p01 = 0.5f * (c.A[0] + c.A[1]);        \
+        const float p12 = 0.5f * (c.A[1] + c.A[2]);        \
+        const float p23 = 0.5f * (c.A[2] + c.A[3]);        \
+        const float p012 = 0.5f * (p01 + p12);             \
+        const float p123 = 0.5f * (p12 + p23);             \
+        const float p0123 = 0.5f * (p012 + p123);          \
+        l.A[0] = c.A[0];                                   \
+        l.A[1] = p01;                                      \
+        l.A[2] = p012;                                     \
+        l.A[3] = p0123;                                    \
+        r.A[0] = p0123;                                    \
+        r.A[1] = p123;                                     \
+        r.A[2] = p23;                                      \
+        r.A[3] = c.A[3];                                   \
+    }
+    CS_SPLIT_AXIS(x)
+    CS_SPLIT_AXIS(y)
+#undef CS_SPLIT_AXIS
+}
+
+// Smallest d with 2^d >= n (n >= 1): the reference's
+// ceil(log2(max(1, edges_per_segment))) (cubic_splatting.py:1733).
+__host__ __device__ __forceinline__ int ceil_log2(int n) {
+    int d = 0;
+    while ((int64_t)1 << d < (int64_t)n) ++d;
+    return d;
+}
+
+// The leaves of the reference's level-by-level subdivision
+// (cubic_splatting.py:1747-1781) of one cubic, visited left to right (the
+// order of its (segment, t0) sort, :1801-1809): node (d, k) covers
+// [k / 2^d, (k + 1) / 2^d] and is a leaf when d == maxd or it is flat.  Each
+// node's control points are recomputed from the root along the bits of k, so
+// they are the same fp32 values the reference's repeated halving produces,
+// with no stack.  leaf(c, d, k) is called once per leaf.
+template <class F>
+__device__ __forceinline__ void decas_leaves(const Cub& root, int maxd, float tol, F&& leaf) {
+    int d = 0;
+    uint32_t k = 0;
+    for (;;) {
+        Cub c = root;
+        for (int i = d - 1; i >= 0; --i) {
+            Cub l, r;
+            cub_split(c, l, r);
+            c = ((k >> i) & 1u) ? r : l;
+        }
+        if (d >= maxd || cub_flat(c, tol)) {
+            leaf(c, d, k);
+            while (d > 0 && (k & 1u)) {
+                k >>= 1;
+                --d;
+            }
+            if (d == 0) break;
+            k += 1;
+        } else {
+            ++d;
+            k <<= 1;
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t decas_count(const Cub& c, int maxd, float tol) {
+    uint32_t n = 0;
+    decas_leaves(c, maxd, tol, [&](const Cub&, int, uint32_t) { ++n; });
+    return n;
+}
+
+// Leaf interval [k / 2^d, (k + 1) / 2^d] (exact: the reference's repeated
+// midpoints 0.5 (t0 + t1) of dyadic values).
+__device__ __forceinline__ float2 leaf_interval(int d, uint32_t k) {
+    const float sc = __builtin_bit_cast(float, (uint32_t)(127 - d) << 23);
+    return make_float2((float)k * sc, (float)(k + 1u) * sc);
+}
+
 __global__ __launch_bounds__(256) void k_project_flatten(
     const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
     const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths,
     const float* __restrict__ opacities, int mode, int nseg, int img_h, int img_w, int block_x,
     int block_y, float aabb_pad, int aniso, int S, float* __restrict__ cubics_px,
     int32_t* __restrict__ seg_tile_ranges, SegRec* __restrict__ seg_recs,
-    EdgeRec* __restrict__ edges, EdgeCull* __restrict__ culls) {
+    EdgeRec* __restrict__ edges, EdgeCull* __restrict__ culls, int adaptive_maxd,
+    float adaptive_tol, uint32_t* __restrict__ leaf_counts) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
     const int p = owner_of(seg_offsets, P, s);
@@ -220,9 +392,22 @@ __global__ __launch_bounds__(256) void k_project_flatten(
     cp[1] = make_float4(r.px[2], r.py[2], r.px[3], r.py[3]);
     reinterpret_cast<int4*>(seg_tile_ranges)[s] = make_int4(r.tx0, r.ty0, r.tx1, r.ty1);
 
+    if (leaf_counts) {
+        // Adaptive flattening: count the leaves here; k_decas_emit writes
+        // them once their offsets are known.
+        Cub c;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            c.x[k] = r.px[k];
+            c.y[k] = r.py[k];
+        }
+        leaf_counts[s] = decas_count(c, adaptive_maxd, adaptive_tol);
+        return;
+    }
+
     // Flatten: pts_i = ((P0 b0 + P1 b1) + P2 b2) + P3 b3 at t_i = linspace(0,1,S)[i].
     float prevx = 0.0f, prevy = 0.0f;
-    float bx0 = __builtin_huge_valf(), by0 = bx0, bx1 = -bx0, by1 = -bx0;
+    VBox box = vbox_empty();
     EdgeRec* er = edges + (size_t)s * (S - 1);
     EdgeCull* ec = culls + (size_t)s * (S - 1);
     for (int i = 0; i < S; ++i) {
@@ -240,42 +425,140 @@ __global__ __launch_bounds__(256) void k_project_flatten(
         y = y + r.py[1] * b1;
         y = y + r.py[2] * b2;
         y = y + r.py[3] * b3;
-        bx0 = fminf(bx0, x); bx1 = fmaxf(bx1, x);
-        by0 = fminf(by0, y); by1 = fmaxf(by1, y);
-        if (i > 0) {
-            const float vx = x - prevx, vy = y - prevy;
-            const float vv = vx * vx + vy * vy;
-            const float ivv = 1.0f / fmaxf(vv, kEps);
-            const float ex0 = fminf(prevx, x), ex1 = fmaxf(prevx, x);
-            const float ey0 = fminf(prevy, y), ey1 = fmaxf(prevy, y);
-            int4* o = reinterpret_cast<int4*>(er + (i - 1));
-            o[0] = make_int4(__builtin_bit_cast(int, prevx), __builtin_bit_cast(int, prevy),
-                             __builtin_bit_cast(int, x), __builtin_bit_cast(int, y));
-            o[1] = make_int4(__builtin_bit_cast(int, vx), __builtin_bit_cast(int, vy),
-                             __builtin_bit_cast(int, vx * ivv), __builtin_bit_cast(int, vy * ivv));
-            const IRange nx = pixel_range(ex0, ex1, D), ny = pixel_range(ey0, ey1, D);
-            const IRange cy = pixel_range(ey0, ey1, 0.0f);
-            reinterpret_cast<int4*>(ec)[i - 1] =
-                make_int4(packed_range(ny, kWaveRowsExt), packed_range(cy, kWaveRowsExt),
-                          packed_range(nx, kWaveColsExt),
-                          (fabsf(prevx) <= kFarCrossMaxX && fabsf(x) <= kFarCrossMaxX)
-                              ? kCullFarCrossExact : 0);
-        }
+        vbox_add(box, x, y);
+        if (i > 0) write_edge(prevx, prevy, x, y, D, er + (i - 1), ec + (i - 1));
         prevx = x;
         prevy = y;
     }
-    const IRange nx = pixel_range(bx0, bx1, D), ny = pixel_range(by0, by1, D);
-    const IRange cy = pixel_range(by0, by1, 0.0f);
-    SegRec sr;
-    sr.ny_lo = ny.lo;
-    sr.ny_span = span_y(ny);
-    sr.cy_lo = cy.lo;
-    sr.cy_span = span_y(cy);
-    sr.nx_lo = nx.lo;
-    sr.nx_span = span_x(nx);
-    sr.x_last = px_index(ceilf(bx1 - 0.5f)) + 1;
-    sr.pad = 0;
-    seg_recs[s] = sr;
+    seg_recs[s] = seg_record(box, D);
+}
+
+// Adaptive flattening, second pass (cubic_splatting.py:1729-1832): the leaves
+// of segment s, left to right, as edges seg_edge_offsets[s] + i (chord P0 ->
+// P3 of leaf i) with their records, the (segment, t0, t1) aux records and the
+// segment record.
+__global__ __launch_bounds__(256) void k_decas_emit(
+    const float* __restrict__ cubics_px, const int32_t* __restrict__ seg_offsets, int P,
+    const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths,
+    const float* __restrict__ opacities, int mode, int nseg, int maxd, float tol,
+    const int32_t* __restrict__ seg_edge_offsets, EdgeRec* __restrict__ edges,
+    EdgeCull* __restrict__ culls, EdgeAux* __restrict__ aux, SegRec* __restrict__ seg_recs) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    const int p = owner_of(seg_offsets, P, s);
+    const float D = prim_params(mode, aa_widths[p], opacities[p], stroke_widths, p).cull_d;
+    const Cub root = load_cub(cubics_px + (size_t)s * 8);
+    const int base = seg_edge_offsets[s];
+    int i = 0;
+    VBox box = vbox_empty();
+    vbox_add(box, root.x[0], root.y[0]);
+    decas_leaves(root, maxd, tol, [&](const Cub& c, int d, uint32_t k) {
+        const int e = base + i;
+        write_edge(c.x[0], c.y[0], c.x[3], c.y[3], D, edges + e, culls + e);
+        const float2 t = leaf_interval(d, k);
+        *reinterpret_cast<int4*>(aux + e) =
+            make_int4(s, __builtin_bit_cast(int, t.x), __builtin_bit_cast(int, t.y), 0);
+        vbox_add(box, c.x[3], c.y[3]);
+        ++i;
+    });
+    seg_recs[s] = seg_record(box, D);
+}
+
+// Reference-layout adaptive flattening (_flatten_cubics_to_edges,
+// cubic_splatting.py:1729-1832): leaf counts, then edges_px [E,2,2] and
+// edge_t_starts / edge_t_ends [E].
+__global__ __launch_bounds__(256) void k_decas_count_ref(const float* __restrict__ cubics_px,
+                                                         int nseg, int maxd, float tol,
+                                                         uint32_t* __restrict__ leaf_counts) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    leaf_counts[s] = decas_count(load_cub(cubics_px + (size_t)s * 8), maxd, tol);
+}
+
+__global__ __launch_bounds__(256) void k_decas_emit_ref(
+    const float* __restrict__ cubics_px, int nseg, int maxd, float tol,
+    const int32_t* __restrict__ seg_edge_offsets, float* __restrict__ edges_px,
+    float* __restrict__ t_starts, float* __restrict__ t_ends) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    const int base = seg_edge_offsets[s];
+    int i = 0;
+    decas_leaves(load_cub(cubics_px + (size_t)s * 8), maxd, tol,
+                 [&](const Cub& c, int d, uint32_t k) {
+                     const int e = base + i;
+                     reinterpret_cast<float4*>(edges_px)[e] =
+                         make_float4(c.x[0], c.y[0], c.x[3], c.y[3]);
+                     const float2 t = leaf_interval(d, k);
+                     t_starts[e] = t.x;
+                     t_ends[e] = t.y;
+                     ++i;
+                 });
+}
+
+// Reference-layout uniform flattening (cubic_splatting.py:1709-1719): the
+// same points as k_project_flatten, edges_px [nseg * (S - 1), 2, 2].
+__global__ __launch_bounds__(256) void k_bernstein_ref(const float* __restrict__ cubics_px,
+                                                       int nseg, int S,
+                                                       float* __restrict__ edges_px) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    const Cub c = load_cub(cubics_px + (size_t)s * 8);
+    float prevx = 0.0f, prevy = 0.0f;
+    for (int i = 0; i < S; ++i) {
+        const float t = linspace01(S, i);
+        const float omt = 1.0f - t;
+        const float b0 = omt * omt * omt;
+        const float b1 = 3.0f * omt * omt * t;
+        const float b2 = 3.0f * omt * t * t;
+        const float b3 = t * t * t;
+        float x = c.x[0] * b0;
+        x = x + c.x[1] * b1;
+        x = x + c.x[2] * b2;
+        x = x + c.x[3] * b3;
+        float y = c.y[0] * b0;
+        y = y + c.y[1] * b1;
+        y = y + c.y[2] * b2;
+        y = y + c.y[3] * b3;
+        if (i > 0)
+            reinterpret_cast<float4*>(edges_px)[(size_t)s * (S - 1) + i - 1] =
+                make_float4(prevx, prevy, x, y);
+        prevx = x;
+        prevy = y;
+    }
+}
+
+// primitive_edge_offsets = segment_edge_offsets[primitive_seg_offsets]
+// (cubic_splatting.py:1822-1826).
+__global__ __launch_bounds__(256) void k_prim_edge_offsets(const int32_t* __restrict__ seo,
+                                                           const int32_t* __restrict__ offs,
+                                                           int n, int nseg,
+                                                           int32_t* __restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = seo[clampi(offs[i], 0, nseg)];
+}
+
+__global__ __launch_bounds__(256) void k_flatness_flags(const float* __restrict__ cubics, int n,
+                                                        float tol, int force,
+                                                        uint8_t* __restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    out[i] = (force || cub_flat(load_cub(cubics + (size_t)i * 8), tol)) ? 1 : 0;
+}
+
+__global__ __launch_bounds__(256) void k_split_half(const float* __restrict__ cubics, int n,
+                                                    float* __restrict__ left,
+                                                    float* __restrict__ right) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    Cub l, r;
+    cub_split(load_cub(cubics + (size_t)i * 8), l, r);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        left[(size_t)i * 8 + 2 * k] = l.x[k];
+        left[(size_t)i * 8 + 2 * k + 1] = l.y[k];
+        right[(size_t)i * 8 + 2 * k] = r.x[k];
+        right[(size_t)i * 8 + 2 * k + 1] = r.y[k];
+    }
 }
 
 __global__ __launch_bounds__(256) void k_prim_prep(
@@ -284,7 +567,8 @@ __global__ __launch_bounds__(256) void k_prim_prep(
     const float* __restrict__ colors, const float* __restrict__ opacities,
     const float* __restrict__ depths, const int32_t* __restrict__ fill_rules,
     const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
-    int tbx, int tby, int mode, int32_t* __restrict__ status,
+    int eps, const int32_t* __restrict__ seg_edge_offsets, int tbx, int tby, int mode,
+    int32_t* __restrict__ status,
     int32_t* __restrict__ prim_tile_ranges, uint32_t* __restrict__ counts,
     float* __restrict__ inv_sigma2s, uint32_t* __restrict__ keys, int32_t* __restrict__ vals,
     PrimRec* __restrict__ recs) {
@@ -332,8 +616,9 @@ __global__ __launch_bounds__(256) void k_prim_prep(
     rec.inv_sigma = q.inv_sigma;
     rec.half_sw = q.half_sw;
     rec.cull_d = q.cull_d;
-    rec.s0 = s0;
-    rec.s1 = s1;
+    // Edge range: uniform flattening s * eps, adaptive the segment CSR.
+    rec.e0 = seg_edge_offsets ? seg_edge_offsets[s0] : s0 * eps;
+    rec.e1 = seg_edge_offsets ? seg_edge_offsets[s1] : s1 * eps;
     rec.rule = fill_rules ? fill_rules[p] : 1;
     int closed = 1;
     IRange nx{kRangeLimit, -kRangeLimit}, ny = nx, cy = nx;
@@ -971,6 +1256,76 @@ static int rank_and_count(uint32_t* keys, int32_t* order, const int4* prim_rects
                                  stream);
 }
 
+// Flatness tolerance of the adaptive flattening, px
+// (DEFAULT_DE_CASTELJAU_FLATNESS_TOL_PX, cubic_splatting.py:18, clamped at
+// 1e-4 as :1731 does).
+constexpr float kDecasTolPx = 0.5f;
+// Deepest subdivision the adaptive entry points accept (2^24 edges per segment).
+constexpr int kDecasMaxDepth = 24;
+
+static int bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const float* colors,
+                       const float* opacities, const float* depths, const int32_t* fill_rules,
+                       const float* aa_widths, const float* stroke_widths, int32_t nseg,
+                       int32_t nprim, int32_t img_h, int32_t img_w, int32_t block_x,
+                       int32_t block_y, int32_t samples, float aabb_pad, int32_t aniso,
+                       int32_t mode, float* cubics_px, int32_t* seg_tile_ranges, void* seg_recs,
+                       void* edges, void* edge_culls, int32_t* prim_tile_ranges,
+                       uint32_t* num_tiles_hit, float* inv_sigma2s, void* prim_recs,
+                       uint32_t* keys, int32_t* order, uint32_t* keys_alt, int32_t* vals_alt,
+                       uint32_t* radix_counts, uint32_t* scan_temp, int32_t* rank_tile_ranges,
+                       uint32_t* tile_part_base, uint32_t* tile_count, uint32_t* tile_scratch,
+                       int32_t* status, int32_t* seg_edge_offsets, void* edge_aux,
+                       uint32_t* leaf_counts, hipStream_t stream) {
+    if (nseg < 0 || nprim <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0 ||
+        samples < 2 || (mode != 0 && mode != 1) || img_h > kMaxImageDim ||
+        img_w > kMaxImageDim)
+        return CS_ERR_ARGS;
+    const bool adaptive = seg_edge_offsets != nullptr;
+    const int eps = samples - 1;
+    const int maxd = ceil_log2(eps);
+    if (adaptive) {
+        if (!edge_aux || !leaf_counts || maxd > kDecasMaxDepth ||
+            (int64_t)nseg << maxd > (int64_t)INT32_MAX)
+            return CS_ERR_ARGS;
+    } else if ((int64_t)nseg * eps > (int64_t)INT32_MAX) {
+        return CS_ERR_ARGS;
+    }
+    const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
+    hipLaunchKernelGGL(k_status_init, dim3(1), dim3(1), 0, stream, seg_offsets, nprim, status);
+    if (nseg > 0)
+        hipLaunchKernelGGL(k_project_flatten, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
+                           cubics_norm, seg_offsets, nprim, aa_widths, stroke_widths, opacities,
+                           mode, nseg, img_h, img_w, block_x, block_y, aabb_pad, aniso, samples,
+                           cubics_px, seg_tile_ranges, reinterpret_cast<SegRec*>(seg_recs),
+                           reinterpret_cast<EdgeRec*>(edges),
+                           reinterpret_cast<EdgeCull*>(edge_culls), maxd, kDecasTolPx,
+                           adaptive ? leaf_counts : nullptr);
+    if (adaptive) {
+        int rc = cs_scan_exclusive_u32(leaf_counts, reinterpret_cast<uint32_t*>(seg_edge_offsets),
+                                       nseg, scan_temp, seg_edge_offsets + nseg, stream);
+        if (rc) return rc;
+        if (nseg > 0)
+            hipLaunchKernelGGL(k_decas_emit, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
+                               cubics_px, seg_offsets, nprim, aa_widths, stroke_widths,
+                               opacities, mode, nseg, maxd, kDecasTolPx, seg_edge_offsets,
+                               reinterpret_cast<EdgeRec*>(edges),
+                               reinterpret_cast<EdgeCull*>(edge_culls),
+                               reinterpret_cast<EdgeAux*>(edge_aux),
+                               reinterpret_cast<SegRec*>(seg_recs));
+    }
+    hipLaunchKernelGGL(k_prim_prep, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
+                       cubics_norm, seg_offsets, nprim, seg_tile_ranges,
+                       reinterpret_cast<const SegRec*>(seg_recs), colors, opacities, depths,
+                       fill_rules, aa_widths, stroke_widths, nseg, eps,
+                       adaptive ? seg_edge_offsets : nullptr, tbx, tby, mode, status,
+                       prim_tile_ranges, num_tiles_hit, inv_sigma2s, keys, order,
+                       reinterpret_cast<PrimRec*>(prim_recs));
+    return rank_and_count(keys, order, reinterpret_cast<const int4*>(prim_tile_ranges),
+                          reinterpret_cast<int4*>(rank_tile_ranges), nprim, tbx, tby, keys_alt,
+                          vals_alt, radix_counts, scan_temp, tile_part_base, tile_count,
+                          tile_scratch, status, stream);
+}
+
 extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets,
                               const float* colors, const float* opacities, const float* depths,
                               const int32_t* fill_rules, const float* aa_widths,
@@ -986,30 +1341,98 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                               int32_t* rank_tile_ranges, uint32_t* tile_part_base,
                               uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
                               hipStream_t stream) {
-    if (nseg < 0 || nprim <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0 ||
-        samples < 2 || (mode != 0 && mode != 1) || img_h > kMaxImageDim ||
-        img_w > kMaxImageDim)
-        return CS_ERR_ARGS;
-    const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
-    hipLaunchKernelGGL(k_status_init, dim3(1), dim3(1), 0, stream, seg_offsets, nprim, status);
+    return bin_prepare(cubics_norm, seg_offsets, colors, opacities, depths, fill_rules,
+                       aa_widths, stroke_widths, nseg, nprim, img_h, img_w, block_x, block_y,
+                       samples, aabb_pad, aniso, mode, cubics_px, seg_tile_ranges, seg_recs,
+                       edges, edge_culls, prim_tile_ranges, num_tiles_hit, inv_sigma2s,
+                       prim_recs, keys, order, keys_alt, vals_alt, radix_counts, scan_temp,
+                       rank_tile_ranges, tile_part_base, tile_count, tile_scratch, status,
+                       nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int32_t cs_de_casteljau_max_edges_per_segment(int32_t samples) {
+    if (samples < 2) return 0;
+    const int d = ceil_log2(samples - 1);
+    return d > kDecasMaxDepth ? 0 : (1 << d);
+}
+
+extern "C" int cs_bin_prepare_de_casteljau(
+    const float* cubics_norm, const int32_t* seg_offsets, const float* colors,
+    const float* opacities, const float* depths, const int32_t* fill_rules,
+    const float* aa_widths, const float* stroke_widths, int32_t nseg, int32_t nprim,
+    int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y, int32_t samples,
+    float aabb_pad, int32_t aniso, int32_t mode, float* cubics_px, int32_t* seg_tile_ranges,
+    void* seg_recs, void* edges, void* edge_culls, int32_t* prim_tile_ranges,
+    uint32_t* num_tiles_hit, float* inv_sigma2s, void* prim_recs, uint32_t* keys,
+    int32_t* order, uint32_t* keys_alt, int32_t* vals_alt, uint32_t* radix_counts,
+    uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_part_base,
+    uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status, int32_t* seg_edge_offsets,
+    void* edge_aux, uint32_t* leaf_counts, hipStream_t stream) {
+    if (!seg_edge_offsets) return CS_ERR_ARGS;
+    return bin_prepare(cubics_norm, seg_offsets, colors, opacities, depths, fill_rules,
+                       aa_widths, stroke_widths, nseg, nprim, img_h, img_w, block_x, block_y,
+                       samples, aabb_pad, aniso, mode, cubics_px, seg_tile_ranges, seg_recs,
+                       edges, edge_culls, prim_tile_ranges, num_tiles_hit, inv_sigma2s,
+                       prim_recs, keys, order, keys_alt, vals_alt, radix_counts, scan_temp,
+                       rank_tile_ranges, tile_part_base, tile_count, tile_scratch, status,
+                       seg_edge_offsets, edge_aux, leaf_counts, stream);
+}
+
+extern "C" int cs_flatten_cubics_de_casteljau(const float* cubics_px, const int32_t* seg_offsets,
+                                              int32_t nprim, int32_t nseg, int32_t samples,
+                                              uint32_t* leaf_counts, uint32_t* scan_temp,
+                                              int32_t* segment_edge_offsets,
+                                              int32_t* primitive_edge_offsets, float* edges_px,
+                                              float* edge_t_starts, float* edge_t_ends,
+                                              hipStream_t stream) {
+    if (nseg < 0 || nprim < 0 || samples < 2 || !segment_edge_offsets) return CS_ERR_ARGS;
+    const int maxd = ceil_log2(samples - 1);
+    if (maxd > kDecasMaxDepth || (int64_t)nseg << maxd > (int64_t)INT32_MAX) return CS_ERR_ARGS;
     if (nseg > 0)
-        hipLaunchKernelGGL(k_project_flatten, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
-                           cubics_norm, seg_offsets, nprim, aa_widths, stroke_widths, opacities,
-                           mode, nseg, img_h, img_w, block_x, block_y, aabb_pad, aniso, samples,
-                           cubics_px, seg_tile_ranges, reinterpret_cast<SegRec*>(seg_recs),
-                           reinterpret_cast<EdgeRec*>(edges),
-                           reinterpret_cast<EdgeCull*>(edge_culls));
-    hipLaunchKernelGGL(k_prim_prep, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
-                       cubics_norm, seg_offsets, nprim, seg_tile_ranges,
-                       reinterpret_cast<const SegRec*>(seg_recs), colors, opacities, depths,
-                       fill_rules, aa_widths, stroke_widths, nseg, tbx, tby, mode, status,
-                       prim_tile_ranges,
-                       num_tiles_hit, inv_sigma2s, keys, order,
-                       reinterpret_cast<PrimRec*>(prim_recs));
-    return rank_and_count(keys, order, reinterpret_cast<const int4*>(prim_tile_ranges),
-                          reinterpret_cast<int4*>(rank_tile_ranges), nprim, tbx, tby, keys_alt,
-                          vals_alt, radix_counts, scan_temp, tile_part_base, tile_count,
-                          tile_scratch, status, stream);
+        hipLaunchKernelGGL(k_decas_count_ref, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
+                           cubics_px, nseg, maxd, kDecasTolPx, leaf_counts);
+    int rc = cs_scan_exclusive_u32(leaf_counts, reinterpret_cast<uint32_t*>(segment_edge_offsets),
+                                   nseg, scan_temp, segment_edge_offsets + nseg, stream);
+    if (rc) return rc;
+    if (nseg > 0)
+        hipLaunchKernelGGL(k_decas_emit_ref, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
+                           cubics_px, nseg, maxd, kDecasTolPx, segment_edge_offsets, edges_px,
+                           edge_t_starts, edge_t_ends);
+    if (primitive_edge_offsets && nprim >= 0 && seg_offsets)
+        hipLaunchKernelGGL(k_prim_edge_offsets, dim3(blocks_for(nprim + 1, 256)), dim3(256), 0,
+                           stream, segment_edge_offsets, seg_offsets, nprim + 1, nseg,
+                           primitive_edge_offsets);
+    return launch_status();
+}
+
+extern "C" int cs_flatten_cubics_bernstein(const float* cubics_px, int32_t nseg,
+                                           int32_t samples, float* edges_px,
+                                           hipStream_t stream) {
+    if (nseg < 0 || samples < 2 || (int64_t)nseg * (samples - 1) > (int64_t)INT32_MAX)
+        return CS_ERR_ARGS;
+    if (nseg == 0) return CS_OK;
+    hipLaunchKernelGGL(k_bernstein_ref, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
+                       cubics_px, nseg, samples, edges_px);
+    return launch_status();
+}
+
+extern "C" int cs_cubic_flatness_flags(const float* cubics, int32_t n, float tol_px,
+                                       int32_t force_flat, uint8_t* out_flat,
+                                       hipStream_t stream) {
+    if (n < 0) return CS_ERR_ARGS;
+    if (n == 0) return CS_OK;
+    hipLaunchKernelGGL(k_flatness_flags, dim3(blocks_for(n, 256)), dim3(256), 0, stream, cubics,
+                       n, fmaxf(1e-4f, tol_px), force_flat ? 1 : 0, out_flat);
+    return launch_status();
+}
+
+extern "C" int cs_cubic_split_half(const float* cubics, int32_t n, float* left, float* right,
+                                   hipStream_t stream) {
+    if (n < 0) return CS_ERR_ARGS;
+    if (n == 0) return CS_OK;
+    hipLaunchKernelGGL(k_split_half, dim3(blocks_for(n, 256)), dim3(256), 0, stream, cubics, n,
+                       left, right);
+    return launch_status();
 }
 
 // 2D Gaussians: the tile rectangle map_gaussian_to_intersects_kernel emits

@@ -80,6 +80,17 @@ __device__ __forceinline__ int32_t pack_lo_span(int32_t lo, int32_t span) {
 __device__ __forceinline__ int32_t packed_lo(int32_t v) { return (int32_t)(v << 16) >> 16; }
 __device__ __forceinline__ int32_t packed_span(int32_t v) { return v >> 16; }
 
+// Per-edge record of the adaptive (de Casteljau) flattening, 16 bytes: the
+// edge's cubic segment and the parameter interval [t0, t1] of the leaf cubic
+// it is the chord of (cubic_splatting.py:1812-1828).  The backward folds an
+// edge's endpoint gradients into its segment's control points with the
+// Bernstein weights at t0 and t1 (cubic_splatting.py:2432-2485).
+struct alignas(16) EdgeAux {
+    int32_t seg;
+    float t0, t1;
+    int32_t pad;
+};
+
 // Per cubic segment: the unions of its edges' ranges, plus the last pixel
 // column that can lie left of one of its vertices (for open chains).
 struct alignas(16) SegRec {
@@ -94,7 +105,7 @@ struct alignas(16) PrimRec {
     float inv_sigma;    // sqrt(max(inv_sigma2, eps))
     float half_sw;      // stroke half width max(0, sw) / 2 (0 for fill)
     float cull_d;       // beyond this distance a pixel's result does not depend on it
-    int32_t s0, s1;     // segment range
+    int32_t e0, e1;     // edge range (all edges of the primitive's segments)
     int32_t rule;       // 0 even-odd, else nonzero (fill)
     int32_t closed;     // 1 if the edge chain is closed
     int32_t ny_lo, ny_span, cy_lo, cy_span;  // unions over the segments

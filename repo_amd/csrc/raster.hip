@@ -27,6 +27,7 @@ namespace cs {
 static_assert(sizeof(EdgeRec) == CS_EDGE_RECORD_BYTES, "edge record layout");
 static_assert(sizeof(PrimRec) == CS_PRIM_RECORD_BYTES, "primitive record layout");
 static_assert(sizeof(EdgeCull) == CS_EDGE_CULL_BYTES, "edge cull record layout");
+static_assert(sizeof(EdgeAux) == CS_EDGE_AUX_BYTES, "edge aux record layout");
 
 // Crossing parity equals winding & 1 (each crossing changes the winding by
 // +-1), so only the winding number is tracked.
@@ -247,7 +248,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
 template <int MODE, bool BEST, bool COUNT>
 __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& W,
                                               const EdgeCull* __restrict__ culls,
-                                              cptr<EdgeRec> edges, int eps, float px,
+                                              cptr<EdgeRec> edges, float px,
                                               const float (&py)[kPix], int4 first,
                                               Geom (&G)[kPix], EvalCounts& n, int npix) {
 #pragma unroll
@@ -260,7 +261,7 @@ __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect&
         G[p].bdy = 0.0f;
     }
     // The first chunk's words were loaded ahead by the caller.
-    const int c0 = pr.s0 * eps, e1 = pr.s1 * eps;
+    const int c0 = pr.e0, e1 = pr.e1;
     chunk_geometry<MODE, BEST, COUNT>(first, c0, e1, W, edges, px, py, G, n, npix);
     for (int c = c0 + kWave; c < e1; c += kWave)
         chunk_geometry<MODE, BEST, COUNT>(load_culls(culls, c, e1), c, e1, W, edges, px, py, G,
@@ -356,7 +357,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
-    int tbx, int ntiles, int eps, float* __restrict__ out, float* __restrict__ final_T,
+    int tbx, int ntiles, float* __restrict__ out, float* __restrict__ final_T,
     int32_t* __restrict__ final_idx, unsigned long long* __restrict__ counts) {
     const int tile = xcd_tile(blockIdx.x, ntiles);
     const int tty = tile / tbx, ttx = tile - tty * tbx;
@@ -381,9 +382,11 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     EvalCounts n{};
     // The cull words of the next entry's first 64 edges are loaded one entry
     // ahead, so that vector load is in flight while this entry is processed.
+    // An empty tile reads no list entry (its bins are (0, 0) and the whole
+    // list may be empty); primitive 0 then stands in for the prefetches.
     int pid = g0 < g1 ? prim_ids[g0] : 0;
-    int pid_next = prim_ids[min(g0 + 1, g1 - 1)];
-    int4 q_next = g0 < g1 ? load_culls(culls, prims[pid].s0 * eps, prims[pid].s1 * eps)
+    int pid_next = g0 < g1 ? prim_ids[min(g0 + 1, g1 - 1)] : 0;
+    int4 q_next = g0 < g1 ? load_culls(culls, prims[pid].e0, prims[pid].e1)
                           : make_int4(0, -1, 0, -1);
     for (int g = g0; g < g1; ++g) {
         bool live[kPix];
@@ -395,10 +398,10 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
         }
         if (__ballot(any_live) == 0) break;
         const PrimRec pr = prims[pid];
-        const int ns0 = prims[pid_next].s0, ns1 = prims[pid_next].s1;
+        const int ne0 = prims[pid_next].e0, ne1 = prims[pid_next].e1;
         const int pid_after = prim_ids[min(g + 2, g1 - 1)];
         const int4 q = q_next;
-        q_next = load_culls(culls, ns0 * eps, ns1 * eps);
+        q_next = load_culls(culls, ne0, ne1);
         pid = pid_next;
         pid_next = pid_after;
         const float D2 = pr.cull_d * pr.cull_d, D2o = pr.cull_out * pr.cull_out;
@@ -409,7 +412,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
             n.entries += 1;
         }
         Geom G[kPix];
-        prim_geometry<MODE, false, COUNT>(pr, W, culls, edges, eps, L.px, L.py, q, G, n, npix);
+        prim_geometry<MODE, false, COUNT>(pr, W, culls, edges, L.px, L.py, q, G, n, npix);
         if constexpr (COUNT) {
             bool ex[kPix];
 #pragma unroll
@@ -460,15 +463,20 @@ __device__ __forceinline__ int div_eps(int n, int eps, uint32_t magic) {
 // the hardware reciprocal (within 1 ulp) instead of an IEEE division.
 __device__ __forceinline__ float grad_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
-// Reference cubic-accumulation basis at t = e / eps (cubic_splatting.py:2353-2371).
-__device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
-    const float t = (float)e * inv_e;
+// Reference cubic-accumulation basis at t (cubic_splatting.py:2353-2371,
+// :2446-2463).
+__device__ __forceinline__ void basis_at(float t, float b[4]) {
     const float o = 1.0f - t;
     const float o2 = o * o, t2 = t * t;
     b[0] = o2 * o;
     b[1] = 3.0f * o2 * t;
     b[2] = 3.0f * o * t2;
     b[3] = t2 * t;
+}
+
+// The same at t = e / eps for edge e of a uniformly flattened segment.
+__device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
+    basis_at((float)e * inv_e, b);
 }
 
 // Backward: the reverse traversal of cubic_splatting.py:1339-1649 (fill) and
@@ -481,12 +489,16 @@ __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
 //     reference's accumulation weights (cubic_splatting.py:2308-2396), then
 //     the pixels that share a segment are summed (one leader pass per distinct
 //     segment) and one 8-lane atomic adds the 8 values to v_cubics_px.
-template <int MODE, bool COUNT>
+// ADAPTIVE: edges come from the de Casteljau flattening; an edge's segment and
+// its leaf interval [t0, t1] are read from its aux record (the CSR weights of
+// cubic_splatting.py:2432-2485) instead of being derived from its index.
+template <int MODE, bool COUNT, bool ADAPTIVE>
 __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
-    int tbx, int ntiles, int eps, uint32_t eps_magic, const float* __restrict__ final_T,
+    int tbx, int ntiles, int eps, uint32_t eps_magic, const EdgeAux* __restrict__ edge_aux,
+    const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
@@ -531,8 +543,8 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
     // As in the forward, the next entry's first cull words are loaded one
     // entry ahead (here the next entry is g - 1).
     int pid = gstart >= g0 ? prim_ids[gstart] : 0;
-    int pid_next = prim_ids[max(gstart - 1, g0)];
-    int4 q_next = gstart >= g0 ? load_culls(culls, prims[pid].s0 * eps, prims[pid].s1 * eps)
+    int pid_next = gstart >= g0 ? prim_ids[max(gstart - 1, g0)] : 0;
+    int4 q_next = gstart >= g0 ? load_culls(culls, prims[pid].e0, prims[pid].e1)
                                : make_int4(0, -1, 0, -1);
     const int slot = reduce8_slot(lane & 7);
     const bool adder = (lane & ~7) == 8;
@@ -546,10 +558,10 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
         }
         const int pid_cur = pid;
         const PrimRec pr = prims[pid_cur];
-        const int ns0 = prims[pid_next].s0, ns1 = prims[pid_next].s1;
+        const int ne0 = prims[pid_next].e0, ne1 = prims[pid_next].e1;
         const int pid_after = prim_ids[max(g - 2, g0)];
         const int4 q = q_next;
-        q_next = load_culls(culls, ns0 * eps, ns1 * eps);
+        q_next = load_culls(culls, ne0, ne1);
         pid = pid_next;
         pid_next = pid_after;
         if (__ballot(any_valid) == 0) continue;
@@ -561,7 +573,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
             n.entries += 1;
         }
         Geom G[kPix];
-        prim_geometry<MODE, true, COUNT>(pr, W, culls, edges, eps, L.px, L.py, q, G, n, npix);
+        prim_geometry<MODE, true, COUNT>(pr, W, culls, edges, L.px, L.py, q, G, n, npix);
         if constexpr (COUNT) {
             bool ex[kPix];
 #pragma unroll
@@ -672,11 +684,18 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
 #pragma unroll
             for (int k = 0; k < 8; ++k) cp[p][k] = 0.0f;
             if (!geom[p]) continue;
-            gseg[p] = div_eps(G[p].best, eps, eps_magic);
-            const int el = G[p].best - gseg[p] * eps;
             float bs[4], be[4];
-            seg_basis(el, inv_e, bs);
-            seg_basis(el + 1, inv_e, be);
+            if constexpr (ADAPTIVE) {
+                const int4 ax = *reinterpret_cast<const int4*>(edge_aux + G[p].best);
+                gseg[p] = ax.x;
+                basis_at(__builtin_bit_cast(float, ax.y), bs);
+                basis_at(__builtin_bit_cast(float, ax.z), be);
+            } else {
+                gseg[p] = div_eps(G[p].best, eps, eps_magic);
+                const int el = G[p].best - gseg[p] * eps;
+                seg_basis(el, inv_e, bs);
+                seg_basis(el + 1, inv_e, be);
+            }
             const float sx = (1.0f - G[p].bproj) * gx[p], sy = (1.0f - G[p].bproj) * gy[p];
             const float ex = G[p].bproj * gx[p], ey = G[p].bproj * gy[p];
 #pragma unroll
@@ -741,6 +760,37 @@ __global__ __launch_bounds__(256) void k_accumulate(const float4* __restrict__ v
     }
 }
 
+// _accumulate_edge_grads_to_cubics_csr_kernel (cubic_splatting.py:2399-2487):
+// v_P_k = sum over the segment's edges of gs b_k(t0) + ge b_k(t1), fused with
+// the px -> normalized scaling.
+__global__ __launch_bounds__(256) void k_accumulate_csr(const float4* __restrict__ v_edges,
+                                                       const float* __restrict__ t_starts,
+                                                       const float* __restrict__ t_ends,
+                                                       const int32_t* __restrict__ seo,
+                                                       int nseg, float half_w, float half_h,
+                                                       float* __restrict__ v_px,
+                                                       float* __restrict__ v_norm) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int e = seo[s]; e < seo[s + 1]; ++e) {
+        float bs[4], be[4];
+        basis_at(t_starts[e], bs);
+        basis_at(t_ends[e], be);
+        const float4 gr = v_edges[e];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            a[2 * k] = __builtin_fmaf(gr.z, be[k], __builtin_fmaf(gr.x, bs[k], a[2 * k]));
+            a[2 * k + 1] = __builtin_fmaf(gr.w, be[k], __builtin_fmaf(gr.y, bs[k], a[2 * k + 1]));
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        v_px[(size_t)s * 8 + k] = a[k];
+        if (v_norm) v_norm[(size_t)s * 8 + k] = a[k] * ((k & 1) ? half_h : half_w);
+    }
+}
+
 // v_cubics_norm = v_cubics_px * (W/2, H/2) (cubic_splatting.py:3096-3100) and
 // v_aa_widths = -2 v_inv_sigma2 / max(w^3, 1e-12) (cubic_splatting.py:3103-3104),
 // w = max(aa_width, 1e-4) (the clamp of cubic_splatting.py:2820).
@@ -782,6 +832,7 @@ struct RasterArgs {
     const float* fT;
     const int32_t* fidx;
     const float* v_out;
+    const EdgeAux* aux;  // adaptive flattening (eps == 0)
     float *v_cub, *v_col, *v_op, *v_is2, *v_sw, *c_rgb, *c_isect;
     // evaluation counters of the counting entry points
     unsigned long long* counts;
@@ -792,18 +843,24 @@ template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
     hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.nt), dim3(kRasterThreads), 0,
                        a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.eps, a.out, a.final_T, a.final_idx, a.counts);
+                       a.nt, a.out, a.final_T, a.final_idx, a.counts);
+}
+
+template <int MODE, bool COUNT, bool ADAPTIVE>
+static void launch_bwd3(const RasterArgs& a) {
+    // ceil(2^32 / eps) for div_eps (unused when eps <= 1).
+    const uint32_t magic =
+        a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
+    hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT, ADAPTIVE>), dim3(a.nt), dim3(kRasterThreads),
+                       0, a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
+                       a.nt, a.eps, magic, a.aux, a.fT, a.fidx, a.v_out, a.v_cub, a.v_col,
+                       a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.counts);
 }
 
 template <int MODE, bool COUNT>
 static void launch_bwd(const RasterArgs& a) {
-    // ceil(2^32 / eps) for div_eps (unused when eps == 1).
-    const uint32_t magic =
-        a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
-    hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT>), dim3(a.nt), dim3(kRasterThreads), 0,
-                       a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.eps, magic, a.fT, a.fidx, a.v_out, a.v_cub, a.v_col, a.v_op,
-                       a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.counts);
+    if (a.aux) launch_bwd3<MODE, COUNT, true>(a);
+    else launch_bwd3<MODE, COUNT, false>(a);
 }
 
 template <bool COUNT>
@@ -845,7 +902,9 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                              int32_t img_w, int32_t edges_per_segment, float* out_img,
                              float* final_Ts, int32_t* final_idx,
                              unsigned long long* eval_counts, hipStream_t stream) {
-    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1 ||
+    // The primitive records hold each primitive's edge range, so the forward
+    // does not use edges_per_segment (0 for adaptively flattened records).
+    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 0 ||
         img_h > kMaxImageDim || img_w > kMaxImageDim)
         return CS_ERR_ARGS;
     RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
@@ -894,9 +953,11 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               float* v_cubics_px, float* v_colors, float* v_opacities,
                               float* v_inv_sigma2s, float* v_stroke_widths,
                               float* curve_contrib_rgb, float* curve_isect_contrib,
-                              unsigned long long* eval_counts, hipStream_t stream) {
-    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 1 ||
-        img_h > kMaxImageDim || img_w > kMaxImageDim)
+                              const void* edge_aux, unsigned long long* eval_counts,
+                              hipStream_t stream) {
+    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 ||
+        (edge_aux == nullptr && edges_per_segment < 1) || img_h > kMaxImageDim ||
+        img_w > kMaxImageDim)
         return CS_ERR_ARGS;
     if (mode == 1 && v_stroke_widths == nullptr) return CS_ERR_ARGS;
     RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
@@ -911,6 +972,8 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
     a.v_sw = v_stroke_widths;
     a.c_rgb = curve_contrib_rgb;
     a.c_isect = curve_isect_contrib;
+    a.aux = reinterpret_cast<const EdgeAux*>(edge_aux);
+    if (edge_aux) a.eps = 0;
     a.counts = eval_counts;
     if (eval_counts) launch_bwd_mode<true>(a);
     else launch_bwd_mode<false>(a);
@@ -932,7 +995,21 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              stream);
+                              nullptr, stream);
+}
+
+extern "C" int cs_rasterize_backward_de_casteljau(
+    int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
+    const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
+    int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
+    const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
+    float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
+    float* curve_isect_contrib, hipStream_t stream) {
+    if (!edge_aux) return CS_ERR_ARGS;
+    return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
+                              background, img_h, img_w, 0, final_Ts, final_idx, v_output,
+                              v_cubics_px, v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
+                              curve_contrib_rgb, curve_isect_contrib, edge_aux, nullptr, stream);
 }
 
 extern "C" int cs_rasterize_backward_counted(
@@ -946,7 +1023,7 @@ extern "C" int cs_rasterize_backward_counted(
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
-                              v_stroke_widths, curve_contrib_rgb, curve_isect_contrib,
+                              v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
                               eval_counts, stream);
 }
 
@@ -960,6 +1037,20 @@ extern "C" int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg,
     hipLaunchKernelGGL(k_accumulate, dim3((nseg + 255) / 256), dim3(256), 0, stream,
                        reinterpret_cast<const float4*>(v_edges), nseg, edges_per_segment, half_w,
                        half_h, v_cubics_px, v_cubics_norm);
+    return raster_status();
+}
+
+extern "C" int cs_accumulate_edge_grads_csr(const float* v_edges, const float* edge_t_starts,
+                                            const float* edge_t_ends,
+                                            const int32_t* segment_edge_offsets, int32_t nseg,
+                                            int32_t img_h, int32_t img_w, float* v_cubics_px,
+                                            float* v_cubics_norm, hipStream_t stream) {
+    if (nseg < 0 || !segment_edge_offsets) return CS_ERR_ARGS;
+    if (nseg == 0) return CS_OK;
+    const float half_w = (float)(0.5 * (double)img_w), half_h = (float)(0.5 * (double)img_h);
+    hipLaunchKernelGGL(k_accumulate_csr, dim3((nseg + 255) / 256), dim3(256), 0, stream,
+                       reinterpret_cast<const float4*>(v_edges), edge_t_starts, edge_t_ends,
+                       segment_edge_offsets, nseg, half_w, half_h, v_cubics_px, v_cubics_norm);
     return raster_status();
 }
 

@@ -78,9 +78,11 @@ def tile_bounds(img_h: int, img_w: int, block_x: int = BLOCK_X, block_y: int = B
 
 # Buffers of one binning, carved from one arena allocation: name -> (dtype,
 # shape).  Shapes depend on (nseg, P, S, T, K, scratch sizes).
-def _binning_fields(nseg, P, E, T, K, radix_elems, scan_elems, grad_elems):
+def _binning_fields(nseg, P, E, T, K, radix_elems, scan_elems, grad_elems, adaptive=False):
     f32, i32 = torch.float32, torch.int32
-    return (
+    extra = ((("seg_edge_offsets", i32, (nseg + 1,)), ("edge_aux", i32, (E, N.EDGE_AUX_INTS)),
+              ("leaf_counts", i32, (nseg,))) if adaptive else ())
+    return extra + (
         ("cubics_px", f32, (nseg, 4, 2)),
         ("seg_tile_ranges", i32, (nseg, 4)),
         ("seg_recs", i32, (nseg, N.SEG_RECORD_INTS)),
@@ -136,10 +138,15 @@ class Binned:
     [E,4], prim_tile_ranges [P,4], num_tiles_hit [P], inv_sigma2s [P],
     prim_recs [P,20], order [P] (depth rank -> primitive id), tile_bins [T,2],
     grad_accum (the backward's accumulators, cleared by the binning's last
-    launch)."""
+    launch).  With the adaptive (de Casteljau) flattening also
+    seg_edge_offsets [nseg+1] (segment -> edge CSR), edge_aux [E,4]
+    (segment, t0, t1 bits) and leaf_counts [nseg]; E is then the capacity
+    nseg * 2^ceil(log2(samples - 1)) and seg_edge_offsets[-1] the edge count."""
 
-    def __init__(self, *, mode, img_h, img_w, samples, nseg, nprim, arena, table):
+    def __init__(self, *, mode, img_h, img_w, samples, nseg, nprim, arena, table,
+                 adaptive=False):
         self.mode, self.img_h, self.img_w, self.samples = mode, img_h, img_w, samples
+        self.adaptive = adaptive
         self.nseg, self.nprim = nseg, nprim
         self.num_intersects = -1
         self.arena = arena
@@ -172,11 +179,18 @@ class Binned:
 
     @property
     def edges_per_segment(self) -> int:
-        return self.samples - 1
+        """Uniform flattening: S - 1; adaptive: 0 (edge ranges are in the records)."""
+        return 0 if self.adaptive else self.samples - 1
+
+    def num_edges(self) -> int:
+        """Edge count (a host read for the adaptive flattening)."""
+        if self.adaptive:
+            return int(self.seg_edge_offsets[-1].item())
+        return self.nseg * (self.samples - 1)
 
     def edges_px(self) -> torch.Tensor:
         """Edges in the reference's [E,2,2] layout."""
-        return self.edges[:, :4].reshape(-1, 2, 2)
+        return self.edges[: self.num_edges(), :4].reshape(-1, 2, 2)
 
 
 @dataclass
@@ -205,7 +219,7 @@ def _give_pinned(pair) -> None:
 def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rules, widths,
                    stroke_widths, img_h, img_w, samples, *, aabb_pad=DEFAULT_AABB_PAD,
                    aniso=False, mode=MODE_FILL, block_x=BLOCK_X, block_y=BLOCK_Y,
-                   capacity_hint=None) -> Binned:
+                   capacity_hint=None, flatten_method=CUBIC_FLATTEN_METHOD_BERNSTEIN) -> Binned:
     """Project, flatten and bin (cubic_splatting.py:2815-2908).  All inputs are
     contiguous device tensors of the reference's dtypes.  Without
     capacity_hint the host reads the intersection count before the lists are
@@ -216,32 +230,46 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     nseg = int(cubics_norm.shape[0])
     P = int(seg_offsets.numel()) - 1
     S = max(2, int(samples))
-    E = nseg * (S - 1)
+    adaptive = flatten_method == CUBIC_FLATTEN_METHOD_DE_CASTELJAU
+    if adaptive:
+        per_seg = int(lib.cs_de_casteljau_max_edges_per_segment(S))
+        if per_seg <= 0 or nseg * per_seg >= 2 ** 31:
+            raise ValueError(
+                f"de_casteljau flattening of {nseg} segments with distance_samples={S} "
+                "exceeds the supported edge count (2^31 - 1, depth <= 24)")
+    else:
+        per_seg = S - 1
+    E = nseg * per_seg
     tbx, tby, _ = tile_bounds(img_h, img_w, block_x, block_y)
     T = tbx * tby
-    key = (dev.index, mode, nseg, P, S, img_h, img_w, block_x, block_y)
+    key = (dev.index, mode, nseg, P, S, img_h, img_w, block_x, block_y, adaptive)
     lay = _LAYOUTS.get(key)
     if lay is None:
         K = int(lib.cs_bin_tile_parts(P, img_h, img_w, block_x, block_y))
         fields = _binning_fields(nseg, P, E, T, K, int(lib.cs_radix_counts_elems(P)),
-                                 int(lib.cs_scan_temp_elems(max(P, T))),
-                                 _grad_accum_elems(nseg, P, mode))
+                                 int(lib.cs_scan_temp_elems(max(P, T, nseg))),
+                                 _grad_accum_elems(nseg, P, mode), adaptive)
         lay = _layout(key, fields)
     table, nbytes = lay
     arena = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
     b = Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P, arena=arena,
-               table=table)
+               table=table, adaptive=adaptive)
     q = b.ptr
     st = N.stream(dev)
+    args = (N.ptr(cubics_norm), N.ptr(seg_offsets), N.ptr(colors), N.ptr(opacities),
+            N.ptr(depths), N.ptr(fill_rules), N.ptr(widths), N.ptr(stroke_widths), nseg, P,
+            img_h, img_w, block_x, block_y, S, float(aabb_pad), int(bool(aniso)), mode,
+            q("cubics_px"), q("seg_tile_ranges"), q("seg_recs"), q("edges"), q("edge_culls"),
+            q("prim_tile_ranges"), q("num_tiles_hit"), q("inv_sigma2s"), q("prim_recs"),
+            q("keys"), q("order"), q("keys_alt"), q("vals_alt"), q("radix_counts"),
+            q("scan_temp"), q("rank_tile_ranges"), q("tile_part_base"), q("tile_count"),
+            q("tile_scratch"), q("status"))
     with N.prof("cubic.fwd.bin_prepare"):
-        N.call("cs_bin_prepare", N.ptr(cubics_norm), N.ptr(seg_offsets), N.ptr(colors),
-               N.ptr(opacities), N.ptr(depths), N.ptr(fill_rules), N.ptr(widths),
-               N.ptr(stroke_widths), nseg, P, img_h, img_w, block_x, block_y, S, float(aabb_pad),
-               int(bool(aniso)), mode, q("cubics_px"), q("seg_tile_ranges"), q("seg_recs"),
-               q("edges"), q("edge_culls"), q("prim_tile_ranges"), q("num_tiles_hit"),
-               q("inv_sigma2s"), q("prim_recs"), q("keys"), q("order"), q("keys_alt"),
-               q("vals_alt"), q("radix_counts"), q("scan_temp"), q("rank_tile_ranges"),
-               q("tile_part_base"), q("tile_count"), q("tile_scratch"), q("status"), st)
+        if adaptive:
+            N.call("cs_bin_prepare_de_casteljau", *args, q("seg_edge_offsets"), q("edge_aux"),
+                   q("leaf_counts"), st)
+        else:
+            N.call("cs_bin_prepare", *args, st)
     grad_n = table["grad_accum"][2][0]
 
     def finish(capacity: int) -> torch.Tensor:
@@ -366,6 +394,17 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_opac = rest[3 * P: 4 * P]
     v_is2 = rest[4 * P: 5 * P]
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
+    if b.adaptive:
+        if eval_counts is not None:
+            raise ValueError("evaluation counts are measured on the uniform flattening only")
+        with N.prof("cubic.bwd.rast"):
+            N.call("cs_rasterize_backward_de_casteljau", b.mode, N.ptr(b.primitive_ids_sorted),
+                   b.ptr("tile_bins"), b.ptr("edges"), b.ptr("edge_culls"), b.ptr("prim_recs"),
+                   N.ptr(background), b.img_h, b.img_w, b.ptr("edge_aux"), N.ptr(final_T),
+                   N.ptr(final_idx), N.ptr(v_output), N.ptr(v_px), N.ptr(v_colors),
+                   N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
+                   N.ptr(curve_isect_contrib), N.stream(dev))
+        return v_px, v_colors, v_opac, v_is2, v_sw
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
             b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(v_output), N.ptr(v_px),
@@ -381,13 +420,22 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
 
 
 def accumulate_edge_grads(b: Binned, v_edges):
-    """Reference building block (cubic_splatting.py:2308-2396): v_edges [E,4]
-    -> (v_cubics_px, v_cubics_norm)."""
+    """Reference building block (cubic_splatting.py:2308-2396; the CSR form
+    :2399-2487 for the adaptive flattening): v_edges [E,4] -> (v_cubics_px,
+    v_cubics_norm)."""
     dev = v_edges.device
     v_px = torch.empty((b.nseg, 4, 2), dtype=torch.float32, device=dev)
     v_norm = torch.empty((b.nseg, 4, 2), dtype=torch.float32, device=dev)
-    N.call("cs_accumulate_edge_grads", N.ptr(v_edges), b.nseg, b.edges_per_segment, b.img_h,
-           b.img_w, N.ptr(v_px), N.ptr(v_norm), N.stream(dev))
+    if b.adaptive:
+        E = b.num_edges()
+        aux = b.edge_aux[:E].view(torch.float32)
+        t0, t1 = aux[:, 1].contiguous(), aux[:, 2].contiguous()
+        N.call("cs_accumulate_edge_grads_csr", N.ptr(v_edges), N.ptr(t0), N.ptr(t1),
+               b.ptr("seg_edge_offsets"), b.nseg, b.img_h, b.img_w, N.ptr(v_px), N.ptr(v_norm),
+               N.stream(dev))
+    else:
+        N.call("cs_accumulate_edge_grads", N.ptr(v_edges), b.nseg, b.edges_per_segment,
+               b.img_h, b.img_w, N.ptr(v_px), N.ptr(v_norm), N.stream(dev))
     return v_px, v_norm
 
 
@@ -425,11 +473,6 @@ def _check_block(block_x: int, block_y: int) -> None:
             f"the MI355X raster kernels use {BLOCK_X}x{BLOCK_Y} tiles; got {block_x}x{block_y}")
 
 
-def _check_flatten(method: str) -> None:
-    if method != CUBIC_FLATTEN_METHOD_BERNSTEIN:
-        raise NotImplementedError("only uniform Bernstein flattening is implemented on MI355X")
-
-
 def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacities, depths,
                    fill_rules, stroke_widths, img_h, img_w, block_x, block_y, background,
                    aabb_pad, aniso_intersects, aa_widths, distance_samples, flatten_method,
@@ -444,7 +487,6 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
         ctx.empty = True
         return bg.view(1, 1, 3).expand(int(img_h), int(img_w), 3).clone()
     _check_block(block_x, block_y)
-    _check_flatten(flatten_method_norm)
     if int(img_h) > N.MAX_IMAGE_DIM or int(img_w) > N.MAX_IMAGE_DIM:
         raise ValueError(f"img_h and img_w must be at most {N.MAX_IMAGE_DIM} "
                          f"(got {int(img_h)}x{int(img_w)})")
@@ -473,12 +515,13 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
     rules_c = _i32(fill_rules).view(-1) if fill_rules is not None else None
     sw_c = _f32(stroke_widths).view(-1) if stroke_widths is not None else None
     hint_key = (cubics_norm.device.index, mode, num_primitives, num_segments, int(img_h),
-                int(img_w), int(distance_samples))
+                int(img_w), int(distance_samples), flatten_method_norm)
     b = bin_primitives(_f32(cubics_norm), offs, colors_c, opac_c, _f32(depths).view(-1),
                        rules_c, widths, sw_c, int(img_h), int(img_w), int(distance_samples),
                        aabb_pad=float(aabb_pad), aniso=bool(aniso_intersects), mode=mode,
                        block_x=int(block_x), block_y=int(block_y),
-                       capacity_hint=_CAPACITY_HINTS.get(hint_key))
+                       capacity_hint=_CAPACITY_HINTS.get(hint_key),
+                       flatten_method=flatten_method_norm)
     # With a hint the raster is enqueued before the host reads the count; if
     # the lists did not fit, they and the raster are redone at full size.
     out, final_T, final_idx = rasterize_forward(b, bg)

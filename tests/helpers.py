@@ -16,15 +16,15 @@ def scene_np(sc):
                 stroke_widths=sw, img_h=sc.img_h, img_w=sc.img_w, S=sc.S)
 
 
-def oracle_forward(sc, rows=None):
+def oracle_forward(sc, rows=None, flatten_method="bernstein"):
     d = scene_np(sc)
     return O.render_forward(d["cubics_norm"], d["offs"], d["colors"], d["opacities"], d["depths"],
                             d["img_h"], d["img_w"], d["background"], fill_rules=d["fill_rules"],
                             aa_widths=d["aa_widths"], S=d["S"], stroke_widths=d["stroke_widths"],
-                            rows=rows)
+                            rows=rows, flatten_method=flatten_method)
 
 
-def hip_bin(sc, device="cuda"):
+def hip_bin(sc, device="cuda", flatten_method="bernstein"):
     from repo_amd import splat
     s = sc.to(device)
     mode = splat.MODE_FILL if s.stroke_widths is None else splat.MODE_STROKE
@@ -34,7 +34,7 @@ def hip_bin(sc, device="cuda"):
         s.colors.contiguous(), s.opacities.contiguous(), s.depths.contiguous(),
         s.fill_rules.to(torch.int32).contiguous() if mode == 0 else None, widths,
         None if s.stroke_widths is None else s.stroke_widths.contiguous(), s.img_h, s.img_w,
-        s.S, mode=mode), s
+        s.S, mode=mode, flatten_method=flatten_method), s
 
 
 def grad_scale_tol(got, ref, rtol=1e-4, floor=1e-30):

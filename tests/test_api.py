@@ -92,6 +92,25 @@ def _params(fn):
     return out
 
 
+# Flattening blocks of ops/cubic_splatting.py:1654-1659, 1918-1923, 2033-2037, 2490-2500.
+FLATTEN_SIGNATURES = {
+    "_flatten_cubics_to_edges": ["cubics_px", "primitive_seg_offsets", "*distance_samples",
+                                 "*flatten_method"],
+    "cubic_adaptive_flatness_flags_tilelang": ["cubics", "*tol_px", "*force_flat", "*threads"],
+    "cubic_split_half_tilelang": ["cubics", "*threads"],
+    "_accumulate_edge_grads_to_cubics": ["v_edges", "num_segments", "*distance_samples",
+                                         "*flatten_method", "*segment_edge_offsets",
+                                         "*edge_t_starts", "*edge_t_ends", "*threads"],
+}
+
+
+@pytest.mark.parametrize("name", list(FLATTEN_SIGNATURES))
+def test_flattening_block_signatures(name):
+    from manbo.ops import cubic_splatting as cs
+    assert _params(getattr(cs, name)) == FLATTEN_SIGNATURES[name]
+    assert cs.DEFAULT_DE_CASTELJAU_FLATNESS_TOL_PX == 0.5
+
+
 @pytest.mark.parametrize("name", list(REFERENCE_SIGNATURES))
 def test_public_signatures(name):
     import manbo
@@ -194,6 +213,8 @@ def test_flatten_method_and_tile_size_scope():
     import manbo
     from repo_amd import splat
     assert splat.normalize_cubic_flatten_method("bernstein") == "bernstein"
+    for alias in ("de_casteljau", "DeCasteljau", "de-casteljau"):
+        assert splat.normalize_cubic_flatten_method(alias) == "de_casteljau"
     with pytest.raises(ValueError):
         splat.normalize_cubic_flatten_method("nope")
     cub, offs, col, op, dep = _scene_args()

@@ -245,3 +245,24 @@ def test_forward_deterministic_and_bounded_cfg3():
     assert torch.equal(o1, o2) and torch.equal(T1, T2) and torch.equal(i1, i2)
     assert float(T1.min()) > 0 and float(T1.max()) <= 1.0
     assert float(o1.min()) >= 0.0 and float(o1.max()) <= 1.0 + 1e-6
+
+
+@pytest.mark.gpu
+def test_all_primitives_off_screen():
+    """Zero intersections: every tile is empty and the intersection list has no
+    entries; the forward returns the background (twice: without and with the
+    capacity hint of the previous forward) and the backward yields no grads."""
+    import manbo
+    print("[off-screen]", flush=True)
+    sc = synth.small_scene(2, P=5).to("cuda")
+    cub = sc.cubics_norm.clone()
+    cub[..., 0] += 6.0
+    cub.requires_grad_(True)
+    for _ in range(2):
+        img = manbo.ops.render_cubic_fill_splat_tilelang(
+            cub, sc.seg_offsets, sc.colors, sc.opacities, sc.depths, sc.img_h, sc.img_w, 16, 16,
+            sc.background, distance_samples=sc.S)
+        torch.cuda.synchronize()
+        assert torch.equal(img, sc.background.view(1, 1, 3).expand_as(img))
+    img.sum().backward()
+    assert cub.grad is None or float(cub.grad.abs().sum()) == 0.0
