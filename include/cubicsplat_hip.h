@@ -201,6 +201,23 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
 
 /* ---------------- rasterization ---------------- */
 
+/* Tile scheduling of the raster entry points (no reference counterpart; it
+ * changes no result).  Every raster entry point takes two optional arguments
+ * before its stream:
+ *   tile_order [T] (NULL: XCD-contiguous order) -- workgroup b rasterizes tile
+ *     tile_order[b]; it must be a permutation of [0, T);
+ *   wave_cost [2T] uint32 out (NULL: not recorded; 8-byte aligned) -- each
+ *     wave's duration in ticks of the 100 MHz constant clock.
+ * T must stay below 1000003 for cs_raster_tile_order.
+ * cs_raster_tile_order turns the costs of one launch into a heavy-first order
+ * for the next ones (the backward of the same forward, the next forward of
+ * the scene): long tiles start first, short ones fill the tail.  chunked != 0
+ * sorts each XCD's contiguous eighth of the tiles on its own (XCD x keeps its
+ * part of the image, and its L2 the records of that part); chunked == 0 sorts
+ * all tiles (balance across XCDs for skewed scenes). */
+int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
+                         int32_t* tile_order, hipStream_t stream);
+
 /* rasterize_cubic_fill_forward_kernel (ops/cubic_splatting.py:918-1194) when
  * mode 0, rasterize_cubic_polyline_forward_kernel
  * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  16x16 tiles only.
@@ -210,7 +227,8 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
                          const void* edges, const void* edge_culls, const void* prim_recs,
                          const float* background, int32_t img_h, int32_t img_w,
                          int32_t edges_per_segment, float* out_img, float* final_Ts,
-                         int32_t* final_idx, hipStream_t stream);
+                         int32_t* final_idx, const int32_t* tile_order, uint32_t* wave_cost,
+    hipStream_t stream);
 
 /* rasterize_cubic_fill_backward_kernel (ops/cubic_splatting.py:1197-1651) /
  * rasterize_cubic_polyline_backward_kernel (ops/cubic_polyline_splatting.py:252-660)
@@ -225,7 +243,8 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
                           const int32_t* final_idx, const float* v_output, float* v_cubics_px,
                           float* v_colors, float* v_opacities, float* v_inv_sigma2s,
                           float* v_stroke_widths, float* curve_contrib_rgb,
-                          float* curve_isect_contrib, hipStream_t stream);
+                          float* curve_isect_contrib, const int32_t* tile_order, uint32_t* wave_cost,
+    hipStream_t stream);
 
 /* cs_rasterize_backward for records from cs_bin_prepare_de_casteljau
  * (the reference's flatten_method="de_casteljau" backward: the raster kernel
@@ -239,7 +258,8 @@ int cs_rasterize_backward_de_casteljau(
     int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
     const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
     float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
-    float* curve_isect_contrib, hipStream_t stream);
+    float* curve_isect_contrib, const int32_t* tile_order, uint32_t* wave_cost,
+    hipStream_t stream);
 
 /* cs_rasterize_forward / cs_rasterize_backward with the same results, plus
  * evaluation counts added into eval_counts[5] (device uint64, caller-zeroed),
@@ -257,7 +277,8 @@ int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                  const float* background, int32_t img_h, int32_t img_w,
                                  int32_t edges_per_segment, float* out_img, float* final_Ts,
                                  int32_t* final_idx, unsigned long long* eval_counts,
-                                 hipStream_t stream);
+                                 const int32_t* tile_order, uint32_t* wave_cost,
+    hipStream_t stream);
 int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                   const int32_t* tile_bins, const void* edges,
                                   const void* edge_culls, const void* prim_recs,
@@ -267,7 +288,8 @@ int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                   float* v_cubics_px, float* v_colors, float* v_opacities,
                                   float* v_inv_sigma2s, float* v_stroke_widths,
                                   float* curve_contrib_rgb, float* curve_isect_contrib,
-                                  unsigned long long* eval_counts, hipStream_t stream);
+                                  unsigned long long* eval_counts, const int32_t* tile_order, uint32_t* wave_cost,
+    hipStream_t stream);
 
 /* _accumulate_edge_grads_to_cubics_kernel (ops/cubic_splatting.py:2308-2396)
  * fused with the v_cubics_norm scaling (ops/cubic_splatting.py:3096-3100). */

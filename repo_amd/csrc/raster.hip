@@ -352,14 +352,34 @@ __device__ __forceinline__ LanePixels lane_pixels(int r0, int c0, int img_h, int
     return L;
 }
 
+// Tile of workgroup b: entry xcd_tile(b) of a heavy-first tile order when one
+// is given (cs_raster_tile_order), else the XCD-contiguous order xcd_tile(b).  Any
+// permutation of the tiles gives the same results: tiles are independent.
+__device__ __forceinline__ int block_tile(const int32_t* __restrict__ tile_order, int ntiles) {
+    const int t = xcd_tile(blockIdx.x, ntiles);
+    return tile_order ? __builtin_amdgcn_readfirstlane(tile_order[t]) : t;
+}
+
+// A wave's duration in ticks of the constant 100 MHz clock, stored in its
+// slot of wave_cost [2 * ntiles] (two waves per tile) for the next ordering.
+__device__ __forceinline__ void record_wave_cost(uint32_t* __restrict__ wave_cost, int tile,
+                                                 uint64_t t_start) {
+    if (wave_cost && (threadIdx.x & (kWave - 1)) == 0) {
+        const uint64_t dt = __builtin_amdgcn_s_memrealtime() - t_start;
+        wave_cost[2 * tile + (threadIdx.x >> 6)] = dt > 0xffffffffull ? 0xffffffffu : (uint32_t)dt;
+    }
+}
+
 template <int MODE, bool COUNT>
 __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
-    int tbx, int ntiles, float* __restrict__ out, float* __restrict__ final_T,
+    int tbx, int ntiles, const int32_t* __restrict__ tile_order,
+    uint32_t* __restrict__ wave_cost, float* __restrict__ out, float* __restrict__ final_T,
     int32_t* __restrict__ final_idx, unsigned long long* __restrict__ counts) {
-    const int tile = xcd_tile(blockIdx.x, ntiles);
+    const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+    const int tile = block_tile(tile_order, ntiles);
     const int tty = tile / tbx, ttx = tile - tty * tbx;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r0 = tty * kTile + wv * kWaveRows;
@@ -448,6 +468,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
         out[3 * pix + 2] = __builtin_fmaf(T[p], bg[2], C2[p]);
     }
     if constexpr (COUNT) flush_counts(n, counts);
+    record_wave_cost(wave_cost, tile, t_start);
 }
 
 // n / eps for 0 <= n < 2^31 with magic = ceil(2^32 / eps) (eps >= 2): the
@@ -497,13 +518,15 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
-    int tbx, int ntiles, int eps, uint32_t eps_magic, const EdgeAux* __restrict__ edge_aux,
-    const float* __restrict__ final_T,
+    int tbx, int ntiles, const int32_t* __restrict__ tile_order,
+    uint32_t* __restrict__ wave_cost, int eps, uint32_t eps_magic,
+    const EdgeAux* __restrict__ edge_aux, const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
     float* __restrict__ isect_contrib, unsigned long long* __restrict__ counts) {
-    const int tile = xcd_tile(blockIdx.x, ntiles);
+    const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+    const int tile = block_tile(tile_order, ntiles);
     const int tty = tile / tbx, ttx = tile - tty * tbx;
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -725,6 +748,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
         }
     }
     if constexpr (COUNT) flush_counts(n, counts);
+    record_wave_cost(wave_cost, tile, t_start);
 }
 
 // _accumulate_edge_grads_to_cubics_kernel (cubic_splatting.py:2308-2396) and
@@ -808,6 +832,121 @@ __global__ __launch_bounds__(256) void k_finalize(const float* __restrict__ v_px
     }
 }
 
+// Heavy-first tile order from the per-wave costs of a previous launch: a
+// counting sort of tiles by a log-linear bucket of their cost (two waves
+// summed; 128 buckets per octave), descending.  The raster takes tile
+// tile_order[xcd_tile(b, n)] for workgroup b, so the layout decides the
+// schedule:
+//   chunked (grid of 8, one workgroup per XCD's contiguous tile chunk): each
+//     chunk sorted in place, so XCD x still works on its own part of the
+//     image (L2 locality) and starts with its longest tiles;
+//   global (grid of 1): rank r at xcd_tile(r, n), so workgroups take the
+//     longest tiles of the whole image first (balance across XCDs).
+// The costs are read once, coalesced, and each tile's bucket is kept in LDS
+// (16 bits per tile, up to kOrderLdsTiles tiles; larger ranges re-read the
+// costs).  Neighbouring tiles cost about the same, so the counting and
+// scatter passes visit tiles in the scrambled order i * kOrderStride mod m
+// (a bijection: the stride is a prime above any tile count) and a wave's LDS
+// atomics rarely share a bucket.  Order within a bucket is whatever the
+// atomics give; every layout is a permutation of the tiles.
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderBuckets = 4096;
+constexpr int kOrderPerThread = kOrderBuckets / kOrderThreads;
+constexpr int kOrderLdsTiles = 16384;
+constexpr uint64_t kOrderStride = 1000003;   // prime; tile counts stay below it
+
+__device__ __forceinline__ uint32_t cost_bucket(uint32_t c) {
+    if (c == 0) return 0;
+    const int e = 31 - __builtin_clz(c);                      // 0..31
+    const uint32_t m = e >= 7 ? (c >> (e - 7)) & 127u : (c << (7 - e)) & 127u;
+    return (uint32_t)e * 128u + m;                            // < 4096
+}
+
+__device__ __forceinline__ uint32_t tile_bucket(const uint32_t* __restrict__ wave_cost, int t) {
+    const uint2 w = reinterpret_cast<const uint2*>(wave_cost)[t];
+    return cost_bucket(w.x + w.y < w.x ? 0xffffffffu : w.x + w.y);
+}
+
+__global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __restrict__ wave_cost,
+                                                            int n, int chunked,
+                                                            int32_t* __restrict__ order) {
+    __shared__ uint32_t start[kOrderBuckets];
+    __shared__ uint16_t bucket[kOrderLdsTiles];
+    __shared__ uint32_t part[kOrderThreads / kWave];
+    const int tid = threadIdx.x;
+    // This workgroup's tile range [lo, lo + m).
+    int lo = 0, m = n;
+    if (chunked) {
+        const int q = n >> 3, r = n & 7, x = blockIdx.x;
+        lo = x * q + min(x, r);
+        m = q + (x < r ? 1 : 0);
+    }
+    if (m <= 0) return;
+    const bool cached = m <= kOrderLdsTiles;
+    for (int i = tid; i < kOrderBuckets; i += kOrderThreads) start[i] = 0;
+    if (cached) {
+        // All of the thread's cost loads in flight at once.
+        constexpr int kPer = kOrderLdsTiles / kOrderThreads;
+        uint2 wc[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int t = tid + k * kOrderThreads;
+            wc[k] = t < m ? reinterpret_cast<const uint2*>(wave_cost)[lo + t]
+                          : make_uint2(0u, 0u);
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int t = tid + k * kOrderThreads;
+            const uint32_t c = wc[k].x + wc[k].y < wc[k].x ? 0xffffffffu : wc[k].x + wc[k].y;
+            if (t < m) bucket[t] = (uint16_t)cost_bucket(c);
+        }
+    }
+    __syncthreads();
+    // Visit i of this thread: local tile i * stride mod m, advanced incrementally.
+    const uint32_t t0 = (uint32_t)(((uint64_t)tid * kOrderStride) % (uint64_t)m);
+    const uint32_t jump = (uint32_t)(((uint64_t)kOrderThreads * kOrderStride) % (uint64_t)m);
+    for (int i = tid, t = (int)t0; i < m; i += kOrderThreads) {
+        const uint32_t b = cached ? bucket[t] : tile_bucket(wave_cost, lo + t);
+        atomicAdd(&start[b], 1u);
+        t += (int)jump;
+        if (t >= m) t -= m;
+    }
+    __syncthreads();
+    // Exclusive scan in descending bucket order: thread i owns descending
+    // positions kOrderPerThread * i + k, i.e. buckets 4095 - 4i - k.
+    uint32_t h[kOrderPerThread];
+    uint32_t v = 0;
+#pragma unroll
+    for (int k = 0; k < kOrderPerThread; ++k) {
+        h[k] = start[kOrderBuckets - 1 - kOrderPerThread * tid - k];
+        v += h[k];
+    }
+    const uint32_t own = v;
+    const int lane = tid & (kWave - 1), w = tid >> 6;
+    for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t o = __shfl_up(v, d);
+        if (lane >= d) v += o;
+    }
+    if (lane == kWave - 1) part[w] = v;
+    __syncthreads();
+    uint32_t acc = 0;
+    for (int k = 0; k < w; ++k) acc += part[k];
+    acc += v - own;
+#pragma unroll
+    for (int k = 0; k < kOrderPerThread; ++k) {
+        start[kOrderBuckets - 1 - kOrderPerThread * tid - k] = acc;
+        acc += h[k];
+    }
+    __syncthreads();
+    for (int i = tid, t = (int)t0; i < m; i += kOrderThreads) {
+        const uint32_t b = cached ? bucket[t] : tile_bucket(wave_cost, lo + t);
+        const int rank = (int)atomicAdd(&start[b], 1u);
+        order[chunked ? lo + rank : xcd_tile(rank, n)] = lo + t;
+        t += (int)jump;
+        if (t >= m) t -= m;
+    }
+}
+
 }  // namespace cs
 
 using namespace cs;
@@ -836,6 +975,9 @@ struct RasterArgs {
     float *v_cub, *v_col, *v_op, *v_is2, *v_sw, *c_rgb, *c_isect;
     // evaluation counters of the counting entry points
     unsigned long long* counts;
+    // heavy-first tile order (NULL: XCD order) and per-wave costs out (NULL: none)
+    const int32_t* order;
+    uint32_t* wave_cost;
     hipStream_t stream;
 };
 
@@ -843,7 +985,7 @@ template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
     hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.nt), dim3(kRasterThreads), 0,
                        a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.out, a.final_T, a.final_idx, a.counts);
+                       a.nt, a.order, a.wave_cost, a.out, a.final_T, a.final_idx, a.counts);
 }
 
 template <int MODE, bool COUNT, bool ADAPTIVE>
@@ -853,7 +995,8 @@ static void launch_bwd3(const RasterArgs& a) {
         a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
     hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT, ADAPTIVE>), dim3(a.nt), dim3(kRasterThreads),
                        0, a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.eps, magic, a.aux, a.fT, a.fidx, a.v_out, a.v_cub, a.v_col,
+                       a.nt, a.order, a.wave_cost, a.eps, magic, a.aux, a.fT, a.fidx, a.v_out,
+                       a.v_cub, a.v_col,
                        a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.counts);
 }
 
@@ -901,7 +1044,8 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                              const void* prim_recs, const float* background, int32_t img_h,
                              int32_t img_w, int32_t edges_per_segment, float* out_img,
                              float* final_Ts, int32_t* final_idx,
-                             unsigned long long* eval_counts, hipStream_t stream) {
+                             unsigned long long* eval_counts, const int32_t* tile_order,
+                             uint32_t* wave_cost, hipStream_t stream) {
     // The primitive records hold each primitive's edge range, so the forward
     // does not use edges_per_segment (0 for adaptively flattened records).
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 0 ||
@@ -913,6 +1057,8 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
     a.final_T = final_Ts;
     a.final_idx = final_idx;
     a.counts = eval_counts;
+    a.order = tile_order;
+    a.wave_cost = wave_cost;
     if (eval_counts) launch_fwd_mode<true>(a);
     else launch_fwd_mode<false>(a);
     return raster_status();
@@ -924,10 +1070,11 @@ extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted
                                     const float* background,
                                     int32_t img_h, int32_t img_w, int32_t edges_per_segment,
                                     float* out_img, float* final_Ts,
-                                    int32_t* final_idx, hipStream_t stream) {
+                                    int32_t* final_idx, const int32_t* tile_order,
+                                    uint32_t* wave_cost, hipStream_t stream) {
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, edges_per_segment, out_img, final_Ts,
-                             final_idx, nullptr, stream);
+                             final_idx, nullptr, tile_order, wave_cost, stream);
 }
 
 extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
@@ -937,11 +1084,12 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
                                             int32_t img_w, int32_t edges_per_segment,
                                             float* out_img, float* final_Ts, int32_t* final_idx,
                                             unsigned long long* eval_counts,
+                                            const int32_t* tile_order, uint32_t* wave_cost,
                                             hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, edges_per_segment, out_img, final_Ts,
-                             final_idx, eval_counts, stream);
+                             final_idx, eval_counts, tile_order, wave_cost, stream);
 }
 
 static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
@@ -954,6 +1102,7 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               float* v_inv_sigma2s, float* v_stroke_widths,
                               float* curve_contrib_rgb, float* curve_isect_contrib,
                               const void* edge_aux, unsigned long long* eval_counts,
+                              const int32_t* tile_order, uint32_t* wave_cost,
                               hipStream_t stream) {
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 ||
         (edge_aux == nullptr && edges_per_segment < 1) || img_h > kMaxImageDim ||
@@ -975,6 +1124,8 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
     a.aux = reinterpret_cast<const EdgeAux*>(edge_aux);
     if (edge_aux) a.eps = 0;
     a.counts = eval_counts;
+    a.order = tile_order;
+    a.wave_cost = wave_cost;
     if (eval_counts) launch_bwd_mode<true>(a);
     else launch_bwd_mode<false>(a);
     return raster_status();
@@ -990,12 +1141,13 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                                      float* v_cubics_px, float* v_colors, float* v_opacities,
                                      float* v_inv_sigma2s, float* v_stroke_widths,
                                      float* curve_contrib_rgb, float* curve_isect_contrib,
+                                     const int32_t* tile_order, uint32_t* wave_cost,
                                      hipStream_t stream) {
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              nullptr, stream);
+                              nullptr, tile_order, wave_cost, stream);
 }
 
 extern "C" int cs_rasterize_backward_de_casteljau(
@@ -1004,12 +1156,14 @@ extern "C" int cs_rasterize_backward_de_casteljau(
     int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
     const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
     float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
-    float* curve_isect_contrib, hipStream_t stream) {
+    float* curve_isect_contrib, const int32_t* tile_order, uint32_t* wave_cost,
+    hipStream_t stream) {
     if (!edge_aux) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, 0, final_Ts, final_idx, v_output,
                               v_cubics_px, v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
-                              curve_contrib_rgb, curve_isect_contrib, edge_aux, nullptr, stream);
+                              curve_contrib_rgb, curve_isect_contrib, edge_aux, nullptr,
+                              tile_order, wave_cost, stream);
 }
 
 extern "C" int cs_rasterize_backward_counted(
@@ -1018,13 +1172,23 @@ extern "C" int cs_rasterize_backward_counted(
     int32_t img_w, int32_t edges_per_segment, const float* final_Ts, const int32_t* final_idx,
     const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
     float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
-    float* curve_isect_contrib, unsigned long long* eval_counts, hipStream_t stream) {
+    float* curve_isect_contrib, unsigned long long* eval_counts, const int32_t* tile_order,
+    uint32_t* wave_cost, hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              eval_counts, stream);
+                              eval_counts, tile_order, wave_cost, stream);
+}
+
+extern "C" int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
+                                    int32_t* tile_order, hipStream_t stream) {
+    if (ntiles <= 0 || (uint64_t)ntiles >= kOrderStride || !wave_cost || !tile_order)
+        return CS_ERR_ARGS;
+    hipLaunchKernelGGL(k_tile_order, dim3(chunked ? 8 : 1), dim3(kOrderThreads), 0, stream,
+                       wave_cost, ntiles, chunked ? 1 : 0, tile_order);
+    return raster_status();
 }
 
 extern "C" int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg,

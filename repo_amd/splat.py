@@ -104,6 +104,7 @@ def _binning_fields(nseg, P, E, T, K, radix_elems, scan_elems, grad_elems, adapt
         ("tile_scratch", i32, (T,)),
         ("status", i32, (4,)),
         ("tile_bins", i32, (T, 2)),
+        ("wave_cost", i32, (2 * T,)),
         ("grad_accum", f32, (grad_elems,)),
     )
 
@@ -154,6 +155,8 @@ class Binned:
         self._base = arena.data_ptr()
         self._views = {}
         self.primitive_ids_sorted: Optional[torch.Tensor] = None
+        # Heavy-first tile order from this forward's raster (for the backward).
+        self.tile_order: Optional[torch.Tensor] = None
         self.grad_accum_clean = True
         # Set while the intersection count has not been read on the host yet
         # (bin_primitives with a capacity hint); resolve_binned() settles it.
@@ -347,24 +350,58 @@ def intersection_capacity(num_intersects: int) -> int:
     return (want + 4095) // 4096 * 4096
 
 
+# Heavy-first tile orders (cs_raster_tile_order) per (device, stream, tile
+# count): the order the last forward's wave durations gave, which the next
+# forward of an image with that many tiles on that stream starts from.  Any
+# permutation gives the same results, so a stale order only changes speed;
+# keying by stream keeps a forward from reading an order another stream is
+# still writing.
+_TILE_ORDERS: "dict[tuple, torch.Tensor]" = {}
+_MAX_ORDERS = 16
+# Sort within each XCD's contiguous tile range (keeps each XCD's L2 on its own
+# part of the image) rather than across all tiles.
+ORDER_CHUNKED = True
+
+
+def _order_key(dev, ntiles):
+    return (dev.index, N.stream(dev), ntiles)
+
+
 def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
     """(image [H,W,3], final_Ts, final_idx).  With eval_counts (int64 [5],
     zeroed, on the device) the counting instantiation runs and adds the
-    evaluation counts of cs_rasterize_forward_counted into it."""
+    evaluation counts of cs_rasterize_forward_counted into it.  The launch
+    takes tiles in the heavy-first order of the previous forward of this image
+    size on this stream (if any) and records its wave durations, from which
+    the order of this forward's backward (b.tile_order) and of the next
+    forward is made."""
     dev = b.arena.device
     out = torch.empty((b.img_h, b.img_w, 3), dtype=torch.float32, device=dev)
     # final_Ts and final_idx share one allocation (both 4-byte, [H, W]).
     tid = torch.empty((2, b.img_h, b.img_w), dtype=torch.float32, device=dev)
     final_T, final_idx = tid[0], tid[1].view(torch.int32)
+    ntiles = int(b.tile_bins.shape[0])
+    key = _order_key(dev, ntiles)
+    prev = _TILE_ORDERS.get(key)
+    st = N.stream(dev)
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
             b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx))
+    cost = b.ptr("wave_cost")
     if eval_counts is not None:
         N.call("cs_rasterize_forward_counted", *args, N.ptr(_counts_buffer(eval_counts)),
-               N.stream(dev))
+               N.ptr(prev), cost, st)
     else:
         with N.prof("cubic.fwd.rast"):
-            N.call("cs_rasterize_forward", *args, N.stream(dev))
+            N.call("cs_rasterize_forward", *args, N.ptr(prev), cost, st)
+    order = torch.empty((ntiles,), dtype=torch.int32, device=dev)
+    with N.prof("cubic.fwd.tile_order"):
+        N.call("cs_raster_tile_order", cost, ntiles, int(ORDER_CHUNKED), N.ptr(order), st)
+    b.tile_order = order
+    _TILE_ORDERS.pop(key, None)
+    if len(_TILE_ORDERS) >= _MAX_ORDERS:
+        _TILE_ORDERS.pop(next(iter(_TILE_ORDERS)))
+    _TILE_ORDERS[key] = order
     return out, final_T, final_idx
 
 
@@ -403,7 +440,7 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
                    N.ptr(background), b.img_h, b.img_w, b.ptr("edge_aux"), N.ptr(final_T),
                    N.ptr(final_idx), N.ptr(v_output), N.ptr(v_px), N.ptr(v_colors),
                    N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
-                   N.ptr(curve_isect_contrib), N.stream(dev))
+                   N.ptr(curve_isect_contrib), N.ptr(b.tile_order), None, N.stream(dev))
         return v_px, v_colors, v_opac, v_is2, v_sw
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
@@ -412,10 +449,10 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
             N.ptr(curve_isect_contrib))
     if eval_counts is not None:
         N.call("cs_rasterize_backward_counted", *args, N.ptr(_counts_buffer(eval_counts)),
-               N.stream(dev))
+               N.ptr(b.tile_order), None, N.stream(dev))
     else:
         with N.prof("cubic.bwd.rast"):
-            N.call("cs_rasterize_backward", *args, N.stream(dev))
+            N.call("cs_rasterize_backward", *args, N.ptr(b.tile_order), None, N.stream(dev))
     return v_px, v_colors, v_opac, v_is2, v_sw
 
 

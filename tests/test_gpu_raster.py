@@ -266,3 +266,40 @@ def test_all_primitives_off_screen():
         assert torch.equal(img, sc.background.view(1, 1, 3).expand_as(img))
     img.sum().backward()
     assert cub.grad is None or float(cub.grad.abs().sum()) == 0.0
+
+
+@pytest.mark.gpu
+def test_heavy_first_tile_order_is_a_permutation_and_changes_no_result():
+    """cs_raster_tile_order yields a permutation of the tiles; a forward that
+    takes tiles in that order is bit-identical to the XCD-order forward, and
+    the backward in that order matches within the atomics' rounding."""
+    print("[tile order]", flush=True)
+    sc = synth.make_scene(2)
+    b, s = hip_bin(sc)
+    bg = s.background.float().contiguous()
+    splat._TILE_ORDERS.clear()
+    out0, T0, idx0 = splat.rasterize_forward(b, bg)   # first forward: makes an order
+    first = b.tile_order
+    order = first.clone()
+    v = random_v_out(sc.img_h, sc.img_w).cuda()
+    b.tile_order = None
+    g0 = [t.clone() for t in splat.rasterize_backward(b, bg, T0, idx0, v)[:4]]
+    n = int(b.tile_bins.shape[0])
+    assert torch.equal(torch.sort(order.long()).values, torch.arange(n, device="cuda"))
+    out1, T1, idx1 = splat.rasterize_forward(b, bg)   # takes `order`
+    assert torch.equal(out0, out1) and torch.equal(T0, T1) and torch.equal(idx0, idx1)
+    assert b.tile_order is not first                   # each forward makes a new order
+    assert torch.equal(torch.sort(b.tile_order.long()).values, torch.arange(n, device="cuda"))
+    splat.ORDER_CHUNKED = False                        # the global layout is a permutation too
+    try:
+        splat.rasterize_forward(b, bg)
+        out2, T2, idx2 = splat.rasterize_forward(b, bg)
+    finally:
+        splat.ORDER_CHUNKED = True
+    assert torch.equal(torch.sort(b.tile_order.long()).values, torch.arange(n, device="cuda"))
+    assert torch.equal(out0, out2) and torch.equal(idx0, idx2)
+    b.grad_accum_clean = False
+    g1 = splat.rasterize_backward(b, bg, T1, idx1, v)[:4]
+    for a, r in zip(g1, g0):
+        ok, err = grad_scale_tol(a.cpu().numpy(), r.cpu().numpy(), rtol=1e-5)
+        assert ok, err
