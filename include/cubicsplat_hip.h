@@ -202,10 +202,11 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
 /* ---------------- rasterization ---------------- */
 
 /* Tile scheduling of the raster entry points (no reference counterpart; it
- * changes no result).  Every raster entry point takes two optional arguments
- * before its stream:
+ * changes no result).  Every raster entry point takes, before its stream,
  *   tile_order [T] (NULL: XCD-contiguous order) -- workgroup b rasterizes tile
- *     tile_order[b]; it must be a permutation of [0, T);
+ *     tile_order[xcd(b)], xcd(b) the XCD-contiguous index of b; it must be a
+ *     permutation of [0, T);
+ * and the forward ones also
  *   wave_cost [2T] uint32 out (NULL: not recorded; 8-byte aligned) -- each
  *     wave's duration in ticks of the 100 MHz constant clock.
  * T must stay below 1000003 for cs_raster_tile_order.
@@ -243,7 +244,7 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
                           const int32_t* final_idx, const float* v_output, float* v_cubics_px,
                           float* v_colors, float* v_opacities, float* v_inv_sigma2s,
                           float* v_stroke_widths, float* curve_contrib_rgb,
-                          float* curve_isect_contrib, const int32_t* tile_order, uint32_t* wave_cost,
+                          float* curve_isect_contrib, const int32_t* tile_order,
     hipStream_t stream);
 
 /* cs_rasterize_backward for records from cs_bin_prepare_de_casteljau
@@ -258,7 +259,7 @@ int cs_rasterize_backward_de_casteljau(
     int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
     const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
     float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
-    float* curve_isect_contrib, const int32_t* tile_order, uint32_t* wave_cost,
+    float* curve_isect_contrib, const int32_t* tile_order,
     hipStream_t stream);
 
 /* cs_rasterize_forward / cs_rasterize_backward with the same results, plus
@@ -288,7 +289,7 @@ int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                   float* v_cubics_px, float* v_colors, float* v_opacities,
                                   float* v_inv_sigma2s, float* v_stroke_widths,
                                   float* curve_contrib_rgb, float* curve_isect_contrib,
-                                  unsigned long long* eval_counts, const int32_t* tile_order, uint32_t* wave_cost,
+                                  unsigned long long* eval_counts, const int32_t* tile_order,
     hipStream_t stream);
 
 /* _accumulate_edge_grads_to_cubics_kernel (ops/cubic_splatting.py:2308-2396)

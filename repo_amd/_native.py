@@ -52,12 +52,12 @@ _SIGNATURES = {
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
                                             _P, _P, _P, _P]),
     "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P,
-                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_rasterize_forward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                                     _P, _P, _P, _P, _P, _P, _P]),
     "cs_rasterize_backward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
                                                      _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                                     _P, _P, _P, _P, _P]),
+                                                     _P, _P, _P, _P]),
     "cs_raster_tile_order": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
     "cs_accumulate_edge_grads": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P]),
     "cs_de_casteljau_max_edges_per_segment": (_I32, [_I32]),
@@ -73,7 +73,7 @@ _SIGNATURES = {
     "cs_cubic_split_half": (ctypes.c_int, [_P, _I32, _P, _P, _P]),
     "cs_rasterize_backward_de_casteljau": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32,
                                                           _I32, _P, _P, _P, _P, _P, _P, _P, _P,
-                                                          _P, _P, _P, _P, _P, _P]),
+                                                          _P, _P, _P, _P, _P]),
     "cs_accumulate_edge_grads_csr": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
                                                     _P]),
     "cs_backward_finalize": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P]),

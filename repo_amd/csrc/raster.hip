@@ -518,14 +518,12 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
-    int tbx, int ntiles, const int32_t* __restrict__ tile_order,
-    uint32_t* __restrict__ wave_cost, int eps, uint32_t eps_magic,
+    int tbx, int ntiles, const int32_t* __restrict__ tile_order, int eps, uint32_t eps_magic,
     const EdgeAux* __restrict__ edge_aux, const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
     float* __restrict__ isect_contrib, unsigned long long* __restrict__ counts) {
-    const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
     const int tile = block_tile(tile_order, ntiles);
     const int tty = tile / tbx, ttx = tile - tty * tbx;
     const int lane = threadIdx.x & 63;
@@ -748,7 +746,6 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
         }
     }
     if constexpr (COUNT) flush_counts(n, counts);
-    record_wave_cost(wave_cost, tile, t_start);
 }
 
 // _accumulate_edge_grads_to_cubics_kernel (cubic_splatting.py:2308-2396) and
@@ -995,7 +992,7 @@ static void launch_bwd3(const RasterArgs& a) {
         a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
     hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT, ADAPTIVE>), dim3(a.nt), dim3(kRasterThreads),
                        0, a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.order, a.wave_cost, a.eps, magic, a.aux, a.fT, a.fidx, a.v_out,
+                       a.nt, a.order, a.eps, magic, a.aux, a.fT, a.fidx, a.v_out,
                        a.v_cub, a.v_col,
                        a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.counts);
 }
@@ -1102,7 +1099,7 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               float* v_inv_sigma2s, float* v_stroke_widths,
                               float* curve_contrib_rgb, float* curve_isect_contrib,
                               const void* edge_aux, unsigned long long* eval_counts,
-                              const int32_t* tile_order, uint32_t* wave_cost,
+                              const int32_t* tile_order,
                               hipStream_t stream) {
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 ||
         (edge_aux == nullptr && edges_per_segment < 1) || img_h > kMaxImageDim ||
@@ -1125,7 +1122,6 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
     if (edge_aux) a.eps = 0;
     a.counts = eval_counts;
     a.order = tile_order;
-    a.wave_cost = wave_cost;
     if (eval_counts) launch_bwd_mode<true>(a);
     else launch_bwd_mode<false>(a);
     return raster_status();
@@ -1141,13 +1137,13 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                                      float* v_cubics_px, float* v_colors, float* v_opacities,
                                      float* v_inv_sigma2s, float* v_stroke_widths,
                                      float* curve_contrib_rgb, float* curve_isect_contrib,
-                                     const int32_t* tile_order, uint32_t* wave_cost,
+                                     const int32_t* tile_order,
                                      hipStream_t stream) {
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              nullptr, tile_order, wave_cost, stream);
+                              nullptr, tile_order, stream);
 }
 
 extern "C" int cs_rasterize_backward_de_casteljau(
@@ -1156,14 +1152,14 @@ extern "C" int cs_rasterize_backward_de_casteljau(
     int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
     const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
     float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
-    float* curve_isect_contrib, const int32_t* tile_order, uint32_t* wave_cost,
+    float* curve_isect_contrib, const int32_t* tile_order,
     hipStream_t stream) {
     if (!edge_aux) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, 0, final_Ts, final_idx, v_output,
                               v_cubics_px, v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
                               curve_contrib_rgb, curve_isect_contrib, edge_aux, nullptr,
-                              tile_order, wave_cost, stream);
+                              tile_order, stream);
 }
 
 extern "C" int cs_rasterize_backward_counted(
@@ -1173,13 +1169,13 @@ extern "C" int cs_rasterize_backward_counted(
     const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
     float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
     float* curve_isect_contrib, unsigned long long* eval_counts, const int32_t* tile_order,
-    uint32_t* wave_cost, hipStream_t stream) {
+    hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              eval_counts, tile_order, wave_cost, stream);
+                              eval_counts, tile_order, stream);
 }
 
 extern "C" int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,

@@ -440,7 +440,7 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
                    N.ptr(background), b.img_h, b.img_w, b.ptr("edge_aux"), N.ptr(final_T),
                    N.ptr(final_idx), N.ptr(v_output), N.ptr(v_px), N.ptr(v_colors),
                    N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
-                   N.ptr(curve_isect_contrib), N.ptr(b.tile_order), None, N.stream(dev))
+                   N.ptr(curve_isect_contrib), N.ptr(b.tile_order), N.stream(dev))
         return v_px, v_colors, v_opac, v_is2, v_sw
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
@@ -449,10 +449,10 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
             N.ptr(curve_isect_contrib))
     if eval_counts is not None:
         N.call("cs_rasterize_backward_counted", *args, N.ptr(_counts_buffer(eval_counts)),
-               N.ptr(b.tile_order), None, N.stream(dev))
+               N.ptr(b.tile_order), N.stream(dev))
     else:
         with N.prof("cubic.bwd.rast"):
-            N.call("cs_rasterize_backward", *args, N.ptr(b.tile_order), None, N.stream(dev))
+            N.call("cs_rasterize_backward", *args, N.ptr(b.tile_order), N.stream(dev))
     return v_px, v_colors, v_opac, v_is2, v_sw
 
 
