@@ -278,7 +278,7 @@ def main():
         train_step(sc, cub, col, opt)
     # The raster launches of the timed steps are bracketed by HIP events on
     # the stream they run on (torch's current stream).
-    timer = profiling.EventTimer(RASTER_LABELS)
+    timer = profiling.EventTimer(RASTER_LABELS, reserve=args.steps)
     _native.set_profile_ctx_factory(timer)
     torch.cuda.synchronize()
     t0 = time.perf_counter()

@@ -219,6 +219,16 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
 int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
                          int32_t* tile_order, hipStream_t stream);
 
+/* Inside log (mode 0): the forward writes, for every list entry g a wave of
+ * tile rows processes, the wave's per-pixel inside bits (its winding test,
+ * two 64-bit masks = 16 bytes) at inside_log[2 g + wave], and the backward of
+ * that forward reads them instead of re-evaluating the crossing terms.  It
+ * holds 2 * (capacity of prim_ids_sorted) 16-byte records; required by the
+ * fill backward, NULL allowed in the forward (then not written).  No
+ * reference counterpart: the reference's backward re-runs the crossing test
+ * (ops/cubic_splatting.py:1485-1501). */
+#define CS_INSIDE_LOG_BYTES 16
+
 /* rasterize_cubic_fill_forward_kernel (ops/cubic_splatting.py:918-1194) when
  * mode 0, rasterize_cubic_polyline_forward_kernel
  * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  16x16 tiles only.
@@ -228,8 +238,8 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
                          const void* edges, const void* edge_culls, const void* prim_recs,
                          const float* background, int32_t img_h, int32_t img_w,
                          int32_t edges_per_segment, float* out_img, float* final_Ts,
-                         int32_t* final_idx, const int32_t* tile_order, uint32_t* wave_cost,
-    hipStream_t stream);
+                         int32_t* final_idx, void* inside_log, const int32_t* tile_order,
+                         uint32_t* wave_cost, hipStream_t stream);
 
 /* rasterize_cubic_fill_backward_kernel (ops/cubic_splatting.py:1197-1651) /
  * rasterize_cubic_polyline_backward_kernel (ops/cubic_polyline_splatting.py:252-660)
@@ -241,11 +251,11 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
                           const void* edges, const void* edge_culls, const void* prim_recs,
                           const float* background, int32_t img_h, int32_t img_w,
                           int32_t edges_per_segment, const float* final_Ts,
-                          const int32_t* final_idx, const float* v_output, float* v_cubics_px,
-                          float* v_colors, float* v_opacities, float* v_inv_sigma2s,
-                          float* v_stroke_widths, float* curve_contrib_rgb,
+                          const int32_t* final_idx, const void* inside_log, const float* v_output,
+                          float* v_cubics_px, float* v_colors, float* v_opacities,
+                          float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
                           float* curve_isect_contrib, const int32_t* tile_order,
-    hipStream_t stream);
+                          hipStream_t stream);
 
 /* cs_rasterize_backward for records from cs_bin_prepare_de_casteljau
  * (the reference's flatten_method="de_casteljau" backward: the raster kernel
@@ -253,14 +263,17 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
  * ops/cubic_splatting.py:2399-2487): each edge's gradient is folded into its
  * segment's control points with the Bernstein weights at its edge_aux
  * interval [t0, t1]. */
-int cs_rasterize_backward_de_casteljau(
-    int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
-    const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
-    int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
-    const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
-    float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
-    float* curve_isect_contrib, const int32_t* tile_order,
-    hipStream_t stream);
+int cs_rasterize_backward_de_casteljau(int32_t mode, const int32_t* prim_ids_sorted,
+                                       const int32_t* tile_bins, const void* edges,
+                                       const void* edge_culls, const void* prim_recs,
+                                       const float* background, int32_t img_h, int32_t img_w,
+                                       const void* edge_aux, const float* final_Ts,
+                                       const int32_t* final_idx, const void* inside_log,
+                                       const float* v_output, float* v_cubics_px, float* v_colors,
+                                       float* v_opacities, float* v_inv_sigma2s,
+                                       float* v_stroke_widths, float* curve_contrib_rgb,
+                                       float* curve_isect_contrib, const int32_t* tile_order,
+                                       hipStream_t stream);
 
 /* cs_rasterize_forward / cs_rasterize_backward with the same results, plus
  * evaluation counts added into eval_counts[5] (device uint64, caller-zeroed),
@@ -277,20 +290,20 @@ int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                  const void* edge_culls, const void* prim_recs,
                                  const float* background, int32_t img_h, int32_t img_w,
                                  int32_t edges_per_segment, float* out_img, float* final_Ts,
-                                 int32_t* final_idx, unsigned long long* eval_counts,
-                                 const int32_t* tile_order, uint32_t* wave_cost,
-    hipStream_t stream);
+                                 int32_t* final_idx, void* inside_log,
+                                 unsigned long long* eval_counts, const int32_t* tile_order,
+                                 uint32_t* wave_cost, hipStream_t stream);
 int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                   const int32_t* tile_bins, const void* edges,
                                   const void* edge_culls, const void* prim_recs,
                                   const float* background, int32_t img_h, int32_t img_w,
                                   int32_t edges_per_segment, const float* final_Ts,
-                                  const int32_t* final_idx, const float* v_output,
-                                  float* v_cubics_px, float* v_colors, float* v_opacities,
-                                  float* v_inv_sigma2s, float* v_stroke_widths,
+                                  const int32_t* final_idx, const void* inside_log,
+                                  const float* v_output, float* v_cubics_px, float* v_colors,
+                                  float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
                                   float* curve_contrib_rgb, float* curve_isect_contrib,
                                   unsigned long long* eval_counts, const int32_t* tile_order,
-    hipStream_t stream);
+                                  hipStream_t stream);
 
 /* _accumulate_edge_grads_to_cubics_kernel (ops/cubic_splatting.py:2308-2396)
  * fused with the v_cubics_norm scaling (ops/cubic_splatting.py:3096-3100). */

@@ -22,6 +22,7 @@ EDGE_CULL_INTS = 4       # 16-byte edge cull record
 MAX_IMAGE_DIM = 16384
 SEG_RECORD_INTS = 8      # 32-byte segment record
 PRIM_RECORD_FLOATS = 20  # 80-byte primitive record
+INSIDE_LOG_INTS = 4      # 16-byte inside-bit record per (list entry, wave)
 EDGE_AUX_INTS = 4        # 16-byte (segment, t0, t1) record of the adaptive flattening
 
 _P = ctypes.c_void_p
@@ -50,14 +51,14 @@ _SIGNATURES = {
     "cs_bin_finish": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P,
                                      _P, _P, _P, _I64, _P]),
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
-                                            _P, _P, _P, _P]),
+                                            _P, _P, _P, _P, _P]),
     "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P,
-                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_rasterize_forward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
-                                                    _P, _P, _P, _P, _P, _P, _P]),
+                                                    _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_rasterize_backward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
                                                      _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                                     _P, _P, _P, _P]),
+                                                     _P, _P, _P, _P, _P]),
     "cs_raster_tile_order": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
     "cs_accumulate_edge_grads": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P]),
     "cs_de_casteljau_max_edges_per_segment": (_I32, [_I32]),
@@ -73,7 +74,7 @@ _SIGNATURES = {
     "cs_cubic_split_half": (ctypes.c_int, [_P, _I32, _P, _P, _P]),
     "cs_rasterize_backward_de_casteljau": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32,
                                                           _I32, _P, _P, _P, _P, _P, _P, _P, _P,
-                                                          _P, _P, _P, _P, _P]),
+                                                          _P, _P, _P, _P, _P, _P]),
     "cs_accumulate_edge_grads_csr": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
                                                     _P]),
     "cs_backward_finalize": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P]),

@@ -273,15 +273,19 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
         const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2, mu12 = mu1 * mu2;
         const float n1 = 2.0f * mu12 + c1, d1 = mu1_sq + mu2_sq + c1;
         const float n2 = 2.0f * s12 + c2, d2 = s1 + s2 + c2;
-        const float l = n1 / d1, cs_ = n2 / d2;
+        // The hardware reciprocal (within 1 ulp): d1 >= c1 and d2 >= c2 up to
+        // rounding, so both are positive normals; the loss and its gradient
+        // are compared to float64 at 1e-5 / 1e-4, far above this rounding.
+        const float r1 = __builtin_amdgcn_rcpf(d1), r2 = __builtin_amdgcn_rcpf(d2);
+        const float l = n1 * r1, cs_ = n2 * r2;
         acc += l * cs_;
         if (abc) {
-            const float dl = 2.0f * (mu2 - l * mu1) / d1;
-            const float dcs = 2.0f * (mu1 * cs_ - mu2) / d2;
+            const float dl = 2.0f * (mu2 - l * mu1) * r1;
+            const float dcs = 2.0f * (mu1 * cs_ - mu2) * r2;
             const size_t oi = (size_t)c * plane + (size_t)oy * ld + ox;
             abc[oi] = cs_ * dl + l * dcs;
-            abc[stride + oi] = -l * cs_ / d2;
-            abc[2 * stride + oi] = 2.0f * l / d2;
+            abc[stride + oi] = -l * cs_ * r2;
+            abc[2 * stride + oi] = 2.0f * l * r2;
         }
     }
     const float bs = block_sum(acc, sh);

@@ -167,7 +167,7 @@ __device__ __forceinline__ void row_cross_term(const EdgeRec& E, float py, Geom&
 //   far, spans a row, flagged, right     row-span crossing term only;
 //   far, spans a row, flagged, left      nothing (its crossing term is 0);
 //   far, spans a row, not flagged        exact crossing term.
-template <int MODE, bool BEST, bool COUNT>
+template <int MODE, bool BEST, bool COUNT, bool CROSS>
 __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const WaveRect& W,
                                                cptr<EdgeRec> edges, float px,
                                                const float (&py)[kPix], Geom (&G)[kPix],
@@ -175,13 +175,13 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
     const bool in = c + (int)(threadIdx.x & (kWave - 1)) < e1;
     const bool dn = in && span_hits(packed_lo(q.x), packed_span(q.x), W.r1) &&
                     span_hits(packed_lo(q.z), packed_span(q.z), W.c1);
-    const bool cb = MODE == 0 && in && span_hits(packed_lo(q.y), packed_span(q.y), W.r1);
+    const bool cb = CROSS && in && span_hits(packed_lo(q.y), packed_span(q.y), W.r1);
     const bool far_exact = cb && !dn && (q.w & kCullFarCrossExact);
     const uint64_t mdn = __ballot(dn);
-    const uint64_t mcb = MODE == 0 ? (uint64_t)__ballot(cb) : 0ull;
-    const uint64_t mfar = MODE == 0 ? (uint64_t)__ballot(far_exact) : 0ull;
+    const uint64_t mcb = CROSS ? (uint64_t)__ballot(cb) : 0ull;
+    const uint64_t mfar = CROSS ? (uint64_t)__ballot(far_exact) : 0ull;
     const uint64_t mright =
-        MODE == 0 ? (uint64_t)__ballot(far_exact && packed_lo(q.z) > W.c1) : 0ull;
+        CROSS ? (uint64_t)__ballot(far_exact && packed_lo(q.z) > W.c1) : 0ull;
     const uint64_t mcross = mcb & ~mfar;  // exact crossing terms
     if constexpr (COUNT) {
         n.dist += (uint64_t)__builtin_popcountll(mdn) * npix;
@@ -196,7 +196,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
             const int k = (int)__builtin_ctzll(todo);
             const EdgeRec E = load_edge(ec, k);
             const float wx = px - E.x0;
-            const bool cross = MODE == 0 && ((mcross >> k) & 1);
+            const bool cross = CROSS && ((mcross >> k) & 1);
 #pragma unroll
             for (int p = 0; p < kPix; ++p) {
                 const float wy = py[p] - E.y0;
@@ -224,7 +224,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
             for (int p = 0; p < kPix; ++p) dist_term<false>(E, 0, wx, py[p] - E.y0, G[p]);
         }
     }
-    if constexpr (MODE == 0) {
+    if constexpr (CROSS) {
         for (uint64_t todo = mcross & ~mdn; todo; todo &= todo - 1) {
             const EdgeRec E = load_edge(ec, (int)__builtin_ctzll(todo));
             const float wx = px - E.x0;
@@ -245,7 +245,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
 // and crossing terms can matter.  The wave then visits only those edges, in
 // ascending index order (so the best edge is the first strict minimum, as in
 // the reference), loading each one's geometry through the scalar cache.
-template <int MODE, bool BEST, bool COUNT>
+template <int MODE, bool BEST, bool COUNT, bool CROSS>
 __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& W,
                                               const EdgeCull* __restrict__ culls,
                                               cptr<EdgeRec> edges, float px,
@@ -262,10 +262,10 @@ __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect&
     }
     // The first chunk's words were loaded ahead by the caller.
     const int c0 = pr.e0, e1 = pr.e1;
-    chunk_geometry<MODE, BEST, COUNT>(first, c0, e1, W, edges, px, py, G, n, npix);
+    chunk_geometry<MODE, BEST, COUNT, CROSS>(first, c0, e1, W, edges, px, py, G, n, npix);
     for (int c = c0 + kWave; c < e1; c += kWave)
-        chunk_geometry<MODE, BEST, COUNT>(load_culls(culls, c, e1), c, e1, W, edges, px, py, G,
-                                          n, npix);
+        chunk_geometry<MODE, BEST, COUNT, CROSS>(load_culls(culls, c, e1), c, e1, W, edges, px,
+                                                 py, G, n, npix);
 }
 
 struct Cov {
@@ -377,7 +377,8 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, const int32_t* __restrict__ tile_order,
     uint32_t* __restrict__ wave_cost, float* __restrict__ out, float* __restrict__ final_T,
-    int32_t* __restrict__ final_idx, unsigned long long* __restrict__ counts) {
+    int32_t* __restrict__ final_idx, uint4* __restrict__ inside_log,
+    unsigned long long* __restrict__ counts) {
     const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
     const int tile = block_tile(tile_order, ntiles);
     const int tty = tile / tbx, ttx = tile - tty * tbx;
@@ -432,7 +433,17 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
             n.entries += 1;
         }
         Geom G[kPix];
-        prim_geometry<MODE, false, COUNT>(pr, W, culls, edges, L.px, L.py, q, G, n, npix);
+        prim_geometry<MODE, false, COUNT, MODE == 0>(pr, W, culls, edges, L.px, L.py, q, G, n,
+                                                     npix);
+        if constexpr (MODE == 0) {
+            // The wave's inside bits of this entry, for the backward.
+            const uint64_t in0 = __ballot(inside_of<MODE>(pr, G[0]));
+            const uint64_t in1 = __ballot(inside_of<MODE>(pr, G[kPix - 1]));
+            if (inside_log && (threadIdx.x & (kWave - 1)) == 0)
+                inside_log[2 * (size_t)g + wv] =
+                    make_uint4((uint32_t)in0, (uint32_t)(in0 >> 32), (uint32_t)in1,
+                               (uint32_t)(in1 >> 32));
+        }
         if constexpr (COUNT) {
             bool ex[kPix];
 #pragma unroll
@@ -514,12 +525,13 @@ __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
 // its leaf interval [t0, t1] are read from its aux record (the CSR weights of
 // cubic_splatting.py:2432-2485) instead of being derived from its index.
 template <int MODE, bool COUNT, bool ADAPTIVE>
-__global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
+__global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(6))) void k_raster_bwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, const int32_t* __restrict__ tile_order, int eps, uint32_t eps_magic,
-    const EdgeAux* __restrict__ edge_aux, const float* __restrict__ final_T,
+    const EdgeAux* __restrict__ edge_aux, const uint4* __restrict__ inside_log_g,
+    const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
@@ -534,6 +546,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
     const cptr<int32_t> prim_ids = as_const(prim_ids_g);
     const cptr<PrimRec> prims = as_const(prims_g);
     const cptr<EdgeRec> edges = as_const(edges_g);
+    const cptr<uint4> inside_log = as_const(inside_log_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
     const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
     float T[kPix], T_final[kPix], v0[kPix], v1[kPix], v2[kPix], bg_dot[kPix];
@@ -594,7 +607,15 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_bwd(
             n.entries += 1;
         }
         Geom G[kPix];
-        prim_geometry<MODE, true, COUNT>(pr, W, culls, edges, L.px, L.py, q, G, n, npix);
+        prim_geometry<MODE, true, COUNT, false>(pr, W, culls, edges, L.px, L.py, q, G, n, npix);
+        if constexpr (MODE == 0) {
+            // Inside bits from the forward's log (its winding test of the same
+            // pixel and entry), instead of the crossing terms.
+            const uint4 lg = inside_log[2 * (size_t)g + wv];
+            const uint64_t in0 = ((uint64_t)lg.y << 32) | lg.x, in1 = ((uint64_t)lg.w << 32) | lg.z;
+            G[0].winding = (int)((in0 >> lane) & 1u);
+            G[kPix - 1].winding = (int)((in1 >> lane) & 1u);
+        }
         if constexpr (COUNT) {
             bool ex[kPix];
 #pragma unroll
@@ -964,6 +985,7 @@ struct RasterArgs {
     float* out;
     float* final_T;
     int32_t* final_idx;
+    uint4* inside_log;  // written by the forward, read by the backward (fill)
     // backward inputs / outputs
     const float* fT;
     const int32_t* fidx;
@@ -982,7 +1004,8 @@ template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
     hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.nt), dim3(kRasterThreads), 0,
                        a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.order, a.wave_cost, a.out, a.final_T, a.final_idx, a.counts);
+                       a.nt, a.order, a.wave_cost, a.out, a.final_T, a.final_idx, a.inside_log,
+                       a.counts);
 }
 
 template <int MODE, bool COUNT, bool ADAPTIVE>
@@ -992,7 +1015,7 @@ static void launch_bwd3(const RasterArgs& a) {
         a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
     hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT, ADAPTIVE>), dim3(a.nt), dim3(kRasterThreads),
                        0, a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.order, a.eps, magic, a.aux, a.fT, a.fidx, a.v_out,
+                       a.nt, a.order, a.eps, magic, a.aux, a.inside_log, a.fT, a.fidx, a.v_out,
                        a.v_cub, a.v_col,
                        a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.counts);
 }
@@ -1041,8 +1064,9 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                              const void* prim_recs, const float* background, int32_t img_h,
                              int32_t img_w, int32_t edges_per_segment, float* out_img,
                              float* final_Ts, int32_t* final_idx,
-                             unsigned long long* eval_counts, const int32_t* tile_order,
-                             uint32_t* wave_cost, hipStream_t stream) {
+                             void* inside_log, unsigned long long* eval_counts,
+                             const int32_t* tile_order, uint32_t* wave_cost,
+                             hipStream_t stream) {
     // The primitive records hold each primitive's edge range, so the forward
     // does not use edges_per_segment (0 for adaptively flattened records).
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 0 ||
@@ -1053,6 +1077,7 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
     a.out = out_img;
     a.final_T = final_Ts;
     a.final_idx = final_idx;
+    a.inside_log = reinterpret_cast<uint4*>(inside_log);
     a.counts = eval_counts;
     a.order = tile_order;
     a.wave_cost = wave_cost;
@@ -1067,11 +1092,12 @@ extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted
                                     const float* background,
                                     int32_t img_h, int32_t img_w, int32_t edges_per_segment,
                                     float* out_img, float* final_Ts,
-                                    int32_t* final_idx, const int32_t* tile_order,
-                                    uint32_t* wave_cost, hipStream_t stream) {
+                                    int32_t* final_idx, void* inside_log,
+                                    const int32_t* tile_order, uint32_t* wave_cost,
+                                    hipStream_t stream) {
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, edges_per_segment, out_img, final_Ts,
-                             final_idx, nullptr, tile_order, wave_cost, stream);
+                             final_idx, inside_log, nullptr, tile_order, wave_cost, stream);
 }
 
 extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
@@ -1080,13 +1106,13 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
                                             const float* background, int32_t img_h,
                                             int32_t img_w, int32_t edges_per_segment,
                                             float* out_img, float* final_Ts, int32_t* final_idx,
-                                            unsigned long long* eval_counts,
+                                            void* inside_log, unsigned long long* eval_counts,
                                             const int32_t* tile_order, uint32_t* wave_cost,
                                             hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, edges_per_segment, out_img, final_Ts,
-                             final_idx, eval_counts, tile_order, wave_cost, stream);
+                             final_idx, inside_log, eval_counts, tile_order, wave_cost, stream);
 }
 
 static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
@@ -1098,14 +1124,15 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               float* v_cubics_px, float* v_colors, float* v_opacities,
                               float* v_inv_sigma2s, float* v_stroke_widths,
                               float* curve_contrib_rgb, float* curve_isect_contrib,
-                              const void* edge_aux, unsigned long long* eval_counts,
-                              const int32_t* tile_order,
+                              const void* edge_aux, const void* inside_log,
+                              unsigned long long* eval_counts, const int32_t* tile_order,
                               hipStream_t stream) {
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 ||
         (edge_aux == nullptr && edges_per_segment < 1) || img_h > kMaxImageDim ||
         img_w > kMaxImageDim)
         return CS_ERR_ARGS;
     if (mode == 1 && v_stroke_widths == nullptr) return CS_ERR_ARGS;
+    if (mode == 0 && inside_log == nullptr) return CS_ERR_ARGS;
     RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                                background, img_h, img_w, edges_per_segment, stream);
     a.fT = final_Ts;
@@ -1120,6 +1147,7 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
     a.c_isect = curve_isect_contrib;
     a.aux = reinterpret_cast<const EdgeAux*>(edge_aux);
     if (edge_aux) a.eps = 0;
+    a.inside_log = reinterpret_cast<uint4*>(const_cast<void*>(inside_log));
     a.counts = eval_counts;
     a.order = tile_order;
     if (eval_counts) launch_bwd_mode<true>(a);
@@ -1133,7 +1161,8 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                                      const float* background,
                                      int32_t img_h, int32_t img_w,
                                      int32_t edges_per_segment, const float* final_Ts,
-                                     const int32_t* final_idx, const float* v_output,
+                                     const int32_t* final_idx, const void* inside_log,
+                                     const float* v_output,
                                      float* v_cubics_px, float* v_colors, float* v_opacities,
                                      float* v_inv_sigma2s, float* v_stroke_widths,
                                      float* curve_contrib_rgb, float* curve_isect_contrib,
@@ -1143,31 +1172,30 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              nullptr, tile_order, stream);
+                              inside_log, nullptr, tile_order, stream);
 }
 
 extern "C" int cs_rasterize_backward_de_casteljau(
     int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
     const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
     int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
-    const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
-    float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
-    float* curve_isect_contrib, const int32_t* tile_order,
-    hipStream_t stream) {
+    const void* inside_log, const float* v_output, float* v_cubics_px, float* v_colors,
+    float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
+    float* curve_isect_contrib, const int32_t* tile_order, hipStream_t stream) {
     if (!edge_aux) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, 0, final_Ts, final_idx, v_output,
                               v_cubics_px, v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
-                              curve_contrib_rgb, curve_isect_contrib, edge_aux, nullptr,
-                              tile_order, stream);
+                              curve_contrib_rgb, curve_isect_contrib, edge_aux, inside_log,
+                              nullptr, tile_order, stream);
 }
 
 extern "C" int cs_rasterize_backward_counted(
     int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
     const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
     int32_t img_w, int32_t edges_per_segment, const float* final_Ts, const int32_t* final_idx,
-    const float* v_output, float* v_cubics_px, float* v_colors, float* v_opacities,
-    float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
+    const void* inside_log, const float* v_output, float* v_cubics_px, float* v_colors,
+    float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
     float* curve_isect_contrib, unsigned long long* eval_counts, const int32_t* tile_order,
     hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
@@ -1175,7 +1203,7 @@ extern "C" int cs_rasterize_backward_counted(
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              eval_counts, tile_order, stream);
+                              inside_log, eval_counts, tile_order, stream);
 }
 
 extern "C" int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,

@@ -35,23 +35,32 @@ from contextlib import contextmanager, nullcontext
 
 
 class EventTimer:
-    """Profile-context factory that times the watched labels with HIP events."""
+    """Profile-context factory that times the watched labels with HIP events.
+    Event pairs are created up front (`reserve` per label) and reused, so a
+    timed launch costs two event records on the host and nothing else."""
 
-    def __init__(self, labels):
+    _NULL = nullcontext()
+
+    def __init__(self, labels, reserve=128):
+        import torch
         self.labels = set(labels)
         self.pairs = {k: [] for k in self.labels}
+        self._pool = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                      for _ in range(reserve * len(self.labels))]
         self.enabled = True
 
     def __call__(self, label):
         if not self.enabled or label not in self.labels:
-            return nullcontext()
+            return self._NULL
         return self._bracket(label)
 
     @contextmanager
     def _bracket(self, label):
         import torch
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
+        if self._pool:
+            a, b = self._pool.pop()
+        else:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         yield
         b.record()

@@ -157,6 +157,8 @@ class Binned:
         self.primitive_ids_sorted: Optional[torch.Tensor] = None
         # Heavy-first tile order from this forward's raster (for the backward).
         self.tile_order: Optional[torch.Tensor] = None
+        # The forward's inside bits per (list entry, wave) (fill; for the backward).
+        self.inside_log: Optional[torch.Tensor] = None
         self.grad_accum_clean = True
         # Set while the intersection count has not been read on the host yet
         # (bin_primitives with a capacity hint); resolve_binned() settles it.
@@ -384,9 +386,14 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
     key = _order_key(dev, ntiles)
     prev = _TILE_ORDERS.get(key)
     st = N.stream(dev)
+    # Inside bits of every (list entry, wave) for the backward (fill only).
+    cap = int(b.primitive_ids_sorted.numel())
+    b.inside_log = (torch.empty((2 * max(cap, 1), N.INSIDE_LOG_INTS), dtype=torch.int32,
+                                device=dev) if b.mode == MODE_FILL else None)
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
-            b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx))
+            b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx),
+            N.ptr(b.inside_log))
     cost = b.ptr("wave_cost")
     if eval_counts is not None:
         N.call("cs_rasterize_forward_counted", *args, N.ptr(_counts_buffer(eval_counts)),
@@ -438,13 +445,16 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
             N.call("cs_rasterize_backward_de_casteljau", b.mode, N.ptr(b.primitive_ids_sorted),
                    b.ptr("tile_bins"), b.ptr("edges"), b.ptr("edge_culls"), b.ptr("prim_recs"),
                    N.ptr(background), b.img_h, b.img_w, b.ptr("edge_aux"), N.ptr(final_T),
-                   N.ptr(final_idx), N.ptr(v_output), N.ptr(v_px), N.ptr(v_colors),
+                   N.ptr(final_idx), N.ptr(b.inside_log), N.ptr(v_output), N.ptr(v_px), N.ptr(v_colors),
                    N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
                    N.ptr(curve_isect_contrib), N.ptr(b.tile_order), N.stream(dev))
         return v_px, v_colors, v_opac, v_is2, v_sw
+    if b.mode == MODE_FILL and b.inside_log is None:
+        raise RuntimeError("the fill backward needs the inside log of a forward of this binning")
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
-            b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(v_output), N.ptr(v_px),
+            b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(b.inside_log),
+            N.ptr(v_output), N.ptr(v_px),
             N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
             N.ptr(curve_isect_contrib))
     if eval_counts is not None:
