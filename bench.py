@@ -75,10 +75,11 @@ def render(sc, cub, col):
 
 def loss_fn(img, target):
     """clamp(0, 1) -> NCHW -> MSE + 0.2 (1 - SSIM), with the fused kernels
-    (the same values as manbo.mse_loss_tilelang + manbo.ssim on
+    that read the [H, W, 3] image in place (the same values as
+    manbo.mse_loss_tilelang + manbo.ssim on
     img.clamp(0, 1).permute(2, 0, 1).unsqueeze(0))."""
     from repo_amd import fused
-    loss, _ = fused.mse_ssim_loss(fused.clamp_to_nchw(img), target, SSIM_WEIGHT)
+    loss, _ = fused.clamp_mse_ssim_loss(img, target, SSIM_WEIGHT)
     return loss
 
 

@@ -394,9 +394,11 @@ int cs_clamp_hwc_to_nchw_backward(const float* img, const float* grad, int32_t h
                                   float lo, float hi, float* grad_img, hipStream_t stream);
 
 /* loss = MSE(x, y) + ssim_weight * (1 - SSIM(x, y)) in one call (the MSE of
- * metric.py:102-212 and the SSIM of metric.py:215-273 as cs_mse_forward and
- * cs_ssim compute them): out[0] = loss, out[1] = MSE, out[2] = SSIM (device);
- * `partials` holds cs_mse_ssim_partials_elems floats; abc as for cs_ssim.
+ * metric.py:102-212 and the SSIM of metric.py:215-273; the SSIM kernel also
+ * sums the squared differences, per tile, so the MSE equals cs_mse_forward's up
+ * to fp32 summation order): out[0] = loss, out[1] = MSE, out[2] = SSIM
+ * (device); `partials` holds cs_mse_ssim_partials_elems floats; abc as for
+ * cs_ssim.
  * The backward writes grad_x = g (2 (x - y) / n - ssim_weight dSSIM/dx) in one
  * pass, g = *grad_loss. */
 size_t cs_mse_ssim_partials_elems(int32_t nc, int32_t h, int32_t w);
@@ -406,6 +408,22 @@ int cs_mse_ssim_loss(const float* x, const float* y, int32_t nc, int32_t h, int3
 int cs_mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                          const float* win1d, int32_t win, const float* abc, float ssim_weight,
                          const float* grad_loss, float* grad_x, hipStream_t stream);
+
+/* The same loss on the renderer's [h, w, 3] image, with the caller's
+ * clamp(0, 1).permute(2, 0, 1) glue (gaussian_trace/render.py:1309-1310)
+ * folded in: the forward writes x = clamp(img, lo, hi) as [3, h, w] into the
+ * caller's buffer x and computes the loss on it; the backward reads img
+ * itself and writes grad_img [h, w, 3] directly, zero where img lies outside
+ * [lo, hi] (no gradient pass through the glue).  y is the [3, h, w] target;
+ * partials / abc as for cs_mse_ssim_loss with nc = 3. */
+int cs_clamp_mse_ssim_loss(const float* img, const float* y, int32_t h, int32_t w, float lo,
+                           float hi, const float* win1d, int32_t win, float c1, float c2,
+                           float ssim_weight, float* x, float* partials, float* out, float* abc,
+                           hipStream_t stream);
+int cs_clamp_mse_ssim_backward(const float* img, const float* y, int32_t h, int32_t w, float lo,
+                               float hi, const float* win1d, int32_t win, const float* abc,
+                               float ssim_weight, const float* grad_loss, float* grad_img,
+                               hipStream_t stream);
 
 /* ---------------- optimizer ---------------- */
 

@@ -169,25 +169,50 @@ __device__ __forceinline__ void load_strip(const float* __restrict__ plane, int 
     }
 }
 
+// Tile (channel, row, column) of workgroup b over nt = ntx * nty * nc tiles,
+// XCD-aware.  With an HWC image the channel is the fastest index, so the three
+// channels of one spatial tile run back to back on one XCD and share the L2
+// lines of the interleaved image and gradient.
+template <bool HWC>
+__device__ __forceinline__ void ssim_tile(int b, int ntx, int nty, int nc, int& c, int& ty,
+                                          int& tx) {
+    const int tile = xcd_tile(b, ntx * nty * nc);
+    int sp;
+    if (HWC) {
+        c = tile % nc;
+        sp = tile / nc;
+    } else {
+        c = tile / (ntx * nty);
+        sp = tile - c * ntx * nty;
+    }
+    ty = sp / ntx;
+    tx = sp - ty * ntx;
+}
+
 // Row stride of the per-pixel maps A, B, C (rows padded to 16 bytes).
 __host__ __device__ __forceinline__ int abc_ld(int ow) { return (ow + 3) & ~3; }
 
+// mse_partials (optional): each workgroup also sums (x - y)^2 over its
+// anchor inputs -- rows [oy0, oy0 + 48) and columns [ox0, ox0 + 32), extended
+// to the image's last row / column in the last tile row / column -- so every
+// input is counted once and no separate MSE pass is needed.
 template <int WIN>
 __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
                                                  const float* __restrict__ y, int h, int w,
                                                  int oh, int ow,
                                                  const float* __restrict__ win1d, float c1,
                                                  float c2, float* __restrict__ partials,
-                                                 float* __restrict__ abc, int nc) {
+                                                 float* __restrict__ abc, int nc,
+                                                 float* __restrict__ mse_partials) {
     using TT = SsimTile<WIN>;
     constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
     __shared__ float hm[5][IT][HP];
     __shared__ float sh[4];
     // 1D grid over (channel, tile row, tile column), XCD-aware.
     const int ntx = (ow + kSsimTW - 1) / kSsimTW, nty = (oh + kSsimTH - 1) / kSsimTH;
-    const int tile = xcd_tile(blockIdx.x, ntx * nty * nc);
-    const int c = tile / (ntx * nty);
-    const int ty = (tile - c * ntx * nty) / ntx, tx = tile - c * ntx * nty - ty * ntx;
+    int c, ty, tx;
+    ssim_tile<false>(blockIdx.x, ntx, nty, nc, c, ty, tx);
+    const int tile = (c * nty + ty) * ntx + tx;
     const int ox0 = tx * kSsimTW, oy0 = ty * kSsimTH;
     const float* xc = x + (size_t)c * h * w;
     const float* yc = y + (size_t)c * h * w;
@@ -202,12 +227,25 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
     const float kx = xc[kpix], ky = yc[kpix];
     const bool vec_ok = ((w & 3) == 0) &&
                         ((reinterpret_cast<uintptr_t>(xc) | reinterpret_cast<uintptr_t>(yc)) & 15) == 0;
+    // MSE anchor: rows [0, mse_rows) of the tile's input rows; columns
+    // [q0, q0 + 8) of each strip, the last strip of the last tile column up
+    // to the end of its inputs (zeros past the image add nothing).
+    const int mse_rows = ty == nty - 1 ? IT : kSsimTH;
+    float mse = 0.0f;
     // Horizontal: thread -> (row, 8-wide strip).
     for (int item = threadIdx.x; item < IT * (kSsimTW / kHStrip); item += 256) {
         const int r = item >> 2, q0 = (item & 3) * kHStrip;
         float a[NIN], b[NIN];
         load_strip<NIN, 0>(xc, h, w, w, oy0 + r, ox0 + q0, vec_ok, a);
         load_strip<NIN, 0>(yc, h, w, w, oy0 + r, ox0 + q0, vec_ok, b);
+        if (mse_partials && r < mse_rows) {
+            const int cols = (tx == ntx - 1 && q0 + kHStrip == kSsimTW) ? NIN : kHStrip;
+#pragma unroll
+            for (int k = 0; k < NIN; ++k) {
+                const float d = a[k] - b[k];
+                mse = k < cols ? __builtin_fmaf(d, d, mse) : mse;
+            }
+        }
         float aa[NIN], bb[NIN], ab[NIN];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
@@ -290,28 +328,35 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
     }
     const float bs = block_sum(acc, sh);
     if (threadIdx.x == 0) partials[tile] = bs;
+    if (mse_partials) {
+        const float ms = block_sum(mse, sh);
+        if (threadIdx.x == 0) mse_partials[tile] = ms;
+    }
 }
 
 // grad_x[p] = scale * sum over map pixels o of the window w(p - o) times
 // (A[o] + 2 x[p] B[o] + y[p] C[o]): a full (transposed) correlation of the
 // three maps, blocked like the forward (horizontal strips read the maps from
 // global memory, vertical strips from LDS).
-template <int WIN>
+// HWC: x is the [h, w, 3] image the forward read as clamp(x, lo, hi) and gx
+// the [h, w, 3] gradient with respect to it: zero where x lies outside
+// [lo, hi] (the clamp's gradient as torch defines it).
+template <int WIN, bool HWC>
 __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
                                                  const float* __restrict__ y, int h, int w,
                                                  int oh, int ow,
                                                  const float* __restrict__ win1d,
                                                  const float* __restrict__ abc,
                                                  const float* __restrict__ grad_out, float ssim_coef,
-                                                 float mse_coef, int nc, float* __restrict__ gx) {
+                                                 float mse_coef, int nc, float lo, float hi,
+                                                 float* __restrict__ gx) {
     using TT = SsimTile<WIN>;
     constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
     __shared__ float hs[3][IT][HP];
     // 1D grid over (channel, tile row, tile column), XCD-aware.
     const int ntx = (w + kSsimTW - 1) / kSsimTW, nty = (h + kSsimTH - 1) / kSsimTH;
-    const int tile = xcd_tile(blockIdx.x, ntx * nty * nc);
-    const int c = tile / (ntx * nty);
-    const int ty = (tile - c * ntx * nty) / ntx, tx = tile - c * ntx * nty - ty * ntx;
+    int c, ty, tx;
+    ssim_tile<HWC>(blockIdx.x, ntx, nty, nc, c, ty, tx);
     const int px0 = tx * kSsimTW, py0 = ty * kSsimTH;
     const size_t ld = abc_ld(ow);
     const size_t plane = (size_t)oh * ld;
@@ -364,19 +409,19 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
     // the MSE gradient is fused in].
     const float go = *grad_out;
     const float scale = go * ssim_coef, mscale = go * mse_coef;
-    const float* xc = x + (size_t)c * h * w;
     const float* yc = y + (size_t)c * h * w;
-    float* gc = gx + (size_t)c * h * w;
     const int px = px0 + q;
 #pragma unroll
     for (int o = 0; o < kVStrip; ++o) {
         const int py = py0 + r0 + o;
         if (py >= h || px >= w) continue;
         const size_t pi = (size_t)py * w + px;
-        const float xv = xc[pi], yv = yc[pi];
+        const float xr = HWC ? x[3 * pi + c] : x[(size_t)c * h * w + pi];
+        const float xv = HWC ? fminf(fmaxf(xr, lo), hi) : xr, yv = yc[pi];
         float gv = scale * (gsum[0][o] + 2.0f * xv * gsum[1][o] + yv * gsum[2][o]);
         if (mse_coef != 0.0f) gv = __builtin_fmaf(mscale, xv - yv, gv);
-        gc[pi] = gv;
+        if (HWC) gx[3 * pi + c] = (xr >= lo) & (xr <= hi) ? gv : 0.0f;
+        else gx[(size_t)c * h * w + pi] = gv;
     }
 }
 
@@ -482,12 +527,13 @@ static bool ssim_args_ok(int32_t nc, int32_t h, int32_t w, int32_t win) {
 // SSIM partial sums (one per output tile) and, when abc != null, the maps.
 static int launch_ssim_fwd(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                            const float* win1d, int32_t win, float c1, float c2,
-                           float* partials, float* abc, hipStream_t stream, int* nblk) {
+                           float* partials, float* abc, hipStream_t stream, int* nblk,
+                           float* mse_partials = nullptr) {
     const int oh = h - win + 1, ow = w - win + 1;
     const dim3 grid(((ow + kSsimTW - 1) / kSsimTW) * ((oh + kSsimTH - 1) / kSsimTH) * nc);
 #define CS_SSIM_FWD(W_)                                                                       \
     hipLaunchKernelGGL(k_ssim_fwd<W_>, grid, dim3(256), 0, stream, x, y, h, w, oh, ow, win1d, \
-                       c1, c2, partials, abc, nc)
+                       c1, c2, partials, abc, nc, mse_partials)
     switch (win) {
         CS_SSIM_DISPATCH(1, CS_SSIM_FWD)
         CS_SSIM_DISPATCH(3, CS_SSIM_FWD)
@@ -504,15 +550,16 @@ static int launch_ssim_fwd(const float* x, const float* y, int32_t nc, int32_t h
     return CS_OK;
 }
 
+template <bool HWC>
 static int launch_ssim_bwd(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                            const float* win1d, int32_t win, const float* abc,
                            const float* grad_out, float ssim_coef, float mse_coef, float* grad_x,
-                           hipStream_t stream) {
+                           hipStream_t stream, float lo = 0.0f, float hi = 1.0f) {
     const int oh = h - win + 1, ow = w - win + 1;
     const dim3 grid(((w + kSsimTW - 1) / kSsimTW) * ((h + kSsimTH - 1) / kSsimTH) * nc);
-#define CS_SSIM_BWD(W_)                                                                     \
-    hipLaunchKernelGGL(k_ssim_bwd<W_>, grid, dim3(256), 0, stream, x, y, h, w, oh, ow, win1d, \
-                       abc, grad_out, ssim_coef, mse_coef, nc, grad_x)
+#define CS_SSIM_BWD(W_)                                                                        \
+    hipLaunchKernelGGL((k_ssim_bwd<W_, HWC>), grid, dim3(256), 0, stream, x, y, h, w, oh, ow, \
+                       win1d, abc, grad_out, ssim_coef, mse_coef, nc, lo, hi, grad_x)
     switch (win) {
         CS_SSIM_DISPATCH(1, CS_SSIM_BWD)
         CS_SSIM_DISPATCH(3, CS_SSIM_BWD)
@@ -533,8 +580,8 @@ extern "C" int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, in
                        float* out, float* abc, hipStream_t stream) {
     if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
     int nblk = 0;
-    const int rc = launch_ssim_fwd(x, y, nc, h, w, win1d, win, c1, c2, partials, abc, stream,
-                                   &nblk);
+    const int rc = launch_ssim_fwd(x, y, nc, h, w, win1d, win, c1, c2, partials, abc,
+                                          stream, &nblk);
     if (rc) return rc;
     const int oh = h - win + 1, ow = w - win + 1;
     hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials, nblk,
@@ -548,49 +595,86 @@ extern "C" int cs_ssim_backward(const float* x, const float* y, int32_t nc, int3
     if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
     const int oh = h - win + 1, ow = w - win + 1;
     const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
-    const int rc = launch_ssim_bwd(x, y, nc, h, w, win1d, win, abc, grad_out, inv_cnt, 0.0f,
-                                   grad_x, stream);
+    const int rc = launch_ssim_bwd<false>(x, y, nc, h, w, win1d, win, abc, grad_out, inv_cnt,
+                                          0.0f, grad_x, stream);
     return rc ? rc : metric_status();
 }
 
 extern "C" size_t cs_mse_ssim_partials_elems(int32_t nc, int32_t h, int32_t w) {
-    return cs_mse_partials_elems((int64_t)nc * h * w) + cs_ssim_partials_elems(nc, h, w);
+    return 2 * cs_ssim_partials_elems(nc, h, w);
+}
+
+// MSE + w (1 - SSIM): the SSIM forward also sums (x - y)^2 over each tile's
+// anchor inputs (so the MSE needs no pass of its own); one workgroup then
+// combines both sets of tile partials.
+static int mse_ssim_loss(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+                         const float* win1d, int32_t win, float c1, float c2, float ssim_weight,
+                         float* partials, float* out, float* abc, hipStream_t stream) {
+    if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
+    const int64_t n = (int64_t)nc * h * w;
+    float* ssim_partials = partials;
+    float* mse_partials = partials + cs_ssim_partials_elems(nc, h, w);
+    int nblk = 0;
+    const int rc = launch_ssim_fwd(x, y, nc, h, w, win1d, win, c1, c2, ssim_partials, abc, stream,
+                                   &nblk, mse_partials);
+    if (rc) return rc;
+    const int oh = h - win + 1, ow = w - win + 1;
+    hipLaunchKernelGGL(k_mse_ssim_combine, dim3(1), dim3(kFinalThreads), 0, stream, mse_partials,
+                       nblk, ssim_partials, nblk, 1.0f / (float)n,
+                       1.0f / ((float)nc * (float)oh * (float)ow), ssim_weight, out);
+    return metric_status();
+}
+
+template <bool HWC>
+static int mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+                             float lo, float hi, const float* win1d, int32_t win,
+                             const float* abc, float ssim_weight, const float* grad_loss,
+                             float* grad_x, hipStream_t stream) {
+    if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
+    const int oh = h - win + 1, ow = w - win + 1;
+    const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
+    const float mse_coef = (float)(2.0 / ((double)nc * h * w));
+    const int rc = launch_ssim_bwd<HWC>(x, y, nc, h, w, win1d, win, abc, grad_loss,
+                                        -ssim_weight * inv_cnt, mse_coef, grad_x, stream, lo, hi);
+    return rc ? rc : metric_status();
 }
 
 extern "C" int cs_mse_ssim_loss(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                                 const float* win1d, int32_t win, float c1, float c2,
                                 float ssim_weight, float* partials, float* out, float* abc,
                                 hipStream_t stream) {
-    if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
-    const int64_t n = (int64_t)nc * h * w;
-    const int64_t nb = (n + kMseChunk - 1) / kMseChunk;
-    if (nb > 0x7fffffff) return CS_ERR_ARGS;
-    float* mse_partials = partials;
-    float* ssim_partials = partials + cs_mse_partials_elems(n);
-    hipLaunchKernelGGL(k_mse_partial, dim3((unsigned)nb), dim3(kMseThreads), 0, stream, x, y, n,
-                       mse_partials);
-    int nblk = 0;
-    const int rc = launch_ssim_fwd(x, y, nc, h, w, win1d, win, c1, c2, ssim_partials, abc,
-                                   stream, &nblk);
-    if (rc) return rc;
-    const int oh = h - win + 1, ow = w - win + 1;
-    hipLaunchKernelGGL(k_mse_ssim_combine, dim3(1), dim3(kFinalThreads), 0, stream, mse_partials,
-                       (int)nb, ssim_partials, nblk, 1.0f / (float)n,
-                       1.0f / ((float)nc * (float)oh * (float)ow), ssim_weight, out);
-    return metric_status();
+    return mse_ssim_loss(x, y, nc, h, w, win1d, win, c1, c2, ssim_weight, partials, out, abc,
+                         stream);
 }
 
 extern "C" int cs_mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h,
                                     int32_t w, const float* win1d, int32_t win, const float* abc,
                                     float ssim_weight, const float* grad_loss, float* grad_x,
                                     hipStream_t stream) {
-    if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
-    const int oh = h - win + 1, ow = w - win + 1;
-    const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
-    const float mse_coef = (float)(2.0 / ((double)nc * h * w));
-    const int rc = launch_ssim_bwd(x, y, nc, h, w, win1d, win, abc, grad_loss,
-                                   -ssim_weight * inv_cnt, mse_coef, grad_x, stream);
-    return rc ? rc : metric_status();
+    return mse_ssim_backward<false>(x, y, nc, h, w, 0.0f, 0.0f, win1d, win, abc, ssim_weight,
+                                    grad_loss, grad_x, stream);
+}
+
+extern "C" int cs_clamp_mse_ssim_loss(const float* img, const float* y, int32_t h, int32_t w,
+                                      float lo, float hi, const float* win1d, int32_t win,
+                                      float c1, float c2, float ssim_weight, float* x,
+                                      float* partials, float* out, float* abc,
+                                      hipStream_t stream) {
+    if (!ssim_args_ok(3, h, w, win) || !x) return CS_ERR_ARGS;
+    const int64_t hw = (int64_t)h * w;
+    hipLaunchKernelGGL(k_clamp_hwc_to_chw, dim3((unsigned)((hw + 255) / 256)), dim3(256), 0,
+                       stream, img, hw, lo, hi, x);
+    return mse_ssim_loss(x, y, 3, h, w, win1d, win, c1, c2, ssim_weight, partials, out, abc,
+                         stream);
+}
+
+extern "C" int cs_clamp_mse_ssim_backward(const float* img, const float* y, int32_t h, int32_t w,
+                                          float lo, float hi, const float* win1d, int32_t win,
+                                          const float* abc, float ssim_weight,
+                                          const float* grad_loss, float* grad_img,
+                                          hipStream_t stream) {
+    return mse_ssim_backward<true>(img, y, 3, h, w, lo, hi, win1d, win, abc, ssim_weight,
+                                   grad_loss, grad_img, stream);
 }
 
 extern "C" int cs_clamp_hwc_to_nchw(const float* img, int32_t h, int32_t w, float lo, float hi,

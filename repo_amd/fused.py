@@ -10,12 +10,14 @@ separate loss calls, that is several full passes over 33 MB images per step
 here each direction is one kernel:
 
 * ``clamp_to_nchw(img)``: one pass forward, one masked pass backward;
-* ``mse_ssim_loss(x, y, w)``: one call for both losses (MSE partial sums,
-  SSIM tiles, one combining workgroup) and one backward kernel that writes
-  ``g * (2 (x - y) / n - w dSSIM/dx)``.
+* ``mse_ssim_loss(x, y, w)``: one call for both losses (the SSIM tiles also
+  sum the squared differences; one combining workgroup) and one backward
+  kernel that writes ``g * (2 (x - y) / n - w dSSIM/dx)``;
+* ``clamp_mse_ssim_loss(img, y, w)``: the two above in one autograd node
+  whose backward writes the [H, W, 3] image gradient directly.
 
-Values equal the separate calls (same kernels and summation structure); the
-autograd graph is shorter.
+Values equal the separate calls up to fp32 summation order; the autograd
+graph is shorter.
 """
 from __future__ import annotations
 
@@ -99,6 +101,72 @@ class _MseSsimLoss(torch.autograd.Function):
                    ctx.win_size, N.ptr(abc), ctx.ssim_weight, N.ptr(go), N.ptr(gx),
                    N.stream(x.device))
         return gx.to(ctx.x_dtype), None, None, None, None, None, None
+
+
+class _ClampMseSsimLoss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, img, y, lo, hi, ssim_weight, win_size, win_sigma, c1, c2):
+        N.require_gpu(img, "img")
+        if img.dim() != 3 or img.shape[2] != 3:
+            raise ValueError(f"img must be [H, W, 3], got {tuple(img.shape)}")
+        x32 = _as_f32(img, "img")
+        h, w = int(x32.shape[0]), int(x32.shape[1])
+        if tuple(y.shape) not in ((1, 3, h, w), (3, h, w)):
+            raise ValueError(f"target must be [1, 3, {h}, {w}], got {tuple(y.shape)}")
+        y32 = _as_f32(y, "target")
+        dev = x32.device
+        g = gaussian_window_1d(win_size, win_sigma, dev)
+        partials = torch.empty((int(N.lib().cs_mse_ssim_partials_elems(3, h, w)),),
+                               dtype=torch.float32, device=dev)
+        out = torch.empty((3,), dtype=torch.float32, device=dev)
+        abc = (torch.empty((int(N.lib().cs_ssim_abc_elems(3, h, w, int(win_size))),),
+                           dtype=torch.float32, device=dev)
+               if ctx.needs_input_grad[0] else None)
+        x = torch.empty((3, h, w), dtype=torch.float32, device=dev)   # clamp(img) as NCHW
+        with N.prof("loss.clamp_mse_ssim"):
+            N.call("cs_clamp_mse_ssim_loss", N.ptr(x32), N.ptr(y32), h, w, float(lo), float(hi),
+                   N.ptr(g), int(win_size), float(c1), float(c2), float(ssim_weight), N.ptr(x),
+                   N.ptr(partials), N.ptr(out), N.ptr(abc), N.stream(dev))
+        ctx.save_for_backward(x32, y32, abc if abc is not None else torch.empty(0), g)
+        ctx.lo, ctx.hi = float(lo), float(hi)
+        ctx.win_size = int(win_size)
+        ctx.ssim_weight = float(ssim_weight)
+        ctx.x_dtype = img.dtype
+        parts = out[1:]
+        ctx.mark_non_differentiable(parts)
+        return out[0], parts
+
+    @staticmethod
+    def backward(ctx, grad_loss, _grad_parts):
+        x, y, abc, g = ctx.saved_tensors
+        if not ctx.needs_input_grad[0]:
+            return (None,) * 9
+        h, w = int(x.shape[0]), int(x.shape[1])
+        gi = torch.empty_like(x)
+        go = grad_loss.detach().to(torch.float32).contiguous()
+        with N.prof("loss.clamp_mse_ssim_bwd"):
+            N.call("cs_clamp_mse_ssim_backward", N.ptr(x), N.ptr(y), h, w, ctx.lo, ctx.hi,
+                   N.ptr(g), ctx.win_size, N.ptr(abc), ctx.ssim_weight, N.ptr(go), N.ptr(gi),
+                   N.stream(x.device))
+        return gi.to(ctx.x_dtype), None, None, None, None, None, None, None, None
+
+
+def clamp_mse_ssim_loss(img, y, ssim_weight: float = 0.2, *, lo: float = 0.0, hi: float = 1.0,
+                        win_size: int = 11, win_sigma: float = 1.5, data_range: float = 1.0,
+                        k1: float = 0.01, k2: float = 0.03):
+    """``mse_ssim_loss(img.clamp(lo, hi).permute(2, 0, 1).unsqueeze(0), y, ssim_weight)``
+    from the renderer's [H, W, 3] image: one clamp/layout pass forward (the
+    SSIM forward also sums the MSE), and a backward that reads the image
+    itself and writes the [H, W, 3] gradient with the clamp's mask, so the
+    glue has no gradient pass.  Returns (loss, [MSE, SSIM])."""
+    if win_size <= 0 or win_size % 2 == 0:
+        raise ValueError("win_size must be odd")
+    if data_range <= 0.0:
+        raise ValueError("data_range must be > 0")
+    c1 = (k1 * data_range) ** 2
+    c2 = (k2 * data_range) ** 2
+    return _ClampMseSsimLoss.apply(img, y, float(lo), float(hi), float(ssim_weight),
+                                   int(win_size), float(win_sigma), c1, c2)
 
 
 def mse_ssim_loss(x, y, ssim_weight: float = 0.2, *, win_size: int = 11, win_sigma: float = 1.5,

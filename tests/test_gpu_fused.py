@@ -68,21 +68,59 @@ def test_fused_step_gradients_match_unfused():
     target = torch.rand((1, 3, sc.img_h, sc.img_w), generator=torch.Generator().manual_seed(4))
     target = target.to(dev)
     grads = []
-    for use_fused in (True, False):
+    for use_fused in ("hwc", True, False):
         cub = sc.cubics_norm.to(dev).requires_grad_(True)
         col = sc.colors.to(dev).requires_grad_(True)
         img = manbo.ops.render_cubic_fill_splat_tilelang(
             cub, sc.seg_offsets.to(dev), col, sc.opacities.to(dev), sc.depths.to(dev), sc.img_h,
             sc.img_w, 16, 16, sc.background.to(dev), aa_widths=sc.aa_widths.to(dev),
             distance_samples=sc.S)
-        if use_fused:
+        if use_fused == "hwc":
+            loss, _ = fused.clamp_mse_ssim_loss(img, target, 0.2)
+        elif use_fused:
             loss, _ = fused.mse_ssim_loss(fused.clamp_to_nchw(img), target, 0.2)
         else:
             x = img.clamp(0, 1).permute(2, 0, 1).unsqueeze(0).contiguous()
             loss = manbo.mse_loss_tilelang(x, target) + 0.2 * (1 - manbo.ssim(x, target))
         loss.backward()
         grads.append((float(loss), cub.grad.cpu().numpy(), col.grad.cpu().numpy()))
-    (lf, cf, kf), (lu, cu, ku) = grads
-    assert abs(lf - lu) <= 2e-6 * abs(lu)
-    for a, b in ((cf, cu), (kf, ku)):
-        assert np.abs(a - b).max() <= 1e-4 * np.abs(b).max()
+    (lh, ch, kh), (lf, cf, kf), (lu, cu, ku) = grads
+    for l_, c_, k_ in ((lh, ch, kh), (lf, cf, kf)):
+        assert abs(l_ - lu) <= 2e-6 * abs(lu)
+        for a, b in ((c_, cu), (k_, ku)):
+            assert np.abs(a - b).max() <= 1e-4 * np.abs(b).max()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("h,w,weight", [(64, 80, 0.2), (45, 61, 0.7), (97, 130, 0.2),
+                                        (11, 11, 0.5)])
+def test_clamp_mse_ssim_loss_on_hwc_image(h, w, weight):
+    """The HWC-direct loss equals torch's clamp/permute glue followed by the
+    separate loss calls (value within 2e-6, gradient w.r.t. the [H, W, 3]
+    image within 1e-4 of float64 autograd, zero where the image lies outside
+    [0, 1]); sizes cover partial last tile rows and columns and the smallest
+    image a window fits."""
+    import manbo
+    from repo_amd import fused
+    print(f"[clamp_mse_ssim] {h}x{w}", flush=True)
+    img = _img(h, w, 5)
+    g = torch.Generator().manual_seed(8)
+    y = torch.rand((1, 3, h, w), generator=g)
+    a = img.cuda().requires_grad_(True)
+    loss, parts = fused.clamp_mse_ssim_loss(a, y.cuda(), weight)
+    x = img.cuda().clamp(0, 1).permute(2, 0, 1).unsqueeze(0).contiguous()
+    sep_mse = manbo.mse_loss_tilelang(x, y.cuda())
+    sep = sep_mse + weight * (1 - manbo.ssim(x, y.cuda()))
+    assert abs(float(loss) - float(sep)) <= 2e-6 * abs(float(sep))
+    assert abs(float(parts[0]) - float(sep_mse)) <= 2e-6 * abs(float(sep_mse))
+    i64 = img.double().requires_grad_(True)
+    x64 = i64.clamp(0, 1).permute(2, 0, 1).unsqueeze(0)
+    ref = ((x64 - y.double()) ** 2).mean() + weight * (1 - O.ssim_torch64(x64, y.double()))
+    assert abs(float(loss) - float(ref)) <= 1e-5 * abs(float(ref))
+    (0.75 * loss).backward()
+    (0.75 * ref).backward()
+    got = a.grad.cpu().double().numpy()
+    want = i64.grad.numpy()
+    assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
+    outside = ((img < 0) | (img > 1)).numpy()
+    assert outside.any() and np.all(got[outside] == 0.0)
