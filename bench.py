@@ -290,6 +290,7 @@ def main():
     _native.set_profile_ctx_factory(None)
     ms = 1000.0 * elapsed / max(1, args.steps)
     launch_ms = {RASTER_LABELS[k]: timer.mean_ms(k) for k in RASTER_LABELS}
+    timer.close()
     st = stage_times(sc, cub, col, args.stage_iters)
     b, T, idx = st.pop("_binned"), st.pop("_T"), st.pop("_idx")
     evals_fwd, evals_bwd = reference_edge_pixel_evals(b, T, idx)

@@ -136,6 +136,67 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+# HIP runtime entry points used by the host code (event timing, the one
+# device->host copy of the forward), bound through the library's handle so
+# they resolve to the runtime torch has loaded (same SONAME).
+_HIP_SIGNATURES = {
+    "hipEventCreateWithFlags": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]),
+    "hipEventRecord": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "hipEventSynchronize": (ctypes.c_int, [ctypes.c_void_p]),
+    "hipEventElapsedTime": (ctypes.c_int, [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                           ctypes.c_void_p]),
+    "hipEventDestroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "hipMemcpyAsync": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_int, ctypes.c_void_p]),
+}
+HIP_EVENT_DEFAULT = 0
+HIP_EVENT_DISABLE_TIMING = 2
+HIP_MEMCPY_DEVICE_TO_HOST = 2
+
+
+class _HipRuntime:
+    def __init__(self):
+        L = ctypes.CDLL(LIB_PATH)
+        lib()
+        for name, (res, args) in _HIP_SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
+            setattr(self, name, fn)
+
+
+_hip_rt = None
+
+
+def hip() -> _HipRuntime:
+    global _hip_rt
+    if _hip_rt is None:
+        _hip_rt = _HipRuntime()
+    return _hip_rt
+
+
+def hip_check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed (HIP status {rc})")
+
+
+def event_create(timing: bool = False) -> int:
+    """A raw hipEvent_t (int); destroy with event_destroy."""
+    h = ctypes.c_void_p()
+    flags = HIP_EVENT_DEFAULT if timing else HIP_EVENT_DISABLE_TIMING
+    hip_check(hip().hipEventCreateWithFlags(ctypes.byref(h), flags), "hipEventCreateWithFlags")
+    return h.value
+
+
+def event_elapsed_ms(a: int, b: int) -> float:
+    out = ctypes.c_float()
+    hip_check(hip().hipEventElapsedTime(ctypes.byref(out), a, b), "hipEventElapsedTime")
+    return float(out.value)
+
+
+def event_destroy(ev: int) -> None:
+    hip_check(hip().hipEventDestroy(ev), "hipEventDestroy")
+
+
 def exported_symbols():
     return list(_SIGNATURES)
 

@@ -103,6 +103,21 @@ class _MseSsimLoss(torch.autograd.Function):
         return gx.to(ctx.x_dtype), None, None, None, None, None, None
 
 
+# Element counts of the loss's work buffers per (h, w, win_size):
+# (partials, abc).
+_CLAMP_LOSS_SIZES: "dict[tuple, tuple]" = {}
+
+
+def _clamp_loss_sizes(h, w, win_size):
+    key = (h, w, win_size)
+    v = _CLAMP_LOSS_SIZES.get(key)
+    if v is None:
+        L = N.lib()
+        v = _CLAMP_LOSS_SIZES[key] = (int(L.cs_mse_ssim_partials_elems(3, h, w)),
+                                      int(L.cs_ssim_abc_elems(3, h, w, win_size)))
+    return v
+
+
 class _ClampMseSsimLoss(torch.autograd.Function):
     @staticmethod
     def forward(ctx, img, y, lo, hi, ssim_weight, win_size, win_sigma, c1, c2):
@@ -116,18 +131,21 @@ class _ClampMseSsimLoss(torch.autograd.Function):
         y32 = _as_f32(y, "target")
         dev = x32.device
         g = gaussian_window_1d(win_size, win_sigma, dev)
-        partials = torch.empty((int(N.lib().cs_mse_ssim_partials_elems(3, h, w)),),
-                               dtype=torch.float32, device=dev)
+        n_part, n_abc = _clamp_loss_sizes(h, w, int(win_size))
+        if not ctx.needs_input_grad[0]:
+            n_abc = 0
+        # clamp(img) as NCHW, the partial sums and the backward's SSIM terms in
+        # one work buffer; the three results in a buffer of their own.
+        work = torch.empty((3 * h * w + n_part + n_abc,), dtype=torch.float32, device=dev)
         out = torch.empty((3,), dtype=torch.float32, device=dev)
-        abc = (torch.empty((int(N.lib().cs_ssim_abc_elems(3, h, w, int(win_size))),),
-                           dtype=torch.float32, device=dev)
-               if ctx.needs_input_grad[0] else None)
-        x = torch.empty((3, h, w), dtype=torch.float32, device=dev)   # clamp(img) as NCHW
+        wp = work.data_ptr()
+        abc_p = wp + 4 * (3 * h * w + n_part) if n_abc else None
         with N.prof("loss.clamp_mse_ssim"):
             N.call("cs_clamp_mse_ssim_loss", N.ptr(x32), N.ptr(y32), h, w, float(lo), float(hi),
-                   N.ptr(g), int(win_size), float(c1), float(c2), float(ssim_weight), N.ptr(x),
-                   N.ptr(partials), N.ptr(out), N.ptr(abc), N.stream(dev))
-        ctx.save_for_backward(x32, y32, abc if abc is not None else torch.empty(0), g)
+                   N.ptr(g), int(win_size), float(c1), float(c2), float(ssim_weight), wp,
+                   wp + 4 * 3 * h * w, N.ptr(out), abc_p, N.stream(dev))
+        ctx.save_for_backward(x32, y32)
+        ctx.work, ctx.abc_p, ctx.g = work, abc_p, g
         ctx.lo, ctx.hi = float(lo), float(hi)
         ctx.win_size = int(win_size)
         ctx.ssim_weight = float(ssim_weight)
@@ -138,17 +156,22 @@ class _ClampMseSsimLoss(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_loss, _grad_parts):
-        x, y, abc, g = ctx.saved_tensors
         if not ctx.needs_input_grad[0]:
             return (None,) * 9
+        x, y = ctx.saved_tensors
         h, w = int(x.shape[0]), int(x.shape[1])
         gi = torch.empty_like(x)
-        go = grad_loss.detach().to(torch.float32).contiguous()
+        go = grad_loss
+        if go.dtype is not torch.float32:
+            go = go.to(torch.float32)
         with N.prof("loss.clamp_mse_ssim_bwd"):
             N.call("cs_clamp_mse_ssim_backward", N.ptr(x), N.ptr(y), h, w, ctx.lo, ctx.hi,
-                   N.ptr(g), ctx.win_size, N.ptr(abc), ctx.ssim_weight, N.ptr(go), N.ptr(gi),
-                   N.stream(x.device))
-        return gi.to(ctx.x_dtype), None, None, None, None, None, None, None, None
+                   N.ptr(ctx.g), ctx.win_size, ctx.abc_p, ctx.ssim_weight, go.data_ptr(),
+                   N.ptr(gi), N.stream(x.device))
+        ctx.work = None
+        if ctx.x_dtype is not torch.float32:
+            gi = gi.to(ctx.x_dtype)
+        return gi, None, None, None, None, None, None, None, None
 
 
 def clamp_mse_ssim_loss(img, y, ssim_weight: float = 0.2, *, lo: float = 0.0, hi: float = 1.0,

@@ -174,12 +174,15 @@ def bin_gaussians(xys, conics, radii, depths, img_h: int, img_w: int, block_x: i
                q_("keys_alt"), q_("vals_alt"), q_("radix_counts"), q_("scan_temp"),
                q_("rank_tile_ranges"), q_("tile_part_base"), q_("tile_count"),
                q_("tile_scratch"), q_("status"), st)
-    status_host, event = _take_pinned()
-    status_host.copy_(b.status, non_blocking=True)
-    event.record(torch.cuda.current_stream(dev))
-    event.synchronize()
+    pinned = _take_pinned(dev.index if dev.index is not None else torch.cuda.current_device())
+    status_host, event = pinned[0], pinned[1]
+    hip = N.hip()
+    N.hip_check(hip.hipMemcpyAsync(status_host.data_ptr(), q_("status"), 16,
+                                   N.HIP_MEMCPY_DEVICE_TO_HOST, st), "hipMemcpyAsync")
+    N.hip_check(hip.hipEventRecord(event, st), "hipEventRecord")
+    N.hip_check(hip.hipEventSynchronize(event), "hipEventSynchronize")
     I = int(status_host[0])
-    _give_pinned((status_host, event))
+    _give_pinned(pinned)
     if I < 0:
         raise RuntimeError(f"intersection count overflowed int32 ({I})")
     if I < 1:

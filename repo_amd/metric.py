@@ -36,12 +36,15 @@ def _as_f32(x: torch.Tensor, name: str) -> torch.Tensor:
     """metric.py:26-33 (device check, float32, contiguous)."""
     if x.device.type != "cuda":
         raise ValueError(f"{name} must be a CUDA tensor")
+    if x.dtype is torch.float32 and x.is_contiguous():
+        return x.detach()
     return x.detach().to(torch.float32).contiguous()
 
 
 def gaussian_window_1d(win_size: int, win_sigma: float, device) -> torch.Tensor:
     """1D factor of metric.py:47-61 (the 2D window is its outer product), fp32."""
-    key = (str(device), int(win_size), float(win_sigma))
+    device = torch.device(device) if not isinstance(device, torch.device) else device
+    key = (device.type, device.index, int(win_size), float(win_sigma))
     g = _WINDOW_CACHE.get(key)
     if g is None:
         coords = torch.arange(win_size, dtype=torch.float32)

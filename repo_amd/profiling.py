@@ -2,7 +2,7 @@
 rocprofv3 output.
 
 EventTimer is a profile-context factory (see _native.set_profile_ctx_factory):
-for the labels it is asked to watch it records a torch.cuda.Event pair on the
+for the labels it is asked to watch it records a HIP event pair on the
 current stream around the launch, so the averages are device time of exactly
 those kernels, measured inside a larger timed region.
 
@@ -31,50 +31,78 @@ import glob
 import json
 import os
 import statistics
-from contextlib import contextmanager, nullcontext
+from contextlib import nullcontext
+
+
+class _Bracket:
+    __slots__ = ("timer", "label", "a", "b")
+
+    def __init__(self, timer, label, a, b):
+        self.timer, self.label, self.a, self.b = timer, label, a, b
+
+    def __enter__(self):
+        t = self.timer
+        rc = t._rec(self.a, t._stream(t._dev()))
+        if rc:
+            t._N.hip_check(rc, "hipEventRecord")
+
+    def __exit__(self, *exc):
+        t = self.timer
+        rc = t._rec(self.b, t._stream(t._dev()))
+        if rc:
+            t._N.hip_check(rc, "hipEventRecord")
+        t.pairs[self.label].append((self.a, self.b))
+        return False
 
 
 class EventTimer:
-    """Profile-context factory that times the watched labels with HIP events.
-    Event pairs are created up front (`reserve` per label) and reused, so a
-    timed launch costs two event records on the host and nothing else."""
+    """Profile-context factory that times the watched labels with HIP events
+    recorded on the current stream around the launch.  Event pairs are created
+    up front (`reserve` per label) and reused, so a timed launch costs two
+    event records on the host and nothing else.  close() releases the events
+    (after the averages have been read)."""
 
     _NULL = nullcontext()
 
     def __init__(self, labels, reserve=128):
         import torch
+        from . import _native as N
         self.labels = set(labels)
         self.pairs = {k: [] for k in self.labels}
-        self._pool = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                      for _ in range(reserve * len(self.labels))]
+        self._N = N
+        self._rec = N.hip().hipEventRecord
+        self._stream = torch._C._cuda_getCurrentRawStream
+        self._dev = torch.cuda.current_device
+        self._all = []
+        self._pool = [self._pair() for _ in range(reserve * len(self.labels))]
         self.enabled = True
+
+    def _pair(self):
+        a, b = self._N.event_create(timing=True), self._N.event_create(timing=True)
+        self._all += [a, b]
+        return a, b
 
     def __call__(self, label):
         if not self.enabled or label not in self.labels:
             return self._NULL
-        return self._bracket(label)
-
-    @contextmanager
-    def _bracket(self, label):
-        import torch
-        if self._pool:
-            a, b = self._pool.pop()
-        else:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        yield
-        b.record()
-        self.pairs[label].append((a, b))
+        a, b = self._pool.pop() if self._pool else self._pair()
+        return _Bracket(self, label, a, b)
 
     def mean_ms(self, label):
         """Mean device time (ms) of the label's launches; call after a sync."""
         p = self.pairs.get(label) or []
         if not p:
             return None
-        return sum(a.elapsed_time(b) for a, b in p) / len(p)
+        return sum(self._N.event_elapsed_ms(a, b) for a, b in p) / len(p)
 
     def count(self, label):
         return len(self.pairs.get(label) or [])
+
+    def close(self):
+        for h in self._all:
+            self._N.event_destroy(h)
+        self._all, self._pool = [], []
+        self.pairs = {k: [] for k in self.labels}
 
 
 def _csvs(directory, suffix):

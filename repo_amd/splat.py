@@ -65,10 +65,14 @@ def _run_process_fn(process_fn, stage, payload):
 
 
 def _f32(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype is torch.float32 and t.is_contiguous():
+        return t.detach()
     return t.detach().to(torch.float32).contiguous()
 
 
 def _i32(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype is torch.int32 and t.is_contiguous():
+        return t.detach()
     return t.detach().to(torch.int32).contiguous()
 
 
@@ -145,8 +149,10 @@ class Binned:
     nseg * 2^ceil(log2(samples - 1)) and seg_edge_offsets[-1] the edge count."""
 
     def __init__(self, *, mode, img_h, img_w, samples, nseg, nprim, arena, table,
-                 adaptive=False):
+                 adaptive=False, ntiles=None):
         self.mode, self.img_h, self.img_w, self.samples = mode, img_h, img_w, samples
+        self.device = arena.device
+        self.ntiles = int(table["tile_bins"][2][0]) if ntiles is None else int(ntiles)
         self.adaptive = adaptive
         self.nseg, self.nprim = nseg, nprim
         self.num_intersects = -1
@@ -200,25 +206,77 @@ class Binned:
 
 @dataclass
 class _PendingCount:
-    status_host: torch.Tensor   # pinned int32 [4], filled by an async copy
-    event: Any                  # recorded after that copy
+    # (pinned int32 [4] filled by an async copy, raw hipEvent_t recorded after
+    # that copy, device index)
+    pinned: tuple
     capacity: int               # elements of the primitive_ids_sorted buffer
     finish: Callable[[int], torch.Tensor]  # cs_bin_finish into a new buffer of that size
 
 
-# Pinned status buffers and their events, reused across forwards.
-_PINNED_POOL: "list[tuple]" = []
+# Pinned status buffers and their (raw, non-timing) events per device, reused
+# across forwards.
+_PINNED_POOL: "dict[int, list]" = {}
 
 
-def _take_pinned():
-    if _PINNED_POOL:
-        return _PINNED_POOL.pop()
-    return (torch.empty((4,), dtype=torch.int32, pin_memory=True), torch.cuda.Event())
+def _take_pinned(dev_index: int):
+    pool = _PINNED_POOL.get(dev_index)
+    if pool:
+        return pool.pop()
+    with torch.cuda.device(dev_index):
+        return (torch.empty((4,), dtype=torch.int32, pin_memory=True), N.event_create(),
+                dev_index)
 
 
-def _give_pinned(pair) -> None:
-    if len(_PINNED_POOL) < 16:
-        _PINNED_POOL.append(pair)
+def _give_pinned(entry) -> None:
+    pool = _PINNED_POOL.setdefault(entry[2], [])
+    if len(pool) < 16:
+        pool.append(entry)
+    else:
+        N.event_destroy(entry[1])
+
+
+# Arena fields passed to cs_bin_prepare / cs_bin_finish, in argument order.
+_PREP_FIELDS = ("cubics_px", "seg_tile_ranges", "seg_recs", "edges", "edge_culls",
+                "prim_tile_ranges", "num_tiles_hit", "inv_sigma2s", "prim_recs", "keys", "order",
+                "keys_alt", "vals_alt", "radix_counts", "scan_temp", "rank_tile_ranges",
+                "tile_part_base", "tile_count", "tile_scratch", "status")
+_DECAS_FIELDS = ("seg_edge_offsets", "edge_aux", "leaf_counts")
+
+
+@dataclass
+class _BinPlan:
+    """Arena layout of one binning shape and the byte offsets of the fields
+    each launch takes (computed once per shape)."""
+    table: dict
+    nbytes: int
+    prep: tuple
+    decas: tuple
+    ntiles: int
+    grad_n: int
+
+
+_PLANS: "dict[tuple, _BinPlan]" = {}
+
+
+def _bin_plan(key, lib, nseg, P, S, img_h, img_w, block_x, block_y, mode, adaptive, per_seg):
+    plan = _PLANS.get(key)
+    if plan is None:
+        tbx, tby, _ = tile_bounds(img_h, img_w, block_x, block_y)
+        T = tbx * tby
+        K = int(lib.cs_bin_tile_parts(P, img_h, img_w, block_x, block_y))
+        fields = _binning_fields(nseg, P, nseg * per_seg, T, K,
+                                 int(lib.cs_radix_counts_elems(P)),
+                                 int(lib.cs_scan_temp_elems(max(P, T, nseg))),
+                                 _grad_accum_elems(nseg, P, mode), adaptive)
+        table, nbytes = _layout(key, fields)
+        plan = _BinPlan(table=table, nbytes=nbytes,
+                        prep=tuple(table[f][0] for f in _PREP_FIELDS),
+                        decas=tuple(table[f][0] for f in _DECAS_FIELDS) if adaptive else (),
+                        ntiles=T, grad_n=table["grad_accum"][2][0])
+        if len(_PLANS) >= 64:
+            _PLANS.pop(next(iter(_PLANS)))
+        _PLANS[key] = plan
+    return plan
 
 
 def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rules, widths,
@@ -244,59 +302,47 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
                 "exceeds the supported edge count (2^31 - 1, depth <= 24)")
     else:
         per_seg = S - 1
-    E = nseg * per_seg
-    tbx, tby, _ = tile_bounds(img_h, img_w, block_x, block_y)
-    T = tbx * tby
     key = (dev.index, mode, nseg, P, S, img_h, img_w, block_x, block_y, adaptive)
-    lay = _LAYOUTS.get(key)
-    if lay is None:
-        K = int(lib.cs_bin_tile_parts(P, img_h, img_w, block_x, block_y))
-        fields = _binning_fields(nseg, P, E, T, K, int(lib.cs_radix_counts_elems(P)),
-                                 int(lib.cs_scan_temp_elems(max(P, T, nseg))),
-                                 _grad_accum_elems(nseg, P, mode), adaptive)
-        lay = _layout(key, fields)
-    table, nbytes = lay
-    arena = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    plan = _bin_plan(key, lib, nseg, P, S, img_h, img_w, block_x, block_y, mode, adaptive,
+                     per_seg)
+    arena = torch.empty((plan.nbytes,), dtype=torch.uint8, device=dev)
     b = Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P, arena=arena,
-               table=table, adaptive=adaptive)
-    q = b.ptr
+               table=plan.table, adaptive=adaptive, ntiles=plan.ntiles)
+    base = b._base
     st = N.stream(dev)
-    args = (N.ptr(cubics_norm), N.ptr(seg_offsets), N.ptr(colors), N.ptr(opacities),
+    args = [N.ptr(cubics_norm), N.ptr(seg_offsets), N.ptr(colors), N.ptr(opacities),
             N.ptr(depths), N.ptr(fill_rules), N.ptr(widths), N.ptr(stroke_widths), nseg, P,
-            img_h, img_w, block_x, block_y, S, float(aabb_pad), int(bool(aniso)), mode,
-            q("cubics_px"), q("seg_tile_ranges"), q("seg_recs"), q("edges"), q("edge_culls"),
-            q("prim_tile_ranges"), q("num_tiles_hit"), q("inv_sigma2s"), q("prim_recs"),
-            q("keys"), q("order"), q("keys_alt"), q("vals_alt"), q("radix_counts"),
-            q("scan_temp"), q("rank_tile_ranges"), q("tile_part_base"), q("tile_count"),
-            q("tile_scratch"), q("status"))
+            img_h, img_w, block_x, block_y, S, float(aabb_pad), int(bool(aniso)), mode]
+    args += [base + o for o in plan.prep]
     with N.prof("cubic.fwd.bin_prepare"):
         if adaptive:
-            N.call("cs_bin_prepare_de_casteljau", *args, q("seg_edge_offsets"), q("edge_aux"),
-                   q("leaf_counts"), st)
+            N.call("cs_bin_prepare_de_casteljau", *args, *[base + o for o in plan.decas], st)
         else:
             N.call("cs_bin_prepare", *args, st)
-    grad_n = table["grad_accum"][2][0]
+    q = b.ptr
+    order_p, ranks_p, status_p = q("order"), q("rank_tile_ranges"), q("status")
+    parts_p, count_p, scratch_p = q("tile_part_base"), q("tile_count"), q("tile_scratch")
+    bins_p, grad_p, grad_n = q("tile_bins"), q("grad_accum"), plan.grad_n
 
     def finish(capacity: int) -> torch.Tensor:
         ids = torch.empty((capacity,), dtype=torch.int32, device=dev)
         with N.prof("cubic.fwd.bin_finish"):
-            N.call("cs_bin_finish", q("order"), q("rank_tile_ranges"), P, q("status"), capacity,
-                   img_h, img_w, block_x, block_y, q("tile_part_base"), q("tile_count"),
-                   q("tile_scratch"), ids.data_ptr(), q("tile_bins"), q("grad_accum"), grad_n,
-                   st)
+            N.call("cs_bin_finish", order_p, ranks_p, P, status_p, capacity, img_h, img_w,
+                   block_x, block_y, parts_p, count_p, scratch_p, ids.data_ptr(), bins_p,
+                   grad_p, grad_n, st)
         return ids
 
     # The one host read of the forward (the reference reads the same count,
     # cubic_splatting.py:2879).  With a capacity hint the lists are built into
     # a buffer of that size first and the count is checked afterwards, so the
     # GPU does not idle while the host waits for it.
-    status_host, event = _take_pinned()
-    status_host.copy_(b.status, non_blocking=True)
-    if dev.index == torch.cuda.current_device():
-        event.record()
-    else:
-        event.record(torch.cuda.current_stream(dev))
-    pending = _PendingCount(status_host, event, -1, finish)
+    pinned = _take_pinned(dev.index if dev.index is not None else torch.cuda.current_device())
+    status_host, event = pinned[0], pinned[1]
+    hip = N.hip()
+    N.hip_check(hip.hipMemcpyAsync(status_host.data_ptr(), status_p, 16,
+                                   N.HIP_MEMCPY_DEVICE_TO_HOST, st), "hipMemcpyAsync")
+    N.hip_check(hip.hipEventRecord(event, st), "hipEventRecord")
+    pending = _PendingCount(pinned, -1, finish)
     if capacity_hint is None:
         I = _read_count(pending, nseg)
         b.primitive_ids_sorted = finish(I)
@@ -313,9 +359,10 @@ def _grad_accum_elems(nseg: int, nprim: int, mode: int) -> int:
 
 
 def _read_count(pending: "_PendingCount", nseg: int) -> int:
-    pending.event.synchronize()
-    I, bad, first, last = pending.status_host.tolist()
-    _give_pinned((pending.status_host, pending.event))
+    status_host, event = pending.pinned[0], pending.pinned[1]
+    N.hip_check(N.hip().hipEventSynchronize(event), "hipEventSynchronize")
+    I, bad, first, last = status_host.tolist()
+    _give_pinned(pending.pinned)
     if bad or first != 0 or last != nseg:
         raise ValueError(
             "primitive_seg_offsets must start at 0 and end at num_segments "
@@ -365,10 +412,6 @@ _MAX_ORDERS = 16
 ORDER_CHUNKED = True
 
 
-def _order_key(dev, ntiles):
-    return (dev.index, N.stream(dev), ntiles)
-
-
 def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
     """(image [H,W,3], final_Ts, final_idx).  With eval_counts (int64 [5],
     zeroed, on the device) the counting instantiation runs and adds the
@@ -377,33 +420,41 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
     size on this stream (if any) and records its wave durations, from which
     the order of this forward's backward (b.tile_order) and of the next
     forward is made."""
-    dev = b.arena.device
-    out = torch.empty((b.img_h, b.img_w, 3), dtype=torch.float32, device=dev)
-    # final_Ts and final_idx share one allocation (both 4-byte, [H, W]).
-    tid = torch.empty((2, b.img_h, b.img_w), dtype=torch.float32, device=dev)
-    final_T, final_idx = tid[0], tid[1].view(torch.int32)
-    ntiles = int(b.tile_bins.shape[0])
-    key = _order_key(dev, ntiles)
-    prev = _TILE_ORDERS.get(key)
+    dev = b.device
+    H, W = b.img_h, b.img_w
+    out = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
+    ntiles = b.ntiles
+    cap = max(int(b.primitive_ids_sorted.numel()), 1)
+    fill = b.mode == MODE_FILL
+    # final_Ts, final_idx, the next tile order and (fill) the inside bits of
+    # every (list entry, wave) for the backward share one allocation.
+    # The log's 16-byte records start on a 256-byte boundary.
+    o_ord = 2 * H * W
+    o_log = (o_ord + ntiles + 63) // 64 * 64
+    n_log = 2 * cap * N.INSIDE_LOG_INTS if fill else 0
+    aux = torch.empty((o_log + n_log,), dtype=torch.int32, device=dev)
+    final_T = aux[:H * W].view(torch.float32).view(H, W)
+    final_idx = aux[H * W:o_ord].view(H, W)
+    order = aux[o_ord:o_ord + ntiles]
+    b.inside_log = aux[o_log:].view(2 * cap, N.INSIDE_LOG_INTS) if fill else None
     st = N.stream(dev)
-    # Inside bits of every (list entry, wave) for the backward (fill only).
-    cap = int(b.primitive_ids_sorted.numel())
-    b.inside_log = (torch.empty((2 * max(cap, 1), N.INSIDE_LOG_INTS), dtype=torch.int32,
-                                device=dev) if b.mode == MODE_FILL else None)
+    key = (dev.index, st, ntiles)
+    prev = _TILE_ORDERS.get(key)
+    base = aux.data_ptr()
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
-            b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
-            b.edges_per_segment, N.ptr(out), N.ptr(final_T), N.ptr(final_idx),
-            N.ptr(b.inside_log))
+            b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), H, W,
+            b.edges_per_segment, N.ptr(out), base, base + 4 * H * W,
+            base + 4 * o_log if fill else None)
     cost = b.ptr("wave_cost")
+    prev_p = None if prev is None else prev.data_ptr()
     if eval_counts is not None:
         N.call("cs_rasterize_forward_counted", *args, N.ptr(_counts_buffer(eval_counts)),
-               N.ptr(prev), cost, st)
+               prev_p, cost, st)
     else:
         with N.prof("cubic.fwd.rast"):
-            N.call("cs_rasterize_forward", *args, N.ptr(prev), cost, st)
-    order = torch.empty((ntiles,), dtype=torch.int32, device=dev)
+            N.call("cs_rasterize_forward", *args, prev_p, cost, st)
     with N.prof("cubic.fwd.tile_order"):
-        N.call("cs_raster_tile_order", cost, ntiles, int(ORDER_CHUNKED), N.ptr(order), st)
+        N.call("cs_raster_tile_order", cost, ntiles, int(ORDER_CHUNKED), base + 4 * o_ord, st)
     b.tile_order = order
     _TILE_ORDERS.pop(key, None)
     if len(_TILE_ORDERS) >= _MAX_ORDERS:
@@ -424,7 +475,7 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_inv_sigma2s [P], v_stroke_widths [P] or None), accumulated into fresh
     zero buffers (cubic_splatting.py:2572-2747).  eval_counts as for
     rasterize_forward (cs_rasterize_backward_counted)."""
-    dev = b.arena.device
+    dev = b.device
     P = b.nprim
     if b.grad_accum_clean:
         zeros = b.grad_accum
@@ -528,7 +579,11 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
     num_segments = int(cubics_norm.shape[0])
     offs = _i32(primitive_seg_offsets).view(-1)
     num_primitives = max(0, int(offs.numel()) - 1)
-    bg = background.to(device=cubics_norm.device, dtype=torch.float32).view(3).contiguous()
+    dev = cubics_norm.device
+    bg = background
+    if bg.dtype is not torch.float32 or bg.device != dev or not bg.is_contiguous():
+        bg = bg.to(device=dev, dtype=torch.float32).contiguous()
+    bg = bg.view(3)
     ctx.img_h, ctx.img_w = int(img_h), int(img_w)
     if num_primitives <= 0:
         ctx.empty = True
@@ -584,47 +639,53 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
     ctx.flatten_method = flatten_method_norm
     ctx.distance_samples = int(distance_samples)
     ctx.mode = mode
-    ctx.save_for_backward(cubics_norm, offs, colors_c, opac_c, depths, widths, bg, final_T,
-                          final_idx, sw_c)
+    # The backward kernels read the binned copies (records, edges); the
+    # inputs are kept for process_fn payloads and gradient shapes.  Tensors
+    # made here are plain attributes.
+    ctx.save_for_backward(colors_c, opac_c, depths, sw_c)
+    ctx.cub_shape = cubics_norm.shape
+    ctx.offs, ctx.widths, ctx.bg, ctx.final_T, ctx.final_idx = offs, widths, bg, final_T, final_idx
     return out
 
 
 def _splat_backward(ctx, grad_out_img):
     b: Binned = ctx.binned
-    (cubics_norm, offs, colors, opacities, depths, widths, bg, final_T, final_idx,
-     stroke_widths) = ctx.saved_tensors
+    colors, opacities, depths, stroke_widths = ctx.saved_tensors
+    offs, widths, bg, final_T, final_idx = ctx.offs, ctx.widths, ctx.bg, ctx.final_T, ctx.final_idx
     process_fn = ctx.process_fn
-    pre = _run_process_fn(process_fn, "pre_backward_rasterize", {
-        "collect_curve_contrib_rgb": False,
-        "collect_curve_isect_contrib": False,
-        "num_primitives": int(colors.shape[0]),
-        "colors": colors,
-    })
-    collect_rgb = bool(pre.get("collect_curve_contrib_rgb", False))
-    collect_isect = bool(pre.get("collect_curve_isect_contrib", False))
-    curve_contrib_rgb = torch.zeros_like(colors) if collect_rgb else None
-    curve_isect_contrib = (torch.zeros((b.num_intersects,), dtype=torch.float32,
-                                       device=colors.device) if collect_isect else None)
+    curve_contrib_rgb = curve_isect_contrib = None
+    if process_fn is not None:
+        pre = _run_process_fn(process_fn, "pre_backward_rasterize", {
+            "collect_curve_contrib_rgb": False,
+            "collect_curve_isect_contrib": False,
+            "num_primitives": int(colors.shape[0]),
+            "colors": colors,
+        })
+        if bool(pre.get("collect_curve_contrib_rgb", False)):
+            curve_contrib_rgb = torch.zeros_like(colors)
+        if bool(pre.get("collect_curve_isect_contrib", False)):
+            curve_isect_contrib = torch.zeros((b.num_intersects,), dtype=torch.float32,
+                                              device=colors.device)
     v_output = _f32(grad_out_img)
     v_cubics_px, v_colors, v_opac, v_is2, v_sw = rasterize_backward(
         b, bg, final_T, final_idx, v_output, curve_contrib_rgb=curve_contrib_rgb,
         curve_isect_contrib=curve_isect_contrib)
-    payload = {
-        "v_cubics_px": v_cubics_px,
-        "v_colors": v_colors,
-        "v_opacity": v_opac,
-        "curve_contrib_rgb": curve_contrib_rgb,
-        "curve_isect_contrib": curve_isect_contrib,
-        "primitive_ids_sorted": b.primitive_ids_sorted,
-        "tile_bins": b.tile_bins,
-        "colors": colors,
-        "opacities": opacities,
-        "primitive_seg_offsets": offs,
-    }
-    if ctx.mode == MODE_STROKE:
-        payload["v_stroke"] = v_sw
-        payload["stroke_widths"] = stroke_widths
     if process_fn is not None:
+        payload = {
+            "v_cubics_px": v_cubics_px,
+            "v_colors": v_colors,
+            "v_opacity": v_opac,
+            "curve_contrib_rgb": curve_contrib_rgb,
+            "curve_isect_contrib": curve_isect_contrib,
+            "primitive_ids_sorted": b.primitive_ids_sorted,
+            "tile_bins": b.tile_bins,
+            "colors": colors,
+            "opacities": opacities,
+            "primitive_seg_offsets": offs,
+        }
+        if ctx.mode == MODE_STROKE:
+            payload["v_stroke"] = v_sw
+            payload["stroke_widths"] = stroke_widths
         payload = _run_process_fn(process_fn, "post_backward_rasterize", payload)
         v_cubics_px = _f32(payload["v_cubics_px"])
         v_colors = payload["v_colors"]
@@ -636,7 +697,7 @@ def _splat_backward(ctx, grad_out_img):
     depth_index = 5 if ctx.mode == MODE_STROKE else 4
     v_depths = (torch.zeros_like(depths, dtype=torch.float32)
                 if ctx.needs_input_grad[depth_index] else None)
-    return v_cubics_norm.view_as(cubics_norm), v_colors, v_opac.view_as(opacities), v_sw, \
+    return v_cubics_norm.view(ctx.cub_shape), v_colors, v_opac.view_as(opacities), v_sw, \
         v_depths, v_aa
 
 
@@ -698,6 +759,18 @@ def _prim_vector(t, num_primitives, name, device, dtype, default):
     return out
 
 
+def _aa_widths(aa_widths, num_primitives, dev, aa_width):
+    """Per-primitive widths, clamped to >= 1e-4 as the reference's render
+    functions do (cubic_splatting.py:3207).  Every kernel that reads a width
+    applies the same floor itself (fmaxf, so a NaN width reads as the floor
+    there), so the clamp is materialised only when a gradient has to flow
+    through it (where it zeroes the gradient of the clamped widths)."""
+    w = _prim_vector(aa_widths, num_primitives, "aa_widths", dev, torch.float32, float(aa_width))
+    if w.requires_grad:
+        return torch.clamp(w.contiguous(), min=1e-4)
+    return w if w.is_contiguous() else w.contiguous()
+
+
 def _common_checks(cubics_norm, offs, colors, opacities, depths, num_primitives,
                    stroke_widths=None):
     if int(colors.shape[0]) != num_primitives:
@@ -740,8 +813,7 @@ def render_cubic_fill_splat_tilelang(cubics_norm, primitive_seg_offsets, colors,
     rules = (None if fill_rules is None else
              _prim_vector(fill_rules, num_primitives, "fill_rules", dev, torch.int32, 1)
              .contiguous())
-    widths = torch.clamp(_prim_vector(aa_widths, num_primitives, "aa_widths", dev,
-                                      torch.float32, float(aa_width)).contiguous(), min=1e-4)
+    widths = _aa_widths(aa_widths, num_primitives, dev, aa_width)
     return _CubicFillSplatFunction.apply(
         cubics_norm, offs.contiguous(), colors.contiguous(), opacities.reshape(-1).contiguous(),
         depths.reshape(-1).contiguous(), rules, int(img_h), int(img_w),
@@ -767,8 +839,7 @@ def render_cubic_polyline_splat_tilelang(cubics_norm, primitive_seg_offsets, col
         return bg.expand(int(img_h), int(img_w), 3).clone()
     _common_checks(cubics_norm, offs, colors, opacities, depths, num_primitives, stroke_widths)
     dev = cubics_norm.device
-    widths = torch.clamp(_prim_vector(aa_widths, num_primitives, "aa_widths", dev,
-                                      torch.float32, float(aa_width)).contiguous(), min=1e-4)
+    widths = _aa_widths(aa_widths, num_primitives, dev, aa_width)
     return _CubicPolylineSplatFunction.apply(
         cubics_norm, offs.contiguous(), colors.contiguous(), opacities.reshape(-1).contiguous(),
         stroke_widths.reshape(-1).contiguous(), depths.reshape(-1).contiguous(), int(img_h),

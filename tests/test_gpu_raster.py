@@ -303,3 +303,60 @@ def test_heavy_first_tile_order_is_a_permutation_and_changes_no_result():
     for a, r in zip(g1, g0):
         ok, err = grad_scale_tol(a.cpu().numpy(), r.cpu().numpy(), rtol=1e-5)
         assert ok, err
+
+
+@pytest.mark.gpu
+def test_event_timer_brackets_the_raster_launches():
+    """profiling.EventTimer as the library's profile-context factory: one HIP
+    event pair per watched launch, positive device times, nothing recorded for
+    unwatched labels, events released by close()."""
+    from repo_amd import _native, profiling
+    print("[event timer]", flush=True)
+    sc = synth.small_scene(3, P=8)
+    b, s = hip_bin(sc)
+    bg = s.background.float().contiguous()
+    timer = profiling.EventTimer({"cubic.fwd.rast": "f", "cubic.bwd.rast": "b"}, reserve=2)
+    _native.set_profile_ctx_factory(timer)
+    try:
+        for _ in range(3):   # one more than reserved: the pool grows
+            out, T, idx = splat.rasterize_forward(b, bg)
+        b.grad_accum_clean = False
+        splat.rasterize_backward(b, bg, T, idx, random_v_out(sc.img_h, sc.img_w).cuda())
+    finally:
+        _native.set_profile_ctx_factory(None)
+    torch.cuda.synchronize()
+    assert timer.count("cubic.fwd.rast") == 3 and timer.count("cubic.bwd.rast") == 1
+    assert timer.count("cubic.fwd.tile_order") == 0
+    assert timer.mean_ms("cubic.fwd.rast") > 0 and timer.mean_ms("cubic.bwd.rast") > 0
+    timer.close()
+    assert timer.count("cubic.fwd.rast") == 0
+
+
+@pytest.mark.gpu
+def test_widths_below_floor_match_the_clamped_widths():
+    """aa_widths under 1e-4 render as 1e-4 (the reference clamps them before
+    its kernels, cubic_splatting.py:3207): bit-identical images for raw and
+    pre-clamped widths; with widths that require a gradient, the clamped
+    entries receive zero gradient."""
+    import manbo
+    print("[width floor]", flush=True)
+    sc = synth.small_scene(4, P=8).to("cuda")
+    raw = sc.aa_widths.clone()
+    raw[::3] = 0.0
+    raw[1::3] = 1e-6
+
+    def render(w):
+        return manbo.ops.render_cubic_fill_splat_tilelang(
+            sc.cubics_norm, sc.seg_offsets, sc.colors, sc.opacities, sc.depths, sc.img_h,
+            sc.img_w, 16, 16, sc.background, aa_widths=w, distance_samples=sc.S)
+
+    a = render(raw)
+    b = render(torch.clamp(raw, min=1e-4))
+    assert torch.equal(a, b)
+    wg = raw.clone().requires_grad_(True)
+    img = render(wg)
+    assert torch.equal(img, a)
+    img.square().sum().backward()
+    low = raw < 1e-4
+    assert float(wg.grad[low].abs().max()) == 0.0
+    assert float(wg.grad[~low].abs().max()) > 0.0
