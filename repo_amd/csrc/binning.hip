@@ -368,6 +368,25 @@ __device__ __forceinline__ float2 leaf_interval(int d, uint32_t k) {
     return make_float2((float)k * sc, (float)(k + 1u) * sc);
 }
 
+// Flattening point at t: ((P0 b0 + P1 b1) + P2 b2) + P3 b3 with the cubic
+// Bernstein weights, the reference's evaluation order.
+__device__ __forceinline__ void bezier_point(const float (&X)[4], const float (&Y)[4], float t,
+                                             float& x, float& y) {
+    const float omt = 1.0f - t;
+    const float b0 = omt * omt * omt;
+    const float b1 = 3.0f * omt * omt * t;
+    const float b2 = 3.0f * omt * t * t;
+    const float b3 = t * t * t;
+    x = X[0] * b0;
+    x = x + X[1] * b1;
+    x = x + X[2] * b2;
+    x = x + X[3] * b3;
+    y = Y[0] * b0;
+    y = y + Y[1] * b1;
+    y = y + Y[2] * b2;
+    y = y + Y[3] * b3;
+}
+
 __global__ __launch_bounds__(256) void k_project_flatten(
     const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
     const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths,
@@ -411,26 +430,78 @@ __global__ __launch_bounds__(256) void k_project_flatten(
     EdgeRec* er = edges + (size_t)s * (S - 1);
     EdgeCull* ec = culls + (size_t)s * (S - 1);
     for (int i = 0; i < S; ++i) {
-        const float t = linspace01(S, i);
-        const float omt = 1.0f - t;
-        const float b0 = omt * omt * omt;
-        const float b1 = 3.0f * omt * omt * t;
-        const float b2 = 3.0f * omt * t * t;
-        const float b3 = t * t * t;
-        float x = r.px[0] * b0;
-        x = x + r.px[1] * b1;
-        x = x + r.px[2] * b2;
-        x = x + r.px[3] * b3;
-        float y = r.py[0] * b0;
-        y = y + r.py[1] * b1;
-        y = y + r.py[2] * b2;
-        y = y + r.py[3] * b3;
+        float x, y;
+        bezier_point(r.px, r.py, linspace01(S, i), x, y);
         vbox_add(box, x, y);
         if (i > 0) write_edge(prevx, prevy, x, y, D, er + (i - 1), ec + (i - 1));
         prevx = x;
         prevy = y;
     }
     seg_recs[s] = seg_record(box, D);
+}
+
+// Uniform flattening with one lane per sample point, for S <= 64: a group of
+// L = 2^ceil(log2 S) consecutive lanes shares segment s.  Lane i evaluates
+// point min(i, S - 1) with the expression of k_project_flatten, takes point
+// i + 1 from its neighbour and writes edge i; a butterfly min/max over the
+// group gives the vertex box (min/max are order-independent), and lane 0
+// writes the projected control points, the tile range and the segment
+// record.  Thread 0 of the grid also sets the status words (k_status_init),
+// which the later launches of the binning update.  Same outputs as
+// k_project_flatten, with nseg * L lanes instead of nseg threads.
+template <int L>
+__global__ __launch_bounds__(256) void k_project_flatten_lanes(
+    const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
+    const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths,
+    const float* __restrict__ opacities, int mode, int nseg, int img_h, int img_w, int block_x,
+    int block_y, float aabb_pad, int aniso, int S, float* __restrict__ cubics_px,
+    int32_t* __restrict__ seg_tile_ranges, SegRec* __restrict__ seg_recs,
+    EdgeRec* __restrict__ edges, EdgeCull* __restrict__ culls, int32_t* __restrict__ status) {
+    static_assert(L >= 2 && L <= kWave && (L & (L - 1)) == 0, "group of lanes");
+    const size_t gt = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gt == 0) {
+        status[0] = 0;
+        status[1] = 0;
+        status[2] = seg_offsets[0];
+        status[3] = seg_offsets[P];
+    }
+    // Groups never straddle a workgroup (256 is a multiple of L), so a
+    // group's lanes leave together.
+    const size_t s64 = gt / L;
+    if (s64 >= (size_t)nseg) return;
+    const int s = (int)s64;
+    const int i = (int)(gt & (L - 1));
+    const int p = owner_of(seg_offsets, P, s);
+    const float w = fmaxf(aa_widths[p], kWidthMin);
+    const float support = fmaxf(0.0f, w * 3.0f);
+    const float half_sw = stroke_widths ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
+    const float D = prim_params(mode, aa_widths[p], opacities[p], stroke_widths, p).cull_d;
+    const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
+    const SegProj r = project_segment(cubics_norm + (size_t)s * 8, 0.5f * (float)img_w,
+                                      0.5f * (float)img_h, half_sw, support, aabb_pad, aniso, tbx,
+                                      tby, (float)block_x, (float)block_y);
+    float x, y;
+    bezier_point(r.px, r.py, linspace01(S, min(i, S - 1)), x, y);
+    const float nx = __shfl_down(x, 1, L), ny = __shfl_down(y, 1, L);
+    if (i < S - 1)
+        write_edge(x, y, nx, ny, D, edges + (size_t)s * (S - 1) + i,
+                   culls + (size_t)s * (S - 1) + i);
+    VBox box = vbox_empty();
+    vbox_add(box, x, y);
+#pragma unroll
+    for (int off = L / 2; off >= 1; off >>= 1) {
+        box.x0 = fminf(box.x0, __shfl_xor(box.x0, off, L));
+        box.x1 = fmaxf(box.x1, __shfl_xor(box.x1, off, L));
+        box.y0 = fminf(box.y0, __shfl_xor(box.y0, off, L));
+        box.y1 = fmaxf(box.y1, __shfl_xor(box.y1, off, L));
+    }
+    if (i == 0) {
+        float4* cp = reinterpret_cast<float4*>(cubics_px + (size_t)s * 8);
+        cp[0] = make_float4(r.px[0], r.py[0], r.px[1], r.py[1]);
+        cp[1] = make_float4(r.px[2], r.py[2], r.px[3], r.py[3]);
+        reinterpret_cast<int4*>(seg_tile_ranges)[s] = make_int4(r.tx0, r.ty0, r.tx1, r.ty1);
+        seg_recs[s] = seg_record(box, D);
+    }
 }
 
 // Adaptive flattening, second pass (cubic_splatting.py:1729-1832): the leaves
@@ -505,20 +576,8 @@ __global__ __launch_bounds__(256) void k_bernstein_ref(const float* __restrict__
     const Cub c = load_cub(cubics_px + (size_t)s * 8);
     float prevx = 0.0f, prevy = 0.0f;
     for (int i = 0; i < S; ++i) {
-        const float t = linspace01(S, i);
-        const float omt = 1.0f - t;
-        const float b0 = omt * omt * omt;
-        const float b1 = 3.0f * omt * omt * t;
-        const float b2 = 3.0f * omt * t * t;
-        const float b3 = t * t * t;
-        float x = c.x[0] * b0;
-        x = x + c.x[1] * b1;
-        x = x + c.x[2] * b2;
-        x = x + c.x[3] * b3;
-        float y = c.y[0] * b0;
-        y = y + c.y[1] * b1;
-        y = y + c.y[2] * b2;
-        y = y + c.y[3] * b3;
+        float x, y;
+        bezier_point(c.x, c.y, linspace01(S, i), x, y);
         if (i > 0)
             reinterpret_cast<float4*>(edges_px)[(size_t)s * (S - 1) + i - 1] =
                 make_float4(prevx, prevy, x, y);
@@ -1291,8 +1350,32 @@ static int bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, con
         return CS_ERR_ARGS;
     }
     const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
-    hipLaunchKernelGGL(k_status_init, dim3(1), dim3(1), 0, stream, seg_offsets, nprim, status);
-    if (nseg > 0)
+    if (!adaptive && nseg > 0 && samples <= kWave) {
+        // One lane per sample point; the kernel also sets the status words.
+        const int lanes = samples <= 2 ? 2 : 1 << ceil_log2(samples);
+        const size_t threads = (size_t)nseg * lanes;
+        const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+#define CS_FLATTEN_LANES(Lv)                                                                   \
+    hipLaunchKernelGGL(k_project_flatten_lanes<Lv>, grid, block, 0, stream, cubics_norm,      \
+                       seg_offsets, nprim, aa_widths, stroke_widths, opacities, mode, nseg,    \
+                       img_h, img_w, block_x, block_y, aabb_pad, aniso, samples, cubics_px,    \
+                       seg_tile_ranges, reinterpret_cast<SegRec*>(seg_recs),                   \
+                       reinterpret_cast<EdgeRec*>(edges), reinterpret_cast<EdgeCull*>(edge_culls), \
+                       status)
+        switch (lanes) {
+            case 2: CS_FLATTEN_LANES(2); break;
+            case 4: CS_FLATTEN_LANES(4); break;
+            case 8: CS_FLATTEN_LANES(8); break;
+            case 16: CS_FLATTEN_LANES(16); break;
+            case 32: CS_FLATTEN_LANES(32); break;
+            default: CS_FLATTEN_LANES(64); break;
+        }
+#undef CS_FLATTEN_LANES
+    } else {
+        hipLaunchKernelGGL(k_status_init, dim3(1), dim3(1), 0, stream, seg_offsets, nprim,
+                           status);
+    }
+    if (nseg > 0 && (adaptive || samples > kWave))
         hipLaunchKernelGGL(k_project_flatten, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
                            cubics_norm, seg_offsets, nprim, aa_widths, stroke_widths, opacities,
                            mode, nseg, img_h, img_w, block_x, block_y, aabb_pad, aniso, samples,

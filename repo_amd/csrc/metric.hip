@@ -420,7 +420,7 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
         const float xv = HWC ? fminf(fmaxf(xr, lo), hi) : xr, yv = yc[pi];
         float gv = scale * (gsum[0][o] + 2.0f * xv * gsum[1][o] + yv * gsum[2][o]);
         if (mse_coef != 0.0f) gv = __builtin_fmaf(mscale, xv - yv, gv);
-        if (HWC) gx[3 * pi + c] = (xr >= lo) & (xr <= hi) ? gv : 0.0f;
+        if (HWC) gx[3 * pi + c] = ((xr >= lo) & (xr <= hi)) ? gv : 0.0f;
         else gx[(size_t)c * h * w + pi] = gv;
     }
 }
