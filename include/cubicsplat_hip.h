@@ -219,15 +219,19 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
 int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
                          int32_t* tile_order, hipStream_t stream);
 
-/* Inside log (mode 0): the forward writes, for every list entry g a wave of
- * tile rows processes, the wave's per-pixel inside bits (its winding test,
- * two 64-bit masks = 16 bytes) at inside_log[2 g + wave], and the backward of
- * that forward reads them instead of re-evaluating the crossing terms.  It
- * holds 2 * (capacity of prim_ids_sorted) 16-byte records; required by the
- * fill backward, NULL allowed in the forward (then not written).  No
- * reference counterpart: the reference's backward re-runs the crossing test
- * (ops/cubic_splatting.py:1485-1501). */
-#define CS_INSIDE_LOG_BYTES 16
+/* Raster log: for every list entry g a wave of tile rows processes, the
+ * forward writes a 544-byte record at raster_log[2 g + wave]: the wave's
+ * per-pixel inside bits (its winding test; zero for strokes) and exact bits
+ * (pixels whose coverage needs the exact distance), each as two 64-bit lane
+ * masks (32 bytes), then the best edge index (nearest, first strict minimum
+ * in ascending edge order) of each exact pixel, packed in lane order (int32
+ * [128]).  The backward of that forward reads it instead of re-running the
+ * edge walk: it recomputes one distance term per exact pixel.  It holds 2 *
+ * (capacity of prim_ids_sorted) records; required by the backward, NULL
+ * allowed in the forward (then not written).  No reference counterpart: the
+ * reference's backward re-runs the edge loop (ops/cubic_splatting.py:1451-1501,
+ * ops/cubic_polyline_splatting.py:465-532). */
+#define CS_RASTER_LOG_BYTES 544
 
 /* rasterize_cubic_fill_forward_kernel (ops/cubic_splatting.py:918-1194) when
  * mode 0, rasterize_cubic_polyline_forward_kernel
@@ -238,7 +242,7 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
                          const void* edges, const void* edge_culls, const void* prim_recs,
                          const float* background, int32_t img_h, int32_t img_w,
                          int32_t edges_per_segment, float* out_img, float* final_Ts,
-                         int32_t* final_idx, void* inside_log, const int32_t* tile_order,
+                         int32_t* final_idx, void* raster_log, const int32_t* tile_order,
                          uint32_t* wave_cost, hipStream_t stream);
 
 /* rasterize_cubic_fill_backward_kernel (ops/cubic_splatting.py:1197-1651) /
@@ -251,7 +255,7 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
                           const void* edges, const void* edge_culls, const void* prim_recs,
                           const float* background, int32_t img_h, int32_t img_w,
                           int32_t edges_per_segment, const float* final_Ts,
-                          const int32_t* final_idx, const void* inside_log, const float* v_output,
+                          const int32_t* final_idx, const void* raster_log, const float* v_output,
                           float* v_cubics_px, float* v_colors, float* v_opacities,
                           float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
                           float* curve_isect_contrib, const int32_t* tile_order,
@@ -268,7 +272,7 @@ int cs_rasterize_backward_de_casteljau(int32_t mode, const int32_t* prim_ids_sor
                                        const void* edge_culls, const void* prim_recs,
                                        const float* background, int32_t img_h, int32_t img_w,
                                        const void* edge_aux, const float* final_Ts,
-                                       const int32_t* final_idx, const void* inside_log,
+                                       const int32_t* final_idx, const void* raster_log,
                                        const float* v_output, float* v_cubics_px, float* v_colors,
                                        float* v_opacities, float* v_inv_sigma2s,
                                        float* v_stroke_widths, float* curve_contrib_rgb,
@@ -290,7 +294,7 @@ int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                  const void* edge_culls, const void* prim_recs,
                                  const float* background, int32_t img_h, int32_t img_w,
                                  int32_t edges_per_segment, float* out_img, float* final_Ts,
-                                 int32_t* final_idx, void* inside_log,
+                                 int32_t* final_idx, void* raster_log,
                                  unsigned long long* eval_counts, const int32_t* tile_order,
                                  uint32_t* wave_cost, hipStream_t stream);
 int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
@@ -298,7 +302,7 @@ int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                   const void* edge_culls, const void* prim_recs,
                                   const float* background, int32_t img_h, int32_t img_w,
                                   int32_t edges_per_segment, const float* final_Ts,
-                                  const int32_t* final_idx, const void* inside_log,
+                                  const int32_t* final_idx, const void* raster_log,
                                   const float* v_output, float* v_cubics_px, float* v_colors,
                                   float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
                                   float* curve_contrib_rgb, float* curve_isect_contrib,

@@ -91,6 +91,19 @@ struct alignas(16) EdgeAux {
     int32_t pad;
 };
 
+// Raster log of one (list entry, wave of tile rows), written by the forward
+// and read by the backward of that forward: the per-pixel inside bits (the
+// winding test; zero for strokes) and exact bits (pixels whose coverage needs
+// the exact distance, all others being decided in closed form), each as one
+// 64-bit lane mask per pixel row p of the lanes, then the best edge (nearest,
+// first strict minimum in ascending edge order) of every exact pixel, packed
+// in lane order: the exact pixels of row 0, then those of row 1.
+struct alignas(16) RasterLog {
+    uint32_t inside[2 * kPix];
+    uint32_t exact[2 * kPix];
+    int32_t best[kWave * kPix];
+};
+
 // Per cubic segment: the unions of its edges' ranges, plus the last pixel
 // column that can lie left of one of its vertices (for open chains).
 struct alignas(16) SegRec {

@@ -28,6 +28,7 @@ static_assert(sizeof(EdgeRec) == CS_EDGE_RECORD_BYTES, "edge record layout");
 static_assert(sizeof(PrimRec) == CS_PRIM_RECORD_BYTES, "primitive record layout");
 static_assert(sizeof(EdgeCull) == CS_EDGE_CULL_BYTES, "edge cull record layout");
 static_assert(sizeof(EdgeAux) == CS_EDGE_AUX_BYTES, "edge aux record layout");
+static_assert(sizeof(RasterLog) == CS_RASTER_LOG_BYTES, "raster log record layout");
 
 // Crossing parity equals winding & 1 (each crossing changes the winding by
 // +-1), so only the winding number is tracked.
@@ -61,9 +62,12 @@ __device__ __forceinline__ bool near_wave(const R& r, const WaveRect& W) {
     return near_rows(r, W) && near_cols(r, W);
 }
 
-// Distance (and optionally the best edge) of one edge, with w = pixel - p0,
-// cubic_splatting.py:1095-1118 / 1451-1484.
-template <bool BEST>
+// Distance of one edge, with w = pixel - p0, cubic_splatting.py:1095-1118 /
+// 1451-1484.  BEST 0 keeps the minimum, 1 also the best edge (the first strict
+// minimum in visiting order), 2 also its projection and offset (for the
+// gradients).  A NaN d2 leaves each variant unchanged, so all three keep the
+// same minimum.
+template <int BEST>
 __device__ __forceinline__ void dist_term(const EdgeRec& E, int eid, float wx, float wy,
                                           Geom& G) {
     float proj = __builtin_fmaf(wx, E.ux, wy * E.uy);
@@ -71,13 +75,18 @@ __device__ __forceinline__ void dist_term(const EdgeRec& E, int eid, float wx, f
     const float dx = __builtin_fmaf(proj, E.vx, -wx);
     const float dy = __builtin_fmaf(proj, E.vy, -wy);
     const float d2 = __builtin_fmaf(dx, dx, dy * dy);
-    if (BEST) {
+    if constexpr (BEST == 2) {
         if (d2 < G.min_d2) {
             G.min_d2 = d2;
             G.best = eid;
             G.bproj = proj;
             G.bdx = dx;
             G.bdy = dy;
+        }
+    } else if constexpr (BEST == 1) {
+        if (d2 < G.min_d2) {
+            G.min_d2 = d2;
+            G.best = eid;
         }
     } else {
         G.min_d2 = fminf(G.min_d2, d2);
@@ -126,6 +135,12 @@ struct EvalCounts {
     uint64_t dist, cross, row, entries, cover;
 };
 
+// Number of lanes below this one with their bit set in mask m.
+__device__ __forceinline__ int lane_rank(uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 // Number of the wave's pixels with `a` set (both pixels of every lane).
 __device__ __forceinline__ int wave_count(const bool (&a)[kPix]) {
     int n = 0;
@@ -167,7 +182,7 @@ __device__ __forceinline__ void row_cross_term(const EdgeRec& E, float py, Geom&
 //   far, spans a row, flagged, right     row-span crossing term only;
 //   far, spans a row, flagged, left      nothing (its crossing term is 0);
 //   far, spans a row, not flagged        exact crossing term.
-template <int MODE, bool BEST, bool COUNT, bool CROSS>
+template <int MODE, int BEST, bool COUNT, bool CROSS>
 __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const WaveRect& W,
                                                cptr<EdgeRec> edges, float px,
                                                const float (&py)[kPix], Geom (&G)[kPix],
@@ -189,7 +204,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
         n.row += (uint64_t)__builtin_popcountll(mright) * npix;
     }
     const cptr<EdgeRec> ec = edges + c;
-    if constexpr (BEST) {
+    if constexpr (BEST > 0) {
         // Distance terms in ascending edge order (the first strict minimum
         // wins ties); the crossing terms' order does not matter.
         for (uint64_t todo = mdn; todo; todo &= todo - 1) {
@@ -200,7 +215,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
 #pragma unroll
             for (int p = 0; p < kPix; ++p) {
                 const float wy = py[p] - E.y0;
-                dist_term<true>(E, c + k, wx, wy, G[p]);
+                dist_term<BEST>(E, c + k, wx, wy, G[p]);
                 if (cross) cross_term(E, wx, wy, py[p], G[p]);
             }
         }
@@ -213,7 +228,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
 #pragma unroll
             for (int p = 0; p < kPix; ++p) {
                 const float wy = py[p] - E.y0;
-                dist_term<false>(E, 0, wx, wy, G[p]);
+                dist_term<0>(E, 0, wx, wy, G[p]);
                 cross_term(E, wx, wy, py[p], G[p]);
             }
         }
@@ -221,7 +236,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
             const EdgeRec E = load_edge(ec, (int)__builtin_ctzll(todo));
             const float wx = px - E.x0;
 #pragma unroll
-            for (int p = 0; p < kPix; ++p) dist_term<false>(E, 0, wx, py[p] - E.y0, G[p]);
+            for (int p = 0; p < kPix; ++p) dist_term<0>(E, 0, wx, py[p] - E.y0, G[p]);
         }
     }
     if constexpr (CROSS) {
@@ -245,7 +260,7 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
 // and crossing terms can matter.  The wave then visits only those edges, in
 // ascending index order (so the best edge is the first strict minimum, as in
 // the reference), loading each one's geometry through the scalar cache.
-template <int MODE, bool BEST, bool COUNT, bool CROSS>
+template <int MODE, int BEST, bool COUNT, bool CROSS>
 __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& W,
                                               const EdgeCull* __restrict__ culls,
                                               cptr<EdgeRec> edges, float px,
@@ -377,7 +392,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, const int32_t* __restrict__ tile_order,
     uint32_t* __restrict__ wave_cost, float* __restrict__ out, float* __restrict__ final_T,
-    int32_t* __restrict__ final_idx, uint4* __restrict__ inside_log,
+    int32_t* __restrict__ final_idx, RasterLog* __restrict__ raster_log,
     unsigned long long* __restrict__ counts) {
     const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
     const int tile = block_tile(tile_order, ntiles);
@@ -433,16 +448,26 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
             n.entries += 1;
         }
         Geom G[kPix];
-        prim_geometry<MODE, false, COUNT, MODE == 0>(pr, W, culls, edges, L.px, L.py, q, G, n,
-                                                     npix);
-        if constexpr (MODE == 0) {
-            // The wave's inside bits of this entry, for the backward.
-            const uint64_t in0 = __ballot(inside_of<MODE>(pr, G[0]));
-            const uint64_t in1 = __ballot(inside_of<MODE>(pr, G[kPix - 1]));
-            if (inside_log && (threadIdx.x & (kWave - 1)) == 0)
-                inside_log[2 * (size_t)g + wv] =
-                    make_uint4((uint32_t)in0, (uint32_t)(in0 >> 32), (uint32_t)in1,
-                               (uint32_t)(in1 >> 32));
+        prim_geometry<MODE, 1, COUNT, MODE == 0>(pr, W, culls, edges, L.px, L.py, q, G, n,
+                                                 npix);
+        if (raster_log) {
+            // This entry's inside and exact bits and the exact pixels' best
+            // edges, for the backward (which then needs no edge walk).
+            const uint64_t in0 = MODE == 0 ? (uint64_t)__ballot(inside_of<MODE>(pr, G[0])) : 0ull;
+            const uint64_t in1 =
+                MODE == 0 ? (uint64_t)__ballot(inside_of<MODE>(pr, G[kPix - 1])) : 0ull;
+            const bool ex0 = needs_exact<MODE>(pr, G[0], D2, D2o);
+            const bool ex1 = needs_exact<MODE>(pr, G[kPix - 1], D2, D2o);
+            const uint64_t x0 = __ballot(ex0), x1 = __ballot(ex1);
+            RasterLog* rec = raster_log + (2 * (size_t)g + wv);
+            if ((threadIdx.x & (kWave - 1)) == 0) {
+                *reinterpret_cast<uint4*>(rec->inside) = make_uint4(
+                    (uint32_t)in0, (uint32_t)(in0 >> 32), (uint32_t)in1, (uint32_t)(in1 >> 32));
+                *reinterpret_cast<uint4*>(rec->exact) = make_uint4(
+                    (uint32_t)x0, (uint32_t)(x0 >> 32), (uint32_t)x1, (uint32_t)(x1 >> 32));
+            }
+            if (ex0) rec->best[lane_rank(x0)] = G[0].best;
+            if (ex1) rec->best[__builtin_popcountll(x0) + lane_rank(x1)] = G[kPix - 1].best;
         }
         if constexpr (COUNT) {
             bool ex[kPix];
@@ -525,12 +550,12 @@ __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
 // its leaf interval [t0, t1] are read from its aux record (the CSR weights of
 // cubic_splatting.py:2432-2485) instead of being derived from its index.
 template <int MODE, bool COUNT, bool ADAPTIVE>
-__global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(6))) void k_raster_bwd(
+__global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(7))) void k_raster_bwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, const int32_t* __restrict__ tile_order, int eps, uint32_t eps_magic,
-    const EdgeAux* __restrict__ edge_aux, const uint4* __restrict__ inside_log_g,
+    const EdgeAux* __restrict__ edge_aux, const RasterLog* __restrict__ raster_log,
     const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
@@ -545,8 +570,6 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     const WaveRect W{ttx * kTile, ttx * kTile + kTile - 1, r0, r0 + kWaveRows - 1};
     const cptr<int32_t> prim_ids = as_const(prim_ids_g);
     const cptr<PrimRec> prims = as_const(prims_g);
-    const cptr<EdgeRec> edges = as_const(edges_g);
-    const cptr<uint4> inside_log = as_const(inside_log_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
     const float bg0 = bg[0], bg1 = bg[1], bg2 = bg[2];
     float T[kPix], T_final[kPix], v0[kPix], v1[kPix], v2[kPix], bg_dot[kPix];
@@ -574,12 +597,10 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     // The wave maximum is uniform; readfirstlane tells the compiler so, which
     // keeps every load that depends on the entry index scalar.
     const int gstart = min(g1 - 1, __builtin_amdgcn_readfirstlane(wave_max_i(fmax)));
-    // As in the forward, the next entry's first cull words are loaded one
-    // entry ahead (here the next entry is g - 1).
+    // The next entry's primitive id is loaded one entry ahead (here the next
+    // entry is g - 1).
     int pid = gstart >= g0 ? prim_ids[gstart] : 0;
     int pid_next = gstart >= g0 ? prim_ids[max(gstart - 1, g0)] : 0;
-    int4 q_next = gstart >= g0 ? load_culls(culls, prims[pid].e0, prims[pid].e1)
-                               : make_int4(0, -1, 0, -1);
     const int slot = reduce8_slot(lane & 7);
     const bool adder = (lane & ~7) == 8;
     for (int g = gstart; g >= g0; --g) {
@@ -592,29 +613,53 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
         }
         const int pid_cur = pid;
         const PrimRec pr = prims[pid_cur];
-        const int ne0 = prims[pid_next].e0, ne1 = prims[pid_next].e1;
         const int pid_after = prim_ids[max(g - 2, g0)];
-        const int4 q = q_next;
-        q_next = load_culls(culls, ne0, ne1);
         pid = pid_next;
         pid_next = pid_after;
         if (__ballot(any_valid) == 0) continue;
         const float D2 = pr.cull_d * pr.cull_d, D2o = pr.cull_out * pr.cull_out;
         if (prim_culled<MODE>(pr, W)) continue;
-        int npix = 0;
-        if constexpr (COUNT) {
-            npix = wave_count(valid);
-            n.entries += 1;
-        }
+        if constexpr (COUNT) n.entries += 1;
+        // The forward's log of this entry and wave: inside bits (its winding
+        // test), exact bits and each exact pixel's best edge, whose distance
+        // terms are recomputed here with the forward's expressions (so
+        // min_d2 is the forward's minimum).  Every other pixel is decided in
+        // closed form and needs no distance.  The index is kept inside the
+        // primitive's edge range.
         Geom G[kPix];
-        prim_geometry<MODE, true, COUNT, false>(pr, W, culls, edges, L.px, L.py, q, G, n, npix);
-        if constexpr (MODE == 0) {
-            // Inside bits from the forward's log (its winding test of the same
-            // pixel and entry), instead of the crossing terms.
-            const uint4 lg = inside_log[2 * (size_t)g + wv];
-            const uint64_t in0 = ((uint64_t)lg.y << 32) | lg.x, in1 = ((uint64_t)lg.w << 32) | lg.z;
-            G[0].winding = (int)((in0 >> lane) & 1u);
-            G[kPix - 1].winding = (int)((in1 >> lane) & 1u);
+        {
+            const RasterLog* rec = raster_log + (2 * (size_t)g + wv);
+            const cptr<uint4> hd = as_const(reinterpret_cast<const uint4*>(rec));
+            const uint4 hin = hd[0], hex = hd[1];
+            const uint64_t in[kPix] = {((uint64_t)hin.y << 32) | hin.x,
+                                       ((uint64_t)hin.w << 32) | hin.z};
+            const uint64_t xm[kPix] = {((uint64_t)hex.y << 32) | hex.x,
+                                       ((uint64_t)hex.w << 32) | hex.z};
+            if constexpr (COUNT)
+                n.dist += (uint64_t)(__builtin_popcountll(xm[0]) + __builtin_popcountll(xm[1]));
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) {
+                G[p].min_d2 = 1e30f;
+                G[p].winding = (int)((in[p] >> lane) & 1u);
+                G[p].best = -1;
+                G[p].bproj = G[p].bdx = G[p].bdy = 0.0f;
+                if ((xm[p] >> lane) & 1u) {
+                    const int slot = (p == 0 ? 0 : __builtin_popcountll(xm[0])) + lane_rank(xm[p]);
+                    const int e = min(max(rec->best[slot], pr.e0), pr.e1 - 1);
+                    const float4* er = reinterpret_cast<const float4*>(edges_g + e);
+                    const float4 a = er[0], b = er[1];
+                    EdgeRec E;
+                    E.x0 = a.x;
+                    E.y0 = a.y;
+                    E.x1 = a.z;
+                    E.y1 = a.w;
+                    E.vx = b.x;
+                    E.vy = b.y;
+                    E.ux = b.z;
+                    E.uy = b.w;
+                    dist_term<2>(E, e, L.px - E.x0, L.py[p] - E.y0, G[p]);
+                }
+            }
         }
         if constexpr (COUNT) {
             bool ex[kPix];
@@ -985,7 +1030,7 @@ struct RasterArgs {
     float* out;
     float* final_T;
     int32_t* final_idx;
-    uint4* inside_log;  // written by the forward, read by the backward (fill)
+    RasterLog* raster_log;  // written by the forward, read by the backward
     // backward inputs / outputs
     const float* fT;
     const int32_t* fidx;
@@ -1004,7 +1049,7 @@ template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
     hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.nt), dim3(kRasterThreads), 0,
                        a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.order, a.wave_cost, a.out, a.final_T, a.final_idx, a.inside_log,
+                       a.nt, a.order, a.wave_cost, a.out, a.final_T, a.final_idx, a.raster_log,
                        a.counts);
 }
 
@@ -1015,7 +1060,7 @@ static void launch_bwd3(const RasterArgs& a) {
         a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
     hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT, ADAPTIVE>), dim3(a.nt), dim3(kRasterThreads),
                        0, a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.order, a.eps, magic, a.aux, a.inside_log, a.fT, a.fidx, a.v_out,
+                       a.nt, a.order, a.eps, magic, a.aux, a.raster_log, a.fT, a.fidx, a.v_out,
                        a.v_cub, a.v_col,
                        a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.counts);
 }
@@ -1064,7 +1109,7 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                              const void* prim_recs, const float* background, int32_t img_h,
                              int32_t img_w, int32_t edges_per_segment, float* out_img,
                              float* final_Ts, int32_t* final_idx,
-                             void* inside_log, unsigned long long* eval_counts,
+                             void* raster_log, unsigned long long* eval_counts,
                              const int32_t* tile_order, uint32_t* wave_cost,
                              hipStream_t stream) {
     // The primitive records hold each primitive's edge range, so the forward
@@ -1077,7 +1122,7 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
     a.out = out_img;
     a.final_T = final_Ts;
     a.final_idx = final_idx;
-    a.inside_log = reinterpret_cast<uint4*>(inside_log);
+    a.raster_log = reinterpret_cast<RasterLog*>(raster_log);
     a.counts = eval_counts;
     a.order = tile_order;
     a.wave_cost = wave_cost;
@@ -1092,12 +1137,12 @@ extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted
                                     const float* background,
                                     int32_t img_h, int32_t img_w, int32_t edges_per_segment,
                                     float* out_img, float* final_Ts,
-                                    int32_t* final_idx, void* inside_log,
+                                    int32_t* final_idx, void* raster_log,
                                     const int32_t* tile_order, uint32_t* wave_cost,
                                     hipStream_t stream) {
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, edges_per_segment, out_img, final_Ts,
-                             final_idx, inside_log, nullptr, tile_order, wave_cost, stream);
+                             final_idx, raster_log, nullptr, tile_order, wave_cost, stream);
 }
 
 extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
@@ -1106,13 +1151,13 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
                                             const float* background, int32_t img_h,
                                             int32_t img_w, int32_t edges_per_segment,
                                             float* out_img, float* final_Ts, int32_t* final_idx,
-                                            void* inside_log, unsigned long long* eval_counts,
+                                            void* raster_log, unsigned long long* eval_counts,
                                             const int32_t* tile_order, uint32_t* wave_cost,
                                             hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, edges_per_segment, out_img, final_Ts,
-                             final_idx, inside_log, eval_counts, tile_order, wave_cost, stream);
+                             final_idx, raster_log, eval_counts, tile_order, wave_cost, stream);
 }
 
 static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
@@ -1124,7 +1169,7 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               float* v_cubics_px, float* v_colors, float* v_opacities,
                               float* v_inv_sigma2s, float* v_stroke_widths,
                               float* curve_contrib_rgb, float* curve_isect_contrib,
-                              const void* edge_aux, const void* inside_log,
+                              const void* edge_aux, const void* raster_log,
                               unsigned long long* eval_counts, const int32_t* tile_order,
                               hipStream_t stream) {
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 ||
@@ -1132,7 +1177,7 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
         img_w > kMaxImageDim)
         return CS_ERR_ARGS;
     if (mode == 1 && v_stroke_widths == nullptr) return CS_ERR_ARGS;
-    if (mode == 0 && inside_log == nullptr) return CS_ERR_ARGS;
+    if (raster_log == nullptr) return CS_ERR_ARGS;
     RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                                background, img_h, img_w, edges_per_segment, stream);
     a.fT = final_Ts;
@@ -1147,7 +1192,7 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
     a.c_isect = curve_isect_contrib;
     a.aux = reinterpret_cast<const EdgeAux*>(edge_aux);
     if (edge_aux) a.eps = 0;
-    a.inside_log = reinterpret_cast<uint4*>(const_cast<void*>(inside_log));
+    a.raster_log = reinterpret_cast<RasterLog*>(const_cast<void*>(raster_log));
     a.counts = eval_counts;
     a.order = tile_order;
     if (eval_counts) launch_bwd_mode<true>(a);
@@ -1161,7 +1206,7 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                                      const float* background,
                                      int32_t img_h, int32_t img_w,
                                      int32_t edges_per_segment, const float* final_Ts,
-                                     const int32_t* final_idx, const void* inside_log,
+                                     const int32_t* final_idx, const void* raster_log,
                                      const float* v_output,
                                      float* v_cubics_px, float* v_colors, float* v_opacities,
                                      float* v_inv_sigma2s, float* v_stroke_widths,
@@ -1172,21 +1217,21 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              inside_log, nullptr, tile_order, stream);
+                              raster_log, nullptr, tile_order, stream);
 }
 
 extern "C" int cs_rasterize_backward_de_casteljau(
     int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
     const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
     int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
-    const void* inside_log, const float* v_output, float* v_cubics_px, float* v_colors,
+    const void* raster_log, const float* v_output, float* v_cubics_px, float* v_colors,
     float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
     float* curve_isect_contrib, const int32_t* tile_order, hipStream_t stream) {
     if (!edge_aux) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, 0, final_Ts, final_idx, v_output,
                               v_cubics_px, v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
-                              curve_contrib_rgb, curve_isect_contrib, edge_aux, inside_log,
+                              curve_contrib_rgb, curve_isect_contrib, edge_aux, raster_log,
                               nullptr, tile_order, stream);
 }
 
@@ -1194,7 +1239,7 @@ extern "C" int cs_rasterize_backward_counted(
     int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
     const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
     int32_t img_w, int32_t edges_per_segment, const float* final_Ts, const int32_t* final_idx,
-    const void* inside_log, const float* v_output, float* v_cubics_px, float* v_colors,
+    const void* raster_log, const float* v_output, float* v_cubics_px, float* v_colors,
     float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
     float* curve_isect_contrib, unsigned long long* eval_counts, const int32_t* tile_order,
     hipStream_t stream) {
@@ -1203,7 +1248,7 @@ extern "C" int cs_rasterize_backward_counted(
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              inside_log, eval_counts, tile_order, stream);
+                              raster_log, eval_counts, tile_order, stream);
 }
 
 extern "C" int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,

@@ -163,8 +163,8 @@ class Binned:
         self.primitive_ids_sorted: Optional[torch.Tensor] = None
         # Heavy-first tile order from this forward's raster (for the backward).
         self.tile_order: Optional[torch.Tensor] = None
-        # The forward's inside bits per (list entry, wave) (fill; for the backward).
-        self.inside_log: Optional[torch.Tensor] = None
+        # The forward's raster log per (list entry, wave), for the backward.
+        self.raster_log: Optional[torch.Tensor] = None
         self.grad_accum_clean = True
         # Set while the intersection count has not been read on the host yet
         # (bin_primitives with a capacity hint); resolve_binned() settles it.
@@ -425,26 +425,24 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
     out = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
     ntiles = b.ntiles
     cap = max(int(b.primitive_ids_sorted.numel()), 1)
-    fill = b.mode == MODE_FILL
-    # final_Ts, final_idx, the next tile order and (fill) the inside bits of
-    # every (list entry, wave) for the backward share one allocation.
-    # The log's 16-byte records start on a 256-byte boundary.
-    o_ord = 2 * H * W
-    o_log = (o_ord + ntiles + 63) // 64 * 64
-    n_log = 2 * cap * N.INSIDE_LOG_INTS if fill else 0
-    aux = torch.empty((o_log + n_log,), dtype=torch.int32, device=dev)
+    # final_Ts, final_idx and the raster log of every (list entry, wave) for
+    # the backward share one allocation; the log's records start on a
+    # 256-byte boundary.
+    o_log = (2 * H * W + 63) // 64 * 64
+    aux = torch.empty((o_log + 2 * cap * N.RASTER_LOG_INTS,), dtype=torch.int32, device=dev)
     final_T = aux[:H * W].view(torch.float32).view(H, W)
-    final_idx = aux[H * W:o_ord].view(H, W)
-    order = aux[o_ord:o_ord + ntiles]
-    b.inside_log = aux[o_log:].view(2 * cap, N.INSIDE_LOG_INTS) if fill else None
+    final_idx = aux[H * W:2 * H * W].view(H, W)
+    b.raster_log = aux[o_log:].view(2 * cap, N.RASTER_LOG_INTS)
+    # The tile order is kept apart: the next forward reads it after this
+    # forward's buffers are gone.
+    order = torch.empty((ntiles,), dtype=torch.int32, device=dev)
     st = N.stream(dev)
     key = (dev.index, st, ntiles)
     prev = _TILE_ORDERS.get(key)
     base = aux.data_ptr()
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), H, W,
-            b.edges_per_segment, N.ptr(out), base, base + 4 * H * W,
-            base + 4 * o_log if fill else None)
+            b.edges_per_segment, N.ptr(out), base, base + 4 * H * W, base + 4 * o_log)
     cost = b.ptr("wave_cost")
     prev_p = None if prev is None else prev.data_ptr()
     if eval_counts is not None:
@@ -454,7 +452,7 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
         with N.prof("cubic.fwd.rast"):
             N.call("cs_rasterize_forward", *args, prev_p, cost, st)
     with N.prof("cubic.fwd.tile_order"):
-        N.call("cs_raster_tile_order", cost, ntiles, int(ORDER_CHUNKED), base + 4 * o_ord, st)
+        N.call("cs_raster_tile_order", cost, ntiles, int(ORDER_CHUNKED), order.data_ptr(), st)
     b.tile_order = order
     _TILE_ORDERS.pop(key, None)
     if len(_TILE_ORDERS) >= _MAX_ORDERS:
@@ -489,6 +487,8 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_opac = rest[3 * P: 4 * P]
     v_is2 = rest[4 * P: 5 * P]
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
+    if b.raster_log is None:
+        raise RuntimeError("the backward needs the raster log of a forward of this binning")
     if b.adaptive:
         if eval_counts is not None:
             raise ValueError("evaluation counts are measured on the uniform flattening only")
@@ -496,15 +496,13 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
             N.call("cs_rasterize_backward_de_casteljau", b.mode, N.ptr(b.primitive_ids_sorted),
                    b.ptr("tile_bins"), b.ptr("edges"), b.ptr("edge_culls"), b.ptr("prim_recs"),
                    N.ptr(background), b.img_h, b.img_w, b.ptr("edge_aux"), N.ptr(final_T),
-                   N.ptr(final_idx), N.ptr(b.inside_log), N.ptr(v_output), N.ptr(v_px), N.ptr(v_colors),
+                   N.ptr(final_idx), N.ptr(b.raster_log), N.ptr(v_output), N.ptr(v_px), N.ptr(v_colors),
                    N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
                    N.ptr(curve_isect_contrib), N.ptr(b.tile_order), N.stream(dev))
         return v_px, v_colors, v_opac, v_is2, v_sw
-    if b.mode == MODE_FILL and b.inside_log is None:
-        raise RuntimeError("the fill backward needs the inside log of a forward of this binning")
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
-            b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(b.inside_log),
+            b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(b.raster_log),
             N.ptr(v_output), N.ptr(v_px),
             N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
             N.ptr(curve_isect_contrib))
