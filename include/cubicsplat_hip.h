@@ -220,18 +220,19 @@ int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chun
                          int32_t* tile_order, hipStream_t stream);
 
 /* Raster log: for every list entry g a wave of tile rows processes, the
- * forward writes a 544-byte record at raster_log[2 g + wave]: the wave's
+ * forward writes a 1056-byte record at raster_log[2 g + wave]: the wave's
  * per-pixel inside bits (its winding test; zero for strokes) and exact bits
- * (pixels whose coverage needs the exact distance), each as two 64-bit lane
- * masks (32 bytes), then the best edge index (nearest, first strict minimum
- * in ascending edge order) of each exact pixel, packed in lane order (int32
- * [128]).  The backward of that forward reads it instead of re-running the
- * edge walk: it recomputes one distance term per exact pixel.  It holds 2 *
- * (capacity of prim_ids_sorted) records; required by the backward, NULL
- * allowed in the forward (then not written).  No reference counterpart: the
- * reference's backward re-runs the edge loop (ops/cubic_splatting.py:1451-1501,
- * ops/cubic_polyline_splatting.py:465-532). */
-#define CS_RASTER_LOG_BYTES 544
+ * (live pixels whose coverage needs the exact distance), each as two 64-bit
+ * lane masks (32 bytes), then for each exact pixel its best edge index
+ * (nearest, first strict minimum in ascending edge order) and the coverage it
+ * composited with, as (int32, float32 bits) pairs packed in lane order.  The
+ * backward of that forward reads it instead of re-running the edge walk and
+ * the coverage function: it recomputes one distance term per exact pixel.  It
+ * holds 2 * (capacity of prim_ids_sorted) records; required by the backward,
+ * NULL allowed in the forward (then not written).  No reference counterpart:
+ * the reference's backward re-runs the edge loop and the coverage
+ * (ops/cubic_splatting.py:1451-1530, ops/cubic_polyline_splatting.py:465-545). */
+#define CS_RASTER_LOG_BYTES 1056
 
 /* rasterize_cubic_fill_forward_kernel (ops/cubic_splatting.py:918-1194) when
  * mode 0, rasterize_cubic_polyline_forward_kernel

@@ -22,7 +22,7 @@ EDGE_CULL_INTS = 4       # 16-byte edge cull record
 MAX_IMAGE_DIM = 16384
 SEG_RECORD_INTS = 8      # 32-byte segment record
 PRIM_RECORD_FLOATS = 20  # 80-byte primitive record
-RASTER_LOG_INTS = 136    # 544-byte raster log record per (list entry, wave)
+RASTER_LOG_INTS = 264    # 1056-byte raster log record per (list entry, wave)
 EDGE_AUX_INTS = 4        # 16-byte (segment, t0, t1) record of the adaptive flattening
 
 _P = ctypes.c_void_p

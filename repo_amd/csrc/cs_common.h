@@ -93,15 +93,16 @@ struct alignas(16) EdgeAux {
 
 // Raster log of one (list entry, wave of tile rows), written by the forward
 // and read by the backward of that forward: the per-pixel inside bits (the
-// winding test; zero for strokes) and exact bits (pixels whose coverage needs
-// the exact distance, all others being decided in closed form), each as one
-// 64-bit lane mask per pixel row p of the lanes, then the best edge (nearest,
-// first strict minimum in ascending edge order) of every exact pixel, packed
-// in lane order: the exact pixels of row 0, then those of row 1.
+// winding test; zero for strokes) and exact bits (live pixels whose coverage
+// needs the exact distance, all others being decided in closed form), each as
+// one 64-bit lane mask per pixel row p of the lanes, then for every exact
+// pixel its best edge (nearest, first strict minimum in ascending edge order)
+// and the coverage the forward composited with, packed in lane order: the
+// exact pixels of row 0, then those of row 1.
 struct alignas(16) RasterLog {
     uint32_t inside[2 * kPix];
     uint32_t exact[2 * kPix];
-    int32_t best[kWave * kPix];
+    int2 px[kWave * kPix];  // (best edge, coverage bits)
 };
 
 // Per cubic segment: the unions of its edges' ranges, plus the last pixel

@@ -450,36 +450,36 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
         Geom G[kPix];
         prim_geometry<MODE, 1, COUNT, MODE == 0>(pr, W, culls, edges, L.px, L.py, q, G, n,
                                                  npix);
+        // This entry's inside and exact bits, and below each exact pixel's
+        // best edge and coverage, for the backward (which then needs neither
+        // the edge walk nor the exact coverage).
+        bool ex[kPix];
+#pragma unroll
+        for (int p = 0; p < kPix; ++p) ex[p] = !done[p] && needs_exact<MODE>(pr, G[p], D2, D2o);
+        RasterLog* rec = nullptr;
+        int slot[kPix] = {0, 0};
         if (raster_log) {
-            // This entry's inside and exact bits and the exact pixels' best
-            // edges, for the backward (which then needs no edge walk).
             const uint64_t in0 = MODE == 0 ? (uint64_t)__ballot(inside_of<MODE>(pr, G[0])) : 0ull;
             const uint64_t in1 =
                 MODE == 0 ? (uint64_t)__ballot(inside_of<MODE>(pr, G[kPix - 1])) : 0ull;
-            const bool ex0 = needs_exact<MODE>(pr, G[0], D2, D2o);
-            const bool ex1 = needs_exact<MODE>(pr, G[kPix - 1], D2, D2o);
-            const uint64_t x0 = __ballot(ex0), x1 = __ballot(ex1);
-            RasterLog* rec = raster_log + (2 * (size_t)g + wv);
+            const uint64_t x0 = __ballot(ex[0]), x1 = __ballot(ex[kPix - 1]);
+            rec = raster_log + (2 * (size_t)g + wv);
             if ((threadIdx.x & (kWave - 1)) == 0) {
                 *reinterpret_cast<uint4*>(rec->inside) = make_uint4(
                     (uint32_t)in0, (uint32_t)(in0 >> 32), (uint32_t)in1, (uint32_t)(in1 >> 32));
                 *reinterpret_cast<uint4*>(rec->exact) = make_uint4(
                     (uint32_t)x0, (uint32_t)(x0 >> 32), (uint32_t)x1, (uint32_t)(x1 >> 32));
             }
-            if (ex0) rec->best[lane_rank(x0)] = G[0].best;
-            if (ex1) rec->best[__builtin_popcountll(x0) + lane_rank(x1)] = G[kPix - 1].best;
+            slot[0] = lane_rank(x0);
+            slot[kPix - 1] = __builtin_popcountll(x0) + lane_rank(x1);
         }
-        if constexpr (COUNT) {
-            bool ex[kPix];
-#pragma unroll
-            for (int p = 0; p < kPix; ++p)
-                ex[p] = live[p] && needs_exact<MODE>(pr, G[p], D2, D2o);
-            n.cover += (uint64_t)wave_count(ex);
-        }
+        if constexpr (COUNT) n.cover += (uint64_t)wave_count(ex);
 #pragma unroll
         for (int p = 0; p < kPix; ++p) {
             if (done[p]) continue;
             const Cov c = coverage<MODE>(pr, G[p], D2, D2o);
+            if (rec && ex[p])
+                rec->px[slot[p]] = make_int2(G[p].best, __builtin_bit_cast(int, c.cov));
             const float alpha = fminf(kAlphaCap, pr.opacity * c.cov);
             if (alpha >= kAlphaMin) {
                 const float nT = T[p] * (1.0f - alpha);
@@ -534,6 +534,34 @@ __device__ __forceinline__ void basis_at(float t, float b[4]) {
 // The same at t = e / eps for edge e of a uniformly flattened segment.
 __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
     basis_at((float)e * inv_e, b);
+}
+
+// Masks of a raster log record (scalar loads; g and wave are uniform).
+struct LogHead {
+    uint64_t in[kPix], xm[kPix];
+};
+
+__device__ __forceinline__ LogHead log_head(const RasterLog* __restrict__ log, int g, int wave) {
+    const cptr<uint4> hd =
+        as_const(reinterpret_cast<const uint4*>(log + (2 * (size_t)g + wave)));
+    const uint4 a = hd[0], b = hd[1];
+    LogHead h;
+    h.in[0] = ((uint64_t)a.y << 32) | a.x;
+    h.in[1] = ((uint64_t)a.w << 32) | a.z;
+    h.xm[0] = ((uint64_t)b.y << 32) | b.x;
+    h.xm[1] = ((uint64_t)b.w << 32) | b.z;
+    return h;
+}
+
+// The lane's (best edge, coverage) pairs of record (g, wave) for its exact
+// pixels (others keep their value).
+__device__ __forceinline__ void log_pixels(const RasterLog* __restrict__ log, int g, int wave,
+                                           const LogHead& h, int lane, int2 (&px)[kPix]) {
+    const RasterLog* rec = log + (2 * (size_t)g + wave);
+#pragma unroll
+    for (int p = 0; p < kPix; ++p)
+        if ((h.xm[p] >> lane) & 1u)
+            px[p] = rec->px[(p == 0 ? 0 : __builtin_popcountll(h.xm[0])) + lane_rank(h.xm[p])];
 }
 
 // Backward: the reverse traversal of cubic_splatting.py:1339-1649 (fill) and
@@ -617,35 +645,36 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
         pid = pid_next;
         pid_next = pid_after;
         if (__ballot(any_valid) == 0) continue;
-        const float D2 = pr.cull_d * pr.cull_d, D2o = pr.cull_out * pr.cull_out;
         if (prim_culled<MODE>(pr, W)) continue;
         if constexpr (COUNT) n.entries += 1;
         // The forward's log of this entry and wave: inside bits (its winding
-        // test), exact bits and each exact pixel's best edge, whose distance
-        // terms are recomputed here with the forward's expressions (so
-        // min_d2 is the forward's minimum).  Every other pixel is decided in
-        // closed form and needs no distance.  The index is kept inside the
-        // primitive's edge range.
+        // test), exact bits, and each exact pixel's best edge and coverage.
+        // The best edge's distance term is recomputed here with the
+        // forward's expressions (so min_d2 is the forward's minimum; the
+        // index is kept inside the primitive's edge range); the coverage is
+        // the forward's own value.  Every other pixel is decided in closed
+        // form and needs no distance.
         Geom G[kPix];
+        bool exact[kPix];
+        float lcov[kPix];
         {
-            const RasterLog* rec = raster_log + (2 * (size_t)g + wv);
-            const cptr<uint4> hd = as_const(reinterpret_cast<const uint4*>(rec));
-            const uint4 hin = hd[0], hex = hd[1];
-            const uint64_t in[kPix] = {((uint64_t)hin.y << 32) | hin.x,
-                                       ((uint64_t)hin.w << 32) | hin.z};
-            const uint64_t xm[kPix] = {((uint64_t)hex.y << 32) | hex.x,
-                                       ((uint64_t)hex.w << 32) | hex.z};
+            const LogHead h = log_head(raster_log, g, wv);
+            int2 lpx[kPix] = {make_int2(0, 0), make_int2(0, 0)};
+            log_pixels(raster_log, g, wv, h, lane, lpx);
             if constexpr (COUNT)
-                n.dist += (uint64_t)(__builtin_popcountll(xm[0]) + __builtin_popcountll(xm[1]));
+                n.dist += (uint64_t)(__builtin_popcountll(h.xm[0]) +
+                                     __builtin_popcountll(h.xm[1]));
 #pragma unroll
             for (int p = 0; p < kPix; ++p) {
                 G[p].min_d2 = 1e30f;
-                G[p].winding = (int)((in[p] >> lane) & 1u);
+                G[p].winding = (int)((h.in[p] >> lane) & 1u);
                 G[p].best = -1;
                 G[p].bproj = G[p].bdx = G[p].bdy = 0.0f;
-                if ((xm[p] >> lane) & 1u) {
-                    const int slot = (p == 0 ? 0 : __builtin_popcountll(xm[0])) + lane_rank(xm[p]);
-                    const int e = min(max(rec->best[slot], pr.e0), pr.e1 - 1);
+                exact[p] = (h.xm[p] >> lane) & 1u;
+                lcov[p] = 0.0f;
+                if (exact[p]) {
+                    lcov[p] = __builtin_bit_cast(float, lpx[p].y);
+                    const int e = min(max(lpx[p].x, pr.e0), pr.e1 - 1);
                     const float4* er = reinterpret_cast<const float4*>(edges_g + e);
                     const float4 a = er[0], b = er[1];
                     EdgeRec E;
@@ -664,8 +693,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
         if constexpr (COUNT) {
             bool ex[kPix];
 #pragma unroll
-            for (int p = 0; p < kPix; ++p)
-                ex[p] = valid[p] && needs_exact<MODE>(pr, G[p], D2, D2o);
+            for (int p = 0; p < kPix; ++p) ex[p] = valid[p] && exact[p];
             n.cover += (uint64_t)wave_count(ex);
         }
         // Per-primitive sums over the lane's pixels: v_r, v_g, v_b, v_opacity,
@@ -680,7 +708,15 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             gx[p] = gy[p] = 0.0f;
             geom[p] = false;
             if (!valid[p]) continue;
-            const Cov c = coverage<MODE>(pr, G[p], D2, D2o);
+            // coverage() of the forward: its value for exact pixels, the
+            // closed form otherwise.  The distance only feeds gradients
+            // (hardware square root, within 1 ulp).
+            Cov c;
+            const bool inside = inside_of<MODE>(pr, G[p]);
+            c.sgn = inside ? -1.0f : 1.0f;
+            c.cov = exact[p] ? lcov[p] : (inside ? 1.0f : 0.0f);
+            c.dist = exact[p] ? __builtin_amdgcn_sqrtf(fmaxf(G[p].min_d2, 0.0f)) : 0.0f;
+            c.ed = (MODE == 1 && exact[p]) ? fmaxf(0.0f, c.dist - pr.half_sw) : 0.0f;
             const float op = pr.opacity;
             const float alpha = fminf(kAlphaCap, op * c.cov);
             if (!(alpha >= kAlphaMin)) continue;
