@@ -664,29 +664,31 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             if constexpr (COUNT)
                 n.dist += (uint64_t)(__builtin_popcountll(h.xm[0]) +
                                      __builtin_popcountll(h.xm[1]));
+            // Only exact pixels read G's distance fields (closed-form pixels
+            // have dist 0 and no geometry gradient), so they are assigned
+            // directly from the best edge: its d2 is the forward's minimum.
+            const char* ebase = reinterpret_cast<const char*>(edges_g);
 #pragma unroll
             for (int p = 0; p < kPix; ++p) {
-                G[p].min_d2 = 1e30f;
                 G[p].winding = (int)((h.in[p] >> lane) & 1u);
-                G[p].best = -1;
-                G[p].bproj = G[p].bdx = G[p].bdy = 0.0f;
                 exact[p] = (h.xm[p] >> lane) & 1u;
-                lcov[p] = 0.0f;
+                lcov[p] = __builtin_bit_cast(float, lpx[p].y);
+                const int e = min(max(lpx[p].x, pr.e0), pr.e1 - 1);
+                G[p].best = e;
+                G[p].min_d2 = G[p].bproj = G[p].bdx = G[p].bdy = 0.0f;
                 if (exact[p]) {
-                    lcov[p] = __builtin_bit_cast(float, lpx[p].y);
-                    const int e = min(max(lpx[p].x, pr.e0), pr.e1 - 1);
-                    const float4* er = reinterpret_cast<const float4*>(edges_g + e);
+                    const float4* er = reinterpret_cast<const float4*>(
+                        ebase + (size_t)(uint32_t)e * sizeof(EdgeRec));
                     const float4 a = er[0], b = er[1];
-                    EdgeRec E;
-                    E.x0 = a.x;
-                    E.y0 = a.y;
-                    E.x1 = a.z;
-                    E.y1 = a.w;
-                    E.vx = b.x;
-                    E.vy = b.y;
-                    E.ux = b.z;
-                    E.uy = b.w;
-                    dist_term<2>(E, e, L.px - E.x0, L.py[p] - E.y0, G[p]);
+                    const float wx = L.px - a.x, wy = L.py[p] - a.y;
+                    float proj = __builtin_fmaf(wx, b.z, wy * b.w);
+                    proj = fminf(fmaxf(proj, 0.0f), 1.0f);
+                    const float dx = __builtin_fmaf(proj, b.x, -wx);
+                    const float dy = __builtin_fmaf(proj, b.y, -wy);
+                    G[p].min_d2 = __builtin_fmaf(dx, dx, dy * dy);
+                    G[p].bproj = proj;
+                    G[p].bdx = dx;
+                    G[p].bdy = dy;
                 }
             }
         }
