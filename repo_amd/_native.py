@@ -158,9 +158,12 @@ class _HipRuntime:
     def __init__(self):
         L = ctypes.CDLL(LIB_PATH)
         lib()
+        fast = _fast_module()
         for name, (res, args) in _HIP_SIGNATURES.items():
-            fn = getattr(L, name)
-            fn.restype, fn.argtypes = res, args
+            fn = getattr(fast, name, None) if fast is not None else None
+            if fn is None:
+                fn = getattr(L, name)
+                fn.restype, fn.argtypes = res, args
             setattr(self, name, fn)
 
 
@@ -232,12 +235,29 @@ def check(rc: int, what: str) -> None:
 
 
 _FUNCS = {}
+_FAST = False   # not looked up yet
+
+
+def _fast_module():
+    """The compiled binding of the same entry points (repo_amd/fastcall.py),
+    or None when it has not been built (ctypes is used then)."""
+    global _FAST
+    if _FAST is False:
+        try:
+            from . import _cs_fast
+        except ImportError:
+            _cs_fast = None
+        _FAST = _cs_fast
+    return _FAST
 
 
 def call(name: str, *args) -> None:
     fn = _FUNCS.get(name)
     if fn is None:
-        fn = _FUNCS[name] = getattr(lib(), name)
+        L = lib()
+        fast = _fast_module()
+        fn = getattr(fast, name, None) if fast is not None else None
+        _FUNCS[name] = fn = fn if fn is not None else getattr(L, name)
     rc = fn(*args)
     if rc != CS_OK:
         check(rc, name)

@@ -52,6 +52,8 @@ def build(verbose: bool = False) -> str:
         print(" ".join(cmd), flush=True)
     subprocess.check_call(cmd)
     os.replace(tmp, LIB)
+    from . import fastcall
+    fastcall.build(LIB, verbose=verbose)
     return LIB
 
 

@@ -270,3 +270,25 @@ def test_fused_ops_argument_errors():
         fused.mse_ssim_loss(x, torch.rand(1, 3, 16, 15))
     with pytest.raises(ValueError):
         fused.mse_ssim_loss(x, x, win_size=4)
+
+
+def test_compiled_binding_matches_ctypes():
+    """repo_amd/_cs_fast (built by build()) wraps every int-returning entry
+    point of the signature tables; it checks its argument count and returns
+    the same status as the ctypes path for arguments the library rejects
+    before any HIP call."""
+    import ctypes
+    from repo_amd import _native as N, fastcall
+    fast = N._fast_module()
+    assert fast is not None, "build() compiles repo_amd/_cs_fast"
+    names = [n for n, _ in fastcall.entry_points()]
+    assert "cs_rasterize_forward" in names and "hipEventRecord" in names
+    for n in names:
+        assert callable(getattr(fast, n)), n
+    with pytest.raises(TypeError):
+        fast.cs_raster_tile_order(None, 0)
+    lib = N.lib()
+    for args in ((None, 0, 1, None, None), (None, 16, 1, None, None)):
+        assert fast.cs_raster_tile_order(*args) == lib.cs_raster_tile_order(*args) == N.CS_ERR_ARGS
+    buf = (ctypes.c_uint32 * 4)()
+    assert fast.cs_raster_tile_order(buf, -3, 0, buf, None) == N.CS_ERR_ARGS
