@@ -268,8 +268,9 @@ def copy_calibration(mib):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; the screen-space sharding "
-                                   "design is described in DESIGN.md", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only (several GPUs would each "
+                                   "own a band of tile rows; not implemented here)",
+                          "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
     from repo_amd import _native, profiling
