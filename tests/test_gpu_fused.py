@@ -44,7 +44,7 @@ def test_mse_ssim_loss_matches_separate_calls_and_oracle(shape, weight):
     loss, parts = fused.mse_ssim_loss(xd, y.cuda(), weight)
     sep = manbo.mse_loss_tilelang(x.cuda(), y.cuda()) + weight * (1 - manbo.ssim(x.cuda(),
                                                                                  y.cuda()))
-    assert abs(float(loss) - float(sep)) <= 2e-6 * abs(float(sep))
+    assert abs(float(loss.detach()) - float(sep)) <= 2e-6 * abs(float(sep))
     x64 = x.double().requires_grad_(True)
     ref = ((x64 - y.double()) ** 2).mean() + weight * (1 - O.ssim_torch64(x64, y.double()))
     assert abs(float(loss) - float(ref)) <= 1e-5 * abs(float(ref))
@@ -111,7 +111,7 @@ def test_clamp_mse_ssim_loss_on_hwc_image(h, w, weight):
     x = img.cuda().clamp(0, 1).permute(2, 0, 1).unsqueeze(0).contiguous()
     sep_mse = manbo.mse_loss_tilelang(x, y.cuda())
     sep = sep_mse + weight * (1 - manbo.ssim(x, y.cuda()))
-    assert abs(float(loss) - float(sep)) <= 2e-6 * abs(float(sep))
+    assert abs(float(loss.detach()) - float(sep)) <= 2e-6 * abs(float(sep))
     assert abs(float(parts[0]) - float(sep_mse)) <= 2e-6 * abs(float(sep_mse))
     i64 = img.double().requires_grad_(True)
     x64 = i64.clamp(0, 1).permute(2, 0, 1).unsqueeze(0)

@@ -360,3 +360,51 @@ def test_widths_below_floor_match_the_clamped_widths():
     low = raw < 1e-4
     assert float(wg.grad[low].abs().max()) == 0.0
     assert float(wg.grad[~low].abs().max()) > 0.0
+
+
+@pytest.mark.gpu
+def test_count_overflow_redo_keeps_backward_consistent():
+    """A forward whose intersection count exceeds the capacity hint rebuilds
+    the lists and re-rasterizes into new buffers (including the raster log);
+    the backward must use the second forward's log.  Small shapes set a small
+    hint, shapes enlarged 30x about their centroids overflow it: the image is
+    bit-identical and the gradients match (atomics order) a run without a hint."""
+    import manbo
+    print("[overflow redo]", flush=True)
+    sc = synth.small_scene(8, P=40, h=512, w=512, rmax=8.0).to("cuda")
+    P, nseg = sc.num_primitives, sc.cubics_norm.shape[0] // sc.num_primitives
+    cub = sc.cubics_norm.view(P, nseg, 4, 2)
+    centre = cub.mean(dim=(1, 2), keepdim=True)
+    big = (centre + 30.0 * (cub - centre)).reshape(-1, 4, 2).contiguous()
+    wgt = random_v_out(sc.img_h, sc.img_w).cuda()
+    redo = []
+    orig = splat.resolve_binned
+
+    def spy(b):
+        r = orig(b)
+        redo.append(r)
+        return r
+
+    def run(c0):
+        c = c0.clone().requires_grad_(True)
+        col = sc.colors.clone().requires_grad_(True)
+        img = manbo.ops.render_cubic_fill_splat_tilelang(
+            c, sc.seg_offsets, col, sc.opacities, sc.depths, sc.img_h, sc.img_w, 16, 16,
+            sc.background, distance_samples=sc.S)
+        (img * wgt).sum().backward()
+        return img.detach(), c.grad, col.grad
+
+    splat._CAPACITY_HINTS.clear()
+    splat.resolve_binned = spy
+    try:
+        run(sc.cubics_norm)
+        img1, gc1, gk1 = run(big)
+    finally:
+        splat.resolve_binned = orig
+    assert redo == [False, True], redo
+    splat._CAPACITY_HINTS.clear()
+    img2, gc2, gk2 = run(big)
+    assert torch.equal(img1, img2)
+    for a, r in ((gc1, gc2), (gk1, gk2)):
+        ok, err = grad_scale_tol(a.cpu().numpy(), r.cpu().numpy(), rtol=1e-5)
+        assert ok, err
