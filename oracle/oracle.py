@@ -266,26 +266,73 @@ def _scene(b, colors, opacities, fill_rules, stroke_widths, background, img_h, i
                   _p(arrs["bg"]).value, img_h, img_w, block_x, block_y, mode)
 
 
+def default_workers() -> int:
+    """Threads for the banded raster: the usable CPUs, at most 16."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def row_bands(rows, img_h: int):
+    """``rows`` as a list of disjoint [a, b) row ranges: None is the whole
+    image, (a, b) one band, a list of such pairs several."""
+    if rows is None:
+        return [(0, int(img_h))]
+    if len(rows) == 2 and not hasattr(rows[0], "__len__"):
+        rows = [rows]
+    out = sorted((max(0, int(a)), min(int(img_h), int(b))) for a, b in rows)
+    for (a0, b0), (a1, _) in zip(out, out[1:]):
+        if a1 < b0:
+            raise ValueError(f"row bands overlap: {out}")
+    return [(a, b) for a, b in out if b > a]
+
+
+def _run_bands(fn, bands, workers: int, band_rows: int = 16) -> None:
+    """fn(a, b) over every row band, cut into pieces of band_rows rows and run
+    on `workers` threads (one call per band when workers is 1)."""
+    workers = max(1, int(workers))
+    if workers == 1:
+        for a, b in bands:
+            fn(a, b)
+        return
+    from concurrent.futures import ThreadPoolExecutor
+    pieces = [(a, min(a + band_rows, b)) for r0, b in bands for a in range(r0, b, band_rows)]
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        for f in [ex.submit(fn, a, b) for a, b in pieces]:
+            f.result()
+
+
 def raster_forward(b, colors, opacities, background, img_h, img_w, *, fill_rules=None,
-                   stroke_widths=None, mode=0, block_x=16, block_y=16, rows=None):
+                   stroke_widths=None, mode=0, block_x=16, block_y=16, rows=None, workers=1):
     """Forward raster; ``rows=(r0, r1)`` restricts it to pixel rows [r0, r1)
-    (other pixels are left as background, T=1, idx=0)."""
+    and a list of such pairs to those bands (other pixels are left as
+    background, T=1, idx=0).  ``workers`` > 1 splits
+    the rows into bands rasterized by that many threads (the C restatement
+    holds no global state and ctypes releases the GIL); every pixel's result is
+    the same as in one pass."""
     keep = []
     sc = _scene(b, colors, opacities, fill_rules, stroke_widths, background, img_h, img_w,
                 block_x, block_y, mode, keep)
-    r0, r1 = (0, img_h) if rows is None else (int(rows[0]), int(rows[1]))
+    bands = row_bands(rows, img_h)
     out = np.empty((img_h, img_w, 3), np.float32)
     out[:] = _f32(background).reshape(1, 1, 3)
     T = np.ones((img_h, img_w), np.float32)
     idx = np.zeros((img_h, img_w), np.int32)
-    lib().orc_raster_forward(ctypes.byref(sc), ctypes.c_int32(r0), ctypes.c_int32(r1), _p(out),
-                             _p(T), _p(idx))
+
+    def band(a, b):
+        lib().orc_raster_forward(ctypes.byref(sc), ctypes.c_int32(a), ctypes.c_int32(b),
+                                 _p(out), _p(T), _p(idx))
+
+    # Bands write disjoint rows of the outputs.
+    _run_bands(band, bands, workers)
     return out, T, idx
 
 
 def raster_backward(b, colors, opacities, background, img_h, img_w, final_T, final_idx,
                     v_out, *, fill_rules=None, stroke_widths=None, mode=0, block_x=16,
-                    block_y=16, rows=None):
+                    block_y=16, rows=None, workers=1):
     keep = []
     sc = _scene(b, colors, opacities, fill_rules, stroke_widths, background, img_h, img_w,
                 block_x, block_y, mode, keep)
@@ -297,10 +344,24 @@ def raster_backward(b, colors, opacities, background, img_h, img_w, final_T, fin
     v_is2 = np.zeros(P, np.float64)
     v_sw = np.zeros(P, np.float64)
     fT, fi, vo = _f32(final_T), _i32(final_idx), _f32(v_out)
-    r0, r1 = (0, img_h) if rows is None else (int(rows[0]), int(rows[1]))
-    lib().orc_raster_backward(ctypes.byref(sc), ctypes.c_int32(r0), ctypes.c_int32(r1), _p(fT),
-                              _p(fi), _p(vo), _p(v_edges), _p(v_col), _p(v_op), _p(v_is2),
-                              _p(v_sw))
+    bands = row_bands(rows, img_h)
+    acc = [v_edges, v_col, v_op, v_is2, v_sw]
+    parts = []
+    single = workers <= 1
+
+    def band(a, b):
+        # With threads, each band sums into its own float64 accumulators, which
+        # are added afterwards (the sums' order differs by rounding only).
+        mine = acc if single else [np.zeros_like(x) for x in acc]
+        lib().orc_raster_backward(ctypes.byref(sc), ctypes.c_int32(a), ctypes.c_int32(b),
+                                  _p(fT), _p(fi), _p(vo), *[_p(x) for x in mine])
+        if mine is not acc:
+            parts.append(mine)
+
+    _run_bands(band, bands, workers)
+    for part in parts:
+        for x, y in zip(acc, part):
+            x += y
     return dict(v_edges=v_edges, v_colors=v_col, v_opacities=v_op, v_inv_sigma2s=v_is2,
                 v_stroke_widths=v_sw)
 
@@ -376,7 +437,7 @@ def accumulate_edge_grads_csr(v_edges, seo, t_starts, t_ends, nseg: int) -> np.n
 def render_forward(cubics_norm, offs, colors, opacities, depths, img_h, img_w, background, *,
                    fill_rules=None, aa_widths=None, aa_width=1.0, S=24, stroke_widths=None,
                    block_x=16, block_y=16, aabb_pad=1.0, aniso=False, rows=None,
-                   flatten_method="bernstein"):
+                   flatten_method="bernstein", workers=1):
     """Whole forward of _CubicFillSplatFunction (cubic_splatting.py:2752-2962) or,
     with stroke_widths, _CubicPolylineSplatFunction (cubic_polyline_splatting.py:964-1173)."""
     offs = _i32(offs)
@@ -389,8 +450,9 @@ def render_forward(cubics_norm, offs, colors, opacities, depths, img_h, img_w, b
                   aabb_pad=aabb_pad, aniso=aniso, flatten_method=flatten_method)
     out, T, idx = raster_forward(b, colors, opacities, background, img_h, img_w,
                                  fill_rules=fill_rules, stroke_widths=stroke_widths, mode=mode,
-                                 block_x=block_x, block_y=block_y, rows=rows)
-    b.update(rows=rows, out=out, final_T=T, final_idx=idx, mode=mode, colors=_f32(colors),
+                                 block_x=block_x, block_y=block_y, rows=rows,
+                                 workers=workers)
+    b.update(rows=rows, workers=workers, out=out, final_T=T, final_idx=idx, mode=mode, colors=_f32(colors),
              opacities=_f32(opacities).reshape(-1), fill_rules=fill_rules,
              stroke_widths=stroke_widths, background=_f32(background).reshape(3),
              img_h=img_h, img_w=img_w, block_x=block_x, block_y=block_y,
@@ -405,7 +467,7 @@ def render_backward(fw, v_out):
                         fw["img_w"], fw["final_T"], fw["final_idx"], v_out,
                         fill_rules=fw["fill_rules"], stroke_widths=fw["stroke_widths"],
                         mode=fw["mode"], block_x=fw["block_x"], block_y=fw["block_y"],
-                        rows=fw.get("rows"))
+                        rows=fw.get("rows"), workers=fw.get("workers", 1))
     if fw.get("flatten_method") == "de_casteljau":
         v_px = accumulate_edge_grads_csr(g["v_edges"], fw["segment_edge_offsets"],
                                          fw["edge_t_starts"], fw["edge_t_ends"], fw["nseg"])
@@ -462,6 +524,38 @@ def ssim_torch64(x, y, win_size=11, win_sigma=1.5, data_range=1.0, k1=0.01, k2=0
     s12 = exy - mu1 * mu2
     m = ((2 * mu1 * mu2 + c1) / (mu1 * mu1 + mu2 * mu2 + c1)) * ((2 * s12 + c2) / (s1 + s2 + c2))
     return m.view(n, c, -1).mean(-1).mean()
+
+
+def ssim64_separable(x, y, win_size=11, win_sigma=1.5, data_range=1.0, k1=0.01, k2=0.03,
+                     size_average=True, nonnegative=False):
+    """The same SSIM as ssim_torch64 with the window applied as two 1D passes
+    (rows, then columns): outer(g, g) * z = g_col * (g_row * z), so the value
+    agrees to float64 rounding, at 2 win instead of win^2 multiply-adds per
+    output (fast enough for full frames).  Returns the mean over pixels and
+    channels, or with size_average=False the per-image means [N]
+    (metric.py:262-273); nonnegative clamps each channel mean at 0 first."""
+    import torch
+    import torch.nn.functional as F
+    g = torch.from_numpy(gaussian_window_1d(win_size, win_sigma).astype(np.float64)).to(x.dtype)
+    n, c, h, wd = x.shape
+    kr = g.view(1, 1, 1, win_size)
+    kc = g.view(1, 1, win_size, 1)
+    z = torch.cat([x, y, x * x, y * y, x * y], 1).reshape(n * c * 5, 1, h, wd)
+    f = F.conv2d(F.conv2d(z, kr), kc).view(n, 5, c, h - win_size + 1, wd - win_size + 1)
+    # The channel-major cat above stacks (x, y, x^2, y^2, xy) per image.
+    f = f.view(n, 5, c, -1)
+    mu1, mu2, ex2, ey2, exy = (f[:, k] for k in range(5))
+    c1 = (k1 * data_range) ** 2
+    c2 = (k2 * data_range) ** 2
+    s1 = ex2 - mu1 * mu1
+    s2 = ey2 - mu2 * mu2
+    s12 = exy - mu1 * mu2
+    m = ((2 * mu1 * mu2 + c1) / (mu1 * mu1 + mu2 * mu2 + c1)) * ((2 * s12 + c2) / (s1 + s2 + c2))
+    per_channel = m.mean(-1)
+    if nonnegative:
+        per_channel = torch.relu(per_channel)
+    per_image = per_channel.mean(-1)
+    return per_image.mean() if size_average else per_image
 
 
 # ------------------------------------------------ closed ring -> Hermite cubics

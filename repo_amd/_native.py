@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import warnings
 from contextlib import nullcontext
 from typing import Callable, ContextManager, Optional
 
@@ -247,6 +248,12 @@ def _fast_module():
             from . import _cs_fast
         except ImportError:
             _cs_fast = None
+        if _cs_fast is not None:
+            from . import fastcall
+            if _cs_fast.signature_hash() != fastcall.signature_hash():
+                warnings.warn("repo_amd._cs_fast was built from other entry-point signatures; "
+                              "using ctypes (run build() again)")
+                _cs_fast = None
         _FAST = _cs_fast
     return _FAST
 

@@ -20,6 +20,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+import warnings
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -53,7 +54,12 @@ def build(verbose: bool = False) -> str:
     subprocess.check_call(cmd)
     os.replace(tmp, LIB)
     from . import fastcall
-    fastcall.build(LIB, verbose=verbose)
+    try:
+        fastcall.build(LIB, verbose=verbose)
+    except (OSError, subprocess.CalledProcessError) as e:
+        # The compiled binding is an optional speed-up: without it the host
+        # path calls the same library through ctypes.
+        warnings.warn(f"the compiled binding _cs_fast was not built ({e}); using ctypes")
     return LIB
 
 

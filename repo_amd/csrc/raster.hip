@@ -954,7 +954,11 @@ constexpr int kOrderThreads = 1024;
 constexpr int kOrderBuckets = 4096;
 constexpr int kOrderPerThread = kOrderBuckets / kOrderThreads;
 constexpr int kOrderLdsTiles = 16384;
-constexpr uint64_t kOrderStride = 1000003;   // prime; tile counts stay below it
+// A prime above the largest tile count (kMaxImageDim^2 / 256 = 2^20 tiles of
+// 16x16), so i -> i * kOrderStride mod m is a bijection for every m.
+constexpr uint64_t kOrderStride = 1048583;
+static_assert(kOrderStride > (uint64_t)(kMaxImageDim / kTile) * (kMaxImageDim / kTile),
+              "the tile-order stride must exceed every tile count");
 
 __device__ __forceinline__ uint32_t cost_bucket(uint32_t c) {
     if (c == 0) return 0;

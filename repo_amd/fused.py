@@ -145,7 +145,9 @@ class _ClampMseSsimLoss(torch.autograd.Function):
                    N.ptr(g), int(win_size), float(c1), float(c2), float(ssim_weight), wp,
                    wp + 4 * 3 * h * w, N.ptr(out), abc_p, N.stream(dev))
         ctx.save_for_backward(x32, y32)
-        ctx.work, ctx.abc_p, ctx.g = work, abc_p, g
+        # The SSIM terms stay in `work`, which lives as long as this node (a
+        # second backward through a retained graph reads them again).
+        ctx.work, ctx.abc_off, ctx.g = work, (abc_p - wp) if n_abc else None, g
         ctx.lo, ctx.hi = float(lo), float(hi)
         ctx.win_size = int(win_size)
         ctx.ssim_weight = float(ssim_weight)
@@ -164,11 +166,11 @@ class _ClampMseSsimLoss(torch.autograd.Function):
         go = grad_loss
         if go.dtype is not torch.float32:
             go = go.to(torch.float32)
+        abc_p = ctx.work.data_ptr() + ctx.abc_off
         with N.prof("loss.clamp_mse_ssim_bwd"):
             N.call("cs_clamp_mse_ssim_backward", N.ptr(x), N.ptr(y), h, w, ctx.lo, ctx.hi,
-                   N.ptr(ctx.g), ctx.win_size, ctx.abc_p, ctx.ssim_weight, go.data_ptr(),
+                   N.ptr(ctx.g), ctx.win_size, abc_p, ctx.ssim_weight, go.data_ptr(),
                    N.ptr(gi), N.stream(x.device))
-        ctx.work = None
         if ctx.x_dtype is not torch.float32:
             gi = gi.to(ctx.x_dtype)
         return gi, None, None, None, None, None, None, None, None

@@ -181,6 +181,27 @@ def make_scene(cfg: int, *, scale: float = 1.0) -> Scene:
     raise ValueError(f"unknown config {cfg}")
 
 
+def segments_as_primitives(sc: Scene) -> Scene:
+    """The same geometry with one primitive per cubic segment, as the
+    reference's training model lays out open strokes
+    (gaussian_trace/render.py:669-677): seg_offsets = arange(nseg + 1) and every
+    per-primitive attribute repeated over its segments.  Segments of one path
+    share their depth, so each path's segments tie and keep segment order."""
+    counts = (sc.seg_offsets[1:] - sc.seg_offsets[:-1]).to(torch.int64)
+    nseg = int(sc.cubics_norm.shape[0])
+
+    def rep(t):
+        return None if t is None else torch.repeat_interleave(t, counts, dim=0).contiguous()
+
+    return Scene(cfg=sc.cfg, img_h=sc.img_h, img_w=sc.img_w, S=sc.S,
+                 cubics_norm=sc.cubics_norm.clone(),
+                 seg_offsets=torch.arange(nseg + 1, dtype=torch.int32),
+                 colors=rep(sc.colors), opacities=rep(sc.opacities), depths=rep(sc.depths),
+                 aa_widths=rep(sc.aa_widths), fill_rules=rep(sc.fill_rules),
+                 background=sc.background.clone(), target=sc.target,
+                 stroke_widths=rep(sc.stroke_widths))
+
+
 def small_scene(seed: int, *, P: int = 6, nseg: int = 4, h: int = 48, w: int = 64, S: int = 8,
                 stroke: bool = False, rmin: float = 3.0, rmax: float = 20.0) -> Scene:
     """Tiny random scene for brute-force parity tests."""

@@ -124,3 +124,48 @@ def test_clamp_mse_ssim_loss_on_hwc_image(h, w, weight):
     assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
     outside = ((img < 0) | (img > 1)).numpy()
     assert outside.any() and np.all(got[outside] == 0.0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("h,w", [(512, 768), (1356, 2040)])
+def test_clamp_mse_ssim_loss_at_frame_size(h, w):
+    """The benchmark's loss (clamp, MSE + 0.2 (1 - SSIM) of the HWC render) at
+    config 2's and config 3's frame sizes against float64 autograd of the
+    separable restatement: value within 1e-5, gradient per tensor and per
+    element, zero where the clamp is active."""
+    from helpers import check_grads
+    from repo_amd import fused
+    print(f"[clamp_mse_ssim] {h}x{w}", flush=True)
+    img = _img(h, w, 11)
+    y = torch.rand((1, 3, h, w), generator=torch.Generator().manual_seed(12))
+    a = img.cuda().requires_grad_(True)
+    loss, parts = fused.clamp_mse_ssim_loss(a, y.cuda(), 0.2)
+    i64 = img.double().requires_grad_(True)
+    x64 = i64.clamp(0, 1).permute(2, 0, 1).unsqueeze(0)
+    mse64 = ((x64 - y.double()) ** 2).mean()
+    ref = mse64 + 0.2 * (1 - O.ssim64_separable(x64, y.double()))
+    assert abs(float(loss) - float(ref)) <= 1e-5 * abs(float(ref))
+    assert abs(float(parts[0]) - float(mse64)) <= 1e-5 * float(mse64)
+    loss.backward()
+    ref.backward()
+    check_grads([("v_img", a.grad, i64.grad.numpy())])
+    outside = ((img < 0) | (img > 1)).numpy()
+    assert np.all(a.grad.cpu().numpy()[outside] == 0.0)
+
+
+@pytest.mark.gpu
+def test_clamp_mse_ssim_loss_second_backward_through_retained_graph():
+    """A second backward through a retained graph reads the SSIM terms the
+    forward stored, so it gives the first gradient again (the buffer lives as
+    long as the graph node; allocations in between must not disturb it)."""
+    from repo_amd import fused
+    img = _img(70, 90, 13).cuda().requires_grad_(True)
+    y = torch.rand((1, 3, 70, 90), generator=torch.Generator().manual_seed(14)).cuda()
+    loss, _ = fused.clamp_mse_ssim_loss(img, y, 0.2)
+    loss.backward(retain_graph=True)
+    first = img.grad.clone()
+    img.grad = None
+    junk = [torch.full((1 << 20,), 7.0, device="cuda") for _ in range(8)]  # reuse freed blocks
+    loss.backward()
+    del junk
+    assert torch.equal(img.grad, first)

@@ -55,15 +55,34 @@ def test_psnr():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", SHAPES[:3])
+@pytest.mark.parametrize("shape", SHAPES)
 def test_ssim_forward(shape):
     import manbo
     x, y = _pair(shape, 4)
     s = float(manbo.ssim(x.cuda(), y.cuda()))
-    ref = float(O.ssim_torch64(x.double(), y.double()))
+    ref = float(O.ssim64_separable(x.double(), y.double()))
     assert abs(s - ref) <= 1e-5 * abs(ref), (s, ref)
     one = float(manbo.ssim(x.cuda(), x.cuda()))
     assert abs(one - 1.0) < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", SHAPES[2:])
+def test_ssim_backward_full_frame(shape):
+    """The SSIM gradient at the benchmark's frame sizes against float64
+    autograd of the separable restatement, per tensor and per element."""
+    import manbo
+    from helpers import check_grads
+    print(f"[ssim backward] {shape}", flush=True)
+    x, y = _pair(shape, 9)
+    xd = x.cuda().requires_grad_(True)
+    s = manbo.ssim(xd, y.cuda())
+    (2.0 * s).backward()
+    x64 = x.double().requires_grad_(True)
+    r = O.ssim64_separable(x64, y.double())
+    (2.0 * r).backward()
+    assert abs(float(s) - float(r)) <= 1e-5 * abs(float(r))
+    check_grads([("v_x", xd.grad, x64.grad.numpy())])
 
 
 @pytest.mark.gpu

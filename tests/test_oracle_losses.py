@@ -97,3 +97,42 @@ def test_ssim_gradient_finite_differences():
         xm[0, 0, i, j] -= h
         fd = (float(O.ssim_torch64(xp, y)) - float(O.ssim_torch64(xm, y))) / (2 * h)
         assert abs(fd - float(xr.grad[0, 0, i, j])) < 1e-7
+
+
+def test_separable_ssim_equals_the_2d_window():
+    """ssim64_separable (two 1D passes) equals ssim_torch64 (the 2D window
+    outer(g, g), itself pinned by the loops above) in value and gradient, for
+    odd windows from 3 to 21 on non-square multi-image inputs; a transposed
+    pass or a wrong channel split breaks the equality."""
+    rng = np.random.default_rng(6)
+    for win, shape in ((11, (2, 3, 30, 41)), (7, (1, 3, 19, 25)), (3, (1, 2, 9, 8)),
+                       (21, (1, 3, 40, 33)), (15, (2, 1, 24, 30))):
+        x = torch.from_numpy(rng.random(shape))
+        y = torch.from_numpy(np.clip(x.numpy() + 0.3 * rng.standard_normal(shape), 0, 1))
+        a = x.clone().requires_grad_(True)
+        b = x.clone().requires_grad_(True)
+        va = O.ssim_torch64(a, y, win_size=win)
+        vb = O.ssim64_separable(b, y, win_size=win)
+        assert abs(float(va) - float(vb)) < 1e-12, win
+        va.backward()
+        vb.backward()
+        assert float((a.grad - b.grad).abs().max()) < 1e-12 * float(a.grad.abs().max()) + 1e-15
+        per = O.ssim64_separable(x, y, win_size=win, size_average=False)
+        assert per.shape == (shape[0],)
+        for i in range(shape[0]):
+            assert abs(float(per[i]) - float(O.ssim_torch64(x[i:i + 1], y[i:i + 1],
+                                                            win_size=win))) < 1e-12
+
+
+def test_separable_ssim_nonnegative_clamps_channel_means():
+    """nonnegative_ssim clamps each channel's mean at zero before averaging
+    (metric.py:266-268): anti-correlated channels read 0, others unchanged."""
+    rng = np.random.default_rng(7)
+    x = torch.from_numpy(rng.random((1, 2, 20, 20)))
+    y = x.clone()
+    y[:, 1] = 1.0 - x[:, 1]                       # channel 1 anti-correlated
+    per_c = [float(O.ssim64_separable(x[:, k:k + 1], y[:, k:k + 1])) for k in range(2)]
+    assert per_c[0] > 0.99 and per_c[1] < 0
+    got = float(O.ssim64_separable(x, y, nonnegative=True))
+    assert abs(got - 0.5 * per_c[0]) < 1e-12
+    assert abs(float(O.ssim64_separable(x, y)) - 0.5 * (per_c[0] + per_c[1])) < 1e-12

@@ -106,6 +106,67 @@ def test_tile_ranges_cover_padded_curve():
         assert nh[k] == max(0, tr[k, 2] - tr[k, 0]) * max(0, tr[k, 3] - tr[k, 1])
 
 
+def test_aniso_pads_of_straight_segments_closed_form():
+    """aniso_intersects (cubic_splatting.py:692-708) on straight segments at a
+    known angle theta: the unit normal of the chord is (|sin theta|,
+    |cos theta|), so the box is the endpoints' box widened by
+    pad + (half_sw + support) max(0.2, |sin theta|) in x and
+    pad + (half_sw + support) max(0.2, |cos theta|) in y.  A swapped normal
+    component, a dropped 0.2 floor, a dropped stroke half width or pad fail at
+    one of the angles."""
+    H = W = 512
+    cases = []
+    for deg in (0.0, 90.0, 45.0, 30.0, 120.0, 3.0, 170.0):
+        for length, sw, sup, pad in ((100.0, 0.0, 3.0, 1.0), (60.0, 6.0, 4.5, 2.0),
+                                     (150.0, 2.5, 0.3, 0.5)):
+            cases.append((math.radians(deg), length, sw, sup, pad))
+    tbx, tby = O.tile_bounds(H, W)
+    checked = 0
+    for k, (th, length, sw, sup, pad) in enumerate(cases):
+        c = np.array([200.3 + 7.1 * k % 50, 230.7 + 3.3 * k % 40])
+        d = np.array([math.cos(th), math.sin(th)])
+        p0, p3 = c - 0.5 * length * d, c + 0.5 * length * d
+        # Evenly spaced collinear control points: the curve is the chord.
+        pts = np.stack([p0 + (p3 - p0) * f for f in (0.0, 1 / 3, 2 / 3, 1.0)])
+        cn = np.empty((1, 4, 2), np.float32)
+        cn[0, :, 0] = pts[:, 0] / (W / 2) - 1
+        cn[0, :, 1] = pts[:, 1] / (H / 2) - 1
+        px, tr, _ = O.project_cubics(cn, np.float32([sw]), np.float32([sup]), H, W,
+                                     aabb_pad=pad, aniso=True)
+        q = px[0].astype(np.float64)
+        radial = 0.5 * sw + sup
+        pad_x = pad + radial * max(0.2, abs(math.sin(th)))
+        pad_y = pad + radial * max(0.2, abs(math.cos(th)))
+        box = (q[:, 0].min() - pad_x, q[:, 1].min() - pad_y, q[:, 0].max() + pad_x,
+               q[:, 1].max() + pad_y)
+        # Skip boxes whose edges sit within rounding of a tile boundary.
+        if min(abs(v / 16 - round(v / 16)) for v in box) < 1e-4:
+            continue
+        want = (min(tbx, max(0, math.floor(box[0] / 16))), min(tby, max(0, math.floor(box[1] / 16))),
+                min(tbx, max(0, math.floor(box[2] / 16) + 1)),
+                min(tby, max(0, math.floor(box[3] / 16) + 1)))
+        assert tuple(int(v) for v in tr[0]) == want, (math.degrees(th), length, sw, sup, pad)
+        checked += 1
+    assert checked >= len(cases) - 3
+
+
+def test_aniso_ranges_transpose_with_the_curve():
+    """Swapping x and y of every control point on a square canvas swaps the
+    aniso tile ranges exactly (the x pad follows the chord's y extent and vice
+    versa; a transposed operand breaks the symmetry)."""
+    g = np.random.default_rng(4)
+    H = W = 320
+    cub = g.uniform(-0.9, 0.9, size=(300, 4, 2)).astype(np.float32)
+    sw = g.uniform(0, 6, size=300).astype(np.float32)
+    sup = g.uniform(0, 5, size=300).astype(np.float32)
+    _, tr, nh = O.project_cubics(cub, sw, sup, H, W, aniso=True)
+    _, trt, nht = O.project_cubics(cub[..., ::-1].copy(), sw, sup, H, W, aniso=True)
+    np.testing.assert_array_equal(trt, tr[:, [1, 0, 3, 2]])
+    np.testing.assert_array_equal(nht, nh)
+    _, tri, _ = O.project_cubics(cub, sw, sup, H, W, aniso=False)
+    assert not np.array_equal(tri, tr)
+
+
 # ------------------------------------------------------------------ flatten
 
 def test_flatten_closed_form_and_endpoints():
