@@ -364,6 +364,20 @@ size_t cs_ssim_abc_elems(int32_t nc, int32_t h, int32_t w, int32_t win);
 int cs_mse_forward(const float* x, const float* y, int64_t n, float* partials, float* loss,
                    hipStream_t stream);
 
+/* No counterpart in the reference: cs_mse_forward for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  The partial sums go to a file-scope
+ * device array of the library (256 KiB per GPU, held until the process ends;
+ * its address is looked up once per device with hipGetSymbolAddress) instead
+ * of a caller workspace; nothing is allocated or freed.  n is limited to
+ * cs_mse_forward_noalloc_max_elems() (2^28) elements; larger n returns
+ * CS_ERR_ARGS.  Every call on one GPU shares that array: calls that overlap on
+ * one GPU (different streams, host threads) race and must be serialized by
+ * the caller.  The result equals cs_mse_forward's bit for bit (same kernels). */
+int64_t cs_mse_forward_noalloc_max_elems(void);
+int cs_mse_forward_noalloc(const float* x, const float* y, int64_t n, float* loss,
+                           hipStream_t stream);
+
 /* mse_backward_diff_kernel (ops/metric.py:166-202) with the scale
  * grad_loss * 2/n read on the device (metric.py:168 reads it on the host):
  * grad_x = s (x - y), grad_y = -s (x - y); either output may be null. */

@@ -83,6 +83,8 @@ _SIGNATURES = {
     "cs_ssim_partials_elems": (_SZ, [_I32, _I32, _I32]),
     "cs_ssim_abc_elems": (_SZ, [_I32, _I32, _I32, _I32]),
     "cs_mse_forward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P]),
+    "cs_mse_forward_noalloc_max_elems": (_I64, []),
+    "cs_mse_forward_noalloc": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "cs_mse_backward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
     "cs_ssim": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _F, _F, _P, _P, _P, _P]),
     "cs_ssim_backward": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P]),

@@ -13,6 +13,8 @@
 // reference) uses the per-pixel partials A = dS/dmu_x, B = dS/dE[x^2],
 // C = dS/dE[xy] and one transposed separable correlation, blocked the same
 // way.
+#include <mutex>
+
 #include "cs_common.h"
 #include "../../include/cubicsplat_hip.h"
 
@@ -489,6 +491,56 @@ extern "C" int cs_mse_forward(const float* x, const float* y, int64_t n, float* 
     if (n <= 0) return CS_ERR_ARGS;
     const int64_t nb = (n + kMseChunk - 1) / kMseChunk;
     if (nb > 0x7fffffff) return CS_ERR_ARGS;
+    hipLaunchKernelGGL(k_mse_partial, dim3((unsigned)nb), dim3(kMseThreads), 0, stream, x, y, n,
+                       partials);
+    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials, (int)nb,
+                       1.0f / (float)n, loss);
+    return metric_status();
+}
+
+// ------------------------------------------- MSE forward without allocation
+
+// Partial sums of cs_mse_forward_noalloc: a file-scope device array, one copy
+// per GPU, held until the process ends.  Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in for the symbol); it
+// passes the device address hipGetSymbolAddress returns for the current GPU.
+constexpr int kNoAllocMsePartials = 65536;   // 256 KiB: n up to 2^28 elements
+static __device__ __align__(256) float scratch[kNoAllocMsePartials];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices];   // scratch's address on each device (null: not looked up)
+
+// scratch's device address on the current GPU, looked up once per device.
+int scratch_on_current_device(float** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return CS_ERR_HIP;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return CS_ERR_HIP;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return CS_OK;
+}
+}  // namespace
+
+extern "C" int64_t cs_mse_forward_noalloc_max_elems(void) {
+    return (int64_t)kNoAllocMsePartials * kMseChunk;
+}
+
+extern "C" int cs_mse_forward_noalloc(const float* x, const float* y, int64_t n, float* loss,
+                                      hipStream_t stream) {
+    if (n <= 0 || n > cs_mse_forward_noalloc_max_elems() || !x || !y || !loss)
+        return CS_ERR_ARGS;
+    float* partials = nullptr;
+    const int rc = scratch_on_current_device(&partials);
+    if (rc) return rc;
+    // Every partial the second launch reads is written by the first, so the
+    // array needs no clearing between calls.
+    const int64_t nb = (n + kMseChunk - 1) / kMseChunk;
     hipLaunchKernelGGL(k_mse_partial, dim3((unsigned)nb), dim3(kMseThreads), 0, stream, x, y, n,
                        partials);
     hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials, (int)nb,
