@@ -209,7 +209,7 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
  * and the forward ones also
  *   wave_cost [2T] uint32 out (NULL: not recorded; 8-byte aligned) -- each
  *     wave's duration in ticks of the 100 MHz constant clock.
- * T must stay below 1000003 for cs_raster_tile_order.
+ * T is at most 2^20 (16384 x 16384 pixels) for cs_raster_tile_order.
  * cs_raster_tile_order turns the costs of one launch into a heavy-first order
  * for the next ones (the backward of the same forward, the next forward of
  * the scene): long tiles start first, short ones fill the tail.  chunked != 0
@@ -219,20 +219,33 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
 int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
                          int32_t* tile_order, hipStream_t stream);
 
-/* Raster log: for every list entry g a wave of tile rows processes, the
- * forward writes a 1056-byte record at raster_log[2 g + wave]: the wave's
- * per-pixel inside bits (its winding test; zero for strokes) and exact bits
- * (live pixels whose coverage needs the exact distance), each as two 64-bit
- * lane masks (32 bytes), then for each exact pixel its best edge index
- * (nearest, first strict minimum in ascending edge order) and the coverage it
- * composited with, as (int32, float32 bits) pairs packed in lane order.  The
- * backward of that forward reads it instead of re-running the edge walk and
- * the coverage function: it recomputes one distance term per exact pixel.  It
- * holds 2 * (capacity of prim_ids_sorted) records; required by the backward,
- * NULL allowed in the forward (then not written).  No reference counterpart:
- * the reference's backward re-runs the edge loop and the coverage
- * (ops/cubic_splatting.py:1451-1530, ops/cubic_polyline_splatting.py:465-545). */
-#define CS_RASTER_LOG_BYTES 1056
+/* Raster log (no reference counterpart: the reference's backward re-runs the
+ * edge loop and the coverage, ops/cubic_splatting.py:1451-1530,
+ * ops/cubic_polyline_splatting.py:465-545).  The forward records, for every
+ * list entry g a wave of tile rows processes, what its backward needs:
+ *   log_index [2 * num_entries] int32 (num_entries: the size of
+ *     prim_ids_sorted, every tile_bins range lies below it), entry 2 g + wave:
+ *     the record's position in log_pool in 16-byte units, or -1 when no pixel
+ *     of the wave is inside the primitive or near it (the entry contributes
+ *     nothing), or -2 when the pool was full (the backward then recomputes
+ *     that entry); entries the wave did not process are not written;
+ *   log_pool (16-byte aligned, log_pool_bytes): unit 0 holds a uint32
+ *     counter; then each wave's own region, log_entry_units units for every
+ *     entry of its tile's list (2 * num_entries * log_entry_units units in
+ *     all, placed by the tile's list range, written without atomics); then
+ *     shared blocks of CS_RASTER_LOG_BLOCK_BYTES that a wave whose records
+ *     outgrow its region reserves through the counter (which the forward
+ *     sets to the first shared unit and which ends at the units reserved,
+ *     plus at most one failed reservation per wave).  A record is 32 bytes of
+ *     lane masks (inside bits of the winding test, zero for strokes; exact
+ *     bits of the live pixels whose coverage needs the exact distance; one
+ *     64-bit mask per pixel row of the lanes), then one (best edge int32,
+ *     coverage fp32 bits) pair per exact pixel in lane order.
+ * Any pool of at least 16 * (1 + 2 * num_entries * log_entry_units) bytes is
+ * correct (a full pool only costs backward time).  log_index NULL: no log
+ * (the forward of a render no backward follows); the backward then
+ * recomputes every entry. */
+#define CS_RASTER_LOG_BLOCK_BYTES 2048
 
 /* rasterize_cubic_fill_forward_kernel (ops/cubic_splatting.py:918-1194) when
  * mode 0, rasterize_cubic_polyline_forward_kernel
@@ -243,8 +256,9 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
                          const void* edges, const void* edge_culls, const void* prim_recs,
                          const float* background, int32_t img_h, int32_t img_w,
                          int32_t edges_per_segment, float* out_img, float* final_Ts,
-                         int32_t* final_idx, void* raster_log, const int32_t* tile_order,
-                         uint32_t* wave_cost, hipStream_t stream);
+                         int32_t* final_idx, int64_t num_entries, int32_t* log_index,
+                         void* log_pool, int64_t log_pool_bytes, int32_t log_entry_units,
+                         const int32_t* tile_order, uint32_t* wave_cost, hipStream_t stream);
 
 /* rasterize_cubic_fill_backward_kernel (ops/cubic_splatting.py:1197-1651) /
  * rasterize_cubic_polyline_backward_kernel (ops/cubic_polyline_splatting.py:252-660)
@@ -256,7 +270,8 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
                           const void* edges, const void* edge_culls, const void* prim_recs,
                           const float* background, int32_t img_h, int32_t img_w,
                           int32_t edges_per_segment, const float* final_Ts,
-                          const int32_t* final_idx, const void* raster_log, const float* v_output,
+                          const int32_t* final_idx, const int32_t* log_index,
+                          const void* log_pool, const float* v_output,
                           float* v_cubics_px, float* v_colors, float* v_opacities,
                           float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
                           float* curve_isect_contrib, const int32_t* tile_order,
@@ -273,8 +288,8 @@ int cs_rasterize_backward_de_casteljau(int32_t mode, const int32_t* prim_ids_sor
                                        const void* edge_culls, const void* prim_recs,
                                        const float* background, int32_t img_h, int32_t img_w,
                                        const void* edge_aux, const float* final_Ts,
-                                       const int32_t* final_idx, const void* raster_log,
-                                       const float* v_output, float* v_cubics_px, float* v_colors,
+                                       const int32_t* final_idx, const int32_t* log_index,
+                                       const void* log_pool, const float* v_output, float* v_cubics_px, float* v_colors,
                                        float* v_opacities, float* v_inv_sigma2s,
                                        float* v_stroke_widths, float* curve_contrib_rgb,
                                        float* curve_isect_contrib, const int32_t* tile_order,
@@ -295,16 +310,17 @@ int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                  const void* edge_culls, const void* prim_recs,
                                  const float* background, int32_t img_h, int32_t img_w,
                                  int32_t edges_per_segment, float* out_img, float* final_Ts,
-                                 int32_t* final_idx, void* raster_log,
-                                 unsigned long long* eval_counts, const int32_t* tile_order,
+                                 int32_t* final_idx, int64_t num_entries, int32_t* log_index,
+                                 void* log_pool, int64_t log_pool_bytes,
+                                 int32_t log_entry_units, unsigned long long* eval_counts, const int32_t* tile_order,
                                  uint32_t* wave_cost, hipStream_t stream);
 int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                   const int32_t* tile_bins, const void* edges,
                                   const void* edge_culls, const void* prim_recs,
                                   const float* background, int32_t img_h, int32_t img_w,
                                   int32_t edges_per_segment, const float* final_Ts,
-                                  const int32_t* final_idx, const void* raster_log,
-                                  const float* v_output, float* v_cubics_px, float* v_colors,
+                                  const int32_t* final_idx, const int32_t* log_index,
+                                  const void* log_pool, const float* v_output, float* v_cubics_px, float* v_colors,
                                   float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
                                   float* curve_contrib_rgb, float* curve_isect_contrib,
                                   unsigned long long* eval_counts, const int32_t* tile_order,

@@ -23,7 +23,7 @@ EDGE_CULL_INTS = 4       # 16-byte edge cull record
 MAX_IMAGE_DIM = 16384
 SEG_RECORD_INTS = 8      # 32-byte segment record
 PRIM_RECORD_FLOATS = 20  # 80-byte primitive record
-RASTER_LOG_INTS = 264    # 1056-byte raster log record per (list entry, wave)
+RASTER_LOG_BLOCK_BYTES = 2048  # log pool reserved per wave at a time
 EDGE_AUX_INTS = 4        # 16-byte (segment, t0, t1) record of the adaptive flattening
 
 _P = ctypes.c_void_p
@@ -52,13 +52,14 @@ _SIGNATURES = {
     "cs_bin_finish": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P,
                                      _P, _P, _P, _I64, _P]),
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
-                                            _P, _P, _P, _P, _P]),
+                                            _P, _I64, _P, _P, _I64, _I32, _P, _P, _P]),
     "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P,
-                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_rasterize_forward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
-                                                    _P, _P, _P, _P, _P, _P, _P, _P]),
+                                                    _P, _P, _P, _I64, _P, _P, _I64, _I32, _P, _P,
+                                                    _P, _P]),
     "cs_rasterize_backward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
-                                                     _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                     _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                                      _P, _P, _P, _P, _P]),
     "cs_raster_tile_order": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
     "cs_accumulate_edge_grads": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P]),
@@ -73,9 +74,9 @@ _SIGNATURES = {
     "cs_flatten_cubics_bernstein": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
     "cs_cubic_flatness_flags": (ctypes.c_int, [_P, _I32, _F, _I32, _P, _P]),
     "cs_cubic_split_half": (ctypes.c_int, [_P, _I32, _P, _P, _P]),
-    "cs_rasterize_backward_de_casteljau": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32,
-                                                          _I32, _P, _P, _P, _P, _P, _P, _P, _P,
-                                                          _P, _P, _P, _P, _P, _P]),
+    "cs_rasterize_backward_de_casteljau": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
+                                                          _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                          _P, _P, _P, _P, _P]),
     "cs_accumulate_edge_grads_csr": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
                                                     _P]),
     "cs_backward_finalize": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P]),
@@ -146,6 +147,7 @@ _HIP_SIGNATURES = {
     "hipEventCreateWithFlags": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]),
     "hipEventRecord": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "hipEventSynchronize": (ctypes.c_int, [ctypes.c_void_p]),
+    "hipEventQuery": (ctypes.c_int, [ctypes.c_void_p]),
     "hipEventElapsedTime": (ctypes.c_int, [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
                                            ctypes.c_void_p]),
     "hipEventDestroy": (ctypes.c_int, [ctypes.c_void_p]),

@@ -125,13 +125,15 @@ __device__ __forceinline__ int owner_of(const int32_t* __restrict__ offs, int P,
 
 // Conservative distance beyond which a pixel's coverage of this primitive is
 // decided without its exact distance: fill -> alpha < 1/255 outside, coverage
-// exactly 1.0f inside (2 d inv_sigma >= 16.64 makes 1 + exp(-.) round to 1);
-// stroke -> alpha < 1/255.  Margins absorb fp32 rounding of the cull tests.
+// exactly 1.0f inside (1 / (1 + exp(-2 d inv_sigma)) evaluated in fp32 with
+// the spec exp is exactly 1 for every d inv_sigma > 8.3177, found by a scan
+// in fp32 steps; 8.5 leaves a 2% margin for the rounding of d); stroke ->
+// alpha < 1/255.  The 1/4 pixel absorbs fp32 rounding of the cull tests.
 __device__ __forceinline__ float cull_distance(int mode, float opacity, float inv_sigma,
                                                float half_sw) {
     if (!(opacity <= 3.0e38f)) return __builtin_huge_valf();
     const float lo = __logf(fmaxf(255.0f * opacity, 1.0f));
-    if (mode == 0) return fmaxf(9.5f, 0.5f * (lo + 1.0f)) / inv_sigma + 0.25f;
+    if (mode == 0) return fmaxf(8.5f, 0.5f * (lo + 1.0f)) / inv_sigma + 0.25f;
     return half_sw + __builtin_sqrtf(2.0f * lo + 1.0f) / inv_sigma + 0.25f;
 }
 

@@ -91,18 +91,33 @@ struct alignas(16) EdgeAux {
     int32_t pad;
 };
 
-// Raster log of one (list entry, wave of tile rows), written by the forward
-// and read by the backward of that forward: the per-pixel inside bits (the
-// winding test; zero for strokes) and exact bits (live pixels whose coverage
-// needs the exact distance, all others being decided in closed form), each as
-// one 64-bit lane mask per pixel row p of the lanes, then for every exact
-// pixel its best edge (nearest, first strict minimum in ascending edge order)
-// and the coverage the forward composited with, packed in lane order: the
-// exact pixels of row 0, then those of row 1.
-struct alignas(16) RasterLog {
+// Raster log (forward -> backward).  For every (list entry g, wave of tile
+// rows) the forward processes, log_index[2 g + wave] holds one of
+//   >= 0          the record's position in the log pool, in 16-byte units;
+//   kLogEmpty     no pixel of the wave is inside the primitive or within its
+//                 exact-coverage distance: the entry contributes nothing;
+//   kLogMissing   not recorded (the pool was full): the backward recomputes
+//                 the entry's geometry with the forward's edge walk;
+//   kLogInside    every pixel of the wave is inside the fill and farther than
+//                 the cull distance from its edges (coverage 1, no record).
+// A record is a header (the per-pixel inside bits of the winding test, zero
+// for strokes, and the exact bits of the live pixels whose coverage needs the
+// exact distance, each as one 64-bit lane mask per pixel row of the lanes)
+// followed by one (best edge, coverage bits) pair per exact pixel, packed in
+// lane order: the exact pixels of row 0, then those of row 1.  The pool's
+// first 16 bytes hold the number of 16-byte units reserved so far (starting
+// at 1); each wave reserves kLogBlockUnits at a time with one atomic and
+// fills its block in order.
+constexpr int32_t kLogEmpty = -1;
+constexpr int32_t kLogMissing = -2;
+constexpr int32_t kLogInside = -3;   // every pixel inside, none near an edge
+constexpr uint32_t kLogHeaderUnits = 2;
+constexpr uint32_t kLogBlockUnits = 128;     // 2 KiB; a record is at most 66 units
+constexpr uint32_t kLogMaxUnits = 1u << 31;  // pool capacity limit (32 GiB)
+
+struct alignas(16) LogHeader {
     uint32_t inside[2 * kPix];
     uint32_t exact[2 * kPix];
-    int2 px[kWave * kPix];  // (best edge, coverage bits)
 };
 
 // Per cubic segment: the unions of its edges' ranges, plus the last pixel
@@ -166,6 +181,48 @@ __device__ __forceinline__ float spec_expf(float x) {
     const float s1 = __builtin_bit_cast(float, (uint32_t)(k1 + 127) << 23);
     const float s2 = __builtin_bit_cast(float, (uint32_t)(k2 + 127) << 23);
     return (p * s1) * s2;
+}
+
+// spec_expf for |x| <= 87: the same reduction and polynomial, without the
+// NaN and range tests, and the final scaling by 2^k as one ldexp, which is
+// exact (and equals the two-step scaling) while p 2^k is a normal float.
+__device__ __forceinline__ float spec_expf_mid(float x) {
+    const float kf = __builtin_rintf(x * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(kf, -0.693145751953125f, x);
+    r = __builtin_fmaf(kf, -1.428606765330187045037746429443359375e-06f, r);
+    float p = 1.98412698412698e-04f;
+    p = __builtin_fmaf(p, r, 1.38888888888889e-03f);
+    p = __builtin_fmaf(p, r, 8.33333333333333e-03f);
+    p = __builtin_fmaf(p, r, 4.16666666666667e-02f);
+    p = __builtin_fmaf(p, r, 1.66666666666667e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)kf);
+}
+
+// Correctly rounded sqrt(x) for finite x >= 2^-96 and x = +0: the hardware
+// square root (within 1 ulp) corrected by the residual of its neighbours,
+// the IEEE expansion without its denormal-range scaling and special-value
+// selects.  Below 2^-96 it stays within a few ulp of sqrt(x) < 2^-48.
+__device__ __forceinline__ float sqrt_rn(float x) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const float s_dn = __builtin_bit_cast(float, __builtin_bit_cast(int, s) - 1);
+    const float s_up = __builtin_bit_cast(float, __builtin_bit_cast(int, s) + 1);
+    const float r_dn = __builtin_fmaf(-s_dn, s, x);
+    const float r_up = __builtin_fmaf(-s_up, s, x);
+    const float t = r_dn <= 0.0f ? s_dn : s;
+    return r_up > 0.0f ? s_up : t;
+}
+
+// Correctly rounded 1 / y for normal y in [1, 2^90]: the hardware reciprocal
+// refined by the fused Newton steps of the IEEE division, which needs its
+// operand scaling and special-value fixup only outside that range.
+__device__ __forceinline__ float rcp_rn(float y) {
+    const float r0 = __builtin_amdgcn_rcpf(y);
+    const float r1 = __builtin_fmaf(__builtin_fmaf(-y, r0, 1.0f), r0, r0);
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-y, r1, 1.0f), r1, r1);
+    return __builtin_fmaf(__builtin_fmaf(-y, q1, 1.0f), r1, q1);
 }
 
 // sin and cos of x in fp32: k = rint(x 2/pi), r = x - k pi/2 by a three-part

@@ -28,7 +28,8 @@ static_assert(sizeof(EdgeRec) == CS_EDGE_RECORD_BYTES, "edge record layout");
 static_assert(sizeof(PrimRec) == CS_PRIM_RECORD_BYTES, "primitive record layout");
 static_assert(sizeof(EdgeCull) == CS_EDGE_CULL_BYTES, "edge cull record layout");
 static_assert(sizeof(EdgeAux) == CS_EDGE_AUX_BYTES, "edge aux record layout");
-static_assert(sizeof(RasterLog) == CS_RASTER_LOG_BYTES, "raster log record layout");
+static_assert(sizeof(LogHeader) == 16 * kLogHeaderUnits, "raster log header layout");
+static_assert(kLogBlockUnits * 16 == CS_RASTER_LOG_BLOCK_BYTES, "raster log block");
 
 // Crossing parity equals winding & 1 (each crossing changes the winding by
 // +-1), so only the winding number is tracked.
@@ -75,22 +76,18 @@ __device__ __forceinline__ void dist_term(const EdgeRec& E, int eid, float wx, f
     const float dx = __builtin_fmaf(proj, E.vx, -wx);
     const float dy = __builtin_fmaf(proj, E.vy, -wy);
     const float d2 = __builtin_fmaf(dx, dx, dy * dy);
+    // Selects on one comparison, not a branch (a per-pixel branch costs an
+    // exec-mask save and restore on every edge); a NaN d2 or a tie keeps the
+    // current minimum.
+    const bool lt = d2 < G.min_d2;
+    if constexpr (BEST >= 1) G.best = lt ? eid : G.best;
     if constexpr (BEST == 2) {
-        if (d2 < G.min_d2) {
-            G.min_d2 = d2;
-            G.best = eid;
-            G.bproj = proj;
-            G.bdx = dx;
-            G.bdy = dy;
-        }
-    } else if constexpr (BEST == 1) {
-        if (d2 < G.min_d2) {
-            G.min_d2 = d2;
-            G.best = eid;
-        }
-    } else {
-        G.min_d2 = fminf(G.min_d2, d2);
+        G.bproj = lt ? proj : G.bproj;
+        G.bdx = lt ? dx : G.bdx;
+        G.bdy = lt ? dy : G.bdy;
     }
+    if constexpr (BEST >= 1) G.min_d2 = lt ? d2 : G.min_d2;
+    else G.min_d2 = fminf(G.min_d2, d2);
 }
 
 // +x ray crossing of one edge, cubic_splatting.py:1119-1134 / 1485-1501.
@@ -385,6 +382,161 @@ __device__ __forceinline__ void record_wave_cost(uint32_t* __restrict__ wave_cos
     }
 }
 
+// Primitive-level cull of one lane's list entry (lane-parallel form of
+// prim_culled): the record's near rows and columns (and, for an open chain in
+// fill mode, its crossing rows and last vertex column) read with vector loads.
+template <int MODE>
+__device__ __forceinline__ bool prim_culled_lane(const PrimRec* __restrict__ p,
+                                                 const WaveRect& W) {
+    const int4 a = *reinterpret_cast<const int4*>(&p->ny_lo);  // ny_lo ny_span cy_lo cy_span
+    const int4 b = *reinterpret_cast<const int4*>(&p->nx_lo);  // nx_lo nx_span x_last -
+    if (span_hits(a.x, a.y, W.r1) && span_hits(b.x, b.y, W.c1)) return false;
+    if (MODE == 1) return true;
+    const int4 c = *reinterpret_cast<const int4*>(&p->e0);     // e0 e1 rule closed
+    if (c.w) return true;
+    return !span_hits(a.z, a.w, W.r1) || W.c0 > b.z;
+}
+
+// Far entry: no edge of the primitive lies within the cull distance of any of
+// the wave's pixels (its near ranges miss the wave), and (fill) every edge
+// whose y-range spans one of the wave's rows carries kCullFarCrossExact.
+// Then no pixel needs the exact coverage, and every pixel has the same
+// winding number: the winding number changes only across an edge, none
+// crosses the wave's rectangle, and for such edges the fp32 crossing test at
+// each pixel gives the geometric side (see kCullFarCrossExact).  q holds the
+// cull words of the first 64 edges.
+template <int MODE>
+__device__ __forceinline__ bool entry_far(const PrimRec& pr, const WaveRect& W,
+                                          const EdgeCull* __restrict__ culls, int4 q) {
+    const int lane = threadIdx.x & (kWave - 1);
+    for (int c = pr.e0; c < pr.e1; c += kWave) {
+        if (c != pr.e0) q = load_culls(culls, c, pr.e1);
+        const bool in = c + lane < pr.e1;
+        bool bad = in && span_hits(packed_lo(q.x), packed_span(q.x), W.r1) &&
+                   span_hits(packed_lo(q.z), packed_span(q.z), W.c1);
+        if (MODE == 0)
+            bad |= in && span_hits(packed_lo(q.y), packed_span(q.y), W.r1) &&
+                   !(q.w & kCullFarCrossExact);
+        if (__ballot(bad)) return false;
+    }
+    return true;
+}
+
+// Winding number of one point (px, py) over all edges of the primitive, one
+// edge per lane: cross_term's expressions, summed with two ballots per chunk.
+__device__ __forceinline__ int point_winding(const PrimRec& pr,
+                                             const EdgeRec* __restrict__ edges_g, float px,
+                                             float py) {
+    const int lane = threadIdx.x & (kWave - 1);
+    int w = 0;
+    for (int c = pr.e0; c < pr.e1; c += kWave) {
+        const int e = c + lane;
+        bool up = false, down = false;
+        if (e < pr.e1) {
+            const float4 a = *reinterpret_cast<const float4*>(edges_g + e);          // x0 y0 x1 y1
+            const float2 v = *reinterpret_cast<const float2*>(&edges_g[e].vx);       // vx vy
+            const bool b0 = a.y <= py, b1 = a.w <= py;
+            const float wx = px - a.x, wy = py - a.y;
+            const float cr = __builtin_fmaf(wy, v.x, -(wx * v.y));
+            const bool hit = (b0 != b1) & ((b0 ? cr : -cr) > 0.0f);
+            up = hit & b0;
+            down = hit & !b0;
+        }
+        w += __builtin_popcountll(__ballot(up)) - __builtin_popcountll(__ballot(down));
+    }
+    return w;
+}
+
+// Exact coverage from the squared distance: coverage()'s expressions and
+// results, evaluated with sqrt_rn / spec_expf_mid / rcp_rn where they equal
+// the IEEE square root, spec_expf and the IEEE division.  d2 >= +0 (or NaN,
+// which fmaxf maps to 0); below 2^-96 sqrt_rn may differ from the IEEE root
+// by a few ulp, but then dist inv_sigma 2 < 2^-48 1e4 2 < 2^-25 (widths are at
+// least 1e-4), exp rounds to exactly 1 and the coverage is 0.5 either way.
+// The logit is clamped to [-60, 60] (spec_expf_mid's range) and 1 + exp lies
+// in [1, 2^87] (rcp_rn's).
+template <int MODE>
+__device__ __forceinline__ float exact_coverage(const PrimRec& pr, float d2, bool inside) {
+    const float dist = sqrt_rn(fmaxf(d2, 0.0f));
+    if (MODE == 0) {
+        float logit = dist * pr.inv_sigma * 2.0f;
+        if (inside) logit = -logit;
+        logit = fmaxf(-60.0f, fminf(60.0f, logit));
+        return rcp_rn(1.0f + spec_expf_mid(logit));
+    } else {
+        const float ed = fmaxf(0.0f, dist - pr.half_sw);
+        const float sigma = 0.5f * ed * ed * pr.inv_sigma2;
+        return spec_expf(-sigma);
+    }
+}
+
+// A wave's position in the log pool: its current region [p, e) in 16-byte
+// units, and whether the pool ran out (then nothing more is recorded).
+struct LogCursor {
+    uint32_t p, e;
+    bool full;
+};
+
+// Position of a record of `units` (<= kLogBlockUnits) units.  A wave first
+// fills its own region of the pool (`per_entry` units for each list entry of
+// its tile, at a position fixed by the tile's list range, so no atomics);
+// when a record does not fit there it reserves blocks of kLogBlockUnits from
+// the shared counter.  kLogMissing when the pool is full.  Wave-uniform;
+// every lane of the wave must be active.
+__device__ __forceinline__ int32_t log_reserve(uint4* __restrict__ pool, uint32_t cap_units,
+                                               LogCursor& c, uint32_t units) {
+    if (c.full) return kLogMissing;
+    if (c.p + units > c.e) {
+        uint32_t base = 0;
+        if ((threadIdx.x & (kWave - 1)) == 0)
+            base = atomicAdd(reinterpret_cast<uint32_t*>(pool), kLogBlockUnits);
+        base = __builtin_amdgcn_readfirstlane(base);
+        if ((uint64_t)base + kLogBlockUnits > cap_units) {
+            c.full = true;
+            return kLogMissing;
+        }
+        c.p = base;
+        c.e = base + kLogBlockUnits;
+    }
+    const uint32_t r = c.p;
+    c.p += units;
+    return (int32_t)r;
+}
+
+// A wave's staged log records: LDS units [0, n) hold pool units
+// [base, base + n).  Records are composed in LDS and copied to the pool in
+// bulk (when the stage fills, when the next record goes to another region
+// of the pool, and when the wave ends): global stores and loads share one
+// completion counter, so log stores issued between the edge walks would make
+// every following load wait for them.
+constexpr uint32_t kLogStageUnits = 256;   // 4 KiB of LDS per wave
+
+struct LogStage {
+    uint32_t base, n;
+};
+
+__device__ __forceinline__ void log_flush(uint4* __restrict__ pool, const uint4* stage,
+                                          LogStage& st) {
+    for (uint32_t u = threadIdx.x & (kWave - 1); u < st.n; u += kWave)
+        pool[st.base + u] = stage[u];
+    st.n = 0;
+}
+
+__device__ __forceinline__ uint32_t pack_d2_inside(float d2, bool inside) {
+    // d2 >= +0 or NaN: its sign bit is free to carry the inside flag.
+    return (__builtin_bit_cast(uint32_t, d2) & 0x7fffffffu) | ((uint32_t)inside << 31);
+}
+
+// Forward raster.  Each wave walks its tile's list in chunks of 64 entries:
+// lane k tests entry k of the chunk against the wave's pixel rectangle
+// (prim_culled_lane), and the wave then processes only the entries that can
+// affect one of its pixels, in list order, until every pixel has reached the
+// transmittance stop.  Per processed entry: the edge walk (prim_geometry),
+// exact coverage for the pixels within the cull distance, the raster log
+// record, compositing.  When both pixel rows of the lanes have exact pixels
+// and they fit in one wave, they are gathered into lanes 0 .. n-1 with
+// ds_permute, so the exact coverage (sqrt, exp, divide) runs once instead of
+// once per row.
 template <int MODE, bool COUNT>
 __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
@@ -392,16 +544,17 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, const int32_t* __restrict__ tile_order,
     uint32_t* __restrict__ wave_cost, float* __restrict__ out, float* __restrict__ final_T,
-    int32_t* __restrict__ final_idx, RasterLog* __restrict__ raster_log,
+    int32_t* __restrict__ final_idx, int32_t* __restrict__ log_index,
+    uint4* __restrict__ log_pool, uint32_t log_units, uint32_t log_per_entry,
     unsigned long long* __restrict__ counts) {
     const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
     const int tile = block_tile(tile_order, ntiles);
     const int tty = tile / tbx, ttx = tile - tty * tbx;
+    const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r0 = tty * kTile + wv * kWaveRows;
     const LanePixels L = lane_pixels(r0, ttx * kTile, img_h, img_w);
     const WaveRect W{ttx * kTile, ttx * kTile + kTile - 1, r0, r0 + kWaveRows - 1};
-    const cptr<int32_t> prim_ids = as_const(prim_ids_g);
     const cptr<PrimRec> prims = as_const(prims_g);
     const cptr<EdgeRec> edges = as_const(edges_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
@@ -416,83 +569,197 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
         done[p] = !L.in_img[p];
     }
     EvalCounts n{};
-    // The cull words of the next entry's first 64 edges are loaded one entry
-    // ahead, so that vector load is in flight while this entry is processed.
-    // An empty tile reads no list entry (its bins are (0, 0) and the whole
-    // list may be empty); primitive 0 then stands in for the prefetches.
-    int pid = g0 < g1 ? prim_ids[g0] : 0;
-    int pid_next = g0 < g1 ? prim_ids[min(g0 + 1, g1 - 1)] : 0;
-    int4 q_next = g0 < g1 ? load_culls(culls, prims[pid].e0, prims[pid].e1)
-                          : make_int4(0, -1, 0, -1);
-    for (int g = g0; g < g1; ++g) {
-        bool live[kPix];
-        bool any_live = false;
-#pragma unroll
-        for (int p = 0; p < kPix; ++p) {
-            live[p] = !done[p];
-            any_live |= live[p];
+    // This wave's own log region: per_entry units for each entry of the
+    // tile's list, the two waves of a tile side by side.
+    const uint32_t len = (uint32_t)(g1 - g0);
+    const uint32_t own = 1u + (2u * (uint32_t)g0 + (uint32_t)wv * len) * log_per_entry;
+    LogCursor lc{own, own + len * log_per_entry, false};
+    __shared__ uint4 log_stage_all[kRasterThreads / kWave][kLogStageUnits];
+    uint4* const stage = log_stage_all[wv];
+    LogStage st{own, 0u};
+    bool finished = false;
+    for (int gc = g0; gc < g1 && !finished; gc += kWave) {
+        const int gl = gc + lane;
+        const bool in_list = gl < g1;
+        const int pid_l = in_list ? prim_ids_g[gl] : 0;
+        const bool keep = in_list && !prim_culled_lane<MODE>(prims_g + pid_l, W);
+        uint64_t todo = __ballot(keep);
+        // Entry gc + k's log index, held by lane k; stored once per chunk.
+        int idx_l = kLogEmpty;
+        uint64_t logged = 0;
+        // The next entry's first 64 cull words are loaded one processed entry
+        // ahead, so that vector load is in flight while this entry runs.
+        int4 q_next = make_int4(0, -1, 0, -1);
+        if (todo) {
+            const int pid0 = __builtin_amdgcn_readlane(pid_l, (int)__builtin_ctzll(todo));
+            q_next = load_culls(culls, prims[pid0].e0, prims[pid0].e1);
         }
-        if (__ballot(any_live) == 0) break;
-        const PrimRec pr = prims[pid];
-        const int ne0 = prims[pid_next].e0, ne1 = prims[pid_next].e1;
-        const int pid_after = prim_ids[min(g + 2, g1 - 1)];
-        const int4 q = q_next;
-        q_next = load_culls(culls, ne0, ne1);
-        pid = pid_next;
-        pid_next = pid_after;
-        const float D2 = pr.cull_d * pr.cull_d, D2o = pr.cull_out * pr.cull_out;
-        if (prim_culled<MODE>(pr, W)) continue;
-        int npix = 0;
-        if constexpr (COUNT) {
-            npix = wave_count(live);
-            n.entries += 1;
-        }
-        Geom G[kPix];
-        prim_geometry<MODE, 1, COUNT, MODE == 0>(pr, W, culls, edges, L.px, L.py, q, G, n,
-                                                 npix);
-        // This entry's inside and exact bits, and below each exact pixel's
-        // best edge and coverage, for the backward (which then needs neither
-        // the edge walk nor the exact coverage).
-        bool ex[kPix];
+        while (todo) {
+            bool any_live = false;
 #pragma unroll
-        for (int p = 0; p < kPix; ++p) ex[p] = !done[p] && needs_exact<MODE>(pr, G[p], D2, D2o);
-        RasterLog* rec = nullptr;
-        int slot[kPix] = {0, 0};
-        if (raster_log) {
-            const uint64_t in0 = MODE == 0 ? (uint64_t)__ballot(inside_of<MODE>(pr, G[0])) : 0ull;
-            const uint64_t in1 =
-                MODE == 0 ? (uint64_t)__ballot(inside_of<MODE>(pr, G[kPix - 1])) : 0ull;
+            for (int p = 0; p < kPix; ++p) any_live |= !done[p];
+            if (__ballot(any_live) == 0) {
+                finished = true;
+                break;
+            }
+            const int k = (int)__builtin_ctzll(todo);
+            todo &= todo - 1;
+            const int g = gc + k;
+            const int pid = __builtin_amdgcn_readlane(pid_l, k);
+            const PrimRec pr = prims[pid];
+            const int4 q = q_next;
+            if (todo) {
+                const int pid2 = __builtin_amdgcn_readlane(pid_l, (int)__builtin_ctzll(todo));
+                q_next = load_culls(culls, prims[pid2].e0, prims[pid2].e1);
+            }
+            const float D2 = pr.cull_d * pr.cull_d, D2o = pr.cull_out * pr.cull_out;
+            int npix = 0;
+            if constexpr (COUNT) {
+                bool live[kPix];
+#pragma unroll
+                for (int p = 0; p < kPix; ++p) live[p] = !done[p];
+                npix = wave_count(live);
+                n.entries += 1;
+            }
+            if (entry_far<MODE>(pr, W, culls, q)) {
+                // Uniform entry: outside (nothing to do) or, for a fill whose
+                // winding at the wave's first pixel says inside, coverage 1
+                // at every pixel.
+                bool inside_all = false;
+                if constexpr (MODE == 0) {
+                    const int w = point_winding(pr, edges_g, (float)W.c0 + 0.5f,
+                                                (float)W.r0 + 0.5f);
+                    inside_all = pr.rule == 0 ? ((w & 1) != 0) : (w != 0);
+                    if constexpr (COUNT) n.cross += (uint64_t)(pr.e1 - pr.e0);
+                }
+                if (log_index) {
+                    idx_l = lane == k ? (inside_all ? kLogInside : kLogEmpty) : idx_l;
+                    logged |= 1ull << k;
+                }
+                if (inside_all) {
+                    const float alpha = fminf(kAlphaCap, pr.opacity * 1.0f);
+                    if (alpha >= kAlphaMin) {
+#pragma unroll
+                        for (int p = 0; p < kPix; ++p) {
+                            if (done[p]) continue;
+                            const float nT = T[p] * (1.0f - alpha);
+                            const float vis = alpha * T[p];
+                            C0[p] = __builtin_fmaf(pr.r, vis, C0[p]);
+                            C1[p] = __builtin_fmaf(pr.g, vis, C1[p]);
+                            C2[p] = __builtin_fmaf(pr.b, vis, C2[p]);
+                            T[p] = nT;
+                            cur[p] = g;
+                            if (nT <= kTStop) done[p] = true;
+                        }
+                    }
+                }
+                continue;
+            }
+            Geom G[kPix];
+            prim_geometry<MODE, 1, COUNT, MODE == 0>(pr, W, culls, edges, L.px, L.py, q, G, n,
+                                                     npix);
+            bool ex[kPix], ins[kPix];
+            float cov[kPix];
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) {
+                ins[p] = inside_of<MODE>(pr, G[p]);
+                ex[p] = !done[p] && !(G[p].min_d2 > (ins[p] ? D2 : D2o));
+                cov[p] = ins[p] ? 1.0f : 0.0f;   // closed form; exact pixels below
+            }
             const uint64_t x0 = __ballot(ex[0]), x1 = __ballot(ex[kPix - 1]);
-            rec = raster_log + (2 * (size_t)g + wv);
-            if ((threadIdx.x & (kWave - 1)) == 0) {
-                *reinterpret_cast<uint4*>(rec->inside) = make_uint4(
-                    (uint32_t)in0, (uint32_t)(in0 >> 32), (uint32_t)in1, (uint32_t)(in1 >> 32));
-                *reinterpret_cast<uint4*>(rec->exact) = make_uint4(
-                    (uint32_t)x0, (uint32_t)(x0 >> 32), (uint32_t)x1, (uint32_t)(x1 >> 32));
-            }
-            slot[0] = lane_rank(x0);
-            slot[kPix - 1] = __builtin_popcountll(x0) + lane_rank(x1);
-        }
-        if constexpr (COUNT) n.cover += (uint64_t)wave_count(ex);
+            const int n0 = __builtin_popcountll(x0), nx = n0 + __builtin_popcountll(x1);
+            const int rk0 = lane_rank(x0), rk1 = lane_rank(x1);
+            if constexpr (COUNT) n.cover += (uint64_t)nx;
+            // Exact coverage.  gathered: lane j < nx holds exact pixel j (row 0's
+            // in lane order, then row 1's) and its best edge.
+            const bool gathered = n0 > 0 && nx > n0 && nx <= kWave;
+            float cov_g = 0.0f;
+            int best_g = 0;
+            if (gathered) {
+                const int d0 = ex[0] ? rk0 : n0 + (lane - rk0);
+                const int nr1 = lane - rk1;
+                const int d1 = ex[1] ? n0 + rk1 : (nr1 < n0 ? nr1 : nr1 + (nx - n0));
+                const uint32_t a = (uint32_t)__builtin_amdgcn_ds_permute(
+                    4 * d0, (int)pack_d2_inside(G[0].min_d2, ins[0]));
+                const uint32_t b = (uint32_t)__builtin_amdgcn_ds_permute(
+                    4 * d1, (int)pack_d2_inside(G[1].min_d2, ins[1]));
+                const int ba = __builtin_amdgcn_ds_permute(4 * d0, G[0].best);
+                const int bb = __builtin_amdgcn_ds_permute(4 * d1, G[1].best);
+                const uint32_t v = lane < n0 ? a : b;
+                best_g = lane < n0 ? ba : bb;
+                if (lane < nx)
+                    cov_g = exact_coverage<MODE>(
+                        pr, __builtin_bit_cast(float, v & 0x7fffffffu), (v >> 31) != 0);
+                const float c0 = __builtin_bit_cast(
+                    float, __builtin_amdgcn_ds_bpermute(4 * rk0, __builtin_bit_cast(int, cov_g)));
+                const float c1 = __builtin_bit_cast(
+                    float,
+                    __builtin_amdgcn_ds_bpermute(4 * (n0 + rk1), __builtin_bit_cast(int, cov_g)));
+                if (ex[0]) cov[0] = c0;
+                if (ex[1]) cov[1] = c1;
+            } else {
 #pragma unroll
-        for (int p = 0; p < kPix; ++p) {
-            if (done[p]) continue;
-            const Cov c = coverage<MODE>(pr, G[p], D2, D2o);
-            if (rec && ex[p])
-                rec->px[slot[p]] = make_int2(G[p].best, __builtin_bit_cast(int, c.cov));
-            const float alpha = fminf(kAlphaCap, pr.opacity * c.cov);
-            if (alpha >= kAlphaMin) {
-                const float nT = T[p] * (1.0f - alpha);
-                const float vis = alpha * T[p];
-                C0[p] = __builtin_fmaf(pr.r, vis, C0[p]);
-                C1[p] = __builtin_fmaf(pr.g, vis, C1[p]);
-                C2[p] = __builtin_fmaf(pr.b, vis, C2[p]);
-                T[p] = nT;
-                cur[p] = g;
-                if (nT <= kTStop) done[p] = true;
+                for (int p = 0; p < kPix; ++p)
+                    if (ex[p]) cov[p] = exact_coverage<MODE>(pr, G[p].min_d2, ins[p]);
+            }
+            // The log record of this entry and wave: inside and exact bits, and
+            // each exact pixel's best edge and coverage, for the backward.
+            if (log_index) {
+                const uint64_t in0 = MODE == 0 ? (uint64_t)__ballot(ins[0]) : 0ull;
+                const uint64_t in1 = MODE == 0 ? (uint64_t)__ballot(ins[kPix - 1]) : 0ull;
+                int32_t at = kLogEmpty;
+                if ((in0 | in1 | x0 | x1) != 0) {
+                    const uint32_t units = kLogHeaderUnits + (uint32_t)((nx + 1) >> 1);
+                    if (st.n + units > kLogStageUnits) log_flush(log_pool, stage, st);
+                    at = log_reserve(log_pool, log_units, lc, units);
+                    if (at >= 0) {
+                        if ((uint32_t)at != st.base + st.n) {   // another region: flush first
+                            log_flush(log_pool, stage, st);
+                            st.base = (uint32_t)at;
+                        }
+                        uint4* rec = stage + st.n;
+                        st.n += units;
+                        if (lane == 0) {
+                            rec[0] = make_uint4((uint32_t)in0, (uint32_t)(in0 >> 32),
+                                                (uint32_t)in1, (uint32_t)(in1 >> 32));
+                            rec[1] = make_uint4((uint32_t)x0, (uint32_t)(x0 >> 32), (uint32_t)x1,
+                                                (uint32_t)(x1 >> 32));
+                        }
+                        int2* pairs = reinterpret_cast<int2*>(rec + kLogHeaderUnits);
+                        if (gathered) {
+                            if (lane < nx)
+                                pairs[lane] = make_int2(best_g, __builtin_bit_cast(int, cov_g));
+                        } else {
+                            if (ex[0])
+                                pairs[rk0] = make_int2(G[0].best, __builtin_bit_cast(int, cov[0]));
+                            if (ex[1])
+                                pairs[n0 + rk1] =
+                                    make_int2(G[1].best, __builtin_bit_cast(int, cov[1]));
+                        }
+                    }
+                }
+                idx_l = lane == k ? at : idx_l;
+                logged |= 1ull << k;
+            }
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) {
+                if (done[p]) continue;
+                const float alpha = fminf(kAlphaCap, pr.opacity * cov[p]);
+                if (alpha >= kAlphaMin) {
+                    const float nT = T[p] * (1.0f - alpha);
+                    const float vis = alpha * T[p];
+                    C0[p] = __builtin_fmaf(pr.r, vis, C0[p]);
+                    C1[p] = __builtin_fmaf(pr.g, vis, C1[p]);
+                    C2[p] = __builtin_fmaf(pr.b, vis, C2[p]);
+                    T[p] = nT;
+                    cur[p] = g;
+                    if (nT <= kTStop) done[p] = true;
+                }
             }
         }
+        if ((logged >> lane) & 1u) log_index[2 * (size_t)gl + wv] = idx_l;
     }
+    if (log_index) log_flush(log_pool, stage, st);
 #pragma unroll
     for (int p = 0; p < kPix; ++p) {
         if (!L.in_img[p]) continue;
@@ -505,6 +772,12 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     }
     if constexpr (COUNT) flush_counts(n, counts);
     record_wave_cost(wave_cost, tile, t_start);
+}
+
+// First unit of the log pool: the counter of the shared blocks, which start
+// after the waves' own regions.
+__global__ void k_log_init(uint4* __restrict__ pool, uint32_t first_shared) {
+    pool[0] = make_uint4(first_shared, 0u, 0u, 0u);
 }
 
 // n / eps for 0 <= n < 2^31 with magic = ceil(2^32 / eps) (eps >= 2): the
@@ -536,14 +809,13 @@ __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
     basis_at((float)e * inv_e, b);
 }
 
-// Masks of a raster log record (scalar loads; g and wave are uniform).
+// Masks of a raster log record at unit `at` of the pool (scalar loads).
 struct LogHead {
     uint64_t in[kPix], xm[kPix];
 };
 
-__device__ __forceinline__ LogHead log_head(const RasterLog* __restrict__ log, int g, int wave) {
-    const cptr<uint4> hd =
-        as_const(reinterpret_cast<const uint4*>(log + (2 * (size_t)g + wave)));
+__device__ __forceinline__ LogHead log_head(const uint4* __restrict__ pool, int32_t at) {
+    const cptr<uint4> hd = as_const(pool + at);
     const uint4 a = hd[0], b = hd[1];
     LogHead h;
     h.in[0] = ((uint64_t)a.y << 32) | a.x;
@@ -553,15 +825,15 @@ __device__ __forceinline__ LogHead log_head(const RasterLog* __restrict__ log, i
     return h;
 }
 
-// The lane's (best edge, coverage) pairs of record (g, wave) for its exact
-// pixels (others keep their value).
-__device__ __forceinline__ void log_pixels(const RasterLog* __restrict__ log, int g, int wave,
+// The lane's (best edge, coverage) pairs of the record at unit `at` for its
+// exact pixels (others keep their value).
+__device__ __forceinline__ void log_pixels(const uint4* __restrict__ pool, int32_t at,
                                            const LogHead& h, int lane, int2 (&px)[kPix]) {
-    const RasterLog* rec = log + (2 * (size_t)g + wave);
+    const int2* pairs = reinterpret_cast<const int2*>(pool + at + kLogHeaderUnits);
 #pragma unroll
     for (int p = 0; p < kPix; ++p)
         if ((h.xm[p] >> lane) & 1u)
-            px[p] = rec->px[(p == 0 ? 0 : __builtin_popcountll(h.xm[0])) + lane_rank(h.xm[p])];
+            px[p] = pairs[(p == 0 ? 0 : __builtin_popcountll(h.xm[0])) + lane_rank(h.xm[p])];
 }
 
 // Backward: the reverse traversal of cubic_splatting.py:1339-1649 (fill) and
@@ -583,8 +855,8 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     int tbx, int ntiles, const int32_t* __restrict__ tile_order, int eps, uint32_t eps_magic,
-    const EdgeAux* __restrict__ edge_aux, const RasterLog* __restrict__ raster_log,
-    const float* __restrict__ final_T,
+    const EdgeAux* __restrict__ edge_aux, const int32_t* __restrict__ log_index_g,
+    const uint4* __restrict__ log_pool, const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
@@ -625,13 +897,22 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     // The wave maximum is uniform; readfirstlane tells the compiler so, which
     // keeps every load that depends on the entry index scalar.
     const int gstart = min(g1 - 1, __builtin_amdgcn_readfirstlane(wave_max_i(fmax)));
-    // The next entry's primitive id is loaded one entry ahead (here the next
-    // entry is g - 1).
-    int pid = gstart >= g0 ? prim_ids[gstart] : 0;
-    int pid_next = gstart >= g0 ? prim_ids[max(gstart - 1, g0)] : 0;
+    const cptr<int32_t> log_index = as_const(log_index_g);
     const int slot = reduce8_slot(lane & 7);
     const bool adder = (lane & ~7) == 8;
-    for (int g = gstart; g >= g0; --g) {
+    // Entries from gstart down to g0 in chunks of 64: lane k tests entry
+    // gc - k with the forward's primitive cull, and the wave visits the
+    // survivors in descending order -- exactly the entries the forward
+    // processed at or below this wave's last contributing entry.
+    for (int gc = gstart; gc >= g0; gc -= kWave) {
+      const int gl = gc - lane;
+      const bool in_list = gl >= g0;
+      const int pid_l = in_list ? prim_ids_g[gl] : 0;
+      uint64_t todo = __ballot(in_list && !prim_culled_lane<MODE>(prims_g + pid_l, W));
+      while (todo) {
+        const int k = (int)__builtin_ctzll(todo);
+        todo &= todo - 1;
+        const int g = gc - k;
         bool valid[kPix];
         bool any_valid = false;
 #pragma unroll
@@ -639,28 +920,51 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             valid[p] = L.in_img[p] & (g <= fidx[p]);
             any_valid |= valid[p];
         }
-        const int pid_cur = pid;
-        const PrimRec pr = prims[pid_cur];
-        const int pid_after = prim_ids[max(g - 2, g0)];
-        pid = pid_next;
-        pid_next = pid_after;
         if (__ballot(any_valid) == 0) continue;
-        if (prim_culled<MODE>(pr, W)) continue;
+        const int pid_cur = __builtin_amdgcn_readlane(pid_l, k);
+        const PrimRec pr = prims[pid_cur];
+        // The forward's log record of this entry and wave, if it has one.
+        const int32_t at = log_index_g ? log_index[2 * (size_t)g + wv] : kLogMissing;
+        if (at == kLogEmpty) continue;   // no pixel inside or near: no contribution
+        const bool uniform_inside = at == kLogInside;
         if constexpr (COUNT) n.entries += 1;
-        // The forward's log of this entry and wave: inside bits (its winding
-        // test), exact bits, and each exact pixel's best edge and coverage.
-        // The best edge's distance term is recomputed here with the
-        // forward's expressions (so min_d2 is the forward's minimum; the
-        // index is kept inside the primitive's edge range); the coverage is
-        // the forward's own value.  Every other pixel is decided in closed
-        // form and needs no distance.
+        // From the record: inside bits (the forward's winding test), exact
+        // bits, and each exact pixel's best edge and coverage.  The best
+        // edge's distance term is recomputed with the forward's expressions
+        // (so min_d2 is the forward's minimum; the index is kept inside the
+        // primitive's edge range); the coverage is the forward's own value.
+        // Every other pixel is decided in closed form and needs no distance.
+        // Without a record the forward's edge walk and coverage run again
+        // (the same expressions, so the same values).
         Geom G[kPix];
         bool exact[kPix];
         float lcov[kPix];
-        {
-            const LogHead h = log_head(raster_log, g, wv);
+        if (uniform_inside) {
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) {
+                G[p].winding = 1;
+                G[p].best = pr.e0;
+                G[p].min_d2 = G[p].bproj = G[p].bdx = G[p].bdy = 0.0f;
+                exact[p] = false;
+                lcov[p] = 1.0f;
+            }
+        } else if (at < 0) {
+            const float D2 = pr.cull_d * pr.cull_d, D2o = pr.cull_out * pr.cull_out;
+            int npix = 0;
+            if constexpr (COUNT) npix = wave_count(valid);
+            prim_geometry<MODE, 2, COUNT, MODE == 0>(pr, W, culls, as_const(edges_g), L.px, L.py,
+                                                     load_culls(culls, pr.e0, pr.e1), G, n, npix);
+#pragma unroll
+            for (int p = 0; p < kPix; ++p) {
+                const bool ins = inside_of<MODE>(pr, G[p]);
+                exact[p] = !(G[p].min_d2 > (ins ? D2 : D2o));
+                lcov[p] = exact[p] ? exact_coverage<MODE>(pr, G[p].min_d2, ins) : 0.0f;
+                G[p].winding = (int)ins;
+            }
+        } else {
+            const LogHead h = log_head(log_pool, at);
             int2 lpx[kPix] = {make_int2(0, 0), make_int2(0, 0)};
-            log_pixels(raster_log, g, wv, h, lane, lpx);
+            log_pixels(log_pool, at, h, lane, lpx);
             if constexpr (COUNT)
                 n.dist += (uint64_t)(__builtin_popcountll(h.xm[0]) +
                                      __builtin_popcountll(h.xm[1]));
@@ -848,6 +1152,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             const float t = wave_reduce8(sv);
             if (adder) atomicAdd(v_cubics + 8 * (size_t)s + slot, t);
         }
+      }
     }
     if constexpr (COUNT) flush_counts(n, counts);
 }
@@ -1072,7 +1377,10 @@ struct RasterArgs {
     float* out;
     float* final_T;
     int32_t* final_idx;
-    RasterLog* raster_log;  // written by the forward, read by the backward
+    int32_t* log_index;     // raster log: written by the forward, read by the backward
+    uint4* log_pool;
+    uint32_t log_units;     // pool capacity in 16-byte units
+    uint32_t log_per_entry; // units of a wave's own region per list entry
     // backward inputs / outputs
     const float* fT;
     const int32_t* fidx;
@@ -1091,8 +1399,8 @@ template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
     hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.nt), dim3(kRasterThreads), 0,
                        a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.order, a.wave_cost, a.out, a.final_T, a.final_idx, a.raster_log,
-                       a.counts);
+                       a.nt, a.order, a.wave_cost, a.out, a.final_T, a.final_idx, a.log_index,
+                       a.log_pool, a.log_units, a.log_per_entry, a.counts);
 }
 
 template <int MODE, bool COUNT, bool ADAPTIVE>
@@ -1102,7 +1410,8 @@ static void launch_bwd3(const RasterArgs& a) {
         a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
     hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT, ADAPTIVE>), dim3(a.nt), dim3(kRasterThreads),
                        0, a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.order, a.eps, magic, a.aux, a.raster_log, a.fT, a.fidx, a.v_out,
+                       a.nt, a.order, a.eps, magic, a.aux, a.log_index, a.log_pool, a.fT, a.fidx,
+                       a.v_out,
                        a.v_cub, a.v_col,
                        a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.counts);
 }
@@ -1150,8 +1459,9 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                              const int32_t* tile_bins, const void* edges, const void* edge_culls,
                              const void* prim_recs, const float* background, int32_t img_h,
                              int32_t img_w, int32_t edges_per_segment, float* out_img,
-                             float* final_Ts, int32_t* final_idx,
-                             void* raster_log, unsigned long long* eval_counts,
+                             float* final_Ts, int32_t* final_idx, int64_t num_entries,
+                             int32_t* log_index, void* log_pool, int64_t log_pool_bytes,
+                             int32_t log_entry_units, unsigned long long* eval_counts,
                              const int32_t* tile_order, uint32_t* wave_cost,
                              hipStream_t stream) {
     // The primitive records hold each primitive's edge range, so the forward
@@ -1159,15 +1469,29 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 0 ||
         img_h > kMaxImageDim || img_w > kMaxImageDim)
         return CS_ERR_ARGS;
+    // The waves' own regions take 2 * num_entries * log_entry_units units after
+    // the counter; shared blocks follow.
+    const int64_t units = log_index ? log_pool_bytes / 16 : 0;
+    const int64_t cap = units < (int64_t)kLogMaxUnits ? units : (int64_t)kLogMaxUnits;
+    const int64_t first_shared = 1 + 2 * num_entries * (int64_t)log_entry_units;
+    if (log_index && (!log_pool || (reinterpret_cast<uintptr_t>(log_pool) & 15) != 0 ||
+                      num_entries < 0 || log_entry_units < 0 || first_shared > cap))
+        return CS_ERR_ARGS;
     RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                                background, img_h, img_w, edges_per_segment, stream);
     a.out = out_img;
     a.final_T = final_Ts;
     a.final_idx = final_idx;
-    a.raster_log = reinterpret_cast<RasterLog*>(raster_log);
+    a.log_index = log_index;
+    a.log_pool = log_index ? reinterpret_cast<uint4*>(log_pool) : nullptr;
+    a.log_units = (uint32_t)cap;
+    a.log_per_entry = log_index ? (uint32_t)log_entry_units : 0u;
     a.counts = eval_counts;
     a.order = tile_order;
     a.wave_cost = wave_cost;
+    if (log_index)
+        hipLaunchKernelGGL(k_log_init, dim3(1), dim3(1), 0, stream, a.log_pool,
+                           (uint32_t)first_shared);
     if (eval_counts) launch_fwd_mode<true>(a);
     else launch_fwd_mode<false>(a);
     return raster_status();
@@ -1178,13 +1502,15 @@ extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted
                                     const void* edge_culls, const void* prim_recs,
                                     const float* background,
                                     int32_t img_h, int32_t img_w, int32_t edges_per_segment,
-                                    float* out_img, float* final_Ts,
-                                    int32_t* final_idx, void* raster_log,
+                                    float* out_img, float* final_Ts, int32_t* final_idx,
+                                    int64_t num_entries, int32_t* log_index, void* log_pool,
+                                    int64_t log_pool_bytes, int32_t log_entry_units,
                                     const int32_t* tile_order, uint32_t* wave_cost,
                                     hipStream_t stream) {
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, edges_per_segment, out_img, final_Ts,
-                             final_idx, raster_log, nullptr, tile_order, wave_cost, stream);
+                             final_idx, num_entries, log_index, log_pool, log_pool_bytes,
+                             log_entry_units, nullptr, tile_order, wave_cost, stream);
 }
 
 extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
@@ -1193,13 +1519,17 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
                                             const float* background, int32_t img_h,
                                             int32_t img_w, int32_t edges_per_segment,
                                             float* out_img, float* final_Ts, int32_t* final_idx,
-                                            void* raster_log, unsigned long long* eval_counts,
+                                            int64_t num_entries, int32_t* log_index,
+                                            void* log_pool, int64_t log_pool_bytes,
+                                            int32_t log_entry_units,
+                                            unsigned long long* eval_counts,
                                             const int32_t* tile_order, uint32_t* wave_cost,
                                             hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, edges_per_segment, out_img, final_Ts,
-                             final_idx, raster_log, eval_counts, tile_order, wave_cost, stream);
+                             final_idx, num_entries, log_index, log_pool, log_pool_bytes,
+                             log_entry_units, eval_counts, tile_order, wave_cost, stream);
 }
 
 static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
@@ -1211,15 +1541,15 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               float* v_cubics_px, float* v_colors, float* v_opacities,
                               float* v_inv_sigma2s, float* v_stroke_widths,
                               float* curve_contrib_rgb, float* curve_isect_contrib,
-                              const void* edge_aux, const void* raster_log,
-                              unsigned long long* eval_counts, const int32_t* tile_order,
-                              hipStream_t stream) {
+                              const void* edge_aux, const int32_t* log_index,
+                              const void* log_pool, unsigned long long* eval_counts,
+                              const int32_t* tile_order, hipStream_t stream) {
     if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 ||
         (edge_aux == nullptr && edges_per_segment < 1) || img_h > kMaxImageDim ||
         img_w > kMaxImageDim)
         return CS_ERR_ARGS;
     if (mode == 1 && v_stroke_widths == nullptr) return CS_ERR_ARGS;
-    if (raster_log == nullptr) return CS_ERR_ARGS;
+    if (log_index && !log_pool) return CS_ERR_ARGS;
     RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                                background, img_h, img_w, edges_per_segment, stream);
     a.fT = final_Ts;
@@ -1234,7 +1564,8 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
     a.c_isect = curve_isect_contrib;
     a.aux = reinterpret_cast<const EdgeAux*>(edge_aux);
     if (edge_aux) a.eps = 0;
-    a.raster_log = reinterpret_cast<RasterLog*>(const_cast<void*>(raster_log));
+    a.log_index = const_cast<int32_t*>(log_index);
+    a.log_pool = log_index ? reinterpret_cast<uint4*>(const_cast<void*>(log_pool)) : nullptr;
     a.counts = eval_counts;
     a.order = tile_order;
     if (eval_counts) launch_bwd_mode<true>(a);
@@ -1248,8 +1579,8 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                                      const float* background,
                                      int32_t img_h, int32_t img_w,
                                      int32_t edges_per_segment, const float* final_Ts,
-                                     const int32_t* final_idx, const void* raster_log,
-                                     const float* v_output,
+                                     const int32_t* final_idx, const int32_t* log_index,
+                                     const void* log_pool, const float* v_output,
                                      float* v_cubics_px, float* v_colors, float* v_opacities,
                                      float* v_inv_sigma2s, float* v_stroke_widths,
                                      float* curve_contrib_rgb, float* curve_isect_contrib,
@@ -1259,38 +1590,39 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              raster_log, nullptr, tile_order, stream);
+                              log_index, log_pool, nullptr, tile_order, stream);
 }
 
 extern "C" int cs_rasterize_backward_de_casteljau(
     int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
     const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
     int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
-    const void* raster_log, const float* v_output, float* v_cubics_px, float* v_colors,
-    float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
-    float* curve_isect_contrib, const int32_t* tile_order, hipStream_t stream) {
+    const int32_t* log_index, const void* log_pool, const float* v_output, float* v_cubics_px,
+    float* v_colors, float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
+    float* curve_contrib_rgb, float* curve_isect_contrib, const int32_t* tile_order,
+    hipStream_t stream) {
     if (!edge_aux) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, 0, final_Ts, final_idx, v_output,
                               v_cubics_px, v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
-                              curve_contrib_rgb, curve_isect_contrib, edge_aux, raster_log,
-                              nullptr, tile_order, stream);
+                              curve_contrib_rgb, curve_isect_contrib, edge_aux, log_index,
+                              log_pool, nullptr, tile_order, stream);
 }
 
 extern "C" int cs_rasterize_backward_counted(
     int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
     const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
     int32_t img_w, int32_t edges_per_segment, const float* final_Ts, const int32_t* final_idx,
-    const void* raster_log, const float* v_output, float* v_cubics_px, float* v_colors,
-    float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
-    float* curve_isect_contrib, unsigned long long* eval_counts, const int32_t* tile_order,
-    hipStream_t stream) {
+    const int32_t* log_index, const void* log_pool, const float* v_output, float* v_cubics_px,
+    float* v_colors, float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
+    float* curve_contrib_rgb, float* curve_isect_contrib, unsigned long long* eval_counts,
+    const int32_t* tile_order, hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              raster_log, eval_counts, tile_order, stream);
+                              log_index, log_pool, eval_counts, tile_order, stream);
 }
 
 extern "C" int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,

@@ -163,8 +163,15 @@ class Binned:
         self.primitive_ids_sorted: Optional[torch.Tensor] = None
         # Heavy-first tile order from this forward's raster (for the backward).
         self.tile_order: Optional[torch.Tensor] = None
-        # The forward's raster log per (list entry, wave), for the backward.
-        self.raster_log: Optional[torch.Tensor] = None
+        # The forward's raster log, for the backward: the per-(list entry,
+        # wave) record index and the record pool (None: no log was written;
+        # the backward then recomputes every entry's geometry).
+        self.log_index: Optional[torch.Tensor] = None
+        self.log_pool: Optional[torch.Tensor] = None
+        # Scene-shape key of the log's sizing, and the 16-byte units per list
+        # entry of each wave's own log region in this forward.
+        self.log_key = None
+        self.log_units = 0
         self.grad_accum_clean = True
         # Set while the intersection count has not been read on the host yet
         # (bin_primitives with a capacity hint); resolve_binned() settles it.
@@ -412,37 +419,118 @@ _MAX_ORDERS = 16
 ORDER_CHUNKED = True
 
 
-def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
+# Raster-log sizing per scene shape: each wave's own region holds
+# `units per entry` 16-byte units for every entry of its tile's list; records
+# that do not fit go to shared blocks after the regions.  The shared blocks a
+# forward used are read back without waiting (an async copy of the pool's
+# counter into pinned memory, polled by the next forward of the shape), and
+# grow the regions of the next forward.
+_LOG_PENDING: "dict[tuple, tuple]" = {}   # key -> ((pinned [4], event, device), units,
+#                                            first shared unit, pool bytes)
+_LOG_UNITS: "dict[tuple, int]" = {}       # key -> units per entry of the next forward
+_MAX_LOG_KEYS = 64
+# Units per (list entry, wave) of the first forward of a shape (the benchmark
+# scenes record about 64 bytes, i.e. 4 units, on average).
+LOG_FIRST_UNITS_PER_ENTRY = 6
+LOG_MAX_UNITS_PER_ENTRY = 66     # a record is at most 66 units
+
+
+def _poll_log_use(key) -> None:
+    pend = _LOG_PENDING.get(key)
+    if pend is None:
+        return
+    entry, units, first_shared, pool_bytes = pend
+    if N.hip().hipEventQuery(entry[1]) != 0:
+        return   # not reached yet (or an error the next synchronizing call reports)
+    _LOG_PENDING.pop(key)
+    shared_used = 16 * max(0, int(entry[0][0]) - first_shared)
+    _give_pinned(entry)
+    regions = 16 * (first_shared - 1)
+    # Shared blocks beyond a twentieth of the regions: widen the regions by
+    # the shared use (so the next forward records almost everything in them).
+    if regions > 0 and shared_used * 20 > regions:
+        grow = -(-shared_used * units // regions)
+        units = min(LOG_MAX_UNITS_PER_ENTRY, units + max(1, grow))
+    if len(_LOG_UNITS) >= _MAX_LOG_KEYS and key not in _LOG_UNITS:
+        _LOG_UNITS.pop(next(iter(_LOG_UNITS)))
+    _LOG_UNITS[key] = units
+
+
+def log_layout(key, capacity: int, ntiles: int):
+    """(units per entry, pool bytes) for a forward of scene shape `key` with
+    `capacity` list entries: the waves' own regions, plus shared blocks for a
+    quarter of them and one block per wave."""
+    _poll_log_use(key)
+    units = _LOG_UNITS.get(key, LOG_FIRST_UNITS_PER_ENTRY)
+    regions = 16 * 2 * capacity * units
+    shared = regions // 4 + 2 * ntiles * N.RASTER_LOG_BLOCK_BYTES + (1 << 20)
+    return units, (16 + regions + shared + 255) // 256 * 256
+
+
+def _read_log_use_later(key, pool: torch.Tensor, units: int, first_shared: int,
+                        pool_bytes: int, st) -> None:
+    """Queues a copy of the pool's counter into pinned memory and an event after
+    it, unless one for this shape is still outstanding."""
+    if key in _LOG_PENDING:
+        return
+    dev = pool.device.index if pool.device.index is not None else torch.cuda.current_device()
+    entry = _take_pinned(dev)
+    hip = N.hip()
+    N.hip_check(hip.hipMemcpyAsync(entry[0].data_ptr(), pool.data_ptr(), 4,
+                                   N.HIP_MEMCPY_DEVICE_TO_HOST, st), "hipMemcpyAsync")
+    N.hip_check(hip.hipEventRecord(entry[1], st), "hipEventRecord")
+    if len(_LOG_PENDING) >= _MAX_LOG_KEYS:
+        _, old = _LOG_PENDING.popitem()
+        N.hip_check(hip.hipEventSynchronize(old[0][1]), "hipEventSynchronize")
+        _give_pinned(old[0])
+    _LOG_PENDING[key] = (entry, units, first_shared, pool_bytes)
+
+
+def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log: bool = True,
+                      log_pool_bytes_override: Optional[int] = None):
     """(image [H,W,3], final_Ts, final_idx).  With eval_counts (int64 [5],
     zeroed, on the device) the counting instantiation runs and adds the
-    evaluation counts of cs_rasterize_forward_counted into it.  The launch
-    takes tiles in the heavy-first order of the previous forward of this image
-    size on this stream (if any) and records its wave durations, from which
-    the order of this forward's backward (b.tile_order) and of the next
-    forward is made."""
+    evaluation counts of cs_rasterize_forward_counted into it.  With log (the
+    default) it writes the raster log its backward reads (b.log_index,
+    b.log_pool); without, nothing is allocated for it and a backward would
+    recompute every entry (log_pool_bytes_override sets the pool size with no
+    per-wave regions, for tests of a pool that runs full).  The launch takes tiles in the heavy-first order
+    of the previous forward of this image size on this stream (if any) and
+    records its wave durations, from which the order of this forward's
+    backward (b.tile_order) and of the next forward is made."""
     dev = b.device
     H, W = b.img_h, b.img_w
     out = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
     ntiles = b.ntiles
     cap = max(int(b.primitive_ids_sorted.numel()), 1)
-    # final_Ts, final_idx and the raster log of every (list entry, wave) for
-    # the backward share one allocation; the log's records start on a
-    # 256-byte boundary.
-    o_log = (2 * H * W + 63) // 64 * 64
-    aux = torch.empty((o_log + 2 * cap * N.RASTER_LOG_INTS,), dtype=torch.int32, device=dev)
+    # final_Ts, final_idx and the log's entry index share one allocation.
+    n_index = 2 * cap if log else 0
+    aux = torch.empty((2 * H * W + n_index,), dtype=torch.int32, device=dev)
     final_T = aux[:H * W].view(torch.float32).view(H, W)
     final_idx = aux[H * W:2 * H * W].view(H, W)
-    b.raster_log = aux[o_log:].view(2 * cap, N.RASTER_LOG_INTS)
+    st = N.stream(dev)
+    if log:
+        key = b.log_key if b.log_key is not None else (
+            dev.index, b.mode, b.nprim, b.nseg, H, W, b.samples, b.adaptive)
+        units, pool_bytes = log_layout(key, cap, ntiles)
+        if log_pool_bytes_override is not None:
+            units, pool_bytes = 0, max(16, int(log_pool_bytes_override) // 16 * 16)
+        b.log_index = aux[2 * H * W:]
+        b.log_pool = torch.empty((pool_bytes,), dtype=torch.uint8, device=dev)
+        b.log_units = units
+        log_args = (cap, b.log_index.data_ptr(), b.log_pool.data_ptr(), pool_bytes, units)
+    else:
+        b.log_index = b.log_pool = None
+        log_args = (cap, None, None, 0, 0)
     # The tile order is kept apart: the next forward reads it after this
     # forward's buffers are gone.
     order = torch.empty((ntiles,), dtype=torch.int32, device=dev)
-    st = N.stream(dev)
-    key = (dev.index, st, ntiles)
-    prev = _TILE_ORDERS.get(key)
+    okey = (dev.index, st, ntiles)
+    prev = _TILE_ORDERS.get(okey)
     base = aux.data_ptr()
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), H, W,
-            b.edges_per_segment, N.ptr(out), base, base + 4 * H * W, base + 4 * o_log)
+            b.edges_per_segment, N.ptr(out), base, base + 4 * H * W, *log_args)
     cost = b.ptr("wave_cost")
     prev_p = None if prev is None else prev.data_ptr()
     if eval_counts is not None:
@@ -451,14 +539,24 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None):
     else:
         with N.prof("cubic.fwd.rast"):
             N.call("cs_rasterize_forward", *args, prev_p, cost, st)
+    if log and log_pool_bytes_override is None:
+        _read_log_use_later(key, b.log_pool, units, 1 + 2 * cap * units, pool_bytes, st)
     with N.prof("cubic.fwd.tile_order"):
         N.call("cs_raster_tile_order", cost, ntiles, int(ORDER_CHUNKED), order.data_ptr(), st)
     b.tile_order = order
-    _TILE_ORDERS.pop(key, None)
+    _TILE_ORDERS.pop(okey, None)
     if len(_TILE_ORDERS) >= _MAX_ORDERS:
         _TILE_ORDERS.pop(next(iter(_TILE_ORDERS)))
-    _TILE_ORDERS[key] = order
+    _TILE_ORDERS[okey] = order
     return out, final_T, final_idx
+
+
+def log_pool_counter(b: Binned) -> int:
+    """The log pool's counter after b's forward: the end of the shared blocks
+    reserved, in 16-byte units (a host read; tests)."""
+    if b.log_pool is None:
+        return 0
+    return int(b.log_pool[:4].view(torch.int32)[0].item())
 
 
 def _counts_buffer(t):
@@ -487,8 +585,7 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_opac = rest[3 * P: 4 * P]
     v_is2 = rest[4 * P: 5 * P]
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
-    if b.raster_log is None:
-        raise RuntimeError("the backward needs the raster log of a forward of this binning")
+    log_index, log_pool = N.ptr(b.log_index), N.ptr(b.log_pool)
     if b.adaptive:
         if eval_counts is not None:
             raise ValueError("evaluation counts are measured on the uniform flattening only")
@@ -496,13 +593,14 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
             N.call("cs_rasterize_backward_de_casteljau", b.mode, N.ptr(b.primitive_ids_sorted),
                    b.ptr("tile_bins"), b.ptr("edges"), b.ptr("edge_culls"), b.ptr("prim_recs"),
                    N.ptr(background), b.img_h, b.img_w, b.ptr("edge_aux"), N.ptr(final_T),
-                   N.ptr(final_idx), N.ptr(b.raster_log), N.ptr(v_output), N.ptr(v_px), N.ptr(v_colors),
+                   N.ptr(final_idx), log_index, log_pool, N.ptr(v_output), N.ptr(v_px),
+                   N.ptr(v_colors),
                    N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
                    N.ptr(curve_isect_contrib), N.ptr(b.tile_order), N.stream(dev))
         return v_px, v_colors, v_opac, v_is2, v_sw
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
-            b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(b.raster_log),
+            b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), log_index, log_pool,
             N.ptr(v_output), N.ptr(v_px),
             N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
             N.ptr(curve_isect_contrib))
@@ -624,9 +722,13 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
                        flatten_method=flatten_method_norm)
     # With a hint the raster is enqueued before the host reads the count; if
     # the lists did not fit, they and the raster are redone at full size.
-    out, final_T, final_idx = rasterize_forward(b, bg)
+    # The raster log is written only when a backward can follow (some input
+    # requires a gradient).
+    log = any(ctx.needs_input_grad)
+    b.log_key = hint_key
+    out, final_T, final_idx = rasterize_forward(b, bg, log=log)
     if resolve_binned(b):
-        out, final_T, final_idx = rasterize_forward(b, bg)
+        out, final_T, final_idx = rasterize_forward(b, bg, log=log)
     _remember_capacity(hint_key, b.num_intersects)
     if b.num_intersects <= 0:
         ctx.empty = True

@@ -426,3 +426,105 @@ def test_count_overflow_redo_keeps_backward_consistent():
     for a, r in ((gc1, gc2), (gk1, gk2)):
         ok, err = grad_scale_tol(a.cpu().numpy(), r.cpu().numpy(), rtol=1e-5)
         assert ok, err
+
+
+LOG_CASES = ["small_fill_big", "small_stroke_big", "cfg2", "cfg4_band"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", LOG_CASES)
+@pytest.mark.parametrize("pool", ["none", "tiny"])
+def test_backward_without_a_complete_raster_log(name, pool):
+    """The backward recomputes the geometry of entries the forward did not
+    record: with no log at all (pool "none", the forward of the reference-layout
+    building blocks) and with a pool that runs full part way (pool "tiny": some
+    entries recorded, the rest missing).  Forward bit-exact either way, and the
+    gradients match the oracle as with a full log."""
+    print(f"[partial log] {name} {pool}", flush=True)
+    make, rows = CASES[name]
+    sc = make()
+    b, s = hip_bin(sc)
+    bg = s.background.float().contiguous()
+    if pool == "none":
+        out, T, idx = splat.rasterize_forward(b, bg, log=False)
+        assert b.log_index is None and b.log_pool is None
+    else:
+        full_out, _, _ = splat.rasterize_forward(b, bg)
+        # Shared blocks for a third of the waves and no per-wave regions.
+        nbytes = 16 + 2048 * max(1, (2 * b.ntiles) // 3)
+        out, T, idx = splat.rasterize_forward(b, bg, log_pool_bytes_override=nbytes)
+        missing = int((b.log_index == -2).sum())
+        print(f"  pool {nbytes} bytes: {missing} entries not recorded", flush=True)
+        assert missing > 0
+        assert torch.equal(out, full_out)
+    fw = oracle_forward(sc, rows)
+    r0, r1 = rows if rows else (0, sc.img_h)
+    np.testing.assert_array_equal(_bits(out.cpu().numpy()[r0:r1]), _bits(fw["out"][r0:r1]))
+    np.testing.assert_array_equal(idx.cpu().numpy()[r0:r1], fw["final_idx"][r0:r1])
+    v = random_v_out(sc.img_h, sc.img_w)
+    if rows:
+        v[: rows[0]] = 0
+        v[rows[1]:] = 0
+    b.grad_accum_clean = False
+    v_px, v_col, v_op, v_is2, v_sw = splat.rasterize_backward(b, bg, T, idx, v.cuda())
+    g = O.render_backward(fw, v.numpy())
+    checks = [("v_colors", v_col, g["v_colors"]), ("v_opacities", v_op, g["v_opacities"]),
+              ("v_inv_sigma2s", v_is2, g["v_inv_sigma2s"]),
+              ("v_cubics_px", v_px, g["v_cubics_px"])]
+    if v_sw is not None:
+        checks.append(("v_stroke_widths", v_sw, g["v_stroke_widths"]))
+    check_grads(checks)
+
+
+@pytest.mark.gpu
+def test_raster_log_size_follows_use():
+    """The log pool holds what the forward records, not a 1056-byte record per
+    (list entry, wave): at config 3 it is a small fraction of that, and the
+    regions of the next forward of the scene grow when the shared blocks
+    took a noticeable part of the records."""
+    sc = synth.make_scene(3)
+    b, s = hip_bin(sc)
+    bg = s.background.float().contiguous()
+    key = (b.device.index, b.mode, b.nprim, b.nseg, b.img_h, b.img_w, b.samples, b.adaptive)
+    for k in range(3):
+        splat.rasterize_forward(b, bg)
+        torch.cuda.synchronize()
+        cap = int(b.primitive_ids_sorted.numel())
+        pool = int(b.log_pool.numel())
+        first_shared = 1 + 2 * cap * b.log_units
+        shared = 16 * (splat.log_pool_counter(b) - first_shared)
+        print(f"[log size] forward {k}: I={b.num_intersects}, {b.log_units} units per entry, "
+              f"pool {pool / 2**20:.1f} MiB, shared blocks {shared / 2**20:.2f} MiB", flush=True)
+        assert pool < 2 * cap * 1056 // 4
+        assert 0 <= shared and 16 * first_shared + shared <= pool
+    assert splat._LOG_UNITS.get(key, splat.LOG_FIRST_UNITS_PER_ENTRY) >= b.log_units
+
+
+@pytest.mark.gpu
+def test_render_without_gradients_writes_no_log():
+    """A render whose inputs need no gradient (evaluation, psnr) allocates no
+    raster log: its peak memory stays below that of a render that records
+    one by at least the log's entry index."""
+    import manbo
+    sc = synth.make_scene(2).to("cuda")
+    args = (sc.seg_offsets, sc.colors, sc.opacities, sc.depths, sc.img_h, sc.img_w, 16, 16,
+            sc.background)
+    kw = dict(fill_rules=sc.fill_rules, aa_widths=sc.aa_widths, distance_samples=sc.S)
+
+    def peak(requires_grad):
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        cub = sc.cubics_norm.clone().requires_grad_(requires_grad)
+        img = manbo.ops.render_cubic_fill_splat_tilelang(cub, *args, **kw)
+        torch.cuda.synchronize()
+        return torch.cuda.max_memory_allocated() - base, img
+
+    peak(False)
+    p_no, img_no = peak(False)
+    p_yes, img_yes = peak(True)
+    b, _ = hip_bin(synth.make_scene(2))
+    I = b.num_intersects
+    print(f"[no-grad log] peak {p_no} vs {p_yes} bytes (I={I})", flush=True)
+    assert p_yes - p_no >= 2 * I * 4
+    assert torch.equal(img_no, img_yes.detach())

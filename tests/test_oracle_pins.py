@@ -359,3 +359,22 @@ def test_transmittance_stop():
     # 0.001^2 = 1e-6: the second entry of the tile's list stops the pixel
     tile = (16 // 16) * 2 + 16 // 16
     assert fw["final_idx"][16, 16] == fw["tile_bins"][tile][0] + 1
+
+
+def test_inside_coverage_is_exactly_one_beyond_the_cull_bound():
+    """The raster kernels decide inside pixels with d inv_sigma > 8.5 in closed
+    form (coverage 1.0f, binning.hip cull_distance): the fp32 coverage
+    1 / (1 + exp(-2 d inv_sigma)) with the spec exp is exactly 1 there, for
+    every inv_sigma, while just below 8.3 it is not (the bound is tight to
+    the rounding of 1 + exp)."""
+    f32 = np.float32
+    for inv_sigma in (1.0, 0.5, 2.0, 1.0 / 1.3, 1e4, 3.3, 0.01):
+        s = f32(inv_sigma)
+        for t in np.arange(8.5, 12.0, 1e-3):
+            d = f32(t) / s
+            logit = max(f32(-60.0), min(f32(60.0), -f32(f32(d * s) * f32(2.0))))
+            cov = f32(1.0) / f32(f32(1.0) + f32(O.expf(float(logit))))
+            assert cov == f32(1.0), (inv_sigma, t)
+        d = f32(8.3) / s
+        logit = -f32(f32(d * s) * f32(2.0))
+        assert f32(1.0) / f32(f32(1.0) + f32(O.expf(float(logit)))) != f32(1.0)
