@@ -247,6 +247,37 @@ int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chun
  * recomputes every entry. */
 #define CS_RASTER_LOG_BLOCK_BYTES 2048
 
+/* Raster records (the edges, edge_culls and prim_recs the raster entry points
+ * read) from the reference's raster inputs: flattened edges_px [E, 2, 2],
+ * prim_ids_sorted [I] and one edge range per intersection,
+ * isect_edge_ranges [I, 2] (rasterize_cubic_fill_forward_tilelang,
+ * ops/cubic_splatting.py:2181-2305, and the backward :2572-2747), colors
+ * [P, 3], opacities [P], inv_sigma2s [P], fill_rules [P] (NULL: nonzero rule;
+ * mode 0) or stroke_widths [P] (mode 1).  The records hold one edge range per
+ * primitive, taken from its intersections: *status (device int32) is set to
+ * 0, or ORs 1 when an id lies outside [0, P), 2 when two intersections of one
+ * primitive carry different ranges (or a range outside [0, E]), 4 when one of
+ * the num_tiles tile_bins ranges is not within [0, I]; the records and a
+ * raster over them are then not meaningful (the raster kernels trust their
+ * inputs).  Scratch: prim_edge_ranges [P, 2] and edge_cull_d [E] int32. */
+int cs_raster_records_from_edges(int32_t mode, const float* edges_px, int32_t num_edges,
+                                 const int32_t* prim_ids_sorted,
+                                 const int32_t* isect_edge_ranges, int64_t num_intersects,
+                                 const float* colors, const float* opacities,
+                                 const float* inv_sigma2s, const int32_t* fill_rules,
+                                 const float* stroke_widths, int32_t nprim,
+                                 const int32_t* tile_bins, int32_t num_tiles,
+                                 int32_t* prim_edge_ranges, int32_t* edge_cull_d,
+                                 int32_t* status, void* edges, void* edge_culls,
+                                 void* prim_recs, hipStream_t stream);
+
+/* The (segment, t0, t1) edge records cs_rasterize_backward_de_casteljau reads,
+ * from the adaptive flattening's segment_edge_offsets [nseg + 1],
+ * edge_t_starts / edge_t_ends [E] (ops/cubic_splatting.py:1812-1828). */
+int cs_edge_aux_from_csr(const int32_t* segment_edge_offsets, int32_t nseg,
+                         const float* edge_t_starts, const float* edge_t_ends, int32_t num_edges,
+                         void* edge_aux, hipStream_t stream);
+
 /* rasterize_cubic_fill_forward_kernel (ops/cubic_splatting.py:918-1194) when
  * mode 0, rasterize_cubic_polyline_forward_kernel
  * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  16x16 tiles only.
@@ -393,6 +424,20 @@ int cs_mse_forward(const float* x, const float* y, int64_t n, float* partials, f
 int64_t cs_mse_forward_noalloc_max_elems(void);
 int cs_mse_forward_noalloc(const float* x, const float* y, int64_t n, float* loss,
                            hipStream_t stream);
+
+/* mse_backward_diff_kernel (ops/metric.py:166-202): grad = scale (lhs - rhs)
+ * over n fp32 elements (the reference's mse_backward_diff_tilelang,
+ * ops/metric.py:344-360). */
+int cs_mse_backward_diff(const float* lhs, const float* rhs, int64_t n, float scale, float* grad,
+                         hipStream_t stream);
+
+/* reduce_sum_partial_kernel applied until one value is left
+ * (reduce_sum_1d_tilelang, ops/metric.py:363-382): *out = sum of x[0..n) in
+ * fp32 (device scalar; partials of cs_reduce_sum_partials_elems(n) floats),
+ * two launches, deterministic order.  n >= 1. */
+size_t cs_reduce_sum_partials_elems(int64_t n);
+int cs_reduce_sum_f32(const float* x, int64_t n, float* partials, float* out,
+                      hipStream_t stream);
 
 /* mse_backward_diff_kernel (ops/metric.py:166-202) with the scale
  * grad_loss * 2/n read on the device (metric.py:168 reads it on the host):

@@ -7,10 +7,13 @@ from .cubic_splatting import (
     closed_cubic_fill_segments_tilelang,
     map_cubic_to_intersects_tilelang,
     project_cubics_2d_forward_tilelang,
+    rasterize_cubic_fill_backward_tilelang,
+    rasterize_cubic_fill_forward_tilelang,
     render_cubic_fill_splat_tilelang,
 )
 from .forward2d import project_gaussians_2d_scale_rot_forward_tilelang
 from .intersects import map_gaussian_meta_to_intersects, map_gaussian_to_intersects_tilelang
+from .metric import mse_backward_diff_tilelang, reduce_sum_1d_tilelang
 from .rasterize import rasterize_backward_tilelang, rasterize_forward_tilelang
 from .tile_bins import get_tile_bin_edges_tilelang
 
@@ -25,6 +28,10 @@ __all__ = [
     "get_tile_bin_edges_tilelang",
     "project_cubics_2d_forward_tilelang",
     "map_cubic_to_intersects_tilelang",
+    "rasterize_cubic_fill_backward_tilelang",
+    "rasterize_cubic_fill_forward_tilelang",
     "render_cubic_fill_splat_tilelang",
     "render_cubic_polyline_splat_tilelang",
+    "mse_backward_diff_tilelang",
+    "reduce_sum_1d_tilelang",
 ]

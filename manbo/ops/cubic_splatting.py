@@ -11,6 +11,10 @@ from repo_amd.blocks import (  # noqa: F401
     primitive_tile_ranges_from_segment_tile_ranges as _primitive_tile_ranges_from_segment_tile_ranges,
     project_cubics_2d_forward_tilelang,
 )
+from repo_amd.raster_ref import (  # noqa: F401
+    rasterize_cubic_fill_backward_tilelang,
+    rasterize_cubic_fill_forward_tilelang,
+)
 from repo_amd.rings import (  # noqa: F401
     _ClosedCubicFillSegmentsFn,
     _closed_fill_piecewise_basis_tensors,
@@ -50,5 +54,7 @@ __all__ = [
     "closed_cubic_fill_segments_tilelang",
     "map_cubic_to_intersects_tilelang",
     "project_cubics_2d_forward_tilelang",
+    "rasterize_cubic_fill_backward_tilelang",
+    "rasterize_cubic_fill_forward_tilelang",
     "render_cubic_fill_splat_tilelang",
 ]

@@ -62,6 +62,10 @@ _SIGNATURES = {
                                                      _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                                      _P, _P, _P, _P, _P]),
     "cs_raster_tile_order": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
+    "cs_raster_records_from_edges": (ctypes.c_int, [_I32, _P, _I32, _P, _P, _I64, _P, _P, _P, _P,
+                                                    _P, _I32, _P, _I32, _P, _P, _P, _P, _P, _P,
+                                                    _P]),
+    "cs_edge_aux_from_csr": (ctypes.c_int, [_P, _I32, _P, _P, _I32, _P, _P]),
     "cs_accumulate_edge_grads": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P]),
     "cs_de_casteljau_max_edges_per_segment": (_I32, [_I32]),
     "cs_bin_prepare_de_casteljau": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32,
@@ -85,6 +89,9 @@ _SIGNATURES = {
     "cs_ssim_abc_elems": (_SZ, [_I32, _I32, _I32, _I32]),
     "cs_mse_forward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P]),
     "cs_mse_forward_noalloc_max_elems": (_I64, []),
+    "cs_mse_backward_diff": (ctypes.c_int, [_P, _P, _I64, _F, _P, _P]),
+    "cs_reduce_sum_partials_elems": (_SZ, [_I64]),
+    "cs_reduce_sum_f32": (ctypes.c_int, [_P, _I64, _P, _P, _P]),
     "cs_mse_forward_noalloc": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "cs_mse_backward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
     "cs_ssim": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _F, _F, _P, _P, _P, _P]),

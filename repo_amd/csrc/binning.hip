@@ -1178,6 +1178,153 @@ __global__ __launch_bounds__(256) void k_isect_edge_ranges(const int32_t* __rest
     out[2 * i + 1] = offs[p + 1] * eps;
 }
 
+// ------------------------------------- raster records from reference layouts
+//
+// The reference's raster wrappers take flattened edges [E, 2, 2] and one edge
+// range per intersection (rasterize_cubic_fill_forward_tilelang,
+// ops/cubic_splatting.py:2181-2305; the backward :2572-2747).  The raster
+// kernels here read per-primitive records, so each primitive's range is taken
+// from its intersections (all of which must agree), and the edge and
+// primitive records are built from the edges.
+
+// range[ids[g]] = isect_edge_ranges[g]; status |= 1 for an id outside [0, P).
+__global__ __launch_bounds__(256) void k_scatter_isect_ranges(const int32_t* __restrict__ ids,
+                                                              const int2* __restrict__ ranges,
+                                                              int64_t n, int P,
+                                                              int2* __restrict__ prim_range,
+                                                              int32_t* __restrict__ status) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n) return;
+    const int p = ids[g];
+    if (p < 0 || p >= P) {
+        atomicOr(status, 1);
+        return;
+    }
+    prim_range[p] = ranges[g];
+}
+
+// status |= 2 where an intersection's range differs from its primitive's
+// (or is not a range within [0, E]).
+__global__ __launch_bounds__(256) void k_check_isect_ranges(const int32_t* __restrict__ ids,
+                                                            const int2* __restrict__ ranges,
+                                                            int64_t n, int P, int E,
+                                                            const int2* __restrict__ prim_range,
+                                                            int32_t* __restrict__ status) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n) return;
+    const int p = ids[g];
+    if (p < 0 || p >= P) return;
+    const int2 r = ranges[g], q = prim_range[p];
+    if (r.x != q.x || r.y != q.y || r.x < 0 || r.y < r.x || r.y > E) atomicOr(status, 2);
+}
+
+// status |= 4 for a tile whose list range is not within [0, num_intersects].
+__global__ __launch_bounds__(256) void k_check_tile_bins(const int2* __restrict__ bins, int T,
+                                                         int64_t n, int32_t* __restrict__ status) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const int2 b = bins[t];
+    if (b.x < 0 || b.y < b.x || (int64_t)b.y > n) atomicOr(status, 4);
+}
+
+__device__ __forceinline__ float prim_cull_d_from_is2(int mode, float opacity, float inv_s2,
+                                                     float half_sw) {
+    return cull_distance(mode, opacity, __builtin_sqrtf(fmaxf(inv_s2, kEps)), half_sw);
+}
+
+__device__ __forceinline__ int2 clamp_range(int2 r, int E) {
+    const int a = clampi(r.x, 0, E);
+    return make_int2(a, clampi(r.y, a, E));
+}
+
+// Every edge's cull distance: the largest over the primitives whose range
+// holds it (positive floats order as their bits).
+__global__ __launch_bounds__(256) void k_edge_cull_d(const int2* __restrict__ prim_range, int P,
+                                                     int E, int mode,
+                                                     const float* __restrict__ opacities,
+                                                     const float* __restrict__ inv_s2,
+                                                     const float* __restrict__ stroke_widths,
+                                                     int32_t* __restrict__ edge_d_bits) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= P) return;
+    const float half_sw =
+        (mode == 1 && stroke_widths) ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
+    const float D = prim_cull_d_from_is2(mode, opacities[p], inv_s2[p], half_sw);
+    const int2 r = clamp_range(prim_range[p], E);
+    for (int e = r.x; e < r.y; ++e) atomicMax(edge_d_bits + e, __builtin_bit_cast(int32_t, D));
+}
+
+__global__ __launch_bounds__(256) void k_edges_from_px(const float4* __restrict__ edges_px, int E,
+                                                       const int32_t* __restrict__ edge_d_bits,
+                                                       EdgeRec* __restrict__ edges,
+                                                       EdgeCull* __restrict__ culls) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const float4 a = edges_px[e];
+    write_edge(a.x, a.y, a.z, a.w, __builtin_bit_cast(float, edge_d_bits[e]), edges + e,
+               culls + e);
+}
+
+// Primitive records as k_prim_prep makes them, with the ranges and the
+// closed flag taken from the primitive's edges: the vertex box of its edges,
+// and closed when each edge starts where the previous one ends and the last
+// one ends where the first starts.
+__global__ __launch_bounds__(256) void k_prim_recs_from_edges(
+    const int2* __restrict__ prim_range, int P, int E, int mode,
+    const float4* __restrict__ edges_px, const float* __restrict__ colors,
+    const float* __restrict__ opacities, const float* __restrict__ inv_s2,
+    const int32_t* __restrict__ fill_rules, const float* __restrict__ stroke_widths,
+    PrimRec* __restrict__ recs) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= P) return;
+    const int2 r = clamp_range(prim_range[p], E);
+    PrimRec rec;
+    rec.r = colors[3 * p];
+    rec.g = colors[3 * p + 1];
+    rec.b = colors[3 * p + 2];
+    rec.opacity = opacities[p];
+    rec.inv_sigma2 = fmaxf(inv_s2[p], kEps);
+    rec.inv_sigma = __builtin_sqrtf(fmaxf(inv_s2[p], kEps));
+    rec.half_sw = (mode == 1 && stroke_widths) ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
+    rec.cull_d = cull_distance(mode, rec.opacity, rec.inv_sigma, rec.half_sw);
+    rec.e0 = r.x;
+    rec.e1 = r.y;
+    rec.rule = fill_rules ? fill_rules[p] : 1;
+    VBox box = vbox_empty();
+    int closed = 1;
+    for (int e = r.x; e < r.y; ++e) {
+        const float4 a = edges_px[e];
+        vbox_add(box, a.x, a.y);
+        vbox_add(box, a.z, a.w);
+        const float4 b = edges_px[e + 1 < r.y ? e + 1 : r.x];
+        closed &= (a.z == b.x) & (a.w == b.y);
+    }
+    const SegRec sr = seg_record(box, rec.cull_d);
+    rec.closed = closed;
+    rec.ny_lo = sr.ny_lo;
+    rec.ny_span = sr.ny_span;
+    rec.cy_lo = sr.cy_lo;
+    rec.cy_span = sr.cy_span;
+    rec.nx_lo = sr.nx_lo;
+    rec.nx_span = sr.nx_span;
+    rec.x_last = r.y > r.x ? sr.x_last : -kRangeLimit;
+    rec.cull_out = cull_distance_outside(mode, rec.opacity, rec.inv_sigma, rec.half_sw);
+    recs[p] = rec;
+}
+
+// Per-edge (segment, t0, t1) records from the adaptive flattening's CSR
+// (segment_edge_offsets, edge_t_starts, edge_t_ends; cubic_splatting.py:1812-1828).
+__global__ __launch_bounds__(256) void k_edge_aux_from_csr(const int32_t* __restrict__ seo,
+                                                          int nseg,
+                                                          const float* __restrict__ t0,
+                                                          const float* __restrict__ t1, int E,
+                                                          EdgeAux* __restrict__ aux) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    const int a = clampi(seo[s], 0, E), b = clampi(seo[s + 1], a, E);
+    for (int e = a; e < b; ++e) aux[e] = EdgeAux{s, t0[e], t1[e], 0};
+}
+
 }  // namespace cs
 
 // ===================================================================== C ABI
@@ -1648,5 +1795,57 @@ extern "C" int cs_isect_edge_ranges(const int32_t* prim_ids_sorted, const int32_
     hipLaunchKernelGGL(k_isect_edge_ranges, dim3(blocks_for(num_intersects, 256)), dim3(256), 0,
                        stream, prim_ids_sorted, seg_offsets, num_intersects, edges_per_segment,
                        out);
+    return launch_status();
+}
+
+extern "C" int cs_raster_records_from_edges(
+    int32_t mode, const float* edges_px, int32_t num_edges, const int32_t* prim_ids_sorted,
+    const int32_t* isect_edge_ranges, int64_t num_intersects, const float* colors,
+    const float* opacities, const float* inv_sigma2s, const int32_t* fill_rules,
+    const float* stroke_widths, int32_t nprim, const int32_t* tile_bins, int32_t num_tiles,
+    int32_t* prim_edge_ranges, int32_t* edge_cull_d, int32_t* status, void* edges,
+    void* edge_culls, void* prim_recs, hipStream_t stream) {
+    if ((mode != 0 && mode != 1) || num_edges < 1 || nprim < 1 || num_intersects < 0 ||
+        !status || (mode == 1 && !stroke_widths) || num_tiles < 0 || (num_tiles > 0 && !tile_bins))
+        return CS_ERR_ARGS;
+    int2* pr = reinterpret_cast<int2*>(prim_edge_ranges);
+    hipLaunchKernelGGL(k_fill_i32, dim3(blocks_for(2 * (int64_t)nprim, 256)), dim3(256), 0, stream,
+                       prim_edge_ranges, 2 * nprim, 0);
+    hipLaunchKernelGGL(k_fill_i32, dim3(blocks_for(num_edges, 256)), dim3(256), 0, stream,
+                       edge_cull_d, num_edges, 0);
+    hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(256), 0, stream, status, 1, 0);
+    if (num_intersects > 0) {
+        const int nb = blocks_for(num_intersects, 256);
+        const int2* rg = reinterpret_cast<const int2*>(isect_edge_ranges);
+        hipLaunchKernelGGL(k_scatter_isect_ranges, dim3(nb), dim3(256), 0, stream, prim_ids_sorted,
+                           rg, num_intersects, nprim, pr, status);
+        hipLaunchKernelGGL(k_check_isect_ranges, dim3(nb), dim3(256), 0, stream, prim_ids_sorted,
+                           rg, num_intersects, nprim, num_edges, pr, status);
+    }
+    if (num_tiles > 0)
+        hipLaunchKernelGGL(k_check_tile_bins, dim3(blocks_for(num_tiles, 256)), dim3(256), 0,
+                           stream, reinterpret_cast<const int2*>(tile_bins), num_tiles,
+                           num_intersects, status);
+    const int pb = blocks_for(nprim, 256);
+    hipLaunchKernelGGL(k_edge_cull_d, dim3(pb), dim3(256), 0, stream, pr, nprim, num_edges, mode,
+                       opacities, inv_sigma2s, stroke_widths, edge_cull_d);
+    hipLaunchKernelGGL(k_edges_from_px, dim3(blocks_for(num_edges, 256)), dim3(256), 0, stream,
+                       reinterpret_cast<const float4*>(edges_px), num_edges, edge_cull_d,
+                       reinterpret_cast<EdgeRec*>(edges), reinterpret_cast<EdgeCull*>(edge_culls));
+    hipLaunchKernelGGL(k_prim_recs_from_edges, dim3(pb), dim3(256), 0, stream, pr, nprim,
+                       num_edges, mode, reinterpret_cast<const float4*>(edges_px), colors,
+                       opacities, inv_sigma2s, fill_rules, stroke_widths,
+                       reinterpret_cast<PrimRec*>(prim_recs));
+    return launch_status();
+}
+
+extern "C" int cs_edge_aux_from_csr(const int32_t* segment_edge_offsets, int32_t nseg,
+                                    const float* edge_t_starts, const float* edge_t_ends,
+                                    int32_t num_edges, void* edge_aux, hipStream_t stream) {
+    if (nseg < 0 || num_edges < 0 || !segment_edge_offsets) return CS_ERR_ARGS;
+    if (nseg == 0) return CS_OK;
+    hipLaunchKernelGGL(k_edge_aux_from_csr, dim3(blocks_for(nseg, 256)), dim3(256), 0, stream,
+                       segment_edge_offsets, nseg, edge_t_starts, edge_t_ends, num_edges,
+                       reinterpret_cast<EdgeAux*>(edge_aux));
     return launch_status();
 }

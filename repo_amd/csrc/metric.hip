@@ -111,6 +111,48 @@ __global__ __launch_bounds__(256) void k_mse_bwd(const float* __restrict__ x,
     }
 }
 
+// grad = scale (lhs - rhs), the expression of mse_backward_diff_kernel
+// (ops/metric.py:166-202), four elements per thread.
+__global__ __launch_bounds__(256) void k_scaled_diff(const float* __restrict__ lhs,
+                                                    const float* __restrict__ rhs, int64_t n,
+                                                    float scale, float* __restrict__ grad) {
+    const int64_t i4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i4 + 4 <= n &&
+        ((reinterpret_cast<uintptr_t>(lhs) | reinterpret_cast<uintptr_t>(rhs) |
+          reinterpret_cast<uintptr_t>(grad)) & 15) == 0) {
+        const float4 a = *reinterpret_cast<const float4*>(lhs + i4);
+        const float4 b = *reinterpret_cast<const float4*>(rhs + i4);
+        *reinterpret_cast<float4*>(grad + i4) = make_float4(
+            scale * (a.x - b.x), scale * (a.y - b.y), scale * (a.z - b.z), scale * (a.w - b.w));
+    } else {
+        for (int64_t i = i4; i < i4 + 4 && i < n; ++i) grad[i] = scale * (lhs[i] - rhs[i]);
+    }
+}
+
+// Partial sums of x over chunks of kMseChunk elements (one per workgroup).
+__global__ __launch_bounds__(kMseThreads) void k_sum_partial(const float* __restrict__ x,
+                                                            int64_t n,
+                                                            float* __restrict__ partials) {
+    __shared__ float sh[kMseThreads / kWave];
+    const int64_t base = (int64_t)blockIdx.x * kMseChunk;
+    float acc = 0.0f;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && base + kMseChunk <= n) {
+        const float4* x4 = reinterpret_cast<const float4*>(x + base);
+        float4 a[kMseItems / 4];
+#pragma unroll
+        for (int k = 0; k < kMseItems / 4; ++k) a[k] = x4[k * kMseThreads + threadIdx.x];
+#pragma unroll
+        for (int k = 0; k < kMseItems / 4; ++k) acc += (a[k].x + a[k].y) + (a[k].z + a[k].w);
+    } else {
+        for (int k = 0; k < kMseItems; ++k) {
+            const int64_t i = base + (int64_t)k * kMseThreads + threadIdx.x;
+            if (i < n) acc += x[i];
+        }
+    }
+    const float bs = block_sum(acc, sh);
+    if (threadIdx.x == 0) partials[blockIdx.x] = bs;
+}
+
 // ------------------------------------------------------------------ SSIM
 
 // Output tile: 32 columns x 48 rows per 256-thread workgroup.  The horizontal
@@ -545,6 +587,31 @@ extern "C" int cs_mse_forward_noalloc(const float* x, const float* y, int64_t n,
                        partials);
     hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials, (int)nb,
                        1.0f / (float)n, loss);
+    return metric_status();
+}
+
+extern "C" int cs_mse_backward_diff(const float* lhs, const float* rhs, int64_t n, float scale,
+                                    float* grad, hipStream_t stream) {
+    if (n < 0 || (n > 0 && (!lhs || !rhs || !grad))) return CS_ERR_ARGS;
+    if (n == 0) return CS_OK;
+    const int64_t nb = ((n + 3) / 4 + 255) / 256;
+    if (nb > 0x7fffffff) return CS_ERR_ARGS;
+    hipLaunchKernelGGL(k_scaled_diff, dim3((unsigned)nb), dim3(256), 0, stream, lhs, rhs, n, scale,
+                       grad);
+    return metric_status();
+}
+
+extern "C" size_t cs_reduce_sum_partials_elems(int64_t n) { return cs_mse_partials_elems(n); }
+
+extern "C" int cs_reduce_sum_f32(const float* x, int64_t n, float* partials, float* out,
+                                 hipStream_t stream) {
+    if (n <= 0 || !x || !partials || !out) return CS_ERR_ARGS;
+    const int64_t nb = (n + kMseChunk - 1) / kMseChunk;
+    if (nb > 0x7fffffff) return CS_ERR_ARGS;
+    hipLaunchKernelGGL(k_sum_partial, dim3((unsigned)nb), dim3(kMseThreads), 0, stream, x, n,
+                       partials);
+    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials, (int)nb,
+                       1.0f, out);
     return metric_status();
 }
 

@@ -69,6 +69,43 @@ def mse_forward(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
     return loss
 
 
+def mse_backward_diff_tilelang(lhs: torch.Tensor, rhs: torch.Tensor, *, scale: float,
+                               threads: int = DEFAULT_THREADS) -> torch.Tensor:
+    """ops/metric.py:344-360: grad = scale * (lhs - rhs) as float32, shaped
+    like lhs (threads is accepted for the reference's signature)."""
+    _ = threads
+    N.require_gpu(lhs, "lhs")
+    lhs_flat = lhs.float().contiguous().view(-1)
+    rhs_flat = rhs.float().contiguous().view(-1)
+    if lhs_flat.numel() != rhs_flat.numel():
+        raise ValueError(f"lhs and rhs must have the same number of elements, "
+                         f"got {lhs_flat.numel()} and {rhs_flat.numel()}")
+    grad = torch.empty_like(lhs_flat, dtype=torch.float32)
+    N.call("cs_mse_backward_diff", N.ptr(lhs_flat), N.ptr(rhs_flat), int(lhs_flat.numel()),
+           float(scale), N.ptr(grad), N.stream(lhs.device))
+    return grad.view(lhs.shape)
+
+
+def reduce_sum_1d_tilelang(x: torch.Tensor, *, threads: int = DEFAULT_THREADS,
+                           items_per_thread: int = DEFAULT_ITEMS_PER_THREAD) -> torch.Tensor:
+    """ops/metric.py:363-382: the float32 sum of a 1D tensor as a 0-d device
+    tensor (threads / items_per_thread are accepted for the reference's
+    signature; the blocks here are fixed)."""
+    _ = (threads, items_per_thread)
+    N.require_gpu(x, "x")
+    cur = x.contiguous().view(-1)
+    n = int(cur.numel())
+    if n <= 1:   # the reference's loop does not run: its first element (or IndexError)
+        return cur[0]
+    if cur.dtype is not torch.float32:
+        cur = cur.to(torch.float32)
+    out = torch.empty((), dtype=torch.float32, device=x.device)
+    partials = torch.empty((int(N.lib().cs_reduce_sum_partials_elems(n)),), dtype=torch.float32,
+                           device=x.device)
+    N.call("cs_reduce_sum_f32", N.ptr(cur), n, N.ptr(partials), N.ptr(out), N.stream(x.device))
+    return out
+
+
 class _TileLangMSEFn(torch.autograd.Function):
     """metric.py:134-195 (same signature)."""
 

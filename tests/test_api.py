@@ -82,6 +82,21 @@ REFERENCE_SIGNATURES = {
     "gs_render": ["means2d", "scales2d", "rotation", "colors", "opacities", "img_h", "img_w",
                   "block_x", "block_y", "bg", "process_fn", "*profile_fwd_prefix",
                   "*profile_bwd_prefix"],
+    # ops/cubic_splatting.py:2181-2201, 2572-2601; ops/metric.py:344-350, 363-368.
+    "rasterize_cubic_fill_forward_tilelang": [
+        "tile_bounds", "block", "img_size", "primitive_ids_sorted", "tile_bins", "cubics_px",
+        "primitive_seg_offsets", "colors", "opacities", "fill_rules", "background", "*aa_widths",
+        "*inv_sigma2s", "*edges_px", "*isect_edge_ranges", "*aa_width", "*distance_samples",
+        "*map_threads"],
+    "rasterize_cubic_fill_backward_tilelang": [
+        "tile_bounds", "block", "img_size", "primitive_ids_sorted", "tile_bins", "cubics_px",
+        "primitive_seg_offsets", "colors", "opacities", "fill_rules", "background", "final_Ts",
+        "final_idx", "v_output", "*aa_widths", "*inv_sigma2s", "*edges_px",
+        "*isect_edge_ranges", "*segment_edge_offsets", "*edge_t_starts", "*edge_t_ends",
+        "*aa_width", "*distance_samples", "*flatten_method", "*map_threads",
+        "*curve_contrib_rgb", "*curve_isect_contrib"],
+    "mse_backward_diff_tilelang": ["lhs", "rhs", "*scale", "*threads"],
+    "reduce_sum_1d_tilelang": ["x", "*threads", "*items_per_thread"],
 }
 
 
