@@ -523,6 +523,21 @@ int cs_adam_step(int32_t ntensors, float* const* params, const float* const* gra
                  const float* weight_decays, double beta1, double beta2, double eps,
                  hipStream_t stream);
 
+/* One Adan step (manbo/optim.py:70-190, adan_step_from_grad_kernel
+ * ops/optim.py:8-113; the default optimizer of train.py:106) over up to
+ * CS_ADAM_MAX_TENSORS fp32 tensors in one launch, updating params, exp_avgs,
+ * exp_avg_sqs, exp_avg_diffs and neg_pre_grads in place.  Host arrays of
+ * ntensors entries: numels; scalars [10 k .. 10 k + 9] = beta1, beta2, beta3,
+ * bias_correction1, bias_correction2, sqrt(bias_correction3), lr,
+ * weight_decay, eps, clip factor of tensor k (fp32, as the reference kernel
+ * casts them); flags [2 k] = 1 on the first step (no previous gradient),
+ * flags [2 k + 1] = no_prox.  clip: a device fp32 global-norm clip factor
+ * that replaces the host ones, or NULL. */
+int cs_adan_step(int32_t ntensors, float* const* params, const float* const* grads,
+                 float* const* exp_avgs, float* const* exp_avg_sqs, float* const* exp_avg_diffs,
+                 float* const* neg_pre_grads, const int64_t* numels, const float* scalars,
+                 const int32_t* flags, const float* clip, hipStream_t stream);
+
 /* ---------------- 2D Gaussian splats (GsRenderFunction) ---------------- */
 
 /* project_gaussians_2d_scale_rot_forward_kernel (ops/forward2d.py:14-164):

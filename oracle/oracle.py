@@ -765,3 +765,35 @@ def gs_project_backward(scales2d, rotation, radii, conics, v_xy, v_conic, img_h:
                                   ctypes.c_int32(img_h), ctypes.c_int32(img_w), _p(v_cov),
                                   _p(v_mean), _p(v_scale), _p(v_rot))
     return v_cov, v_mean, v_scale, v_rot
+
+
+# ------------------------------------------------------------------ Adan
+
+
+def adan_step64(p, g, m, n, d, npg, *, step, lr=1e-3, betas=(0.98, 0.92, 0.99), eps=1e-8,
+                weight_decay=0.0, no_prox=False, clip=1.0):
+    """adan_step_from_grad_kernel (ops/optim.py:78-110) in float64 on numpy
+    arrays: returns the new (p, m, n, d, neg_pre_grad)."""
+    p, g, m, n, d, npg = (np.asarray(a, np.float64) for a in (p, g, m, n, d, npg))
+    b1, b2, b3 = (float(b) for b in betas)
+    bc1 = 1.0 - b1 ** step
+    bc2 = 1.0 - b2 ** step
+    bc3_sqrt = (1.0 - b3 ** step) ** 0.5
+    g = g * clip
+    ngod = np.zeros_like(g) if step == 1 else npg + g
+    m = m * b1 + g * (1.0 - b1)
+    d = d * b2 + ngod * (1.0 - b2)
+    ngod2 = ngod * b2 + g
+    n = n * b3 + ngod2 * ngod2 * (1.0 - b3)
+    denom = np.sqrt(n) / bc3_sqrt + eps
+    step_size = lr / bc1
+    step_size_diff = lr * b2 / bc2
+    if no_prox:
+        p = p * (1.0 - lr * weight_decay)
+        p = p - step_size * m / denom
+        p = p - step_size_diff * d / denom
+    else:
+        p = p - step_size * m / denom
+        p = p - step_size_diff * d / denom
+        p = p / (1.0 + lr * weight_decay)
+    return p, m, n, d, -g

@@ -111,6 +111,7 @@ _SIGNATURES = {
     "cs_clamp_mse_ssim_backward": (ctypes.c_int, [_P, _P, _I32, _I32, _F, _F, _P, _I32, _P, _F,
                                                   _P, _P, _P]),
     "cs_adam_step": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _D, _D, _D, _P]),
+    "cs_adan_step": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_gs_project_forward": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
                                              _P, _P, _P]),
     "cs_gs_bin_prepare": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
