@@ -4,9 +4,10 @@ One step = render (fused binning + forward raster) of 4096 closed cubic paths
 (4 segments, S=16) at 2040x1356 -> clamp(0,1) -> NCHW -> loss
 MSE + 0.2 * (1 - SSIM(11, 1.5)) against the synthetic target -> backward ->
 Adam on control points and colors.  Prints one JSON line (see the contract
-in the repository's build notes).
+in the repository's build notes).  --config N runs BASELINE.json's config N
+instead (1-5, each with its own loss; see WORKLOADS).
 
-python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-cpu-baseline]
+python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--config 3] [--no-cpu-baseline]
 """
 from __future__ import annotations
 
@@ -73,19 +74,36 @@ def render(sc, cub, col):
         sc.background, aa_widths=sc.aa_widths, distance_samples=sc.S)
 
 
-def loss_fn(img, target):
-    """clamp(0, 1) -> NCHW -> MSE + 0.2 (1 - SSIM), with the fused kernels
-    that read the [H, W, 3] image in place (the same values as
+# The configurations of BASELINE.json: workload text and SSIM weight of the
+# loss (0: MSE only).
+WORKLOADS = {
+    1: ("64 closed cubic paths x 4 segments, S=8, 128x128, MSE", 0.0),
+    2: ("512 closed cubic paths x 4 segments, S=16, 768x512, MSE+0.2*(1-SSIM 11x11 s=1.5)",
+        SSIM_WEIGHT),
+    3: ("4096 closed cubic paths x 4 segments, S=16, 2040x1356, "
+        "MSE+0.2*(1-SSIM 11x11 s=1.5), Adam on control points+colors", SSIM_WEIGHT),
+    4: ("8192 open cubic strokes x 3 segments, S=16, widths U[1,4] px, 1024x1024, MSE", 0.0),
+    5: ("16384 closed cubic paths x 6 segments, S=32, 2048x2048, 70% of centres in 8 "
+        "clusters, MSE+0.2*(1-SSIM 11x11 s=1.5)", SSIM_WEIGHT),
+}
+
+
+def loss_fn(img, target, ssim_weight):
+    """clamp(0, 1) -> NCHW -> MSE + w (1 - SSIM), with the fused kernels that
+    read the [H, W, 3] image in place (the same values as
     manbo.mse_loss_tilelang + manbo.ssim on
-    img.clamp(0, 1).permute(2, 0, 1).unsqueeze(0))."""
+    img.clamp(0, 1).permute(2, 0, 1).unsqueeze(0)); MSE alone for w = 0."""
+    import manbo
     from repo_amd import fused
-    loss, _ = fused.clamp_mse_ssim_loss(img, target, SSIM_WEIGHT)
+    if ssim_weight == 0:
+        return manbo.mse_loss_tilelang(fused.clamp_to_nchw(img), target)
+    loss, _ = fused.clamp_mse_ssim_loss(img, target, ssim_weight)
     return loss
 
 
-def train_step(sc, cub, col, opt):
+def train_step(sc, cub, col, opt, ssim_weight=SSIM_WEIGHT):
     opt.zero_grad(set_to_none=True)
-    loss = loss_fn(render(sc, cub, col), sc.target)
+    loss = loss_fn(render(sc, cub, col), sc.target, ssim_weight)
     loss.backward()
     opt.step()
     return loss
@@ -148,6 +166,21 @@ def stage_times(sc, cub, col, iters):
     return res
 
 
+def binning_bytes(sc, n_isect):
+    """Minimal HBM bytes of one binning (the algorithmic unit of its
+    roofline): project 32 B read + 16 B written per segment, 16 B per
+    flattened edge vertex pair written, and per intersection 12 B emitted,
+    24 B for one sort pass (read + write of key and value) and 8 B of bins,
+    plus 8 B of bins per tile."""
+    nseg = int(sc.cubics_norm.shape[0])
+    edges = nseg * (sc.S - 1)
+    tiles = ((sc.img_w + 15) // 16) * ((sc.img_h + 15) // 16)
+    parts = {"project": 48 * nseg, "flatten": 16 * edges, "emit": 12 * n_isect,
+             "sort_one_pass": 24 * n_isect, "bins": 8 * n_isect + 8 * tiles}
+    parts["total"] = sum(parts.values())
+    return parts
+
+
 def reference_edge_pixel_evals(b, T, idx):
     """(forward, backward) edge-pixel evaluations of the reference's kernels.
     Forward: every pixel evaluates all edges of each entry of its tile list up
@@ -195,54 +228,112 @@ def performed_evaluations(b, bg, T, idx, v):
     return res
 
 
-def cpu_baseline(cfg):
-    """Times the CPU oracle (single thread) on a bounded sample of one training
-    step: full binning, the forward and backward raster on four 32-row bands
-    spread over the image (scaled to all rows), and the float64 losses."""
+def cpu_model_name():
+    """The host CPU's model name (as lscpu prints it), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def ssim_cpu(x, y, win_size=11, win_sigma=1.5, k1=0.01, k2=0.03):
+    """SSIM of [N, C, H, W] tensors as the CPU baseline computes it: the
+    separable Gaussian window as sums of shifted slices (torch's CPU conv2d
+    is several times slower for 1 x 11 kernels), valid window, mean over
+    pixels, channels and images (metric.py:215-273), differentiable."""
+    import numpy as np
+    import torch
+    # The window in fp32, as the reference builds it (metric.py:47-61).
+    r = np.arange(win_size, dtype=np.float32) - np.float32(win_size // 2)
+    g = np.exp(-(r * r) / np.float32(2 * win_sigma ** 2)).astype(np.float32)
+    g = torch.from_numpy(g / g.sum(dtype=np.float32)).to(x.dtype)
+    z = torch.cat([x, y, x * x, y * y, x * y], 1)
+    w = z.shape[-1] - win_size + 1
+    z = sum(g[k] * z[..., k:k + w] for k in range(win_size))
+    h = z.shape[-2] - win_size + 1
+    z = sum(g[k] * z[..., k:k + h, :] for k in range(win_size))
+    mu1, mu2, ex2, ey2, exy = z.chunk(5, 1)
+    c1, c2 = k1 * k1, k2 * k2
+    s1 = ex2 - mu1 * mu1
+    s2 = ey2 - mu2 * mu2
+    s12 = exy - mu1 * mu2
+    m = ((2 * mu1 * mu2 + c1) / (mu1 * mu1 + mu2 * mu2 + c1)) * ((2 * s12 + c2) / (s1 + s2 + c2))
+    return m.mean()
+
+
+def cpu_train_step(sc, workers, ssim_weight):
+    """One training step of scene ``sc`` on the CPU oracle: binning and the
+    forward raster, clamp -> NCHW -> MSE (+ ssim_weight * (1 - SSIM) when
+    ssim_weight > 0) in fp32 torch autograd (the reference's loss dtype)
+    against the scene's target, the raster backward of that loss's image
+    gradient, and an Adam update of control points and colors.  Returns
+    per-stage seconds."""
     import numpy as np
     import torch
     from oracle import oracle as O
-    from repo_amd import synth
-    sc = synth.make_scene(cfg)
-    d = dict(cubics_norm=sc.cubics_norm.numpy(), offs=sc.seg_offsets.numpy(),
-             colors=sc.colors.numpy(), opac=sc.opacities.numpy(), depths=sc.depths.numpy(),
-             aa=sc.aa_widths.numpy(), bg=sc.background.numpy())
-    H, W = sc.img_h, sc.img_w
+    t = {}
     t0 = time.perf_counter()
-    b = O.bin_scene(d["cubics_norm"], d["offs"], d["depths"], d["aa"], H, W, sc.S)
-    t_bin = time.perf_counter() - t0
-    band = 32
-    starts = [int(H * f) for f in (0.1, 0.35, 0.6, 0.85)]
-    t_fwd = t_bwd = 0.0
-    rng = np.random.default_rng(0)
-    for r0 in starts:
-        rows = (r0, r0 + band)
-        t0 = time.perf_counter()
-        out, T, idx = O.raster_forward(b, d["colors"], d["opac"], d["bg"], H, W, rows=rows)
-        t_fwd += time.perf_counter() - t0
-        fw = dict(b, out=out, final_T=T, final_idx=idx, mode=0, colors=d["colors"],
-                  opacities=d["opac"], fill_rules=None, stroke_widths=None, background=d["bg"],
-                  img_h=H, img_w=W, block_x=16, block_y=16, nseg=d["cubics_norm"].shape[0],
-                  rows=rows)
-        v = rng.standard_normal((H, W, 3)).astype(np.float32)
-        t0 = time.perf_counter()
-        O.render_backward(fw, v)
-        t_bwd += time.perf_counter() - t0
-    scale = H / float(band * len(starts))
-    x = torch.rand((1, 3, H, W), dtype=torch.float64)
-    y = torch.rand((1, 3, H, W), dtype=torch.float64)
-    torch.set_num_threads(1)
+    fw = O.render_forward(sc.cubics_norm.numpy(), sc.seg_offsets.numpy(), sc.colors.numpy(),
+                          sc.opacities.numpy(), sc.depths.numpy(), sc.img_h, sc.img_w,
+                          sc.background.numpy(), fill_rules=sc.fill_rules.numpy(),
+                          aa_widths=sc.aa_widths.numpy(), S=sc.S, workers=workers)
+    t["forward"] = time.perf_counter() - t0
     t0 = time.perf_counter()
-    xr = x.clone().requires_grad_(True)
-    loss = ((xr - y) ** 2).mean() + SSIM_WEIGHT * (1 - O.ssim_torch64(xr, y))
+    img = torch.from_numpy(fw["out"]).requires_grad_(True)
+    x = img.clamp(0, 1).permute(2, 0, 1).unsqueeze(0)
+    y = sc.target
+    loss = ((x - y) ** 2).mean()
+    if ssim_weight > 0:
+        loss = loss + ssim_weight * (1 - ssim_cpu(x, y))
     loss.backward()
-    t_loss = time.perf_counter() - t0
-    step_s = t_bin + (t_fwd + t_bwd) * scale + t_loss
-    return {"value": 1.0 / step_s, "unit": "it/s", "cores": 1, "kind": "port",
-            "sample": (f"C oracle, 1 thread: full binning ({t_bin:.2f}s), forward+backward "
-                       f"raster on {len(starts)}x{band} pixel rows ({t_fwd + t_bwd:.2f}s, scaled "
-                       f"x{scale:.1f} to {H} rows), float64 MSE+SSIM fwd+bwd ({t_loss:.2f}s); "
-                       f"{step_s:.1f}s per step")}
+    v = img.grad.float().numpy()
+    t["loss"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    g = O.render_backward(fw, v)
+    t["backward"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    params = [sc.cubics_norm.clone().requires_grad_(True), sc.colors.clone().requires_grad_(True)]
+    params[0].grad = torch.from_numpy(np.asarray(g["v_cubics_norm"], np.float32)).view_as(params[0])
+    params[1].grad = torch.from_numpy(np.asarray(g["v_colors"], np.float32)).view_as(params[1])
+    torch.optim.Adam(params, lr=1e-3, foreach=False).step()
+    t["adam"] = time.perf_counter() - t0
+    t["step"] = sum(t.values())
+    return t
+
+
+def cpu_baseline(cfg):
+    """The CPU oracle timed on the host's cores (threaded row bands, torch
+    threads likewise): whole training steps of configs 1 (MSE) and 2
+    (MSE + SSIM), one warm-up and the median of five each, then one whole
+    step of the benchmarked config."""
+    import statistics
+    import torch
+    from oracle import oracle as O
+    from repo_amd import synth
+    workers = O.default_workers()
+    torch.set_num_threads(workers)
+    others = {}
+    for c, w in ((1, 0.0), (2, SSIM_WEIGHT)):
+        if c == cfg:
+            continue
+        s = synth.make_scene(c)
+        cpu_train_step(s, workers, w)
+        med = statistics.median(cpu_train_step(s, workers, w)["step"] for _ in range(5))
+        others[f"config{c}"] = {"value": round(1.0 / med, 3), "unit": "it/s",
+                                "ms_per_step": round(1000.0 * med, 2),
+                                "loss": "MSE" if w == 0 else f"MSE+{w}*(1-SSIM)"}
+    st = cpu_train_step(synth.make_scene(cfg), workers, SSIM_WEIGHT)
+    stages = ", ".join(f"{k} {v:.2f}s" for k, v in st.items() if k != "step")
+    return {"value": round(1.0 / st["step"], 4), "unit": "it/s", "cores": workers,
+            "kind": "port", "cpu_count": os.cpu_count(), "cpu_model": cpu_model_name(),
+            "sample": (f"C oracle + fp32 torch losses on {workers} threads: one whole "
+                       f"config{cfg} training step, nothing extrapolated ({stages}; "
+                       f"{st['step']:.2f}s per step)"),
+            "other_configs": others}
 
 
 def load_traffic(kernel, cfg):
@@ -275,9 +366,10 @@ def main():
     import torch
     from repo_amd import _native, profiling
     torch.backends.cudnn.benchmark = False
+    workload, ssim_weight = WORKLOADS[args.config]
     sc, cub, col, opt = make_problem(args.config)
     for _ in range(args.warmup):
-        train_step(sc, cub, col, opt)
+        train_step(sc, cub, col, opt, ssim_weight)
     # The raster launches of the timed steps are bracketed by HIP events on
     # the stream they run on (torch's current stream).
     timer = profiling.EventTimer(RASTER_LABELS, reserve=args.steps)
@@ -285,7 +377,7 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        loss = train_step(sc, cub, col, opt)
+        loss = train_step(sc, cub, col, opt, ssim_weight)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     _native.set_profile_ctx_factory(None)
@@ -304,6 +396,7 @@ def main():
     kern["mse_bwd_GBs"] = round(gbs(12 * n_img, st["mse_bwd_ms"]), 1)
     kern["ssim_fwd_GBs"] = round(gbs(8 * n_img, st["ssim_fwd_ms"]), 1)
     kern["reference_edge_pixel_evals"] = {"raster_fwd": evals_fwd, "raster_bwd": evals_bwd}
+    kern["binning_algorithmic_bytes"] = binning_bytes(sc, st["num_intersects"])
     kern["timed_region_launch_ms"] = {k: round(v, 4) for k, v in launch_ms.items()}
     kern["performed_evaluations"] = performed
     # Dominant kernel: the longer raster launch of the timed steps.  Its
@@ -317,7 +410,8 @@ def main():
     achieved = flops / (dom_ms * 1e-3) / 1e12
     ref_units = evals_bwd if dom == "raster_bwd" else evals_fwd
     ref_equiv = ref_units * FLOPS_PER_EVAL[b.mode] / (dom_ms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
+    roofline = {"bound": "mfma", "compute": "fp32 vector ALU (no matrix instructions)",
+                "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
                 "traffic": load_traffic(dom, args.config), "kernel": dom,
                 "launch_ms": round(dom_ms, 4),
@@ -331,18 +425,18 @@ def main():
                         "reference_equivalent_TFLOPs prices the reference kernel's full "
                         "edge loop over the same launch time"}
     line = {
-        "metric": "train it/s, 4096 closed cubics @2040x1356 fp32",
+        "metric": ("train it/s, 4096 closed cubics @2040x1356 fp32" if args.config == 3
+                   else f"train it/s, config {args.config} fp32"),
         "value": round(1000.0 / ms, 3), "unit": "it/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"config{args.config}: "
-                   + ("4096 closed cubic paths x 4 segments, S=16, 2040x1356, "
-                      "MSE+0.2*(1-SSIM 11x11 s=1.5), Adam on control points+colors"
-                      if args.config == 3 else "see repo_amd/synth.py"),
+        "config": {"workload": f"config{args.config}: {workload}",
                    "num_intersects": st["num_intersects"], "final_loss": float(loss)},
         "kernels": kern, "roofline": roofline,
     }
-    if not args.no_cpu_baseline:
+    # The CPU step of configs 4 and 5 would take minutes; their lines carry
+    # no cpu_baseline.
+    if not args.no_cpu_baseline and args.config in (1, 2, 3):
         line["cpu_baseline"] = cpu_baseline(args.config)
     if args.copy_calibration_mib > 0:
         copy_calibration(args.copy_calibration_mib)

@@ -136,3 +136,18 @@ def test_separable_ssim_nonnegative_clamps_channel_means():
     got = float(O.ssim64_separable(x, y, nonnegative=True))
     assert abs(got - 0.5 * per_c[0]) < 1e-12
     assert abs(float(O.ssim64_separable(x, y)) - 0.5 * (per_c[0] + per_c[1])) < 1e-12
+
+
+def test_bench_cpu_ssim_equals_the_oracle():
+    """The shifted-slice SSIM the CPU baseline times computes the oracle's
+    SSIM (value and gradient, float64)."""
+    import bench
+    g = torch.Generator().manual_seed(4)
+    x = torch.rand((2, 3, 40, 57), generator=g, dtype=torch.float64, requires_grad=True)
+    y = torch.rand((2, 3, 40, 57), generator=g, dtype=torch.float64)
+    a = bench.ssim_cpu(x, y)
+    (ga,) = torch.autograd.grad(a, x)
+    b = O.ssim_torch64(x, y)
+    (gb,) = torch.autograd.grad(b, x)
+    assert abs(float(a) - float(b)) <= 1e-12
+    assert float((ga - gb).abs().max()) <= 1e-12 * float(gb.abs().max()) + 1e-15
