@@ -97,16 +97,13 @@ int cs_isect_edge_ranges(const int32_t* prim_ids_sorted, const int32_t* seg_offs
  * (ops/cubic_splatting.py:1709-1719), per-primitive tile counts, depth ranks
  * (order[r] = primitive of depth rank r, ties by primitive id, and
  * rank_tile_ranges [nprim,4] its tile rectangle), per-tile list lengths
- * (tile_count [T]) with their per-part offsets (tile_part_base [K*T],
- * K = cs_bin_tile_parts(...)), per-row-segment first slots (tile_scratch [T]),
+ * (tile_count [T]), per-row-segment first slots (tile_scratch [T]),
  * and status[4] (device int32) = {intersection total, 1 if seg_offsets is not
  * a valid CSR of nseg segments (the kernels then clamp every range),
  * seg_offsets[0], seg_offsets[nprim]}.  T = ceil(W/block_x) * ceil(H/block_y).
  * keys, keys_alt, vals_alt hold nprim elements; radix_counts
  * cs_radix_counts_elems(nprim); scan_temp cs_scan_temp_elems(max(nprim, T)).
  * mode 0 = closed fill, 1 = open stroke (stroke_widths required). */
-int32_t cs_bin_tile_parts(int32_t nprim, int32_t img_h, int32_t img_w, int32_t block_x,
-                          int32_t block_y);
 int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const float* colors,
                    const float* opacities, const float* depths, const int32_t* fill_rules,
                    const float* aa_widths, const float* stroke_widths, int32_t nseg,
@@ -116,8 +113,7 @@ int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const f
                    void* edge_culls, int32_t* prim_tile_ranges, uint32_t* num_tiles_hit,
                    float* inv_sigma2s, void* prim_recs, uint32_t* keys, int32_t* order,
                    uint32_t* keys_alt, int32_t* vals_alt, uint32_t* radix_counts,
-                   uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_part_base,
-                   uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
+                   uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
                    hipStream_t stream);
 
 /* ---------------- adaptive (de Casteljau) flattening ---------------- */
@@ -148,8 +144,7 @@ int cs_bin_prepare_de_casteljau(
     void* seg_recs, void* edges, void* edge_culls, int32_t* prim_tile_ranges,
     uint32_t* num_tiles_hit, float* inv_sigma2s, void* prim_recs, uint32_t* keys,
     int32_t* order, uint32_t* keys_alt, int32_t* vals_alt, uint32_t* radix_counts,
-    uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_part_base,
-    uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status, int32_t* seg_edge_offsets,
+    uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status, int32_t* seg_edge_offsets,
     void* edge_aux, uint32_t* leaf_counts, hipStream_t stream);
 
 /* _flatten_cubics_to_edges, de Casteljau branch (ops/cubic_splatting.py:1729-1832),
@@ -195,8 +190,7 @@ int cs_cubic_split_half(const float* cubics, int32_t n, float* left, float* righ
  * saves that step a separate fill. */
 int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t nprim,
                   const int32_t* status, int64_t capacity, int32_t img_h, int32_t img_w,
-                  int32_t block_x, int32_t block_y, uint32_t* tile_part_base,
-                  uint32_t* tile_count, uint32_t* tile_scratch, int32_t* prim_ids_sorted,
+                  int32_t block_x, int32_t block_y, uint32_t* tile_count, uint32_t* tile_scratch, int32_t* prim_ids_sorted,
                   int32_t* tile_bins, float* zero_buf, int64_t zero_n, hipStream_t stream);
 
 /* ---------------- rasterization ---------------- */
@@ -563,7 +557,7 @@ int cs_gs_bin_prepare(const float* xys, const float* conics, const int32_t* radi
                       int32_t block_x, int32_t block_y, int32_t* tile_rects, uint32_t* keys,
                       int32_t* order, uint32_t* keys_alt, int32_t* vals_alt,
                       uint32_t* radix_counts, uint32_t* scan_temp, int32_t* rank_tile_ranges,
-                      uint32_t* tile_part_base, uint32_t* tile_count, uint32_t* tile_scratch,
+                      uint32_t* tile_count, uint32_t* tile_scratch,
                       int32_t* status, hipStream_t stream);
 
 /* The per-Gaussian raster records (48 bytes each, 16-byte aligned) that the

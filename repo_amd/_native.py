@@ -36,7 +36,6 @@ _SZ = ctypes.c_size_t
 _SIGNATURES = {
     "cs_scan_temp_elems": (_SZ, [_I32]),
     "cs_radix_counts_elems": (_SZ, [_I32]),
-    "cs_bin_tile_parts": (_I32, [_I32, _I32, _I32, _I32, _I32]),
     "cs_scan_exclusive_u32": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P]),
     "cs_radix_sort_pairs_u32": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _P, _P, _P]),
     "cs_project_cubics_2d_forward": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F,
@@ -47,9 +46,8 @@ _SIGNATURES = {
     "cs_isect_edge_ranges": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _P]),
     "cs_bin_prepare": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                       _I32, _I32, _I32, _F, _I32, _I32, _P, _P, _P, _P, _P, _P,
-                                      _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                      _P]),
-    "cs_bin_finish": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P,
+                                      _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cs_bin_finish": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _I32, _I32, _I32, _I32, _P, _P,
                                      _P, _P, _P, _I64, _P]),
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
                                             _P, _I64, _P, _P, _I64, _I32, _P, _P, _P]),
@@ -72,7 +70,7 @@ _SIGNATURES = {
                                                    _I32, _I32, _I32, _I32, _I32, _F, _I32, _I32,
                                                    _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                                    _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                                   _P, _P]),
+                                                   _P]),
     "cs_flatten_cubics_de_casteljau": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P,
                                                       _P, _P, _P, _P]),
     "cs_flatten_cubics_bernstein": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
@@ -115,7 +113,7 @@ _SIGNATURES = {
     "cs_gs_project_forward": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
                                              _P, _P, _P]),
     "cs_gs_bin_prepare": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,
-                                         _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+                                         _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_gs_pack_records": (ctypes.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
     "cs_gs_rasterize_forward": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _P, _P,
                                                _P]),

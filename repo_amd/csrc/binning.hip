@@ -1,19 +1,23 @@
 // Tile binning for the cubic splat path on MI355X (gfx950).
 //
 // Pipeline (one forward):
-//   k_project_flatten  thread per cubic segment: normalized -> pixel space,
-//                      exact AABB -> padded 16x16 tile range, uniform
-//                      Bernstein flattening into 32-byte edge records and a
-//                      per-segment vertex bounding box.
+//   k_project_flatten_wave  workgroup per 64 cubic segments: normalized ->
+//                      pixel space, exact AABB -> padded 16x16 tile range
+//                      (lane per segment), then uniform Bernstein flattening
+//                      into 32-byte edge records and a per-segment vertex
+//                      bounding box (lane per sample point).
 //   k_prim_prep        thread per primitive: union of its segments' tile
-//                      ranges, tile count, depth sort key, raster record.
+//                      ranges, tile count, depth sort key, raster record;
+//                      ranks each workgroup's 256 keys among themselves when
+//                      the merge ranks the keys.
 //   depth rank         stable rank of the 32-bit depth keys (ties by
-//                      primitive id): one rank-by-counting launch up to 16K
-//                      primitives, LSD radix sort above.
-//   k_tile_lists<0>    per (tile, rank part) counts of the primitives whose
-//                      tile rectangle covers the tile, prefix over parts.
-//   exclusive scan     tile totals -> first slot of each tile, total I.
-//   k_tile_lists<1>    each tile's primitives, in rank order, into its slots;
+//                      primitive id): all-pairs counting up to 8K
+//                      primitives, merge of the ranked blocks by binary
+//                      search up to 16K, LSD radix sort above.
+//   k_tile_counts      per-tile counts of the primitives whose tile rectangle
+//                      covers the tile, per row segment of 64 tiles.
+//   exclusive scan     segment totals -> first slot of each segment, total I.
+//   k_tile_scatter     each tile's primitives, in rank order, into its slots;
 //                      tile_bins [start, end) per tile.
 //
 // Listing each tile's primitives in depth-rank order yields exactly the order
@@ -442,17 +446,24 @@ __global__ __launch_bounds__(256) void k_project_flatten(
     seg_recs[s] = seg_record(box, D);
 }
 
-// Uniform flattening with one lane per sample point, for S <= 64: a group of
-// L = 2^ceil(log2 S) consecutive lanes shares segment s.  Lane i evaluates
-// point min(i, S - 1) with the expression of k_project_flatten, takes point
-// i + 1 from its neighbour and writes edge i; a butterfly min/max over the
-// group gives the vertex box (min/max are order-independent), and lane 0
-// writes the projected control points, the tile range and the segment
-// record.  Thread 0 of the grid also sets the status words (k_status_init),
-// which the later launches of the binning update.  Same outputs as
-// k_project_flatten, with nseg * L lanes instead of nseg threads.
+// Uniform flattening for S <= 64, one workgroup of four waves per 64
+// consecutive segments.  Projection: lane j of wave 0 projects segment
+// base + j (owning primitive, cull distance, exact AABB, tile range), writes
+// its pixel-space control points and tile range, and stages the control
+// points and cull distance in LDS.  Flattening: groups of L = 2^ceil(log2 S)
+// lanes take the staged segments 64 / L at a time, the four waves taking
+// turns; lane i of a group evaluates point min(i, S - 1) with the expression
+// of k_project_flatten, takes point i + 1 from its neighbour and writes
+// edge i (consecutive lanes write consecutive records); a butterfly min/max
+// over the group gives the vertex box (min/max are order-independent) and
+// lane 0 writes the segment record.  Each segment is projected once, not
+// once per sample.  Thread 0 of the grid also sets the status words
+// (k_status_init), which the later launches of the binning update.  Same
+// outputs as k_project_flatten.
+constexpr int kFlattenWaves = 4;
+
 template <int L>
-__global__ __launch_bounds__(256) void k_project_flatten_lanes(
+__global__ __launch_bounds__(kWave * kFlattenWaves) void k_project_flatten_wave(
     const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
     const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths,
     const float* __restrict__ opacities, int mode, int nseg, int img_h, int img_w, int block_x,
@@ -460,49 +471,70 @@ __global__ __launch_bounds__(256) void k_project_flatten_lanes(
     int32_t* __restrict__ seg_tile_ranges, SegRec* __restrict__ seg_recs,
     EdgeRec* __restrict__ edges, EdgeCull* __restrict__ culls, int32_t* __restrict__ status) {
     static_assert(L >= 2 && L <= kWave && (L & (L - 1)) == 0, "group of lanes");
-    const size_t gt = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gt == 0) {
+    constexpr int G = kWave / L;  // segments per flattening step
+    __shared__ float stage[9][kWave];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
         status[0] = 0;
         status[1] = 0;
         status[2] = seg_offsets[0];
         status[3] = seg_offsets[P];
     }
-    // Groups never straddle a workgroup (256 is a multiple of L), so a
-    // group's lanes leave together.
-    const size_t s64 = gt / L;
-    if (s64 >= (size_t)nseg) return;
-    const int s = (int)s64;
-    const int i = (int)(gt & (L - 1));
-    const int p = owner_of(seg_offsets, P, s);
-    const float w = fmaxf(aa_widths[p], kWidthMin);
-    const float support = fmaxf(0.0f, w * 3.0f);
-    const float half_sw = stroke_widths ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
-    const float D = prim_params(mode, aa_widths[p], opacities[p], stroke_widths, p).cull_d;
-    const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
-    const SegProj r = project_segment(cubics_norm + (size_t)s * 8, 0.5f * (float)img_w,
-                                      0.5f * (float)img_h, half_sw, support, aabb_pad, aniso, tbx,
-                                      tby, (float)block_x, (float)block_y);
-    float x, y;
-    bezier_point(r.px, r.py, linspace01(S, min(i, S - 1)), x, y);
-    const float nx = __shfl_down(x, 1, L), ny = __shfl_down(y, 1, L);
-    if (i < S - 1)
-        write_edge(x, y, nx, ny, D, edges + (size_t)s * (S - 1) + i,
-                   culls + (size_t)s * (S - 1) + i);
-    VBox box = vbox_empty();
-    vbox_add(box, x, y);
-#pragma unroll
-    for (int off = L / 2; off >= 1; off >>= 1) {
-        box.x0 = fminf(box.x0, __shfl_xor(box.x0, off, L));
-        box.x1 = fmaxf(box.x1, __shfl_xor(box.x1, off, L));
-        box.y0 = fminf(box.y0, __shfl_xor(box.y0, off, L));
-        box.y1 = fmaxf(box.y1, __shfl_xor(box.y1, off, L));
-    }
-    if (i == 0) {
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t base = (int64_t)blockIdx.x * kWave;
+    const int nw = (int)min((int64_t)kWave, (int64_t)nseg - base);
+    if (w == 0 && lane < nw) {
+        const int s = (int)base + lane;
+        const int p = owner_of(seg_offsets, P, s);
+        const float wd = fmaxf(aa_widths[p], kWidthMin);
+        const float support = fmaxf(0.0f, wd * 3.0f);
+        const float half_sw = stroke_widths ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
+        const float D = prim_params(mode, aa_widths[p], opacities[p], stroke_widths, p).cull_d;
+        const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
+        const SegProj r = project_segment(cubics_norm + (size_t)s * 8, 0.5f * (float)img_w,
+                                          0.5f * (float)img_h, half_sw, support, aabb_pad, aniso,
+                                          tbx, tby, (float)block_x, (float)block_y);
         float4* cp = reinterpret_cast<float4*>(cubics_px + (size_t)s * 8);
         cp[0] = make_float4(r.px[0], r.py[0], r.px[1], r.py[1]);
         cp[1] = make_float4(r.px[2], r.py[2], r.px[3], r.py[3]);
         reinterpret_cast<int4*>(seg_tile_ranges)[s] = make_int4(r.tx0, r.ty0, r.tx1, r.ty1);
-        seg_recs[s] = seg_record(box, D);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            stage[k][lane] = r.px[k];
+            stage[4 + k][lane] = r.py[k];
+        }
+        stage[8][lane] = D;
+    }
+    __syncthreads();
+    const int g = lane / L, i = lane & (L - 1);
+    const float t = linspace01(S, min(i, S - 1));
+    for (int q = w * G; q < nw; q += kFlattenWaves * G) {
+        const int j = q + g;
+        const bool seg_ok = j < nw;
+        const int jc = seg_ok ? j : nw - 1;
+        float X[4], Y[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            X[k] = stage[k][jc];
+            Y[k] = stage[4 + k][jc];
+        }
+        const float D = stage[8][jc];
+        float x, y;
+        bezier_point(X, Y, t, x, y);
+        const float nx = __shfl_down(x, 1, L), ny = __shfl_down(y, 1, L);
+        const size_t s = (size_t)base + j;
+        if (seg_ok && i < S - 1)
+            write_edge(x, y, nx, ny, D, edges + s * (S - 1) + i, culls + s * (S - 1) + i);
+        VBox box = vbox_empty();
+        vbox_add(box, x, y);
+#pragma unroll
+        for (int off = L / 2; off >= 1; off >>= 1) {
+            box.x0 = fminf(box.x0, __shfl_xor(box.x0, off, L));
+            box.x1 = fmaxf(box.x1, __shfl_xor(box.x1, off, L));
+            box.y0 = fminf(box.y0, __shfl_xor(box.y0, off, L));
+            box.y1 = fmaxf(box.y1, __shfl_xor(box.y1, off, L));
+        }
+        if (seg_ok && i == 0) seg_recs[s] = seg_record(box, D);
     }
 }
 
@@ -622,19 +654,42 @@ __global__ __launch_bounds__(256) void k_split_half(const float* __restrict__ cu
     }
 }
 
-__global__ __launch_bounds__(256) void k_prim_prep(
+// Depth ranks of at most kRankPairsMax keys: one launch of all-pairs
+// counting.  Up to kRankSortMax: the first stage ranks each block of
+// kRankBlock keys among themselves (k_prim_prep does it for the cubic path,
+// k_rank_blocks for the others), the second merges the blocks.
+constexpr int kRankPairsMax = 8192;
+constexpr int kRankSortMax = 16384;
+constexpr int kRankBlock = 256;
+
+// Position of key ki (thread t) among the 256 keys of ks in (key, index)
+// order.  Slots past a block's end hold the largest key: they sit after every
+// real slot, so they never precede one.
+__device__ __forceinline__ int rank_in_block(const uint4* ks, uint32_t ki, int t) {
+    int r = 0;
+#pragma unroll 16
+    for (int q = 0; q < kRankBlock / 4; ++q) {
+        const uint4 k4 = ks[q];
+        const int j = 4 * q;
+        r += (int)((k4.x < ki) | ((k4.x == ki) & (j < t)));
+        r += (int)((k4.y < ki) | ((k4.y == ki) & (j + 1 < t)));
+        r += (int)((k4.z < ki) | ((k4.z == ki) & (j + 2 < t)));
+        r += (int)((k4.w < ki) | ((k4.w == ki) & (j + 3 < t)));
+    }
+    return r;
+}
+
+// One primitive of k_prim_prep; returns its depth key.
+__device__ __forceinline__ uint32_t prim_prep_one(
     const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
     const int32_t* __restrict__ seg_tile_ranges, const SegRec* __restrict__ seg_recs,
     const float* __restrict__ colors, const float* __restrict__ opacities,
     const float* __restrict__ depths, const int32_t* __restrict__ fill_rules,
     const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
     int eps, const int32_t* __restrict__ seg_edge_offsets, int tbx, int tby, int mode,
-    int32_t* __restrict__ status,
-    int32_t* __restrict__ prim_tile_ranges, uint32_t* __restrict__ counts,
-    float* __restrict__ inv_sigma2s, uint32_t* __restrict__ keys, int32_t* __restrict__ vals,
-    PrimRec* __restrict__ recs) {
-    const int p = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= P) return;
+    int32_t* __restrict__ status, int32_t* __restrict__ prim_tile_ranges,
+    uint32_t* __restrict__ counts, float* __restrict__ inv_sigma2s, uint32_t* __restrict__ keys,
+    int32_t* __restrict__ vals, PrimRec* __restrict__ recs, int p) {
     int s0 = seg_offsets[p], s1 = seg_offsets[p + 1];
     // Invalid CSR offsets are reported through status[1] and clamped so that
     // no kernel reads outside the segment arrays.
@@ -665,7 +720,8 @@ __global__ __launch_bounds__(256) void k_prim_prep(
 
     // cubic_splatting.py:801-805: float order as unsigned order.
     const int32_t bits = __builtin_bit_cast(int32_t, depths[p]);
-    keys[p] = (uint32_t)(bits ^ ((bits >> 31) | (int32_t)0x80000000));
+    const uint32_t key = (uint32_t)(bits ^ ((bits >> 31) | (int32_t)0x80000000));
+    keys[p] = key;
     vals[p] = p;
 
     PrimRec rec;
@@ -708,6 +764,40 @@ __global__ __launch_bounds__(256) void k_prim_prep(
     rec.x_last = x_last;
     rec.cull_out = cull_distance_outside(mode, opacities[p], q.inv_sigma, q.half_sw);
     recs[p] = rec;
+    return key;
+}
+
+__global__ __launch_bounds__(256) void k_prim_prep(
+    const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
+    const int32_t* __restrict__ seg_tile_ranges, const SegRec* __restrict__ seg_recs,
+    const float* __restrict__ colors, const float* __restrict__ opacities,
+    const float* __restrict__ depths, const int32_t* __restrict__ fill_rules,
+    const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
+    int eps, const int32_t* __restrict__ seg_edge_offsets, int tbx, int tby, int mode,
+    int32_t* __restrict__ status,
+    int32_t* __restrict__ prim_tile_ranges, uint32_t* __restrict__ counts,
+    float* __restrict__ inv_sigma2s, uint32_t* __restrict__ keys, int32_t* __restrict__ vals,
+    PrimRec* __restrict__ recs, uint32_t* __restrict__ block_sorted,
+    int32_t* __restrict__ block_rank) {
+    static_assert(kRankBlock == 256, "one rank block per workgroup");
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t key = 0xffffffffu;
+    if (p < P) key = prim_prep_one(cubics_norm, seg_offsets, P, seg_tile_ranges, seg_recs,
+                                   colors, opacities, depths, fill_rules, aa_widths,
+                                   stroke_widths, nseg, eps, seg_edge_offsets, tbx, tby, mode,
+                                   status, prim_tile_ranges, counts, inv_sigma2s, keys, vals,
+                                   recs, p);
+    if (block_sorted) {
+        // The first stage of the depth rank (as k_rank_blocks).
+        __shared__ uint4 ks[kRankBlock / 4];
+        reinterpret_cast<uint32_t*>(ks)[threadIdx.x] = key;
+        __syncthreads();
+        if (p < P) {
+            const int r = rank_in_block(ks, key, (int)threadIdx.x);
+            block_sorted[blockIdx.x * kRankBlock + r] = key;
+            block_rank[p] = r;
+        }
+    }
 }
 
 // status = [intersection total, bad-offsets flag, offs[0], offs[P]].
@@ -883,13 +973,20 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_scatter(
     }
 }
 
-// Stable sort of up to kRankSortMax keys by counting, one wave per key: key
-// i's position in the ascending stable order is the number of keys that are
-// smaller, or equal with a smaller index.  Lanes count over interleaved
-// (coalesced) slices of the key array, which every wave reads from cache, and
-// one wave sum gives the position.  n^2 comparisons spread over n waves: one
-// launch, where the radix sort needs five per 8-bit pass.
-constexpr int kRankSortMax = 16384;
+// Stable sort of up to kRankSortMax keys (ascending, ties by index) in two
+// launches.  k_rank_blocks: each 256-key block ranks its keys among
+// themselves in LDS (the number of block keys that are smaller, or equal with
+// a smaller index) and writes the block in sorted order.  k_rank_merge: a
+// workgroup takes 64 keys and holds all sorted blocks in LDS (at most
+// 64 KB); its 16 waves split the other blocks and, for each, count that
+// block's keys that precede the key: keys <= it in earlier blocks (smaller
+// indices), keys < it in later ones, each a binary search, four searches
+// interleaved.
+// In-block rank plus those counts is the key's position in the stable order:
+// n log(256) n / 256 comparisons instead of n^2.
+constexpr int kMergeKeys = kWave;  // keys per workgroup, 64 per key group
+constexpr int kMergeWaves = 16;    // waves per key group, each a 16th of the blocks
+constexpr int kMergeThreads = kMergeKeys * kMergeWaves;
 
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
@@ -897,15 +994,119 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     return v;
 }
 
-__device__ __forceinline__ int precedes(uint32_t kj, int j, uint32_t ki, int i) {
-    return (int)((kj < ki) | ((kj == ki) & (j < i)));
+__global__ __launch_bounds__(kRankBlock) void k_rank_blocks(const uint32_t* __restrict__ keys,
+                                                           int n,
+                                                           uint32_t* __restrict__ sorted_keys,
+                                                           int32_t* __restrict__ block_rank) {
+    __shared__ uint4 ks[kRankBlock / 4];
+    const int t = threadIdx.x;
+    const int base = blockIdx.x * kRankBlock;
+    const int len = min(kRankBlock, n - base);
+    const uint32_t ki = t < len ? keys[base + t] : 0xffffffffu;
+    reinterpret_cast<uint32_t*>(ks)[t] = ki;
+    __syncthreads();
+    if (t >= len) return;
+    const int r = rank_in_block(ks, ki, t);
+    sorted_keys[base + r] = ki;
+    block_rank[base + t] = r;
 }
 
-// Lanes take 4 consecutive keys per step (one 16-byte load), 4 steps unrolled
-// so that the loads overlap.
-__device__ __forceinline__ int stable_rank(const uint32_t* __restrict__ keys, int n, int i,
-                                           uint32_t ki) {
+// Keys of the sorted block at sk[base, base + len) before ki: a prefix of
+// the block (<= ki when `earlier`, < ki otherwise); steps 256, 128, ..., 1
+// cover every count 0..256.
+__device__ __forceinline__ int count_before(const uint32_t* sk, int base, int len, uint32_t ki,
+                                            bool earlier) {
+    int cnt = 0;
+#pragma unroll
+    for (int step = kRankBlock; step >= 1; step >>= 1) {
+        const int probe = cnt + step;
+        const uint32_t v = sk[base + min(probe, len) - 1];
+        if (probe <= len && (earlier ? v <= ki : v < ki)) cnt = probe;
+    }
+    return cnt;
+}
+
+// PAIRS: kout[pos] = key i, vout[pos] = vals[i]; otherwise order[pos] = i and
+// rank_rects[pos] = rects[i].
+template <bool PAIRS>
+__global__ __launch_bounds__(kMergeThreads) void k_rank_merge(
+    const uint32_t* __restrict__ keys, const uint32_t* __restrict__ sorted_keys,
+    const int32_t* __restrict__ block_rank, int n, const int32_t* __restrict__ vals,
+    uint32_t* __restrict__ kout, int32_t* __restrict__ vout, const int4* __restrict__ rects,
+    int32_t* __restrict__ order, int4* __restrict__ rank_rects) {
+    __shared__ uint32_t sk[kRankSortMax];
+    {
+        // All loads in flight before the first LDS store.
+        constexpr int kPer = kRankSortMax / kMergeThreads;
+        uint32_t v[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int j = k * kMergeThreads + (int)threadIdx.x;
+            if (k * kMergeThreads < n) v[k] = j < n ? sorted_keys[j] : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
+            if (k * kMergeThreads < n) sk[k * kMergeThreads + threadIdx.x] = v[k];
+    }
+    __syncthreads();
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+    const int grp = wv / kMergeWaves, w = wv - grp * kMergeWaves;
     const int lane = threadIdx.x & (kWave - 1);
+    const int i = blockIdx.x * kMergeKeys + grp * kWave + lane;
+    const bool ok = i < n;
+    const uint32_t ki = ok ? keys[i] : 0u;
+    const int own = i / kRankBlock;
+    const int nblocks = (n + kRankBlock - 1) / kRankBlock;
+    int cnt = 0;
+    // Wave w of the group takes blocks w, w + 16, ...; four searches per step.
+    for (int b0 = w; b0 < nblocks; b0 += 4 * kMergeWaves) {
+        int c[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int b = b0 + u * kMergeWaves;
+            const int bb = min(b, nblocks - 1);
+            const int base = bb * kRankBlock;
+            const int len = min(kRankBlock, n - base);
+            c[u] = count_before(sk, base, len, ki, bb < own);
+            if (b >= nblocks || b == own) c[u] = 0;
+        }
+        cnt += (c[0] + c[1]) + (c[2] + c[3]);
+    }
+    // The partial counts reuse the key array once every search is done.
+    __syncthreads();
+    int* part = reinterpret_cast<int*>(sk);
+    part[(grp * kMergeWaves + w) * kWave + lane] = cnt;
+    __syncthreads();
+    if (w != 0 || !ok) return;
+    const int* pg = part + grp * kMergeWaves * kWave + lane;
+    int sum = 0;
+#pragma unroll
+    for (int q = 0; q < kMergeWaves; ++q) sum += pg[q * kWave];
+    const int pos = block_rank[i] + sum;
+    if (PAIRS) {
+        kout[pos] = ki;
+        vout[pos] = vals[i];
+    } else {
+        order[pos] = i;
+        rank_rects[pos] = rects[i];
+    }
+}
+
+// Stable rank by counting, one wave per key, for at most kRankPairsMax keys:
+// key i's position is the number of keys that are smaller, or equal with a
+// smaller index.  Lanes count over interleaved (coalesced) 4-key slices of
+// the key array, which every wave reads from cache, and one wave sum gives
+// the position: n^2 comparisons in one launch, the cheapest form while n is
+// small.  PAIRS and the outputs as for k_rank_merge.
+template <bool PAIRS>
+__global__ __launch_bounds__(256) void k_rank_allpairs(
+    const uint32_t* __restrict__ keys, int n, const int32_t* __restrict__ vals,
+    uint32_t* __restrict__ kout, int32_t* __restrict__ vout, const int4* __restrict__ rects,
+    int32_t* __restrict__ order, int4* __restrict__ rank_rects) {
+    const int i = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (i >= n) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t ki = keys[i];
     int cnt = 0;
     const int n4 = n & ~3;
     const bool vec = (reinterpret_cast<uintptr_t>(keys) & 15) == 0;
@@ -914,27 +1115,26 @@ __device__ __forceinline__ int stable_rank(const uint32_t* __restrict__ keys, in
 #pragma unroll 4
         for (j0 = 4 * lane; j0 < n4; j0 += 4 * kWave) {
             const uint4 q = *reinterpret_cast<const uint4*>(keys + j0);
-            cnt += precedes(q.x, j0, ki, i) + precedes(q.y, j0 + 1, ki, i) +
-                   precedes(q.z, j0 + 2, ki, i) + precedes(q.w, j0 + 3, ki, i);
+            cnt += (int)((q.x < ki) | ((q.x == ki) & (j0 < i)));
+            cnt += (int)((q.y < ki) | ((q.y == ki) & (j0 + 1 < i)));
+            cnt += (int)((q.z < ki) | ((q.z == ki) & (j0 + 2 < i)));
+            cnt += (int)((q.w < ki) | ((q.w == ki) & (j0 + 3 < i)));
         }
         j0 = n4;
     }
-    for (int j = j0 + lane; j < n; j += kWave) cnt += precedes(keys[j], j, ki, i);
-    return wave_sum_i(cnt);
-}
-
-// order[position of key i] = i.
-// Also copies primitive i's tile rectangle to its rank's slot of rank_rects.
-__global__ __launch_bounds__(256) void k_rank_order(const uint32_t* __restrict__ keys, int n,
-                                                   const int4* __restrict__ prim_rects,
-                                                   int32_t* __restrict__ order,
-                                                   int4* __restrict__ rank_rects) {
-    const int i = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (i >= n) return;
-    const int pos = stable_rank(keys, n, i, keys[i]);
-    if ((threadIdx.x & (kWave - 1)) == 0) {
-        order[pos] = i;
-        rank_rects[pos] = prim_rects[i];
+    for (int j = j0 + lane; j < n; j += kWave) {
+        const uint32_t kj = keys[j];
+        cnt += (int)((kj < ki) | ((kj == ki) & (j < i)));
+    }
+    const int pos = wave_sum_i(cnt);
+    if (lane == 0) {
+        if (PAIRS) {
+            kout[pos] = ki;
+            vout[pos] = vals[i];
+        } else {
+            order[pos] = i;
+            rank_rects[pos] = rects[i];
+        }
     }
 }
 
@@ -946,21 +1146,6 @@ __global__ __launch_bounds__(256) void k_gather_rects(const int32_t* __restrict_
     if (r < n) rank_rects[r] = prim_rects[order[r]];
 }
 
-// (key, value) pairs into their stable sorted positions of kout / vout.
-__global__ __launch_bounds__(256) void k_rank_pairs(const uint32_t* __restrict__ keys,
-                                                   const int32_t* __restrict__ vals, int n,
-                                                   uint32_t* __restrict__ kout,
-                                                   int32_t* __restrict__ vout) {
-    const int i = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (i >= n) return;
-    const uint32_t ki = keys[i];
-    const int pos = stable_rank(keys, n, i, ki);
-    if ((threadIdx.x & (kWave - 1)) == 0) {
-        kout[pos] = ki;
-        vout[pos] = vals[i];
-    }
-}
-
 // ------------------------------------------------------------ emit and bins
 
 __global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ a, int n, int32_t v) {
@@ -970,110 +1155,186 @@ __global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ a, int n
 
 // Per-tile lists without a global sort.  Primitives cover rectangles of
 // tiles and arrive in depth-rank order (order[r], rank_rects[r]), so the list
-// of tile t is the subsequence of ranks whose rectangle contains t, and a
-// stable counting sort by tile needs, per (tile, rank), the number of earlier
-// ranks covering the tile.  One workgroup owns a row segment of up to 64 tiles
-// (lane = tile column) and splits the ranks into K contiguous parts, one wave
-// each.  A wave walks its part in 64-rank chunks (the next chunk's loads in
-// flight): lanes test one rectangle each against the segment's row and
-// columns, and for each hit (in rank order) every lane checks its own column.
-//   counting launch: per-part counts -> their prefix over parts (part_base),
-//     tile totals (tile_count) and the segment's total (seg_scratch[seg]);
+// of tile t is the subsequence of ranks whose rectangle contains t.  One
+// workgroup owns a row segment of up to 64 tiles.
+//   counting launch: the waves stride over all ranks (eight 64-rank loads in
+//     flight per wave); each rectangle that meets the segment adds +1 at its
+//     first column and -1 past its last in an LDS difference array, whose
+//     prefix sum is the per-tile count: tile_count, and the segment's total
+//     in seg_scratch[seg];
 //   exclusive scan of the segment totals (in place; its total is I);
 //   scatter launch: tile start = segment start + prefix of the segment's tile
-//     totals; each wave walks its ranks again with a per-lane cursor, and the
-//     first wave writes tile_bins.
+//     totals (wave 0 writes tile_bins), then the ranks in chunks of
+//     kListChunk:
+//     1. each wave takes a contiguous slice of the chunk and tests its
+//        rectangles against the segment; the hits (primitive id and column
+//        range within the segment) go to one LDS list in rank order, each
+//        wave's after the hits of the slices before it;
+//     2. each wave owns kListTilesPerWave tile columns and reads that list 64
+//        hits at a time: per owned tile a ballot of the hits whose range
+//        contains it gives, in rank order, the tile's next entries, written
+//        to consecutive slots (mbcnt) of its list.
 constexpr int kSegTiles = kWave;
-constexpr int kMaxTileParts = 16;
+constexpr int kListWaves = 8;
+constexpr int kListTilesPerWave = kSegTiles / kListWaves;
+constexpr int kListChunk = 4096;
+constexpr int kListSlice = kListChunk / kListWaves;
+constexpr int kListSteps = kListSlice / kWave;
 
-template <bool SCATTER>
-__global__ __launch_bounds__(kWave * kMaxTileParts) void k_tile_lists(
-    const int32_t* __restrict__ order, const int4* __restrict__ rank_rects, int P,
-    int ranks_per_part, int tbx, int tby, int nsegcols, uint32_t* __restrict__ part_base,
-    uint32_t* __restrict__ tile_count, uint32_t* __restrict__ seg_scratch,
-    int32_t* __restrict__ prim_ids_sorted, int32_t* __restrict__ tile_bins,
-    float* __restrict__ zero_buf, int64_t zero_n, const int32_t* __restrict__ total,
-    int64_t capacity) {
-    __shared__ uint32_t cnt[kMaxTileParts][kWave];
-    if (SCATTER && zero_buf) {
-        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += stride)
-            zero_buf[i] = 0.0f;
-    }
-    const int K = (int)(blockDim.x / kWave);
-    const int part = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__device__ __forceinline__ bool rect_meets_row(const int4& q, int ty, int sx0, int sx1) {
+    return q.y <= ty && ty < q.w && q.x < sx1 && q.z > sx0;
+}
+
+__global__ __launch_bounds__(kWave * kListWaves) void k_tile_counts(
+    const int4* __restrict__ rank_rects, int P, int tbx, int nsegcols,
+    uint32_t* __restrict__ tile_count, uint32_t* __restrict__ seg_scratch) {
+    __shared__ int diff[kSegTiles + 1];
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     const int lane = threadIdx.x & (kWave - 1);
     const int ty = blockIdx.x / nsegcols;
     const int sx0 = (blockIdx.x - ty * nsegcols) * kSegTiles;
     const int sx1 = min(sx0 + kSegTiles, tbx);
-    const int tx = sx0 + lane;
-    const bool tile_ok = tx < sx1;
-    const size_t T = (size_t)tbx * tby;
-    const size_t t = (size_t)ty * tbx + tx;
-    const int r0 = part * ranks_per_part, r1 = min(r0 + ranks_per_part, P);
-    uint32_t cur = 0;
-    if (SCATTER) {
-        if ((uint64_t)(uint32_t)*total > (uint64_t)capacity) {
-            // The lists do not fit the caller's buffer: every tile reads as
-            // empty, nothing is scattered, and the caller retries at full size.
-            if (part == 0 && tile_ok) {
-                tile_bins[2 * t] = 0;
-                tile_bins[2 * t + 1] = 0;
-            }
-            return;
+    if (threadIdx.x <= kSegTiles) diff[threadIdx.x] = 0;
+    __syncthreads();
+    for (int r0 = w * kWave * kListSteps; r0 < P; r0 += kListWaves * kWave * kListSteps) {
+        int4 tr[kListSteps];
+#pragma unroll
+        for (int k = 0; k < kListSteps; ++k) {
+            const int rr = r0 + k * kWave + lane;
+            tr[k] = rr < P ? rank_rects[rr] : make_int4(0, 0, 0, 0);
         }
-        const uint32_t n = tile_ok ? tile_count[t] : 0u;
+#pragma unroll
+        for (int k = 0; k < kListSteps; ++k) {
+            const int4 q = tr[k];
+            if (rect_meets_row(q, ty, sx0, sx1)) {
+                atomicAdd(&diff[max(q.x, sx0) - sx0], 1);
+                atomicAdd(&diff[min(q.z, sx1) - sx0], -1);
+            }
+        }
+    }
+    __syncthreads();
+    if (w == 0) {
+        const uint32_t n = (uint32_t)wave_incl_scan((uint32_t)diff[lane], lane);
+        const bool tile_ok = sx0 + lane < sx1;
+        if (tile_ok) tile_count[(size_t)ty * tbx + sx0 + lane] = n;
+        const uint32_t seg = (uint32_t)wave_sum_i(tile_ok ? (int)n : 0);
+        if (lane == 0) seg_scratch[blockIdx.x] = seg;
+    }
+}
+
+__global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
+    const int32_t* __restrict__ order, const int4* __restrict__ rank_rects, int P, int tbx,
+    int nsegcols, const uint32_t* __restrict__ tile_count,
+    const uint32_t* __restrict__ seg_scratch, int32_t* __restrict__ prim_ids_sorted,
+    int32_t* __restrict__ tile_bins, float* __restrict__ zero_buf, int64_t zero_n,
+    const int32_t* __restrict__ total, int64_t capacity) {
+    __shared__ int32_t hit_pid[kListChunk];
+    __shared__ uint32_t hit_cols[kListChunk];
+    __shared__ int hit_n[kListWaves];
+    __shared__ uint32_t tile_start[kSegTiles];
+    if (zero_buf) {
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += stride)
+            zero_buf[i] = 0.0f;
+    }
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+    const int lane = threadIdx.x & (kWave - 1);
+    const int ty = blockIdx.x / nsegcols;
+    const int sx0 = (blockIdx.x - ty * nsegcols) * kSegTiles;
+    const int sx1 = min(sx0 + kSegTiles, tbx);
+    const size_t row0 = (size_t)ty * tbx + sx0;
+    if ((uint64_t)(uint32_t)*total > (uint64_t)capacity) {
+        // The lists do not fit the caller's buffer: every tile reads as
+        // empty, nothing is scattered, and the caller retries at full size.
+        if (w == 0 && sx0 + lane < sx1) {
+            tile_bins[2 * (row0 + lane)] = 0;
+            tile_bins[2 * (row0 + lane) + 1] = 0;
+        }
+        return;
+    }
+    if (w == 0) {
+        const bool tile_ok = sx0 + lane < sx1;
+        const uint32_t n = tile_ok ? tile_count[row0 + lane] : 0u;
         const uint32_t start = seg_scratch[blockIdx.x] + wave_incl_scan(n, lane) - n;
-        if (tile_ok) cur = start + part_base[(size_t)part * T + t];
-        if (part == 0 && tile_ok) {
+        tile_start[lane] = start;
+        if (tile_ok) {
             // tile_bins.py:10-43: [start, end) per tile, (0, 0) when empty.
-            tile_bins[2 * t] = n ? (int32_t)start : 0;
-            tile_bins[2 * t + 1] = n ? (int32_t)(start + n) : 0;
+            tile_bins[2 * (row0 + lane)] = n ? (int32_t)start : 0;
+            tile_bins[2 * (row0 + lane) + 1] = n ? (int32_t)(start + n) : 0;
         }
     }
-    int p_next = 0;
-    int4 tr_next = make_int4(0, 0, 0, 0);
-    if (r0 + lane < r1) {
-        p_next = order[r0 + lane];
-        tr_next = rank_rects[r0 + lane];
-    }
-    for (int c = r0; c < r1; c += kWave) {
-        const int p = p_next;
-        const int4 tr = tr_next;
-        const bool valid = c + lane < r1;
-        if (c + kWave + lane < r1) {
-            p_next = order[c + kWave + lane];
-            tr_next = rank_rects[c + kWave + lane];
+    __syncthreads();
+    uint32_t cur[kListTilesPerWave];
+#pragma unroll
+    for (int k = 0; k < kListTilesPerWave; ++k) cur[k] = tile_start[w * kListTilesPerWave + k];
+    for (int c0 = 0; c0 < P; c0 += kListChunk) {
+        // 1. Compact the chunk's hits into one list (this wave's loads all
+        //    in flight before the first test).
+        const int r0 = c0 + w * kListSlice;
+        const int r1 = min(r0 + kListSlice, P);
+        int4 tr[kListSteps];
+        int pid[kListSteps];
+#pragma unroll
+        for (int k = 0; k < kListSteps; ++k) {
+            const int rr = r0 + k * kWave + lane;
+            tr[k] = rr < r1 ? rank_rects[rr] : make_int4(0, 0, 0, 0);
+            pid[k] = rr < r1 ? order[rr] : 0;
         }
-        const bool hit = valid && tr.y <= ty && ty < tr.w && tr.x < sx1 && tr.z > sx0;
-        for (uint64_t m = __ballot(hit); m; m &= m - 1) {
-            const int b = (int)__builtin_ctzll(m);
-            const int x0 = __builtin_amdgcn_readlane(tr.x, b);
-            const int x1 = __builtin_amdgcn_readlane(tr.z, b);
-            const bool in = tile_ok && tx >= x0 && tx < x1;
-            if (SCATTER) {
-                const int pid = __builtin_amdgcn_readlane(p, b);
-                if (in) prim_ids_sorted[cur] = pid;
-            }
-            cur += in ? 1u : 0u;
+        bool hit[kListSteps];
+        int n_w = 0;
+#pragma unroll
+        for (int k = 0; k < kListSteps; ++k) {
+            hit[k] = rect_meets_row(tr[k], ty, sx0, sx1);
+            n_w += __builtin_popcountll(__ballot(hit[k]));
         }
-    }
-    if (!SCATTER) {
-        cnt[part][lane] = cur;
+        if (lane == 0) hit_n[w] = n_w;
         __syncthreads();
-        if (part == 0) {
-            uint32_t acc = 0;
-            if (tile_ok) {
-                for (int k = 0; k < K; ++k) {
-                    const uint32_t v = cnt[k][lane];
-                    part_base[(size_t)k * T + t] = acc;
-                    acc += v;
-                }
-                tile_count[t] = acc;
-            }
-            const uint32_t seg = (uint32_t)wave_sum_i((int)acc);
-            if (lane == 0) seg_scratch[blockIdx.x] = seg;
+        int nh = 0, slot0 = 0;
+#pragma unroll
+        for (int v = 0; v < kListWaves; ++v) {
+            const int c = hit_n[v];
+            slot0 += v < w ? c : 0;
+            nh += c;
         }
+#pragma unroll
+        for (int k = 0; k < kListSteps; ++k) {
+            const uint64_t m = __ballot(hit[k]);
+            if (hit[k]) {
+                const int4 q = tr[k];
+                const int slot = slot0 + (int)lanes_below(m);
+                hit_pid[slot] = pid[k];
+                hit_cols[slot] = (uint32_t)(max(q.x, sx0) - sx0) |
+                                 ((uint32_t)(min(q.z, sx1) - sx0) << 16);
+            }
+            slot0 += __builtin_popcountll(m);
+        }
+        __syncthreads();
+        // 2. The owned tiles' next entries, 64 hits at a time (the next
+        //    group's LDS reads in flight).
+        uint32_t cols_n = lane < nh ? hit_cols[lane] : 0u;
+        int pid_n = lane < nh ? hit_pid[lane] : 0;
+        for (int j = 0; j < nh; j += kWave) {
+            const uint32_t cols = cols_n;
+            const int pidv = pid_n;
+            const int jn = j + kWave + lane;
+            cols_n = jn < nh ? hit_cols[jn] : 0u;
+            pid_n = jn < nh ? hit_pid[jn] : 0;
+            const int x0 = (int)(cols & 0xffffu), x1 = (int)(cols >> 16);
+#pragma unroll
+            for (int k = 0; k < kListTilesPerWave; ++k) {
+                const int col = w * kListTilesPerWave + k;
+                const bool in = x0 <= col && col < x1;
+                const uint64_t m = __ballot(in);
+                if (in) prim_ids_sorted[cur[k] + lanes_below(m)] = pidv;
+                cur[k] += (uint32_t)__builtin_popcountll(m);
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -1371,7 +1632,10 @@ extern "C" int cs_scan_exclusive_u32(const uint32_t* in, uint32_t* out, int32_t 
 
 extern "C" size_t cs_radix_counts_elems(int32_t n) {
     const int nb = blocks_for(n > 0 ? n : 1, kRsTile);
-    return (size_t)256 * nb;
+    const size_t radix = (size_t)256 * nb;
+    // The sort of at most kRankSortMax keys stages 2n words here.
+    const size_t rank = n > kRankPairsMax && n <= kRankSortMax ? (size_t)2 * n : 0;
+    return radix > rank ? radix : rank;
 }
 
 extern "C" int cs_radix_sort_pairs_u32(uint32_t* keys, int32_t* vals, uint32_t* keys_alt,
@@ -1383,8 +1647,24 @@ extern "C" int cs_radix_sort_pairs_u32(uint32_t* keys, int32_t* vals, uint32_t* 
     const int nb = blocks_for(n, kRsTile);
     const int passes = (key_bits + 7) / 8;
     if (n <= kRankSortMax) {
-        hipLaunchKernelGGL(k_rank_pairs, dim3((n + 3) / 4), dim3(256), 0, stream, keys, vals, n,
-                           keys_alt, vals_alt);
+        // Ranked into the *_alt buffers and copied back; the block sort of
+        // the merge path stages its sorted blocks in counts[0, n) and the
+        // in-block ranks in counts[n, 2n).
+        if (n <= kRankPairsMax) {
+            hipLaunchKernelGGL(k_rank_allpairs<true>, dim3((n + 3) / 4), dim3(256), 0, stream,
+                               keys, n, vals, keys_alt, vals_alt, (const int4*)nullptr,
+                               (int32_t*)nullptr, (int4*)nullptr);
+        } else {
+            uint32_t* sorted = counts;
+            int32_t* brank = reinterpret_cast<int32_t*>(counts + n);
+            const int nblk = blocks_for(n, kRankBlock);
+            hipLaunchKernelGGL(k_rank_blocks, dim3(nblk), dim3(kRankBlock), 0, stream, keys, n,
+                               sorted, brank);
+            hipLaunchKernelGGL(k_rank_merge<true>, dim3(blocks_for(n, kMergeKeys)),
+                               dim3(kMergeThreads), 0, stream, keys, sorted, brank, n, vals,
+                               keys_alt, vals_alt, (const int4*)nullptr, (int32_t*)nullptr,
+                               (int4*)nullptr);
+        }
         if (hipMemcpyAsync(keys, keys_alt, sizeof(uint32_t) * n, hipMemcpyDeviceToDevice,
                            stream) != hipSuccess ||
             hipMemcpyAsync(vals, vals_alt, sizeof(int32_t) * n, hipMemcpyDeviceToDevice,
@@ -1416,35 +1696,30 @@ extern "C" int cs_radix_sort_pairs_u32(uint32_t* keys, int32_t* vals, uint32_t* 
 }
 
 
-// Parts per row segment for the tile lists: enough waves to fill the chip
-// (about 4096), at least 64 ranks per part, at most kMaxTileParts.
-static int tile_parts(int nprim, int tbx, int tby) {
-    const int64_t nsegs = (int64_t)tby * ((tbx + kSegTiles - 1) / kSegTiles);
-    int64_t k = (4096 + nsegs - 1) / nsegs;
-    const int64_t by_ranks = (nprim + kWave - 1) / kWave;
-    if (k > by_ranks) k = by_ranks;
-    if (k > kMaxTileParts) k = kMaxTileParts;
-    return (int)(k < 1 ? 1 : k);
-}
-
-extern "C" int32_t cs_bin_tile_parts(int32_t nprim, int32_t img_h, int32_t img_w,
-                                     int32_t block_x, int32_t block_y) {
-    if (nprim <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0) return 0;
-    return tile_parts(nprim, (img_w + block_x - 1) / block_x, (img_h + block_y - 1) / block_y);
-}
-
 // Depth ranks, then the tile-list counts: order[r] = primitive with the r-th
 // smallest key (ties by primitive id) and rank_rects[r] its tile rectangle;
-// per-(part, tile) counts and their prefix over parts, per-segment totals,
-// then the segments' first slots; status[0] receives the intersection total.
-static int rank_and_count(uint32_t* keys, int32_t* order, const int4* prim_rects,
+// per-tile counts, per-segment totals, then the segments' first slots;
+// status[0] receives the intersection total.
+static int rank_and_count(bool blocks_ranked, uint32_t* keys, int32_t* order,
+                          const int4* prim_rects,
                           int4* rank_rects, int nprim, int tbx, int tby, uint32_t* keys_alt,
                           int32_t* vals_alt, uint32_t* radix_counts, uint32_t* scan_temp,
-                          uint32_t* tile_part_base, uint32_t* tile_count,
+                          uint32_t* tile_count,
                           uint32_t* tile_scratch, int32_t* status, hipStream_t stream) {
-    if (nprim <= kRankSortMax) {
-        hipLaunchKernelGGL(k_rank_order, dim3((nprim + 3) / 4), dim3(256), 0, stream, keys,
-                           nprim, prim_rects, order, rank_rects);
+    if (nprim <= kRankPairsMax) {
+        hipLaunchKernelGGL(k_rank_allpairs<false>, dim3((nprim + 3) / 4), dim3(256), 0, stream,
+                           keys, nprim, (const int32_t*)nullptr, (uint32_t*)nullptr,
+                           (int32_t*)nullptr, prim_rects, order, rank_rects);
+    } else if (nprim <= kRankSortMax) {
+        // Block ranks into keys_alt / vals_alt (already there when
+        // blocks_ranked: k_prim_prep wrote them).
+        if (!blocks_ranked)
+            hipLaunchKernelGGL(k_rank_blocks, dim3(blocks_for(nprim, kRankBlock)),
+                               dim3(kRankBlock), 0, stream, keys, nprim, keys_alt, vals_alt);
+        hipLaunchKernelGGL(k_rank_merge<false>, dim3(blocks_for(nprim, kMergeKeys)),
+                           dim3(kMergeThreads), 0, stream, keys,
+                           keys_alt, vals_alt, nprim, (const int32_t*)nullptr,
+                           (uint32_t*)nullptr, (int32_t*)nullptr, prim_rects, order, rank_rects);
     } else {
         const int rc = cs_radix_sort_pairs_u32(keys, order, keys_alt, vals_alt, nprim, 32,
                                                radix_counts, scan_temp, stream);
@@ -1452,14 +1727,9 @@ static int rank_and_count(uint32_t* keys, int32_t* order, const int4* prim_rects
         hipLaunchKernelGGL(k_gather_rects, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
                            order, nprim, prim_rects, rank_rects);
     }
-    const int K = tile_parts(nprim, tbx, tby);
     const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
-    const int ranks_per_part = (nprim + K - 1) / K;
-    hipLaunchKernelGGL(k_tile_lists<false>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
-                       order, rank_rects, nprim, ranks_per_part, tbx, tby, nsegcols,
-                       tile_part_base, tile_count, tile_scratch, (int32_t*)nullptr,
-                       (int32_t*)nullptr, (float*)nullptr, (int64_t)0, (const int32_t*)nullptr,
-                       (int64_t)0);
+    hipLaunchKernelGGL(k_tile_counts, dim3(nsegcols * tby), dim3(kWave * kListWaves), 0,
+                       stream, rank_rects, nprim, tbx, nsegcols, tile_count, tile_scratch);
     return cs_scan_exclusive_u32(tile_scratch, tile_scratch, nsegcols * tby, scan_temp, status,
                                  stream);
 }
@@ -1481,7 +1751,7 @@ static int bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, con
                        uint32_t* num_tiles_hit, float* inv_sigma2s, void* prim_recs,
                        uint32_t* keys, int32_t* order, uint32_t* keys_alt, int32_t* vals_alt,
                        uint32_t* radix_counts, uint32_t* scan_temp, int32_t* rank_tile_ranges,
-                       uint32_t* tile_part_base, uint32_t* tile_count, uint32_t* tile_scratch,
+                       uint32_t* tile_count, uint32_t* tile_scratch,
                        int32_t* status, int32_t* seg_edge_offsets, void* edge_aux,
                        uint32_t* leaf_counts, hipStream_t stream) {
     if (nseg < 0 || nprim <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0 ||
@@ -1502,10 +1772,9 @@ static int bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, con
     if (!adaptive && nseg > 0 && samples <= kWave) {
         // One lane per sample point; the kernel also sets the status words.
         const int lanes = samples <= 2 ? 2 : 1 << ceil_log2(samples);
-        const size_t threads = (size_t)nseg * lanes;
-        const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+        const dim3 grid((unsigned)blocks_for(nseg, kWave)), block(kWave * kFlattenWaves);
 #define CS_FLATTEN_LANES(Lv)                                                                   \
-    hipLaunchKernelGGL(k_project_flatten_lanes<Lv>, grid, block, 0, stream, cubics_norm,      \
+    hipLaunchKernelGGL(k_project_flatten_wave<Lv>, grid, block, 0, stream, cubics_norm,       \
                        seg_offsets, nprim, aa_widths, stroke_widths, opacities, mode, nseg,    \
                        img_h, img_w, block_x, block_y, aabb_pad, aniso, samples, cubics_px,    \
                        seg_tile_ranges, reinterpret_cast<SegRec*>(seg_recs),                   \
@@ -1551,10 +1820,12 @@ static int bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, con
                        fill_rules, aa_widths, stroke_widths, nseg, eps,
                        adaptive ? seg_edge_offsets : nullptr, tbx, tby, mode, status,
                        prim_tile_ranges, num_tiles_hit, inv_sigma2s, keys, order,
-                       reinterpret_cast<PrimRec*>(prim_recs));
-    return rank_and_count(keys, order, reinterpret_cast<const int4*>(prim_tile_ranges),
+                       reinterpret_cast<PrimRec*>(prim_recs),
+                       nprim > kRankPairsMax && nprim <= kRankSortMax ? keys_alt : nullptr,
+                       nprim > kRankPairsMax && nprim <= kRankSortMax ? vals_alt : nullptr);
+    return rank_and_count(true, keys, order, reinterpret_cast<const int4*>(prim_tile_ranges),
                           reinterpret_cast<int4*>(rank_tile_ranges), nprim, tbx, tby, keys_alt,
-                          vals_alt, radix_counts, scan_temp, tile_part_base, tile_count,
+                          vals_alt, radix_counts, scan_temp, tile_count,
                           tile_scratch, status, stream);
 }
 
@@ -1570,15 +1841,14 @@ extern "C" int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offse
                               float* inv_sigma2s, void* prim_recs, uint32_t* keys,
                               int32_t* order, uint32_t* keys_alt, int32_t* vals_alt,
                               uint32_t* radix_counts, uint32_t* scan_temp,
-                              int32_t* rank_tile_ranges, uint32_t* tile_part_base,
-                              uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
+                              int32_t* rank_tile_ranges, uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
                               hipStream_t stream) {
     return bin_prepare(cubics_norm, seg_offsets, colors, opacities, depths, fill_rules,
                        aa_widths, stroke_widths, nseg, nprim, img_h, img_w, block_x, block_y,
                        samples, aabb_pad, aniso, mode, cubics_px, seg_tile_ranges, seg_recs,
                        edges, edge_culls, prim_tile_ranges, num_tiles_hit, inv_sigma2s,
                        prim_recs, keys, order, keys_alt, vals_alt, radix_counts, scan_temp,
-                       rank_tile_ranges, tile_part_base, tile_count, tile_scratch, status,
+                       rank_tile_ranges, tile_count, tile_scratch, status,
                        nullptr, nullptr, nullptr, stream);
 }
 
@@ -1597,8 +1867,7 @@ extern "C" int cs_bin_prepare_de_casteljau(
     void* seg_recs, void* edges, void* edge_culls, int32_t* prim_tile_ranges,
     uint32_t* num_tiles_hit, float* inv_sigma2s, void* prim_recs, uint32_t* keys,
     int32_t* order, uint32_t* keys_alt, int32_t* vals_alt, uint32_t* radix_counts,
-    uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_part_base,
-    uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status, int32_t* seg_edge_offsets,
+    uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status, int32_t* seg_edge_offsets,
     void* edge_aux, uint32_t* leaf_counts, hipStream_t stream) {
     if (!seg_edge_offsets) return CS_ERR_ARGS;
     return bin_prepare(cubics_norm, seg_offsets, colors, opacities, depths, fill_rules,
@@ -1606,7 +1875,7 @@ extern "C" int cs_bin_prepare_de_casteljau(
                        samples, aabb_pad, aniso, mode, cubics_px, seg_tile_ranges, seg_recs,
                        edges, edge_culls, prim_tile_ranges, num_tiles_hit, inv_sigma2s,
                        prim_recs, keys, order, keys_alt, vals_alt, radix_counts, scan_temp,
-                       rank_tile_ranges, tile_part_base, tile_count, tile_scratch, status,
+                       rank_tile_ranges, tile_count, tile_scratch, status,
                        seg_edge_offsets, edge_aux, leaf_counts, stream);
 }
 
@@ -1699,8 +1968,7 @@ extern "C" int cs_gs_bin_prepare(const float* xys, const float* conics, const in
                                  int32_t block_x, int32_t block_y, int32_t* tile_rects,
                                  uint32_t* keys, int32_t* order, uint32_t* keys_alt,
                                  int32_t* vals_alt, uint32_t* radix_counts, uint32_t* scan_temp,
-                                 int32_t* rank_tile_ranges, uint32_t* tile_part_base,
-                                 uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
+                                 int32_t* rank_tile_ranges, uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
                                  hipStream_t stream) {
     if (n <= 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0 ||
         (reinterpret_cast<uintptr_t>(tile_rects) & 15) != 0 ||
@@ -1710,16 +1978,16 @@ extern "C" int cs_gs_bin_prepare(const float* xys, const float* conics, const in
     hipLaunchKernelGGL(k_gs_keys_rects, dim3(blocks_for(n, 256)), dim3(256), 0, stream, xys,
                        conics, radii, depths, n, block_x, block_y, tbx, tby,
                        reinterpret_cast<int4*>(tile_rects), keys, order, status);
-    return rank_and_count(keys, order, reinterpret_cast<const int4*>(tile_rects),
+    return rank_and_count(false, keys, order, reinterpret_cast<const int4*>(tile_rects),
                           reinterpret_cast<int4*>(rank_tile_ranges), n, tbx, tby, keys_alt,
-                          vals_alt, radix_counts, scan_temp, tile_part_base, tile_count,
+                          vals_alt, radix_counts, scan_temp, tile_count,
                           tile_scratch, status, stream);
 }
 
 extern "C" int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges,
                              int32_t nprim, const int32_t* status, int64_t capacity,
                              int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
-                             uint32_t* tile_part_base, uint32_t* tile_count,
+                             uint32_t* tile_count,
                              uint32_t* tile_scratch, int32_t* prim_ids_sorted,
                              int32_t* tile_bins, float* zero_buf, int64_t zero_n,
                              hipStream_t stream) {
@@ -1727,13 +1995,10 @@ extern "C" int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_rang
         block_y <= 0 || zero_n < 0 || (zero_n > 0 && !zero_buf))
         return CS_ERR_ARGS;
     const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
-    const int K = tile_parts(nprim, tbx, tby);
     const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
-    const int ranks_per_part = (nprim + K - 1) / K;
-    hipLaunchKernelGGL(k_tile_lists<true>, dim3(nsegcols * tby), dim3(kWave * K), 0, stream,
-                       order, reinterpret_cast<const int4*>(rank_tile_ranges), nprim,
-                       ranks_per_part, tbx, tby, nsegcols, tile_part_base, tile_count,
-                       tile_scratch, prim_ids_sorted, tile_bins,
+    hipLaunchKernelGGL(k_tile_scatter, dim3(nsegcols * tby), dim3(kWave * kListWaves), 0,
+                       stream, order, reinterpret_cast<const int4*>(rank_tile_ranges), nprim, tbx,
+                       nsegcols, tile_count, tile_scratch, prim_ids_sorted, tile_bins,
                        zero_n > 0 ? zero_buf : nullptr, zero_n, status, capacity);
     return launch_status();
 }

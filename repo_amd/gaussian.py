@@ -90,7 +90,7 @@ def project_backward(scales2d, rotation, radii, conics, v_xy, v_conic, img_h: in
 # -------------------------------------------------------------------- binning
 
 
-def _gs_fields(n, T, K, radix_elems, scan_elems):
+def _gs_fields(n, T, radix_elems, scan_elems):
     f32, i32 = torch.float32, torch.int32
     return (
         ("tile_rects", i32, (n, 4)),
@@ -101,7 +101,6 @@ def _gs_fields(n, T, K, radix_elems, scan_elems):
         ("radix_counts", i32, (radix_elems,)),
         ("scan_temp", i32, (scan_elems,)),
         ("rank_tile_ranges", i32, (n, 4)),
-        ("tile_part_base", i32, (K * T,)),
         ("tile_count", i32, (T,)),
         ("tile_scratch", i32, (T,)),
         ("status", i32, (4,)),
@@ -161,8 +160,7 @@ def bin_gaussians(xys, conics, radii, depths, img_h: int, img_w: int, block_x: i
     tbx, tby, _ = tile_bounds(img_h, img_w, block_x, block_y)
     T = tbx * tby
     key = ("gs", dev.index, n, img_h, img_w, block_x, block_y)
-    K = int(lib.cs_bin_tile_parts(n, img_h, img_w, block_x, block_y))
-    table, nbytes = _layout(key, _gs_fields(n, T, K, int(lib.cs_radix_counts_elems(n)),
+    table, nbytes = _layout(key, _gs_fields(n, T, int(lib.cs_radix_counts_elems(n)),
                                             int(lib.cs_scan_temp_elems(max(n, T)))))
     arena = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
     b = GsBinned(n, img_h, img_w, block_x, block_y, arena, table)
@@ -172,8 +170,7 @@ def bin_gaussians(xys, conics, radii, depths, img_h: int, img_w: int, block_x: i
         N.call("cs_gs_bin_prepare", N.ptr(xy), N.ptr(q), N.ptr(rad), N.ptr(d), n, int(img_h),
                int(img_w), int(block_x), int(block_y), q_("tile_rects"), q_("keys"), q_("order"),
                q_("keys_alt"), q_("vals_alt"), q_("radix_counts"), q_("scan_temp"),
-               q_("rank_tile_ranges"), q_("tile_part_base"), q_("tile_count"),
-               q_("tile_scratch"), q_("status"), st)
+               q_("rank_tile_ranges"), q_("tile_count"), q_("tile_scratch"), q_("status"), st)
     pinned = _take_pinned(dev.index if dev.index is not None else torch.cuda.current_device())
     status_host, event = pinned[0], pinned[1]
     hip = N.hip()
@@ -190,8 +187,8 @@ def bin_gaussians(xys, conics, radii, depths, img_h: int, img_w: int, block_x: i
     ids = torch.empty((I,), dtype=torch.int32, device=dev)
     with N.prof("gs.fwd.bin_finish"):
         N.call("cs_bin_finish", q_("order"), q_("rank_tile_ranges"), n, q_("status"), I,
-               int(img_h), int(img_w), int(block_x), int(block_y), q_("tile_part_base"),
-               q_("tile_count"), q_("tile_scratch"), N.ptr(ids), q_("tile_bins"),
+               int(img_h), int(img_w), int(block_x), int(block_y), q_("tile_count"),
+               q_("tile_scratch"), N.ptr(ids), q_("tile_bins"),
                q_("grad_accum"), 9 * n, st)
     b.gaussian_ids_sorted = ids
     b.num_intersects = I

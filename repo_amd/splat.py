@@ -81,8 +81,8 @@ def tile_bounds(img_h: int, img_w: int, block_x: int = BLOCK_X, block_y: int = B
 
 
 # Buffers of one binning, carved from one arena allocation: name -> (dtype,
-# shape).  Shapes depend on (nseg, P, S, T, K, scratch sizes).
-def _binning_fields(nseg, P, E, T, K, radix_elems, scan_elems, grad_elems, adaptive=False):
+# shape).  Shapes depend on (nseg, P, S, T, scratch sizes).
+def _binning_fields(nseg, P, E, T, radix_elems, scan_elems, grad_elems, adaptive=False):
     f32, i32 = torch.float32, torch.int32
     extra = ((("seg_edge_offsets", i32, (nseg + 1,)), ("edge_aux", i32, (E, N.EDGE_AUX_INTS)),
               ("leaf_counts", i32, (nseg,))) if adaptive else ())
@@ -103,7 +103,6 @@ def _binning_fields(nseg, P, E, T, K, radix_elems, scan_elems, grad_elems, adapt
         ("radix_counts", i32, (radix_elems,)),
         ("scan_temp", i32, (scan_elems,)),
         ("rank_tile_ranges", i32, (P, 4)),
-        ("tile_part_base", i32, (K * T,)),
         ("tile_count", i32, (T,)),
         ("tile_scratch", i32, (T,)),
         ("status", i32, (4,)),
@@ -246,7 +245,7 @@ def _give_pinned(entry) -> None:
 _PREP_FIELDS = ("cubics_px", "seg_tile_ranges", "seg_recs", "edges", "edge_culls",
                 "prim_tile_ranges", "num_tiles_hit", "inv_sigma2s", "prim_recs", "keys", "order",
                 "keys_alt", "vals_alt", "radix_counts", "scan_temp", "rank_tile_ranges",
-                "tile_part_base", "tile_count", "tile_scratch", "status")
+                "tile_count", "tile_scratch", "status")
 _DECAS_FIELDS = ("seg_edge_offsets", "edge_aux", "leaf_counts")
 
 
@@ -270,8 +269,7 @@ def _bin_plan(key, lib, nseg, P, S, img_h, img_w, block_x, block_y, mode, adapti
     if plan is None:
         tbx, tby, _ = tile_bounds(img_h, img_w, block_x, block_y)
         T = tbx * tby
-        K = int(lib.cs_bin_tile_parts(P, img_h, img_w, block_x, block_y))
-        fields = _binning_fields(nseg, P, nseg * per_seg, T, K,
+        fields = _binning_fields(nseg, P, nseg * per_seg, T,
                                  int(lib.cs_radix_counts_elems(P)),
                                  int(lib.cs_scan_temp_elems(max(P, T, nseg))),
                                  _grad_accum_elems(nseg, P, mode), adaptive)
@@ -328,14 +326,14 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
             N.call("cs_bin_prepare", *args, st)
     q = b.ptr
     order_p, ranks_p, status_p = q("order"), q("rank_tile_ranges"), q("status")
-    parts_p, count_p, scratch_p = q("tile_part_base"), q("tile_count"), q("tile_scratch")
+    count_p, scratch_p = q("tile_count"), q("tile_scratch")
     bins_p, grad_p, grad_n = q("tile_bins"), q("grad_accum"), plan.grad_n
 
     def finish(capacity: int) -> torch.Tensor:
         ids = torch.empty((capacity,), dtype=torch.int32, device=dev)
         with N.prof("cubic.fwd.bin_finish"):
             N.call("cs_bin_finish", order_p, ranks_p, P, status_p, capacity, img_h, img_w,
-                   block_x, block_y, parts_p, count_p, scratch_p, ids.data_ptr(), bins_p,
+                   block_x, block_y, count_p, scratch_p, ids.data_ptr(), bins_p,
                    grad_p, grad_n, st)
         return ids
 
