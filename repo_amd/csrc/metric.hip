@@ -250,7 +250,9 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
                                                  float* __restrict__ mse_partials) {
     using TT = SsimTile<WIN>;
     constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
-    __shared__ float hm[5][IT][HP];
+    // Four filtered moments: x, y, x^2 + y^2 and xy (SSIM needs the two
+    // variances only as their sum, so E[x^2] and E[y^2] are filtered as one).
+    __shared__ float hm[4][IT][HP];
     __shared__ float sh[4];
     // 1D grid over (channel, tile row, tile column), XCD-aware.
     const int ntx = (ow + kSsimTW - 1) / kSsimTW, nty = (oh + kSsimTH - 1) / kSsimTH;
@@ -290,52 +292,49 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
                 mse = k < cols ? __builtin_fmaf(d, d, mse) : mse;
             }
         }
-        float aa[NIN], bb[NIN], ab[NIN];
+        float ss[NIN], ab[NIN];
 #pragma unroll
         for (int k = 0; k < NIN; ++k) {
             a[k] -= kx;
             b[k] -= ky;
-            aa[k] = a[k] * a[k];
-            bb[k] = b[k] * b[k];
+            ss[k] = __builtin_fmaf(b[k], b[k], a[k] * a[k]);
             ab[k] = a[k] * b[k];
         }
 #pragma unroll
         for (int o = 0; o < kHStrip; ++o) {
-            float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f, m4 = 0.f;
+            float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
 #pragma unroll
             for (int k = 0; k < WIN; ++k) {
                 m0 = __builtin_fmaf(g[k], a[o + k], m0);
                 m1 = __builtin_fmaf(g[k], b[o + k], m1);
-                m2 = __builtin_fmaf(g[k], aa[o + k], m2);
-                m3 = __builtin_fmaf(g[k], bb[o + k], m3);
-                m4 = __builtin_fmaf(g[k], ab[o + k], m4);
+                m2 = __builtin_fmaf(g[k], ss[o + k], m2);
+                m3 = __builtin_fmaf(g[k], ab[o + k], m3);
             }
             hm[0][r][q0 + o] = m0;
             hm[1][r][q0 + o] = m1;
             hm[2][r][q0 + o] = m2;
             hm[3][r][q0 + o] = m3;
-            hm[4][r][q0 + o] = m4;
         }
     }
     __syncthreads();
     // Vertical: thread -> (column, 6-tall strip).
     const int q = threadIdx.x & (kSsimTW - 1), r0 = (threadIdx.x / kSsimTW) * kVStrip;
-    float mom[5][kVStrip];
+    float mom[4][kVStrip];
 #pragma unroll
-    for (int m = 0; m < 5; ++m)
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
         for (int o = 0; o < kVStrip; ++o) mom[m][o] = 0.0f;
 #pragma unroll
     for (int k = 0; k < kVStrip + WIN - 1; ++k) {
-        float v[5];
+        float v[4];
 #pragma unroll
-        for (int m = 0; m < 5; ++m) v[m] = hm[m][r0 + k][q];
+        for (int m = 0; m < 4; ++m) v[m] = hm[m][r0 + k][q];
 #pragma unroll
         for (int o = 0; o < kVStrip; ++o) {
             const int t = k - o;
             if (t >= 0 && t < WIN) {
 #pragma unroll
-                for (int m = 0; m < 5; ++m) mom[m][o] = __builtin_fmaf(g[t], v[m], mom[m][o]);
+                for (int m = 0; m < 4; ++m) mom[m][o] = __builtin_fmaf(g[t], v[m], mom[m][o]);
             }
         }
     }
@@ -349,12 +348,13 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
         const int oy = oy0 + r0 + o;
         if (oy >= oh || ox >= ow) continue;
         const float m1 = mom[0][o], m2 = mom[1][o];  // shifted means
-        const float s1 = mom[2][o] - m1 * m1, s2 = mom[3][o] - m2 * m2;
-        const float s12 = mom[4][o] - m1 * m2;
+        // sigma_x^2 + sigma_y^2 from the one filtered E[x^2 + y^2].
+        const float s1s2 = mom[2][o] - __builtin_fmaf(m2, m2, m1 * m1);
+        const float s12 = mom[3][o] - m1 * m2;
         const float mu1 = m1 + kx, mu2 = m2 + ky;
         const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2, mu12 = mu1 * mu2;
         const float n1 = 2.0f * mu12 + c1, d1 = mu1_sq + mu2_sq + c1;
-        const float n2 = 2.0f * s12 + c2, d2 = s1 + s2 + c2;
+        const float n2 = 2.0f * s12 + c2, d2 = s1s2 + c2;
         // The hardware reciprocal (within 1 ulp): d1 >= c1 and d2 >= c2 up to
         // rounding, so both are positive normals; the loss and its gradient
         // are compared to float64 at 1e-5 / 1e-4, far above this rounding.
