@@ -170,31 +170,44 @@ __device__ __forceinline__ void row_cross_term(const EdgeRec& E, float py, Geom&
     G.winding += (b0 != b1) ? (b0 ? 1 : -1) : 0;
 }
 
-// One 64-edge chunk starting at edge c: lane tests, ballots and the edge walks
-// for the lane's pixels (one column px, rows py[p]).  Each edge record is
-// loaded once through the scalar cache and evaluated for every pixel.  Edge
-// classes (all exact):
-//   near (distance can matter)           distance term, and the crossing
-//                                        term when the edge spans a row;
-//   far, spans a row, flagged, right     row-span crossing term only;
-//   far, spans a row, flagged, left      nothing (its crossing term is 0);
-//   far, spans a row, not flagged        exact crossing term.
-template <int MODE, int BEST, bool COUNT, bool CROSS>
-__device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const WaveRect& W,
-                                               cptr<EdgeRec> edges, float px,
-                                               const float (&py)[kPix], Geom (&G)[kPix],
-                                               EvalCounts& n, int npix) {
+// Edge classes of one 64-edge chunk starting at edge c (lane k: edge c + k,
+// cull words q), as ballots.  All exact:
+//   dist   near (distance can matter): distance term, and the crossing term
+//          when the edge spans a row;
+//   cross  exact crossing terms: spans a row and is near or not flagged;
+//   right  far, spans a row, flagged, right of the wave: row-span crossing
+//          term only (far, flagged, left: nothing -- its crossing term is 0).
+struct ChunkMasks {
+    uint64_t dist, cross, right;
+};
+
+template <bool CROSS>
+__device__ __forceinline__ ChunkMasks chunk_masks(int4 q, int c, int e1, const WaveRect& W) {
     const bool in = c + (int)(threadIdx.x & (kWave - 1)) < e1;
     const bool dn = in && span_hits(packed_lo(q.x), packed_span(q.x), W.r1) &&
                     span_hits(packed_lo(q.z), packed_span(q.z), W.c1);
-    const bool cb = CROSS && in && span_hits(packed_lo(q.y), packed_span(q.y), W.r1);
-    const bool far_exact = cb && !dn && (q.w & kCullFarCrossExact);
-    const uint64_t mdn = __ballot(dn);
-    const uint64_t mcb = CROSS ? (uint64_t)__ballot(cb) : 0ull;
-    const uint64_t mfar = CROSS ? (uint64_t)__ballot(far_exact) : 0ull;
-    const uint64_t mright =
-        CROSS ? (uint64_t)__ballot(far_exact && packed_lo(q.z) > W.c1) : 0ull;
-    const uint64_t mcross = mcb & ~mfar;  // exact crossing terms
+    ChunkMasks m;
+    m.dist = __ballot(dn);
+    m.cross = 0ull;
+    m.right = 0ull;
+    if constexpr (CROSS) {
+        const bool cb = in && span_hits(packed_lo(q.y), packed_span(q.y), W.r1);
+        const bool flagged = (q.w & kCullFarCrossExact) != 0;
+        m.cross = __ballot(cb && (dn || !flagged));
+        m.right = __ballot(cb && !dn && flagged && packed_lo(q.z) > W.c1);
+    }
+    return m;
+}
+
+// The edge walks of one chunk for the lane's pixels (one column px, rows
+// py[p]).  Each edge record is loaded once through the scalar cache and
+// evaluated for every pixel.
+template <int MODE, int BEST, bool COUNT, bool CROSS>
+__device__ __forceinline__ void chunk_geometry(const ChunkMasks& cm, int c,
+                                               cptr<EdgeRec> edges, float px,
+                                               const float (&py)[kPix], Geom (&G)[kPix],
+                                               EvalCounts& n, int npix) {
+    const uint64_t mdn = cm.dist, mcross = cm.cross, mright = cm.right;
     if constexpr (COUNT) {
         n.dist += (uint64_t)__builtin_popcountll(mdn) * npix;
         n.cross += (uint64_t)__builtin_popcountll(mcross) * npix;
@@ -253,15 +266,16 @@ __device__ __forceinline__ void chunk_geometry(int4 q, int c, int e1, const Wave
 
 // All edges of a primitive with per-edge culling decided lane-parallel: lane
 // k holds the packed ranges of edge k of a 64-edge chunk (one vector load),
-// tests them against the wave, and two ballots give the edges whose distance
+// tests them against the wave, and ballots give the edges whose distance
 // and crossing terms can matter.  The wave then visits only those edges, in
 // ascending index order (so the best edge is the first strict minimum, as in
 // the reference), loading each one's geometry through the scalar cache.
+// `first` holds the first chunk's masks (computed by the caller).
 template <int MODE, int BEST, bool COUNT, bool CROSS>
 __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect& W,
                                               const EdgeCull* __restrict__ culls,
                                               cptr<EdgeRec> edges, float px,
-                                              const float (&py)[kPix], int4 first,
+                                              const float (&py)[kPix], const ChunkMasks& first,
                                               Geom (&G)[kPix], EvalCounts& n, int npix) {
 #pragma unroll
     for (int p = 0; p < kPix; ++p) {
@@ -272,12 +286,11 @@ __device__ __forceinline__ void prim_geometry(const PrimRec& pr, const WaveRect&
         G[p].bdx = 0.0f;
         G[p].bdy = 0.0f;
     }
-    // The first chunk's words were loaded ahead by the caller.
     const int c0 = pr.e0, e1 = pr.e1;
-    chunk_geometry<MODE, BEST, COUNT, CROSS>(first, c0, e1, W, edges, px, py, G, n, npix);
+    chunk_geometry<MODE, BEST, COUNT, CROSS>(first, c0, edges, px, py, G, n, npix);
     for (int c = c0 + kWave; c < e1; c += kWave)
-        chunk_geometry<MODE, BEST, COUNT, CROSS>(load_culls(culls, c, e1), c, e1, W, edges, px,
-                                                 py, G, n, npix);
+        chunk_geometry<MODE, BEST, COUNT, CROSS>(
+            chunk_masks<CROSS>(load_culls(culls, c, e1), c, e1, W), c, edges, px, py, G, n, npix);
 }
 
 struct Cov {
@@ -403,21 +416,17 @@ __device__ __forceinline__ bool prim_culled_lane(const PrimRec* __restrict__ p,
 // Then no pixel needs the exact coverage, and every pixel has the same
 // winding number: the winding number changes only across an edge, none
 // crosses the wave's rectangle, and for such edges the fp32 crossing test at
-// each pixel gives the geometric side (see kCullFarCrossExact).  q holds the
-// cull words of the first 64 edges.
+// each pixel gives the geometric side (see kCullFarCrossExact).  `first`
+// holds the masks of the first 64 edges: the entry is far when no edge has a
+// distance or exact crossing term.
 template <int MODE>
 __device__ __forceinline__ bool entry_far(const PrimRec& pr, const WaveRect& W,
-                                          const EdgeCull* __restrict__ culls, int4 q) {
-    const int lane = threadIdx.x & (kWave - 1);
-    for (int c = pr.e0; c < pr.e1; c += kWave) {
-        if (c != pr.e0) q = load_culls(culls, c, pr.e1);
-        const bool in = c + lane < pr.e1;
-        bool bad = in && span_hits(packed_lo(q.x), packed_span(q.x), W.r1) &&
-                   span_hits(packed_lo(q.z), packed_span(q.z), W.c1);
-        if (MODE == 0)
-            bad |= in && span_hits(packed_lo(q.y), packed_span(q.y), W.r1) &&
-                   !(q.w & kCullFarCrossExact);
-        if (__ballot(bad)) return false;
+                                          const EdgeCull* __restrict__ culls,
+                                          const ChunkMasks& first) {
+    if (first.dist | first.cross) return false;
+    for (int c = pr.e0 + kWave; c < pr.e1; c += kWave) {
+        const ChunkMasks m = chunk_masks<MODE == 0>(load_culls(culls, c, pr.e1), c, pr.e1, W);
+        if (m.dist | m.cross) return false;
     }
     return true;
 }
@@ -621,7 +630,8 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
                 npix = wave_count(live);
                 n.entries += 1;
             }
-            if (entry_far<MODE>(pr, W, culls, q)) {
+            const ChunkMasks cm0 = chunk_masks<MODE == 0>(q, pr.e0, pr.e1, W);
+            if (entry_far<MODE>(pr, W, culls, cm0)) {
                 // Uniform entry: outside (nothing to do) or, for a fill whose
                 // winding at the wave's first pixel says inside, coverage 1
                 // at every pixel.
@@ -656,7 +666,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
                 continue;
             }
             Geom G[kPix];
-            prim_geometry<MODE, 1, COUNT, MODE == 0>(pr, W, culls, edges, L.px, L.py, q, G, n,
+            prim_geometry<MODE, 1, COUNT, MODE == 0>(pr, W, culls, edges, L.px, L.py, cm0, G, n,
                                                      npix);
             bool ex[kPix], ins[kPix];
             float cov[kPix];
@@ -952,8 +962,10 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             const float D2 = pr.cull_d * pr.cull_d, D2o = pr.cull_out * pr.cull_out;
             int npix = 0;
             if constexpr (COUNT) npix = wave_count(valid);
-            prim_geometry<MODE, 2, COUNT, MODE == 0>(pr, W, culls, as_const(edges_g), L.px, L.py,
-                                                     load_culls(culls, pr.e0, pr.e1), G, n, npix);
+            prim_geometry<MODE, 2, COUNT, MODE == 0>(
+                pr, W, culls, as_const(edges_g), L.px, L.py,
+                chunk_masks<MODE == 0>(load_culls(culls, pr.e0, pr.e1), pr.e0, pr.e1, W), G, n,
+                npix);
 #pragma unroll
             for (int p = 0; p < kPix; ++p) {
                 const bool ins = inside_of<MODE>(pr, G[p]);
