@@ -439,22 +439,30 @@ int cs_reduce_sum_f32(const float* x, int64_t n, float* partials, float* out,
 int cs_mse_backward(const float* x, const float* y, int64_t n, const float* grad_loss,
                     float* grad_x, float* grad_y, hipStream_t stream);
 
-/* ssim_map_kernel (ops/metric.py:205-341) + the means of metric.py:267-273,
- * separable window `win1d` [win] (the 2D window is its outer product): *out =
- * mean over the valid SSIM map of every (image, channel), then over them.
- * If abc != null also stores, per map pixel, dS/dmu_x, dS/dE[x^2], dS/dE[xy]
- * (cs_ssim_abc_elems floats: [3, nc, oh, ow] with rows padded to a multiple of
- * 4 floats) for cs_ssim_backward.  x, y: [nc, h, w]. */
-int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
-            const float* win1d, int32_t win, float c1, float c2, float* partials, float* out,
-            float* abc, hipStream_t stream);
+/* Floats of the scratch buffer cs_ssim and cs_ssim_backward need for a
+ * window wider than 15 (0 otherwise: pass NULL). */
+size_t cs_ssim_scratch_elems(int32_t nc, int32_t h, int32_t w, int32_t win);
 
-/* Gradient of the SSIM mean w.r.t. x (the reference has no SSIM backward):
- * grad_x = g * [W*(A) + 2 x W*(B) + y W*(C)] / (nc*oh*ow), W* the transposed
- * (full) window correlation, g = *grad_out (device scalar). */
+/* ssim_map_kernel (ops/metric.py:205-341) + the means of metric.py:262-273,
+ * separable window `win1d` [win] (any odd win <= h, w; the 2D window is its
+ * outer product), valid window.  per_map = 0: *out = mean over the SSIM map
+ * of every (image, channel), then over them; per_map = 1: out[i] = the mean
+ * of map i (the per-image, per-channel values of size_average=False and
+ * nonnegative_ssim).  If abc != null also stores, per map pixel, dS/dmu_x,
+ * dS/dE[x^2], dS/dE[xy] (cs_ssim_abc_elems floats: [3, nc, oh, ow] with rows
+ * padded to a multiple of 4 floats) for cs_ssim_backward.  x, y: [nc, h, w];
+ * scratch: cs_ssim_scratch_elems floats. */
+int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
+            const float* win1d, int32_t win, float c1, float c2, int32_t per_map,
+            float* partials, float* out, float* abc, float* scratch, hipStream_t stream);
+
+/* Gradient of cs_ssim's output w.r.t. x (the reference has no SSIM backward):
+ * grad_x = g * [W*(A) + 2 x W*(B) + y W*(C)] / count, W* the transposed (full)
+ * window correlation; per_map = 0: g = *grad_out, count = nc*oh*ow; per_map =
+ * 1: g = grad_out[i] for map i, count = oh*ow.  scratch as for cs_ssim. */
 int cs_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                      const float* win1d, int32_t win, const float* abc, const float* grad_out,
-                     float* grad_x, hipStream_t stream);
+                     int32_t per_map, float* grad_x, float* scratch, hipStream_t stream);
 
 /* ---------------- fused training-step operations ---------------- */
 

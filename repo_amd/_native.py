@@ -92,8 +92,11 @@ _SIGNATURES = {
     "cs_reduce_sum_f32": (ctypes.c_int, [_P, _I64, _P, _P, _P]),
     "cs_mse_forward_noalloc": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "cs_mse_backward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
-    "cs_ssim": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _F, _F, _P, _P, _P, _P]),
-    "cs_ssim_backward": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P]),
+    "cs_ssim_scratch_elems": (_SZ, [_I32, _I32, _I32, _I32]),
+    "cs_ssim": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _F, _F, _I32, _P, _P, _P, _P,
+                               _P]),
+    "cs_ssim_backward": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _I32, _P, _P,
+                                        _P]),
     "cs_clamp_hwc_to_nchw": (ctypes.c_int, [_P, _I32, _I32, _F, _F, _P, _P]),
     "cs_clamp_hwc_to_nchw_backward": (ctypes.c_int, [_P, _P, _I32, _I32, _F, _F, _P, _P]),
     "cs_mse_ssim_partials_elems": (_SZ, [_I32, _I32, _I32]),

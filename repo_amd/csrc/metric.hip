@@ -161,6 +161,7 @@ __global__ __launch_bounds__(kMseThreads) void k_sum_partial(const float* __rest
 // global memory (through the vector cache, float4 where the strip is inside
 // the image); only the horizontal results live in LDS.  The vertical pass
 // gives each thread a column and a 6-tall row strip (32 x 8 items).
+constexpr int kSsimTiledMaxWin = 15;  // widest window of the tiled kernels
 constexpr int kSsimTW = 32;   // output tile width
 constexpr int kSsimTH = 48;   // output tile height
 constexpr int kHStrip = 8;    // horizontal-pass outputs per thread
@@ -235,6 +236,40 @@ __device__ __forceinline__ void ssim_tile(int b, int ntx, int nty, int nc, int& 
 
 // Row stride of the per-pixel maps A, B, C (rows padded to 16 bytes).
 __host__ __device__ __forceinline__ int abc_ld(int ow) { return (ow + 3) & ~3; }
+
+// SSIM at one map pixel from its four filtered moments about (kx, ky) (means
+// m1, m2 of x - kx and y - ky, E of the squared sum and of the product), and,
+// when `grad`, the partials A = dS/dmu_x, B = dS/dE[x^2], C = dS/dE[xy].
+struct SsimPixel {
+    float s, a, b, c;
+};
+
+__device__ __forceinline__ SsimPixel ssim_pixel(float m1, float m2, float mss, float mxy, float kx,
+                                                float ky, float c1, float c2, bool grad) {
+    // sigma_x^2 + sigma_y^2 from the one filtered E[x^2 + y^2].
+    const float s1s2 = mss - __builtin_fmaf(m2, m2, m1 * m1);
+    const float s12 = mxy - m1 * m2;
+    const float mu1 = m1 + kx, mu2 = m2 + ky;
+    const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2, mu12 = mu1 * mu2;
+    const float n1 = 2.0f * mu12 + c1, d1 = mu1_sq + mu2_sq + c1;
+    const float n2 = 2.0f * s12 + c2, d2 = s1s2 + c2;
+    // The hardware reciprocal (within 1 ulp): d1 >= c1 and d2 >= c2 up to
+    // rounding, so both are positive normals; the loss and its gradient are
+    // compared to float64 at 1e-5 / 1e-4, far above this rounding.
+    const float r1 = __builtin_amdgcn_rcpf(d1), r2 = __builtin_amdgcn_rcpf(d2);
+    const float l = n1 * r1, cs_ = n2 * r2;
+    SsimPixel o;
+    o.s = l * cs_;
+    o.a = o.b = o.c = 0.0f;
+    if (grad) {
+        const float dl = 2.0f * (mu2 - l * mu1) * r1;
+        const float dcs = 2.0f * (mu1 * cs_ - mu2) * r2;
+        o.a = cs_ * dl + l * dcs;
+        o.b = -l * cs_ * r2;
+        o.c = 2.0f * l * r2;
+    }
+    return o;
+}
 
 // mse_partials (optional): each workgroup also sums (x - y)^2 over its
 // anchor inputs -- rows [oy0, oy0 + 48) and columns [ox0, ox0 + 32), extended
@@ -347,27 +382,14 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
     for (int o = 0; o < kVStrip; ++o) {
         const int oy = oy0 + r0 + o;
         if (oy >= oh || ox >= ow) continue;
-        const float m1 = mom[0][o], m2 = mom[1][o];  // shifted means
-        // sigma_x^2 + sigma_y^2 from the one filtered E[x^2 + y^2].
-        const float s1s2 = mom[2][o] - __builtin_fmaf(m2, m2, m1 * m1);
-        const float s12 = mom[3][o] - m1 * m2;
-        const float mu1 = m1 + kx, mu2 = m2 + ky;
-        const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2, mu12 = mu1 * mu2;
-        const float n1 = 2.0f * mu12 + c1, d1 = mu1_sq + mu2_sq + c1;
-        const float n2 = 2.0f * s12 + c2, d2 = s1s2 + c2;
-        // The hardware reciprocal (within 1 ulp): d1 >= c1 and d2 >= c2 up to
-        // rounding, so both are positive normals; the loss and its gradient
-        // are compared to float64 at 1e-5 / 1e-4, far above this rounding.
-        const float r1 = __builtin_amdgcn_rcpf(d1), r2 = __builtin_amdgcn_rcpf(d2);
-        const float l = n1 * r1, cs_ = n2 * r2;
-        acc += l * cs_;
+        const SsimPixel sp = ssim_pixel(mom[0][o], mom[1][o], mom[2][o], mom[3][o], kx, ky, c1,
+                                        c2, abc != nullptr);
+        acc += sp.s;
         if (abc) {
-            const float dl = 2.0f * (mu2 - l * mu1) * r1;
-            const float dcs = 2.0f * (mu1 * cs_ - mu2) * r2;
             const size_t oi = (size_t)c * plane + (size_t)oy * ld + ox;
-            abc[oi] = cs_ * dl + l * dcs;
-            abc[stride + oi] = -l * cs_ * r2;
-            abc[2 * stride + oi] = 2.0f * l * r2;
+            abc[oi] = sp.a;
+            abc[stride + oi] = sp.b;
+            abc[2 * stride + oi] = sp.c;
         }
     }
     const float bs = block_sum(acc, sh);
@@ -391,9 +413,9 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
                                                  int oh, int ow,
                                                  const float* __restrict__ win1d,
                                                  const float* __restrict__ abc,
-                                                 const float* __restrict__ grad_out, float ssim_coef,
-                                                 float mse_coef, int nc, float lo, float hi,
-                                                 float* __restrict__ gx) {
+                                                 const float* __restrict__ grad_out, int go_per_map,
+                                                 float ssim_coef, float mse_coef, int nc, float lo,
+                                                 float hi, float* __restrict__ gx) {
     using TT = SsimTile<WIN>;
     constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
     __shared__ float hs[3][IT][HP];
@@ -450,8 +472,9 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
         }
     }
     // grad = g * ssim_coef * (SSIM-mean term) [+ g * mse_coef * (x - y) when
-    // the MSE gradient is fused in].
-    const float go = *grad_out;
+    // the MSE gradient is fused in]; g is the map's own incoming gradient
+    // when go_per_map.
+    const float go = grad_out[go_per_map ? c : 0];
     const float scale = go * ssim_coef, mscale = go * mse_coef;
     const float* yc = y + (size_t)c * h * w;
     const int px = px0 + q;
@@ -467,6 +490,162 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
         if (HWC) gx[3 * pi + c] = ((xr >= lo) & (xr <= hi)) ? gv : 0.0f;
         else gx[(size_t)c * h * w + pi] = gv;
     }
+}
+
+// Windows wider than the tiled kernels take (any odd size up to the image):
+// two passes through a scratch buffer, one thread per output of each pass.
+// Moments are taken about one constant per map (its centre pixel), as the
+// tiled kernel takes them about one per tile.
+constexpr int kSsimGenThreads = 256;
+
+__device__ __forceinline__ void map_shift(const float* __restrict__ xc,
+                                          const float* __restrict__ yc, int h, int w, float& kx,
+                                          float& ky) {
+    const size_t k = (size_t)(h / 2) * w + w / 2;
+    kx = xc[k];
+    ky = yc[k];
+}
+
+// hm[m][c][row][ox] = sum_k g[k] f_m(row, ox + k) for f = x - kx, y - ky,
+// (x - kx)^2 + (y - ky)^2, (x - kx)(y - ky): [4, nc, h, ow].
+__global__ __launch_bounds__(kSsimGenThreads) void k_ssim_gen_h(
+    const float* __restrict__ x, const float* __restrict__ y, int nc, int h, int w, int ow,
+    const float* __restrict__ win1d, int win, float* __restrict__ hm) {
+    const int64_t total = (int64_t)nc * h * ow;
+    const int64_t i = (int64_t)blockIdx.x * kSsimGenThreads + threadIdx.x;
+    if (i >= total) return;
+    const int ox = (int)(i % ow);
+    const int64_t rc = i / ow;
+    const int row = (int)(rc % h), c = (int)(rc / h);
+    const float* xc = x + (size_t)c * h * w;
+    const float* yc = y + (size_t)c * h * w;
+    float kx, ky;
+    map_shift(xc, yc, h, w, kx, ky);
+    const float* xr = xc + (size_t)row * w + ox;
+    const float* yr = yc + (size_t)row * w + ox;
+    float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
+    for (int k = 0; k < win; ++k) {
+        const float g = win1d[k];
+        const float a = xr[k] - kx, b = yr[k] - ky;
+        m0 = __builtin_fmaf(g, a, m0);
+        m1 = __builtin_fmaf(g, b, m1);
+        m2 = __builtin_fmaf(g, __builtin_fmaf(b, b, a * a), m2);
+        m3 = __builtin_fmaf(g, a * b, m3);
+    }
+    hm[i] = m0;
+    hm[total + i] = m1;
+    hm[2 * total + i] = m2;
+    hm[3 * total + i] = m3;
+}
+
+// The vertical pass of hm and the SSIM of each output; workgroup b of map c
+// (blocks_per_map per map) writes partials[c * blocks_per_map + b].
+__global__ __launch_bounds__(kSsimGenThreads) void k_ssim_gen_v(
+    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ hm,
+    int nc, int h, int w, int oh, int ow, const float* __restrict__ win1d, int win, float c1,
+    float c2, int blocks_per_map, float* __restrict__ partials, float* __restrict__ abc) {
+    __shared__ float sh[4];
+    const int c = blockIdx.x / blocks_per_map, b = blockIdx.x - c * blocks_per_map;
+    const int64_t j = (int64_t)b * kSsimGenThreads + threadIdx.x;
+    float acc = 0.0f;
+    if (j < (int64_t)oh * ow) {
+        const int oy = (int)(j / ow), ox = (int)(j - (int64_t)oy * ow);
+        float kx, ky;
+        map_shift(x + (size_t)c * h * w, y + (size_t)c * h * w, h, w, kx, ky);
+        const size_t plane = (size_t)nc * h * ow;
+        const float* col = hm + ((size_t)c * h + oy) * ow + ox;
+        float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
+        for (int k = 0; k < win; ++k) {
+            const float g = win1d[k];
+            const float* q = col + (size_t)k * ow;
+            m0 = __builtin_fmaf(g, q[0], m0);
+            m1 = __builtin_fmaf(g, q[plane], m1);
+            m2 = __builtin_fmaf(g, q[2 * plane], m2);
+            m3 = __builtin_fmaf(g, q[3 * plane], m3);
+        }
+        const SsimPixel sp = ssim_pixel(m0, m1, m2, m3, kx, ky, c1, c2, abc != nullptr);
+        acc = sp.s;
+        if (abc) {
+            const size_t ld = abc_ld(ow);
+            const size_t mplane = (size_t)oh * ld, stride = (size_t)nc * mplane;
+            const size_t oi = (size_t)c * mplane + (size_t)oy * ld + ox;
+            abc[oi] = sp.a;
+            abc[stride + oi] = sp.b;
+            abc[2 * stride + oi] = sp.c;
+        }
+    }
+    const float bs = block_sum(acc, sh);
+    if (threadIdx.x == 0) partials[blockIdx.x] = bs;
+}
+
+// hs[m][c][oy][px] = sum over 0 <= px - k < ow of g[k] M_m[c][oy][px - k]
+// (M = A, B, C): [3, nc, oh, w].
+__global__ __launch_bounds__(kSsimGenThreads) void k_ssim_gen_bh(
+    const float* __restrict__ abc, int nc, int oh, int ow, int w, const float* __restrict__ win1d,
+    int win, float* __restrict__ hs) {
+    const int64_t total = (int64_t)nc * oh * w;
+    const int64_t i = (int64_t)blockIdx.x * kSsimGenThreads + threadIdx.x;
+    if (i >= total) return;
+    const int px = (int)(i % w);
+    const int64_t rc = i / w;
+    const int oy = (int)(rc % oh), c = (int)(rc / oh);
+    const size_t ld = abc_ld(ow);
+    const size_t plane = (size_t)oh * ld, stride = (size_t)nc * plane;
+    const float* row = abc + (size_t)c * plane + (size_t)oy * ld;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+    const int k0 = max(0, px - ow + 1), k1 = min(win - 1, px);
+    for (int k = k0; k <= k1; ++k) {
+        const float g = win1d[k];
+        const float* q = row + (px - k);
+        s0 = __builtin_fmaf(g, q[0], s0);
+        s1 = __builtin_fmaf(g, q[stride], s1);
+        s2 = __builtin_fmaf(g, q[2 * stride], s2);
+    }
+    hs[i] = s0;
+    hs[total + i] = s1;
+    hs[2 * total + i] = s2;
+}
+
+// grad_x[c][py][px] = go * ssim_coef * (SA + 2 x SB + y SC), S_m = sum over
+// 0 <= py - k < oh of g[k] hs[m][c][py - k][px]; go = grad_out[c] when
+// go_per_map, else *grad_out.
+__global__ __launch_bounds__(kSsimGenThreads) void k_ssim_gen_bv(
+    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ hs,
+    int nc, int h, int w, int oh, const float* __restrict__ win1d, int win,
+    const float* __restrict__ grad_out, int go_per_map, float ssim_coef,
+    float* __restrict__ gx) {
+    const int64_t total = (int64_t)nc * h * w;
+    const int64_t i = (int64_t)blockIdx.x * kSsimGenThreads + threadIdx.x;
+    if (i >= total) return;
+    const int px = (int)(i % w);
+    const int64_t rc = i / w;
+    const int py = (int)(rc % h), c = (int)(rc / h);
+    const size_t plane = (size_t)nc * oh * w;
+    const float* col = hs + (size_t)c * oh * w + px;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+    const int k0 = max(0, py - oh + 1), k1 = min(win - 1, py);
+    for (int k = k0; k <= k1; ++k) {
+        const float g = win1d[k];
+        const float* q = col + (size_t)(py - k) * w;
+        s0 = __builtin_fmaf(g, q[0], s0);
+        s1 = __builtin_fmaf(g, q[plane], s1);
+        s2 = __builtin_fmaf(g, q[2 * plane], s2);
+    }
+    const float go = grad_out[go_per_map ? c : 0];
+    gx[i] = go * ssim_coef * (s0 + 2.0f * x[i] * s1 + y[i] * s2);
+}
+
+// out[c] = inv * (sum of partials [c * per_map, (c + 1) * per_map)), one
+// workgroup per map, fixed summation order.
+__global__ __launch_bounds__(256) void k_ssim_map_sums(const float* __restrict__ partials,
+                                                      int per_map, float inv,
+                                                      float* __restrict__ out) {
+    __shared__ float sh[4];
+    const float* p = partials + (size_t)blockIdx.x * per_map;
+    float s = 0.0f;
+    for (int t = threadIdx.x; t < per_map; t += 256) s += p[t];
+    const float bs = block_sum(s, sh);
+    if (threadIdx.x == 0) out[blockIdx.x] = bs * inv;
 }
 
 // loss = mse_sum * inv_n + w * (1 - ssim_sum * inv_m); out[1] = MSE, out[2] =
@@ -625,9 +804,24 @@ extern "C" int cs_mse_backward(const float* x, const float* y, int64_t n, const 
     return metric_status();
 }
 
+// Partials per map: one per output tile (tiled windows) or per 256 outputs
+// (wider windows); h x w outputs bound both for any window.
+static int64_t ssim_partials_per_map(int64_t oh, int64_t ow, int win) {
+    if (win <= kSsimTiledMaxWin)
+        return ((ow + kSsimTW - 1) / kSsimTW) * ((oh + kSsimTH - 1) / kSsimTH);
+    return (oh * ow + kSsimGenThreads - 1) / kSsimGenThreads;
+}
+
 extern "C" size_t cs_ssim_partials_elems(int32_t nc, int32_t h, int32_t w) {
-    const int64_t oh = h, ow = w;  // upper bound for any window
-    return (size_t)(((ow + kSsimTW - 1) / kSsimTW) * ((oh + kSsimTH - 1) / kSsimTH) * nc);
+    if (nc <= 0 || h <= 0 || w <= 0) return 0;
+    return (size_t)nc * (size_t)ssim_partials_per_map(h, w, kSsimTiledMaxWin + 2);
+}
+
+extern "C" size_t cs_ssim_scratch_elems(int32_t nc, int32_t h, int32_t w, int32_t win) {
+    if (nc <= 0 || win <= kSsimTiledMaxWin || h < win || w < win) return 0;
+    const int64_t oh = h - win + 1, ow = w - win + 1;
+    const int64_t fwd = 4 * (int64_t)nc * h * ow, bwd = 3 * (int64_t)nc * oh * w;
+    return (size_t)(fwd > bwd ? fwd : bwd);
 }
 
 extern "C" size_t cs_ssim_abc_elems(int32_t nc, int32_t h, int32_t w, int32_t win) {
@@ -640,7 +834,12 @@ extern "C" size_t cs_ssim_abc_elems(int32_t nc, int32_t h, int32_t w, int32_t wi
     case WIN_: CALL(WIN_); break;
 
 static bool ssim_args_ok(int32_t nc, int32_t h, int32_t w, int32_t win) {
-    return nc > 0 && win > 0 && (win & 1) == 1 && win <= 15 && h >= win && w >= win;
+    return nc > 0 && win > 0 && (win & 1) == 1 && h >= win && w >= win;
+}
+
+// The fused losses take the tiled kernels' windows only.
+static bool ssim_tiled_ok(int32_t nc, int32_t h, int32_t w, int32_t win) {
+    return ssim_args_ok(nc, h, w, win) && win <= kSsimTiledMaxWin;
 }
 
 // SSIM partial sums (one per output tile) and, when abc != null, the maps.
@@ -672,13 +871,15 @@ static int launch_ssim_fwd(const float* x, const float* y, int32_t nc, int32_t h
 template <bool HWC>
 static int launch_ssim_bwd(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                            const float* win1d, int32_t win, const float* abc,
-                           const float* grad_out, float ssim_coef, float mse_coef, float* grad_x,
-                           hipStream_t stream, float lo = 0.0f, float hi = 1.0f) {
+                           const float* grad_out, int go_per_map, float ssim_coef,
+                           float mse_coef, float* grad_x, hipStream_t stream, float lo = 0.0f,
+                           float hi = 1.0f) {
     const int oh = h - win + 1, ow = w - win + 1;
     const dim3 grid(((w + kSsimTW - 1) / kSsimTW) * ((h + kSsimTH - 1) / kSsimTH) * nc);
 #define CS_SSIM_BWD(W_)                                                                        \
     hipLaunchKernelGGL((k_ssim_bwd<W_, HWC>), grid, dim3(256), 0, stream, x, y, h, w, oh, ow, \
-                       win1d, abc, grad_out, ssim_coef, mse_coef, nc, lo, hi, grad_x)
+                       win1d, abc, grad_out, go_per_map, ssim_coef, mse_coef, nc, lo, hi,     \
+                       grad_x)
     switch (win) {
         CS_SSIM_DISPATCH(1, CS_SSIM_BWD)
         CS_SSIM_DISPATCH(3, CS_SSIM_BWD)
@@ -695,28 +896,58 @@ static int launch_ssim_bwd(const float* x, const float* y, int32_t nc, int32_t h
 }
 
 extern "C" int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
-                       const float* win1d, int32_t win, float c1, float c2, float* partials,
-                       float* out, float* abc, hipStream_t stream) {
+                       const float* win1d, int32_t win, float c1, float c2, int32_t per_map,
+                       float* partials, float* out, float* abc, float* scratch,
+                       hipStream_t stream) {
     if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
-    int nblk = 0;
-    const int rc = launch_ssim_fwd(x, y, nc, h, w, win1d, win, c1, c2, partials, abc,
-                                          stream, &nblk);
-    if (rc) return rc;
     const int oh = h - win + 1, ow = w - win + 1;
-    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials, nblk,
-                       1.0f / ((float)nc * (float)oh * (float)ow), out);
+    const int64_t per = ssim_partials_per_map(oh, ow, win);
+    if (win <= kSsimTiledMaxWin) {
+        int nblk = 0;
+        const int rc = launch_ssim_fwd(x, y, nc, h, w, win1d, win, c1, c2, partials, abc, stream,
+                                       &nblk);
+        if (rc) return rc;
+    } else {
+        if (!scratch) return CS_ERR_ARGS;
+        const int64_t nh = (int64_t)nc * h * ow;
+        hipLaunchKernelGGL(k_ssim_gen_h,
+                           dim3((unsigned)((nh + kSsimGenThreads - 1) / kSsimGenThreads)),
+                           dim3(kSsimGenThreads), 0, stream, x, y, nc, h, w, ow, win1d, win,
+                           scratch);
+        hipLaunchKernelGGL(k_ssim_gen_v, dim3((unsigned)(per * nc)), dim3(kSsimGenThreads), 0,
+                           stream, x, y, scratch, nc, h, w, oh, ow, win1d, win, c1, c2, (int)per,
+                           partials, abc);
+    }
+    if (per_map)
+        hipLaunchKernelGGL(k_ssim_map_sums, dim3((unsigned)nc), dim3(256), 0, stream, partials,
+                           (int)per, 1.0f / ((float)oh * (float)ow), out);
+    else
+        hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kFinalThreads), 0, stream, partials,
+                           (int)(per * nc), 1.0f / ((float)nc * (float)oh * (float)ow), out);
     return metric_status();
 }
 
 extern "C" int cs_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                                 const float* win1d, int32_t win, const float* abc,
-                                const float* grad_out, float* grad_x, hipStream_t stream) {
+                                const float* grad_out, int32_t per_map, float* grad_x,
+                                float* scratch, hipStream_t stream) {
     if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
     const int oh = h - win + 1, ow = w - win + 1;
-    const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
-    const int rc = launch_ssim_bwd<false>(x, y, nc, h, w, win1d, win, abc, grad_out, inv_cnt,
-                                          0.0f, grad_x, stream);
-    return rc ? rc : metric_status();
+    const float inv_cnt =
+        per_map ? 1.0f / ((float)oh * (float)ow) : 1.0f / ((float)nc * (float)oh * (float)ow);
+    if (win <= kSsimTiledMaxWin) {
+        const int rc = launch_ssim_bwd<false>(x, y, nc, h, w, win1d, win, abc, grad_out, per_map,
+                                              inv_cnt, 0.0f, grad_x, stream);
+        return rc ? rc : metric_status();
+    }
+    if (!scratch) return CS_ERR_ARGS;
+    const int64_t nh = (int64_t)nc * oh * w, nx = (int64_t)nc * h * w;
+    hipLaunchKernelGGL(k_ssim_gen_bh, dim3((unsigned)((nh + kSsimGenThreads - 1) / kSsimGenThreads)),
+                       dim3(kSsimGenThreads), 0, stream, abc, nc, oh, ow, w, win1d, win, scratch);
+    hipLaunchKernelGGL(k_ssim_gen_bv, dim3((unsigned)((nx + kSsimGenThreads - 1) / kSsimGenThreads)),
+                       dim3(kSsimGenThreads), 0, stream, x, y, scratch, nc, h, w, oh, win1d, win,
+                       grad_out, per_map, inv_cnt, grad_x);
+    return metric_status();
 }
 
 extern "C" size_t cs_mse_ssim_partials_elems(int32_t nc, int32_t h, int32_t w) {
@@ -729,7 +960,7 @@ extern "C" size_t cs_mse_ssim_partials_elems(int32_t nc, int32_t h, int32_t w) {
 static int mse_ssim_loss(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                          const float* win1d, int32_t win, float c1, float c2, float ssim_weight,
                          float* partials, float* out, float* abc, hipStream_t stream) {
-    if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
+    if (!ssim_tiled_ok(nc, h, w, win)) return CS_ERR_ARGS;
     const int64_t n = (int64_t)nc * h * w;
     float* ssim_partials = partials;
     float* mse_partials = partials + cs_ssim_partials_elems(nc, h, w);
@@ -749,11 +980,11 @@ static int mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t
                              float lo, float hi, const float* win1d, int32_t win,
                              const float* abc, float ssim_weight, const float* grad_loss,
                              float* grad_x, hipStream_t stream) {
-    if (!ssim_args_ok(nc, h, w, win)) return CS_ERR_ARGS;
+    if (!ssim_tiled_ok(nc, h, w, win)) return CS_ERR_ARGS;
     const int oh = h - win + 1, ow = w - win + 1;
     const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
     const float mse_coef = (float)(2.0 / ((double)nc * h * w));
-    const int rc = launch_ssim_bwd<HWC>(x, y, nc, h, w, win1d, win, abc, grad_loss,
+    const int rc = launch_ssim_bwd<HWC>(x, y, nc, h, w, win1d, win, abc, grad_loss, 0,
                                         -ssim_weight * inv_cnt, mse_coef, grad_x, stream, lo, hi);
     return rc ? rc : metric_status();
 }
@@ -779,7 +1010,7 @@ extern "C" int cs_clamp_mse_ssim_loss(const float* img, const float* y, int32_t 
                                       float c1, float c2, float ssim_weight, float* x,
                                       float* partials, float* out, float* abc,
                                       hipStream_t stream) {
-    if (!ssim_args_ok(3, h, w, win) || !x) return CS_ERR_ARGS;
+    if (!ssim_tiled_ok(3, h, w, win) || !x) return CS_ERR_ARGS;
     const int64_t hw = (int64_t)h * w;
     hipLaunchKernelGGL(k_clamp_hwc_to_chw, dim3((unsigned)((hw + 255) / 256)), dim3(256), 0,
                        stream, img, hw, lo, hi, x);

@@ -160,35 +160,46 @@ def psnr(x, y, *, data_range=1.0, eps=1e-12, threads=DEFAULT_THREADS,
     return 10.0 * torch.log10((data_range * data_range) / (mse + eps))
 
 
-def _ssim_forward(x32, y32, win_size, win_sigma, c1, c2, want_grad):
+def _ssim_scratch(nc, h, w, win_size, dev):
+    n = int(N.lib().cs_ssim_scratch_elems(nc, h, w, int(win_size)))
+    return torch.empty((n,), dtype=torch.float32, device=dev) if n else None
+
+
+def _ssim_forward(x32, y32, win_size, win_sigma, c1, c2, want_grad, per_map=False):
+    """cs_ssim: the mean SSIM of every (image, channel) map (a device scalar),
+    or with per_map each map's mean [n * c]; abc holds the backward's
+    per-pixel partials when want_grad."""
     n, c, h, w = x32.shape
     dev = x32.device
     g = gaussian_window_1d(win_size, win_sigma, dev)
     partials = torch.empty((int(N.lib().cs_ssim_partials_elems(n * c, h, w)),),
                            dtype=torch.float32, device=dev)
-    out = torch.empty((), dtype=torch.float32, device=dev)
+    out = torch.empty((n * c,) if per_map else (), dtype=torch.float32, device=dev)
     # Per-pixel partials for the backward, [3, n*c, oh, ow rounded up to 4].
     abc = (torch.empty((int(N.lib().cs_ssim_abc_elems(n * c, h, w, int(win_size))),),
                        dtype=torch.float32, device=dev)
            if want_grad else None)
+    scratch = _ssim_scratch(n * c, h, w, win_size, dev)
     with N.prof("loss.ssim_fwd"):
         N.call("cs_ssim", N.ptr(x32), N.ptr(y32), n * c, h, w, N.ptr(g), int(win_size),
-               float(c1), float(c2), N.ptr(partials), N.ptr(out), N.ptr(abc),
-               N.stream(dev))
+               float(c1), float(c2), int(bool(per_map)), N.ptr(partials), N.ptr(out),
+               N.ptr(abc), N.ptr(scratch), N.stream(dev))
     return out, abc, g
 
 
 class _SSIMFn(torch.autograd.Function):
-    """Mean SSIM over all (image, channel) maps with a backward w.r.t. x."""
+    """Mean SSIM over all (image, channel) maps, or (per_map) each map's mean
+    [n * c], with a backward w.r.t. x."""
 
     @staticmethod
-    def forward(ctx, x, y, win_size, win_sigma, c1, c2):
+    def forward(ctx, x, y, win_size, win_sigma, c1, c2, per_map=False):
         x32 = _as_f32(x, "x")
         y32 = _as_f32(y, "y")
         out, abc, g = _ssim_forward(x32, y32, win_size, win_sigma, c1, c2,
-                                    ctx.needs_input_grad[0])
+                                    ctx.needs_input_grad[0], per_map)
         ctx.save_for_backward(x32, y32, abc if abc is not None else torch.empty(0), g)
         ctx.win_size = int(win_size)
+        ctx.per_map = bool(per_map)
         ctx.x_dtype = x.dtype
         return out
 
@@ -196,22 +207,26 @@ class _SSIMFn(torch.autograd.Function):
     def backward(ctx, grad_output):
         x, y, abc, g = ctx.saved_tensors
         if not ctx.needs_input_grad[0]:
-            return None, None, None, None, None, None
+            return None, None, None, None, None, None, None
         n, c, h, w = x.shape
         gx = torch.empty_like(x)
         go = grad_output.detach().to(torch.float32).contiguous()
+        scratch = _ssim_scratch(n * c, h, w, ctx.win_size, x.device)
         with N.prof("loss.ssim_bwd"):
             N.call("cs_ssim_backward", N.ptr(x), N.ptr(y), n * c, h, w, N.ptr(g), ctx.win_size,
-                   N.ptr(abc), N.ptr(go), N.ptr(gx), N.stream(x.device))
-        return gx.to(ctx.x_dtype), None, None, None, None, None
+                   N.ptr(abc), N.ptr(go), int(ctx.per_map), N.ptr(gx), N.ptr(scratch),
+                   N.stream(x.device))
+        return gx.to(ctx.x_dtype), None, None, None, None, None, None
 
 
 def ssim(x, y, *, data_range=1.0, size_average=True, win_size=11, win_sigma=1.5, k1=0.01,
          k2=0.03, nonnegative_ssim=False, block_h=DEFAULT_SSIM_BLOCK_H,
          block_w=DEFAULT_SSIM_BLOCK_W, threads=DEFAULT_SSIM_THREADS):
-    """metric.py:215-273.  With size_average=True (the default) the result is a
-    differentiable device scalar; per-image means (size_average=False) or
-    nonnegative_ssim are computed per map and are forward-only."""
+    """metric.py:215-273, differentiable w.r.t. x in every mode (the
+    reference's SSIM has no backward).  Any odd win_size up to the image
+    size: windows up to 15 run the tiled kernels, wider ones a two-pass
+    kernel through a scratch buffer.  size_average=False and nonnegative_ssim
+    take every (image, channel) mean from one launch."""
     _validate_pair_4d(x, y)
     if data_range <= 0.0:
         raise ValueError("data_range must be > 0")
@@ -222,20 +237,14 @@ def ssim(x, y, *, data_range=1.0, size_average=True, win_size=11, win_sigma=1.5,
     n, c, h, w = x.shape
     if h - win_size + 1 <= 0 or w - win_size + 1 <= 0:
         raise ValueError(f"input spatial size {(h, w)} is smaller than win_size {win_size}")
-    if win_size > 15:
-        raise NotImplementedError("SSIM windows larger than 15 are not implemented on MI355X")
     c1 = (k1 * data_range) ** 2
     c2 = (k2 * data_range) ** 2
     if size_average and not nonnegative_ssim:
         return _SSIMFn.apply(x, y, int(win_size), float(win_sigma), float(c1), float(c2))
-    x32 = _as_f32(x, "x")
-    y32 = _as_f32(y, "y")
-    per = torch.empty((n, c), dtype=torch.float32, device=x.device)
-    for b in range(n):
-        for ch in range(c):
-            v, _, _ = _ssim_forward(x32[b:b + 1, ch:ch + 1], y32[b:b + 1, ch:ch + 1], win_size,
-                                    win_sigma, c1, c2, False)
-            per[b, ch] = v
+    # metric.py:262-273: per (image, channel) means, clamped at 0 when
+    # nonnegative_ssim, then averaged over channels (and images).
+    per = _SSIMFn.apply(x, y, int(win_size), float(win_sigma), float(c1), float(c2),
+                        True).view(n, c)
     if nonnegative_ssim:
         per = torch.relu(per)
     if size_average:
