@@ -195,21 +195,28 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
 
 /* ---------------- rasterization ---------------- */
 
-/* Tile scheduling of the raster entry points (no reference counterpart; it
- * changes no result).  Every raster entry point takes, before its stream,
- *   tile_order [T] (NULL: XCD-contiguous order) -- workgroup b rasterizes tile
- *     tile_order[xcd(b)], xcd(b) the XCD-contiguous index of b; it must be a
- *     permutation of [0, T);
+/* Tiles: every raster entry point takes the tile size block_x x block_y of
+ * the binning whose tile_bins it reads (ops/cubic_splatting.py:2778-2782);
+ * both must be positive multiples of 16 with (block_x / 16) * (block_y / 16)
+ * <= 16.  The raster runs one workgroup of two waves (16 x 8 pixels each) per
+ * 16 x 16 sub-block of the image; the 2 (block_x / 16) (block_y / 16) waves
+ * of a tile all walk its list, and S = ceil(W / 16) * ceil(H / 16) counts the
+ * sub-blocks.
+ * Scheduling (no reference counterpart; it changes no result).  Every raster
+ * entry point takes, before its stream,
+ *   tile_order [S] (NULL: XCD-contiguous order) -- workgroup b rasterizes
+ *     sub-block tile_order[xcd(b)], xcd(b) the XCD-contiguous index of b; it
+ *     must be a permutation of [0, S);
  * and the forward ones also
- *   wave_cost [2T] uint32 out (NULL: not recorded; 8-byte aligned) -- each
+ *   wave_cost [2S] uint32 out (NULL: not recorded; 8-byte aligned) -- each
  *     wave's duration in ticks of the 100 MHz constant clock.
- * T is at most 2^20 (16384 x 16384 pixels) for cs_raster_tile_order.
+ * S is at most 2^20 (16384 x 16384 pixels) for cs_raster_tile_order.
  * cs_raster_tile_order turns the costs of one launch into a heavy-first order
  * for the next ones (the backward of the same forward, the next forward of
- * the scene): long tiles start first, short ones fill the tail.  chunked != 0
- * sorts each XCD's contiguous eighth of the tiles on its own (XCD x keeps its
- * part of the image, and its L2 the records of that part); chunked == 0 sorts
- * all tiles (balance across XCDs for skewed scenes). */
+ * the scene): long sub-blocks start first, short ones fill the tail.
+ * chunked != 0 sorts each XCD's contiguous eighth of the sub-blocks on its own
+ * (XCD x keeps its part of the image, and its L2 the records of that part);
+ * chunked == 0 sorts all of them (balance across XCDs for skewed scenes). */
 int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
                          int32_t* tile_order, hipStream_t stream);
 
@@ -217,15 +224,17 @@ int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chun
  * edge loop and the coverage, ops/cubic_splatting.py:1451-1530,
  * ops/cubic_polyline_splatting.py:465-545).  The forward records, for every
  * list entry g a wave of tile rows processes, what its backward needs:
- *   log_index [2 * num_entries] int32 (num_entries: the size of
- *     prim_ids_sorted, every tile_bins range lies below it), entry 2 g + wave:
+ *   log_index [V * num_entries] int32 (V = 2 (block_x / 16) (block_y / 16),
+ *     the waves of a tile; num_entries: the size of prim_ids_sorted, every
+ *     tile_bins range lies below it), entry V g + wave (the wave's slot in
+ *     its tile, 2 (16 x 16 sub-block in row-major order) + wave of the pair):
  *     the record's position in log_pool in 16-byte units, or -1 when no pixel
  *     of the wave is inside the primitive or near it (the entry contributes
  *     nothing), or -2 when the pool was full (the backward then recomputes
  *     that entry); entries the wave did not process are not written;
  *   log_pool (16-byte aligned, log_pool_bytes): unit 0 holds a uint32
  *     counter; then each wave's own region, log_entry_units units for every
- *     entry of its tile's list (2 * num_entries * log_entry_units units in
+ *     entry of its tile's list (V * num_entries * log_entry_units units in
  *     all, placed by the tile's list range, written without atomics); then
  *     shared blocks of CS_RASTER_LOG_BLOCK_BYTES that a wave whose records
  *     outgrow its region reserves through the counter (which the forward
@@ -235,7 +244,7 @@ int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chun
  *     bits of the live pixels whose coverage needs the exact distance; one
  *     64-bit mask per pixel row of the lanes), then one (best edge int32,
  *     coverage fp32 bits) pair per exact pixel in lane order.
- * Any pool of at least 16 * (1 + 2 * num_entries * log_entry_units) bytes is
+ * Any pool of at least 16 * (1 + V * num_entries * log_entry_units) bytes is
  * correct (a full pool only costs backward time).  log_index NULL: no log
  * (the forward of a render no backward follows); the backward then
  * recomputes every entry. */
@@ -274,12 +283,13 @@ int cs_edge_aux_from_csr(const int32_t* segment_edge_offsets, int32_t nseg,
 
 /* rasterize_cubic_fill_forward_kernel (ops/cubic_splatting.py:918-1194) when
  * mode 0, rasterize_cubic_polyline_forward_kernel
- * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  16x16 tiles only.
+ * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  Tiles as above.
  * The primitive records hold each primitive's edge range, so
  * edges_per_segment is not used (>= 0; 0 for adaptive records). */
 int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
                          const void* edges, const void* edge_culls, const void* prim_recs,
                          const float* background, int32_t img_h, int32_t img_w,
+                         int32_t block_x, int32_t block_y,
                          int32_t edges_per_segment, float* out_img, float* final_Ts,
                          int32_t* final_idx, int64_t num_entries, int32_t* log_index,
                          void* log_pool, int64_t log_pool_bytes, int32_t log_entry_units,
@@ -294,6 +304,7 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
 int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
                           const void* edges, const void* edge_culls, const void* prim_recs,
                           const float* background, int32_t img_h, int32_t img_w,
+                         int32_t block_x, int32_t block_y,
                           int32_t edges_per_segment, const float* final_Ts,
                           const int32_t* final_idx, const int32_t* log_index,
                           const void* log_pool, const float* v_output,
@@ -312,6 +323,7 @@ int cs_rasterize_backward_de_casteljau(int32_t mode, const int32_t* prim_ids_sor
                                        const int32_t* tile_bins, const void* edges,
                                        const void* edge_culls, const void* prim_recs,
                                        const float* background, int32_t img_h, int32_t img_w,
+                         int32_t block_x, int32_t block_y,
                                        const void* edge_aux, const float* final_Ts,
                                        const int32_t* final_idx, const int32_t* log_index,
                                        const void* log_pool, const float* v_output, float* v_cubics_px, float* v_colors,
@@ -334,6 +346,7 @@ int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                  const int32_t* tile_bins, const void* edges,
                                  const void* edge_culls, const void* prim_recs,
                                  const float* background, int32_t img_h, int32_t img_w,
+                         int32_t block_x, int32_t block_y,
                                  int32_t edges_per_segment, float* out_img, float* final_Ts,
                                  int32_t* final_idx, int64_t num_entries, int32_t* log_index,
                                  void* log_pool, int64_t log_pool_bytes,
@@ -343,6 +356,7 @@ int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                   const int32_t* tile_bins, const void* edges,
                                   const void* edge_culls, const void* prim_recs,
                                   const float* background, int32_t img_h, int32_t img_w,
+                         int32_t block_x, int32_t block_y,
                                   int32_t edges_per_segment, const float* final_Ts,
                                   const int32_t* final_idx, const int32_t* log_index,
                                   const void* log_pool, const float* v_output, float* v_cubics_px, float* v_colors,

@@ -49,16 +49,18 @@ _SIGNATURES = {
                                       _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_bin_finish": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _I32, _I32, _I32, _I32, _P, _P,
                                      _P, _P, _P, _I64, _P]),
-    "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
-                                            _P, _I64, _P, _P, _I64, _I32, _P, _P, _P]),
-    "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P,
-                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
+                                            _I32, _P, _P, _P, _I64, _P, _P, _I64, _I32, _P, _P,
+                                            _P]),
+    "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
+                                             _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                             _P, _P]),
     "cs_rasterize_forward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
-                                                    _P, _P, _P, _I64, _P, _P, _I64, _I32, _P, _P,
-                                                    _P, _P]),
+                                                    _I32, _I32, _P, _P, _P, _I64, _P, _P, _I64,
+                                                    _I32, _P, _P, _P, _P]),
     "cs_rasterize_backward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
-                                                     _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                                     _P, _P, _P, _P, _P]),
+                                                     _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P,
+                                                     _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_raster_tile_order": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
     "cs_raster_records_from_edges": (ctypes.c_int, [_I32, _P, _I32, _P, _P, _I64, _P, _P, _P, _P,
                                                     _P, _I32, _P, _I32, _P, _P, _P, _P, _P, _P,
@@ -77,8 +79,8 @@ _SIGNATURES = {
     "cs_cubic_flatness_flags": (ctypes.c_int, [_P, _I32, _F, _I32, _P, _P]),
     "cs_cubic_split_half": (ctypes.c_int, [_P, _I32, _P, _P, _P]),
     "cs_rasterize_backward_de_casteljau": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
-                                                          _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                                          _P, _P, _P, _P, _P]),
+                                                          _I32, _I32, _P, _P, _P, _P, _P, _P, _P,
+                                                          _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_accumulate_edge_grads_csr": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
                                                     _P]),
     "cs_backward_finalize": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P]),

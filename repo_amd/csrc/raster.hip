@@ -377,21 +377,52 @@ __device__ __forceinline__ LanePixels lane_pixels(int r0, int c0, int img_h, int
     return L;
 }
 
-// Tile of workgroup b: entry xcd_tile(b) of a heavy-first tile order when one
-// is given (cs_raster_tile_order), else the XCD-contiguous order xcd_tile(b).  Any
-// permutation of the tiles gives the same results: tiles are independent.
-__device__ __forceinline__ int block_tile(const int32_t* __restrict__ tile_order, int ntiles) {
-    const int t = xcd_tile(blockIdx.x, ntiles);
-    return tile_order ? __builtin_amdgcn_readfirstlane(tile_order[t]) : t;
+// The raster's workgroups: one per 16x16 sub-block of the image (two waves
+// of 16 x 8 pixels).  A tile of block_x x block_y pixels (multiples of 16)
+// holds sbx x sby sub-blocks, whose 2 sbx sby waves all walk the tile's list.
+// Largest tile: 16 sub-blocks (for example 64 x 64 pixels), 32 waves.
+constexpr int kRasterMaxWavesPerTile = 32;
+
+struct TileGrid {
+    int tbx;    // tiles per row
+    int sbtx;   // sub-blocks per row (ceil(img_w / 16))
+    int nsb;    // sub-blocks in the image
+    int sbx, sby;
+    int waves;  // waves per tile, 2 sbx sby
+};
+
+struct SubBlock {
+    int index;  // sub-block (the unit of the tile order and the wave costs)
+    int tile;   // its tile
+    int slot;   // this wave's slot among the tile's waves
+    int r0, c0; // its first pixel row and column
+};
+
+// Sub-block of workgroup b: entry xcd_tile(b) of a heavy-first order when one
+// is given (cs_raster_tile_order), else the XCD-contiguous order xcd_tile(b).
+// Any permutation gives the same results: sub-blocks are independent.
+__device__ __forceinline__ SubBlock sub_block(const TileGrid& tg,
+                                              const int32_t* __restrict__ tile_order, int wv) {
+    const int t = xcd_tile(blockIdx.x, tg.nsb);
+    SubBlock b;
+    b.index = tile_order ? __builtin_amdgcn_readfirstlane(tile_order[t]) : t;
+    const int sy = b.index / tg.sbtx, sx = b.index - sy * tg.sbtx;
+    const int ty = sy / tg.sby, tx = sx / tg.sbx;
+    b.tile = ty * tg.tbx + tx;
+    b.slot = 2 * ((sy - ty * tg.sby) * tg.sbx + (sx - tx * tg.sbx)) + wv;
+    b.r0 = sy * kTile;
+    b.c0 = sx * kTile;
+    return b;
 }
 
 // A wave's duration in ticks of the constant 100 MHz clock, stored in its
-// slot of wave_cost [2 * ntiles] (two waves per tile) for the next ordering.
-__device__ __forceinline__ void record_wave_cost(uint32_t* __restrict__ wave_cost, int tile,
+// slot of wave_cost [2 * sub-blocks] (two waves per sub-block) for the next
+// ordering.
+__device__ __forceinline__ void record_wave_cost(uint32_t* __restrict__ wave_cost, int sb,
                                                  uint64_t t_start) {
     if (wave_cost && (threadIdx.x & (kWave - 1)) == 0) {
         const uint64_t dt = __builtin_amdgcn_s_memrealtime() - t_start;
-        wave_cost[2 * tile + (threadIdx.x >> 6)] = dt > 0xffffffffull ? 0xffffffffu : (uint32_t)dt;
+        wave_cost[2 * sb + (threadIdx.x >> 6)] = dt > 0xffffffffull ? 0xffffffffu : (uint32_t)dt;
     }
 }
 
@@ -551,19 +582,19 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
-    int tbx, int ntiles, const int32_t* __restrict__ tile_order,
+    TileGrid tg, const int32_t* __restrict__ tile_order,
     uint32_t* __restrict__ wave_cost, float* __restrict__ out, float* __restrict__ final_T,
     int32_t* __restrict__ final_idx, int32_t* __restrict__ log_index,
     uint4* __restrict__ log_pool, uint32_t log_units, uint32_t log_per_entry,
     unsigned long long* __restrict__ counts) {
     const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
-    const int tile = block_tile(tile_order, ntiles);
-    const int tty = tile / tbx, ttx = tile - tty * tbx;
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r0 = tty * kTile + wv * kWaveRows;
-    const LanePixels L = lane_pixels(r0, ttx * kTile, img_h, img_w);
-    const WaveRect W{ttx * kTile, ttx * kTile + kTile - 1, r0, r0 + kWaveRows - 1};
+    const SubBlock sb = sub_block(tg, tile_order, wv);
+    const int tile = sb.tile;
+    const int r0 = sb.r0 + wv * kWaveRows;
+    const LanePixels L = lane_pixels(r0, sb.c0, img_h, img_w);
+    const WaveRect W{sb.c0, sb.c0 + kTile - 1, r0, r0 + kWaveRows - 1};
     const cptr<PrimRec> prims = as_const(prims_g);
     const cptr<EdgeRec> edges = as_const(edges_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
@@ -579,9 +610,10 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     }
     EvalCounts n{};
     // This wave's own log region: per_entry units for each entry of the
-    // tile's list, the two waves of a tile side by side.
+    // tile's list, the tile's waves side by side.
     const uint32_t len = (uint32_t)(g1 - g0);
-    const uint32_t own = 1u + (2u * (uint32_t)g0 + (uint32_t)wv * len) * log_per_entry;
+    const uint32_t own =
+        1u + ((uint32_t)tg.waves * (uint32_t)g0 + (uint32_t)sb.slot * len) * log_per_entry;
     LogCursor lc{own, own + len * log_per_entry, false};
     __shared__ uint4 log_stage_all[kRasterThreads / kWave][kLogStageUnits];
     uint4* const stage = log_stage_all[wv];
@@ -767,7 +799,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
                 }
             }
         }
-        if ((logged >> lane) & 1u) log_index[2 * (size_t)gl + wv] = idx_l;
+        if ((logged >> lane) & 1u) log_index[(size_t)tg.waves * gl + sb.slot] = idx_l;
     }
     if (log_index) log_flush(log_pool, stage, st);
 #pragma unroll
@@ -781,7 +813,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
         out[3 * pix + 2] = __builtin_fmaf(T[p], bg[2], C2[p]);
     }
     if constexpr (COUNT) flush_counts(n, counts);
-    record_wave_cost(wave_cost, tile, t_start);
+    record_wave_cost(wave_cost, sb.index, t_start);
 }
 
 // First unit of the log pool: the counter of the shared blocks, which start
@@ -864,20 +896,20 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
-    int tbx, int ntiles, const int32_t* __restrict__ tile_order, int eps, uint32_t eps_magic,
+    TileGrid tg, const int32_t* __restrict__ tile_order, int eps, uint32_t eps_magic,
     const EdgeAux* __restrict__ edge_aux, const int32_t* __restrict__ log_index_g,
     const uint4* __restrict__ log_pool, const float* __restrict__ final_T,
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
     float* __restrict__ isect_contrib, unsigned long long* __restrict__ counts) {
-    const int tile = block_tile(tile_order, ntiles);
-    const int tty = tile / tbx, ttx = tile - tty * tbx;
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r0 = tty * kTile + wv * kWaveRows;
-    const LanePixels L = lane_pixels(r0, ttx * kTile, img_h, img_w);
-    const WaveRect W{ttx * kTile, ttx * kTile + kTile - 1, r0, r0 + kWaveRows - 1};
+    const SubBlock sb = sub_block(tg, tile_order, wv);
+    const int tile = sb.tile;
+    const int r0 = sb.r0 + wv * kWaveRows;
+    const LanePixels L = lane_pixels(r0, sb.c0, img_h, img_w);
+    const WaveRect W{sb.c0, sb.c0 + kTile - 1, r0, r0 + kWaveRows - 1};
     const cptr<int32_t> prim_ids = as_const(prim_ids_g);
     const cptr<PrimRec> prims = as_const(prims_g);
     const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
@@ -934,7 +966,8 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
         const int pid_cur = __builtin_amdgcn_readlane(pid_l, k);
         const PrimRec pr = prims[pid_cur];
         // The forward's log record of this entry and wave, if it has one.
-        const int32_t at = log_index_g ? log_index[2 * (size_t)g + wv] : kLogMissing;
+        const int32_t at =
+            log_index_g ? log_index[(size_t)tg.waves * g + sb.slot] : kLogMissing;
         if (at == kLogEmpty) continue;   // no pixel inside or near: no contribution
         const bool uniform_inside = at == kLogInside;
         if constexpr (COUNT) n.entries += 1;
@@ -1378,7 +1411,8 @@ static int raster_status() {
 }
 
 struct RasterArgs {
-    int mode, nt, tbx, img_h, img_w, eps;
+    int mode, img_h, img_w, eps;
+    TileGrid tg;
     const int32_t* ids;
     const int32_t* bins;
     const EdgeRec* E;
@@ -1409,9 +1443,9 @@ struct RasterArgs {
 
 template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
-    hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.nt), dim3(kRasterThreads), 0,
-                       a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.order, a.wave_cost, a.out, a.final_T, a.final_idx, a.log_index,
+    hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.tg.nsb), dim3(kRasterThreads), 0,
+                       a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tg,
+                       a.order, a.wave_cost, a.out, a.final_T, a.final_idx, a.log_index,
                        a.log_pool, a.log_units, a.log_per_entry, a.counts);
 }
 
@@ -1420,9 +1454,10 @@ static void launch_bwd3(const RasterArgs& a) {
     // ceil(2^32 / eps) for div_eps (unused when eps <= 1).
     const uint32_t magic =
         a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
-    hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT, ADAPTIVE>), dim3(a.nt), dim3(kRasterThreads),
-                       0, a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tbx,
-                       a.nt, a.order, a.eps, magic, a.aux, a.log_index, a.log_pool, a.fT, a.fidx,
+    hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT, ADAPTIVE>), dim3(a.tg.nsb),
+                       dim3(kRasterThreads), 0, a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg,
+                       a.img_h, a.img_w, a.tg, a.order, a.eps, magic, a.aux, a.log_index,
+                       a.log_pool, a.fT, a.fidx,
                        a.v_out,
                        a.v_cub, a.v_col,
                        a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.counts);
@@ -1446,14 +1481,30 @@ static void launch_bwd_mode(const RasterArgs& a) {
     else launch_bwd<1, COUNT>(a);
 }
 
+// Tiles of block_x x block_y pixels, both positive multiples of 16 (the
+// 16x16 sub-blocks of the raster's workgroups), at most 16 waves per tile.
+static bool tile_grid(int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
+                      TileGrid& tg) {
+    if (img_h <= 0 || img_w <= 0 || img_h > kMaxImageDim || img_w > kMaxImageDim ||
+        block_x <= 0 || block_y <= 0 || block_x % kTile != 0 || block_y % kTile != 0)
+        return false;
+    tg.sbx = block_x / kTile;
+    tg.sby = block_y / kTile;
+    tg.waves = 2 * tg.sbx * tg.sby;
+    if (tg.waves > kRasterMaxWavesPerTile) return false;
+    tg.tbx = (img_w + block_x - 1) / block_x;
+    tg.sbtx = (img_w + kTile - 1) / kTile;
+    tg.nsb = tg.sbtx * ((img_h + kTile - 1) / kTile);
+    return true;
+}
+
 static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* bins,
                               const void* edges, const void* edge_culls, const void* prims,
-                              const float* bg, int32_t img_h, int32_t img_w, int32_t eps,
-                              hipStream_t stream) {
+                              const float* bg, int32_t img_h, int32_t img_w, const TileGrid& tg,
+                              int32_t eps, hipStream_t stream) {
     RasterArgs a{};
     a.mode = mode;
-    a.tbx = (img_w + kTile - 1) / kTile;
-    a.nt = a.tbx * ((img_h + kTile - 1) / kTile);
+    a.tg = tg;
     a.img_h = img_h;
     a.img_w = img_w;
     a.eps = eps;
@@ -1470,7 +1521,8 @@ static RasterArgs raster_args(int32_t mode, const int32_t* ids, const int32_t* b
 static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                              const int32_t* tile_bins, const void* edges, const void* edge_culls,
                              const void* prim_recs, const float* background, int32_t img_h,
-                             int32_t img_w, int32_t edges_per_segment, float* out_img,
+                             int32_t img_w, int32_t block_x, int32_t block_y,
+                             int32_t edges_per_segment, float* out_img,
                              float* final_Ts, int32_t* final_idx, int64_t num_entries,
                              int32_t* log_index, void* log_pool, int64_t log_pool_bytes,
                              int32_t log_entry_units, unsigned long long* eval_counts,
@@ -1478,19 +1530,20 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                              hipStream_t stream) {
     // The primitive records hold each primitive's edge range, so the forward
     // does not use edges_per_segment (0 for adaptively flattened records).
-    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 || edges_per_segment < 0 ||
-        img_h > kMaxImageDim || img_w > kMaxImageDim)
+    TileGrid tg;
+    if ((mode != 0 && mode != 1) || edges_per_segment < 0 ||
+        !tile_grid(img_h, img_w, block_x, block_y, tg))
         return CS_ERR_ARGS;
-    // The waves' own regions take 2 * num_entries * log_entry_units units after
-    // the counter; shared blocks follow.
+    // The waves' own regions take waves-per-tile * num_entries *
+    // log_entry_units units after the counter; shared blocks follow.
     const int64_t units = log_index ? log_pool_bytes / 16 : 0;
     const int64_t cap = units < (int64_t)kLogMaxUnits ? units : (int64_t)kLogMaxUnits;
-    const int64_t first_shared = 1 + 2 * num_entries * (int64_t)log_entry_units;
+    const int64_t first_shared = 1 + (int64_t)tg.waves * num_entries * (int64_t)log_entry_units;
     if (log_index && (!log_pool || (reinterpret_cast<uintptr_t>(log_pool) & 15) != 0 ||
                       num_entries < 0 || log_entry_units < 0 || first_shared > cap))
         return CS_ERR_ARGS;
     RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
-                               background, img_h, img_w, edges_per_segment, stream);
+                               background, img_h, img_w, tg, edges_per_segment, stream);
     a.out = out_img;
     a.final_T = final_Ts;
     a.final_idx = final_idx;
@@ -1512,15 +1565,16 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
 extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                                     const int32_t* tile_bins, const void* edges,
                                     const void* edge_culls, const void* prim_recs,
-                                    const float* background,
-                                    int32_t img_h, int32_t img_w, int32_t edges_per_segment,
+                                    const float* background, int32_t img_h, int32_t img_w,
+                                    int32_t block_x, int32_t block_y, int32_t edges_per_segment,
                                     float* out_img, float* final_Ts, int32_t* final_idx,
                                     int64_t num_entries, int32_t* log_index, void* log_pool,
                                     int64_t log_pool_bytes, int32_t log_entry_units,
                                     const int32_t* tile_order, uint32_t* wave_cost,
                                     hipStream_t stream) {
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
-                             background, img_h, img_w, edges_per_segment, out_img, final_Ts,
+                             background, img_h, img_w, block_x, block_y, edges_per_segment,
+                             out_img, final_Ts,
                              final_idx, num_entries, log_index, log_pool, log_pool_bytes,
                              log_entry_units, nullptr, tile_order, wave_cost, stream);
 }
@@ -1529,7 +1583,8 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
                                             const int32_t* tile_bins, const void* edges,
                                             const void* edge_culls, const void* prim_recs,
                                             const float* background, int32_t img_h,
-                                            int32_t img_w, int32_t edges_per_segment,
+                                            int32_t img_w, int32_t block_x, int32_t block_y,
+                                            int32_t edges_per_segment,
                                             float* out_img, float* final_Ts, int32_t* final_idx,
                                             int64_t num_entries, int32_t* log_index,
                                             void* log_pool, int64_t log_pool_bytes,
@@ -1539,7 +1594,8 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
                                             hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
-                             background, img_h, img_w, edges_per_segment, out_img, final_Ts,
+                             background, img_h, img_w, block_x, block_y, edges_per_segment,
+                             out_img, final_Ts,
                              final_idx, num_entries, log_index, log_pool, log_pool_bytes,
                              log_entry_units, eval_counts, tile_order, wave_cost, stream);
 }
@@ -1548,6 +1604,7 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               const int32_t* tile_bins, const void* edges,
                               const void* edge_culls, const void* prim_recs,
                               const float* background, int32_t img_h, int32_t img_w,
+                              int32_t block_x, int32_t block_y,
                               int32_t edges_per_segment, const float* final_Ts,
                               const int32_t* final_idx, const float* v_output,
                               float* v_cubics_px, float* v_colors, float* v_opacities,
@@ -1556,14 +1613,14 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               const void* edge_aux, const int32_t* log_index,
                               const void* log_pool, unsigned long long* eval_counts,
                               const int32_t* tile_order, hipStream_t stream) {
-    if ((mode != 0 && mode != 1) || img_h <= 0 || img_w <= 0 ||
-        (edge_aux == nullptr && edges_per_segment < 1) || img_h > kMaxImageDim ||
-        img_w > kMaxImageDim)
+    TileGrid tg;
+    if ((mode != 0 && mode != 1) || (edge_aux == nullptr && edges_per_segment < 1) ||
+        !tile_grid(img_h, img_w, block_x, block_y, tg))
         return CS_ERR_ARGS;
     if (mode == 1 && v_stroke_widths == nullptr) return CS_ERR_ARGS;
     if (log_index && !log_pool) return CS_ERR_ARGS;
     RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
-                               background, img_h, img_w, edges_per_segment, stream);
+                               background, img_h, img_w, tg, edges_per_segment, stream);
     a.fT = final_Ts;
     a.fidx = final_idx;
     a.v_out = v_output;
@@ -1588,8 +1645,8 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
 extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                                      const int32_t* tile_bins, const void* edges,
                                      const void* edge_culls, const void* prim_recs,
-                                     const float* background,
-                                     int32_t img_h, int32_t img_w,
+                                     const float* background, int32_t img_h, int32_t img_w,
+                                     int32_t block_x, int32_t block_y,
                                      int32_t edges_per_segment, const float* final_Ts,
                                      const int32_t* final_idx, const int32_t* log_index,
                                      const void* log_pool, const float* v_output,
@@ -1599,23 +1656,26 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                                      const int32_t* tile_order,
                                      hipStream_t stream) {
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
-                              background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
-                              v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
-                              v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              log_index, log_pool, nullptr, tile_order, stream);
+                              background, img_h, img_w, block_x, block_y, edges_per_segment,
+                              final_Ts, final_idx, v_output, v_cubics_px, v_colors, v_opacities,
+                              v_inv_sigma2s, v_stroke_widths, curve_contrib_rgb,
+                              curve_isect_contrib, nullptr, log_index, log_pool, nullptr,
+                              tile_order, stream);
 }
 
 extern "C" int cs_rasterize_backward_de_casteljau(
     int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
     const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
-    int32_t img_w, const void* edge_aux, const float* final_Ts, const int32_t* final_idx,
+    int32_t img_w, int32_t block_x, int32_t block_y, const void* edge_aux,
+    const float* final_Ts, const int32_t* final_idx,
     const int32_t* log_index, const void* log_pool, const float* v_output, float* v_cubics_px,
     float* v_colors, float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
     float* curve_contrib_rgb, float* curve_isect_contrib, const int32_t* tile_order,
     hipStream_t stream) {
     if (!edge_aux) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
-                              background, img_h, img_w, 0, final_Ts, final_idx, v_output,
+                              background, img_h, img_w, block_x, block_y, 0, final_Ts,
+                              final_idx, v_output,
                               v_cubics_px, v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
                               curve_contrib_rgb, curve_isect_contrib, edge_aux, log_index,
                               log_pool, nullptr, tile_order, stream);
@@ -1624,14 +1684,16 @@ extern "C" int cs_rasterize_backward_de_casteljau(
 extern "C" int cs_rasterize_backward_counted(
     int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
     const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
-    int32_t img_w, int32_t edges_per_segment, const float* final_Ts, const int32_t* final_idx,
+    int32_t img_w, int32_t block_x, int32_t block_y, int32_t edges_per_segment,
+    const float* final_Ts, const int32_t* final_idx,
     const int32_t* log_index, const void* log_pool, const float* v_output, float* v_cubics_px,
     float* v_colors, float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
     float* curve_contrib_rgb, float* curve_isect_contrib, unsigned long long* eval_counts,
     const int32_t* tile_order, hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
-                              background, img_h, img_w, edges_per_segment, final_Ts, final_idx,
+                              background, img_h, img_w, block_x, block_y, edges_per_segment,
+                              final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
                               log_index, log_pool, eval_counts, tile_order, stream);

@@ -79,10 +79,9 @@ def _check_ranges(isect_edge_ranges, num_intersects):
 
 
 def _check_block(block):
-    if int(block[0]) != BLOCK_X or int(block[1]) != BLOCK_Y:
-        raise NotImplementedError(
-            f"the MI355X raster kernels use {BLOCK_X}x{BLOCK_Y} tiles; got "
-            f"{int(block[0])}x{int(block[1])}")
+    from .splat import check_block
+    check_block(int(block[0]), int(block[1]))
+    return int(block[0]), int(block[1])
 
 
 def _check_pixels(name, t, shape):
@@ -91,14 +90,14 @@ def _check_pixels(name, t, shape):
 
 
 def raster_records(edges_px, ids, ranges, colors, opacities, inv_s2, fill_rules, tile_bins,
-                   img_h, img_w, *, stroke_widths=None):
+                   img_h, img_w, *, stroke_widths=None, block_x=BLOCK_X, block_y=BLOCK_Y):
     """(edges, edge_culls, prim_recs) for the raster entry points, built on
     the device from the reference's inputs; raises ValueError when the
     intersections of one primitive carry different edge ranges, or tile_bins
     does not hold a list range within [0, num_intersects] for each of the
-    image's 16x16 tiles."""
+    image's block_x x block_y tiles."""
     dev = edges_px.device
-    T = ((img_w + BLOCK_X - 1) // BLOCK_X) * ((img_h + BLOCK_Y - 1) // BLOCK_Y)
+    T = ((img_w + block_x - 1) // block_x) * ((img_h + block_y - 1) // block_y)
     if int(tile_bins.numel()) < 2 * T:
         raise ValueError(f"tile_bins must hold [{T}, 2] ranges for a {img_h}x{img_w} image, "
                          f"got {tuple(tile_bins.shape)}")
@@ -160,15 +159,17 @@ def rasterize_cubic_fill_forward_tilelang(tile_bounds, block, img_size, primitiv
     if int(e_px.shape[0]) <= 0:
         return empty()
     ranges = _check_ranges(isect_edge_ranges, num_intersects)
-    _check_block(block)
+    bx, by = _check_block(block)
     N.require_gpu(cubics_px, "cubics_px")
     ids = _i32(primitive_ids_sorted).view(-1)
     bins = _i32(tile_bins)
     edges, culls, prims = raster_records(e_px, ids, ranges, _f32(colors),
                                          _f32(opacities).view(-1), inv_s2,
-                                         _i32(fill_rules).view(-1), bins, H, W)
+                                         _i32(fill_rules).view(-1), bins, H, W, block_x=bx,
+                                         block_y=by)
     N.call("cs_rasterize_forward", 0, N.ptr(ids), N.ptr(bins), N.ptr(edges),
-           N.ptr(culls), N.ptr(prims), N.ptr(bg), H, W, 0, N.ptr(out_img), N.ptr(final_Ts),
+           N.ptr(culls), N.ptr(prims), N.ptr(bg), H, W, bx, by, 0, N.ptr(out_img),
+           N.ptr(final_Ts),
            N.ptr(final_idx), num_intersects, None, None, 0, 0, None, None, N.stream(dev))
     return out_img, final_Ts, final_idx
 
@@ -208,7 +209,7 @@ def rasterize_cubic_fill_backward_tilelang(tile_bounds, block, img_size, primiti
     if E <= 0:
         return v_cubics_px, v_colors, v_opacities, v_inv_sigma2s
     ranges = _check_ranges(isect_edge_ranges, int(primitive_ids_sorted.shape[0]))
-    _check_block(block)
+    bx, by = _check_block(block)
     contrib = None
     if curve_contrib_rgb is not None:
         if curve_contrib_rgb.shape != colors.shape:
@@ -230,12 +231,13 @@ def rasterize_cubic_fill_backward_tilelang(tile_bounds, block, img_size, primiti
     _check_pixels("v_output", v_output, (H, W, 3))
     edges, culls, prims = raster_records(e_px, ids, ranges, _f32(colors),
                                          _f32(opacities).view(-1), inv_s2,
-                                         _i32(fill_rules).view(-1), bins, H, W)
+                                         _i32(fill_rules).view(-1), bins, H, W, block_x=bx,
+                                         block_y=by)
     bg = background.to(device=dev, dtype=torch.float32).contiguous().view(3)
     v_px = v_cubics_px if (v_cubics_px.dtype is torch.float32 and v_cubics_px.is_contiguous()) \
         else torch.zeros((num_segments, 4, 2), dtype=torch.float32, device=dev)
     common = (0, N.ptr(ids), N.ptr(bins), N.ptr(edges), N.ptr(culls), N.ptr(prims), N.ptr(bg),
-              H, W)
+              H, W, bx, by)
     grads = (N.ptr(v_px), N.ptr(v_colors), N.ptr(v_opacities), N.ptr(v_inv_sigma2s), None,
              N.ptr(contrib), N.ptr(isect_contrib), None, N.stream(dev))
     fT, fi, vo = _f32(final_Ts), _i32(final_idx), _f32(v_output)

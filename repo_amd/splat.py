@@ -80,9 +80,14 @@ def tile_bounds(img_h: int, img_w: int, block_x: int = BLOCK_X, block_y: int = B
     return ((img_w + block_x - 1) // block_x, (img_h + block_y - 1) // block_y, 1)
 
 
+def sub_blocks(img_h: int, img_w: int) -> int:
+    """The raster's workgroups: 16 x 16 sub-blocks of the image."""
+    return ((img_w + BLOCK_X - 1) // BLOCK_X) * ((img_h + BLOCK_Y - 1) // BLOCK_Y)
+
+
 # Buffers of one binning, carved from one arena allocation: name -> (dtype,
 # shape).  Shapes depend on (nseg, P, S, T, scratch sizes).
-def _binning_fields(nseg, P, E, T, radix_elems, scan_elems, grad_elems, adaptive=False):
+def _binning_fields(nseg, P, E, T, nsub, radix_elems, scan_elems, grad_elems, adaptive=False):
     f32, i32 = torch.float32, torch.int32
     extra = ((("seg_edge_offsets", i32, (nseg + 1,)), ("edge_aux", i32, (E, N.EDGE_AUX_INTS)),
               ("leaf_counts", i32, (nseg,))) if adaptive else ())
@@ -107,7 +112,7 @@ def _binning_fields(nseg, P, E, T, radix_elems, scan_elems, grad_elems, adaptive
         ("tile_scratch", i32, (T,)),
         ("status", i32, (4,)),
         ("tile_bins", i32, (T, 2)),
-        ("wave_cost", i32, (2 * T,)),
+        ("wave_cost", i32, (2 * nsub,)),
         ("grad_accum", f32, (grad_elems,)),
     )
 
@@ -148,10 +153,15 @@ class Binned:
     nseg * 2^ceil(log2(samples - 1)) and seg_edge_offsets[-1] the edge count."""
 
     def __init__(self, *, mode, img_h, img_w, samples, nseg, nprim, arena, table,
-                 adaptive=False, ntiles=None):
+                 adaptive=False, ntiles=None, block_x=BLOCK_X, block_y=BLOCK_Y):
         self.mode, self.img_h, self.img_w, self.samples = mode, img_h, img_w, samples
         self.device = arena.device
         self.ntiles = int(table["tile_bins"][2][0]) if ntiles is None else int(ntiles)
+        # The raster's tiles: block_x x block_y pixels, rasterized as 16 x 16
+        # sub-blocks of two waves each, all of a tile's waves on its list.
+        self.block_x, self.block_y = int(block_x), int(block_y)
+        self.nsub = sub_blocks(img_h, img_w)
+        self.waves_per_tile = 2 * (self.block_x // BLOCK_X) * (self.block_y // BLOCK_Y)
         self.adaptive = adaptive
         self.nseg, self.nprim = nseg, nprim
         self.num_intersects = -1
@@ -269,7 +279,7 @@ def _bin_plan(key, lib, nseg, P, S, img_h, img_w, block_x, block_y, mode, adapti
     if plan is None:
         tbx, tby, _ = tile_bounds(img_h, img_w, block_x, block_y)
         T = tbx * tby
-        fields = _binning_fields(nseg, P, nseg * per_seg, T,
+        fields = _binning_fields(nseg, P, nseg * per_seg, T, sub_blocks(img_h, img_w),
                                  int(lib.cs_radix_counts_elems(P)),
                                  int(lib.cs_scan_temp_elems(max(P, T, nseg))),
                                  _grad_accum_elems(nseg, P, mode), adaptive)
@@ -312,7 +322,8 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
                      per_seg)
     arena = torch.empty((plan.nbytes,), dtype=torch.uint8, device=dev)
     b = Binned(mode=mode, img_h=img_h, img_w=img_w, samples=S, nseg=nseg, nprim=P, arena=arena,
-               table=plan.table, adaptive=adaptive, ntiles=plan.ntiles)
+               table=plan.table, adaptive=adaptive, ntiles=plan.ntiles, block_x=block_x,
+               block_y=block_y)
     base = b._base
     st = N.stream(dev)
     args = [N.ptr(cubics_norm), N.ptr(seg_offsets), N.ptr(colors), N.ptr(opacities),
@@ -454,14 +465,15 @@ def _poll_log_use(key) -> None:
     _LOG_UNITS[key] = units
 
 
-def log_layout(key, capacity: int, ntiles: int):
+def log_layout(key, capacity: int, nsub: int, waves_per_tile: int = 2):
     """(units per entry, pool bytes) for a forward of scene shape `key` with
-    `capacity` list entries: the waves' own regions, plus shared blocks for a
-    quarter of them and one block per wave."""
+    `capacity` list entries and tiles of `waves_per_tile` waves: the waves'
+    own regions, plus shared blocks for a quarter of them and one block per
+    wave (two per 16 x 16 sub-block)."""
     _poll_log_use(key)
     units = _LOG_UNITS.get(key, LOG_FIRST_UNITS_PER_ENTRY)
-    regions = 16 * 2 * capacity * units
-    shared = regions // 4 + 2 * ntiles * N.RASTER_LOG_BLOCK_BYTES + (1 << 20)
+    regions = 16 * waves_per_tile * capacity * units
+    shared = regions // 4 + 2 * nsub * N.RASTER_LOG_BLOCK_BYTES + (1 << 20)
     return units, (16 + regions + shared + 255) // 256 * 256
 
 
@@ -499,18 +511,19 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
     dev = b.device
     H, W = b.img_h, b.img_w
     out = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
-    ntiles = b.ntiles
+    nsub, wpt = b.nsub, b.waves_per_tile
     cap = max(int(b.primitive_ids_sorted.numel()), 1)
     # final_Ts, final_idx and the log's entry index share one allocation.
-    n_index = 2 * cap if log else 0
+    n_index = wpt * cap if log else 0
     aux = torch.empty((2 * H * W + n_index,), dtype=torch.int32, device=dev)
     final_T = aux[:H * W].view(torch.float32).view(H, W)
     final_idx = aux[H * W:2 * H * W].view(H, W)
     st = N.stream(dev)
     if log:
         key = b.log_key if b.log_key is not None else (
-            dev.index, b.mode, b.nprim, b.nseg, H, W, b.samples, b.adaptive)
-        units, pool_bytes = log_layout(key, cap, ntiles)
+            dev.index, b.mode, b.nprim, b.nseg, H, W, b.samples, b.adaptive, b.block_x,
+            b.block_y)
+        units, pool_bytes = log_layout(key, cap, nsub, wpt)
         if log_pool_bytes_override is not None:
             units, pool_bytes = 0, max(16, int(log_pool_bytes_override) // 16 * 16)
         b.log_index = aux[2 * H * W:]
@@ -522,13 +535,13 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
         log_args = (cap, None, None, 0, 0)
     # The tile order is kept apart: the next forward reads it after this
     # forward's buffers are gone.
-    order = torch.empty((ntiles,), dtype=torch.int32, device=dev)
-    okey = (dev.index, st, ntiles)
+    order = torch.empty((nsub,), dtype=torch.int32, device=dev)
+    okey = (dev.index, st, nsub)
     prev = _TILE_ORDERS.get(okey)
     base = aux.data_ptr()
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
-            b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), H, W,
-            b.edges_per_segment, N.ptr(out), base, base + 4 * H * W, *log_args)
+            b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), H, W, b.block_x,
+            b.block_y, b.edges_per_segment, N.ptr(out), base, base + 4 * H * W, *log_args)
     cost = b.ptr("wave_cost")
     prev_p = None if prev is None else prev.data_ptr()
     if eval_counts is not None:
@@ -538,9 +551,9 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
         with N.prof("cubic.fwd.rast"):
             N.call("cs_rasterize_forward", *args, prev_p, cost, st)
     if log and log_pool_bytes_override is None:
-        _read_log_use_later(key, b.log_pool, units, 1 + 2 * cap * units, pool_bytes, st)
+        _read_log_use_later(key, b.log_pool, units, 1 + wpt * cap * units, pool_bytes, st)
     with N.prof("cubic.fwd.tile_order"):
-        N.call("cs_raster_tile_order", cost, ntiles, int(ORDER_CHUNKED), order.data_ptr(), st)
+        N.call("cs_raster_tile_order", cost, nsub, int(ORDER_CHUNKED), order.data_ptr(), st)
     b.tile_order = order
     _TILE_ORDERS.pop(okey, None)
     if len(_TILE_ORDERS) >= _MAX_ORDERS:
@@ -590,7 +603,8 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
         with N.prof("cubic.bwd.rast"):
             N.call("cs_rasterize_backward_de_casteljau", b.mode, N.ptr(b.primitive_ids_sorted),
                    b.ptr("tile_bins"), b.ptr("edges"), b.ptr("edge_culls"), b.ptr("prim_recs"),
-                   N.ptr(background), b.img_h, b.img_w, b.ptr("edge_aux"), N.ptr(final_T),
+                   N.ptr(background), b.img_h, b.img_w, b.block_x, b.block_y,
+                   b.ptr("edge_aux"), N.ptr(final_T),
                    N.ptr(final_idx), log_index, log_pool, N.ptr(v_output), N.ptr(v_px),
                    N.ptr(v_colors),
                    N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
@@ -598,7 +612,8 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
         return v_px, v_colors, v_opac, v_is2, v_sw
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
-            b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), log_index, log_pool,
+            b.block_x, b.block_y, b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx),
+            log_index, log_pool,
             N.ptr(v_output), N.ptr(v_px),
             N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
             N.ptr(curve_isect_contrib))
@@ -659,10 +674,24 @@ def _remember_capacity(key, num_intersects: int) -> None:
     _CAPACITY_HINTS[key] = intersection_capacity(max(0, num_intersects))
 
 
-def _check_block(block_x: int, block_y: int) -> None:
-    if int(block_x) != BLOCK_X or int(block_y) != BLOCK_Y:
+# Largest tile: 16 sub-blocks of 16 x 16 pixels.
+MAX_SUB_BLOCKS_PER_TILE = 16
+
+
+def check_block(block_x: int, block_y: int) -> None:
+    """Tiles the MI355X raster takes: positive multiples of 16 in both
+    directions (it rasterizes 16 x 16 sub-blocks, every one inside one tile),
+    at most 16 sub-blocks per tile."""
+    bx, by = int(block_x), int(block_y)
+    if (bx <= 0 or by <= 0 or bx % BLOCK_X or by % BLOCK_Y
+            or (bx // BLOCK_X) * (by // BLOCK_Y) > MAX_SUB_BLOCKS_PER_TILE):
         raise NotImplementedError(
-            f"the MI355X raster kernels use {BLOCK_X}x{BLOCK_Y} tiles; got {block_x}x{block_y}")
+            f"the MI355X raster takes tiles whose sides are multiples of {BLOCK_X} pixels, at "
+            f"most {MAX_SUB_BLOCKS_PER_TILE} sub-blocks of {BLOCK_X}x{BLOCK_Y}; got "
+            f"{block_x}x{block_y}")
+
+
+_check_block = check_block
 
 
 def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacities, depths,
@@ -711,7 +740,8 @@ def _splat_forward(ctx, mode, cubics_norm, primitive_seg_offsets, colors, opacit
     rules_c = _i32(fill_rules).view(-1) if fill_rules is not None else None
     sw_c = _f32(stroke_widths).view(-1) if stroke_widths is not None else None
     hint_key = (cubics_norm.device.index, mode, num_primitives, num_segments, int(img_h),
-                int(img_w), int(distance_samples), flatten_method_norm)
+                int(img_w), int(distance_samples), flatten_method_norm, int(block_x),
+                int(block_y))
     b = bin_primitives(_f32(cubics_norm), offs, colors_c, opac_c, _f32(depths).view(-1),
                        rules_c, widths, sw_c, int(img_h), int(img_w), int(distance_samples),
                        aabb_pad=float(aabb_pad), aniso=bool(aniso_intersects), mode=mode,

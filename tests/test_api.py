@@ -348,3 +348,14 @@ def test_visual_debug_shim_calls_the_hook():
     emit_visual_debug(lambda stage, payload: seen.append((stage, dict(payload))), "post_forward",
                       {"step": 3})
     assert seen == [("post_forward", {"step": 3})]
+
+
+def test_tile_sizes_accepted_and_refused():
+    """The raster takes tiles whose sides are multiples of 16 (16 x 16
+    sub-blocks), at most 16 sub-blocks; others are refused before any work."""
+    from repo_amd.splat import check_block
+    for bx, by in ((16, 16), (32, 32), (16, 48), (64, 64), (256, 16)):
+        check_block(bx, by)
+    for bx, by in ((8, 8), (16, 8), (24, 16), (80, 64), (0, 16), (272, 16)):
+        with pytest.raises(NotImplementedError):
+            check_block(bx, by)

@@ -485,7 +485,8 @@ def test_raster_log_size_follows_use():
     sc = synth.make_scene(3)
     b, s = hip_bin(sc)
     bg = s.background.float().contiguous()
-    key = (b.device.index, b.mode, b.nprim, b.nseg, b.img_h, b.img_w, b.samples, b.adaptive)
+    key = (b.device.index, b.mode, b.nprim, b.nseg, b.img_h, b.img_w, b.samples, b.adaptive,
+           b.block_x, b.block_y)
     for k in range(3):
         splat.rasterize_forward(b, bg)
         torch.cuda.synchronize()
