@@ -113,7 +113,8 @@ int cs_bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, const f
                    void* edge_culls, int32_t* prim_tile_ranges, uint32_t* num_tiles_hit,
                    float* inv_sigma2s, void* prim_recs, uint32_t* keys, int32_t* order,
                    uint32_t* keys_alt, int32_t* vals_alt, uint32_t* radix_counts,
-                   uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status,
+                   uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_count,
+                   uint32_t* tile_scratch, int32_t* status,
                    hipStream_t stream);
 
 /* ---------------- adaptive (de Casteljau) flattening ---------------- */
@@ -144,7 +145,8 @@ int cs_bin_prepare_de_casteljau(
     void* seg_recs, void* edges, void* edge_culls, int32_t* prim_tile_ranges,
     uint32_t* num_tiles_hit, float* inv_sigma2s, void* prim_recs, uint32_t* keys,
     int32_t* order, uint32_t* keys_alt, int32_t* vals_alt, uint32_t* radix_counts,
-    uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_count, uint32_t* tile_scratch, int32_t* status, int32_t* seg_edge_offsets,
+    uint32_t* scan_temp, int32_t* rank_tile_ranges, uint32_t* tile_count, uint32_t* tile_scratch,
+    int32_t* status, int32_t* seg_edge_offsets,
     void* edge_aux, uint32_t* leaf_counts, hipStream_t stream);
 
 /* _flatten_cubics_to_edges, de Casteljau branch (ops/cubic_splatting.py:1729-1832),
@@ -190,7 +192,8 @@ int cs_cubic_split_half(const float* cubics, int32_t n, float* left, float* righ
  * saves that step a separate fill. */
 int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t nprim,
                   const int32_t* status, int64_t capacity, int32_t img_h, int32_t img_w,
-                  int32_t block_x, int32_t block_y, uint32_t* tile_count, uint32_t* tile_scratch, int32_t* prim_ids_sorted,
+                  int32_t block_x, int32_t block_y, uint32_t* tile_count, uint32_t* tile_scratch,
+                  int32_t* prim_ids_sorted,
                   int32_t* tile_bins, float* zero_buf, int64_t zero_n, hipStream_t stream);
 
 /* ---------------- rasterization ---------------- */
@@ -304,7 +307,7 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
 int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
                           const void* edges, const void* edge_culls, const void* prim_recs,
                           const float* background, int32_t img_h, int32_t img_w,
-                         int32_t block_x, int32_t block_y,
+                          int32_t block_x, int32_t block_y,
                           int32_t edges_per_segment, const float* final_Ts,
                           const int32_t* final_idx, const int32_t* log_index,
                           const void* log_pool, const float* v_output,
@@ -323,10 +326,11 @@ int cs_rasterize_backward_de_casteljau(int32_t mode, const int32_t* prim_ids_sor
                                        const int32_t* tile_bins, const void* edges,
                                        const void* edge_culls, const void* prim_recs,
                                        const float* background, int32_t img_h, int32_t img_w,
-                         int32_t block_x, int32_t block_y,
+                                       int32_t block_x, int32_t block_y,
                                        const void* edge_aux, const float* final_Ts,
                                        const int32_t* final_idx, const int32_t* log_index,
-                                       const void* log_pool, const float* v_output, float* v_cubics_px, float* v_colors,
+                                       const void* log_pool, const float* v_output,
+                                       float* v_cubics_px, float* v_colors,
                                        float* v_opacities, float* v_inv_sigma2s,
                                        float* v_stroke_widths, float* curve_contrib_rgb,
                                        float* curve_isect_contrib, const int32_t* tile_order,
@@ -346,20 +350,22 @@ int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                  const int32_t* tile_bins, const void* edges,
                                  const void* edge_culls, const void* prim_recs,
                                  const float* background, int32_t img_h, int32_t img_w,
-                         int32_t block_x, int32_t block_y,
+                                 int32_t block_x, int32_t block_y,
                                  int32_t edges_per_segment, float* out_img, float* final_Ts,
                                  int32_t* final_idx, int64_t num_entries, int32_t* log_index,
                                  void* log_pool, int64_t log_pool_bytes,
-                                 int32_t log_entry_units, unsigned long long* eval_counts, const int32_t* tile_order,
+                                 int32_t log_entry_units, unsigned long long* eval_counts,
+                                 const int32_t* tile_order,
                                  uint32_t* wave_cost, hipStream_t stream);
 int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                   const int32_t* tile_bins, const void* edges,
                                   const void* edge_culls, const void* prim_recs,
                                   const float* background, int32_t img_h, int32_t img_w,
-                         int32_t block_x, int32_t block_y,
+                                  int32_t block_x, int32_t block_y,
                                   int32_t edges_per_segment, const float* final_Ts,
                                   const int32_t* final_idx, const int32_t* log_index,
-                                  const void* log_pool, const float* v_output, float* v_cubics_px, float* v_colors,
+                                  const void* log_pool, const float* v_output,
+                                  float* v_cubics_px, float* v_colors,
                                   float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
                                   float* curve_contrib_rgb, float* curve_isect_contrib,
                                   unsigned long long* eval_counts, const int32_t* tile_order,

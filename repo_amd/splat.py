@@ -504,7 +504,8 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
     default) it writes the raster log its backward reads (b.log_index,
     b.log_pool); without, nothing is allocated for it and a backward would
     recompute every entry (log_pool_bytes_override sets the pool size with no
-    per-wave regions, for tests of a pool that runs full).  The launch takes tiles in the heavy-first order
+    per-wave regions, for tests of a pool that runs full).  The launch takes
+    tiles in the heavy-first order
     of the previous forward of this image size on this stream (if any) and
     records its wave durations, from which the order of this forward's
     backward (b.tile_order) and of the next forward is made."""
