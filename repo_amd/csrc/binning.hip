@@ -185,6 +185,15 @@ __device__ __forceinline__ IRange pixel_range(float lo, float hi, float d) {
     return IRange{px_index(floorf(lo - d - 0.5f)) - 1, px_index(ceilf(hi + d - 0.5f)) + 1};
 }
 
+// Rows k with lo <= k + 0.5 < hi, where the crossing test y0 <= py != y1 <= py
+// (py = k + 0.5) can count an edge whose y-range is [lo, hi]: k from
+// ceil(lo - 0.5) to ceil(hi - 0.5) - 1.  lo - 0.5 and hi - 0.5 are exact for
+// magnitudes below 2^23; larger ones clamp past every pixel row.  Empty
+// (hi < lo) when lo == hi or both are NaN.
+__device__ __forceinline__ IRange crossing_rows(float lo, float hi) {
+    return IRange{px_index(ceilf(lo - 0.5f)), px_index(ceilf(hi - 0.5f)) - 1};
+}
+
 __device__ __forceinline__ int32_t span_x(IRange r) { return r.hi - r.lo + kWaveColsExt; }
 __device__ __forceinline__ int32_t span_y(IRange r) { return r.hi - r.lo + kWaveRowsExt; }
 
@@ -195,6 +204,12 @@ __device__ __forceinline__ int32_t packed_range(IRange r, int ext) {
     const int lo = clampi(r.lo, -2, kMaxImageDim + 16);
     const int hi = clampi(r.hi, -2, kMaxImageDim + 16);
     return pack_lo_span(lo, hi - lo + ext);
+}
+
+// packed_range of a range that may be empty; an empty one meets no wave
+// (its first row lies past every image row).
+__device__ __forceinline__ int32_t packed_range_or_empty(IRange r, int ext) {
+    return r.hi < r.lo ? pack_lo_span(kMaxImageDim + 16, 0) : packed_range(r, ext);
 }
 
 // torch.linspace(0, 1, S)[i] as ATen's device kernel computes it.
@@ -217,12 +232,13 @@ __device__ __forceinline__ void write_edge(float ax, float ay, float bx, float b
     o[1] = make_int4(__builtin_bit_cast(int, vx), __builtin_bit_cast(int, vy),
                      __builtin_bit_cast(int, vx * ivv), __builtin_bit_cast(int, vy * ivv));
     const IRange nx = pixel_range(ex0, ex1, D), ny = pixel_range(ey0, ey1, D);
-    const IRange cy = pixel_range(ey0, ey1, 0.0f);
+    const IRange cy = crossing_rows(ey0, ey1);
+    const int32_t flags =
+        ((fabsf(ax) <= kFarCrossMaxX && fabsf(bx) <= kFarCrossMaxX) ? kCullFarCrossExact : 0) |
+        (ay < by ? kCullUp : 0);
     *reinterpret_cast<int4*>(ec) =
-        make_int4(packed_range(ny, kWaveRowsExt), packed_range(cy, kWaveRowsExt),
-                  packed_range(nx, kWaveColsExt),
-                  (fabsf(ax) <= kFarCrossMaxX && fabsf(bx) <= kFarCrossMaxX) ? kCullFarCrossExact
-                                                                             : 0);
+        make_int4(packed_range(ny, kWaveRowsExt), packed_range_or_empty(cy, kWaveRowsExt),
+                  packed_range(nx, kWaveColsExt), flags);
 }
 
 // Bounding box of a segment's polyline vertices -> its segment record.

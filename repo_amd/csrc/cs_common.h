@@ -50,9 +50,10 @@ struct alignas(16) EdgeRec {
 };
 
 // The cull ranges of one edge, 16 bytes, each range packed as two int16
-// (low half lo, high half span): near rows, crossing rows (the edge's
-// y-range, where a +x ray crossing is possible; a subset of the near rows),
-// near columns.  Kept apart from the geometry so that the forward reads only
+// (low half lo, high half span): near rows, crossing rows (exactly the rows k
+// whose centre k + 0.5 lies in [min(y0, y1), max(y0, y1)), the rows where the
+// +x ray crossing test can count the edge; a subset of the near rows), near
+// columns, then flags.  Kept apart from the geometry so that the forward reads only
 // geometry and the backward reads the ranges of a whole primitive with one
 // vector load.  Packing limits pixel indices to int16, so images are at most
 // kMaxImageDim on a side.
@@ -71,6 +72,8 @@ struct alignas(16) EdgeCull {
 // then +1 / -1 on every row it spans when it lies right of the wave and 0
 // when it lies left, exactly as the per-pixel test evaluates it.
 constexpr int32_t kCullFarCrossExact = 1;
+// EdgeCull.flags bit: y1 > y0, so the edge's crossings count +1 (else -1).
+constexpr int32_t kCullUp = 2;
 constexpr float kFarCrossMaxX = 1048576.0f;
 constexpr int kMaxImageDim = 16384;
 

@@ -441,50 +441,45 @@ __device__ __forceinline__ bool prim_culled_lane(const PrimRec* __restrict__ p,
     return !span_hits(a.z, a.w, W.r1) || W.c0 > b.z;
 }
 
+// Winding number at the pixel row r of a wave over the edges c + lane < e1 of
+// one chunk, when none of them has a distance or exact crossing term for the
+// wave (a far chunk): an edge whose crossing rows (exact) contain r is then
+// flagged kCullFarCrossExact and misses the wave's near columns, so its
+// crossing term there is +1 (upward) or -1 when it lies right of the wave and
+// 0 when it lies left -- the values cross_term computes at every pixel of
+// that row.  One lane per edge, two ballots; no edge geometry is read.
+__device__ __forceinline__ int far_winding(int4 q, int c, int e1, const WaveRect& W) {
+    const bool in = c + (int)(threadIdx.x & (kWave - 1)) < e1;
+    const bool hit = in && span_hits(packed_lo(q.y), packed_span(q.y) - kWaveRowsExt, W.r0) &&
+                     packed_lo(q.z) > W.c1;
+    const bool up = (q.w & kCullUp) != 0;
+    return __builtin_popcountll(__ballot(hit && up)) - __builtin_popcountll(__ballot(hit && !up));
+}
+
 // Far entry: no edge of the primitive lies within the cull distance of any of
 // the wave's pixels (its near ranges miss the wave), and (fill) every edge
 // whose y-range spans one of the wave's rows carries kCullFarCrossExact.
 // Then no pixel needs the exact coverage, and every pixel has the same
 // winding number: the winding number changes only across an edge, none
 // crosses the wave's rectangle, and for such edges the fp32 crossing test at
-// each pixel gives the geometric side (see kCullFarCrossExact).  `first`
-// holds the masks of the first 64 edges: the entry is far when no edge has a
-// distance or exact crossing term.
+// each pixel gives the geometric side (see kCullFarCrossExact).  `q0` and
+// `first` hold the cull words and masks of the first 64 edges: the entry is
+// far when no edge has a distance or exact crossing term.  For a fill,
+// `winding` receives the winding number of the wave's pixels (far_winding).
 template <int MODE>
 __device__ __forceinline__ bool entry_far(const PrimRec& pr, const WaveRect& W,
-                                          const EdgeCull* __restrict__ culls,
-                                          const ChunkMasks& first) {
+                                          const EdgeCull* __restrict__ culls, int4 q0,
+                                          const ChunkMasks& first, int& winding) {
     if (first.dist | first.cross) return false;
+    int w = MODE == 0 ? far_winding(q0, pr.e0, pr.e1, W) : 0;
     for (int c = pr.e0 + kWave; c < pr.e1; c += kWave) {
-        const ChunkMasks m = chunk_masks<MODE == 0>(load_culls(culls, c, pr.e1), c, pr.e1, W);
+        const int4 q = load_culls(culls, c, pr.e1);
+        const ChunkMasks m = chunk_masks<MODE == 0>(q, c, pr.e1, W);
         if (m.dist | m.cross) return false;
+        if (MODE == 0) w += far_winding(q, c, pr.e1, W);
     }
+    winding = w;
     return true;
-}
-
-// Winding number of one point (px, py) over all edges of the primitive, one
-// edge per lane: cross_term's expressions, summed with two ballots per chunk.
-__device__ __forceinline__ int point_winding(const PrimRec& pr,
-                                             const EdgeRec* __restrict__ edges_g, float px,
-                                             float py) {
-    const int lane = threadIdx.x & (kWave - 1);
-    int w = 0;
-    for (int c = pr.e0; c < pr.e1; c += kWave) {
-        const int e = c + lane;
-        bool up = false, down = false;
-        if (e < pr.e1) {
-            const float4 a = *reinterpret_cast<const float4*>(edges_g + e);          // x0 y0 x1 y1
-            const float2 v = *reinterpret_cast<const float2*>(&edges_g[e].vx);       // vx vy
-            const bool b0 = a.y <= py, b1 = a.w <= py;
-            const float wx = px - a.x, wy = py - a.y;
-            const float cr = __builtin_fmaf(wy, v.x, -(wx * v.y));
-            const bool hit = (b0 != b1) & ((b0 ? cr : -cr) > 0.0f);
-            up = hit & b0;
-            down = hit & !b0;
-        }
-        w += __builtin_popcountll(__ballot(up)) - __builtin_popcountll(__ballot(down));
-    }
-    return w;
 }
 
 // Exact coverage from the squared distance: coverage()'s expressions and
@@ -557,8 +552,11 @@ struct LogStage {
 
 __device__ __forceinline__ void log_flush(uint4* __restrict__ pool, const uint4* stage,
                                           LogStage& st) {
-    for (uint32_t u = threadIdx.x & (kWave - 1); u < st.n; u += kWave)
-        pool[st.base + u] = stage[u];
+    // A wave-uniform loop (the lane test inside), so that the stage's
+    // position and size stay scalar values.
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    for (uint32_t u0 = 0; u0 < st.n; u0 += kWave)
+        if (u0 + lane < st.n) pool[st.base + u0 + lane] = stage[u0 + lane];
     st.n = 0;
 }
 
@@ -663,16 +661,14 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
                 n.entries += 1;
             }
             const ChunkMasks cm0 = chunk_masks<MODE == 0>(q, pr.e0, pr.e1, W);
-            if (entry_far<MODE>(pr, W, culls, cm0)) {
+            int wnd = 0;
+            if (entry_far<MODE>(pr, W, culls, q, cm0, wnd)) {
                 // Uniform entry: outside (nothing to do) or, for a fill whose
-                // winding at the wave's first pixel says inside, coverage 1
-                // at every pixel.
+                // winding number says inside, coverage 1 at every pixel.
                 bool inside_all = false;
                 if constexpr (MODE == 0) {
-                    const int w = point_winding(pr, edges_g, (float)W.c0 + 0.5f,
-                                                (float)W.r0 + 0.5f);
-                    inside_all = pr.rule == 0 ? ((w & 1) != 0) : (w != 0);
-                    if constexpr (COUNT) n.cross += (uint64_t)(pr.e1 - pr.e0);
+                    inside_all = pr.rule == 0 ? ((wnd & 1) != 0) : (wnd != 0);
+                    if constexpr (COUNT) n.row += (uint64_t)(pr.e1 - pr.e0);
                 }
                 if (log_index) {
                     idx_l = lane == k ? (inside_all ? kLogInside : kLogEmpty) : idx_l;
@@ -709,6 +705,17 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
                 cov[p] = ins[p] ? 1.0f : 0.0f;   // closed form; exact pixels below
             }
             const uint64_t x0 = __ballot(ex[0]), x1 = __ballot(ex[kPix - 1]);
+            const uint64_t in0 = MODE == 0 ? (uint64_t)__ballot(ins[0]) : 0ull;
+            const uint64_t in1 = MODE == 0 ? (uint64_t)__ballot(ins[kPix - 1]) : 0ull;
+            if ((in0 | in1 | x0 | x1) == 0) {
+                // No pixel inside or within the exact distance: every
+                // coverage is 0 and the entry changes nothing.
+                if (log_index) {
+                    idx_l = lane == k ? kLogEmpty : idx_l;
+                    logged |= 1ull << k;
+                }
+                continue;
+            }
             const int n0 = __builtin_popcountll(x0), nx = n0 + __builtin_popcountll(x1);
             const int rk0 = lane_rank(x0), rk1 = lane_rank(x1);
             if constexpr (COUNT) n.cover += (uint64_t)nx;
@@ -747,37 +754,31 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
             // The log record of this entry and wave: inside and exact bits, and
             // each exact pixel's best edge and coverage, for the backward.
             if (log_index) {
-                const uint64_t in0 = MODE == 0 ? (uint64_t)__ballot(ins[0]) : 0ull;
-                const uint64_t in1 = MODE == 0 ? (uint64_t)__ballot(ins[kPix - 1]) : 0ull;
-                int32_t at = kLogEmpty;
-                if ((in0 | in1 | x0 | x1) != 0) {
-                    const uint32_t units = kLogHeaderUnits + (uint32_t)((nx + 1) >> 1);
-                    if (st.n + units > kLogStageUnits) log_flush(log_pool, stage, st);
-                    at = log_reserve(log_pool, log_units, lc, units);
-                    if (at >= 0) {
-                        if ((uint32_t)at != st.base + st.n) {   // another region: flush first
-                            log_flush(log_pool, stage, st);
-                            st.base = (uint32_t)at;
-                        }
-                        uint4* rec = stage + st.n;
-                        st.n += units;
-                        if (lane == 0) {
-                            rec[0] = make_uint4((uint32_t)in0, (uint32_t)(in0 >> 32),
-                                                (uint32_t)in1, (uint32_t)(in1 >> 32));
-                            rec[1] = make_uint4((uint32_t)x0, (uint32_t)(x0 >> 32), (uint32_t)x1,
-                                                (uint32_t)(x1 >> 32));
-                        }
-                        int2* pairs = reinterpret_cast<int2*>(rec + kLogHeaderUnits);
-                        if (gathered) {
-                            if (lane < nx)
-                                pairs[lane] = make_int2(best_g, __builtin_bit_cast(int, cov_g));
-                        } else {
-                            if (ex[0])
-                                pairs[rk0] = make_int2(G[0].best, __builtin_bit_cast(int, cov[0]));
-                            if (ex[1])
-                                pairs[n0 + rk1] =
-                                    make_int2(G[1].best, __builtin_bit_cast(int, cov[1]));
-                        }
+                const uint32_t units = kLogHeaderUnits + (uint32_t)((nx + 1) >> 1);
+                if (st.n + units > kLogStageUnits) log_flush(log_pool, stage, st);
+                const int32_t at = log_reserve(log_pool, log_units, lc, units);
+                if (at >= 0) {
+                    if ((uint32_t)at != st.base + st.n) {   // another region: flush first
+                        log_flush(log_pool, stage, st);
+                        st.base = (uint32_t)at;
+                    }
+                    uint4* rec = stage + st.n;
+                    st.n += units;
+                    if (lane == 0) {
+                        rec[0] = make_uint4((uint32_t)in0, (uint32_t)(in0 >> 32),
+                                            (uint32_t)in1, (uint32_t)(in1 >> 32));
+                        rec[1] = make_uint4((uint32_t)x0, (uint32_t)(x0 >> 32), (uint32_t)x1,
+                                            (uint32_t)(x1 >> 32));
+                    }
+                    int2* pairs = reinterpret_cast<int2*>(rec + kLogHeaderUnits);
+                    if (gathered) {
+                        if (lane < nx)
+                            pairs[lane] = make_int2(best_g, __builtin_bit_cast(int, cov_g));
+                    } else {
+                        if (ex[0])
+                            pairs[rk0] = make_int2(G[0].best, __builtin_bit_cast(int, cov[0]));
+                        if (ex[1])
+                            pairs[n0 + rk1] = make_int2(G[1].best, __builtin_bit_cast(int, cov[1]));
                     }
                 }
                 idx_l = lane == k ? at : idx_l;
