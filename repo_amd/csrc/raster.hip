@@ -852,19 +852,23 @@ __device__ __forceinline__ void seg_basis(int e, float inv_e, float b[4]) {
     basis_at((float)e * inv_e, b);
 }
 
-// Masks of a raster log record at unit `at` of the pool (scalar loads).
+// Masks of a raster log record's header: per pixel row of the lanes, the
+// inside bits and the exact bits.
 struct LogHead {
     uint64_t in[kPix], xm[kPix];
 };
 
-__device__ __forceinline__ LogHead log_head(const uint4* __restrict__ pool, int32_t at) {
-    const cptr<uint4> hd = as_const(pool + at);
-    const uint4 a = hd[0], b = hd[1];
+// The header that lane k read (ha, hb: its first two units).
+__device__ __forceinline__ LogHead log_head_lane(uint4 ha, uint4 hb, int k) {
     LogHead h;
-    h.in[0] = ((uint64_t)a.y << 32) | a.x;
-    h.in[1] = ((uint64_t)a.w << 32) | a.z;
-    h.xm[0] = ((uint64_t)b.y << 32) | b.x;
-    h.xm[1] = ((uint64_t)b.w << 32) | b.z;
+    h.in[0] = ((uint64_t)__builtin_amdgcn_readlane(ha.y, k) << 32) |
+              (uint32_t)__builtin_amdgcn_readlane(ha.x, k);
+    h.in[1] = ((uint64_t)__builtin_amdgcn_readlane(ha.w, k) << 32) |
+              (uint32_t)__builtin_amdgcn_readlane(ha.z, k);
+    h.xm[0] = ((uint64_t)__builtin_amdgcn_readlane(hb.y, k) << 32) |
+              (uint32_t)__builtin_amdgcn_readlane(hb.x, k);
+    h.xm[1] = ((uint64_t)__builtin_amdgcn_readlane(hb.w, k) << 32) |
+              (uint32_t)__builtin_amdgcn_readlane(hb.z, k);
     return h;
 }
 
@@ -940,7 +944,6 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     // The wave maximum is uniform; readfirstlane tells the compiler so, which
     // keeps every load that depends on the entry index scalar.
     const int gstart = min(g1 - 1, __builtin_amdgcn_readfirstlane(wave_max_i(fmax)));
-    const cptr<int32_t> log_index = as_const(log_index_g);
     const int slot = reduce8_slot(lane & 7);
     const bool adder = (lane & ~7) == 8;
     // Entries from gstart down to g0 in chunks of 64: lane k tests entry
@@ -951,7 +954,19 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
       const int gl = gc - lane;
       const bool in_list = gl >= g0;
       const int pid_l = in_list ? prim_ids_g[gl] : 0;
-      uint64_t todo = __ballot(in_list && !prim_culled_lane<MODE>(prims_g + pid_l, W));
+      // Lane k also reads entry gc - k's log index and, when it has a record,
+      // the record's header, so that no entry waits for them.  Every entry at
+      // or below gstart that passes the cull was processed by the forward,
+      // so its index is written; the others are not read.
+      const bool kept = in_list && !prim_culled_lane<MODE>(prims_g + pid_l, W);
+      const int32_t at_l = (kept && log_index_g) ? log_index_g[(size_t)tg.waves * gl + sb.slot]
+                                                 : kLogMissing;
+      uint4 ha = make_uint4(0u, 0u, 0u, 0u), hb = ha;
+      if (at_l >= 0) {
+          ha = log_pool[at_l];
+          hb = log_pool[at_l + 1];
+      }
+      uint64_t todo = __ballot(kept && at_l != kLogEmpty);
       while (todo) {
         const int k = (int)__builtin_ctzll(todo);
         todo &= todo - 1;
@@ -966,10 +981,9 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
         if (__ballot(any_valid) == 0) continue;
         const int pid_cur = __builtin_amdgcn_readlane(pid_l, k);
         const PrimRec pr = prims[pid_cur];
-        // The forward's log record of this entry and wave, if it has one.
-        const int32_t at =
-            log_index_g ? log_index[(size_t)tg.waves * g + sb.slot] : kLogMissing;
-        if (at == kLogEmpty) continue;   // no pixel inside or near: no contribution
+        // The forward's log record of this entry and wave, if it has one
+        // (entries without a contribution, kLogEmpty, are not visited).
+        const int32_t at = __builtin_amdgcn_readlane(at_l, k);
         const bool uniform_inside = at == kLogInside;
         if constexpr (COUNT) n.entries += 1;
         // From the record: inside bits (the forward's winding test), exact
@@ -1008,7 +1022,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
                 G[p].winding = (int)ins;
             }
         } else {
-            const LogHead h = log_head(log_pool, at);
+            const LogHead h = log_head_lane(ha, hb, k);
             int2 lpx[kPix] = {make_int2(0, 0), make_int2(0, 0)};
             log_pixels(log_pool, at, h, lane, lpx);
             if constexpr (COUNT)
