@@ -883,16 +883,55 @@ __device__ __forceinline__ void log_pixels(const uint4* __restrict__ pool, int32
             px[p] = pairs[(p == 0 ? 0 : __builtin_popcountll(h.xm[0])) + lane_rank(h.xm[p])];
 }
 
+// A wave's gradient contributions, collected in LDS and added to global
+// memory in bulk (one 64-lane atomic instruction per 64 of them) when the
+// buffer would overflow and when the wave ends.  One counter tracks a wave's
+// outstanding vector loads and stores alike, so an atomic issued before a
+// load makes the wait for that load wait for the atomic too: added right
+// away, every entry's atomics would put an L2 round trip before the next
+// entry's first load.  Entries with a null destination are skipped.
+struct GradRec {
+    float* dst;
+    float v;
+};
+constexpr uint32_t kGradBufRecs = 256;   // 4 KiB of LDS per wave
+
+struct GradBuf {
+    GradRec* rec;
+    uint32_t n;   // wave-uniform
+};
+
+__device__ __forceinline__ void grad_flush(GradBuf& gb) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    for (uint32_t i0 = 0; i0 < gb.n; i0 += kWave) {
+        if (i0 + lane < gb.n) {
+            const GradRec r = gb.rec[i0 + lane];
+            if (r.dst) atomicAdd(r.dst, r.v);
+        }
+    }
+    gb.n = 0;
+}
+
+// Records (dst, v) from the lanes with `add` (lanes 8..15 after
+// wave_reduce8, each its slot); eight records per call.
+__device__ __forceinline__ void grad_push8(GradBuf& gb, bool add, float* dst, float v) {
+    if (gb.n + 8 > kGradBufRecs) grad_flush(gb);
+    const int lane = threadIdx.x & (kWave - 1);
+    if (lane >= 8 && lane < 16) gb.rec[gb.n + (lane - 8)] = GradRec{add ? dst : nullptr, v};
+    gb.n += 8;
+}
+
 // Backward: the reverse traversal of cubic_splatting.py:1339-1649 (fill) and
 // cubic_polyline_splatting.py:393-658 (stroke).  Per-pixel terms are those of
 // the reference; the sums differ in how they are formed:
 //   * per-primitive gradients: the lane's two pixels are added, then one DPP
-//     wave reduction and one atomic per value, wave and entry;
+//     wave reduction and one atomic addition per value, wave and entry
+//     (issued in bulk from the wave's GradBuf);
 //   * geometry: each pixel folds its best edge's endpoint gradients straight
 //     into the 8 control-point gradients of the edge's cubic segment with the
 //     reference's accumulation weights (cubic_splatting.py:2308-2396), then
 //     the pixels that share a segment are summed (one leader pass per distinct
-//     segment) and one 8-lane atomic adds the 8 values to v_cubics_px.
+//     segment) and the 8 values are added to v_cubics_px (through GradBuf).
 // ADAPTIVE: edges come from the de Casteljau flattening; an edge's segment and
 // its leaf interval [t0, t1] are read from its aux record (the CSR weights of
 // cubic_splatting.py:2432-2485) instead of being derived from its index.
@@ -946,6 +985,8 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     const int gstart = min(g1 - 1, __builtin_amdgcn_readfirstlane(wave_max_i(fmax)));
     const int slot = reduce8_slot(lane & 7);
     const bool adder = (lane & ~7) == 8;
+    __shared__ GradRec grad_rec_all[kRasterThreads / kWave][kGradBufRecs];
+    GradBuf gbuf{grad_rec_all[wv], 0u};
     // Entries from gstart down to g0 in chunks of 64: lane k tests entry
     // gc - k with the forward's primitive cull, and the wave visits the
     // survivors in descending order -- exactly the entries the forward
@@ -1141,19 +1182,18 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
         // then hold the totals and each adds one of them.
         {
             const float t = wave_reduce8(pv);
-            if (adder && slot < (MODE == 1 ? 6 : 5)) {
-                float* dst = slot < 3 ? v_colors + 3 * pid_cur + slot
-                           : slot == 3 ? v_opac + pid_cur
-                           : slot == 4 ? v_is2 + pid_cur
-                                       : v_sw + pid_cur;
-                atomicAdd(dst, t);
-            }
+            float* dst = slot < 3 ? v_colors + 3 * pid_cur + slot
+                       : slot == 3 ? v_opac + pid_cur
+                       : slot == 4 ? v_is2 + pid_cur
+                                   : v_sw + pid_cur;
+            grad_push8(gbuf, adder && slot < (MODE == 1 ? 6 : 5), dst, t);
         }
         if (want_contrib) {
             const float cw[8] = {cv[0], cv[1], cv[2], cv[3], 0.0f, 0.0f, 0.0f, 0.0f};
             const float t = wave_reduce8(cw);
-            if (adder && slot < 3 && contrib_rgb) atomicAdd(contrib_rgb + 3 * pid_cur + slot, t);
-            if (adder && slot == 3 && isect_contrib) atomicAdd(isect_contrib + g, t);
+            float* dst = slot < 3 ? (contrib_rgb ? contrib_rgb + 3 * pid_cur + slot : nullptr)
+                                  : (isect_contrib ? isect_contrib + g : nullptr);
+            grad_push8(gbuf, adder && slot < 4, dst, t);
         }
         // Geometry: endpoint gradients ((1-t) g, t g) of each pixel's best
         // edge, folded into its segment's control points.
@@ -1210,10 +1250,11 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
                 for (int k = 0; k < 8; ++k) sv[k] += mine ? cp[p][k] : 0.0f;
             }
             const float t = wave_reduce8(sv);
-            if (adder) atomicAdd(v_cubics + 8 * (size_t)s + slot, t);
+            grad_push8(gbuf, adder, v_cubics + 8 * (size_t)s + slot, t);
         }
       }
     }
+    grad_flush(gbuf);
     if constexpr (COUNT) flush_counts(n, counts);
 }
 
