@@ -313,8 +313,18 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
                           const void* log_pool, const float* v_output,
                           float* v_cubics_px, float* v_colors, float* v_opacities,
                           float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
-                          float* curve_isect_contrib, const int32_t* tile_order,
-                          hipStream_t stream);
+                          float* curve_isect_contrib, int32_t nprim, float* prim_scratch,
+                          const int32_t* tile_order, hipStream_t stream);
+
+/* Floats of the prim_scratch buffer the backward entry points take for
+ * nprim primitives (mode 0 fill, 1 stroke).  With prim_scratch (zero on
+ * entry; the call leaves it zero), the per-primitive gradients (v_colors,
+ * v_opacities, v_inv_sigma2s, v_stroke_widths) are first summed into 8
+ * copies, one per XCD of the launch, then added into the caller's arrays:
+ * the atomic additions of the many tiles a large primitive covers no longer
+ * meet at one address.  NULL: direct atomic additions (nprim unused).  No
+ * reference counterpart; it changes no value beyond fp32 summation order. */
+size_t cs_raster_prim_scratch_elems(int32_t nprim, int32_t mode);
 
 /* cs_rasterize_backward for records from cs_bin_prepare_de_casteljau
  * (the reference's flatten_method="de_casteljau" backward: the raster kernel
@@ -333,7 +343,8 @@ int cs_rasterize_backward_de_casteljau(int32_t mode, const int32_t* prim_ids_sor
                                        float* v_cubics_px, float* v_colors,
                                        float* v_opacities, float* v_inv_sigma2s,
                                        float* v_stroke_widths, float* curve_contrib_rgb,
-                                       float* curve_isect_contrib, const int32_t* tile_order,
+                                       float* curve_isect_contrib, int32_t nprim,
+                                       float* prim_scratch, const int32_t* tile_order,
                                        hipStream_t stream);
 
 /* cs_rasterize_forward / cs_rasterize_backward with the same results, plus
@@ -368,7 +379,8 @@ int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                   float* v_cubics_px, float* v_colors,
                                   float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
                                   float* curve_contrib_rgb, float* curve_isect_contrib,
-                                  unsigned long long* eval_counts, const int32_t* tile_order,
+                                  unsigned long long* eval_counts, int32_t nprim,
+                                  float* prim_scratch, const int32_t* tile_order,
                                   hipStream_t stream);
 
 /* _accumulate_edge_grads_to_cubics_kernel (ops/cubic_splatting.py:2308-2396)

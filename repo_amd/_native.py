@@ -54,13 +54,14 @@ _SIGNATURES = {
                                             _P]),
     "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                              _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                             _P, _P]),
+                                             _I32, _P, _P, _P]),
+    "cs_raster_prim_scratch_elems": (_SZ, [_I32, _I32]),
     "cs_rasterize_forward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                                     _I32, _I32, _P, _P, _P, _I64, _P, _P, _I64,
                                                     _I32, _P, _P, _P, _P]),
     "cs_rasterize_backward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
                                                      _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P,
-                                                     _P, _P, _P, _P, _P, _P, _P, _P]),
+                                                     _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
     "cs_raster_tile_order": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
     "cs_raster_records_from_edges": (ctypes.c_int, [_I32, _P, _I32, _P, _P, _I64, _P, _P, _P, _P,
                                                     _P, _I32, _P, _I32, _P, _P, _P, _P, _P, _P,
@@ -80,7 +81,8 @@ _SIGNATURES = {
     "cs_cubic_split_half": (ctypes.c_int, [_P, _I32, _P, _P, _P]),
     "cs_rasterize_backward_de_casteljau": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
                                                           _I32, _I32, _P, _P, _P, _P, _P, _P, _P,
-                                                          _P, _P, _P, _P, _P, _P, _P, _P]),
+                                                          _P, _P, _P, _P, _P, _P, _I32, _P, _P,
+                                                          _P]),
     "cs_accumulate_edge_grads_csr": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
                                                     _P]),
     "cs_backward_finalize": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P]),

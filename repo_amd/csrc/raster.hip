@@ -896,6 +896,34 @@ struct GradRec {
 };
 constexpr uint32_t kGradBufRecs = 256;   // 4 KiB of LDS per wave
 
+// Per-primitive gradients (colour, opacity, inverse variance, stroke width)
+// go, when the caller gives a scratch buffer, to one of kGradReplicas copies
+// chosen by the workgroup's XCD (workgroup b runs on XCD b mod 8): a large
+// primitive covers thousands of tiles, and their atomic additions to the same
+// few addresses serialize; spread over the XCDs they do not.  A second launch
+// adds the copies into the caller's arrays and clears them.
+constexpr int kGradReplicas = 8;
+
+template <int NV>
+__global__ __launch_bounds__(256) void k_prim_rep_reduce(float* __restrict__ rep, int nprim,
+                                                        float* __restrict__ v_col,
+                                                        float* __restrict__ v_op,
+                                                        float* __restrict__ v_is2,
+                                                        float* __restrict__ v_sw) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)nprim * NV) return;
+    const int p = (int)(i / NV), v = (int)(i - (int64_t)p * NV);
+    float sum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kGradReplicas; ++r) {
+        float* q = rep + (int64_t)r * nprim * NV + i;
+        sum += *q;
+        *q = 0.0f;
+    }
+    float* dst = v < 3 ? v_col + 3 * p + v : v == 3 ? v_op + p : v == 4 ? v_is2 + p : v_sw + p;
+    *dst += sum;
+}
+
 struct GradBuf {
     GradRec* rec;
     uint32_t n;   // wave-uniform
@@ -946,7 +974,8 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
-    float* __restrict__ isect_contrib, unsigned long long* __restrict__ counts) {
+    float* __restrict__ isect_contrib, float* __restrict__ prim_rep, int nprim,
+    unsigned long long* __restrict__ counts) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const SubBlock sb = sub_block(tg, tile_order, wv);
@@ -1181,12 +1210,15 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
         // Per-primitive gradients: one 8-way transposed reduction; lanes 8..15
         // then hold the totals and each adds one of them.
         {
+            constexpr int NV = MODE == 1 ? 6 : 5;
             const float t = wave_reduce8(pv);
-            float* dst = slot < 3 ? v_colors + 3 * pid_cur + slot
+            float* dst = prim_rep ? prim_rep + ((int64_t)(blockIdx.x % kGradReplicas) * nprim +
+                                                pid_cur) * NV + slot
+                       : slot < 3 ? v_colors + 3 * pid_cur + slot
                        : slot == 3 ? v_opac + pid_cur
                        : slot == 4 ? v_is2 + pid_cur
                                    : v_sw + pid_cur;
-            grad_push8(gbuf, adder && slot < (MODE == 1 ? 6 : 5), dst, t);
+            grad_push8(gbuf, adder && slot < NV, dst, t);
         }
         if (want_contrib) {
             const float cw[8] = {cv[0], cv[1], cv[2], cv[3], 0.0f, 0.0f, 0.0f, 0.0f};
@@ -1489,6 +1521,8 @@ struct RasterArgs {
     const float* v_out;
     const EdgeAux* aux;  // adaptive flattening (eps == 0)
     float *v_cub, *v_col, *v_op, *v_is2, *v_sw, *c_rgb, *c_isect;
+    float* prim_rep;  // per-primitive gradient copies (NULL: direct atomics)
+    int nprim;
     // evaluation counters of the counting entry points
     unsigned long long* counts;
     // heavy-first tile order (NULL: XCD order) and per-wave costs out (NULL: none)
@@ -1516,7 +1550,14 @@ static void launch_bwd3(const RasterArgs& a) {
                        a.log_pool, a.fT, a.fidx,
                        a.v_out,
                        a.v_cub, a.v_col,
-                       a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.counts);
+                       a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.prim_rep, a.nprim,
+                       a.counts);
+    if (a.prim_rep) {
+        constexpr int NV = MODE == 1 ? 6 : 5;
+        const int64_t n = (int64_t)a.nprim * NV;
+        hipLaunchKernelGGL(k_prim_rep_reduce<NV>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                           a.stream, a.prim_rep, a.nprim, a.v_col, a.v_op, a.v_is2, a.v_sw);
+    }
 }
 
 template <int MODE, bool COUNT>
@@ -1668,10 +1709,13 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               float* curve_contrib_rgb, float* curve_isect_contrib,
                               const void* edge_aux, const int32_t* log_index,
                               const void* log_pool, unsigned long long* eval_counts,
+                              int32_t nprim, float* prim_scratch,
                               const int32_t* tile_order, hipStream_t stream) {
     TileGrid tg;
     if ((mode != 0 && mode != 1) || (edge_aux == nullptr && edges_per_segment < 1) ||
         !tile_grid(img_h, img_w, block_x, block_y, tg))
+        return CS_ERR_ARGS;
+    if (prim_scratch && (nprim <= 0 || !v_colors || !v_opacities || !v_inv_sigma2s))
         return CS_ERR_ARGS;
     if (mode == 1 && v_stroke_widths == nullptr) return CS_ERR_ARGS;
     if (log_index && !log_pool) return CS_ERR_ARGS;
@@ -1693,9 +1737,16 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
     a.log_pool = log_index ? reinterpret_cast<uint4*>(const_cast<void*>(log_pool)) : nullptr;
     a.counts = eval_counts;
     a.order = tile_order;
+    a.prim_rep = prim_scratch;
+    a.nprim = prim_scratch ? nprim : 0;
     if (eval_counts) launch_bwd_mode<true>(a);
     else launch_bwd_mode<false>(a);
     return raster_status();
+}
+
+extern "C" size_t cs_raster_prim_scratch_elems(int32_t nprim, int32_t mode) {
+    if (nprim <= 0 || (mode != 0 && mode != 1)) return 0;
+    return (size_t)kGradReplicas * (size_t)nprim * (mode == 1 ? 6u : 5u);
 }
 
 extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
@@ -1709,14 +1760,14 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                                      float* v_cubics_px, float* v_colors, float* v_opacities,
                                      float* v_inv_sigma2s, float* v_stroke_widths,
                                      float* curve_contrib_rgb, float* curve_isect_contrib,
-                                     const int32_t* tile_order,
-                                     hipStream_t stream) {
+                                     int32_t nprim, float* prim_scratch,
+                                     const int32_t* tile_order, hipStream_t stream) {
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, block_x, block_y, edges_per_segment,
                               final_Ts, final_idx, v_output, v_cubics_px, v_colors, v_opacities,
                               v_inv_sigma2s, v_stroke_widths, curve_contrib_rgb,
-                              curve_isect_contrib, nullptr, log_index, log_pool, nullptr,
-                              tile_order, stream);
+                              curve_isect_contrib, nullptr, log_index, log_pool, nullptr, nprim,
+                              prim_scratch, tile_order, stream);
 }
 
 extern "C" int cs_rasterize_backward_de_casteljau(
@@ -1726,15 +1777,15 @@ extern "C" int cs_rasterize_backward_de_casteljau(
     const float* final_Ts, const int32_t* final_idx,
     const int32_t* log_index, const void* log_pool, const float* v_output, float* v_cubics_px,
     float* v_colors, float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
-    float* curve_contrib_rgb, float* curve_isect_contrib, const int32_t* tile_order,
-    hipStream_t stream) {
+    float* curve_contrib_rgb, float* curve_isect_contrib, int32_t nprim, float* prim_scratch,
+    const int32_t* tile_order, hipStream_t stream) {
     if (!edge_aux) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, block_x, block_y, 0, final_Ts,
                               final_idx, v_output,
                               v_cubics_px, v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
                               curve_contrib_rgb, curve_isect_contrib, edge_aux, log_index,
-                              log_pool, nullptr, tile_order, stream);
+                              log_pool, nullptr, nprim, prim_scratch, tile_order, stream);
 }
 
 extern "C" int cs_rasterize_backward_counted(
@@ -1745,14 +1796,15 @@ extern "C" int cs_rasterize_backward_counted(
     const int32_t* log_index, const void* log_pool, const float* v_output, float* v_cubics_px,
     float* v_colors, float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
     float* curve_contrib_rgb, float* curve_isect_contrib, unsigned long long* eval_counts,
-    const int32_t* tile_order, hipStream_t stream) {
+    int32_t nprim, float* prim_scratch, const int32_t* tile_order, hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, block_x, block_y, edges_per_segment,
                               final_Ts, final_idx,
                               v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
-                              log_index, log_pool, eval_counts, tile_order, stream);
+                              log_index, log_pool, eval_counts, nprim, prim_scratch, tile_order,
+                              stream);
 }
 
 extern "C" int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,

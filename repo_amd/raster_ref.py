@@ -238,8 +238,9 @@ def rasterize_cubic_fill_backward_tilelang(tile_bounds, block, img_size, primiti
         else torch.zeros((num_segments, 4, 2), dtype=torch.float32, device=dev)
     common = (0, N.ptr(ids), N.ptr(bins), N.ptr(edges), N.ptr(culls), N.ptr(prims), N.ptr(bg),
               H, W, bx, by)
+    # No scratch copies here: direct atomic additions (nprim is then unused).
     grads = (N.ptr(v_px), N.ptr(v_colors), N.ptr(v_opacities), N.ptr(v_inv_sigma2s), None,
-             N.ptr(contrib), N.ptr(isect_contrib), None, N.stream(dev))
+             N.ptr(contrib), N.ptr(isect_contrib), 0, None, None, N.stream(dev))
     fT, fi, vo = _f32(final_Ts), _i32(final_idx), _f32(v_output)
     if method == "bernstein":
         eps = max(2, int(distance_samples)) - 1

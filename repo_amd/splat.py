@@ -370,8 +370,16 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     return b
 
 
+# Copies of the per-primitive gradients the backward sums into before adding
+# them to v_colors etc. (cs_raster_prim_scratch_elems: 8 copies).
+PRIM_GRAD_COPIES = 8
+
+
 def _grad_accum_elems(nseg: int, nprim: int, mode: int) -> int:
-    return nseg * 8 + nprim * (6 if mode == MODE_STROKE else 5)
+    """The backward's accumulators (v_cubics_px, then the per-primitive
+    gradients) followed by its per-primitive scratch copies, all zero."""
+    nv = 6 if mode == MODE_STROKE else 5
+    return nseg * 8 + nprim * nv * (1 + PRIM_GRAD_COPIES)
 
 
 def _read_count(pending: "_PendingCount", nseg: int) -> int:
@@ -597,6 +605,8 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_opac = rest[3 * P: 4 * P]
     v_is2 = rest[4 * P: 5 * P]
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
+    nv = 6 if b.mode == MODE_STROKE else 5
+    prim_scratch = N.ptr(rest[nv * P:])
     log_index, log_pool = N.ptr(b.log_index), N.ptr(b.log_pool)
     if b.adaptive:
         if eval_counts is not None:
@@ -609,7 +619,8 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
                    N.ptr(final_idx), log_index, log_pool, N.ptr(v_output), N.ptr(v_px),
                    N.ptr(v_colors),
                    N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
-                   N.ptr(curve_isect_contrib), N.ptr(b.tile_order), N.stream(dev))
+                   N.ptr(curve_isect_contrib), P, prim_scratch, N.ptr(b.tile_order),
+                   N.stream(dev))
         return v_px, v_colors, v_opac, v_is2, v_sw
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
@@ -620,10 +631,11 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
             N.ptr(curve_isect_contrib))
     if eval_counts is not None:
         N.call("cs_rasterize_backward_counted", *args, N.ptr(_counts_buffer(eval_counts)),
-               N.ptr(b.tile_order), N.stream(dev))
+               P, prim_scratch, N.ptr(b.tile_order), N.stream(dev))
     else:
         with N.prof("cubic.bwd.rast"):
-            N.call("cs_rasterize_backward", *args, N.ptr(b.tile_order), N.stream(dev))
+            N.call("cs_rasterize_backward", *args, P, prim_scratch, N.ptr(b.tile_order),
+                   N.stream(dev))
     return v_px, v_colors, v_opac, v_is2, v_sw
 
 
