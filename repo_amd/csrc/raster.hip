@@ -304,9 +304,13 @@ struct Cov {
 // stroke) beyond the smaller outside bound its alpha is below 1/255, which
 // cov = 0 reproduces.  The exact branch only runs when some lane of the wave
 // needs it.
+// Winding-number mask of the fill rule: inside when (winding & mask) != 0
+// (1: even-odd, all bits: nonzero).
+__device__ __forceinline__ int rule_mask(const PrimRec& pr) { return pr.rule == 0 ? 1 : -1; }
+
 template <int MODE>
 __device__ __forceinline__ bool inside_of(const PrimRec& pr, const Geom& G) {
-    return MODE == 0 && (pr.rule == 0 ? ((G.winding & 1) != 0) : (G.winding != 0));
+    return MODE == 0 && (G.winding & rule_mask(pr)) != 0;
 }
 
 // Squared distance beyond which the lane's coverage is decided in closed form:
@@ -565,6 +569,25 @@ __device__ __forceinline__ uint32_t pack_d2_inside(float d2, bool inside) {
     return (__builtin_bit_cast(uint32_t, d2) & 0x7fffffffu) | ((uint32_t)inside << 31);
 }
 
+// Front-to-back compositing of one entry at one pixel
+// (cubic_splatting.py:1171-1183): unless the pixel has stopped, an alpha of at
+// least 1/255 blends the colour at weight alpha T and multiplies T by
+// 1 - alpha; the pixel stops once T reaches the transmittance stop.  Written
+// with selects, so the lanes that skip the entry need no branch.
+__device__ __forceinline__ void composite(const PrimRec& pr, float alpha, int g, float& T,
+                                          float& C0, float& C1, float& C2, int& cur,
+                                          bool& done) {
+    const bool take = !done && alpha >= kAlphaMin;
+    const float vis = alpha * T;
+    const float nT = T * (1.0f - alpha);
+    C0 = take ? __builtin_fmaf(pr.r, vis, C0) : C0;
+    C1 = take ? __builtin_fmaf(pr.g, vis, C1) : C1;
+    C2 = take ? __builtin_fmaf(pr.b, vis, C2) : C2;
+    T = take ? nT : T;
+    cur = take ? g : cur;
+    done = done || (take && nT <= kTStop);
+}
+
 // Forward raster.  Each wave walks its tile's list in chunks of 64 entries:
 // lane k tests entry k of the chunk against the wave's pixel rectangle
 // (prim_culled_lane), and the wave then processes only the entries that can
@@ -667,7 +690,7 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
                 // winding number says inside, coverage 1 at every pixel.
                 bool inside_all = false;
                 if constexpr (MODE == 0) {
-                    inside_all = pr.rule == 0 ? ((wnd & 1) != 0) : (wnd != 0);
+                    inside_all = (wnd & rule_mask(pr)) != 0;
                     if constexpr (COUNT) n.row += (uint64_t)(pr.e1 - pr.e0);
                 }
                 if (log_index) {
@@ -676,20 +699,9 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
                 }
                 if (inside_all) {
                     const float alpha = fminf(kAlphaCap, pr.opacity * 1.0f);
-                    if (alpha >= kAlphaMin) {
 #pragma unroll
-                        for (int p = 0; p < kPix; ++p) {
-                            if (done[p]) continue;
-                            const float nT = T[p] * (1.0f - alpha);
-                            const float vis = alpha * T[p];
-                            C0[p] = __builtin_fmaf(pr.r, vis, C0[p]);
-                            C1[p] = __builtin_fmaf(pr.g, vis, C1[p]);
-                            C2[p] = __builtin_fmaf(pr.b, vis, C2[p]);
-                            T[p] = nT;
-                            cur[p] = g;
-                            if (nT <= kTStop) done[p] = true;
-                        }
-                    }
+                    for (int p = 0; p < kPix; ++p)
+                        composite(pr, alpha, g, T[p], C0[p], C1[p], C2[p], cur[p], done[p]);
                 }
                 continue;
             }
@@ -785,20 +797,9 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
                 logged |= 1ull << k;
             }
 #pragma unroll
-            for (int p = 0; p < kPix; ++p) {
-                if (done[p]) continue;
-                const float alpha = fminf(kAlphaCap, pr.opacity * cov[p]);
-                if (alpha >= kAlphaMin) {
-                    const float nT = T[p] * (1.0f - alpha);
-                    const float vis = alpha * T[p];
-                    C0[p] = __builtin_fmaf(pr.r, vis, C0[p]);
-                    C1[p] = __builtin_fmaf(pr.g, vis, C1[p]);
-                    C2[p] = __builtin_fmaf(pr.b, vis, C2[p]);
-                    T[p] = nT;
-                    cur[p] = g;
-                    if (nT <= kTStop) done[p] = true;
-                }
-            }
+            for (int p = 0; p < kPix; ++p)
+                composite(pr, fminf(kAlphaCap, pr.opacity * cov[p]), g, T[p], C0[p], C1[p],
+                          C2[p], cur[p], done[p]);
         }
         if ((logged >> lane) & 1u) log_index[(size_t)tg.waves * gl + sb.slot] = idx_l;
     }
