@@ -48,6 +48,12 @@ def test_library_loads_and_exports_every_symbol():
     assert lib.cs_scan_temp_elems(0) >= 0
     assert lib.cs_radix_counts_elems(1 << 20) > 0
     assert lib.cs_mse_partials_elems(1 << 20) > 0
+    # Per-XCD copies of the per-primitive gradients: 8 copies of 5 (fill) or
+    # 6 (stroke) floats per primitive; 0 for invalid arguments.
+    assert lib.cs_raster_prim_scratch_elems(4096, 0) == 8 * 4096 * 5
+    assert lib.cs_raster_prim_scratch_elems(3, 1) == 8 * 3 * 6
+    assert lib.cs_raster_prim_scratch_elems(0, 0) == 0
+    assert lib.cs_raster_prim_scratch_elems(5, 2) == 0
 
 
 def test_record_sizes_match_header():

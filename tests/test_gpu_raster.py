@@ -529,3 +529,44 @@ def test_render_without_gradients_writes_no_log():
     print(f"[no-grad log] peak {p_no} vs {p_yes} bytes (I={I})", flush=True)
     assert p_yes - p_no >= 2 * I * 4
     assert torch.equal(img_no, img_yes.detach())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("stroke", [False, True])
+def test_prim_gradient_copies_left_zero_and_equal_direct_atomics(stroke):
+    """The backward's per-XCD copies of the per-primitive gradients
+    (prim_scratch) are zero again after the call, and the gradients equal
+    those of plain atomic additions (prim_scratch NULL) up to fp32 summation
+    order."""
+    from repo_amd import _native as N
+    sc = synth.make_scene(4, scale=0.25) if stroke else synth.make_scene(2)
+    print(f"[prim copies] stroke={stroke}", flush=True)
+    b, s = hip_bin(sc)
+    bg = s.background.float().contiguous()
+    out, T, idx = splat.rasterize_forward(b, bg)
+    v = random_v_out(sc.img_h, sc.img_w, seed=5).to("cuda")
+    grads = splat.rasterize_backward(b, bg, T, idx, v)
+    P = b.nprim
+    nv = 6 if stroke else 5
+    rest = b.grad_accum[b.nseg * 8:]
+    assert int(torch.count_nonzero(rest[nv * P:]).item()) == 0
+    # The same backward with plain atomics.
+    z = torch.zeros_like(b.grad_accum)
+    v_px = z[: b.nseg * 8]
+    r = z[b.nseg * 8:]
+    N.call("cs_rasterize_backward", b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"),
+           b.ptr("edges"), b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(bg), b.img_h, b.img_w,
+           b.block_x, b.block_y, b.edges_per_segment, N.ptr(T), N.ptr(idx), N.ptr(b.log_index),
+           N.ptr(b.log_pool), N.ptr(v), N.ptr(v_px), N.ptr(r), r.data_ptr() + 12 * P,
+           r.data_ptr() + 16 * P, r.data_ptr() + 20 * P if stroke else None, None, None, 0,
+           None, N.ptr(b.tile_order), N.stream(v.device))
+    torch.cuda.synchronize()
+    direct = [r[: 3 * P].view(P, 3), r[3 * P: 4 * P], r[4 * P: 5 * P]] + (
+        [r[5 * P: 6 * P]] if stroke else [])
+    copied = [grads[1], grads[2], grads[3]] + ([grads[4]] if stroke else [])
+    for got, ref in zip(copied, direct):
+        ok, rel = grad_scale_tol(got.cpu().numpy(), ref.cpu().numpy(), rtol=1e-5)
+        assert ok, f"max error {rel:.3e} of max|ref|"
+    ok, rel = grad_scale_tol(grads[0].cpu().numpy(), v_px.view(b.nseg, 4, 2).cpu().numpy(),
+                             rtol=1e-5)
+    assert ok, f"v_cubics_px: max error {rel:.3e} of max|ref|"
