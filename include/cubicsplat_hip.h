@@ -303,7 +303,10 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
  * fused with _accumulate_edge_grads_to_cubics (ops/cubic_splatting.py:2308-2396):
  * accumulates (atomically) into zero-initialised v_cubics_px [nseg,4,2],
  * v_colors [P,3], v_opacities [P], v_inv_sigma2s [P], v_stroke_widths [P]
- * (mode 1), and optionally curve_contrib_rgb [P,3] / curve_isect_contrib [I]. */
+ * (mode 1), and optionally curve_contrib_rgb [P,3] / curve_isect_contrib [I].
+ * v_output is the gradient of out_img: [H, W, 3] interleaved, or, when
+ * v_output_planar != 0, three [H, W] planes (channel c at v_output + c H W;
+ * the layout cs_clamp_mse_ssim_backward writes with grad_planar). */
 int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
                           const void* edges, const void* edge_culls, const void* prim_recs,
                           const float* background, int32_t img_h, int32_t img_w,
@@ -311,6 +314,7 @@ int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted, const in
                           int32_t edges_per_segment, const float* final_Ts,
                           const int32_t* final_idx, const int32_t* log_index,
                           const void* log_pool, const float* v_output,
+                          int32_t v_output_planar,
                           float* v_cubics_px, float* v_colors, float* v_opacities,
                           float* v_inv_sigma2s, float* v_stroke_widths, float* curve_contrib_rgb,
                           float* curve_isect_contrib, int32_t nprim, float* prim_scratch,
@@ -340,6 +344,7 @@ int cs_rasterize_backward_de_casteljau(int32_t mode, const int32_t* prim_ids_sor
                                        const void* edge_aux, const float* final_Ts,
                                        const int32_t* final_idx, const int32_t* log_index,
                                        const void* log_pool, const float* v_output,
+                                       int32_t v_output_planar,
                                        float* v_cubics_px, float* v_colors,
                                        float* v_opacities, float* v_inv_sigma2s,
                                        float* v_stroke_widths, float* curve_contrib_rgb,
@@ -376,6 +381,7 @@ int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                   int32_t edges_per_segment, const float* final_Ts,
                                   const int32_t* final_idx, const int32_t* log_index,
                                   const void* log_pool, const float* v_output,
+                                  int32_t v_output_planar,
                                   float* v_cubics_px, float* v_colors,
                                   float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
                                   float* curve_contrib_rgb, float* curve_isect_contrib,
@@ -527,9 +533,11 @@ int cs_mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, 
  * clamp(0, 1).permute(2, 0, 1) glue (gaussian_trace/render.py:1309-1310)
  * folded in: the forward writes x = clamp(img, lo, hi) as [3, h, w] into the
  * caller's buffer x and computes the loss on it; the backward reads img
- * itself and writes grad_img [h, w, 3] directly, zero where img lies outside
- * [lo, hi] (no gradient pass through the glue).  y is the [3, h, w] target;
- * partials / abc as for cs_mse_ssim_loss with nc = 3. */
+ * itself and writes grad_img directly, zero where img lies outside [lo, hi]
+ * (no gradient pass through the glue): [h, w, 3], or, with grad_planar != 0,
+ * three [h, w] planes (whole-line writes; cs_rasterize_backward reads that
+ * layout with v_output_planar).  y is the [3, h, w] target; partials / abc as
+ * for cs_mse_ssim_loss with nc = 3. */
 int cs_clamp_mse_ssim_loss(const float* img, const float* y, int32_t h, int32_t w, float lo,
                            float hi, const float* win1d, int32_t win, float c1, float c2,
                            float ssim_weight, float* x, float* partials, float* out, float* abc,
@@ -537,7 +545,7 @@ int cs_clamp_mse_ssim_loss(const float* img, const float* y, int32_t h, int32_t 
 int cs_clamp_mse_ssim_backward(const float* img, const float* y, int32_t h, int32_t w, float lo,
                                float hi, const float* win1d, int32_t win, const float* abc,
                                float ssim_weight, const float* grad_loss, float* grad_img,
-                               hipStream_t stream);
+                               int32_t grad_planar, hipStream_t stream);
 
 /* ---------------- optimizer ---------------- */
 

@@ -53,15 +53,16 @@ _SIGNATURES = {
                                             _I32, _P, _P, _P, _I64, _P, _P, _I64, _I32, _P, _P,
                                             _P]),
     "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
-                                             _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                             _I32, _P, _P, _P]),
+                                             _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P,
+                                             _P, _P, _I32, _P, _P, _P]),
     "cs_raster_prim_scratch_elems": (_SZ, [_I32, _I32]),
     "cs_rasterize_forward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                                     _I32, _I32, _P, _P, _P, _I64, _P, _P, _I64,
                                                     _I32, _P, _P, _P, _P]),
     "cs_rasterize_backward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
-                                                     _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P,
-                                                     _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
+                                                     _I32, _I32, _I32, _P, _P, _P, _P, _P, _I32,
+                                                     _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P,
+                                                     _P]),
     "cs_raster_tile_order": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
     "cs_raster_records_from_edges": (ctypes.c_int, [_I32, _P, _I32, _P, _P, _I64, _P, _P, _P, _P,
                                                     _P, _I32, _P, _I32, _P, _P, _P, _P, _P, _P,
@@ -80,9 +81,9 @@ _SIGNATURES = {
     "cs_cubic_flatness_flags": (ctypes.c_int, [_P, _I32, _F, _I32, _P, _P]),
     "cs_cubic_split_half": (ctypes.c_int, [_P, _I32, _P, _P, _P]),
     "cs_rasterize_backward_de_casteljau": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
-                                                          _I32, _I32, _P, _P, _P, _P, _P, _P, _P,
-                                                          _P, _P, _P, _P, _P, _P, _I32, _P, _P,
-                                                          _P]),
+                                                          _I32, _I32, _P, _P, _P, _P, _P, _P,
+                                                          _I32, _P, _P, _P, _P, _P, _P, _P,
+                                                          _I32, _P, _P, _P]),
     "cs_accumulate_edge_grads_csr": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
                                                     _P]),
     "cs_backward_finalize": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P]),
@@ -114,7 +115,7 @@ _SIGNATURES = {
     "cs_clamp_mse_ssim_loss": (ctypes.c_int, [_P, _P, _I32, _I32, _F, _F, _P, _I32, _F, _F, _F,
                                               _P, _P, _P, _P, _P]),
     "cs_clamp_mse_ssim_backward": (ctypes.c_int, [_P, _P, _I32, _I32, _F, _F, _P, _I32, _P, _F,
-                                                  _P, _P, _P]),
+                                                  _P, _P, _I32, _P]),
     "cs_adam_step": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _D, _D, _D, _P]),
     "cs_adan_step": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_gs_project_forward": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,

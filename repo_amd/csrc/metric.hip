@@ -405,8 +405,9 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
 // three maps, blocked like the forward (horizontal strips read the maps from
 // global memory, vertical strips from LDS).
 // HWC: x is the [h, w, 3] image the forward read as clamp(x, lo, hi) and gx
-// the [h, w, 3] gradient with respect to it: zero where x lies outside
-// [lo, hi] (the clamp's gradient as torch defines it).
+// the gradient with respect to it, zero where x lies outside [lo, hi] (the
+// clamp's gradient as torch defines it): [h, w, 3], or, with gx_planar, three
+// [h, w] planes (each channel tile then writes whole lines).
 template <int WIN, bool HWC>
 __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
                                                  const float* __restrict__ y, int h, int w,
@@ -415,7 +416,7 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
                                                  const float* __restrict__ abc,
                                                  const float* __restrict__ grad_out, int go_per_map,
                                                  float ssim_coef, float mse_coef, int nc, float lo,
-                                                 float hi, float* __restrict__ gx) {
+                                                 float hi, int gx_planar, float* __restrict__ gx) {
     using TT = SsimTile<WIN>;
     constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
     __shared__ float hs[3][IT][HP];
@@ -487,8 +488,8 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
         const float xv = HWC ? fminf(fmaxf(xr, lo), hi) : xr, yv = yc[pi];
         float gv = scale * (gsum[0][o] + 2.0f * xv * gsum[1][o] + yv * gsum[2][o]);
         if (mse_coef != 0.0f) gv = __builtin_fmaf(mscale, xv - yv, gv);
-        if (HWC) gx[3 * pi + c] = ((xr >= lo) & (xr <= hi)) ? gv : 0.0f;
-        else gx[(size_t)c * h * w + pi] = gv;
+        if (HWC) gv = ((xr >= lo) & (xr <= hi)) ? gv : 0.0f;
+        gx[(HWC && !gx_planar) ? 3 * pi + c : (size_t)c * h * w + pi] = gv;
     }
 }
 
@@ -873,13 +874,13 @@ static int launch_ssim_bwd(const float* x, const float* y, int32_t nc, int32_t h
                            const float* win1d, int32_t win, const float* abc,
                            const float* grad_out, int go_per_map, float ssim_coef,
                            float mse_coef, float* grad_x, hipStream_t stream, float lo = 0.0f,
-                           float hi = 1.0f) {
+                           float hi = 1.0f, int gx_planar = 0) {
     const int oh = h - win + 1, ow = w - win + 1;
     const dim3 grid(((w + kSsimTW - 1) / kSsimTW) * ((h + kSsimTH - 1) / kSsimTH) * nc);
 #define CS_SSIM_BWD(W_)                                                                        \
     hipLaunchKernelGGL((k_ssim_bwd<W_, HWC>), grid, dim3(256), 0, stream, x, y, h, w, oh, ow, \
                        win1d, abc, grad_out, go_per_map, ssim_coef, mse_coef, nc, lo, hi,     \
-                       grad_x)
+                       gx_planar, grad_x)
     switch (win) {
         CS_SSIM_DISPATCH(1, CS_SSIM_BWD)
         CS_SSIM_DISPATCH(3, CS_SSIM_BWD)
@@ -979,13 +980,14 @@ template <bool HWC>
 static int mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                              float lo, float hi, const float* win1d, int32_t win,
                              const float* abc, float ssim_weight, const float* grad_loss,
-                             float* grad_x, hipStream_t stream) {
+                             float* grad_x, hipStream_t stream, int gx_planar = 0) {
     if (!ssim_tiled_ok(nc, h, w, win)) return CS_ERR_ARGS;
     const int oh = h - win + 1, ow = w - win + 1;
     const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
     const float mse_coef = (float)(2.0 / ((double)nc * h * w));
     const int rc = launch_ssim_bwd<HWC>(x, y, nc, h, w, win1d, win, abc, grad_loss, 0,
-                                        -ssim_weight * inv_cnt, mse_coef, grad_x, stream, lo, hi);
+                                        -ssim_weight * inv_cnt, mse_coef, grad_x, stream, lo, hi,
+                                        gx_planar);
     return rc ? rc : metric_status();
 }
 
@@ -1022,9 +1024,9 @@ extern "C" int cs_clamp_mse_ssim_backward(const float* img, const float* y, int3
                                           float lo, float hi, const float* win1d, int32_t win,
                                           const float* abc, float ssim_weight,
                                           const float* grad_loss, float* grad_img,
-                                          hipStream_t stream) {
+                                          int32_t grad_planar, hipStream_t stream) {
     return mse_ssim_backward<true>(img, y, 3, h, w, lo, hi, win1d, win, abc, ssim_weight,
-                                   grad_loss, grad_img, stream);
+                                   grad_loss, grad_img, stream, grad_planar ? 1 : 0);
 }
 
 extern "C" int cs_clamp_hwc_to_nchw(const float* img, int32_t h, int32_t w, float lo, float hi,

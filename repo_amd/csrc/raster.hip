@@ -972,7 +972,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     TileGrid tg, const int32_t* __restrict__ tile_order, int eps, uint32_t eps_magic,
     const EdgeAux* __restrict__ edge_aux, const int32_t* __restrict__ log_index_g,
     const uint4* __restrict__ log_pool, const float* __restrict__ final_T,
-    const int32_t* __restrict__ final_idx, const float* __restrict__ v_out,
+    const int32_t* __restrict__ final_idx, const float* __restrict__ v_out, int v_planar,
     float* __restrict__ v_cubics, float* __restrict__ v_colors, float* __restrict__ v_opac,
     float* __restrict__ v_is2, float* __restrict__ v_sw, float* __restrict__ contrib_rgb,
     float* __restrict__ isect_contrib, float* __restrict__ prim_rep, int nprim,
@@ -999,9 +999,12 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
         T[p] = in ? final_T[pix] : 1.0f;
         T_final[p] = T[p];
         fidx[p] = in ? final_idx[pix] : -1;
-        v0[p] = in ? v_out[3 * pix + 0] : 0.0f;
-        v1[p] = in ? v_out[3 * pix + 1] : 0.0f;
-        v2[p] = in ? v_out[3 * pix + 2] : 0.0f;
+        // v_out: [H, W, 3] interleaved, or (v_planar) three [H, W] planes.
+        const size_t hw = (size_t)img_h * img_w;
+        const size_t o0 = v_planar ? pix : 3 * pix, step = v_planar ? hw : 1;
+        v0[p] = in ? v_out[o0] : 0.0f;
+        v1[p] = in ? v_out[o0 + step] : 0.0f;
+        v2[p] = in ? v_out[o0 + 2 * step] : 0.0f;
         bg_dot[p] = __builtin_fmaf(bg2, v2[p], __builtin_fmaf(bg1, v1[p], bg0 * v0[p]));
         b0[p] = b1[p] = b2[p] = 0.0f;
         fmax = max(fmax, fidx[p]);
@@ -1520,6 +1523,7 @@ struct RasterArgs {
     const float* fT;
     const int32_t* fidx;
     const float* v_out;
+    int v_planar;        // v_out as three [H, W] planes instead of [H, W, 3]
     const EdgeAux* aux;  // adaptive flattening (eps == 0)
     float *v_cub, *v_col, *v_op, *v_is2, *v_sw, *c_rgb, *c_isect;
     float* prim_rep;  // per-primitive gradient copies (NULL: direct atomics)
@@ -1549,7 +1553,7 @@ static void launch_bwd3(const RasterArgs& a) {
                        dim3(kRasterThreads), 0, a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg,
                        a.img_h, a.img_w, a.tg, a.order, a.eps, magic, a.aux, a.log_index,
                        a.log_pool, a.fT, a.fidx,
-                       a.v_out,
+                       a.v_out, a.v_planar,
                        a.v_cub, a.v_col,
                        a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.prim_rep, a.nprim,
                        a.counts);
@@ -1705,6 +1709,7 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               int32_t block_x, int32_t block_y,
                               int32_t edges_per_segment, const float* final_Ts,
                               const int32_t* final_idx, const float* v_output,
+                              int32_t v_output_planar,
                               float* v_cubics_px, float* v_colors, float* v_opacities,
                               float* v_inv_sigma2s, float* v_stroke_widths,
                               float* curve_contrib_rgb, float* curve_isect_contrib,
@@ -1725,6 +1730,7 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
     a.fT = final_Ts;
     a.fidx = final_idx;
     a.v_out = v_output;
+    a.v_planar = v_output_planar ? 1 : 0;
     a.v_cub = v_cubics_px;
     a.v_col = v_colors;
     a.v_op = v_opacities;
@@ -1758,6 +1764,7 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                                      int32_t edges_per_segment, const float* final_Ts,
                                      const int32_t* final_idx, const int32_t* log_index,
                                      const void* log_pool, const float* v_output,
+                                     int32_t v_output_planar,
                                      float* v_cubics_px, float* v_colors, float* v_opacities,
                                      float* v_inv_sigma2s, float* v_stroke_widths,
                                      float* curve_contrib_rgb, float* curve_isect_contrib,
@@ -1765,7 +1772,8 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                                      const int32_t* tile_order, hipStream_t stream) {
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, block_x, block_y, edges_per_segment,
-                              final_Ts, final_idx, v_output, v_cubics_px, v_colors, v_opacities,
+                              final_Ts, final_idx, v_output, v_output_planar, v_cubics_px,
+                              v_colors, v_opacities,
                               v_inv_sigma2s, v_stroke_widths, curve_contrib_rgb,
                               curve_isect_contrib, nullptr, log_index, log_pool, nullptr, nprim,
                               prim_scratch, tile_order, stream);
@@ -1776,14 +1784,15 @@ extern "C" int cs_rasterize_backward_de_casteljau(
     const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
     int32_t img_w, int32_t block_x, int32_t block_y, const void* edge_aux,
     const float* final_Ts, const int32_t* final_idx,
-    const int32_t* log_index, const void* log_pool, const float* v_output, float* v_cubics_px,
+    const int32_t* log_index, const void* log_pool, const float* v_output,
+    int32_t v_output_planar, float* v_cubics_px,
     float* v_colors, float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
     float* curve_contrib_rgb, float* curve_isect_contrib, int32_t nprim, float* prim_scratch,
     const int32_t* tile_order, hipStream_t stream) {
     if (!edge_aux) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, block_x, block_y, 0, final_Ts,
-                              final_idx, v_output,
+                              final_idx, v_output, v_output_planar,
                               v_cubics_px, v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
                               curve_contrib_rgb, curve_isect_contrib, edge_aux, log_index,
                               log_pool, nullptr, nprim, prim_scratch, tile_order, stream);
@@ -1794,15 +1803,16 @@ extern "C" int cs_rasterize_backward_counted(
     const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
     int32_t img_w, int32_t block_x, int32_t block_y, int32_t edges_per_segment,
     const float* final_Ts, const int32_t* final_idx,
-    const int32_t* log_index, const void* log_pool, const float* v_output, float* v_cubics_px,
+    const int32_t* log_index, const void* log_pool, const float* v_output,
+    int32_t v_output_planar, float* v_cubics_px,
     float* v_colors, float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
     float* curve_contrib_rgb, float* curve_isect_contrib, unsigned long long* eval_counts,
     int32_t nprim, float* prim_scratch, const int32_t* tile_order, hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                               background, img_h, img_w, block_x, block_y, edges_per_segment,
-                              final_Ts, final_idx,
-                              v_output, v_cubics_px, v_colors, v_opacities, v_inv_sigma2s,
+                              final_Ts, final_idx, v_output, v_output_planar, v_cubics_px,
+                              v_colors, v_opacities, v_inv_sigma2s,
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
                               log_index, log_pool, eval_counts, nprim, prim_scratch, tile_order,
                               stream);

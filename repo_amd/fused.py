@@ -162,7 +162,10 @@ class _ClampMseSsimLoss(torch.autograd.Function):
             return (None,) * 9
         x, y = ctx.saved_tensors
         h, w = int(x.shape[0]), int(x.shape[1])
-        gi = torch.empty_like(x)
+        # The image gradient is written as three [H, W] planes (whole-line
+        # writes) and returned as an [H, W, 3] view of them; the renderer's
+        # backward reads that layout in place (splat.image_grad_layout).
+        planes = torch.empty((3, h, w), dtype=torch.float32, device=x.device)
         go = grad_loss
         if go.dtype is not torch.float32:
             go = go.to(torch.float32)
@@ -170,7 +173,8 @@ class _ClampMseSsimLoss(torch.autograd.Function):
         with N.prof("loss.clamp_mse_ssim_bwd"):
             N.call("cs_clamp_mse_ssim_backward", N.ptr(x), N.ptr(y), h, w, ctx.lo, ctx.hi,
                    N.ptr(ctx.g), ctx.win_size, abc_p, ctx.ssim_weight, go.data_ptr(),
-                   N.ptr(gi), N.stream(x.device))
+                   planes.data_ptr(), 1, N.stream(x.device))
+        gi = planes.permute(1, 2, 0)
         if ctx.x_dtype is not torch.float32:
             gi = gi.to(ctx.x_dtype)
         return gi, None, None, None, None, None, None, None, None

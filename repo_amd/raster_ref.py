@@ -247,7 +247,7 @@ def rasterize_cubic_fill_backward_tilelang(tile_bounds, block, img_size, primiti
         if E != num_segments * eps:
             raise ValueError(f"v_edges size mismatch: got {E}, expected {num_segments * eps}")
         N.call("cs_rasterize_backward", *common, eps, N.ptr(fT), N.ptr(fi), None, None,
-               N.ptr(vo), *grads)
+               N.ptr(vo), 0, *grads)
     else:
         if segment_edge_offsets is None or edge_t_starts is None or edge_t_ends is None:
             raise ValueError("de_casteljau flatten backward requires CSR metadata "
@@ -260,7 +260,7 @@ def rasterize_cubic_fill_backward_tilelang(tile_bounds, block, img_size, primiti
         N.call("cs_edge_aux_from_csr", N.ptr(seo), num_segments, N.ptr(_f32(edge_t_starts)),
                N.ptr(_f32(edge_t_ends)), E, N.ptr(aux), N.stream(dev))
         N.call("cs_rasterize_backward_de_casteljau", *common, N.ptr(aux), N.ptr(fT), N.ptr(fi),
-               None, None, N.ptr(vo), *grads)
+               None, None, N.ptr(vo), 0, *grads)
     if v_px is not v_cubics_px:
         v_cubics_px.copy_(v_px)
     # As in the reference, the contribution sums land in the caller's tensors

@@ -70,6 +70,22 @@ def _f32(t: torch.Tensor) -> torch.Tensor:
     return t.detach().to(torch.float32).contiguous()
 
 
+def image_grad_layout(v: torch.Tensor):
+    """(tensor, planar) for an upstream image gradient of shape [H, W, 3]:
+    the gradient itself when it is float32 and [H, W, 3]-contiguous
+    (planar 0), or, when it is an [H, W, 3] view of three contiguous [H, W]
+    planes (as the fused loss's backward returns it), its planes (planar 1);
+    otherwise a contiguous float32 copy."""
+    v = v.detach()
+    if v.dtype is torch.float32 and v.dim() == 3 and v.shape[2] == 3:
+        if v.is_contiguous():
+            return v, 0
+        h, w = int(v.shape[0]), int(v.shape[1])
+        if v.stride() == (w, 1, h * w):
+            return v.permute(2, 0, 1), 1
+    return v.to(torch.float32).contiguous(), 0
+
+
 def _i32(t: torch.Tensor) -> torch.Tensor:
     if t.dtype is torch.int32 and t.is_contiguous():
         return t.detach()
@@ -605,6 +621,7 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_opac = rest[3 * P: 4 * P]
     v_is2 = rest[4 * P: 5 * P]
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
+    v_output, planar = image_grad_layout(v_output)
     nv = 6 if b.mode == MODE_STROKE else 5
     prim_scratch = N.ptr(rest[nv * P:])
     log_index, log_pool = N.ptr(b.log_index), N.ptr(b.log_pool)
@@ -616,8 +633,8 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
                    b.ptr("tile_bins"), b.ptr("edges"), b.ptr("edge_culls"), b.ptr("prim_recs"),
                    N.ptr(background), b.img_h, b.img_w, b.block_x, b.block_y,
                    b.ptr("edge_aux"), N.ptr(final_T),
-                   N.ptr(final_idx), log_index, log_pool, N.ptr(v_output), N.ptr(v_px),
-                   N.ptr(v_colors),
+                   N.ptr(final_idx), log_index, log_pool, N.ptr(v_output), planar,
+                   N.ptr(v_px), N.ptr(v_colors),
                    N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
                    N.ptr(curve_isect_contrib), P, prim_scratch, N.ptr(b.tile_order),
                    N.stream(dev))
@@ -626,7 +643,7 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), b.img_h, b.img_w,
             b.block_x, b.block_y, b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx),
             log_index, log_pool,
-            N.ptr(v_output), N.ptr(v_px),
+            N.ptr(v_output), planar, N.ptr(v_px),
             N.ptr(v_colors), N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb),
             N.ptr(curve_isect_contrib))
     if eval_counts is not None:
@@ -807,9 +824,10 @@ def _splat_backward(ctx, grad_out_img):
         if bool(pre.get("collect_curve_isect_contrib", False)):
             curve_isect_contrib = torch.zeros((b.num_intersects,), dtype=torch.float32,
                                               device=colors.device)
-    v_output = _f32(grad_out_img)
+    # rasterize_backward takes the gradient in either layout (no copy of a
+    # planar one).
     v_cubics_px, v_colors, v_opac, v_is2, v_sw = rasterize_backward(
-        b, bg, final_T, final_idx, v_output, curve_contrib_rgb=curve_contrib_rgb,
+        b, bg, final_T, final_idx, grad_out_img, curve_contrib_rgb=curve_contrib_rgb,
         curve_isect_contrib=curve_isect_contrib)
     if process_fn is not None:
         payload = {

@@ -557,7 +557,7 @@ def test_prim_gradient_copies_left_zero_and_equal_direct_atomics(stroke):
     N.call("cs_rasterize_backward", b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"),
            b.ptr("edges"), b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(bg), b.img_h, b.img_w,
            b.block_x, b.block_y, b.edges_per_segment, N.ptr(T), N.ptr(idx), N.ptr(b.log_index),
-           N.ptr(b.log_pool), N.ptr(v), N.ptr(v_px), N.ptr(r), r.data_ptr() + 12 * P,
+           N.ptr(b.log_pool), N.ptr(v), 0, N.ptr(v_px), N.ptr(r), r.data_ptr() + 12 * P,
            r.data_ptr() + 16 * P, r.data_ptr() + 20 * P if stroke else None, None, None, 0,
            None, N.ptr(b.tile_order), N.stream(v.device))
     torch.cuda.synchronize()
