@@ -386,16 +386,12 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     return b
 
 
-# Copies of the per-primitive gradients the backward sums into before adding
-# them to v_colors etc. (cs_raster_prim_scratch_elems: 8 copies).
-PRIM_GRAD_COPIES = 8
-
-
 def _grad_accum_elems(nseg: int, nprim: int, mode: int) -> int:
     """The backward's accumulators (v_cubics_px, then the per-primitive
-    gradients) followed by its per-primitive scratch copies, all zero."""
+    gradients) followed by the copies the backward sums the per-primitive
+    gradients into (cs_raster_prim_scratch_elems), all zero."""
     nv = 6 if mode == MODE_STROKE else 5
-    return nseg * 8 + nprim * nv * (1 + PRIM_GRAD_COPIES)
+    return nseg * 8 + nprim * nv + int(N.lib().cs_raster_prim_scratch_elems(nprim, mode))
 
 
 def _read_count(pending: "_PendingCount", nseg: int) -> int:
