@@ -442,7 +442,13 @@ def intersection_capacity(num_intersects: int) -> int:
 # keying by stream keeps a forward from reading an order another stream is
 # still writing.
 _TILE_ORDERS: "dict[tuple, torch.Tensor]" = {}
+_ORDER_AGE: "dict[tuple, int]" = {}   # forwards since the order was made
 _MAX_ORDERS = 16
+# A new heavy-first order is made from every ORDER_EVERY-th forward's wave
+# durations (a tile's cost changes slowly between training steps); the
+# forwards in between reuse it and record no durations.  Any order gives the
+# same results.
+ORDER_EVERY = 4
 # Sort within each XCD's contiguous tile range (keeps each XCD's L2 on its own
 # part of the image) rather than across all tiles.
 ORDER_CHUNKED = True
@@ -525,10 +531,10 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
     b.log_pool); without, nothing is allocated for it and a backward would
     recompute every entry (log_pool_bytes_override sets the pool size with no
     per-wave regions, for tests of a pool that runs full).  The launch takes
-    tiles in the heavy-first order
-    of the previous forward of this image size on this stream (if any) and
-    records its wave durations, from which the order of this forward's
-    backward (b.tile_order) and of the next forward is made."""
+    tiles in the heavy-first order made from an earlier forward of this image
+    size on this stream (if any); every ORDER_EVERY-th forward records its
+    wave durations and makes a new order from them, which its backward
+    (b.tile_order) and the following forwards take."""
     dev = b.device
     H, W = b.img_h, b.img_w
     out = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
@@ -556,14 +562,15 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
         log_args = (cap, None, None, 0, 0)
     # The tile order is kept apart: the next forward reads it after this
     # forward's buffers are gone.
-    order = torch.empty((nsub,), dtype=torch.int32, device=dev)
     okey = (dev.index, st, nsub)
     prev = _TILE_ORDERS.get(okey)
+    age = _ORDER_AGE.get(okey, 0) + 1
+    remake = prev is None or age >= ORDER_EVERY or eval_counts is not None
     base = aux.data_ptr()
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), H, W, b.block_x,
             b.block_y, b.edges_per_segment, N.ptr(out), base, base + 4 * H * W, *log_args)
-    cost = b.ptr("wave_cost")
+    cost = b.ptr("wave_cost") if remake else None
     prev_p = None if prev is None else prev.data_ptr()
     if eval_counts is not None:
         N.call("cs_rasterize_forward_counted", *args, N.ptr(_counts_buffer(eval_counts)),
@@ -573,13 +580,22 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
             N.call("cs_rasterize_forward", *args, prev_p, cost, st)
     if log and log_pool_bytes_override is None:
         _read_log_use_later(key, b.log_pool, units, 1 + wpt * cap * units, pool_bytes, st)
+    if not remake:
+        b.tile_order = prev
+        _ORDER_AGE[okey] = age
+        return out, final_T, final_idx
+    order = torch.empty((nsub,), dtype=torch.int32, device=dev)
     with N.prof("cubic.fwd.tile_order"):
         N.call("cs_raster_tile_order", cost, nsub, int(ORDER_CHUNKED), order.data_ptr(), st)
     b.tile_order = order
     _TILE_ORDERS.pop(okey, None)
+    _ORDER_AGE.pop(okey, None)
     if len(_TILE_ORDERS) >= _MAX_ORDERS:
-        _TILE_ORDERS.pop(next(iter(_TILE_ORDERS)))
+        old = next(iter(_TILE_ORDERS))
+        _TILE_ORDERS.pop(old)
+        _ORDER_AGE.pop(old, None)
     _TILE_ORDERS[okey] = order
+    _ORDER_AGE[okey] = 0
     return out, final_T, final_idx
 
 

@@ -277,6 +277,8 @@ def test_heavy_first_tile_order_is_a_permutation_and_changes_no_result():
     b, s = hip_bin(sc)
     bg = s.background.float().contiguous()
     splat._TILE_ORDERS.clear()
+    every = splat.ORDER_EVERY
+    splat.ORDER_EVERY = 1                              # a new order from every forward
     out0, T0, idx0 = splat.rasterize_forward(b, bg)   # first forward: makes an order
     first = b.tile_order
     order = first.clone()
@@ -295,6 +297,7 @@ def test_heavy_first_tile_order_is_a_permutation_and_changes_no_result():
         out2, T2, idx2 = splat.rasterize_forward(b, bg)
     finally:
         splat.ORDER_CHUNKED = True
+        splat.ORDER_EVERY = every
     assert torch.equal(torch.sort(b.tile_order.long()).values, torch.arange(n, device="cuda"))
     assert torch.equal(out0, out2) and torch.equal(idx0, idx2)
     b.grad_accum_clean = False
@@ -302,6 +305,17 @@ def test_heavy_first_tile_order_is_a_permutation_and_changes_no_result():
     for a, r in zip(g1, g0):
         ok, err = grad_scale_tol(a.cpu().numpy(), r.cpu().numpy(), rtol=1e-5)
         assert ok, err
+    # Between new orders, forwards reuse the last one (and their backward
+    # takes it too).
+    splat._TILE_ORDERS.clear()
+    splat.rasterize_forward(b, bg)
+    made = b.tile_order
+    for _ in range(splat.ORDER_EVERY - 1):
+        out3, _, _ = splat.rasterize_forward(b, bg)
+        assert b.tile_order is made
+        assert torch.equal(out0, out3)
+    splat.rasterize_forward(b, bg)
+    assert b.tile_order is not made
 
 
 @pytest.mark.gpu
