@@ -288,15 +288,20 @@ int cs_edge_aux_from_csr(const int32_t* segment_edge_offsets, int32_t nseg,
  * mode 0, rasterize_cubic_polyline_forward_kernel
  * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  Tiles as above.
  * The primitive records hold each primitive's edge range, so
- * edges_per_segment is not used (>= 0; 0 for adaptive records). */
+ * edges_per_segment is not used (>= 0; 0 for adaptive records).  out_img is
+ * written as [H, W, 3], or, when out_planar != 0, as three [H, W] planes
+ * (channel c at out_img + c H W; the layout cs_clamp_mse_ssim_loss reads
+ * with img_planar, and the clamp(0, 1).permute(2, 0, 1) glue of
+ * gaussian_trace/render.py:1309-1310 then needs no copy). */
 int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
                          const void* edges, const void* edge_culls, const void* prim_recs,
                          const float* background, int32_t img_h, int32_t img_w,
                          int32_t block_x, int32_t block_y,
-                         int32_t edges_per_segment, float* out_img, float* final_Ts,
-                         int32_t* final_idx, int64_t num_entries, int32_t* log_index,
-                         void* log_pool, int64_t log_pool_bytes, int32_t log_entry_units,
-                         const int32_t* tile_order, uint32_t* wave_cost, hipStream_t stream);
+                         int32_t edges_per_segment, float* out_img, int32_t out_planar,
+                         float* final_Ts, int32_t* final_idx, int64_t num_entries,
+                         int32_t* log_index, void* log_pool, int64_t log_pool_bytes,
+                         int32_t log_entry_units, const int32_t* tile_order,
+                         uint32_t* wave_cost, hipStream_t stream);
 
 /* rasterize_cubic_fill_backward_kernel (ops/cubic_splatting.py:1197-1651) /
  * rasterize_cubic_polyline_backward_kernel (ops/cubic_polyline_splatting.py:252-660)
@@ -367,10 +372,11 @@ int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                  const void* edge_culls, const void* prim_recs,
                                  const float* background, int32_t img_h, int32_t img_w,
                                  int32_t block_x, int32_t block_y,
-                                 int32_t edges_per_segment, float* out_img, float* final_Ts,
-                                 int32_t* final_idx, int64_t num_entries, int32_t* log_index,
-                                 void* log_pool, int64_t log_pool_bytes,
-                                 int32_t log_entry_units, unsigned long long* eval_counts,
+                                 int32_t edges_per_segment, float* out_img,
+                                 int32_t out_planar, float* final_Ts, int32_t* final_idx,
+                                 int64_t num_entries, int32_t* log_index, void* log_pool,
+                                 int64_t log_pool_bytes, int32_t log_entry_units,
+                                 unsigned long long* eval_counts,
                                  const int32_t* tile_order,
                                  uint32_t* wave_cost, hipStream_t stream);
 int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,
@@ -529,23 +535,26 @@ int cs_mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, 
                          const float* win1d, int32_t win, const float* abc, float ssim_weight,
                          const float* grad_loss, float* grad_x, hipStream_t stream);
 
-/* The same loss on the renderer's [h, w, 3] image, with the caller's
+/* The same loss on the renderer's image, with the caller's
  * clamp(0, 1).permute(2, 0, 1) glue (gaussian_trace/render.py:1309-1310)
- * folded in: the forward writes x = clamp(img, lo, hi) as [3, h, w] into the
- * caller's buffer x and computes the loss on it; the backward reads img
- * itself and writes grad_img directly, zero where img lies outside [lo, hi]
- * (no gradient pass through the glue): [h, w, 3], or, with grad_planar != 0,
- * three [h, w] planes (whole-line writes; cs_rasterize_backward reads that
- * layout with v_output_planar).  y is the [3, h, w] target; partials / abc as
- * for cs_mse_ssim_loss with nc = 3. */
-int cs_clamp_mse_ssim_loss(const float* img, const float* y, int32_t h, int32_t w, float lo,
-                           float hi, const float* win1d, int32_t win, float c1, float c2,
-                           float ssim_weight, float* x, float* partials, float* out, float* abc,
-                           hipStream_t stream);
-int cs_clamp_mse_ssim_backward(const float* img, const float* y, int32_t h, int32_t w, float lo,
-                               float hi, const float* win1d, int32_t win, const float* abc,
-                               float ssim_weight, const float* grad_loss, float* grad_img,
-                               int32_t grad_planar, hipStream_t stream);
+ * folded in.  img is [h, w, 3], or, when img_planar != 0, three [h, w] planes
+ * (cs_rasterize_forward's out_planar layout).  The forward computes the loss
+ * on x = clamp(img, lo, hi): from [h, w, 3] it first writes x as [3, h, w]
+ * into the caller's buffer x; planes it reads clamped in place (x unused,
+ * may be NULL).  The backward reads img itself and writes grad_img directly,
+ * zero where img lies outside [lo, hi] (no gradient pass through the glue):
+ * [h, w, 3], or, with grad_planar != 0, three [h, w] planes (whole-line
+ * writes; cs_rasterize_backward reads that layout with v_output_planar).  A
+ * planar img takes grad_planar != 0.  y is the [3, h, w] target; partials /
+ * abc as for cs_mse_ssim_loss with nc = 3. */
+int cs_clamp_mse_ssim_loss(const float* img, int32_t img_planar, const float* y, int32_t h,
+                           int32_t w, float lo, float hi, const float* win1d, int32_t win,
+                           float c1, float c2, float ssim_weight, float* x, float* partials,
+                           float* out, float* abc, hipStream_t stream);
+int cs_clamp_mse_ssim_backward(const float* img, int32_t img_planar, const float* y, int32_t h,
+                               int32_t w, float lo, float hi, const float* win1d, int32_t win,
+                               const float* abc, float ssim_weight, const float* grad_loss,
+                               float* grad_img, int32_t grad_planar, hipStream_t stream);
 
 /* ---------------- optimizer ---------------- */
 

@@ -50,15 +50,15 @@ _SIGNATURES = {
     "cs_bin_finish": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _I32, _I32, _I32, _I32, _P, _P,
                                      _P, _P, _P, _I64, _P]),
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
-                                            _I32, _P, _P, _P, _I64, _P, _P, _I64, _I32, _P, _P,
-                                            _P]),
+                                            _I32, _P, _I32, _P, _P, _I64, _P, _P, _I64, _I32, _P,
+                                            _P, _P]),
     "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                              _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P,
                                              _P, _P, _I32, _P, _P, _P]),
     "cs_raster_prim_scratch_elems": (_SZ, [_I32, _I32]),
     "cs_rasterize_forward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
-                                                    _I32, _I32, _P, _P, _P, _I64, _P, _P, _I64,
-                                                    _I32, _P, _P, _P, _P]),
+                                                    _I32, _I32, _P, _I32, _P, _P, _I64, _P, _P,
+                                                    _I64, _I32, _P, _P, _P, _P]),
     "cs_rasterize_backward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
                                                      _I32, _I32, _I32, _P, _P, _P, _P, _P, _I32,
                                                      _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P,
@@ -112,10 +112,10 @@ _SIGNATURES = {
     "cs_closed_ring_segments": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
     "cs_closed_ring_segments_backward": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P,
                                                         _P]),
-    "cs_clamp_mse_ssim_loss": (ctypes.c_int, [_P, _P, _I32, _I32, _F, _F, _P, _I32, _F, _F, _F,
-                                              _P, _P, _P, _P, _P]),
-    "cs_clamp_mse_ssim_backward": (ctypes.c_int, [_P, _P, _I32, _I32, _F, _F, _P, _I32, _P, _F,
-                                                  _P, _P, _I32, _P]),
+    "cs_clamp_mse_ssim_loss": (ctypes.c_int, [_P, _I32, _P, _I32, _I32, _F, _F, _P, _I32, _F, _F,
+                                              _F, _P, _P, _P, _P, _P]),
+    "cs_clamp_mse_ssim_backward": (ctypes.c_int, [_P, _I32, _P, _I32, _I32, _F, _F, _P, _I32, _P,
+                                                  _F, _P, _P, _I32, _P]),
     "cs_adam_step": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _D, _D, _D, _P]),
     "cs_adan_step": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_gs_project_forward": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P,

@@ -1154,6 +1154,67 @@ __global__ __launch_bounds__(256) void k_rank_allpairs(
     }
 }
 
+// Depth key of a float: its order as unsigned order (cubic_splatting.py:801-805),
+// as prim_prep_one computes it.
+__device__ __forceinline__ uint32_t depth_key(float d) {
+    const int32_t bits = __builtin_bit_cast(int32_t, d);
+    return (uint32_t)(bits ^ ((bits >> 31) | (int32_t)0x80000000));
+}
+
+// k_prim_prep and k_rank_allpairs<false> in one launch, for at most
+// kRankPairsMax primitives: one wave per primitive counts the keys that
+// precede its own (lane-parallel, the keys computed from the depths, since no
+// other wave's keys are written yet), and lane 0 makes the primitive's
+// records (prim_prep_one) and writes order[pos] = p, rank_rects[pos] = its
+// tile rectangle.
+__global__ __launch_bounds__(256) void k_prim_prep_rank(
+    const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
+    const int32_t* __restrict__ seg_tile_ranges, const SegRec* __restrict__ seg_recs,
+    const float* __restrict__ colors, const float* __restrict__ opacities,
+    const float* __restrict__ depths, const int32_t* __restrict__ fill_rules,
+    const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
+    int eps, const int32_t* __restrict__ seg_edge_offsets, int tbx, int tby, int mode,
+    int32_t* __restrict__ status, int32_t* __restrict__ prim_tile_ranges,
+    uint32_t* __restrict__ counts, float* __restrict__ inv_sigma2s, uint32_t* __restrict__ keys,
+    int32_t* __restrict__ vals, PrimRec* __restrict__ recs, int32_t* __restrict__ order,
+    int4* __restrict__ rank_rects) {
+    const int p = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (p >= P) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t ki = depth_key(depths[p]);
+    int cnt = 0;
+    const int n4 = P & ~3;
+    const bool vec = (reinterpret_cast<uintptr_t>(depths) & 15) == 0;
+    int j0 = 0;
+    if (vec) {
+#pragma unroll 4
+        for (j0 = 4 * lane; j0 < n4; j0 += 4 * kWave) {
+            const float4 d = *reinterpret_cast<const float4*>(depths + j0);
+            const uint32_t a = depth_key(d.x), b = depth_key(d.y), c = depth_key(d.z),
+                           e = depth_key(d.w);
+            cnt += (int)((a < ki) | ((a == ki) & (j0 < p)));
+            cnt += (int)((b < ki) | ((b == ki) & (j0 + 1 < p)));
+            cnt += (int)((c < ki) | ((c == ki) & (j0 + 2 < p)));
+            cnt += (int)((e < ki) | ((e == ki) & (j0 + 3 < p)));
+        }
+        j0 = n4;
+    }
+    for (int j = j0 + lane; j < P; j += kWave) {
+        const uint32_t kj = depth_key(depths[j]);
+        cnt += (int)((kj < ki) | ((kj == ki) & (j < p)));
+    }
+    const int pos = wave_sum_i(cnt);
+    if (lane == 0) {
+        prim_prep_one(cubics_norm, seg_offsets, P, seg_tile_ranges, seg_recs, colors, opacities,
+                      depths, fill_rules, aa_widths, stroke_widths, nseg, eps, seg_edge_offsets,
+                      tbx, tby, mode, status, prim_tile_ranges, counts, inv_sigma2s, keys, vals,
+                      recs, p);
+        order[pos] = p;
+        // The rectangle this thread has just written.
+        rank_rects[pos] = reinterpret_cast<const int4*>(prim_tile_ranges)[p];
+    }
+}
+
 // rank_rects[r] = prim_rects[order[r]] (after the radix sort of many keys).
 __global__ __launch_bounds__(256) void k_gather_rects(const int32_t* __restrict__ order, int n,
                                                      const int4* __restrict__ prim_rects,
@@ -1713,16 +1774,18 @@ extern "C" int cs_radix_sort_pairs_u32(uint32_t* keys, int32_t* vals, uint32_t* 
 
 
 // Depth ranks, then the tile-list counts: order[r] = primitive with the r-th
-// smallest key (ties by primitive id) and rank_rects[r] its tile rectangle;
-// per-tile counts, per-segment totals, then the segments' first slots;
-// status[0] receives the intersection total.
+// smallest key (ties by primitive id) and rank_rects[r] its tile rectangle
+// (already written when `ranked`); per-tile counts, per-segment totals, then
+// the segments' first slots; status[0] receives the intersection total.
 static int rank_and_count(bool blocks_ranked, uint32_t* keys, int32_t* order,
                           const int4* prim_rects,
                           int4* rank_rects, int nprim, int tbx, int tby, uint32_t* keys_alt,
                           int32_t* vals_alt, uint32_t* radix_counts, uint32_t* scan_temp,
                           uint32_t* tile_count,
-                          uint32_t* tile_scratch, int32_t* status, hipStream_t stream) {
-    if (nprim <= kRankPairsMax) {
+                          uint32_t* tile_scratch, int32_t* status, hipStream_t stream,
+                          bool ranked = false) {
+    if (ranked) {
+    } else if (nprim <= kRankPairsMax) {
         hipLaunchKernelGGL(k_rank_allpairs<false>, dim3((nprim + 3) / 4), dim3(256), 0, stream,
                            keys, nprim, (const int32_t*)nullptr, (uint32_t*)nullptr,
                            (int32_t*)nullptr, prim_rects, order, rank_rects);
@@ -1830,6 +1893,22 @@ static int bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, con
                                reinterpret_cast<EdgeAux*>(edge_aux),
                                reinterpret_cast<SegRec*>(seg_recs));
     }
+    if (nprim <= kRankPairsMax) {
+        // Records and depth ranks in one launch.
+        hipLaunchKernelGGL(k_prim_prep_rank, dim3((nprim + 3) / 4), dim3(256), 0, stream,
+                           cubics_norm, seg_offsets, nprim, seg_tile_ranges,
+                           reinterpret_cast<const SegRec*>(seg_recs), colors, opacities, depths,
+                           fill_rules, aa_widths, stroke_widths, nseg, eps,
+                           adaptive ? seg_edge_offsets : nullptr, tbx, tby, mode, status,
+                           prim_tile_ranges, num_tiles_hit, inv_sigma2s, keys,
+                           reinterpret_cast<int32_t*>(keys_alt),
+                           reinterpret_cast<PrimRec*>(prim_recs), order,
+                           reinterpret_cast<int4*>(rank_tile_ranges));
+        return rank_and_count(true, keys, order, reinterpret_cast<const int4*>(prim_tile_ranges),
+                              reinterpret_cast<int4*>(rank_tile_ranges), nprim, tbx, tby,
+                              keys_alt, vals_alt, radix_counts, scan_temp, tile_count,
+                              tile_scratch, status, stream, true);
+    }
     hipLaunchKernelGGL(k_prim_prep, dim3(blocks_for(nprim, 256)), dim3(256), 0, stream,
                        cubics_norm, seg_offsets, nprim, seg_tile_ranges,
                        reinterpret_cast<const SegRec*>(seg_recs), colors, opacities, depths,
@@ -1837,8 +1916,8 @@ static int bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, con
                        adaptive ? seg_edge_offsets : nullptr, tbx, tby, mode, status,
                        prim_tile_ranges, num_tiles_hit, inv_sigma2s, keys, order,
                        reinterpret_cast<PrimRec*>(prim_recs),
-                       nprim > kRankPairsMax && nprim <= kRankSortMax ? keys_alt : nullptr,
-                       nprim > kRankPairsMax && nprim <= kRankSortMax ? vals_alt : nullptr);
+                       nprim <= kRankSortMax ? keys_alt : nullptr,
+                       nprim <= kRankSortMax ? vals_alt : nullptr);
     return rank_and_count(true, keys, order, reinterpret_cast<const int4*>(prim_tile_ranges),
                           reinterpret_cast<int4*>(rank_tile_ranges), nprim, tbx, tby, keys_alt,
                           vals_alt, radix_counts, scan_temp, tile_count,

@@ -177,14 +177,21 @@ struct SsimTile {
     static constexpr int BOFF = (4 - (WIN - 1) % 4) % 4;
 };
 
+// clamp(v, lo, hi) as torch.clamp computes it for ordered values, when CLAMP.
+template <bool CLAMP>
+__device__ __forceinline__ float clamp_if(float v, float lo, float hi) {
+    return CLAMP ? fminf(fmaxf(v, lo), hi) : v;
+}
+
 // Loads plane[gy][gx0 .. gx0 + N) of an image with h rows of w valid columns
-// stored with row stride ld (zero outside).  When rows are 16-byte aligned
-// (vec_ok), gx0 - OFF is a multiple of 4 and the rounded-up strip lies inside
-// the row, it uses float4 loads starting OFF columns early.
-template <int N, int OFF>
+// stored with row stride ld (zero outside; with CLAMP the values inside are
+// clamped to [lo, hi], the zeros outside are not).  When rows are 16-byte
+// aligned (vec_ok), gx0 - OFF is a multiple of 4 and the rounded-up strip lies
+// inside the row, it uses float4 loads starting OFF columns early.
+template <int N, int OFF, bool CLAMP = false>
 __device__ __forceinline__ void load_strip(const float* __restrict__ plane, int h, int w,
                                            size_t ld, int gy, int gx0, bool vec_ok,
-                                           float (&dst)[N]) {
+                                           float (&dst)[N], float lo = 0.0f, float hi = 0.0f) {
     constexpr int NV4 = (N + OFF + 3) / 4;
     if (gy < 0 || gy >= h) {
 #pragma unroll
@@ -204,12 +211,12 @@ __device__ __forceinline__ void load_strip(const float* __restrict__ plane, int 
             t[4 * v + 3] = q.w;
         }
 #pragma unroll
-        for (int k = 0; k < N; ++k) dst[k] = t[OFF + k];
+        for (int k = 0; k < N; ++k) dst[k] = clamp_if<CLAMP>(t[OFF + k], lo, hi);
     } else {
 #pragma unroll
         for (int k = 0; k < N; ++k) {
             const int gx = gx0 + k;
-            dst[k] = (gx >= 0 && gx < w) ? row[gx] : 0.0f;
+            dst[k] = (gx >= 0 && gx < w) ? clamp_if<CLAMP>(row[gx], lo, hi) : 0.0f;
         }
     }
 }
@@ -275,14 +282,17 @@ __device__ __forceinline__ SsimPixel ssim_pixel(float m1, float m2, float mss, f
 // anchor inputs -- rows [oy0, oy0 + 48) and columns [ox0, ox0 + 32), extended
 // to the image's last row / column in the last tile row / column -- so every
 // input is counted once and no separate MSE pass is needed.
-template <int WIN>
+// CLAMP: x is read as clamp(x, lo, hi) (the caller's clamp glue, applied on
+// load instead of in a pass of its own).
+template <int WIN, bool CLAMP>
 __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
                                                  const float* __restrict__ y, int h, int w,
                                                  int oh, int ow,
                                                  const float* __restrict__ win1d, float c1,
                                                  float c2, float* __restrict__ partials,
                                                  float* __restrict__ abc, int nc,
-                                                 float* __restrict__ mse_partials) {
+                                                 float* __restrict__ mse_partials, float lo,
+                                                 float hi) {
     using TT = SsimTile<WIN>;
     constexpr int IT = TT::IT, HP = TT::HP, NIN = TT::NIN;
     // Four filtered moments: x, y, x^2 + y^2 and xy (SSIM needs the two
@@ -305,7 +315,7 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
     // avoids the cancellation of E[x^2] - mu^2 in flat regions (where it
     // would leave fp32 noise of order 1e-7 against c2 = 9e-4).
     const size_t kpix = (size_t)min(oy0 + kSsimTH / 2, h - 1) * w + min(ox0 + kSsimTW / 2, w - 1);
-    const float kx = xc[kpix], ky = yc[kpix];
+    const float kx = clamp_if<CLAMP>(xc[kpix], lo, hi), ky = yc[kpix];
     const bool vec_ok = ((w & 3) == 0) &&
                         ((reinterpret_cast<uintptr_t>(xc) | reinterpret_cast<uintptr_t>(yc)) & 15) == 0;
     // MSE anchor: rows [0, mse_rows) of the tile's input rows; columns
@@ -317,7 +327,7 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
     for (int item = threadIdx.x; item < IT * (kSsimTW / kHStrip); item += 256) {
         const int r = item >> 2, q0 = (item & 3) * kHStrip;
         float a[NIN], b[NIN];
-        load_strip<NIN, 0>(xc, h, w, w, oy0 + r, ox0 + q0, vec_ok, a);
+        load_strip<NIN, 0, CLAMP>(xc, h, w, w, oy0 + r, ox0 + q0, vec_ok, a, lo, hi);
         load_strip<NIN, 0>(yc, h, w, w, oy0 + r, ox0 + q0, vec_ok, b);
         if (mse_partials && r < mse_rows) {
             const int cols = (tx == ntx - 1 && q0 + kHStrip == kSsimTW) ? NIN : kHStrip;
@@ -404,11 +414,13 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
 // (A[o] + 2 x[p] B[o] + y[p] C[o]): a full (transposed) correlation of the
 // three maps, blocked like the forward (horizontal strips read the maps from
 // global memory, vertical strips from LDS).
-// HWC: x is the [h, w, 3] image the forward read as clamp(x, lo, hi) and gx
-// the gradient with respect to it, zero where x lies outside [lo, hi] (the
-// clamp's gradient as torch defines it): [h, w, 3], or, with gx_planar, three
-// [h, w] planes (each channel tile then writes whole lines).
-template <int WIN, bool HWC>
+// XL, the layout of x: 0, nc planes read as they are; 1 (HWC), the [h, w, 3]
+// image the forward read as clamp(x, lo, hi); 2, three [h, w] planes read as
+// clamp(x, lo, hi).  With a clamp, gx is the gradient with respect to x
+// itself, zero where x lies outside [lo, hi] (the clamp's gradient as torch
+// defines it).  gx: planes, or, for XL 1 without gx_planar, [h, w, 3]
+// (planes let each channel tile write whole lines).
+template <int WIN, int XL>
 __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
                                                  const float* __restrict__ y, int h, int w,
                                                  int oh, int ow,
@@ -423,7 +435,7 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
     // 1D grid over (channel, tile row, tile column), XCD-aware.
     const int ntx = (w + kSsimTW - 1) / kSsimTW, nty = (h + kSsimTH - 1) / kSsimTH;
     int c, ty, tx;
-    ssim_tile<HWC>(blockIdx.x, ntx, nty, nc, c, ty, tx);
+    ssim_tile<XL == 1>(blockIdx.x, ntx, nty, nc, c, ty, tx);
     const int px0 = tx * kSsimTW, py0 = ty * kSsimTH;
     const size_t ld = abc_ld(ow);
     const size_t plane = (size_t)oh * ld;
@@ -484,12 +496,12 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
         const int py = py0 + r0 + o;
         if (py >= h || px >= w) continue;
         const size_t pi = (size_t)py * w + px;
-        const float xr = HWC ? x[3 * pi + c] : x[(size_t)c * h * w + pi];
-        const float xv = HWC ? fminf(fmaxf(xr, lo), hi) : xr, yv = yc[pi];
+        const float xr = XL == 1 ? x[3 * pi + c] : x[(size_t)c * h * w + pi];
+        const float xv = clamp_if<XL != 0>(xr, lo, hi), yv = yc[pi];
         float gv = scale * (gsum[0][o] + 2.0f * xv * gsum[1][o] + yv * gsum[2][o]);
         if (mse_coef != 0.0f) gv = __builtin_fmaf(mscale, xv - yv, gv);
-        if (HWC) gv = ((xr >= lo) & (xr <= hi)) ? gv : 0.0f;
-        gx[(HWC && !gx_planar) ? 3 * pi + c : (size_t)c * h * w + pi] = gv;
+        if (XL != 0) gv = ((xr >= lo) & (xr <= hi)) ? gv : 0.0f;
+        gx[(XL == 1 && !gx_planar) ? 3 * pi + c : (size_t)c * h * w + pi] = gv;
     }
 }
 
@@ -655,9 +667,25 @@ __global__ __launch_bounds__(kFinalThreads) void k_mse_ssim_combine(
     const float* __restrict__ mse_partials, int n_mse, const float* __restrict__ ssim_partials,
     int n_ssim, float inv_n, float inv_m, float weight, float* __restrict__ out) {
     __shared__ float sh[kFinalThreads / kWave];
+    // Each thread adds its elements in index order, eight of each array
+    // loaded before the first addition (one memory round trip per eight).
+    constexpr int kU = 8;
     float a = 0.0f, b = 0.0f;
-    for (int i = threadIdx.x; i < n_mse; i += kFinalThreads) a += mse_partials[i];
-    for (int i = threadIdx.x; i < n_ssim; i += kFinalThreads) b += ssim_partials[i];
+    const int n = max(n_mse, n_ssim);
+    for (int i0 = threadIdx.x; i0 < n; i0 += kU * kFinalThreads) {
+        float va[kU], vb[kU];
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            const int i = i0 + k * kFinalThreads;
+            va[k] = i < n_mse ? mse_partials[i] : 0.0f;
+            vb[k] = i < n_ssim ? ssim_partials[i] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            a += va[k];
+            b += vb[k];
+        }
+    }
     const float ta = block_sum(a, sh);
     const float tb = block_sum(b, sh);
     if (threadIdx.x == 0) {
@@ -843,16 +871,18 @@ static bool ssim_tiled_ok(int32_t nc, int32_t h, int32_t w, int32_t win) {
     return ssim_args_ok(nc, h, w, win) && win <= kSsimTiledMaxWin;
 }
 
-// SSIM partial sums (one per output tile) and, when abc != null, the maps.
+// SSIM partial sums (one per output tile) and, when abc != null, the maps;
+// with `clamp`, x is read as clamp(x, lo, hi).
+template <bool CLAMP>
 static int launch_ssim_fwd(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                            const float* win1d, int32_t win, float c1, float c2,
                            float* partials, float* abc, hipStream_t stream, int* nblk,
-                           float* mse_partials = nullptr) {
+                           float* mse_partials = nullptr, float lo = 0.0f, float hi = 0.0f) {
     const int oh = h - win + 1, ow = w - win + 1;
     const dim3 grid(((ow + kSsimTW - 1) / kSsimTW) * ((oh + kSsimTH - 1) / kSsimTH) * nc);
-#define CS_SSIM_FWD(W_)                                                                       \
-    hipLaunchKernelGGL(k_ssim_fwd<W_>, grid, dim3(256), 0, stream, x, y, h, w, oh, ow, win1d, \
-                       c1, c2, partials, abc, nc, mse_partials)
+#define CS_SSIM_FWD(W_)                                                                        \
+    hipLaunchKernelGGL((k_ssim_fwd<W_, CLAMP>), grid, dim3(256), 0, stream, x, y, h, w, oh, ow, \
+                       win1d, c1, c2, partials, abc, nc, mse_partials, lo, hi)
     switch (win) {
         CS_SSIM_DISPATCH(1, CS_SSIM_FWD)
         CS_SSIM_DISPATCH(3, CS_SSIM_FWD)
@@ -869,7 +899,7 @@ static int launch_ssim_fwd(const float* x, const float* y, int32_t nc, int32_t h
     return CS_OK;
 }
 
-template <bool HWC>
+template <int XL>
 static int launch_ssim_bwd(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                            const float* win1d, int32_t win, const float* abc,
                            const float* grad_out, int go_per_map, float ssim_coef,
@@ -878,7 +908,7 @@ static int launch_ssim_bwd(const float* x, const float* y, int32_t nc, int32_t h
     const int oh = h - win + 1, ow = w - win + 1;
     const dim3 grid(((w + kSsimTW - 1) / kSsimTW) * ((h + kSsimTH - 1) / kSsimTH) * nc);
 #define CS_SSIM_BWD(W_)                                                                        \
-    hipLaunchKernelGGL((k_ssim_bwd<W_, HWC>), grid, dim3(256), 0, stream, x, y, h, w, oh, ow, \
+    hipLaunchKernelGGL((k_ssim_bwd<W_, XL>), grid, dim3(256), 0, stream, x, y, h, w, oh, ow,  \
                        win1d, abc, grad_out, go_per_map, ssim_coef, mse_coef, nc, lo, hi,     \
                        gx_planar, grad_x)
     switch (win) {
@@ -905,8 +935,8 @@ extern "C" int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, in
     const int64_t per = ssim_partials_per_map(oh, ow, win);
     if (win <= kSsimTiledMaxWin) {
         int nblk = 0;
-        const int rc = launch_ssim_fwd(x, y, nc, h, w, win1d, win, c1, c2, partials, abc, stream,
-                                       &nblk);
+        const int rc = launch_ssim_fwd<false>(x, y, nc, h, w, win1d, win, c1, c2, partials,
+                                              abc, stream, &nblk);
         if (rc) return rc;
     } else {
         if (!scratch) return CS_ERR_ARGS;
@@ -937,8 +967,8 @@ extern "C" int cs_ssim_backward(const float* x, const float* y, int32_t nc, int3
     const float inv_cnt =
         per_map ? 1.0f / ((float)oh * (float)ow) : 1.0f / ((float)nc * (float)oh * (float)ow);
     if (win <= kSsimTiledMaxWin) {
-        const int rc = launch_ssim_bwd<false>(x, y, nc, h, w, win1d, win, abc, grad_out, per_map,
-                                              inv_cnt, 0.0f, grad_x, stream);
+        const int rc = launch_ssim_bwd<0>(x, y, nc, h, w, win1d, win, abc, grad_out, per_map,
+                                          inv_cnt, 0.0f, grad_x, stream);
         return rc ? rc : metric_status();
     }
     if (!scratch) return CS_ERR_ARGS;
@@ -957,26 +987,28 @@ extern "C" size_t cs_mse_ssim_partials_elems(int32_t nc, int32_t h, int32_t w) {
 
 // MSE + w (1 - SSIM): the SSIM forward also sums (x - y)^2 over each tile's
 // anchor inputs (so the MSE needs no pass of its own); one workgroup then
-// combines both sets of tile partials.
+// combines both sets of tile partials.  CLAMP: x read as clamp(x, lo, hi).
+template <bool CLAMP>
 static int mse_ssim_loss(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                          const float* win1d, int32_t win, float c1, float c2, float ssim_weight,
-                         float* partials, float* out, float* abc, hipStream_t stream) {
+                         float* partials, float* out, float* abc, hipStream_t stream,
+                         float lo = 0.0f, float hi = 0.0f) {
     if (!ssim_tiled_ok(nc, h, w, win)) return CS_ERR_ARGS;
     const int64_t n = (int64_t)nc * h * w;
+    const int oh = h - win + 1, ow = w - win + 1;
+    const float inv_n = 1.0f / (float)n, inv_m = 1.0f / ((float)nc * (float)oh * (float)ow);
     float* ssim_partials = partials;
     float* mse_partials = partials + cs_ssim_partials_elems(nc, h, w);
     int nblk = 0;
-    const int rc = launch_ssim_fwd(x, y, nc, h, w, win1d, win, c1, c2, ssim_partials, abc, stream,
-                                   &nblk, mse_partials);
+    const int rc = launch_ssim_fwd<CLAMP>(x, y, nc, h, w, win1d, win, c1, c2, ssim_partials, abc,
+                                          stream, &nblk, mse_partials, lo, hi);
     if (rc) return rc;
-    const int oh = h - win + 1, ow = w - win + 1;
     hipLaunchKernelGGL(k_mse_ssim_combine, dim3(1), dim3(kFinalThreads), 0, stream, mse_partials,
-                       nblk, ssim_partials, nblk, 1.0f / (float)n,
-                       1.0f / ((float)nc * (float)oh * (float)ow), ssim_weight, out);
+                       nblk, ssim_partials, nblk, inv_n, inv_m, ssim_weight, out);
     return metric_status();
 }
 
-template <bool HWC>
+template <int XL>
 static int mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
                              float lo, float hi, const float* win1d, int32_t win,
                              const float* abc, float ssim_weight, const float* grad_loss,
@@ -985,7 +1017,7 @@ static int mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t
     const int oh = h - win + 1, ow = w - win + 1;
     const float inv_cnt = 1.0f / ((float)nc * (float)oh * (float)ow);
     const float mse_coef = (float)(2.0 / ((double)nc * h * w));
-    const int rc = launch_ssim_bwd<HWC>(x, y, nc, h, w, win1d, win, abc, grad_loss, 0,
+    const int rc = launch_ssim_bwd<XL>(x, y, nc, h, w, win1d, win, abc, grad_loss, 0,
                                         -ssim_weight * inv_cnt, mse_coef, grad_x, stream, lo, hi,
                                         gx_planar);
     return rc ? rc : metric_status();
@@ -995,38 +1027,50 @@ extern "C" int cs_mse_ssim_loss(const float* x, const float* y, int32_t nc, int3
                                 const float* win1d, int32_t win, float c1, float c2,
                                 float ssim_weight, float* partials, float* out, float* abc,
                                 hipStream_t stream) {
-    return mse_ssim_loss(x, y, nc, h, w, win1d, win, c1, c2, ssim_weight, partials, out, abc,
-                         stream);
+    return mse_ssim_loss<false>(x, y, nc, h, w, win1d, win, c1, c2, ssim_weight, partials, out,
+                                abc, stream);
 }
 
 extern "C" int cs_mse_ssim_backward(const float* x, const float* y, int32_t nc, int32_t h,
                                     int32_t w, const float* win1d, int32_t win, const float* abc,
                                     float ssim_weight, const float* grad_loss, float* grad_x,
                                     hipStream_t stream) {
-    return mse_ssim_backward<false>(x, y, nc, h, w, 0.0f, 0.0f, win1d, win, abc, ssim_weight,
-                                    grad_loss, grad_x, stream);
+    return mse_ssim_backward<0>(x, y, nc, h, w, 0.0f, 0.0f, win1d, win, abc, ssim_weight,
+                                grad_loss, grad_x, stream);
 }
 
-extern "C" int cs_clamp_mse_ssim_loss(const float* img, const float* y, int32_t h, int32_t w,
-                                      float lo, float hi, const float* win1d, int32_t win,
-                                      float c1, float c2, float ssim_weight, float* x,
-                                      float* partials, float* out, float* abc,
-                                      hipStream_t stream) {
-    if (!ssim_tiled_ok(3, h, w, win) || !x) return CS_ERR_ARGS;
+extern "C" int cs_clamp_mse_ssim_loss(const float* img, int32_t img_planar, const float* y,
+                                      int32_t h, int32_t w, float lo, float hi,
+                                      const float* win1d, int32_t win, float c1, float c2,
+                                      float ssim_weight, float* x, float* partials, float* out,
+                                      float* abc, hipStream_t stream) {
+    if (!ssim_tiled_ok(3, h, w, win)) return CS_ERR_ARGS;
+    // Planes: the SSIM forward reads them clamped; no copy.
+    if (img_planar)
+        return mse_ssim_loss<true>(img, y, 3, h, w, win1d, win, c1, c2, ssim_weight, partials,
+                                   out, abc, stream, lo, hi);
+    if (!x) return CS_ERR_ARGS;
     const int64_t hw = (int64_t)h * w;
     hipLaunchKernelGGL(k_clamp_hwc_to_chw, dim3((unsigned)((hw + 255) / 256)), dim3(256), 0,
                        stream, img, hw, lo, hi, x);
-    return mse_ssim_loss(x, y, 3, h, w, win1d, win, c1, c2, ssim_weight, partials, out, abc,
-                         stream);
+    return mse_ssim_loss<false>(x, y, 3, h, w, win1d, win, c1, c2, ssim_weight, partials, out,
+                                abc, stream);
 }
 
-extern "C" int cs_clamp_mse_ssim_backward(const float* img, const float* y, int32_t h, int32_t w,
-                                          float lo, float hi, const float* win1d, int32_t win,
-                                          const float* abc, float ssim_weight,
-                                          const float* grad_loss, float* grad_img,
-                                          int32_t grad_planar, hipStream_t stream) {
-    return mse_ssim_backward<true>(img, y, 3, h, w, lo, hi, win1d, win, abc, ssim_weight,
-                                   grad_loss, grad_img, stream, grad_planar ? 1 : 0);
+extern "C" int cs_clamp_mse_ssim_backward(const float* img, int32_t img_planar, const float* y,
+                                          int32_t h, int32_t w, float lo, float hi,
+                                          const float* win1d, int32_t win, const float* abc,
+                                          float ssim_weight, const float* grad_loss,
+                                          float* grad_img, int32_t grad_planar,
+                                          hipStream_t stream) {
+    if (img_planar) {
+        // The gradient of a planar image is written as planes.
+        if (!grad_planar) return CS_ERR_ARGS;
+        return mse_ssim_backward<2>(img, y, 3, h, w, lo, hi, win1d, win, abc, ssim_weight,
+                                    grad_loss, grad_img, stream, 1);
+    }
+    return mse_ssim_backward<1>(img, y, 3, h, w, lo, hi, win1d, win, abc, ssim_weight,
+                                grad_loss, grad_img, stream, grad_planar ? 1 : 0);
 }
 
 extern "C" int cs_clamp_hwc_to_nchw(const float* img, int32_t h, int32_t w, float lo, float hi,

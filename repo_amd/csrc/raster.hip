@@ -604,10 +604,10 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     TileGrid tg, const int32_t* __restrict__ tile_order,
-    uint32_t* __restrict__ wave_cost, float* __restrict__ out, float* __restrict__ final_T,
-    int32_t* __restrict__ final_idx, int32_t* __restrict__ log_index,
-    uint4* __restrict__ log_pool, uint32_t log_units, uint32_t log_per_entry,
-    unsigned long long* __restrict__ counts) {
+    uint32_t* __restrict__ wave_cost, float* __restrict__ out, int out_planar,
+    float* __restrict__ final_T, int32_t* __restrict__ final_idx,
+    int32_t* __restrict__ log_index, uint4* __restrict__ log_pool, uint32_t log_units,
+    uint32_t log_per_entry, unsigned long long* __restrict__ counts) {
     const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -804,15 +804,18 @@ __global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
         if ((logged >> lane) & 1u) log_index[(size_t)tg.waves * gl + sb.slot] = idx_l;
     }
     if (log_index) log_flush(log_pool, stage, st);
+    // The image as [H, W, 3], or as three [H, W] planes (out_planar).
+    const size_t ch = out_planar ? (size_t)img_h * img_w : 1;
 #pragma unroll
     for (int p = 0; p < kPix; ++p) {
         if (!L.in_img[p]) continue;
         const size_t pix = (size_t)L.i[p] * img_w + L.j;
         final_T[pix] = T[p];
         final_idx[pix] = cur[p];
-        out[3 * pix + 0] = __builtin_fmaf(T[p], bg[0], C0[p]);
-        out[3 * pix + 1] = __builtin_fmaf(T[p], bg[1], C1[p]);
-        out[3 * pix + 2] = __builtin_fmaf(T[p], bg[2], C2[p]);
+        float* const o = out + (out_planar ? pix : 3 * pix);
+        o[0] = __builtin_fmaf(T[p], bg[0], C0[p]);
+        o[ch] = __builtin_fmaf(T[p], bg[1], C1[p]);
+        o[2 * ch] = __builtin_fmaf(T[p], bg[2], C2[p]);
     }
     if constexpr (COUNT) flush_counts(n, counts);
     record_wave_cost(wave_cost, sb.index, t_start);
@@ -1513,6 +1516,7 @@ struct RasterArgs {
     const float* bg;
     // forward outputs
     float* out;
+    int out_planar;      // out as three [H, W] planes instead of [H, W, 3]
     float* final_T;
     int32_t* final_idx;
     int32_t* log_index;     // raster log: written by the forward, read by the backward
@@ -1540,7 +1544,8 @@ template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
     hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.tg.nsb), dim3(kRasterThreads), 0,
                        a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tg,
-                       a.order, a.wave_cost, a.out, a.final_T, a.final_idx, a.log_index,
+                       a.order, a.wave_cost, a.out, a.out_planar, a.final_T, a.final_idx,
+                       a.log_index,
                        a.log_pool, a.log_units, a.log_per_entry, a.counts);
 }
 
@@ -1624,7 +1629,7 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                              const int32_t* tile_bins, const void* edges, const void* edge_culls,
                              const void* prim_recs, const float* background, int32_t img_h,
                              int32_t img_w, int32_t block_x, int32_t block_y,
-                             int32_t edges_per_segment, float* out_img,
+                             int32_t edges_per_segment, float* out_img, int32_t out_planar,
                              float* final_Ts, int32_t* final_idx, int64_t num_entries,
                              int32_t* log_index, void* log_pool, int64_t log_pool_bytes,
                              int32_t log_entry_units, unsigned long long* eval_counts,
@@ -1647,6 +1652,7 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
     RasterArgs a = raster_args(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                                background, img_h, img_w, tg, edges_per_segment, stream);
     a.out = out_img;
+    a.out_planar = out_planar ? 1 : 0;
     a.final_T = final_Ts;
     a.final_idx = final_idx;
     a.log_index = log_index;
@@ -1669,14 +1675,14 @@ extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted
                                     const void* edge_culls, const void* prim_recs,
                                     const float* background, int32_t img_h, int32_t img_w,
                                     int32_t block_x, int32_t block_y, int32_t edges_per_segment,
-                                    float* out_img, float* final_Ts, int32_t* final_idx,
-                                    int64_t num_entries, int32_t* log_index, void* log_pool,
-                                    int64_t log_pool_bytes, int32_t log_entry_units,
-                                    const int32_t* tile_order, uint32_t* wave_cost,
-                                    hipStream_t stream) {
+                                    float* out_img, int32_t out_planar, float* final_Ts,
+                                    int32_t* final_idx, int64_t num_entries, int32_t* log_index,
+                                    void* log_pool, int64_t log_pool_bytes,
+                                    int32_t log_entry_units, const int32_t* tile_order,
+                                    uint32_t* wave_cost, hipStream_t stream) {
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, block_x, block_y, edges_per_segment,
-                             out_img, final_Ts,
+                             out_img, out_planar, final_Ts,
                              final_idx, num_entries, log_index, log_pool, log_pool_bytes,
                              log_entry_units, nullptr, tile_order, wave_cost, stream);
 }
@@ -1686,18 +1692,18 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
                                             const void* edge_culls, const void* prim_recs,
                                             const float* background, int32_t img_h,
                                             int32_t img_w, int32_t block_x, int32_t block_y,
-                                            int32_t edges_per_segment,
-                                            float* out_img, float* final_Ts, int32_t* final_idx,
-                                            int64_t num_entries, int32_t* log_index,
-                                            void* log_pool, int64_t log_pool_bytes,
-                                            int32_t log_entry_units,
+                                            int32_t edges_per_segment, float* out_img,
+                                            int32_t out_planar, float* final_Ts,
+                                            int32_t* final_idx, int64_t num_entries,
+                                            int32_t* log_index, void* log_pool,
+                                            int64_t log_pool_bytes, int32_t log_entry_units,
                                             unsigned long long* eval_counts,
                                             const int32_t* tile_order, uint32_t* wave_cost,
                                             hipStream_t stream) {
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, block_x, block_y, edges_per_segment,
-                             out_img, final_Ts,
+                             out_img, out_planar, final_Ts,
                              final_idx, num_entries, log_index, log_pool, log_pool_bytes,
                              log_entry_units, eval_counts, tile_order, wave_cost, stream);
 }

@@ -14,7 +14,9 @@ here each direction is one kernel:
   sum the squared differences; one combining workgroup) and one backward
   kernel that writes ``g * (2 (x - y) / n - w dSSIM/dx)``;
 * ``clamp_mse_ssim_loss(img, y, w)``: the two above in one autograd node
-  whose backward writes the [H, W, 3] image gradient directly.
+  whose backward writes the [H, W, 3] image gradient directly; the
+  renderer's planar image needs no clamp pass at all (the SSIM forward reads
+  it clamped).
 
 Values equal the separate calls up to fp32 summation order; the autograd
 graph is shorter.
@@ -86,12 +88,14 @@ class _MseSsimLoss(torch.autograd.Function):
         ctx.x_dtype = x.dtype
         parts = out[1:]
         ctx.mark_non_differentiable(parts)
+        # No zero gradient is made for `parts` (non-differentiable).
+        ctx.set_materialize_grads(False)
         return out[0], parts
 
     @staticmethod
     def backward(ctx, grad_loss, _grad_parts):
         x, y, abc, g = ctx.saved_tensors
-        if not ctx.needs_input_grad[0]:
+        if not ctx.needs_input_grad[0] or grad_loss is None:
             return (None,) * 7
         n, c, h, w = x.shape
         gx = torch.empty_like(x)
@@ -101,6 +105,18 @@ class _MseSsimLoss(torch.autograd.Function):
                    ctx.win_size, N.ptr(abc), ctx.ssim_weight, N.ptr(go), N.ptr(gx),
                    N.stream(x.device))
         return gx.to(ctx.x_dtype), None, None, None, None, None, None
+
+
+def _planes_of(img: torch.Tensor):
+    """The three [H, W] planes behind an [H, W, 3] float32 view of them (the
+    renderer's image layout: strides (W, 1, H W)), or None for any other
+    layout."""
+    if img.dtype is not torch.float32 or img.dim() != 3 or img.shape[2] != 3:
+        return None
+    h, w = int(img.shape[0]), int(img.shape[1])
+    if img.is_contiguous() or img.stride() != (w, 1, h * w):
+        return None
+    return img.detach().permute(2, 0, 1)
 
 
 # Element counts of the loss's work buffers per (h, w, win_size):
@@ -124,8 +140,12 @@ class _ClampMseSsimLoss(torch.autograd.Function):
         N.require_gpu(img, "img")
         if img.dim() != 3 or img.shape[2] != 3:
             raise ValueError(f"img must be [H, W, 3], got {tuple(img.shape)}")
-        x32 = _as_f32(img, "img")
-        h, w = int(x32.shape[0]), int(x32.shape[1])
+        # The renderer's planar image is read in place (clamped on load);
+        # any other layout as a contiguous [H, W, 3] copy.
+        planes = _planes_of(img)
+        x32 = planes if planes is not None else _as_f32(img, "img")
+        planar = 1 if planes is not None else 0
+        h, w = int(img.shape[0]), int(img.shape[1])
         if tuple(y.shape) not in ((1, 3, h, w), (3, h, w)):
             raise ValueError(f"target must be [1, 3, {h}, {w}], got {tuple(y.shape)}")
         y32 = _as_f32(y, "target")
@@ -134,16 +154,20 @@ class _ClampMseSsimLoss(torch.autograd.Function):
         n_part, n_abc = _clamp_loss_sizes(h, w, int(win_size))
         if not ctx.needs_input_grad[0]:
             n_abc = 0
-        # clamp(img) as NCHW, the partial sums and the backward's SSIM terms in
-        # one work buffer; the three results in a buffer of their own.
-        work = torch.empty((3 * h * w + n_part + n_abc,), dtype=torch.float32, device=dev)
+        # clamp(img) as NCHW (not for planes), the partial sums and the
+        # backward's SSIM terms in one work buffer; the three results in a
+        # buffer of their own.
+        n_x = 0 if planar else 3 * h * w
+        work = torch.empty((n_x + n_part + n_abc,), dtype=torch.float32, device=dev)
         out = torch.empty((3,), dtype=torch.float32, device=dev)
         wp = work.data_ptr()
-        abc_p = wp + 4 * (3 * h * w + n_part) if n_abc else None
+        abc_p = wp + 4 * (n_x + n_part) if n_abc else None
         with N.prof("loss.clamp_mse_ssim"):
-            N.call("cs_clamp_mse_ssim_loss", N.ptr(x32), N.ptr(y32), h, w, float(lo), float(hi),
-                   N.ptr(g), int(win_size), float(c1), float(c2), float(ssim_weight), wp,
-                   wp + 4 * 3 * h * w, N.ptr(out), abc_p, N.stream(dev))
+            N.call("cs_clamp_mse_ssim_loss", x32.data_ptr(), planar, N.ptr(y32), h, w, float(lo),
+                   float(hi), N.ptr(g), int(win_size), float(c1), float(c2),
+                   float(ssim_weight), None if planar else wp, wp + 4 * n_x, N.ptr(out), abc_p,
+                   N.stream(dev))
+        ctx.planar = planar
         ctx.save_for_backward(x32, y32)
         # The SSIM terms stay in `work`, which lives as long as this node (a
         # second backward through a retained graph reads them again).
@@ -154,14 +178,17 @@ class _ClampMseSsimLoss(torch.autograd.Function):
         ctx.x_dtype = img.dtype
         parts = out[1:]
         ctx.mark_non_differentiable(parts)
+        # No zero gradient is made for `parts` (non-differentiable).
+        ctx.set_materialize_grads(False)
         return out[0], parts
 
     @staticmethod
     def backward(ctx, grad_loss, _grad_parts):
-        if not ctx.needs_input_grad[0]:
+        if not ctx.needs_input_grad[0] or grad_loss is None:
             return (None,) * 9
         x, y = ctx.saved_tensors
-        h, w = int(x.shape[0]), int(x.shape[1])
+        h, w = (int(x.shape[1]), int(x.shape[2])) if ctx.planar else (int(x.shape[0]),
+                                                                       int(x.shape[1]))
         # The image gradient is written as three [H, W] planes (whole-line
         # writes) and returned as an [H, W, 3] view of them; the renderer's
         # backward reads that layout in place (splat.image_grad_layout).
@@ -171,9 +198,9 @@ class _ClampMseSsimLoss(torch.autograd.Function):
             go = go.to(torch.float32)
         abc_p = ctx.work.data_ptr() + ctx.abc_off
         with N.prof("loss.clamp_mse_ssim_bwd"):
-            N.call("cs_clamp_mse_ssim_backward", N.ptr(x), N.ptr(y), h, w, ctx.lo, ctx.hi,
-                   N.ptr(ctx.g), ctx.win_size, abc_p, ctx.ssim_weight, go.data_ptr(),
-                   planes.data_ptr(), 1, N.stream(x.device))
+            N.call("cs_clamp_mse_ssim_backward", x.data_ptr(), ctx.planar, N.ptr(y), h, w,
+                   ctx.lo, ctx.hi, N.ptr(ctx.g), ctx.win_size, abc_p, ctx.ssim_weight,
+                   go.data_ptr(), planes.data_ptr(), 1, N.stream(x.device))
         gi = planes.permute(1, 2, 0)
         if ctx.x_dtype is not torch.float32:
             gi = gi.to(ctx.x_dtype)
@@ -184,10 +211,12 @@ def clamp_mse_ssim_loss(img, y, ssim_weight: float = 0.2, *, lo: float = 0.0, hi
                         win_size: int = 11, win_sigma: float = 1.5, data_range: float = 1.0,
                         k1: float = 0.01, k2: float = 0.03):
     """``mse_ssim_loss(img.clamp(lo, hi).permute(2, 0, 1).unsqueeze(0), y, ssim_weight)``
-    from the renderer's [H, W, 3] image: one clamp/layout pass forward (the
-    SSIM forward also sums the MSE), and a backward that reads the image
-    itself and writes the [H, W, 3] gradient with the clamp's mask, so the
-    glue has no gradient pass.  Returns (loss, [MSE, SSIM])."""
+    from the renderer's [H, W, 3] image.  The renderer's planar image (an
+    [H, W, 3] view of three planes) is read in place, clamped on load; another
+    layout takes one clamp/layout pass first.  The SSIM forward also sums the
+    MSE; the backward reads the image itself and writes the [H, W, 3]
+    gradient (a view of three planes) with the clamp's mask, so the glue has
+    no gradient pass.  Returns (loss, [MSE, SSIM])."""
     if win_size <= 0 or win_size % 2 == 0:
         raise ValueError("win_size must be odd")
     if data_range <= 0.0:

@@ -524,7 +524,11 @@ def _read_log_use_later(key, pool: torch.Tensor, units: int, first_shared: int,
 
 def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log: bool = True,
                       log_pool_bytes_override: Optional[int] = None):
-    """(image [H,W,3], final_Ts, final_idx).  With eval_counts (int64 [5],
+    """(image [H,W,3], final_Ts, final_idx).  The image is an [H, W, 3] view of
+    three [H, W] planes (strides (W, 1, H W)): the caller's
+    clamp(0, 1).permute(2, 0, 1) (gaussian_trace/render.py:1309-1310) then
+    gives a contiguous [3, H, W] tensor without a copy, and the fused loss
+    reads the planes in place.  With eval_counts (int64 [5],
     zeroed, on the device) the counting instantiation runs and adds the
     evaluation counts of cs_rasterize_forward_counted into it.  With log (the
     default) it writes the raster log its backward reads (b.log_index,
@@ -537,7 +541,8 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
     (b.tile_order) and the following forwards take."""
     dev = b.device
     H, W = b.img_h, b.img_w
-    out = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
+    planes = torch.empty((3, H, W), dtype=torch.float32, device=dev)
+    out = planes.permute(1, 2, 0)
     nsub, wpt = b.nsub, b.waves_per_tile
     cap = max(int(b.primitive_ids_sorted.numel()), 1)
     # final_Ts, final_idx and the log's entry index share one allocation.
@@ -569,7 +574,8 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
     base = aux.data_ptr()
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), H, W, b.block_x,
-            b.block_y, b.edges_per_segment, N.ptr(out), base, base + 4 * H * W, *log_args)
+            b.block_y, b.edges_per_segment, planes.data_ptr(), 1, base, base + 4 * H * W,
+            *log_args)
     cost = b.ptr("wave_cost") if remake else None
     prev_p = None if prev is None else prev.data_ptr()
     if eval_counts is not None:

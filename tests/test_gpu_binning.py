@@ -11,6 +11,10 @@ SCENES = {
     "small_fill": lambda: synth.small_scene(0),
     "small_fill_big": lambda: synth.small_scene(3, P=40, h=100, w=130, rmax=60.0),
     "small_stroke": lambda: synth.small_scene(1, stroke=True),
+    # One tile column: no spare tile_scratch word, so the segment scan runs
+    # as a launch of its own; and two row segments per tile row.
+    "narrow_fill": lambda: synth.small_scene(4, P=12, h=100, w=16, rmax=20.0),
+    "wide_fill": lambda: synth.small_scene(5, P=30, h=40, w=1100, rmax=60.0),
     "cfg1": lambda: synth.make_scene(1),
     "cfg2": lambda: synth.make_scene(2),
     "cfg3": lambda: synth.make_scene(3),
