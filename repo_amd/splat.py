@@ -503,12 +503,26 @@ def log_layout(key, capacity: int, nsub: int, waves_per_tile: int = 2):
     return units, (16 + regions + shared + 255) // 256 * 256
 
 
+# The pool's use is read back from every LOG_READ_EVERY-th forward of a shape
+# (the first one included); each read is a device-to-host copy in the stream.
+LOG_READ_EVERY = 4
+_LOG_READ_AGE: "dict[tuple, int]" = {}
+
+
 def _read_log_use_later(key, pool: torch.Tensor, units: int, first_shared: int,
                         pool_bytes: int, st) -> None:
     """Queues a copy of the pool's counter into pinned memory and an event after
-    it, unless one for this shape is still outstanding."""
+    it, unless one for this shape is still outstanding or this forward is not
+    one of every LOG_READ_EVERY."""
     if key in _LOG_PENDING:
         return
+    age = _LOG_READ_AGE.get(key, LOG_READ_EVERY - 1) + 1
+    if len(_LOG_READ_AGE) >= _MAX_LOG_KEYS and key not in _LOG_READ_AGE:
+        _LOG_READ_AGE.pop(next(iter(_LOG_READ_AGE)))
+    if age < LOG_READ_EVERY:
+        _LOG_READ_AGE[key] = age
+        return
+    _LOG_READ_AGE[key] = 0
     dev = pool.device.index if pool.device.index is not None else torch.cuda.current_device()
     entry = _take_pinned(dev)
     hip = N.hip()
