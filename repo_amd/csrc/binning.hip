@@ -695,28 +695,37 @@ __device__ __forceinline__ int rank_in_block(const uint4* ks, uint32_t ki, int t
     return r;
 }
 
-// One primitive of k_prim_prep; returns its depth key.
-__device__ __forceinline__ uint32_t prim_prep_one(
-    const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
+// One primitive's outputs of k_prim_prep.
+struct PrimPrep {
+    int4 tr;           // tile rectangle
+    uint32_t area;     // tiles in it
+    float inv_sigma2;  // clamped width's 1 / sigma^2
+    uint32_t key;      // depth key
+    bool bad;          // invalid CSR offsets
+    PrimRec rec;
+};
+
+// One primitive of k_prim_prep, computed (no stores).  Every load depends on
+// p only, so with a wave-uniform p they are scalar loads.
+__device__ __forceinline__ PrimPrep prim_prep_compute(
+    const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets,
     const int32_t* __restrict__ seg_tile_ranges, const SegRec* __restrict__ seg_recs,
     const float* __restrict__ colors, const float* __restrict__ opacities,
     const float* __restrict__ depths, const int32_t* __restrict__ fill_rules,
     const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
-    int eps, const int32_t* __restrict__ seg_edge_offsets, int tbx, int tby, int mode,
-    int32_t* __restrict__ status, int32_t* __restrict__ prim_tile_ranges,
-    uint32_t* __restrict__ counts, float* __restrict__ inv_sigma2s, uint32_t* __restrict__ keys,
-    int32_t* __restrict__ vals, PrimRec* __restrict__ recs, int p) {
+    int eps, const int32_t* __restrict__ seg_edge_offsets, int tbx, int tby, int mode, int p) {
+    PrimPrep o;
     int s0 = seg_offsets[p], s1 = seg_offsets[p + 1];
     // Invalid CSR offsets are reported through status[1] and clamped so that
     // no kernel reads outside the segment arrays.
-    if (s0 < 0 || s1 < s0 || s1 > nseg) {
-        atomicOr(status + 1, 1);
+    o.bad = s0 < 0 || s1 < s0 || s1 > nseg;
+    if (o.bad) {
         s0 = clampi(s0, 0, nseg);
         s1 = clampi(s1, s0, nseg);
     }
     // cubic_splatting.py:2103-2135
-    int4 tr = make_int4(0, 0, 0, 0);
-    uint32_t area = 0;
+    o.tr = make_int4(0, 0, 0, 0);
+    o.area = 0;
     if (s1 > s0) {
         int mnx = tbx, mny = tby, mxx = 0, mxy = 0;
         for (int s = s0; s < s1; ++s) {
@@ -724,23 +733,19 @@ __device__ __forceinline__ uint32_t prim_prep_one(
             mnx = min(mnx, r.x); mny = min(mny, r.y);
             mxx = max(mxx, r.z); mxy = max(mxy, r.w);
         }
-        tr = make_int4(mnx, mny, mxx, mxy);
-        area = (uint32_t)(max(0, mxx - mnx) * max(0, mxy - mny));
+        o.tr = make_int4(mnx, mny, mxx, mxy);
+        o.area = (uint32_t)(max(0, mxx - mnx) * max(0, mxy - mny));
     }
-    reinterpret_cast<int4*>(prim_tile_ranges)[p] = tr;
-    counts[p] = area;
 
     // cubic_splatting.py:2820-2821 (widths clamp, inv_sigma2) and the cull distance.
     const PrimParams q = prim_params(mode, aa_widths[p], opacities[p], stroke_widths, p);
-    inv_sigma2s[p] = q.inv_sigma2;
+    o.inv_sigma2 = q.inv_sigma2;
 
     // cubic_splatting.py:801-805: float order as unsigned order.
     const int32_t bits = __builtin_bit_cast(int32_t, depths[p]);
-    const uint32_t key = (uint32_t)(bits ^ ((bits >> 31) | (int32_t)0x80000000));
-    keys[p] = key;
-    vals[p] = p;
+    o.key = (uint32_t)(bits ^ ((bits >> 31) | (int32_t)0x80000000));
 
-    PrimRec rec;
+    PrimRec& rec = o.rec;
     rec.r = colors[3 * p];
     rec.g = colors[3 * p + 1];
     rec.b = colors[3 * p + 2];
@@ -779,8 +784,25 @@ __device__ __forceinline__ uint32_t prim_prep_one(
     rec.nx_span = span_x(nx);
     rec.x_last = x_last;
     rec.cull_out = cull_distance_outside(mode, opacities[p], q.inv_sigma, q.half_sw);
-    recs[p] = rec;
-    return key;
+    return o;
+}
+
+// Stores primitive p's outputs of k_prim_prep.
+__device__ __forceinline__ void prim_prep_store(const PrimPrep& o, int p,
+                                                int32_t* __restrict__ status,
+                                                int32_t* __restrict__ prim_tile_ranges,
+                                                uint32_t* __restrict__ counts,
+                                                float* __restrict__ inv_sigma2s,
+                                                uint32_t* __restrict__ keys,
+                                                int32_t* __restrict__ vals,
+                                                PrimRec* __restrict__ recs) {
+    if (o.bad) atomicOr(status + 1, 1);
+    reinterpret_cast<int4*>(prim_tile_ranges)[p] = o.tr;
+    counts[p] = o.area;
+    inv_sigma2s[p] = o.inv_sigma2;
+    keys[p] = o.key;
+    vals[p] = p;
+    recs[p] = o.rec;
 }
 
 __global__ __launch_bounds__(256) void k_prim_prep(
@@ -798,11 +820,14 @@ __global__ __launch_bounds__(256) void k_prim_prep(
     static_assert(kRankBlock == 256, "one rank block per workgroup");
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     uint32_t key = 0xffffffffu;
-    if (p < P) key = prim_prep_one(cubics_norm, seg_offsets, P, seg_tile_ranges, seg_recs,
-                                   colors, opacities, depths, fill_rules, aa_widths,
-                                   stroke_widths, nseg, eps, seg_edge_offsets, tbx, tby, mode,
-                                   status, prim_tile_ranges, counts, inv_sigma2s, keys, vals,
-                                   recs, p);
+    if (p < P) {
+        const PrimPrep o = prim_prep_compute(cubics_norm, seg_offsets, seg_tile_ranges, seg_recs,
+                                             colors, opacities, depths, fill_rules, aa_widths,
+                                             stroke_widths, nseg, eps, seg_edge_offsets, tbx,
+                                             tby, mode, p);
+        prim_prep_store(o, p, status, prim_tile_ranges, counts, inv_sigma2s, keys, vals, recs);
+        key = o.key;
+    }
     if (block_sorted) {
         // The first stage of the depth rank (as k_rank_blocks).
         __shared__ uint4 ks[kRankBlock / 4];
@@ -1155,7 +1180,7 @@ __global__ __launch_bounds__(256) void k_rank_allpairs(
 }
 
 // Depth key of a float: its order as unsigned order (cubic_splatting.py:801-805),
-// as prim_prep_one computes it.
+// as prim_prep_compute computes it.
 __device__ __forceinline__ uint32_t depth_key(float d) {
     const int32_t bits = __builtin_bit_cast(int32_t, d);
     return (uint32_t)(bits ^ ((bits >> 31) | (int32_t)0x80000000));
@@ -1164,9 +1189,10 @@ __device__ __forceinline__ uint32_t depth_key(float d) {
 // k_prim_prep and k_rank_allpairs<false> in one launch, for at most
 // kRankPairsMax primitives: one wave per primitive counts the keys that
 // precede its own (lane-parallel, the keys computed from the depths, since no
-// other wave's keys are written yet), and lane 0 makes the primitive's
-// records (prim_prep_one) and writes order[pos] = p, rank_rects[pos] = its
-// tile rectangle.
+// other wave's keys are written yet); the primitive's records are computed
+// wave-uniformly (scalar loads, issued before the counting loop's vector
+// loads are waited for) and lane 0 stores them and writes order[pos] = p,
+// rank_rects[pos] = its tile rectangle.
 __global__ __launch_bounds__(256) void k_prim_prep_rank(
     const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
     const int32_t* __restrict__ seg_tile_ranges, const SegRec* __restrict__ seg_recs,
@@ -1181,7 +1207,11 @@ __global__ __launch_bounds__(256) void k_prim_prep_rank(
     const int p = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     if (p >= P) return;
     const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t ki = depth_key(depths[p]);
+    const PrimPrep o = prim_prep_compute(cubics_norm, seg_offsets, seg_tile_ranges, seg_recs,
+                                         colors, opacities, depths, fill_rules, aa_widths,
+                                         stroke_widths, nseg, eps, seg_edge_offsets, tbx, tby,
+                                         mode, p);
+    const uint32_t ki = o.key;
     int cnt = 0;
     const int n4 = P & ~3;
     const bool vec = (reinterpret_cast<uintptr_t>(depths) & 15) == 0;
@@ -1205,13 +1235,9 @@ __global__ __launch_bounds__(256) void k_prim_prep_rank(
     }
     const int pos = wave_sum_i(cnt);
     if (lane == 0) {
-        prim_prep_one(cubics_norm, seg_offsets, P, seg_tile_ranges, seg_recs, colors, opacities,
-                      depths, fill_rules, aa_widths, stroke_widths, nseg, eps, seg_edge_offsets,
-                      tbx, tby, mode, status, prim_tile_ranges, counts, inv_sigma2s, keys, vals,
-                      recs, p);
+        prim_prep_store(o, p, status, prim_tile_ranges, counts, inv_sigma2s, keys, vals, recs);
         order[pos] = p;
-        // The rectangle this thread has just written.
-        rank_rects[pos] = reinterpret_cast<const int4*>(prim_tile_ranges)[p];
+        rank_rects[pos] = o.tr;
     }
 }
 

@@ -597,9 +597,11 @@ __device__ __forceinline__ void composite(const PrimRec& pr, float alpha, int g,
 // record, compositing.  When both pixel rows of the lanes have exact pixels
 // and they fit in one wave, they are gathered into lanes 0 .. n-1 with
 // ds_permute, so the exact coverage (sqrt, exp, divide) runs once instead of
-// once per row.
+// once per row.  Eight waves per SIMD (the register budget that allows; a
+// few scalar values then live in vector-register lanes): the edge walks wait
+// on scalar loads, and more waves hide more of that wait.
 template <int MODE, bool COUNT>
-__global__ __launch_bounds__(kRasterThreads) void k_raster_fwd(
+__global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(8))) void k_raster_fwd(
     const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
