@@ -127,6 +127,40 @@ __device__ __forceinline__ int owner_of(const int32_t* __restrict__ offs, int P,
     return lo;
 }
 
+// owner_of for segment base + lane, where base is the first of a wave's 64
+// consecutive segments; every lane of the wave must be active.  The first
+// segment's owner by a 64-way search (one offset per lane per step, so
+// ceil(log64 P) dependent loads instead of log2 P), then each lane counts
+// the primitive boundaries at or below its segment among the next 64 offsets
+// (staged in sh[64]); a lane that finds all 64 below it (runs of primitives
+// without segments) searches on its own.  Offsets that are not
+// non-decreasing (reported through status) give some index in [0, P).
+__device__ int wave_owner(const int32_t* __restrict__ offs, int P, int base, int32_t* sh) {
+    const int lane = threadIdx.x & (kWave - 1);
+    int lo = 0, hi = P - 1;   // wave-uniform; the owner lies in [lo, hi]
+    while (hi - lo >= kWave) {
+        const int step = (hi - lo + kWave) / kWave;
+        const int idx = lo + lane * step;
+        const uint64_t m = __ballot(idx <= hi && offs[idx] <= base);
+        lo += m ? (kWave - 1 - __builtin_clzll(m)) * step : 0;
+        hi = min(hi, lo + step - 1);
+    }
+    {
+        const int idx = lo + lane;
+        const uint64_t m = __ballot(idx <= hi && offs[idx] <= base);
+        lo += m ? kWave - 1 - __builtin_clzll(m) : 0;
+    }
+    const int bi = lo + 1 + lane;
+    sh[lane] = bi < P ? offs[bi] : INT32_MAX;
+    const int seg = base + lane;
+    int c = 0;
+#pragma unroll
+    for (int step = kWave / 2; step >= 1; step >>= 1)
+        if (sh[c + step - 1] <= seg) c += step;
+    if (c == kWave - 1 && sh[kWave - 1] <= seg) return owner_of(offs, P, seg);
+    return lo + c;
+}
+
 // Conservative distance beyond which a pixel's coverage of this primitive is
 // decided without its exact distance: fill -> alpha < 1/255 outside, coverage
 // exactly 1.0f inside (1 / (1 + exp(-2 d inv_sigma)) evaluated in fp32 with
@@ -489,6 +523,7 @@ __global__ __launch_bounds__(kWave * kFlattenWaves) void k_project_flatten_wave(
     static_assert(L >= 2 && L <= kWave && (L & (L - 1)) == 0, "group of lanes");
     constexpr int G = kWave / L;  // segments per flattening step
     __shared__ float stage[9][kWave];
+    __shared__ int32_t bounds[kWave];
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         status[0] = 0;
         status[1] = 0;
@@ -499,9 +534,9 @@ __global__ __launch_bounds__(kWave * kFlattenWaves) void k_project_flatten_wave(
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t base = (int64_t)blockIdx.x * kWave;
     const int nw = (int)min((int64_t)kWave, (int64_t)nseg - base);
+    const int p = w == 0 ? wave_owner(seg_offsets, P, (int)base, bounds) : 0;
     if (w == 0 && lane < nw) {
         const int s = (int)base + lane;
-        const int p = owner_of(seg_offsets, P, s);
         const float wd = fmaxf(aa_widths[p], kWidthMin);
         const float support = fmaxf(0.0f, wd * 3.0f);
         const float half_sw = stroke_widths ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;

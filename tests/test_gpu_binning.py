@@ -50,6 +50,48 @@ def test_binning_bit_exact(name):
     np.testing.assert_array_equal(b.tile_bins.cpu().numpy(), ob["tile_bins"])
 
 
+def _with_empty_primitives(sc, runs):
+    """Scene sc with runs[i] primitives without segments inserted before
+    primitive i (their attributes copied from primitive i)."""
+    import dataclasses
+    offs = sc.seg_offsets.tolist()
+    P = len(offs) - 1
+    new_offs, src = [0], []
+    for i in range(P):
+        for _ in range(runs[i]):
+            new_offs.append(offs[i])
+            src.append(i)
+        new_offs.append(offs[i + 1])
+        src.append(i)
+    idx = torch.tensor(src)
+    return dataclasses.replace(
+        sc, seg_offsets=torch.tensor(new_offs, dtype=torch.int32), colors=sc.colors[idx],
+        opacities=sc.opacities[idx], depths=sc.depths[idx] + 1e-3 * torch.arange(len(src)),
+        aa_widths=sc.aa_widths[idx], fill_rules=sc.fill_rules[idx])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("runs", [(0, 1, 0, 3, 0, 0, 2, 0, 0, 1), (0, 70, 0, 0, 130, 1, 0, 64, 0, 0)])
+def test_binning_bit_exact_with_primitives_without_segments(runs):
+    """Primitives without segments (repeated offsets), also in runs longer
+    than a wave's 64 offsets (where a segment's owner is searched on its
+    own): binning bit-exact against the oracle."""
+    sc = _with_empty_primitives(synth.small_scene(6, P=10, nseg=4, h=70, w=90, rmax=30.0), runs)
+    print(f"[binning empty prims] P={sc.num_primitives}", flush=True)
+    b, _ = hip_bin(sc)
+    d = scene_np(sc)
+    ob = O.bin_scene(d["cubics_norm"], d["offs"], d["depths"], d["aa_widths"], d["img_h"],
+                     d["img_w"], d["S"])
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(b.cubics_px.cpu().numpy()), _bits(ob["cubics_px"]))
+    np.testing.assert_array_equal(b.seg_tile_ranges.cpu().numpy(), ob["seg_tile_ranges"])
+    np.testing.assert_array_equal(b.prim_tile_ranges.cpu().numpy(), ob["prim_tile_ranges"])
+    np.testing.assert_array_equal(_bits(b.edges_px().cpu().numpy()), _bits(ob["edges"]))
+    np.testing.assert_array_equal(b.primitive_ids_sorted.cpu().numpy(),
+                                  ob["primitive_ids_sorted"])
+    np.testing.assert_array_equal(b.tile_bins.cpu().numpy(), ob["tile_bins"])
+
+
 @pytest.mark.gpu
 def test_binning_ties_stable_by_primitive_id():
     """Equal depths (the training default, depth = sigmoid(1)) order each tile
