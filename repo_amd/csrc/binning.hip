@@ -12,11 +12,12 @@
 //                      the merge ranks the keys.
 //   depth rank         stable rank of the 32-bit depth keys (ties by
 //                      primitive id): all-pairs counting up to 8K
-//                      primitives, merge of the ranked blocks by binary
-//                      search up to 16K, LSD radix sort above.
+//                      primitives (in one launch with the primitive records,
+//                      k_prim_prep_rank), merge of the ranked blocks by
+//                      binary search up to 16K, LSD radix sort above.
 //   k_tile_counts      per-tile counts of the primitives whose tile rectangle
-//                      covers the tile, per row segment of 64 tiles.
-//   exclusive scan     segment totals -> first slot of each segment, total I.
+//                      covers the tile, per row segment of 64 tiles; each
+//                      segment's first slot and the total I in closed form.
 //   k_tile_scatter     each tile's primitives, in rank order, into its slots;
 //                      tile_bins [start, end) per tile.
 //
@@ -1064,6 +1065,12 @@ constexpr int kMergeKeys = kWave;  // keys per workgroup, 64 per key group
 constexpr int kMergeWaves = 16;    // waves per key group, each a 16th of the blocks
 constexpr int kMergeThreads = kMergeKeys * kMergeWaves;
 
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, kWave);
+    return v;
+}
+
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
@@ -1298,9 +1305,12 @@ __global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ a, int n
 //   counting launch: the waves stride over all ranks (eight 64-rank loads in
 //     flight per wave); each rectangle that meets the segment adds +1 at its
 //     first column and -1 past its last in an LDS difference array, whose
-//     prefix sum is the per-tile count: tile_count, and the segment's total
-//     in seg_scratch[seg];
-//   exclusive scan of the segment totals (in place; its total is I);
+//     prefix sum is the per-tile count: tile_count.  The segment's first slot
+//     (the entries of all tiles before it in row-major order) is a sum over
+//     the same rectangles in closed form -- each one's tiles in the rows
+//     above plus those left of the segment in its row -- so no scan of the
+//     segment totals is needed: seg_scratch[seg]; workgroup 0 also sums the
+//     rectangles' areas into the total I;
 //   scatter launch: tile start = segment start + prefix of the segment's tile
 //     totals (wave 0 writes tile_bins), then the ranks in chunks of
 //     kListChunk:
@@ -1328,10 +1338,25 @@ __device__ __forceinline__ bool rect_meets_row(const int4& q, int ty, int sx0, i
     return q.y <= ty && ty < q.w && q.x < sx1 && q.z > sx0;
 }
 
+// Tiles of rectangle q (clipped to the tbx-column grid) that precede tile
+// (sx0, ty) in row-major order: its tiles in rows above ty and those left of
+// column sx0 in row ty.  `total` receives all its tiles.
+__device__ __forceinline__ uint32_t rect_tiles_before(const int4& q, int ty, int sx0, int tbx,
+                                                      uint32_t& total) {
+    const int x0 = max(q.x, 0), x1 = min(q.z, tbx), y0 = max(q.y, 0);
+    const uint32_t wd = (uint32_t)max(0, x1 - x0);
+    total = (uint32_t)max(0, q.w - y0) * wd;
+    const uint32_t above = (uint32_t)max(0, min(q.w, ty) - y0) * wd;
+    const bool in_row = y0 <= ty && ty < q.w;
+    return above + (in_row ? (uint32_t)max(0, min(x1, sx0) - x0) : 0u);
+}
+
 __global__ __launch_bounds__(kWave * kListWaves) void k_tile_counts(
     const int4* __restrict__ rank_rects, int P, int tbx, int nsegcols,
-    uint32_t* __restrict__ tile_count, uint32_t* __restrict__ seg_scratch) {
+    uint32_t* __restrict__ tile_count, uint32_t* __restrict__ seg_scratch,
+    int32_t* __restrict__ total_out) {
     __shared__ int diff[kSegTiles + 1];
+    __shared__ uint32_t part[2][kListWaves];
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     const int lane = threadIdx.x & (kWave - 1);
     const int ty = blockIdx.x / nsegcols;
@@ -1339,6 +1364,9 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_counts(
     const int sx1 = min(sx0 + kSegTiles, tbx);
     if (threadIdx.x <= kSegTiles) diff[threadIdx.x] = 0;
     __syncthreads();
+    // Sums mod 2^32, as the list positions are formed (a total beyond int32 is
+    // reported by the caller).
+    uint32_t before = 0, total = 0;
     for (int r0 = w * kWave * kListSteps; r0 < P; r0 += kListWaves * kWave * kListSteps) {
         int4 tr[kListSteps];
 #pragma unroll
@@ -1349,19 +1377,36 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_counts(
 #pragma unroll
         for (int k = 0; k < kListSteps; ++k) {
             const int4 q = tr[k];
+            uint32_t area;
+            before += rect_tiles_before(q, ty, sx0, tbx, area);
+            total += area;
             if (rect_meets_row(q, ty, sx0, sx1)) {
                 atomicAdd(&diff[max(q.x, sx0) - sx0], 1);
                 atomicAdd(&diff[min(q.z, sx1) - sx0], -1);
             }
         }
     }
+    before = wave_sum_u(before);
+    total = wave_sum_u(total);
+    if (lane == 0) {
+        part[0][w] = before;
+        part[1][w] = total;
+    }
     __syncthreads();
     if (w == 0) {
         const uint32_t n = (uint32_t)wave_incl_scan((uint32_t)diff[lane], lane);
         const bool tile_ok = sx0 + lane < sx1;
         if (tile_ok) tile_count[(size_t)ty * tbx + sx0 + lane] = n;
-        const uint32_t seg = (uint32_t)wave_sum_i(tile_ok ? (int)n : 0);
-        if (lane == 0) seg_scratch[blockIdx.x] = seg;
+        if (lane == 0) {
+            uint32_t b = 0, t = 0;
+#pragma unroll
+            for (int v = 0; v < kListWaves; ++v) {
+                b += part[0][v];
+                t += part[1][v];
+            }
+            seg_scratch[blockIdx.x] = b;
+            if (blockIdx.x == 0) *total_out = (int32_t)t;
+        }
     }
 }
 
@@ -1869,9 +1914,9 @@ static int rank_and_count(bool blocks_ranked, uint32_t* keys, int32_t* order,
     }
     const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
     hipLaunchKernelGGL(k_tile_counts, dim3(nsegcols * tby), dim3(kWave * kListWaves), 0,
-                       stream, rank_rects, nprim, tbx, nsegcols, tile_count, tile_scratch);
-    return cs_scan_exclusive_u32(tile_scratch, tile_scratch, nsegcols * tby, scan_temp, status,
-                                 stream);
+                       stream, rank_rects, nprim, tbx, nsegcols, tile_count, tile_scratch,
+                       status);
+    return launch_status();
 }
 
 // Flatness tolerance of the adaptive flattening, px
