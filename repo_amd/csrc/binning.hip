@@ -1338,16 +1338,16 @@ __device__ __forceinline__ bool rect_meets_row(const int4& q, int ty, int sx0, i
     return q.y <= ty && ty < q.w && q.x < sx1 && q.z > sx0;
 }
 
-// Tiles of rectangle q (clipped to the tbx-column grid) that precede tile
+// Tiles of rectangle q (clipped to the tbx x tby grid) that precede tile
 // (sx0, ty) in row-major order: its tiles in rows above ty and those left of
 // column sx0 in row ty.  `total` receives all its tiles.
 __device__ __forceinline__ uint32_t rect_tiles_before(const int4& q, int ty, int sx0, int tbx,
-                                                      uint32_t& total) {
-    const int x0 = max(q.x, 0), x1 = min(q.z, tbx), y0 = max(q.y, 0);
+                                                      int tby, uint32_t& total) {
+    const int x0 = max(q.x, 0), x1 = min(q.z, tbx), y0 = max(q.y, 0), y1 = min(q.w, tby);
     const uint32_t wd = (uint32_t)max(0, x1 - x0);
-    total = (uint32_t)max(0, q.w - y0) * wd;
-    const uint32_t above = (uint32_t)max(0, min(q.w, ty) - y0) * wd;
-    const bool in_row = y0 <= ty && ty < q.w;
+    total = (uint32_t)max(0, y1 - y0) * wd;
+    const uint32_t above = (uint32_t)max(0, min(y1, ty) - y0) * wd;
+    const bool in_row = y0 <= ty && ty < y1;
     return above + (in_row ? (uint32_t)max(0, min(x1, sx0) - x0) : 0u);
 }
 
@@ -1367,6 +1367,7 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_counts(
     // Sums mod 2^32, as the list positions are formed (a total beyond int32 is
     // reported by the caller).
     uint32_t before = 0, total = 0;
+    const int tby = (int)gridDim.x / nsegcols;
     for (int r0 = w * kWave * kListSteps; r0 < P; r0 += kListWaves * kWave * kListSteps) {
         int4 tr[kListSteps];
 #pragma unroll
@@ -1378,7 +1379,7 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_counts(
         for (int k = 0; k < kListSteps; ++k) {
             const int4 q = tr[k];
             uint32_t area;
-            before += rect_tiles_before(q, ty, sx0, tbx, area);
+            before += rect_tiles_before(q, ty, sx0, tbx, tby, area);
             total += area;
             if (rect_meets_row(q, ty, sx0, sx1)) {
                 atomicAdd(&diff[max(q.x, sx0) - sx0], 1);
