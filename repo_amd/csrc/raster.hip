@@ -560,7 +560,16 @@ __device__ __forceinline__ void log_flush(uint4* __restrict__ pool, const uint4*
     // position and size stay scalar values.
     const uint32_t lane = threadIdx.x & (kWave - 1);
     for (uint32_t u0 = 0; u0 < st.n; u0 += kWave)
-        if (u0 + lane < st.n) pool[st.base + u0 + lane] = stage[u0 + lane];
+        if (u0 + lane < st.n) {
+            // Streaming stores: the backward reads the log long after the
+            // loss kernels, which want the caches for the image and target.
+            const uint4 v = stage[u0 + lane];
+            uint4* d = pool + st.base + u0 + lane;
+            __builtin_nontemporal_store(v.x, &d->x);
+            __builtin_nontemporal_store(v.y, &d->y);
+            __builtin_nontemporal_store(v.z, &d->z);
+            __builtin_nontemporal_store(v.w, &d->w);
+        }
     st.n = 0;
 }
 
@@ -803,7 +812,8 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
                 composite(pr, fminf(kAlphaCap, pr.opacity * cov[p]), g, T[p], C0[p], C1[p],
                           C2[p], cur[p], done[p]);
         }
-        if ((logged >> lane) & 1u) log_index[(size_t)tg.waves * gl + sb.slot] = idx_l;
+        if ((logged >> lane) & 1u)
+            __builtin_nontemporal_store(idx_l, log_index + (size_t)tg.waves * gl + sb.slot);
     }
     if (log_index) log_flush(log_pool, stage, st);
     // The image as [H, W, 3], or as three [H, W] planes (out_planar).
@@ -812,8 +822,8 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     for (int p = 0; p < kPix; ++p) {
         if (!L.in_img[p]) continue;
         const size_t pix = (size_t)L.i[p] * img_w + L.j;
-        final_T[pix] = T[p];
-        final_idx[pix] = cur[p];
+        __builtin_nontemporal_store(T[p], final_T + pix);
+        __builtin_nontemporal_store(cur[p], final_idx + pix);
         float* const o = out + (out_planar ? pix : 3 * pix);
         o[0] = __builtin_fmaf(T[p], bg[0], C0[p]);
         o[ch] = __builtin_fmaf(T[p], bg[1], C1[p]);
