@@ -920,6 +920,10 @@ constexpr uint32_t kGradBufRecs = 256;   // 4 KiB of LDS per wave
 // adds the copies into the caller's arrays and clears them.
 constexpr int kGradReplicas = 8;
 
+// Largest edges-per-segment count whose accumulation weights the backward
+// keeps in an LDS table.
+constexpr int kBasisTable = 64;
+
 template <int NV>
 __global__ __launch_bounds__(256) void k_prim_rep_reduce(float* __restrict__ rep, int nprim,
                                                         float* __restrict__ v_col,
@@ -1034,6 +1038,19 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     const int slot = reduce8_slot(lane & 7);
     const bool adder = (lane & ~7) == 8;
     __shared__ GradRec grad_rec_all[kRasterThreads / kWave][kGradBufRecs];
+    // Uniform flattening with at most kBasisTable edges per segment: the
+    // accumulation weights at t = e / eps for every e, computed once per
+    // workgroup with seg_basis (so the same values) and read per pixel.
+    __shared__ float4 basis_tab[kBasisTable + 1];
+    const bool use_tab = !ADAPTIVE && eps <= kBasisTable;
+    if (use_tab) {
+        for (int e = (int)threadIdx.x; e <= eps; e += kRasterThreads) {
+            float bb[4];
+            seg_basis(e, inv_e, bb);
+            basis_tab[e] = make_float4(bb[0], bb[1], bb[2], bb[3]);
+        }
+        __syncthreads();
+    }
     GradBuf gbuf{grad_rec_all[wv], 0u};
     // Entries from gstart down to g0 in chunks of 64: lane k tests entry
     // gc - k with the forward's primitive cull, and the wave visits the
@@ -1273,8 +1290,14 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             } else {
                 gseg[p] = div_eps(G[p].best, eps, eps_magic);
                 const int el = G[p].best - gseg[p] * eps;
-                seg_basis(el, inv_e, bs);
-                seg_basis(el + 1, inv_e, be);
+                if (use_tab) {
+                    const float4 ta = basis_tab[el], tb = basis_tab[el + 1];
+                    bs[0] = ta.x; bs[1] = ta.y; bs[2] = ta.z; bs[3] = ta.w;
+                    be[0] = tb.x; be[1] = tb.y; be[2] = tb.z; be[3] = tb.w;
+                } else {
+                    seg_basis(el, inv_e, bs);
+                    seg_basis(el + 1, inv_e, be);
+                }
             }
             const float sx = (1.0f - G[p].bproj) * gx[p], sy = (1.0f - G[p].bproj) * gy[p];
             const float ex = G[p].bproj * gx[p], ey = G[p].bproj * gy[p];
