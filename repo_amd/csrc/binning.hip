@@ -1253,7 +1253,8 @@ __global__ __launch_bounds__(256) void k_prim_prep_rank(
                                          colors, opacities, depths, fill_rules, aa_widths,
                                          stroke_widths, nseg, eps, seg_edge_offsets, tbx, tby,
                                          mode, p);
-    const uint32_t ki = o.key;
+    // (key, index) pairs in lexicographic order: one 64-bit comparison each.
+    const uint64_t kp = ((uint64_t)o.key << 32) | (uint32_t)p;
     int cnt = 0;
     const int n4 = P & ~3;
     const bool vec = (reinterpret_cast<uintptr_t>(depths) & 15) == 0;
@@ -1262,19 +1263,15 @@ __global__ __launch_bounds__(256) void k_prim_prep_rank(
 #pragma unroll 4
         for (j0 = 4 * lane; j0 < n4; j0 += 4 * kWave) {
             const float4 d = *reinterpret_cast<const float4*>(depths + j0);
-            const uint32_t a = depth_key(d.x), b = depth_key(d.y), c = depth_key(d.z),
-                           e = depth_key(d.w);
-            cnt += (int)((a < ki) | ((a == ki) & (j0 < p)));
-            cnt += (int)((b < ki) | ((b == ki) & (j0 + 1 < p)));
-            cnt += (int)((c < ki) | ((c == ki) & (j0 + 2 < p)));
-            cnt += (int)((e < ki) | ((e == ki) & (j0 + 3 < p)));
+            cnt += (int)((((uint64_t)depth_key(d.x) << 32) | (uint32_t)j0) < kp);
+            cnt += (int)((((uint64_t)depth_key(d.y) << 32) | (uint32_t)(j0 + 1)) < kp);
+            cnt += (int)((((uint64_t)depth_key(d.z) << 32) | (uint32_t)(j0 + 2)) < kp);
+            cnt += (int)((((uint64_t)depth_key(d.w) << 32) | (uint32_t)(j0 + 3)) < kp);
         }
         j0 = n4;
     }
-    for (int j = j0 + lane; j < P; j += kWave) {
-        const uint32_t kj = depth_key(depths[j]);
-        cnt += (int)((kj < ki) | ((kj == ki) & (j < p)));
-    }
+    for (int j = j0 + lane; j < P; j += kWave)
+        cnt += (int)((((uint64_t)depth_key(depths[j]) << 32) | (uint32_t)j) < kp);
     const int pos = wave_sum_i(cnt);
     if (lane == 0) {
         prim_prep_store(o, p, status, prim_tile_ranges, counts, inv_sigma2s, keys, vals, recs);

@@ -177,10 +177,11 @@ struct SsimTile {
     static constexpr int BOFF = (4 - (WIN - 1) % 4) % 4;
 };
 
-// clamp(v, lo, hi) as torch.clamp computes it for ordered values, when CLAMP.
+// clamp(v, lo, hi) as torch.clamp computes it for ordered values (lo <= hi,
+// v not NaN), when CLAMP: the median of the three, one instruction.
 template <bool CLAMP>
 __device__ __forceinline__ float clamp_if(float v, float lo, float hi) {
-    return CLAMP ? fminf(fmaxf(v, lo), hi) : v;
+    return CLAMP ? __builtin_amdgcn_fmed3f(v, lo, hi) : v;
 }
 
 // Loads plane[gy][gx0 .. gx0 + N) of an image with h rows of w valid columns
