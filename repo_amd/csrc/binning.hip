@@ -717,16 +717,22 @@ constexpr int kRankBlock = 256;
 // Position of key ki (thread t) among the 256 keys of ks in (key, index)
 // order.  Slots past a block's end hold the largest key: they sit after every
 // real slot, so they never precede one.
+// (key, index) as one 64-bit value: lexicographic order is integer order.
+__device__ __forceinline__ uint64_t key_index(uint32_t key, int index) {
+    return ((uint64_t)key << 32) | (uint32_t)index;
+}
+
 __device__ __forceinline__ int rank_in_block(const uint4* ks, uint32_t ki, int t) {
+    const uint64_t kt = key_index(ki, t);
     int r = 0;
 #pragma unroll 16
     for (int q = 0; q < kRankBlock / 4; ++q) {
         const uint4 k4 = ks[q];
         const int j = 4 * q;
-        r += (int)((k4.x < ki) | ((k4.x == ki) & (j < t)));
-        r += (int)((k4.y < ki) | ((k4.y == ki) & (j + 1 < t)));
-        r += (int)((k4.z < ki) | ((k4.z == ki) & (j + 2 < t)));
-        r += (int)((k4.w < ki) | ((k4.w == ki) & (j + 3 < t)));
+        r += (int)(key_index(k4.x, j) < kt);
+        r += (int)(key_index(k4.y, j + 1) < kt);
+        r += (int)(key_index(k4.z, j + 2) < kt);
+        r += (int)(key_index(k4.w, j + 3) < kt);
     }
     return r;
 }
@@ -1190,6 +1196,7 @@ __global__ __launch_bounds__(256) void k_rank_allpairs(
     if (i >= n) return;
     const int lane = threadIdx.x & (kWave - 1);
     const uint32_t ki = keys[i];
+    const uint64_t kt = key_index(ki, i);
     int cnt = 0;
     const int n4 = n & ~3;
     const bool vec = (reinterpret_cast<uintptr_t>(keys) & 15) == 0;
@@ -1198,17 +1205,14 @@ __global__ __launch_bounds__(256) void k_rank_allpairs(
 #pragma unroll 4
         for (j0 = 4 * lane; j0 < n4; j0 += 4 * kWave) {
             const uint4 q = *reinterpret_cast<const uint4*>(keys + j0);
-            cnt += (int)((q.x < ki) | ((q.x == ki) & (j0 < i)));
-            cnt += (int)((q.y < ki) | ((q.y == ki) & (j0 + 1 < i)));
-            cnt += (int)((q.z < ki) | ((q.z == ki) & (j0 + 2 < i)));
-            cnt += (int)((q.w < ki) | ((q.w == ki) & (j0 + 3 < i)));
+            cnt += (int)(key_index(q.x, j0) < kt);
+            cnt += (int)(key_index(q.y, j0 + 1) < kt);
+            cnt += (int)(key_index(q.z, j0 + 2) < kt);
+            cnt += (int)(key_index(q.w, j0 + 3) < kt);
         }
         j0 = n4;
     }
-    for (int j = j0 + lane; j < n; j += kWave) {
-        const uint32_t kj = keys[j];
-        cnt += (int)((kj < ki) | ((kj == ki) & (j < i)));
-    }
+    for (int j = j0 + lane; j < n; j += kWave) cnt += (int)(key_index(keys[j], j) < kt);
     const int pos = wave_sum_i(cnt);
     if (lane == 0) {
         if (PAIRS) {
@@ -1254,7 +1258,7 @@ __global__ __launch_bounds__(256) void k_prim_prep_rank(
                                          stroke_widths, nseg, eps, seg_edge_offsets, tbx, tby,
                                          mode, p);
     // (key, index) pairs in lexicographic order: one 64-bit comparison each.
-    const uint64_t kp = ((uint64_t)o.key << 32) | (uint32_t)p;
+    const uint64_t kp = key_index(o.key, p);
     int cnt = 0;
     const int n4 = P & ~3;
     const bool vec = (reinterpret_cast<uintptr_t>(depths) & 15) == 0;
@@ -1263,15 +1267,15 @@ __global__ __launch_bounds__(256) void k_prim_prep_rank(
 #pragma unroll 4
         for (j0 = 4 * lane; j0 < n4; j0 += 4 * kWave) {
             const float4 d = *reinterpret_cast<const float4*>(depths + j0);
-            cnt += (int)((((uint64_t)depth_key(d.x) << 32) | (uint32_t)j0) < kp);
-            cnt += (int)((((uint64_t)depth_key(d.y) << 32) | (uint32_t)(j0 + 1)) < kp);
-            cnt += (int)((((uint64_t)depth_key(d.z) << 32) | (uint32_t)(j0 + 2)) < kp);
-            cnt += (int)((((uint64_t)depth_key(d.w) << 32) | (uint32_t)(j0 + 3)) < kp);
+            cnt += (int)(key_index(depth_key(d.x), j0) < kp);
+            cnt += (int)(key_index(depth_key(d.y), j0 + 1) < kp);
+            cnt += (int)(key_index(depth_key(d.z), j0 + 2) < kp);
+            cnt += (int)(key_index(depth_key(d.w), j0 + 3) < kp);
         }
         j0 = n4;
     }
     for (int j = j0 + lane; j < P; j += kWave)
-        cnt += (int)((((uint64_t)depth_key(depths[j]) << 32) | (uint32_t)j) < kp);
+        cnt += (int)(key_index(depth_key(depths[j]), j) < kp);
     const int pos = wave_sum_i(cnt);
     if (lane == 0) {
         prim_prep_store(o, p, status, prim_tile_ranges, counts, inv_sigma2s, keys, vals, recs);
