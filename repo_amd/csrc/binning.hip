@@ -1236,9 +1236,8 @@ __device__ __forceinline__ uint32_t depth_key(float d) {
 // kRankPairsMax primitives: one wave per primitive counts the keys that
 // precede its own (lane-parallel, the keys computed from the depths, since no
 // other wave's keys are written yet); the primitive's records are computed
-// wave-uniformly (scalar loads, issued before the counting loop's vector
-// loads are waited for) and lane 0 stores them and writes order[pos] = p,
-// rank_rects[pos] = its tile rectangle.
+// wave-uniformly (scalar loads), and lane 0 stores them and writes
+// order[pos] = p, rank_rects[pos] = its tile rectangle.
 __global__ __launch_bounds__(256) void k_prim_prep_rank(
     const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
     const int32_t* __restrict__ seg_tile_ranges, const SegRec* __restrict__ seg_recs,
