@@ -597,6 +597,22 @@ __device__ __forceinline__ void composite(const PrimRec& pr, float alpha, int g,
     done = done || (take && nT <= kTStop);
 }
 
+// The fields of a primitive record the forward uses after the primitive cull
+// (three 16-byte scalar loads and one dword: colour, opacity, widths, cull
+// distances, edge range, rule); the cull ranges stay in memory (the cull
+// reads them lane-parallel), so they take no scalar registers here.
+__device__ __forceinline__ PrimRec load_prim_fwd(cptr<PrimRec> prims, int pid) {
+    const cptr<float4> f = reinterpret_cast<cptr<float4>>(prims + pid);
+    const float4 a = f[0], b = f[1];
+    const int4 c = reinterpret_cast<cptr<int4>>(f)[2];
+    PrimRec pr{};
+    pr.r = a.x; pr.g = a.y; pr.b = a.z; pr.opacity = a.w;
+    pr.inv_sigma2 = b.x; pr.inv_sigma = b.y; pr.half_sw = b.z; pr.cull_d = b.w;
+    pr.e0 = c.x; pr.e1 = c.y; pr.rule = c.z;
+    pr.cull_out = prims[pid].cull_out;
+    return pr;
+}
+
 // Forward raster.  Each wave walks its tile's list in chunks of 64 entries:
 // lane k tests entry k of the chunk against the wave's pixel rectangle
 // (prim_culled_lane), and the wave then processes only the entries that can
@@ -679,7 +695,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             todo &= todo - 1;
             const int g = gc + k;
             const int pid = __builtin_amdgcn_readlane(pid_l, k);
-            const PrimRec pr = prims[pid];
+            const PrimRec pr = load_prim_fwd(prims, pid);
             const int4 q = q_next;
             if (todo) {
                 const int pid2 = __builtin_amdgcn_readlane(pid_l, (int)__builtin_ctzll(todo));
