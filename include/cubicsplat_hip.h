@@ -292,7 +292,10 @@ int cs_edge_aux_from_csr(const int32_t* segment_edge_offsets, int32_t nseg,
  * written as [H, W, 3], or, when out_planar != 0, as three [H, W] planes
  * (channel c at out_img + c H W; the layout cs_clamp_mse_ssim_loss reads
  * with img_planar, and the clamp(0, 1).permute(2, 0, 1) glue of
- * gaussian_trace/render.py:1309-1310 then needs no copy). */
+ * gaussian_trace/render.py:1309-1310 then needs no copy).  log_counter: NULL,
+ * or a device word that is zero on entry, which then counts the raster log's
+ * shared blocks (the call takes no launch of its own to set up the counter in
+ * the pool's first unit; the word is left at the count used). */
 int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins,
                          const void* edges, const void* edge_culls, const void* prim_recs,
                          const float* background, int32_t img_h, int32_t img_w,
@@ -300,8 +303,8 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
                          int32_t edges_per_segment, float* out_img, int32_t out_planar,
                          float* final_Ts, int32_t* final_idx, int64_t num_entries,
                          int32_t* log_index, void* log_pool, int64_t log_pool_bytes,
-                         int32_t log_entry_units, const int32_t* tile_order,
-                         uint32_t* wave_cost, hipStream_t stream);
+                         int32_t log_entry_units, uint32_t* log_counter,
+                         const int32_t* tile_order, uint32_t* wave_cost, hipStream_t stream);
 
 /* rasterize_cubic_fill_backward_kernel (ops/cubic_splatting.py:1197-1651) /
  * rasterize_cubic_polyline_backward_kernel (ops/cubic_polyline_splatting.py:252-660)
@@ -376,7 +379,7 @@ int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                  int32_t out_planar, float* final_Ts, int32_t* final_idx,
                                  int64_t num_entries, int32_t* log_index, void* log_pool,
                                  int64_t log_pool_bytes, int32_t log_entry_units,
-                                 unsigned long long* eval_counts,
+                                 uint32_t* log_counter, unsigned long long* eval_counts,
                                  const int32_t* tile_order,
                                  uint32_t* wave_cost, hipStream_t stream);
 int cs_rasterize_backward_counted(int32_t mode, const int32_t* prim_ids_sorted,

@@ -51,14 +51,14 @@ _SIGNATURES = {
                                      _P, _P, _P, _I64, _P]),
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                             _I32, _P, _I32, _P, _P, _I64, _P, _P, _I64, _I32, _P,
-                                            _P, _P]),
+                                            _P, _P, _P]),
     "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                              _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P,
                                              _P, _P, _I32, _P, _P, _P]),
     "cs_raster_prim_scratch_elems": (_SZ, [_I32, _I32]),
     "cs_rasterize_forward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                                     _I32, _I32, _P, _I32, _P, _P, _I64, _P, _P,
-                                                    _I64, _I32, _P, _P, _P, _P]),
+                                                    _I64, _I32, _P, _P, _P, _P, _P]),
     "cs_rasterize_backward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
                                                      _I32, _I32, _I32, _P, _P, _P, _P, _P, _I32,
                                                      _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P,

@@ -520,15 +520,15 @@ struct LogCursor {
 // fills its own region of the pool (`per_entry` units for each list entry of
 // its tile, at a position fixed by the tile's list range, so no atomics);
 // when a record does not fit there it reserves blocks of kLogBlockUnits from
-// the shared counter.  kLogMissing when the pool is full.  Wave-uniform;
-// every lane of the wave must be active.
-__device__ __forceinline__ int32_t log_reserve(uint4* __restrict__ pool, uint32_t cap_units,
-                                               LogCursor& c, uint32_t units) {
+// the shared counter (the next block is at `first` + *ctr).  kLogMissing when
+// the pool is full.  Wave-uniform; every lane of the wave must be active.
+__device__ __forceinline__ int32_t log_reserve(uint32_t* __restrict__ ctr, uint32_t first,
+                                               uint32_t cap_units, LogCursor& c,
+                                               uint32_t units) {
     if (c.full) return kLogMissing;
     if (c.p + units > c.e) {
         uint32_t base = 0;
-        if ((threadIdx.x & (kWave - 1)) == 0)
-            base = atomicAdd(reinterpret_cast<uint32_t*>(pool), kLogBlockUnits);
+        if ((threadIdx.x & (kWave - 1)) == 0) base = first + atomicAdd(ctr, kLogBlockUnits);
         base = __builtin_amdgcn_readfirstlane(base);
         if ((uint64_t)base + kLogBlockUnits > cap_units) {
             c.full = true;
@@ -633,7 +633,8 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     TileGrid tg, const int32_t* __restrict__ tile_order,
     uint32_t* __restrict__ wave_cost, float* __restrict__ out, int out_planar,
     float* __restrict__ final_T, int32_t* __restrict__ final_idx,
-    int32_t* __restrict__ log_index, uint4* __restrict__ log_pool, uint32_t log_units,
+    int32_t* __restrict__ log_index, uint4* __restrict__ log_pool, uint32_t* __restrict__ log_ctr,
+    uint32_t log_first, uint32_t log_units,
     uint32_t log_per_entry, unsigned long long* __restrict__ counts) {
     const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
     const int lane = threadIdx.x & (kWave - 1);
@@ -795,7 +796,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             if (log_index) {
                 const uint32_t units = kLogHeaderUnits + (uint32_t)((nx + 1) >> 1);
                 if (st.n + units > kLogStageUnits) log_flush(log_pool, stage, st);
-                const int32_t at = log_reserve(log_pool, log_units, lc, units);
+                const int32_t at = log_reserve(log_ctr, log_first, log_units, lc, units);
                 if (at >= 0) {
                     if ((uint32_t)at != st.base + st.n) {   // another region: flush first
                         log_flush(log_pool, stage, st);
@@ -1572,6 +1573,8 @@ struct RasterArgs {
     int32_t* final_idx;
     int32_t* log_index;     // raster log: written by the forward, read by the backward
     uint4* log_pool;
+    uint32_t* log_ctr;      // shared-block counter (the next block at log_first + *log_ctr)
+    uint32_t log_first;
     uint32_t log_units;     // pool capacity in 16-byte units
     uint32_t log_per_entry; // units of a wave's own region per list entry
     // backward inputs / outputs
@@ -1597,7 +1600,8 @@ static void launch_fwd(const RasterArgs& a) {
                        a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tg,
                        a.order, a.wave_cost, a.out, a.out_planar, a.final_T, a.final_idx,
                        a.log_index,
-                       a.log_pool, a.log_units, a.log_per_entry, a.counts);
+                       a.log_pool, a.log_ctr, a.log_first, a.log_units, a.log_per_entry,
+                       a.counts);
 }
 
 template <int MODE, bool COUNT, bool ADAPTIVE>
@@ -1683,9 +1687,9 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                              int32_t edges_per_segment, float* out_img, int32_t out_planar,
                              float* final_Ts, int32_t* final_idx, int64_t num_entries,
                              int32_t* log_index, void* log_pool, int64_t log_pool_bytes,
-                             int32_t log_entry_units, unsigned long long* eval_counts,
-                             const int32_t* tile_order, uint32_t* wave_cost,
-                             hipStream_t stream) {
+                             int32_t log_entry_units, uint32_t* log_counter,
+                             unsigned long long* eval_counts, const int32_t* tile_order,
+                             uint32_t* wave_cost, hipStream_t stream) {
     // The primitive records hold each primitive's edge range, so the forward
     // does not use edges_per_segment (0 for adaptively flattened records).
     TileGrid tg;
@@ -1713,9 +1717,17 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
     a.counts = eval_counts;
     a.order = tile_order;
     a.wave_cost = wave_cost;
-    if (log_index)
+    // The shared blocks' counter: the caller's zeroed word, or the pool's first
+    // unit, set to the first shared unit here.
+    if (log_index && log_counter) {
+        a.log_ctr = log_counter;
+        a.log_first = (uint32_t)first_shared;
+    } else if (log_index) {
+        a.log_ctr = reinterpret_cast<uint32_t*>(a.log_pool);
+        a.log_first = 0;
         hipLaunchKernelGGL(k_log_init, dim3(1), dim3(1), 0, stream, a.log_pool,
                            (uint32_t)first_shared);
+    }
     if (eval_counts) launch_fwd_mode<true>(a);
     else launch_fwd_mode<false>(a);
     return raster_status();
@@ -1729,13 +1741,15 @@ extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted
                                     float* out_img, int32_t out_planar, float* final_Ts,
                                     int32_t* final_idx, int64_t num_entries, int32_t* log_index,
                                     void* log_pool, int64_t log_pool_bytes,
-                                    int32_t log_entry_units, const int32_t* tile_order,
-                                    uint32_t* wave_cost, hipStream_t stream) {
+                                    int32_t log_entry_units, uint32_t* log_counter,
+                                    const int32_t* tile_order, uint32_t* wave_cost,
+                                    hipStream_t stream) {
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, block_x, block_y, edges_per_segment,
                              out_img, out_planar, final_Ts,
                              final_idx, num_entries, log_index, log_pool, log_pool_bytes,
-                             log_entry_units, nullptr, tile_order, wave_cost, stream);
+                             log_entry_units, log_counter, nullptr, tile_order, wave_cost,
+                             stream);
 }
 
 extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
@@ -1748,6 +1762,7 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
                                             int32_t* final_idx, int64_t num_entries,
                                             int32_t* log_index, void* log_pool,
                                             int64_t log_pool_bytes, int32_t log_entry_units,
+                                            uint32_t* log_counter,
                                             unsigned long long* eval_counts,
                                             const int32_t* tile_order, uint32_t* wave_cost,
                                             hipStream_t stream) {
@@ -1756,7 +1771,8 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
                              background, img_h, img_w, block_x, block_y, edges_per_segment,
                              out_img, out_planar, final_Ts,
                              final_idx, num_entries, log_index, log_pool, log_pool_bytes,
-                             log_entry_units, eval_counts, tile_order, wave_cost, stream);
+                             log_entry_units, log_counter, eval_counts, tile_order, wave_cost,
+                             stream);
 }
 
 static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,

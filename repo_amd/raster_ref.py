@@ -170,7 +170,7 @@ def rasterize_cubic_fill_forward_tilelang(tile_bounds, block, img_size, primitiv
     N.call("cs_rasterize_forward", 0, N.ptr(ids), N.ptr(bins), N.ptr(edges),
            N.ptr(culls), N.ptr(prims), N.ptr(bg), H, W, bx, by, 0, N.ptr(out_img), 0,
            N.ptr(final_Ts),
-           N.ptr(final_idx), num_intersects, None, None, 0, 0, None, None, N.stream(dev))
+           N.ptr(final_idx), num_intersects, None, None, 0, 0, None, None, None, N.stream(dev))
     return out_img, final_Ts, final_idx
 
 

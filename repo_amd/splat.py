@@ -198,6 +198,11 @@ class Binned:
         self.log_key = None
         self.log_units = 0
         self.grad_accum_clean = True
+        # The last 4 words of grad_accum (zeroed with it by the binning) count
+        # the raster log's shared blocks of the first forward after a binning;
+        # log_ctr = (address, first shared unit) when a forward used them.
+        self.log_ctr_clean = True
+        self.log_ctr = None
         # Set while the intersection count has not been read on the host yet
         # (bin_primitives with a capacity hint); resolve_binned() settles it.
         self.pending: Optional["_PendingCount"] = None
@@ -386,12 +391,18 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     return b
 
 
+# Words at the end of the gradient buffer for the raster log's counter (16 B).
+_LOG_COUNTER_ELEMS = 4
+
+
 def _grad_accum_elems(nseg: int, nprim: int, mode: int) -> int:
     """The backward's accumulators (v_cubics_px, then the per-primitive
     gradients) followed by the copies the backward sums the per-primitive
-    gradients into (cs_raster_prim_scratch_elems), all zero."""
+    gradients into (cs_raster_prim_scratch_elems), all zero, then the
+    forward's raster-log counter word (and padding to 16 bytes)."""
     nv = 6 if mode == MODE_STROKE else 5
-    return nseg * 8 + nprim * nv + int(N.lib().cs_raster_prim_scratch_elems(nprim, mode))
+    return (nseg * 8 + nprim * nv + int(N.lib().cs_raster_prim_scratch_elems(nprim, mode))
+            + _LOG_COUNTER_ELEMS)
 
 
 def _read_count(pending: "_PendingCount", nseg: int) -> int:
@@ -425,6 +436,7 @@ def resolve_binned(b: Binned) -> bool:
         return False
     b.primitive_ids_sorted = pend.finish(I)
     b.grad_accum_clean = True
+    b.log_ctr_clean = True
     return True
 
 
@@ -461,7 +473,8 @@ ORDER_CHUNKED = True
 # counter into pinned memory, polled by the next forward of the shape), and
 # grow the regions of the next forward.
 _LOG_PENDING: "dict[tuple, tuple]" = {}   # key -> ((pinned [4], event, device), units,
-#                                            first shared unit, pool bytes)
+#                                            first shared unit, pool bytes, the counter's
+#                                            value for no shared block)
 _LOG_UNITS: "dict[tuple, int]" = {}       # key -> units per entry of the next forward
 _MAX_LOG_KEYS = 64
 # Units per (list entry, wave) of the first forward of a shape (the benchmark
@@ -474,11 +487,11 @@ def _poll_log_use(key) -> None:
     pend = _LOG_PENDING.get(key)
     if pend is None:
         return
-    entry, units, first_shared, pool_bytes = pend
+    entry, units, first_shared, pool_bytes, zero = pend
     if N.hip().hipEventQuery(entry[1]) != 0:
         return   # not reached yet (or an error the next synchronizing call reports)
     _LOG_PENDING.pop(key)
-    shared_used = 16 * max(0, int(entry[0][0]) - first_shared)
+    shared_used = 16 * max(0, int(entry[0][0]) - zero)
     _give_pinned(entry)
     regions = 16 * (first_shared - 1)
     # Shared blocks beyond a twentieth of the regions: widen the regions by
@@ -509,9 +522,10 @@ LOG_READ_EVERY = 4
 _LOG_READ_AGE: "dict[tuple, int]" = {}
 
 
-def _read_log_use_later(key, pool: torch.Tensor, units: int, first_shared: int,
-                        pool_bytes: int, st) -> None:
-    """Queues a copy of the pool's counter into pinned memory and an event after
+def _read_log_use_later(key, dev_index: int, src: int, zero: int, units: int,
+                        first_shared: int, pool_bytes: int, st) -> None:
+    """Queues a copy of the shared-block counter at device address `src`
+    (whose value `zero` means none used) into pinned memory and an event after
     it, unless one for this shape is still outstanding or this forward is not
     one of every LOG_READ_EVERY."""
     if key in _LOG_PENDING:
@@ -523,17 +537,16 @@ def _read_log_use_later(key, pool: torch.Tensor, units: int, first_shared: int,
         _LOG_READ_AGE[key] = age
         return
     _LOG_READ_AGE[key] = 0
-    dev = pool.device.index if pool.device.index is not None else torch.cuda.current_device()
-    entry = _take_pinned(dev)
+    entry = _take_pinned(dev_index)
     hip = N.hip()
-    N.hip_check(hip.hipMemcpyAsync(entry[0].data_ptr(), pool.data_ptr(), 4,
+    N.hip_check(hip.hipMemcpyAsync(entry[0].data_ptr(), src, 4,
                                    N.HIP_MEMCPY_DEVICE_TO_HOST, st), "hipMemcpyAsync")
     N.hip_check(hip.hipEventRecord(entry[1], st), "hipEventRecord")
     if len(_LOG_PENDING) >= _MAX_LOG_KEYS:
         _, old = _LOG_PENDING.popitem()
         N.hip_check(hip.hipEventSynchronize(old[0][1]), "hipEventSynchronize")
         _give_pinned(old[0])
-    _LOG_PENDING[key] = (entry, units, first_shared, pool_bytes)
+    _LOG_PENDING[key] = (entry, units, first_shared, pool_bytes, zero)
 
 
 def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log: bool = True,
@@ -575,10 +588,21 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
         b.log_index = aux[2 * H * W:]
         b.log_pool = torch.empty((pool_bytes,), dtype=torch.uint8, device=dev)
         b.log_units = units
-        log_args = (cap, b.log_index.data_ptr(), b.log_pool.data_ptr(), pool_bytes, units)
+        # The first forward after a binning counts its shared blocks in the
+        # gradient buffer's zeroed counter word (no set-up launch); a repeated
+        # forward lets the library set up the pool's own counter.
+        ctr = None
+        first_shared = 1 + wpt * cap * units
+        if b.log_ctr_clean and b.grad_accum is not None:
+            ga = b.grad_accum
+            ctr = ga.data_ptr() + 4 * (ga.numel() - _LOG_COUNTER_ELEMS)
+            b.log_ctr_clean = False
+        b.log_ctr = None if ctr is None else (ctr, first_shared)
+        log_args = (cap, b.log_index.data_ptr(), b.log_pool.data_ptr(), pool_bytes, units, ctr)
     else:
         b.log_index = b.log_pool = None
-        log_args = (cap, None, None, 0, 0)
+        b.log_ctr = None
+        log_args = (cap, None, None, 0, 0, None)
     # The tile order is kept apart: the next forward reads it after this
     # forward's buffers are gone.
     okey = (dev.index, st, nsub)
@@ -599,7 +623,12 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
         with N.prof("cubic.fwd.rast"):
             N.call("cs_rasterize_forward", *args, prev_p, cost, st)
     if log and log_pool_bytes_override is None:
-        _read_log_use_later(key, b.log_pool, units, 1 + wpt * cap * units, pool_bytes, st)
+        dix = dev.index if dev.index is not None else torch.cuda.current_device()
+        if b.log_ctr is not None:
+            _read_log_use_later(key, dix, b.log_ctr[0], 0, units, first_shared, pool_bytes, st)
+        else:
+            _read_log_use_later(key, dix, b.log_pool.data_ptr(), first_shared, units,
+                                first_shared, pool_bytes, st)
     if not remake:
         b.tile_order = prev
         _ORDER_AGE[okey] = age
@@ -620,10 +649,14 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
 
 
 def log_pool_counter(b: Binned) -> int:
-    """The log pool's counter after b's forward: the end of the shared blocks
-    reserved, in 16-byte units (a host read; tests)."""
+    """The end of the shared blocks b's forward reserved in its log pool, in
+    16-byte units (a host read; tests)."""
     if b.log_pool is None:
         return 0
+    if b.log_ctr is not None:
+        ga = b.grad_accum
+        used = int(ga[ga.numel() - _LOG_COUNTER_ELEMS:].view(torch.int32)[0].item())
+        return b.log_ctr[1] + used
     return int(b.log_pool[:4].view(torch.int32)[0].item())
 
 

@@ -563,7 +563,8 @@ def test_prim_gradient_copies_left_zero_and_equal_direct_atomics(stroke):
     P = b.nprim
     nv = 6 if stroke else 5
     rest = b.grad_accum[b.nseg * 8:]
-    assert int(torch.count_nonzero(rest[nv * P:]).item()) == 0
+    n_copies = int(N.lib().cs_raster_prim_scratch_elems(P, b.mode))
+    assert int(torch.count_nonzero(rest[nv * P:nv * P + n_copies]).item()) == 0
     # The same backward with plain atomics.
     z = torch.zeros_like(b.grad_accum)
     v_px = z[: b.nseg * 8]
