@@ -1,7 +1,7 @@
 // Tile binning for the cubic splat path on MI355X (gfx950).
 //
 // Pipeline (one forward):
-//   k_project_flatten_wave  workgroup per 64 cubic segments: normalized ->
+//   k_project_flatten_wave  workgroup per 32 or 64 cubic segments: normalized ->
 //                      pixel space, exact AABB -> padded 16x16 tile range
 //                      (lane per segment), then uniform Bernstein flattening
 //                      into 32-byte edge records and a per-segment vertex
@@ -512,6 +512,11 @@ __global__ __launch_bounds__(256) void k_project_flatten(
 // (k_status_init), which the later launches of the binning update.  Same
 // outputs as k_project_flatten.
 constexpr int kFlattenWaves = 4;
+// Segments per workgroup for L sample lanes (at most a wave: wave 0 projects
+// one per lane).  With few samples per segment, 32 puts more workgroups, and
+// so more of the projection's dependent loads, in flight on each CU; with
+// many, the flattening's vector work dominates and 64 does it in fewer steps.
+__host__ __device__ constexpr int flatten_segs(int lanes) { return lanes >= 32 ? 64 : 32; }
 
 template <int L>
 __global__ __launch_bounds__(kWave * kFlattenWaves) void k_project_flatten_wave(
@@ -533,8 +538,10 @@ __global__ __launch_bounds__(kWave * kFlattenWaves) void k_project_flatten_wave(
     }
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t base = (int64_t)blockIdx.x * kWave;
-    const int nw = (int)min((int64_t)kWave, (int64_t)nseg - base);
+    constexpr int kSegs = flatten_segs(L);
+    static_assert(kSegs <= kWave, "one projecting lane per segment");
+    const int64_t base = (int64_t)blockIdx.x * kSegs;
+    const int nw = (int)min((int64_t)kSegs, (int64_t)nseg - base);
     const int p = w == 0 ? wave_owner(seg_offsets, P, (int)base, bounds) : 0;
     if (w == 0 && lane < nw) {
         const int s = (int)base + lane;
@@ -1958,7 +1965,8 @@ static int bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, con
     if (!adaptive && nseg > 0 && samples <= kWave) {
         // One lane per sample point; the kernel also sets the status words.
         const int lanes = samples <= 2 ? 2 : 1 << ceil_log2(samples);
-        const dim3 grid((unsigned)blocks_for(nseg, kWave)), block(kWave * kFlattenWaves);
+        const dim3 grid((unsigned)blocks_for(nseg, flatten_segs(lanes))),
+            block(kWave * kFlattenWaves);
 #define CS_FLATTEN_LANES(Lv)                                                                   \
     hipLaunchKernelGGL(k_project_flatten_wave<Lv>, grid, block, 0, stream, cubics_norm,       \
                        seg_offsets, nprim, aa_widths, stroke_widths, opacities, mode, nseg,    \
