@@ -331,11 +331,20 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
         load_strip<NIN, 0, CLAMP>(xc, h, w, w, oy0 + r, ox0 + q0, vec_ok, a, lo, hi);
         load_strip<NIN, 0>(yc, h, w, w, oy0 + r, ox0 + q0, vec_ok, b);
         if (mse_partials && r < mse_rows) {
-            const int cols = (tx == ntx - 1 && q0 + kHStrip == kSsimTW) ? NIN : kHStrip;
+            // The strip's own 8 columns; the last strip of the last tile
+            // column also takes the inputs past them (to the end of its
+            // inputs), in the same order as one loop over all of them.
 #pragma unroll
-            for (int k = 0; k < NIN; ++k) {
+            for (int k = 0; k < kHStrip; ++k) {
                 const float d = a[k] - b[k];
-                mse = k < cols ? __builtin_fmaf(d, d, mse) : mse;
+                mse = __builtin_fmaf(d, d, mse);
+            }
+            if (tx == ntx - 1 && q0 + kHStrip == kSsimTW) {
+#pragma unroll
+                for (int k = kHStrip; k < NIN; ++k) {
+                    const float d = a[k] - b[k];
+                    mse = __builtin_fmaf(d, d, mse);
+                }
             }
         }
         float ss[NIN], ab[NIN];
