@@ -34,6 +34,14 @@ FP32_PEAK_TFLOPS = 157.3
 FLOPS_DIST, FLOPS_CROSS, FLOPS_ROW = 15.0, 6.0, 3.0
 FLOPS_PER_EVAL = {0: FLOPS_DIST + FLOPS_CROSS, 1: FLOPS_DIST}
 RASTER_LABELS = {"cubic.fwd.rast": "raster_fwd", "cubic.bwd.rast": "raster_bwd"}
+# Every stage of the step bracketed by HIP events in the sampled timed steps
+# (device time of that stage's launches, on the step's own drifting scene).
+STEP_LABELS = {"cubic.fwd.bin_prepare": "bin_prepare", "cubic.fwd.bin_finish": "bin_finish",
+               "cubic.fwd.tile_order": "tile_order", "loss.clamp_mse_ssim": "loss_fwd",
+               "loss.clamp_mse_ssim_bwd": "loss_bwd", "loss.mse_fwd": "mse_fwd",
+               "loss.mse_bwd": "mse_bwd", "glue.clamp_nchw": "clamp_nchw",
+               "glue.clamp_nchw_bwd": "clamp_nchw_bwd", "cubic.bwd.finalize": "finalize",
+               "optim.adam": "adam", **RASTER_LABELS}
 # The raster launches of every EVENT_EVERY-th timed step are bracketed by HIP
 # events (two event records per launch cost the step about 4%; a sample of
 # the steps gives the same mean launch time).
@@ -113,11 +121,15 @@ def train_step(sc, cub, col, opt, ssim_weight=SSIM_WEIGHT):
     return loss
 
 
-def stage_times(sc, cub, col, iters):
-    """Average ms of the main stages, timed with HIP events on the stream the
-    kernels are launched on (torch's current stream)."""
+def stage_times(sc, iters):
+    """Average ms of the main stages on scene ``sc`` (the step-0 scene: fresh
+    control points and colours, so the figures do not drift with --steps),
+    timed with HIP events on the stream the kernels are launched on (torch's
+    current stream).  Every loss stage calls its kernels directly (no
+    autograd in the loop), so the figures are device time of those kernels
+    plus launch gaps."""
     import torch
-    from repo_amd import splat, metric
+    from repo_amd import _native as N, splat, metric
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     offs = sc.seg_offsets.to(torch.int32).contiguous()
     widths = torch.clamp(sc.aa_widths.float(), min=1e-4).contiguous()
@@ -136,8 +148,8 @@ def stage_times(sc, cub, col, iters):
         return out
 
     mode = splat.MODE_FILL if sc.stroke_widths is None else splat.MODE_STROKE
-    cubd = cub.detach().contiguous()
-    cold = col.detach().contiguous()
+    cubd = sc.cubics_norm.contiguous()
+    cold = sc.colors.contiguous()
     rules = sc.fill_rules.to(torch.int32).contiguous() if mode == 0 else None
     sw = sc.stroke_widths
 
@@ -149,25 +161,56 @@ def stage_times(sc, cub, col, iters):
     g = torch.randn_like(out)
     timed("raster_bwd_ms", lambda: splat.rasterize_backward(b, sc.background, T, idx, g))
     x = out.clamp(0, 1).permute(2, 0, 1).unsqueeze(0).contiguous()
-    tgt = sc.target
+    tgt = sc.target.contiguous()
+    n = x.numel()
+    stream = N.stream(x.device)
     timed("mse_fwd_ms", lambda: metric.mse_forward(x.view(-1), tgt.view(-1)))
-    xr = x.detach().requires_grad_(True)
-    m = metric._TileLangMSEFn.apply(xr, tgt, 256, 8, 1)
-    timed("mse_bwd_ms", lambda: torch.autograd.grad(m, xr, retain_graph=True))
+    one = torch.ones((), dtype=torch.float32, device=x.device)
+    gx = torch.empty_like(x)
+    # the reference's MSE backward: gx = 2 g (x - y) / N (read x, y; write gx)
+    timed("mse_bwd_ms", lambda: N.call("cs_mse_backward", N.ptr(x), N.ptr(tgt), n, N.ptr(one),
+                                       N.ptr(gx), None, stream))
     timed("ssim_fwd_ms", lambda: metric._ssim_forward(x, tgt, 11, 1.5, 1e-4, 9e-4, False))
-    timed("ssim_fwd_grad_ms", lambda: metric._ssim_forward(x, tgt, 11, 1.5, 1e-4, 9e-4, True))
-    s = metric._SSIMFn.apply(xr, tgt, 11, 1.5, 1e-4, 9e-4)
-    timed("ssim_bwd_ms", lambda: torch.autograd.grad(s, xr, retain_graph=True))
+    _, abc, win = timed("ssim_fwd_grad_ms",
+                        lambda: metric._ssim_forward(x, tgt, 11, 1.5, 1e-4, 9e-4, True))
+    nc, h, w = 3, sc.img_h, sc.img_w
+    scratch = metric._ssim_scratch(nc, h, w, 11, x.device)
+    timed("ssim_bwd_ms", lambda: N.call("cs_ssim_backward", N.ptr(x), N.ptr(tgt), nc, h, w,
+                                        N.ptr(win), 11, N.ptr(abc), N.ptr(one), 0, N.ptr(gx),
+                                        N.ptr(scratch), stream))
     from repo_amd import fused
     timed("glue_clamp_nchw_ms", lambda: fused.clamp_to_nchw(out))
-    timed("loss_fused_fwd_ms", lambda: fused.mse_ssim_loss(xr, tgt, SSIM_WEIGHT))
-    lf, _ = fused.mse_ssim_loss(xr, tgt, SSIM_WEIGHT)
-    timed("loss_fused_bwd_ms", lambda: torch.autograd.grad(lf, xr, retain_graph=True))
+    # The step's fused loss on the renderer's image (clamp on load, MSE summed
+    # in the SSIM forward), its forward and its backward kernel.
+    loss, _ = timed("loss_fused_fwd_ms",
+                    lambda: fused.clamp_mse_ssim_loss(out.detach().requires_grad_(True), tgt,
+                                                      SSIM_WEIGHT))
+    fn = loss.grad_fn
+    planes = torch.empty((3, h, w), dtype=torch.float32, device=x.device)
+    timed("loss_fused_bwd_ms", lambda: N.call(
+        "cs_clamp_mse_ssim_backward", fn.saved_tensors[0].data_ptr(), fn.planar,
+        N.ptr(fn.saved_tensors[1]), h, w, fn.lo, fn.hi, N.ptr(fn.g), fn.win_size,
+        fn.work.data_ptr() + fn.abc_off, fn.ssim_weight, one.data_ptr(), planes.data_ptr(), 1,
+        stream))
     res["num_intersects"] = b.num_intersects
     res["_binned"] = b
     res["_T"] = T
     res["_idx"] = idx
     return res
+
+
+def opt_scene_intersects(sc, cub, col):
+    """Intersection count of the scene as the timed steps left it."""
+    import torch
+    from repo_amd import splat
+    mode = splat.MODE_FILL if sc.stroke_widths is None else splat.MODE_STROKE
+    b = splat.bin_primitives(
+        cub.detach().contiguous(), sc.seg_offsets.to(torch.int32).contiguous(),
+        col.detach().contiguous(), sc.opacities, sc.depths,
+        sc.fill_rules.to(torch.int32).contiguous() if mode == 0 else None,
+        torch.clamp(sc.aa_widths.float(), min=1e-4).contiguous(), sc.stroke_widths, sc.img_h,
+        sc.img_w, sc.S, mode=mode)
+    return b.num_intersects
 
 
 def binning_bytes(sc, n_isect):
@@ -389,7 +432,21 @@ def main():
     ms = 1000.0 * elapsed / max(1, args.steps)
     launch_ms = {RASTER_LABELS[k]: timer.mean_ms(k) for k in RASTER_LABELS}
     timer.close()
-    st = stage_times(sc, cub, col, args.stage_iters)
+    # After the timed region: a few more steps with every stage bracketed by
+    # HIP events (the per-stage device times of the step, not counted in value).
+    n_prof = max(4, args.steps // 5)
+    timer = profiling.EventTimer(STEP_LABELS, reserve=n_prof + 1)
+    _native.set_profile_ctx_factory(timer)
+    for _ in range(n_prof):
+        train_step(sc, cub, col, opt, ssim_weight)
+    torch.cuda.synchronize()
+    _native.set_profile_ctx_factory(None)
+    step_ms = {v: round(timer.mean_ms(k), 4) for k, v in STEP_LABELS.items()
+               if timer.pairs[k]}
+    timer.close()
+    n_isect_end = int(opt_scene_intersects(sc, cub, col))
+    from repo_amd import synth
+    st = stage_times(synth.make_scene(args.config).to("cuda"), args.stage_iters)
     b, T, idx = st.pop("_binned"), st.pop("_T"), st.pop("_idx")
     evals_fwd, evals_bwd = reference_edge_pixel_evals(b, T, idx)
     performed = performed_evaluations(b, sc.background, T, idx,
@@ -397,9 +454,14 @@ def main():
     n_img = 3 * sc.img_h * sc.img_w
     kern = {k: round(v, 4) for k, v in st.items() if k.endswith("_ms")}
     gbs = lambda nbytes, ms_: nbytes / (ms_ * 1e-3) / 1e9  # noqa: E731
+    kern["stage_scene"] = "step 0 (fresh control points and colours)"
     kern["mse_fwd_GBs"] = round(gbs(8 * n_img, st["mse_fwd_ms"]), 1)
     kern["mse_bwd_GBs"] = round(gbs(12 * n_img, st["mse_bwd_ms"]), 1)
     kern["ssim_fwd_GBs"] = round(gbs(8 * n_img, st["ssim_fwd_ms"]), 1)
+    kern["ssim_bwd_GBs"] = round(gbs(12 * n_img, st["ssim_bwd_ms"]), 1)
+    kern["in_step_launch_ms"] = step_ms
+    kern["in_step_note"] = ("HIP-event means of each stage's launches in %d training steps "
+                            "right after the timed ones (same scene as Adam moves it)" % n_prof)
     kern["reference_edge_pixel_evals"] = {"raster_fwd": evals_fwd, "raster_bwd": evals_bwd}
     kern["binning_algorithmic_bytes"] = binning_bytes(sc, st["num_intersects"])
     kern["timed_region_launch_ms"] = {k: round(v, 4) for k, v in launch_ms.items()}
@@ -415,7 +477,9 @@ def main():
     achieved = flops / (dom_ms * 1e-3) / 1e12
     ref_units = evals_bwd if dom == "raster_bwd" else evals_fwd
     ref_equiv = ref_units * FLOPS_PER_EVAL[b.mode] / (dom_ms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "compute": "fp32 vector ALU (no matrix instructions)",
+    # "bound": the raster is bound by the fp32 vector ALUs (the compute roof;
+    # it issues no matrix instruction), not by HBM.
+    roofline = {"bound": "valu", "compute": "fp32 vector ALU (no matrix instructions)",
                 "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
                 "traffic": load_traffic(dom, args.config), "kernel": dom,
@@ -436,7 +500,9 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"config{args.config}: {workload}",
-                   "num_intersects": st["num_intersects"], "final_loss": float(loss)},
+                   "num_intersects": st["num_intersects"],
+                   "num_intersects_after_timed_steps": n_isect_end,
+                   "final_loss": float(loss)},
         "kernels": kern, "roofline": roofline,
     }
     # The CPU step of configs 4 and 5 would take minutes; their lines carry

@@ -382,11 +382,17 @@ void orc_raster_forward(const orc_scene_t *sc, int32_t row0, int32_t row1, float
 
 /* Reverse traversal recomputing transmittance (cubic_splatting.py:1339-1649,
  * cubic_polyline_splatting.py:393-658) for pixel rows [row0, row1).  Sums go
- * to double accumulators. */
+ * to double accumulators.  contrib_rgb [P,3] and isect_contrib [I] may be
+ * NULL; when given they receive the contribution statistics of
+ * cubic_splatting.py:1540-1546, 1617-1638 (cubic_polyline_splatting.py:548-553,
+ * 625-645): per primitive the sum over its pixels of fac * rgb (fac = alpha * T
+ * after the T / (1 - alpha) step, only where alpha >= 1/255), per list entry
+ * gidx the sum over the tile's pixels of fac*r + fac*g + fac*b. */
 void orc_raster_backward(const orc_scene_t *sc, int32_t row0, int32_t row1,
                          const float *final_T, const int32_t *final_idx, const float *v_out,
                          double *v_edges, double *v_colors, double *v_opacity,
-                         double *v_inv_sigma2, double *v_stroke)
+                         double *v_inv_sigma2, double *v_stroke, double *contrib_rgb,
+                         double *isect_contrib)
 {
     const int32_t W = sc->img_w;
     const int32_t tbx = (W + sc->block_x - 1) / sc->block_x;
@@ -421,6 +427,15 @@ void orc_raster_backward(const orc_scene_t *sc, int32_t row0, int32_t row1,
                 v_colors[pid * 3 + 0] += (double)(fac * v0);
                 v_colors[pid * 3 + 1] += (double)(fac * v1);
                 v_colors[pid * 3 + 2] += (double)(fac * v2);
+                if (contrib_rgb || isect_contrib) {
+                    const float cr = fac * col[0], cg = fac * col[1], cb = fac * col[2];
+                    if (contrib_rgb) {
+                        contrib_rgb[pid * 3 + 0] += (double)cr;
+                        contrib_rgb[pid * 3 + 1] += (double)cg;
+                        contrib_rgb[pid * 3 + 2] += (double)cb;
+                    }
+                    if (isect_contrib) isect_contrib[gidx] += (double)cr + (double)cg + (double)cb;
+                }
                 float va = fmaf(col[0], T, -(b0 * ra)) * v0;
                 va = fmaf(fmaf(col[1], T, -(b1 * ra)), v1, va);
                 va = fmaf(fmaf(col[2], T, -(b2 * ra)), v2, va);

@@ -332,7 +332,10 @@ def raster_forward(b, colors, opacities, background, img_h, img_w, *, fill_rules
 
 def raster_backward(b, colors, opacities, background, img_h, img_w, final_T, final_idx,
                     v_out, *, fill_rules=None, stroke_widths=None, mode=0, block_x=16,
-                    block_y=16, rows=None, workers=1):
+                    block_y=16, rows=None, workers=1, contrib=False):
+    """Backward raster (cubic_splatting.py:1197-1651) in float64 sums; with
+    ``contrib`` also the contribution statistics ``contrib_rgb`` [P,3] and
+    ``isect_contrib`` [I] (cubic_splatting.py:1540-1546, 1617-1638)."""
     keep = []
     sc = _scene(b, colors, opacities, fill_rules, stroke_widths, background, img_h, img_w,
                 block_x, block_y, mode, keep)
@@ -346,6 +349,9 @@ def raster_backward(b, colors, opacities, background, img_h, img_w, final_T, fin
     fT, fi, vo = _f32(final_T), _i32(final_idx), _f32(v_out)
     bands = row_bands(rows, img_h)
     acc = [v_edges, v_col, v_op, v_is2, v_sw]
+    if contrib:
+        acc += [np.zeros((P, 3), np.float64),
+                np.zeros(b["primitive_ids_sorted"].shape[0], np.float64)]
     parts = []
     single = workers <= 1
 
@@ -353,8 +359,9 @@ def raster_backward(b, colors, opacities, background, img_h, img_w, final_T, fin
         # With threads, each band sums into its own float64 accumulators, which
         # are added afterwards (the sums' order differs by rounding only).
         mine = acc if single else [np.zeros_like(x) for x in acc]
+        ptrs = [_p(x) for x in mine] + ([] if contrib else [None, None])
         lib().orc_raster_backward(ctypes.byref(sc), ctypes.c_int32(a), ctypes.c_int32(b),
-                                  _p(fT), _p(fi), _p(vo), *[_p(x) for x in mine])
+                                  _p(fT), _p(fi), _p(vo), *ptrs)
         if mine is not acc:
             parts.append(mine)
 
@@ -362,8 +369,11 @@ def raster_backward(b, colors, opacities, background, img_h, img_w, final_T, fin
     for part in parts:
         for x, y in zip(acc, part):
             x += y
-    return dict(v_edges=v_edges, v_colors=v_col, v_opacities=v_op, v_inv_sigma2s=v_is2,
-                v_stroke_widths=v_sw)
+    out = dict(v_edges=v_edges, v_colors=v_col, v_opacities=v_op, v_inv_sigma2s=v_is2,
+               v_stroke_widths=v_sw)
+    if contrib:
+        out.update(contrib_rgb=acc[5], isect_contrib=acc[6])
+    return out
 
 
 def accumulate_edge_grads(v_edges, nseg: int, S: int) -> np.ndarray:
@@ -460,14 +470,15 @@ def render_forward(cubics_norm, offs, colors, opacities, depths, img_h, img_w, b
     return b
 
 
-def render_backward(fw, v_out):
+def render_backward(fw, v_out, contrib=False):
     """_CubicFillSplatFunction.backward (cubic_splatting.py:2964-3125) in float64 sums:
-    returns grads for cubics_norm, colors, opacities, aa_widths (and stroke widths)."""
+    returns grads for cubics_norm, colors, opacities, aa_widths (and stroke widths);
+    with ``contrib`` also contrib_rgb and isect_contrib (:3014-3094)."""
     g = raster_backward(fw, fw["colors"], fw["opacities"], fw["background"], fw["img_h"],
                         fw["img_w"], fw["final_T"], fw["final_idx"], v_out,
                         fill_rules=fw["fill_rules"], stroke_widths=fw["stroke_widths"],
                         mode=fw["mode"], block_x=fw["block_x"], block_y=fw["block_y"],
-                        rows=fw.get("rows"), workers=fw.get("workers", 1))
+                        rows=fw.get("rows"), workers=fw.get("workers", 1), contrib=contrib)
     if fw.get("flatten_method") == "de_casteljau":
         v_px = accumulate_edge_grads_csr(g["v_edges"], fw["segment_edge_offsets"],
                                          fw["edge_t_starts"], fw["edge_t_ends"], fw["nseg"])

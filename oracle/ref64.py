@@ -34,9 +34,14 @@ def winding_by_angles(poly: torch.Tensor, px: torch.Tensor, py: torch.Tensor) ->
 
 def render64(edges, prim_edge_offsets, colors, opacities, inv_sigma2s, order, prim_tile_ranges,
              img_h, img_w, background, *, mode=0, fill_rules=None, stroke_widths=None,
-             block=16):
+             block=16, contrib=None):
     """Returns the [H,W,3] float64 image; ``edges``, ``colors``, ``opacities``,
-    ``inv_sigma2s`` and ``stroke_widths`` may require grad."""
+    ``inv_sigma2s`` and ``stroke_widths`` may require grad.
+
+    ``contrib``, a dict, receives each primitive's composited term: "rgb"
+    [P,3] = sum over pixels of alpha * T_before * colour, and "tile" =
+    {(primitive, tile id): sum over the tile's pixels of alpha * T_before *
+    (r + g + b)} (what the backward's contribution statistics must equal)."""
     dev = edges.device
     jj, ii = torch.meshgrid(torch.arange(img_w, dtype=torch.float64),
                             torch.arange(img_h, dtype=torch.float64), indexing="xy")
@@ -48,6 +53,10 @@ def render64(edges, prim_edge_offsets, colors, opacities, inv_sigma2s, order, pr
     T = torch.ones(npx, dtype=torch.float64, device=dev)
     C = torch.zeros(npx, 3, dtype=torch.float64, device=dev)
     done = torch.zeros(npx, dtype=torch.bool, device=dev)
+    tbx = (img_w + block - 1) // block
+    if contrib is not None:
+        contrib["rgb"] = np.zeros((len(order), 3), np.float64)
+        contrib["tile"] = {}
     for p in [int(v) for v in order]:
         r = [int(v) for v in prim_tile_ranges[p]]
         member = (tx >= r[0]) & (tx < r[2]) & (ty >= r[1]) & (ty < r[3])
@@ -82,6 +91,14 @@ def render64(edges, prim_edge_offsets, colors, opacities, inv_sigma2s, order, pr
         alpha = torch.clamp(opacities[p] * cov, max=0.999)
         use = member & (~done) & (alpha.detach() >= 1.0 / 255.0)
         a_use = torch.where(use, alpha, torch.zeros_like(alpha))
+        if contrib is not None:
+            w = (a_use * T).detach()
+            col = colors[p].detach().double()
+            contrib["rgb"][p] = (w.sum() * col).numpy()
+            tid = (ty * tbx + tx)[use]
+            wt = torch.bincount(tid, weights=w[use] * col.sum())
+            for t in torch.nonzero(wt).reshape(-1).tolist():
+                contrib["tile"][(p, t)] = float(wt[t])
         C = C + (a_use * T).unsqueeze(1) * colors[p].unsqueeze(0)
         T = T * (1.0 - a_use)
         done = done | (use & (T.detach() <= 1e-4))

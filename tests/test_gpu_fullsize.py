@@ -8,9 +8,8 @@
   bit-exact (this also takes the multi-pass depth-rank sort for P > 16,384),
   forward and backward over the whole frame;
 * config 5 (16,384 clustered paths x 6 segments, S = 32, 2048x2048, about
-  7.2 million intersections): binning bit-exact, and forward / backward on
-  32-row bands through the tiles with the longest lists (chosen from the
-  GPU's own tile_bins);
+  7.2 million intersections): binning bit-exact, and forward / backward over
+  the whole frame;
 * aniso_intersects=True (cubic_splatting.py:692-708): binning and raster
   bit-exact.
 
@@ -122,33 +121,20 @@ def test_cfg5_full_size_binning_bit_exact():
     _assert_binning(b, ob)
 
 
-def _heaviest_bands(tile_bins, tbx, tby, n=3, rows=32):
-    """n disjoint bands of `rows` pixel rows, each starting at the tile row of
-    one of the tiles with the longest lists (heaviest first)."""
-    lens = tile_bins[:, 1] - tile_bins[:, 0]
-    bands = []
-    for t in np.argsort(-lens, kind="stable"):
-        r0 = int(t // tbx) * 16
-        r0 = min(r0, tby * 16 - rows)
-        if all(r0 + rows <= a or r0 >= b for a, b in bands):
-            bands.append((r0, r0 + rows))
-        if len(bands) == n:
-            break
-    return sorted(bands)
-
-
 @pytest.mark.gpu
-def test_cfg5_heavy_bands_forward_and_backward():
+def test_cfg5_full_frame_forward_and_backward():
+    """Config 5 over the whole 2048x2048 frame: every tile row (the first and
+    last ones, the eight clusters, the lightest tiles), forward bit-exact and
+    backward within the gradient tolerance."""
     sc = _scene("cfg5")
     b, s = hip_bin(sc)
     out, T, idx = splat.rasterize_forward(b, s.background.float().contiguous())
     bins = b.tile_bins.cpu().numpy()
-    tbx, tby = O.tile_bounds(sc.img_h, sc.img_w)
-    bands = _heaviest_bands(bins, tbx, tby)
     lens = bins[:, 1] - bins[:, 0]
-    print(f"[cfg5] bands {bands}; longest list {int(lens.max())}, mean {lens.mean():.1f}",
-          flush=True)
-    fw = oracle_forward(sc, rows=bands)
+    print(f"[cfg5] full frame; longest list {int(lens.max())}, mean {lens.mean():.1f}, "
+          f"empty tiles {int((lens == 0).sum())}", flush=True)
+    fw = oracle_forward(sc)
+    bands = [(0, sc.img_h)]
     _assert_forward(out, T, idx, fw, bands)
     _check_backward(sc, s, b, T, idx, fw, bands)
 
@@ -189,3 +175,45 @@ def test_aniso_through_the_render_entry_point():
         distance_samples=sc.S, aniso_intersects=True)
     fw = oracle_forward(ANISO["cfg2"](), aniso=True)
     np.testing.assert_array_equal(_bits(img.cpu().numpy()), _bits(fw["out"]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4"])
+def test_full_frame_contrib_outputs_through_process_fn(name):
+    """curve_contrib_rgb / curve_isect_contrib requested by a
+    pre_backward_rasterize hook (cubic_splatting.py:3014-3094; the polyline
+    path.s cubic_polyline_splatting.py:1225-1310) over the whole frame,
+    against the oracle's per-primitive and per-list-entry sums
+    (cubic_splatting.py:1540-1546, 1617-1638)."""
+    import manbo
+    print(f"[contrib] {name}", flush=True)
+    sc = _scene(name)
+    s = sc.to("cuda")
+    seen = {}
+
+    def hook(stage, payload):
+        seen[stage] = payload
+        if stage == "pre_backward_rasterize":
+            return {"collect_curve_contrib_rgb": True, "collect_curve_isect_contrib": True}
+        return None
+
+    col = s.colors.clone().requires_grad_(True)
+    if s.stroke_widths is None:
+        img = manbo.ops.render_cubic_fill_splat_tilelang(
+            s.cubics_norm, s.seg_offsets, col, s.opacities, s.depths, sc.img_h, sc.img_w, 16, 16,
+            s.background, fill_rules=s.fill_rules, aa_widths=s.aa_widths, distance_samples=sc.S,
+            process_fn=hook)
+    else:
+        img = manbo.ops.render_cubic_polyline_splat_tilelang(
+            s.cubics_norm, s.seg_offsets, col, s.opacities, s.stroke_widths, s.depths, sc.img_h,
+            sc.img_w, 16, 16, s.background, aa_widths=s.aa_widths, distance_samples=sc.S,
+            process_fn=hook)
+    v = random_v_out(sc.img_h, sc.img_w, seed=21)
+    img.backward(v.cuda())
+    post = seen["post_backward_rasterize"]
+    fw = oracle_forward(sc)
+    g = O.render_backward(fw, v.numpy(), contrib=True)
+    assert post["curve_isect_contrib"].shape == g["isect_contrib"].shape
+    check_grads([("curve_contrib_rgb", post["curve_contrib_rgb"], g["contrib_rgb"]),
+                 ("curve_isect_contrib", post["curve_isect_contrib"], g["isect_contrib"]),
+                 ("v_colors", col.grad, g["v_colors"])])

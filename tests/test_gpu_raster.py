@@ -161,7 +161,8 @@ def test_autograd_function_end_to_end(stroke):
 @pytest.mark.gpu
 def test_process_fn_hooks_and_contrib_outputs():
     """pre/post_backward_rasterize hooks (cubic_splatting.py:3014-3094): the
-    contribution outputs equal sums the oracle recomputes; a hook can replace
+    contribution outputs they request equal the oracle's (per primitive and per
+    list entry, cubic_splatting.py:1540-1546, 1617-1638); a hook can replace
     the color gradient."""
     import manbo
     sc = synth.small_scene(2, P=12, h=64, w=64, rmax=25.0)
@@ -184,10 +185,10 @@ def test_process_fn_hooks_and_contrib_outputs():
     contrib = post["curve_contrib_rgb"]
     isect = post["curve_isect_contrib"]
     assert contrib.shape == (12, 3) and isect.shape == post["primitive_ids_sorted"].shape
-    # sum_e fac_e * rgb over intersections == per-primitive totals
-    pid = post["primitive_ids_sorted"].long()
-    per = torch.zeros(12, device=dev).index_add_(0, pid, isect)
-    assert torch.allclose(per, contrib.sum(1), rtol=1e-4, atol=1e-4)
+    fw = oracle_forward(sc)
+    g = O.render_backward(fw, np.ones((sc.img_h, sc.img_w, 3), np.float32), contrib=True)
+    check_grads([("curve_contrib_rgb", contrib, g["contrib_rgb"]),
+                 ("curve_isect_contrib", isect, g["isect_contrib"])])
     # the hook saw the kernel's v_colors and doubled it
     ref = post["v_colors"] * 2.0
     assert torch.allclose(col.grad, ref)

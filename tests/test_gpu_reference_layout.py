@@ -116,12 +116,13 @@ def test_reference_layout_raster_widths_contrib_and_empty():
         *_positional(t), T, idx, v, **kw, distance_samples=sc.S, curve_contrib_rgb=crgb,
         curve_isect_contrib=cis)
     assert float(crgb.abs().sum()) > 0 and float(cis.abs().sum()) > 0
-    # Each intersection's contribution summed over a primitive's intersections
-    # equals the primitive's summed rgb contribution (r + g + b).
-    per_prim = torch.zeros((P,), device="cuda").index_add_(0, t["primitive_ids_sorted"].long(),
-                                                           cis)
-    np.testing.assert_allclose(per_prim.cpu().numpy(), crgb.sum(1).cpu().numpy(), rtol=1e-4,
-                               atol=1e-4 * float(per_prim.abs().max()))
+    # Against the oracle's contribution statistics (cubic_splatting.py:1540-1546,
+    # 1617-1638), per primitive and per list entry.
+    g = O.raster_backward(ob, d["colors"], d["opacities"], d["background"], sc.img_h, sc.img_w,
+                          T.cpu().numpy(), idx.cpu().numpy(), v.cpu().numpy(),
+                          fill_rules=d["fill_rules"], workers=O.default_workers(), contrib=True)
+    check_grads([("curve_contrib_rgb", crgb, g["contrib_rgb"]),
+                 ("curve_isect_contrib", cis, g["isect_contrib"])])
     t0 = dict(t)
     t0["primitive_ids_sorted"] = t["primitive_ids_sorted"][:0]
     kw0 = dict(kw)

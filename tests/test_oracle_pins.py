@@ -287,6 +287,48 @@ def test_raster_vs_independent_float64(seed, stroke):
         assert err < 1e-4, (name, err)
 
 
+@pytest.mark.parametrize("seed,stroke", [(0, False), (7, False), (2, True)])
+def test_contrib_outputs_vs_float64_composite(seed, stroke):
+    """The backward's contribution statistics (cubic_splatting.py:1540-1546,
+    1617-1638) are each primitive's term of the forward composite: per
+    primitive sum(alpha T_before rgb) and per (primitive, tile) list entry
+    sum(alpha T_before (r+g+b)), against the independent float64 renderer;
+    and summed over primitives they rebuild the image minus T * background."""
+    sc = synth.small_scene(seed, P=9, h=56, w=72, S=8, stroke=stroke)
+    sw = sc.stroke_widths.numpy() if stroke else None
+    fw = O.render_forward(sc.cubics_norm.numpy(), sc.seg_offsets.numpy(), sc.colors.numpy(),
+                          sc.opacities.numpy(), sc.depths.numpy(), sc.img_h, sc.img_w,
+                          sc.background.numpy(), S=sc.S, stroke_widths=sw)
+    _, edges = _ref64_inputs(fw, sc, stroke)
+    c64 = {}
+    ref64.render64(edges.detach(), fw["prim_edge_offsets"], sc.colors.double(),
+                   sc.opacities.double(), torch.from_numpy(fw["inv_sigma2s"].astype(np.float64)),
+                   ref64.depth_order(sc.depths.numpy()), fw["prim_tile_ranges"], sc.img_h,
+                   sc.img_w, sc.background.double(), mode=int(stroke),
+                   stroke_widths=None if sw is None else torch.from_numpy(sw.astype(np.float64)),
+                   contrib=c64)
+    v = np.random.default_rng(seed).standard_normal((sc.img_h, sc.img_w, 3)).astype(np.float32)
+    g = O.render_backward(fw, v, contrib=True)
+    rgb, isect = g["contrib_rgb"], g["isect_contrib"]
+    assert rgb.shape == (9, 3) and isect.shape == fw["primitive_ids_sorted"].shape
+    assert np.abs(rgb).max() > 1.0
+    np.testing.assert_allclose(rgb, c64["rgb"], rtol=0, atol=1e-5 * np.abs(c64["rgb"]).max())
+    # per list entry: key (primitive, tile) of global index g
+    bins, ids = fw["tile_bins"], fw["primitive_ids_sorted"]
+    tile_of = np.repeat(np.arange(bins.shape[0]), bins[:, 1] - bins[:, 0])
+    got = {(int(p), int(t)): float(x) for p, t, x in zip(ids, tile_of, isect)}
+    for k in set(got) | set(c64["tile"]):
+        assert abs(got.get(k, 0.0) - c64["tile"].get(k, 0.0)) <= 1e-5 * max(
+            1.0, abs(c64["tile"].get(k, 0.0))), k
+    # entries contribute nothing past a pixel's final index: zero beyond the tile's last
+    assert np.all(isect[fw["final_idx"].max() + 1:] == 0)
+    # the composite: out = sum of terms + T * background
+    bg = fw["background"].astype(np.float64)
+    rebuilt = rgb.sum(0) + fw["final_T"].astype(np.float64).sum() * bg
+    np.testing.assert_allclose(rebuilt, fw["out"].astype(np.float64).sum((0, 1)), rtol=1e-6)
+    np.testing.assert_allclose(isect.sum(), rgb.sum(), rtol=1e-9)
+
+
 def _square(x0, y0, x1, y1, n_per_side=1):
     """Closed axis-aligned square as 4 straight cubics (counter-clockwise)."""
     corners = [(x0, y0), (x1, y0), (x1, y1), (x0, y1)]
