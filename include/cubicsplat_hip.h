@@ -201,7 +201,7 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
 /* Tiles: every raster entry point takes the tile size block_x x block_y of
  * the binning whose tile_bins it reads (ops/cubic_splatting.py:2778-2782);
  * both must be positive multiples of 16 with (block_x / 16) * (block_y / 16)
- * <= 16.  The raster runs one workgroup of two waves (16 x 8 pixels each) per
+ * <= 16 (other sizes: the _any_tile entry points below).  The raster runs one workgroup of two waves (16 x 8 pixels each) per
  * 16 x 16 sub-block of the image; the 2 (block_x / 16) (block_y / 16) waves
  * of a tile all walk its list, and S = ceil(W / 16) * ceil(H / 16) counts the
  * sub-blocks.
@@ -222,6 +222,42 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
  * chunked == 0 sorts all of them (balance across XCDs for skewed scenes). */
 int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
                          int32_t* tile_order, hipStream_t stream);
+
+/* Tiles of any size (block_x * block_y <= 1024, the reference's
+ * one-thread-per-pixel launch threads=(block_x, block_y)), for sizes the
+ * 16 x 16 sub-block entry points above do not take (for example 8 x 8 or
+ * 16 x 8): one workgroup per tile, one lane per pixel, every edge of every
+ * list entry evaluated with the same expressions (image, final_Ts and
+ * final_idx identical to the sub-block kernels' on tiles both take).  No
+ * raster log, no tile order.
+ * cs_rasterize_forward_any_tile replaces rasterize_cubic_fill_forward_kernel
+ * (ops/cubic_splatting.py:918-1194, wrapper :2181-2305; mode 1:
+ * ops/cubic_polyline_splatting.py:33-249); edges [E] edge records, prim_recs
+ * [P] primitive records as for cs_rasterize_forward; out_img [H,W,3] or, with
+ * out_planar, three [H,W] planes.
+ * cs_rasterize_backward_any_tile replaces rasterize_cubic_fill_backward_kernel
+ * (ops/cubic_splatting.py:1197-1651, wrapper :2572-2747; mode 1:
+ * ops/cubic_polyline_splatting.py:252-660): adds into v_edges [E,2,2]
+ * (zeroed by the caller; fold with cs_accumulate_edge_grads or
+ * cs_accumulate_edge_grads_csr), v_colors [P,3], v_opacities, v_inv_sigma2s
+ * [P], v_stroke_widths [P] (mode 1) and, when not NULL, curve_contrib_rgb
+ * [P,3] / curve_isect_contrib [I]. */
+int cs_rasterize_forward_any_tile(int32_t mode, const int32_t* prim_ids_sorted,
+                                  const int32_t* tile_bins, const void* edges,
+                                  const void* prim_recs, const float* background, int32_t img_h,
+                                  int32_t img_w, int32_t block_x, int32_t block_y,
+                                  float* out_img, int32_t out_planar, float* final_Ts,
+                                  int32_t* final_idx, hipStream_t stream);
+int cs_rasterize_backward_any_tile(int32_t mode, const int32_t* prim_ids_sorted,
+                                   const int32_t* tile_bins, const void* edges,
+                                   const void* prim_recs, const float* background, int32_t img_h,
+                                   int32_t img_w, int32_t block_x, int32_t block_y,
+                                   const float* final_Ts, const int32_t* final_idx,
+                                   const float* v_output, int32_t v_output_planar,
+                                   float* v_edges, float* v_colors, float* v_opacities,
+                                   float* v_inv_sigma2s, float* v_stroke_widths,
+                                   float* curve_contrib_rgb, float* curve_isect_contrib,
+                                   hipStream_t stream);
 
 /* Raster log (no reference counterpart: the reference's backward re-runs the
  * edge loop and the coverage, ops/cubic_splatting.py:1451-1530,

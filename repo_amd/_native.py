@@ -64,6 +64,11 @@ _SIGNATURES = {
                                                      _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P,
                                                      _P]),
     "cs_raster_tile_order": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
+    "cs_rasterize_forward_any_tile": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                                     _I32, _P, _I32, _P, _P, _P]),
+    "cs_rasterize_backward_any_tile": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                                      _I32, _P, _P, _P, _I32, _P, _P, _P, _P,
+                                                      _P, _P, _P, _P]),
     "cs_raster_records_from_edges": (ctypes.c_int, [_I32, _P, _I32, _P, _P, _I64, _P, _P, _P, _P,
                                                     _P, _I32, _P, _I32, _P, _P, _P, _P, _P, _P,
                                                     _P]),

@@ -1549,6 +1549,234 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
     }
 }
 
+// ---------------------------------------------------------------------------
+// Tiles of any size.  The 16 x 16 kernels above need tiles whose sides are
+// multiples of 16; the reference takes any block_x x block_y and launches one
+// thread per pixel of a tile (threads=(block_x, block_y),
+// cubic_splatting.py:918-1194 and :1197-1651, cubic_polyline_splatting.py:
+// 33-249 and :252-660).  These kernels keep that shape: one workgroup per
+// tile, one lane per pixel (the workgroup rounded up to whole waves), each
+// wave walking the tile's list and evaluating every edge of every entry at
+// its pixels, with the expressions of the 16 x 16 kernels and the exact
+// coverage everywhere (no culling, so no culling argument is needed for
+// exactness).  Edge records and primitive records are wave-uniform scalar
+// loads.
+constexpr int kAnyMaxThreads = 1024;
+
+struct AnyPixel {
+    int i, j;
+    bool valid;   // inside the tile and the image
+    float px, py;
+};
+
+__device__ __forceinline__ AnyPixel any_pixel(int tile, int bx, int by, int tbx, int img_h,
+                                              int img_w) {
+    AnyPixel q;
+    const int ty = tile / tbx, tx = tile - ty * tbx;
+    const int t = (int)threadIdx.x;
+    const bool in_tile = t < bx * by;
+    const int li = in_tile ? t / bx : 0;
+    const int lj = in_tile ? t - li * bx : 0;
+    q.i = ty * by + li;
+    q.j = tx * bx + lj;
+    q.valid = in_tile && q.i < img_h && q.j < img_w;
+    q.px = (float)q.j + 0.5f;
+    q.py = (float)q.i + 0.5f;
+    return q;
+}
+
+// Minimum distance (with the best edge, its projection and offset), and for
+// fills the winding number, over edges [e0, e1) (cubic_splatting.py:1095-1134).
+template <int MODE>
+__device__ __forceinline__ Geom any_geometry(cptr<EdgeRec> edges, int e0, int e1, float px,
+                                             float py) {
+    Geom G;
+    G.min_d2 = 1e30f;
+    G.winding = 0;
+    G.best = -1;
+    G.bproj = G.bdx = G.bdy = 0.0f;
+    for (int e = e0; e < e1; ++e) {
+        const EdgeRec E = edges[e];
+        const float wx = px - E.x0, wy = py - E.y0;
+        dist_term<2>(E, e, wx, wy, G);
+        if (MODE == 0) cross_term(E, wx, wy, py, G);
+    }
+    return G;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kAnyMaxThreads) void k_raster_fwd_any(
+    const int32_t* __restrict__ ids, const int32_t* __restrict__ bins,
+    const EdgeRec* __restrict__ edges_g, const PrimRec* __restrict__ prims_g,
+    const float* __restrict__ bg, int img_h, int img_w, int bx, int by, int tbx,
+    float* __restrict__ out, int out_planar, float* __restrict__ final_T,
+    int32_t* __restrict__ final_idx) {
+    const int tile = blockIdx.x;
+    const AnyPixel q = any_pixel(tile, bx, by, tbx, img_h, img_w);
+    const cptr<PrimRec> prims = as_const(prims_g);
+    const cptr<EdgeRec> edges = as_const(edges_g);
+    const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
+    float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
+    int cur = 0;
+    bool done = !q.valid;
+    for (int g = g0; g < g1; ++g) {
+        if (__ballot(!done) == 0) break;
+        const int pid = __builtin_amdgcn_readfirstlane(ids[g]);
+        const PrimRec pr = load_prim_fwd(prims, pid);
+        const Geom G = any_geometry<MODE>(edges, pr.e0, pr.e1, q.px, q.py);
+        const Cov c = coverage<MODE>(pr, G, __builtin_huge_valf(), __builtin_huge_valf());
+        composite(pr, fminf(kAlphaCap, pr.opacity * c.cov), g, T, C0, C1, C2, cur, done);
+    }
+    if (!q.valid) return;
+    const size_t pix = (size_t)q.i * img_w + q.j;
+    final_T[pix] = T;
+    final_idx[pix] = cur;
+    const size_t ch = out_planar ? (size_t)img_h * img_w : 1;
+    float* const o = out + (out_planar ? pix : 3 * pix);
+    o[0] = __builtin_fmaf(T, bg[0], C0);
+    o[ch] = __builtin_fmaf(T, bg[1], C1);
+    o[2 * ch] = __builtin_fmaf(T, bg[2], C2);
+}
+
+__device__ __forceinline__ float any_wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Reverse walk over the entries at or below each pixel's final index,
+// recomputing the geometry, the coverage and the transmittance
+// (cubic_splatting.py:1339-1649).  Per-primitive gradients (and the
+// contribution statistics) are summed over the wave and added by one lane;
+// each pixel adds its best edge's endpoint gradients to v_edges [E] x
+// (x0, y0, x1, y1), which the caller folds into the control points.
+template <int MODE>
+__global__ __launch_bounds__(kAnyMaxThreads) void k_raster_bwd_any(
+    const int32_t* __restrict__ ids, const int32_t* __restrict__ bins,
+    const EdgeRec* __restrict__ edges_g, const PrimRec* __restrict__ prims_g,
+    const float* __restrict__ bg, int img_h, int img_w, int bx, int by, int tbx,
+    const float* __restrict__ fT, const int32_t* __restrict__ fidx,
+    const float* __restrict__ v_out, int v_planar, float* __restrict__ v_edges,
+    float* __restrict__ v_col, float* __restrict__ v_op, float* __restrict__ v_is2,
+    float* __restrict__ v_sw, float* __restrict__ c_rgb, float* __restrict__ c_isect) {
+    const int tile = blockIdx.x;
+    const AnyPixel q = any_pixel(tile, bx, by, tbx, img_h, img_w);
+    const cptr<PrimRec> prims = as_const(prims_g);
+    const cptr<EdgeRec> edges = as_const(edges_g);
+    const int g0 = bins[2 * tile], g1 = bins[2 * tile + 1];
+    const int lane = threadIdx.x & (kWave - 1);
+    const size_t pix = q.valid ? (size_t)q.i * img_w + q.j : 0;
+    float T = q.valid ? fT[pix] : 1.0f;
+    const float T_final = T;
+    const int last = q.valid ? fidx[pix] : g0 - 1;
+    const size_t ch = v_planar ? (size_t)img_h * img_w : 1;
+    const float* const vo = v_out + (v_planar ? pix : 3 * pix);
+    const float v0 = q.valid ? vo[0] : 0.0f;
+    const float v1 = q.valid ? vo[ch] : 0.0f;
+    const float v2 = q.valid ? vo[2 * ch] : 0.0f;
+    const float bg_dot = __builtin_fmaf(bg[2], v2, __builtin_fmaf(bg[1], v1, bg[0] * v0));
+    float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
+    // The wave's last entry to visit: the largest final index among its pixels.
+    int gmax = last;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) gmax = max(gmax, __shfl_xor(gmax, off, kWave));
+    gmax = __builtin_amdgcn_readfirstlane(gmax < g1 - 1 ? gmax : g1 - 1);
+    const bool want_contrib = (c_rgb != nullptr) | (c_isect != nullptr);
+    for (int g = gmax; g >= g0; --g) {
+        const int pid = __builtin_amdgcn_readfirstlane(ids[g]);
+        const PrimRec pr = load_prim_fwd(prims, pid);
+        const bool live = q.valid && g <= last;
+        const Geom G = any_geometry<MODE>(edges, pr.e0, pr.e1, q.px, q.py);
+        const Cov c = coverage<MODE>(pr, G, __builtin_huge_valf(), __builtin_huge_valf());
+        const float op = pr.opacity;
+        const float alpha = fminf(kAlphaCap, op * c.cov);
+        const bool contrib = live && alpha >= kAlphaMin;
+        if (__ballot(contrib) == 0) continue;
+        float pv[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        float cv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float gx = 0.0f, gy = 0.0f;
+        bool geom = false;
+        if (contrib) {
+            const float ra = 1.0f / (1.0f - alpha);
+            T = T * ra;
+            const float fac = alpha * T;
+            pv[0] = fac * v0;
+            pv[1] = fac * v1;
+            pv[2] = fac * v2;
+            if (want_contrib) {
+                cv[0] = fac * pr.r;
+                cv[1] = fac * pr.g;
+                cv[2] = fac * pr.b;
+                cv[3] = cv[0] + cv[1] + cv[2];
+            }
+            float va = __builtin_fmaf(pr.r, T, -(b0 * ra)) * v0;
+            va = __builtin_fmaf(__builtin_fmaf(pr.g, T, -(b1 * ra)), v1, va);
+            va = __builtin_fmaf(__builtin_fmaf(pr.b, T, -(b2 * ra)), v2, va);
+            va = __builtin_fmaf(T_final * ra, -bg_dot, va);
+            b0 = __builtin_fmaf(pr.r, fac, b0);
+            b1 = __builtin_fmaf(pr.g, fac, b1);
+            b2 = __builtin_fmaf(pr.b, fac, b2);
+            if (alpha < kAlphaCap) {
+                pv[3] = c.cov * va;
+                if (MODE == 0) {
+                    const float v_logit = -(op * va) * c.cov * (1.0f - c.cov);
+                    pv[4] = v_logit * c.sgn * c.dist * 2.0f * 0.5f / fmaxf(pr.inv_sigma, kEps);
+                    if (c.dist > kEps && G.best >= 0) {
+                        const float v_dist = v_logit * c.sgn * pr.inv_sigma * 2.0f;
+                        gx = v_dist * G.bdx / c.dist;
+                        gy = v_dist * G.bdy / c.dist;
+                        geom = true;
+                    }
+                } else {
+                    const float v_sigma = -op * c.cov * va;
+                    pv[4] = 0.5f * c.ed * c.ed * v_sigma;
+                    if (c.ed > 0.0f) {
+                        const float v_e = v_sigma * c.ed * pr.inv_sigma2;
+                        pv[5] = -0.5f * v_e;
+                        if (c.dist > kEps && G.best >= 0) {
+                            gx = v_e * G.bdx / c.dist;
+                            gy = v_e * G.bdy / c.dist;
+                            geom = true;
+                        }
+                    }
+                }
+            }
+        }
+        constexpr int NV = MODE == 1 ? 6 : 5;
+        float tot[6];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) tot[k] = any_wave_sum(pv[k]);
+        if (lane == 0) {
+            atomicAdd(v_col + 3 * pid + 0, tot[0]);
+            atomicAdd(v_col + 3 * pid + 1, tot[1]);
+            atomicAdd(v_col + 3 * pid + 2, tot[2]);
+            atomicAdd(v_op + pid, tot[3]);
+            atomicAdd(v_is2 + pid, tot[4]);
+            if (MODE == 1) atomicAdd(v_sw + pid, tot[5]);
+        }
+        if (want_contrib) {
+            float ct[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ct[k] = any_wave_sum(cv[k]);
+            if (lane == 0) {
+                if (c_rgb) {
+                    atomicAdd(c_rgb + 3 * pid + 0, ct[0]);
+                    atomicAdd(c_rgb + 3 * pid + 1, ct[1]);
+                    atomicAdd(c_rgb + 3 * pid + 2, ct[2]);
+                }
+                if (c_isect) atomicAdd(c_isect + g, ct[3]);
+            }
+        }
+        if (geom) {
+            float* ve = v_edges + 4 * (size_t)G.best;
+            atomicAdd(ve + 0, (1.0f - G.bproj) * gx);
+            atomicAdd(ve + 1, (1.0f - G.bproj) * gy);
+            atomicAdd(ve + 2, G.bproj * gx);
+            atomicAdd(ve + 3, G.bproj * gy);
+        }
+    }
+}
+
 }  // namespace cs
 
 using namespace cs;
@@ -1939,5 +2167,78 @@ extern "C" int cs_backward_finalize(const float* v_cubics_px, int32_t nseg, int3
     hipLaunchKernelGGL(k_finalize, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                        v_cubics_px, nseg, half_w, half_h, widths, v_inv_sigma2s, nprim,
                        v_cubics_norm, v_aa_widths);
+    return raster_status();
+}
+
+// Tiles of any size (at most kAnyMaxThreads pixels): the grid is one
+// workgroup per tile.
+static bool any_tile_grid(int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
+                          int& ntiles, int& tbx, int& threads) {
+    if (img_h <= 0 || img_w <= 0 || img_h > kMaxImageDim || img_w > kMaxImageDim ||
+        block_x <= 0 || block_y <= 0 || (int64_t)block_x * block_y > kAnyMaxThreads)
+        return false;
+    tbx = (img_w + block_x - 1) / block_x;
+    ntiles = tbx * ((img_h + block_y - 1) / block_y);
+    threads = ((block_x * block_y + kWave - 1) / kWave) * kWave;
+    return true;
+}
+
+extern "C" int cs_rasterize_forward_any_tile(int32_t mode, const int32_t* prim_ids_sorted,
+                                             const int32_t* tile_bins, const void* edges,
+                                             const void* prim_recs, const float* background,
+                                             int32_t img_h, int32_t img_w, int32_t block_x,
+                                             int32_t block_y, float* out_img,
+                                             int32_t out_planar, float* final_Ts,
+                                             int32_t* final_idx, hipStream_t stream) {
+    int ntiles, tbx, threads;
+    if ((mode != 0 && mode != 1) || !any_tile_grid(img_h, img_w, block_x, block_y, ntiles, tbx,
+                                                    threads))
+        return CS_ERR_ARGS;
+    if (!tile_bins || !prim_recs || !edges || !background || !out_img || !final_Ts ||
+        !final_idx)
+        return CS_ERR_ARGS;
+    const auto* E = reinterpret_cast<const EdgeRec*>(edges);
+    const auto* P = reinterpret_cast<const PrimRec*>(prim_recs);
+    if (mode == 0)
+        hipLaunchKernelGGL(k_raster_fwd_any<0>, dim3(ntiles), dim3(threads), 0, stream,
+                           prim_ids_sorted, tile_bins, E, P, background, img_h, img_w, block_x,
+                           block_y, tbx, out_img, out_planar ? 1 : 0, final_Ts, final_idx);
+    else
+        hipLaunchKernelGGL(k_raster_fwd_any<1>, dim3(ntiles), dim3(threads), 0, stream,
+                           prim_ids_sorted, tile_bins, E, P, background, img_h, img_w, block_x,
+                           block_y, tbx, out_img, out_planar ? 1 : 0, final_Ts, final_idx);
+    return raster_status();
+}
+
+extern "C" int cs_rasterize_backward_any_tile(
+    int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
+    const void* prim_recs, const float* background, int32_t img_h, int32_t img_w,
+    int32_t block_x, int32_t block_y, const float* final_Ts, const int32_t* final_idx,
+    const float* v_output, int32_t v_output_planar, float* v_edges, float* v_colors,
+    float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
+    float* curve_contrib_rgb, float* curve_isect_contrib, hipStream_t stream) {
+    int ntiles, tbx, threads;
+    if ((mode != 0 && mode != 1) || !any_tile_grid(img_h, img_w, block_x, block_y, ntiles, tbx,
+                                                    threads))
+        return CS_ERR_ARGS;
+    if (!tile_bins || !prim_recs || !edges || !background || !final_Ts || !final_idx ||
+        !v_output || !v_edges || !v_colors || !v_opacities || !v_inv_sigma2s ||
+        (mode == 1 && !v_stroke_widths))
+        return CS_ERR_ARGS;
+    const auto* E = reinterpret_cast<const EdgeRec*>(edges);
+    const auto* P = reinterpret_cast<const PrimRec*>(prim_recs);
+    const int planar = v_output_planar ? 1 : 0;
+    if (mode == 0)
+        hipLaunchKernelGGL(k_raster_bwd_any<0>, dim3(ntiles), dim3(threads), 0, stream,
+                           prim_ids_sorted, tile_bins, E, P, background, img_h, img_w, block_x,
+                           block_y, tbx, final_Ts, final_idx, v_output, planar, v_edges,
+                           v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
+                           curve_contrib_rgb, curve_isect_contrib);
+    else
+        hipLaunchKernelGGL(k_raster_bwd_any<1>, dim3(ntiles), dim3(threads), 0, stream,
+                           prim_ids_sorted, tile_bins, E, P, background, img_h, img_w, block_x,
+                           block_y, tbx, final_Ts, final_idx, v_output, planar, v_edges,
+                           v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths,
+                           curve_contrib_rgb, curve_isect_contrib);
     return raster_status();
 }

@@ -84,6 +84,11 @@ def _check_block(block):
     return int(block[0]), int(block[1])
 
 
+def is_sub_block_tile(bx, by):
+    from .splat import is_sub_block_tile as f
+    return f(bx, by)
+
+
 def _check_pixels(name, t, shape):
     if tuple(t.shape) != tuple(shape):
         raise ValueError(f"{name} must be {list(shape)}, got {list(t.shape)}")
@@ -167,6 +172,11 @@ def rasterize_cubic_fill_forward_tilelang(tile_bounds, block, img_size, primitiv
                                          _f32(opacities).view(-1), inv_s2,
                                          _i32(fill_rules).view(-1), bins, H, W, block_x=bx,
                                          block_y=by)
+    if not is_sub_block_tile(bx, by):
+        N.call("cs_rasterize_forward_any_tile", 0, N.ptr(ids), N.ptr(bins), N.ptr(edges),
+               N.ptr(prims), N.ptr(bg), H, W, bx, by, N.ptr(out_img), 0, N.ptr(final_Ts),
+               N.ptr(final_idx), N.stream(dev))
+        return out_img, final_Ts, final_idx
     N.call("cs_rasterize_forward", 0, N.ptr(ids), N.ptr(bins), N.ptr(edges),
            N.ptr(culls), N.ptr(prims), N.ptr(bg), H, W, bx, by, 0, N.ptr(out_img), 0,
            N.ptr(final_Ts),
@@ -242,6 +252,35 @@ def rasterize_cubic_fill_backward_tilelang(tile_bounds, block, img_size, primiti
     grads = (N.ptr(v_px), N.ptr(v_colors), N.ptr(v_opacities), N.ptr(v_inv_sigma2s), None,
              N.ptr(contrib), N.ptr(isect_contrib), 0, None, None, N.stream(dev))
     fT, fi, vo = _f32(final_Ts), _i32(final_idx), _f32(v_output)
+    if not is_sub_block_tile(bx, by):
+        # Tiles of any size: endpoint gradients per edge, then folded into
+        # the control points (cubic_splatting.py:2308-2487).
+        v_edges = torch.zeros((E, 4), dtype=torch.float32, device=dev)
+        N.call("cs_rasterize_backward_any_tile", 0, N.ptr(ids), N.ptr(bins), N.ptr(edges),
+               N.ptr(prims), N.ptr(bg), H, W, bx, by, N.ptr(fT), N.ptr(fi), N.ptr(vo), 0,
+               N.ptr(v_edges), N.ptr(v_colors), N.ptr(v_opacities), N.ptr(v_inv_sigma2s), None,
+               N.ptr(contrib), N.ptr(isect_contrib), N.stream(dev))
+        v_norm = torch.empty_like(v_px)
+        if method == "bernstein":
+            eps = max(2, int(distance_samples)) - 1
+            if E != num_segments * eps:
+                raise ValueError(f"v_edges size mismatch: got {E}, expected {num_segments * eps}")
+            N.call("cs_accumulate_edge_grads", N.ptr(v_edges), num_segments, eps, H, W,
+                   N.ptr(v_px), N.ptr(v_norm), N.stream(dev))
+        else:
+            if segment_edge_offsets is None or edge_t_starts is None or edge_t_ends is None:
+                raise ValueError("de_casteljau flatten backward requires CSR metadata "
+                                 "(segment_edge_offsets, edge_t_starts, edge_t_ends)")
+            seo = _i32(segment_edge_offsets).view(-1)
+            if int(seo.numel()) != num_segments + 1:
+                raise ValueError(f"segment_edge_offsets size mismatch: got {int(seo.numel())}, "
+                                 f"expected {num_segments + 1}")
+            N.call("cs_accumulate_edge_grads_csr", N.ptr(v_edges), N.ptr(_f32(edge_t_starts)),
+                   N.ptr(_f32(edge_t_ends)), N.ptr(seo), num_segments, H, W, N.ptr(v_px),
+                   N.ptr(v_norm), N.stream(dev))
+        if v_px is not v_cubics_px:
+            v_cubics_px.copy_(v_px)
+        return v_cubics_px, v_colors, v_opacities, v_inv_sigma2s
     if method == "bernstein":
         eps = max(2, int(distance_samples)) - 1
         if E != num_segments * eps:

@@ -178,6 +178,9 @@ class Binned:
         self.block_x, self.block_y = int(block_x), int(block_y)
         self.nsub = sub_blocks(img_h, img_w)
         self.waves_per_tile = 2 * (self.block_x // BLOCK_X) * (self.block_y // BLOCK_Y)
+        # Tiles whose sides are not multiples of 16 take the any-size kernels
+        # (a lane per pixel, no raster log, no tile order).
+        self.any_tile = not is_sub_block_tile(self.block_x, self.block_y)
         self.adaptive = adaptive
         self.nseg, self.nprim = nseg, nprim
         self.num_intersects = -1
@@ -570,6 +573,8 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
     H, W = b.img_h, b.img_w
     planes = torch.empty((3, H, W), dtype=torch.float32, device=dev)
     out = planes.permute(1, 2, 0)
+    if b.any_tile:
+        return _rasterize_forward_any(b, background, planes, out, eval_counts)
     nsub, wpt = b.nsub, b.waves_per_tile
     cap = max(int(b.primitive_ids_sorted.numel()), 1)
     # final_Ts, final_idx and the log's entry index share one allocation.
@@ -648,6 +653,55 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
     return out, final_T, final_idx
 
 
+def _rasterize_forward_any(b: Binned, background, planes, out, eval_counts):
+    """rasterize_forward for tiles whose sides are not multiples of 16: the
+    any-size kernel (a lane per pixel, every edge evaluated), no raster log."""
+    if eval_counts is not None:
+        raise ValueError("evaluation counts are measured on 16x16 sub-block tiles only")
+    dev = b.device
+    H, W = b.img_h, b.img_w
+    aux = torch.empty((2 * H * W,), dtype=torch.int32, device=dev)
+    final_T = aux[:H * W].view(torch.float32).view(H, W)
+    final_idx = aux[H * W:].view(H, W)
+    b.log_index = b.log_pool = None
+    b.log_ctr = None
+    b.tile_order = None
+    with N.prof("cubic.fwd.rast"):
+        N.call("cs_rasterize_forward_any_tile", b.mode, N.ptr(b.primitive_ids_sorted),
+               b.ptr("tile_bins"), b.ptr("edges"), b.ptr("prim_recs"), N.ptr(background), H, W,
+               b.block_x, b.block_y, planes.data_ptr(), 1, final_T.data_ptr(),
+               final_idx.data_ptr(), N.stream(dev))
+    return out, final_T, final_idx
+
+
+def _rasterize_backward_any(b: Binned, background, final_T, final_idx, v_output, planar, v_px,
+                            v_colors, v_opac, v_is2, v_sw, curve_contrib_rgb,
+                            curve_isect_contrib):
+    """rasterize_backward for tiles whose sides are not multiples of 16: the
+    any-size kernel adds endpoint gradients per edge, which are then folded
+    into the control points (cubic_splatting.py:2308-2396, :2399-2487)."""
+    dev = b.device
+    E = int(b.edges.shape[0])
+    v_edges = torch.zeros((E, 4), dtype=torch.float32, device=dev)
+    with N.prof("cubic.bwd.rast"):
+        N.call("cs_rasterize_backward_any_tile", b.mode, N.ptr(b.primitive_ids_sorted),
+               b.ptr("tile_bins"), b.ptr("edges"), b.ptr("prim_recs"), N.ptr(background),
+               b.img_h, b.img_w, b.block_x, b.block_y, N.ptr(final_T), N.ptr(final_idx),
+               N.ptr(v_output), planar, v_edges.data_ptr(), N.ptr(v_colors), N.ptr(v_opac),
+               N.ptr(v_is2), N.ptr(v_sw), N.ptr(curve_contrib_rgb), N.ptr(curve_isect_contrib),
+               N.stream(dev))
+    v_norm = torch.empty_like(v_px)
+    if b.adaptive:
+        aux = b.edge_aux.view(torch.float32)
+        t0, t1 = aux[:, 1].contiguous(), aux[:, 2].contiguous()
+        N.call("cs_accumulate_edge_grads_csr", v_edges.data_ptr(), N.ptr(t0), N.ptr(t1),
+               b.ptr("seg_edge_offsets"), b.nseg, b.img_h, b.img_w, N.ptr(v_px), N.ptr(v_norm),
+               N.stream(dev))
+    else:
+        N.call("cs_accumulate_edge_grads", v_edges.data_ptr(), b.nseg, b.edges_per_segment,
+               b.img_h, b.img_w, N.ptr(v_px), N.ptr(v_norm), N.stream(dev))
+
+
 def log_pool_counter(b: Binned) -> int:
     """The end of the shared blocks b's forward reserved in its log pool, in
     16-byte units (a host read; tests)."""
@@ -687,6 +741,13 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     v_is2 = rest[4 * P: 5 * P]
     v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
     v_output, planar = image_grad_layout(v_output)
+    if b.any_tile:
+        if eval_counts is not None:
+            raise ValueError("evaluation counts are measured on 16x16 sub-block tiles only")
+        _rasterize_backward_any(b, background, final_T, final_idx, v_output, planar, v_px,
+                                v_colors, v_opac, v_is2, v_sw, curve_contrib_rgb,
+                                curve_isect_contrib)
+        return v_px, v_colors, v_opac, v_is2, v_sw
     nv = 6 if b.mode == MODE_STROKE else 5
     prim_scratch = N.ptr(rest[nv * P:])
     log_index, log_pool = N.ptr(b.log_index), N.ptr(b.log_pool)
@@ -769,21 +830,33 @@ def _remember_capacity(key, num_intersects: int) -> None:
     _CAPACITY_HINTS[key] = intersection_capacity(max(0, num_intersects))
 
 
-# Largest tile: 16 sub-blocks of 16 x 16 pixels.
+# Largest tile of the 16 x 16 sub-block kernels: 16 sub-blocks.
 MAX_SUB_BLOCKS_PER_TILE = 16
+# Largest tile of the any-size kernels (a lane per pixel): the reference's
+# one-thread-per-pixel launch, threads=(block_x, block_y), allows 1024.
+MAX_ANY_TILE_PIXELS = 1024
+
+
+def is_sub_block_tile(block_x: int, block_y: int) -> bool:
+    """Tiles the 16 x 16 sub-block raster takes: positive multiples of 16 in
+    both directions, at most 16 sub-blocks."""
+    bx, by = int(block_x), int(block_y)
+    return (bx > 0 and by > 0 and bx % BLOCK_X == 0 and by % BLOCK_Y == 0
+            and (bx // BLOCK_X) * (by // BLOCK_Y) <= MAX_SUB_BLOCKS_PER_TILE)
 
 
 def check_block(block_x: int, block_y: int) -> None:
-    """Tiles the MI355X raster takes: positive multiples of 16 in both
-    directions (it rasterizes 16 x 16 sub-blocks, every one inside one tile),
-    at most 16 sub-blocks per tile."""
+    """Tiles the MI355X raster takes: multiples of 16 (up to 16 sub-blocks of
+    16 x 16, the fast kernels), or any other positive size of at most 1024
+    pixels (the any-size kernels, a lane per pixel as in the reference)."""
     bx, by = int(block_x), int(block_y)
-    if (bx <= 0 or by <= 0 or bx % BLOCK_X or by % BLOCK_Y
-            or (bx // BLOCK_X) * (by // BLOCK_Y) > MAX_SUB_BLOCKS_PER_TILE):
+    if is_sub_block_tile(bx, by):
+        return
+    if bx <= 0 or by <= 0 or bx * by > MAX_ANY_TILE_PIXELS:
         raise NotImplementedError(
-            f"the MI355X raster takes tiles whose sides are multiples of {BLOCK_X} pixels, at "
-            f"most {MAX_SUB_BLOCKS_PER_TILE} sub-blocks of {BLOCK_X}x{BLOCK_Y}; got "
-            f"{block_x}x{block_y}")
+            f"the MI355X raster takes tiles whose sides are multiples of {BLOCK_X} pixels (at "
+            f"most {MAX_SUB_BLOCKS_PER_TILE} sub-blocks of {BLOCK_X}x{BLOCK_Y}) or tiles of at "
+            f"most {MAX_ANY_TILE_PIXELS} pixels; got {block_x}x{block_y}")
 
 
 _check_block = check_block

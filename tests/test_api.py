@@ -247,7 +247,7 @@ def test_flatten_method_and_tile_size_scope():
         splat.normalize_cubic_flatten_method("nope")
     cub, offs, col, op, dep = _scene_args()
     with pytest.raises(NotImplementedError):
-        manbo.ops.render_cubic_fill_splat_tilelang(cub, offs, col, op, dep, 32, 32, 8, 8,
+        manbo.ops.render_cubic_fill_splat_tilelang(cub, offs, col, op, dep, 32, 32, 40, 40,
                                                    torch.ones(3))
 
 
@@ -374,10 +374,18 @@ def test_visual_debug_shim_calls_the_hook():
 
 def test_tile_sizes_accepted_and_refused():
     """The raster takes tiles whose sides are multiples of 16 (16 x 16
-    sub-blocks), at most 16 sub-blocks; others are refused before any work."""
-    from repo_amd.splat import check_block
+    sub-blocks, at most 16 of them: the fast kernels) and any other tile of at
+    most 1024 pixels (the reference's one-thread-per-pixel launch: the
+    any-size kernels); others are refused before any work."""
+    from repo_amd.splat import check_block, is_sub_block_tile
     for bx, by in ((16, 16), (32, 32), (16, 48), (64, 64), (256, 16)):
         check_block(bx, by)
-    for bx, by in ((8, 8), (16, 8), (24, 16), (80, 64), (0, 16), (272, 16)):
+        assert is_sub_block_tile(bx, by)
+    for bx, by in ((8, 8), (16, 8), (8, 16), (24, 16), (12, 12), (1, 1), (32, 32),
+                   (1024, 1), (33, 31)):
+        check_block(bx, by)
+    for bx, by in ((8, 8), (16, 8), (24, 16), (12, 12), (1024, 1)):
+        assert not is_sub_block_tile(bx, by)
+    for bx, by in ((80, 64), (0, 16), (272, 16), (40, 40), (33, 32), (-8, 8), (1025, 1)):
         with pytest.raises(NotImplementedError):
             check_block(bx, by)
