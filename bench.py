@@ -180,11 +180,12 @@ def stage_times(sc, iters):
                                         N.ptr(scratch), stream))
     from repo_amd import fused
     timed("glue_clamp_nchw_ms", lambda: fused.clamp_to_nchw(out))
-    # The step's fused loss on the renderer's image (clamp on load, MSE summed
-    # in the SSIM forward), its forward and its backward kernel.
+    # The step's fused loss on the renderer's image (its planar copy read in
+    # place, clamped on load; MSE summed in the SSIM forward), its forward and
+    # its backward kernel.
+    out.requires_grad_(True)
     loss, _ = timed("loss_fused_fwd_ms",
-                    lambda: fused.clamp_mse_ssim_loss(out.detach().requires_grad_(True), tgt,
-                                                      SSIM_WEIGHT))
+                    lambda: fused.clamp_mse_ssim_loss(out, tgt, SSIM_WEIGHT))
     fn = loss.grad_fn
     planes = torch.empty((3, h, w), dtype=torch.float32, device=x.device)
     timed("loss_fused_bwd_ms", lambda: N.call(

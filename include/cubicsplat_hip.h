@@ -234,7 +234,7 @@ int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chun
  * (ops/cubic_splatting.py:918-1194, wrapper :2181-2305; mode 1:
  * ops/cubic_polyline_splatting.py:33-249); edges [E] edge records, prim_recs
  * [P] primitive records as for cs_rasterize_forward; out_img [H,W,3] or, with
- * out_planar, three [H,W] planes.
+ * out_planar, three [H,W] planes; out_planes as for cs_rasterize_forward.
  * cs_rasterize_backward_any_tile replaces rasterize_cubic_fill_backward_kernel
  * (ops/cubic_splatting.py:1197-1651, wrapper :2572-2747; mode 1:
  * ops/cubic_polyline_splatting.py:252-660): adds into v_edges [E,2,2]
@@ -246,8 +246,8 @@ int cs_rasterize_forward_any_tile(int32_t mode, const int32_t* prim_ids_sorted,
                                   const int32_t* tile_bins, const void* edges,
                                   const void* prim_recs, const float* background, int32_t img_h,
                                   int32_t img_w, int32_t block_x, int32_t block_y,
-                                  float* out_img, int32_t out_planar, float* final_Ts,
-                                  int32_t* final_idx, hipStream_t stream);
+                                  float* out_img, int32_t out_planar, float* out_planes,
+                                  float* final_Ts, int32_t* final_idx, hipStream_t stream);
 int cs_rasterize_backward_any_tile(int32_t mode, const int32_t* prim_ids_sorted,
                                    const int32_t* tile_bins, const void* edges,
                                    const void* prim_recs, const float* background, int32_t img_h,
@@ -325,10 +325,12 @@ int cs_edge_aux_from_csr(const int32_t* segment_edge_offsets, int32_t nseg,
  * (ops/cubic_polyline_splatting.py:33-249) when mode 1.  Tiles as above.
  * The primitive records hold each primitive's edge range, so
  * edges_per_segment is not used (>= 0; 0 for adaptive records).  out_img is
- * written as [H, W, 3], or, when out_planar != 0, as three [H, W] planes
- * (channel c at out_img + c H W; the layout cs_clamp_mse_ssim_loss reads
- * with img_planar, and the clamp(0, 1).permute(2, 0, 1) glue of
- * gaussian_trace/render.py:1309-1310 then needs no copy).  log_counter: NULL,
+ * written as [H, W, 3] (the reference's layout), or, when out_planar != 0, as
+ * three [H, W] planes (channel c at out_img + c H W).  out_planes, when not
+ * NULL, receives the image once more as three [H, W] planes (the layout
+ * cs_clamp_mse_ssim_loss reads with img_planar, clamping on load, so the
+ * clamp(0, 1).permute(2, 0, 1) glue of gaussian_trace/render.py:1309-1310
+ * needs no pass of its own).  log_counter: NULL,
  * or a device word that is zero on entry, which then counts the raster log's
  * shared blocks (the call takes no launch of its own to set up the counter in
  * the pool's first unit; the word is left at the count used). */
@@ -337,10 +339,11 @@ int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted, const int
                          const float* background, int32_t img_h, int32_t img_w,
                          int32_t block_x, int32_t block_y,
                          int32_t edges_per_segment, float* out_img, int32_t out_planar,
-                         float* final_Ts, int32_t* final_idx, int64_t num_entries,
-                         int32_t* log_index, void* log_pool, int64_t log_pool_bytes,
-                         int32_t log_entry_units, uint32_t* log_counter,
-                         const int32_t* tile_order, uint32_t* wave_cost, hipStream_t stream);
+                         float* out_planes, float* final_Ts, int32_t* final_idx,
+                         int64_t num_entries, int32_t* log_index, void* log_pool,
+                         int64_t log_pool_bytes, int32_t log_entry_units,
+                         uint32_t* log_counter, const int32_t* tile_order, uint32_t* wave_cost,
+                         hipStream_t stream);
 
 /* rasterize_cubic_fill_backward_kernel (ops/cubic_splatting.py:1197-1651) /
  * rasterize_cubic_polyline_backward_kernel (ops/cubic_polyline_splatting.py:252-660)
@@ -412,8 +415,9 @@ int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_ids_sorted,
                                  const float* background, int32_t img_h, int32_t img_w,
                                  int32_t block_x, int32_t block_y,
                                  int32_t edges_per_segment, float* out_img,
-                                 int32_t out_planar, float* final_Ts, int32_t* final_idx,
-                                 int64_t num_entries, int32_t* log_index, void* log_pool,
+                                 int32_t out_planar, float* out_planes, float* final_Ts,
+                                 int32_t* final_idx, int64_t num_entries, int32_t* log_index,
+                                 void* log_pool,
                                  int64_t log_pool_bytes, int32_t log_entry_units,
                                  uint32_t* log_counter, unsigned long long* eval_counts,
                                  const int32_t* tile_order,

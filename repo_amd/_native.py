@@ -50,22 +50,22 @@ _SIGNATURES = {
     "cs_bin_finish": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _I32, _I32, _I32, _I32, _P, _P,
                                      _P, _P, _P, _I64, _P]),
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
-                                            _I32, _P, _I32, _P, _P, _I64, _P, _P, _I64, _I32, _P,
-                                            _P, _P, _P]),
+                                            _I32, _P, _I32, _P, _P, _P, _I64, _P, _P, _I64, _I32,
+                                            _P, _P, _P, _P]),
     "cs_rasterize_backward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                              _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P,
                                              _P, _P, _I32, _P, _P, _P]),
     "cs_raster_prim_scratch_elems": (_SZ, [_I32, _I32]),
     "cs_rasterize_forward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
-                                                    _I32, _I32, _P, _I32, _P, _P, _I64, _P, _P,
-                                                    _I64, _I32, _P, _P, _P, _P, _P]),
+                                                    _I32, _I32, _P, _I32, _P, _P, _P, _I64, _P,
+                                                    _P, _I64, _I32, _P, _P, _P, _P, _P]),
     "cs_rasterize_backward_counted": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
                                                      _I32, _I32, _I32, _P, _P, _P, _P, _P, _I32,
                                                      _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P,
                                                      _P]),
     "cs_raster_tile_order": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
     "cs_rasterize_forward_any_tile": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _I32, _I32, _I32,
-                                                     _I32, _P, _I32, _P, _P, _P]),
+                                                     _I32, _P, _I32, _P, _P, _P, _P]),
     "cs_rasterize_backward_any_tile": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                                       _I32, _P, _P, _P, _I32, _P, _P, _P, _P,
                                                       _P, _P, _P, _P]),

@@ -632,7 +632,8 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
     TileGrid tg, const int32_t* __restrict__ tile_order,
     uint32_t* __restrict__ wave_cost, float* __restrict__ out, int out_planar,
-    float* __restrict__ final_T, int32_t* __restrict__ final_idx,
+    float* __restrict__ out_planes, float* __restrict__ final_T,
+    int32_t* __restrict__ final_idx,
     int32_t* __restrict__ log_index, uint4* __restrict__ log_pool, uint32_t* __restrict__ log_ctr,
     uint32_t log_first, uint32_t log_units,
     uint32_t log_per_entry, unsigned long long* __restrict__ counts) {
@@ -833,18 +834,28 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             __builtin_nontemporal_store(idx_l, log_index + (size_t)tg.waves * gl + sb.slot);
     }
     if (log_index) log_flush(log_pool, stage, st);
-    // The image as [H, W, 3], or as three [H, W] planes (out_planar).
-    const size_t ch = out_planar ? (size_t)img_h * img_w : 1;
+    // The image as [H, W, 3], or as three [H, W] planes (out_planar), and
+    // optionally also as three planes at out_planes.
+    const size_t np = (size_t)img_h * img_w;
+    const size_t ch = out_planar ? np : 1;
 #pragma unroll
     for (int p = 0; p < kPix; ++p) {
         if (!L.in_img[p]) continue;
         const size_t pix = (size_t)L.i[p] * img_w + L.j;
         __builtin_nontemporal_store(T[p], final_T + pix);
         __builtin_nontemporal_store(cur[p], final_idx + pix);
+        const float o0 = __builtin_fmaf(T[p], bg[0], C0[p]);
+        const float o1 = __builtin_fmaf(T[p], bg[1], C1[p]);
+        const float o2 = __builtin_fmaf(T[p], bg[2], C2[p]);
         float* const o = out + (out_planar ? pix : 3 * pix);
-        o[0] = __builtin_fmaf(T[p], bg[0], C0[p]);
-        o[ch] = __builtin_fmaf(T[p], bg[1], C1[p]);
-        o[2 * ch] = __builtin_fmaf(T[p], bg[2], C2[p]);
+        o[0] = o0;
+        o[ch] = o1;
+        o[2 * ch] = o2;
+        if (out_planes) {
+            out_planes[pix] = o0;
+            out_planes[np + pix] = o1;
+            out_planes[2 * np + pix] = o2;
+        }
     }
     if constexpr (COUNT) flush_counts(n, counts);
     record_wave_cost(wave_cost, sb.index, t_start);
@@ -1609,8 +1620,8 @@ __global__ __launch_bounds__(kAnyMaxThreads) void k_raster_fwd_any(
     const int32_t* __restrict__ ids, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const PrimRec* __restrict__ prims_g,
     const float* __restrict__ bg, int img_h, int img_w, int bx, int by, int tbx,
-    float* __restrict__ out, int out_planar, float* __restrict__ final_T,
-    int32_t* __restrict__ final_idx) {
+    float* __restrict__ out, int out_planar, float* __restrict__ out_planes,
+    float* __restrict__ final_T, int32_t* __restrict__ final_idx) {
     const int tile = blockIdx.x;
     const AnyPixel q = any_pixel(tile, bx, by, tbx, img_h, img_w);
     const cptr<PrimRec> prims = as_const(prims_g);
@@ -1631,11 +1642,20 @@ __global__ __launch_bounds__(kAnyMaxThreads) void k_raster_fwd_any(
     const size_t pix = (size_t)q.i * img_w + q.j;
     final_T[pix] = T;
     final_idx[pix] = cur;
-    const size_t ch = out_planar ? (size_t)img_h * img_w : 1;
+    const size_t np = (size_t)img_h * img_w;
+    const size_t ch = out_planar ? np : 1;
+    const float o0 = __builtin_fmaf(T, bg[0], C0);
+    const float o1 = __builtin_fmaf(T, bg[1], C1);
+    const float o2 = __builtin_fmaf(T, bg[2], C2);
     float* const o = out + (out_planar ? pix : 3 * pix);
-    o[0] = __builtin_fmaf(T, bg[0], C0);
-    o[ch] = __builtin_fmaf(T, bg[1], C1);
-    o[2 * ch] = __builtin_fmaf(T, bg[2], C2);
+    o[0] = o0;
+    o[ch] = o1;
+    o[2 * ch] = o2;
+    if (out_planes) {
+        out_planes[pix] = o0;
+        out_planes[np + pix] = o1;
+        out_planes[2 * np + pix] = o2;
+    }
 }
 
 __device__ __forceinline__ float any_wave_sum(float v) {
@@ -1797,6 +1817,7 @@ struct RasterArgs {
     // forward outputs
     float* out;
     int out_planar;      // out as three [H, W] planes instead of [H, W, 3]
+    float* out_planes;   // also the image as three [H, W] planes (or null)
     float* final_T;
     int32_t* final_idx;
     int32_t* log_index;     // raster log: written by the forward, read by the backward
@@ -1826,7 +1847,8 @@ template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
     hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.tg.nsb), dim3(kRasterThreads), 0,
                        a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tg,
-                       a.order, a.wave_cost, a.out, a.out_planar, a.final_T, a.final_idx,
+                       a.order, a.wave_cost, a.out, a.out_planar, a.out_planes, a.final_T,
+                       a.final_idx,
                        a.log_index,
                        a.log_pool, a.log_ctr, a.log_first, a.log_units, a.log_per_entry,
                        a.counts);
@@ -1913,7 +1935,8 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                              const void* prim_recs, const float* background, int32_t img_h,
                              int32_t img_w, int32_t block_x, int32_t block_y,
                              int32_t edges_per_segment, float* out_img, int32_t out_planar,
-                             float* final_Ts, int32_t* final_idx, int64_t num_entries,
+                             float* out_planes, float* final_Ts, int32_t* final_idx,
+                             int64_t num_entries,
                              int32_t* log_index, void* log_pool, int64_t log_pool_bytes,
                              int32_t log_entry_units, uint32_t* log_counter,
                              unsigned long long* eval_counts, const int32_t* tile_order,
@@ -1936,6 +1959,7 @@ static int rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted,
                                background, img_h, img_w, tg, edges_per_segment, stream);
     a.out = out_img;
     a.out_planar = out_planar ? 1 : 0;
+    a.out_planes = out_planes;
     a.final_T = final_Ts;
     a.final_idx = final_idx;
     a.log_index = log_index;
@@ -1966,15 +1990,16 @@ extern "C" int cs_rasterize_forward(int32_t mode, const int32_t* prim_ids_sorted
                                     const void* edge_culls, const void* prim_recs,
                                     const float* background, int32_t img_h, int32_t img_w,
                                     int32_t block_x, int32_t block_y, int32_t edges_per_segment,
-                                    float* out_img, int32_t out_planar, float* final_Ts,
-                                    int32_t* final_idx, int64_t num_entries, int32_t* log_index,
+                                    float* out_img, int32_t out_planar, float* out_planes,
+                                    float* final_Ts, int32_t* final_idx, int64_t num_entries,
+                                    int32_t* log_index,
                                     void* log_pool, int64_t log_pool_bytes,
                                     int32_t log_entry_units, uint32_t* log_counter,
                                     const int32_t* tile_order, uint32_t* wave_cost,
                                     hipStream_t stream) {
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, block_x, block_y, edges_per_segment,
-                             out_img, out_planar, final_Ts,
+                             out_img, out_planar, out_planes, final_Ts,
                              final_idx, num_entries, log_index, log_pool, log_pool_bytes,
                              log_entry_units, log_counter, nullptr, tile_order, wave_cost,
                              stream);
@@ -1986,8 +2011,9 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
                                             const float* background, int32_t img_h,
                                             int32_t img_w, int32_t block_x, int32_t block_y,
                                             int32_t edges_per_segment, float* out_img,
-                                            int32_t out_planar, float* final_Ts,
-                                            int32_t* final_idx, int64_t num_entries,
+                                            int32_t out_planar, float* out_planes,
+                                            float* final_Ts, int32_t* final_idx,
+                                            int64_t num_entries,
                                             int32_t* log_index, void* log_pool,
                                             int64_t log_pool_bytes, int32_t log_entry_units,
                                             uint32_t* log_counter,
@@ -1997,7 +2023,7 @@ extern "C" int cs_rasterize_forward_counted(int32_t mode, const int32_t* prim_id
     if (!eval_counts) return CS_ERR_ARGS;
     return rasterize_forward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
                              background, img_h, img_w, block_x, block_y, edges_per_segment,
-                             out_img, out_planar, final_Ts,
+                             out_img, out_planar, out_planes, final_Ts,
                              final_idx, num_entries, log_index, log_pool, log_pool_bytes,
                              log_entry_units, log_counter, eval_counts, tile_order, wave_cost,
                              stream);
@@ -2188,8 +2214,9 @@ extern "C" int cs_rasterize_forward_any_tile(int32_t mode, const int32_t* prim_i
                                              const void* prim_recs, const float* background,
                                              int32_t img_h, int32_t img_w, int32_t block_x,
                                              int32_t block_y, float* out_img,
-                                             int32_t out_planar, float* final_Ts,
-                                             int32_t* final_idx, hipStream_t stream) {
+                                             int32_t out_planar, float* out_planes,
+                                             float* final_Ts, int32_t* final_idx,
+                                             hipStream_t stream) {
     int ntiles, tbx, threads;
     if ((mode != 0 && mode != 1) || !any_tile_grid(img_h, img_w, block_x, block_y, ntiles, tbx,
                                                     threads))
@@ -2202,11 +2229,13 @@ extern "C" int cs_rasterize_forward_any_tile(int32_t mode, const int32_t* prim_i
     if (mode == 0)
         hipLaunchKernelGGL(k_raster_fwd_any<0>, dim3(ntiles), dim3(threads), 0, stream,
                            prim_ids_sorted, tile_bins, E, P, background, img_h, img_w, block_x,
-                           block_y, tbx, out_img, out_planar ? 1 : 0, final_Ts, final_idx);
+                           block_y, tbx, out_img, out_planar ? 1 : 0, out_planes, final_Ts,
+                           final_idx);
     else
         hipLaunchKernelGGL(k_raster_fwd_any<1>, dim3(ntiles), dim3(threads), 0, stream,
                            prim_ids_sorted, tile_bins, E, P, background, img_h, img_w, block_x,
-                           block_y, tbx, out_img, out_planar ? 1 : 0, final_Ts, final_idx);
+                           block_y, tbx, out_img, out_planar ? 1 : 0, out_planes, final_Ts,
+                           final_idx);
     return raster_status();
 }
 

@@ -108,11 +108,16 @@ class _MseSsimLoss(torch.autograd.Function):
 
 
 def _planes_of(img: torch.Tensor):
-    """The three [H, W] planes behind an [H, W, 3] float32 view of them (the
-    renderer's image layout: strides (W, 1, H W)), or None for any other
-    layout."""
+    """Three [H, W] planes holding the values of the [H, W, 3] float32 image:
+    the planar copy the renderer wrote beside its image (while the image is
+    unmodified), or the planes behind an [H, W, 3] view of them (strides
+    (W, 1, H W)); None for any other tensor."""
     if img.dtype is not torch.float32 or img.dim() != 3 or img.shape[2] != 3:
         return None
+    from .splat import planar_copy_of
+    pc = planar_copy_of(img)
+    if pc is not None:
+        return pc
     h, w = int(img.shape[0]), int(img.shape[1])
     if img.is_contiguous() or img.stride() != (w, 1, h * w):
         return None

@@ -174,11 +174,11 @@ def rasterize_cubic_fill_forward_tilelang(tile_bounds, block, img_size, primitiv
                                          block_y=by)
     if not is_sub_block_tile(bx, by):
         N.call("cs_rasterize_forward_any_tile", 0, N.ptr(ids), N.ptr(bins), N.ptr(edges),
-               N.ptr(prims), N.ptr(bg), H, W, bx, by, N.ptr(out_img), 0, N.ptr(final_Ts),
+               N.ptr(prims), N.ptr(bg), H, W, bx, by, N.ptr(out_img), 0, None, N.ptr(final_Ts),
                N.ptr(final_idx), N.stream(dev))
         return out_img, final_Ts, final_idx
     N.call("cs_rasterize_forward", 0, N.ptr(ids), N.ptr(bins), N.ptr(edges),
-           N.ptr(culls), N.ptr(prims), N.ptr(bg), H, W, bx, by, 0, N.ptr(out_img), 0,
+           N.ptr(culls), N.ptr(prims), N.ptr(bg), H, W, bx, by, 0, N.ptr(out_img), 0, None,
            N.ptr(final_Ts),
            N.ptr(final_idx), num_intersects, None, None, 0, 0, None, None, None, N.stream(dev))
     return out_img, final_Ts, final_idx

@@ -86,6 +86,21 @@ def image_grad_layout(v: torch.Tensor):
     return v.to(torch.float32).contiguous(), 0
 
 
+def attach_planar_copy(img: torch.Tensor, planes: torch.Tensor) -> None:
+    """Attach to the renderer's [H, W, 3] image the [3, H, W] planes its launch
+    also wrote, with the image's version counter at that time."""
+    img._cs_planar_copy = (planes, img._version)
+
+
+def planar_copy_of(img: torch.Tensor):
+    """The [3, H, W] planes the renderer wrote beside its [H, W, 3] image, or
+    None (another tensor, or the image was modified in place since)."""
+    pc = getattr(img, "_cs_planar_copy", None)
+    if pc is None or img._version != pc[1]:
+        return None
+    return pc[0]
+
+
 def _i32(t: torch.Tensor) -> torch.Tensor:
     if t.dtype is torch.int32 and t.is_contiguous():
         return t.detach()
@@ -554,11 +569,12 @@ def _read_log_use_later(key, dev_index: int, src: int, zero: int, units: int,
 
 def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log: bool = True,
                       log_pool_bytes_override: Optional[int] = None):
-    """(image [H,W,3], final_Ts, final_idx).  The image is an [H, W, 3] view of
-    three [H, W] planes (strides (W, 1, H W)): the caller's
-    clamp(0, 1).permute(2, 0, 1) (gaussian_trace/render.py:1309-1310) then
-    gives a contiguous [3, H, W] tensor without a copy, and the fused loss
-    reads the planes in place.  With eval_counts (int64 [5],
+    """(image [H,W,3], final_Ts, final_idx).  The image is a contiguous
+    [H, W, 3] tensor, as the reference returns it
+    (cubic_splatting.py:2207-2209); the same launch also writes it as three
+    [H, W] planes, attached to it (planar_copy_of), which the fused loss reads
+    in place (clamping on load) while the image is unmodified.  With
+    eval_counts (int64 [5],
     zeroed, on the device) the counting instantiation runs and adds the
     evaluation counts of cs_rasterize_forward_counted into it.  With log (the
     default) it writes the raster log its backward reads (b.log_index,
@@ -571,8 +587,9 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
     (b.tile_order) and the following forwards take."""
     dev = b.device
     H, W = b.img_h, b.img_w
+    out = torch.empty((H, W, 3), dtype=torch.float32, device=dev)
     planes = torch.empty((3, H, W), dtype=torch.float32, device=dev)
-    out = planes.permute(1, 2, 0)
+    attach_planar_copy(out, planes)
     if b.any_tile:
         return _rasterize_forward_any(b, background, planes, out, eval_counts)
     nsub, wpt = b.nsub, b.waves_per_tile
@@ -617,7 +634,8 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
     base = aux.data_ptr()
     args = (b.mode, N.ptr(b.primitive_ids_sorted), b.ptr("tile_bins"), b.ptr("edges"),
             b.ptr("edge_culls"), b.ptr("prim_recs"), N.ptr(background), H, W, b.block_x,
-            b.block_y, b.edges_per_segment, planes.data_ptr(), 1, base, base + 4 * H * W,
+            b.block_y, b.edges_per_segment, out.data_ptr(), 0, planes.data_ptr(), base,
+            base + 4 * H * W,
             *log_args)
     cost = b.ptr("wave_cost") if remake else None
     prev_p = None if prev is None else prev.data_ptr()
@@ -669,7 +687,7 @@ def _rasterize_forward_any(b: Binned, background, planes, out, eval_counts):
     with N.prof("cubic.fwd.rast"):
         N.call("cs_rasterize_forward_any_tile", b.mode, N.ptr(b.primitive_ids_sorted),
                b.ptr("tile_bins"), b.ptr("edges"), b.ptr("prim_recs"), N.ptr(background), H, W,
-               b.block_x, b.block_y, planes.data_ptr(), 1, final_T.data_ptr(),
+               b.block_x, b.block_y, out.data_ptr(), 0, planes.data_ptr(), final_T.data_ptr(),
                final_idx.data_ptr(), N.stream(dev))
     return out, final_T, final_idx
 

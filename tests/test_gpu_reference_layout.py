@@ -157,10 +157,15 @@ def test_reference_layout_raster_rejects_inconsistent_inputs():
     tb["tile_bins"] = bins
     with pytest.raises(ValueError, match="tile_bins"):
         manbo.ops.rasterize_cubic_fill_forward_tilelang(*_positional(tb), **kw)
-    with pytest.raises(NotImplementedError):
-        t8 = dict(t)
-        t8["block"] = (8, 8, 1)
+    # 8x8 tiles are taken, but these tile_bins hold 16x16 tiles' lists
+    t8 = dict(t)
+    t8["block"] = (8, 8, 1)
+    with pytest.raises(ValueError, match="tile_bins"):
         manbo.ops.rasterize_cubic_fill_forward_tilelang(*_positional(t8), **kw)
+    with pytest.raises(NotImplementedError):
+        t40 = dict(t)
+        t40["block"] = (40, 40, 1)
+        manbo.ops.rasterize_cubic_fill_forward_tilelang(*_positional(t40), **kw)
 
 
 @pytest.mark.gpu
