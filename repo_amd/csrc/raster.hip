@@ -466,16 +466,17 @@ __device__ __forceinline__ int far_winding(int4 q, int c, int e1, const WaveRect
 // Then no pixel needs the exact coverage, and every pixel has the same
 // winding number: the winding number changes only across an edge, none
 // crosses the wave's rectangle, and for such edges the fp32 crossing test at
-// each pixel gives the geometric side (see kCullFarCrossExact).  `q0` and
-// `first` hold the cull words and masks of the first 64 edges: the entry is
-// far when no edge has a distance or exact crossing term.  For a fill,
-// `winding` receives the winding number of the wave's pixels (far_winding).
+// each pixel gives the geometric side (see kCullFarCrossExact).  `first`
+// holds the masks of the first 64 edges and `w0` their far_winding (computed
+// by the caller when first has no distance or exact crossing term): the
+// entry is far when no edge has a distance or exact crossing term.  For a
+// fill, `winding` receives the winding number of the wave's pixels.
 template <int MODE>
 __device__ __forceinline__ bool entry_far(const PrimRec& pr, const WaveRect& W,
-                                          const EdgeCull* __restrict__ culls, int4 q0,
-                                          const ChunkMasks& first, int& winding) {
+                                          const EdgeCull* __restrict__ culls,
+                                          const ChunkMasks& first, int w0, int& winding) {
     if (first.dist | first.cross) return false;
-    int w = MODE == 0 ? far_winding(q0, pr.e0, pr.e1, W) : 0;
+    int w = MODE == 0 ? w0 : 0;
     for (int c = pr.e0 + kWave; c < pr.e1; c += kWave) {
         const int4 q = load_culls(culls, c, pr.e1);
         const ChunkMasks m = chunk_masks<MODE == 0>(q, c, pr.e1, W);
@@ -698,7 +699,11 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             const int g = gc + k;
             const int pid = __builtin_amdgcn_readlane(pid_l, k);
             const PrimRec pr = load_prim_fwd(prims, pid);
-            const int4 q = q_next;
+            // Everything this entry needs from its first cull words is taken
+            // before the next entry's load reuses their registers.
+            const ChunkMasks cm0 = chunk_masks<MODE == 0>(q_next, pr.e0, pr.e1, W);
+            const int w0 = (MODE == 0 && (cm0.dist | cm0.cross) == 0)
+                               ? far_winding(q_next, pr.e0, pr.e1, W) : 0;
             if (todo) {
                 const int pid2 = __builtin_amdgcn_readlane(pid_l, (int)__builtin_ctzll(todo));
                 q_next = load_culls(culls, prims[pid2].e0, prims[pid2].e1);
@@ -712,9 +717,11 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
                 npix = wave_count(live);
                 n.entries += 1;
             }
-            const ChunkMasks cm0 = chunk_masks<MODE == 0>(q, pr.e0, pr.e1, W);
             int wnd = 0;
-            if (entry_far<MODE>(pr, W, culls, q, cm0, wnd)) {
+            // Coverage of each pixel; one compositing site below for every
+            // path (so the pixels' state stays in the same registers).
+            float cov[kPix];
+            if (entry_far<MODE>(pr, W, culls, cm0, w0, wnd)) {
                 // Uniform entry: outside (nothing to do) or, for a fill whose
                 // winding number says inside, coverage 1 at every pixel.
                 bool inside_all = false;
@@ -726,104 +733,103 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
                     idx_l = lane == k ? (inside_all ? kLogInside : kLogEmpty) : idx_l;
                     logged |= 1ull << k;
                 }
-                if (inside_all) {
-                    const float alpha = fminf(kAlphaCap, pr.opacity * 1.0f);
+                if (!inside_all) continue;
+#pragma unroll
+                for (int p = 0; p < kPix; ++p) cov[p] = 1.0f;
+            } else {
+                Geom G[kPix];
+                prim_geometry<MODE, 1, COUNT, MODE == 0>(pr, W, culls, edges, L.px, L.py, cm0, G,
+                                                         n, npix);
+                bool ex[kPix], ins[kPix];
+#pragma unroll
+                for (int p = 0; p < kPix; ++p) {
+                    ins[p] = inside_of<MODE>(pr, G[p]);
+                    ex[p] = !done[p] && !(G[p].min_d2 > (ins[p] ? D2 : D2o));
+                    cov[p] = ins[p] ? 1.0f : 0.0f;   // closed form; exact pixels below
+                }
+                const uint64_t x0 = __ballot(ex[0]), x1 = __ballot(ex[kPix - 1]);
+                const uint64_t in0 = MODE == 0 ? (uint64_t)__ballot(ins[0]) : 0ull;
+                const uint64_t in1 = MODE == 0 ? (uint64_t)__ballot(ins[kPix - 1]) : 0ull;
+                if ((in0 | in1 | x0 | x1) == 0) {
+                    // No pixel inside or within the exact distance: every
+                    // coverage is 0 and the entry changes nothing.
+                    if (log_index) {
+                        idx_l = lane == k ? kLogEmpty : idx_l;
+                        logged |= 1ull << k;
+                    }
+                    continue;
+                }
+                const int n0 = __builtin_popcountll(x0), nx = n0 + __builtin_popcountll(x1);
+                const int rk0 = lane_rank(x0), rk1 = lane_rank(x1);
+                if constexpr (COUNT) n.cover += (uint64_t)nx;
+                // Exact coverage.  gathered: lane j < nx holds exact pixel j (row 0's
+                // in lane order, then row 1's) and its best edge.
+                const bool gathered = n0 > 0 && nx > n0 && nx <= kWave;
+                float cov_g = 0.0f;
+                int best_g = 0;
+                if (gathered) {
+                    const int d0 = ex[0] ? rk0 : n0 + (lane - rk0);
+                    const int nr1 = lane - rk1;
+                    const int d1 = ex[1] ? n0 + rk1 : (nr1 < n0 ? nr1 : nr1 + (nx - n0));
+                    const uint32_t a = (uint32_t)__builtin_amdgcn_ds_permute(
+                        4 * d0, (int)pack_d2_inside(G[0].min_d2, ins[0]));
+                    const uint32_t b = (uint32_t)__builtin_amdgcn_ds_permute(
+                        4 * d1, (int)pack_d2_inside(G[1].min_d2, ins[1]));
+                    const int ba = __builtin_amdgcn_ds_permute(4 * d0, G[0].best);
+                    const int bb = __builtin_amdgcn_ds_permute(4 * d1, G[1].best);
+                    const uint32_t v = lane < n0 ? a : b;
+                    best_g = lane < n0 ? ba : bb;
+                    if (lane < nx)
+                        cov_g = exact_coverage<MODE>(
+                            pr, __builtin_bit_cast(float, v & 0x7fffffffu), (v >> 31) != 0);
+                    const float c0 = __builtin_bit_cast(
+                        float,
+                        __builtin_amdgcn_ds_bpermute(4 * rk0, __builtin_bit_cast(int, cov_g)));
+                    const float c1 = __builtin_bit_cast(
+                        float,
+                        __builtin_amdgcn_ds_bpermute(4 * (n0 + rk1),
+                                                     __builtin_bit_cast(int, cov_g)));
+                    if (ex[0]) cov[0] = c0;
+                    if (ex[1]) cov[1] = c1;
+                } else {
 #pragma unroll
                     for (int p = 0; p < kPix; ++p)
-                        composite(pr, alpha, g, T[p], C0[p], C1[p], C2[p], cur[p], done[p]);
+                        if (ex[p]) cov[p] = exact_coverage<MODE>(pr, G[p].min_d2, ins[p]);
                 }
-                continue;
-            }
-            Geom G[kPix];
-            prim_geometry<MODE, 1, COUNT, MODE == 0>(pr, W, culls, edges, L.px, L.py, cm0, G, n,
-                                                     npix);
-            bool ex[kPix], ins[kPix];
-            float cov[kPix];
-#pragma unroll
-            for (int p = 0; p < kPix; ++p) {
-                ins[p] = inside_of<MODE>(pr, G[p]);
-                ex[p] = !done[p] && !(G[p].min_d2 > (ins[p] ? D2 : D2o));
-                cov[p] = ins[p] ? 1.0f : 0.0f;   // closed form; exact pixels below
-            }
-            const uint64_t x0 = __ballot(ex[0]), x1 = __ballot(ex[kPix - 1]);
-            const uint64_t in0 = MODE == 0 ? (uint64_t)__ballot(ins[0]) : 0ull;
-            const uint64_t in1 = MODE == 0 ? (uint64_t)__ballot(ins[kPix - 1]) : 0ull;
-            if ((in0 | in1 | x0 | x1) == 0) {
-                // No pixel inside or within the exact distance: every
-                // coverage is 0 and the entry changes nothing.
+                // The log record of this entry and wave: inside and exact bits, and
+                // each exact pixel's best edge and coverage, for the backward.
                 if (log_index) {
-                    idx_l = lane == k ? kLogEmpty : idx_l;
+                    const uint32_t units = kLogHeaderUnits + (uint32_t)((nx + 1) >> 1);
+                    if (st.n + units > kLogStageUnits) log_flush(log_pool, stage, st);
+                    const int32_t at = log_reserve(log_ctr, log_first, log_units, lc, units);
+                    if (at >= 0) {
+                        if ((uint32_t)at != st.base + st.n) {   // another region: flush first
+                            log_flush(log_pool, stage, st);
+                            st.base = (uint32_t)at;
+                        }
+                        uint4* rec = stage + st.n;
+                        st.n += units;
+                        if (lane == 0) {
+                            rec[0] = make_uint4((uint32_t)in0, (uint32_t)(in0 >> 32),
+                                                (uint32_t)in1, (uint32_t)(in1 >> 32));
+                            rec[1] = make_uint4((uint32_t)x0, (uint32_t)(x0 >> 32), (uint32_t)x1,
+                                                (uint32_t)(x1 >> 32));
+                        }
+                        int2* pairs = reinterpret_cast<int2*>(rec + kLogHeaderUnits);
+                        if (gathered) {
+                            if (lane < nx)
+                                pairs[lane] = make_int2(best_g, __builtin_bit_cast(int, cov_g));
+                        } else {
+                            if (ex[0])
+                                pairs[rk0] = make_int2(G[0].best, __builtin_bit_cast(int, cov[0]));
+                            if (ex[1])
+                                pairs[n0 + rk1] =
+                                    make_int2(G[1].best, __builtin_bit_cast(int, cov[1]));
+                        }
+                    }
+                    idx_l = lane == k ? at : idx_l;
                     logged |= 1ull << k;
                 }
-                continue;
-            }
-            const int n0 = __builtin_popcountll(x0), nx = n0 + __builtin_popcountll(x1);
-            const int rk0 = lane_rank(x0), rk1 = lane_rank(x1);
-            if constexpr (COUNT) n.cover += (uint64_t)nx;
-            // Exact coverage.  gathered: lane j < nx holds exact pixel j (row 0's
-            // in lane order, then row 1's) and its best edge.
-            const bool gathered = n0 > 0 && nx > n0 && nx <= kWave;
-            float cov_g = 0.0f;
-            int best_g = 0;
-            if (gathered) {
-                const int d0 = ex[0] ? rk0 : n0 + (lane - rk0);
-                const int nr1 = lane - rk1;
-                const int d1 = ex[1] ? n0 + rk1 : (nr1 < n0 ? nr1 : nr1 + (nx - n0));
-                const uint32_t a = (uint32_t)__builtin_amdgcn_ds_permute(
-                    4 * d0, (int)pack_d2_inside(G[0].min_d2, ins[0]));
-                const uint32_t b = (uint32_t)__builtin_amdgcn_ds_permute(
-                    4 * d1, (int)pack_d2_inside(G[1].min_d2, ins[1]));
-                const int ba = __builtin_amdgcn_ds_permute(4 * d0, G[0].best);
-                const int bb = __builtin_amdgcn_ds_permute(4 * d1, G[1].best);
-                const uint32_t v = lane < n0 ? a : b;
-                best_g = lane < n0 ? ba : bb;
-                if (lane < nx)
-                    cov_g = exact_coverage<MODE>(
-                        pr, __builtin_bit_cast(float, v & 0x7fffffffu), (v >> 31) != 0);
-                const float c0 = __builtin_bit_cast(
-                    float, __builtin_amdgcn_ds_bpermute(4 * rk0, __builtin_bit_cast(int, cov_g)));
-                const float c1 = __builtin_bit_cast(
-                    float,
-                    __builtin_amdgcn_ds_bpermute(4 * (n0 + rk1), __builtin_bit_cast(int, cov_g)));
-                if (ex[0]) cov[0] = c0;
-                if (ex[1]) cov[1] = c1;
-            } else {
-#pragma unroll
-                for (int p = 0; p < kPix; ++p)
-                    if (ex[p]) cov[p] = exact_coverage<MODE>(pr, G[p].min_d2, ins[p]);
-            }
-            // The log record of this entry and wave: inside and exact bits, and
-            // each exact pixel's best edge and coverage, for the backward.
-            if (log_index) {
-                const uint32_t units = kLogHeaderUnits + (uint32_t)((nx + 1) >> 1);
-                if (st.n + units > kLogStageUnits) log_flush(log_pool, stage, st);
-                const int32_t at = log_reserve(log_ctr, log_first, log_units, lc, units);
-                if (at >= 0) {
-                    if ((uint32_t)at != st.base + st.n) {   // another region: flush first
-                        log_flush(log_pool, stage, st);
-                        st.base = (uint32_t)at;
-                    }
-                    uint4* rec = stage + st.n;
-                    st.n += units;
-                    if (lane == 0) {
-                        rec[0] = make_uint4((uint32_t)in0, (uint32_t)(in0 >> 32),
-                                            (uint32_t)in1, (uint32_t)(in1 >> 32));
-                        rec[1] = make_uint4((uint32_t)x0, (uint32_t)(x0 >> 32), (uint32_t)x1,
-                                            (uint32_t)(x1 >> 32));
-                    }
-                    int2* pairs = reinterpret_cast<int2*>(rec + kLogHeaderUnits);
-                    if (gathered) {
-                        if (lane < nx)
-                            pairs[lane] = make_int2(best_g, __builtin_bit_cast(int, cov_g));
-                    } else {
-                        if (ex[0])
-                            pairs[rk0] = make_int2(G[0].best, __builtin_bit_cast(int, cov[0]));
-                        if (ex[1])
-                            pairs[n0 + rk1] = make_int2(G[1].best, __builtin_bit_cast(int, cov[1]));
-                    }
-                }
-                idx_l = lane == k ? at : idx_l;
-                logged |= 1ull << k;
             }
 #pragma unroll
             for (int p = 0; p < kPix; ++p)
