@@ -96,8 +96,10 @@ int cs_isect_edge_ranges(const int32_t* prim_ids_sorted, const int32_t* seg_offs
  * project + exact AABB + tile ranges, uniform Bernstein flattening
  * (ops/cubic_splatting.py:1709-1719), per-primitive tile counts, depth ranks
  * (order[r] = primitive of depth rank r, ties by primitive id, and
- * rank_tile_ranges [nprim,4] its tile rectangle), per-tile list lengths
- * (tile_count [T]), per-row-segment first slots (tile_scratch [T]),
+ * rank_tile_ranges [nprim,4] its tile rectangle), per-tile list lengths per
+ * rank slab (tile_count) and per-row-segment first slots per slab
+ * (tile_scratch), each of cs_bin_list_elems(nprim, img_h, img_w, block_x,
+ * block_y) elements,
  * and status[4] (device int32) = {intersection total, 1 if seg_offsets is not
  * a valid CSR of nseg segments (the kernels then clamp every range),
  * seg_offsets[0], seg_offsets[nprim]}.  T = ceil(W/block_x) * ceil(H/block_y).
@@ -190,6 +192,15 @@ int cs_cubic_split_half(const float* cubics, int32_t n, float* left, float* righ
  * larger buffer).  zero_buf (optional, zero_n floats) is cleared by the same
  * launch: the caller's gradient accumulators for cs_rasterize_backward, which
  * saves that step a separate fill. */
+/* Elements of the tile_count and tile_scratch buffers that cs_bin_prepare,
+ * cs_bin_prepare_de_casteljau, cs_gs_bin_prepare and cs_bin_finish take:
+ * the list build splits the depth ranks into at most 64 slabs of whole
+ * 1024-rank chunks (one workgroup per slab and row segment of 64 tiles) and
+ * keeps a count per slab and tile (no reference counterpart: the reference's
+ * cumsum and sort need no such buffer, cubic_splatting.py:2877-2896). */
+size_t cs_bin_list_elems(int32_t nprim, int32_t img_h, int32_t img_w, int32_t block_x,
+                         int32_t block_y);
+
 int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t nprim,
                   const int32_t* status, int64_t capacity, int32_t img_h, int32_t img_w,
                   int32_t block_x, int32_t block_y, uint32_t* tile_count, uint32_t* tile_scratch,

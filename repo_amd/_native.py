@@ -47,6 +47,7 @@ _SIGNATURES = {
     "cs_bin_prepare": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                       _I32, _I32, _I32, _F, _I32, _I32, _P, _P, _P, _P, _P, _P,
                                       _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cs_bin_list_elems": (_SZ, [_I32, _I32, _I32, _I32, _I32]),
     "cs_bin_finish": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _I32, _I32, _I32, _I32, _P, _P,
                                      _P, _P, _P, _I64, _P]),
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,

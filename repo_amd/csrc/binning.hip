@@ -1307,19 +1307,25 @@ __global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ a, int n
 
 // Per-tile lists without a global sort.  Primitives cover rectangles of
 // tiles and arrive in depth-rank order (order[r], rank_rects[r]), so the list
-// of tile t is the subsequence of ranks whose rectangle contains t.  One
-// workgroup owns a row segment of up to 64 tiles.
-//   counting launch: the waves stride over all ranks (eight 64-rank loads in
-//     flight per wave); each rectangle that meets the segment adds +1 at its
-//     first column and -1 past its last in an LDS difference array, whose
-//     prefix sum is the per-tile count: tile_count.  The segment's first slot
-//     (the entries of all tiles before it in row-major order) is a sum over
-//     the same rectangles in closed form -- each one's tiles in the rows
-//     above plus those left of the segment in its row -- so no scan of the
-//     segment totals is needed: seg_scratch[seg]; workgroup 0 also sums the
-//     rectangles' areas into the total I;
-//   scatter launch: tile start = segment start + prefix of the segment's tile
-//     totals (wave 0 writes tile_bins), then the ranks in chunks of
+// of tile t is the subsequence of ranks whose rectangle contains t.  The work
+// is split two ways: a row segment of up to 64 tiles, and a slab of
+// consecutive ranks (list_slabs: at most kMaxSlabs slabs of at least
+// kSlabChunksMin whole 1024-rank chunks), one workgroup per (slab, segment),
+// so that large scenes fill the GPU and every rectangle is still read once
+// per segment of its rows.
+//   counting launch: each rectangle of the slab that meets the segment adds
+//     +1 at its first column and -1 past its last in an LDS difference array,
+//     whose prefix sum is the slab's count per tile: tile_count[slab][tile].
+//     The segment's first slot (the entries of all tiles before it in
+//     row-major order) is a sum over the rectangles in closed form -- each
+//     one's tiles in the rows above plus those left of the segment in its
+//     row -- taken per slab: seg_scratch[slab][segment]; the workgroups of
+//     segment 0 add their slab's areas into the total I (integer atomics,
+//     exact in any order; the total starts at 0).
+//   scatter launch: a tile's list starts at the segment's first slot (the
+//     sum over slabs) plus the totals of the tiles before it in the segment,
+//     and the slab's entries follow those of the slabs before it (the slab-0
+//     workgroup writes tile_bins); then the slab's ranks in chunks of
 //     kListChunk:
 //     1. each wave takes a contiguous slice of the chunk and tests its
 //        rectangles against the segment; the hits (primitive id and column
@@ -1327,14 +1333,37 @@ __global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ a, int n
 //        wave's after the hits of the slices before it;
 //     2. each wave owns kListTilesPerWave tile columns and reads that list 64
 //        hits at a time: per owned tile a ballot of the hits whose range
-//        contains it gives, in rank order, the tile's next entries, written
-//        to consecutive slots (mbcnt) of its list.
+//        contains it gives, in rank order, the tile's next entries, staged
+//        in LDS at consecutive positions (mbcnt); every 64 staged entries
+//        leave as one 64-lane store of consecutive slots of the tile's list
+//        (a few wide stores instead of one narrow store per ballot), the
+//        rest at the end of the slab.
 constexpr int kSegTiles = kWave;
 constexpr int kListWaves = 8;
 constexpr int kListTilesPerWave = kSegTiles / kListWaves;
-constexpr int kListChunk = 4096;
+constexpr int kListChunk = 1024;
 constexpr int kListSlice = kListChunk / kListWaves;
 constexpr int kListSteps = kListSlice / kWave;
+constexpr int kMaxSlabs = 64;
+
+// Rank slabs of the list build: nslab slabs of `slab` ranks (a multiple of
+// kListChunk; the last one shorter).
+struct ListSlabs {
+    int slab, nslab;
+};
+
+constexpr int kSlabChunksMin = 4;
+
+__host__ __device__ inline ListSlabs list_slabs(int P) {
+    const int chunks = (P + kListChunk - 1) / kListChunk;
+    int per = (chunks + kMaxSlabs - 1) / kMaxSlabs;
+    per = per < kSlabChunksMin ? kSlabChunksMin : per;
+    ListSlabs s;
+    s.slab = (per > 0 ? per : 1) * kListChunk;
+    s.nslab = (P + s.slab - 1) / s.slab;
+    if (s.nslab < 1) s.nslab = 1;
+    return s;
+}
 
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
@@ -1358,39 +1387,53 @@ __device__ __forceinline__ uint32_t rect_tiles_before(const int4& q, int ty, int
     return above + (in_row ? (uint32_t)max(0, min(x1, sx0) - x0) : 0u);
 }
 
+// Workgroup b's slab, segment, tile row and segment columns [sx0, sx1).
+struct ListPart {
+    int slab, seg, ty, sx0, sx1;
+};
+
+__device__ __forceinline__ ListPart list_part(int nsegs, int nsegcols, int tbx) {
+    ListPart q;
+    q.slab = (int)blockIdx.x / nsegs;
+    q.seg = (int)blockIdx.x - q.slab * nsegs;
+    q.ty = q.seg / nsegcols;
+    q.sx0 = (q.seg - q.ty * nsegcols) * kSegTiles;
+    q.sx1 = min(q.sx0 + kSegTiles, tbx);
+    return q;
+}
+
 __global__ __launch_bounds__(kWave * kListWaves) void k_tile_counts(
-    const int4* __restrict__ rank_rects, int P, int tbx, int nsegcols,
+    const int4* __restrict__ rank_rects, int P, int tbx, int tby, int nsegcols, int slab,
     uint32_t* __restrict__ tile_count, uint32_t* __restrict__ seg_scratch,
     int32_t* __restrict__ total_out) {
     __shared__ int diff[kSegTiles + 1];
     __shared__ uint32_t part[2][kListWaves];
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     const int lane = threadIdx.x & (kWave - 1);
-    const int ty = blockIdx.x / nsegcols;
-    const int sx0 = (blockIdx.x - ty * nsegcols) * kSegTiles;
-    const int sx1 = min(sx0 + kSegTiles, tbx);
+    const int nsegs = nsegcols * tby;
+    const ListPart lp = list_part(nsegs, nsegcols, tbx);
+    const int rb = lp.slab * slab, re = min(P, rb + slab);
     if (threadIdx.x <= kSegTiles) diff[threadIdx.x] = 0;
     __syncthreads();
     // Sums mod 2^32, as the list positions are formed (a total beyond int32 is
     // reported by the caller).
     uint32_t before = 0, total = 0;
-    const int tby = (int)gridDim.x / nsegcols;
-    for (int r0 = w * kWave * kListSteps; r0 < P; r0 += kListWaves * kWave * kListSteps) {
+    for (int r0 = rb + w * kWave * kListSteps; r0 < re; r0 += kListWaves * kWave * kListSteps) {
         int4 tr[kListSteps];
 #pragma unroll
         for (int k = 0; k < kListSteps; ++k) {
             const int rr = r0 + k * kWave + lane;
-            tr[k] = rr < P ? rank_rects[rr] : make_int4(0, 0, 0, 0);
+            tr[k] = rr < re ? rank_rects[rr] : make_int4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int k = 0; k < kListSteps; ++k) {
             const int4 q = tr[k];
             uint32_t area;
-            before += rect_tiles_before(q, ty, sx0, tbx, tby, area);
+            before += rect_tiles_before(q, lp.ty, lp.sx0, tbx, tby, area);
             total += area;
-            if (rect_meets_row(q, ty, sx0, sx1)) {
-                atomicAdd(&diff[max(q.x, sx0) - sx0], 1);
-                atomicAdd(&diff[min(q.z, sx1) - sx0], -1);
+            if (rect_meets_row(q, lp.ty, lp.sx0, lp.sx1)) {
+                atomicAdd(&diff[max(q.x, lp.sx0) - lp.sx0], 1);
+                atomicAdd(&diff[min(q.z, lp.sx1) - lp.sx0], -1);
             }
         }
     }
@@ -1403,8 +1446,9 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_counts(
     __syncthreads();
     if (w == 0) {
         const uint32_t n = (uint32_t)wave_incl_scan((uint32_t)diff[lane], lane);
-        const bool tile_ok = sx0 + lane < sx1;
-        if (tile_ok) tile_count[(size_t)ty * tbx + sx0 + lane] = n;
+        const bool tile_ok = lp.sx0 + lane < lp.sx1;
+        const size_t tiles = (size_t)tbx * tby;
+        if (tile_ok) tile_count[lp.slab * tiles + (size_t)lp.ty * tbx + lp.sx0 + lane] = n;
         if (lane == 0) {
             uint32_t b = 0, t = 0;
 #pragma unroll
@@ -1412,15 +1456,15 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_counts(
                 b += part[0][v];
                 t += part[1][v];
             }
-            seg_scratch[blockIdx.x] = b;
-            if (blockIdx.x == 0) *total_out = (int32_t)t;
+            seg_scratch[(size_t)lp.slab * nsegs + lp.seg] = b;
+            if (lp.seg == 0) atomicAdd(reinterpret_cast<uint32_t*>(total_out), t);
         }
     }
 }
 
 __global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
     const int32_t* __restrict__ order, const int4* __restrict__ rank_rects, int P, int tbx,
-    int nsegcols, const uint32_t* __restrict__ tile_count,
+    int tby, int nsegcols, int slab, int nslab, const uint32_t* __restrict__ tile_count,
     const uint32_t* __restrict__ seg_scratch, int32_t* __restrict__ prim_ids_sorted,
     int32_t* __restrict__ tile_bins, float* __restrict__ zero_buf, int64_t zero_n,
     const int32_t* __restrict__ total, int64_t capacity) {
@@ -1428,6 +1472,9 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
     __shared__ uint32_t hit_cols[kListChunk];
     __shared__ int hit_n[kListWaves];
     __shared__ uint32_t tile_start[kSegTiles];
+    // Per owned tile: entries staged for the next wide store (at most 63
+    // left plus 64 new).
+    __shared__ int32_t staged_all[kListWaves][kListTilesPerWave][2 * kWave];
     if (zero_buf) {
         const int64_t stride = (int64_t)gridDim.x * blockDim.x;
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += stride)
@@ -1435,25 +1482,45 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
     }
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     const int lane = threadIdx.x & (kWave - 1);
-    const int ty = blockIdx.x / nsegcols;
-    const int sx0 = (blockIdx.x - ty * nsegcols) * kSegTiles;
-    const int sx1 = min(sx0 + kSegTiles, tbx);
+    const int nsegs = nsegcols * tby;
+    const ListPart lp = list_part(nsegs, nsegcols, tbx);
+    const int ty = lp.ty, sx0 = lp.sx0, sx1 = lp.sx1;
+    const size_t tiles = (size_t)tbx * tby;
     const size_t row0 = (size_t)ty * tbx + sx0;
     if ((uint64_t)(uint32_t)*total > (uint64_t)capacity) {
         // The lists do not fit the caller's buffer: every tile reads as
         // empty, nothing is scattered, and the caller retries at full size.
-        if (w == 0 && sx0 + lane < sx1) {
+        if (lp.slab == 0 && w == 0 && sx0 + lane < sx1) {
             tile_bins[2 * (row0 + lane)] = 0;
             tile_bins[2 * (row0 + lane) + 1] = 0;
         }
         return;
     }
     if (w == 0) {
+        // The tile's count over all slabs, the slabs' counts before this one,
+        // and the segment's first slot (summed over the slabs).
         const bool tile_ok = sx0 + lane < sx1;
-        const uint32_t n = tile_ok ? tile_count[row0 + lane] : 0u;
-        const uint32_t start = seg_scratch[blockIdx.x] + wave_incl_scan(n, lane) - n;
-        tile_start[lane] = start;
-        if (tile_ok) {
+        uint32_t n = 0, n_before = 0, seg_first = 0;
+        // Eight slabs' loads in flight at a time (the loop would otherwise
+        // wait for each load before issuing the next).
+        for (int c0 = 0; c0 < nslab; c0 += 8) {
+            uint32_t v[8], f[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int c = c0 + k;
+                v[k] = tile_ok && c < nslab ? tile_count[c * tiles + row0 + lane] : 0u;
+                f[k] = c < nslab ? seg_scratch[(size_t)c * nsegs + lp.seg] : 0u;
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                n += v[k];
+                n_before += c0 + k < lp.slab ? v[k] : 0u;
+                seg_first += f[k];
+            }
+        }
+        const uint32_t start = seg_first + wave_incl_scan(n, lane) - n;
+        tile_start[lane] = start + n_before;
+        if (lp.slab == 0 && tile_ok) {
             // tile_bins.py:10-43: [start, end) per tile, (0, 0) when empty.
             tile_bins[2 * (row0 + lane)] = n ? (int32_t)start : 0;
             tile_bins[2 * (row0 + lane) + 1] = n ? (int32_t)(start + n) : 0;
@@ -1461,13 +1528,19 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
     }
     __syncthreads();
     uint32_t cur[kListTilesPerWave];
+    int nst[kListTilesPerWave];
 #pragma unroll
-    for (int k = 0; k < kListTilesPerWave; ++k) cur[k] = tile_start[w * kListTilesPerWave + k];
-    for (int c0 = 0; c0 < P; c0 += kListChunk) {
+    for (int k = 0; k < kListTilesPerWave; ++k) {
+        cur[k] = tile_start[w * kListTilesPerWave + k];
+        nst[k] = 0;
+    }
+    int32_t (*const staged)[2 * kWave] = staged_all[w];
+    const int rb = lp.slab * slab, re = min(P, rb + slab);
+    for (int c0 = rb; c0 < re; c0 += kListChunk) {
         // 1. Compact the chunk's hits into one list (this wave's loads all
         //    in flight before the first test).
         const int r0 = c0 + w * kListSlice;
-        const int r1 = min(r0 + kListSlice, P);
+        const int r1 = min(r0 + kListSlice, re);
         int4 tr[kListSteps];
         int pid[kListSteps];
 #pragma unroll
@@ -1521,12 +1594,24 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
                 const int col = w * kListTilesPerWave + k;
                 const bool in = x0 <= col && col < x1;
                 const uint64_t m = __ballot(in);
-                if (in) prim_ids_sorted[cur[k] + lanes_below(m)] = pidv;
-                cur[k] += (uint32_t)__builtin_popcountll(m);
+                if (in) staged[k][nst[k] + (int)lanes_below(m)] = pidv;
+                nst[k] += __builtin_popcountll(m);
+                if (nst[k] >= kWave) {
+                    // 64 entries out in one store; the rest move to the front
+                    // (LDS operations of a wave take effect in order).
+                    prim_ids_sorted[cur[k] + lane] = staged[k][lane];
+                    const int32_t rest = staged[k][kWave + lane];
+                    if (lane < nst[k] - kWave) staged[k][lane] = rest;
+                    cur[k] += kWave;
+                    nst[k] -= kWave;
+                }
             }
         }
         __syncthreads();
     }
+#pragma unroll
+    for (int k = 0; k < kListTilesPerWave; ++k)
+        if (lane < nst[k]) prim_ids_sorted[cur[k] + lane] = staged[k][lane];
 }
 
 // tile_bins.py:10-43 on the reference's int64 (tile << 32 | depth) keys.
@@ -1921,9 +2006,10 @@ static int rank_and_count(bool blocks_ranked, uint32_t* keys, int32_t* order,
                            order, nprim, prim_rects, rank_rects);
     }
     const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
-    hipLaunchKernelGGL(k_tile_counts, dim3(nsegcols * tby), dim3(kWave * kListWaves), 0,
-                       stream, rank_rects, nprim, tbx, nsegcols, tile_count, tile_scratch,
-                       status);
+    const ListSlabs ls = list_slabs(nprim);
+    hipLaunchKernelGGL(k_tile_counts, dim3(nsegcols * tby * ls.nslab),
+                       dim3(kWave * kListWaves), 0, stream, rank_rects, nprim, tbx, tby,
+                       nsegcols, ls.slab, tile_count, tile_scratch, status);
     return launch_status();
 }
 
@@ -2157,6 +2243,7 @@ __global__ __launch_bounds__(256) void k_gs_keys_rects(
     int32_t* __restrict__ order, int32_t* __restrict__ status) {
     const int g = blockIdx.x * blockDim.x + threadIdx.x;
     if (g == 0) {
+        status[0] = 0;
         status[1] = 0;
         status[2] = 0;
         status[3] = 0;
@@ -2194,6 +2281,14 @@ extern "C" int cs_gs_bin_prepare(const float* xys, const float* conics, const in
                           tile_scratch, status, stream);
 }
 
+extern "C" size_t cs_bin_list_elems(int32_t nprim, int32_t img_h, int32_t img_w, int32_t block_x,
+                                     int32_t block_y) {
+    if (nprim < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0) return 0;
+    const size_t tiles = (size_t)((img_w + block_x - 1) / block_x) *
+                         (size_t)((img_h + block_y - 1) / block_y);
+    return (size_t)list_slabs(nprim).nslab * tiles;
+}
+
 extern "C" int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges,
                              int32_t nprim, const int32_t* status, int64_t capacity,
                              int32_t img_h, int32_t img_w, int32_t block_x, int32_t block_y,
@@ -2206,9 +2301,11 @@ extern "C" int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_rang
         return CS_ERR_ARGS;
     const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
     const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
-    hipLaunchKernelGGL(k_tile_scatter, dim3(nsegcols * tby), dim3(kWave * kListWaves), 0,
-                       stream, order, reinterpret_cast<const int4*>(rank_tile_ranges), nprim, tbx,
-                       nsegcols, tile_count, tile_scratch, prim_ids_sorted, tile_bins,
+    const ListSlabs ls = list_slabs(nprim);
+    hipLaunchKernelGGL(k_tile_scatter, dim3(nsegcols * tby * ls.nslab),
+                       dim3(kWave * kListWaves), 0, stream, order,
+                       reinterpret_cast<const int4*>(rank_tile_ranges), nprim, tbx, tby, nsegcols,
+                       ls.slab, ls.nslab, tile_count, tile_scratch, prim_ids_sorted, tile_bins,
                        zero_n > 0 ? zero_buf : nullptr, zero_n, status, capacity);
     return launch_status();
 }

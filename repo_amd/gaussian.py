@@ -90,7 +90,7 @@ def project_backward(scales2d, rotation, radii, conics, v_xy, v_conic, img_h: in
 # -------------------------------------------------------------------- binning
 
 
-def _gs_fields(n, T, radix_elems, scan_elems):
+def _gs_fields(n, T, radix_elems, scan_elems, list_elems):
     f32, i32 = torch.float32, torch.int32
     return (
         ("tile_rects", i32, (n, 4)),
@@ -101,8 +101,8 @@ def _gs_fields(n, T, radix_elems, scan_elems):
         ("radix_counts", i32, (radix_elems,)),
         ("scan_temp", i32, (scan_elems,)),
         ("rank_tile_ranges", i32, (n, 4)),
-        ("tile_count", i32, (T,)),
-        ("tile_scratch", i32, (T,)),
+        ("tile_count", i32, (list_elems,)),
+        ("tile_scratch", i32, (list_elems,)),
         ("status", i32, (4,)),
         ("tile_bins", i32, (T, 2)),
         ("records", f32, (n, GS_RECORD_FLOATS)),
@@ -160,8 +160,9 @@ def bin_gaussians(xys, conics, radii, depths, img_h: int, img_w: int, block_x: i
     tbx, tby, _ = tile_bounds(img_h, img_w, block_x, block_y)
     T = tbx * tby
     key = ("gs", dev.index, n, img_h, img_w, block_x, block_y)
-    table, nbytes = _layout(key, _gs_fields(n, T, int(lib.cs_radix_counts_elems(n)),
-                                            int(lib.cs_scan_temp_elems(max(n, T)))))
+    table, nbytes = _layout(key, _gs_fields(
+        n, T, int(lib.cs_radix_counts_elems(n)), int(lib.cs_scan_temp_elems(max(n, T))),
+        int(lib.cs_bin_list_elems(n, img_h, img_w, block_x, block_y))))
     arena = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
     b = GsBinned(n, img_h, img_w, block_x, block_y, arena, table)
     q_ = b.ptr

@@ -118,7 +118,8 @@ def sub_blocks(img_h: int, img_w: int) -> int:
 
 # Buffers of one binning, carved from one arena allocation: name -> (dtype,
 # shape).  Shapes depend on (nseg, P, S, T, scratch sizes).
-def _binning_fields(nseg, P, E, T, nsub, radix_elems, scan_elems, grad_elems, adaptive=False):
+def _binning_fields(nseg, P, E, T, nsub, radix_elems, scan_elems, grad_elems, list_elems,
+                    adaptive=False):
     f32, i32 = torch.float32, torch.int32
     extra = ((("seg_edge_offsets", i32, (nseg + 1,)), ("edge_aux", i32, (E, N.EDGE_AUX_INTS)),
               ("leaf_counts", i32, (nseg,))) if adaptive else ())
@@ -139,8 +140,8 @@ def _binning_fields(nseg, P, E, T, nsub, radix_elems, scan_elems, grad_elems, ad
         ("radix_counts", i32, (radix_elems,)),
         ("scan_temp", i32, (scan_elems,)),
         ("rank_tile_ranges", i32, (P, 4)),
-        ("tile_count", i32, (T,)),
-        ("tile_scratch", i32, (T,)),
+        ("tile_count", i32, (list_elems,)),
+        ("tile_scratch", i32, (list_elems,)),
         ("status", i32, (4,)),
         ("tile_bins", i32, (T, 2)),
         ("wave_cost", i32, (2 * nsub,)),
@@ -321,7 +322,9 @@ def _bin_plan(key, lib, nseg, P, S, img_h, img_w, block_x, block_y, mode, adapti
         fields = _binning_fields(nseg, P, nseg * per_seg, T, sub_blocks(img_h, img_w),
                                  int(lib.cs_radix_counts_elems(P)),
                                  int(lib.cs_scan_temp_elems(max(P, T, nseg))),
-                                 _grad_accum_elems(nseg, P, mode), adaptive)
+                                 _grad_accum_elems(nseg, P, mode),
+                                 int(lib.cs_bin_list_elems(P, img_h, img_w, block_x, block_y)),
+                                 adaptive)
         table, nbytes = _layout(key, fields)
         plan = _BinPlan(table=table, nbytes=nbytes,
                         prep=tuple(table[f][0] for f in _PREP_FIELDS),
