@@ -195,7 +195,8 @@ int cs_cubic_split_half(const float* cubics, int32_t n, float* left, float* righ
 /* Elements of the tile_count and tile_scratch buffers that cs_bin_prepare,
  * cs_bin_prepare_de_casteljau, cs_gs_bin_prepare and cs_bin_finish take:
  * the list build splits the depth ranks into at most 64 slabs of whole
- * 1024-rank chunks (one workgroup per slab and row segment of 64 tiles) and
+ * 1024-rank chunks, about a thousand workgroups' worth (one workgroup per
+ * slab and row segment of 64 tiles), and
  * keeps a count per slab and tile (no reference counterpart: the reference's
  * cumsum and sort need no such buffer, cubic_splatting.py:2877-2896). */
 size_t cs_bin_list_elems(int32_t nprim, int32_t img_h, int32_t img_w, int32_t block_x,

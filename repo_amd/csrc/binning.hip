@@ -1309,10 +1309,10 @@ __global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ a, int n
 // tiles and arrive in depth-rank order (order[r], rank_rects[r]), so the list
 // of tile t is the subsequence of ranks whose rectangle contains t.  The work
 // is split two ways: a row segment of up to 64 tiles, and a slab of
-// consecutive ranks (list_slabs: at most kMaxSlabs slabs of at least
-// kSlabChunksMin whole 1024-rank chunks), one workgroup per (slab, segment),
-// so that large scenes fill the GPU and every rectangle is still read once
-// per segment of its rows.
+// consecutive ranks (list_slabs: whole 1024-rank chunks, as many slabs as
+// bring the launch to about a thousand workgroups), one workgroup per (slab,
+// segment), so that small and large scenes fill the GPU and every rectangle
+// is still read once per segment of its rows.
 //   counting launch: each rectangle of the slab that meets the segment adds
 //     +1 at its first column and -1 past its last in an LDS difference array,
 //     whose prefix sum is the slab's count per tile: tile_count[slab][tile].
@@ -1333,11 +1333,9 @@ __global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ a, int n
 //        wave's after the hits of the slices before it;
 //     2. each wave owns kListTilesPerWave tile columns and reads that list 64
 //        hits at a time: per owned tile a ballot of the hits whose range
-//        contains it gives, in rank order, the tile's next entries, staged
-//        in LDS at consecutive positions (mbcnt); every 64 staged entries
-//        leave as one 64-lane store of consecutive slots of the tile's list
-//        (a few wide stores instead of one narrow store per ballot), the
-//        rest at the end of the slab.
+//        contains it gives, in rank order, the tile's next entries, written
+//        to consecutive slots (mbcnt) of its list.  (Staging them in LDS for
+//        64-wide stores measured slower.)
 constexpr int kSegTiles = kWave;
 constexpr int kListWaves = 8;
 constexpr int kListTilesPerWave = kSegTiles / kListWaves;
@@ -1347,17 +1345,23 @@ constexpr int kListSteps = kListSlice / kWave;
 constexpr int kMaxSlabs = 64;
 
 // Rank slabs of the list build: nslab slabs of `slab` ranks (a multiple of
-// kListChunk; the last one shorter).
+// kListChunk; the last one shorter), as many as bring the launch to about
+// kListTargetGroups workgroups over the nsegs row segments (at most
+// kMaxSlabs, at most one per chunk): few segments take more, shorter slabs,
+// many segments fewer, longer ones (each slab's workgroup reads its ranks
+// once per segment either way).
 struct ListSlabs {
     int slab, nslab;
 };
 
-constexpr int kSlabChunksMin = 4;
+constexpr int kListTargetGroups = 1024;
 
-__host__ __device__ inline ListSlabs list_slabs(int P) {
+__host__ __device__ inline ListSlabs list_slabs(int P, int nsegs) {
     const int chunks = (P + kListChunk - 1) / kListChunk;
-    int per = (chunks + kMaxSlabs - 1) / kMaxSlabs;
-    per = per < kSlabChunksMin ? kSlabChunksMin : per;
+    int want = (kListTargetGroups + nsegs - 1) / (nsegs > 0 ? nsegs : 1);
+    want = want < 1 ? 1 : (want > kMaxSlabs ? kMaxSlabs : want);
+    want = want > chunks ? chunks : want;
+    const int per = want > 0 ? (chunks + want - 1) / want : 1;
     ListSlabs s;
     s.slab = (per > 0 ? per : 1) * kListChunk;
     s.nslab = (P + s.slab - 1) / s.slab;
@@ -1472,9 +1476,6 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
     __shared__ uint32_t hit_cols[kListChunk];
     __shared__ int hit_n[kListWaves];
     __shared__ uint32_t tile_start[kSegTiles];
-    // Per owned tile: entries staged for the next wide store (at most 63
-    // left plus 64 new).
-    __shared__ int32_t staged_all[kListWaves][kListTilesPerWave][2 * kWave];
     if (zero_buf) {
         const int64_t stride = (int64_t)gridDim.x * blockDim.x;
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += stride)
@@ -1534,7 +1535,7 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
         cur[k] = tile_start[w * kListTilesPerWave + k];
         nst[k] = 0;
     }
-    int32_t (*const staged)[2 * kWave] = staged_all[w];
+
     const int rb = lp.slab * slab, re = min(P, rb + slab);
     for (int c0 = rb; c0 < re; c0 += kListChunk) {
         // 1. Compact the chunk's hits into one list (this wave's loads all
@@ -1594,24 +1595,12 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
                 const int col = w * kListTilesPerWave + k;
                 const bool in = x0 <= col && col < x1;
                 const uint64_t m = __ballot(in);
-                if (in) staged[k][nst[k] + (int)lanes_below(m)] = pidv;
-                nst[k] += __builtin_popcountll(m);
-                if (nst[k] >= kWave) {
-                    // 64 entries out in one store; the rest move to the front
-                    // (LDS operations of a wave take effect in order).
-                    prim_ids_sorted[cur[k] + lane] = staged[k][lane];
-                    const int32_t rest = staged[k][kWave + lane];
-                    if (lane < nst[k] - kWave) staged[k][lane] = rest;
-                    cur[k] += kWave;
-                    nst[k] -= kWave;
-                }
+                if (in) prim_ids_sorted[cur[k] + lanes_below(m)] = pidv;
+                cur[k] += (uint32_t)__builtin_popcountll(m);
             }
         }
         __syncthreads();
     }
-#pragma unroll
-    for (int k = 0; k < kListTilesPerWave; ++k)
-        if (lane < nst[k]) prim_ids_sorted[cur[k] + lane] = staged[k][lane];
 }
 
 // tile_bins.py:10-43 on the reference's int64 (tile << 32 | depth) keys.
@@ -2006,7 +1995,7 @@ static int rank_and_count(bool blocks_ranked, uint32_t* keys, int32_t* order,
                            order, nprim, prim_rects, rank_rects);
     }
     const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
-    const ListSlabs ls = list_slabs(nprim);
+    const ListSlabs ls = list_slabs(nprim, nsegcols * tby);
     hipLaunchKernelGGL(k_tile_counts, dim3(nsegcols * tby * ls.nslab),
                        dim3(kWave * kListWaves), 0, stream, rank_rects, nprim, tbx, tby,
                        nsegcols, ls.slab, tile_count, tile_scratch, status);
@@ -2286,7 +2275,9 @@ extern "C" size_t cs_bin_list_elems(int32_t nprim, int32_t img_h, int32_t img_w,
     if (nprim < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 || block_y <= 0) return 0;
     const size_t tiles = (size_t)((img_w + block_x - 1) / block_x) *
                          (size_t)((img_h + block_y - 1) / block_y);
-    return (size_t)list_slabs(nprim).nslab * tiles;
+    const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
+    const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
+    return (size_t)list_slabs(nprim, nsegcols * tby).nslab * tiles;
 }
 
 extern "C" int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges,
@@ -2301,7 +2292,7 @@ extern "C" int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_rang
         return CS_ERR_ARGS;
     const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
     const int nsegcols = (tbx + kSegTiles - 1) / kSegTiles;
-    const ListSlabs ls = list_slabs(nprim);
+    const ListSlabs ls = list_slabs(nprim, nsegcols * tby);
     hipLaunchKernelGGL(k_tile_scatter, dim3(nsegcols * tby * ls.nslab),
                        dim3(kWave * kListWaves), 0, stream, order,
                        reinterpret_cast<const int4*>(rank_tile_ranges), nprim, tbx, tby, nsegcols,
