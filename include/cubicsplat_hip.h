@@ -219,9 +219,12 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
  * sub-blocks.
  * Scheduling (no reference counterpart; it changes no result).  Every raster
  * entry point takes, before its stream,
- *   tile_order [S] (NULL: XCD-contiguous order) -- workgroup b rasterizes
- *     sub-block tile_order[xcd(b)], xcd(b) the XCD-contiguous index of b; it
- *     must be a permutation of [0, S);
+ *   tile_order [cs_raster_tile_order_elems(S)] (NULL: XCD-contiguous order,
+ *     one workgroup per sub-block) -- an order written by
+ *     cs_raster_tile_order: the launch then has one workgroup per position,
+ *     workgroup b (on XCD b mod 8) rasterizes the sub-block at position
+ *     (b mod 8) * cap + b / 8 (cap = cs_raster_tile_order_elems(S) / 8), and
+ *     positions holding -1 do nothing; every sub-block must appear once;
  * and the forward ones also
  *   wave_cost [2S] uint32 out (NULL: not recorded; 8-byte aligned) -- each
  *     wave's duration in ticks of the 100 MHz constant clock.
@@ -229,9 +232,12 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
  * cs_raster_tile_order turns the costs of one launch into a heavy-first order
  * for the next ones (the backward of the same forward, the next forward of
  * the scene): long sub-blocks start first, short ones fill the tail.
- * chunked != 0 sorts each XCD's contiguous eighth of the sub-blocks on its own
- * (XCD x keeps its part of the image, and its L2 the records of that part);
- * chunked == 0 sorts all of them (balance across XCDs for skewed scenes). */
+ * chunked != 0 cuts the sub-blocks into eight contiguous runs of about equal
+ * total cost (at most cap each) and sorts run x onto XCD x's positions (XCD x
+ * keeps its part of the image, and its L2 the records of that part, and the
+ * XCDs finish together); chunked == 0 sorts all of them and deals them out
+ * over the XCDs in turn (balance for skewed scenes). */
+size_t cs_raster_tile_order_elems(int32_t ntiles);
 int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
                          int32_t* tile_order, hipStream_t stream);
 

@@ -393,23 +393,37 @@ struct TileGrid {
     int nsb;    // sub-blocks in the image
     int sbx, sby;
     int waves;  // waves per tile, 2 sbx sby
+    int ocap;   // positions per XCD of a tile order (order_cap(nsb))
 };
 
+// Positions per XCD of a heavy-first tile order for n sub-blocks: an eighth
+// of them and an eighth of that again, so that each XCD's run of sub-blocks
+// can be sized to an equal share of the cost (k_tile_order).
+__host__ __device__ __forceinline__ int order_cap(int n) {
+    const int q = (n + 7) >> 3;
+    return q + (q >> 3) + 1;
+}
+
 struct SubBlock {
-    int index;  // sub-block (the unit of the tile order and the wave costs)
+    int index;  // sub-block (the unit of the tile order and the wave costs), -1: none
     int tile;   // its tile
     int slot;   // this wave's slot among the tile's waves
     int r0, c0; // its first pixel row and column
 };
 
-// Sub-block of workgroup b: entry xcd_tile(b) of a heavy-first order when one
-// is given (cs_raster_tile_order), else the XCD-contiguous order xcd_tile(b).
-// Any permutation gives the same results: sub-blocks are independent.
+// Sub-block of workgroup b: with a heavy-first order (cs_raster_tile_order,
+// 8 ocap positions; the launch has 8 ocap workgroups, workgroup b on XCD
+// b mod 8) the entry at position (b mod 8) ocap + b / 8, which is -1 for the
+// positions past XCD b mod 8's run; else the XCD-contiguous order
+// xcd_tile(b).  Any permutation gives the same results: sub-blocks are
+// independent.
 __device__ __forceinline__ SubBlock sub_block(const TileGrid& tg,
                                               const int32_t* __restrict__ tile_order, int wv) {
-    const int t = xcd_tile(blockIdx.x, tg.nsb);
     SubBlock b;
-    b.index = tile_order ? __builtin_amdgcn_readfirstlane(tile_order[t]) : t;
+    b.index = tile_order
+                  ? __builtin_amdgcn_readfirstlane(
+                        tile_order[(blockIdx.x & 7) * tg.ocap + (blockIdx.x >> 3)])
+                  : xcd_tile(blockIdx.x, tg.nsb);
     const int sy = b.index / tg.sbtx, sx = b.index - sy * tg.sbtx;
     const int ty = sy / tg.sby, tx = sx / tg.sbx;
     b.tile = ty * tg.tbx + tx;
@@ -642,6 +656,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const SubBlock sb = sub_block(tg, tile_order, wv);
+    if (sb.index < 0) return;  // a position past this XCD's run (whole workgroup)
     const int tile = sb.tile;
     const int r0 = sb.r0 + wv * kWaveRows;
     const LanePixels L = lane_pixels(r0, sb.c0, img_h, img_w);
@@ -1033,6 +1048,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const SubBlock sb = sub_block(tg, tile_order, wv);
+    if (sb.index < 0) return;  // a position past this XCD's run (whole workgroup)
     const int tile = sb.tile;
     const int r0 = sb.r0 + wv * kWaveRows;
     const LanePixels L = lane_pixels(r0, sb.c0, img_h, img_w);
@@ -1449,21 +1465,24 @@ __global__ __launch_bounds__(256) void k_finalize(const float* __restrict__ v_px
 
 // Heavy-first tile order from the per-wave costs of a previous launch: a
 // counting sort of tiles by a log-linear bucket of their cost (two waves
-// summed; 128 buckets per octave), descending.  The raster takes tile
-// tile_order[xcd_tile(b, n)] for workgroup b, so the layout decides the
-// schedule:
-//   chunked (grid of 8, one workgroup per XCD's contiguous tile chunk): each
-//     chunk sorted in place, so XCD x still works on its own part of the
-//     image (L2 locality) and starts with its longest tiles;
-//   global (grid of 1): rank r at xcd_tile(r, n), so workgroups take the
-//     longest tiles of the whole image first (balance across XCDs).
+// summed; 128 buckets per octave), descending.  The order has order_cap(n)
+// positions per XCD (XCD x's at x * cap .. x * cap + cap - 1, the rest -1),
+// and workgroup b takes position (b mod 8) cap + b / 8, so the layout decides
+// the schedule:
+//   chunked (grid of 8, one workgroup per XCD): the tiles cut into eight
+//     contiguous runs of about equal total cost (each at most cap tiles),
+//     run x sorted onto XCD x's positions, so XCD x still works on its own
+//     part of the image (L2 locality), starts with its longest tiles, and
+//     the XCDs finish together;
+//   global (grid of 1): rank r at position (r mod 8) cap + r / 8, so
+//     workgroups take the longest tiles of the whole image first.
 // The costs are read once, coalesced, and each tile's bucket is kept in LDS
 // (16 bits per tile, up to kOrderLdsTiles tiles; larger ranges re-read the
 // costs).  Neighbouring tiles cost about the same, so the counting and
 // scatter passes visit tiles in the scrambled order i * kOrderStride mod m
 // (a bijection: the stride is a prime above any tile count) and a wave's LDS
 // atomics rarely share a bucket.  Order within a bucket is whatever the
-// atomics give; every layout is a permutation of the tiles.
+// atomics give; every layout holds each tile once.
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderBuckets = 4096;
 constexpr int kOrderPerThread = kOrderBuckets / kOrderThreads;
@@ -1481,9 +1500,58 @@ __device__ __forceinline__ uint32_t cost_bucket(uint32_t c) {
     return (uint32_t)e * 128u + m;                            // < 4096
 }
 
-__device__ __forceinline__ uint32_t tile_bucket(const uint32_t* __restrict__ wave_cost, int t) {
+__device__ __forceinline__ uint32_t tile_cost(const uint32_t* __restrict__ wave_cost, int t) {
     const uint2 w = reinterpret_cast<const uint2*>(wave_cost)[t];
-    return cost_bucket(w.x + w.y < w.x ? 0xffffffffu : w.x + w.y);
+    return w.x + w.y < w.x ? 0xffffffffu : w.x + w.y;
+}
+
+// Run boundaries bnd[0..8] of the chunked layout: bnd[k] the first tile whose
+// preceding tiles cost at least k/8 of the total, clamped so that every run
+// holds at most cap tiles (a feasible choice: 8 cap >= n).  Every workgroup
+// of the launch computes the same boundaries from the same costs.
+__device__ void order_bounds(const uint32_t* __restrict__ wave_cost, int n, int cap,
+                             int* __restrict__ bnd, unsigned long long* __restrict__ part) {
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid >> 6;
+    const int per = (n + kOrderThreads - 1) / kOrderThreads;
+    const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
+    unsigned long long own = 0;
+    for (int i = i0; i < i1; ++i) own += tile_cost(wave_cost, i);
+    // Exclusive prefix of `own` over the threads: wave scans, then the waves'
+    // totals.
+    unsigned long long v = own;
+    for (int d = 1; d < kWave; d <<= 1) {
+        const unsigned long long o = __shfl_up(v, (unsigned)d);
+        if (lane >= d) v += o;
+    }
+    if (lane == kWave - 1) part[w] = v;
+    __syncthreads();
+    unsigned long long before = v - own, total = 0;
+    for (int k = 0; k < kOrderThreads / kWave; ++k) {
+        if (k < w) before += part[k];
+        total += part[k];
+    }
+    // The thread whose range holds the k/8 cost mark finds its tile.
+    for (int k = 1; k < 8; ++k) {
+        const unsigned long long mark = total * (unsigned long long)k / 8ull;
+        if (mark == 0) {
+            if (tid == 0) bnd[k] = 0;
+        } else if (before < mark && mark <= before + own) {
+            unsigned long long c = before;
+            int j = i0;
+            while (c < mark) c += tile_cost(wave_cost, j++);
+            bnd[k] = j;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        bnd[0] = 0;
+        for (int k = 1; k < 8; ++k) {
+            const int lo = max(bnd[k - 1], n - (8 - k) * cap);
+            bnd[k] = min(max(bnd[k], lo), bnd[k - 1] + cap);
+        }
+        bnd[8] = n;
+    }
+    __syncthreads();
 }
 
 __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __restrict__ wave_cost,
@@ -1492,13 +1560,22 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
     __shared__ uint32_t start[kOrderBuckets];
     __shared__ uint16_t bucket[kOrderLdsTiles];
     __shared__ uint32_t part[kOrderThreads / kWave];
+    __shared__ unsigned long long cpart[kOrderThreads / kWave];
+    __shared__ int bnd[9];
     const int tid = threadIdx.x;
-    // This workgroup's tile range [lo, lo + m).
+    const int cap = order_cap(n);
+    // This workgroup's tile range [lo, lo + m); its unused positions are -1.
     int lo = 0, m = n;
     if (chunked) {
-        const int q = n >> 3, r = n & 7, x = blockIdx.x;
-        lo = x * q + min(x, r);
-        m = q + (x < r ? 1 : 0);
+        order_bounds(wave_cost, n, cap, bnd, cpart);
+        const int x = blockIdx.x;
+        lo = bnd[x];
+        m = bnd[x + 1] - lo;
+        for (int k = m + tid; k < cap; k += kOrderThreads) order[x * cap + k] = -1;
+    } else {
+        for (int x = 0; x < 8; ++x)
+            for (int k = ((n - x + 7) >> 3) + tid; k < cap; k += kOrderThreads)
+                order[x * cap + k] = -1;
     }
     if (m <= 0) return;
     const bool cached = m <= kOrderLdsTiles;
@@ -1525,7 +1602,7 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
     const uint32_t t0 = (uint32_t)(((uint64_t)tid * kOrderStride) % (uint64_t)m);
     const uint32_t jump = (uint32_t)(((uint64_t)kOrderThreads * kOrderStride) % (uint64_t)m);
     for (int i = tid, t = (int)t0; i < m; i += kOrderThreads) {
-        const uint32_t b = cached ? bucket[t] : tile_bucket(wave_cost, lo + t);
+        const uint32_t b = cached ? bucket[t] : cost_bucket(tile_cost(wave_cost, lo + t));
         atomicAdd(&start[b], 1u);
         t += (int)jump;
         if (t >= m) t -= m;
@@ -1558,9 +1635,9 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
     }
     __syncthreads();
     for (int i = tid, t = (int)t0; i < m; i += kOrderThreads) {
-        const uint32_t b = cached ? bucket[t] : tile_bucket(wave_cost, lo + t);
+        const uint32_t b = cached ? bucket[t] : cost_bucket(tile_cost(wave_cost, lo + t));
         const int rank = (int)atomicAdd(&start[b], 1u);
-        order[chunked ? lo + rank : xcd_tile(rank, n)] = lo + t;
+        order[chunked ? blockIdx.x * cap + rank : (rank & 7) * cap + (rank >> 3)] = lo + t;
         t += (int)jump;
         if (t >= m) t -= m;
     }
@@ -1849,9 +1926,15 @@ struct RasterArgs {
     hipStream_t stream;
 };
 
+// Workgroups of a raster launch: one per sub-block, or with a tile order
+// one per position of it (8 ocap, the positions past each XCD's run exit).
+static unsigned raster_groups(const RasterArgs& a) {
+    return (unsigned)(a.order ? 8 * a.tg.ocap : a.tg.nsb);
+}
+
 template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
-    hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(a.tg.nsb), dim3(kRasterThreads), 0,
+    hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(raster_groups(a)), dim3(kRasterThreads), 0,
                        a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tg,
                        a.order, a.wave_cost, a.out, a.out_planar, a.out_planes, a.final_T,
                        a.final_idx,
@@ -1865,7 +1948,7 @@ static void launch_bwd3(const RasterArgs& a) {
     // ceil(2^32 / eps) for div_eps (unused when eps <= 1).
     const uint32_t magic =
         a.eps > 1 ? (uint32_t)((0x100000000ull + (uint64_t)(a.eps - 1)) / (uint64_t)a.eps) : 0u;
-    hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT, ADAPTIVE>), dim3(a.tg.nsb),
+    hipLaunchKernelGGL((k_raster_bwd<MODE, COUNT, ADAPTIVE>), dim3(raster_groups(a)),
                        dim3(kRasterThreads), 0, a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg,
                        a.img_h, a.img_w, a.tg, a.order, a.eps, magic, a.aux, a.log_index,
                        a.log_pool, a.fT, a.fidx,
@@ -1913,6 +1996,7 @@ static bool tile_grid(int32_t img_h, int32_t img_w, int32_t block_x, int32_t blo
     tg.tbx = (img_w + block_x - 1) / block_x;
     tg.sbtx = (img_w + kTile - 1) / kTile;
     tg.nsb = tg.sbtx * ((img_h + kTile - 1) / kTile);
+    tg.ocap = order_cap(tg.nsb);
     return true;
 }
 
@@ -2149,6 +2233,11 @@ extern "C" int cs_rasterize_backward_counted(
                               v_stroke_widths, curve_contrib_rgb, curve_isect_contrib, nullptr,
                               log_index, log_pool, eval_counts, nprim, prim_scratch, tile_order,
                               stream);
+}
+
+extern "C" size_t cs_raster_tile_order_elems(int32_t ntiles) {
+    if (ntiles <= 0 || (uint64_t)ntiles >= kOrderStride) return 0;
+    return (size_t)8 * (size_t)order_cap(ntiles);
 }
 
 extern "C" int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,

@@ -659,7 +659,8 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
         b.tile_order = prev
         _ORDER_AGE[okey] = age
         return out, final_T, final_idx
-    order = torch.empty((nsub,), dtype=torch.int32, device=dev)
+    order = torch.empty((int(N.lib().cs_raster_tile_order_elems(nsub)),), dtype=torch.int32,
+                        device=dev)
     with N.prof("cubic.fwd.tile_order"):
         N.call("cs_raster_tile_order", cost, nsub, int(ORDER_CHUNKED), order.data_ptr(), st)
     b.tile_order = order

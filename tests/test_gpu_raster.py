@@ -57,6 +57,38 @@ def _bits(a):
     return np.ascontiguousarray(a).view(np.int32)
 
 
+def _order_runs(order, n):
+    """Checks a tile order's layout (8 rows of cap positions, each a run of
+    sub-blocks then -1s, every sub-block once) and returns the runs."""
+    from repo_amd import _native as N
+    cap = int(N.lib().cs_raster_tile_order_elems(n)) // 8
+    o = order.cpu().numpy()
+    assert o.size == 8 * cap
+    runs = []
+    for row in o.reshape(8, cap):
+        k = int((row >= 0).sum())
+        assert (row[:k] >= 0).all() and (row[k:] == -1).all()
+        runs.append(row[:k])
+    assert np.array_equal(np.sort(np.concatenate(runs)), np.arange(n))
+    return runs, cap
+
+
+def _expected_bounds(cost, n, cap):
+    """The chunked order's run boundaries restated: bnd[k] the first tile
+    whose predecessors cost at least floor(total k / 8), clamped so that every
+    run holds at most cap tiles."""
+    tile = cost.reshape(-1, 2).astype(np.uint64).sum(1)
+    csum = np.concatenate([[0], np.cumsum(tile)])
+    total = int(csum[-1])
+    bnd = [0]
+    for k in range(1, 8):
+        mark = total * k // 8
+        j = int(np.searchsorted(csum, mark, side="left"))
+        lo = max(bnd[-1], n - (8 - k) * cap)
+        bnd.append(min(max(j, lo), bnd[-1] + cap))
+    return bnd + [n]
+
+
 def _run(name):
     make, rows = CASES[name]
     sc = make()
@@ -287,11 +319,13 @@ def test_heavy_first_tile_order_is_a_permutation_and_changes_no_result():
     b.tile_order = None
     g0 = [t.clone() for t in splat.rasterize_backward(b, bg, T0, idx0, v)[:4]]
     n = int(b.tile_bins.shape[0])
-    assert torch.equal(torch.sort(order.long()).values, torch.arange(n, device="cuda"))
+    runs, _ = _order_runs(order, n)
+    for r in runs:                                     # chunked: contiguous runs
+        assert r.size == 0 or np.array_equal(np.sort(r), np.arange(r.min(), r.min() + r.size))
     out1, T1, idx1 = splat.rasterize_forward(b, bg)   # takes `order`
     assert torch.equal(out0, out1) and torch.equal(T0, T1) and torch.equal(idx0, idx1)
     assert b.tile_order is not first                   # each forward makes a new order
-    assert torch.equal(torch.sort(b.tile_order.long()).values, torch.arange(n, device="cuda"))
+    _order_runs(b.tile_order, n)
     splat.ORDER_CHUNKED = False                        # the global layout is a permutation too
     try:
         splat.rasterize_forward(b, bg)
@@ -299,7 +333,7 @@ def test_heavy_first_tile_order_is_a_permutation_and_changes_no_result():
     finally:
         splat.ORDER_CHUNKED = True
         splat.ORDER_EVERY = every
-    assert torch.equal(torch.sort(b.tile_order.long()).values, torch.arange(n, device="cuda"))
+    _order_runs(b.tile_order, n)
     assert torch.equal(out0, out2) and torch.equal(idx0, idx2)
     b.grad_accum_clean = False
     g1 = splat.rasterize_backward(b, bg, T1, idx1, v)[:4]
@@ -323,19 +357,55 @@ def test_heavy_first_tile_order_is_a_permutation_and_changes_no_result():
 @pytest.mark.parametrize("chunked", [1, 0])
 def test_tile_order_at_the_largest_tile_count(chunked):
     """A 16384 x 16384 image has 2^20 tiles, the most the kernels accept:
-    cs_raster_tile_order takes that count and returns a permutation (its
-    visiting stride stays a bijection), with random per-wave costs."""
+    cs_raster_tile_order takes that count and lays out every tile once (its
+    visiting stride stays a bijection), with random per-wave costs; chunked,
+    its eight runs are the restated cost-balanced ones."""
     from repo_amd import _native as N
     n = (16384 // 16) ** 2
     g = torch.Generator().manual_seed(5)
-    cost = torch.randint(0, 1 << 20, (2 * n,), generator=g, dtype=torch.int32).cuda()
-    order = torch.full((n,), -1, dtype=torch.int32, device="cuda")
-    N.call("cs_raster_tile_order", cost.data_ptr(), n, chunked, order.data_ptr(),
-           N.stream(cost.device))
-    assert torch.equal(torch.sort(order.long()).values, torch.arange(n, device="cuda"))
+    cost = torch.randint(0, 1 << 20, (2 * n,), generator=g, dtype=torch.int32)
+    order = torch.full((int(N.lib().cs_raster_tile_order_elems(n)),), -7, dtype=torch.int32,
+                       device="cuda")
+    N.call("cs_raster_tile_order", cost.cuda().data_ptr(), n, chunked, order.data_ptr(),
+           N.stream(order.device))
+    runs, cap = _order_runs(order, n)
+    if chunked:
+        bnd = _expected_bounds(cost.numpy(), n, cap)
+        for x in range(8):
+            assert np.array_equal(np.sort(runs[x]), np.arange(bnd[x], bnd[x + 1]))
+    else:
+        assert [r.size for r in runs] == [(n - x + 7) // 8 for x in range(8)]
+    assert N.lib().cs_raster_tile_order_elems(1048583) == 0
     with pytest.raises(RuntimeError):
-        N.call("cs_raster_tile_order", cost.data_ptr(), 1048583, chunked, order.data_ptr(),
-               N.stream(cost.device))
+        N.call("cs_raster_tile_order", cost.cuda().data_ptr(), 1048583, chunked,
+               order.data_ptr(), N.stream(order.device))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 7, 9, 4096, 10880])
+def test_tile_order_runs_balance_cost_within_their_cap(n):
+    """Chunked orders cut the tiles into eight runs of about equal cost: with
+    the heavy tiles all in the first sixteenth the first runs are short and the
+    cap (an eighth of the tiles and an eighth more) bounds the later ones; the
+    runs equal the restated boundaries, for tile counts below 8 too."""
+    from repo_amd import _native as N
+    g = torch.Generator().manual_seed(n)
+    cost = torch.randint(1, 50, (2 * n,), generator=g, dtype=torch.int32)
+    cost[: 2 * max(1, n // 16)] *= 1000
+    order = torch.full((int(N.lib().cs_raster_tile_order_elems(n)),), -7, dtype=torch.int32,
+                       device="cuda")
+    N.call("cs_raster_tile_order", cost.cuda().data_ptr(), n, 1, order.data_ptr(),
+           N.stream(order.device))
+    runs, cap = _order_runs(order, n)
+    bnd = _expected_bounds(cost.numpy(), n, cap)
+    assert all(bnd[x + 1] - bnd[x] <= cap for x in range(8))
+    for x in range(8):
+        assert np.array_equal(np.sort(runs[x]), np.arange(bnd[x], bnd[x + 1]))
+    # Heavy first within a run.
+    tile = cost.numpy().reshape(-1, 2).sum(1)
+    for r in runs:
+        if r.size > 1:
+            assert tile[r[0]] >= np.median(tile[r])
 
 
 @pytest.mark.gpu
