@@ -241,6 +241,16 @@ size_t cs_raster_tile_order_elems(int32_t ntiles);
 int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
                          int32_t* tile_order, hipStream_t stream);
 
+/* cs_raster_tile_order from running averages (no reference counterpart): a
+ * sub-block's cost is its two waves' durations summed, averaged with its
+ * previous cost cost_in [S] when given (round half up), and the costs used
+ * are written to cost_out [S] (or NULL) for the next call's cost_in; cost_out
+ * must not be cost_in.  One launch's durations vary by about a fifth from
+ * launch to launch, so the average orders the next launches better. */
+int cs_raster_tile_order_averaged(const uint32_t* wave_cost, const uint32_t* cost_in,
+                                  uint32_t* cost_out, int32_t ntiles, int32_t chunked,
+                                  int32_t* tile_order, hipStream_t stream);
+
 /* Tiles of any size (block_x * block_y <= 1024, the reference's
  * one-thread-per-pixel launch threads=(block_x, block_y)), for sizes the
  * 16 x 16 sub-block entry points above do not take (for example 8 x 8 or

@@ -66,6 +66,7 @@ _SIGNATURES = {
                                                      _P]),
     "cs_raster_tile_order_elems": (_SZ, [_I32]),
     "cs_raster_tile_order": (ctypes.c_int, [_P, _I32, _I32, _P, _P]),
+    "cs_raster_tile_order_averaged": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _P]),
     "cs_rasterize_forward_any_tile": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                                      _I32, _P, _I32, _P, _P, _P, _P]),
     "cs_rasterize_backward_any_tile": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _I32, _I32, _I32,

@@ -1500,22 +1500,32 @@ __device__ __forceinline__ uint32_t cost_bucket(uint32_t c) {
     return (uint32_t)e * 128u + m;                            // < 4096
 }
 
-__device__ __forceinline__ uint32_t tile_cost(const uint32_t* __restrict__ wave_cost, int t) {
-    const uint2 w = reinterpret_cast<const uint2*>(wave_cost)[t];
-    return w.x + w.y < w.x ? 0xffffffffu : w.x + w.y;
+// A tile's cost: its two waves' durations summed (saturating), averaged with
+// the tile's previous cost when one is given.  One launch's durations vary by
+// about a fifth from launch to launch (a wave's time depends on what runs
+// beside it), so the running average predicts the next launch better.
+struct TileCosts {
+    const uint32_t* wave_cost;  // [2n] this launch's wave durations
+    const uint32_t* prev;       // [n] previous costs, or null
+};
+
+__device__ __forceinline__ uint32_t tile_cost(const TileCosts& tc, int t) {
+    const uint2 w = reinterpret_cast<const uint2*>(tc.wave_cost)[t];
+    const uint32_t c = w.x + w.y < w.x ? 0xffffffffu : w.x + w.y;
+    return tc.prev ? (uint32_t)(((uint64_t)tc.prev[t] + c + 1) >> 1) : c;
 }
 
 // Run boundaries bnd[0..8] of the chunked layout: bnd[k] the first tile whose
 // preceding tiles cost at least k/8 of the total, clamped so that every run
 // holds at most cap tiles (a feasible choice: 8 cap >= n).  Every workgroup
 // of the launch computes the same boundaries from the same costs.
-__device__ void order_bounds(const uint32_t* __restrict__ wave_cost, int n, int cap,
+__device__ void order_bounds(const TileCosts& tc, int n, int cap,
                              int* __restrict__ bnd, unsigned long long* __restrict__ part) {
     const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid >> 6;
     const int per = (n + kOrderThreads - 1) / kOrderThreads;
     const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
     unsigned long long own = 0;
-    for (int i = i0; i < i1; ++i) own += tile_cost(wave_cost, i);
+    for (int i = i0; i < i1; ++i) own += tile_cost(tc, i);
     // Exclusive prefix of `own` over the threads: wave scans, then the waves'
     // totals.
     unsigned long long v = own;
@@ -1538,7 +1548,7 @@ __device__ void order_bounds(const uint32_t* __restrict__ wave_cost, int n, int 
         } else if (before < mark && mark <= before + own) {
             unsigned long long c = before;
             int j = i0;
-            while (c < mark) c += tile_cost(wave_cost, j++);
+            while (c < mark) c += tile_cost(tc, j++);
             bnd[k] = j;
         }
     }
@@ -1554,9 +1564,14 @@ __device__ void order_bounds(const uint32_t* __restrict__ wave_cost, int n, int 
     __syncthreads();
 }
 
+// cost_out (or null): the costs the order was made from, for the next order's
+// average (never the same buffer as cost_in).
 __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __restrict__ wave_cost,
+                                                            const uint32_t* __restrict__ cost_in,
+                                                            uint32_t* __restrict__ cost_out,
                                                             int n, int chunked,
                                                             int32_t* __restrict__ order) {
+    const TileCosts tc{wave_cost, cost_in};
     __shared__ uint32_t start[kOrderBuckets];
     __shared__ uint16_t bucket[kOrderLdsTiles];
     __shared__ uint32_t part[kOrderThreads / kWave];
@@ -1567,7 +1582,7 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
     // This workgroup's tile range [lo, lo + m); its unused positions are -1.
     int lo = 0, m = n;
     if (chunked) {
-        order_bounds(wave_cost, n, cap, bnd, cpart);
+        order_bounds(tc, n, cap, bnd, cpart);
         const int x = blockIdx.x;
         lo = bnd[x];
         m = bnd[x + 1] - lo;
@@ -1578,23 +1593,23 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
                 order[x * cap + k] = -1;
     }
     if (m <= 0) return;
+    if (cost_out)
+        for (int i = tid; i < m; i += kOrderThreads) cost_out[lo + i] = tile_cost(tc, lo + i);
     const bool cached = m <= kOrderLdsTiles;
     for (int i = tid; i < kOrderBuckets; i += kOrderThreads) start[i] = 0;
     if (cached) {
         // All of the thread's cost loads in flight at once.
         constexpr int kPer = kOrderLdsTiles / kOrderThreads;
-        uint2 wc[kPer];
+        uint32_t wc[kPer];
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const int t = tid + k * kOrderThreads;
-            wc[k] = t < m ? reinterpret_cast<const uint2*>(wave_cost)[lo + t]
-                          : make_uint2(0u, 0u);
+            wc[k] = t < m ? tile_cost(tc, lo + t) : 0u;
         }
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const int t = tid + k * kOrderThreads;
-            const uint32_t c = wc[k].x + wc[k].y < wc[k].x ? 0xffffffffu : wc[k].x + wc[k].y;
-            if (t < m) bucket[t] = (uint16_t)cost_bucket(c);
+            if (t < m) bucket[t] = (uint16_t)cost_bucket(wc[k]);
         }
     }
     __syncthreads();
@@ -1602,7 +1617,7 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
     const uint32_t t0 = (uint32_t)(((uint64_t)tid * kOrderStride) % (uint64_t)m);
     const uint32_t jump = (uint32_t)(((uint64_t)kOrderThreads * kOrderStride) % (uint64_t)m);
     for (int i = tid, t = (int)t0; i < m; i += kOrderThreads) {
-        const uint32_t b = cached ? bucket[t] : cost_bucket(tile_cost(wave_cost, lo + t));
+        const uint32_t b = cached ? bucket[t] : cost_bucket(tile_cost(tc, lo + t));
         atomicAdd(&start[b], 1u);
         t += (int)jump;
         if (t >= m) t -= m;
@@ -1635,7 +1650,7 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
     }
     __syncthreads();
     for (int i = tid, t = (int)t0; i < m; i += kOrderThreads) {
-        const uint32_t b = cached ? bucket[t] : cost_bucket(tile_cost(wave_cost, lo + t));
+        const uint32_t b = cached ? bucket[t] : cost_bucket(tile_cost(tc, lo + t));
         const int rank = (int)atomicAdd(&start[b], 1u);
         order[chunked ? blockIdx.x * cap + rank : (rank & 7) * cap + (rank >> 3)] = lo + t;
         t += (int)jump;
@@ -2240,13 +2255,27 @@ extern "C" size_t cs_raster_tile_order_elems(int32_t ntiles) {
     return (size_t)8 * (size_t)order_cap(ntiles);
 }
 
-extern "C" int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
-                                    int32_t* tile_order, hipStream_t stream) {
+static int tile_order_launch(const uint32_t* wave_cost, const uint32_t* cost_in,
+                             uint32_t* cost_out, int32_t ntiles, int32_t chunked,
+                             int32_t* tile_order, hipStream_t stream) {
     if (ntiles <= 0 || (uint64_t)ntiles >= kOrderStride || !wave_cost || !tile_order)
         return CS_ERR_ARGS;
+    if (cost_in && cost_in == cost_out) return CS_ERR_ARGS;
     hipLaunchKernelGGL(k_tile_order, dim3(chunked ? 8 : 1), dim3(kOrderThreads), 0, stream,
-                       wave_cost, ntiles, chunked ? 1 : 0, tile_order);
+                       wave_cost, cost_in, cost_out, ntiles, chunked ? 1 : 0, tile_order);
     return raster_status();
+}
+
+extern "C" int cs_raster_tile_order(const uint32_t* wave_cost, int32_t ntiles, int32_t chunked,
+                                    int32_t* tile_order, hipStream_t stream) {
+    return tile_order_launch(wave_cost, nullptr, nullptr, ntiles, chunked, tile_order, stream);
+}
+
+extern "C" int cs_raster_tile_order_averaged(const uint32_t* wave_cost, const uint32_t* cost_in,
+                                             uint32_t* cost_out, int32_t ntiles,
+                                             int32_t chunked, int32_t* tile_order,
+                                             hipStream_t stream) {
+    return tile_order_launch(wave_cost, cost_in, cost_out, ntiles, chunked, tile_order, stream);
 }
 
 extern "C" int cs_accumulate_edge_grads(const float* v_edges, int32_t nseg,

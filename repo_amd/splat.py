@@ -476,6 +476,10 @@ def intersection_capacity(num_intersects: int) -> int:
 # still writing.
 _TILE_ORDERS: "dict[tuple, torch.Tensor]" = {}
 _ORDER_AGE: "dict[tuple, int]" = {}   # forwards since the order was made
+# Per key, the sub-block costs the last order was made from (a running
+# average over the orders, cs_raster_tile_order_averaged) and a spare buffer
+# for the next ones.
+_TILE_COSTS: "dict[tuple, tuple]" = {}
 _MAX_ORDERS = 16
 # A new heavy-first order is made from every ORDER_EVERY-th forward's wave
 # durations (a tile's cost changes slowly between training steps); the
@@ -661,15 +665,21 @@ def rasterize_forward(b: Binned, background: torch.Tensor, eval_counts=None, log
         return out, final_T, final_idx
     order = torch.empty((int(N.lib().cs_raster_tile_order_elems(nsub)),), dtype=torch.int32,
                         device=dev)
+    last, spare = _TILE_COSTS.get(okey, (None, None))
+    if spare is None:
+        spare = torch.empty((nsub,), dtype=torch.int32, device=dev)
     with N.prof("cubic.fwd.tile_order"):
-        N.call("cs_raster_tile_order", cost, nsub, int(ORDER_CHUNKED), order.data_ptr(), st)
+        N.call("cs_raster_tile_order_averaged", cost, N.ptr(last), spare.data_ptr(), nsub,
+               int(ORDER_CHUNKED), order.data_ptr(), st)
     b.tile_order = order
+    _TILE_COSTS[okey] = (spare, last)
     _TILE_ORDERS.pop(okey, None)
     _ORDER_AGE.pop(okey, None)
     if len(_TILE_ORDERS) >= _MAX_ORDERS:
         old = next(iter(_TILE_ORDERS))
         _TILE_ORDERS.pop(old)
         _ORDER_AGE.pop(old, None)
+        _TILE_COSTS.pop(old, None)
     _TILE_ORDERS[okey] = order
     _ORDER_AGE[okey] = 0
     return out, final_T, final_idx

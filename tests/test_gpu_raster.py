@@ -73,11 +73,14 @@ def _order_runs(order, n):
     return runs, cap
 
 
-def _expected_bounds(cost, n, cap):
+def _expected_bounds(cost, n, cap, tile=None):
     """The chunked order's run boundaries restated: bnd[k] the first tile
     whose predecessors cost at least floor(total k / 8), clamped so that every
-    run holds at most cap tiles."""
-    tile = cost.reshape(-1, 2).astype(np.uint64).sum(1)
+    run holds at most cap tiles (tile costs: the wave pairs summed, or
+    `tile`)."""
+    if tile is None:
+        tile = cost.reshape(-1, 2).astype(np.uint64).sum(1)
+    tile = np.asarray(tile, dtype=np.uint64)
     csum = np.concatenate([[0], np.cumsum(tile)])
     total = int(csum[-1])
     bnd = [0]
@@ -406,6 +409,41 @@ def test_tile_order_runs_balance_cost_within_their_cap(n):
     for r in runs:
         if r.size > 1:
             assert tile[r[0]] >= np.median(tile[r])
+
+
+@pytest.mark.gpu
+def test_averaged_tile_order_costs_and_runs():
+    """cs_raster_tile_order_averaged: the costs it writes are the tile's wave
+    pair averaged with the previous cost (round half up), the runs are the
+    restated ones of those averages, no previous cost gives the plain pair
+    sums, and the same buffer for both costs is refused."""
+    from repo_amd import _native as N
+    n = 10880
+    g = torch.Generator().manual_seed(11)
+    wave = torch.randint(0, 4000, (2 * n,), generator=g, dtype=torch.int32)
+    prev = torch.randint(0, 9000, (n,), generator=g, dtype=torch.int32)
+    elems = int(N.lib().cs_raster_tile_order_elems(n))
+    order = torch.full((elems,), -7, dtype=torch.int32, device="cuda")
+    out = torch.full((n,), -1, dtype=torch.int32, device="cuda")
+    wave_d, prev_d = wave.cuda(), prev.cuda()
+    st = N.stream(order.device)
+    pair = wave.numpy().reshape(-1, 2).astype(np.int64).sum(1)
+    N.call("cs_raster_tile_order_averaged", wave_d.data_ptr(), None, out.data_ptr(), n, 1,
+           order.data_ptr(), st)
+    assert np.array_equal(out.cpu().numpy(), pair)
+    N.call("cs_raster_tile_order_averaged", wave_d.data_ptr(), prev_d.data_ptr(),
+           out.data_ptr(), n, 1, order.data_ptr(), st)
+    want = (prev.numpy().astype(np.int64) + pair + 1) >> 1
+    assert np.array_equal(out.cpu().numpy(), want)
+    runs, cap = _order_runs(order, n)
+    bnd = _expected_bounds(None, n, cap, tile=want)
+    for x in range(8):
+        assert np.array_equal(np.sort(runs[x]), np.arange(bnd[x], bnd[x + 1]))
+        if runs[x].size > 1:
+            assert want[runs[x][0]] >= np.median(want[runs[x]])
+    with pytest.raises(RuntimeError):
+        N.call("cs_raster_tile_order_averaged", wave_d.data_ptr(), out.data_ptr(),
+               out.data_ptr(), n, 1, order.data_ptr(), st)
 
 
 @pytest.mark.gpu
