@@ -349,6 +349,24 @@ __device__ __forceinline__ float wave_sum_lane63(float x) {
     return x;
 }
 
+template <int CTRL, int ROW_MASK, bool ZERO_OOB>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, ZERO_OOB);
+}
+
+// Inclusive sum over lanes 0..i in lane i, the same six DPP steps as
+// wave_sum_lane63 (each lane's partial sums are its own prefix).  Every lane
+// must be active.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x) {
+    x += dpp_u32<0x111, 0xf, true>(x);
+    x += dpp_u32<0x112, 0xf, true>(x);
+    x += dpp_u32<0x114, 0xf, true>(x);
+    x += dpp_u32<0x118, 0xf, true>(x);
+    x += dpp_u32<0x142, 0xa, false>(x);
+    x += dpp_u32<0x143, 0xc, false>(x);
+    return x;
+}
+
 // t + (t moved by `STRIDE` lanes) on the lower half of each 2*STRIDE group,
 // with v_permlane16_swap / v_permlane32_swap: the swap exchanges the upper
 // rows of its first register with the lower rows of its second, so swapping t

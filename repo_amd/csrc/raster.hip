@@ -1515,41 +1515,73 @@ __device__ __forceinline__ uint32_t tile_cost(const TileCosts& tc, int t) {
     return tc.prev ? (uint32_t)(((uint64_t)tc.prev[t] + c + 1) >> 1) : c;
 }
 
-// Run boundaries bnd[0..8] of the chunked layout: bnd[k] the first tile whose
-// preceding tiles cost at least k/8 of the total, clamped so that every run
-// holds at most cap tiles (a feasible choice: 8 cap >= n).  Every workgroup
-// of the launch computes the same boundaries from the same costs.
-__device__ void order_bounds(const TileCosts& tc, int n, int cap,
-                             int* __restrict__ bnd, unsigned long long* __restrict__ part) {
+// Run boundaries bnd[0..8] of the chunked layout, from the tiles' costs in
+// units of 16 ticks capped at 4095 (scale_cost; 12 bits, so the sums of up to
+// 2^20 tiles fit 32 bits): bnd[k] the first tile whose preceding tiles cost at
+// least floor(k total / 8), clamped so that every run holds at most cap tiles
+// (a feasible choice: 8 cap >= n).  Every workgroup of the launch computes the
+// same boundaries from the same costs.  Thread i sums the contiguous tiles
+// [i per, i per + per); with per <= kOrderScanRegs the scaled costs are
+// loaded coalesced and staged through LDS (the sort's bucket array, free until
+// the sort) so that each thread reads its range from there; the block's
+// prefix is a DPP scan per wave and the waves' totals.  The thread whose
+// range takes the running cost across a mark finds its tile.
+constexpr int kOrderScanRegs = 16;
+constexpr int kOrderWaves = kOrderThreads / kWave;
+static_assert(kOrderScanRegs * kOrderThreads <= kOrderLdsTiles, "staging fits the bucket array");
+
+__device__ __forceinline__ uint32_t scale_cost(uint32_t c) { return min(c >> 4, 4095u); }
+
+__device__ void order_bounds(const TileCosts& tc, int n, int cap, int* __restrict__ bnd,
+                             uint16_t* __restrict__ stage, uint32_t* __restrict__ part) {
     const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid >> 6;
     const int per = (n + kOrderThreads - 1) / kOrderThreads;
     const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
-    unsigned long long own = 0;
-    for (int i = i0; i < i1; ++i) own += tile_cost(tc, i);
-    // Exclusive prefix of `own` over the threads: wave scans, then the waves'
-    // totals.
-    unsigned long long v = own;
-    for (int d = 1; d < kWave; d <<= 1) {
-        const unsigned long long o = __shfl_up(v, (unsigned)d);
-        if (lane >= d) v += o;
+    const bool staged = per <= kOrderScanRegs;
+    uint32_t c[kOrderScanRegs];
+    uint32_t own = 0;
+    if (staged) {
+#pragma unroll
+        for (int k = 0; k < kOrderScanRegs; ++k) {
+            const int t = k * kOrderThreads + tid;
+            if (t < n) stage[t] = (uint16_t)scale_cost(tile_cost(tc, t));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kOrderScanRegs; ++k) {
+            c[k] = k < i1 - i0 ? (uint32_t)stage[i0 + k] : 0u;
+            own += c[k];
+        }
+    } else {
+        for (int i = i0; i < i1; ++i) own += scale_cost(tile_cost(tc, i));
     }
-    if (lane == kWave - 1) part[w] = v;
+    const uint32_t incl = wave_incl_scan_u32(own);
+    if (lane == kWave - 1) part[w] = incl;
     __syncthreads();
-    unsigned long long before = v - own, total = 0;
-    for (int k = 0; k < kOrderThreads / kWave; ++k) {
-        if (k < w) before += part[k];
-        total += part[k];
+    uint32_t before = incl - own, total = 0;
+    for (int x = 0; x < kOrderWaves; ++x) {
+        const uint32_t px = part[x];
+        before += x < w ? px : 0u;
+        total += px;
     }
-    // The thread whose range holds the k/8 cost mark finds its tile.
-    for (int k = 1; k < 8; ++k) {
-        const unsigned long long mark = total * (unsigned long long)k / 8ull;
+    for (int q = 1; q < 8; ++q) {
+        const uint32_t mark = (uint32_t)((uint64_t)total * (uint64_t)q / 8ull);
         if (mark == 0) {
-            if (tid == 0) bnd[k] = 0;
+            if (tid == 0) bnd[q] = 0;
         } else if (before < mark && mark <= before + own) {
-            unsigned long long c = before;
+            uint32_t acc = before;
             int j = i0;
-            while (c < mark) c += tile_cost(tc, j++);
-            bnd[k] = j;
+            if (staged) {
+#pragma unroll
+                for (int k = 0; k < kOrderScanRegs; ++k)
+                    if (acc < mark) {
+                        acc += c[k];
+                        ++j;
+                    }
+            } else {
+                while (acc < mark) acc += scale_cost(tile_cost(tc, j++));
+            }
+            bnd[q] = j;
         }
     }
     __syncthreads();
@@ -1575,14 +1607,13 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
     __shared__ uint32_t start[kOrderBuckets];
     __shared__ uint16_t bucket[kOrderLdsTiles];
     __shared__ uint32_t part[kOrderThreads / kWave];
-    __shared__ unsigned long long cpart[kOrderThreads / kWave];
     __shared__ int bnd[9];
     const int tid = threadIdx.x;
     const int cap = order_cap(n);
     // This workgroup's tile range [lo, lo + m); its unused positions are -1.
     int lo = 0, m = n;
     if (chunked) {
-        order_bounds(tc, n, cap, bnd, cpart);
+        order_bounds(tc, n, cap, bnd, bucket, part);
         const int x = blockIdx.x;
         lo = bnd[x];
         m = bnd[x + 1] - lo;
@@ -1593,9 +1624,9 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
                 order[x * cap + k] = -1;
     }
     if (m <= 0) return;
-    if (cost_out)
-        for (int i = tid; i < m; i += kOrderThreads) cost_out[lo + i] = tile_cost(tc, lo + i);
     const bool cached = m <= kOrderLdsTiles;
+    if (cost_out && !cached)
+        for (int i = tid; i < m; i += kOrderThreads) cost_out[lo + i] = tile_cost(tc, lo + i);
     for (int i = tid; i < kOrderBuckets; i += kOrderThreads) start[i] = 0;
     if (cached) {
         // All of the thread's cost loads in flight at once.
@@ -1609,7 +1640,10 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const uint32_t* __
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const int t = tid + k * kOrderThreads;
-            if (t < m) bucket[t] = (uint16_t)cost_bucket(wc[k]);
+            if (t < m) {
+                bucket[t] = (uint16_t)cost_bucket(wc[k]);
+                if (cost_out) cost_out[lo + t] = wc[k];
+            }
         }
     }
     __syncthreads();

@@ -74,19 +74,19 @@ def _order_runs(order, n):
 
 
 def _expected_bounds(cost, n, cap, tile=None):
-    """The chunked order's run boundaries restated: bnd[k] the first tile
-    whose predecessors cost at least floor(total k / 8), clamped so that every
-    run holds at most cap tiles (tile costs: the wave pairs summed, or
-    `tile`)."""
+    """The chunked order's run boundaries restated: with each tile's cost (the
+    wave pairs summed, or `tile`) in units of 16 ticks capped at 4095, bnd[k]
+    the first tile whose predecessors cost at least floor(total k / 8),
+    clamped so that every run holds at most cap tiles."""
     if tile is None:
         tile = cost.reshape(-1, 2).astype(np.uint64).sum(1)
-    tile = np.asarray(tile, dtype=np.uint64)
-    csum = np.concatenate([[0], np.cumsum(tile)])
+    tile = np.minimum(np.asarray(tile, dtype=np.uint64) >> np.uint64(4), np.uint64(4095))
+    csum = np.concatenate([np.zeros(1, np.uint64), np.cumsum(tile, dtype=np.uint64)])
     total = int(csum[-1])
     bnd = [0]
     for k in range(1, 8):
         mark = total * k // 8
-        j = int(np.searchsorted(csum, mark, side="left"))
+        j = int(np.searchsorted(csum, np.uint64(mark), side="left"))
         lo = max(bnd[-1], n - (8 - k) * cap)
         bnd.append(min(max(j, lo), bnd[-1] + cap))
     return bnd + [n]
