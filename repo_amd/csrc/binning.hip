@@ -906,25 +906,16 @@ constexpr int kScanItems = 4;
 constexpr int kScanItemsLarge = 16;
 constexpr int kScanChunk = kScanThreads * kScanItems;
 
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x, int lane) {
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const uint32_t y = __shfl_up(x, off, kWave);
-        if (lane >= off) x += y;
-    }
-    return x;
-}
-
 // Exclusive scan of one value per thread over a 1024-thread block; returns the
 // block total in *total.
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* sh, uint32_t* total) {
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const uint32_t incl = wave_incl_scan(v, lane);
+    const uint32_t incl = wave_incl_scan_u32(v);
     if (lane == kWave - 1) sh[w] = incl;
     __syncthreads();
     if (w == 0) {
         const uint32_t x = lane < (kScanThreads / kWave) ? sh[lane] : 0u;
-        const uint32_t xi = wave_incl_scan(x, lane);
+        const uint32_t xi = wave_incl_scan_u32(x);
         if (lane < (kScanThreads / kWave)) sh[lane] = xi - x;
         if (lane == kWave - 1) sh[kScanThreads / kWave] = xi;
     }
@@ -1449,7 +1440,7 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_counts(
     }
     __syncthreads();
     if (w == 0) {
-        const uint32_t n = (uint32_t)wave_incl_scan((uint32_t)diff[lane], lane);
+        const uint32_t n = wave_incl_scan_u32((uint32_t)diff[lane]);
         const bool tile_ok = lp.sx0 + lane < lp.sx1;
         const size_t tiles = (size_t)tbx * tby;
         if (tile_ok) tile_count[lp.slab * tiles + (size_t)lp.ty * tbx + lp.sx0 + lane] = n;
@@ -1519,7 +1510,7 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
                 seg_first += f[k];
             }
         }
-        const uint32_t start = seg_first + wave_incl_scan(n, lane) - n;
+        const uint32_t start = seg_first + wave_incl_scan_u32(n) - n;
         tile_start[lane] = start + n_before;
         if (lp.slab == 0 && tile_ok) {
             // tile_bins.py:10-43: [start, end) per tile, (0, 0) when empty.
