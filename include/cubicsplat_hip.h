@@ -213,8 +213,9 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
 /* Tiles: every raster entry point takes the tile size block_x x block_y of
  * the binning whose tile_bins it reads (ops/cubic_splatting.py:2778-2782);
  * both must be positive multiples of 16 with (block_x / 16) * (block_y / 16)
- * <= 16 (other sizes: the _any_tile entry points below).  The raster runs one workgroup of two waves (16 x 8 pixels each) per
- * 16 x 16 sub-block of the image; the 2 (block_x / 16) (block_y / 16) waves
+ * <= 16 (other sizes: the _any_tile entry points below).  The raster runs
+ * one workgroup of two waves (16 x 8 pixels each) per 16 x 16 sub-block of
+ * the image; the 2 (block_x / 16) (block_y / 16) waves
  * of a tile all walk its list, and S = ceil(W / 16) * ceil(H / 16) counts the
  * sub-blocks.
  * Scheduling (no reference counterpart; it changes no result).  Every raster
