@@ -60,6 +60,10 @@ def parse():
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the run, copy a buffer of this size three times (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--next-rows", action="store_true",
+                    help="instead of the training step, time the components either side of "
+                         "the path (ring conversion, Adan, contribution outputs, the Gaussian "
+                         "renderer, de Casteljau flattening) and print them as one JSON line")
     return ap.parse_args()
 
 
@@ -404,8 +408,159 @@ def copy_calibration(mib):
     torch.cuda.synchronize()
 
 
+def _events_ms(fn, iters, warm=3):
+    """Mean device ms of fn() over iters calls (HIP events on the current
+    stream, after warm untimed calls)."""
+    import torch
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def next_rows(iters=50):
+    """Times of the components either side of the path, each on a stated
+    synthetic workload (ms per call by HIP events, HBM GB/s where the bytes
+    are plain): the closed-ring -> Hermite cubic conversion forward and
+    backward, Adan against Adam on config 3's parameters, the cubic raster
+    backward with and without the contribution outputs, the 2D Gaussian
+    renderer, and config 3 rendered with de Casteljau against uniform
+    flattening."""
+    import torch
+    import manbo
+    from repo_amd import gaussian as G
+    from repo_amd import optim, profiling, rings, splat, synth, _native
+    rows = {}
+    g = torch.Generator(device="cuda").manual_seed(7)
+
+    # Ring conversion: train.py's cubic_fill model (K = 10 control points,
+    # subdiv 4: 8 cubics per path) for config 3's 4096 paths.
+    n, k = 4096, 10
+    th = torch.linspace(0.0, 6.283185307179586, k + 1, device="cuda")[:k]
+    cen = torch.rand((n, 1, 2), generator=g, device="cuda") * 1.6 - 0.8
+    rad = torch.rand((n, 1, 1), generator=g, device="cuda") * 0.1 + 0.01
+    cp = (cen + rad * torch.stack([th.cos(), th.sin()], -1)[None]).contiguous()
+    cp.requires_grad_(True)
+    segs, _ = rings.closed_cubic_fill_segments_tilelang(cp, subdiv=4)
+    gseg = torch.randn(segs.shape, generator=g, device="cuda")
+    fwd = _events_ms(lambda: rings.closed_cubic_fill_segments_tilelang(cp, subdiv=4), iters)
+
+    def ring_fwd_bwd():
+        s_, _ = rings.closed_cubic_fill_segments_tilelang(cp, subdiv=4)
+        torch.autograd.grad(s_, cp, gseg)
+    both = _events_ms(ring_fwd_bwd, iters)
+    b_cp, b_seg = cp.numel() * 4, segs.numel() * 4
+    rows["f1_rings"] = {
+        "workload": f"{n} closed rings, K={k}, subdiv 4 -> {segs.shape[0]} cubics",
+        "fwd_ms": round(fwd, 4), "bwd_ms": round(both - fwd, 4),
+        "fwd_GBs": round((b_cp + b_seg) / fwd / 1e6, 1),
+        "bwd_GBs": round((b_cp + b_seg) / max(both - fwd, 1e-6) / 1e6, 1)}
+
+    # Optimizers on config 3's parameters (control points and colours).
+    sc = synth.make_scene(3).to("cuda")
+    params = [sc.cubics_norm.clone().requires_grad_(True), sc.colors.clone().requires_grad_(True)]
+    for prm in params:
+        prm.grad = torch.randn(prm.shape, generator=g, device="cuda") * 1e-3
+    nparam = sum(prm.numel() for prm in params)
+    times = {}
+    for name, cls in (("adam", optim.Adam), ("adan", optim.Adan)):
+        opt = cls(params, lr=1e-3)
+        times[name] = _events_ms(opt.step, iters)
+    rows["f2_optimizers"] = {
+        "workload": f"config 3 parameters ({nparam} floats)",
+        "adam_ms": round(times["adam"], 4), "adan_ms": round(times["adan"], 4),
+        "adam_GBs": round(28 * nparam / times["adam"] / 1e6, 1),
+        "adan_GBs": round(40 * nparam / times["adan"] / 1e6, 1)}
+
+    # Contribution outputs: the cubic raster backward at config 3 with and
+    # without curve_contrib_rgb / curve_isect_contrib.
+    widths = torch.clamp(sc.aa_widths.float(), min=1e-4).contiguous()
+    b = splat.bin_primitives(sc.cubics_norm.contiguous(), sc.seg_offsets.to(torch.int32).contiguous(),
+                             sc.colors.contiguous(), sc.opacities, sc.depths,
+                             sc.fill_rules.to(torch.int32).contiguous(), widths, None, sc.img_h,
+                             sc.img_w, sc.S)
+    img, T, idx = splat.rasterize_forward(b, sc.background)
+    v = torch.randn(img.shape, generator=g, device="cuda") * 1e-3
+    crgb = torch.zeros_like(sc.colors)
+    cis = torch.zeros((b.num_intersects,), dtype=torch.float32, device="cuda")
+    plain = _events_ms(lambda: splat.rasterize_backward(b, sc.background, T, idx, v), iters)
+    contrib = _events_ms(lambda: splat.rasterize_backward(
+        b, sc.background, T, idx, v, curve_contrib_rgb=crgb, curve_isect_contrib=cis), iters)
+    rows["f2_contribution_outputs"] = {
+        "workload": "config 3 raster backward (fresh zeroed accumulators per call)",
+        "bwd_ms": round(plain, 4), "bwd_with_contrib_ms": round(contrib, 4)}
+
+    # 2D Gaussian renderer: 100k Gaussians at 1024 x 1024, 16 x 16 tiles.
+    ng, H, W = 100000, 1024, 1024
+    u = lambda *sh: torch.rand(sh, generator=g, device="cuda")  # noqa: E731
+    means, scales = u(ng, 2) * 2 - 1, 0.5 + u(ng, 2) * 5.5
+    rot, colors, opac = (u(ng) * 2 - 1) * 4.0, u(ng, 3), 0.05 + u(ng) * 0.95
+    bg = torch.tensor([0.5, 0.5, 0.5], device="cuda")
+    proj = _events_ms(lambda: G.project_forward(means, scales, rot, H, W, 16, 16), iters)
+    xys, depths, radii, conics, _ = G.project_forward(means, scales, rot, H, W, 16, 16)
+    binning = _events_ms(lambda: G.bin_gaussians(xys, conics, radii, depths, H, W, 16, 16), iters)
+    gb = G.bin_gaussians(xys, conics, radii, depths, H, W, 16, 16)
+    rec = G.pack_records(xys, conics, colors, opac)
+    rf = _events_ms(lambda: G.rasterize_forward(gb.gaussian_ids_sorted, gb.tile_bins, rec, bg, H,
+                                                W, 16, 16), iters)
+    out, fT, fi = G.rasterize_forward(gb.gaussian_ids_sorted, gb.tile_bins, rec, bg, H, W, 16, 16)
+    vg = torch.randn(out.shape, generator=g, device="cuda") * 1e-3
+    rb = _events_ms(lambda: G.rasterize_backward(gb.gaussian_ids_sorted, gb.tile_bins, rec, bg, H,
+                                                 W, 16, 16, fT, fi, vg), iters)
+    ins = [t.clone().requires_grad_(True) for t in (means, scales, rot, colors, opac)]
+
+    def gs_step():
+        o = manbo.gs_render(*ins, H, W, 16, 16, bg)
+        o.backward(vg)
+    step = _events_ms(gs_step, iters)
+    rows["f3_gaussian_renderer"] = {
+        "workload": f"{ng} Gaussians, {W}x{H}, 16x16 tiles, {int(gb.num_intersects)} intersections",
+        "project_ms": round(proj, 4), "binning_ms": round(binning, 4),
+        "raster_fwd_ms": round(rf, 4), "raster_bwd_ms": round(rb, 4),
+        "render_fwd_bwd_ms": round(step, 4)}
+
+    # de Casteljau against uniform flattening: config 3's render forward and
+    # backward through the reference entry point, per-stage device times.
+    cub = sc.cubics_norm.clone().requires_grad_(True)
+    col = sc.colors.clone().requires_grad_(True)
+    vimg = torch.randn((sc.img_h, sc.img_w, 3), generator=g, device="cuda") * 1e-3
+    for method in ("bernstein", "de_casteljau"):
+        def render_step():
+            o = manbo.ops.render_cubic_fill_splat_tilelang(
+                cub, sc.seg_offsets, col, sc.opacities, sc.depths, sc.img_h, sc.img_w, 16, 16,
+                sc.background, aa_widths=sc.aa_widths, distance_samples=sc.S,
+                flatten_method=method)
+            o.backward(vimg)
+        total = _events_ms(render_step, iters)
+        timer = profiling.EventTimer(STEP_LABELS, reserve=iters + 1)
+        _native.set_profile_ctx_factory(timer)
+        for _ in range(iters):
+            render_step()
+        torch.cuda.synchronize()
+        _native.set_profile_ctx_factory(None)
+        stages = {STEP_LABELS[lab]: round(timer.mean_ms(lab), 4) for lab in STEP_LABELS
+                  if timer.count(lab)}
+        timer.close()
+        rows.setdefault("f4_de_casteljau", {"workload": "config 3 render forward + backward"})
+        rows["f4_de_casteljau"][method] = {"fwd_bwd_ms": round(total, 4), "stages_ms": stages}
+    return rows
+
+
 def main():
     args = parse()
+    if args.next_rows:
+        if args.gpus != 1:
+            sys.exit(2)
+        print(json.dumps({"next_rows": next_rows(), "n_gpus": 1, "data": "synthetic"}),
+              flush=True)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only (several GPUs would each "
                                    "own a band of tile rows; not implemented here)",
