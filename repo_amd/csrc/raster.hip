@@ -543,7 +543,12 @@ __device__ __forceinline__ int32_t log_reserve(uint32_t* __restrict__ ctr, uint3
     if (c.full) return kLogMissing;
     if (c.p + units > c.e) {
         uint32_t base = 0;
-        if ((threadIdx.x & (kWave - 1)) == 0) base = first + atomicAdd(ctr, kLogBlockUnits);
+        // An opaque copy of the lane index, so that the comparison is made
+        // here rather than kept as a 64-bit lane mask in scalar registers for
+        // the whole list walk (the forward has none to spare).
+        int lane_o = (int)(threadIdx.x & (kWave - 1));
+        asm volatile("" : "+v"(lane_o));
+        if (lane_o == 0) base = first + atomicAdd(ctr, kLogBlockUnits);
         base = __builtin_amdgcn_readfirstlane(base);
         if ((uint64_t)base + kLogBlockUnits > cap_units) {
             c.full = true;
@@ -640,18 +645,36 @@ __device__ __forceinline__ PrimRec load_prim_fwd(cptr<PrimRec> prims, int pid) {
 // once per row.  Eight waves per SIMD (the register budget that allows; a
 // few scalar values then live in vector-register lanes): the edge walks wait
 // on scalar loads, and more waves hide more of that wait.
-template <int MODE, bool COUNT>
+// The forward's arguments that only its last instructions use (the image,
+// T, index, wave cost and counter outputs).  The kernel takes them as its
+// first argument, which the kernel-argument segment holds at offset 0, and
+// reads them at the end through the segment pointer, so they hold no scalar
+// registers during the list walk: at eight waves per SIMD a wave has 78 of
+// them, and values that do not fit are kept in vector-register lanes, each
+// reload a vector instruction.  LOG (the kernel's other specialization):
+// the raster log is written, without a null test per entry.
+struct FwdTail {
+    const float* bg;
+    float* out;
+    float* out_planes;
+    float* final_T;
+    int32_t* final_idx;
+    uint32_t* wave_cost;
+    unsigned long long* counts;
+    int out_planar;
+    int img_h, img_w;
+};
+typedef const __attribute__((address_space(4))) FwdTail* KernargTail;
+
+template <int MODE, bool COUNT, bool LOG>
 __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(8))) void k_raster_fwd(
-    const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
+    FwdTail tail_arg, const int32_t* __restrict__ prim_ids_g, const int32_t* __restrict__ bins,
     const EdgeRec* __restrict__ edges_g, const EdgeCull* __restrict__ culls,
-    const PrimRec* __restrict__ prims_g, const float* __restrict__ bg, int img_h, int img_w,
+    const PrimRec* __restrict__ prims_g, int img_h, int img_w,
     TileGrid tg, const int32_t* __restrict__ tile_order,
-    uint32_t* __restrict__ wave_cost, float* __restrict__ out, int out_planar,
-    float* __restrict__ out_planes, float* __restrict__ final_T,
-    int32_t* __restrict__ final_idx,
     int32_t* __restrict__ log_index, uint4* __restrict__ log_pool, uint32_t* __restrict__ log_ctr,
-    uint32_t log_first, uint32_t log_units,
-    uint32_t log_per_entry, unsigned long long* __restrict__ counts) {
+    uint32_t log_first, uint32_t log_units, uint32_t log_per_entry) {
+    (void)tail_arg;
     const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -744,7 +767,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
                     inside_all = (wnd & rule_mask(pr)) != 0;
                     if constexpr (COUNT) n.row += (uint64_t)(pr.e1 - pr.e0);
                 }
-                if (log_index) {
+                if (LOG) {
                     idx_l = lane == k ? (inside_all ? kLogInside : kLogEmpty) : idx_l;
                     logged |= 1ull << k;
                 }
@@ -768,7 +791,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
                 if ((in0 | in1 | x0 | x1) == 0) {
                     // No pixel inside or within the exact distance: every
                     // coverage is 0 and the entry changes nothing.
-                    if (log_index) {
+                    if (LOG) {
                         idx_l = lane == k ? kLogEmpty : idx_l;
                         logged |= 1ull << k;
                     }
@@ -813,7 +836,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
                 }
                 // The log record of this entry and wave: inside and exact bits, and
                 // each exact pixel's best edge and coverage, for the backward.
-                if (log_index) {
+                if (LOG) {
                     const uint32_t units = kLogHeaderUnits + (uint32_t)((nx + 1) >> 1);
                     if (st.n + units > kLogStageUnits) log_flush(log_pool, stage, st);
                     const int32_t at = log_reserve(log_ctr, log_first, log_units, lc, units);
@@ -824,7 +847,9 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
                         }
                         uint4* rec = stage + st.n;
                         st.n += units;
-                        if (lane == 0) {
+                        int lane_o = lane;   // compared here, as in log_reserve
+                        asm volatile("" : "+v"(lane_o));
+                        if (lane_o == 0) {
                             rec[0] = make_uint4((uint32_t)in0, (uint32_t)(in0 >> 32),
                                                 (uint32_t)in1, (uint32_t)(in1 >> 32));
                             rec[1] = make_uint4((uint32_t)x0, (uint32_t)(x0 >> 32), (uint32_t)x1,
@@ -854,14 +879,23 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
         if ((logged >> lane) & 1u)
             __builtin_nontemporal_store(idx_l, log_index + (size_t)tg.waves * gl + sb.slot);
     }
-    if (log_index) log_flush(log_pool, stage, st);
+    if (LOG) log_flush(log_pool, stage, st);
+    const KernargTail kt = (KernargTail)__builtin_amdgcn_kernarg_segment_ptr();
+    const float* const bg = kt->bg;
+    float* const out = kt->out;
+    float* const out_planes = kt->out_planes;
+    float* const final_T = kt->final_T;
+    int32_t* const final_idx = kt->final_idx;
+    const int out_planar = kt->out_planar;
+    img_h = kt->img_h;
+    img_w = kt->img_w;
     // The image as [H, W, 3], or as three [H, W] planes (out_planar), and
     // optionally also as three planes at out_planes.
     const size_t np = (size_t)img_h * img_w;
     const size_t ch = out_planar ? np : 1;
 #pragma unroll
     for (int p = 0; p < kPix; ++p) {
-        if (!L.in_img[p]) continue;
+        if (!((L.i[p] < img_h) & (L.j < img_w))) continue;
         const size_t pix = (size_t)L.i[p] * img_w + L.j;
         __builtin_nontemporal_store(T[p], final_T + pix);
         __builtin_nontemporal_store(cur[p], final_idx + pix);
@@ -878,8 +912,8 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             out_planes[2 * np + pix] = o2;
         }
     }
-    if constexpr (COUNT) flush_counts(n, counts);
-    record_wave_cost(wave_cost, sb.index, t_start);
+    if constexpr (COUNT) flush_counts(n, kt->counts);
+    record_wave_cost(kt->wave_cost, sb.index, t_start);
 }
 
 // First unit of the log pool: the counter of the shared blocks, which start
@@ -1990,13 +2024,13 @@ static unsigned raster_groups(const RasterArgs& a) {
 
 template <int MODE, bool COUNT>
 static void launch_fwd(const RasterArgs& a) {
-    hipLaunchKernelGGL((k_raster_fwd<MODE, COUNT>), dim3(raster_groups(a)), dim3(kRasterThreads), 0,
-                       a.stream, a.ids, a.bins, a.E, a.C, a.P, a.bg, a.img_h, a.img_w, a.tg,
-                       a.order, a.wave_cost, a.out, a.out_planar, a.out_planes, a.final_T,
-                       a.final_idx,
-                       a.log_index,
-                       a.log_pool, a.log_ctr, a.log_first, a.log_units, a.log_per_entry,
-                       a.counts);
+    const FwdTail tail{a.bg,        a.out,    a.out_planes, a.final_T, a.final_idx,
+                       a.wave_cost, a.counts, a.out_planar, a.img_h,   a.img_w};
+    auto kern = a.log_index ? k_raster_fwd<MODE, COUNT, true> : k_raster_fwd<MODE, COUNT, false>;
+    hipLaunchKernelGGL(kern, dim3(raster_groups(a)), dim3(kRasterThreads), 0,
+                       a.stream, tail, a.ids, a.bins, a.E, a.C, a.P, a.img_h, a.img_w, a.tg,
+                       a.order, a.log_index, a.log_pool, a.log_ctr, a.log_first, a.log_units,
+                       a.log_per_entry);
 }
 
 template <int MODE, bool COUNT, bool ADAPTIVE, bool LEAN>
