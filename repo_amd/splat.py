@@ -482,10 +482,11 @@ _ORDER_AGE: "dict[tuple, int]" = {}   # forwards since the order was made
 _TILE_COSTS: "dict[tuple, tuple]" = {}
 _MAX_ORDERS = 16
 # A new heavy-first order is made from every ORDER_EVERY-th forward's wave
-# durations (a tile's cost changes slowly between training steps); the
-# forwards in between reuse it and record no durations.  Any order gives the
-# same results.
-ORDER_EVERY = 4
+# durations (a tile's cost changes slowly between training steps: every 4th
+# and every 8th forward gave the same raster times, and the ordering launch
+# costs the step it runs in about 16 us at config 3); the forwards in between
+# reuse it and record no durations.  Any order gives the same results.
+ORDER_EVERY = 8
 # Sort within each XCD's contiguous tile range (keeps each XCD's L2 on its own
 # part of the image) rather than across all tiles.
 ORDER_CHUNKED = True
