@@ -184,21 +184,19 @@ __device__ __forceinline__ float clamp_if(float v, float lo, float hi) {
     return CLAMP ? __builtin_amdgcn_fmed3f(v, lo, hi) : v;
 }
 
-// Loads plane[gy][gx0 .. gx0 + N) of an image with h rows of w valid columns
-// stored with row stride ld (zero outside; with CLAMP the values inside are
-// clamped to [lo, hi], the zeros outside are not).  When rows are 16-byte
-// aligned (vec_ok), gx0 - OFF is a multiple of 4 and the rounded-up strip lies
-// inside the row, it uses float4 loads starting OFF columns early.
+// Loads plane[gy][gx0 .. gx0 + N) of an image with w valid columns stored with
+// row stride ld, for a row gy inside the image (zero outside the columns; with
+// CLAMP the values inside are clamped to [lo, hi], the zeros outside are not).
+// The callers handle rows outside the image themselves (their results are
+// zero rows), so that the values loaded here need no zero defaults.  When rows
+// are 16-byte aligned (vec_ok), gx0 - OFF is a multiple of 4 and the
+// rounded-up strip lies inside the row, it uses float4 loads starting OFF
+// columns early.
 template <int N, int OFF, bool CLAMP = false>
-__device__ __forceinline__ void load_strip(const float* __restrict__ plane, int h, int w,
-                                           size_t ld, int gy, int gx0, bool vec_ok,
-                                           float (&dst)[N], float lo = 0.0f, float hi = 0.0f) {
+__device__ __forceinline__ void load_strip(const float* __restrict__ plane, int w, size_t ld,
+                                           int gy, int gx0, bool vec_ok, float (&dst)[N],
+                                           float lo = 0.0f, float hi = 0.0f) {
     constexpr int NV4 = (N + OFF + 3) / 4;
-    if (gy < 0 || gy >= h) {
-#pragma unroll
-        for (int k = 0; k < N; ++k) dst[k] = 0.0f;
-        return;
-    }
     const float* row = plane + (size_t)gy * ld;
     const int s0 = gx0 - OFF;
     if (vec_ok && s0 >= 0 && s0 + 4 * NV4 <= w) {
@@ -327,9 +325,21 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
     // Horizontal: thread -> (row, 8-wide strip).
     for (int item = threadIdx.x; item < IT * (kSsimTW / kHStrip); item += 256) {
         const int r = item >> 2, q0 = (item & 3) * kHStrip;
+        if (oy0 + r >= h) {
+            // Input rows past the image (the last tile row's windows): only
+            // output rows past the valid map read them.
+#pragma unroll
+            for (int o = 0; o < kHStrip; ++o) {
+                hm[0][r][q0 + o] = 0.0f;
+                hm[1][r][q0 + o] = 0.0f;
+                hm[2][r][q0 + o] = 0.0f;
+                hm[3][r][q0 + o] = 0.0f;
+            }
+            continue;
+        }
         float a[NIN], b[NIN];
-        load_strip<NIN, 0, CLAMP>(xc, h, w, w, oy0 + r, ox0 + q0, vec_ok, a, lo, hi);
-        load_strip<NIN, 0>(yc, h, w, w, oy0 + r, ox0 + q0, vec_ok, b);
+        load_strip<NIN, 0, CLAMP>(xc, w, w, oy0 + r, ox0 + q0, vec_ok, a, lo, hi);
+        load_strip<NIN, 0>(yc, w, w, oy0 + r, ox0 + q0, vec_ok, b);
         if (mse_partials && r < mse_rows) {
             // The strip's own 8 columns; the last strip of the last tile
             // column also takes the inputs past them (to the end of its
@@ -459,10 +469,18 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
     for (int item = threadIdx.x; item < IT * (kSsimTW / kHStrip); item += 256) {
         const int r = item >> 2, q0 = (item & 3) * kHStrip;
         const int my = py0 - (WIN - 1) + r, mx0 = px0 - (WIN - 1) + q0;
+        if (my < 0 || my >= oh) {
+            // Map rows outside the map: the correlation's zero padding.
+#pragma unroll
+            for (int m = 0; m < 3; ++m)
+#pragma unroll
+                for (int o = 0; o < kHStrip; ++o) hs[m][r][q0 + o] = 0.0f;
+            continue;
+        }
 #pragma unroll
         for (int m = 0; m < 3; ++m) {
             float a[NIN];
-            load_strip<NIN, TT::BOFF>(abc + m * stride + (size_t)c * plane, oh, ow, ld, my, mx0,
+            load_strip<NIN, TT::BOFF>(abc + m * stride + (size_t)c * plane, ow, ld, my, mx0,
                                       vec_ok, a);
 #pragma unroll
             for (int o = 0; o < kHStrip; ++o) {
