@@ -184,39 +184,51 @@ __device__ __forceinline__ float clamp_if(float v, float lo, float hi) {
     return CLAMP ? __builtin_amdgcn_fmed3f(v, lo, hi) : v;
 }
 
-// Loads plane[gy][gx0 .. gx0 + N) of an image with w valid columns stored with
-// row stride ld, for a row gy inside the image (zero outside the columns; with
-// CLAMP the values inside are clamped to [lo, hi], the zeros outside are not).
+// Loads columns gx0 .. gx0 + N of M rows (rows[m], each of an image with w
+// valid columns and inside it: zero outside the columns; with CLAMP0 the
+// values of row 0 inside are clamped to [lo, hi], the zeros outside are not).
 // The callers handle rows outside the image themselves (their results are
-// zero rows), so that the values loaded here need no zero defaults.  When rows
-// are 16-byte aligned (vec_ok), gx0 - OFF is a multiple of 4 and the
-// rounded-up strip lies inside the row, it uses float4 loads starting OFF
-// columns early.
-template <int N, int OFF, bool CLAMP = false>
-__device__ __forceinline__ void load_strip(const float* __restrict__ plane, int w, size_t ld,
-                                           int gy, int gx0, bool vec_ok, float (&dst)[N],
-                                           float lo = 0.0f, float hi = 0.0f) {
+// zero rows), so that the values loaded here need no zero defaults.  When the
+// rows are 16-byte aligned (vec_ok), gx0 - OFF is a multiple of 4 and the
+// rounded-up strips lie inside the rows, it uses float4 loads starting OFF
+// columns early, every row's loads issued before the first is used (one
+// memory round trip for all of them).
+template <int M, int N, int OFF, bool CLAMP0 = false>
+__device__ __forceinline__ void load_strips(const float* const (&rows)[M], int w, int gx0,
+                                            bool vec_ok, float (&dst)[M][N], float lo = 0.0f,
+                                            float hi = 0.0f) {
     constexpr int NV4 = (N + OFF + 3) / 4;
-    const float* row = plane + (size_t)gy * ld;
     const int s0 = gx0 - OFF;
     if (vec_ok && s0 >= 0 && s0 + 4 * NV4 <= w) {
-        float t[4 * NV4];
+        float4 q[M][NV4];
 #pragma unroll
-        for (int v = 0; v < NV4; ++v) {
-            const float4 q = *reinterpret_cast<const float4*>(row + s0 + 4 * v);
-            t[4 * v] = q.x;
-            t[4 * v + 1] = q.y;
-            t[4 * v + 2] = q.z;
-            t[4 * v + 3] = q.w;
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int v = 0; v < NV4; ++v)
+                q[m][v] = *reinterpret_cast<const float4*>(rows[m] + s0 + 4 * v);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float t[4 * NV4];
+#pragma unroll
+            for (int v = 0; v < NV4; ++v) {
+                t[4 * v] = q[m][v].x;
+                t[4 * v + 1] = q[m][v].y;
+                t[4 * v + 2] = q[m][v].z;
+                t[4 * v + 3] = q[m][v].w;
+            }
+#pragma unroll
+            for (int k = 0; k < N; ++k)
+                dst[m][k] = m == 0 ? clamp_if<CLAMP0>(t[OFF + k], lo, hi) : t[OFF + k];
         }
-#pragma unroll
-        for (int k = 0; k < N; ++k) dst[k] = clamp_if<CLAMP>(t[OFF + k], lo, hi);
     } else {
 #pragma unroll
-        for (int k = 0; k < N; ++k) {
-            const int gx = gx0 + k;
-            dst[k] = (gx >= 0 && gx < w) ? clamp_if<CLAMP>(row[gx], lo, hi) : 0.0f;
-        }
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int k = 0; k < N; ++k) {
+                const int gx = gx0 + k;
+                const float v = (gx >= 0 && gx < w) ? rows[m][gx] : 0.0f;
+                dst[m][k] = (m == 0 && gx >= 0 && gx < w) ? clamp_if<CLAMP0>(v, lo, hi) : v;
+            }
     }
 }
 
@@ -337,9 +349,14 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
             }
             continue;
         }
-        float a[NIN], b[NIN];
-        load_strip<NIN, 0, CLAMP>(xc, w, w, oy0 + r, ox0 + q0, vec_ok, a, lo, hi);
-        load_strip<NIN, 0>(yc, w, w, oy0 + r, ox0 + q0, vec_ok, b);
+        float ab_in[2][NIN];
+        {
+            const size_t ro = (size_t)(oy0 + r) * w;
+            const float* const rows[2] = {xc + ro, yc + ro};
+            load_strips<2, NIN, 0, CLAMP>(rows, w, ox0 + q0, vec_ok, ab_in, lo, hi);
+        }
+        float (&a)[NIN] = ab_in[0];
+        float (&b)[NIN] = ab_in[1];
         if (mse_partials && r < mse_rows) {
             // The strip's own 8 columns; the last strip of the last tile
             // column also takes the inputs past them (to the end of its
@@ -477,16 +494,20 @@ __global__ __launch_bounds__(256) void k_ssim_bwd(const float* __restrict__ x,
                 for (int o = 0; o < kHStrip; ++o) hs[m][r][q0 + o] = 0.0f;
             continue;
         }
+        // One map at a time: loading the three strips together would take
+        // 60 more registers and cost this HBM-bound kernel a wave per SIMD
+        // (measured slower).
+        const float* const m0 = abc + (size_t)c * plane + (size_t)my * ld;
 #pragma unroll
         for (int m = 0; m < 3; ++m) {
-            float a[NIN];
-            load_strip<NIN, TT::BOFF>(abc + m * stride + (size_t)c * plane, ow, ld, my, mx0,
-                                      vec_ok, a);
+            float a1[1][NIN];
+            const float* const rows[1] = {m0 + m * stride};
+            load_strips<1, NIN, TT::BOFF>(rows, ow, mx0, vec_ok, a1);
 #pragma unroll
             for (int o = 0; o < kHStrip; ++o) {
                 float s = 0.0f;
 #pragma unroll
-                for (int k = 0; k < WIN; ++k) s = __builtin_fmaf(g[k], a[o + WIN - 1 - k], s);
+                for (int k = 0; k < WIN; ++k) s = __builtin_fmaf(g[k], a1[0][o + WIN - 1 - k], s);
                 hs[m][r][q0 + o] = s;
             }
         }
