@@ -447,16 +447,17 @@ __device__ __forceinline__ void record_wave_cost(uint32_t* __restrict__ wave_cos
 // Primitive-level cull of one lane's list entry (lane-parallel form of
 // prim_culled): the record's near rows and columns (and, for an open chain in
 // fill mode, its crossing rows and last vertex column) read with vector loads.
+// All three loads are issued before any test, so that they take one memory
+// round trip (a test between them would make each wait for the one before).
 template <int MODE>
 __device__ __forceinline__ bool prim_culled_lane(const PrimRec* __restrict__ p,
                                                  const WaveRect& W) {
     const int4 a = *reinterpret_cast<const int4*>(&p->ny_lo);  // ny_lo ny_span cy_lo cy_span
     const int4 b = *reinterpret_cast<const int4*>(&p->nx_lo);  // nx_lo nx_span x_last -
-    if (span_hits(a.x, a.y, W.r1) && span_hits(b.x, b.y, W.c1)) return false;
-    if (MODE == 1) return true;
-    const int4 c = *reinterpret_cast<const int4*>(&p->e0);     // e0 e1 rule closed
-    if (c.w) return true;
-    return !span_hits(a.z, a.w, W.r1) || W.c0 > b.z;
+    const int closed = MODE == 1 ? 1 : p->closed;
+    const bool near = span_hits(a.x, a.y, W.r1) & span_hits(b.x, b.y, W.c1);
+    if (MODE == 1) return !near;
+    return !near & ((closed != 0) | !span_hits(a.z, a.w, W.r1) | (W.c0 > b.z));
 }
 
 // Winding number at the pixel row r of a wave over the edges c + lane < e1 of
@@ -1154,9 +1155,12 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
       // the record's header, so that no entry waits for them.  Every entry at
       // or below gstart that passes the cull was processed by the forward,
       // so its index is written; the others are not read.
+      // The entry's log index is loaded beside its cull fields (one round
+      // trip for both) and kept only for entries that pass the cull.
+      const int32_t at_ld = (in_list && log_index_g)
+                                ? log_index_g[(size_t)tg.waves * gl + sb.slot] : kLogMissing;
       const bool kept = in_list && !prim_culled_lane<MODE>(prims_g + pid_l, W);
-      const int32_t at_l = (kept && log_index_g) ? log_index_g[(size_t)tg.waves * gl + sb.slot]
-                                                 : kLogMissing;
+      const int32_t at_l = kept ? at_ld : kLogMissing;
       uint4 ha = make_uint4(0u, 0u, 0u, 0u), hb = ha;
       if (at_l >= 0) {
           ha = log_pool[at_l];
