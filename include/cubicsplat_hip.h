@@ -488,6 +488,26 @@ int cs_backward_finalize(const float* v_cubics_px, int32_t nseg, int32_t img_h, 
                          const float* widths, const float* v_inv_sigma2s, int32_t nprim,
                          float* v_cubics_norm, float* v_aa_widths, hipStream_t stream);
 
+/* cs_rasterize_backward (with prim_scratch, no contribution outputs) followed
+ * by cs_backward_finalize (ops/cubic_splatting.py:1197-1651, then
+ * :3096-3104), with the per-XCD copies' reduction and the epilogue in one
+ * launch: v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths receive the
+ * copies' sums as with cs_rasterize_backward, v_cubics_px the control-point
+ * gradients, and v_cubics_norm [nseg,4,2] / v_aa_widths [P] what
+ * cs_backward_finalize computes from them (widths: the aa widths, clamped to
+ * 1e-4 inside).  For callers with nothing to run between the two (the
+ * reference's process_fn hook post_backward_rasterize absent); the results
+ * equal the two calls'. */
+int cs_rasterize_backward_finalized(
+    int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
+    const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
+    int32_t img_w, int32_t block_x, int32_t block_y, int32_t edges_per_segment,
+    const float* final_Ts, const int32_t* final_idx, const int32_t* log_index,
+    const void* log_pool, const float* v_output, int32_t v_output_planar, float* v_cubics_px,
+    float* v_colors, float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
+    int32_t nprim, float* prim_scratch, const int32_t* tile_order, int32_t nseg,
+    const float* widths, float* v_cubics_norm, float* v_aa_widths, hipStream_t stream);
+
 /* ---------------- closed rings -> cubic segments ---------------- */
 
 /* closed_cubic_fill_segments_forward_kernel (ops/cubic_splatting.py:137-268):

@@ -95,6 +95,10 @@ _SIGNATURES = {
     "cs_accumulate_edge_grads_csr": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P,
                                                     _P]),
     "cs_backward_finalize": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P]),
+    "cs_rasterize_backward_finalized": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32,
+                                                       _I32, _I32, _I32, _P, _P, _P, _P, _P,
+                                                       _I32, _P, _P, _P, _P, _P, _I32, _P, _P,
+                                                       _I32, _P, _P, _P, _P]),
     "cs_mse_partials_elems": (_SZ, [_I64]),
     "cs_ssim_partials_elems": (_SZ, [_I32, _I32, _I32]),
     "cs_ssim_abc_elems": (_SZ, [_I32, _I32, _I32, _I32]),

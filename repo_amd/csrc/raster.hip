@@ -1028,6 +1028,39 @@ __global__ __launch_bounds__(256) void k_prim_rep_reduce(float* __restrict__ rep
     *dst += sum;
 }
 
+// k_prim_rep_reduce and k_finalize in one launch, for a backward whose
+// per-primitive gradients go straight to the epilogue (no hook between them):
+// thread t < nprim adds primitive t's copies into the caller's arrays (the
+// same sums as k_prim_rep_reduce), clears them and takes v_aa[t] from the
+// final v_is2[t] (the expression of k_finalize); thread t < 8 nseg scales
+// v_px[t] into v_norm[t].
+template <int NV>
+__global__ __launch_bounds__(256) void k_prim_rep_finalize(
+    float* __restrict__ rep, int nprim, float* __restrict__ v_col, float* __restrict__ v_op,
+    float* __restrict__ v_is2, float* __restrict__ v_sw, const float* __restrict__ v_px,
+    int nseg, float half_w, float half_h, const float* __restrict__ widths,
+    float* __restrict__ v_norm, float* __restrict__ v_aa) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < (int64_t)nseg * 8) v_norm[t] = v_px[t] * ((t & 1) ? half_h : half_w);
+    if (t >= nprim) return;
+    const int p = (int)t;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const int64_t i = (int64_t)p * NV + v;
+        float sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kGradReplicas; ++r) {
+            float* q = rep + (int64_t)r * nprim * NV + i;
+            sum += *q;
+            *q = 0.0f;
+        }
+        float* dst = v < 3 ? v_col + 3 * p + v : v == 3 ? v_op + p : v == 4 ? v_is2 + p : v_sw + p;
+        *dst += sum;
+    }
+    const float w = fmaxf(widths[p], kWidthMin);
+    v_aa[p] = (-2.0f * v_is2[p]) / fmaxf(w * w * w, (float)1e-12);
+}
+
 struct GradBuf {
     GradRec* rec;
     uint32_t n;   // wave-uniform
@@ -2012,6 +2045,10 @@ struct RasterArgs {
     float *v_cub, *v_col, *v_op, *v_is2, *v_sw, *c_rgb, *c_isect;
     float* prim_rep;  // per-primitive gradient copies (NULL: direct atomics)
     int nprim;
+    // backward epilogue fused with the copies' reduction (NULL: none)
+    const float* fin_widths;
+    float *fin_norm, *fin_aa;
+    int nseg;
     // evaluation counters of the counting entry points
     unsigned long long* counts;
     // heavy-first tile order (NULL: XCD order) and per-wave costs out (NULL: none)
@@ -2050,7 +2087,14 @@ static void launch_bwd4(const RasterArgs& a) {
                        a.v_cub, a.v_col,
                        a.v_op, a.v_is2, a.v_sw, a.c_rgb, a.c_isect, a.prim_rep, a.nprim,
                        a.counts);
-    if (a.prim_rep) {
+    if (a.prim_rep && a.fin_norm) {
+        constexpr int NV = MODE == 1 ? 6 : 5;
+        const int64_t n = (int64_t)a.nseg * 8 > a.nprim ? (int64_t)a.nseg * 8 : a.nprim;
+        const float half_w = (float)(0.5 * (double)a.img_w), half_h = (float)(0.5 * (double)a.img_h);
+        hipLaunchKernelGGL(k_prim_rep_finalize<NV>, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                           0, a.stream, a.prim_rep, a.nprim, a.v_col, a.v_op, a.v_is2, a.v_sw,
+                           a.v_cub, a.nseg, half_w, half_h, a.fin_widths, a.fin_norm, a.fin_aa);
+    } else if (a.prim_rep) {
         constexpr int NV = MODE == 1 ? 6 : 5;
         const int64_t n = (int64_t)a.nprim * NV;
         hipLaunchKernelGGL(k_prim_rep_reduce<NV>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
@@ -2235,7 +2279,9 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
                               const void* edge_aux, const int32_t* log_index,
                               const void* log_pool, unsigned long long* eval_counts,
                               int32_t nprim, float* prim_scratch,
-                              const int32_t* tile_order, hipStream_t stream) {
+                              const int32_t* tile_order, hipStream_t stream,
+                              int32_t nseg = 0, const float* fin_widths = nullptr,
+                              float* fin_norm = nullptr, float* fin_aa = nullptr) {
     TileGrid tg;
     if ((mode != 0 && mode != 1) || (edge_aux == nullptr && edges_per_segment < 1) ||
         !tile_grid(img_h, img_w, block_x, block_y, tg))
@@ -2265,6 +2311,10 @@ static int rasterize_backward(int32_t mode, const int32_t* prim_ids_sorted,
     a.order = tile_order;
     a.prim_rep = prim_scratch;
     a.nprim = prim_scratch ? nprim : 0;
+    a.nseg = nseg;
+    a.fin_widths = fin_widths;
+    a.fin_norm = fin_norm;
+    a.fin_aa = fin_aa;
     if (eval_counts) launch_bwd_mode<true>(a);
     else launch_bwd_mode<false>(a);
     return raster_status();
@@ -2296,6 +2346,25 @@ extern "C" int cs_rasterize_backward(int32_t mode, const int32_t* prim_ids_sorte
                               v_inv_sigma2s, v_stroke_widths, curve_contrib_rgb,
                               curve_isect_contrib, nullptr, log_index, log_pool, nullptr, nprim,
                               prim_scratch, tile_order, stream);
+}
+
+extern "C" int cs_rasterize_backward_finalized(
+    int32_t mode, const int32_t* prim_ids_sorted, const int32_t* tile_bins, const void* edges,
+    const void* edge_culls, const void* prim_recs, const float* background, int32_t img_h,
+    int32_t img_w, int32_t block_x, int32_t block_y, int32_t edges_per_segment,
+    const float* final_Ts, const int32_t* final_idx, const int32_t* log_index,
+    const void* log_pool, const float* v_output, int32_t v_output_planar, float* v_cubics_px,
+    float* v_colors, float* v_opacities, float* v_inv_sigma2s, float* v_stroke_widths,
+    int32_t nprim, float* prim_scratch, const int32_t* tile_order, int32_t nseg,
+    const float* widths, float* v_cubics_norm, float* v_aa_widths, hipStream_t stream) {
+    if (!prim_scratch || nseg < 0 || !widths || !v_cubics_norm || !v_aa_widths)
+        return CS_ERR_ARGS;
+    return rasterize_backward(mode, prim_ids_sorted, tile_bins, edges, edge_culls, prim_recs,
+                              background, img_h, img_w, block_x, block_y, edges_per_segment,
+                              final_Ts, final_idx, v_output, v_output_planar, v_cubics_px,
+                              v_colors, v_opacities, v_inv_sigma2s, v_stroke_widths, nullptr,
+                              nullptr, nullptr, log_index, log_pool, nullptr, nprim, prim_scratch,
+                              tile_order, stream, nseg, widths, v_cubics_norm, v_aa_widths);
 }
 
 extern "C" int cs_rasterize_backward_de_casteljau(

@@ -815,6 +815,44 @@ def rasterize_backward(b: Binned, background, final_T, final_idx, v_output, *,
     return v_px, v_colors, v_opac, v_is2, v_sw
 
 
+def rasterize_backward_finalized(b: Binned, background, final_T, final_idx, v_output, widths):
+    """rasterize_backward followed by backward_finalize, with the per-XCD
+    copies' reduction and the epilogue in one launch
+    (cs_rasterize_backward_finalized): returns (v_cubics_norm [nseg,4,2],
+    v_colors [P,3], v_opacities [P], v_aa_widths [P], v_stroke_widths [P] or
+    None), the values of the two calls.  Uniform flattening and 16 x 16
+    sub-block tiles (the other backward kernels keep the two calls)."""
+    dev = b.device
+    P = b.nprim
+    if b.grad_accum_clean:
+        zeros = b.grad_accum
+        b.grad_accum_clean = False
+    else:  # a second backward through the same forward
+        zeros = torch.zeros((_grad_accum_elems(b.nseg, P, b.mode),), dtype=torch.float32,
+                            device=dev)
+    v_px = zeros[: b.nseg * 8]
+    rest = zeros[b.nseg * 8:]
+    v_colors = rest[: 3 * P].view(P, 3)
+    v_opac = rest[3 * P: 4 * P]
+    v_is2 = rest[4 * P: 5 * P]
+    v_sw = rest[5 * P: 6 * P] if b.mode == MODE_STROKE else None
+    nv = 6 if b.mode == MODE_STROKE else 5
+    out = torch.empty((b.nseg * 8 + P,), dtype=torch.float32, device=dev)
+    v_norm = out[: b.nseg * 8].view(b.nseg, 4, 2)
+    v_aa = out[b.nseg * 8:]
+    v_output, planar = image_grad_layout(v_output)
+    with N.prof("cubic.bwd.rast"):
+        N.call("cs_rasterize_backward_finalized", b.mode, N.ptr(b.primitive_ids_sorted),
+               b.ptr("tile_bins"), b.ptr("edges"), b.ptr("edge_culls"), b.ptr("prim_recs"),
+               N.ptr(background), b.img_h, b.img_w, b.block_x, b.block_y,
+               b.edges_per_segment, N.ptr(final_T), N.ptr(final_idx), N.ptr(b.log_index),
+               N.ptr(b.log_pool), N.ptr(v_output), planar, N.ptr(v_px), N.ptr(v_colors),
+               N.ptr(v_opac), N.ptr(v_is2), N.ptr(v_sw), P, N.ptr(rest[nv * P:]),
+               N.ptr(b.tile_order), b.nseg, N.ptr(widths), N.ptr(v_norm), N.ptr(v_aa),
+               N.stream(dev))
+    return v_norm, v_colors, v_opac, v_aa, v_sw
+
+
 def accumulate_edge_grads(b: Binned, v_edges):
     """Reference building block (cubic_splatting.py:2308-2396; the CSR form
     :2399-2487 for the adaptive flattening): v_edges [E,4] -> (v_cubics_px,
@@ -996,7 +1034,16 @@ def _splat_backward(ctx, grad_out_img):
             curve_isect_contrib = torch.zeros((b.num_intersects,), dtype=torch.float32,
                                               device=colors.device)
     # rasterize_backward takes the gradient in either layout (no copy of a
-    # planar one).
+    # planar one).  Without the hooks the epilogue runs in the backward's
+    # own last launch.
+    if process_fn is None and not b.any_tile and not b.adaptive:
+        v_cubics_norm, v_colors, v_opac, v_aa, v_sw = rasterize_backward_finalized(
+            b, bg, final_T, final_idx, grad_out_img, widths)
+        depth_index = 5 if ctx.mode == MODE_STROKE else 4
+        v_depths = (torch.zeros_like(depths, dtype=torch.float32)
+                    if ctx.needs_input_grad[depth_index] else None)
+        return v_cubics_norm.view(ctx.cub_shape), v_colors, v_opac.view_as(opacities), v_sw, \
+            v_depths, v_aa
     v_cubics_px, v_colors, v_opac, v_is2, v_sw = rasterize_backward(
         b, bg, final_T, final_idx, grad_out_img, curve_contrib_rgb=curve_contrib_rgb,
         curve_isect_contrib=curve_isect_contrib)

@@ -138,6 +138,30 @@ def test_backward_matches_oracle(name):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("name", list(CASES))
+def test_backward_finalized_matches_oracle(name):
+    """cs_rasterize_backward_finalized (the backward with the per-XCD copies'
+    reduction and the epilogue in one launch) against the oracle, as the two
+    calls it replaces."""
+    print(f"[backward finalized] {name}", flush=True)
+    sc, s, b, out, T, idx, fw, rows = _run(name)
+    v = random_v_out(sc.img_h, sc.img_w)
+    if rows:
+        v[: rows[0]] = 0
+        v[rows[1]:] = 0
+    widths = torch.clamp(s.aa_widths.float(), min=1e-4).contiguous()
+    v_norm, v_col, v_op, v_aa, v_sw = splat.rasterize_backward_finalized(
+        b, s.background.float(), T, idx, v.cuda(), widths)
+    g = O.render_backward(fw, v.numpy())
+    checks = [("v_colors", v_col, g["v_colors"]), ("v_opacities", v_op, g["v_opacities"]),
+              ("v_cubics_norm", v_norm, g["v_cubics_norm"]),
+              ("v_aa_widths", v_aa, g["v_aa_widths"])]
+    if v_sw is not None:
+        checks.append(("v_stroke_widths", v_sw, g["v_stroke_widths"]))
+    check_grads(checks)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("S", [2, 8, 16, 33])
 def test_accumulate_edge_grads_block(S):
     """_accumulate_edge_grads_to_cubics (cubic_splatting.py:2308-2396) on
