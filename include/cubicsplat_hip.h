@@ -586,8 +586,10 @@ size_t cs_ssim_scratch_elems(int32_t nc, int32_t h, int32_t w, int32_t win);
  * of map i (the per-image, per-channel values of size_average=False and
  * nonnegative_ssim).  If abc != null also stores, per map pixel, dS/dmu_x,
  * dS/dE[x^2], dS/dE[xy] (cs_ssim_abc_elems floats: [3, nc, oh, ow] with rows
- * padded to a multiple of 4 floats) for cs_ssim_backward.  x, y: [nc, h, w];
- * scratch: cs_ssim_scratch_elems floats. */
+ * padded to a multiple of 4 floats) for cs_ssim_backward; with windows up
+ * to 15 one map plane (oh rows of the padded ow) holds at most 2^30 floats
+ * (CS_ERR_ARGS beyond).  x, y: [nc, h, w]; scratch: cs_ssim_scratch_elems
+ * floats. */
 int cs_ssim(const float* x, const float* y, int32_t nc, int32_t h, int32_t w,
             const float* win1d, int32_t win, float c1, float c2, int32_t per_map,
             float* partials, float* out, float* abc, float* scratch, hipStream_t stream);

@@ -162,6 +162,7 @@ __global__ __launch_bounds__(kMseThreads) void k_sum_partial(const float* __rest
 // the image); only the horizontal results live in LDS.  The vertical pass
 // gives each thread a column and a 6-tall row strip (32 x 8 items).
 constexpr int kSsimTiledMaxWin = 15;  // widest window of the tiled kernels
+constexpr int64_t kSsimMaxMapPlane = 1ll << 30;  // floats of one map plane (oh x padded ow)
 constexpr int kSsimTW = 32;   // output tile width
 constexpr int kSsimTH = 48;   // output tile height
 constexpr int kHStrip = 8;    // horizontal-pass outputs per thread
@@ -266,11 +267,11 @@ __device__ __forceinline__ SsimPixel ssim_pixel(float m1, float m2, float mss, f
                                                 float ky, float c1, float c2, bool grad) {
     // sigma_x^2 + sigma_y^2 from the one filtered E[x^2 + y^2].
     const float s1s2 = mss - __builtin_fmaf(m2, m2, m1 * m1);
-    const float s12 = mxy - m1 * m2;
+    const float s12 = __builtin_fmaf(-m1, m2, mxy);
     const float mu1 = m1 + kx, mu2 = m2 + ky;
-    const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2, mu12 = mu1 * mu2;
-    const float n1 = 2.0f * mu12 + c1, d1 = mu1_sq + mu2_sq + c1;
-    const float n2 = 2.0f * s12 + c2, d2 = s1s2 + c2;
+    const float n1 = __builtin_fmaf(mu1 + mu1, mu2, c1);
+    const float d1 = __builtin_fmaf(mu1, mu1, __builtin_fmaf(mu2, mu2, c1));
+    const float n2 = __builtin_fmaf(2.0f, s12, c2), d2 = s1s2 + c2;
     // The hardware reciprocal (within 1 ulp): d1 >= c1 and d2 >= c2 up to
     // rounding, so both are positive normals; the loss and its gradient are
     // compared to float64 at 1e-5 / 1e-4, far above this rounding.
@@ -280,11 +281,14 @@ __device__ __forceinline__ SsimPixel ssim_pixel(float m1, float m2, float mss, f
     o.s = l * cs_;
     o.a = o.b = o.c = 0.0f;
     if (grad) {
-        const float dl = 2.0f * (mu2 - l * mu1) * r1;
-        const float dcs = 2.0f * (mu1 * cs_ - mu2) * r2;
-        o.a = cs_ * dl + l * dcs;
-        o.b = -l * cs_ * r2;
-        o.c = 2.0f * l * r2;
+        // dl/dmu1 = 2 (mu2 - l mu1) r1 and dcs/dmu1 = 2 (mu1 cs - mu2) r2, so
+        // A = cs dl + l dcs = 2 (cs r1 (mu2 - l mu1) + l r2 (mu1 cs - mu2));
+        // B = -l cs r2 and C = 2 l r2.
+        const float t = __builtin_fmaf(-l, mu1, mu2), u = __builtin_fmaf(mu1, cs_, -mu2);
+        const float p = cs_ * r1, q = l * r2;
+        o.a = 2.0f * __builtin_fmaf(p, t, q * u);
+        o.b = -(cs_ * q);
+        o.c = q + q;
     }
     return o;
 }
@@ -295,7 +299,8 @@ __device__ __forceinline__ SsimPixel ssim_pixel(float m1, float m2, float mss, f
 // input is counted once and no separate MSE pass is needed.
 // CLAMP: x is read as clamp(x, lo, hi) (the caller's clamp glue, applied on
 // load instead of in a pass of its own).
-template <int WIN, bool CLAMP>
+// GRAD: abc is given (the three maps are written).
+template <int WIN, bool CLAMP, bool GRAD>
 __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
                                                  const float* __restrict__ y, int h, int w,
                                                  int oh, int ow,
@@ -421,22 +426,28 @@ __global__ __launch_bounds__(256) void k_ssim_fwd(const float* __restrict__ x,
         }
     }
     float acc = 0.0f;
-    const size_t ld = abc_ld(ow);
+    const int ld = abc_ld(ow);
     const size_t plane = (size_t)oh * ld;
     const size_t stride = (size_t)nc * plane;
+    // The maps of channel c from workgroup-uniform bases, at 32-bit byte
+    // offsets within a plane (the launch checks that a plane's bytes fit).
+    char* const map_a = reinterpret_cast<char*>(abc + (size_t)c * plane);
+    char* const map_b = map_a + stride * sizeof(float);
+    char* const map_c = map_b + stride * sizeof(float);
     const int ox = ox0 + q;
+    const int oy_s = oy0 + r0;
+    const uint32_t ob0 = ((uint32_t)oy_s * (uint32_t)ld + (uint32_t)ox) * 4u;
 #pragma unroll
     for (int o = 0; o < kVStrip; ++o) {
-        const int oy = oy0 + r0 + o;
-        if (oy >= oh || ox >= ow) continue;
+        if (oy_s + o >= oh || ox >= ow) continue;
         const SsimPixel sp = ssim_pixel(mom[0][o], mom[1][o], mom[2][o], mom[3][o], kx, ky, c1,
-                                        c2, abc != nullptr);
+                                        c2, GRAD);
         acc += sp.s;
-        if (abc) {
-            const size_t oi = (size_t)c * plane + (size_t)oy * ld + ox;
-            abc[oi] = sp.a;
-            abc[stride + oi] = sp.b;
-            abc[2 * stride + oi] = sp.c;
+        if (GRAD) {
+            const uint32_t ob = ob0 + (uint32_t)(o * ld) * 4u;
+            *reinterpret_cast<float*>(map_a + ob) = sp.a;
+            *reinterpret_cast<float*>(map_b + ob) = sp.b;
+            *reinterpret_cast<float*>(map_c + ob) = sp.c;
         }
     }
     const float bs = block_sum(acc, sh);
@@ -928,10 +939,13 @@ static int launch_ssim_fwd(const float* x, const float* y, int32_t nc, int32_t h
                            float* partials, float* abc, hipStream_t stream, int* nblk,
                            float* mse_partials = nullptr, float lo = 0.0f, float hi = 0.0f) {
     const int oh = h - win + 1, ow = w - win + 1;
+    // The map stores address a plane with 32-bit byte offsets.
+    if (abc && (int64_t)oh * abc_ld(ow) > kSsimMaxMapPlane) return CS_ERR_ARGS;
     const dim3 grid(((ow + kSsimTW - 1) / kSsimTW) * ((oh + kSsimTH - 1) / kSsimTH) * nc);
-#define CS_SSIM_FWD(W_)                                                                        \
-    hipLaunchKernelGGL((k_ssim_fwd<W_, CLAMP>), grid, dim3(256), 0, stream, x, y, h, w, oh, ow, \
-                       win1d, c1, c2, partials, abc, nc, mse_partials, lo, hi)
+#define CS_SSIM_FWD(W_)                                                                       \
+    hipLaunchKernelGGL((abc ? k_ssim_fwd<W_, CLAMP, true> : k_ssim_fwd<W_, CLAMP, false>),     \
+                       grid, dim3(256), 0, stream, x, y, h, w, oh, ow, win1d, c1, c2, partials, \
+                       abc, nc, mse_partials, lo, hi)
     switch (win) {
         CS_SSIM_DISPATCH(1, CS_SSIM_FWD)
         CS_SSIM_DISPATCH(3, CS_SSIM_FWD)

@@ -316,6 +316,21 @@ def test_fused_loss_layout_arguments_rejected_before_any_launch():
                                           buf, buf, 0, None) == N.CS_ERR_ARGS
 
 
+def test_ssim_map_plane_limit_rejected_before_any_launch():
+    """The SSIM forward writes its gradient maps at 32-bit byte offsets
+    within a map plane, so a plane of more than 2^30 floats is refused, with
+    the maps asked for, before any HIP call (the value alone is not)."""
+    import ctypes
+    from repo_amd import _native as N
+    lib = N.lib()
+    buf = (ctypes.c_float * 4)()
+    side = 32779  # map 32769 x 32769, rows padded to 32772 floats
+    assert lib.cs_ssim(buf, buf, 1, side, side, buf, 11, 1e-4, 9e-4, 0, buf, buf, buf, None,
+                       None) == N.CS_ERR_ARGS
+    assert lib.cs_mse_ssim_loss(buf, buf, 1, side, side, buf, 11, 1e-4, 9e-4, 0.2, buf, buf,
+                                buf, None) == N.CS_ERR_ARGS
+
+
 def test_compiled_binding_matches_ctypes():
     """repo_amd/_cs_fast (built by build()) wraps every int-returning entry
     point of the signature tables; it checks its argument count and returns
