@@ -1030,10 +1030,12 @@ __global__ __launch_bounds__(256) void k_prim_rep_reduce(float* __restrict__ rep
 
 // k_prim_rep_reduce and k_finalize in one launch, for a backward whose
 // per-primitive gradients go straight to the epilogue (no hook between them):
-// thread t < nprim adds primitive t's copies into the caller's arrays (the
-// same sums as k_prim_rep_reduce), clears them and takes v_aa[t] from the
-// final v_is2[t] (the expression of k_finalize); thread t < 8 nseg scales
-// v_px[t] into v_norm[t].
+// thread t < NV nprim adds value t % NV of primitive t / NV from its copies
+// into the caller's array (the same sums as k_prim_rep_reduce) and clears
+// them, and the thread of v_is2 takes v_aa from the final value (the
+// expression of k_finalize); thread t < 8 nseg scales v_px[t] into v_norm[t].
+// One value per thread keeps eight loads in flight per thread on about NV
+// times the threads of one primitive per thread.
 template <int NV>
 __global__ __launch_bounds__(256) void k_prim_rep_finalize(
     float* __restrict__ rep, int nprim, float* __restrict__ v_col, float* __restrict__ v_op,
@@ -1042,23 +1044,22 @@ __global__ __launch_bounds__(256) void k_prim_rep_finalize(
     float* __restrict__ v_norm, float* __restrict__ v_aa) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t < (int64_t)nseg * 8) v_norm[t] = v_px[t] * ((t & 1) ? half_h : half_w);
-    if (t >= nprim) return;
-    const int p = (int)t;
+    if (t >= (int64_t)nprim * NV) return;
+    const int p = (int)(t / NV), v = (int)(t - (int64_t)p * NV);
+    float sum = 0.0f;
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-        const int64_t i = (int64_t)p * NV + v;
-        float sum = 0.0f;
-#pragma unroll
-        for (int r = 0; r < kGradReplicas; ++r) {
-            float* q = rep + (int64_t)r * nprim * NV + i;
-            sum += *q;
-            *q = 0.0f;
-        }
-        float* dst = v < 3 ? v_col + 3 * p + v : v == 3 ? v_op + p : v == 4 ? v_is2 + p : v_sw + p;
-        *dst += sum;
+    for (int r = 0; r < kGradReplicas; ++r) {
+        float* q = rep + (int64_t)r * nprim * NV + t;
+        sum += *q;
+        *q = 0.0f;
     }
-    const float w = fmaxf(widths[p], kWidthMin);
-    v_aa[p] = (-2.0f * v_is2[p]) / fmaxf(w * w * w, (float)1e-12);
+    float* dst = v < 3 ? v_col + 3 * p + v : v == 3 ? v_op + p : v == 4 ? v_is2 + p : v_sw + p;
+    const float tot = *dst + sum;
+    *dst = tot;
+    if (v == 4) {
+        const float w = fmaxf(widths[p], kWidthMin);
+        v_aa[p] = (-2.0f * tot) / fmaxf(w * w * w, (float)1e-12);
+    }
 }
 
 struct GradBuf {
@@ -2089,7 +2090,8 @@ static void launch_bwd4(const RasterArgs& a) {
                        a.counts);
     if (a.prim_rep && a.fin_norm) {
         constexpr int NV = MODE == 1 ? 6 : 5;
-        const int64_t n = (int64_t)a.nseg * 8 > a.nprim ? (int64_t)a.nseg * 8 : a.nprim;
+        const int64_t n = (int64_t)a.nseg * 8 > (int64_t)a.nprim * NV ? (int64_t)a.nseg * 8
+                                                                       : (int64_t)a.nprim * NV;
         const float half_w = (float)(0.5 * (double)a.img_w), half_h = (float)(0.5 * (double)a.img_h);
         hipLaunchKernelGGL(k_prim_rep_finalize<NV>, dim3((unsigned)((n + 255) / 256)), dim3(256),
                            0, a.stream, a.prim_rep, a.nprim, a.v_col, a.v_op, a.v_is2, a.v_sw,
