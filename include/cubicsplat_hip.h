@@ -191,7 +191,10 @@ int cs_cubic_split_half(const float* cubics, int32_t n, float* left, float* righ
  * it, nothing is written except empty tile_bins (the caller retries with a
  * larger buffer).  zero_buf (optional, zero_n floats) is cleared by the same
  * launch: the caller's gradient accumulators for cs_rasterize_backward, which
- * saves that step a separate fill. */
+ * saves that step a separate fill.  status_host (optional): pinned host memory
+ * (a device-accessible address of it, hipHostGetDevicePointer) that receives
+ * the four status words; they are there once the launch has completed (an
+ * event recorded after the call), with no separate device-to-host copy. */
 /* Elements of the tile_count and tile_scratch buffers that cs_bin_prepare,
  * cs_bin_prepare_de_casteljau, cs_gs_bin_prepare and cs_bin_finish take:
  * the list build splits the depth ranks into at most 64 slabs of whole
@@ -206,7 +209,8 @@ int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_ranges, int32_t
                   const int32_t* status, int64_t capacity, int32_t img_h, int32_t img_w,
                   int32_t block_x, int32_t block_y, uint32_t* tile_count, uint32_t* tile_scratch,
                   int32_t* prim_ids_sorted,
-                  int32_t* tile_bins, float* zero_buf, int64_t zero_n, hipStream_t stream);
+                  int32_t* tile_bins, float* zero_buf, int64_t zero_n, int32_t* status_host,
+                  hipStream_t stream);
 
 /* ---------------- rasterization ---------------- */
 

@@ -49,7 +49,7 @@ _SIGNATURES = {
                                       _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cs_bin_list_elems": (_SZ, [_I32, _I32, _I32, _I32, _I32]),
     "cs_bin_finish": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _I32, _I32, _I32, _I32, _P, _P,
-                                     _P, _P, _P, _I64, _P]),
+                                     _P, _P, _P, _I64, _P, _P]),
     "cs_rasterize_forward": (ctypes.c_int, [_I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                             _I32, _P, _I32, _P, _P, _P, _I64, _P, _P, _I64, _I32,
                                             _P, _P, _P, _P]),
@@ -179,6 +179,9 @@ _HIP_SIGNATURES = {
     "hipEventDestroy": (ctypes.c_int, [ctypes.c_void_p]),
     "hipMemcpyAsync": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_int, ctypes.c_void_p]),
+    "hipHostGetDevicePointer": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p,
+                                               ctypes.c_uint]),
+    "hipGetLastError": (ctypes.c_int, []),
 }
 HIP_EVENT_DEFAULT = 0
 HIP_EVENT_DISABLE_TIMING = 2
@@ -225,6 +228,16 @@ def event_elapsed_ms(a: int, b: int) -> float:
     out = ctypes.c_float()
     hip_check(hip().hipEventElapsedTime(ctypes.byref(out), a, b), "hipEventElapsedTime")
     return float(out.value)
+
+
+def host_device_ptr(host_ptr: int) -> Optional[int]:
+    """The device-accessible address of pinned host memory, or None where the
+    runtime gives none (the caller then copies instead)."""
+    d = ctypes.c_void_p()
+    if hip().hipHostGetDevicePointer(ctypes.byref(d), host_ptr, 0) != 0:
+        hip().hipGetLastError()  # clear it: the entry points report the last error
+        return None
+    return d.value or None
 
 
 def event_destroy(ev: int) -> None:

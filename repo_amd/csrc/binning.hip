@@ -1462,11 +1462,15 @@ __global__ __launch_bounds__(kWave * kListWaves) void k_tile_scatter(
     int tby, int nsegcols, int slab, int nslab, const uint32_t* __restrict__ tile_count,
     const uint32_t* __restrict__ seg_scratch, int32_t* __restrict__ prim_ids_sorted,
     int32_t* __restrict__ tile_bins, float* __restrict__ zero_buf, int64_t zero_n,
-    const int32_t* __restrict__ total, int64_t capacity) {
+    const int32_t* __restrict__ total, int64_t capacity, int32_t* __restrict__ status_host) {
     __shared__ int32_t hit_pid[kListChunk];
     __shared__ uint32_t hit_cols[kListChunk];
     __shared__ int hit_n[kListWaves];
     __shared__ uint32_t tile_start[kSegTiles];
+    // The four status words (final once the counting launch has ended) to the
+    // caller's host buffer, which it reads after this launch.
+    if (status_host && blockIdx.x == 0 && threadIdx.x < 4)
+        status_host[threadIdx.x] = total[threadIdx.x];
     if (zero_buf) {
         const int64_t stride = (int64_t)gridDim.x * blockDim.x;
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += stride)
@@ -2277,7 +2281,7 @@ extern "C" int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_rang
                              uint32_t* tile_count,
                              uint32_t* tile_scratch, int32_t* prim_ids_sorted,
                              int32_t* tile_bins, float* zero_buf, int64_t zero_n,
-                             hipStream_t stream) {
+                             int32_t* status_host, hipStream_t stream) {
     if (nprim <= 0 || !status || capacity < 0 || img_h <= 0 || img_w <= 0 || block_x <= 0 ||
         block_y <= 0 || zero_n < 0 || (zero_n > 0 && !zero_buf))
         return CS_ERR_ARGS;
@@ -2288,7 +2292,7 @@ extern "C" int cs_bin_finish(const int32_t* order, const int32_t* rank_tile_rang
                        dim3(kWave * kListWaves), 0, stream, order,
                        reinterpret_cast<const int4*>(rank_tile_ranges), nprim, tbx, tby, nsegcols,
                        ls.slab, ls.nslab, tile_count, tile_scratch, prim_ids_sorted, tile_bins,
-                       zero_n > 0 ? zero_buf : nullptr, zero_n, status, capacity);
+                       zero_n > 0 ? zero_buf : nullptr, zero_n, status, capacity, status_host);
     return launch_status();
 }
 

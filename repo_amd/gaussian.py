@@ -190,7 +190,7 @@ def bin_gaussians(xys, conics, radii, depths, img_h: int, img_w: int, block_x: i
         N.call("cs_bin_finish", q_("order"), q_("rank_tile_ranges"), n, q_("status"), I,
                int(img_h), int(img_w), int(block_x), int(block_y), q_("tile_count"),
                q_("tile_scratch"), N.ptr(ids), q_("tile_bins"),
-               q_("grad_accum"), 9 * n, st)
+               q_("grad_accum"), 9 * n, None, st)
     b.gaussian_ids_sorted = ids
     b.num_intersects = I
     return b

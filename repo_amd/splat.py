@@ -262,8 +262,9 @@ class Binned:
 
 @dataclass
 class _PendingCount:
-    # (pinned int32 [4] filled by an async copy, raw hipEvent_t recorded after
-    # that copy, device index)
+    # (pinned int32 [4] that receives the status words, raw hipEvent_t
+    # recorded after the launch or copy that writes them, device index, the
+    # buffer's device-accessible address or None)
     pinned: tuple
     capacity: int               # elements of the primitive_ids_sorted buffer
     finish: Callable[[int], torch.Tensor]  # cs_bin_finish into a new buffer of that size
@@ -279,8 +280,8 @@ def _take_pinned(dev_index: int):
     if pool:
         return pool.pop()
     with torch.cuda.device(dev_index):
-        return (torch.empty((4,), dtype=torch.int32, pin_memory=True), N.event_create(),
-                dev_index)
+        host = torch.empty((4,), dtype=torch.int32, pin_memory=True)
+        return (host, N.event_create(), dev_index, N.host_device_ptr(host.data_ptr()))
 
 
 def _give_pinned(entry) -> None:
@@ -382,32 +383,38 @@ def bin_primitives(cubics_norm, seg_offsets, colors, opacities, depths, fill_rul
     count_p, scratch_p = q("tile_count"), q("tile_scratch")
     bins_p, grad_p, grad_n = q("tile_bins"), q("grad_accum"), plan.grad_n
 
-    def finish(capacity: int) -> torch.Tensor:
+    def finish(capacity: int, status_dev=None) -> torch.Tensor:
         ids = torch.empty((capacity,), dtype=torch.int32, device=dev)
         with N.prof("cubic.fwd.bin_finish"):
             N.call("cs_bin_finish", order_p, ranks_p, P, status_p, capacity, img_h, img_w,
                    block_x, block_y, count_p, scratch_p, ids.data_ptr(), bins_p,
-                   grad_p, grad_n, st)
+                   grad_p, grad_n, status_dev, st)
         return ids
 
     # The one host read of the forward (the reference reads the same count,
     # cubic_splatting.py:2879).  With a capacity hint the lists are built into
     # a buffer of that size first and the count is checked afterwards, so the
-    # GPU does not idle while the host waits for it.
+    # GPU does not idle while the host waits for it; the list launch then also
+    # writes the status words to the pinned buffer (no copy of their own).
     pinned = _take_pinned(dev.index if dev.index is not None else torch.cuda.current_device())
-    status_host, event = pinned[0], pinned[1]
+    status_host, event, status_dev = pinned[0], pinned[1], pinned[3]
     hip = N.hip()
-    N.hip_check(hip.hipMemcpyAsync(status_host.data_ptr(), status_p, 16,
-                                   N.HIP_MEMCPY_DEVICE_TO_HOST, st), "hipMemcpyAsync")
-    N.hip_check(hip.hipEventRecord(event, st), "hipEventRecord")
     pending = _PendingCount(pinned, -1, finish)
+    if capacity_hint is None or status_dev is None:
+        N.hip_check(hip.hipMemcpyAsync(status_host.data_ptr(), status_p, 16,
+                                       N.HIP_MEMCPY_DEVICE_TO_HOST, st), "hipMemcpyAsync")
+        N.hip_check(hip.hipEventRecord(event, st), "hipEventRecord")
     if capacity_hint is None:
         I = _read_count(pending, nseg)
         b.primitive_ids_sorted = finish(I)
         b.num_intersects = I
     else:
         pending.capacity = max(0, int(capacity_hint))
-        b.primitive_ids_sorted = finish(pending.capacity)
+        if status_dev is None:
+            b.primitive_ids_sorted = finish(pending.capacity)
+        else:
+            b.primitive_ids_sorted = finish(pending.capacity, status_dev)
+            N.hip_check(hip.hipEventRecord(event, st), "hipEventRecord")
         b.pending = pending
     return b
 

@@ -217,6 +217,8 @@ def test_deferred_count_matches_synchronous(hint):
         s.colors.contiguous(), s.opacities.contiguous(), s.depths.contiguous(),
         s.fill_rules.to(torch.int32).contiguous(), widths, None, s.img_h, s.img_w, s.S,
         capacity_hint=hint if hint is not None else ref.num_intersects)
+    # The list launch writes the status words to the pinned buffer itself.
+    assert b.pending is not None and b.pending.pinned[3] is not None
     out, T, idx = splat.rasterize_forward(b, bg)
     rebuilt = splat.resolve_binned(b)
     cap = hint if hint is not None else ref.num_intersects
@@ -228,6 +230,27 @@ def test_deferred_count_matches_synchronous(hint):
                                   ref.primitive_ids_sorted.cpu().numpy())
     np.testing.assert_array_equal(b.tile_bins.cpu().numpy(), ref.tile_bins.cpu().numpy())
     assert torch.equal(out, out_ref) and torch.equal(T, T_ref) and torch.equal(idx, idx_ref)
+
+
+@pytest.mark.gpu
+def test_deferred_count_reports_invalid_offsets():
+    """The status words the list launch writes to pinned memory carry the CSR
+    checks too: offsets that decrease, or that end short of the segment count,
+    raise when the deferred count is read."""
+    from repo_amd import splat
+    sc = synth.small_scene(0, P=3)
+    s = sc.to("cuda")
+    widths = torch.clamp(s.aa_widths.float(), min=1e-4).contiguous()
+    for offs in ([0, 4, 3, 12], [0, 4, 8, 11]):
+        print(f"[deferred offsets] {offs}", flush=True)
+        b = splat.bin_primitives(
+            s.cubics_norm.contiguous(), torch.tensor(offs, dtype=torch.int32, device="cuda"),
+            s.colors.contiguous(), s.opacities.contiguous(), s.depths.contiguous(),
+            s.fill_rules.to(torch.int32).contiguous(), widths, None, s.img_h, s.img_w, s.S,
+            capacity_hint=4096)
+        assert b.pending is not None and b.pending.pinned[3] is not None
+        with pytest.raises(ValueError, match="primitive_seg_offsets"):
+            splat.resolve_binned(b)
 
 
 @pytest.mark.gpu
