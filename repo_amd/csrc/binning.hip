@@ -754,17 +754,25 @@ struct PrimPrep {
     PrimRec rec;
 };
 
-// One primitive of k_prim_prep, computed (no stores).  Every load depends on
-// p only, so with a wave-uniform p they are scalar loads.
-__device__ __forceinline__ PrimPrep prim_prep_compute(
-    const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets,
-    const int32_t* __restrict__ seg_tile_ranges, const SegRec* __restrict__ seg_recs,
-    const float* __restrict__ colors, const float* __restrict__ opacities,
-    const float* __restrict__ depths, const int32_t* __restrict__ fill_rules,
-    const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
-    int eps, const int32_t* __restrict__ seg_edge_offsets, int tbx, int tby, int mode, int p) {
+// Segments whose records prim_prep_compute_at reads in one round trip.
+constexpr int kPrepSegGroup = 4;
+
+// One primitive of k_prim_prep, computed (no stores), from its CSR offsets
+// s0 = seg_offsets[p], s1 = seg_offsets[p + 1] (loaded by the caller, whose
+// other loads can then overlap them).  Every load depends on p only, so with
+// a wave-uniform p they are scalar loads.  The segments are read
+// kPrepSegGroup at a time, every load of a group issued before the first is
+// used; a group's positions past the last segment repeat the last one, which
+// changes none of the minima, maxima and conjunctions taken over them.
+__device__ __forceinline__ PrimPrep prim_prep_compute_at(
+    const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_tile_ranges,
+    const SegRec* __restrict__ seg_recs, const float* __restrict__ colors,
+    const float* __restrict__ opacities, const float* __restrict__ depths,
+    const int32_t* __restrict__ fill_rules, const float* __restrict__ aa_widths,
+    const float* __restrict__ stroke_widths, int nseg, int eps,
+    const int32_t* __restrict__ seg_edge_offsets, int tbx, int tby, int mode, int p, int s0,
+    int s1) {
     PrimPrep o;
-    int s0 = seg_offsets[p], s1 = seg_offsets[p + 1];
     // Invalid CSR offsets are reported through status[1] and clamped so that
     // no kernel reads outside the segment arrays.
     o.bad = s0 < 0 || s1 < s0 || s1 > nseg;
@@ -772,16 +780,44 @@ __device__ __forceinline__ PrimPrep prim_prep_compute(
         s0 = clampi(s0, 0, nseg);
         s1 = clampi(s1, s0, nseg);
     }
-    // cubic_splatting.py:2103-2135
+    // cubic_splatting.py:2103-2135 (the tile rectangle), and the unions of
+    // the segments' ranges and the chain's closure for the raster record.
+    int mnx = tbx, mny = tby, mxx = 0, mxy = 0;
+    int closed = 1;
+    IRange nx{kRangeLimit, -kRangeLimit}, ny = nx, cy = nx;
+    int32_t x_last = -kRangeLimit;
+    for (int sc = s0; sc < s1; sc += kPrepSegGroup) {
+        int4 tr[kPrepSegGroup];
+        SegRec sr[kPrepSegGroup];
+        float2 ae[kPrepSegGroup], bs[kPrepSegGroup];
+#pragma unroll
+        for (int u = 0; u < kPrepSegGroup; ++u) {
+            const int s = min(sc + u, s1 - 1);
+            const int nxt = (s + 1 < s1) ? s + 1 : s0;
+            tr[u] = reinterpret_cast<const int4*>(seg_tile_ranges)[s];
+            sr[u] = seg_recs[s];
+            const float* ca = cubics_norm + (size_t)s * 8;
+            const float* cb = cubics_norm + (size_t)nxt * 8;
+            ae[u] = make_float2(ca[6], ca[7]);
+            bs[u] = make_float2(cb[0], cb[1]);
+        }
+#pragma unroll
+        for (int u = 0; u < kPrepSegGroup; ++u) {
+            mnx = min(mnx, tr[u].x); mny = min(mny, tr[u].y);
+            mxx = max(mxx, tr[u].z); mxy = max(mxy, tr[u].w);
+            closed &= (ae[u].x == bs[u].x) & (ae[u].y == bs[u].y);
+            nx.lo = min(nx.lo, sr[u].nx_lo);
+            nx.hi = max(nx.hi, sr[u].nx_lo + sr[u].nx_span - kWaveColsExt);
+            ny.lo = min(ny.lo, sr[u].ny_lo);
+            ny.hi = max(ny.hi, sr[u].ny_lo + sr[u].ny_span - kWaveRowsExt);
+            cy.lo = min(cy.lo, sr[u].cy_lo);
+            cy.hi = max(cy.hi, sr[u].cy_lo + sr[u].cy_span - kWaveRowsExt);
+            x_last = max(x_last, sr[u].x_last);
+        }
+    }
     o.tr = make_int4(0, 0, 0, 0);
     o.area = 0;
     if (s1 > s0) {
-        int mnx = tbx, mny = tby, mxx = 0, mxy = 0;
-        for (int s = s0; s < s1; ++s) {
-            const int4 r = reinterpret_cast<const int4*>(seg_tile_ranges)[s];
-            mnx = min(mnx, r.x); mny = min(mny, r.y);
-            mxx = max(mxx, r.z); mxy = max(mxy, r.w);
-        }
         o.tr = make_int4(mnx, mny, mxx, mxy);
         o.area = (uint32_t)(max(0, mxx - mnx) * max(0, mxy - mny));
     }
@@ -807,23 +843,6 @@ __device__ __forceinline__ PrimPrep prim_prep_compute(
     rec.e0 = seg_edge_offsets ? seg_edge_offsets[s0] : s0 * eps;
     rec.e1 = seg_edge_offsets ? seg_edge_offsets[s1] : s1 * eps;
     rec.rule = fill_rules ? fill_rules[p] : 1;
-    int closed = 1;
-    IRange nx{kRangeLimit, -kRangeLimit}, ny = nx, cy = nx;
-    int32_t x_last = -kRangeLimit;
-    for (int s = s0; s < s1; ++s) {
-        const int nxt = (s + 1 < s1) ? s + 1 : s0;
-        const float* a = cubics_norm + (size_t)s * 8;
-        const float* b = cubics_norm + (size_t)nxt * 8;
-        closed &= (a[6] == b[0]) & (a[7] == b[1]);
-        const SegRec sr = seg_recs[s];
-        nx.lo = min(nx.lo, sr.nx_lo);
-        nx.hi = max(nx.hi, sr.nx_lo + sr.nx_span - kWaveColsExt);
-        ny.lo = min(ny.lo, sr.ny_lo);
-        ny.hi = max(ny.hi, sr.ny_lo + sr.ny_span - kWaveRowsExt);
-        cy.lo = min(cy.lo, sr.cy_lo);
-        cy.hi = max(cy.hi, sr.cy_lo + sr.cy_span - kWaveRowsExt);
-        x_last = max(x_last, sr.x_last);
-    }
     rec.closed = closed;
     rec.ny_lo = ny.lo;
     rec.ny_span = span_y(ny);
@@ -834,6 +853,19 @@ __device__ __forceinline__ PrimPrep prim_prep_compute(
     rec.x_last = x_last;
     rec.cull_out = cull_distance_outside(mode, opacities[p], q.inv_sigma, q.half_sw);
     return o;
+}
+
+__device__ __forceinline__ PrimPrep prim_prep_compute(
+    const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets,
+    const int32_t* __restrict__ seg_tile_ranges, const SegRec* __restrict__ seg_recs,
+    const float* __restrict__ colors, const float* __restrict__ opacities,
+    const float* __restrict__ depths, const int32_t* __restrict__ fill_rules,
+    const float* __restrict__ aa_widths, const float* __restrict__ stroke_widths, int nseg,
+    int eps, const int32_t* __restrict__ seg_edge_offsets, int tbx, int tby, int mode, int p) {
+    return prim_prep_compute_at(cubics_norm, seg_tile_ranges, seg_recs, colors, opacities,
+                                depths, fill_rules, aa_widths, stroke_widths, nseg, eps,
+                                seg_edge_offsets, tbx, tby, mode, p, seg_offsets[p],
+                                seg_offsets[p + 1]);
 }
 
 // Stores primitive p's outputs of k_prim_prep.
@@ -1231,11 +1263,17 @@ __device__ __forceinline__ uint32_t depth_key(float d) {
 }
 
 // k_prim_prep and k_rank_allpairs<false> in one launch, for at most
-// kRankPairsMax primitives: one wave per primitive counts the keys that
-// precede its own (lane-parallel, the keys computed from the depths, since no
-// other wave's keys are written yet); the primitive's records are computed
-// wave-uniformly (scalar loads), and lane 0 stores them and writes
-// order[pos] = p, rank_rects[pos] = its tile rectangle.
+// kRankPairsMax primitives: each wave takes kPrepRankPerWave consecutive
+// primitives, lane k < kPrepRankPerWave computing primitive base + k's
+// records, and counts for all of them the keys that precede each one's own
+// (lane-parallel over the depths, each key computed once and compared with
+// every primitive's; the keys come from the depths, since no other wave's
+// keys are written yet); lane k then stores its primitive's records and
+// writes order[pos] = p, rank_rects[pos] = its tile rectangle.  Several
+// primitives per wave read the depths that many times less often and share
+// the key computation among them.
+constexpr int kPrepRankPerWave = 4;
+
 __global__ __launch_bounds__(256) void k_prim_prep_rank(
     const float* __restrict__ cubics_norm, const int32_t* __restrict__ seg_offsets, int P,
     const int32_t* __restrict__ seg_tile_ranges, const SegRec* __restrict__ seg_recs,
@@ -1247,34 +1285,63 @@ __global__ __launch_bounds__(256) void k_prim_prep_rank(
     uint32_t* __restrict__ counts, float* __restrict__ inv_sigma2s, uint32_t* __restrict__ keys,
     int32_t* __restrict__ vals, PrimRec* __restrict__ recs, int32_t* __restrict__ order,
     int4* __restrict__ rank_rects) {
-    const int p = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    if (p >= P) return;
+    constexpr int NP = kPrepRankPerWave;
+    const int base =
+        (blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6))) * NP;
+    if (base >= P) return;
     const int lane = threadIdx.x & (kWave - 1);
-    const PrimPrep o = prim_prep_compute(cubics_norm, seg_offsets, seg_tile_ranges, seg_recs,
-                                         colors, opacities, depths, fill_rules, aa_widths,
-                                         stroke_widths, nseg, eps, seg_edge_offsets, tbx, tby,
-                                         mode, p);
+    const int p = base + lane;
+    const bool mine = lane < NP && p < P;
+    // Lane k's CSR offsets, loaded first so that they arrive with the depths.
+    int s0 = 0, s1 = 0;
+    if (mine) {
+        s0 = seg_offsets[p];
+        s1 = seg_offsets[p + 1];
+    }
+    // The primitives' (key, index) values, from their depths (the key
+    // prim_prep_compute_at derives); past P the largest value (never stored).
+    uint64_t kp[NP];
+#pragma unroll
+    for (int k = 0; k < NP; ++k)
+        kp[k] = base + k < P ? key_index(depth_key(depths[base + k]), base + k) : ~0ull;
     // (key, index) pairs in lexicographic order: one 64-bit comparison each.
-    const uint64_t kp = key_index(o.key, p);
-    int cnt = 0;
+    int cnt[NP];
+#pragma unroll
+    for (int k = 0; k < NP; ++k) cnt[k] = 0;
     const int n4 = P & ~3;
     const bool vec = (reinterpret_cast<uintptr_t>(depths) & 15) == 0;
     int j0 = 0;
     if (vec) {
-#pragma unroll 4
+#pragma unroll 8
         for (j0 = 4 * lane; j0 < n4; j0 += 4 * kWave) {
             const float4 d = *reinterpret_cast<const float4*>(depths + j0);
-            cnt += (int)(key_index(depth_key(d.x), j0) < kp);
-            cnt += (int)(key_index(depth_key(d.y), j0 + 1) < kp);
-            cnt += (int)(key_index(depth_key(d.z), j0 + 2) < kp);
-            cnt += (int)(key_index(depth_key(d.w), j0 + 3) < kp);
+            const uint64_t e0 = key_index(depth_key(d.x), j0);
+            const uint64_t e1 = key_index(depth_key(d.y), j0 + 1);
+            const uint64_t e2 = key_index(depth_key(d.z), j0 + 2);
+            const uint64_t e3 = key_index(depth_key(d.w), j0 + 3);
+#pragma unroll
+            for (int k = 0; k < NP; ++k)
+                cnt[k] += (int)(e0 < kp[k]) + (int)(e1 < kp[k]) + (int)(e2 < kp[k]) +
+                          (int)(e3 < kp[k]);
         }
         j0 = n4;
     }
-    for (int j = j0 + lane; j < P; j += kWave)
-        cnt += (int)(key_index(depth_key(depths[j]), j) < kp);
-    const int pos = wave_sum_i(cnt);
-    if (lane == 0) {
+    for (int j = j0 + lane; j < P; j += kWave) {
+        const uint64_t e = key_index(depth_key(depths[j]), j);
+#pragma unroll
+        for (int k = 0; k < NP; ++k) cnt[k] += (int)(e < kp[k]);
+    }
+    int pos = 0;
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+        const int t = wave_sum_i(cnt[k]);
+        pos = lane == k ? t : pos;
+    }
+    if (mine) {
+        const PrimPrep o = prim_prep_compute_at(cubics_norm, seg_tile_ranges, seg_recs, colors,
+                                                opacities, depths, fill_rules, aa_widths,
+                                                stroke_widths, nseg, eps, seg_edge_offsets, tbx,
+                                                tby, mode, p, s0, s1);
         prim_prep_store(o, p, status, prim_tile_ranges, counts, inv_sigma2s, keys, vals, recs);
         order[pos] = p;
         rank_rects[pos] = o.tr;
@@ -2080,7 +2147,9 @@ static int bin_prepare(const float* cubics_norm, const int32_t* seg_offsets, con
     }
     if (nprim <= kRankPairsMax) {
         // Records and depth ranks in one launch.
-        hipLaunchKernelGGL(k_prim_prep_rank, dim3((nprim + 3) / 4), dim3(256), 0, stream,
+        constexpr int per_block = 4 * kPrepRankPerWave;
+        hipLaunchKernelGGL(k_prim_prep_rank, dim3((nprim + per_block - 1) / per_block),
+                           dim3(256), 0, stream,
                            cubics_norm, seg_offsets, nprim, seg_tile_ranges,
                            reinterpret_cast<const SegRec*>(seg_recs), colors, opacities, depths,
                            fill_rules, aa_widths, stroke_widths, nseg, eps,
