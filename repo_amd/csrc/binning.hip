@@ -542,6 +542,14 @@ __global__ __launch_bounds__(kWave * kFlattenWaves) void k_project_flatten_wave(
     static_assert(kSegs <= kWave, "one projecting lane per segment");
     const int64_t base = (int64_t)blockIdx.x * kSegs;
     const int nw = (int)min((int64_t)kSegs, (int64_t)nseg - base);
+    // The projecting lane's control points are loaded before the owner search,
+    // whose dependent loads they do not wait for.
+    float cub[8];
+    if (w == 0 && lane < nw) {
+        const float* c = cubics_norm + (size_t)(base + lane) * 8;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) cub[k] = c[k];
+    }
     const int p = w == 0 ? wave_owner(seg_offsets, P, (int)base, bounds) : 0;
     if (w == 0 && lane < nw) {
         const int s = (int)base + lane;
@@ -550,7 +558,7 @@ __global__ __launch_bounds__(kWave * kFlattenWaves) void k_project_flatten_wave(
         const float half_sw = stroke_widths ? fmaxf(0.0f, stroke_widths[p]) * 0.5f : 0.0f;
         const float D = prim_params(mode, aa_widths[p], opacities[p], stroke_widths, p).cull_d;
         const int tbx = (img_w + block_x - 1) / block_x, tby = (img_h + block_y - 1) / block_y;
-        const SegProj r = project_segment(cubics_norm + (size_t)s * 8, 0.5f * (float)img_w,
+        const SegProj r = project_segment(cub, 0.5f * (float)img_w,
                                           0.5f * (float)img_h, half_sw, support, aabb_pad, aniso,
                                           tbx, tby, (float)block_x, (float)block_y);
         float4* cp = reinterpret_cast<float4*>(cubics_px + (size_t)s * 8);
