@@ -485,12 +485,19 @@ __device__ __forceinline__ int far_winding(int4 q, int c, int e1, const WaveRect
 // holds the masks of the first 64 edges and `w0` their far_winding (computed
 // by the caller when first has no distance or exact crossing term): the
 // entry is far when no edge has a distance or exact crossing term.  For a
-// fill, `winding` receives the winding number of the wave's pixels.
+// fill, `winding` receives the winding number of the wave's pixels.  Only a
+// closed chain's crossing count is the same on every row of the wave: an
+// open chain filled (no closing edge; a ring whose segments' shared end
+// points an optimizer moved apart is one) changes it between rows where one
+// of its edges ends right of the wave, so such entries take the edge walk,
+// whose far edges count per row (row_cross_term).  (Comparing the counts of
+// all eight rows instead was measured: slower than the edge walk.)
 template <int MODE>
 __device__ __forceinline__ bool entry_far(const PrimRec& pr, const WaveRect& W,
                                           const EdgeCull* __restrict__ culls,
                                           const ChunkMasks& first, int w0, int& winding) {
     if (first.dist | first.cross) return false;
+    if (MODE == 0 && !pr.closed) return false;
     int w = MODE == 0 ? w0 : 0;
     for (int c = pr.e0 + kWave; c < pr.e1; c += kWave) {
         const int4 q = load_culls(culls, c, pr.e1);
@@ -620,7 +627,7 @@ __device__ __forceinline__ void composite(const PrimRec& pr, float alpha, int g,
 
 // The fields of a primitive record the forward uses after the primitive cull
 // (three 16-byte scalar loads and one dword: colour, opacity, widths, cull
-// distances, edge range, rule); the cull ranges stay in memory (the cull
+// distances, edge range, rule, closed flag); the cull ranges stay in memory (the cull
 // reads them lane-parallel), so they take no scalar registers here.
 __device__ __forceinline__ PrimRec load_prim_fwd(cptr<PrimRec> prims, int pid) {
     const cptr<float4> f = reinterpret_cast<cptr<float4>>(prims + pid);
@@ -629,7 +636,7 @@ __device__ __forceinline__ PrimRec load_prim_fwd(cptr<PrimRec> prims, int pid) {
     PrimRec pr{};
     pr.r = a.x; pr.g = a.y; pr.b = a.z; pr.opacity = a.w;
     pr.inv_sigma2 = b.x; pr.inv_sigma = b.y; pr.half_sw = b.z; pr.cull_d = b.w;
-    pr.e0 = c.x; pr.e1 = c.y; pr.rule = c.z;
+    pr.e0 = c.x; pr.e1 = c.y; pr.rule = c.z; pr.closed = c.w;
     pr.cull_out = prims[pid].cull_out;
     return pr;
 }
@@ -741,7 +748,7 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             // Everything this entry needs from its first cull words is taken
             // before the next entry's load reuses their registers.
             const ChunkMasks cm0 = chunk_masks<MODE == 0>(q_next, pr.e0, pr.e1, W);
-            const int w0 = (MODE == 0 && (cm0.dist | cm0.cross) == 0)
+            const int w0 = (MODE == 0 && pr.closed && (cm0.dist | cm0.cross) == 0)
                                ? far_winding(q_next, pr.e0, pr.e1, W) : 0;
             if (todo) {
                 const int pid2 = __builtin_amdgcn_readlane(pid_l, (int)__builtin_ctzll(todo));
@@ -1309,13 +1316,18 @@ __global__ __launch_bounds__(kRasterThreads) __attribute__((amdgpu_waves_per_eu(
             geom[p] = false;
             if (!valid[p]) continue;
             // coverage() of the forward: its value for exact pixels, the
-            // closed form otherwise.  The distance only feeds gradients
-            // (hardware square root, within 1 ulp).
+            // closed form otherwise.  The distance only feeds gradients: a
+            // fill's terms are proportional to it (hardware square root,
+            // within 1 ulp), but a stroke's take dist - half_sw, which cancels
+            // at the stroke's edge and is then scaled by inv_sigma2 (up to
+            // 1e8 at the width floor), so strokes take the IEEE root.
             Cov c;
             const bool inside = inside_of<MODE>(pr, G[p]);
             c.sgn = inside ? -1.0f : 1.0f;
             c.cov = exact[p] ? lcov[p] : (inside ? 1.0f : 0.0f);
-            c.dist = exact[p] ? __builtin_amdgcn_sqrtf(fmaxf(G[p].min_d2, 0.0f)) : 0.0f;
+            const float d2c = fmaxf(G[p].min_d2, 0.0f);
+            c.dist = !exact[p] ? 0.0f
+                     : MODE == 1 ? sqrt_rn(d2c) : __builtin_amdgcn_sqrtf(d2c);
             c.ed = (MODE == 1 && exact[p]) ? fmaxf(0.0f, c.dist - pr.half_sw) : 0.0f;
             const float op = pr.opacity;
             const float alpha = fminf(kAlphaCap, op * c.cov);
