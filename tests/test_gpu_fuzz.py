@@ -5,7 +5,8 @@ Each scene draws its properties independently, so combinations that the
 structured cases hold one at a time meet here. The properties are:
 * canvas sides that are not multiples of 16;
 * ragged segment counts, including primitives with no segments;
-* closed rings, open chains filled, and random cubic loops;
+* closed rings, open chains filled, random cubic loops, and rings whose segment
+  junctions drifted apart (as Adam moves them);
 * primitives partly or wholly off the image;
 * degenerate segments (all four control points equal);
 * depth ties;
@@ -41,7 +42,7 @@ def _fuzz_scene(seed):
     S = int(rng.choice([2, 3, 7, 8, 16, 33]))
     counts = rng.integers(1, 7, size=P)
     counts[rng.random(P) < 0.1] = 0           # primitives without segments
-    kind = rng.integers(0, 3, size=P)         # 0 ring, 1 open chain, 2 random loop
+    kind = rng.integers(0, 4, size=P)         # 0 ring, 1 open chain, 2 random loop, 3 drifted ring
     segs = []
     for p in range(P):
         n = int(counts[p])
@@ -54,7 +55,7 @@ def _fuzz_scene(seed):
             # An open chain: a random walk of 3 n + 1 points.
             pts = np.cumsum(rng.normal(0.0, 0.3 * r + 1.0, size=(3 * n + 1, 2)), 0)
             pts += np.array([cx, cy])
-        elif kind[p] == 0:
+        elif kind[p] in (0, 3):
             th = np.sort(rng.uniform(0, 2 * np.pi, size=3 * n))
             pts = np.stack([cx + r * np.cos(th), cy + r * np.sin(th)], 1)
             pts = np.concatenate([pts, pts[:1]], 0)          # closes
@@ -62,6 +63,13 @@ def _fuzz_scene(seed):
             pts = rng.uniform([cx - r, cy - r], [cx + r, cy + r], size=(3 * n, 2))
             pts = np.concatenate([pts, pts[:1]], 0)
         cub = np.stack([pts[0:-1:3], pts[1::3], pts[2::3], pts[3::3]], 1)
+        if kind[p] == 3 and not stroke:
+            # A ring whose segments' shared end points moved apart, as an
+            # optimizer moves them: mostly by a few ulp, sometimes by up to
+            # 0.4 px (which can put the two points in different pixel cells).
+            big_drift = rng.random(n) < 0.3
+            amt = np.where(big_drift, 0.4, 1e-5)[:, None] * rng.uniform(-1, 1, size=(n, 2))
+            cub[:, 3] += amt
         for k in range(n):
             if rng.random() < 0.08:                          # degenerate segment
                 cub[k] = cub[k, 0]
